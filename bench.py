@@ -1,0 +1,217 @@
+"""GA-ANS coder benchmark on one MI355X.
+
+Workload: the coder-only case of a 512x768 RGB image under an M=192
+factorized prior -- 1x192x32x48 int32 symbols, per-channel discretized
+Laplacian (scale log-uniform [0.1, 8]), 16-bit CDFs <= 64 entries, P = 4 --
+with inputs resident in HBM.  One step = WarpDivBackend.encode + .decode of
+the batch through the public API (one host sync each, as a caller sees it).
+
+Prints one JSON line: value = raw-RGB GB/s of the encode+decode round trip;
+encode/decode GB/s and Gsym/s alongside; ``roofline`` for the dominant
+kernel (timed with HIP events on the launch stream); ``cpu_baseline`` = the
+CompressAI-equivalent Rans64 coder (oracle/gaans_oracle.c, one stream per
+image, single thread) on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _sub in ("fast-compressai_amd", "oracle"):
+    sys.path.insert(0, os.path.join(REPO, _sub))
+
+METRIC = "ANS encode/decode GB/s (raw RGB bytes) & Gsym/s at 512x768, M=192, P=4"
+HBM_PEAK_GBPS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--p-ch", type=int, default=4)
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this coder's "
+              "multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from fast_compressai import synthetic
+    from fast_compressai.coders import WarpDivBackend, _native
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    w = synthetic.coder_512x768(seed=0, p_ch=args.p_ch)
+    B, N, C, P = w.batch, w.n, w.channels, w.p_ch
+    sym = torch.from_numpy(w.symbols).to(dev)
+    idx = torch.from_numpy(w.explicit_indexes()).to(dev)
+    cdfs, sizes, offs = (torch.from_numpy(a).to(dev) for a in (w.cdfs, w.cdf_sizes, w.offsets))
+    backend = WarpDivBackend()
+    payload = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=P)
+    assert torch.equal(backend.decode(payload, idx, cdfs, sizes, offs), sym)
+    payload_bytes = int(payload.packed.numel())
+
+    # ---- whole-step throughput through the public API -----------------------
+    def step():
+        p = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=P)
+        return backend.decode(p, idx, cdfs, sizes, offs)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    total_s = time.perf_counter() - t0
+    ms_per_step = 1e3 * total_s / args.steps
+
+    def timed(fn, reps):
+        for _ in range(max(3, reps // 10)):
+            fn()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t) / reps
+
+    enc_s = timed(lambda: backend.encode(sym, idx, cdfs, sizes, offs, p_ch=P), args.steps)
+    dec_s = timed(lambda: backend.decode(payload, idx, cdfs, sizes, offs), args.steps)
+
+    # ---- kernel time with HIP events on the launch stream -----------------
+    L = _native.lib()
+    tables = backend.prepared_tables(cdfs, sizes, offs)
+    lay = _native.layout(B, N, C, P)
+    ws = torch.empty(int(lay.workspace_bytes), dtype=torch.uint8, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = torch.empty_like(sym)
+    stream = torch.cuda.current_stream(dev)
+
+    def event_time(launch, reps=200):
+        for _ in range(10):
+            launch()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            launch()
+            e1.record(stream)
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e-3)
+        return statistics.median(times), sum(times) / len(times)
+
+    def launch_decode():
+        _native.check(L.gaans_decode_symbols(stream.cuda_stream, payload.packed.data_ptr(),
+                                             payload_bytes, idx.data_ptr(),
+                                             tables.blob.data_ptr(), tables.nbytes, tables.M,
+                                             B, N, C, P, out.data_ptr(), status.data_ptr()),
+                      "decode")
+
+    def launch_encode_stage():
+        _native.check(L.gaans_encode_symbols(stream.cuda_stream, sym.data_ptr(), idx.data_ptr(),
+                                             tables.blob.data_ptr(), tables.nbytes, tables.M,
+                                             B, N, C, P, ws.data_ptr(), ws.numel()), "encode")
+
+    dec_med, dec_avg = event_time(launch_decode)
+    enc_med, enc_avg = event_time(launch_encode_stage)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0 and torch.equal(out, sym)
+
+    # algorithmic bytes per launch: symbols + indexes (int32) + payload
+    alg_bytes = 4 * B * N + 4 * B * N + payload_bytes
+    if dec_avg >= enc_avg:
+        kernel, dur = "k_decode<false> (gaans_decode_symbols)", dec_avg
+    else:
+        kernel, dur = "k_encode<false> + k_scan (gaans_encode_symbols)", enc_avg
+    achieved = alg_bytes / dur / 1e9
+
+    # ---- CPU baseline: CompressAI-equivalent Rans64, one stream per image --
+    import oracle
+
+    row_sym = np.ascontiguousarray(w.symbols[0])
+    row_idx = np.ascontiguousarray(w.explicit_indexes()[0])
+    cpu_enc, cpu_dec = [], []
+    t_end = time.perf_counter() + args.cpu_seconds
+    data = b""
+    while time.perf_counter() < t_end or len(cpu_enc) < 3:
+        t = time.perf_counter()
+        data = oracle.rans64_encode(row_sym, row_idx, w.cdfs, w.cdf_sizes, w.offsets)
+        t1 = time.perf_counter()
+        dec = oracle.rans64_decode(data, row_idx, w.cdfs, w.cdf_sizes, w.offsets)
+        t2 = time.perf_counter()
+        cpu_enc.append(t1 - t)
+        cpu_dec.append(t2 - t1)
+    assert (dec == row_sym).all()
+    cpu_step = statistics.median(cpu_enc) + statistics.median(cpu_dec)
+    raw = w.raw_rgb_bytes
+    cpu_gbps = raw / cpu_step / 1e9
+
+    value = raw / (ms_per_step * 1e-3) / 1e9
+    rec = {
+        "metric": METRIC,
+        "value": round(value, 4),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u32",
+        "data": "synthetic",
+        "config": {
+            "workload": "coder-only 1x192x32x48 int32 symbols + indexes (512x768 RGB, M=192, "
+                        "Laplacian scales log-U[0.1,8], CDF<=64), P=4, encode+decode via "
+                        "WarpDivBackend",
+            "batch": B, "p_ch": P, "symbols": B * N, "raw_rgb_bytes": raw,
+        },
+        "encode_gbps": round(raw / enc_s / 1e9, 4),
+        "decode_gbps": round(raw / dec_s / 1e9, 4),
+        "encode_gsym_s": round(B * N / enc_s / 1e9, 5),
+        "decode_gsym_s": round(B * N / dec_s / 1e9, 5),
+        "roundtrip_gsym_s": round(B * N / (ms_per_step * 1e-3) / 1e9, 5),
+        "encode_api_ms": round(enc_s * 1e3, 5),
+        "decode_api_ms": round(dec_s * 1e3, 5),
+        "encode_stage_kernel_us": round(enc_avg * 1e6, 3),
+        "decode_kernel_us": round(dec_avg * 1e6, 3),
+        "payload_bytes": payload_bytes,
+        "bpp": round(8 * payload_bytes / (B * 512 * 768), 5),
+        "cpu_rans64_bytes": len(data),
+        "roofline": {
+            "bound": "hbm", "kernel": kernel, "achieved": round(achieved, 3),
+            "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 6),
+            "traffic": None, "alg_bytes_per_launch": alg_bytes,
+            "avg_launch_us": round(dur * 1e6, 3),
+        },
+        "cpu_baseline": {
+            "value": round(cpu_gbps, 5), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": (f"{len(cpu_enc)} encode+decode round trips of the same 1x192x32x48 "
+                       "image, CompressAI-equivalent Rans64 (64-bit state, one stream per "
+                       "image, oracle/gaans_oracle.c, numpy arrays in, no Python list "
+                       f"conversion); median encode {statistics.median(cpu_enc)*1e3:.3f} ms, "
+                       f"decode {statistics.median(cpu_dec)*1e3:.3f} ms"),
+            "speedup_gpu_over_cpu": round(value / cpu_gbps, 2),
+        },
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

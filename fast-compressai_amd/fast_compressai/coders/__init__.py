@@ -1,0 +1,28 @@
+"""GA-ANS (MI355X) and CompressAI RANS entropy coder backends."""
+
+from .capabilities import CoderCapability, coder_catalog, create_coder, warp_div_capability
+from .compressai_ans import Bitstream, CompressAIANSBackend
+from .errors import (
+    BitstreamError,
+    CoderDependencyError,
+    CoderError,
+    CoderInputError,
+    CoderStateError,
+)
+from .warp_div import WarpDivBackend, WarpDivPayload
+
+__all__ = [
+    "Bitstream",
+    "BitstreamError",
+    "CoderCapability",
+    "CoderDependencyError",
+    "CoderError",
+    "CoderInputError",
+    "CoderStateError",
+    "CompressAIANSBackend",
+    "WarpDivBackend",
+    "WarpDivPayload",
+    "coder_catalog",
+    "create_coder",
+    "warp_div_capability",
+]

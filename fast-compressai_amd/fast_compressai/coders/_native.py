@@ -1,0 +1,131 @@
+"""ctypes binding of the HIP GA-ANS library (``include/gaans_w64.h``).
+
+The library is loaded lazily and only from this package's ``lib/`` folder;
+there is no fallback: if it is missing, :class:`CoderDependencyError` is
+raised.  Replaces the reference's pybind11 module
+``fast_compressai.coders._warp_div`` (``src/fast_compressai/coders/cuda/ans_gpu.cpp:25-30``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+from .errors import CoderDependencyError
+
+LIB_NAME = "libgaans_w64.so"
+ABI_VERSION = 1
+
+# return codes
+OK, EINVAL, ETABLE, EHIP = 0, 1, 2, 3
+# device status bits
+ST_RANGE = 0x01
+ST_INDEX = 0x02
+ST_HEADER = 0x04
+ST_TABLES = 0x08
+ST_CORRUPT = 0x10
+ST_INDEXHASH = 0x20
+ST_SIZE = 0x40
+
+STATUS_TEXT = {
+    ST_RANGE: "a symbol cannot be coded (escape value >= 2^32 or non-finite latent)",
+    ST_INDEX: "indexes contain a value outside the CDF table range",
+    ST_HEADER: "payload header is inconsistent with the decode call",
+    ST_TABLES: "coding tables do not match the payload",
+    ST_CORRUPT: "payload chunk offsets or rANS stream are corrupt",
+    ST_INDEXHASH: "indexes do not match the payload",
+    ST_SIZE: "payload would exceed the 4 GiB format limit",
+}
+
+
+class Layout(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_int64) for name in (
+        "B", "N", "C", "P", "HW", "K", "chunk_len", "BK", "header_bytes",
+        "max_payload_bytes", "cap_words", "workspace_bytes", "ws_chunk_words",
+        "ws_chunk_status", "ws_index_hash", "ws_end_off", "ws_info", "ws_states",
+        "ws_words")]
+
+
+def library_path() -> str:
+    return os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", LIB_NAME)
+
+
+def library_available() -> bool:
+    return os.path.exists(library_path())
+
+
+_lib = None
+_lock = threading.Lock()
+
+
+def _declare(L) -> None:
+    p, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    sig = {
+        "gaans_abi_version": ([], ctypes.c_int),
+        "gaans_last_error": ([], ctypes.c_char_p),
+        "gaans_get_layout": ([i64, i64, i64, i64, ctypes.POINTER(Layout)], ctypes.c_int),
+        "gaans_tables_bytes": ([p, i32, i32, ctypes.POINTER(ctypes.c_int64)], ctypes.c_int),
+        "gaans_tables_prepare": ([p, p, p, i32, i32, p, i64, ctypes.POINTER(ctypes.c_uint64)],
+                                 ctypes.c_int),
+        "gaans_encode_symbols": ([p, p, p, p, i64, i32, i64, i64, i64, i64, p, i64],
+                                 ctypes.c_int),
+        "gaans_encode_latents": ([p, p, p, p, p, i64, i32, i64, i64, i64, i64, p, i64],
+                                 ctypes.c_int),
+        "gaans_encode_pack": ([p, p, i64, p, i64, i32, i64, i64, i64, i64, p, i64],
+                              ctypes.c_int),
+        "gaans_decode_symbols": ([p, p, i64, p, p, i64, i32, i64, i64, i64, i64, p, p],
+                                 ctypes.c_int),
+        "gaans_decode_latents": ([p, p, i64, p, p, i64, i32, p, i64, i64, i64, i64, p, p],
+                                 ctypes.c_int),
+        "gaans_host_selftest": ([], ctypes.c_int),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+
+
+def lib():
+    """Load the HIP library (once).  Raises CoderDependencyError if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            path = library_path()
+            if not os.path.exists(path):
+                raise CoderDependencyError(
+                    f"GA-ANS HIP library is not built ({path}); run __graft_entry__.build()")
+            try:
+                L = ctypes.CDLL(path)
+                _declare(L)
+            except (OSError, AttributeError) as exc:
+                raise CoderDependencyError(f"GA-ANS HIP library could not be loaded: {exc}") from exc
+            if L.gaans_abi_version() != ABI_VERSION:
+                raise CoderDependencyError("GA-ANS HIP library ABI version mismatch")
+            _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    msg = lib().gaans_last_error()
+    return msg.decode("utf-8", "replace") if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    if rc != OK:
+        from .errors import CoderInputError
+
+        raise CoderInputError(f"{what} failed: {last_error()} (code {rc})")
+
+
+def layout(B: int, N: int, C: int, P: int) -> Layout:
+    out = Layout()
+    check(lib().gaans_get_layout(B, N, C, P, ctypes.byref(out)), "layout")
+    return out
+
+
+def describe_status(status: int) -> str:
+    parts = [text for bit, text in STATUS_TEXT.items() if status & bit]
+    return "; ".join(parts) if parts else f"status 0x{status:x}"

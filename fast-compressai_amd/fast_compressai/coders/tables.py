@@ -1,0 +1,98 @@
+"""Table upload: CompressAI quantized CDFs laid out for the GA-ANS kernels.
+
+CompressAI keeps ``_quantized_cdf`` as a zero-padded ``[M, Lmax]`` int32
+tensor with ``_cdf_length`` and ``_offset`` (reference
+``src/fast_compressai/coders/factorized.py:23-31``).  The kernels instead read
+a compact blob built once per table set by ``gaans_tables_prepare``: per-table
+metadata, packed ``start | (freq - 1) << 16`` entries and a 256-bucket
+decode lookup.  The blob also carries the table digest that every payload
+records, so decoding with other tables is detected on the device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from collections import OrderedDict
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _native
+from .errors import CoderInputError
+
+
+@dataclass(frozen=True)
+class PreparedTables:
+    blob: torch.Tensor  # device uint8
+    nbytes: int
+    M: int
+    Lmax: int
+    digest: int
+
+    @property
+    def digest_hex(self) -> str:
+        return f"{self.digest:016x}"
+
+
+def prepare_tables(cdfs: torch.Tensor, cdf_sizes: torch.Tensor, offsets: torch.Tensor,
+                   device: torch.device | None = None) -> PreparedTables:
+    """Validate and lay out tables; the blob is placed on ``device``
+    (default: the device of ``cdfs``)."""
+    if cdfs.ndim != 2 or cdf_sizes.ndim != 1 or offsets.ndim != 1:
+        raise CoderInputError("CDF must be [M,L] and CDF sizes/offsets must be [M]")
+    M, Lmax = int(cdfs.shape[0]), int(cdfs.shape[1])
+    if M <= 0 or Lmax < 2:
+        raise CoderInputError("CDF table cannot be empty")
+    if cdf_sizes.numel() != M or offsets.numel() != M:
+        raise CoderInputError("CDF, CDF sizes, and offsets must have the same table count")
+    c = np.ascontiguousarray(cdfs.detach().to("cpu").numpy().astype(np.int32, copy=False))
+    s = np.ascontiguousarray(cdf_sizes.detach().to("cpu").numpy().astype(np.int32, copy=False))
+    o = np.ascontiguousarray(offsets.detach().to("cpu").numpy().astype(np.int32, copy=False))
+    L = _native.lib()
+    nbytes = ctypes.c_int64(0)
+    rc = L.gaans_tables_bytes(s.ctypes.data, M, Lmax, ctypes.byref(nbytes))
+    if rc != _native.OK:
+        raise CoderInputError(f"invalid CDF tables: {_native.last_error()}")
+    host = np.zeros(nbytes.value, dtype=np.uint8)
+    digest = ctypes.c_uint64(0)
+    rc = L.gaans_tables_prepare(c.ctypes.data, s.ctypes.data, o.ctypes.data, M, Lmax,
+                                host.ctypes.data, nbytes.value, ctypes.byref(digest))
+    if rc != _native.OK:
+        raise CoderInputError(f"invalid CDF tables: {_native.last_error()}")
+    dev = device if device is not None else cdfs.device
+    blob = torch.from_numpy(host).to(dev)
+    return PreparedTables(blob=blob, nbytes=int(nbytes.value), M=M, Lmax=Lmax,
+                          digest=int(digest.value))
+
+
+class TableCache:
+    """Small LRU of prepared tables keyed by the identity and in-place version
+    of the source tensors.  Entries keep the source tensors alive, so a key
+    cannot be reused by another allocation while it is cached."""
+
+    def __init__(self, capacity: int = 8) -> None:
+        self._capacity = capacity
+        self._entries: OrderedDict = OrderedDict()
+        self._lock = threading.Lock()
+
+    @staticmethod
+    def _key(tensors):
+        return tuple((t.data_ptr(), t._version, tuple(t.shape), t.dtype, str(t.device))
+                     for t in tensors)
+
+    def get(self, cdfs: torch.Tensor, cdf_sizes: torch.Tensor,
+            offsets: torch.Tensor) -> PreparedTables:
+        key = self._key((cdfs, cdf_sizes, offsets))
+        with self._lock:
+            hit = self._entries.get(key)
+            if hit is not None:
+                self._entries.move_to_end(key)
+                return hit[0]
+        prepared = prepare_tables(cdfs, cdf_sizes, offsets)
+        with self._lock:
+            self._entries[key] = (prepared, (cdfs, cdf_sizes, offsets))
+            while len(self._entries) > self._capacity:
+                self._entries.popitem(last=False)
+        return prepared

@@ -1,0 +1,273 @@
+"""GA-ANS ``warp_div`` backend for MI355X: the reference's WarpDivBackend
+surface on top of the wave64 HIP coder.
+
+Same public surface as ``src/fast_compressai/coders/warp_div.py:20-215``:
+``WarpDivBackend().encode(symbols, indexes, cdfs, cdf_sizes, offsets, *,
+p_ch) -> WarpDivPayload`` and ``.decode(payload, indexes, cdfs, cdf_sizes,
+offsets) -> int32 [B, N]``, with ``CoderInputError`` for bad inputs or
+payloads and ``CoderDependencyError`` for a missing library or device.
+
+Differences that follow from the new format:
+
+* ``format_id`` is ``"gaans-w64-v1"``; payloads of the reference's
+  ``warpans-v2`` format are rejected.
+* ``WarpDivPayload.chunk_ends`` (uint32 ``[B, K]``, exposed also under the
+  reference's name ``max_rounds``) holds each chunk's end offset in the
+  payload data, not a round count.
+* Index range, index content and table identity are checked on the device
+  (status word) instead of with host syncs and a SHA-256 of every index.
+  ``coding_fingerprint`` is a SHA-256 of the table digest and the shapes, so
+  it stays cheap to recompute on every decode.
+* ``channels=`` (keyword, optional) chunks over latent channels instead of
+  CDF tables, for GaussianConditional-style per-element indexes.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import struct
+from dataclasses import dataclass
+from typing import Sequence
+
+import torch
+
+from . import gaans
+from .capabilities import warp_div_capability
+from .errors import CoderDependencyError, CoderInputError
+from .tables import PreparedTables, TableCache
+
+FORMAT_ID = "gaans-w64-v1"
+FORMAT_VERSION = 1
+_HEADER_MAGIC = 0x31574147
+_FIXED_HEADER_BYTES = 64
+
+
+def header_bytes_for(batch: int, chunks: int) -> int:
+    return (_FIXED_HEADER_BYTES + 8 * batch * chunks + 15) // 16 * 16
+
+
+def coding_fingerprint(table_digest: int, batch: int, symbols_per_batch: int, channels: int,
+                       cdf_count: int) -> str:
+    """SHA-256 over the table digest and the coding shapes."""
+    text = (f"{FORMAT_ID}|tables={table_digest:016x}|B={batch}|N={symbols_per_batch}"
+            f"|C={channels}|M={cdf_count}")
+    return hashlib.sha256(text.encode("ascii")).hexdigest()
+
+
+@dataclass(frozen=True)
+class WarpDivPayload:
+    packed: torch.Tensor
+    chunk_ends: torch.Tensor
+    header_bytes: int
+    chunk_len: int
+    p_ch: int
+    batch: int
+    symbols_per_batch: int
+    cdf_count: int
+    coding_fingerprint: str | None = None
+    format_id: str = FORMAT_ID
+    format_version: int = FORMAT_VERSION
+    channels: int | None = None
+
+    def __post_init__(self) -> None:
+        if self.format_id != FORMAT_ID or self.format_version != FORMAT_VERSION:
+            raise CoderInputError("unsupported warp_div payload format")
+        if (not isinstance(self.packed, torch.Tensor) or self.packed.device.type != "cuda"
+                or self.packed.dtype != torch.uint8 or not self.packed.is_contiguous()):
+            raise CoderInputError("packed payload must be contiguous GPU uint8")
+        if (not isinstance(self.chunk_ends, torch.Tensor)
+                or self.chunk_ends.device != self.packed.device
+                or self.chunk_ends.dtype != torch.uint32 or not self.chunk_ends.is_contiguous()):
+            raise CoderInputError(
+                "chunk_ends must be contiguous GPU uint32 on the packed payload device")
+        if self.coding_fingerprint is not None and (
+            not isinstance(self.coding_fingerprint, str) or len(self.coding_fingerprint) != 64
+            or any(char not in "0123456789abcdef" for char in self.coding_fingerprint)
+        ):
+            raise CoderInputError("coding_fingerprint must be a SHA-256 hex digest")
+        ints = (self.header_bytes, self.chunk_len, self.p_ch, self.batch,
+                self.symbols_per_batch, self.cdf_count)
+        if any(type(v) is not int for v in ints) or min(ints) <= 0:
+            raise CoderInputError("warp_div metadata values must be positive integers")
+        channels = self.coded_channels
+        if type(channels) is not int or channels <= 0:
+            raise CoderInputError("warp_div channels must be a positive integer")
+        if self.p_ch > channels or self.symbols_per_batch % channels:
+            raise CoderInputError("warp_div payload P_ch/channel metadata is inconsistent")
+        expected_chunks = (channels + self.p_ch - 1) // self.p_ch
+        if tuple(self.chunk_ends.shape) != (self.batch, expected_chunks):
+            raise CoderInputError("warp_div chunk table shape does not match payload metadata")
+        if self.chunk_len != self.p_ch * (self.symbols_per_batch // channels):
+            raise CoderInputError("warp_div chunk_len does not match P_ch and symbol dimensions")
+        if self.header_bytes != header_bytes_for(self.batch, expected_chunks):
+            raise CoderInputError("warp_div header size does not match chunk metadata")
+        if self.header_bytes > self.packed.numel():
+            raise CoderInputError("warp_div header exceeds packed payload size")
+        if self.packed.numel() % 4:
+            raise CoderInputError("warp_div packed payload must be uint32 aligned")
+
+    @property
+    def coded_channels(self) -> int:
+        return self.cdf_count if self.channels is None else self.channels
+
+    @property
+    def max_rounds(self) -> torch.Tensor:
+        """The per-chunk table ``[B, K]`` under the reference's attribute name
+        (here: chunk end offsets, see ``chunk_ends``)."""
+        return self.chunk_ends
+
+    @property
+    def chunks(self) -> int:
+        return int(self.chunk_ends.shape[1])
+
+    def to_bytes(self) -> bytes:
+        """Host copy of the payload (header + chunk streams); the format is
+        self-describing, so ``from_bytes`` restores an equal payload."""
+        return self.packed.cpu().numpy().tobytes()
+
+    @classmethod
+    def from_bytes(cls, data: bytes, device: torch.device | str = "cuda",
+                   cdf_count: int | None = None) -> "WarpDivPayload":
+        """Rebuild a payload from ``to_bytes`` output (header fields
+        B, N, C, P, K, chunk_len, M, table digest and chunk offsets)."""
+        if len(data) < _FIXED_HEADER_BYTES:
+            raise CoderInputError("warp_div payload header is truncated")
+        words = struct.unpack_from("<16I", data, 0)
+        if words[0] != _HEADER_MAGIC or words[1] != FORMAT_VERSION:
+            raise CoderInputError("warp_div payload header has an unknown magic or version")
+        B, N, C, P, K, chunk_len, M = words[2:9]
+        if B <= 0 or K <= 0:
+            raise CoderInputError("warp_div payload header is inconsistent")
+        hb = header_bytes_for(B, K)
+        if len(data) < hb:
+            raise CoderInputError("warp_div payload header is truncated")
+        if cdf_count is not None and cdf_count != M:
+            raise CoderInputError("CDF count does not match payload metadata")
+        digest = words[10] | (words[11] << 32)
+        ends = torch.frombuffer(bytearray(data[64: 64 + 4 * B * K]), dtype=torch.uint8)
+        dev = torch.device(device)
+        packed = torch.frombuffer(bytearray(data), dtype=torch.uint8).to(dev)
+        return cls(packed=packed, chunk_ends=ends.to(dev).view(torch.uint32).view(B, K),
+                   header_bytes=hb, chunk_len=chunk_len, p_ch=P, batch=B,
+                   symbols_per_batch=N, cdf_count=M,
+                   coding_fingerprint=coding_fingerprint(digest, B, N, C, M),
+                   channels=None if C == M else C)
+
+
+class WarpDivBackend:
+    """MI355X GA-ANS coder behind the reference's ``warp_div`` surface."""
+
+    name = "warp_div"
+    format_id = FORMAT_ID
+    format_version = FORMAT_VERSION
+
+    def __init__(self) -> None:
+        capability = warp_div_capability()
+        if not capability.available:
+            raise CoderDependencyError(f"warp_div unavailable: {capability.reason}")
+        from . import _native
+
+        _native.lib()  # raises CoderDependencyError when it cannot be loaded
+        self._tables = TableCache()
+
+    def prepared_tables(self, cdfs: torch.Tensor, cdf_sizes: torch.Tensor,
+                        offsets: torch.Tensor) -> PreparedTables:
+        return self._tables.get(cdfs, cdf_sizes, offsets)
+
+    def encode(
+        self,
+        symbols: torch.Tensor,
+        indexes: torch.Tensor,
+        cdfs: torch.Tensor,
+        cdf_sizes: torch.Tensor,
+        offsets: torch.Tensor,
+        *,
+        p_ch: int,
+        channels: int | None = None,
+    ) -> WarpDivPayload:
+        C = _validate_inputs(symbols, indexes, cdfs, cdf_sizes, offsets, p_ch, channels)
+        tables = self.prepared_tables(cdfs, cdf_sizes, offsets)
+        B, N = int(symbols.shape[0]), int(symbols.shape[1])
+        enc = gaans.encode(tables, B, N, C, p_ch, symbols.device, symbols=symbols,
+                           indexes=indexes)
+        return WarpDivPayload(
+            packed=enc.packed,
+            chunk_ends=enc.chunk_ends,
+            header_bytes=enc.header_bytes,
+            chunk_len=enc.chunk_len,
+            p_ch=int(p_ch),
+            batch=B,
+            symbols_per_batch=N,
+            cdf_count=int(cdfs.shape[0]),
+            coding_fingerprint=coding_fingerprint(tables.digest, B, N, C, int(cdfs.shape[0])),
+            channels=None if channels is None else int(channels),
+        )
+
+    def decode(
+        self,
+        payload: WarpDivPayload,
+        indexes: torch.Tensor,
+        cdfs: torch.Tensor,
+        cdf_sizes: torch.Tensor,
+        offsets: torch.Tensor,
+    ) -> torch.Tensor:
+        if not isinstance(payload, WarpDivPayload):
+            raise CoderInputError("warp_div decode expects WarpDivPayload")
+        C = _validate_inputs(indexes, indexes, cdfs, cdf_sizes, offsets, payload.p_ch,
+                             payload.channels)
+        if tuple(indexes.shape) != (payload.batch, payload.symbols_per_batch):
+            raise CoderInputError("indexes shape does not match payload metadata")
+        if cdfs.shape[0] != payload.cdf_count or indexes.device != payload.packed.device:
+            raise CoderInputError("CDF count or GPU device does not match payload metadata")
+        tables = self.prepared_tables(cdfs, cdf_sizes, offsets)
+        B, N = payload.batch, payload.symbols_per_batch
+        if payload.coding_fingerprint is not None and payload.coding_fingerprint != \
+                coding_fingerprint(tables.digest, B, N, C, payload.cdf_count):
+            raise CoderInputError("coding tables or indexes do not match warp_div payload")
+        return gaans.decode(payload.packed, tables, B, N, C, payload.p_ch,
+                            payload.packed.device, indexes=indexes)
+
+
+def _validate_inputs(
+    symbols: torch.Tensor,
+    indexes: torch.Tensor,
+    cdfs: torch.Tensor,
+    cdf_sizes: torch.Tensor,
+    offsets: torch.Tensor,
+    p_ch: int,
+    channels: int | None = None,
+) -> int:
+    """Host-side checks of the reference (``warp_div.py:179-215``) without the
+    index min/max sync (index range is checked on the device).  Returns the
+    channel count used for chunking."""
+    if not isinstance(symbols, torch.Tensor) or not isinstance(indexes, torch.Tensor):
+        raise CoderInputError("symbols and indexes must be torch tensors")
+    tensors: Sequence[torch.Tensor] = (symbols, indexes, cdfs, cdf_sizes, offsets)
+    if any(not isinstance(value, torch.Tensor) for value in tensors):
+        raise CoderInputError("indexes, CDFs, CDF sizes, and offsets must be tensors")
+    if type(p_ch) is not int or p_ch <= 0:
+        raise CoderInputError("p_ch must be a positive integer")
+    if symbols.device.type != "cuda" or any(value.device != symbols.device for value in tensors):
+        raise CoderInputError("all coder inputs must be GPU tensors on the same device")
+    if any(value.dtype != torch.int32 for value in tensors):
+        raise CoderInputError("all warp_div input tensors must use torch.int32")
+    if any(not value.is_contiguous() for value in tensors):
+        raise CoderInputError("all warp_div input tensors must be contiguous")
+    if symbols.ndim != 2 or indexes.shape != symbols.shape:
+        raise CoderInputError("symbols and indexes must have matching [B, N] shape")
+    if cdfs.ndim != 2 or cdf_sizes.ndim != 1 or offsets.ndim != 1:
+        raise CoderInputError("CDF must be [M,L] and CDF sizes/offsets must be [M]")
+    if cdfs.shape[0] <= 0 or cdfs.shape[1] < 2:
+        raise CoderInputError("CDF table cannot be empty")
+    if cdf_sizes.numel() != cdfs.shape[0] or offsets.numel() != cdfs.shape[0]:
+        raise CoderInputError("CDF, CDF sizes, and offsets must have the same table count")
+    if symbols.shape[0] <= 0 or symbols.shape[1] <= 0:
+        raise CoderInputError("empty symbols are not supported by this WarpANS format")
+    C = int(cdfs.shape[0]) if channels is None else channels
+    if type(C) is not int or C <= 0:
+        raise CoderInputError("channels must be a positive integer")
+    if symbols.shape[1] % C != 0:
+        raise CoderInputError("symbols per batch must be divisible by the channel count")
+    if p_ch > C:
+        raise CoderInputError("p_ch cannot exceed the number of CDF channels")
+    return C

@@ -1,0 +1,158 @@
+/*
+ * gaans_w64.h -- C ABI of the MI355X (gfx950) GA-ANS latent coder.
+ *
+ * Library: fast-compressai_amd/fast_compressai/coders/lib/libgaans_w64.so
+ *
+ * The library replaces the reference's pybind11 module
+ * fast_compressai.coders._warp_div (src/fast_compressai/coders/cuda/ans_gpu.cpp:25-30):
+ *   encode_warp_div(symbols, indexes, cdfs, cdf_sizes, offsets, P)
+ *       -> gaans_encode_symbols + gaans_encode_pack   (+ gaans_encode_latents,
+ *          which also fuses CompressAI's quantize, reference
+ *          src/fast_compressai/coders/factorized.py:46-49)
+ *   decode_warp_div(packed, max_rounds, header_bytes, chunk_len, P, indexes,
+ *                   cdfs, cdf_sizes, offsets)
+ *       -> gaans_decode_symbols                       (+ gaans_decode_latents,
+ *          which also fuses dequantize, reference factorized.py:99-101)
+ * The table layout step (gaans_tables_prepare) replaces the per-call reads of
+ * the padded [M, Lmax] int32 CDF tensor and the 512 KB magic table
+ * (reference warp_ans_kernel_v2.cu:230-247).
+ *
+ * Conventions
+ *  - Every function returns 0 (GAANS_OK) or a positive GAANS_E* code and
+ *    leaves a message for gaans_last_error() (thread-local).  No C++
+ *    exception crosses this boundary.
+ *  - Pointers named *_dev are device pointers; the library never allocates
+ *    device memory: the caller passes every buffer, sized with
+ *    gaans_get_layout / gaans_tables_bytes.
+ *  - `stream` is a hipStream_t (NULL = the legacy default stream).  Device
+ *    functions only enqueue work on that stream; none of them synchronises.
+ *  - Kernel-detected problems (bad symbols, corrupt payloads) are reported as
+ *    GAANS_ST_* bits in a device status word that the caller reads after the
+ *    stream has finished.
+ *
+ * Payload format "gaans-w64-v1": documented in DESIGN.md and in
+ * oracle/gaans_oracle.c (the CPU definition of the bytes).
+ */
+#ifndef GAANS_W64_H
+#define GAANS_W64_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GAANS_ABI_VERSION 1
+
+/* return codes */
+#define GAANS_OK 0
+#define GAANS_EINVAL 1  /* bad argument, shape or buffer size */
+#define GAANS_ETABLE 2  /* CDF tables are not valid 16-bit quantized CDFs */
+#define GAANS_EHIP 3    /* a HIP runtime call failed */
+
+/* device status bits (encode: info word 1; decode: the status word) */
+#define GAANS_ST_RANGE 0x01u     /* symbol cannot be coded (escape >= 2^32, non-finite latent) */
+#define GAANS_ST_INDEX 0x02u     /* table index out of range */
+#define GAANS_ST_HEADER 0x04u    /* payload header does not match the call */
+#define GAANS_ST_TABLES 0x08u    /* payload made with other tables, or bad table blob */
+#define GAANS_ST_CORRUPT 0x10u   /* chunk offsets or rANS stream inconsistent */
+#define GAANS_ST_INDEXHASH 0x20u /* payload made with other indexes */
+#define GAANS_ST_SIZE 0x40u      /* payload would exceed the 4 GiB format limit */
+
+/* Shape of one coding call (pure host arithmetic, see gaans_get_layout). */
+typedef struct gaans_layout {
+  int64_t B, N, C, P;     /* batch rows, symbols per row, channels, channels per chunk */
+  int64_t HW, K, chunk_len, BK;
+  int64_t header_bytes;   /* payload header size (multiple of 16) */
+  int64_t max_payload_bytes;
+  int64_t cap_words;      /* staging words per chunk (worst case) */
+  int64_t workspace_bytes;
+  /* byte offsets inside the encode workspace */
+  int64_t ws_chunk_words, ws_chunk_status, ws_index_hash, ws_end_off, ws_info,
+      ws_states, ws_words;
+} gaans_layout;
+
+int gaans_abi_version(void);
+const char* gaans_last_error(void);
+
+/* Chunking and buffer sizes for B rows of N symbols, C channels, P per chunk.
+ * Requires B, N, C, P >= 1, N % C == 0, P <= C. */
+int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, gaans_layout* out);
+
+/* ---- table upload (host memory) ----------------------------------------- */
+
+/* Bytes of the prepared table blob for M tables (cdf_sizes in host memory). */
+int gaans_tables_bytes(const int32_t* cdf_sizes, int32_t M, int32_t Lmax, int64_t* bytes);
+
+/* Validate CompressAI-style tables (cdfs [M, Lmax] int32 row-major, rows
+ * zero-padded beyond cdf_sizes[t]; cdf[0] = 0, cdf[S-1] = 65536, strictly
+ * increasing) and lay them out for the kernels: per-table metadata, packed
+ * (start, freq-1) entries and a 256-bucket decode lookup.  The caller copies
+ * `out` to device memory unchanged.  *digest receives the table digest that
+ * payloads record.  Replaces the reference's use of the raw tensors at
+ * src/fast_compressai/coders/factorized.py:23-31. */
+int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes,
+                         const int32_t* offsets, int32_t M, int32_t Lmax,
+                         void* out, int64_t out_bytes, uint64_t* digest);
+
+/* ---- encode ------------------------------------------------------------- */
+
+/* Stage 1: code every chunk into `workspace_dev` (layout->workspace_bytes)
+ * and write the chunk offsets plus info = {u64 payload bytes incl. header,
+ * u64 status} at workspace + layout->ws_info.  `indexes_dev` may be NULL:
+ * then position i of a row uses table i / HW (CompressAI EntropyBottleneck
+ * indexes).  Reference: encode_with_indexes_warp_v2_cuda,
+ * src/fast_compressai/coders/cuda/warp_ans_kernel_v2.cu:183-273. */
+int gaans_encode_symbols(void* stream, const int32_t* symbols_dev,
+                         const int32_t* indexes_dev, const void* tables_dev,
+                         int64_t tables_bytes, int32_t M, int64_t B, int64_t N,
+                         int64_t C, int64_t P, void* workspace_dev,
+                         int64_t workspace_bytes);
+
+/* Stage 1 with CompressAI's quantize fused in: symbol = int32(rint(y -
+ * medians[c])) for latents y [B, C, HW] fp32 and per-channel medians [C].
+ * Reference: FactorizedWarpDivCodec.compress, factorized.py:46-59. */
+int gaans_encode_latents(void* stream, const float* y_dev, const float* medians_dev,
+                         const int32_t* indexes_dev, const void* tables_dev,
+                         int64_t tables_bytes, int32_t M, int64_t B, int64_t N,
+                         int64_t C, int64_t P, void* workspace_dev,
+                         int64_t workspace_bytes);
+
+/* Stage 2: after the caller has read info[0] (payload bytes) from the
+ * workspace, write the payload (header + chunks) to out_dev, which holds at
+ * least that many bytes.  Reference: write_warp_tight_header_kernel and
+ * warp_pack_tight_payload_kernel, warp_ans_kernel_v2.cu:274-296. */
+int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace_bytes,
+                      const void* tables_dev, int64_t tables_bytes, int32_t M,
+                      int64_t B, int64_t N, int64_t C, int64_t P, uint8_t* out_dev,
+                      int64_t out_bytes);
+
+/* ---- decode ------------------------------------------------------------- */
+
+/* Decode a payload into int32 symbols [B, N].  `status_dev` is one u32 that
+ * the caller zeroes beforehand; kernels OR GAANS_ST_* bits into it.
+ * Reference: decode_with_indexes_warp_cuda, warp_ans_kernel.cu:477-544. */
+int gaans_decode_symbols(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
+                         const int32_t* indexes_dev, const void* tables_dev,
+                         int64_t tables_bytes, int32_t M, int64_t B, int64_t N,
+                         int64_t C, int64_t P, int32_t* out_dev, uint32_t* status_dev);
+
+/* Decode with CompressAI's dequantize fused in: y_hat = fp32(symbol) +
+ * medians[c], written as [B, C, HW] fp32. */
+int gaans_decode_latents(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
+                         const int32_t* indexes_dev, const void* tables_dev,
+                         int64_t tables_bytes, int32_t M, const float* medians_dev,
+                         int64_t B, int64_t N, int64_t C, int64_t P, float* y_hat_dev,
+                         uint32_t* status_dev);
+
+/* ---- host self test ------------------------------------------------------- */
+
+/* Checks the host-computed division constants the kernels use; returns 0
+ * when every check passes (no GPU needed). */
+int gaans_host_selftest(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

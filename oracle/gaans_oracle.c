@@ -1,0 +1,650 @@
+/*
+ * CPU oracle for the GA-ANS latent-coding path.  TEST INFRASTRUCTURE ONLY
+ * (see gaans_oracle.h): the product path never links or calls this file.
+ *
+ * ===========================================================================
+ * The wave64 GA-ANS payload format, "gaans-w64-v1"
+ * ===========================================================================
+ * Coding parameters: 16-bit CDF precision; one 32-bit rANS state per lane,
+ * x in [2^16, 2^32), initial state 2^16; 16-bit renormalisation words;
+ * 4-bit bypass escapes; 64 lanes per chunk.
+ *
+ * Chunking.  A batch row holds N symbols, channel-major: C channels of
+ * HW = N / C positions.  P channels form one chunk, K = ceil(C / P) chunks per
+ * row, chunk_len = P * HW.  Chunk g = b * K + k covers positions
+ * [k*chunk_len, min((k+1)*chunk_len, N)) of row b; len = its symbol count.
+ * A = min(64, len) lanes are active; lane l owns positions l + 64 t (t >= 0)
+ * of the chunk, so the 64 lanes of one step read 64 consecutive positions.
+ *
+ * Symbol mapping (CompressAI's escape scheme; reference
+ * warp_ans_kernel_v2.cu:139-169).  With table tb = index of the position,
+ * S = cdf_sizes[tb], maxv = S - 2, v = symbol - offsets[tb] (64-bit):
+ *   v <  0    -> escape, raw = -2 v - 1, v = maxv
+ *   v >= maxv -> escape, raw = 2 (v - maxv), v = maxv
+ * raw must be < 2^32.  Escape ops: n = raw ? msb(raw) / 4 + 1 : 0 nibbles.
+ * Ops of one symbol in DECODE order:
+ *   op 0       : main  (start = cdf[v], freq = cdf[v+1] - cdf[v])
+ *   op 1       : bits(n)                  (escapes only)
+ *   op 2 + j   : bits((raw >> 4 j) & 15)  (escapes only, j = 0 .. n-1)
+ * Encoder arithmetic (x is u32):
+ *   main : if (x >> 16) >= freq: emit x & 0xffff, x >>= 16;
+ *          x = (x / freq) << 16 | ... = ((x / freq) << 16) + x % freq + start
+ *   bits : if x >= 2^28:        emit x & 0xffff, x >>= 16;
+ *          x = (x << 4) | val
+ * Decoder arithmetic:
+ *   main : cum = x & 0xffff; v = the symbol with cdf[v] <= cum < cdf[v+1];
+ *          x = freq * (x >> 16) + cum - start
+ *   bits : val = x & 15; x >>= 4
+ *   then : if x < 2^16: x = (x << 16) | next word
+ *
+ * Word order.  The encoder walks steps t = T-1 .. 0 and, inside a step,
+ * sub-rounds d = Mt-1 .. 0 (Mt = largest op count of any lane at step t);
+ * in sub-round d every active lane that has an op d runs it.  The words
+ * emitted in one sub-round form a group, ordered by lane index; each group
+ * is PREPENDED to the chunk's word stream.  The decoder therefore reads the
+ * stream forwards: steps t = 0 .. T-1, sub-rounds d = 0, 1, ..., and in each
+ * sub-round the lanes that need a refill take the next words in lane order.
+ *
+ * Chunk bytes: A final states (u32 LE, lane order), the word stream (u16 LE),
+ * one zero u16 if the word count is odd.  After decoding, every active lane
+ * is back at 2^16 and the whole stream (pad excluded) has been consumed.
+ *
+ * Header (u32 LE words):
+ *   0 magic 0x31574147 ("GAW1")   1 version (1)     2 B    3 N
+ *   4 C    5 P    6 K    7 chunk_len    8 M (table count)
+ *   9 params 0x00041040 (lanes 64 | precision 16 << 8 | bypass 4 << 16)
+ *   10,11 table digest (FNV-1a 64, low word first)   12..15 zero
+ *   then B*K u32 chunk end offsets (bytes, relative to the data start),
+ *   then B*K u32 index hashes; zero padding to a multiple of 16 bytes.
+ * Data start = header bytes; chunk g spans [end[g-1], end[g]) of the data.
+ * Index hash of a chunk: sum over its positions p (0-based in the chunk) of
+ *   ((tb + 1) XOR (p * 0x9E3779B9)) mod 2^32.
+ * Table digest: FNV-1a 64 over the little-endian bytes of u32 M, then for
+ * every table: u32 S, i32 offset, u32 cdf[0..S-1].
+ * ===========================================================================
+ */
+#include "gaans_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- shared helpers ------------------------------------------------------ */
+
+static int check_tables(const int32_t* cdfs, int32_t M, int32_t Lmax,
+                        const int32_t* sizes) {
+  if (M <= 0 || Lmax < 2) return GAANS_REF_EINVAL;
+  for (int32_t t = 0; t < M; ++t) {
+    int32_t S = sizes[t];
+    const int32_t* c = cdfs + (int64_t)t * Lmax;
+    if (S < 2 || S > Lmax) return GAANS_REF_ETABLE;
+    if (c[0] != 0 || c[S - 1] != 65536) return GAANS_REF_ETABLE;
+    for (int32_t j = 0; j + 1 < S; ++j)
+      if (c[j + 1] <= c[j]) return GAANS_REF_ETABLE;
+  }
+  return GAANS_REF_OK;
+}
+
+/* escape mapping; returns 0 ok, GAANS_REF_ERANGE if raw >= 2^32 */
+static int map_symbol(int32_t sym, int32_t S, int32_t offset, int32_t* v_out,
+                      int* esc, uint32_t* raw) {
+  int64_t maxv = (int64_t)S - 2;
+  int64_t v = (int64_t)sym - (int64_t)offset;
+  int64_t r = 0;
+  *esc = 0;
+  if (v < 0) {
+    r = -2 * v - 1;
+    v = maxv;
+    *esc = 1;
+  } else if (v >= maxv) {
+    r = 2 * (v - maxv);
+    v = maxv;
+    *esc = 1;
+  }
+  if (r >= ((int64_t)1 << 32)) return GAANS_REF_ERANGE;
+  *v_out = (int32_t)v;
+  *raw = (uint32_t)r;
+  return GAANS_REF_OK;
+}
+
+static int nibble_count(uint32_t raw) {
+  int n = 0;
+  while (n < 8 && (((uint64_t)raw) >> (4 * n)) != 0) ++n;
+  return n;
+}
+
+/* symbol v of table c (S entries) containing cum; plain linear scan */
+static int32_t find_symbol(const int32_t* c, int32_t S, uint32_t cum) {
+  int32_t v = 0;
+  while (v + 1 < S - 1 && (uint32_t)c[v + 1] <= cum) ++v;
+  return v;
+}
+
+static int unmap_escape(uint32_t raw, int32_t S, int32_t offset, int32_t* sym) {
+  int64_t maxv = (int64_t)S - 2;
+  int64_t v = (raw & 1u) ? -(int64_t)(raw >> 1) - 1 : (int64_t)(raw >> 1) + maxv;
+  int64_t s = v + offset;
+  if (s < INT32_MIN || s > INT32_MAX) return GAANS_REF_ECORRUPT;
+  *sym = (int32_t)s;
+  return GAANS_REF_OK;
+}
+
+/* ===========================================================================
+ * 1. CompressAI-equivalent Rans64 (64-bit state, L = 2^31, 32-bit words)
+ * ======================================================================== */
+
+#define R64_L ((uint64_t)1 << 31)
+
+typedef struct {
+  uint32_t start, freq; /* freq may be 65536 for a one-entry alphabet */
+  int bypass;           /* 1: 4-bit raw value in start */
+} r64_op;
+
+/* reference rans64_gpu.cuh:21-32 */
+static void r64_put(uint64_t* r, uint32_t** pptr, uint32_t start, uint32_t freq) {
+  uint64_t x = *r;
+  uint64_t x_max = ((R64_L >> 16) << 32) * (uint64_t)freq;
+  if (x >= x_max) {
+    *pptr -= 1;
+    **pptr = (uint32_t)x;
+    x >>= 32;
+  }
+  *r = ((x / freq) << 16) + (x % freq) + start;
+}
+
+/* reference rans64_gpu.cuh:42-55 with nbits = 4 */
+static void r64_put_bits(uint64_t* r, uint32_t** pptr, uint32_t val) {
+  uint64_t x = *r;
+  uint64_t x_max = ((R64_L >> 16) << 32) * (uint64_t)(1u << 12);
+  if (x >= x_max) {
+    *pptr -= 1;
+    **pptr = (uint32_t)x;
+    x >>= 32;
+  }
+  *r = (x << 4) | val;
+}
+
+int rans64_ref_encode(const int32_t* symbols, const int32_t* indexes, int64_t n,
+                      const int32_t* cdfs, int32_t M, int32_t Lmax,
+                      const int32_t* cdf_sizes, const int32_t* offsets,
+                      uint32_t* out_words, int64_t cap_words, int64_t* n_words) {
+  int rc = check_tables(cdfs, M, Lmax, cdf_sizes);
+  if (rc) return rc;
+  if (n < 0) return GAANS_REF_EINVAL;
+  /* push ops in CompressAI order (main, count nibbles, raw nibbles j=0..) */
+  int64_t cap_ops = n * 11 + 1;
+  r64_op* ops = (r64_op*)malloc(sizeof(r64_op) * (size_t)cap_ops);
+  if (!ops) return GAANS_REF_ESPACE;
+  int64_t nops = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    int32_t tb = indexes[i];
+    if (tb < 0 || tb >= M) { free(ops); return GAANS_REF_EINDEX; }
+    const int32_t* c = cdfs + (int64_t)tb * Lmax;
+    int32_t v; int esc; uint32_t raw;
+    rc = map_symbol(symbols[i], cdf_sizes[tb], offsets[tb], &v, &esc, &raw);
+    if (rc) { free(ops); return rc; }
+    ops[nops].start = (uint32_t)c[v];
+    ops[nops].freq = (uint32_t)(c[v + 1] - c[v]);
+    ops[nops].bypass = 0;
+    ++nops;
+    if (esc) {
+      int nb = nibble_count(raw);
+      int32_t val = nb;
+      while (val >= 15) {
+        ops[nops].start = 15; ops[nops].freq = 16; ops[nops].bypass = 1; ++nops;
+        val -= 15;
+      }
+      ops[nops].start = (uint32_t)val; ops[nops].freq = 16; ops[nops].bypass = 1; ++nops;
+      for (int j = 0; j < nb; ++j) {
+        ops[nops].start = (raw >> (4 * j)) & 15u; ops[nops].freq = 16; ops[nops].bypass = 1;
+        ++nops;
+      }
+    }
+  }
+  /* BufferedRansEncoder::flush: encode in reverse into a backward buffer */
+  int64_t cap = nops * 2 + 2; /* <= 1 word per op + 2 flush words */
+  uint32_t* buf = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)cap);
+  if (!buf) { free(ops); return GAANS_REF_ESPACE; }
+  uint32_t* end = buf + cap;
+  uint32_t* ptr = end;
+  uint64_t x = R64_L;
+  for (int64_t k = nops - 1; k >= 0; --k) {
+    if (ops[k].bypass) r64_put_bits(&x, &ptr, ops[k].start);
+    else r64_put(&x, &ptr, ops[k].start, ops[k].freq);
+  }
+  ptr -= 2; /* rans64_gpu.cuh:34-39 */
+  ptr[0] = (uint32_t)(x >> 0);
+  ptr[1] = (uint32_t)(x >> 32);
+  int64_t used = end - ptr;
+  free(ops);
+  if (used > cap_words) { free(buf); return GAANS_REF_ESPACE; }
+  memcpy(out_words, ptr, sizeof(uint32_t) * (size_t)used);
+  *n_words = used;
+  free(buf);
+  return GAANS_REF_OK;
+}
+
+typedef struct {
+  uint64_t x;
+  const uint32_t* p;
+  const uint32_t* end;
+  int bad;
+} r64_dec;
+
+static uint32_t r64_next(r64_dec* d) {
+  if (d->p >= d->end) { d->bad = 1; return 0; }
+  return *d->p++;
+}
+
+/* reference rans64dec_gpu.cuh:35-48 with n_bits = 4 */
+static uint32_t r64_get_bits(r64_dec* d) {
+  uint32_t val = (uint32_t)(d->x & 15u);
+  d->x >>= 4;
+  if (d->x < R64_L) d->x = (d->x << 32) | (uint64_t)r64_next(d);
+  return val;
+}
+
+int rans64_ref_decode(const uint32_t* words, int64_t n_words,
+                      const int32_t* indexes, int64_t n,
+                      const int32_t* cdfs, int32_t M, int32_t Lmax,
+                      const int32_t* cdf_sizes, const int32_t* offsets,
+                      int32_t* out_symbols) {
+  int rc = check_tables(cdfs, M, Lmax, cdf_sizes);
+  if (rc) return rc;
+  if (n == 0) return GAANS_REF_OK;
+  if (n_words < 2) return GAANS_REF_ECORRUPT;
+  r64_dec d;
+  d.x = (uint64_t)words[0] | ((uint64_t)words[1] << 32); /* rans64dec_gpu.cuh:8-14 */
+  d.p = words + 2;
+  d.end = words + n_words;
+  d.bad = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    int32_t tb = indexes[i];
+    if (tb < 0 || tb >= M) return GAANS_REF_EINDEX;
+    const int32_t* c = cdfs + (int64_t)tb * Lmax;
+    int32_t S = cdf_sizes[tb];
+    uint32_t cum = (uint32_t)(d.x & 0xffffu);
+    int32_t v = find_symbol(c, S, cum);
+    uint32_t start = (uint32_t)c[v], freq = (uint32_t)(c[v + 1] - c[v]);
+    /* rans64dec_gpu.cuh:20-32 */
+    d.x = (uint64_t)freq * (d.x >> 16) + (d.x & 0xffffu) - start;
+    if (d.x < R64_L) d.x = (d.x << 32) | (uint64_t)r64_next(&d);
+    if (v == S - 2) {
+      int32_t val = (int32_t)r64_get_bits(&d);
+      int32_t nb = val;
+      while (val == 15 && !d.bad) {
+        val = (int32_t)r64_get_bits(&d);
+        nb += val;
+      }
+      if (nb > 8) return GAANS_REF_ECORRUPT;
+      uint32_t raw = 0;
+      for (int j = 0; j < nb; ++j) raw |= r64_get_bits(&d) << (4 * j);
+      rc = unmap_escape(raw, S, offsets[tb], &out_symbols[i]);
+      if (rc) return rc;
+    } else {
+      out_symbols[i] = v + offsets[tb];
+    }
+    if (d.bad) return GAANS_REF_ECORRUPT;
+  }
+  return GAANS_REF_OK;
+}
+
+/* ===========================================================================
+ * 2. wave64 GA-ANS format
+ * ======================================================================== */
+
+#define W_LANES 64
+#define W_L ((uint32_t)1 << 16)
+#define W_MAGIC 0x31574147u
+#define W_VERSION 1u
+#define W_PARAMS 0x00041040u
+#define W_FIXED_WORDS 16
+
+typedef struct {
+  int32_t K, chunk_len, HW;
+  int64_t BK, header_bytes;
+} w_layout;
+
+static int w_layout_of(int32_t B, int32_t N, int32_t C, int32_t P, w_layout* L) {
+  if (B <= 0 || N <= 0 || C <= 0 || P <= 0 || P > C || N % C != 0)
+    return GAANS_REF_EINVAL;
+  L->HW = N / C;
+  L->K = (C + P - 1) / P;
+  if ((int64_t)P * L->HW > INT32_MAX) return GAANS_REF_EINVAL;
+  L->chunk_len = P * L->HW;
+  L->BK = (int64_t)B * L->K;
+  L->header_bytes = ((4 * W_FIXED_WORDS + 8 * L->BK) + 15) / 16 * 16;
+  return GAANS_REF_OK;
+}
+
+int64_t gaans_ref_max_payload_bytes(int32_t B, int32_t N, int32_t C, int32_t P) {
+  w_layout L;
+  if (w_layout_of(B, N, C, P, &L)) return -1;
+  /* per symbol at most 10 ops of one word; per chunk 64 states + pad */
+  return L.header_bytes + (int64_t)B * N * 20 + L.BK * (4 * W_LANES + 4);
+}
+
+static uint64_t fnv_bytes(uint64_t h, const void* p, size_t n) {
+  const uint8_t* b = (const uint8_t*)p;
+  for (size_t i = 0; i < n; ++i) {
+    h ^= b[i];
+    h *= 0x100000001b3ull;
+  }
+  return h;
+}
+
+static uint64_t fnv_u32(uint64_t h, uint32_t v) {
+  uint8_t b[4] = {(uint8_t)v, (uint8_t)(v >> 8), (uint8_t)(v >> 16), (uint8_t)(v >> 24)};
+  return fnv_bytes(h, b, 4);
+}
+
+uint64_t gaans_ref_table_digest(const int32_t* cdfs, int32_t M, int32_t Lmax,
+                                const int32_t* cdf_sizes, const int32_t* offsets) {
+  uint64_t h = 0xcbf29ce484222325ull;
+  h = fnv_u32(h, (uint32_t)M);
+  for (int32_t t = 0; t < M; ++t) {
+    h = fnv_u32(h, (uint32_t)cdf_sizes[t]);
+    h = fnv_u32(h, (uint32_t)offsets[t]);
+    for (int32_t j = 0; j < cdf_sizes[t]; ++j)
+      h = fnv_u32(h, (uint32_t)cdfs[(int64_t)t * Lmax + j]);
+  }
+  return h;
+}
+
+static void put_u32(uint8_t* p, uint32_t v) {
+  p[0] = (uint8_t)v; p[1] = (uint8_t)(v >> 8); p[2] = (uint8_t)(v >> 16); p[3] = (uint8_t)(v >> 24);
+}
+static uint32_t get_u32(const uint8_t* p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+typedef struct {
+  int active;
+  int nops;          /* ops in decode order: 1 (main) or n + 2 */
+  uint32_t start, freq;
+  uint32_t raw;
+  int n;
+} w_sym;
+
+/* value carried by op d of symbol s (bits ops only) */
+static uint32_t w_bits_val(const w_sym* s, int d) {
+  if (d == 1) return (uint32_t)s->n;
+  return (s->raw >> (4 * (d - 2))) & 15u;
+}
+
+static int w_encode_chunk(const int32_t* sym, const int32_t* idx_row, int64_t start,
+                          int32_t len, int32_t HW, const int32_t* cdfs, int32_t M,
+                          int32_t Lmax, const int32_t* sizes, const int32_t* offsets,
+                          uint8_t** out, int64_t* out_bytes, uint32_t* hash_out) {
+  int A = len < W_LANES ? len : W_LANES;
+  int T = (len + W_LANES - 1) / W_LANES;
+  int64_t cap = (int64_t)len * 10 + 2;
+  uint16_t* buf = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)cap);
+  if (!buf) return GAANS_REF_ESPACE;
+  int64_t wp = cap;
+  uint32_t x[W_LANES];
+  w_sym s[W_LANES];
+  uint32_t hash = 0;
+  for (int l = 0; l < W_LANES; ++l) x[l] = W_L;
+  for (int t = T - 1; t >= 0; --t) {
+    int Mt = 0;
+    for (int l = 0; l < W_LANES; ++l) {
+      int64_t p = l + (int64_t)W_LANES * t;
+      s[l].active = p < len;
+      s[l].nops = 0;
+      if (!s[l].active) continue;
+      int64_t i = start + p;
+      int32_t tb = idx_row ? idx_row[i] : (int32_t)(i / HW);
+      if (tb < 0 || tb >= M) { free(buf); return GAANS_REF_EINDEX; }
+      hash += (uint32_t)(tb + 1) ^ ((uint32_t)p * 0x9E3779B9u);
+      const int32_t* c = cdfs + (int64_t)tb * Lmax;
+      int32_t v; int esc; uint32_t raw;
+      int rc = map_symbol(sym[i], sizes[tb], offsets[tb], &v, &esc, &raw);
+      if (rc) { free(buf); return rc; }
+      s[l].start = (uint32_t)c[v];
+      s[l].freq = (uint32_t)(c[v + 1] - c[v]);
+      s[l].raw = raw;
+      s[l].n = esc ? nibble_count(raw) : 0;
+      s[l].nops = esc ? s[l].n + 2 : 1;
+      if (s[l].nops > Mt) Mt = s[l].nops;
+    }
+    for (int d = Mt - 1; d >= 0; --d) {
+      int emit[W_LANES];
+      int cnt = 0;
+      for (int l = 0; l < W_LANES; ++l) {
+        emit[l] = 0;
+        if (!s[l].active || d >= s[l].nops) continue;
+        if (d == 0) emit[l] = (x[l] >> 16) >= s[l].freq;
+        else emit[l] = x[l] >= ((uint32_t)1 << 28);
+        cnt += emit[l];
+      }
+      wp -= cnt;
+      int64_t r = wp;
+      for (int l = 0; l < W_LANES; ++l) {
+        if (!s[l].active || d >= s[l].nops) continue;
+        if (emit[l]) {
+          buf[r++] = (uint16_t)(x[l] & 0xffffu);
+          x[l] >>= 16;
+        }
+        if (d == 0) {
+          uint32_t f = s[l].freq;
+          x[l] = ((x[l] / f) << 16) + (x[l] % f) + s[l].start;
+        } else {
+          x[l] = (x[l] << 4) | w_bits_val(&s[l], d);
+        }
+      }
+    }
+  }
+  int64_t W = cap - wp;
+  int64_t bytes = 4 * (int64_t)A + 2 * W + ((W & 1) ? 2 : 0);
+  uint8_t* o = (uint8_t*)calloc((size_t)bytes, 1);
+  if (!o) { free(buf); return GAANS_REF_ESPACE; }
+  for (int l = 0; l < A; ++l) put_u32(o + 4 * l, x[l]);
+  for (int64_t k = 0; k < W; ++k) {
+    o[4 * A + 2 * k] = (uint8_t)buf[wp + k];
+    o[4 * A + 2 * k + 1] = (uint8_t)(buf[wp + k] >> 8);
+  }
+  free(buf);
+  *out = o;
+  *out_bytes = bytes;
+  *hash_out = hash;
+  return GAANS_REF_OK;
+}
+
+int gaans_ref_encode(const int32_t* symbols, const int32_t* indexes,
+                     int32_t B, int32_t N, int32_t C, int32_t P,
+                     const int32_t* cdfs, int32_t M, int32_t Lmax,
+                     const int32_t* cdf_sizes, const int32_t* offsets,
+                     uint8_t* out, int64_t out_cap, int64_t* out_len) {
+  w_layout L;
+  int rc = w_layout_of(B, N, C, P, &L);
+  if (rc) return rc;
+  rc = check_tables(cdfs, M, Lmax, cdf_sizes);
+  if (rc) return rc;
+  uint8_t** chunks = (uint8_t**)calloc((size_t)L.BK, sizeof(uint8_t*));
+  int64_t* cbytes = (int64_t*)calloc((size_t)L.BK, sizeof(int64_t));
+  uint32_t* hashes = (uint32_t*)calloc((size_t)L.BK, sizeof(uint32_t));
+  if (!chunks || !cbytes || !hashes) { rc = GAANS_REF_ESPACE; goto done; }
+  for (int64_t g = 0; g < L.BK; ++g) {
+    int64_t b = g / L.K, k = g % L.K;
+    int64_t start = k * (int64_t)L.chunk_len;
+    int64_t end = start + L.chunk_len < N ? start + L.chunk_len : N;
+    rc = w_encode_chunk(symbols + b * (int64_t)N, indexes ? indexes + b * (int64_t)N : NULL,
+                        start, (int32_t)(end - start), L.HW, cdfs, M, Lmax, cdf_sizes,
+                        offsets, &chunks[g], &cbytes[g], &hashes[g]);
+    if (rc) goto done;
+  }
+  {
+    int64_t total = L.header_bytes;
+    for (int64_t g = 0; g < L.BK; ++g) total += cbytes[g];
+    if (total - L.header_bytes > (int64_t)UINT32_MAX) { rc = GAANS_REF_ESPACE; goto done; }
+    if (total > out_cap) { rc = GAANS_REF_ESPACE; goto done; }
+    memset(out, 0, (size_t)L.header_bytes);
+    uint64_t digest = gaans_ref_table_digest(cdfs, M, Lmax, cdf_sizes, offsets);
+    uint32_t hw[W_FIXED_WORDS] = {W_MAGIC, W_VERSION, (uint32_t)B, (uint32_t)N,
+                                  (uint32_t)C, (uint32_t)P, (uint32_t)L.K,
+                                  (uint32_t)L.chunk_len, (uint32_t)M, W_PARAMS,
+                                  (uint32_t)digest, (uint32_t)(digest >> 32), 0, 0, 0, 0};
+    for (int w = 0; w < W_FIXED_WORDS; ++w) put_u32(out + 4 * w, hw[w]);
+    int64_t pos = 0;
+    for (int64_t g = 0; g < L.BK; ++g) {
+      memcpy(out + L.header_bytes + pos, chunks[g], (size_t)cbytes[g]);
+      pos += cbytes[g];
+      put_u32(out + 4 * W_FIXED_WORDS + 4 * g, (uint32_t)pos);
+      put_u32(out + 4 * W_FIXED_WORDS + 4 * L.BK + 4 * g, hashes[g]);
+    }
+    *out_len = total;
+  }
+done:
+  if (chunks)
+    for (int64_t g = 0; g < L.BK; ++g) free(chunks[g]);
+  free(chunks);
+  free(cbytes);
+  free(hashes);
+  return rc;
+}
+
+int gaans_ref_decode(const uint8_t* payload, int64_t payload_len,
+                     const int32_t* indexes,
+                     int32_t B, int32_t N, int32_t C, int32_t P,
+                     const int32_t* cdfs, int32_t M, int32_t Lmax,
+                     const int32_t* cdf_sizes, const int32_t* offsets,
+                     int32_t* out_symbols) {
+  w_layout L;
+  int rc = w_layout_of(B, N, C, P, &L);
+  if (rc) return rc;
+  rc = check_tables(cdfs, M, Lmax, cdf_sizes);
+  if (rc) return rc;
+  if (payload_len < L.header_bytes) return GAANS_REF_ECORRUPT;
+  uint64_t digest = gaans_ref_table_digest(cdfs, M, Lmax, cdf_sizes, offsets);
+  uint32_t want[12] = {W_MAGIC, W_VERSION, (uint32_t)B, (uint32_t)N, (uint32_t)C,
+                       (uint32_t)P, (uint32_t)L.K, (uint32_t)L.chunk_len, (uint32_t)M,
+                       W_PARAMS, (uint32_t)digest, (uint32_t)(digest >> 32)};
+  for (int w = 0; w < 10; ++w)
+    if (get_u32(payload + 4 * w) != want[w]) return GAANS_REF_ECORRUPT;
+  for (int w = 10; w < 12; ++w)
+    if (get_u32(payload + 4 * w) != want[w]) return GAANS_REF_EMISMATCH;
+  const uint8_t* data = payload + L.header_bytes;
+  int64_t data_len = payload_len - L.header_bytes;
+  uint32_t prev = 0;
+  for (int64_t g = 0; g < L.BK; ++g) {
+    uint32_t endo = get_u32(payload + 4 * W_FIXED_WORDS + 4 * g);
+    uint32_t want_hash = get_u32(payload + 4 * W_FIXED_WORDS + 4 * L.BK + 4 * g);
+    if (endo < prev || (int64_t)endo > data_len) return GAANS_REF_ECORRUPT;
+    int64_t b = g / L.K, k = g % L.K;
+    int64_t start = k * (int64_t)L.chunk_len;
+    int64_t end = start + L.chunk_len < N ? start + L.chunk_len : N;
+    int32_t len = (int32_t)(end - start);
+    int A = len < W_LANES ? len : W_LANES;
+    int T = (len + W_LANES - 1) / W_LANES;
+    const uint8_t* cp = data + prev;
+    int64_t cbytes = (int64_t)endo - prev;
+    if (cbytes < 4 * A || ((cbytes - 4 * A) & 3)) return GAANS_REF_ECORRUPT;
+    int64_t q = (cbytes - 4 * A) / 2; /* words incl. pad */
+    const uint8_t* wbase = cp + 4 * A;
+    int64_t rp = 0;
+    uint32_t x[W_LANES];
+    for (int l = 0; l < W_LANES; ++l) x[l] = l < A ? get_u32(cp + 4 * l) : W_L;
+    const int32_t* idx_row = indexes ? indexes + b * (int64_t)N : NULL;
+    int32_t* orow = out_symbols + b * (int64_t)N;
+    uint32_t hash = 0;
+    for (int t = 0; t < T; ++t) {
+      int32_t tbs[W_LANES], S_[W_LANES], vv[W_LANES];
+      uint32_t raw[W_LANES];
+      int nops[W_LANES], active[W_LANES];
+      for (int l = 0; l < W_LANES; ++l) {
+        int64_t p = l + (int64_t)W_LANES * t;
+        active[l] = p < len;
+        nops[l] = active[l] ? 1 : 0;
+        raw[l] = 0;
+        if (!active[l]) continue;
+        int64_t i = start + p;
+        int32_t tb = idx_row ? idx_row[i] : (int32_t)(i / L.HW);
+        if (tb < 0 || tb >= M) return GAANS_REF_EINDEX;
+        hash += (uint32_t)(tb + 1) ^ ((uint32_t)p * 0x9E3779B9u);
+        tbs[l] = tb;
+        S_[l] = cdf_sizes[tb];
+      }
+      for (int d = 0;; ++d) {
+        int any = 0;
+        int need[W_LANES];
+        for (int l = 0; l < W_LANES; ++l) {
+          need[l] = 0;
+          if (!active[l] || d >= nops[l]) continue;
+          any = 1;
+          if (d == 0) {
+            const int32_t* c = cdfs + (int64_t)tbs[l] * Lmax;
+            uint32_t cum = x[l] & 0xffffu;
+            int32_t v = find_symbol(c, S_[l], cum);
+            uint32_t st = (uint32_t)c[v], f = (uint32_t)(c[v + 1] - c[v]);
+            x[l] = f * (x[l] >> 16) + cum - st;
+            vv[l] = v;
+            if (v == S_[l] - 2) nops[l] = 2; /* count nibble next */
+          } else {
+            uint32_t val = x[l] & 15u;
+            x[l] >>= 4;
+            if (d == 1) {
+              if (val > 8) return GAANS_REF_ECORRUPT;
+              nops[l] = 2 + (int)val;
+            } else {
+              raw[l] |= val << (4 * (d - 2));
+            }
+          }
+          need[l] = x[l] < W_L;
+        }
+        if (!any) break;
+        for (int l = 0; l < W_LANES; ++l) {
+          if (!need[l]) continue;
+          uint32_t w = 0;
+          if (rp < q) w = (uint32_t)wbase[2 * rp] | ((uint32_t)wbase[2 * rp + 1] << 8);
+          else return GAANS_REF_ECORRUPT;
+          ++rp;
+          x[l] = (x[l] << 16) | w;
+        }
+      }
+      for (int l = 0; l < W_LANES; ++l) {
+        if (!active[l]) continue;
+        int64_t i = start + l + (int64_t)W_LANES * t;
+        int32_t tb = tbs[l];
+        if (vv[l] == S_[l] - 2) {
+          rc = unmap_escape(raw[l], S_[l], offsets[tb], &orow[i]);
+          if (rc) return rc;
+        } else {
+          orow[i] = vv[l] + offsets[tb];
+        }
+      }
+    }
+    for (int l = 0; l < A; ++l)
+      if (x[l] != W_L) return GAANS_REF_ECORRUPT;
+    if (!(rp == q || (rp == q - 1 && (q & 1) == 0))) return GAANS_REF_ECORRUPT;
+    if (hash != want_hash) return GAANS_REF_EMISMATCH;
+    prev = endo;
+  }
+  if ((int64_t)prev != data_len) return GAANS_REF_ECORRUPT;
+  return GAANS_REF_OK;
+}
+
+/* ---- quantize / dequantize closed forms ----------------------------------- */
+
+void gaans_ref_quantize(const float* y, const float* medians, int32_t B, int32_t C,
+                        int64_t HW, int32_t* symbols) {
+  for (int64_t b = 0; b < B; ++b)
+    for (int64_t c = 0; c < C; ++c)
+      for (int64_t p = 0; p < HW; ++p) {
+        int64_t i = (b * C + c) * HW + p;
+        volatile float d = y[i] - medians[c]; /* one fp32 rounding, no contraction */
+        float r = rintf(d);                   /* round half to even */
+        symbols[i] = (int32_t)r;              /* callers keep |r| < 2^31 */
+      }
+}
+
+void gaans_ref_dequantize(const int32_t* symbols, const float* medians, int32_t B,
+                          int32_t C, int64_t HW, float* y_hat) {
+  for (int64_t b = 0; b < B; ++b)
+    for (int64_t c = 0; c < C; ++c)
+      for (int64_t p = 0; p < HW; ++p) {
+        int64_t i = (b * C + c) * HW + p;
+        volatile float f = (float)symbols[i];
+        y_hat[i] = f + medians[c];
+      }
+}

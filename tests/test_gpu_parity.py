@@ -1,0 +1,286 @@
+"""GPU parity of the HIP GA-ANS coder against the CPU oracle, through the
+C ABI (via WarpDivBackend / the engine).  Bar: payload bytes identical to
+oracle/gaans_oracle.c, decoded symbols identical to the input, fused
+quantize/dequantize identical to CompressAI's closed forms."""
+
+import math
+from dataclasses import replace
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from fast_compressai import synthetic
+from fast_compressai.coders import CoderInputError, WarpDivBackend, WarpDivPayload, gaans
+from fast_compressai.coders.tables import prepare_tables
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def backend(gpu_device):
+    return WarpDivBackend()
+
+
+def dev(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def tables_on(w, device):
+    return dev(w.cdfs, device), dev(w.cdf_sizes, device), dev(w.offsets, device)
+
+
+def check_workload(backend, device, w, channels=None, bytes_check=True):
+    say("case:", w.name, "P =", w.p_ch, "shape", w.symbols.shape)
+    sym = dev(w.symbols, device)
+    idx = dev(w.explicit_indexes(), device)
+    cdfs, sizes, offs = tables_on(w, device)
+    payload = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=w.p_ch, channels=channels)
+    torch.cuda.synchronize()
+    if bytes_check:
+        ref = O.gaans_encode(w.symbols, w.indexes, w.cdfs, w.cdf_sizes, w.offsets, w.p_ch,
+                             channels)
+        got = payload.to_bytes()
+        assert len(got) == len(ref)
+        assert got == ref
+    out = backend.decode(payload, idx, cdfs, sizes, offs)
+    assert torch.equal(out, sym)
+    return payload
+
+
+# ---- reference GPU test cases (tests/gpu/test_warp_div_cuda.py:18-41) ------
+
+REF_CDFS = [[0, 8192, 16384, 32768, 65536]] * 4
+
+
+def ref_case(backend, device, symbols, p_ch):
+    s = np.array([symbols], np.int32)
+    idx = np.array([[0, 1, 2, 3] * (s.shape[1] // 4)], np.int32)
+    w = synthetic.Workload("reference 4-table case", s, idx, np.array(REF_CDFS, np.int32),
+                           np.array([5] * 4, np.int32), np.array([-2, -1, 0, 1], np.int32), 4,
+                           p_ch, 0)
+    payload = check_workload(backend, device, w)
+    assert payload.p_ch == p_ch
+    assert tuple(payload.max_rounds.shape) == (1, 4 // p_ch)
+
+
+@pytest.mark.parametrize("p_ch", [1, 2, 4])
+def test_reference_round_trip_multiple_p_ch(backend, gpu_device, p_ch):
+    ref_case(backend, gpu_device, [0, 1, 2, 3] * 16, p_ch)
+
+
+def test_reference_round_trip_escape_symbols(backend, gpu_device):
+    ref_case(backend, gpu_device, [-100, 100, -101, 102] * 16, 2)
+
+
+# ---- hand-derived KAT payloads (see tests/test_oracle.py) -------------------
+
+def test_kat_payloads_bit_exact(backend, gpu_device):
+    cdf = list(range(17)) + [65536]
+    s = [(5 * p + 3) % 16 for p in range(130)]
+    s[129] = 17
+    w = synthetic.Workload("KAT 130", np.array([s], np.int32), None, np.array([cdf], np.int32),
+                           np.array([18], np.int32), np.array([0], np.int32), 1, 1, 0)
+    check_workload(backend, gpu_device, w)
+    w = synthetic.Workload("KAT 2", np.zeros((1, 2), np.int32), None,
+                           np.array([[0, 32768, 65536]], np.int32), np.array([3], np.int32),
+                           np.array([0], np.int32), 1, 1, 0)
+    check_workload(backend, gpu_device, w)
+
+
+# ---- random shapes, ragged chunks, escapes ---------------------------------
+
+def random_tables(rng, M, max_size):
+    cdfs = np.zeros((M, max_size), np.int32)
+    sizes = np.zeros(M, np.int32)
+    for t in range(M):
+        S = int(rng.integers(2, max_size + 1))
+        f = rng.integers(1, 1000, S - 1).astype(np.float64)
+        f = np.floor(f / f.sum() * (65536 - (S - 1))).astype(np.int64) + 1
+        f[np.argmax(f)] += 65536 - f.sum()
+        cdfs[t, :S] = np.concatenate([[0], np.cumsum(f)])
+        sizes[t] = S
+    return cdfs, sizes, rng.integers(-20, 20, M).astype(np.int32)
+
+
+def test_random_shapes_bit_exact(backend, gpu_device):
+    rng = np.random.default_rng(11)
+    for trial in range(40):
+        B, C = int(rng.integers(1, 4)), int(rng.integers(1, 13))
+        HW = int(rng.choice([1, 3, 16, 63, 64, 65, 200, 777]))
+        P = int(rng.integers(1, C + 1))
+        cdfs, sizes, offs = random_tables(rng, C, int(rng.integers(2, 70)))
+        s = np.rint(rng.laplace(0, rng.uniform(0.2, 30), (B, C * HW))).astype(np.int32)
+        if trial % 3 == 0:
+            k = int(rng.integers(s.size))
+            s.flat[k] = int(rng.choice([2**30 + 7, -(2**31) + 40, 2**20, -(2**16)]))
+        w = synthetic.Workload(f"random trial {trial}", s, None, cdfs, sizes, offs, C, P, 0)
+        check_workload(backend, gpu_device, w)
+
+
+def test_explicit_random_indexes_bit_exact(backend, gpu_device):
+    rng = np.random.default_rng(12)
+    for trial in range(10):
+        M, C, HW = int(rng.integers(1, 9)), int(rng.integers(1, 9)), int(rng.integers(1, 300))
+        P = int(rng.integers(1, C + 1))
+        cdfs, sizes, offs = random_tables(rng, M, 40)
+        s = rng.integers(-30, 30, (2, C * HW)).astype(np.int32)
+        idx = rng.integers(0, M, (2, C * HW)).astype(np.int32)
+        w = synthetic.Workload(f"explicit trial {trial}", s, idx, cdfs, sizes, offs, C, P, 0)
+        check_workload(backend, gpu_device, w, channels=C)
+
+
+# ---- benchmark shapes at full size -----------------------------------------
+
+def test_coder_512x768_p4_bit_exact(backend, gpu_device):
+    check_workload(backend, gpu_device, synthetic.coder_512x768())
+
+
+@pytest.mark.parametrize("p_ch", [1, 16, 192])
+def test_coder_512x768_other_p(backend, gpu_device, p_ch):
+    check_workload(backend, gpu_device, synthetic.coder_512x768(p_ch=p_ch))
+
+
+@pytest.mark.parametrize("p_ch", [1, 4, 16, 64, 192])
+def test_hyperprior_y_gaussian_tables(backend, gpu_device, p_ch):
+    yw, zw, _, _ = synthetic.hyperprior_512x768(p_ch=p_ch)
+    check_workload(backend, gpu_device, yw, channels=192)
+    zw.p_ch = min(p_ch, 128)
+    check_workload(backend, gpu_device, zw)
+
+
+def test_highres_2160x3840_p8(backend, gpu_device):
+    check_workload(backend, gpu_device, synthetic.highres_2160x3840())
+
+
+@pytest.mark.parametrize("make", [synthetic.batch_skew, synthetic.batch_uniform])
+def test_batch64_p16(backend, gpu_device, make):
+    check_workload(backend, gpu_device, make())
+
+
+# ---- fused quantize / dequantize -------------------------------------------
+
+def test_fused_latents_match_quantize_then_encode(gpu_device):
+    w = synthetic.coder_512x768(seed=3)
+    rng = np.random.default_rng(3)
+    B, N, C = w.batch, w.n, w.channels
+    med = rng.normal(0, 0.3, C).astype(np.float32)
+    HW = N // C
+    y = (w.symbols.reshape(B, C, HW) + med[None, :, None]
+         + rng.uniform(-0.5, 0.5, (B, C, HW))).astype(np.float32)
+    y[0, 0, :8] = med[0] + np.array([0.5, -0.5, 1.5, -1.5, 2.5, -0.0, 1e7, -3e6], np.float32)
+    sym_ref = O.quantize(y, med)
+    tables = prepare_tables(*tables_on(w, gpu_device))
+    say("case: fused latents 1x192x32x48 P=4")
+    enc = gaans.encode(tables, B, N, C, 4, gpu_device, y=dev(y, gpu_device),
+                       medians=dev(med, gpu_device))
+    ref = O.gaans_encode(sym_ref.reshape(B, N), None, w.cdfs, w.cdf_sizes, w.offsets, 4)
+    assert enc.packed.cpu().numpy().tobytes() == ref
+    y_hat = gaans.decode(enc.packed, tables, B, N, C, 4, gpu_device,
+                         medians=dev(med, gpu_device))
+    ref_hat = O.dequantize(sym_ref, med).reshape(B, N)
+    assert np.array_equal(y_hat.cpu().numpy().view(np.uint32), ref_hat.view(np.uint32))
+    # and against torch on the GPU (CompressAI's quantize / dequantize expressions)
+    yt, mt = dev(y, gpu_device), dev(med, gpu_device)[None, :, None]
+    sym_t = torch.round(yt - mt).int()
+    assert np.array_equal(sym_t.cpu().numpy(), sym_ref)
+    assert torch.equal(y_hat.view(B, C, HW), sym_t.type_as(mt) + mt)
+
+
+def test_fused_latents_reject_non_finite(gpu_device):
+    w = synthetic.coder_512x768()
+    tables = prepare_tables(*tables_on(w, gpu_device))
+    y = np.zeros((1, 192, 1536), np.float32)
+    y[0, 5, 7] = np.nan
+    say("case: fused latents with NaN")
+    with pytest.raises(CoderInputError, match="non-finite"):
+        gaans.encode(tables, 1, w.n, 192, 4, gpu_device, y=dev(y, gpu_device),
+                     medians=torch.zeros(192, device=gpu_device))
+
+
+# ---- negative cases (tests/gpu/test_factorized_gaans.py:75-98) -------------
+
+@pytest.fixture(scope="module")
+def encoded(backend, gpu_device):
+    w = synthetic.coder_512x768(seed=5)
+    sym, idx = dev(w.symbols, gpu_device), dev(w.explicit_indexes(), gpu_device)
+    cdfs, sizes, offs = tables_on(w, gpu_device)
+    payload = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=4)
+    return w, sym, idx, cdfs, sizes, offs, payload
+
+
+def test_flipped_header_byte_rejected(backend, encoded):
+    w, sym, idx, cdfs, sizes, offs, payload = encoded
+    say("case: flipped header byte")
+    bad = payload.packed.clone()
+    bad[0] ^= 1
+    with pytest.raises(CoderInputError, match="header"):
+        backend.decode(replace(payload, packed=bad), idx, cdfs, sizes, offs)
+
+
+def test_corrupt_stream_rejected(backend, encoded):
+    w, sym, idx, cdfs, sizes, offs, payload = encoded
+    for pos in (payload.header_bytes + 3, payload.header_bytes + 5000,
+                payload.packed.numel() - 7):
+        say("case: corrupt stream byte", pos)
+        bad = payload.packed.clone()
+        bad[pos] ^= 0x21
+        with pytest.raises(CoderInputError):
+            backend.decode(replace(payload, packed=bad), idx, cdfs, sizes, offs)
+    say("case: corrupt chunk offset")
+    bad = payload.packed.clone()
+    bad[64 + 4 * 3] ^= 0x04
+    with pytest.raises(CoderInputError):
+        backend.decode(replace(payload, packed=bad), idx, cdfs, sizes, offs)
+
+
+def test_other_tables_or_indexes_rejected(backend, encoded):
+    w, sym, idx, cdfs, sizes, offs, payload = encoded
+    say("case: fingerprint mismatch")
+    with pytest.raises(CoderInputError, match="match"):
+        backend.decode(replace(payload, coding_fingerprint="0" * 64), idx, cdfs, sizes, offs)
+    say("case: other tables")
+    offs2 = offs.clone()
+    offs2[0] += 1
+    with pytest.raises(CoderInputError, match="match"):
+        backend.decode(payload, idx, cdfs, sizes, offs2)
+    say("case: other indexes")
+    idx2 = idx.clone()
+    idx2[0, 100] = 1
+    with pytest.raises(CoderInputError):
+        backend.decode(payload, idx2, cdfs, sizes, offs)
+    with pytest.raises(CoderInputError, match="match"):
+        replace(payload, p_ch=3, chunk_len=12)
+
+
+def test_out_of_range_index_rejected(backend, gpu_device, encoded):
+    w, sym, idx, cdfs, sizes, offs, payload = encoded
+    say("case: index out of range")
+    idx2 = idx.clone()
+    idx2[0, 17] = 192
+    with pytest.raises(CoderInputError, match="outside"):
+        backend.encode(sym, idx2, cdfs, sizes, offs, p_ch=4)
+
+
+def test_payload_bytes_round_trip(backend, gpu_device, encoded):
+    w, sym, idx, cdfs, sizes, offs, payload = encoded
+    again = WarpDivPayload.from_bytes(payload.to_bytes(), device=gpu_device)
+    assert again.coding_fingerprint == payload.coding_fingerprint
+    assert torch.equal(again.chunk_ends, payload.chunk_ends)
+    assert torch.equal(backend.decode(again, idx, cdfs, sizes, offs), sym)
+
+
+def test_bpp_against_compressai_equivalent_stream(backend, gpu_device):
+    # the payload's overhead over one CompressAI-style stream per image is the
+    # lane flush (64 x 32 bits per chunk) plus the header; at P=192 (one chunk)
+    # it must be within 1%.
+    w = synthetic.coder_512x768(p_ch=192)
+    payload = check_workload(backend, gpu_device, w, bytes_check=False)
+    single = len(O.rans64_encode(w.symbols[0], w.explicit_indexes()[0], w.cdfs, w.cdf_sizes,
+                                 w.offsets))
+    assert payload.packed.numel() <= single * 1.01

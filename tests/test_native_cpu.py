@@ -1,0 +1,121 @@
+"""CPU checks of the HIP library's host side: it loads without a GPU, exports
+every symbol include/gaans_w64.h declares, computes layouts, and prepares
+tables whose digest and decode lookup agree with the oracle / a brute-force
+search.  No kernel is launched here."""
+
+import ctypes
+import os
+import re
+import struct
+
+import numpy as np
+import pytest
+
+import oracle as O
+from fast_compressai.coders import _native
+from fast_compressai import synthetic
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_library_exports_every_declared_symbol():
+    header = open(os.path.join(REPO, "include", "gaans_w64.h")).read()
+    declared = set(re.findall(r"^\s*(?:int|const char\*)\s+(gaans_\w+)\s*\(", header, re.M))
+    assert "gaans_encode_symbols" in declared and len(declared) >= 11
+    lib = ctypes.CDLL(_native.library_path())
+    for name in sorted(declared):
+        assert hasattr(lib, name), name
+    assert _native.lib().gaans_abi_version() == _native.ABI_VERSION
+
+
+def test_host_selftest_division_constants():
+    assert _native.lib().gaans_host_selftest() == 0, _native.last_error()
+
+
+def test_layout_matches_format():
+    lay = _native.layout(1, 192 * 32 * 48, 192, 4)
+    assert (lay.K, lay.chunk_len, lay.BK, lay.HW) == (48, 6144, 48, 1536)
+    assert lay.header_bytes == (64 + 8 * 48 + 15) // 16 * 16
+    lay = _native.layout(64, 192 * 1536, 192, 16)
+    assert (lay.K, lay.BK, lay.chunk_len) == (12, 768, 24576)
+    assert lay.workspace_bytes >= lay.BK * lay.cap_words * 2
+    lay = _native.layout(1, 128 * 96, 128, 5)  # C not a multiple of P
+    assert lay.K == 26 and lay.chunk_len == 480
+    for bad in ((0, 4, 1, 1), (1, 5, 2, 1), (1, 4, 2, 3)):
+        with pytest.raises(Exception):
+            _native.layout(*bad)
+
+
+def prepare_host(cdfs, sizes, offs):
+    L = _native.lib()
+    cdfs = np.ascontiguousarray(cdfs, np.int32)
+    sizes = np.ascontiguousarray(sizes, np.int32)
+    offs = np.ascontiguousarray(offs, np.int32)
+    nb = ctypes.c_int64()
+    rc = L.gaans_tables_bytes(sizes.ctypes.data, cdfs.shape[0], cdfs.shape[1], ctypes.byref(nb))
+    if rc:
+        return rc, None, None
+    out = np.zeros(nb.value, np.uint8)
+    dg = ctypes.c_uint64()
+    rc = L.gaans_tables_prepare(cdfs.ctypes.data, sizes.ctypes.data, offs.ctypes.data,
+                                cdfs.shape[0], cdfs.shape[1], out.ctypes.data, nb.value,
+                                ctypes.byref(dg))
+    return rc, out, dg.value
+
+
+def host_lookup(blob, t, cum):
+    """Decode lookup as the kernel does it, read from the prepared blob."""
+    hdr = struct.unpack_from("<16I", blob, 0)
+    meta_off, ent_off, lut_off = hdr[6], hdr[7], hdr[8]
+    ent_base, nsym, offset, lut_base = struct.unpack_from("<IIiI", blob, meta_off + 16 * t)
+    e = struct.unpack_from("<Q", blob, lut_off + 8 * (lut_base + (cum >> 8)))[0]
+    lo, hi = e & 0xFFFFFFFF, e >> 32
+    s, span = hi & 0xFFFF, hi >> 16
+    ent = lambda v: struct.unpack_from("<I", blob, ent_off + 4 * (ent_base + v))[0]
+    if span == 0:
+        return s, lo & 0xFFFF, (lo >> 16) + 1
+    a, b = s, s + span
+    while a < b:
+        mid = (a + b + 1) >> 1
+        if (ent(mid) & 0xFFFF) <= cum:
+            a = mid
+        else:
+            b = mid - 1
+    return a, ent(a) & 0xFFFF, (ent(a) >> 16) + 1
+
+
+def test_prepared_tables_digest_and_lookup_exhaustive():
+    w = synthetic.coder_512x768()
+    cdfs, sizes, offs = w.cdfs[:6], w.cdf_sizes[:6], w.offsets[:6]
+    rc, blob, dg = prepare_host(cdfs, sizes, offs)
+    assert rc == 0
+    assert dg == O.table_digest(cdfs, sizes, offs)
+    blob = blob.tobytes()
+    for t in range(6):
+        c = cdfs[t, : sizes[t]]
+        want = np.searchsorted(c, np.arange(65536), side="right") - 1
+        for cum in range(0, 65536, 7):
+            v, start, freq = host_lookup(blob, t, cum)
+            assert v == want[cum] and start == c[v] and freq == c[v + 1] - c[v], (t, cum)
+
+
+def test_prepared_tables_dense_tail_lookup():
+    # GaussianConditional-style table with many freq-1 tail bins
+    yw, _, _, _ = synthetic.hyperprior_512x768()
+    t = 63
+    c = yw.cdfs[t, : yw.cdf_sizes[t]]
+    rc, blob, _ = prepare_host(yw.cdfs[t:t + 1], yw.cdf_sizes[t:t + 1], yw.offsets[t:t + 1])
+    assert rc == 0
+    blob = blob.tobytes()
+    want = np.searchsorted(c, np.arange(65536), side="right") - 1
+    for cum in list(range(0, 65536, 13)) + [0, 1, 65535, int(c[1]), int(c[-2]) - 1]:
+        assert host_lookup(blob, 0, cum)[0] == want[cum]
+
+
+@pytest.mark.parametrize("cdf,size", [([1, 65536], 2), ([0, 65535], 2), ([0, 100, 100, 65536], 4),
+                                      ([0, 65536], 1), ([0, 65536], 3)])
+def test_invalid_tables_rejected(cdf, size):
+    cdfs = np.zeros((1, max(len(cdf), 3)), np.int32)
+    cdfs[0, : len(cdf)] = cdf
+    rc, _, _ = prepare_host(cdfs, [size], [0])
+    assert rc == _native.ETABLE

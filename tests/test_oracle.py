@@ -1,0 +1,308 @@
+"""Pins the CPU oracle (oracle/gaans_oracle.c) before it is trusted as the
+checker of the HIP kernels.
+
+* Rans64 (CompressAI-equivalent) stream: hand-derived known-answer vectors,
+  including the survey's KAT for cdf [0, 32768, 65536] and the escape cases of
+  the reference's CPU coder tests (tests/test_coders.py:25-31, :78-81).
+* wave64 format: hand-derived payloads in which every coding step can be
+  followed on paper (freq-1 tables make each renormalisation word equal to a
+  known symbol), so lane order, group order, escape sub-rounds, states and
+  the header layout are each pinned by a literal value.
+* Round trips of the reference's GPU test cases
+  (tests/gpu/test_warp_div_cuda.py:18-41) and of random cases.
+* Quantize/dequantize closed forms against torch's own round / add.
+"""
+
+import math
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+CDF2 = [[0, 32768, 65536]]  # two bins: value 0 and the escape bin
+
+
+# ---------------------------------------------------------------------------
+# Rans64 single stream (CompressAI BufferedRansEncoder equivalent)
+# ---------------------------------------------------------------------------
+
+def words(data: bytes):
+    return list(struct.unpack(f"<{len(data) // 4}I", data))
+
+
+def test_rans64_kat_single_symbol():
+    # x = 2^31 < x_max = 2^62, so x' = (2^31 / 2^15) << 16 = 2^32; flush (lo, hi) = (0, 1)
+    assert O.rans64_encode([0], [0], CDF2, [3], [0]).hex() == "0000000001000000"
+
+
+def test_rans64_kat_escape_pattern_of_reference_cpu_test():
+    # symbols [0, 1, 0, 1]: with cdf_size 3 the value 1 is the escape bin, raw = 0,
+    # so each 1 pushes main(32768, 32768) + bits(0).  Reverse encoding from 2^31:
+    #   bits(0): 2^35; main esc: 2^36 + 2^15; main 0: 2^37 + 2^16;
+    #   bits(0): 2^41 + 2^20; main esc: 2^42 + 2^21 + 2^15; main 0: 2^43 + 2^22 + 2^16
+    x = 2**43 + 2**22 + 2**16
+    data = O.rans64_encode([0, 1, 0, 1], [0] * 4, CDF2, [3], [0])
+    assert words(data) == [x & 0xFFFFFFFF, x >> 32]
+    assert list(O.rans64_decode(data, [0] * 4, CDF2, [3], [0])) == [0, 1, 0, 1]
+
+
+def test_rans64_kat_escape_value_two():
+    # symbol 2 -> raw 2 (one nibble): bits(2): 2^35 + 2; bits(n=1): 2^39 + 33;
+    # main esc: (2^39 + 33) / 2^15 = 2^24 r 33 -> 2^40 + 33 + 32768
+    x = 2**40 + 32801
+    data = O.rans64_encode([2], [0], CDF2, [3], [0])
+    assert data.hex() == "2180000000010000"
+    assert words(data) == [x & 0xFFFFFFFF, x >> 32]
+    assert list(O.rans64_decode(data, [0], CDF2, [3], [0])) == [2]
+
+
+def test_rans64_kat_renormalisation_word():
+    # cdf [0, 1, 2, 65536]: symbol 1 has start 1, freq 1 (x_max = 2^47).
+    # last symbol: x = 2^31 << 16 | 1 = 2^47 + 1; first symbol: x >= 2^47 emits its
+    # low word 1, x = 2^15, x' = 2^31 + 1.  Memory order: flush lo, flush hi, word.
+    cdf = [[0, 1, 2, 65536]]
+    data = O.rans64_encode([1, 1], [0, 0], cdf, [4], [0])
+    assert words(data) == [0x80000001, 0x00000000, 0x00000001]
+    assert list(O.rans64_decode(data, [0, 0], cdf, [4], [0])) == [1, 1]
+
+
+def test_rans64_reference_cpu_cases_round_trip():
+    for syms in ([0, 1, 0, 1], [2], [0], [5, -3, 1000000, 0, -(2**26)]):
+        data = O.rans64_encode(syms, [0] * len(syms), CDF2, [3], [0])
+        assert list(O.rans64_decode(data, [0] * len(syms), CDF2, [3], [0])) == syms
+
+
+def test_rans64_length_close_to_information_content():
+    rng = np.random.default_rng(1)
+    freq = np.array([30000, 20000, 10000, 5000, 536])
+    cdf = [np.concatenate([[0], np.cumsum(freq)]).tolist()]
+    p = freq[:-1] / freq[:-1].sum()
+    syms = rng.choice(4, size=200000, p=p)
+    data = O.rans64_encode(syms, np.zeros_like(syms), cdf, [6], [0])
+    info_bits = float(-np.log2(freq[syms] / 65536.0).sum())
+    bits = 8 * len(data)
+    assert info_bits <= bits <= info_bits * 1.001 + 64
+
+
+# ---------------------------------------------------------------------------
+# wave64 GA-ANS format
+# ---------------------------------------------------------------------------
+
+def fnv1a64(data: bytes) -> int:
+    h = 0xCBF29CE484222325
+    for b in data:
+        h = ((h ^ b) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def test_fnv1a_published_vectors():
+    assert fnv1a64(b"") == 0xCBF29CE484222325
+    assert fnv1a64(b"a") == 0xAF63DC4C8601EC8C
+    assert fnv1a64(b"foobar") == 0x85944171F73967E8
+
+
+def table_digest_bytes(cdfs, sizes, offsets) -> bytes:
+    out = struct.pack("<I", len(sizes))
+    for row, s, o in zip(cdfs, sizes, offsets):
+        out += struct.pack("<Ii", s, o) + struct.pack(f"<{s}I", *row[:s])
+    return out
+
+
+def test_table_digest_definition():
+    cdfs = np.array([[0, 8192, 16384, 32768, 65536], [0, 32768, 65536, 0, 0]], np.int32)
+    sizes, offs = [5, 3], [-2, 7]
+    assert O.table_digest(cdfs, sizes, offs) == fnv1a64(table_digest_bytes(cdfs, sizes, offs))
+
+
+def hash_of(tables_per_position):
+    h = 0
+    for p, tb in enumerate(tables_per_position):
+        h += (tb + 1) ^ ((p * 0x9E3779B9) & 0xFFFFFFFF)
+    return h & 0xFFFFFFFF
+
+
+def header_words(B, N, C, P, K, chunk_len, M, digest):
+    return [0x31574147, 1, B, N, C, P, K, chunk_len, M, 0x00041040,
+            digest & 0xFFFFFFFF, digest >> 32, 0, 0, 0, 0]
+
+
+def test_gaans_kat_two_lanes_no_renorm():
+    # 2 symbols, 2 lanes, table cdf [0, 32768, 65536]: each lane x = 2^16 ->
+    # (2^16 / 2^15) << 16 = 2^17, no word.  Payload: 80-byte header, 2 states.
+    cdfs, sizes, offs = CDF2, [3], [0]
+    data = O.gaans_encode([[0, 0]], None, cdfs, sizes, offs, 1)
+    dg = fnv1a64(table_digest_bytes(cdfs, sizes, offs))
+    hdr = header_words(1, 2, 1, 1, 1, 2, 1, dg) + [8, hash_of([0, 0]), 0, 0]
+    assert data == struct.pack("<20I", *hdr) + struct.pack("<2I", 1 << 17, 1 << 17)
+    assert O.gaans_decode(data, None, 1, 2, cdfs, sizes, offs, 1).tolist() == [[0, 0]]
+
+
+def kat_130():
+    # Table: 17 symbols, values 0..15 have freq 1 (start = value), 16 is the
+    # escape bin (start 16, freq 65520).  A freq-1 symbol v maps x in
+    # [2^16, 2^17) to: emit x & 0xffff, x = 0x10000 + v.  So every word a lane
+    # emits is the symbol it coded one step earlier (0 for the initial state).
+    S = 18
+    cdf = list(range(17)) + [65536]
+    s = [(5 * p + 3) % 16 for p in range(130)]
+    s[129] = 17  # lane 1, step 2: escape, raw = 2 * (17 - 16) = 2, one nibble
+    return [cdf], [S], [0], s
+
+
+def test_gaans_kat_lane_order_group_order_and_escape_subrounds():
+    cdfs, sizes, offs, s = kat_130()
+    data = O.gaans_encode([s], None, cdfs, sizes, offs, 1)
+    # Step t=2 (lanes 0, 1): lane 1 runs bits(2) -> 0x100002, bits(n=1) ->
+    # 0x1000021 (no words), then in sub-round 0 lane 0 emits 0x0000 and lane 1's
+    # escape main op gives 0x1000021 = 256 * 65520 + 4129 -> (256 << 16) + 4129 + 16
+    # = 0x01001031 with no word.
+    # Step t=1: lane 0 emits s[128], lane 1 emits 0x1031 (x >> 16 = 256 >= 1) and
+    # becomes 0x01000000 + s[65]; lanes 2..63 emit their initial 0x0000.
+    # Step t=0: lane l emits s[64 + l]; states end at 0x10000 + s[l], lane 1 at
+    # 0x01000000 + s[1].
+    stream = s[64:128] + [s[128], 0x1031] + [0] * 62 + [0]
+    stream += [0]  # odd word count: one zero pad word
+    states = [0x10000 + s[l] for l in range(64)]
+    states[1] = 0x01000000 + s[1]
+    chunk = struct.pack("<64I", *states) + struct.pack(f"<{len(stream)}H", *stream)
+    assert len(chunk) == 516
+    dg = fnv1a64(table_digest_bytes(cdfs, sizes, offs))
+    hdr = header_words(1, 130, 1, 1, 1, 130, 1, dg) + [516, hash_of([0] * 130), 0, 0]
+    assert data == struct.pack("<20I", *hdr) + chunk
+    assert O.gaans_decode(data, None, 1, 130, cdfs, sizes, offs, 1).tolist() == [s]
+
+
+def test_gaans_chunking_and_header_offsets():
+    # 3 channels of HW = 2, P = 2 -> chunks of 4 and 2 symbols; 2 rows.
+    cdfs = np.array([[0, 32768, 65536]] * 3, np.int32)
+    sym = np.zeros((2, 6), np.int32)
+    data = O.gaans_encode(sym, None, cdfs, [3] * 3, [0] * 3, 2)
+    hb = (64 + 8 * 4 + 15) // 16 * 16
+    ends = struct.unpack_from("<4I", data, 64)
+    assert ends == (16, 24, 40, 48)  # 4 states, 2 states, 4, 2 (no words)
+    assert len(data) == hb + 48
+    hashes = struct.unpack_from("<4I", data, 64 + 16)
+    assert hashes == (hash_of([0, 0, 1, 1]), hash_of([2, 2]), hash_of([0, 0, 1, 1]),
+                      hash_of([2, 2]))
+
+
+REF_CDFS = [[0, 8192, 16384, 32768, 65536]] * 4
+REF_OFFS = [-2, -1, 0, 1]
+
+
+@pytest.mark.parametrize("symbols,p_ch", [([0, 1, 2, 3] * 16, 1), ([0, 1, 2, 3] * 16, 2),
+                                          ([0, 1, 2, 3] * 16, 4),
+                                          ([-100, 100, -101, 102] * 16, 2)])
+def test_gaans_reference_gpu_test_cases_round_trip(symbols, p_ch):
+    # tests/gpu/test_warp_div_cuda.py:18-41: four tables, indexes [0,1,2,3]*16
+    s = np.array([symbols], np.int32)
+    idx = np.array([[0, 1, 2, 3] * 16], np.int32)
+    data = O.gaans_encode(s, idx, REF_CDFS, [5] * 4, REF_OFFS, p_ch)
+    assert (O.gaans_decode(data, idx, 1, 64, REF_CDFS, [5] * 4, REF_OFFS, p_ch) == s).all()
+
+
+def random_tables(rng, M, max_size):
+    cdfs = np.zeros((M, max_size), np.int32)
+    sizes = np.zeros(M, np.int32)
+    for t in range(M):
+        S = int(rng.integers(2, max_size + 1))
+        f = rng.integers(1, 1000, S - 1).astype(np.float64)
+        f = np.floor(f / f.sum() * (65536 - (S - 1))).astype(np.int64) + 1
+        f[np.argmax(f)] += 65536 - f.sum()
+        cdfs[t, :S] = np.concatenate([[0], np.cumsum(f)])
+        sizes[t] = S
+    return cdfs, sizes, rng.integers(-20, 20, M).astype(np.int32)
+
+
+def test_gaans_random_round_trips_and_implicit_indexes():
+    rng = np.random.default_rng(0)
+    for trial in range(60):
+        B, C = int(rng.integers(1, 3)), int(rng.integers(1, 9))
+        HW, P = int(rng.integers(1, 150)), int(rng.integers(1, C + 1))
+        cdfs, sizes, offs = random_tables(rng, C, int(rng.integers(2, 24)))
+        s = rng.integers(-40, 40, (B, C * HW)).astype(np.int32)
+        if trial % 4 == 0:
+            s.flat[int(rng.integers(s.size))] = 2**30 + 5
+        idx = np.broadcast_to(np.repeat(np.arange(C, dtype=np.int32), HW), s.shape)
+        data = O.gaans_encode(s, None, cdfs, sizes, offs, P)
+        assert data == O.gaans_encode(s, idx, cdfs, sizes, offs, P)
+        assert (O.gaans_decode(data, idx, B, C * HW, cdfs, sizes, offs, P) == s).all()
+
+
+def test_gaans_escape_extremes_and_range_error():
+    cdfs, sizes = CDF2, [3]
+    s = np.array([[-(2**31), 2**31 - 1, 0, 1, 2**31 - 2]], np.int32)
+    data = O.gaans_encode(s, None, cdfs, sizes, [0], 1)
+    assert (O.gaans_decode(data, None, 1, 5, cdfs, sizes, [0], 1) == s).all()
+    with pytest.raises(O.OracleError) as err:  # raw = 2 * (2^31 - 1 + 100 - 1) >= 2^32
+        O.gaans_encode(np.array([[2**31 - 1]], np.int32), None, cdfs, sizes, [-100], 1)
+    assert err.value.code == -4
+
+
+def test_gaans_detects_corruption_and_mismatch():
+    rng = np.random.default_rng(3)
+    cdfs, sizes, offs = random_tables(rng, 4, 16)
+    s = rng.integers(-5, 5, (1, 4 * 100)).astype(np.int32)
+    data = bytearray(O.gaans_encode(s, None, cdfs, sizes, offs, 2))
+    hb = (64 + 8 * 2 + 15) // 16 * 16
+    bad = bytearray(data)
+    bad[hb + 300] ^= 0x40  # inside the first chunk's word stream
+    with pytest.raises(O.OracleError):
+        out = O.gaans_decode(bytes(bad), None, 1, 400, cdfs, sizes, offs, 2)
+        assert not (out == s).all()
+        raise O.OracleError(-6, "undetected corruption")
+    other = cdfs.copy()
+    other[0, 1] += 1
+    with pytest.raises(O.OracleError) as err:
+        O.gaans_decode(bytes(data), None, 1, 400, other, sizes, offs, 2)
+    assert err.value.code == -7
+    idx = np.broadcast_to(np.repeat(np.arange(4, dtype=np.int32), 100), (1, 400)).copy()
+    idx[0, 5] = 1  # same first chunk, other table for one symbol
+    with pytest.raises(O.OracleError):
+        O.gaans_decode(bytes(data), idx, 1, 400, cdfs, sizes, offs, 2)
+
+
+def test_gaans_bpp_overhead_is_the_lane_flush():
+    # per chunk the format adds ~64 states * 32 bits over the ideal stream;
+    # a single CompressAI-style stream carries one 64-bit flush.
+    rng = np.random.default_rng(5)
+    cdfs, sizes, offs = random_tables(rng, 8, 32)
+    s = rng.integers(-6, 6, (1, 8 * 4096)).astype(np.int32)
+    idx = np.repeat(np.arange(8, dtype=np.int32), 4096)
+    single = len(O.rans64_encode(s[0], idx, cdfs, sizes, offs))
+    for P in (1, 2, 8):
+        data = O.gaans_encode(s, None, cdfs, sizes, offs, P)
+        K = math.ceil(8 / P)
+        hb = (64 + 8 * K + 15) // 16 * 16
+        overhead = len(data) - hb - single
+        assert 0 < overhead <= K * (64 * 4 + 2) + 0.003 * single
+
+
+# ---------------------------------------------------------------------------
+# quantize / dequantize closed forms (CompressAI EntropyModel.quantize("symbols")
+# = round(y - means).int(), dequantize = symbols.type_as(means) + means)
+# ---------------------------------------------------------------------------
+
+def test_quantize_matches_torch_round_half_even():
+    med = np.array([0.0, 0.25, -1.5, 1e3], np.float32)
+    base = np.array([0.5, -0.5, 1.5, -1.5, 2.5, -2.5, -0.0, 0.49999997, 1e6 + 0.5,
+                     8388607.5, -8388608.5, 3.0], np.float32)
+    y = np.stack([base + m for m in med])[None]  # [1, 4, 12]
+    ours = O.quantize(y, med)
+    ref = torch.round(torch.from_numpy(y) - torch.from_numpy(med)[None, :, None]).int().numpy()
+    assert (ours == ref).all()
+    rng = np.random.default_rng(0)
+    y = (rng.standard_normal((2, 4, 300)) * 50).astype(np.float32)
+    ref = torch.round(torch.from_numpy(y) - torch.from_numpy(med)[None, :, None]).int().numpy()
+    assert (O.quantize(y, med) == ref).all()
+
+
+def test_dequantize_matches_torch_add():
+    med = np.array([0.1, -3.3, 7.77], np.float32)
+    s = np.array([[[0, 1, -1, 2**24 + 1, -(2**25) - 3], [5, 6, 7, 8, 9],
+                   [-100, 100, 2**30, -(2**31), 2**31 - 1]]], np.int32)
+    ref = (torch.from_numpy(s).float() + torch.from_numpy(med)[None, :, None]).numpy()
+    assert np.array_equal(O.dequantize(s, med).view(np.uint32), ref.view(np.uint32))
