@@ -15,7 +15,8 @@ import threading
 from .errors import CoderDependencyError
 
 LIB_NAME = "libgaans_w64.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
+CTRL_BYTES = 256
 
 # return codes
 OK, EINVAL, ETABLE, EHIP = 0, 1, 2, 3
@@ -47,6 +48,14 @@ class Layout(ctypes.Structure):
         "ws_words")]
 
 
+class Tables(ctypes.Structure):
+    """``gaans_tables``: descriptor of a prepared table blob."""
+
+    _fields_ = [("dev", ctypes.c_void_p), ("bytes", ctypes.c_int64), ("M", ctypes.c_int32),
+                ("max_nsym", ctypes.c_int32), ("total_nsym", ctypes.c_int64),
+                ("digest", ctypes.c_uint64)]
+
+
 def library_path() -> str:
     return os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", LIB_NAME)
 
@@ -61,22 +70,19 @@ _lock = threading.Lock()
 
 def _declare(L) -> None:
     p, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    T = ctypes.POINTER(Tables)
     sig = {
         "gaans_abi_version": ([], ctypes.c_int),
         "gaans_last_error": ([], ctypes.c_char_p),
         "gaans_get_layout": ([i64, i64, i64, i64, ctypes.POINTER(Layout)], ctypes.c_int),
         "gaans_tables_bytes": ([p, i32, i32, ctypes.POINTER(ctypes.c_int64)], ctypes.c_int),
-        "gaans_tables_prepare": ([p, p, p, i32, i32, p, i64, ctypes.POINTER(ctypes.c_uint64)],
+        "gaans_tables_prepare": ([p, p, p, i32, i32, p, i64, T], ctypes.c_int),
+        "gaans_encode_symbols": ([p, p, p, T, i64, i64, i64, i64, p, i64, p, p], ctypes.c_int),
+        "gaans_encode_latents": ([p, p, p, p, T, i64, i64, i64, i64, p, i64, p, p],
                                  ctypes.c_int),
-        "gaans_encode_symbols": ([p, p, p, p, i64, i32, i64, i64, i64, i64, p, i64],
-                                 ctypes.c_int),
-        "gaans_encode_latents": ([p, p, p, p, p, i64, i32, i64, i64, i64, i64, p, i64],
-                                 ctypes.c_int),
-        "gaans_encode_pack": ([p, p, i64, p, i64, i32, i64, i64, i64, i64, p, i64],
-                              ctypes.c_int),
-        "gaans_decode_symbols": ([p, p, i64, p, p, i64, i32, i64, i64, i64, i64, p, p],
-                                 ctypes.c_int),
-        "gaans_decode_latents": ([p, p, i64, p, p, i64, i32, p, i64, i64, i64, i64, p, p],
+        "gaans_encode_pack": ([p, p, i64, T, i64, i64, i64, i64, p, i64], ctypes.c_int),
+        "gaans_decode_symbols": ([p, p, i64, p, T, i64, i64, i64, i64, p, p, p], ctypes.c_int),
+        "gaans_decode_latents": ([p, p, i64, p, T, p, i64, i64, i64, i64, p, p, p],
                                  ctypes.c_int),
         "gaans_host_selftest": ([], ctypes.c_int),
     }
@@ -120,9 +126,18 @@ def check(rc: int, what: str) -> None:
         raise CoderInputError(f"{what} failed: {last_error()} (code {rc})")
 
 
+_layouts: dict = {}
+
+
 def layout(B: int, N: int, C: int, P: int) -> Layout:
-    out = Layout()
-    check(lib().gaans_get_layout(B, N, C, P, ctypes.byref(out)), "layout")
+    key = (B, N, C, P)
+    out = _layouts.get(key)
+    if out is None:
+        out = Layout()
+        check(lib().gaans_get_layout(B, N, C, P, ctypes.byref(out)), "layout")
+        if len(_layouts) > 256:
+            _layouts.clear()
+        _layouts[key] = out
     return out
 
 

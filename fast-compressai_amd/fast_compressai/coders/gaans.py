@@ -1,15 +1,23 @@
-"""Device-side GA-ANS engine: thin wrappers over the C ABI that allocate the
-buffers with the PyTorch caching allocator and launch on the current stream.
+"""Device-side GA-ANS engine: thin wrappers over the C ABI.
 
-Each encode makes exactly one host synchronisation (reading the payload size
-and the device status word before the payload is allocated); each decode
-makes one (reading the status word).  Reference host APIs replaced:
-``encode_with_indexes_warp_v2_cuda`` (``warp_ans_kernel_v2.cu:183-306``) and
-``decode_with_indexes_warp_cuda`` (``warp_ans_kernel.cu:477-544``).
+Per (device, stream) the engine keeps a control block (device memory, zeroed
+once; every launch leaves it zeroed), a reusable workspace, and two small
+pinned host buffers that the kernels' last workgroup writes the payload
+size / status into.  Calls on one stream are ordered, so these buffers are
+never shared by two calls in flight.
+
+Encode enqueues the coding kernel and the pack kernel back to back (the
+pack writes into a worst-case-sized buffer), then makes its one host
+synchronisation and reads the payload size.  Decode enqueues one kernel and
+synchronises once to read the status word.  Reference host APIs replaced:
+``encode_with_indexes_warp_v2_cuda`` (``warp_ans_kernel_v2.cu:183-306``, two
+syncs and six launches) and ``decode_with_indexes_warp_cuda``
+(``warp_ans_kernel.cu:477-544``, one sync and four launches).
 """
 
 from __future__ import annotations
 
+import threading
 from dataclasses import dataclass
 
 import torch
@@ -18,79 +26,123 @@ from . import _native
 from .errors import CoderInputError
 from .tables import PreparedTables
 
+_CLONE_SLACK_BYTES = 32 << 20  # keep a view of the worst-case buffer below this waste
 
-def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+
+class _StreamState:
+    def __init__(self, device: torch.device) -> None:
+        self.ctrl = torch.zeros(_native.CTRL_BYTES, dtype=torch.uint8, device=device)
+        self.info = torch.zeros(4, dtype=torch.int64, pin_memory=True)
+        self.status = torch.zeros(4, dtype=torch.int32, pin_memory=True)
+        self.workspace = torch.empty(0, dtype=torch.uint8, device=device)
+
+    def ws(self, nbytes: int) -> torch.Tensor:
+        if self.workspace.numel() < nbytes:
+            self.workspace = torch.empty(nbytes, dtype=torch.uint8,
+                                         device=self.workspace.device)
+        return self.workspace
+
+
+_states: dict = {}
+_states_lock = threading.Lock()
+
+
+def _state(device: torch.device, stream: torch.cuda.Stream) -> _StreamState:
+    key = (device.index, stream.cuda_stream)
+    st = _states.get(key)
+    if st is None:
+        with _states_lock:
+            st = _states.get(key)
+            if st is None:
+                with torch.cuda.device(device):
+                    st = _StreamState(device)
+                torch.cuda.current_stream(device).synchronize()  # ctrl zeroed before first use
+                _states[key] = st
+    return st
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+def _device(device) -> torch.device:
+    d = torch.device(device)
+    if d.index is None:
+        d = torch.device(d.type, torch.cuda.current_device())
+    return d
+
+
 @dataclass(frozen=True)
 class EncodedChunks:
     packed: torch.Tensor      # uint8 [payload bytes]
-    chunk_ends: torch.Tensor  # uint32 [B, K], end offset of every chunk after the header
+    chunk_ends: torch.Tensor  # uint32 [B, K] view of the header's chunk end offsets
     header_bytes: int
     chunk_len: int
     K: int
 
 
-def encode(tables: PreparedTables, B: int, N: int, C: int, P: int, device: torch.device, *,
+def encode(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,
            symbols: torch.Tensor | None = None, indexes: torch.Tensor | None = None,
            y: torch.Tensor | None = None, medians: torch.Tensor | None = None) -> EncodedChunks:
     """Encode int32 ``symbols`` [B, N], or fp32 latents ``y`` with per-channel
     ``medians`` (quantize fused).  ``indexes`` None means channel-major tables."""
     L = _native.lib()
     lay = _native.layout(B, N, C, P)
-    ws = torch.empty(int(lay.workspace_bytes), dtype=torch.uint8, device=device)
-    stream = _stream(device)
+    device = _device(device)
     with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device)
+        st = _state(device, stream)
+        ws = st.ws(int(lay.workspace_bytes))
+        out = torch.empty(int(lay.max_payload_bytes), dtype=torch.uint8, device=device)
+        sp = stream.cuda_stream
         if y is not None:
-            rc = L.gaans_encode_latents(stream, y.data_ptr(), medians.data_ptr(), _ptr(indexes),
-                                        tables.blob.data_ptr(), tables.nbytes, tables.M, B, N, C,
-                                        P, ws.data_ptr(), ws.numel())
+            rc = L.gaans_encode_latents(sp, y.data_ptr(), medians.data_ptr(), _ptr(indexes),
+                                        tables.ref, B, N, C, P, ws.data_ptr(), ws.numel(),
+                                        st.ctrl.data_ptr(), st.info.data_ptr())
         else:
-            rc = L.gaans_encode_symbols(stream, symbols.data_ptr(), _ptr(indexes),
-                                        tables.blob.data_ptr(), tables.nbytes, tables.M, B, N, C,
-                                        P, ws.data_ptr(), ws.numel())
+            rc = L.gaans_encode_symbols(sp, symbols.data_ptr(), _ptr(indexes), tables.ref, B, N,
+                                        C, P, ws.data_ptr(), ws.numel(), st.ctrl.data_ptr(),
+                                        st.info.data_ptr())
         _native.check(rc, "GA-ANS encode")
-        info = ws[lay.ws_info: lay.ws_info + 16].view(torch.int64).cpu()  # the one sync
-        total, status = int(info[0]), int(info[1])
-        if status:
-            raise CoderInputError(f"GA-ANS encode failed: {_native.describe_status(status)}")
-        packed = torch.empty(total, dtype=torch.uint8, device=device)
-        rc = L.gaans_encode_pack(stream, ws.data_ptr(), ws.numel(), tables.blob.data_ptr(),
-                                 tables.nbytes, tables.M, B, N, C, P, packed.data_ptr(), total)
+        rc = L.gaans_encode_pack(sp, ws.data_ptr(), ws.numel(), tables.ref, B, N, C, P,
+                                 out.data_ptr(), out.numel())
         _native.check(rc, "GA-ANS pack")
-        ends = ws[lay.ws_end_off: lay.ws_end_off + 4 * lay.BK].clone()
-    chunk_ends = ends.view(torch.uint32).view(B, int(lay.K))
-    return EncodedChunks(packed, chunk_ends, int(lay.header_bytes), int(lay.chunk_len),
-                         int(lay.K))
+        stream.synchronize()  # the one host synchronisation
+        total, status = int(st.info[0]), int(st.info[1])
+    if status:
+        raise CoderInputError(f"GA-ANS encode failed: {_native.describe_status(status)}")
+    packed = out[:total]
+    if out.numel() - total > _CLONE_SLACK_BYTES:
+        packed = packed.clone()
+    BK = int(lay.BK)
+    ends = packed[64: 64 + 4 * BK].view(torch.uint32).view(B, int(lay.K))
+    return EncodedChunks(packed, ends, int(lay.header_bytes), int(lay.chunk_len), int(lay.K))
 
 
 def decode(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int, P: int,
-           device: torch.device, *, indexes: torch.Tensor | None = None,
+           device, *, indexes: torch.Tensor | None = None,
            medians: torch.Tensor | None = None) -> torch.Tensor:
     """Decode to int32 symbols [B, N], or (``medians`` given) to fp32 y_hat
     [B, N] with dequantize fused."""
     L = _native.lib()
-    status = torch.zeros(1, dtype=torch.int32, device=device)
-    stream = _stream(device)
+    device = _device(device)
     with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device)
+        st = _state(device, stream)
+        sp = stream.cuda_stream
         if medians is not None:
             out = torch.empty((B, N), dtype=torch.float32, device=device)
-            rc = L.gaans_decode_latents(stream, packed.data_ptr(), packed.numel(), _ptr(indexes),
-                                        tables.blob.data_ptr(), tables.nbytes, tables.M,
-                                        medians.data_ptr(), B, N, C, P, out.data_ptr(),
-                                        status.data_ptr())
+            rc = L.gaans_decode_latents(sp, packed.data_ptr(), packed.numel(), _ptr(indexes),
+                                        tables.ref, medians.data_ptr(), B, N, C, P,
+                                        out.data_ptr(), st.ctrl.data_ptr(), st.status.data_ptr())
         else:
             out = torch.empty((B, N), dtype=torch.int32, device=device)
-            rc = L.gaans_decode_symbols(stream, packed.data_ptr(), packed.numel(), _ptr(indexes),
-                                        tables.blob.data_ptr(), tables.nbytes, tables.M, B, N, C,
-                                        P, out.data_ptr(), status.data_ptr())
+            rc = L.gaans_decode_symbols(sp, packed.data_ptr(), packed.numel(), _ptr(indexes),
+                                        tables.ref, B, N, C, P, out.data_ptr(),
+                                        st.ctrl.data_ptr(), st.status.data_ptr())
         _native.check(rc, "GA-ANS decode")
-        st = int(status.item())  # the one sync
-    if st:
-        raise CoderInputError(f"warp_div decode failed: {_native.describe_status(st)}")
+        stream.synchronize()  # the one host synchronisation
+        status = int(st.status[0])
+    if status:
+        raise CoderInputError(f"warp_div decode failed: {_native.describe_status(status)}")
     return out

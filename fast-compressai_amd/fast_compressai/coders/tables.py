@@ -30,6 +30,11 @@ class PreparedTables:
     M: int
     Lmax: int
     digest: int
+    desc: _native.Tables  # C descriptor pointing at ``blob``
+
+    @property
+    def ref(self):
+        return ctypes.byref(self.desc)
 
     @property
     def digest_hex(self) -> str:
@@ -56,15 +61,16 @@ def prepare_tables(cdfs: torch.Tensor, cdf_sizes: torch.Tensor, offsets: torch.T
     if rc != _native.OK:
         raise CoderInputError(f"invalid CDF tables: {_native.last_error()}")
     host = np.zeros(nbytes.value, dtype=np.uint8)
-    digest = ctypes.c_uint64(0)
+    desc = _native.Tables()
     rc = L.gaans_tables_prepare(c.ctypes.data, s.ctypes.data, o.ctypes.data, M, Lmax,
-                                host.ctypes.data, nbytes.value, ctypes.byref(digest))
+                                host.ctypes.data, nbytes.value, ctypes.byref(desc))
     if rc != _native.OK:
         raise CoderInputError(f"invalid CDF tables: {_native.last_error()}")
     dev = device if device is not None else cdfs.device
     blob = torch.from_numpy(host).to(dev)
+    desc.dev = blob.data_ptr()
     return PreparedTables(blob=blob, nbytes=int(nbytes.value), M=M, Lmax=Lmax,
-                          digest=int(digest.value))
+                          digest=int(desc.digest), desc=desc)
 
 
 class TableCache:

@@ -13,22 +13,27 @@
  *                   cdfs, cdf_sizes, offsets)
  *       -> gaans_decode_symbols                       (+ gaans_decode_latents,
  *          which also fuses dequantize, reference factorized.py:99-101)
- * The table layout step (gaans_tables_prepare) replaces the per-call reads of
- * the padded [M, Lmax] int32 CDF tensor and the 512 KB magic table
- * (reference warp_ans_kernel_v2.cu:230-247).
+ * gaans_tables_prepare replaces the kernels' reads of the padded [M, Lmax]
+ * int32 CDF tensor and of the 512 KB magic table (reference
+ * warp_ans_kernel_v2.cu:230-247).
  *
  * Conventions
  *  - Every function returns 0 (GAANS_OK) or a positive GAANS_E* code and
  *    leaves a message for gaans_last_error() (thread-local).  No C++
  *    exception crosses this boundary.
- *  - Pointers named *_dev are device pointers; the library never allocates
- *    device memory: the caller passes every buffer, sized with
- *    gaans_get_layout / gaans_tables_bytes.
+ *  - Pointers named *_dev are device pointers.  The library never allocates
+ *    memory: the caller passes every buffer, sized with gaans_get_layout /
+ *    gaans_tables_bytes.
  *  - `stream` is a hipStream_t (NULL = the legacy default stream).  Device
  *    functions only enqueue work on that stream; none of them synchronises.
- *  - Kernel-detected problems (bad symbols, corrupt payloads) are reported as
- *    GAANS_ST_* bits in a device status word that the caller reads after the
- *    stream has finished.
+ *  - ctrl_dev is a caller-owned control block of GAANS_CTRL_BYTES bytes of
+ *    device memory, zeroed once by the caller; every encode/decode leaves it
+ *    zeroed again.  Calls that share one control block must be ordered on
+ *    one stream (each stream should own its own block).
+ *  - Problems the kernels find (bad symbols, corrupt payloads) are reported
+ *    as GAANS_ST_* bits in a status word that the last block of the launch
+ *    writes to caller memory (device or pinned host memory); read it after
+ *    the stream has finished.
  *
  * Payload format "gaans-w64-v1": documented in DESIGN.md and in
  * oracle/gaans_oracle.c (the CPU definition of the bytes).
@@ -43,7 +48,8 @@
 extern "C" {
 #endif
 
-#define GAANS_ABI_VERSION 1
+#define GAANS_ABI_VERSION 2
+#define GAANS_CTRL_BYTES 256
 
 /* return codes */
 #define GAANS_OK 0
@@ -51,7 +57,7 @@ extern "C" {
 #define GAANS_ETABLE 2  /* CDF tables are not valid 16-bit quantized CDFs */
 #define GAANS_EHIP 3    /* a HIP runtime call failed */
 
-/* device status bits (encode: info word 1; decode: the status word) */
+/* status bits written by the kernels */
 #define GAANS_ST_RANGE 0x01u     /* symbol cannot be coded (escape >= 2^32, non-finite latent) */
 #define GAANS_ST_INDEX 0x02u     /* table index out of range */
 #define GAANS_ST_HEADER 0x04u    /* payload header does not match the call */
@@ -65,13 +71,24 @@ typedef struct gaans_layout {
   int64_t B, N, C, P;     /* batch rows, symbols per row, channels, channels per chunk */
   int64_t HW, K, chunk_len, BK;
   int64_t header_bytes;   /* payload header size (multiple of 16) */
-  int64_t max_payload_bytes;
+  int64_t max_payload_bytes; /* worst case: every symbol an escape with 8 nibbles */
   int64_t cap_words;      /* staging words per chunk (worst case) */
   int64_t workspace_bytes;
   /* byte offsets inside the encode workspace */
   int64_t ws_chunk_words, ws_chunk_status, ws_index_hash, ws_end_off, ws_info,
       ws_states, ws_words;
 } gaans_layout;
+
+/* Prepared tables: filled by gaans_tables_prepare except `dev`, which the
+ * caller sets to the device copy of the prepared blob. */
+typedef struct gaans_tables {
+  const void* dev;    /* device copy of the prepared blob */
+  int64_t bytes;      /* blob size */
+  int32_t M;          /* number of tables */
+  int32_t max_nsym;   /* largest alphabet (cdf_size - 1) */
+  int64_t total_nsym; /* sum of the alphabets */
+  uint64_t digest;    /* table digest recorded in payload headers */
+} gaans_tables;
 
 int gaans_abi_version(void);
 const char* gaans_last_error(void);
@@ -88,63 +105,66 @@ int gaans_tables_bytes(const int32_t* cdf_sizes, int32_t M, int32_t Lmax, int64_
 /* Validate CompressAI-style tables (cdfs [M, Lmax] int32 row-major, rows
  * zero-padded beyond cdf_sizes[t]; cdf[0] = 0, cdf[S-1] = 65536, strictly
  * increasing) and lay them out for the kernels: per-table metadata, packed
- * (start, freq-1) entries and a 256-bucket decode lookup.  The caller copies
- * `out` to device memory unchanged.  *digest receives the table digest that
- * payloads record.  Replaces the reference's use of the raw tensors at
+ * (start, freq-1) entries and a 256-bucket decode lookup per table.  The
+ * caller copies `out` to device memory unchanged and stores its address in
+ * desc->dev.  Replaces the reference's use of the raw tensors at
  * src/fast_compressai/coders/factorized.py:23-31. */
 int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes,
                          const int32_t* offsets, int32_t M, int32_t Lmax,
-                         void* out, int64_t out_bytes, uint64_t* digest);
+                         void* out, int64_t out_bytes, gaans_tables* desc);
 
 /* ---- encode ------------------------------------------------------------- */
 
-/* Stage 1: code every chunk into `workspace_dev` (layout->workspace_bytes)
- * and write the chunk offsets plus info = {u64 payload bytes incl. header,
- * u64 status} at workspace + layout->ws_info.  `indexes_dev` may be NULL:
- * then position i of a row uses table i / HW (CompressAI EntropyBottleneck
+/* Stage 1: code every chunk into `workspace_dev` (layout->workspace_bytes).
+ * The launch's last block scans the chunk sizes into payload offsets and
+ * writes info = {u64 payload bytes incl. header, u64 status} both to the
+ * workspace (at layout->ws_info) and, when info_out is not NULL, to
+ * info_out (device or pinned host memory).  `indexes_dev` may be NULL: then
+ * position i of a row uses table i / HW (CompressAI EntropyBottleneck
  * indexes).  Reference: encode_with_indexes_warp_v2_cuda,
  * src/fast_compressai/coders/cuda/warp_ans_kernel_v2.cu:183-273. */
 int gaans_encode_symbols(void* stream, const int32_t* symbols_dev,
-                         const int32_t* indexes_dev, const void* tables_dev,
-                         int64_t tables_bytes, int32_t M, int64_t B, int64_t N,
-                         int64_t C, int64_t P, void* workspace_dev,
-                         int64_t workspace_bytes);
+                         const int32_t* indexes_dev, const gaans_tables* tables,
+                         int64_t B, int64_t N, int64_t C, int64_t P,
+                         void* workspace_dev, int64_t workspace_bytes, void* ctrl_dev,
+                         uint64_t* info_out);
 
 /* Stage 1 with CompressAI's quantize fused in: symbol = int32(rint(y -
  * medians[c])) for latents y [B, C, HW] fp32 and per-channel medians [C].
  * Reference: FactorizedWarpDivCodec.compress, factorized.py:46-59. */
 int gaans_encode_latents(void* stream, const float* y_dev, const float* medians_dev,
-                         const int32_t* indexes_dev, const void* tables_dev,
-                         int64_t tables_bytes, int32_t M, int64_t B, int64_t N,
-                         int64_t C, int64_t P, void* workspace_dev,
-                         int64_t workspace_bytes);
+                         const int32_t* indexes_dev, const gaans_tables* tables,
+                         int64_t B, int64_t N, int64_t C, int64_t P,
+                         void* workspace_dev, int64_t workspace_bytes, void* ctrl_dev,
+                         uint64_t* info_out);
 
-/* Stage 2: after the caller has read info[0] (payload bytes) from the
- * workspace, write the payload (header + chunks) to out_dev, which holds at
- * least that many bytes.  Reference: write_warp_tight_header_kernel and
- * warp_pack_tight_payload_kernel, warp_ans_kernel_v2.cu:274-296. */
+/* Stage 2: write the payload (header + chunks) to out_dev.  May be enqueued
+ * right after stage 1 on the same stream into a buffer of
+ * layout->max_payload_bytes, or after the caller has read the payload size
+ * into an exact buffer; chunks that would not fit out_bytes are skipped.
+ * Reference: write_warp_tight_header_kernel and warp_pack_tight_payload_kernel,
+ * warp_ans_kernel_v2.cu:274-296. */
 int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace_bytes,
-                      const void* tables_dev, int64_t tables_bytes, int32_t M,
-                      int64_t B, int64_t N, int64_t C, int64_t P, uint8_t* out_dev,
-                      int64_t out_bytes);
+                      const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
+                      int64_t P, uint8_t* out_dev, int64_t out_bytes);
 
 /* ---- decode ------------------------------------------------------------- */
 
-/* Decode a payload into int32 symbols [B, N].  `status_dev` is one u32 that
- * the caller zeroes beforehand; kernels OR GAANS_ST_* bits into it.
+/* Decode a payload into int32 symbols [B, N].  The last block writes the
+ * OR of all GAANS_ST_* bits (0 when the payload decoded cleanly) to
+ * *status_out (device or pinned host memory).
  * Reference: decode_with_indexes_warp_cuda, warp_ans_kernel.cu:477-544. */
 int gaans_decode_symbols(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
-                         const int32_t* indexes_dev, const void* tables_dev,
-                         int64_t tables_bytes, int32_t M, int64_t B, int64_t N,
-                         int64_t C, int64_t P, int32_t* out_dev, uint32_t* status_dev);
+                         const int32_t* indexes_dev, const gaans_tables* tables,
+                         int64_t B, int64_t N, int64_t C, int64_t P, int32_t* out_dev,
+                         void* ctrl_dev, uint32_t* status_out);
 
 /* Decode with CompressAI's dequantize fused in: y_hat = fp32(symbol) +
  * medians[c], written as [B, C, HW] fp32. */
 int gaans_decode_latents(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
-                         const int32_t* indexes_dev, const void* tables_dev,
-                         int64_t tables_bytes, int32_t M, const float* medians_dev,
-                         int64_t B, int64_t N, int64_t C, int64_t P, float* y_hat_dev,
-                         uint32_t* status_dev);
+                         const int32_t* indexes_dev, const gaans_tables* tables,
+                         const float* medians_dev, int64_t B, int64_t N, int64_t C,
+                         int64_t P, float* y_hat_dev, void* ctrl_dev, uint32_t* status_out);
 
 /* ---- host self test ------------------------------------------------------- */
 

@@ -56,11 +56,15 @@ def prepare_host(cdfs, sizes, offs):
     if rc:
         return rc, None, None
     out = np.zeros(nb.value, np.uint8)
-    dg = ctypes.c_uint64()
+    desc = _native.Tables()
     rc = L.gaans_tables_prepare(cdfs.ctypes.data, sizes.ctypes.data, offs.ctypes.data,
                                 cdfs.shape[0], cdfs.shape[1], out.ctypes.data, nb.value,
-                                ctypes.byref(dg))
-    return rc, out, dg.value
+                                ctypes.byref(desc))
+    if rc == 0:
+        assert desc.bytes == nb.value and desc.M == cdfs.shape[0]
+        assert desc.max_nsym == int(np.max(sizes)) - 1
+        assert desc.total_nsym == int(np.sum(sizes)) - cdfs.shape[0]
+    return rc, out, desc.digest
 
 
 def host_lookup(blob, t, cum):
@@ -70,11 +74,14 @@ def host_lookup(blob, t, cum):
     ent_base, nsym, offset, lut_base = struct.unpack_from("<IIiI", blob, meta_off + 16 * t)
     e = struct.unpack_from("<Q", blob, lut_off + 8 * (lut_base + (cum >> 8)))[0]
     lo, hi = e & 0xFFFFFFFF, e >> 32
-    s, span = hi & 0xFFFF, hi >> 16
+    s0, nxt = hi & 0xFFFF, hi >> 16
+    st, fr = lo & 0xFFFF, (lo >> 16) + 1
     ent = lambda v: struct.unpack_from("<I", blob, ent_off + 4 * (ent_base + v))[0]
-    if span == 0:
-        return s, lo & 0xFFFF, (lo >> 16) + 1
-    a, b = s, s + span
+    if nxt != 0xFFFF:
+        if cum >= st + fr:
+            return s0 + 1, st + fr, nxt + 1
+        return s0, st, fr
+    a, b = s0, min(s0 + 256, nsym - 1)
     while a < b:
         mid = (a + b + 1) >> 1
         if (ent(mid) & 0xFFFF) <= cum:
@@ -109,7 +116,8 @@ def test_prepared_tables_dense_tail_lookup():
     blob = blob.tobytes()
     want = np.searchsorted(c, np.arange(65536), side="right") - 1
     for cum in list(range(0, 65536, 13)) + [0, 1, 65535, int(c[1]), int(c[-2]) - 1]:
-        assert host_lookup(blob, 0, cum)[0] == want[cum]
+        v, start, freq = host_lookup(blob, 0, cum)
+        assert v == want[cum] and start == c[v] and freq == c[v + 1] - c[v], cum
 
 
 @pytest.mark.parametrize("cdf,size", [([1, 65536], 2), ([0, 65535], 2), ([0, 100, 100, 65536], 4),
