@@ -1,29 +1,29 @@
 // GA-ANS wave64 latent coder for MI355X (gfx950): HIP kernels + C ABI.
 //
-// One wave64 codes one chunk of P latent channels.  Each lane carries one
-// 32-bit rANS state (x in [2^16, 2^32), 16-bit renormalisation words, 16-bit
-// CDF precision).  Lane l of a chunk owns positions l + 64 t, so a wave reads
-// 64 consecutive symbols per step.  The renormalisation words a step emits
-// are compacted in lane order with a wave ballot + mbcnt prefix count; the
-// decoder hands refill words out in the same order.
+// Format: one chunk = P latent channels; 64 lanes, one 32-bit rANS state per
+// lane (x in [2^16, 2^32), 16-bit renormalisation words, 16-bit CDF
+// precision); lane l owns positions l + 64 t of the chunk.  The words a step
+// emits are ordered by lane (wave ballot + mbcnt prefix); the decoder hands
+// refill words out in the same order.  The bytes are defined by the CPU
+// oracle (oracle/gaans_oracle.c).
 //
-// Per chunk (one 64-thread workgroup):
-//  - the CDF tables of the chunk's channels (or all tables, when they fit)
-//    are staged in LDS: packed (start, freq-1) entries, and for decode a
-//    256-bucket lookup per table; tables that are not staged are read
-//    through L1/L2;
-//  - symbols / indexes / latents are prefetched kSB steps ahead in registers
-//    (coalesced 256-byte loads per step);
-//  - encode: emitted words go to an LDS ring that is flushed to a per-chunk
-//    staging slot when it fills; decode: the word stream is prefetched from
-//    HBM into registers and copied into an LDS ring ahead of use;
-//  - the last workgroup of a launch (device-scope counter in a caller-owned
+// Work mapping: one 256-thread workgroup per chunk.
+//  - Wave 0 is the coder: it owns the 64 lane states and runs only the
+//    serial part of every step (renormalisation, ballot compaction, state
+//    update).
+//  - Waves 1-3 are mappers: one block of kSB steps ahead of the coder they
+//    load symbols / indexes / latents from HBM (a block ahead again, so the
+//    loads are in flight while the previous block is mapped), look the
+//    tables up, split escapes, hash the indexes and write one 16-byte op
+//    record per lane and step into LDS.
+//  - The CDF tables of the chunk's channels (or all tables, when they fit) are
+//    staged in LDS by the whole workgroup; others are read through L1/L2.
+//  - encode: emitted words go to an LDS ring, flushed to a per-chunk staging
+//    slot when full; decode: the word stream is prefetched from HBM into
+//    registers and copied into an LDS ring ahead of use.
+//  - The last workgroup of a launch (device-scope counter in a caller-owned
 //    control block) scans the chunk sizes into payload offsets (encode) or
 //    reduces the status words (decode) and writes them to caller memory.
-//
-// Payload format "gaans-w64-v1" (the bytes are defined by the CPU oracle,
-// oracle/gaans_oracle.c): header, then per chunk the final lane states (u32)
-// and the word stream (u16, decode order).
 //
 // Reference path replaced: src/fast_compressai/coders/cuda/warp_ans_kernel_v2.cu:71-306
 // (encode), warp_ans_kernel.cu:178-369 and :477-544 (pack, header, decode),
@@ -37,34 +37,39 @@
 #include <string.h>
 
 #include <string>
+#include <type_traits>
 
 #include "gaans_w64.h"
 
 namespace {
 
 constexpr int kLanes = 64;
-constexpr uint32_t kStateLow = 1u << 16;   // rANS L
-constexpr uint32_t kBitsEmit = 1u << 28;   // renorm bound of a 4-bit bypass op
-constexpr uint32_t kMagic = 0x31574147u;   // "GAW1"
+#ifndef GAANS_MAPPERS
+#define GAANS_MAPPERS 3
+#endif
+constexpr int kMappers = GAANS_MAPPERS;  // mapper waves per workgroup
+constexpr int kWaves = kMappers + 1;     // + the coder wave
+constexpr int kThreads = kWaves * kLanes;
+constexpr uint32_t kStateLow = 1u << 16;  // rANS L
+constexpr uint32_t kBitsEmit = 1u << 28;  // renorm bound of a 4-bit bypass op
+constexpr uint32_t kMagic = 0x31574147u;  // "GAW1"
 constexpr uint32_t kVersion = 1u;
 constexpr uint32_t kParams = 0x00041040u;  // lanes 64 | precision 16 << 8 | bypass 4 << 16
 constexpr int kFixedWords = 16;
-constexpr uint32_t kTabMagic = 0x31425447u;  // "GTB1"
+constexpr uint32_t kTabMagic = 0x32425447u;  // "GTB2"
 constexpr int kLutBits = 8;
 constexpr int kLutSize = 1 << kLutBits;
 constexpr uint32_t kHashMul = 0x9E3779B9u;
 constexpr int kMaxOpsPerSymbol = 10;  // main + count + 8 nibbles
 
-#ifndef GAANS_PREFETCH_STEPS
-#define GAANS_PREFETCH_STEPS 8
-#endif
-constexpr int kSB = GAANS_PREFETCH_STEPS;  // steps per register prefetch block
-constexpr int kRingWords = 4096;    // encoder LDS output ring (u16 words)
-constexpr int kStreamRing = 2048;   // decoder LDS stream ring (u16 words)
-constexpr int kPfU32 = 4;           // decoder stream prefetch: u32 per lane (512 words)
+constexpr int kSB = 8;                 // steps per block (mapper lead)
+constexpr int kPer = (kSB + kMappers - 1) / kMappers;  // steps per mapper wave and block
+constexpr int kPartBytes = (8 * kWaves + 15) / 16 * 16;  // per-wave hash + status
+constexpr int kRingWords = 4096;       // encoder LDS output ring (u16 words)
+constexpr int kStreamRing = 2048;      // decoder LDS stream ring (u16 words)
+constexpr int kPfU32 = 4;              // decoder stream prefetch: u32 per lane
 constexpr int kPfWords = 2 * kPfU32 * kLanes;
-constexpr int64_t kEncTableBudget = 32 * 1024;
-constexpr int64_t kDecTableBudget = 48 * 1024;
+constexpr int64_t kLdsMax = 64 * 1024;  // LDS of one workgroup
 // control block (u32 words); encoder and decoder fields on separate 64-byte lines
 constexpr int kCtrlEncDone = 0;
 constexpr int kCtrlDecDone = 16;
@@ -85,26 +90,34 @@ int fail(int code, const char* fmt, ...) {
 int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
 // ---- prepared table blob ---------------------------------------------------
-// [TabHdr 64 B][TabMeta x M][u32 entries: start | (freq-1) << 16][u64 lut: M x 256]
-// lut entry of bucket j (cum in [j << 8, (j << 8) + 255]):
-//   low word  = entry of the symbol s containing cum = j << 8
-//   high word = s | next << 16: next = freq(s + 1) - 1 if the bucket holds at
-//               most one symbol boundary, else 0xffff (search the entries)
+// [TabHdr 64 B][TabMeta x M][entries: 2 x u32 per symbol][lut: u64 x 256 x M]
+// [dense blocks: 256 x u8 each]
+// entry of symbol v: word 0 = start | (freq - 1) << 16;
+//                    word 1 = division magic of freq (enc_magic).
+// lut entry of bucket j (cum in [j << 8, (j << 8) + 255]), s = the symbol
+// containing cum = j << 8:
+//   at most one other symbol starts in the bucket:
+//     low word = entry word 0 of s, high word = s | (freq(s + 1) - 1) << 16
+//   two or more (a dense bucket):
+//     low word = index of the bucket's dense block, high word = s | 0xffff << 16;
+//     byte i of the block = (symbol containing cum = (j << 8) + i) - s
 struct TabHdr {
   uint32_t magic, M, total_syms, lut_bits;
   uint32_t digest_lo, digest_hi;
   uint32_t meta_off, ent_off, lut_off;  // byte offsets
   uint32_t total_bytes;
   uint32_t max_nsym;
-  uint32_t reserved[5];
+  uint32_t dense_off;    // byte offset of the dense blocks
+  uint32_t total_dense;  // dense blocks over all tables
+  uint32_t reserved[3];
 };
 static_assert(sizeof(TabHdr) == 64, "table header is 64 bytes");
 
 struct TabMeta {
-  uint32_t ent_base;  // first entry of the table
-  uint32_t nsym;      // S - 1 symbols; the last one (nsym - 1) is the escape bin
+  uint32_t ent_base;    // first entry of the table
+  uint32_t nsym;        // S - 1 symbols; the last one (nsym - 1) is the escape bin
   int32_t offset;
-  uint32_t lut_base;  // first lut entry of the table
+  uint32_t dense_base;  // first dense block of the table
 };
 
 // Division by a wave-uniform divisor d in [1, 2^31) for numerators n < 2^31:
@@ -115,13 +128,16 @@ struct UDiv {
   uint32_t m, s;
 };
 
-__host__ __device__ inline uint32_t udiv(uint32_t n, UDiv d) {
+__host__ __device__ inline uint32_t mulhi32(uint32_t a, uint32_t b) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  uint32_t t = __umulhi(n, d.m);
+  return __umulhi(a, b);
 #else
-  uint32_t t = (uint32_t)(((uint64_t)n * d.m) >> 32);
+  return (uint32_t)(((uint64_t)a * b) >> 32);
 #endif
-  return (t + n) >> d.s;
+}
+
+__host__ __device__ inline uint32_t udiv(uint32_t n, UDiv d) {
+  return (mulhi32(n, d.m) + n) >> d.s;
 }
 
 UDiv make_udiv(uint32_t d) {
@@ -129,6 +145,32 @@ UDiv make_udiv(uint32_t d) {
   while (((uint64_t)1 << s) < d) ++s;
   uint64_t m = (((uint64_t)1 << (32 + s)) / d) - ((uint64_t)1 << 32) + 1;
   return UDiv{(uint32_t)m, s};
+}
+
+// Encoder division x / f over the full 32-bit range for f in [2, 65536]
+// (Granlund & Montgomery, PLDI 1994, figure 4.1): l = ceil(log2 f),
+// m = floor(2^32 (2^l - f) / f) + 1, t = mulhi(x, m),
+// q = (t + ((x - t) >> 1)) >> (l - 1).  f = 1 is handled by the caller.
+uint32_t enc_magic(uint32_t f) {
+  if (f < 2) return 0;
+  uint32_t l = 0;
+  while (((uint64_t)1 << l) < f) ++l;
+  return (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << l) - f)) / f + 1);
+}
+
+__host__ __device__ inline uint32_t enc_shift(uint32_t f) {  // l - 1, for f >= 2
+#if defined(__HIP_DEVICE_COMPILE__)
+  return 31u - (uint32_t)__clz((int)(f - 1u));
+#else
+  uint32_t l = 0;
+  while (((uint64_t)1 << l) < f) ++l;
+  return l - 1;
+#endif
+}
+
+__host__ __device__ inline uint32_t enc_div(uint32_t x, uint32_t m, uint32_t sh) {
+  const uint32_t t = mulhi32(x, m);
+  return (t + ((x - t) >> 1)) >> sh;
 }
 
 struct Layout {
@@ -152,6 +194,8 @@ int make_layout(int64_t B, int64_t N, int64_t C, int64_t P, Layout* L) {
   L->chunk_len = P * L->HW;
   L->BK = B * L->K;
   if (L->BK >= ((int64_t)1 << 31)) return fail(GAANS_EINVAL, "too many chunks");
+  if ((int64_t)kMaxOpsPerSymbol * L->chunk_len + 2 >= ((int64_t)1 << 31))
+    return fail(GAANS_EINVAL, "chunk of %lld symbols is too large", (long long)L->chunk_len);
   L->header_bytes = align_up(4 * kFixedWords + 8 * L->BK, 16);
   L->max_payload = L->header_bytes + B * N * 2 * kMaxOpsPerSymbol + L->BK * (4 * kLanes + 4);
   L->cap_words = align_up((int64_t)kMaxOpsPerSymbol * L->chunk_len + 2, 2);
@@ -184,9 +228,9 @@ __device__ __forceinline__ uint32_t wave_or(uint32_t v) {
   return v;
 }
 
-__device__ __forceinline__ int wave_max(int v) {
+__device__ __forceinline__ uint32_t wave_max(uint32_t v) {
   for (int off = 32; off > 0; off >>= 1) {
-    int o = __shfl_xor(v, off, 64);
+    const uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
     v = o > v ? o : v;
   }
   return v;
@@ -199,23 +243,6 @@ __device__ __forceinline__ uint64_t wave_incl_scan(uint64_t v, int lane) {
     if (lane >= off) v += ((uint64_t)hi << 32) | lo;
   }
   return v;
-}
-
-// Encoder main op on a renormalised state x < freq << 16:
-// x' = ((x / freq) << 16) + x % freq + start.  The quotient comes from a fp32
-// reciprocal (error < 2^-6 because x / freq < 2^16) and one signed correction,
-// written without branches.
-__device__ __forceinline__ uint32_t enc_main(uint32_t x, uint32_t start, uint32_t freq,
-                                             float rcp) {
-  uint32_t q = (uint32_t)((float)x * rcp);
-  uint32_t r = x - q * freq;                       // in (-freq, 2 freq) as a signed value
-  const uint32_t neg = (uint32_t)((int32_t)r >> 31);  // all ones when r < 0
-  q += neg;
-  r += freq & neg;
-  const uint32_t over = r >= freq ? 0xffffffffu : 0u;
-  q -= over;
-  r -= freq & over;
-  return (q << 16) + r + start;
 }
 
 // Keep a wave-uniform value in a scalar register.
@@ -234,37 +261,82 @@ __device__ __forceinline__ int chunk_len_of(int64_t g, int32_t K, int32_t chunk_
   return (int)(e - s);
 }
 
+__device__ __forceinline__ void chunk_range(int64_t g, int64_t K, int64_t N, int32_t chunk_len,
+                                            int64_t& row, int32_t& start, int& len, int& k) {
+  const int64_t b = g / K;
+  k = (int)(g - b * K);
+  row = b * N;
+  start = k * chunk_len;
+  const int32_t endp = (int64_t)start + chunk_len < N ? start + chunk_len : (int32_t)N;
+  len = endp - start;
+}
+
 // Tables of one chunk: a staged range [t_lo, t_lo + nt) in LDS, the rest in
 // global memory.
 struct Tabs {
   const TabMeta* __restrict__ gmeta;
-  const uint32_t* __restrict__ gent;
+  const uint2* __restrict__ gent;
   const uint64_t* __restrict__ glut;
-  const uint4* lmeta;     // {ent_base (LDS-local), nsym, offset, 0}
-  const uint32_t* lent;
-  const uint64_t* llut;   // nt x 256
+  const uint8_t* __restrict__ gdense;
+  const uint4* lmeta;      // {ent_base (LDS-local), nsym, offset, 0}
+  const uint2* lent;       // encoder: both entry words
+  const uint32_t* lent32;  // decoder: entry word 0
+  const uint64_t* llut;    // nt x 256
+  const uint8_t* ldense;
   int t_lo, nt;
+  uint32_t dense_first;    // first staged dense block
 };
 
-// Stage tables [t_lo, t_hi) of the blob into LDS (one wave).
-__device__ void stage_tables(Tabs& T, uint4* lmeta, uint32_t* lent, uint64_t* llut, int t_lo,
-                             int t_hi, int lane) {
+// Stage tables [t_lo, t_hi) of the blob into LDS (whole workgroup): the
+// encoder's metadata and entries (lent), or the decoder's metadata, entry
+// words 0 (lent32), lookups (llut) and dense blocks (ldense).
+__device__ void stage_tables(Tabs& T, uint4* lmeta, uint2* lent, uint32_t* lent32,
+                             uint64_t* llut, uint8_t* ldense, uint32_t total_dense, uint32_t M,
+                             int t_lo, int t_hi, int tid) {
   T.t_lo = t_lo;
   T.nt = t_hi > t_lo ? t_hi - t_lo : 0;
-  if (T.nt == 0) return;
-  const uint32_t base0 = T.gmeta[t_lo].ent_base;
-  const TabMeta last = T.gmeta[t_hi - 1];
-  const uint32_t n_ent = last.ent_base + last.nsym - base0;
-  for (int i = lane; i < T.nt; i += kLanes) {
-    const TabMeta m = T.gmeta[t_lo + i];
-    lmeta[i] = make_uint4(m.ent_base - base0, m.nsym, (uint32_t)m.offset, 0u);
-  }
-  for (uint32_t i = lane; i < n_ent; i += kLanes) lent[i] = T.gent[base0 + i];
-  if (llut) {
-    const uint64_t* src = T.glut + T.gmeta[t_lo].lut_base;  // tables' luts are contiguous
-    for (int i = lane; i < T.nt * kLutSize; i += kLanes) llut[i] = src[i];
+  T.dense_first = 0;
+  if (T.nt > 0) {
+    const uint32_t base0 = T.gmeta[t_lo].ent_base;
+    const TabMeta last = T.gmeta[t_hi - 1];
+    const uint32_t n_ent = last.ent_base + last.nsym - base0;
+    for (int i = tid; i < T.nt; i += kThreads) {
+      const TabMeta m = T.gmeta[t_lo + i];
+      lmeta[i] = make_uint4(m.ent_base - base0, m.nsym, (uint32_t)m.offset, 0u);
+    }
+    if (lent)
+      for (uint32_t i = tid; i < n_ent; i += kThreads) lent[i] = T.gent[base0 + i];
+    if (lent32)
+      for (uint32_t i = tid; i < n_ent; i += kThreads) lent32[i] = T.gent[base0 + i].x;
+    if (llut) {
+      const uint64_t* src = T.glut + (int64_t)t_lo * kLutSize;  // luts are contiguous
+      for (int i = tid; i < T.nt * kLutSize; i += kThreads) llut[i] = src[i];
+    }
+    if (ldense) {
+      const uint32_t d0 = T.gmeta[t_lo].dense_base;
+      const uint32_t d1 = (uint32_t)t_hi < M ? T.gmeta[t_hi].dense_base : total_dense;
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(T.gdense + (size_t)d0 * kLutSize);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(ldense);
+      for (uint32_t i = tid; i < (d1 - d0) * (kLutSize / 4); i += kThreads) dst[i] = src[i];
+      T.dense_first = d0;
+    }
   }
   __syncthreads();
+}
+
+// Staged table range of chunk k: all tables, or the chunk's P channels.
+__device__ __forceinline__ void stage_range(int nt_cap, int stage_all, int k, int P, int M,
+                                            int& t_lo, int& t_hi) {
+  t_lo = 0;
+  t_hi = 0;
+  if (nt_cap > 0) {
+    if (stage_all) {
+      t_hi = M;
+    } else {
+      t_lo = k * P;
+      t_hi = t_lo + P < M ? t_lo + P : M;
+    }
+  }
 }
 
 // ============================================================================
@@ -295,17 +367,14 @@ struct EncArgs {
   uint64_t* __restrict__ info_out;
 };
 
-// One symbol ready for the rANS update.  Inactive lanes carry the identity op
-// (start 0, freq 65536: no word, x unchanged).  The escape split is finished
-// only in steps where some lane escapes (enc_escape_ops).
-struct EncSym {
-  uint32_t st, fr;
-  float rcp;
-  int32_t v, maxv, sym;  // v = sym - offset (wrapped), maxv = escape bin
-  bool esc, ovf;         // ovf: sym - offset does not fit int32
-};
+// Encoder LDS layout (bytes)
+constexpr int kEncRingBytes = 2 * (kRingWords + kLanes);  // + one spare slot per lane
+constexpr int kEncRecBytes = 2 * kSB * kLanes * 16;        // two blocks of op records
+constexpr int kEncInfoBytes = 2 * kSB * 4;                 // per-step escape op count
+constexpr int kEncFixedLds = kEncRingBytes + kEncRecBytes + kEncInfoBytes + kPartBytes;
 
-// last workgroup of an encode launch: chunk offsets + payload size + status
+// last workgroup of an encode launch (wave 0): chunk offsets + payload size +
+// status
 __device__ void encode_finish(const EncArgs& a, int lane) {
   uint64_t carry = 0;
   uint32_t st = 0;
@@ -341,20 +410,29 @@ __device__ void encode_finish(const EncArgs& a, int lane) {
   }
 }
 
-// Branch-free mapping of one symbol: table (LDS or global), escape flag,
-// entry lookup and index hash.  Reports bad indexes / non-finite latents in
-// `status`.
-template <bool kLatents, bool kImplicit, bool kLds>
-__device__ __forceinline__ EncSym enc_map(const EncArgs& a, const Tabs& tb, int lane, int t,
-                                          int len, int32_t start, int32_t in_a, int32_t in_b,
-                                          float in_m, uint32_t& hash, uint32_t& status) {
+// Op record of one lane and step (16 bytes):
+//   x: start | (65536 - freq) << 16      (identity op: 0)
+//   y: division magic of freq            (enc_div)
+//   z: shift | (freq == 1) << 5 | nops << 8   (nops: ops in decode order)
+//   w: escape raw value
+// CompressAI's escape split (reference warp_ans_kernel_v2.cu:139-164):
+// v = sym - offset; v < 0 -> raw = -2v - 1, v >= maxv -> raw = 2 (v - maxv),
+// both coded as the escape bin maxv, then n = raw ? msb(raw) / 4 + 1 : 0
+// nibbles.  v is computed in 32-bit arithmetic; when sym - offset overflows
+// int32 the sign of sym tells the side and raw = 2 (v - maxv) (wrapped) is
+// exact whenever raw < 2^32, else the symbol is uncodable.
+template <bool kLatents, bool kImplicit>
+__device__ __forceinline__ uint4 enc_record(const EncArgs& a, const Tabs& tb, bool lds, int lane,
+                                            int t, int len, int32_t start, int32_t in_a,
+                                            int32_t in_b, float in_m, uint32_t& hash,
+                                            uint32_t& status) {
   const int p = lane + kLanes * t;
   const bool act = p < len;
   int32_t tbi = kImplicit ? (int32_t)udiv((uint32_t)(start + p), a.div_hw) : in_b;
   const bool bad = act & ((uint32_t)tbi >= a.M);
   const bool ok = act & !bad;
   status |= bad ? GAANS_ST_INDEX : 0u;
-  tbi = ok ? tbi : (kLds ? tb.t_lo : 0);
+  tbi = ok ? tbi : (lds ? tb.t_lo : 0);
   hash += ok ? ((uint32_t)(tbi + 1) ^ ((uint32_t)p * kHashMul)) : 0u;
   int32_t sym;
   if (kLatents) {
@@ -367,7 +445,7 @@ __device__ __forceinline__ EncSym enc_map(const EncArgs& a, const Tabs& tb, int 
   }
   uint32_t ebase, nsym;
   int32_t offset;
-  if (kLds) {
+  if (lds) {
     const uint4 m = tb.lmeta[tbi - tb.t_lo];
     ebase = m.x;
     nsym = m.y;
@@ -378,52 +456,48 @@ __device__ __forceinline__ EncSym enc_map(const EncArgs& a, const Tabs& tb, int 
     nsym = m.nsym;
     offset = m.offset;
   }
-  EncSym s;
-  s.sym = sym;
-  s.v = (int32_t)((uint32_t)sym - (uint32_t)offset);
-  s.maxv = (int32_t)nsym - 1;
-  s.ovf = ok & (((sym ^ offset) & (sym ^ s.v)) < 0);
-  const bool out = ((uint32_t)s.v >= (uint32_t)s.maxv) | s.ovf;  // v < 0 or v >= maxv
-  s.esc = ok & out;
-  const int32_t vv = out ? s.maxv : s.v;
-  const uint32_t e = kLds ? tb.lent[ebase + (uint32_t)vv] : tb.gent[ebase + (uint32_t)vv];
-  s.st = ok ? (e & 0xffffu) : 0u;
-  s.fr = ok ? ((e >> 16) + 1u) : 65536u;
-  s.rcp = __builtin_amdgcn_rcpf((float)s.fr);
-  return s;
-}
-
-// Escape details of one symbol (CompressAI's split, reference
-// warp_ans_kernel_v2.cu:139-164): raw value and the op count in decode
-// order (1, or nibbles + 2).  v is the wrapped 32-bit sym - offset; when it
-// overflowed, the sign of sym tells the side, and raw = 2 (v - maxv) is
-// exact whenever the true raw is < 2^32 (else the symbol is uncodable).
-__device__ __forceinline__ void enc_escape_split(const EncSym& s, uint32_t& raw,
-                                                 uint32_t& nops, uint32_t& status) {
-  const uint32_t d = (uint32_t)s.v - (uint32_t)s.maxv;
-  const bool lo = s.ovf ? (s.sym < 0) : (s.v < 0);
-  const bool uncodable = s.ovf & (lo | (d >= 0x80000000u));
-  status |= uncodable ? GAANS_ST_RANGE : 0u;
-  const uint32_t r = lo ? ~((uint32_t)s.v << 1) : (d << 1);
-  raw = s.esc ? r : 0u;
+  const int32_t v = (int32_t)((uint32_t)sym - (uint32_t)offset);
+  const int32_t maxv = (int32_t)nsym - 1;
+  const bool ovf = ((sym ^ offset) & (sym ^ v)) < 0;
+  const bool out = ((uint32_t)v >= (uint32_t)maxv) | ovf;
+  const bool esc = ok & out;
+  const int32_t vv = out ? maxv : v;
+  const uint2 e = lds ? tb.lent[ebase + (uint32_t)vv] : tb.gent[ebase + (uint32_t)vv];
+  // escape split
+  const uint32_t d = (uint32_t)v - (uint32_t)maxv;
+  const bool lo = ovf ? (sym < 0) : (v < 0);
+  status |= (ok & ovf & (lo | (d >= 0x80000000u))) ? GAANS_ST_RANGE : 0u;
+  const uint32_t raw = esc ? (lo ? ~((uint32_t)v << 1) : (d << 1)) : 0u;
   const uint32_t nn = raw ? ((31u - (uint32_t)__clz((int)raw)) >> 2) + 1u : 0u;
-  nops = s.esc ? nn + 2u : 1u;
+  const uint32_t nops = esc ? nn + 2u : 1u;
+  const uint32_t fr = (e.x >> 16) + 1u;
+  const uint32_t sh = fr >= 2u ? enc_shift(fr) : 0u;
+  uint4 r;
+  r.x = ok ? ((e.x & 0xffffu) | ((65536u - fr) << 16)) : 0u;
+  r.y = ok ? e.y : 1u;
+  r.z = (ok ? sh : 15u) | ((ok & (fr == 1u)) ? 32u : 0u) | (nops << 8);
+  r.w = raw;
+  return r;
 }
 
 // Encoder LDS ring: kRingWords words + one spare slot per lane, which lanes
 // that emit nothing write to (so the store needs no branch).
-__device__ __forceinline__ void ring_flush(uint16_t* __restrict__ wbuf,
-                                           const uint16_t* ring, int wp, int fl, int lane) {
-  __syncthreads();
+__device__ __forceinline__ void ring_flush(uint16_t* __restrict__ wbuf, const uint16_t* ring,
+                                           int wp, int fl, int lane) {
   for (int pos = wp + lane; pos < fl; pos += kLanes) wbuf[pos] = ring[pos & (kRingWords - 1)];
 }
 
+// The ring holds the words [wp, fl) (positions mod kRingWords).  The coder
+// flushes it at the start of a block when fewer than kSB * kLanes slots are
+// free, so the fast steps of a block need no check; escape sub-rounds
+// (kCheck) keep that much room free for the rest of their block.
+template <bool kCheck>
 __device__ __forceinline__ void emit_words(bool emit, uint32_t& x, uint16_t* ring,
                                            uint16_t* __restrict__ wbuf, int& wp, int& fl,
                                            int lane) {
   const uint64_t m = __ballot(emit);
   const int c = __popcll(m);
-  if (fl - wp + c > kRingWords) {
+  if (kCheck && fl - wp + c > kRingWords - kSB * kLanes) {
     ring_flush(wbuf, ring, wp, fl, lane);
     fl = uni(wp);
   }
@@ -434,155 +508,234 @@ __device__ __forceinline__ void emit_words(bool emit, uint32_t& x, uint16_t* rin
   x = emit ? (x >> 16) : x;
 }
 
+// main rANS op: x' = ((x / freq) << 16) + x % freq + start = x + start + q (65536 - freq)
+__device__ __forceinline__ uint32_t enc_apply(uint32_t x, uint4 r) {
+  const uint32_t q = enc_div(x, r.y, r.z & 31u);
+  const uint32_t xn = __umul24(q, r.x >> 16) + (x + (r.x & 0xffffu));
+  return (r.z & 32u) ? ((x << 16) + (r.x & 0xffffu)) : xn;
+}
+
 template <bool kLatents, bool kImplicit>
-__global__ __launch_bounds__(64) void k_encode(EncArgs a) {
+__global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t* ring = reinterpret_cast<uint16_t*>(smem);
-  constexpr int kRingBytes = 2 * (kRingWords + kLanes);
-  uint4* lmeta = reinterpret_cast<uint4*>(smem + kRingBytes);
-  uint32_t* lent = reinterpret_cast<uint32_t*>(smem + kRingBytes + 16 * a.nt_cap);
+  uint4* recs = reinterpret_cast<uint4*>(smem + kEncRingBytes);
+  uint32_t* info = reinterpret_cast<uint32_t*>(smem + kEncRingBytes + kEncRecBytes);
+  uint32_t* part = info + 2 * kSB;  // per-wave hash [0, kWaves) and status [kWaves, 2 kWaves)
+  uint4* lmeta = reinterpret_cast<uint4*>(smem + kEncFixedLds);
+  uint2* lent = reinterpret_cast<uint2*>(smem + kEncFixedLds + 16 * a.nt_cap);
 
-  const int g = blockIdx.x;
-  const int lane = threadIdx.x;
-  const int64_t b = g / a.K;
-  const int k = g - (int)(b * a.K);
-  const int64_t row = b * a.N;
-  const int32_t start = k * a.chunk_len;
-  const int32_t endp = (int64_t)start + a.chunk_len < a.N ? start + a.chunk_len : (int32_t)a.N;
-  const int len = endp - start;
+  const int64_t g = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kLanes - 1);
+  const int wid = uni(tid >> 6);  // wave role, kept in a scalar register
+  int64_t row;
+  int32_t start;
+  int len, k;
+  chunk_range(g, a.K, a.N, a.chunk_len, row, start, len, k);
   const int T = (len + kLanes - 1) / kLanes;
   const int A = len < kLanes ? len : kLanes;
-  uint16_t* __restrict__ wbuf = a.words + (int64_t)g * a.cap_words;
-  int wp = a.cap_words;  // wave-uniform write cursor (backwards)
-  int fl = a.cap_words;  // words at [fl, cap) are already in wbuf
+  const int nblk = (T + kSB - 1) / kSB;
+  uint16_t* __restrict__ wbuf = a.words + g * a.cap_words;
+  int wp = a.cap_words;  // coder: wave-uniform write cursor (backwards)
+  int fl = a.cap_words;  // coder: words at [fl, cap) are already in wbuf
   uint32_t x = kStateLow;
   uint32_t hash = 0, status = 0;
 
-  if (tables_ok(a.tables, a.M, a.tables_bytes)) {
+  const bool tab = tables_ok(a.tables, a.M, a.tables_bytes);  // uniform
+  if (!tab) status |= GAANS_ST_TABLES;
+  if (tab) {
     const TabHdr* th = reinterpret_cast<const TabHdr*>(a.tables);
     Tabs tb;
     tb.gmeta = reinterpret_cast<const TabMeta*>(a.tables + th->meta_off);
-    tb.gent = reinterpret_cast<const uint32_t*>(a.tables + th->ent_off);
+    tb.gent = reinterpret_cast<const uint2*>(a.tables + th->ent_off);
     tb.glut = nullptr;
+    tb.gdense = nullptr;
     tb.lmeta = lmeta;
     tb.lent = lent;
+    tb.lent32 = nullptr;
     tb.llut = nullptr;
-    int t_lo = 0, t_hi = 0;
-    if (a.nt_cap > 0) {
-      if (a.stage_all) {
-        t_hi = (int)a.M;
-      } else {
-        t_lo = k * a.P;
-        t_hi = t_lo + a.P < (int)a.M ? t_lo + a.P : (int)a.M;
-      }
-    }
-    stage_tables(tb, lmeta, lent, nullptr, t_lo, t_hi, lane);
+    tb.ldense = nullptr;
+    int t_lo, t_hi;
+    stage_range(a.nt_cap, a.stage_all, k, a.P, (int)a.M, t_lo, t_hi);
+    stage_tables(tb, lmeta, lent, nullptr, nullptr, nullptr, 0u, a.M, t_lo, t_hi, tid);
 
-    int32_t ca[kSB], cb[kSB], na[kSB], nb[kSB];
-    float cm[kSB], nm[kSB];
-    // loads are issued for every lane (inactive lanes read the chunk's last
-    // position) so that no branch separates them from their use one block later
+    // mapper wave w (1..kMappers) owns steps u = w - 1 + kMappers e of every block
+    int32_t ca[kPer], cb[kPer], na[kPer], nb[kPer];
+    float cm[kPer], nm[kPer];
     auto load_block = [&](int j, int32_t* ia, int32_t* ib, float* im) {
 #pragma unroll
-      for (int u = 0; u < kSB; ++u) {
+      for (int e = 0; e < kPer; ++e) {
+        const int u = (wid - 1) + kMappers * e;
+        if (kSB % kMappers != 0 && u >= kSB) break;
         int p = lane + kLanes * (j * kSB + u);
-        p = p < len ? p : len - 1;
+        p = p < len ? p : len - 1;  // loads stay in the chunk; results are masked
         const int64_t i = row + start + p;
         if (kLatents) {
-          ia[u] = __float_as_int(a.y[i]);
-          im[u] = a.medians[udiv((uint32_t)(start + p), a.div_hw)];
+          ia[e] = __float_as_int(a.y[i]);
+          im[e] = a.medians[udiv((uint32_t)(start + p), a.div_hw)];
         } else {
-          ia[u] = a.symbols[i];
-          im[u] = 0.0f;
+          ia[e] = a.symbols[i];
+          im[e] = 0.0f;
         }
-        ib[u] = kImplicit ? 0 : a.indexes[i];
+        ib[e] = kImplicit ? 0 : a.indexes[i];
       }
     };
-
-    const int nblk = (T + kSB - 1) / kSB;
-    if (nblk > 0) load_block(nblk - 1, ca, cb, cm);
-    for (int j = nblk - 1; j >= 0; --j) {
-      if (j > 0) load_block(j - 1, na, nb, nm);
+    auto map_steps = [&](int j, auto lds_tag) {
+      constexpr bool kLds = decltype(lds_tag)::value;
+      uint4* dst = recs + (j & 1) * kSB * kLanes;
+      uint32_t nops[kPer];
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) {
+        const int u = (wid - 1) + kMappers * e;
+        if (kSB % kMappers != 0 && u >= kSB) break;
+        const uint4 r = enc_record<kLatents, kImplicit>(a, tb, kLds, lane, j * kSB + u, len,
+                                                        start, ca[e], cb[e], cm[e], hash, status);
+        dst[u * kLanes + lane] = r;
+        nops[e] = r.z >> 8;
+      }
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) {
+        const int u = (wid - 1) + kMappers * e;
+        if (kSB % kMappers != 0 && u >= kSB) break;
+        uint32_t mt = 0;
+        if (__ballot(nops[e] > 1u)) mt = wave_max(nops[e]);  // escapes are rare
+        if (lane == 0) info[(j & 1) * kSB + u] = mt;
+      }
+    };
+    auto map_block = [&](int j) {
+      // LDS tables for the whole block when every active lane's table is staged
       bool lds = tb.nt > 0;
       if (!kImplicit && lds) {
-        bool in = true;
+        bool outside = false;
 #pragma unroll
-        for (int u = 0; u < kSB; ++u)
-          in = in && (lane + kLanes * (j * kSB + u) >= len ||
-                      (uint32_t)(cb[u] - tb.t_lo) < (uint32_t)tb.nt);
-        lds = __ballot(!in) == 0;
+        for (int e = 0; e < kPer; ++e) {
+          const int u = (wid - 1) + kMappers * e;
+          outside |= u < kSB && lane + kLanes * (j * kSB + u) < len &&
+                     (uint32_t)(cb[e] - tb.t_lo) >= (uint32_t)tb.nt;
+        }
+        lds = __ballot(outside) == 0;
       }
-      EncSym s[kSB];
-      if (lds) {
+      if (lds) map_steps(j, std::true_type{});
+      else map_steps(j, std::false_type{});
+    };
+
+    // The coder and the mappers run separate code (the wave role is uniform
+    // per wave) that meets at the same barriers: one before the first block
+    // and one per block.  Keeping the roles apart also keeps the mappers'
+    // loads in flight out of the coder's wait bookkeeping.
+    if (wid == 0) {
+      __syncthreads();
+      for (int j = nblk - 1; j >= 0; --j) {
+        // coder: steps of block j, last to first
+        if (fl - wp > kRingWords - kSB * kLanes) {
+          ring_flush(wbuf, ring, wp, fl, lane);
+          fl = wp;
+        }
+        const uint4* src = recs + (j & 1) * kSB * kLanes;
+        uint4 r[kSB];
+        uint32_t mt[kSB];
 #pragma unroll
-        for (int u = 0; u < kSB; ++u)
-          s[u] = enc_map<kLatents, kImplicit, true>(a, tb, lane, j * kSB + u, len, start, ca[u],
-                                                    cb[u], cm[u], hash, status);
-      } else {
+        for (int u = 0; u < kSB; ++u) {
+          r[u] = src[u * kLanes + lane];
+          mt[u] = (uint32_t)uni((int)info[(j & 1) * kSB + u]);
+        }
+        uint32_t any_esc = 0;
 #pragma unroll
-        for (int u = 0; u < kSB; ++u)
-          s[u] = enc_map<kLatents, kImplicit, false>(a, tb, lane, j * kSB + u, len, start, ca[u],
-                                                     cb[u], cm[u], hash, status);
-      }
+        for (int u = 0; u < kSB; ++u) any_esc |= mt[u];
+        if ((j + 1) * kSB <= T && any_esc == 0) {
+          // common case: a full block without escapes, no per-step branches
 #pragma unroll
-      for (int u = kSB - 1; u >= 0; --u) {
-        if (j * kSB + u >= T) continue;
-        const EncSym& e = s[u];
-        if (__ballot(e.esc) == 0) {
-          emit_words((x >> 16) >= e.fr, x, ring, wbuf, wp, fl, lane);
-          x = enc_main(x, e.st, e.fr, e.rcp);
+          for (int u = kSB - 1; u >= 0; --u) {
+            emit_words<false>((x >> 16) >= 65536u - (r[u].x >> 16), x, ring, wbuf, wp, fl, lane);
+            x = enc_apply(x, r[u]);
+          }
         } else {
-          // escape sub-rounds, decode order d = 0 (main), 1 (count), 2.. (nibbles);
-          // encoded from the last op to the first
-          uint32_t raw, nops;
-          enc_escape_split(e, raw, nops, status);
-          const int Mt = uni(wave_max((int)nops));
-          for (int d = Mt - 1; d >= 0; --d) {
-            const bool part = (uint32_t)d < nops;
-            const bool want = d == 0 ? (x >> 16) >= e.fr : x >= kBitsEmit;
-            const uint32_t x0 = x;
-            emit_words(part & want, x, ring, wbuf, wp, fl, lane);
-            uint32_t xn;
-            if (d == 0) {
-              xn = enc_main(x, e.st, e.fr, e.rcp);
-            } else {
-              const uint32_t val = d == 1 ? nops - 2u : (raw >> (4 * (d - 2))) & 15u;
-              xn = (x << 4) | val;
+#pragma unroll
+        for (int u = kSB - 1; u >= 0; --u) {
+          if (j * kSB + u >= T) continue;
+          const uint4 e = r[u];
+          const uint32_t fr = 65536u - (e.x >> 16);
+          if (mt[u] == 0) {
+            emit_words<false>((x >> 16) >= fr, x, ring, wbuf, wp, fl, lane);
+            x = enc_apply(x, e);
+          } else {
+            // escape sub-rounds in decode order d = 0 (main), 1 (count),
+            // 2.. (nibbles), encoded from the last op to the first
+            const uint32_t nops = e.z >> 8;
+            for (int d = (int)mt[u] - 1; d >= 0; --d) {
+              const bool part_d = (uint32_t)d < nops;
+              const bool want = d == 0 ? (x >> 16) >= fr : x >= kBitsEmit;
+              const uint32_t x0 = x;
+              emit_words<true>(part_d & want, x, ring, wbuf, wp, fl, lane);
+              uint32_t xn;
+              if (d == 0) {
+                xn = enc_apply(x, e);
+              } else {
+                const uint32_t val = d == 1 ? nops - 2u : (e.w >> (4 * (d - 2))) & 15u;
+                xn = (x << 4) | val;
+              }
+              x = part_d ? xn : x0;
             }
-            x = part ? xn : x0;
           }
         }
+        }
+        __syncthreads();
       }
+      if (fl > wp) ring_flush(wbuf, ring, wp, fl, lane);
+    } else {
+      if (nblk > 0) {
+        load_block(nblk - 1, ca, cb, cm);
+        if (nblk > 1) load_block(nblk - 2, na, nb, nm);
+        map_block(nblk - 1);
+      }
+      __syncthreads();
+      for (int j = nblk - 1; j >= 0; --j) {
+        if (j > 0) {  // mappers: block j - 1 while the coder codes block j
 #pragma unroll
-      for (int u = 0; u < kSB; ++u) {
-        ca[u] = na[u];
-        cb[u] = nb[u];
-        cm[u] = nm[u];
+          for (int e = 0; e < kPer; ++e) {
+            ca[e] = na[e];
+            cb[e] = nb[e];
+            cm[e] = nm[e];
+          }
+          if (j > 1) load_block(j - 2, na, nb, nm);
+          map_block(j - 1);
+        }
+        __syncthreads();
       }
     }
-    if (fl > wp) ring_flush(wbuf, ring, wp, fl, lane);
-  } else {
-    status |= GAANS_ST_TABLES;
   }
 
-  if (lane < A) a.states[(int64_t)g * kLanes + lane] = x;
+  if (wid == 0 && lane < A) a.states[g * kLanes + lane] = x;
   hash = wave_sum(hash);
   status = wave_or(status);
   if (lane == 0) {
+    part[wid] = hash;
+    part[kWaves + wid] = status;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t hs = 0, ss = 0;
+    for (int w = 0; w < kWaves; ++w) {
+      hs += part[w];
+      ss |= part[kWaves + w];
+    }
     a.chunk_words[g] = (uint32_t)(a.cap_words - wp);
-    a.chunk_status[g] = status;
-    a.index_hash[g] = hash;
+    a.chunk_status[g] = ss;
+    a.index_hash[g] = hs;
   }
   __threadfence();
   __syncthreads();
-  uint32_t done = 0;
-  if (lane == 0)
-    done = __hip_atomic_fetch_add(&a.ctrl[kCtrlEncDone], 1u, __ATOMIC_ACQ_REL,
-                                  __HIP_MEMORY_SCOPE_AGENT);
-  done = (uint32_t)__shfl((int)done, 0, 64);
-  if (done == (uint32_t)(a.BK - 1)) {
-    __threadfence();
-    encode_finish(a, lane);
+  if (wid == 0) {
+    uint32_t done = 0;
+    if (lane == 0)
+      done = __hip_atomic_fetch_add(&a.ctrl[kCtrlEncDone], 1u, __ATOMIC_ACQ_REL,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    done = (uint32_t)__shfl((int)done, 0, 64);
+    if (done == (uint32_t)(a.BK - 1)) {
+      __threadfence();
+      encode_finish(a, lane);
+    }
   }
 }
 
@@ -673,48 +826,65 @@ struct DecArgs {
   uint32_t* __restrict__ status_out;
 };
 
-struct DecMeta {
-  uint32_t lbase, ebase, nsym;
-  int32_t offset;
-};
+// Decoder LDS layout (bytes); the median buffer is there for latents only
+constexpr int kDecRingBytes = 2 * kStreamRing;
+constexpr int kDecRecBytes = 2 * kSB * kLanes * 16;
+constexpr int kDecInfoBytes = 2 * kSB * 4;
+constexpr int kDecMedBytes = 2 * kSB * kLanes * 4;
+constexpr int dec_fixed_lds(bool latents) {
+  return kDecRingBytes + kDecRecBytes + kDecInfoBytes + kPartBytes +
+         (latents ? kDecMedBytes : 0);
+}
 
-// Per-step table metadata (branch-free), index hash and index checks.
-template <bool kImplicit, bool kLds>
-__device__ __forceinline__ DecMeta dec_map(const DecArgs& a, const Tabs& tb, int lane, int t,
-                                           int len, int32_t start, int32_t in_b,
-                                           uint32_t& hash, uint32_t& status) {
+// Mapper record of one lane and step (16 bytes), tables in LDS when the
+// step's flag is 1:
+//   x: the lane's table (LDS-local or global index)
+//   y: escape symbol (nsym - 1), or 0xffffffff for a lane past the chunk end
+//   z: table offset            w: first entry of the table
+// The coder overwrites x with the decoded value.
+template <bool kImplicit>
+__device__ __forceinline__ uint4 dec_record(const DecArgs& a, const Tabs& tb, int lane, int t,
+                                            int len, int32_t start, int32_t in_b,
+                                            uint32_t& hash, uint32_t& status, bool& all_lds) {
   const int p = lane + kLanes * t;
   const bool act = p < len;
   int32_t tbi = kImplicit ? (int32_t)udiv((uint32_t)(start + p), a.div_hw) : in_b;
   const bool bad = act & ((uint32_t)tbi >= a.M);
   const bool ok = act & !bad;
   status |= bad ? GAANS_ST_INDEX : 0u;
-  tbi = ok ? tbi : (kLds ? tb.t_lo : 0);
+  tbi = ok ? tbi : (tb.nt > 0 ? tb.t_lo : 0);
   hash += ok ? ((uint32_t)(tbi + 1) ^ ((uint32_t)p * kHashMul)) : 0u;
-  DecMeta m;
-  if (kLds) {
+  const bool staged = (uint32_t)(tbi - tb.t_lo) < (uint32_t)tb.nt;
+  all_lds = __ballot(!staged) == 0;
+  uint32_t nsym, ebase;
+  int32_t offset;
+  if (all_lds) {
     const uint4 lm = tb.lmeta[tbi - tb.t_lo];
-    m.ebase = lm.x;
-    m.nsym = lm.y;
-    m.offset = (int32_t)lm.z;
-    m.lbase = (uint32_t)(tbi - tb.t_lo) * kLutSize;
+    ebase = lm.x;
+    nsym = lm.y;
+    offset = (int32_t)lm.z;
   } else {
     const TabMeta gm = tb.gmeta[tbi];
-    m.ebase = gm.ent_base;
-    m.nsym = gm.nsym;
-    m.offset = gm.offset;
-    m.lbase = gm.lut_base;
+    ebase = gm.ent_base;
+    nsym = gm.nsym;
+    offset = gm.offset;
   }
-  return m;
+  uint4 r;
+  r.x = (uint32_t)(all_lds ? tbi - tb.t_lo : tbi);
+  r.y = act ? nsym - 1u : 0xffffffffu;
+  r.z = (uint32_t)offset;
+  r.w = ebase;
+  return r;
 }
 
-// cum -> (symbol, start, freq).  One lookup resolves every bucket with at most
-// one symbol boundary; buckets with more (the marker 0xffff) are searched.
+// cum -> (symbol, start, freq).  One lookup resolves every bucket in which at
+// most one other symbol starts; a dense bucket (marker 0xffff) reads the
+// symbol from its dense block and then the symbol's entry.
 template <bool kLds>
-__device__ __forceinline__ void dec_lookup(const Tabs& tb, const DecMeta& m, uint32_t cum,
-                                           bool act, uint32_t& s, uint32_t& st, uint32_t& fr) {
-  const uint64_t e = kLds ? tb.llut[m.lbase + (cum >> (16 - kLutBits))]
-                          : tb.glut[m.lbase + (cum >> (16 - kLutBits))];
+__device__ __forceinline__ void dec_lookup(const Tabs& tb, const uint4 r, uint32_t cum, bool act,
+                                           uint32_t& s, uint32_t& st, uint32_t& fr) {
+  const uint32_t li = (r.x << kLutBits) + (cum >> (16 - kLutBits));
+  const uint64_t e = kLds ? tb.llut[li] : tb.glut[li];
   const uint32_t lo = (uint32_t)e, hi = (uint32_t)(e >> 32);
   const uint32_t s0 = hi & 0xffffu, nxt = hi >> 16;
   const uint32_t st0 = lo & 0xffffu, fr0 = (lo >> 16) + 1u;
@@ -722,86 +892,111 @@ __device__ __forceinline__ void dec_lookup(const Tabs& tb, const DecMeta& m, uin
   s = up ? s0 + 1u : s0;
   st = up ? st0 + fr0 : st0;
   fr = up ? nxt + 1u : fr0;
-  const bool slow = act & (nxt == 0xffffu);
-  if (__ballot(slow)) {
-    if (slow) {
-      // largest s' in [s0, s0 + 256] with start(s') <= cum (a bucket spans 256 values)
-      uint32_t a0 = s0, b0 = s0 + (1u << (16 - kLutBits));
-      if (b0 > m.nsym - 1u) b0 = m.nsym - 1u;
-      while (a0 < b0) {
-        const uint32_t mid = (a0 + b0 + 1u) >> 1;
-        const uint32_t en = kLds ? tb.lent[m.ebase + mid] : tb.gent[m.ebase + mid];
-        if ((en & 0xffffu) <= cum) a0 = mid;
-        else b0 = mid - 1u;
-      }
-      const uint32_t en = kLds ? tb.lent[m.ebase + a0] : tb.gent[m.ebase + a0];
-      s = a0;
-      st = en & 0xffffu;
-      fr = (en >> 16) + 1u;
-    }
+  if (act & (nxt == 0xffffu)) {
+    const uint32_t blk = kLds ? lo - tb.dense_first : lo;
+    const uint32_t di = (blk << kLutBits) + (cum & (kLutSize - 1));
+    s = s0 + (uint32_t)(kLds ? tb.ldense[di] : tb.gdense[di]);
+    const uint32_t en = kLds ? tb.lent32[r.w + s] : tb.gent[r.w + s].x;
+    st = en & 0xffffu;
+    fr = (en >> 16) + 1u;
   }
 }
 
 // Word stream of one chunk: prefetched from HBM into registers (kPfWords words
 // ahead) and copied into an LDS ring that refills read from.
+// The word stream of a chunk is copied into an LDS ring holding the words
+// [rp, filled) (positions mod kStreamRing), kPfWords words at a time.
+//  - At the start of every block the coder commits the batch prefetched into
+//    registers (pf, words [filled, filled + kPfWords)) when fewer than
+//    kLowWater words are buffered, then prefetches the next batch.  This is the
+//    only place pf is loaded, so the loads stay in flight between blocks.
+//  - The main-op refills of a block (at most one word per lane and step) need
+//    no check: a block starts with at least kSB * kLanes buffered words.
+//  - Escape refills check that margin and, when a block has consumed that
+//    much, copy the next batch synchronously (its own loads; pf is marked stale
+//    and refetched at the next block start).
+constexpr int kLowWater = 1024;
+static_assert(kLowWater >= kSB * kLanes && kLowWater + kPfWords <= kStreamRing,
+              "decoder stream ring too small");
 struct Stream {
   const uint32_t* __restrict__ s32;
   const uint32_t* __restrict__ safe;  // an in-bounds word of the chunk
   int q, q32, rp, filled;
+  bool pf_live;  // pf holds words [filled, filled + kPfWords)
   uint32_t pf[kPfU32];
 };
 
 // Words past the stream end read the chunk's first state word instead (always
-// in bounds) and are replaced by zero, so the loads need no branch.
-__device__ __forceinline__ void stream_fetch(Stream& S, int lane) {
+// in bounds), so the loads need no branch; a refill that reaches them marks
+// the chunk corrupt.
+__device__ __forceinline__ uint32_t stream_word32(const Stream& S, int i32) {
+  return *(i32 < S.q32 ? S.s32 + i32 : S.safe);
+}
+
+// Block start: commit pf if needed, then (re)fetch pf.
+__device__ __forceinline__ void stream_block_start(Stream& S, uint32_t* ring32, int lane) {
+  const bool commit = S.pf_live && S.filled - S.rp < kLowWater && S.filled < S.q;
+  if (commit) {
 #pragma unroll
-  for (int kk = 0; kk < kPfU32; ++kk) {
-    const int i32 = (S.filled >> 1) + kk * kLanes + lane;
-    const bool in = i32 < S.q32;
-    const uint32_t w = *(in ? S.s32 + i32 : S.safe);
-    S.pf[kk] = in ? w : 0u;
+    for (int kk = 0; kk < kPfU32; ++kk)
+      ring32[((S.filled >> 1) + kk * kLanes + lane) & (kStreamRing / 2 - 1)] = S.pf[kk];
+    S.filled = uni(S.filled + kPfWords);
+  }
+  if (commit || !S.pf_live) {
+#pragma unroll
+    for (int kk = 0; kk < kPfU32; ++kk)
+      S.pf[kk] = stream_word32(S, (S.filled >> 1) + kk * kLanes + lane);
+    S.pf_live = true;
   }
 }
 
-__device__ __forceinline__ void stream_commit(Stream& S, uint32_t* ring32, int lane) {
+// Escape refill with fewer than kSB * kLanes buffered words: copy the next
+// batch now.
+__device__ __forceinline__ void stream_sync_batch(Stream& S, uint32_t* ring32, int lane) {
+  uint32_t w[kPfU32];
+#pragma unroll
+  for (int kk = 0; kk < kPfU32; ++kk) w[kk] = stream_word32(S, (S.filled >> 1) + kk * kLanes + lane);
 #pragma unroll
   for (int kk = 0; kk < kPfU32; ++kk)
-    ring32[((S.filled >> 1) + kk * kLanes + lane) & (kStreamRing / 2 - 1)] = S.pf[kk];
+    ring32[((S.filled >> 1) + kk * kLanes + lane) & (kStreamRing / 2 - 1)] = w[kk];
   S.filled = uni(S.filled + kPfWords);
-  stream_fetch(S, lane);
+  S.pf_live = false;
 }
 
+// A refill past the stream end reads stale ring words; the chunk is then
+// marked corrupt by the final check that exactly the stream was consumed.
+template <bool kCheck>
 __device__ __forceinline__ void dec_refill(bool need, uint32_t& x, Stream& S,
-                                           const uint16_t* ring, uint32_t* ring32,
-                                           uint32_t& status, int lane) {
-  if (S.filled - S.rp < kLanes && S.filled < S.q) stream_commit(S, ring32, lane);
+                                           const uint16_t* ring, uint32_t* ring32, int lane) {
+  if (kCheck && S.filled - S.rp < kSB * kLanes && S.filled < S.q)
+    stream_sync_batch(S, ring32, lane);
   const uint64_t m = __ballot(need);
-  const int r = S.rp + (int)lane_rank(m);
-  const uint32_t w = ring[r & (kStreamRing - 1)];
-  status |= (need & (r >= S.q)) ? GAANS_ST_CORRUPT : 0u;
+  const uint32_t w = ring[(S.rp + (int)lane_rank(m)) & (kStreamRing - 1)];
   x = need ? ((x << 16) | w) : x;
-  S.rp = uni(S.rp + __popcll(m));
+  S.rp += __popcll(m);
 }
 
-template <bool kLatents, bool kLds>
-__device__ __forceinline__ void dec_step(const DecArgs& a, const Tabs& tb, const DecMeta& m,
-                                         int lane, int t, int len, int64_t row, int32_t start,
-                                         float med, uint32_t& x, Stream& S, const uint16_t* ring,
-                                         uint32_t* ring32, uint32_t& status) {
-  const int p = lane + kLanes * t;
-  const bool act = p < len;
+// One decode step of the coder wave; returns the decoded value.
+template <bool kLds>
+__device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint4 r, uint32_t& x,
+                                             Stream& S, const uint16_t* ring, uint32_t* ring32,
+                                             uint32_t& status, int lane) {
+  const bool act = r.y != 0xffffffffu;
   const uint32_t cum = x & 0xffffu;
   uint32_t s, st, fr;
-  dec_lookup<kLds>(tb, m, cum, act, s, st, fr);
+  dec_lookup<kLds>(tb, r, cum, act, s, st, fr);
   const uint32_t xn = __umul24(fr, x >> 16) + cum - st;
   x = act ? xn : x;
-  dec_refill(act & (x < kStateLow), x, S, ring, ring32, status, lane);
-  const bool esc = act & (s == m.nsym - 1u);
-  int64_t value = (int64_t)s;
+  dec_refill<false>(act & (x < kStateLow), x, S, ring, ring32, lane);
+  const bool esc = s == r.y;
+  // value + offset for an ordinary symbol: s < 2^16, so the int32 sum overflows
+  // exactly when it wraps below the offset
+  int32_t o = (int32_t)(s + r.z);
+  bool oob = o < (int32_t)r.z;
   if (__ballot(esc)) {
     uint32_t n = esc ? (x & 15u) : 0u;
     x = esc ? (x >> 4) : x;
-    dec_refill(esc & (x < kStateLow), x, S, ring, ring32, status, lane);
+    dec_refill<true>(esc & (x < kStateLow), x, S, ring, ring32, lane);
     const bool badn = n > 8u;
     status |= (esc & badn) ? GAANS_ST_CORRUPT : 0u;
     n = badn ? 0u : n;
@@ -811,39 +1006,42 @@ __device__ __forceinline__ void dec_step(const DecArgs& a, const Tabs& tb, const
       if (__ballot(part) == 0) break;
       raw |= part ? ((x & 15u) << (4 * jj)) : 0u;
       x = part ? (x >> 4) : x;
-      dec_refill(part & (x < kStateLow), x, S, ring, ring32, status, lane);
+      dec_refill<true>(part & (x < kStateLow), x, S, ring, ring32, lane);
     }
-    const int64_t maxv = (int64_t)m.nsym - 1;
-    const int64_t ev = (raw & 1u) ? -(int64_t)(raw >> 1) - 1 : (int64_t)(raw >> 1) + maxv;
-    value = esc ? ev : value;
+    const int64_t ev = (raw & 1u) ? -(int64_t)(raw >> 1) - 1 : (int64_t)(raw >> 1) + r.y;
+    const int64_t sv = ev + (int32_t)r.z;
+    o = esc ? (int32_t)sv : o;
+    oob = esc ? ((sv < INT32_MIN) | (sv > INT32_MAX)) : oob;
   }
-  int64_t sv = value + m.offset;
-  const bool oob = act & ((sv < INT32_MIN) | (sv > INT32_MAX));
+  oob &= act;
   status |= oob ? GAANS_ST_CORRUPT : 0u;
-  if (act) {
-    const int64_t i = row + start + p;
-    const int32_t o = oob ? 0 : (int32_t)sv;
-    if (kLatents) a.out_y[i] = __fadd_rn((float)o, med);
-    else a.out_sym[i] = o;
-  }
+  return (uint32_t)(oob ? 0 : o);
 }
 
 template <bool kLatents, bool kImplicit>
-__global__ __launch_bounds__(64) void k_decode(DecArgs a) {
+__global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t* sring = reinterpret_cast<uint16_t*>(smem);
   uint32_t* sring32 = reinterpret_cast<uint32_t*>(smem);
-  uint64_t* llut = reinterpret_cast<uint64_t*>(smem + 2 * kStreamRing);
-  uint4* lmeta = reinterpret_cast<uint4*>(smem + 2 * kStreamRing + 8 * kLutSize * a.nt_cap);
-  uint32_t* lent = reinterpret_cast<uint32_t*>(smem + 2 * kStreamRing +
-                                               (8 * kLutSize + 16) * a.nt_cap);
+  uint4* recs = reinterpret_cast<uint4*>(smem + kDecRingBytes);
+  uint32_t* info = reinterpret_cast<uint32_t*>(smem + kDecRingBytes + kDecRecBytes);
+  uint32_t* part = info + 2 * kSB;  // per-wave hash [0, kWaves) and status [kWaves, 2 kWaves)
+  float* med = reinterpret_cast<float*>(smem + kDecRingBytes + kDecRecBytes + kDecInfoBytes +
+                                        kPartBytes);
+  uint8_t* tsm = smem + dec_fixed_lds(kLatents);
+  uint64_t* llut = reinterpret_cast<uint64_t*>(tsm);
+  uint4* lmeta = reinterpret_cast<uint4*>(tsm + 8 * kLutSize * a.nt_cap);
+  uint32_t* lent32 = reinterpret_cast<uint32_t*>(tsm + (8 * kLutSize + 16) * a.nt_cap);
+  uint8_t* ldense = tsm + (8 * kLutSize + 16) * a.nt_cap + 4 * a.ne_cap;
 
   const int64_t g = blockIdx.x;
-  const int lane = threadIdx.x;
-  uint32_t status = 0;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kLanes - 1);
+  const int wid = uni(tid >> 6);  // wave role, kept in a scalar register
+  uint32_t status = 0, hash = 0;
   const uint32_t* __restrict__ hdr = reinterpret_cast<const uint32_t*>(a.payload);
   const TabHdr* th = reinterpret_cast<const TabHdr*>(a.tables);
-  bool ok = true;
+  bool ok = true;  // uniform over the workgroup
   if (a.payload_bytes < a.header_bytes || hdr[0] != kMagic || hdr[1] != kVersion ||
       hdr[2] != a.B || hdr[3] != (uint32_t)a.N || hdr[4] != a.C || hdr[5] != a.P ||
       hdr[6] != a.K || hdr[7] != a.chunk_len || hdr[8] != a.M || hdr[9] != kParams) {
@@ -854,15 +1052,13 @@ __global__ __launch_bounds__(64) void k_decode(DecArgs a) {
     status |= GAANS_ST_TABLES;
     ok = false;
   }
-  const int64_t b = g / a.K;
-  const int k = (int)(g - b * a.K);
-  const int64_t row = b * a.N;
-  const int32_t start = k * (int32_t)a.chunk_len;
-  const int32_t endp = (int64_t)start + a.chunk_len < a.N ? start + (int32_t)a.chunk_len
-                                                            : (int32_t)a.N;
-  const int len = endp - start;
+  int64_t row;
+  int32_t start;
+  int len, k;
+  chunk_range(g, a.K, a.N, (int32_t)a.chunk_len, row, start, len, k);
   const int T = (len + kLanes - 1) / kLanes;
   const int A = len < kLanes ? len : kLanes;
+  const int nblk = (T + kSB - 1) / kSB;
   uint32_t beg = 0, endo = 0, want_hash = 0;
   int64_t cb = 0;
   if (ok) {
@@ -870,8 +1066,8 @@ __global__ __launch_bounds__(64) void k_decode(DecArgs a) {
     endo = hdr[kFixedWords + g];
     want_hash = hdr[kFixedWords + a.BK + g];
     cb = (int64_t)endo - (int64_t)beg;
-    if (endo < beg || (int64_t)endo > a.payload_bytes - a.header_bytes || cb < 4 * A ||
-        ((cb - 4 * A) & 3)) {
+    if (endo < beg || (int64_t)endo > a.payload_bytes - a.header_bytes || (beg & 3u) ||
+        cb < 4 * A || ((cb - 4 * A) & 3)) {
       status |= GAANS_ST_CORRUPT;
       ok = false;
     }
@@ -879,110 +1075,168 @@ __global__ __launch_bounds__(64) void k_decode(DecArgs a) {
   if (ok) {
     Tabs tb;
     tb.gmeta = reinterpret_cast<const TabMeta*>(a.tables + th->meta_off);
-    tb.gent = reinterpret_cast<const uint32_t*>(a.tables + th->ent_off);
+    tb.gent = reinterpret_cast<const uint2*>(a.tables + th->ent_off);
     tb.glut = reinterpret_cast<const uint64_t*>(a.tables + th->lut_off);
+    tb.gdense = a.tables + th->dense_off;
     tb.lmeta = lmeta;
-    tb.lent = lent;
+    tb.lent = nullptr;
+    tb.lent32 = lent32;
     tb.llut = llut;
-    int t_lo = 0, t_hi = 0;
-    if (a.nt_cap > 0) {
-      if (a.stage_all) {
-        t_hi = (int)a.M;
-      } else {
-        t_lo = k * (int)a.P;
-        t_hi = t_lo + (int)a.P < (int)a.M ? t_lo + (int)a.P : (int)a.M;
-      }
-    }
-    stage_tables(tb, lmeta, lent, llut, t_lo, t_hi, lane);
+    tb.ldense = ldense;
+    int t_lo, t_hi;
+    stage_range(a.nt_cap, a.stage_all, k, (int)a.P, (int)a.M, t_lo, t_hi);
+    stage_tables(tb, lmeta, nullptr, lent32, llut, ldense, th->total_dense, a.M, t_lo, t_hi,
+                 tid);
 
     const uint8_t* cdata = a.payload + a.header_bytes + beg;
-    Stream S;
-    S.s32 = reinterpret_cast<const uint32_t*>(cdata + 4 * A);
-    S.safe = reinterpret_cast<const uint32_t*>(cdata);
-    S.q = (int)((cb - 4 * A) / 2);  // stream words incl. pad (even)
-    S.q32 = S.q / 2;
-    S.rp = 0;
-    S.filled = 0;
-    stream_fetch(S, lane);
-    stream_commit(S, sring32, lane);
 
-    uint32_t x = lane < A ? reinterpret_cast<const uint32_t*>(cdata)[lane] : kStateLow;
-    uint32_t hash = 0;
-
-    int32_t cbx[kSB], nbx[kSB];
-    float cm[kSB], nm[kSB];
+    int32_t cbx[kPer], nbx[kPer];
+    float cm[kPer], nm[kPer];
     auto load_block = [&](int j, int32_t* ib, float* im) {
 #pragma unroll
-      for (int u = 0; u < kSB; ++u) {
+      for (int e = 0; e < kPer; ++e) {
+        const int u = (wid - 1) + kMappers * e;
+        if (kSB % kMappers != 0 && u >= kSB) break;
         int p = lane + kLanes * (j * kSB + u);
-        p = p < len ? p : len - 1;
-        ib[u] = kImplicit ? 0 : a.indexes[row + start + p];
-        im[u] = kLatents ? a.medians[udiv((uint32_t)(start + p), a.div_hw)] : 0.0f;
+        p = p < len ? p : len - 1;  // loads stay in the chunk; results are masked
+        ib[e] = kImplicit ? 0 : a.indexes[row + start + p];
+        im[e] = kLatents ? a.medians[udiv((uint32_t)(start + p), a.div_hw)] : 0.0f;
       }
     };
-    const int nblk = (T + kSB - 1) / kSB;
-    if (nblk > 0) load_block(0, cbx, cm);
-    for (int j = 0; j < nblk; ++j) {
-      if (j + 1 < nblk) load_block(j + 1, nbx, nm);
-      bool lds = tb.nt > 0;
-      if (!kImplicit && lds) {
-        bool in = true;
+    auto store_block = [&](int j) {  // decoded values of block j -> HBM
+      const uint4* src = recs + (j & 1) * kSB * kLanes;
 #pragma unroll
-        for (int u = 0; u < kSB; ++u)
-          in = in && (lane + kLanes * (j * kSB + u) >= len ||
-                      (uint32_t)(cbx[u] - tb.t_lo) < (uint32_t)tb.nt);
-        lds = __ballot(!in) == 0;
+      for (int e = 0; e < kPer; ++e) {
+        const int u = (wid - 1) + kMappers * e;
+        if (kSB % kMappers != 0 && u >= kSB) break;
+        const uint32_t v = src[u * kLanes + lane].x;
+        const int p = lane + kLanes * (j * kSB + u);
+        if (p < len) {
+          const int64_t i = row + start + p;
+          if (kLatents)
+            a.out_y[i] = __fadd_rn((float)(int32_t)v, med[((j & 1) * kSB + u) * kLanes + lane]);
+          else a.out_sym[i] = (int32_t)v;
+        }
       }
-      DecMeta ms[kSB];
-      if (lds) {
+    };
+    auto map_block = [&](int j) {
+      uint4* dst = recs + (j & 1) * kSB * kLanes;
 #pragma unroll
-        for (int u = 0; u < kSB; ++u)
-          ms[u] = dec_map<kImplicit, true>(a, tb, lane, j * kSB + u, len, start, cbx[u], hash,
-                                           status);
-#pragma unroll
-        for (int u = 0; u < kSB; ++u)
-          if (j * kSB + u < T)
-            dec_step<kLatents, true>(a, tb, ms[u], lane, j * kSB + u, len, row, start, cm[u], x,
-                                     S, sring, sring32, status);
-      } else {
-#pragma unroll
-        for (int u = 0; u < kSB; ++u)
-          ms[u] = dec_map<kImplicit, false>(a, tb, lane, j * kSB + u, len, start, cbx[u], hash,
-                                            status);
-#pragma unroll
-        for (int u = 0; u < kSB; ++u)
-          if (j * kSB + u < T)
-            dec_step<kLatents, false>(a, tb, ms[u], lane, j * kSB + u, len, row, start, cm[u],
-                                      x, S, sring, sring32, status);
+      for (int e = 0; e < kPer; ++e) {
+        const int u = (wid - 1) + kMappers * e;
+        if (kSB % kMappers != 0 && u >= kSB) break;
+        bool all_lds;
+        const uint4 r = dec_record<kImplicit>(a, tb, lane, j * kSB + u, len, start, cbx[e], hash,
+                                              status, all_lds);
+        dst[u * kLanes + lane] = r;
+        if (kLatents) med[((j & 1) * kSB + u) * kLanes + lane] = cm[e];
+        if (lane == 0) info[(j & 1) * kSB + u] = all_lds ? 1u : 0u;
       }
+    };
+
+    // The coder and the mappers run separate code (the wave role is uniform
+    // per wave) that meets at the same barriers: one before the first block
+    // and one per block.  Keeping the roles apart also keeps the mappers'
+    // loads in flight out of the coder's wait bookkeeping.
+    if (wid == 0) {
+      Stream S;
+      S.s32 = reinterpret_cast<const uint32_t*>(cdata + 4 * A);
+      S.safe = reinterpret_cast<const uint32_t*>(cdata);
+      S.q = (int)((cb - 4 * A) / 2);  // stream words incl. pad (even)
+      S.q32 = S.q / 2;
+      S.rp = 0;
+      S.filled = 0;
+      S.pf_live = false;
+      // the initial states are loaded first, so that waiting for them does not
+      // also wait for the stream prefetch
+      uint32_t x = lane < A ? reinterpret_cast<const uint32_t*>(cdata)[lane] : kStateLow;
+      for (int b = 0; b < kLowWater / kPfWords; ++b) stream_sync_batch(S, sring32, lane);
+      __syncthreads();
+      for (int j = 0; j < nblk; ++j) {
+        stream_block_start(S, sring32, lane);
+        uint4* src = recs + (j & 1) * kSB * kLanes;
+        uint4 r[kSB];
+        uint32_t fl[kSB], ov[kSB];
 #pragma unroll
-      for (int u = 0; u < kSB; ++u) {
-        cbx[u] = nbx[u];
-        cm[u] = nm[u];
+        for (int u = 0; u < kSB; ++u) {
+          r[u] = src[u * kLanes + lane];
+          fl[u] = (uint32_t)uni((int)info[(j & 1) * kSB + u]);
+        }
+        uint32_t all_lds = 1;
+#pragma unroll
+        for (int u = 0; u < kSB; ++u) all_lds &= fl[u];
+        if ((j + 1) * kSB <= T && all_lds) {
+          // common case: a full block with LDS tables, no per-step branches
+#pragma unroll
+          for (int u = 0; u < kSB; ++u)
+            ov[u] = dec_step<true>(tb, r[u], x, S, sring, sring32, status, lane);
+        } else {
+#pragma unroll
+          for (int u = 0; u < kSB; ++u) {
+            ov[u] = 0;
+            if (j * kSB + u >= T) continue;
+            if (fl[u]) ov[u] = dec_step<true>(tb, r[u], x, S, sring, sring32, status, lane);
+            else ov[u] = dec_step<false>(tb, r[u], x, S, sring, sring32, status, lane);
+          }
+        }
+        // decoded values replace the records' x words; the mappers store them
+#pragma unroll
+        for (int u = 0; u < kSB; ++u) reinterpret_cast<uint32_t*>(src + u * kLanes + lane)[0] = ov[u];
+        __syncthreads();
       }
+      if (lane < A && x != kStateLow) status |= GAANS_ST_CORRUPT;
+      if (!(S.rp == S.q || (S.rp == S.q - 1 && (S.q & 1) == 0))) status |= GAANS_ST_CORRUPT;
+    } else {
+      if (nblk > 0) {
+        load_block(0, cbx, cm);
+        if (nblk > 1) load_block(1, nbx, nm);
+        map_block(0);
+      }
+      __syncthreads();
+      for (int j = 0; j < nblk; ++j) {
+        // mappers: store block j - 1 and map block j + 1 while the coder decodes block j
+        if (j > 0) store_block(j - 1);
+        if (j + 1 < nblk) {
+#pragma unroll
+          for (int e = 0; e < kPer; ++e) {
+            cbx[e] = nbx[e];
+            cm[e] = nm[e];
+          }
+          if (j + 2 < nblk) load_block(j + 2, nbx, nm);
+          map_block(j + 1);
+        }
+        __syncthreads();
+      }
+      if (nblk > 0) store_block(nblk - 1);
     }
-    if (lane < A && x != kStateLow) status |= GAANS_ST_CORRUPT;
-    if (!(S.rp == S.q || (S.rp == S.q - 1 && (S.q & 1) == 0))) status |= GAANS_ST_CORRUPT;
-    hash = wave_sum(hash);
-    if (hash != want_hash) status |= GAANS_ST_INDEXHASH;
   }
+  hash = wave_sum(hash);
   status = wave_or(status);
-  if (lane == 0 && status)
-    __hip_atomic_fetch_or(&a.ctrl[kCtrlDecStatus], status, __ATOMIC_RELAXED,
-                          __HIP_MEMORY_SCOPE_AGENT);
-  __threadfence();
+  if (lane == 0) {
+    part[wid] = hash;
+    part[kWaves + wid] = status;
+  }
   __syncthreads();
-  uint32_t done = 0;
-  if (lane == 0)
-    done = __hip_atomic_fetch_add(&a.ctrl[kCtrlDecDone], 1u, __ATOMIC_ACQ_REL,
-                                  __HIP_MEMORY_SCOPE_AGENT);
-  done = (uint32_t)__shfl((int)done, 0, 64);
-  if (done == (uint32_t)(a.BK - 1) && lane == 0) {
-    const uint32_t st = __hip_atomic_exchange(&a.ctrl[kCtrlDecStatus], 0u, __ATOMIC_ACQ_REL,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-    *a.status_out = st;
-    __threadfence_system();
-    __hip_atomic_store(&a.ctrl[kCtrlDecDone], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) {
+    uint32_t hs = 0, st = 0;
+    for (int w = 0; w < kWaves; ++w) {
+      hs += part[w];
+      st |= part[kWaves + w];
+    }
+    if (ok && hs != want_hash) st |= GAANS_ST_INDEXHASH;
+    if (st)
+      __hip_atomic_fetch_or(&a.ctrl[kCtrlDecStatus], st, __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    __threadfence();
+    const uint32_t done = __hip_atomic_fetch_add(&a.ctrl[kCtrlDecDone], 1u, __ATOMIC_ACQ_REL,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    if (done == (uint32_t)(a.BK - 1)) {
+      const uint32_t all = __hip_atomic_exchange(&a.ctrl[kCtrlDecStatus], 0u, __ATOMIC_ACQ_REL,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+      *a.status_out = all;
+      __threadfence_system();
+      __hip_atomic_store(&a.ctrl[kCtrlDecDone], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -999,28 +1253,33 @@ int check_tables_arg(const gaans_tables* t) {
   if (t->M < 1) return fail(GAANS_EINVAL, "table count M must be >= 1");
   if (t->bytes < (int64_t)sizeof(TabHdr) || t->bytes > 0xffffffffll)
     return fail(GAANS_EINVAL, "tables bytes %lld out of range", (long long)t->bytes);
-  if (t->max_nsym < 1 || t->total_nsym < t->max_nsym)
+  if (t->max_nsym < 1 || t->total_nsym < t->max_nsym || t->max_dense < 0 ||
+      t->total_dense < t->max_dense)
     return fail(GAANS_EINVAL, "tables descriptor is inconsistent");
   return GAANS_OK;
 }
 
 // LDS staging plan: all tables if they fit the budget, else the chunk's
-// channel range (P tables), else none.
+// channel range (P tables, bounded by P times the largest table), else none.
 struct Stage {
-  int32_t nt_cap, ne_cap, stage_all;
+  int32_t nt_cap, ne_cap, nd_cap, stage_all;
 };
 
-Stage plan_stage(const gaans_tables* t, int64_t P, int64_t per_table, int64_t budget) {
-  Stage s{0, 0, 0};
-  const int64_t all = t->M * per_table + 4 * t->total_nsym;
-  const int64_t range = P * per_table + 4 * P * (int64_t)t->max_nsym;
+Stage plan_stage(const gaans_tables* t, int64_t P, int64_t per_table, int64_t per_sym,
+                 int64_t per_dense, int64_t budget) {
+  Stage s{0, 0, 0, 0};
+  const int64_t all = t->M * per_table + per_sym * t->total_nsym + per_dense * t->total_dense;
+  const int64_t range = P * (per_table + per_sym * (int64_t)t->max_nsym +
+                             per_dense * (int64_t)t->max_dense);
   if (all <= budget) {
     s.nt_cap = t->M;
     s.ne_cap = (int32_t)t->total_nsym;
+    s.nd_cap = per_dense ? (int32_t)t->total_dense : 0;
     s.stage_all = 1;
   } else if (range <= budget) {
     s.nt_cap = (int32_t)P;
     s.ne_cap = (int32_t)(P * t->max_nsym);
+    s.nd_cap = per_dense ? (int32_t)(P * t->max_dense) : 0;
   }
   return s;
 }
@@ -1039,7 +1298,7 @@ int encode_stage1(bool latents, void* stream, const int32_t* symbols, const floa
     return fail(GAANS_EINVAL, "workspace too small (%lld < %lld bytes)", (long long)ws_bytes,
                 (long long)L.ws_bytes);
   uint8_t* w = static_cast<uint8_t*>(ws);
-  const Stage st = plan_stage(tables, P, 16, kEncTableBudget);
+  const Stage st = plan_stage(tables, P, 16, 8, 0, kLdsMax - kEncFixedLds);
   EncArgs a;
   a.symbols = symbols;
   a.y = y;
@@ -1068,9 +1327,9 @@ int encode_stage1(bool latents, void* stream, const int32_t* symbols, const floa
   a.words = reinterpret_cast<uint16_t*>(w + L.o_words);
   a.ctrl = static_cast<uint32_t*>(ctrl);
   a.info_out = info_out;
-  const size_t lds = 2 * (kRingWords + kLanes) + 16 * (size_t)st.nt_cap + 4 * (size_t)st.ne_cap;
+  const size_t lds = kEncFixedLds + 16 * (size_t)st.nt_cap + 8 * (size_t)st.ne_cap;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid((uint32_t)L.BK), block(kLanes);
+  const dim3 grid((uint32_t)L.BK), block(kThreads);
   if (latents) {
     if (indexes) k_encode<true, false><<<grid, block, lds, s>>>(a);
     else k_encode<true, true><<<grid, block, lds, s>>>(a);
@@ -1094,7 +1353,8 @@ int decode_impl(bool latents, void* stream, const uint8_t* payload, int64_t payl
   if (payload_bytes < L.header_bytes)
     return fail(GAANS_EINVAL, "payload (%lld bytes) is shorter than its header (%lld bytes)",
                 (long long)payload_bytes, (long long)L.header_bytes);
-  const Stage st = plan_stage(tables, P, 8 * kLutSize + 16, kDecTableBudget);
+  const Stage st = plan_stage(tables, P, 8 * kLutSize + 16, 4, kLutSize,
+                              kLdsMax - dec_fixed_lds(latents));
   DecArgs a;
   a.payload = payload;
   a.payload_bytes = payload_bytes;
@@ -1119,10 +1379,10 @@ int decode_impl(bool latents, void* stream, const uint8_t* payload, int64_t payl
   a.stage_all = st.stage_all;
   a.ctrl = static_cast<uint32_t*>(ctrl);
   a.status_out = status_out;
-  const size_t lds = 2 * kStreamRing + (8 * kLutSize + 16) * (size_t)st.nt_cap +
-                     4 * (size_t)st.ne_cap;
+  const size_t lds = dec_fixed_lds(latents) + (8 * kLutSize + 16) * (size_t)st.nt_cap +
+                     4 * (size_t)st.ne_cap + (size_t)kLutSize * st.nd_cap;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid((uint32_t)L.BK), block(kLanes);
+  const dim3 grid((uint32_t)L.BK), block(kThreads);
   if (latents) {
     if (indexes) k_decode<true, false><<<grid, block, lds, s>>>(a);
     else k_decode<true, true><<<grid, block, lds, s>>>(a);
@@ -1141,12 +1401,29 @@ uint64_t fnv_u32(uint64_t h, uint32_t v) {
   return h;
 }
 
-int64_t tables_size(int32_t M, int64_t total_syms) {
+int64_t tables_size(int32_t M, int64_t total_syms, int64_t total_dense) {
   int64_t o = sizeof(TabHdr);
   o += (int64_t)sizeof(TabMeta) * M;
-  o = align_up(o + 4 * total_syms, 8);
+  o = align_up(o, 8) + 8 * total_syms;
   o += 8ll * kLutSize * M;
+  o += (int64_t)kLutSize * total_dense;
   return o;
+}
+
+// Dense decode buckets of one CDF: buckets [j << 8, (j << 8) + 255] in which
+// two or more symbols start after the bucket's first value.
+int32_t count_dense(const int32_t* c, int32_t S) {
+  int32_t n = 0, prev = -1, cnt = 0;
+  for (int32_t v = 1; v + 1 < S; ++v) {  // starts of symbols 1 .. S - 2
+    if ((c[v] & (kLutSize - 1)) == 0) continue;  // starts the bucket itself
+    const int32_t b = c[v] >> (16 - kLutBits);
+    if (b != prev) {
+      prev = b;
+      cnt = 0;
+    }
+    if (++cnt == 2) ++n;
+  }
+  return n;
 }
 
 }  // namespace
@@ -1182,17 +1459,19 @@ int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, gaans_layout* o
   return GAANS_OK;
 }
 
-int gaans_tables_bytes(const int32_t* cdf_sizes, int32_t M, int32_t Lmax, int64_t* bytes) {
-  if (!cdf_sizes || !bytes) return fail(GAANS_EINVAL, "NULL argument");
+int gaans_tables_bytes(const int32_t* cdfs, const int32_t* cdf_sizes, int32_t M, int32_t Lmax,
+                       int64_t* bytes) {
+  if (!cdfs || !cdf_sizes || !bytes) return fail(GAANS_EINVAL, "NULL argument");
   if (M < 1 || Lmax < 2) return fail(GAANS_EINVAL, "need M >= 1 tables of Lmax >= 2 entries");
-  int64_t total = 0;
+  int64_t total = 0, dense = 0;
   for (int32_t t = 0; t < M; ++t) {
     const int32_t S = cdf_sizes[t];
     if (S < 2 || S > Lmax || S > 65537)
       return fail(GAANS_ETABLE, "table %d: cdf size %d outside [2, %d]", t, S, Lmax);
     total += S - 1;
+    dense += count_dense(cdfs + (int64_t)t * Lmax, S);
   }
-  *bytes = tables_size(M, total);
+  *bytes = tables_size(M, total, dense);
   if (*bytes > 0xffffffffll) return fail(GAANS_ETABLE, "tables exceed 4 GiB");
   return GAANS_OK;
 }
@@ -1202,7 +1481,7 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
                          gaans_tables* desc) {
   if (!cdfs || !offsets || !out || !desc) return fail(GAANS_EINVAL, "NULL argument");
   int64_t need = 0;
-  int rc = gaans_tables_bytes(cdf_sizes, M, Lmax, &need);
+  int rc = gaans_tables_bytes(cdfs, cdf_sizes, M, Lmax, &need);
   if (rc) return rc;
   if (out_bytes < need)
     return fail(GAANS_EINVAL, "table buffer too small (%lld < %lld)", (long long)out_bytes,
@@ -1220,16 +1499,23 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
   memset(o, 0, (size_t)need);
   TabHdr* h = reinterpret_cast<TabHdr*>(o);
   TabMeta* meta = reinterpret_cast<TabMeta*>(o + sizeof(TabHdr));
-  const int64_t ent_off = sizeof(TabHdr) + (int64_t)sizeof(TabMeta) * M;
+  const int64_t ent_off = align_up(sizeof(TabHdr) + (int64_t)sizeof(TabMeta) * M, 8);
   uint32_t* ent = reinterpret_cast<uint32_t*>(o + ent_off);
-  int64_t total = 0;
+  int64_t total = 0, total_dense = 0;
   uint32_t max_nsym = 0;
+  int32_t max_dense = 0;
   for (int32_t t = 0; t < M; ++t) {
     total += cdf_sizes[t] - 1;
     if ((uint32_t)(cdf_sizes[t] - 1) > max_nsym) max_nsym = (uint32_t)(cdf_sizes[t] - 1);
+    const int32_t nd = count_dense(cdfs + (int64_t)t * Lmax, cdf_sizes[t]);
+    total_dense += nd;
+    if (nd > max_dense) max_dense = nd;
   }
-  const int64_t lut_off = align_up(ent_off + 4 * total, 8);
+  const int64_t lut_off = ent_off + 8 * total;
   uint64_t* lut = reinterpret_cast<uint64_t*>(o + lut_off);
+  const int64_t dense_off = lut_off + 8ll * kLutSize * M;
+  uint8_t* dense = o + dense_off;
+  uint32_t dblk = 0;
   uint64_t dg = 0xcbf29ce484222325ull;
   dg = fnv_u32(dg, (uint32_t)M);
   uint32_t base = 0;
@@ -1243,13 +1529,13 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
     meta[t].ent_base = base;
     meta[t].nsym = nsym;
     meta[t].offset = offsets[t];
-    meta[t].lut_base = (uint32_t)t * kLutSize;
-    for (uint32_t v = 0; v < nsym; ++v)
-      ent[base + v] = (uint32_t)c[v] | ((uint32_t)(c[v + 1] - c[v] - 1) << 16);
-    // bucket j covers cum in [j << 8, (j << 8) + 255]; low word = entry of
-    // the symbol s holding the bucket's first value; high word = s | next << 16,
-    // next = freq(s + 1) - 1 when the bucket holds at most one boundary, else
-    // the marker 0xffff (freq(s + 1) <= 65535, so next never equals it).
+    meta[t].dense_base = dblk;
+    for (uint32_t v = 0; v < nsym; ++v) {
+      const uint32_t f = (uint32_t)(c[v + 1] - c[v]);
+      ent[2 * (base + v)] = (uint32_t)c[v] | ((f - 1u) << 16);
+      ent[2 * (base + v) + 1] = enc_magic(f);
+    }
+    // bucket j covers cum in [j << 8, (j << 8) + 255]
     uint32_t s = 0;
     for (int j = 0; j < kLutSize; ++j) {
       const uint32_t lo = (uint32_t)j << (16 - kLutBits);
@@ -1257,11 +1543,21 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
       while (s + 1 < nsym && (uint32_t)c[s + 1] <= lo) ++s;
       uint32_t e = s;
       while (e + 1 < nsym && (uint32_t)c[e + 1] <= hi) ++e;
-      uint32_t next = 0;
-      if (e - s >= 2) next = 0xffffu;
-      else if (s + 1 < nsym) next = (uint32_t)(c[s + 2] - c[s + 1] - 1);
-      const uint32_t lo_word = (uint32_t)c[s] | ((uint32_t)(c[s + 1] - c[s] - 1) << 16);
-      const uint32_t hi_word = s | (next << 16);
+      uint32_t lo_word, hi_word;
+      if (e - s >= 2) {  // dense bucket: exact symbol offsets of its 256 values
+        uint8_t* blk = dense + (int64_t)dblk * kLutSize;
+        uint32_t v = s;
+        for (uint32_t i = 0; i < (uint32_t)kLutSize; ++i) {
+          while (v + 1 < nsym && (uint32_t)c[v + 1] <= lo + i) ++v;
+          blk[i] = (uint8_t)(v - s);
+        }
+        lo_word = dblk++;
+        hi_word = s | (0xffffu << 16);
+      } else {
+        const uint32_t next = s + 1 < nsym ? (uint32_t)(c[s + 2] - c[s + 1] - 1) : 0u;
+        lo_word = (uint32_t)c[s] | ((uint32_t)(c[s + 1] - c[s] - 1) << 16);
+        hi_word = s | (next << 16);
+      }
       lut[(int64_t)t * kLutSize + j] = (uint64_t)lo_word | ((uint64_t)hi_word << 32);
     }
     base += nsym;
@@ -1277,12 +1573,17 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
   h->lut_off = (uint32_t)lut_off;
   h->total_bytes = (uint32_t)need;
   h->max_nsym = max_nsym;
+  h->dense_off = (uint32_t)dense_off;
+  h->total_dense = (uint32_t)total_dense;
   desc->dev = nullptr;
   desc->bytes = need;
   desc->M = M;
   desc->max_nsym = (int32_t)max_nsym;
   desc->total_nsym = total;
   desc->digest = dg;
+  desc->max_dense = max_dense;
+  desc->reserved = 0;
+  desc->total_dense = total_dense;
   return GAANS_OK;
 }
 
@@ -1355,7 +1656,7 @@ int gaans_decode_latents(void* stream, const uint8_t* payload_dev, int64_t paylo
 }
 
 int gaans_host_selftest(void) {
-  // 1. magic division: every divisor class against exact division
+  // 1. magic division by the channel length: every divisor class against exact division
   const uint32_t ds[] = {1, 2, 3, 5, 7, 16, 48, 64, 96, 100, 255, 256, 1000, 1536, 4096,
                          32640, 65535, 65536, 65537, 1000003, (1u << 30) - 1, 1u << 30,
                          (1u << 31) - 1};
@@ -1373,24 +1674,23 @@ int gaans_host_selftest(void) {
     if (udiv((1u << 31) - 1u, u) != ((1u << 31) - 1u) / d)
       return fail(1, "udiv selftest failed at n=2^31-1, d=%u", d);
   }
-  // 2. encoder quotient: fp32 reciprocal (exact, and one ulp either side to
-  //    cover v_rcp_f32's error) with one signed correction, for every freq
-  for (uint32_t f = 1; f <= 65536; ++f) {
-    const float r0 = 1.0f / (float)f;
-    const float rs[3] = {r0, nextafterf(r0, 0.0f), nextafterf(r0, 1.0f)};
+  // 2. encoder division: the full-range magic of every freq in [2, 65536] at
+  //    quotient boundaries and at the ends of the coded range [0, f 2^16)
+  for (uint32_t f = 2; f <= 65536; ++f) {
+    const uint32_t m = enc_magic(f), sh = enc_shift(f);
     const uint32_t xmax = (uint32_t)(((uint64_t)f << 16) - 1u);
-    uint32_t xs[8] = {0u, 1u, f - 1u, f, xmax, xmax - 1u, xmax - f, xmax / 2u};
-    for (int k = 0; k < 8; ++k) {
+    const uint32_t xs[10] = {0u, 1u, f - 1u, f, f + 1u, xmax, xmax - 1u, xmax - f,
+                             xmax / 2u, (uint32_t)(((uint64_t)xmax * 2654435761u) >> 32)};
+    for (int k = 0; k < 10; ++k) {
       const uint32_t x = xs[k];
-      if ((uint64_t)x > xmax) continue;
-      for (int j = 0; j < 3; ++j) {
-        uint32_t q = (uint32_t)((float)x * rs[j]);
-        int32_t r = (int32_t)(x - q * f);
-        if (r < 0) { q -= 1u; r += (int32_t)f; }
-        else if (r >= (int32_t)f) { q += 1u; r -= (int32_t)f; }
-        if (q != x / f || (uint32_t)r != x % f)
-          return fail(2, "division selftest failed f=%u x=%u", f, x);
-      }
+      if (enc_div(x, m, sh) != x / f)
+        return fail(2, "encoder division selftest failed f=%u x=%u", f, x);
+    }
+    for (uint32_t qq = 1; qq < 65536u; qq = qq * 3u + 1u) {
+      const uint64_t lo = (uint64_t)qq * f;
+      if (lo > xmax) break;
+      if (enc_div((uint32_t)lo, m, sh) != qq || enc_div((uint32_t)(lo - 1u), m, sh) != qq - 1u)
+        return fail(2, "encoder division selftest failed f=%u q=%u", f, qq);
     }
   }
   return GAANS_OK;

@@ -15,7 +15,7 @@ import threading
 from .errors import CoderDependencyError
 
 LIB_NAME = "libgaans_w64.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 CTRL_BYTES = 256
 
 # return codes
@@ -53,7 +53,8 @@ class Tables(ctypes.Structure):
 
     _fields_ = [("dev", ctypes.c_void_p), ("bytes", ctypes.c_int64), ("M", ctypes.c_int32),
                 ("max_nsym", ctypes.c_int32), ("total_nsym", ctypes.c_int64),
-                ("digest", ctypes.c_uint64)]
+                ("digest", ctypes.c_uint64), ("max_dense", ctypes.c_int32),
+                ("reserved", ctypes.c_int32), ("total_dense", ctypes.c_int64)]
 
 
 def library_path() -> str:
@@ -75,7 +76,7 @@ def _declare(L) -> None:
         "gaans_abi_version": ([], ctypes.c_int),
         "gaans_last_error": ([], ctypes.c_char_p),
         "gaans_get_layout": ([i64, i64, i64, i64, ctypes.POINTER(Layout)], ctypes.c_int),
-        "gaans_tables_bytes": ([p, i32, i32, ctypes.POINTER(ctypes.c_int64)], ctypes.c_int),
+        "gaans_tables_bytes": ([p, p, i32, i32, ctypes.POINTER(ctypes.c_int64)], ctypes.c_int),
         "gaans_tables_prepare": ([p, p, p, i32, i32, p, i64, T], ctypes.c_int),
         "gaans_encode_symbols": ([p, p, p, T, i64, i64, i64, i64, p, i64, p, p], ctypes.c_int),
         "gaans_encode_latents": ([p, p, p, p, T, i64, i64, i64, i64, p, i64, p, p],

@@ -4,8 +4,9 @@ CompressAI keeps ``_quantized_cdf`` as a zero-padded ``[M, Lmax]`` int32
 tensor with ``_cdf_length`` and ``_offset`` (reference
 ``src/fast_compressai/coders/factorized.py:23-31``).  The kernels instead read
 a compact blob built once per table set by ``gaans_tables_prepare``: per-table
-metadata, packed ``start | (freq - 1) << 16`` entries and a 256-bucket
-decode lookup.  The blob also carries the table digest that every payload
+metadata, per-symbol entries (``start | (freq - 1) << 16`` and the
+encoder's division magic of ``freq``), a 256-bucket decode lookup and, for
+buckets in which several symbols start, an exact 256-value block.  The blob also carries the table digest that every payload
 records, so decoding with other tables is detected on the device.
 """
 
@@ -57,7 +58,7 @@ def prepare_tables(cdfs: torch.Tensor, cdf_sizes: torch.Tensor, offsets: torch.T
     o = np.ascontiguousarray(offsets.detach().to("cpu").numpy().astype(np.int32, copy=False))
     L = _native.lib()
     nbytes = ctypes.c_int64(0)
-    rc = L.gaans_tables_bytes(s.ctypes.data, M, Lmax, ctypes.byref(nbytes))
+    rc = L.gaans_tables_bytes(c.ctypes.data, s.ctypes.data, M, Lmax, ctypes.byref(nbytes))
     if rc != _native.OK:
         raise CoderInputError(f"invalid CDF tables: {_native.last_error()}")
     host = np.zeros(nbytes.value, dtype=np.uint8)

@@ -35,8 +35,8 @@
  *    writes to caller memory (device or pinned host memory); read it after
  *    the stream has finished.
  *
- * Payload format "gaans-w64-v1": documented in DESIGN.md and in
- * oracle/gaans_oracle.c (the CPU definition of the bytes).
+ * Payload format "gaans-w64-v1": defined byte for byte by the CPU oracle,
+ * oracle/gaans_oracle.c.
  */
 #ifndef GAANS_W64_H
 #define GAANS_W64_H
@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define GAANS_ABI_VERSION 2
+#define GAANS_ABI_VERSION 3
 #define GAANS_CTRL_BYTES 256
 
 /* return codes */
@@ -88,6 +88,9 @@ typedef struct gaans_tables {
   int32_t max_nsym;   /* largest alphabet (cdf_size - 1) */
   int64_t total_nsym; /* sum of the alphabets */
   uint64_t digest;    /* table digest recorded in payload headers */
+  int32_t max_dense;  /* most 256-value decode buckets with >= 2 symbol starts in one table */
+  int32_t reserved;
+  int64_t total_dense; /* such buckets over all tables */
 } gaans_tables;
 
 int gaans_abi_version(void);
@@ -99,13 +102,17 @@ int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, gaans_layout* o
 
 /* ---- table upload (host memory) ----------------------------------------- */
 
-/* Bytes of the prepared table blob for M tables (cdf_sizes in host memory). */
-int gaans_tables_bytes(const int32_t* cdf_sizes, int32_t M, int32_t Lmax, int64_t* bytes);
+/* Bytes of the prepared table blob for M tables (cdfs [M, Lmax] and
+ * cdf_sizes in host memory; the size depends on the CDF values). */
+int gaans_tables_bytes(const int32_t* cdfs, const int32_t* cdf_sizes, int32_t M, int32_t Lmax,
+                       int64_t* bytes);
 
 /* Validate CompressAI-style tables (cdfs [M, Lmax] int32 row-major, rows
  * zero-padded beyond cdf_sizes[t]; cdf[0] = 0, cdf[S-1] = 65536, strictly
  * increasing) and lay them out for the kernels: per-table metadata, packed
- * (start, freq-1) entries and a 256-bucket decode lookup per table.  The
+ * (start, freq-1) entries with the encoder's division constant, a 256-bucket
+ * decode lookup per table and an exact 256-value block for each bucket in
+ * which two or more symbols start.  The
  * caller copies `out` to device memory unchanged and stores its address in
  * desc->dev.  Replaces the reference's use of the raw tensors at
  * src/fast_compressai/coders/factorized.py:23-31. */

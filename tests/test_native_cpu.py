@@ -52,7 +52,8 @@ def prepare_host(cdfs, sizes, offs):
     sizes = np.ascontiguousarray(sizes, np.int32)
     offs = np.ascontiguousarray(offs, np.int32)
     nb = ctypes.c_int64()
-    rc = L.gaans_tables_bytes(sizes.ctypes.data, cdfs.shape[0], cdfs.shape[1], ctypes.byref(nb))
+    rc = L.gaans_tables_bytes(cdfs.ctypes.data, sizes.ctypes.data, cdfs.shape[0], cdfs.shape[1],
+                              ctypes.byref(nb))
     if rc:
         return rc, None, None
     out = np.zeros(nb.value, np.uint8)
@@ -70,25 +71,20 @@ def prepare_host(cdfs, sizes, offs):
 def host_lookup(blob, t, cum):
     """Decode lookup as the kernel does it, read from the prepared blob."""
     hdr = struct.unpack_from("<16I", blob, 0)
-    meta_off, ent_off, lut_off = hdr[6], hdr[7], hdr[8]
-    ent_base, nsym, offset, lut_base = struct.unpack_from("<IIiI", blob, meta_off + 16 * t)
-    e = struct.unpack_from("<Q", blob, lut_off + 8 * (lut_base + (cum >> 8)))[0]
+    meta_off, ent_off, lut_off, dense_off = hdr[6], hdr[7], hdr[8], hdr[11]
+    ent_base, nsym, offset, dense_base = struct.unpack_from("<IIiI", blob, meta_off + 16 * t)
+    e = struct.unpack_from("<Q", blob, lut_off + 8 * (256 * t + (cum >> 8)))[0]
     lo, hi = e & 0xFFFFFFFF, e >> 32
     s0, nxt = hi & 0xFFFF, hi >> 16
-    st, fr = lo & 0xFFFF, (lo >> 16) + 1
-    ent = lambda v: struct.unpack_from("<I", blob, ent_off + 4 * (ent_base + v))[0]
+    ent = lambda v: struct.unpack_from("<I", blob, ent_off + 8 * (ent_base + v))[0]
     if nxt != 0xFFFF:
+        st, fr = lo & 0xFFFF, (lo >> 16) + 1
         if cum >= st + fr:
             return s0 + 1, st + fr, nxt + 1
         return s0, st, fr
-    a, b = s0, min(s0 + 256, nsym - 1)
-    while a < b:
-        mid = (a + b + 1) >> 1
-        if (ent(mid) & 0xFFFF) <= cum:
-            a = mid
-        else:
-            b = mid - 1
-    return a, ent(a) & 0xFFFF, (ent(a) >> 16) + 1
+    assert dense_base <= lo < hdr[12]
+    v = s0 + blob[dense_off + 256 * lo + (cum & 255)]
+    return v, ent(v) & 0xFFFF, (ent(v) >> 16) + 1
 
 
 def test_prepared_tables_digest_and_lookup_exhaustive():
@@ -98,6 +94,19 @@ def test_prepared_tables_digest_and_lookup_exhaustive():
     assert rc == 0
     assert dg == O.table_digest(cdfs, sizes, offs)
     blob = blob.tobytes()
+    # entry word 1 is the encoder's division constant: q = x // freq on [0, freq << 16)
+    hdr = struct.unpack_from("<16I", blob, 0)
+    for t in range(6):
+        ent_base, nsym = struct.unpack_from("<II", blob, hdr[6] + 16 * t)
+        for v in range(nsym):
+            w0, m = struct.unpack_from("<II", blob, hdr[7] + 8 * (ent_base + v))
+            f = (w0 >> 16) + 1
+            if f == 1:
+                continue
+            sh = (f - 1).bit_length() - 1
+            for x in (0, f - 1, f, (f << 16) - 1, (f << 15) + 12345, 0xFFFF * f):
+                tt = (x * m) >> 32
+                assert (tt + ((x - tt) >> 1)) >> sh == x // f, (t, v, f, x)
     for t in range(6):
         c = cdfs[t, : sizes[t]]
         want = np.searchsorted(c, np.arange(65536), side="right") - 1
