@@ -45,7 +45,7 @@ namespace {
 
 constexpr int kLanes = 64;
 #ifndef GAANS_MAPPERS
-#define GAANS_MAPPERS 3
+#define GAANS_MAPPERS 4
 #endif
 constexpr int kMappers = GAANS_MAPPERS;  // mapper waves per workgroup
 constexpr int kWaves = kMappers + 1;     // + the coder wave
@@ -489,8 +489,8 @@ __device__ __forceinline__ void ring_flush(uint16_t* __restrict__ wbuf, const ui
 
 // The ring holds the words [wp, fl) (positions mod kRingWords).  The coder
 // flushes it at the start of a block when fewer than kSB * kLanes slots are
-// free, so the fast steps of a block need no check; escape sub-rounds
-// (kCheck) keep that much room free for the rest of their block.
+// free, so the ordinary steps of a block need no check; a step with escapes
+// first makes room for its own words and the rest of its block.
 template <bool kCheck>
 __device__ __forceinline__ void emit_words(bool emit, uint32_t& x, uint16_t* ring,
                                            uint16_t* __restrict__ wbuf, int& wp, int& fl,
@@ -513,6 +513,60 @@ __device__ __forceinline__ uint32_t enc_apply(uint32_t x, uint4 r) {
   const uint32_t q = enc_div(x, r.y, r.z & 31u);
   const uint32_t xn = __umul24(q, r.x >> 16) + (x + (r.x & 0xffffu));
   return (r.z & 32u) ? ((x << 16) + (r.x & 0xffffu)) : xn;
+}
+
+// Step with escapes: each lane codes nops ops in decode order d = 0 (main),
+// 1 (count), 2.. (nibbles), an ordinary lane only d = 0; encoding runs from
+// the last op to the first, and the words of one op index are ordered by
+// lane.  M is the largest nops of the step.  Kept out of line (rare, and the
+// unrolled steps stay small); the coder state goes in and out by value.
+struct EncCur {
+  uint32_t x;
+  int wp, fl;
+};
+
+__device__ __forceinline__ EncCur enc_escape_step(const uint4 e, uint32_t M, EncCur c,
+                                               uint16_t* ring, uint16_t* __restrict__ wbuf,
+                                               int lane) {
+  uint32_t x = c.x;
+  int wp = c.wp, fl = c.fl;
+  // room for the whole step and the rest of the block
+  if (fl - wp > kRingWords - (int)(M + kSB) * kLanes) {
+    ring_flush(wbuf, ring, wp, fl, lane);
+    fl = wp;
+  }
+  const uint32_t nops = e.z >> 8;
+  const bool escl = nops > 1u;
+  const uint64_t em = __ballot(escl);
+  if (__popcll(em) == 1) {
+    // one escaping lane: each op index has at most its word, so the lane
+    // prepends its words itself
+    int k = 0;
+    if (escl) {
+      uint32_t xl = x;
+      for (int d = (int)nops - 1; d >= 1; --d) {
+        const uint32_t val = d == 1 ? nops - 2u : (e.w >> ((4 * (d - 2)) & 31)) & 15u;
+        if (xl >= kBitsEmit) {
+          ring[(uint32_t)(wp - 1 - k) & (kRingWords - 1)] = (uint16_t)xl;
+          xl >>= 16;
+          ++k;
+        }
+        xl = (xl << 4) | val;
+      }
+      x = xl;
+    }
+    wp -= __builtin_amdgcn_readlane(k, __ffsll((unsigned long long)em) - 1);
+  } else {
+    for (int d = (int)M - 1; d >= 1; --d) {
+      const bool part_d = (uint32_t)d < nops;
+      const uint32_t val = d == 1 ? nops - 2u : (e.w >> ((4 * (d - 2)) & 31)) & 15u;
+      const uint32_t x0 = x;
+      emit_words<false>(part_d & (x >= kBitsEmit), x, ring, wbuf, wp, fl, lane);
+      x = part_d ? ((x << 4) | val) : x0;
+    }
+  }
+  emit_words<false>((x >> 16) >= 65536u - (e.x >> 16), x, ring, wbuf, wp, fl, lane);
+  return EncCur{enc_apply(x, e), wp, fl};
 }
 
 template <bool kLatents, bool kImplicit>
@@ -651,34 +705,20 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
             x = enc_apply(x, r[u]);
           }
         } else {
+          // last block or escapes: per-step branches
 #pragma unroll
-        for (int u = kSB - 1; u >= 0; --u) {
-          if (j * kSB + u >= T) continue;
-          const uint4 e = r[u];
-          const uint32_t fr = 65536u - (e.x >> 16);
-          if (mt[u] == 0) {
-            emit_words<false>((x >> 16) >= fr, x, ring, wbuf, wp, fl, lane);
-            x = enc_apply(x, e);
-          } else {
-            // escape sub-rounds in decode order d = 0 (main), 1 (count),
-            // 2.. (nibbles), encoded from the last op to the first
-            const uint32_t nops = e.z >> 8;
-            for (int d = (int)mt[u] - 1; d >= 0; --d) {
-              const bool part_d = (uint32_t)d < nops;
-              const bool want = d == 0 ? (x >> 16) >= fr : x >= kBitsEmit;
-              const uint32_t x0 = x;
-              emit_words<true>(part_d & want, x, ring, wbuf, wp, fl, lane);
-              uint32_t xn;
-              if (d == 0) {
-                xn = enc_apply(x, e);
-              } else {
-                const uint32_t val = d == 1 ? nops - 2u : (e.w >> (4 * (d - 2))) & 15u;
-                xn = (x << 4) | val;
-              }
-              x = part_d ? xn : x0;
+          for (int u = kSB - 1; u >= 0; --u) {
+            if (j * kSB + u >= T) continue;
+            if (mt[u] == 0) {
+              emit_words<false>((x >> 16) >= 65536u - (r[u].x >> 16), x, ring, wbuf, wp, fl, lane);
+              x = enc_apply(x, r[u]);
+            } else {
+              const EncCur c = enc_escape_step(r[u], mt[u], EncCur{x, wp, fl}, ring, wbuf, lane);
+              x = c.x;
+              wp = uni(c.wp);
+              fl = uni(c.fl);
             }
           }
-        }
         }
         __syncthreads();
       }
