@@ -708,8 +708,8 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
           // last block or escapes: per-step branches
 #pragma unroll
           for (int u = kSB - 1; u >= 0; --u) {
-            if (j * kSB + u >= T) continue;
-            if (mt[u] == 0) {
+            if (__builtin_expect(j * kSB + u >= T, 0)) continue;
+            if (__builtin_expect(mt[u] == 0, 1)) {
               emit_words<false>((x >> 16) >= 65536u - (r[u].x >> 16), x, ring, wbuf, wp, fl, lane);
               x = enc_apply(x, r[u]);
             } else {
@@ -932,7 +932,7 @@ __device__ __forceinline__ void dec_lookup(const Tabs& tb, const uint4 r, uint32
   s = up ? s0 + 1u : s0;
   st = up ? st0 + fr0 : st0;
   fr = up ? nxt + 1u : fr0;
-  if (act & (nxt == 0xffffu)) {
+  if (__builtin_expect(act & (nxt == 0xffffu), 0)) {
     const uint32_t blk = kLds ? lo - tb.dense_first : lo;
     const uint32_t di = (blk << kLutBits) + (cum & (kLutSize - 1));
     s = s0 + (uint32_t)(kLds ? tb.ldense[di] : tb.gdense[di]);
@@ -1033,7 +1033,7 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint4 r, uint
   // exactly when it wraps below the offset
   int32_t o = (int32_t)(s + r.z);
   bool oob = o < (int32_t)r.z;
-  if (__ballot(esc)) {
+  if (__builtin_expect(__ballot(esc) != 0, 0)) {
     uint32_t n = esc ? (x & 15u) : 0u;
     x = esc ? (x >> 4) : x;
     dec_refill<true>(esc & (x < kStateLow), x, S, ring, ring32, lane);
@@ -1123,11 +1123,6 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
     tb.lent32 = lent32;
     tb.llut = llut;
     tb.ldense = ldense;
-    int t_lo, t_hi;
-    stage_range(a.nt_cap, a.stage_all, k, (int)a.P, (int)a.M, t_lo, t_hi);
-    stage_tables(tb, lmeta, nullptr, lent32, llut, ldense, th->total_dense, a.M, t_lo, t_hi,
-                 tid);
-
     const uint8_t* cdata = a.payload + a.header_bytes + beg;
 
     int32_t cbx[kPer], nbx[kPer];
@@ -1174,12 +1169,14 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
       }
     };
 
-    // The coder and the mappers run separate code (the wave role is uniform
-    // per wave) that meets at the same barriers: one before the first block
-    // and one per block.  Keeping the roles apart also keeps the mappers'
-    // loads in flight out of the coder's wait bookkeeping.
+    // Loads that do not depend on the tables are issued before the tables are
+    // staged, so that they overlap: the coder's initial states and first
+    // stream words, the mappers' first two blocks of inputs.
+    constexpr int kPre = kLowWater / kPfWords;
+    Stream S;
+    uint32_t x = kStateLow;
+    uint32_t w0[kPre][kPfU32];
     if (wid == 0) {
-      Stream S;
       S.s32 = reinterpret_cast<const uint32_t*>(cdata + 4 * A);
       S.safe = reinterpret_cast<const uint32_t*>(cdata);
       S.q = (int)((cb - 4 * A) / 2);  // stream words incl. pad (even)
@@ -1187,10 +1184,32 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
       S.rp = 0;
       S.filled = 0;
       S.pf_live = false;
-      // the initial states are loaded first, so that waiting for them does not
-      // also wait for the stream prefetch
-      uint32_t x = lane < A ? reinterpret_cast<const uint32_t*>(cdata)[lane] : kStateLow;
-      for (int b = 0; b < kLowWater / kPfWords; ++b) stream_sync_batch(S, sring32, lane);
+      x = lane < A ? reinterpret_cast<const uint32_t*>(cdata)[lane] : kStateLow;
+#pragma unroll
+      for (int b = 0; b < kPre; ++b)
+#pragma unroll
+        for (int kk = 0; kk < kPfU32; ++kk)
+          w0[b][kk] = stream_word32(S, b * (kPfWords / 2) + kk * kLanes + lane);
+    } else if (nblk > 0) {
+      load_block(0, cbx, cm);
+      if (nblk > 1) load_block(1, nbx, nm);
+    }
+    int t_lo, t_hi;
+    stage_range(a.nt_cap, a.stage_all, k, (int)a.P, (int)a.M, t_lo, t_hi);
+    stage_tables(tb, lmeta, nullptr, lent32, llut, ldense, th->total_dense, a.M, t_lo, t_hi,
+                 tid);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load crosses the role split
+
+    // The coder and the mappers run separate code (the wave role is uniform
+    // per wave) that meets at the same barriers: one before the first block
+    // and one per block.
+    if (wid == 0) {
+#pragma unroll
+      for (int b = 0; b < kPre; ++b)
+#pragma unroll
+        for (int kk = 0; kk < kPfU32; ++kk)
+          sring32[(b * (kPfWords / 2) + kk * kLanes + lane) & (kStreamRing / 2 - 1)] = w0[b][kk];
+      S.filled = kPre * kPfWords;
       __syncthreads();
       for (int j = 0; j < nblk; ++j) {
         stream_block_start(S, sring32, lane);
@@ -1214,7 +1233,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
 #pragma unroll
           for (int u = 0; u < kSB; ++u) {
             ov[u] = 0;
-            if (j * kSB + u >= T) continue;
+            if (__builtin_expect(j * kSB + u >= T, 0)) continue;
             if (fl[u]) ov[u] = dec_step<true>(tb, r[u], x, S, sring, sring32, status, lane);
             else ov[u] = dec_step<false>(tb, r[u], x, S, sring, sring32, status, lane);
           }
@@ -1227,11 +1246,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
       if (lane < A && x != kStateLow) status |= GAANS_ST_CORRUPT;
       if (!(S.rp == S.q || (S.rp == S.q - 1 && (S.q & 1) == 0))) status |= GAANS_ST_CORRUPT;
     } else {
-      if (nblk > 0) {
-        load_block(0, cbx, cm);
-        if (nblk > 1) load_block(1, nbx, nm);
-        map_block(0);
-      }
+      if (nblk > 0) map_block(0);
       __syncthreads();
       for (int j = 0; j < nblk; ++j) {
         // mappers: store block j - 1 and map block j + 1 while the coder decodes block j

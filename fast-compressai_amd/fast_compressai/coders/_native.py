@@ -115,6 +115,23 @@ def lib():
     return _lib
 
 
+_hip = None
+
+
+def stream_synchronize(stream_ptr: int) -> None:
+    """hipStreamSynchronize on a raw stream handle (torch's streams are HIP
+    streams); cheaper than constructing a torch stream object per call."""
+    global _hip
+    if _hip is None:
+        h = ctypes.CDLL("libamdhip64.so")
+        h.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+        h.hipStreamSynchronize.restype = ctypes.c_int
+        _hip = h
+    rc = _hip.hipStreamSynchronize(stream_ptr)
+    if rc != 0:
+        raise CoderDependencyError(f"hipStreamSynchronize failed with HIP error {rc}")
+
+
 def last_error() -> str:
     msg = lib().gaans_last_error()
     return msg.decode("utf-8", "replace") if msg else ""

@@ -34,6 +34,8 @@ class _StreamState:
         self.ctrl = torch.zeros(_native.CTRL_BYTES, dtype=torch.uint8, device=device)
         self.info = torch.zeros(4, dtype=torch.int64, pin_memory=True)
         self.status = torch.zeros(4, dtype=torch.int32, pin_memory=True)
+        self.info_np = self.info.numpy()      # host views of the pinned words
+        self.status_np = self.status.numpy()
         self.workspace = torch.empty(0, dtype=torch.uint8, device=device)
 
     def ws(self, nbytes: int) -> torch.Tensor:
@@ -47,16 +49,17 @@ _states: dict = {}
 _states_lock = threading.Lock()
 
 
-def _state(device: torch.device, stream: torch.cuda.Stream) -> _StreamState:
-    key = (device.index, stream.cuda_stream)
+def _state(index: int, stream_ptr: int) -> _StreamState:
+    key = (index, stream_ptr)
     st = _states.get(key)
     if st is None:
         with _states_lock:
             st = _states.get(key)
             if st is None:
+                device = torch.device("cuda", index)
                 with torch.cuda.device(device):
                     st = _StreamState(device)
-                torch.cuda.current_stream(device).synchronize()  # ctrl zeroed before first use
+                    torch.cuda.current_stream(device).synchronize()  # ctrl zeroed before use
                 _states[key] = st
     return st
 
@@ -65,11 +68,31 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
-def _device(device) -> torch.device:
-    d = torch.device(device)
-    if d.index is None:
-        d = torch.device(d.type, torch.cuda.current_device())
-    return d
+def _index(device) -> int:
+    d = device if isinstance(device, torch.device) else torch.device(device)
+    return torch.cuda.current_device() if d.index is None else d.index
+
+
+class _on_device:
+    """Make ``index`` the current device for the call (no-op when it is)."""
+
+    __slots__ = ("index", "prev")
+
+    def __init__(self, index: int) -> None:
+        self.index = index
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if cur != self.index:
+            self.prev = cur
+            torch.cuda.set_device(self.index)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
 
 
 @dataclass(frozen=True)
@@ -88,13 +111,12 @@ def encode(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,
     ``medians`` (quantize fused).  ``indexes`` None means channel-major tables."""
     L = _native.lib()
     lay = _native.layout(B, N, C, P)
-    device = _device(device)
-    with torch.cuda.device(device):
-        stream = torch.cuda.current_stream(device)
-        st = _state(device, stream)
+    index = _index(device)
+    with _on_device(index):
+        sp = torch._C._cuda_getCurrentRawStream(index)
+        st = _state(index, sp)
         ws = st.ws(int(lay.workspace_bytes))
-        out = torch.empty(int(lay.max_payload_bytes), dtype=torch.uint8, device=device)
-        sp = stream.cuda_stream
+        out = torch.empty(int(lay.max_payload_bytes), dtype=torch.uint8, device=ws.device)
         if y is not None:
             rc = L.gaans_encode_latents(sp, y.data_ptr(), medians.data_ptr(), _ptr(indexes),
                                         tables.ref, B, N, C, P, ws.data_ptr(), ws.numel(),
@@ -107,16 +129,16 @@ def encode(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,
         rc = L.gaans_encode_pack(sp, ws.data_ptr(), ws.numel(), tables.ref, B, N, C, P,
                                  out.data_ptr(), out.numel())
         _native.check(rc, "GA-ANS pack")
-        stream.synchronize()  # the one host synchronisation
-        total, status = int(st.info[0]), int(st.info[1])
+        _native.stream_synchronize(sp)  # the one host synchronisation
+        total, status = int(st.info_np[0]), int(st.info_np[1])
     if status:
         raise CoderInputError(f"GA-ANS encode failed: {_native.describe_status(status)}")
     packed = out[:total]
     if out.numel() - total > _CLONE_SLACK_BYTES:
         packed = packed.clone()
-    BK = int(lay.BK)
-    ends = packed[64: 64 + 4 * BK].view(torch.uint32).view(B, int(lay.K))
-    return EncodedChunks(packed, ends, int(lay.header_bytes), int(lay.chunk_len), int(lay.K))
+    K = int(lay.K)
+    ends = packed[64: 64 + 4 * B * K].view(torch.uint32).view(B, K)
+    return EncodedChunks(packed, ends, int(lay.header_bytes), int(lay.chunk_len), K)
 
 
 def decode(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int, P: int,
@@ -125,24 +147,23 @@ def decode(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int,
     """Decode to int32 symbols [B, N], or (``medians`` given) to fp32 y_hat
     [B, N] with dequantize fused."""
     L = _native.lib()
-    device = _device(device)
-    with torch.cuda.device(device):
-        stream = torch.cuda.current_stream(device)
-        st = _state(device, stream)
-        sp = stream.cuda_stream
+    index = _index(device)
+    with _on_device(index):
+        sp = torch._C._cuda_getCurrentRawStream(index)
+        st = _state(index, sp)
         if medians is not None:
-            out = torch.empty((B, N), dtype=torch.float32, device=device)
+            out = torch.empty((B, N), dtype=torch.float32, device=packed.device)
             rc = L.gaans_decode_latents(sp, packed.data_ptr(), packed.numel(), _ptr(indexes),
                                         tables.ref, medians.data_ptr(), B, N, C, P,
                                         out.data_ptr(), st.ctrl.data_ptr(), st.status.data_ptr())
         else:
-            out = torch.empty((B, N), dtype=torch.int32, device=device)
+            out = torch.empty((B, N), dtype=torch.int32, device=packed.device)
             rc = L.gaans_decode_symbols(sp, packed.data_ptr(), packed.numel(), _ptr(indexes),
                                         tables.ref, B, N, C, P, out.data_ptr(),
                                         st.ctrl.data_ptr(), st.status.data_ptr())
         _native.check(rc, "GA-ANS decode")
-        stream.synchronize()  # the one host synchronisation
-        status = int(st.status[0])
+        _native.stream_synchronize(sp)  # the one host synchronisation
+        status = int(st.status_np[0])
     if status:
         raise CoderInputError(f"warp_div decode failed: {_native.describe_status(status)}")
     return out

@@ -86,8 +86,9 @@ class TableCache:
 
     @staticmethod
     def _key(tensors):
-        return tuple((t.data_ptr(), t._version, tuple(t.shape), t.dtype, str(t.device))
-                     for t in tensors)
+        # device pointers are unique across devices; dtype and device are
+        # checked by the callers before tables are prepared
+        return tuple((t.data_ptr(), t._version, t.shape) for t in tensors)
 
     def get(self, cdfs: torch.Tensor, cdf_sizes: torch.Tensor,
             offsets: torch.Tensor) -> PreparedTables:

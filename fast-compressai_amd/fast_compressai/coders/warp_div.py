@@ -24,9 +24,11 @@ Differences that follow from the new format:
 
 from __future__ import annotations
 
+import functools
 import hashlib
+import re
 import struct
-from dataclasses import dataclass
+from dataclasses import dataclass, fields
 from typing import Sequence
 
 import torch
@@ -40,12 +42,14 @@ FORMAT_ID = "gaans-w64-v1"
 FORMAT_VERSION = 1
 _HEADER_MAGIC = 0x31574147
 _FIXED_HEADER_BYTES = 64
+_SHA256_HEX = re.compile(r"[0-9a-f]{64}")
 
 
 def header_bytes_for(batch: int, chunks: int) -> int:
     return (_FIXED_HEADER_BYTES + 8 * batch * chunks + 15) // 16 * 16
 
 
+@functools.lru_cache(maxsize=256)
 def coding_fingerprint(table_digest: int, batch: int, symbols_per_batch: int, channels: int,
                        cdf_count: int) -> str:
     """SHA-256 over the table digest and the coding shapes."""
@@ -81,8 +85,8 @@ class WarpDivPayload:
             raise CoderInputError(
                 "chunk_ends must be contiguous GPU uint32 on the packed payload device")
         if self.coding_fingerprint is not None and (
-            not isinstance(self.coding_fingerprint, str) or len(self.coding_fingerprint) != 64
-            or any(char not in "0123456789abcdef" for char in self.coding_fingerprint)
+            not isinstance(self.coding_fingerprint, str)
+            or _SHA256_HEX.fullmatch(self.coding_fingerprint) is None
         ):
             raise CoderInputError("coding_fingerprint must be a SHA-256 hex digest")
         ints = (self.header_bytes, self.chunk_len, self.p_ch, self.batch,
@@ -105,6 +109,15 @@ class WarpDivPayload:
             raise CoderInputError("warp_div header exceeds packed payload size")
         if self.packed.numel() % 4:
             raise CoderInputError("warp_div packed payload must be uint32 aligned")
+
+    @classmethod
+    def _from_encoder(cls, **values) -> "WarpDivPayload":
+        """Payload built by ``WarpDivBackend.encode`` from values it has just
+        produced and checked; skips the field validation of ``__init__``."""
+        obj = object.__new__(cls)
+        for f in fields(cls):
+            object.__setattr__(obj, f.name, values.get(f.name, f.default))
+        return obj
 
     @property
     def coded_channels(self) -> int:
@@ -190,7 +203,7 @@ class WarpDivBackend:
         B, N = int(symbols.shape[0]), int(symbols.shape[1])
         enc = gaans.encode(tables, B, N, C, p_ch, symbols.device, symbols=symbols,
                            indexes=indexes)
-        return WarpDivPayload(
+        return WarpDivPayload._from_encoder(
             packed=enc.packed,
             chunk_ends=enc.chunk_ends,
             header_bytes=enc.header_bytes,
