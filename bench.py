@@ -37,7 +37,79 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--p-ch", type=int, default=4)
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the kernel timings of the other workload shapes")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="after the measurement, run one device-to-device copy of MIB MiB "
+                         "(reference kernel for HBM byte counters)")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "hbm_traffic_coder_512x768_p4.txt")
+
+
+def read_traffic(kernel_key: str):
+    """HBM bytes per launch of ``kernel_key`` from the committed counter
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy's reading);
+    None when there is no summary for it."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) >= 2 and parts[0] == kernel_key and parts[1].startswith("bytes="):
+                    return int(parts[1].split("=", 1)[1])
+    except OSError:
+        return None
+    return None
+
+
+def kernel_times(L, _native, torch, backend, w, dev, reps=20):
+    """Event-timed encode / decode kernels of one workload (median, seconds)."""
+    import statistics
+
+    B, N, C, P = w.batch, w.n, w.channels, w.p_ch
+    sym = torch.from_numpy(w.symbols).to(dev)
+    idx = torch.from_numpy(w.explicit_indexes()).to(dev)
+    cdfs, sizes, offs = (torch.from_numpy(a).to(dev) for a in (w.cdfs, w.cdf_sizes, w.offsets))
+    payload = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=P)
+    tables = backend.prepared_tables(cdfs, sizes, offs)
+    lay = _native.layout(B, N, C, P)
+    ws = torch.empty(int(lay.workspace_bytes), dtype=torch.uint8, device=dev)
+    ctrl = torch.zeros(_native.CTRL_BYTES, dtype=torch.uint8, device=dev)
+    info = torch.zeros(4, dtype=torch.int64, device=dev)
+    status = torch.zeros(4, dtype=torch.int32, device=dev)
+    out = torch.empty_like(sym)
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+
+    def enc():
+        _native.check(L.gaans_encode_symbols(sp, sym.data_ptr(), idx.data_ptr(), tables.ref, B, N,
+                                             C, P, ws.data_ptr(), ws.numel(), ctrl.data_ptr(),
+                                             info.data_ptr()), "encode")
+
+    def dec():
+        _native.check(L.gaans_decode_symbols(sp, payload.packed.data_ptr(),
+                                             payload.packed.numel(), idx.data_ptr(), tables.ref,
+                                             B, N, C, P, out.data_ptr(), ctrl.data_ptr(),
+                                             status.data_ptr()), "decode")
+
+    res = {}
+    for name, fn in (("encode", enc), ("decode", dec)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e-3)
+        res[name] = statistics.median(ts)
+    torch.cuda.synchronize()
+    assert int(status[0].item()) == 0 and torch.equal(out, sym)
+    return res, int(payload.packed.numel())
 
 
 def main():
@@ -139,10 +211,35 @@ def main():
     # algorithmic bytes per launch: symbols + indexes (int32) + payload
     alg_bytes = 4 * B * N + 4 * B * N + payload_bytes
     if dec_avg >= enc_avg:
-        kernel, dur = "k_decode<false,false> (gaans_decode_symbols)", dec_avg
+        kernel, key, dur = "k_decode<false,false> (gaans_decode_symbols)", "k_decode", dec_avg
     else:
-        kernel, dur = "k_encode<false,false> (gaans_encode_symbols)", enc_avg
+        kernel, key, dur = "k_encode<false,false> (gaans_encode_symbols)", "k_encode", enc_avg
     achieved = alg_bytes / dur / 1e9
+    traffic = read_traffic(key)
+
+    # ---- kernel times of the other workload shapes (parity-tested configs) --
+    extra = {}
+    if not args.no_extra:
+        for label, wl in (("highres_1x320x136x240_p8", synthetic.highres_2160x3840()),
+                          ("batch64_skew_p16", synthetic.batch_skew()),
+                          ("batch64_uniform_p16", synthetic.batch_uniform())):
+            kt, pb = kernel_times(L, _native, torch, backend, wl, dev)
+            n_sym = wl.batch * wl.n
+            extra[label] = {
+                "symbols": n_sym, "payload_bytes": pb,
+                "encode_kernel_us": round(kt["encode"] * 1e6, 2),
+                "decode_kernel_us": round(kt["decode"] * 1e6, 2),
+                "encode_gsym_s": round(n_sym / kt["encode"] / 1e9, 3),
+                "decode_gsym_s": round(n_sym / kt["decode"] / 1e9, 3),
+                "raw_rgb_gbps_roundtrip_kernels": round(
+                    wl.raw_rgb_bytes / (kt["encode"] + kt["decode"]) / 1e9, 2),
+            }
+    if args.copy_probe > 0:
+        nb = args.copy_probe << 20
+        src = torch.empty(nb, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
 
     # ---- CPU baseline: CompressAI-equivalent Rans64, one stream per image --
     import oracle
@@ -200,7 +297,7 @@ def main():
         "roofline": {
             "bound": "hbm", "kernel": kernel, "achieved": round(achieved, 3),
             "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 6),
-            "traffic": None, "alg_bytes_per_launch": alg_bytes,
+            "traffic": traffic, "alg_bytes_per_launch": alg_bytes,
             "avg_launch_us": round(dur * 1e6, 3),
         },
         "cpu_baseline": {
@@ -212,6 +309,7 @@ def main():
                        f"decode {statistics.median(cpu_dec)*1e3:.3f} ms"),
             "speedup_gpu_over_cpu": round(value / cpu_gbps, 2),
         },
+        "other_configs_kernels": extra,
     }
     print(json.dumps(rec), flush=True)
 

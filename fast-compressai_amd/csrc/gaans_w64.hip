@@ -69,7 +69,7 @@ constexpr int kRingWords = 4096;       // encoder LDS output ring (u16 words)
 constexpr int kStreamRing = 2048;      // decoder LDS stream ring (u16 words)
 constexpr int kPfU32 = 4;              // decoder stream prefetch: u32 per lane
 constexpr int kPfWords = 2 * kPfU32 * kLanes;
-constexpr int64_t kLdsMax = 64 * 1024;  // LDS of one workgroup
+constexpr int kMaxDevices = 64;
 // control block (u32 words); encoder and decoder fields on separate 64-byte lines
 constexpr int kCtrlEncDone = 0;
 constexpr int kCtrlDecDone = 16;
@@ -539,23 +539,24 @@ __device__ __forceinline__ EncCur enc_escape_step(const uint4 e, uint32_t M, Enc
   const bool escl = nops > 1u;
   const uint64_t em = __ballot(escl);
   if (__popcll(em) == 1) {
-    // one escaping lane: each op index has at most its word, so the lane
-    // prepends its words itself
+    // one escaping lane: each op index has at most its word, so its ops run
+    // on the scalar unit and lane 0 prepends the words
+    const int L = __ffsll((unsigned long long)em) - 1;
+    uint32_t xs = __builtin_amdgcn_readlane(x, L);
+    const uint32_t ns = __builtin_amdgcn_readlane(nops, L);
+    const uint32_t raws = __builtin_amdgcn_readlane(e.w, L);
     int k = 0;
-    if (escl) {
-      uint32_t xl = x;
-      for (int d = (int)nops - 1; d >= 1; --d) {
-        const uint32_t val = d == 1 ? nops - 2u : (e.w >> ((4 * (d - 2)) & 31)) & 15u;
-        if (xl >= kBitsEmit) {
-          ring[(uint32_t)(wp - 1 - k) & (kRingWords - 1)] = (uint16_t)xl;
-          xl >>= 16;
-          ++k;
-        }
-        xl = (xl << 4) | val;
+    for (int d = (int)ns - 1; d >= 1; --d) {
+      const uint32_t val = d == 1 ? ns - 2u : (raws >> ((4 * (d - 2)) & 31)) & 15u;
+      if (xs >= kBitsEmit) {
+        if (lane == 0) ring[(uint32_t)(wp - 1 - k) & (kRingWords - 1)] = (uint16_t)xs;
+        xs >>= 16;
+        ++k;
       }
-      x = xl;
+      xs = (xs << 4) | val;
     }
-    wp -= __builtin_amdgcn_readlane(k, __ffsll((unsigned long long)em) - 1);
+    x = lane == L ? xs : x;
+    wp -= k;
   } else {
     for (int d = (int)M - 1; d >= 1; --d) {
       const bool part_d = (uint32_t)d < nops;
@@ -861,7 +862,7 @@ struct DecArgs {
   int64_t N, header_bytes, BK;
   uint32_t B, C, P, K, chunk_len;
   UDiv div_hw;
-  int32_t nt_cap, ne_cap, stage_all;
+  int32_t nt_cap, ne_cap, nd_cap, stage_all;
   uint32_t* __restrict__ ctrl;
   uint32_t* __restrict__ status_out;
 };
@@ -1033,7 +1034,50 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint4 r, uint
   // exactly when it wraps below the offset
   int32_t o = (int32_t)(s + r.z);
   bool oob = o < (int32_t)r.z;
-  if (__builtin_expect(__ballot(esc) != 0, 0)) {
+  const uint64_t em = __ballot(esc);
+  if (__builtin_expect(em != 0, 0)) {
+   if (__popcll(em) == 1) {
+    // one escaping lane: its refill words are consecutive in the stream; the
+    // lane takes them from 5 or 6 words read at once (the margin covers the
+    // at most 9 words and the rest of the block)
+    if (S.filled - S.rp < kSB * kLanes && S.filled < S.q) stream_sync_batch(S, ring32, lane);
+    const int rp = S.rp;
+    const int e0 = rp & ~1;  // even word at or below rp
+    const uint32_t d0 = ring32[(e0 >> 1) & (kStreamRing / 2 - 1)];
+    const uint32_t d1 = ring32[((e0 >> 1) + 1) & (kStreamRing / 2 - 1)];
+    const uint32_t d2 = ring32[((e0 >> 1) + 2) & (kStreamRing / 2 - 1)];
+    const uint64_t win = ((uint64_t)d1 << 32) | d0;
+    int k = rp - e0;  // next word, counted from e0
+    uint32_t raw1 = 0;
+    if (esc) {
+      auto take = [&]() -> uint32_t {
+        uint32_t w;
+        if (k < 4) w = (uint32_t)(win >> (16 * k)) & 0xffffu;
+        else if (k < 6) w = (d2 >> (16 * (k - 4))) & 0xffffu;
+        else w = ring[(e0 + k) & (kStreamRing - 1)];
+        ++k;
+        return w;
+      };
+      uint32_t n = x & 15u;
+      x >>= 4;
+      if (x < kStateLow) x = (x << 16) | take();
+      if (n > 8u) {
+        status |= GAANS_ST_CORRUPT;
+        n = 0;
+      }
+      for (uint32_t jj = 0; jj < n; ++jj) {
+        raw1 |= (x & 15u) << (4 * jj);
+        x >>= 4;
+        if (x < kStateLow) x = (x << 16) | take();
+      }
+    }
+    S.rp = e0 + __builtin_amdgcn_readlane(k, __ffsll((unsigned long long)em) - 1);
+    const uint32_t raw = raw1;
+    const int64_t ev = (raw & 1u) ? -(int64_t)(raw >> 1) - 1 : (int64_t)(raw >> 1) + r.y;
+    const int64_t sv = ev + (int32_t)r.z;
+    o = esc ? (int32_t)sv : o;
+    oob = esc ? ((sv < INT32_MIN) | (sv > INT32_MAX)) : oob;
+   } else {
     uint32_t n = esc ? (x & 15u) : 0u;
     x = esc ? (x >> 4) : x;
     dec_refill<true>(esc & (x < kStateLow), x, S, ring, ring32, lane);
@@ -1052,6 +1096,7 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint4 r, uint
     const int64_t sv = ev + (int32_t)r.z;
     o = esc ? (int32_t)sv : o;
     oob = esc ? ((sv < INT32_MIN) | (sv > INT32_MAX)) : oob;
+   }
   }
   oob &= act;
   status |= oob ? GAANS_ST_CORRUPT : 0u;
@@ -1196,8 +1241,8 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
     }
     int t_lo, t_hi;
     stage_range(a.nt_cap, a.stage_all, k, (int)a.P, (int)a.M, t_lo, t_hi);
-    stage_tables(tb, lmeta, nullptr, lent32, llut, ldense, th->total_dense, a.M, t_lo, t_hi,
-                 tid);
+    stage_tables(tb, lmeta, nullptr, a.ne_cap ? lent32 : nullptr, llut,
+                 a.nd_cap ? ldense : nullptr, th->total_dense, a.M, t_lo, t_hi, tid);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load crosses the role split
 
     // The coder and the mappers run separate code (the wave role is uniform
@@ -1229,18 +1274,22 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
 #pragma unroll
           for (int u = 0; u < kSB; ++u)
             ov[u] = dec_step<true>(tb, r[u], x, S, sring, sring32, status, lane);
-        } else {
+          // decoded values replace the records' x words; the mappers store them
 #pragma unroll
-          for (int u = 0; u < kSB; ++u) {
-            ov[u] = 0;
-            if (__builtin_expect(j * kSB + u >= T, 0)) continue;
-            if (fl[u]) ov[u] = dec_step<true>(tb, r[u], x, S, sring, sring32, status, lane);
-            else ov[u] = dec_step<false>(tb, r[u], x, S, sring, sring32, status, lane);
+          for (int u = 0; u < kSB; ++u)
+            reinterpret_cast<uint32_t*>(src + u * kLanes + lane)[0] = ov[u];
+        } else {
+          // last block or tables outside LDS: one step at a time
+#pragma unroll 1
+          for (int u = 0; u < kSB && j * kSB + u < T; ++u) {
+            const uint4 ru = src[u * kLanes + lane];
+            const uint32_t v =
+                uni((int)info[(j & 1) * kSB + u])
+                    ? dec_step<true>(tb, ru, x, S, sring, sring32, status, lane)
+                    : dec_step<false>(tb, ru, x, S, sring, sring32, status, lane);
+            reinterpret_cast<uint32_t*>(src + u * kLanes + lane)[0] = v;
           }
         }
-        // decoded values replace the records' x words; the mappers store them
-#pragma unroll
-        for (int u = 0; u < kSB; ++u) reinterpret_cast<uint32_t*>(src + u * kLanes + lane)[0] = ov[u];
         __syncthreads();
       }
       if (lane < A && x != kStateLow) status |= GAANS_ST_CORRUPT;
@@ -1314,29 +1363,84 @@ int check_tables_arg(const gaans_tables* t) {
   return GAANS_OK;
 }
 
-// LDS staging plan: all tables if they fit the budget, else the chunk's
-// channel range (P tables, bounded by P times the largest table), else none.
+// LDS of the current device: per workgroup and per CU, and the CU count
+// (queried once per device).
+struct DevLds {
+  int per_block, per_cu, cus;
+};
+
+int device_lds(DevLds* out) {
+  static DevLds cache[kMaxDevices];
+  static int ready[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(GAANS_EHIP, "hipGetDevice failed");
+  if (!__atomic_load_n(&ready[dev], __ATOMIC_ACQUIRE)) {
+    DevLds d{0, 0, 0};
+    if (hipDeviceGetAttribute(&d.per_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) !=
+            hipSuccess ||
+        hipDeviceGetAttribute(&d.per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
+                              dev) != hipSuccess ||
+        hipDeviceGetAttribute(&d.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        d.per_block <= 0 || d.cus <= 0)
+      return fail(GAANS_EHIP, "device attribute query failed");
+    if (d.per_cu < d.per_block) d.per_cu = d.per_block;
+    cache[dev] = d;
+    __atomic_store_n(&ready[dev], 1, __ATOMIC_RELEASE);
+  }
+  *out = cache[dev];
+  return GAANS_OK;
+}
+
+// LDS staging plan for a launch of BK workgroups: all tables if they fit
+// and are not much larger than a chunk's channel range, else that range (P
+// tables, bounded by P times the largest table), else none.  The budget per workgroup keeps the launch in one round
+// of workgroups when the tables allow it (BK / CUs workgroups per CU), and
+// otherwise gives up workgroups per CU before it gives up staging.
 struct Stage {
   int32_t nt_cap, ne_cap, nd_cap, stage_all;
 };
 
 Stage plan_stage(const gaans_tables* t, int64_t P, int64_t per_table, int64_t per_sym,
-                 int64_t per_dense, int64_t budget) {
+                 int64_t per_dense, int64_t fixed, int64_t BK, const DevLds& d) {
   Stage s{0, 0, 0, 0};
   const int64_t all = t->M * per_table + per_sym * t->total_nsym + per_dense * t->total_dense;
   const int64_t range = P * (per_table + per_sym * (int64_t)t->max_nsym +
                              per_dense * (int64_t)t->max_dense);
-  if (all <= budget) {
-    s.nt_cap = t->M;
-    s.ne_cap = (int32_t)t->total_nsym;
-    s.nd_cap = per_dense ? (int32_t)t->total_dense : 0;
-    s.stage_all = 1;
-  } else if (range <= budget) {
-    s.nt_cap = (int32_t)P;
-    s.ne_cap = (int32_t)(P * t->max_nsym);
-    s.nd_cap = per_dense ? (int32_t)(P * t->max_dense) : 0;
+  int64_t occ = (BK + d.cus - 1) / d.cus;
+  if (occ > 4) occ = 4;
+  if (occ < 1) occ = 1;
+  for (; occ >= 1; --occ) {
+    int64_t budget = d.per_cu / occ;
+    if (budget > d.per_block) budget = d.per_block;
+    budget -= fixed;
+    // all tables when that is not much more to copy than the chunk's range
+    // (or the range does not fit): explicit indexes may use any table
+    if (all <= budget && (all <= 2 * range || range > budget)) {
+      s.nt_cap = t->M;
+      s.ne_cap = per_sym ? (int32_t)t->total_nsym : 0;
+      s.nd_cap = per_dense ? (int32_t)t->total_dense : 0;
+      s.stage_all = 1;
+      return s;
+    }
+    if (range <= budget) {
+      s.nt_cap = (int32_t)P;
+      s.ne_cap = per_sym ? (int32_t)(P * t->max_nsym) : 0;
+      s.nd_cap = per_dense ? (int32_t)(P * t->max_dense) : 0;
+      return s;
+    }
   }
   return s;
+}
+
+// Allow dynamic LDS above the default limit (once per kernel and device).
+template <typename K>
+int allow_lds(K kernel, size_t bytes, const DevLds& d) {
+  if (bytes <= 64 * 1024) return GAANS_OK;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, d.per_block) != hipSuccess)
+    return fail(GAANS_EHIP, "cannot raise the LDS limit of a kernel to %d bytes", d.per_block);
+  return GAANS_OK;
 }
 
 int encode_stage1(bool latents, void* stream, const int32_t* symbols, const float* y,
@@ -1353,7 +1457,9 @@ int encode_stage1(bool latents, void* stream, const int32_t* symbols, const floa
     return fail(GAANS_EINVAL, "workspace too small (%lld < %lld bytes)", (long long)ws_bytes,
                 (long long)L.ws_bytes);
   uint8_t* w = static_cast<uint8_t*>(ws);
-  const Stage st = plan_stage(tables, P, 16, 8, 0, kLdsMax - kEncFixedLds);
+  DevLds dl;
+  if ((rc = device_lds(&dl))) return rc;
+  const Stage st = plan_stage(tables, P, 16, 8, 0, kEncFixedLds, L.BK, dl);
   EncArgs a;
   a.symbols = symbols;
   a.y = y;
@@ -1385,14 +1491,14 @@ int encode_stage1(bool latents, void* stream, const int32_t* symbols, const floa
   const size_t lds = kEncFixedLds + 16 * (size_t)st.nt_cap + 8 * (size_t)st.ne_cap;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid((uint32_t)L.BK), block(kThreads);
-  if (latents) {
-    if (indexes) k_encode<true, false><<<grid, block, lds, s>>>(a);
-    else k_encode<true, true><<<grid, block, lds, s>>>(a);
-  } else {
-    if (indexes) k_encode<false, false><<<grid, block, lds, s>>>(a);
-    else k_encode<false, true><<<grid, block, lds, s>>>(a);
-  }
-  return check_launch("encode");
+  auto launch = [&](auto kernel) -> int {
+    int r = allow_lds(kernel, lds, dl);
+    if (r) return r;
+    kernel<<<grid, block, lds, s>>>(a);
+    return check_launch("encode");
+  };
+  if (latents) return indexes ? launch(k_encode<true, false>) : launch(k_encode<true, true>);
+  return indexes ? launch(k_encode<false, false>) : launch(k_encode<false, true>);
 }
 
 int decode_impl(bool latents, void* stream, const uint8_t* payload, int64_t payload_bytes,
@@ -1408,8 +1514,11 @@ int decode_impl(bool latents, void* stream, const uint8_t* payload, int64_t payl
   if (payload_bytes < L.header_bytes)
     return fail(GAANS_EINVAL, "payload (%lld bytes) is shorter than its header (%lld bytes)",
                 (long long)payload_bytes, (long long)L.header_bytes);
-  const Stage st = plan_stage(tables, P, 8 * kLutSize + 16, 4, kLutSize,
-                              kLdsMax - dec_fixed_lds(latents));
+  DevLds dl;
+  if ((rc = device_lds(&dl))) return rc;
+  // entry words are read only by dense-bucket lookups
+  const Stage st = plan_stage(tables, P, 8 * kLutSize + 16, tables->total_dense ? 4 : 0,
+                              kLutSize, dec_fixed_lds(latents), L.BK, dl);
   DecArgs a;
   a.payload = payload;
   a.payload_bytes = payload_bytes;
@@ -1431,6 +1540,7 @@ int decode_impl(bool latents, void* stream, const uint8_t* payload, int64_t payl
   a.div_hw = make_udiv((uint32_t)L.HW);
   a.nt_cap = st.nt_cap;
   a.ne_cap = st.ne_cap;
+  a.nd_cap = st.nd_cap;
   a.stage_all = st.stage_all;
   a.ctrl = static_cast<uint32_t*>(ctrl);
   a.status_out = status_out;
@@ -1438,14 +1548,14 @@ int decode_impl(bool latents, void* stream, const uint8_t* payload, int64_t payl
                      4 * (size_t)st.ne_cap + (size_t)kLutSize * st.nd_cap;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid((uint32_t)L.BK), block(kThreads);
-  if (latents) {
-    if (indexes) k_decode<true, false><<<grid, block, lds, s>>>(a);
-    else k_decode<true, true><<<grid, block, lds, s>>>(a);
-  } else {
-    if (indexes) k_decode<false, false><<<grid, block, lds, s>>>(a);
-    else k_decode<false, true><<<grid, block, lds, s>>>(a);
-  }
-  return check_launch("decode");
+  auto launch = [&](auto kernel) -> int {
+    int r = allow_lds(kernel, lds, dl);
+    if (r) return r;
+    kernel<<<grid, block, lds, s>>>(a);
+    return check_launch("decode");
+  };
+  if (latents) return indexes ? launch(k_decode<true, false>) : launch(k_decode<true, true>);
+  return indexes ? launch(k_decode<false, false>) : launch(k_decode<false, true>);
 }
 
 uint64_t fnv_u32(uint64_t h, uint32_t v) {
