@@ -225,8 +225,11 @@ def main():
                           ("batch64_uniform_p16", synthetic.batch_uniform())):
             kt, pb = kernel_times(L, _native, torch, backend, wl, dev)
             n_sym = wl.batch * wl.n
+            alg = 8 * n_sym + pb  # symbols + indexes (int32) + payload, either direction
             extra[label] = {
                 "symbols": n_sym, "payload_bytes": pb,
+                "encode_hbm_frac": round(alg / kt["encode"] / 1e9 / HBM_PEAK_GBPS, 4),
+                "decode_hbm_frac": round(alg / kt["decode"] / 1e9 / HBM_PEAK_GBPS, 4),
                 "encode_kernel_us": round(kt["encode"] * 1e6, 2),
                 "decode_kernel_us": round(kt["decode"] * 1e6, 2),
                 "encode_gsym_s": round(n_sym / kt["encode"] / 1e9, 3),
@@ -237,7 +240,9 @@ def main():
     if args.copy_probe > 0:
         nb = args.copy_probe << 20
         src = torch.empty(nb, dtype=torch.uint8, device=dev)
+        src.fill_(7)  # written first, so that the copy reads ordinary resident data
         dst = torch.empty_like(src)
+        torch.cuda.synchronize()
         dst.copy_(src)
         torch.cuda.synchronize()
 
