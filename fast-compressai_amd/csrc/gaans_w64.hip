@@ -7,17 +7,20 @@
 // refill words out in the same order.  The bytes are defined by the CPU
 // oracle (oracle/gaans_oracle.c).
 //
-// Work mapping: one 256-thread workgroup per chunk.
+// Work mapping: one workgroup per chunk (a coder wave and kMappers mapper
+// waves, 320 threads by default).
 //  - Wave 0 is the coder: it owns the 64 lane states and runs only the
 //    serial part of every step (renormalisation, ballot compaction, state
 //    update).
-//  - Waves 1-3 are mappers: one block of kSB steps ahead of the coder they
+//  - The other waves are mappers: one block of steps ahead of the coder they
 //    load symbols / indexes / latents from HBM (a block ahead again, so the
 //    loads are in flight while the previous block is mapped), look the
 //    tables up, split escapes, hash the indexes and write one 16-byte op
-//    record per lane and step into LDS.
-//  - The CDF tables of the chunk's channels (or all tables, when they fit) are
-//    staged in LDS by the whole workgroup; others are read through L1/L2.
+//    record per lane and step into LDS; the decoder's mappers also store the
+//    decoded values a block behind.
+//  - The CDF tables of the chunk's channels (or all tables, when they are
+//    few) are staged in LDS by the whole workgroup; others are read through
+//    L1/L2.
 //  - encode: emitted words go to an LDS ring, flushed to a per-chunk staging
 //    slot when full; decode: the word stream is prefetched from HBM into
 //    registers and copied into an LDS ring ahead of use.
@@ -62,8 +65,18 @@ constexpr int kLutSize = 1 << kLutBits;
 constexpr uint32_t kHashMul = 0x9E3779B9u;
 constexpr int kMaxOpsPerSymbol = 10;  // main + count + 8 nibbles
 
-constexpr int kSB = 8;                 // steps per block (mapper lead)
-constexpr int kPer = (kSB + kMappers - 1) / kMappers;  // steps per mapper wave and block
+// steps per block: the mappers' lead over the coder, and the steps between
+// two barriers
+#ifndef GAANS_ENC_SB
+#define GAANS_ENC_SB 4
+#endif
+#ifndef GAANS_DEC_SB
+#define GAANS_DEC_SB 8
+#endif
+constexpr int kEncSB = GAANS_ENC_SB;
+constexpr int kDecSB = GAANS_DEC_SB;
+constexpr int kEncPer = (kEncSB + kMappers - 1) / kMappers;  // steps per mapper wave and block
+constexpr int kDecPer = (kDecSB + kMappers - 1) / kMappers;
 constexpr int kPartBytes = (8 * kWaves + 15) / 16 * 16;  // per-wave hash + status
 constexpr int kRingWords = 4096;       // encoder LDS output ring (u16 words)
 constexpr int kStreamRing = 2048;      // decoder LDS stream ring (u16 words)
@@ -245,6 +258,9 @@ __device__ __forceinline__ uint64_t wave_incl_scan(uint64_t v, int lane) {
   return v;
 }
 
+// Lanes (of the active ones) where pred holds, as a scalar mask.
+__device__ __forceinline__ uint64_t ballot(bool pred) { return __builtin_amdgcn_ballot_w64(pred); }
+
 // Keep a wave-uniform value in a scalar register.
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
@@ -369,8 +385,8 @@ struct EncArgs {
 
 // Encoder LDS layout (bytes)
 constexpr int kEncRingBytes = 2 * (kRingWords + kLanes);  // + one spare slot per lane
-constexpr int kEncRecBytes = 2 * kSB * kLanes * 16;        // two blocks of op records
-constexpr int kEncInfoBytes = 2 * kSB * 4;                 // per-step escape op count
+constexpr int kEncRecBytes = 2 * kEncSB * kLanes * 16;        // two blocks of op records
+constexpr int kEncInfoBytes = 2 * kEncSB * 4;                 // per-step escape op count
 constexpr int kEncFixedLds = kEncRingBytes + kEncRecBytes + kEncInfoBytes + kPartBytes;
 
 // last workgroup of an encode launch (wave 0): chunk offsets + payload size +
@@ -488,16 +504,16 @@ __device__ __forceinline__ void ring_flush(uint16_t* __restrict__ wbuf, const ui
 }
 
 // The ring holds the words [wp, fl) (positions mod kRingWords).  The coder
-// flushes it at the start of a block when fewer than kSB * kLanes slots are
+// flushes it at the start of a block when fewer than kEncSB * kLanes slots are
 // free, so the ordinary steps of a block need no check; a step with escapes
 // first makes room for its own words and the rest of its block.
 template <bool kCheck>
 __device__ __forceinline__ void emit_words(bool emit, uint32_t& x, uint16_t* ring,
                                            uint16_t* __restrict__ wbuf, int& wp, int& fl,
                                            int lane) {
-  const uint64_t m = __ballot(emit);
+  const uint64_t m = ballot(emit);
   const int c = __popcll(m);
-  if (kCheck && fl - wp + c > kRingWords - kSB * kLanes) {
+  if (kCheck && fl - wp + c > kRingWords - kEncSB * kLanes) {
     ring_flush(wbuf, ring, wp, fl, lane);
     fl = uni(wp);
   }
@@ -531,13 +547,13 @@ __device__ __forceinline__ EncCur enc_escape_step(const uint4 e, uint32_t M, Enc
   uint32_t x = c.x;
   int wp = c.wp, fl = c.fl;
   // room for the whole step and the rest of the block
-  if (fl - wp > kRingWords - (int)(M + kSB) * kLanes) {
+  if (fl - wp > kRingWords - (int)(M + kEncSB) * kLanes) {
     ring_flush(wbuf, ring, wp, fl, lane);
     fl = wp;
   }
   const uint32_t nops = e.z >> 8;
   const bool escl = nops > 1u;
-  const uint64_t em = __ballot(escl);
+  const uint64_t em = ballot(escl);
   if (__popcll(em) == 1) {
     // one escaping lane: each op index has at most its word, so its ops run
     // on the scalar unit and lane 0 prepends the words
@@ -576,7 +592,7 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
   uint16_t* ring = reinterpret_cast<uint16_t*>(smem);
   uint4* recs = reinterpret_cast<uint4*>(smem + kEncRingBytes);
   uint32_t* info = reinterpret_cast<uint32_t*>(smem + kEncRingBytes + kEncRecBytes);
-  uint32_t* part = info + 2 * kSB;  // per-wave hash [0, kWaves) and status [kWaves, 2 kWaves)
+  uint32_t* part = info + 2 * kEncSB;  // per-wave hash [0, kWaves) and status [kWaves, 2 kWaves)
   uint4* lmeta = reinterpret_cast<uint4*>(smem + kEncFixedLds);
   uint2* lent = reinterpret_cast<uint2*>(smem + kEncFixedLds + 16 * a.nt_cap);
 
@@ -590,7 +606,7 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
   chunk_range(g, a.K, a.N, a.chunk_len, row, start, len, k);
   const int T = (len + kLanes - 1) / kLanes;
   const int A = len < kLanes ? len : kLanes;
-  const int nblk = (T + kSB - 1) / kSB;
+  const int nblk = (T + kEncSB - 1) / kEncSB;
   uint16_t* __restrict__ wbuf = a.words + g * a.cap_words;
   int wp = a.cap_words;  // coder: wave-uniform write cursor (backwards)
   int fl = a.cap_words;  // coder: words at [fl, cap) are already in wbuf
@@ -616,14 +632,14 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
     stage_tables(tb, lmeta, lent, nullptr, nullptr, nullptr, 0u, a.M, t_lo, t_hi, tid);
 
     // mapper wave w (1..kMappers) owns steps u = w - 1 + kMappers e of every block
-    int32_t ca[kPer], cb[kPer], na[kPer], nb[kPer];
-    float cm[kPer], nm[kPer];
+    int32_t ca[kEncPer], cb[kEncPer], na[kEncPer], nb[kEncPer];
+    float cm[kEncPer], nm[kEncPer];
     auto load_block = [&](int j, int32_t* ia, int32_t* ib, float* im) {
 #pragma unroll
-      for (int e = 0; e < kPer; ++e) {
+      for (int e = 0; e < kEncPer; ++e) {
         const int u = (wid - 1) + kMappers * e;
-        if (kSB % kMappers != 0 && u >= kSB) break;
-        int p = lane + kLanes * (j * kSB + u);
+        if (kEncSB % kMappers != 0 && u >= kEncSB) break;
+        int p = lane + kLanes * (j * kEncSB + u);
         p = p < len ? p : len - 1;  // loads stay in the chunk; results are masked
         const int64_t i = row + start + p;
         if (kLatents) {
@@ -638,24 +654,24 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
     };
     auto map_steps = [&](int j, auto lds_tag) {
       constexpr bool kLds = decltype(lds_tag)::value;
-      uint4* dst = recs + (j & 1) * kSB * kLanes;
-      uint32_t nops[kPer];
+      uint4* dst = recs + (j & 1) * kEncSB * kLanes;
+      uint32_t nops[kEncPer];
 #pragma unroll
-      for (int e = 0; e < kPer; ++e) {
+      for (int e = 0; e < kEncPer; ++e) {
         const int u = (wid - 1) + kMappers * e;
-        if (kSB % kMappers != 0 && u >= kSB) break;
-        const uint4 r = enc_record<kLatents, kImplicit>(a, tb, kLds, lane, j * kSB + u, len,
+        if (kEncSB % kMappers != 0 && u >= kEncSB) break;
+        const uint4 r = enc_record<kLatents, kImplicit>(a, tb, kLds, lane, j * kEncSB + u, len,
                                                         start, ca[e], cb[e], cm[e], hash, status);
         dst[u * kLanes + lane] = r;
         nops[e] = r.z >> 8;
       }
 #pragma unroll
-      for (int e = 0; e < kPer; ++e) {
+      for (int e = 0; e < kEncPer; ++e) {
         const int u = (wid - 1) + kMappers * e;
-        if (kSB % kMappers != 0 && u >= kSB) break;
+        if (kEncSB % kMappers != 0 && u >= kEncSB) break;
         uint32_t mt = 0;
-        if (__ballot(nops[e] > 1u)) mt = wave_max(nops[e]);  // escapes are rare
-        if (lane == 0) info[(j & 1) * kSB + u] = mt;
+        if (ballot(nops[e] > 1u)) mt = wave_max(nops[e]);  // escapes are rare
+        if (lane == 0) info[(j & 1) * kEncSB + u] = mt;
       }
     };
     auto map_block = [&](int j) {
@@ -664,12 +680,12 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
       if (!kImplicit && lds) {
         bool outside = false;
 #pragma unroll
-        for (int e = 0; e < kPer; ++e) {
+        for (int e = 0; e < kEncPer; ++e) {
           const int u = (wid - 1) + kMappers * e;
-          outside |= u < kSB && lane + kLanes * (j * kSB + u) < len &&
+          outside |= u < kEncSB && lane + kLanes * (j * kEncSB + u) < len &&
                      (uint32_t)(cb[e] - tb.t_lo) >= (uint32_t)tb.nt;
         }
-        lds = __ballot(outside) == 0;
+        lds = ballot(outside) == 0;
       }
       if (lds) map_steps(j, std::true_type{});
       else map_steps(j, std::false_type{});
@@ -683,33 +699,33 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
       __syncthreads();
       for (int j = nblk - 1; j >= 0; --j) {
         // coder: steps of block j, last to first
-        if (fl - wp > kRingWords - kSB * kLanes) {
+        if (fl - wp > kRingWords - kEncSB * kLanes) {
           ring_flush(wbuf, ring, wp, fl, lane);
           fl = wp;
         }
-        const uint4* src = recs + (j & 1) * kSB * kLanes;
-        uint4 r[kSB];
-        uint32_t mt[kSB];
+        const uint4* src = recs + (j & 1) * kEncSB * kLanes;
+        uint4 r[kEncSB];
+        uint32_t mt[kEncSB];
 #pragma unroll
-        for (int u = 0; u < kSB; ++u) {
+        for (int u = 0; u < kEncSB; ++u) {
           r[u] = src[u * kLanes + lane];
-          mt[u] = (uint32_t)uni((int)info[(j & 1) * kSB + u]);
+          mt[u] = (uint32_t)uni((int)info[(j & 1) * kEncSB + u]);
         }
         uint32_t any_esc = 0;
 #pragma unroll
-        for (int u = 0; u < kSB; ++u) any_esc |= mt[u];
-        if ((j + 1) * kSB <= T && any_esc == 0) {
+        for (int u = 0; u < kEncSB; ++u) any_esc |= mt[u];
+        if ((j + 1) * kEncSB <= T && any_esc == 0) {
           // common case: a full block without escapes, no per-step branches
 #pragma unroll
-          for (int u = kSB - 1; u >= 0; --u) {
+          for (int u = kEncSB - 1; u >= 0; --u) {
             emit_words<false>((x >> 16) >= 65536u - (r[u].x >> 16), x, ring, wbuf, wp, fl, lane);
             x = enc_apply(x, r[u]);
           }
         } else {
           // last block or escapes: per-step branches
 #pragma unroll
-          for (int u = kSB - 1; u >= 0; --u) {
-            if (__builtin_expect(j * kSB + u >= T, 0)) continue;
+          for (int u = kEncSB - 1; u >= 0; --u) {
+            if (__builtin_expect(j * kEncSB + u >= T, 0)) continue;
             if (__builtin_expect(mt[u] == 0, 1)) {
               emit_words<false>((x >> 16) >= 65536u - (r[u].x >> 16), x, ring, wbuf, wp, fl, lane);
               x = enc_apply(x, r[u]);
@@ -734,7 +750,7 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
       for (int j = nblk - 1; j >= 0; --j) {
         if (j > 0) {  // mappers: block j - 1 while the coder codes block j
 #pragma unroll
-          for (int e = 0; e < kPer; ++e) {
+          for (int e = 0; e < kEncPer; ++e) {
             ca[e] = na[e];
             cb[e] = nb[e];
             cm[e] = nm[e];
@@ -869,9 +885,9 @@ struct DecArgs {
 
 // Decoder LDS layout (bytes); the median buffer is there for latents only
 constexpr int kDecRingBytes = 2 * kStreamRing;
-constexpr int kDecRecBytes = 2 * kSB * kLanes * 16;
-constexpr int kDecInfoBytes = 2 * kSB * 4;
-constexpr int kDecMedBytes = 2 * kSB * kLanes * 4;
+constexpr int kDecRecBytes = 2 * kDecSB * kLanes * 16;
+constexpr int kDecInfoBytes = 2 * kDecSB * 4;
+constexpr int kDecMedBytes = 2 * kDecSB * kLanes * 4;
 constexpr int dec_fixed_lds(bool latents) {
   return kDecRingBytes + kDecRecBytes + kDecInfoBytes + kPartBytes +
          (latents ? kDecMedBytes : 0);
@@ -896,7 +912,7 @@ __device__ __forceinline__ uint4 dec_record(const DecArgs& a, const Tabs& tb, in
   tbi = ok ? tbi : (tb.nt > 0 ? tb.t_lo : 0);
   hash += ok ? ((uint32_t)(tbi + 1) ^ ((uint32_t)p * kHashMul)) : 0u;
   const bool staged = (uint32_t)(tbi - tb.t_lo) < (uint32_t)tb.nt;
-  all_lds = __ballot(!staged) == 0;
+  all_lds = ballot(!staged) == 0;
   uint32_t nsym, ebase;
   int32_t offset;
   if (all_lds) {
@@ -952,12 +968,12 @@ __device__ __forceinline__ void dec_lookup(const Tabs& tb, const uint4 r, uint32
 //    kLowWater words are buffered, then prefetches the next batch.  This is the
 //    only place pf is loaded, so the loads stay in flight between blocks.
 //  - The main-op refills of a block (at most one word per lane and step) need
-//    no check: a block starts with at least kSB * kLanes buffered words.
+//    no check: a block starts with at least kDecSB * kLanes buffered words.
 //  - Escape refills check that margin and, when a block has consumed that
 //    much, copy the next batch synchronously (its own loads; pf is marked stale
 //    and refetched at the next block start).
 constexpr int kLowWater = 1024;
-static_assert(kLowWater >= kSB * kLanes && kLowWater + kPfWords <= kStreamRing,
+static_assert(kLowWater >= kDecSB * kLanes && kLowWater + kPfWords <= kStreamRing,
               "decoder stream ring too small");
 struct Stream {
   const uint32_t* __restrict__ s32;
@@ -991,7 +1007,7 @@ __device__ __forceinline__ void stream_block_start(Stream& S, uint32_t* ring32, 
   }
 }
 
-// Escape refill with fewer than kSB * kLanes buffered words: copy the next
+// Escape refill with fewer than kDecSB * kLanes buffered words: copy the next
 // batch now.
 __device__ __forceinline__ void stream_sync_batch(Stream& S, uint32_t* ring32, int lane) {
   uint32_t w[kPfU32];
@@ -1009,11 +1025,12 @@ __device__ __forceinline__ void stream_sync_batch(Stream& S, uint32_t* ring32, i
 template <bool kCheck>
 __device__ __forceinline__ void dec_refill(bool need, uint32_t& x, Stream& S,
                                            const uint16_t* ring, uint32_t* ring32, int lane) {
-  if (kCheck && S.filled - S.rp < kSB * kLanes && S.filled < S.q)
+  if (kCheck && S.filled - S.rp < kDecSB * kLanes && S.filled < S.q)
     stream_sync_batch(S, ring32, lane);
-  const uint64_t m = __ballot(need);
+  const uint64_t m = ballot(need);
+  // every lane reads (no branch around the read); only refilling lanes keep it
   const uint32_t w = ring[(S.rp + (int)lane_rank(m)) & (kStreamRing - 1)];
-  x = need ? ((x << 16) | w) : x;
+  x = (x << (need ? 16u : 0u)) | (w & (need ? 0xffffu : 0u));
   S.rp += __popcll(m);
 }
 
@@ -1034,13 +1051,13 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint4 r, uint
   // exactly when it wraps below the offset
   int32_t o = (int32_t)(s + r.z);
   bool oob = o < (int32_t)r.z;
-  const uint64_t em = __ballot(esc);
+  const uint64_t em = ballot(esc);
   if (__builtin_expect(em != 0, 0)) {
    if (__popcll(em) == 1) {
     // one escaping lane: its refill words are consecutive in the stream; the
     // lane takes them from 5 or 6 words read at once (the margin covers the
     // at most 9 words and the rest of the block)
-    if (S.filled - S.rp < kSB * kLanes && S.filled < S.q) stream_sync_batch(S, ring32, lane);
+    if (S.filled - S.rp < kDecSB * kLanes && S.filled < S.q) stream_sync_batch(S, ring32, lane);
     const int rp = S.rp;
     const int e0 = rp & ~1;  // even word at or below rp
     const uint32_t d0 = ring32[(e0 >> 1) & (kStreamRing / 2 - 1)];
@@ -1087,7 +1104,7 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint4 r, uint
     uint32_t raw = 0;
     for (uint32_t jj = 0; jj < 8u; ++jj) {
       const bool part = esc & (jj < n);
-      if (__ballot(part) == 0) break;
+      if (ballot(part) == 0) break;
       raw |= part ? ((x & 15u) << (4 * jj)) : 0u;
       x = part ? (x >> 4) : x;
       dec_refill<true>(part & (x < kStateLow), x, S, ring, ring32, lane);
@@ -1110,7 +1127,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
   uint32_t* sring32 = reinterpret_cast<uint32_t*>(smem);
   uint4* recs = reinterpret_cast<uint4*>(smem + kDecRingBytes);
   uint32_t* info = reinterpret_cast<uint32_t*>(smem + kDecRingBytes + kDecRecBytes);
-  uint32_t* part = info + 2 * kSB;  // per-wave hash [0, kWaves) and status [kWaves, 2 kWaves)
+  uint32_t* part = info + 2 * kDecSB;  // per-wave hash [0, kWaves) and status [kWaves, 2 kWaves)
   float* med = reinterpret_cast<float*>(smem + kDecRingBytes + kDecRecBytes + kDecInfoBytes +
                                         kPartBytes);
   uint8_t* tsm = smem + dec_fixed_lds(kLatents);
@@ -1143,7 +1160,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
   chunk_range(g, a.K, a.N, (int32_t)a.chunk_len, row, start, len, k);
   const int T = (len + kLanes - 1) / kLanes;
   const int A = len < kLanes ? len : kLanes;
-  const int nblk = (T + kSB - 1) / kSB;
+  const int nblk = (T + kDecSB - 1) / kDecSB;
   uint32_t beg = 0, endo = 0, want_hash = 0;
   int64_t cb = 0;
   if (ok) {
@@ -1170,47 +1187,47 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
     tb.ldense = ldense;
     const uint8_t* cdata = a.payload + a.header_bytes + beg;
 
-    int32_t cbx[kPer], nbx[kPer];
-    float cm[kPer], nm[kPer];
+    int32_t cbx[kDecPer], nbx[kDecPer];
+    float cm[kDecPer], nm[kDecPer];
     auto load_block = [&](int j, int32_t* ib, float* im) {
 #pragma unroll
-      for (int e = 0; e < kPer; ++e) {
+      for (int e = 0; e < kDecPer; ++e) {
         const int u = (wid - 1) + kMappers * e;
-        if (kSB % kMappers != 0 && u >= kSB) break;
-        int p = lane + kLanes * (j * kSB + u);
+        if (kDecSB % kMappers != 0 && u >= kDecSB) break;
+        int p = lane + kLanes * (j * kDecSB + u);
         p = p < len ? p : len - 1;  // loads stay in the chunk; results are masked
         ib[e] = kImplicit ? 0 : a.indexes[row + start + p];
         im[e] = kLatents ? a.medians[udiv((uint32_t)(start + p), a.div_hw)] : 0.0f;
       }
     };
     auto store_block = [&](int j) {  // decoded values of block j -> HBM
-      const uint4* src = recs + (j & 1) * kSB * kLanes;
+      const uint4* src = recs + (j & 1) * kDecSB * kLanes;
 #pragma unroll
-      for (int e = 0; e < kPer; ++e) {
+      for (int e = 0; e < kDecPer; ++e) {
         const int u = (wid - 1) + kMappers * e;
-        if (kSB % kMappers != 0 && u >= kSB) break;
+        if (kDecSB % kMappers != 0 && u >= kDecSB) break;
         const uint32_t v = src[u * kLanes + lane].x;
-        const int p = lane + kLanes * (j * kSB + u);
+        const int p = lane + kLanes * (j * kDecSB + u);
         if (p < len) {
           const int64_t i = row + start + p;
           if (kLatents)
-            a.out_y[i] = __fadd_rn((float)(int32_t)v, med[((j & 1) * kSB + u) * kLanes + lane]);
+            a.out_y[i] = __fadd_rn((float)(int32_t)v, med[((j & 1) * kDecSB + u) * kLanes + lane]);
           else a.out_sym[i] = (int32_t)v;
         }
       }
     };
     auto map_block = [&](int j) {
-      uint4* dst = recs + (j & 1) * kSB * kLanes;
+      uint4* dst = recs + (j & 1) * kDecSB * kLanes;
 #pragma unroll
-      for (int e = 0; e < kPer; ++e) {
+      for (int e = 0; e < kDecPer; ++e) {
         const int u = (wid - 1) + kMappers * e;
-        if (kSB % kMappers != 0 && u >= kSB) break;
+        if (kDecSB % kMappers != 0 && u >= kDecSB) break;
         bool all_lds;
-        const uint4 r = dec_record<kImplicit>(a, tb, lane, j * kSB + u, len, start, cbx[e], hash,
+        const uint4 r = dec_record<kImplicit>(a, tb, lane, j * kDecSB + u, len, start, cbx[e], hash,
                                               status, all_lds);
         dst[u * kLanes + lane] = r;
-        if (kLatents) med[((j & 1) * kSB + u) * kLanes + lane] = cm[e];
-        if (lane == 0) info[(j & 1) * kSB + u] = all_lds ? 1u : 0u;
+        if (kLatents) med[((j & 1) * kDecSB + u) * kLanes + lane] = cm[e];
+        if (lane == 0) info[(j & 1) * kDecSB + u] = all_lds ? 1u : 0u;
       }
     };
 
@@ -1258,33 +1275,33 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
       __syncthreads();
       for (int j = 0; j < nblk; ++j) {
         stream_block_start(S, sring32, lane);
-        uint4* src = recs + (j & 1) * kSB * kLanes;
-        uint4 r[kSB];
-        uint32_t fl[kSB], ov[kSB];
+        uint4* src = recs + (j & 1) * kDecSB * kLanes;
+        uint4 r[kDecSB];
+        uint32_t fl[kDecSB], ov[kDecSB];
 #pragma unroll
-        for (int u = 0; u < kSB; ++u) {
+        for (int u = 0; u < kDecSB; ++u) {
           r[u] = src[u * kLanes + lane];
-          fl[u] = (uint32_t)uni((int)info[(j & 1) * kSB + u]);
+          fl[u] = (uint32_t)uni((int)info[(j & 1) * kDecSB + u]);
         }
         uint32_t all_lds = 1;
 #pragma unroll
-        for (int u = 0; u < kSB; ++u) all_lds &= fl[u];
-        if ((j + 1) * kSB <= T && all_lds) {
+        for (int u = 0; u < kDecSB; ++u) all_lds &= fl[u];
+        if ((j + 1) * kDecSB <= T && all_lds) {
           // common case: a full block with LDS tables, no per-step branches
 #pragma unroll
-          for (int u = 0; u < kSB; ++u)
+          for (int u = 0; u < kDecSB; ++u)
             ov[u] = dec_step<true>(tb, r[u], x, S, sring, sring32, status, lane);
           // decoded values replace the records' x words; the mappers store them
 #pragma unroll
-          for (int u = 0; u < kSB; ++u)
+          for (int u = 0; u < kDecSB; ++u)
             reinterpret_cast<uint32_t*>(src + u * kLanes + lane)[0] = ov[u];
         } else {
           // last block or tables outside LDS: one step at a time
 #pragma unroll 1
-          for (int u = 0; u < kSB && j * kSB + u < T; ++u) {
+          for (int u = 0; u < kDecSB && j * kDecSB + u < T; ++u) {
             const uint4 ru = src[u * kLanes + lane];
             const uint32_t v =
-                uni((int)info[(j & 1) * kSB + u])
+                uni((int)info[(j & 1) * kDecSB + u])
                     ? dec_step<true>(tb, ru, x, S, sring, sring32, status, lane)
                     : dec_step<false>(tb, ru, x, S, sring, sring32, status, lane);
             reinterpret_cast<uint32_t*>(src + u * kLanes + lane)[0] = v;
@@ -1302,7 +1319,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
         if (j > 0) store_block(j - 1);
         if (j + 1 < nblk) {
 #pragma unroll
-          for (int e = 0; e < kPer; ++e) {
+          for (int e = 0; e < kDecPer; ++e) {
             cbx[e] = nbx[e];
             cm[e] = nm[e];
           }
