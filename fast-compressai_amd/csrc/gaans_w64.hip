@@ -122,8 +122,11 @@ struct TabHdr {
   uint32_t max_nsym;
   uint32_t dense_off;    // byte offset of the dense blocks
   uint32_t total_dense;  // dense blocks over all tables
-  uint32_t reserved[3];
+  uint32_t flags;        // kTabOffsetsSafe
+  uint32_t reserved[2];
 };
+// every offset <= INT32_MAX - 65535: symbol index + offset cannot overflow
+constexpr uint32_t kTabOffsetsSafe = 1u;
 static_assert(sizeof(TabHdr) == 64, "table header is 64 bytes");
 
 struct TabMeta {
@@ -1030,16 +1033,18 @@ __device__ __forceinline__ void dec_refill(bool need, uint32_t& x, Stream& S,
   const uint64_t m = ballot(need);
   // every lane reads (no branch around the read); only refilling lanes keep it
   const uint32_t w = ring[(S.rp + (int)lane_rank(m)) & (kStreamRing - 1)];
-  x = (x << (need ? 16u : 0u)) | (w & (need ? 0xffffu : 0u));
+  asm volatile("" ::"v"(w));
+  x = need ? ((x << 16) | w) : x;
   S.rp += __popcll(m);
 }
 
-// One decode step of the coder wave; returns the decoded value.
-template <bool kLds>
+// One decode step of the coder wave; returns the decoded value.  kFull: every
+// lane is active and no offset can overflow with a symbol index.
+template <bool kLds, bool kFull>
 __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint4 r, uint32_t& x,
                                              Stream& S, const uint16_t* ring, uint32_t* ring32,
                                              uint32_t& status, int lane) {
-  const bool act = r.y != 0xffffffffu;
+  const bool act = kFull || r.y != 0xffffffffu;
   const uint32_t cum = x & 0xffffu;
   uint32_t s, st, fr;
   dec_lookup<kLds>(tb, r, cum, act, s, st, fr);
@@ -1050,7 +1055,7 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint4 r, uint
   // value + offset for an ordinary symbol: s < 2^16, so the int32 sum overflows
   // exactly when it wraps below the offset
   int32_t o = (int32_t)(s + r.z);
-  bool oob = o < (int32_t)r.z;
+  bool oob = !kFull && o < (int32_t)r.z;
   const uint64_t em = ballot(esc);
   if (__builtin_expect(em != 0, 0)) {
    if (__popcll(em) == 1) {
@@ -1180,6 +1185,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
     tb.gent = reinterpret_cast<const uint2*>(a.tables + th->ent_off);
     tb.glut = reinterpret_cast<const uint64_t*>(a.tables + th->lut_off);
     tb.gdense = a.tables + th->dense_off;
+    const bool offsets_safe = (th->flags & kTabOffsetsSafe) != 0;
     tb.lmeta = lmeta;
     tb.lent = nullptr;
     tb.lent32 = lent32;
@@ -1286,11 +1292,12 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
         uint32_t all_lds = 1;
 #pragma unroll
         for (int u = 0; u < kDecSB; ++u) all_lds &= fl[u];
-        if ((j + 1) * kDecSB <= T && all_lds) {
-          // common case: a full block with LDS tables, no per-step branches
+        if ((j + 1) * kDecSB * kLanes <= len && all_lds && offsets_safe) {
+          // common case: every lane of the block active, LDS tables, no
+          // per-step branches
 #pragma unroll
           for (int u = 0; u < kDecSB; ++u)
-            ov[u] = dec_step<true>(tb, r[u], x, S, sring, sring32, status, lane);
+            ov[u] = dec_step<true, true>(tb, r[u], x, S, sring, sring32, status, lane);
           // decoded values replace the records' x words; the mappers store them
 #pragma unroll
           for (int u = 0; u < kDecSB; ++u)
@@ -1302,8 +1309,8 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
             const uint4 ru = src[u * kLanes + lane];
             const uint32_t v =
                 uni((int)info[(j & 1) * kDecSB + u])
-                    ? dec_step<true>(tb, ru, x, S, sring, sring32, status, lane)
-                    : dec_step<false>(tb, ru, x, S, sring, sring32, status, lane);
+                    ? dec_step<true, false>(tb, ru, x, S, sring, sring32, status, lane)
+                    : dec_step<false, false>(tb, ru, x, S, sring, sring32, status, lane);
             reinterpret_cast<uint32_t*>(src + u * kLanes + lane)[0] = v;
           }
         }
@@ -1757,6 +1764,9 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
   h->max_nsym = max_nsym;
   h->dense_off = (uint32_t)dense_off;
   h->total_dense = (uint32_t)total_dense;
+  bool safe = true;
+  for (int32_t t = 0; t < M; ++t) safe &= offsets[t] <= INT32_MAX - 65535;
+  h->flags = safe ? kTabOffsetsSafe : 0u;
   desc->dev = nullptr;
   desc->bytes = need;
   desc->M = M;
