@@ -39,6 +39,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include <string>
 #include <type_traits>
 
@@ -425,6 +427,9 @@ __device__ void encode_finish(const EncArgs& a, int lane) {
       a.info_out[1] = st;
     }
     __threadfence_system();
+    // completion word, written after the info words are visible to the host
+    if (a.info_out)
+      __hip_atomic_store(&a.info_out[2], 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     __hip_atomic_store(&a.ctrl[kCtrlEncDone], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
@@ -1361,8 +1366,9 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
     if (done == (uint32_t)(a.BK - 1)) {
       const uint32_t all = __hip_atomic_exchange(&a.ctrl[kCtrlDecStatus], 0u, __ATOMIC_ACQ_REL,
                                                  __HIP_MEMORY_SCOPE_AGENT);
-      *a.status_out = all;
+      a.status_out[0] = all;
       __threadfence_system();
+      __hip_atomic_store(&a.status_out[1], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
       __hip_atomic_store(&a.ctrl[kCtrlDecDone], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
@@ -1390,7 +1396,7 @@ int check_tables_arg(const gaans_tables* t) {
 // LDS of the current device: per workgroup and per CU, and the CU count
 // (queried once per device).
 struct DevLds {
-  int per_block, per_cu, cus;
+  int per_block, per_cu, cus, dev;
 };
 
 int device_lds(DevLds* out) {
@@ -1400,7 +1406,7 @@ int device_lds(DevLds* out) {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
     return fail(GAANS_EHIP, "hipGetDevice failed");
   if (!__atomic_load_n(&ready[dev], __ATOMIC_ACQUIRE)) {
-    DevLds d{0, 0, 0};
+    DevLds d{0, 0, 0, dev};
     if (hipDeviceGetAttribute(&d.per_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) !=
             hipSuccess ||
         hipDeviceGetAttribute(&d.per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
@@ -1409,6 +1415,7 @@ int device_lds(DevLds* out) {
         d.per_block <= 0 || d.cus <= 0)
       return fail(GAANS_EHIP, "device attribute query failed");
     if (d.per_cu < d.per_block) d.per_cu = d.per_block;
+    d.dev = dev;
     cache[dev] = d;
     __atomic_store_n(&ready[dev], 1, __ATOMIC_RELEASE);
   }
@@ -1458,12 +1465,22 @@ Stage plan_stage(const gaans_tables* t, int64_t P, int64_t per_table, int64_t pe
 }
 
 // Allow dynamic LDS above the default limit (once per kernel and device).
-template <typename K>
-int allow_lds(K kernel, size_t bytes, const DevLds& d) {
+int allow_lds(const void* kernel, size_t bytes, const DevLds& d) {
   if (bytes <= 64 * 1024) return GAANS_OK;
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, d.per_block) != hipSuccess)
+  static std::mutex mu;
+  static const void* done_fn[64];
+  static int done_dev[64];
+  static int n_done = 0;
+  std::lock_guard<std::mutex> g(mu);
+  for (int i = 0; i < n_done; ++i)
+    if (done_fn[i] == kernel && done_dev[i] == d.dev) return GAANS_OK;
+  if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, d.per_block) !=
+      hipSuccess)
     return fail(GAANS_EHIP, "cannot raise the LDS limit of a kernel to %d bytes", d.per_block);
+  if (n_done < 64) {
+    done_fn[n_done] = kernel;
+    done_dev[n_done++] = d.dev;
+  }
   return GAANS_OK;
 }
 
@@ -1516,7 +1533,7 @@ int encode_stage1(bool latents, void* stream, const int32_t* symbols, const floa
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid((uint32_t)L.BK), block(kThreads);
   auto launch = [&](auto kernel) -> int {
-    int r = allow_lds(kernel, lds, dl);
+    int r = allow_lds(reinterpret_cast<const void*>(kernel), lds, dl);
     if (r) return r;
     kernel<<<grid, block, lds, s>>>(a);
     return check_launch("encode");
@@ -1573,7 +1590,7 @@ int decode_impl(bool latents, void* stream, const uint8_t* payload, int64_t payl
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid((uint32_t)L.BK), block(kThreads);
   auto launch = [&](auto kernel) -> int {
-    int r = allow_lds(kernel, lds, dl);
+    int r = allow_lds(reinterpret_cast<const void*>(kernel), lds, dl);
     if (r) return r;
     kernel<<<grid, block, lds, s>>>(a);
     return check_launch("decode");
@@ -1845,6 +1862,22 @@ int gaans_decode_latents(void* stream, const uint8_t* payload_dev, int64_t paylo
                          float* y_hat_dev, void* ctrl_dev, uint32_t* status_out) {
   return decode_impl(true, stream, payload_dev, payload_bytes, indexes_dev, tables, medians_dev,
                      B, N, C, P, nullptr, y_hat_dev, ctrl_dev, status_out);
+}
+
+int gaans_wait_host_word(void* stream, const uint32_t* word) {
+  if (!word) return fail(GAANS_EINVAL, "completion word pointer is NULL");
+  for (uint32_t i = 1;; ++i) {
+    if (__atomic_load_n(word, __ATOMIC_ACQUIRE) != 0) return GAANS_OK;
+    if ((i & 255u) == 0) {
+      const hipError_t e = hipStreamQuery(static_cast<hipStream_t>(stream));
+      if (e == hipSuccess) {
+        if (__atomic_load_n(word, __ATOMIC_ACQUIRE) != 0) return GAANS_OK;
+        return fail(GAANS_EHIP, "stream finished without setting the completion word");
+      }
+      if (e != hipErrorNotReady)
+        return fail(GAANS_EHIP, "stream reported an error: %s", hipGetErrorString(e));
+    }
+  }
 }
 
 int gaans_host_selftest(void) {

@@ -15,7 +15,7 @@ import threading
 from .errors import CoderDependencyError
 
 LIB_NAME = "libgaans_w64.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 CTRL_BYTES = 256
 
 # return codes
@@ -85,6 +85,7 @@ def _declare(L) -> None:
         "gaans_decode_symbols": ([p, p, i64, p, T, i64, i64, i64, i64, p, p, p], ctypes.c_int),
         "gaans_decode_latents": ([p, p, i64, p, T, p, i64, i64, i64, i64, p, p, p],
                                  ctypes.c_int),
+        "gaans_wait_host_word": ([p, p], ctypes.c_int),
         "gaans_host_selftest": ([], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
@@ -115,21 +116,10 @@ def lib():
     return _lib
 
 
-_hip = None
-
-
-def stream_synchronize(stream_ptr: int) -> None:
-    """hipStreamSynchronize on a raw stream handle (torch's streams are HIP
-    streams); cheaper than constructing a torch stream object per call."""
-    global _hip
-    if _hip is None:
-        h = ctypes.CDLL("libamdhip64.so")
-        h.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
-        h.hipStreamSynchronize.restype = ctypes.c_int
-        _hip = h
-    rc = _hip.hipStreamSynchronize(stream_ptr)
-    if rc != 0:
-        raise CoderDependencyError(f"hipStreamSynchronize failed with HIP error {rc}")
+def wait_host_word(stream_ptr: int, word_ptr: int, what: str) -> None:
+    """Wait for a launch's completion word in pinned host memory (the one
+    host synchronisation of an encode or decode call)."""
+    check(_lib.gaans_wait_host_word(stream_ptr, word_ptr), what)
 
 
 def last_error() -> str:

@@ -3,13 +3,15 @@
 Per (device, stream) the engine keeps a control block (device memory, zeroed
 once; every launch leaves it zeroed), a reusable workspace, and two small
 pinned host buffers that the kernels' last workgroup writes the payload
-size / status into.  Calls on one stream are ordered, so these buffers are
-never shared by two calls in flight.
+size / status into, followed by a completion word.  Calls on one stream are
+ordered, so these buffers are never shared by two calls in flight.
 
 Encode enqueues the coding kernel and the pack kernel back to back (the
-pack writes into a worst-case-sized buffer), then makes its one host
-synchronisation and reads the payload size.  Decode enqueues one kernel and
-synchronises once to read the status word.  Reference host APIs replaced:
+pack writes into a worst-case-sized buffer), then waits for the coding
+kernel's completion word and reads the payload size; the pack kernel may
+still be running when encode returns, ordered before any later work on the
+stream.  Decode enqueues one kernel and waits for its completion word to
+read the status word.  Reference host APIs replaced:
 ``encode_with_indexes_warp_v2_cuda`` (``warp_ans_kernel_v2.cu:183-306``, two
 syncs and six launches) and ``decode_with_indexes_warp_cuda``
 (``warp_ans_kernel.cu:477-544``, one sync and four launches).
@@ -36,6 +38,8 @@ class _StreamState:
         self.status = torch.zeros(4, dtype=torch.int32, pin_memory=True)
         self.info_np = self.info.numpy()      # host views of the pinned words
         self.status_np = self.status.numpy()
+        self.info_done = self.info.data_ptr() + 16    # completion words
+        self.status_done = self.status.data_ptr() + 4
         self.workspace = torch.empty(0, dtype=torch.uint8, device=device)
 
     def ws(self, nbytes: int) -> torch.Tensor:
@@ -117,6 +121,7 @@ def encode(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,
         st = _state(index, sp)
         ws = st.ws(int(lay.workspace_bytes))
         out = torch.empty(int(lay.max_payload_bytes), dtype=torch.uint8, device=ws.device)
+        st.info_np[2] = 0
         if y is not None:
             rc = L.gaans_encode_latents(sp, y.data_ptr(), medians.data_ptr(), _ptr(indexes),
                                         tables.ref, B, N, C, P, ws.data_ptr(), ws.numel(),
@@ -129,7 +134,7 @@ def encode(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,
         rc = L.gaans_encode_pack(sp, ws.data_ptr(), ws.numel(), tables.ref, B, N, C, P,
                                  out.data_ptr(), out.numel())
         _native.check(rc, "GA-ANS pack")
-        _native.stream_synchronize(sp)  # the one host synchronisation
+        _native.wait_host_word(sp, st.info_done, "GA-ANS encode")  # the one host wait
         total, status = int(st.info_np[0]), int(st.info_np[1])
     if status:
         raise CoderInputError(f"GA-ANS encode failed: {_native.describe_status(status)}")
@@ -151,6 +156,7 @@ def decode(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int,
     with _on_device(index):
         sp = torch._C._cuda_getCurrentRawStream(index)
         st = _state(index, sp)
+        st.status_np[1] = 0
         if medians is not None:
             out = torch.empty((B, N), dtype=torch.float32, device=packed.device)
             rc = L.gaans_decode_latents(sp, packed.data_ptr(), packed.numel(), _ptr(indexes),
@@ -162,7 +168,7 @@ def decode(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int,
                                         tables.ref, B, N, C, P, out.data_ptr(),
                                         st.ctrl.data_ptr(), st.status.data_ptr())
         _native.check(rc, "GA-ANS decode")
-        _native.stream_synchronize(sp)  # the one host synchronisation
+        _native.wait_host_word(sp, st.status_done, "GA-ANS decode")  # the one host wait
         status = int(st.status_np[0])
     if status:
         raise CoderInputError(f"warp_div decode failed: {_native.describe_status(status)}")

@@ -33,7 +33,8 @@
  *  - Problems the kernels find (bad symbols, corrupt payloads) are reported
  *    as GAANS_ST_* bits in a status word that the last block of the launch
  *    writes to caller memory (device or pinned host memory); read it after
- *    the stream has finished.
+ *    the stream has finished, or, with pinned host memory, once the
+ *    launch's completion word is set (gaans_wait_host_word).
  *
  * Payload format "gaans-w64-v1": defined byte for byte by the CPU oracle,
  * oracle/gaans_oracle.c.
@@ -48,7 +49,7 @@
 extern "C" {
 #endif
 
-#define GAANS_ABI_VERSION 3
+#define GAANS_ABI_VERSION 4
 #define GAANS_CTRL_BYTES 256
 
 /* return codes */
@@ -126,7 +127,8 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes,
  * The launch's last block scans the chunk sizes into payload offsets and
  * writes info = {u64 payload bytes incl. header, u64 status} both to the
  * workspace (at layout->ws_info) and, when info_out is not NULL, to
- * info_out (device or pinned host memory).  `indexes_dev` may be NULL: then
+ * info_out[0..1] (device or pinned host memory), then sets the completion
+ * word info_out[2] to 1 (info_out holds 3 u64).  `indexes_dev` may be NULL: then
  * position i of a row uses table i / HW (CompressAI EntropyBottleneck
  * indexes).  Reference: encode_with_indexes_warp_v2_cuda,
  * src/fast_compressai/coders/cuda/warp_ans_kernel_v2.cu:183-273. */
@@ -159,7 +161,8 @@ int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace
 
 /* Decode a payload into int32 symbols [B, N].  The last block writes the
  * OR of all GAANS_ST_* bits (0 when the payload decoded cleanly) to
- * *status_out (device or pinned host memory).
+ * status_out[0] (device or pinned host memory), then sets the completion
+ * word status_out[1] to 1 (status_out holds 2 u32).
  * Reference: decode_with_indexes_warp_cuda, warp_ans_kernel.cu:477-544. */
 int gaans_decode_symbols(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
                          const int32_t* indexes_dev, const gaans_tables* tables,
@@ -172,6 +175,18 @@ int gaans_decode_latents(void* stream, const uint8_t* payload_dev, int64_t paylo
                          const int32_t* indexes_dev, const gaans_tables* tables,
                          const float* medians_dev, int64_t B, int64_t N, int64_t C,
                          int64_t P, float* y_hat_dev, void* ctrl_dev, uint32_t* status_out);
+
+/* ---- completion ------------------------------------------------------------ */
+
+/* Wait on the host for a launch's completion word (encode: low half of
+ * info_out[2]; decode: status_out[1]) in pinned host memory that the caller
+ * set to 0 before the launch.  Returns GAANS_OK once the word is nonzero:
+ * the info/status words are then valid, while later work on the stream (the
+ * pack kernel) may still run, ordered on `stream` as usual.  Returns
+ * GAANS_EHIP when the stream reports an error or drains without setting the
+ * word.  Replaces the stream synchronisations of the reference's host code
+ * (warp_ans_kernel_v2.cu:275-276, warp_div.py:63-65). */
+int gaans_wait_host_word(void* stream, const uint32_t* word);
 
 /* ---- host self test ------------------------------------------------------- */
 

@@ -141,6 +141,31 @@ def test_coder_512x768_p4_bit_exact(backend, gpu_device):
     check_workload(backend, gpu_device, synthetic.coder_512x768())
 
 
+def test_side_stream_calls_without_device_sync(backend, gpu_device):
+    # encode returns once the coding kernel's completion word is set, while
+    # its pack kernel may still run: work ordered on the same stream (the
+    # host copy, the decode) must see the finished payload
+    w = synthetic.coder_512x768()
+    say("case: side stream, back-to-back calls", w.name)
+    ref = O.gaans_encode(w.symbols, w.indexes, w.cdfs, w.cdf_sizes, w.offsets, w.p_ch)
+    side = torch.cuda.Stream(gpu_device)
+    with torch.cuda.stream(side):
+        sym = dev(w.symbols, gpu_device)
+        idx = dev(w.explicit_indexes(), gpu_device)
+        cdfs, sizes, offs = tables_on(w, gpu_device)
+        for rep in range(4):
+            payload = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=w.p_ch)
+            assert payload.to_bytes() == ref, rep
+            out = backend.decode(payload, idx, cdfs, sizes, offs)
+            assert torch.equal(out, sym), rep
+            sym_next = torch.flip(sym, dims=[1]).contiguous()
+            payload2 = backend.encode(sym_next, idx.flip(1).contiguous(), cdfs, sizes, offs,
+                                      p_ch=1)
+            out2 = backend.decode(payload2, idx.flip(1).contiguous(), cdfs, sizes, offs)
+            assert torch.equal(out2, sym_next), rep
+    side.synchronize()
+
+
 @pytest.mark.parametrize("p_ch", [1, 16, 192])
 def test_coder_512x768_other_p(backend, gpu_device, p_ch):
     check_workload(backend, gpu_device, synthetic.coder_512x768(p_ch=p_ch))
