@@ -56,16 +56,15 @@ constexpr int kMappers = GAANS_MAPPERS;  // mapper waves per workgroup
 constexpr int kWaves = kMappers + 1;     // + the coder wave
 constexpr int kThreads = kWaves * kLanes;
 constexpr uint32_t kStateLow = 1u << 16;  // rANS L
-constexpr uint32_t kBitsEmit = 1u << 28;  // renorm bound of a 4-bit bypass op
 constexpr uint32_t kMagic = 0x31574147u;  // "GAW1"
-constexpr uint32_t kVersion = 1u;
+constexpr uint32_t kVersion = 2u;
 constexpr uint32_t kParams = 0x00041040u;  // lanes 64 | precision 16 << 8 | bypass 4 << 16
 constexpr int kFixedWords = 16;
 constexpr uint32_t kTabMagic = 0x32425447u;  // "GTB2"
 constexpr int kLutBits = 8;
 constexpr int kLutSize = 1 << kLutBits;
 constexpr uint32_t kHashMul = 0x9E3779B9u;
-constexpr int kMaxOpsPerSymbol = 10;  // main + count + 8 nibbles
+constexpr int kMaxEscNibbles = 9;  // escape count + 8 nibbles of raw
 
 // steps per block: the mappers' lead over the coder, and the steps between
 // two barriers
@@ -79,7 +78,8 @@ constexpr int kEncSB = GAANS_ENC_SB;
 constexpr int kDecSB = GAANS_DEC_SB;
 constexpr int kEncPer = (kEncSB + kMappers - 1) / kMappers;  // steps per mapper wave and block
 constexpr int kDecPer = (kDecSB + kMappers - 1) / kMappers;
-constexpr int kPartBytes = (8 * kWaves + 15) / 16 * 16;  // per-wave hash + status
+// per-wave hash, status and escape nibbles, then the escape count
+constexpr int kPartBytes = (12 * kWaves + 4 + 15) / 16 * 16;
 constexpr int kRingWords = 4096;       // encoder LDS output ring (u16 words)
 constexpr int kStreamRing = 2048;      // decoder LDS stream ring (u16 words)
 constexpr int kPfU32 = 4;              // decoder stream prefetch: u32 per lane
@@ -193,7 +193,7 @@ __host__ __device__ inline uint32_t enc_div(uint32_t x, uint32_t m, uint32_t sh)
 
 struct Layout {
   int64_t B, N, C, P, HW, K, chunk_len, BK, header_bytes, max_payload, cap_words, ws_bytes;
-  int64_t o_words_cnt, o_status, o_hash, o_end, o_info, o_states, o_words;
+  int64_t o_words_cnt, o_status, o_hash, o_end, o_info, o_states, o_words, o_esc, o_esc_raw;
 };
 
 int make_layout(int64_t B, int64_t N, int64_t C, int64_t P, Layout* L) {
@@ -212,11 +212,13 @@ int make_layout(int64_t B, int64_t N, int64_t C, int64_t P, Layout* L) {
   L->chunk_len = P * L->HW;
   L->BK = B * L->K;
   if (L->BK >= ((int64_t)1 << 31)) return fail(GAANS_EINVAL, "too many chunks");
-  if ((int64_t)kMaxOpsPerSymbol * L->chunk_len + 2 >= ((int64_t)1 << 31))
+  if ((int64_t)kMaxEscNibbles * L->chunk_len + 8 >= ((int64_t)1 << 31))
     return fail(GAANS_EINVAL, "chunk of %lld symbols is too large", (long long)L->chunk_len);
   L->header_bytes = align_up(4 * kFixedWords + 8 * L->BK, 16);
-  L->max_payload = L->header_bytes + B * N * 2 * kMaxOpsPerSymbol + L->BK * (4 * kLanes + 4);
-  L->cap_words = align_up((int64_t)kMaxOpsPerSymbol * L->chunk_len + 2, 2);
+  // per symbol at most one stream word and 9 escape nibbles; per chunk the
+  // states, a pad word and a partly used escape word
+  L->max_payload = L->header_bytes + B * N * 7 + L->BK * (4 * kLanes + 8);
+  L->cap_words = align_up(L->chunk_len + 2, 2);
   int64_t o = 0;
   L->o_words_cnt = o; o = align_up(o + 4 * L->BK, 256);
   L->o_status = o;    o = align_up(o + 4 * L->BK, 256);
@@ -225,6 +227,8 @@ int make_layout(int64_t B, int64_t N, int64_t C, int64_t P, Layout* L) {
   L->o_info = o;      o = align_up(o + 32, 256);
   L->o_states = o;    o = align_up(o + 4 * kLanes * L->BK, 256);
   L->o_words = o;     o = align_up(o + 2 * L->cap_words * L->BK, 256);
+  L->o_esc = o;       o = align_up(o + 8 * L->BK, 256);
+  L->o_esc_raw = o;   o = align_up(o + 4 * L->chunk_len * L->BK, 256);
   L->ws_bytes = o;
   return GAANS_OK;
 }
@@ -243,14 +247,6 @@ __device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
 
 __device__ __forceinline__ uint32_t wave_or(uint32_t v) {
   for (int off = 32; off > 0; off >>= 1) v |= (uint32_t)__shfl_xor((int)v, off, 64);
-  return v;
-}
-
-__device__ __forceinline__ uint32_t wave_max(uint32_t v) {
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
-    v = o > v ? o : v;
-  }
   return v;
 }
 
@@ -384,6 +380,8 @@ struct EncArgs {
   uint64_t* __restrict__ ws_info;
   uint32_t* __restrict__ states;
   uint16_t* __restrict__ words;
+  uint2* __restrict__ esc;          // per chunk: escape count, escape nibbles
+  uint32_t* __restrict__ esc_raw;   // per chunk: chunk_len slots, filled from the end
   uint32_t* __restrict__ ctrl;
   uint64_t* __restrict__ info_out;
 };
@@ -391,7 +389,7 @@ struct EncArgs {
 // Encoder LDS layout (bytes)
 constexpr int kEncRingBytes = 2 * (kRingWords + kLanes);  // + one spare slot per lane
 constexpr int kEncRecBytes = 2 * kEncSB * kLanes * 16;        // two blocks of op records
-constexpr int kEncInfoBytes = 2 * kEncSB * 4;                 // per-step escape op count
+constexpr int kEncInfoBytes = 2 * kEncSB * 4;                 // per-step escape flag
 constexpr int kEncFixedLds = kEncRingBytes + kEncRecBytes + kEncInfoBytes + kPartBytes;
 
 // last workgroup of an encode launch (wave 0): chunk offsets + payload size +
@@ -407,7 +405,10 @@ __device__ void encode_finish(const EncArgs& a, int lane) {
       const uint32_t A = len < kLanes ? (uint32_t)len : (uint32_t)kLanes;
       const uint32_t W = __hip_atomic_load(&a.chunk_words[g], __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT);
-      v = 4ull * A + 2ull * (W + (W & 1u));
+      const uint32_t Z = __hip_atomic_load(&a.esc[g].y, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+      const uint64_t U = (uint64_t)W + (Z + 3u) / 4u;  // stream + escape words
+      v = 4ull * A + 2ull * (U + (U & 1u));
       st |= __hip_atomic_load(&a.chunk_status[g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     const uint64_t incl = wave_incl_scan(v, lane) + carry;
@@ -437,19 +438,20 @@ __device__ void encode_finish(const EncArgs& a, int lane) {
 // Op record of one lane and step (16 bytes):
 //   x: start | (65536 - freq) << 16      (identity op: 0)
 //   y: division magic of freq            (enc_div)
-//   z: shift | (freq == 1) << 5 | nops << 8   (nops: ops in decode order)
+//   z: shift | (freq == 1) << 5 | escape << 8
 //   w: escape raw value
 // CompressAI's escape split (reference warp_ans_kernel_v2.cu:139-164):
 // v = sym - offset; v < 0 -> raw = -2v - 1, v >= maxv -> raw = 2 (v - maxv),
-// both coded as the escape bin maxv, then n = raw ? msb(raw) / 4 + 1 : 0
-// nibbles.  v is computed in 32-bit arithmetic; when sym - offset overflows
-// int32 the sign of sym tells the side and raw = 2 (v - maxv) (wrapped) is
-// exact whenever raw < 2^32, else the symbol is uncodable.
+// both coded as the escape bin maxv; raw goes to the escape section as
+// n = raw ? msb(raw) / 4 + 1 : 0 nibbles after the count (1 + n nibbles,
+// added to znib).  v is computed in 32-bit arithmetic; when sym - offset
+// overflows int32 the sign of sym tells the side and raw = 2 (v - maxv)
+// (wrapped) is exact whenever raw < 2^32, else the symbol is uncodable.
 template <bool kLatents, bool kImplicit>
 __device__ __forceinline__ uint4 enc_record(const EncArgs& a, const Tabs& tb, bool lds, int lane,
                                             int t, int len, int32_t start, int32_t in_a,
                                             int32_t in_b, float in_m, uint32_t& hash,
-                                            uint32_t& status) {
+                                            uint32_t& status, uint32_t& znib) {
   const int p = lane + kLanes * t;
   const bool act = p < len;
   int32_t tbi = kImplicit ? (int32_t)udiv((uint32_t)(start + p), a.div_hw) : in_b;
@@ -493,13 +495,13 @@ __device__ __forceinline__ uint4 enc_record(const EncArgs& a, const Tabs& tb, bo
   status |= (ok & ovf & (lo | (d >= 0x80000000u))) ? GAANS_ST_RANGE : 0u;
   const uint32_t raw = esc ? (lo ? ~((uint32_t)v << 1) : (d << 1)) : 0u;
   const uint32_t nn = raw ? ((31u - (uint32_t)__clz((int)raw)) >> 2) + 1u : 0u;
-  const uint32_t nops = esc ? nn + 2u : 1u;
+  znib += esc ? nn + 1u : 0u;
   const uint32_t fr = (e.x >> 16) + 1u;
   const uint32_t sh = fr >= 2u ? enc_shift(fr) : 0u;
   uint4 r;
   r.x = ok ? ((e.x & 0xffffu) | ((65536u - fr) << 16)) : 0u;
   r.y = ok ? e.y : 1u;
-  r.z = (ok ? sh : 15u) | ((ok & (fr == 1u)) ? 32u : 0u) | (nops << 8);
+  r.z = (ok ? sh : 15u) | ((ok & (fr == 1u)) ? 32u : 0u) | (esc ? 256u : 0u);
   r.w = raw;
   return r;
 }
@@ -513,18 +515,11 @@ __device__ __forceinline__ void ring_flush(uint16_t* __restrict__ wbuf, const ui
 
 // The ring holds the words [wp, fl) (positions mod kRingWords).  The coder
 // flushes it at the start of a block when fewer than kEncSB * kLanes slots are
-// free, so the ordinary steps of a block need no check; a step with escapes
-// first makes room for its own words and the rest of its block.
-template <bool kCheck>
-__device__ __forceinline__ void emit_words(bool emit, uint32_t& x, uint16_t* ring,
-                                           uint16_t* __restrict__ wbuf, int& wp, int& fl,
+// free (a step emits at most one word per lane), so the steps need no check.
+__device__ __forceinline__ void emit_words(bool emit, uint32_t& x, uint16_t* ring, int& wp,
                                            int lane) {
   const uint64_t m = ballot(emit);
   const int c = __popcll(m);
-  if (kCheck && fl - wp + c > kRingWords - kEncSB * kLanes) {
-    ring_flush(wbuf, ring, wp, fl, lane);
-    fl = uni(wp);
-  }
   wp = uni(wp - c);
   const uint32_t slot =
       emit ? ((uint32_t)(wp + (int)lane_rank(m)) & (kRingWords - 1)) : (uint32_t)(kRingWords + lane);
@@ -539,59 +534,16 @@ __device__ __forceinline__ uint32_t enc_apply(uint32_t x, uint4 r) {
   return (r.z & 32u) ? ((x << 16) + (r.x & 0xffffu)) : xn;
 }
 
-// Step with escapes: each lane codes nops ops in decode order d = 0 (main),
-// 1 (count), 2.. (nibbles), an ordinary lane only d = 0; encoding runs from
-// the last op to the first, and the words of one op index are ordered by
-// lane.  M is the largest nops of the step.  Kept out of line (rare, and the
-// unrolled steps stay small); the coder state goes in and out by value.
-struct EncCur {
-  uint32_t x;
-  int wp, fl;
-};
-
-__device__ __forceinline__ EncCur enc_escape_step(const uint4 e, uint32_t M, EncCur c,
-                                               uint16_t* ring, uint16_t* __restrict__ wbuf,
-                                               int lane) {
-  uint32_t x = c.x;
-  int wp = c.wp, fl = c.fl;
-  // room for the whole step and the rest of the block
-  if (fl - wp > kRingWords - (int)(M + kEncSB) * kLanes) {
-    ring_flush(wbuf, ring, wp, fl, lane);
-    fl = wp;
-  }
-  const uint32_t nops = e.z >> 8;
-  const bool escl = nops > 1u;
-  const uint64_t em = ballot(escl);
-  if (__popcll(em) == 1) {
-    // one escaping lane: each op index has at most its word, so its ops run
-    // on the scalar unit and lane 0 prepends the words
-    const int L = __ffsll((unsigned long long)em) - 1;
-    uint32_t xs = __builtin_amdgcn_readlane(x, L);
-    const uint32_t ns = __builtin_amdgcn_readlane(nops, L);
-    const uint32_t raws = __builtin_amdgcn_readlane(e.w, L);
-    int k = 0;
-    for (int d = (int)ns - 1; d >= 1; --d) {
-      const uint32_t val = d == 1 ? ns - 2u : (raws >> ((4 * (d - 2)) & 31)) & 15u;
-      if (xs >= kBitsEmit) {
-        if (lane == 0) ring[(uint32_t)(wp - 1 - k) & (kRingWords - 1)] = (uint16_t)xs;
-        xs >>= 16;
-        ++k;
-      }
-      xs = (xs << 4) | val;
-    }
-    x = lane == L ? xs : x;
-    wp -= k;
-  } else {
-    for (int d = (int)M - 1; d >= 1; --d) {
-      const bool part_d = (uint32_t)d < nops;
-      const uint32_t val = d == 1 ? nops - 2u : (e.w >> ((4 * (d - 2)) & 31)) & 15u;
-      const uint32_t x0 = x;
-      emit_words<false>(part_d & (x >= kBitsEmit), x, ring, wbuf, wp, fl, lane);
-      x = part_d ? ((x << 4) | val) : x0;
-    }
-  }
-  emit_words<false>((x >> 16) >= 65536u - (e.x >> 16), x, ring, wbuf, wp, fl, lane);
-  return EncCur{enc_apply(x, e), wp, fl};
+// Escapes of one step into the chunk's escape list: slots are taken from the
+// end of the list, highest lane first, so that the list, read forwards, is in
+// position order (the coder walks the steps last to first).
+__device__ __forceinline__ void enc_escapes(const uint4 r, uint32_t* __restrict__ list,
+                                            int& cnt, int lane) {
+  const bool esc = (r.z & 256u) != 0u;
+  const uint64_t em = ballot(esc);
+  const int above = __popcll(lane < 63 ? em >> (lane + 1) : 0ull);
+  if (esc) list[-1 - (cnt + above)] = r.w;
+  cnt = uni(cnt + __popcll(em));
 }
 
 template <bool kLatents, bool kImplicit>
@@ -619,7 +571,9 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
   int wp = a.cap_words;  // coder: wave-uniform write cursor (backwards)
   int fl = a.cap_words;  // coder: words at [fl, cap) are already in wbuf
   uint32_t x = kStateLow;
-  uint32_t hash = 0, status = 0;
+  uint32_t hash = 0, status = 0, znib = 0;
+  int n_esc = 0;  // coder: escapes listed so far
+  uint32_t* __restrict__ esc_list = a.esc_raw + g * a.chunk_len + a.chunk_len;
 
   const bool tab = tables_ok(a.tables, a.M, a.tables_bytes);  // uniform
   if (!tab) status |= GAANS_ST_TABLES;
@@ -663,23 +617,16 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
     auto map_steps = [&](int j, auto lds_tag) {
       constexpr bool kLds = decltype(lds_tag)::value;
       uint4* dst = recs + (j & 1) * kEncSB * kLanes;
-      uint32_t nops[kEncPer];
 #pragma unroll
       for (int e = 0; e < kEncPer; ++e) {
         const int u = (wid - 1) + kMappers * e;
         if (kEncSB % kMappers != 0 && u >= kEncSB) break;
         const uint4 r = enc_record<kLatents, kImplicit>(a, tb, kLds, lane, j * kEncSB + u, len,
-                                                        start, ca[e], cb[e], cm[e], hash, status);
+                                                        start, ca[e], cb[e], cm[e], hash, status,
+                                                        znib);
         dst[u * kLanes + lane] = r;
-        nops[e] = r.z >> 8;
-      }
-#pragma unroll
-      for (int e = 0; e < kEncPer; ++e) {
-        const int u = (wid - 1) + kMappers * e;
-        if (kEncSB % kMappers != 0 && u >= kEncSB) break;
-        uint32_t mt = 0;
-        if (ballot(nops[e] > 1u)) mt = wave_max(nops[e]);  // escapes are rare
-        if (lane == 0) info[(j & 1) * kEncSB + u] = mt;
+        const uint32_t esc_step = ballot((r.z & 256u) != 0u) != 0ull;
+        if (lane == 0) info[(j & 1) * kEncSB + u] = esc_step;
       }
     };
     auto map_block = [&](int j) {
@@ -713,37 +660,32 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
         }
         const uint4* src = recs + (j & 1) * kEncSB * kLanes;
         uint4 r[kEncSB];
-        uint32_t mt[kEncSB];
+        uint32_t any_esc = 0;
 #pragma unroll
         for (int u = 0; u < kEncSB; ++u) {
           r[u] = src[u * kLanes + lane];
-          mt[u] = (uint32_t)uni((int)info[(j & 1) * kEncSB + u]);
+          any_esc |= (uint32_t)uni((int)info[(j & 1) * kEncSB + u]) << u;
         }
-        uint32_t any_esc = 0;
-#pragma unroll
-        for (int u = 0; u < kEncSB; ++u) any_esc |= mt[u];
-        if ((j + 1) * kEncSB <= T && any_esc == 0) {
-          // common case: a full block without escapes, no per-step branches
+        if ((j + 1) * kEncSB <= T) {
+          // common case: a full block, no per-step branches
 #pragma unroll
           for (int u = kEncSB - 1; u >= 0; --u) {
-            emit_words<false>((x >> 16) >= 65536u - (r[u].x >> 16), x, ring, wbuf, wp, fl, lane);
+            emit_words((x >> 16) >= 65536u - (r[u].x >> 16), x, ring, wp, lane);
             x = enc_apply(x, r[u]);
           }
         } else {
-          // last block or escapes: per-step branches
 #pragma unroll
           for (int u = kEncSB - 1; u >= 0; --u) {
-            if (__builtin_expect(j * kEncSB + u >= T, 0)) continue;
-            if (__builtin_expect(mt[u] == 0, 1)) {
-              emit_words<false>((x >> 16) >= 65536u - (r[u].x >> 16), x, ring, wbuf, wp, fl, lane);
-              x = enc_apply(x, r[u]);
-            } else {
-              const EncCur c = enc_escape_step(r[u], mt[u], EncCur{x, wp, fl}, ring, wbuf, lane);
-              x = c.x;
-              wp = uni(c.wp);
-              fl = uni(c.fl);
-            }
+            if (j * kEncSB + u >= T) continue;
+            emit_words((x >> 16) >= 65536u - (r[u].x >> 16), x, ring, wp, lane);
+            x = enc_apply(x, r[u]);
           }
+        }
+        // escapes of the block (their bins are coded above): list them
+        if (__builtin_expect(any_esc != 0, 0)) {
+#pragma unroll
+          for (int u = kEncSB - 1; u >= 0; --u)
+            if (any_esc & (1u << u)) enc_escapes(r[u], esc_list, n_esc, lane);
         }
         __syncthreads();
       }
@@ -774,20 +716,25 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
   if (wid == 0 && lane < A) a.states[g * kLanes + lane] = x;
   hash = wave_sum(hash);
   status = wave_or(status);
+  znib = wave_sum(znib);
   if (lane == 0) {
     part[wid] = hash;
     part[kWaves + wid] = status;
+    part[2 * kWaves + wid] = znib;
+    if (wid == 0) part[3 * kWaves] = (uint32_t)n_esc;
   }
   __syncthreads();
   if (tid == 0) {
-    uint32_t hs = 0, ss = 0;
+    uint32_t hs = 0, ss = 0, zs = 0;
     for (int w = 0; w < kWaves; ++w) {
       hs += part[w];
       ss |= part[kWaves + w];
+      zs += part[2 * kWaves + w];
     }
     a.chunk_words[g] = (uint32_t)(a.cap_words - wp);
     a.chunk_status[g] = ss;
     a.index_hash[g] = hs;
+    a.esc[g] = make_uint2(part[3 * kWaves], zs);
   }
   __threadfence();
   __syncthreads();
@@ -814,6 +761,8 @@ struct PackArgs {
   const uint32_t* __restrict__ end_off;
   const uint32_t* __restrict__ states;
   const uint16_t* __restrict__ words;
+  const uint2* __restrict__ esc;
+  const uint32_t* __restrict__ esc_raw;
   const uint8_t* __restrict__ tables;
   uint8_t* __restrict__ out;
   int64_t out_bytes, header_bytes, cap_words, BK, N;
@@ -857,16 +806,62 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
   const int len = chunk_len_of(g, (int32_t)a.K, (int32_t)a.chunk_len, a.N);
   const int A = len < kLanes ? len : kLanes;
   const int64_t W = a.chunk_words[g];
+  const uint2 ez = a.esc[g];  // escape count, escape nibbles
+  int64_t U = W + (ez.y + 3u) / 4u;
+  U += U & 1;  // u16 words after the states: stream, pad, escape words
   uint8_t* dst = a.out + a.header_bytes + beg;
   uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
   for (int j = tid; j < A; j += 256) d32[j] = a.states[g * kLanes + j];
   const uint16_t* src = a.words + g * a.cap_words + (a.cap_words - W);
   uint32_t* w32 = reinterpret_cast<uint32_t*>(dst + 4 * A);
-  const int64_t n32 = (W + 1) / 2;
+  const int64_t n32 = U / 2;
   for (int64_t j = tid; j < n32; j += 256) {
-    const uint32_t lo = src[2 * j];
+    const uint32_t lo = (2 * j < W) ? src[2 * j] : 0u;
     const uint32_t hi = (2 * j + 1 < W) ? src[2 * j + 1] : 0u;
     w32[j] = lo | (hi << 16);
+  }
+  if (ez.x == 0) return;
+  // Escape section: entry i (position order) is the count n then the n
+  // nibbles of raw, at nibble offset o_i = sum of (1 + n) over the entries
+  // before it.  Escape word j is the u16 at U - 1 - j, so the nibbles
+  // [8m, 8m + 8) (escape words 2m, 2m + 1) form the u32 at U / 2 - 1 - m with
+  // its halves swapped.  Entries share words: they are OR-ed into the zeros
+  // written above.
+  __shared__ uint32_t wtot[4];
+  __syncthreads();
+  const int wv = tid >> 6, lane = tid & 63;
+  const uint32_t E = ez.x;
+  const uint32_t* __restrict__ lst = a.esc_raw + g * (int64_t)a.chunk_len + (a.chunk_len - E);
+  uint32_t carry = 0;
+  for (uint32_t i0 = 0; i0 < E; i0 += 256) {
+    const uint32_t i = i0 + tid;
+    const uint32_t raw = i < E ? lst[i] : 0u;
+    const uint32_t n = raw ? ((31u - (uint32_t)__clz((int)raw)) >> 2) + 1u : 0u;
+    const uint32_t c = i < E ? n + 1u : 0u;
+    uint32_t incl = c;
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t o = (uint32_t)__shfl_up((int)incl, off, 64);
+      if (lane >= off) incl += o;
+    }
+    if (lane == 63) wtot[wv] = incl;
+    __syncthreads();
+    uint32_t before = 0, total = 0;
+    for (int w = 0; w < 4; ++w) {
+      before += w < wv ? wtot[w] : 0u;
+      total += wtot[w];
+    }
+    __syncthreads();
+    const uint32_t o = carry + before + incl - c;
+    carry += total;
+    const uint64_t v = ((uint64_t)n | ((uint64_t)raw << 4)) << (4 * (o & 7u));
+    const int64_t m = o >> 3;
+    const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+    if (lo && m < n32)
+      __hip_atomic_fetch_or(&w32[n32 - 1 - m], (lo >> 16) | (lo << 16), __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    if (hi && m + 1 < n32)
+      __hip_atomic_fetch_or(&w32[n32 - 2 - m], (hi >> 16) | (hi << 16), __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -968,18 +963,14 @@ __device__ __forceinline__ void dec_lookup(const Tabs& tb, const uint4 r, uint32
 }
 
 // Word stream of one chunk: prefetched from HBM into registers (kPfWords words
-// ahead) and copied into an LDS ring that refills read from.
-// The word stream of a chunk is copied into an LDS ring holding the words
-// [rp, filled) (positions mod kStreamRing), kPfWords words at a time.
-//  - At the start of every block the coder commits the batch prefetched into
-//    registers (pf, words [filled, filled + kPfWords)) when fewer than
-//    kLowWater words are buffered, then prefetches the next batch.  This is the
-//    only place pf is loaded, so the loads stay in flight between blocks.
-//  - The main-op refills of a block (at most one word per lane and step) need
-//    no check: a block starts with at least kDecSB * kLanes buffered words.
-//  - Escape refills check that margin and, when a block has consumed that
-//    much, copy the next batch synchronously (its own loads; pf is marked stale
-//    and refetched at the next block start).
+// ahead) and copied into an LDS ring holding the words [rp, filled)
+// (positions mod kStreamRing), kPfWords words at a time.  At the start of
+// every block the coder commits the batch prefetched into registers (pf,
+// words [filled, filled + kPfWords)) when fewer than kLowWater words are
+// buffered, then prefetches the next batch.  This is the only place pf is
+// loaded, so the loads stay in flight between blocks.  A step refills at most
+// one word per lane, and a block starts with at least kDecSB * kLanes
+// buffered words, so refills need no check.
 constexpr int kLowWater = 1024;
 static_assert(kLowWater >= kDecSB * kLanes && kLowWater + kPfWords <= kStreamRing,
               "decoder stream ring too small");
@@ -987,7 +978,6 @@ struct Stream {
   const uint32_t* __restrict__ s32;
   const uint32_t* __restrict__ safe;  // an in-bounds word of the chunk
   int q, q32, rp, filled;
-  bool pf_live;  // pf holds words [filled, filled + kPfWords)
   uint32_t pf[kPfU32];
 };
 
@@ -998,43 +988,24 @@ __device__ __forceinline__ uint32_t stream_word32(const Stream& S, int i32) {
   return *(i32 < S.q32 ? S.s32 + i32 : S.safe);
 }
 
-// Block start: commit pf if needed, then (re)fetch pf.
+// Block start: commit pf if needed, then fetch the next batch.
 __device__ __forceinline__ void stream_block_start(Stream& S, uint32_t* ring32, int lane) {
-  const bool commit = S.pf_live && S.filled - S.rp < kLowWater && S.filled < S.q;
+  const bool commit = S.filled - S.rp < kLowWater && S.filled < S.q;
   if (commit) {
 #pragma unroll
     for (int kk = 0; kk < kPfU32; ++kk)
       ring32[((S.filled >> 1) + kk * kLanes + lane) & (kStreamRing / 2 - 1)] = S.pf[kk];
     S.filled = uni(S.filled + kPfWords);
-  }
-  if (commit || !S.pf_live) {
 #pragma unroll
     for (int kk = 0; kk < kPfU32; ++kk)
       S.pf[kk] = stream_word32(S, (S.filled >> 1) + kk * kLanes + lane);
-    S.pf_live = true;
   }
-}
-
-// Escape refill with fewer than kDecSB * kLanes buffered words: copy the next
-// batch now.
-__device__ __forceinline__ void stream_sync_batch(Stream& S, uint32_t* ring32, int lane) {
-  uint32_t w[kPfU32];
-#pragma unroll
-  for (int kk = 0; kk < kPfU32; ++kk) w[kk] = stream_word32(S, (S.filled >> 1) + kk * kLanes + lane);
-#pragma unroll
-  for (int kk = 0; kk < kPfU32; ++kk)
-    ring32[((S.filled >> 1) + kk * kLanes + lane) & (kStreamRing / 2 - 1)] = w[kk];
-  S.filled = uni(S.filled + kPfWords);
-  S.pf_live = false;
 }
 
 // A refill past the stream end reads stale ring words; the chunk is then
 // marked corrupt by the final check that exactly the stream was consumed.
-template <bool kCheck>
-__device__ __forceinline__ void dec_refill(bool need, uint32_t& x, Stream& S,
-                                           const uint16_t* ring, uint32_t* ring32, int lane) {
-  if (kCheck && S.filled - S.rp < kDecSB * kLanes && S.filled < S.q)
-    stream_sync_batch(S, ring32, lane);
+__device__ __forceinline__ void dec_refill(bool need, uint32_t& x, Stream& S, const uint16_t* ring,
+                                           int lane) {
   const uint64_t m = ballot(need);
   // every lane reads (no branch around the read); only refilling lanes keep it
   const uint32_t w = ring[(S.rp + (int)lane_rank(m)) & (kStreamRing - 1)];
@@ -1043,11 +1014,55 @@ __device__ __forceinline__ void dec_refill(bool need, uint32_t& x, Stream& S,
   S.rp += __popcll(m);
 }
 
+// Escape section of one chunk, read from the chunk's end: escape u32 m holds
+// the nibbles [8m, 8m + 8), nibble 8m + r at bits 4r; it is the stream's u32
+// n32 - 1 - m with its halves swapped.  The coder keeps escape u32s
+// [wb, wb + 128) in two registers across the wave and reads the entries in
+// order with the nibble cursor q (both wave-uniform).
+struct Esc {
+  const uint32_t* __restrict__ w32;   // the chunk's words after the states
+  const uint32_t* __restrict__ safe;  // an in-bounds word of the chunk
+  int n32, wb;
+  uint32_t q;
+  uint32_t win0, win1;  // escape u32 wb + lane, wb + 64 + lane
+};
+
+// Escape u32 m; past the start of the chunk's words it reads as zero
+// (corrupt payloads only).
+__device__ __forceinline__ uint32_t esc_u32(const Esc& E, int m) {
+  const bool in = m < E.n32;
+  const uint32_t v = *(in ? E.w32 + (E.n32 - 1 - m) : E.safe);
+  return in ? ((v >> 16) | (v << 16)) : 0u;
+}
+
+// Next entry of the escape section: its raw value (count n <= 8, else the
+// chunk is corrupt).  Wave-uniform.
+__device__ __forceinline__ uint32_t esc_next(Esc& E, uint32_t& status, int lane) {
+  int i = uni((int)(E.q >> 3) - E.wb);  // 0 .. 65: an entry spans at most 2 u32s
+  if (i >= kLanes) {
+    E.win0 = E.win1;
+    E.wb = uni(E.wb + kLanes);
+    i -= kLanes;
+    E.win1 = esc_u32(E, E.wb + kLanes + lane);
+  }
+  const uint32_t a0 = __builtin_amdgcn_readlane(E.win0, i);
+  const uint32_t a1 = i + 1 < kLanes ? __builtin_amdgcn_readlane(E.win0, i + 1)
+                                     : __builtin_amdgcn_readlane(E.win1, 0);
+  const uint64_t v = ((((uint64_t)a1) << 32) | a0) >> (4u * (E.q & 7u));
+  uint32_t n = (uint32_t)v & 15u;
+  if (n > 8u) {
+    status |= GAANS_ST_CORRUPT;
+    n = 0;
+  }
+  E.q = (uint32_t)uni((int)(E.q + 1u + n));
+  return (uint32_t)((v >> 4) & ((1ull << (4u * n)) - 1ull));
+}
+
 // One decode step of the coder wave; returns the decoded value.  kFull: every
 // lane is active and no offset can overflow with a symbol index.
 template <bool kLds, bool kFull>
 __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint4 r, uint32_t& x,
-                                             Stream& S, const uint16_t* ring, uint32_t* ring32,
+                                             Stream& S, const uint16_t* ring, Esc& E,
                                              uint32_t& status, int lane) {
   const bool act = kFull || r.y != 0xffffffffu;
   const uint32_t cum = x & 0xffffu;
@@ -1055,75 +1070,27 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint4 r, uint
   dec_lookup<kLds>(tb, r, cum, act, s, st, fr);
   const uint32_t xn = __umul24(fr, x >> 16) + cum - st;
   x = act ? xn : x;
-  dec_refill<false>(act & (x < kStateLow), x, S, ring, ring32, lane);
-  const bool esc = s == r.y;
+  dec_refill(act & (x < kStateLow), x, S, ring, lane);
   // value + offset for an ordinary symbol: s < 2^16, so the int32 sum overflows
   // exactly when it wraps below the offset
   int32_t o = (int32_t)(s + r.z);
   bool oob = !kFull && o < (int32_t)r.z;
-  const uint64_t em = ballot(esc);
+  const bool esc = act & (s == r.y);
+  uint64_t em = ballot(esc);
   if (__builtin_expect(em != 0, 0)) {
-   if (__popcll(em) == 1) {
-    // one escaping lane: its refill words are consecutive in the stream; the
-    // lane takes them from 5 or 6 words read at once (the margin covers the
-    // at most 9 words and the rest of the block)
-    if (S.filled - S.rp < kDecSB * kLanes && S.filled < S.q) stream_sync_batch(S, ring32, lane);
-    const int rp = S.rp;
-    const int e0 = rp & ~1;  // even word at or below rp
-    const uint32_t d0 = ring32[(e0 >> 1) & (kStreamRing / 2 - 1)];
-    const uint32_t d1 = ring32[((e0 >> 1) + 1) & (kStreamRing / 2 - 1)];
-    const uint32_t d2 = ring32[((e0 >> 1) + 2) & (kStreamRing / 2 - 1)];
-    const uint64_t win = ((uint64_t)d1 << 32) | d0;
-    int k = rp - e0;  // next word, counted from e0
-    uint32_t raw1 = 0;
-    if (esc) {
-      auto take = [&]() -> uint32_t {
-        uint32_t w;
-        if (k < 4) w = (uint32_t)(win >> (16 * k)) & 0xffffu;
-        else if (k < 6) w = (d2 >> (16 * (k - 4))) & 0xffffu;
-        else w = ring[(e0 + k) & (kStreamRing - 1)];
-        ++k;
-        return w;
-      };
-      uint32_t n = x & 15u;
-      x >>= 4;
-      if (x < kStateLow) x = (x << 16) | take();
-      if (n > 8u) {
-        status |= GAANS_ST_CORRUPT;
-        n = 0;
-      }
-      for (uint32_t jj = 0; jj < n; ++jj) {
-        raw1 |= (x & 15u) << (4 * jj);
-        x >>= 4;
-        if (x < kStateLow) x = (x << 16) | take();
-      }
-    }
-    S.rp = e0 + __builtin_amdgcn_readlane(k, __ffsll((unsigned long long)em) - 1);
-    const uint32_t raw = raw1;
-    const int64_t ev = (raw & 1u) ? -(int64_t)(raw >> 1) - 1 : (int64_t)(raw >> 1) + r.y;
-    const int64_t sv = ev + (int32_t)r.z;
-    o = esc ? (int32_t)sv : o;
-    oob = esc ? ((sv < INT32_MIN) | (sv > INT32_MAX)) : oob;
-   } else {
-    uint32_t n = esc ? (x & 15u) : 0u;
-    x = esc ? (x >> 4) : x;
-    dec_refill<true>(esc & (x < kStateLow), x, S, ring, ring32, lane);
-    const bool badn = n > 8u;
-    status |= (esc & badn) ? GAANS_ST_CORRUPT : 0u;
-    n = badn ? 0u : n;
+    // escapes of the step take the next entries of the escape section in
+    // lane order
     uint32_t raw = 0;
-    for (uint32_t jj = 0; jj < 8u; ++jj) {
-      const bool part = esc & (jj < n);
-      if (ballot(part) == 0) break;
-      raw |= part ? ((x & 15u) << (4 * jj)) : 0u;
-      x = part ? (x >> 4) : x;
-      dec_refill<true>(part & (x < kStateLow), x, S, ring, ring32, lane);
-    }
+    do {
+      const int L = __ffsll((unsigned long long)em) - 1;
+      const uint32_t rv = esc_next(E, status, lane);
+      raw = lane == L ? rv : raw;
+      em &= em - 1ull;
+    } while (em);
     const int64_t ev = (raw & 1u) ? -(int64_t)(raw >> 1) - 1 : (int64_t)(raw >> 1) + r.y;
     const int64_t sv = ev + (int32_t)r.z;
     o = esc ? (int32_t)sv : o;
     oob = esc ? ((sv < INT32_MIN) | (sv > INT32_MAX)) : oob;
-   }
   }
   oob &= act;
   status |= oob ? GAANS_ST_CORRUPT : 0u;
@@ -1247,22 +1214,32 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
     // stream words, the mappers' first two blocks of inputs.
     constexpr int kPre = kLowWater / kPfWords;
     Stream S;
+    Esc E;
     uint32_t x = kStateLow;
     uint32_t w0[kPre][kPfU32];
     if (wid == 0) {
       S.s32 = reinterpret_cast<const uint32_t*>(cdata + 4 * A);
       S.safe = reinterpret_cast<const uint32_t*>(cdata);
-      S.q = (int)((cb - 4 * A) / 2);  // stream words incl. pad (even)
+      S.q = (int)((cb - 4 * A) / 2);  // u16 words after the states (even)
       S.q32 = S.q / 2;
       S.rp = 0;
       S.filled = 0;
-      S.pf_live = false;
       x = lane < A ? reinterpret_cast<const uint32_t*>(cdata)[lane] : kStateLow;
 #pragma unroll
       for (int b = 0; b < kPre; ++b)
 #pragma unroll
         for (int kk = 0; kk < kPfU32; ++kk)
           w0[b][kk] = stream_word32(S, b * (kPfWords / 2) + kk * kLanes + lane);
+#pragma unroll
+      for (int kk = 0; kk < kPfU32; ++kk)
+        S.pf[kk] = stream_word32(S, kPre * (kPfWords / 2) + kk * kLanes + lane);
+      E.w32 = S.s32;
+      E.safe = S.safe;
+      E.n32 = S.q32;
+      E.wb = 0;
+      E.q = 0;
+      E.win0 = esc_u32(E, lane);
+      E.win1 = esc_u32(E, kLanes + lane);
     } else if (nblk > 0) {
       load_block(0, cbx, cm);
       if (nblk > 1) load_block(1, nbx, nm);
@@ -1302,7 +1279,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
           // per-step branches
 #pragma unroll
           for (int u = 0; u < kDecSB; ++u)
-            ov[u] = dec_step<true, true>(tb, r[u], x, S, sring, sring32, status, lane);
+            ov[u] = dec_step<true, true>(tb, r[u], x, S, sring, E, status, lane);
           // decoded values replace the records' x words; the mappers store them
 #pragma unroll
           for (int u = 0; u < kDecSB; ++u)
@@ -1314,15 +1291,29 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
             const uint4 ru = src[u * kLanes + lane];
             const uint32_t v =
                 uni((int)info[(j & 1) * kDecSB + u])
-                    ? dec_step<true, false>(tb, ru, x, S, sring, sring32, status, lane)
-                    : dec_step<false, false>(tb, ru, x, S, sring, sring32, status, lane);
+                    ? dec_step<true, false>(tb, ru, x, S, sring, E, status, lane)
+                    : dec_step<false, false>(tb, ru, x, S, sring, E, status, lane);
             reinterpret_cast<uint32_t*>(src + u * kLanes + lane)[0] = v;
           }
         }
         __syncthreads();
       }
+      // every state back at 2^16; stream, pad and escape words consumed
+      // exactly; the pad word and the unused nibbles of the last escape word
+      // are zero
       if (lane < A && x != kStateLow) status |= GAANS_ST_CORRUPT;
-      if (!(S.rp == S.q || (S.rp == S.q - 1 && (S.q & 1) == 0))) status |= GAANS_ST_CORRUPT;
+      const int qe = (int)((E.q + 3u) >> 2);
+      const int pad = (S.rp + qe) & 1;
+      if (S.rp + qe + pad != S.q) {
+        status |= GAANS_ST_CORRUPT;
+      } else {
+        const uint16_t* s16 = reinterpret_cast<const uint16_t*>(S.s32);
+        if (pad && s16[S.rp] != 0) status |= GAANS_ST_CORRUPT;
+        if (E.q & 3u) {
+          const uint32_t last = esc_u32(E, (int)(E.q >> 3)) >> (4u * (E.q & 7u));
+          if (last & ((1u << (4u * (4u - (E.q & 3u)))) - 1u)) status |= GAANS_ST_CORRUPT;
+        }
+      }
     } else {
       if (nblk > 0) map_block(0);
       __syncthreads();
@@ -1527,6 +1518,8 @@ int encode_stage1(bool latents, void* stream, const int32_t* symbols, const floa
   a.ws_info = reinterpret_cast<uint64_t*>(w + L.o_info);
   a.states = reinterpret_cast<uint32_t*>(w + L.o_states);
   a.words = reinterpret_cast<uint16_t*>(w + L.o_words);
+  a.esc = reinterpret_cast<uint2*>(w + L.o_esc);
+  a.esc_raw = reinterpret_cast<uint32_t*>(w + L.o_esc_raw);
   a.ctrl = static_cast<uint32_t*>(ctrl);
   a.info_out = info_out;
   const size_t lds = kEncFixedLds + 16 * (size_t)st.nt_cap + 8 * (size_t)st.ne_cap;
@@ -1662,6 +1655,8 @@ int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, gaans_layout* o
   out->ws_info = L.o_info;
   out->ws_states = L.o_states;
   out->ws_words = L.o_words;
+  out->ws_esc = L.o_esc;
+  out->ws_esc_raw = L.o_esc_raw;
   return GAANS_OK;
 }
 
@@ -1830,6 +1825,8 @@ int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace
   a.end_off = reinterpret_cast<const uint32_t*>(w + L.o_end);
   a.states = reinterpret_cast<const uint32_t*>(w + L.o_states);
   a.words = reinterpret_cast<const uint16_t*>(w + L.o_words);
+  a.esc = reinterpret_cast<const uint2*>(w + L.o_esc);
+  a.esc_raw = reinterpret_cast<const uint32_t*>(w + L.o_esc_raw);
   a.tables = static_cast<const uint8_t*>(tables->dev);
   a.out = out_dev;
   a.out_bytes = out_bytes;

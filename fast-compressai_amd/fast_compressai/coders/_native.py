@@ -45,7 +45,7 @@ class Layout(ctypes.Structure):
         "B", "N", "C", "P", "HW", "K", "chunk_len", "BK", "header_bytes",
         "max_payload_bytes", "cap_words", "workspace_bytes", "ws_chunk_words",
         "ws_chunk_status", "ws_index_hash", "ws_end_off", "ws_info", "ws_states",
-        "ws_words")]
+        "ws_words", "ws_esc", "ws_esc_raw")]
 
 
 class Tables(ctypes.Structure):

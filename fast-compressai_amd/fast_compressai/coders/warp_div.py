@@ -9,7 +9,7 @@ payloads and ``CoderDependencyError`` for a missing library or device.
 
 Differences that follow from the new format:
 
-* ``format_id`` is ``"gaans-w64-v1"``; payloads of the reference's
+* ``format_id`` is ``"gaans-w64-v2"``; payloads of the reference's
   ``warpans-v2`` format are rejected.
 * ``WarpDivPayload.chunk_ends`` (uint32 ``[B, K]``, exposed also under the
   reference's name ``max_rounds``) holds each chunk's end offset in the
@@ -38,8 +38,8 @@ from .capabilities import warp_div_capability
 from .errors import CoderDependencyError, CoderInputError
 from .tables import PreparedTables, TableCache
 
-FORMAT_ID = "gaans-w64-v1"
-FORMAT_VERSION = 1
+FORMAT_ID = "gaans-w64-v2"
+FORMAT_VERSION = 2
 _HEADER_MAGIC = 0x31574147
 _FIXED_HEADER_BYTES = 64
 _SHA256_HEX = re.compile(r"[0-9a-f]{64}")

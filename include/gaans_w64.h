@@ -36,7 +36,7 @@
  *    the stream has finished, or, with pinned host memory, once the
  *    launch's completion word is set (gaans_wait_host_word).
  *
- * Payload format "gaans-w64-v1": defined byte for byte by the CPU oracle,
+ * Payload format "gaans-w64-v2": defined byte for byte by the CPU oracle,
  * oracle/gaans_oracle.c.
  */
 #ifndef GAANS_W64_H
@@ -77,7 +77,7 @@ typedef struct gaans_layout {
   int64_t workspace_bytes;
   /* byte offsets inside the encode workspace */
   int64_t ws_chunk_words, ws_chunk_status, ws_index_hash, ws_end_off, ws_info,
-      ws_states, ws_words;
+      ws_states, ws_words, ws_esc, ws_esc_raw;
 } gaans_layout;
 
 /* Prepared tables: filled by gaans_tables_prepare except `dev`, which the

@@ -3,11 +3,11 @@
  * (see gaans_oracle.h): the product path never links or calls this file.
  *
  * ===========================================================================
- * The wave64 GA-ANS payload format, "gaans-w64-v1"
+ * The wave64 GA-ANS payload format, "gaans-w64-v2"
  * ===========================================================================
  * Coding parameters: 16-bit CDF precision; one 32-bit rANS state per lane,
  * x in [2^16, 2^32), initial state 2^16; 16-bit renormalisation words;
- * 4-bit bypass escapes; 64 lanes per chunk.
+ * 4-bit escape nibbles; 64 lanes per chunk.
  *
  * Chunking.  A batch row holds N symbols, channel-major: C channels of
  * HW = N / C positions.  P channels form one chunk, K = ceil(C / P) chunks per
@@ -21,36 +21,36 @@
  * S = cdf_sizes[tb], maxv = S - 2, v = symbol - offsets[tb] (64-bit):
  *   v <  0    -> escape, raw = -2 v - 1, v = maxv
  *   v >= maxv -> escape, raw = 2 (v - maxv), v = maxv
- * raw must be < 2^32.  Escape ops: n = raw ? msb(raw) / 4 + 1 : 0 nibbles.
- * Ops of one symbol in DECODE order:
- *   op 0       : main  (start = cdf[v], freq = cdf[v+1] - cdf[v])
- *   op 1       : bits(n)                  (escapes only)
- *   op 2 + j   : bits((raw >> 4 j) & 15)  (escapes only, j = 0 .. n-1)
- * Encoder arithmetic (x is u32):
- *   main : if (x >> 16) >= freq: emit x & 0xffff, x >>= 16;
- *          x = (x / freq) << 16 | ... = ((x / freq) << 16) + x % freq + start
- *   bits : if x >= 2^28:        emit x & 0xffff, x >>= 16;
- *          x = (x << 4) | val
- * Decoder arithmetic:
- *   main : cum = x & 0xffff; v = the symbol with cdf[v] <= cum < cdf[v+1];
- *          x = freq * (x >> 16) + cum - start
- *   bits : val = x & 15; x >>= 4
- *   then : if x < 2^16: x = (x << 16) | next word
+ * raw must be < 2^32.  An escape carries n = raw ? msb(raw) / 4 + 1 : 0
+ * nibbles of raw (the 4-bit bypass values of CompressAI's coder).
  *
- * Word order.  The encoder walks steps t = T-1 .. 0 and, inside a step,
- * sub-rounds d = Mt-1 .. 0 (Mt = largest op count of any lane at step t);
- * in sub-round d every active lane that has an op d runs it.  The words
- * emitted in one sub-round form a group, ordered by lane index; each group
- * is PREPENDED to the chunk's word stream.  The decoder therefore reads the
- * stream forwards: steps t = 0 .. T-1, sub-rounds d = 0, 1, ..., and in each
- * sub-round the lanes that need a refill take the next words in lane order.
+ * rANS stream.  Every symbol is one rANS op on its lane's state with
+ * start = cdf[v], freq = cdf[v+1] - cdf[v] (an escape codes its bin maxv):
+ *   encode: if (x >> 16) >= freq: emit x & 0xffff, x >>= 16;
+ *           x = ((x / freq) << 16) + x % freq + start
+ *   decode: cum = x & 0xffff; v = the symbol with cdf[v] <= cum < cdf[v+1];
+ *           x = freq * (x >> 16) + cum - start;
+ *           if x < 2^16: x = (x << 16) | next word
+ * The encoder walks steps t = T-1 .. 0; the words emitted in one step form
+ * a group, ordered by lane index, and each group is PREPENDED to the chunk's
+ * word stream.  The decoder reads the stream forwards: at step t the lanes
+ * that need a refill take the next words in lane order.
  *
- * Chunk bytes: A final states (u32 LE, lane order), the word stream (u16 LE),
- * one zero u16 if the word count is odd.  After decoding, every active lane
- * is back at 2^16 and the whole stream (pad excluded) has been consumed.
+ * Escape section.  The escapes of a chunk, in position order, form a nibble
+ * sequence: for each escape its count n, then its n nibbles of raw, low
+ * nibble first (the same 4 + 4n bits as CompressAI's bypass coding).
+ * Nibble i of the sequence is bits 4 (i & 3) of escape word i >> 2; unused
+ * nibbles of the last word are zero; Q = ceil(nibbles / 4) words.
+ *
+ * Chunk bytes: A final states (u32 LE, lane order), the W words of the rANS
+ * stream (u16 LE), one zero u16 if W + Q is odd, then the Q escape words in
+ * REVERSE order (escape word 0 is the last u16 of the chunk), so a decoder
+ * finds every escape from the chunk's end without knowing W.  After
+ * decoding, every active lane is back at 2^16, the stream, the pad and the
+ * escape words have all been consumed, and every count is <= 8.
  *
  * Header (u32 LE words):
- *   0 magic 0x31574147 ("GAW1")   1 version (1)     2 B    3 N
+ *   0 magic 0x31574147 ("GAW1")   1 version (2)     2 B    3 N
  *   4 C    5 P    6 K    7 chunk_len    8 M (table count)
  *   9 params 0x00041040 (lanes 64 | precision 16 << 8 | bypass 4 << 16)
  *   10,11 table digest (FNV-1a 64, low word first)   12..15 zero
@@ -296,7 +296,7 @@ int rans64_ref_decode(const uint32_t* words, int64_t n_words,
 #define W_LANES 64
 #define W_L ((uint32_t)1 << 16)
 #define W_MAGIC 0x31574147u
-#define W_VERSION 1u
+#define W_VERSION 2u
 #define W_PARAMS 0x00041040u
 #define W_FIXED_WORDS 16
 
@@ -320,8 +320,9 @@ static int w_layout_of(int32_t B, int32_t N, int32_t C, int32_t P, w_layout* L) 
 int64_t gaans_ref_max_payload_bytes(int32_t B, int32_t N, int32_t C, int32_t P) {
   w_layout L;
   if (w_layout_of(B, N, C, P, &L)) return -1;
-  /* per symbol at most 10 ops of one word; per chunk 64 states + pad */
-  return L.header_bytes + (int64_t)B * N * 20 + L.BK * (4 * W_LANES + 4);
+  /* per symbol at most one word and 9 escape nibbles; per chunk 64 states,
+   * a pad word and a partly used escape word */
+  return L.header_bytes + (int64_t)B * N * 7 + L.BK * (4 * W_LANES + 8);
 }
 
 static uint64_t fnv_bytes(uint64_t h, const void* p, size_t n) {
@@ -358,18 +359,22 @@ static uint32_t get_u32(const uint8_t* p) {
   return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
 }
 
+/* nibble sequence of a chunk's escape section (grows as needed) */
 typedef struct {
-  int active;
-  int nops;          /* ops in decode order: 1 (main) or n + 2 */
-  uint32_t start, freq;
-  uint32_t raw;
-  int n;
-} w_sym;
+  uint8_t* nib;
+  int64_t n, cap;
+} w_nibs;
 
-/* value carried by op d of symbol s (bits ops only) */
-static uint32_t w_bits_val(const w_sym* s, int d) {
-  if (d == 1) return (uint32_t)s->n;
-  return (s->raw >> (4 * (d - 2))) & 15u;
+static int w_nibs_push(w_nibs* z, uint32_t v) {
+  if (z->n == z->cap) {
+    int64_t cap = z->cap ? 2 * z->cap : 64;
+    uint8_t* p = (uint8_t*)realloc(z->nib, (size_t)cap);
+    if (!p) return GAANS_REF_ESPACE;
+    z->nib = p;
+    z->cap = cap;
+  }
+  z->nib[z->n++] = (uint8_t)(v & 15u);
+  return GAANS_REF_OK;
 }
 
 static int w_encode_chunk(const int32_t* sym, const int32_t* idx_row, int64_t start,
@@ -378,77 +383,89 @@ static int w_encode_chunk(const int32_t* sym, const int32_t* idx_row, int64_t st
                           uint8_t** out, int64_t* out_bytes, uint32_t* hash_out) {
   int A = len < W_LANES ? len : W_LANES;
   int T = (len + W_LANES - 1) / W_LANES;
-  int64_t cap = (int64_t)len * 10 + 2;
+  uint32_t* st_ = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)(2 * (int64_t)len + 1));
+  int64_t cap = (int64_t)len + 2;
   uint16_t* buf = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)cap);
-  if (!buf) return GAANS_REF_ESPACE;
-  int64_t wp = cap;
-  uint32_t x[W_LANES];
-  w_sym s[W_LANES];
+  w_nibs z = {NULL, 0, 0};
+  int rc = GAANS_REF_OK;
+  if (!st_ || !buf) { rc = GAANS_REF_ESPACE; goto fail; }
+  uint32_t* starts = st_;
+  uint32_t* freqs = st_ + len;
   uint32_t hash = 0;
+  /* pass 1, position order: rANS op of every symbol and the escape section */
+  for (int32_t p = 0; p < len; ++p) {
+    int64_t i = start + p;
+    int32_t tb = idx_row ? idx_row[i] : (int32_t)(i / HW);
+    if (tb < 0 || tb >= M) { rc = GAANS_REF_EINDEX; goto fail; }
+    hash += (uint32_t)(tb + 1) ^ ((uint32_t)p * 0x9E3779B9u);
+    const int32_t* c = cdfs + (int64_t)tb * Lmax;
+    int32_t v; int esc; uint32_t raw;
+    rc = map_symbol(sym[i], sizes[tb], offsets[tb], &v, &esc, &raw);
+    if (rc) goto fail;
+    starts[p] = (uint32_t)c[v];
+    freqs[p] = (uint32_t)(c[v + 1] - c[v]);
+    if (esc) {
+      int n = nibble_count(raw);
+      rc = w_nibs_push(&z, (uint32_t)n);
+      for (int j = 0; !rc && j < n; ++j) rc = w_nibs_push(&z, raw >> (4 * j));
+      if (rc) goto fail;
+    }
+  }
+  /* pass 2: rANS, steps last to first, one word group per step */
+  uint32_t x[W_LANES];
   for (int l = 0; l < W_LANES; ++l) x[l] = W_L;
+  int64_t wp = cap;
   for (int t = T - 1; t >= 0; --t) {
-    int Mt = 0;
+    int emit[W_LANES];
+    int cnt = 0;
     for (int l = 0; l < W_LANES; ++l) {
       int64_t p = l + (int64_t)W_LANES * t;
-      s[l].active = p < len;
-      s[l].nops = 0;
-      if (!s[l].active) continue;
-      int64_t i = start + p;
-      int32_t tb = idx_row ? idx_row[i] : (int32_t)(i / HW);
-      if (tb < 0 || tb >= M) { free(buf); return GAANS_REF_EINDEX; }
-      hash += (uint32_t)(tb + 1) ^ ((uint32_t)p * 0x9E3779B9u);
-      const int32_t* c = cdfs + (int64_t)tb * Lmax;
-      int32_t v; int esc; uint32_t raw;
-      int rc = map_symbol(sym[i], sizes[tb], offsets[tb], &v, &esc, &raw);
-      if (rc) { free(buf); return rc; }
-      s[l].start = (uint32_t)c[v];
-      s[l].freq = (uint32_t)(c[v + 1] - c[v]);
-      s[l].raw = raw;
-      s[l].n = esc ? nibble_count(raw) : 0;
-      s[l].nops = esc ? s[l].n + 2 : 1;
-      if (s[l].nops > Mt) Mt = s[l].nops;
+      emit[l] = p < len && (x[l] >> 16) >= freqs[p];
+      cnt += emit[l];
     }
-    for (int d = Mt - 1; d >= 0; --d) {
-      int emit[W_LANES];
-      int cnt = 0;
-      for (int l = 0; l < W_LANES; ++l) {
-        emit[l] = 0;
-        if (!s[l].active || d >= s[l].nops) continue;
-        if (d == 0) emit[l] = (x[l] >> 16) >= s[l].freq;
-        else emit[l] = x[l] >= ((uint32_t)1 << 28);
-        cnt += emit[l];
+    wp -= cnt;
+    int64_t r = wp;
+    for (int l = 0; l < W_LANES; ++l) {
+      int64_t p = l + (int64_t)W_LANES * t;
+      if (p >= len) continue;
+      if (emit[l]) {
+        buf[r++] = (uint16_t)(x[l] & 0xffffu);
+        x[l] >>= 16;
       }
-      wp -= cnt;
-      int64_t r = wp;
-      for (int l = 0; l < W_LANES; ++l) {
-        if (!s[l].active || d >= s[l].nops) continue;
-        if (emit[l]) {
-          buf[r++] = (uint16_t)(x[l] & 0xffffu);
-          x[l] >>= 16;
-        }
-        if (d == 0) {
-          uint32_t f = s[l].freq;
-          x[l] = ((x[l] / f) << 16) + (x[l] % f) + s[l].start;
-        } else {
-          x[l] = (x[l] << 4) | w_bits_val(&s[l], d);
-        }
-      }
+      uint32_t f = freqs[p];
+      x[l] = ((x[l] / f) << 16) + (x[l] % f) + starts[p];
     }
   }
-  int64_t W = cap - wp;
-  int64_t bytes = 4 * (int64_t)A + 2 * W + ((W & 1) ? 2 : 0);
-  uint8_t* o = (uint8_t*)calloc((size_t)bytes, 1);
-  if (!o) { free(buf); return GAANS_REF_ESPACE; }
-  for (int l = 0; l < A; ++l) put_u32(o + 4 * l, x[l]);
-  for (int64_t k = 0; k < W; ++k) {
-    o[4 * A + 2 * k] = (uint8_t)buf[wp + k];
-    o[4 * A + 2 * k + 1] = (uint8_t)(buf[wp + k] >> 8);
+  {
+    int64_t W = cap - wp;
+    int64_t Q = (z.n + 3) / 4;
+    int64_t pad = (W + Q) & 1;
+    int64_t U = W + pad + Q;
+    int64_t bytes = 4 * (int64_t)A + 2 * U;
+    uint8_t* o = (uint8_t*)calloc((size_t)bytes, 1);
+    if (!o) { rc = GAANS_REF_ESPACE; goto fail; }
+    for (int l = 0; l < A; ++l) put_u32(o + 4 * l, x[l]);
+    uint8_t* w16 = o + 4 * A;
+    for (int64_t k = 0; k < W; ++k) {
+      w16[2 * k] = (uint8_t)buf[wp + k];
+      w16[2 * k + 1] = (uint8_t)(buf[wp + k] >> 8);
+    }
+    for (int64_t j = 0; j < Q; ++j) {
+      uint32_t e = 0;
+      for (int q = 0; q < 4 && 4 * j + q < z.n; ++q) e |= (uint32_t)z.nib[4 * j + q] << (4 * q);
+      int64_t pos = U - 1 - j; /* escape word j, counted from the chunk end */
+      w16[2 * pos] = (uint8_t)e;
+      w16[2 * pos + 1] = (uint8_t)(e >> 8);
+    }
+    *out = o;
+    *out_bytes = bytes;
+    *hash_out = hash;
   }
+fail:
+  free(st_);
   free(buf);
-  *out = o;
-  *out_bytes = bytes;
-  *hash_out = hash;
-  return GAANS_REF_OK;
+  free(z.nib);
+  return rc;
 }
 
 int gaans_ref_encode(const int32_t* symbols, const int32_t* indexes,
@@ -540,83 +557,77 @@ int gaans_ref_decode(const uint8_t* payload, int64_t payload_len,
     const uint8_t* cp = data + prev;
     int64_t cbytes = (int64_t)endo - prev;
     if (cbytes < 4 * A || ((cbytes - 4 * A) & 3)) return GAANS_REF_ECORRUPT;
-    int64_t q = (cbytes - 4 * A) / 2; /* words incl. pad */
+    int64_t U = (cbytes - 4 * A) / 2; /* u16 words: stream, pad, escapes */
     const uint8_t* wbase = cp + 4 * A;
-    int64_t rp = 0;
+    int64_t rp = 0;  /* stream words read */
+    int64_t eq = 0;  /* escape nibbles read */
     uint32_t x[W_LANES];
     for (int l = 0; l < W_LANES; ++l) x[l] = l < A ? get_u32(cp + 4 * l) : W_L;
     const int32_t* idx_row = indexes ? indexes + b * (int64_t)N : NULL;
     int32_t* orow = out_symbols + b * (int64_t)N;
     uint32_t hash = 0;
     for (int t = 0; t < T; ++t) {
-      int32_t tbs[W_LANES], S_[W_LANES], vv[W_LANES];
-      uint32_t raw[W_LANES];
-      int nops[W_LANES], active[W_LANES];
+      int need[W_LANES];
       for (int l = 0; l < W_LANES; ++l) {
         int64_t p = l + (int64_t)W_LANES * t;
-        active[l] = p < len;
-        nops[l] = active[l] ? 1 : 0;
-        raw[l] = 0;
-        if (!active[l]) continue;
+        need[l] = 0;
+        if (p >= len) continue;
         int64_t i = start + p;
         int32_t tb = idx_row ? idx_row[i] : (int32_t)(i / L.HW);
         if (tb < 0 || tb >= M) return GAANS_REF_EINDEX;
         hash += (uint32_t)(tb + 1) ^ ((uint32_t)p * 0x9E3779B9u);
-        tbs[l] = tb;
-        S_[l] = cdf_sizes[tb];
-      }
-      for (int d = 0;; ++d) {
-        int any = 0;
-        int need[W_LANES];
-        for (int l = 0; l < W_LANES; ++l) {
-          need[l] = 0;
-          if (!active[l] || d >= nops[l]) continue;
-          any = 1;
-          if (d == 0) {
-            const int32_t* c = cdfs + (int64_t)tbs[l] * Lmax;
-            uint32_t cum = x[l] & 0xffffu;
-            int32_t v = find_symbol(c, S_[l], cum);
-            uint32_t st = (uint32_t)c[v], f = (uint32_t)(c[v + 1] - c[v]);
-            x[l] = f * (x[l] >> 16) + cum - st;
-            vv[l] = v;
-            if (v == S_[l] - 2) nops[l] = 2; /* count nibble next */
-          } else {
-            uint32_t val = x[l] & 15u;
-            x[l] >>= 4;
-            if (d == 1) {
-              if (val > 8) return GAANS_REF_ECORRUPT;
-              nops[l] = 2 + (int)val;
-            } else {
-              raw[l] |= val << (4 * (d - 2));
+        const int32_t* c = cdfs + (int64_t)tb * Lmax;
+        int32_t S = cdf_sizes[tb];
+        uint32_t cum = x[l] & 0xffffu;
+        int32_t v = find_symbol(c, S, cum);
+        uint32_t st = (uint32_t)c[v], f = (uint32_t)(c[v + 1] - c[v]);
+        x[l] = f * (x[l] >> 16) + cum - st;
+        need[l] = x[l] < W_L;
+        if (v == S - 2) { /* escape: the next entry of the escape section */
+          uint32_t nib[9];
+          for (int j = 0; j < 9; ++j) nib[j] = 0;
+          int n = 0;
+          for (int j = 0; j <= n; ++j) {
+            int64_t wi = (eq + j) >> 2; /* escape word, from the chunk end */
+            if (wi >= U) return GAANS_REF_ECORRUPT;
+            int64_t pos = U - 1 - wi;
+            uint32_t e = (uint32_t)wbase[2 * pos] | ((uint32_t)wbase[2 * pos + 1] << 8);
+            nib[j] = (e >> (4 * ((eq + j) & 3))) & 15u;
+            if (j == 0) {
+              n = (int)nib[0];
+              if (n > 8) return GAANS_REF_ECORRUPT;
             }
           }
-          need[l] = x[l] < W_L;
-        }
-        if (!any) break;
-        for (int l = 0; l < W_LANES; ++l) {
-          if (!need[l]) continue;
-          uint32_t w = 0;
-          if (rp < q) w = (uint32_t)wbase[2 * rp] | ((uint32_t)wbase[2 * rp + 1] << 8);
-          else return GAANS_REF_ECORRUPT;
-          ++rp;
-          x[l] = (x[l] << 16) | w;
+          uint32_t raw = 0;
+          for (int j = 0; j < n; ++j) raw |= nib[1 + j] << (4 * j);
+          eq += 1 + n;
+          rc = unmap_escape(raw, S, offsets[tb], &orow[i]);
+          if (rc) return rc;
+        } else {
+          orow[i] = v + offsets[tb];
         }
       }
       for (int l = 0; l < W_LANES; ++l) {
-        if (!active[l]) continue;
-        int64_t i = start + l + (int64_t)W_LANES * t;
-        int32_t tb = tbs[l];
-        if (vv[l] == S_[l] - 2) {
-          rc = unmap_escape(raw[l], S_[l], offsets[tb], &orow[i]);
-          if (rc) return rc;
-        } else {
-          orow[i] = vv[l] + offsets[tb];
-        }
+        if (!need[l]) continue;
+        if (rp >= U) return GAANS_REF_ECORRUPT;
+        uint32_t w = (uint32_t)wbase[2 * rp] | ((uint32_t)wbase[2 * rp + 1] << 8);
+        ++rp;
+        x[l] = (x[l] << 16) | w;
       }
     }
     for (int l = 0; l < A; ++l)
       if (x[l] != W_L) return GAANS_REF_ECORRUPT;
-    if (!(rp == q || (rp == q - 1 && (q & 1) == 0))) return GAANS_REF_ECORRUPT;
+    {
+      int64_t Q = (eq + 3) / 4;
+      int64_t pad = (rp + Q) & 1;
+      if (rp + pad + Q != U) return GAANS_REF_ECORRUPT;
+      if (pad && (wbase[2 * rp] | wbase[2 * rp + 1])) return GAANS_REF_ECORRUPT;
+      if (eq & 3) { /* unused nibbles of the last escape word */
+        int64_t pos = U - Q;
+        uint32_t e = (uint32_t)wbase[2 * pos] | ((uint32_t)wbase[2 * pos + 1] << 8);
+        if (e >> (4 * (eq & 3))) return GAANS_REF_ECORRUPT;
+      }
+    }
     if (hash != want_hash) return GAANS_REF_EMISMATCH;
     prev = endo;
   }

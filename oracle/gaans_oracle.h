@@ -22,7 +22,7 @@
  *     information content.
  *
  *  2. gaans_ref_*   -- a sequential emulation of the wave64 GA-ANS payload
- *     format ("gaans-w64-v1") that the GPU kernels must reproduce byte for
+ *     format ("gaans-w64-v2") that the GPU kernels must reproduce byte for
  *     byte.  The format is specified in the comment block of gaans_oracle.c.
  *
  * Every function returns 0 on success or a negative GAANS_REF_E* code.

@@ -6,8 +6,9 @@ checker of the HIP kernels.
   the reference's CPU coder tests (tests/test_coders.py:25-31, :78-81).
 * wave64 format: hand-derived payloads in which every coding step can be
   followed on paper (freq-1 tables make each renormalisation word equal to a
-  known symbol), so lane order, group order, escape sub-rounds, states and
-  the header layout are each pinned by a literal value.
+  known symbol), so lane order, group order, the escape section (nibble
+  order, word order, pad), states and the header layout are each pinned by a
+  literal value.
 * Round trips of the reference's GPU test cases
   (tests/gpu/test_warp_div_cuda.py:18-41) and of random cases.
 * Quantize/dequantize closed forms against torch's own round / add.
@@ -125,7 +126,7 @@ def hash_of(tables_per_position):
 
 
 def header_words(B, N, C, P, K, chunk_len, M, digest):
-    return [0x31574147, 1, B, N, C, P, K, chunk_len, M, 0x00041040,
+    return [0x31574147, 2, B, N, C, P, K, chunk_len, M, 0x00041040,
             digest & 0xFFFFFFFF, digest >> 32, 0, 0, 0, 0]
 
 
@@ -148,31 +149,60 @@ def kat_130():
     S = 18
     cdf = list(range(17)) + [65536]
     s = [(5 * p + 3) % 16 for p in range(130)]
-    s[129] = 17  # lane 1, step 2: escape, raw = 2 * (17 - 16) = 2, one nibble
+    s[3] = -1    # step 0, lane 3: raw = -2 * -1 - 1 = 1, one nibble
+    s[70] = 56   # step 1, lane 6: raw = 2 * (56 - 16) = 0x50, two nibbles
+    s[129] = 17  # step 2, lane 1: raw = 2 * (17 - 16) = 2, one nibble
     return [cdf], [S], [0], s
 
 
-def test_gaans_kat_lane_order_group_order_and_escape_subrounds():
+def test_gaans_kat_lane_order_group_order_and_escape_section():
     cdfs, sizes, offs, s = kat_130()
     data = O.gaans_encode([s], None, cdfs, sizes, offs, 1)
-    # Step t=2 (lanes 0, 1): lane 1 runs bits(2) -> 0x100002, bits(n=1) ->
-    # 0x1000021 (no words), then in sub-round 0 lane 0 emits 0x0000 and lane 1's
-    # escape main op gives 0x1000021 = 256 * 65520 + 4129 -> (256 << 16) + 4129 + 16
-    # = 0x01001031 with no word.
-    # Step t=1: lane 0 emits s[128], lane 1 emits 0x1031 (x >> 16 = 256 >= 1) and
-    # becomes 0x01000000 + s[65]; lanes 2..63 emit their initial 0x0000.
-    # Step t=0: lane l emits s[64 + l]; states end at 0x10000 + s[l], lane 1 at
-    # 0x01000000 + s[1].
-    stream = s[64:128] + [s[128], 0x1031] + [0] * 62 + [0]
-    stream += [0]  # odd word count: one zero pad word
+    # An escape codes the bin (start 16, freq 65520): from x = 0x10000 + u
+    # (u < 16) it gives ((x // 65520) << 16) + x % 65520 + 16 = 0x10020 + u with
+    # no word.  Step t=2 (lanes 0, 1): lane 0 emits its initial 0x0000, lane 1
+    # (escape) becomes 0x10020.  Step t=1: lane 0 emits s[128], lane 1 emits
+    # 0x0020, lane 6 (escape) emits nothing and becomes 0x10020, the other
+    # lanes emit 0x0000.  Step t=0: lane l emits s[64 + l], lane 6 emits 0x0020,
+    # lane 3 (escape) emits nothing and ends at 0x10020 + s[67]; the others end
+    # at 0x10000 + s[l].  Groups are prepended, so the stream is step 0's group,
+    # then step 1's, then step 2's: 63 + 63 + 1 = 127 words.
+    g0 = [s[64 + l] for l in range(64) if l != 3]
+    g0[5] = 0x0020  # lane 6 (index 5 once lane 3 is dropped)
+    g1 = [s[128], 0x0020] + [0] * 61
+    stream = g0 + g1 + [0]
+    assert len(stream) == 127
+    # escape section, position order: p=3 -> [1, 1], p=70 -> [2, 0, 5],
+    # p=129 -> [1, 2]; nibbles 1,1,2,0 | 5,1,2 -> words 0x0211, 0x0215, stored
+    # last word first at the chunk end, after a zero pad (127 + 2 is odd)
+    stream += [0, 0x0215, 0x0211]
     states = [0x10000 + s[l] for l in range(64)]
-    states[1] = 0x01000000 + s[1]
+    states[3] = 0x10020 + s[67]
     chunk = struct.pack("<64I", *states) + struct.pack(f"<{len(stream)}H", *stream)
     assert len(chunk) == 516
     dg = fnv1a64(table_digest_bytes(cdfs, sizes, offs))
     hdr = header_words(1, 130, 1, 1, 1, 130, 1, dg) + [516, hash_of([0] * 130), 0, 0]
     assert data == struct.pack("<20I", *hdr) + chunk
     assert O.gaans_decode(data, None, 1, 130, cdfs, sizes, offs, 1).tolist() == [s]
+
+
+def test_gaans_escape_section_word_order_without_pad():
+    # one escape with raw 0x12345 (5 nibbles): nibbles 5,5,4,3 | 2,1 -> words
+    # 0x3455, 0x0012 at the chunk end, last word first; no rANS words (one lane,
+    # escape bin freq 32768 from x = 2^16 gives 2^17 + 32768, no emit), so
+    # W + Q = 2 is even and there is no pad
+    cdfs, sizes, offs = CDF2, [3], [0]
+    raw = 0x12345  # odd: value -(raw >> 1) - 1
+    sym = -(raw >> 1) - 1
+    data = O.gaans_encode([[sym]], None, cdfs, sizes, offs, 1)
+    hb = (64 + 8 + 15) // 16 * 16
+    chunk = data[hb:]
+    assert struct.unpack("<IHH", chunk) == ((1 << 17) + 32768, 0x0012, 0x3455)
+    assert O.gaans_decode(data, None, 1, 1, cdfs, sizes, offs, 1).tolist() == [[sym]]
+    bad = bytearray(data)
+    bad[hb + 5] |= 0x80  # an unused nibble of the last escape word (bits 12..15)
+    with pytest.raises(O.OracleError):
+        O.gaans_decode(bytes(bad), None, 1, 1, cdfs, sizes, offs, 1)
 
 
 def test_gaans_chunking_and_header_offsets():
@@ -267,7 +297,9 @@ def test_gaans_detects_corruption_and_mismatch():
 
 def test_gaans_bpp_overhead_is_the_lane_flush():
     # per chunk the format adds ~64 states * 32 bits over the ideal stream;
-    # a single CompressAI-style stream carries one 64-bit flush.
+    # a single CompressAI-style stream carries one 64-bit flush.  The rest is
+    # the quantisation loss of 32-bit states renormalised by 16 bits (x / freq
+    # can be small), here under 0.5% with 73% of the symbols escapes.
     rng = np.random.default_rng(5)
     cdfs, sizes, offs = random_tables(rng, 8, 32)
     s = rng.integers(-6, 6, (1, 8 * 4096)).astype(np.int32)
@@ -278,7 +310,7 @@ def test_gaans_bpp_overhead_is_the_lane_flush():
         K = math.ceil(8 / P)
         hb = (64 + 8 * K + 15) // 16 * 16
         overhead = len(data) - hb - single
-        assert 0 < overhead <= K * (64 * 4 + 2) + 0.003 * single
+        assert 0 < overhead <= K * (64 * 4 + 2) + 0.005 * single
 
 
 # ---------------------------------------------------------------------------
