@@ -392,45 +392,71 @@ constexpr int kEncRecBytes = 2 * kEncSB * kLanes * 16;        // two blocks of o
 constexpr int kEncInfoBytes = 2 * kEncSB * 4;                 // per-step escape flag
 constexpr int kEncFixedLds = kEncRingBytes + kEncRecBytes + kEncInfoBytes + kPartBytes;
 
-// last workgroup of an encode launch (wave 0): chunk offsets + payload size +
-// status
-__device__ void encode_finish(const EncArgs& a, int lane) {
+// Payload bytes of chunk g: states, stream and escape words, pad.
+__device__ __forceinline__ uint64_t chunk_bytes(const EncArgs& a, int64_t g) {
+  const int len = chunk_len_of(g, a.K, a.chunk_len, a.N);
+  const uint32_t A = len < kLanes ? (uint32_t)len : (uint32_t)kLanes;
+  const uint32_t W = __hip_atomic_load(&a.chunk_words[g], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t Z = __hip_atomic_load(&a.esc[g].y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t U = (uint64_t)W + (Z + 3u) / 4u;  // stream + escape words
+  return 4ull * A + 2ull * (U + (U & 1u));
+}
+
+// Last workgroup of an encode launch (all waves): chunk end offsets, payload
+// size and status.  The chunks are scanned kThreads at a time, one per
+// thread, with the next tile's loads issued before the current tile's scan.
+// The completion word carries size and status in one 64-bit store, so the
+// host can read it as soon as it lands (no system-wide cache write-back).
+__device__ void encode_finish(const EncArgs& a, int tid, uint64_t* sh) {
+  const int lane = tid & (kLanes - 1), wv = tid >> 6;
   uint64_t carry = 0;
   uint32_t st = 0;
-  for (int64_t base = 0; base < a.BK; base += kLanes) {
-    const int64_t g = base + lane;
-    uint64_t v = 0;
-    if (g < a.BK) {
-      const int len = chunk_len_of(g, a.K, a.chunk_len, a.N);
-      const uint32_t A = len < kLanes ? (uint32_t)len : (uint32_t)kLanes;
-      const uint32_t W = __hip_atomic_load(&a.chunk_words[g], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-      const uint32_t Z = __hip_atomic_load(&a.esc[g].y, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-      const uint64_t U = (uint64_t)W + (Z + 3u) / 4u;  // stream + escape words
-      v = 4ull * A + 2ull * (U + (U & 1u));
-      st |= __hip_atomic_load(&a.chunk_status[g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint64_t v = 0;
+  if (tid < a.BK) {
+    v = chunk_bytes(a, tid);
+    st |= __hip_atomic_load(&a.chunk_status[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  for (int64_t base = 0; base < a.BK; base += kThreads) {
+    const int64_t g = base + tid;
+    uint64_t vn = 0;
+    if (g + kThreads < a.BK) {
+      vn = chunk_bytes(a, g + kThreads);
+      st |= __hip_atomic_load(&a.chunk_status[g + kThreads], __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
     }
-    const uint64_t incl = wave_incl_scan(v, lane) + carry;
+    uint64_t incl = wave_incl_scan(v, lane);
+    if (lane == kLanes - 1) sh[wv] = incl;
+    __syncthreads();
+    uint64_t before = 0, tot = 0;
+    for (int w = 0; w < kWaves; ++w) {
+      before += w < wv ? sh[w] : 0ull;
+      tot += sh[w];
+    }
+    __syncthreads();
+    incl += before + carry;
     if (g < a.BK) {
       a.end_off[g] = (uint32_t)incl;
       if (incl > 0xffffffffull) st |= GAANS_ST_SIZE;
     }
-    carry = (uint64_t)__shfl((long long)incl, 63, 64);
+    carry += tot;
+    v = vn;
   }
   st = wave_or(st);
-  if (lane == 0) {
+  uint32_t* sst = reinterpret_cast<uint32_t*>(sh);
+  if (lane == 0) sst[wv] = st;
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kWaves; ++w) st |= sst[w];
     const uint64_t total = (uint64_t)a.header_bytes + carry;
     a.ws_info[0] = total;
     a.ws_info[1] = st;
     if (a.info_out) {
       a.info_out[0] = total;
       a.info_out[1] = st;
+      __hip_atomic_store(&a.info_out[2], 1ull | ((uint64_t)st << 1) | (total << 16),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
-    __threadfence_system();
-    // completion word, written after the info words are visible to the host
-    if (a.info_out)
-      __hip_atomic_store(&a.info_out[2], 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     __hip_atomic_store(&a.ctrl[kCtrlEncDone], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
@@ -731,23 +757,24 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
       ss |= part[kWaves + w];
       zs += part[2 * kWaves + w];
     }
-    a.chunk_words[g] = (uint32_t)(a.cap_words - wp);
-    a.chunk_status[g] = ss;
-    a.index_hash[g] = hs;
-    a.esc[g] = make_uint2(part[3 * kWaves], zs);
+    a.index_hash[g] = hs;          // read by the pack kernel only
+    a.esc[g].x = part[3 * kWaves];
+    // What the last workgroup reads (maybe on another XCD, behind another L2)
+    // is stored with agent-scope atomics, which are coherent across the
+    // device, and has completed before the counter is raised: no fence, so
+    // no write-back of the XCD's whole L2.
+    __hip_atomic_store(&a.chunk_words[g], (uint32_t)(a.cap_words - wp), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&a.chunk_status[g], ss, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&a.esc[g].y, zs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    part[0] = __hip_atomic_fetch_add(&a.ctrl[kCtrlEncDone], 1u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
   }
-  __threadfence();
   __syncthreads();
-  if (wid == 0) {
-    uint32_t done = 0;
-    if (lane == 0)
-      done = __hip_atomic_fetch_add(&a.ctrl[kCtrlEncDone], 1u, __ATOMIC_ACQ_REL,
-                                    __HIP_MEMORY_SCOPE_AGENT);
-    done = (uint32_t)__shfl((int)done, 0, 64);
-    if (done == (uint32_t)(a.BK - 1)) {
-      __threadfence();
-      encode_finish(a, lane);
-    }
+  if (part[0] == (uint32_t)(a.BK - 1)) {  // uniform: the last workgroup to finish
+    __syncthreads();  // every wave has read part[0] before it is reused
+    encode_finish(a, tid, reinterpret_cast<uint64_t*>(part));
   }
 }
 
@@ -947,12 +974,15 @@ __device__ __forceinline__ void dec_lookup(const Tabs& tb, const uint4 r, uint32
   const uint64_t e = kLds ? tb.llut[li] : tb.glut[li];
   const uint32_t lo = (uint32_t)e, hi = (uint32_t)(e >> 32);
   const uint32_t s0 = hi & 0xffffu, nxt = hi >> 16;
+  // the dense test first: its scalar result is ready by the branch below
+  const uint64_t dm = ballot(act & (nxt == 0xffffu));
+  asm volatile("" ::"s"(dm));
   const uint32_t st0 = lo & 0xffffu, fr0 = (lo >> 16) + 1u;
   const bool up = cum >= st0 + fr0;
   s = up ? s0 + 1u : s0;
   st = up ? st0 + fr0 : st0;
   fr = up ? nxt + 1u : fr0;
-  if (__builtin_expect(act & (nxt == 0xffffu), 0)) {
+  if (__builtin_expect(dm != 0ull, 0) && (act & (nxt == 0xffffu))) {
     const uint32_t blk = kLds ? lo - tb.dense_first : lo;
     const uint32_t di = (blk << kLutBits) + (cum & (kLutSize - 1));
     s = s0 + (uint32_t)(kLds ? tb.ldense[di] : tb.gdense[di]);
@@ -1058,11 +1088,33 @@ __device__ __forceinline__ uint32_t esc_next(Esc& E, uint32_t& status, int lane)
   return (uint32_t)((v >> 4) & ((1ull << (4u * n)) - 1ull));
 }
 
-// One decode step of the coder wave; returns the decoded value.  kFull: every
-// lane is active and no offset can overflow with a symbol index.
+// Values of the escaping lanes em of one step (record r): each takes the next
+// entry of the escape section, in lane order.  v holds the lanes' values and
+// is updated for the escaping ones.
+__device__ __forceinline__ void dec_escapes(uint64_t em, const uint4 r, uint32_t& v, Esc& E,
+                                            uint32_t& status, int lane) {
+  const bool esc = (em >> lane) & 1ull;
+  uint32_t raw = 0;
+  do {
+    const int L = __ffsll((unsigned long long)em) - 1;
+    const uint32_t rv = esc_next(E, status, lane);
+    raw = lane == L ? rv : raw;
+    em &= em - 1ull;
+  } while (em);
+  const int64_t ev = (raw & 1u) ? -(int64_t)(raw >> 1) - 1 : (int64_t)(raw >> 1) + r.y;
+  const int64_t sv = ev + (int32_t)r.z;
+  const bool oob = esc & ((sv < INT32_MIN) | (sv > INT32_MAX));
+  status |= oob ? GAANS_ST_CORRUPT : 0u;
+  v = esc ? (oob ? 0u : (uint32_t)(int32_t)sv) : v;
+}
+
+// One decode step of the coder wave; returns the decoded value and, in em,
+// the lanes that decoded the escape bin (their values are set afterwards by
+// dec_escapes, off the state chain).  kFull: every lane is active and no
+// offset can overflow with a symbol index.
 template <bool kLds, bool kFull>
 __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint4 r, uint32_t& x,
-                                             Stream& S, const uint16_t* ring, Esc& E,
+                                             Stream& S, const uint16_t* ring, uint64_t& em,
                                              uint32_t& status, int lane) {
   const bool act = kFull || r.y != 0xffffffffu;
   const uint32_t cum = x & 0xffffu;
@@ -1073,26 +1125,10 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint4 r, uint
   dec_refill(act & (x < kStateLow), x, S, ring, lane);
   // value + offset for an ordinary symbol: s < 2^16, so the int32 sum overflows
   // exactly when it wraps below the offset
-  int32_t o = (int32_t)(s + r.z);
-  bool oob = !kFull && o < (int32_t)r.z;
+  const int32_t o = (int32_t)(s + r.z);
   const bool esc = act & (s == r.y);
-  uint64_t em = ballot(esc);
-  if (__builtin_expect(em != 0, 0)) {
-    // escapes of the step take the next entries of the escape section in
-    // lane order
-    uint32_t raw = 0;
-    do {
-      const int L = __ffsll((unsigned long long)em) - 1;
-      const uint32_t rv = esc_next(E, status, lane);
-      raw = lane == L ? rv : raw;
-      em &= em - 1ull;
-    } while (em);
-    const int64_t ev = (raw & 1u) ? -(int64_t)(raw >> 1) - 1 : (int64_t)(raw >> 1) + r.y;
-    const int64_t sv = ev + (int32_t)r.z;
-    o = esc ? (int32_t)sv : o;
-    oob = esc ? ((sv < INT32_MIN) | (sv > INT32_MAX)) : oob;
-  }
-  oob &= act;
+  em = ballot(esc);
+  const bool oob = act & !esc & !kFull & (o < (int32_t)r.z);
   status |= oob ? GAANS_ST_CORRUPT : 0u;
   return (uint32_t)(oob ? 0 : o);
 }
@@ -1277,9 +1313,17 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
         if ((j + 1) * kDecSB * kLanes <= len && all_lds && offsets_safe) {
           // common case: every lane of the block active, LDS tables, no
           // per-step branches
+          uint64_t em[kDecSB], any_em = 0;
 #pragma unroll
-          for (int u = 0; u < kDecSB; ++u)
-            ov[u] = dec_step<true, true>(tb, r[u], x, S, sring, E, status, lane);
+          for (int u = 0; u < kDecSB; ++u) {
+            ov[u] = dec_step<true, true>(tb, r[u], x, S, sring, em[u], status, lane);
+            any_em |= em[u];
+          }
+          if (__builtin_expect(any_em != 0ull, 0)) {
+#pragma unroll
+            for (int u = 0; u < kDecSB; ++u)
+              if (em[u]) dec_escapes(em[u], r[u], ov[u], E, status, lane);
+          }
           // decoded values replace the records' x words; the mappers store them
 #pragma unroll
           for (int u = 0; u < kDecSB; ++u)
@@ -1289,10 +1333,11 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
 #pragma unroll 1
           for (int u = 0; u < kDecSB && j * kDecSB + u < T; ++u) {
             const uint4 ru = src[u * kLanes + lane];
-            const uint32_t v =
-                uni((int)info[(j & 1) * kDecSB + u])
-                    ? dec_step<true, false>(tb, ru, x, S, sring, E, status, lane)
-                    : dec_step<false, false>(tb, ru, x, S, sring, E, status, lane);
+            uint64_t em;
+            uint32_t v = uni((int)info[(j & 1) * kDecSB + u])
+                             ? dec_step<true, false>(tb, ru, x, S, sring, em, status, lane)
+                             : dec_step<false, false>(tb, ru, x, S, sring, em, status, lane);
+            if (em) dec_escapes(em, ru, v, E, status, lane);
             reinterpret_cast<uint32_t*>(src + u * kLanes + lane)[0] = v;
           }
         }
@@ -1348,18 +1393,22 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
       st |= part[kWaves + w];
     }
     if (ok && hs != want_hash) st |= GAANS_ST_INDEXHASH;
+    // status and counter are agent-scope atomics; the status has completed
+    // before the counter is raised (no fence: decoded values need no
+    // visibility before the kernel ends)
     if (st)
       __hip_atomic_fetch_or(&a.ctrl[kCtrlDecStatus], st, __ATOMIC_RELAXED,
                             __HIP_MEMORY_SCOPE_AGENT);
-    __threadfence();
-    const uint32_t done = __hip_atomic_fetch_add(&a.ctrl[kCtrlDecDone], 1u, __ATOMIC_ACQ_REL,
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const uint32_t done = __hip_atomic_fetch_add(&a.ctrl[kCtrlDecDone], 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
     if (done == (uint32_t)(a.BK - 1)) {
-      const uint32_t all = __hip_atomic_exchange(&a.ctrl[kCtrlDecStatus], 0u, __ATOMIC_ACQ_REL,
+      const uint32_t all = __hip_atomic_exchange(&a.ctrl[kCtrlDecStatus], 0u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
       a.status_out[0] = all;
-      __threadfence_system();
-      __hip_atomic_store(&a.status_out[1], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+      // completion word with the status, one store (no system-wide write-back)
+      __hip_atomic_store(&a.status_out[1], 1u | (all << 1), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
       __hip_atomic_store(&a.ctrl[kCtrlDecDone], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }

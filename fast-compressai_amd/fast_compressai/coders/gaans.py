@@ -3,7 +3,7 @@
 Per (device, stream) the engine keeps a control block (device memory, zeroed
 once; every launch leaves it zeroed), a reusable workspace, and two small
 pinned host buffers that the kernels' last workgroup writes the payload
-size / status into, followed by a completion word.  Calls on one stream are
+size / status into, and a completion word that carries both.  Calls on one stream are
 ordered, so these buffers are never shared by two calls in flight.
 
 Encode enqueues the coding kernel and the pack kernel back to back (the
@@ -135,7 +135,8 @@ def encode(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,
                                  out.data_ptr(), out.numel())
         _native.check(rc, "GA-ANS pack")
         _native.wait_host_word(sp, st.info_done, "GA-ANS encode")  # the one host wait
-        total, status = int(st.info_np[0]), int(st.info_np[1])
+        word = int(st.info_np[2])  # 1 | status << 1 | payload bytes << 16
+        total, status = word >> 16, (word >> 1) & 0x7FFF
     if status:
         raise CoderInputError(f"GA-ANS encode failed: {_native.describe_status(status)}")
     packed = out[:total]
@@ -169,7 +170,7 @@ def decode(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int,
                                         st.ctrl.data_ptr(), st.status.data_ptr())
         _native.check(rc, "GA-ANS decode")
         _native.wait_host_word(sp, st.status_done, "GA-ANS decode")  # the one host wait
-        status = int(st.status_np[0])
+        status = int(st.status_np[1]) >> 1  # 1 | status << 1
     if status:
         raise CoderInputError(f"warp_div decode failed: {_native.describe_status(status)}")
     return out

@@ -127,8 +127,9 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes,
  * The launch's last block scans the chunk sizes into payload offsets and
  * writes info = {u64 payload bytes incl. header, u64 status} both to the
  * workspace (at layout->ws_info) and, when info_out is not NULL, to
- * info_out[0..1] (device or pinned host memory), then sets the completion
- * word info_out[2] to 1 (info_out holds 3 u64).  `indexes_dev` may be NULL: then
+ * info_out[0..1] (device or pinned host memory), and the completion word
+ * info_out[2] = 1 | status << 1 | payload bytes << 16 in one 64-bit store
+ * (info_out holds 3 u64).  `indexes_dev` may be NULL: then
  * position i of a row uses table i / HW (CompressAI EntropyBottleneck
  * indexes).  Reference: encode_with_indexes_warp_v2_cuda,
  * src/fast_compressai/coders/cuda/warp_ans_kernel_v2.cu:183-273. */
@@ -161,8 +162,8 @@ int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace
 
 /* Decode a payload into int32 symbols [B, N].  The last block writes the
  * OR of all GAANS_ST_* bits (0 when the payload decoded cleanly) to
- * status_out[0] (device or pinned host memory), then sets the completion
- * word status_out[1] to 1 (status_out holds 2 u32).
+ * status_out[0] (device or pinned host memory), and the completion word
+ * status_out[1] = 1 | status << 1 (status_out holds 2 u32).
  * Reference: decode_with_indexes_warp_cuda, warp_ans_kernel.cu:477-544. */
 int gaans_decode_symbols(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
                          const int32_t* indexes_dev, const gaans_tables* tables,
@@ -180,9 +181,10 @@ int gaans_decode_latents(void* stream, const uint8_t* payload_dev, int64_t paylo
 
 /* Wait on the host for a launch's completion word (encode: low half of
  * info_out[2]; decode: status_out[1]) in pinned host memory that the caller
- * set to 0 before the launch.  Returns GAANS_OK once the word is nonzero:
- * the info/status words are then valid, while later work on the stream (the
- * pack kernel) may still run, ordered on `stream` as usual.  Returns
+ * set to 0 before the launch.  Returns GAANS_OK once the word is nonzero; the
+ * word itself carries the size and status (info_out[0..1] and status_out[0]
+ * are only guaranteed after the stream has finished).  Later work on the
+ * stream (the pack kernel) may still run, ordered on `stream` as usual.  Returns
  * GAANS_EHIP when the stream reports an error or drains without setting the
  * word.  Replaces the stream synchronisations of the reference's host code
  * (warp_ans_kernel_v2.cu:275-276, warp_div.py:63-65). */
