@@ -304,9 +304,70 @@ struct Tabs {
   uint32_t dense_first;    // first staged dense block
 };
 
+// Copy n 16-byte words global -> LDS with the whole workgroup, U loads in
+// flight per thread before their stores (slots past n re-copy word n - 1, so
+// nothing branches and the loads are issued together).
+template <int U>
+__device__ __forceinline__ void copy16(uint4* dst, const uint4* __restrict__ src, uint32_t n,
+                                       int tid) {
+  for (uint32_t b = tid; b < n; b += U * kThreads) {
+    uint4 v[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const uint32_t i = b + k * kThreads;
+      v[k] = src[i < n ? i : n - 1];
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const uint32_t i = b + k * kThreads;
+      dst[i < n ? i : n - 1] = v[k];
+    }
+  }
+}
+
+// One pass over the staged metadata (nt), entries (ne) and dense 16-byte
+// words (nd) with U loads of each kind in flight per thread before the
+// stores.  Indexes past a count re-copy its last item, so nothing branches
+// (the kinds are compile-time choices; counts are >= 1).
+template <bool kEnt, bool kEnt32, bool kDense>
+__device__ __forceinline__ void stage_pass(const Tabs& T, uint4* lmeta, uint2* lent,
+                                           uint32_t* lent32, uint4* ldense,
+                                           const uint4* __restrict__ dsrc, uint32_t nt,
+                                           uint32_t ne, uint32_t nd, uint32_t base0, int t_lo,
+                                           int tid) {
+  constexpr int U = 4;
+  uint32_t items = nt;
+  if (kEnt || kEnt32) items = items > ne ? items : ne;
+  if (kDense) items = items > nd ? items : nd;
+  for (uint32_t b = tid; b < items; b += U * kThreads) {
+    TabMeta mv[U];
+    uint2 ev[U];
+    uint4 dv[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const uint32_t i = b + k * kThreads;
+      mv[k] = T.gmeta[t_lo + (i < nt ? i : nt - 1)];
+      if (kEnt || kEnt32) ev[k] = T.gent[base0 + (i < ne ? i : ne - 1)];
+      if (kDense) dv[k] = dsrc[i < nd ? i : nd - 1];
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const uint32_t i = b + k * kThreads;
+      lmeta[i < nt ? i : nt - 1] =
+          make_uint4(mv[k].ent_base - base0, mv[k].nsym, (uint32_t)mv[k].offset, 0u);
+      if (kEnt) lent[i < ne ? i : ne - 1] = ev[k];
+      if (kEnt32) lent32[i < ne ? i : ne - 1] = ev[k].x;
+      if (kDense) ldense[i < nd ? i : nd - 1] = dv[k];
+    }
+  }
+}
+
 // Stage tables [t_lo, t_hi) of the blob into LDS (whole workgroup): the
-// encoder's metadata and entries (lent), or the decoder's metadata, entry
-// words 0 (lent32), lookups (llut) and dense blocks (ldense).
+// encoder's metadata and entries (lent), or the decoder's lookups (llut),
+// metadata, dense blocks (ldense) and, when dense blocks are staged, entry
+// words 0 (lent32).  The lookups, which need no metadata, are copied while
+// the metadata loads are in flight; lookups and dense blocks are 16-byte
+// aligned in the blob.
 __device__ void stage_tables(Tabs& T, uint4* lmeta, uint2* lent, uint32_t* lent32,
                              uint64_t* llut, uint8_t* ldense, uint32_t total_dense, uint32_t M,
                              int t_lo, int t_hi, int tid) {
@@ -314,28 +375,31 @@ __device__ void stage_tables(Tabs& T, uint4* lmeta, uint2* lent, uint32_t* lent3
   T.nt = t_hi > t_lo ? t_hi - t_lo : 0;
   T.dense_first = 0;
   if (T.nt > 0) {
+    const uint32_t nt = (uint32_t)T.nt;
     const uint32_t base0 = T.gmeta[t_lo].ent_base;
     const TabMeta last = T.gmeta[t_hi - 1];
-    const uint32_t n_ent = last.ent_base + last.nsym - base0;
-    for (int i = tid; i < T.nt; i += kThreads) {
-      const TabMeta m = T.gmeta[t_lo + i];
-      lmeta[i] = make_uint4(m.ent_base - base0, m.nsym, (uint32_t)m.offset, 0u);
-    }
-    if (lent)
-      for (uint32_t i = tid; i < n_ent; i += kThreads) lent[i] = T.gent[base0 + i];
-    if (lent32)
-      for (uint32_t i = tid; i < n_ent; i += kThreads) lent32[i] = T.gent[base0 + i].x;
-    if (llut) {
-      const uint64_t* src = T.glut + (int64_t)t_lo * kLutSize;  // luts are contiguous
-      for (int i = tid; i < T.nt * kLutSize; i += kThreads) llut[i] = src[i];
-    }
-    if (ldense) {
-      const uint32_t d0 = T.gmeta[t_lo].dense_base;
-      const uint32_t d1 = (uint32_t)t_hi < M ? T.gmeta[t_hi].dense_base : total_dense;
-      const uint32_t* src = reinterpret_cast<const uint32_t*>(T.gdense + (size_t)d0 * kLutSize);
-      uint32_t* dst = reinterpret_cast<uint32_t*>(ldense);
-      for (uint32_t i = tid; i < (d1 - d0) * (kLutSize / 4); i += kThreads) dst[i] = src[i];
-      T.dense_first = d0;
+    const uint32_t ne = last.ent_base + last.nsym - base0;
+    if (lent) {
+      stage_pass<true, false, false>(T, lmeta, lent, nullptr, nullptr, nullptr, nt, ne, 0u,
+                                     base0, t_lo, tid);
+    } else {
+      const uint4* lut_src = reinterpret_cast<const uint4*>(T.glut + (int64_t)t_lo * kLutSize);
+      copy16<4>(reinterpret_cast<uint4*>(llut), lut_src, nt * (kLutSize / 2), tid);
+      if (lent32) {
+        const uint32_t d0 = T.gmeta[t_lo].dense_base;
+        const uint32_t d1 = (uint32_t)t_hi < M ? T.gmeta[t_hi].dense_base : total_dense;
+        T.dense_first = d0;
+        // without dense blocks, the pass re-copies the first lookup word
+        const bool any = d1 > d0;
+        stage_pass<false, true, true>(
+            T, lmeta, nullptr, lent32,
+            any ? reinterpret_cast<uint4*>(ldense) : reinterpret_cast<uint4*>(llut),
+            any ? reinterpret_cast<const uint4*>(T.gdense + (size_t)d0 * kLutSize) : lut_src,
+            nt, ne, any ? (d1 - d0) * (kLutSize / 16) : 1u, base0, t_lo, tid);
+      } else {
+        stage_pass<false, false, false>(T, lmeta, nullptr, nullptr, nullptr, nullptr, nt, 1u,
+                                        0u, base0, t_lo, tid);
+      }
     }
   }
   __syncthreads();
@@ -1046,23 +1110,27 @@ __device__ __forceinline__ void dec_refill(bool need, uint32_t& x, Stream& S, co
 
 // Escape section of one chunk, read from the chunk's end: escape u32 m holds
 // the nibbles [8m, 8m + 8), nibble 8m + r at bits 4r; it is the stream's u32
-// n32 - 1 - m with its halves swapped.  The coder keeps escape u32s
-// [wb, wb + 128) in two registers across the wave and reads the entries in
+// n32 - 1 - m with its halves swapped.  The coder keeps the stream u32s of
+// escape u32s [wb, wb + 128) in two registers across the wave (loaded as
+// stored; swapped and range-checked when read) and reads the entries in
 // order with the nibble cursor q (both wave-uniform).
 struct Esc {
   const uint32_t* __restrict__ w32;   // the chunk's words after the states
   const uint32_t* __restrict__ safe;  // an in-bounds word of the chunk
   int n32, wb;
   uint32_t q;
-  uint32_t win0, win1;  // escape u32 wb + lane, wb + 64 + lane
+  uint32_t win0, win1;  // stored form of escape u32 wb + lane, wb + 64 + lane
 };
 
-// Escape u32 m; past the start of the chunk's words it reads as zero
-// (corrupt payloads only).
-__device__ __forceinline__ uint32_t esc_u32(const Esc& E, int m) {
-  const bool in = m < E.n32;
-  const uint32_t v = *(in ? E.w32 + (E.n32 - 1 - m) : E.safe);
-  return in ? ((v >> 16) | (v << 16)) : 0u;
+// Stored form of escape u32 m (any word of the chunk when m is out of range).
+__device__ __forceinline__ uint32_t esc_load(const Esc& E, int m) {
+  return *(m < E.n32 ? E.w32 + (E.n32 - 1 - m) : E.safe);
+}
+
+// Escape u32 m from its stored form v; past the start of the chunk's words it
+// reads as zero (corrupt payloads only).
+__device__ __forceinline__ uint32_t esc_value(const Esc& E, int m, uint32_t v) {
+  return m < E.n32 ? ((v >> 16) | (v << 16)) : 0u;
 }
 
 // Next entry of the escape section: its raw value (count n <= 8, else the
@@ -1073,11 +1141,13 @@ __device__ __forceinline__ uint32_t esc_next(Esc& E, uint32_t& status, int lane)
     E.win0 = E.win1;
     E.wb = uni(E.wb + kLanes);
     i -= kLanes;
-    E.win1 = esc_u32(E, E.wb + kLanes + lane);
+    E.win1 = esc_load(E, E.wb + kLanes + lane);
   }
-  const uint32_t a0 = __builtin_amdgcn_readlane(E.win0, i);
-  const uint32_t a1 = i + 1 < kLanes ? __builtin_amdgcn_readlane(E.win0, i + 1)
-                                     : __builtin_amdgcn_readlane(E.win1, 0);
+  const int m = E.wb + i;
+  const uint32_t a0 = esc_value(E, m, __builtin_amdgcn_readlane(E.win0, i));
+  const uint32_t a1 = esc_value(E, m + 1, i + 1 < kLanes
+                                              ? __builtin_amdgcn_readlane(E.win0, i + 1)
+                                              : __builtin_amdgcn_readlane(E.win1, 0));
   const uint64_t v = ((((uint64_t)a1) << 32) | a0) >> (4u * (E.q & 7u));
   uint32_t n = (uint32_t)v & 15u;
   if (n > 8u) {
@@ -1146,8 +1216,9 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
   uint8_t* tsm = smem + dec_fixed_lds(kLatents);
   uint64_t* llut = reinterpret_cast<uint64_t*>(tsm);
   uint4* lmeta = reinterpret_cast<uint4*>(tsm + 8 * kLutSize * a.nt_cap);
-  uint32_t* lent32 = reinterpret_cast<uint32_t*>(tsm + (8 * kLutSize + 16) * a.nt_cap);
-  uint8_t* ldense = tsm + (8 * kLutSize + 16) * a.nt_cap + 4 * a.ne_cap;
+  // [luts][meta][dense blocks][entry words 0]: every part 16-byte aligned
+  uint8_t* ldense = tsm + (8 * kLutSize + 16) * a.nt_cap;
+  uint32_t* lent32 = reinterpret_cast<uint32_t*>(ldense + (size_t)kLutSize * a.nd_cap);
 
   const int64_t g = blockIdx.x;
   const int tid = threadIdx.x;
@@ -1260,7 +1331,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
       S.q32 = S.q / 2;
       S.rp = 0;
       S.filled = 0;
-      x = lane < A ? reinterpret_cast<const uint32_t*>(cdata)[lane] : kStateLow;
+      x = reinterpret_cast<const uint32_t*>(cdata)[lane < A ? lane : 0];  // lane < A: below
 #pragma unroll
       for (int b = 0; b < kPre; ++b)
 #pragma unroll
@@ -1274,8 +1345,8 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
       E.n32 = S.q32;
       E.wb = 0;
       E.q = 0;
-      E.win0 = esc_u32(E, lane);
-      E.win1 = esc_u32(E, kLanes + lane);
+      E.win0 = esc_load(E, lane);
+      E.win1 = esc_load(E, kLanes + lane);
     } else if (nblk > 0) {
       load_block(0, cbx, cm);
       if (nblk > 1) load_block(1, nbx, nm);
@@ -1290,6 +1361,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
     // per wave) that meets at the same barriers: one before the first block
     // and one per block.
     if (wid == 0) {
+      x = lane < A ? x : kStateLow;
 #pragma unroll
       for (int b = 0; b < kPre; ++b)
 #pragma unroll
@@ -1355,7 +1427,8 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
         const uint16_t* s16 = reinterpret_cast<const uint16_t*>(S.s32);
         if (pad && s16[S.rp] != 0) status |= GAANS_ST_CORRUPT;
         if (E.q & 3u) {
-          const uint32_t last = esc_u32(E, (int)(E.q >> 3)) >> (4u * (E.q & 7u));
+          const int m = (int)(E.q >> 3);
+          const uint32_t last = esc_value(E, m, esc_load(E, m)) >> (4u * (E.q & 7u));
           if (last & ((1u << (4u * (4u - (E.q & 3u)))) - 1u)) status |= GAANS_ST_CORRUPT;
         }
       }
@@ -1652,7 +1725,7 @@ uint64_t fnv_u32(uint64_t h, uint32_t v) {
 int64_t tables_size(int32_t M, int64_t total_syms, int64_t total_dense) {
   int64_t o = sizeof(TabHdr);
   o += (int64_t)sizeof(TabMeta) * M;
-  o = align_up(o, 8) + 8 * total_syms;
+  o = align_up(align_up(o, 8) + 8 * total_syms, 16);
   o += 8ll * kLutSize * M;
   o += (int64_t)kLutSize * total_dense;
   return o;
@@ -1761,7 +1834,7 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
     total_dense += nd;
     if (nd > max_dense) max_dense = nd;
   }
-  const int64_t lut_off = ent_off + 8 * total;
+  const int64_t lut_off = align_up(ent_off + 8 * total, 16);
   uint64_t* lut = reinterpret_cast<uint64_t*>(o + lut_off);
   const int64_t dense_off = lut_off + 8ll * kLutSize * M;
   uint8_t* dense = o + dense_off;
