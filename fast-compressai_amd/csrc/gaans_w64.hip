@@ -1110,16 +1110,19 @@ __device__ __forceinline__ void dec_refill(bool need, uint32_t& x, Stream& S, co
 
 // Escape section of one chunk, read from the chunk's end: escape u32 m holds
 // the nibbles [8m, 8m + 8), nibble 8m + r at bits 4r; it is the stream's u32
-// n32 - 1 - m with its halves swapped.  The coder keeps the stream u32s of
-// escape u32s [wb, wb + 128) in two registers across the wave (loaded as
-// stored; swapped and range-checked when read) and reads the entries in
-// order with the nibble cursor q (both wave-uniform).
+// n32 - 1 - m with its halves swapped.  The coder holds escape u32s [0, 128)
+// (1,024 nibbles, swapped, zero past the chunk's words) in registers across
+// the wave, loaded once before the blocks: lane i of w0 / w1 holds u32 i /
+// 64 + i, of h0 / h1 u32 i + 1 / 65 + i, so an entry (at most 2 u32s) is two
+// readlanes at one index.  Entries past the window (sections that long are
+// rare) come through scalar loads.  No vector load is issued in the loop, so
+// reading an entry never waits on the stream prefetch.
 struct Esc {
   const uint32_t* __restrict__ w32;   // the chunk's words after the states
   const uint32_t* __restrict__ safe;  // an in-bounds word of the chunk
-  int n32, wb;
-  uint32_t q;
-  uint32_t win0, win1;  // stored form of escape u32 wb + lane, wb + 64 + lane
+  int n32;
+  uint32_t q;  // nibbles read
+  uint32_t w0, h0, w1, h1;
 };
 
 // Stored form of escape u32 m (any word of the chunk when m is out of range).
@@ -1127,27 +1130,46 @@ __device__ __forceinline__ uint32_t esc_load(const Esc& E, int m) {
   return *(m < E.n32 ? E.w32 + (E.n32 - 1 - m) : E.safe);
 }
 
-// Escape u32 m from its stored form v; past the start of the chunk's words it
-// reads as zero (corrupt payloads only).
+// Escape u32 m from its stored form v.
 __device__ __forceinline__ uint32_t esc_value(const Esc& E, int m, uint32_t v) {
   return m < E.n32 ? ((v >> 16) | (v << 16)) : 0u;
 }
 
+// Once the window loads (stored forms of u32 lane, 64 + lane in w0, w1) have
+// completed: swap, zero past the words, fill the companions.
+__device__ __forceinline__ void esc_window(Esc& E, int lane) {
+  E.w0 = esc_value(E, lane, E.w0);
+  E.w1 = esc_value(E, kLanes + lane, E.w1);
+  const uint32_t n0 = (uint32_t)__shfl_down((int)E.w0, 1, kLanes);
+  const uint32_t n1 = (uint32_t)__shfl_down((int)E.w1, 1, kLanes);
+  const uint32_t f1 = (uint32_t)__shfl((int)E.w1, 0, kLanes);
+  E.h0 = lane == kLanes - 1 ? f1 : n0;
+  E.h1 = lane == kLanes - 1 ? 0u : n1;  // u32 128 is read from memory
+}
+
+// The same u32 through a scalar load (wave-uniform m): the payload is
+// read-only for the whole kernel, so it can be read through the constant
+// address space.
+typedef const __attribute__((address_space(4))) uint32_t* const_u32_ptr;
+__device__ __forceinline__ uint32_t esc_u32_s(const Esc& E, int m) {
+  return esc_value(E, m, *(const_u32_ptr)(m < E.n32 ? E.w32 + (E.n32 - 1 - m) : E.safe));
+}
+
 // Next entry of the escape section: its raw value (count n <= 8, else the
 // chunk is corrupt).  Wave-uniform.
-__device__ __forceinline__ uint32_t esc_next(Esc& E, uint32_t& status, int lane) {
-  int i = uni((int)(E.q >> 3) - E.wb);  // 0 .. 65: an entry spans at most 2 u32s
-  if (i >= kLanes) {
-    E.win0 = E.win1;
-    E.wb = uni(E.wb + kLanes);
-    i -= kLanes;
-    E.win1 = esc_load(E, E.wb + kLanes + lane);
+__device__ __forceinline__ uint32_t esc_next(Esc& E, uint32_t& status) {
+  const int m = (int)(E.q >> 3);  // an entry spans at most 2 u32s
+  uint32_t a0, a1;
+  if (m < kLanes) {
+    a0 = __builtin_amdgcn_readlane(E.w0, m);
+    a1 = __builtin_amdgcn_readlane(E.h0, m);
+  } else if (m < 2 * kLanes - 1) {
+    a0 = __builtin_amdgcn_readlane(E.w1, m - kLanes);
+    a1 = __builtin_amdgcn_readlane(E.h1, m - kLanes);
+  } else {
+    a0 = esc_u32_s(E, m);
+    a1 = esc_u32_s(E, m + 1);
   }
-  const int m = E.wb + i;
-  const uint32_t a0 = esc_value(E, m, __builtin_amdgcn_readlane(E.win0, i));
-  const uint32_t a1 = esc_value(E, m + 1, i + 1 < kLanes
-                                              ? __builtin_amdgcn_readlane(E.win0, i + 1)
-                                              : __builtin_amdgcn_readlane(E.win1, 0));
   const uint64_t v = ((((uint64_t)a1) << 32) | a0) >> (4u * (E.q & 7u));
   uint32_t n = (uint32_t)v & 15u;
   if (n > 8u) {
@@ -1158,24 +1180,26 @@ __device__ __forceinline__ uint32_t esc_next(Esc& E, uint32_t& status, int lane)
   return (uint32_t)((v >> 4) & ((1ull << (4u * n)) - 1ull));
 }
 
-// Values of the escaping lanes em of one step (record r): each takes the next
-// entry of the escape section, in lane order.  v holds the lanes' values and
-// is updated for the escaping ones.
+// Values of the escaping lanes em of one step (record r, values v): each takes
+// the next entry of the escape section, in lane order; the mapping
+// (CompressAI's, reference warp_ans_kernel.cu:316-327) runs on the scalar unit
+// with the lane's escape bin and offset read from r.
 __device__ __forceinline__ void dec_escapes(uint64_t em, const uint4 r, uint32_t& v, Esc& E,
                                             uint32_t& status, int lane) {
-  const bool esc = (em >> lane) & 1ull;
-  uint32_t raw = 0;
+  uint32_t bad = 0;
   do {
     const int L = __ffsll((unsigned long long)em) - 1;
-    const uint32_t rv = esc_next(E, status, lane);
-    raw = lane == L ? rv : raw;
     em &= em - 1ull;
+    const uint32_t raw = esc_next(E, status);
+    const uint32_t maxv = __builtin_amdgcn_readlane(r.y, L);
+    const int32_t off = (int32_t)__builtin_amdgcn_readlane(r.z, L);
+    const int64_t ev = (raw & 1u) ? -(int64_t)(raw >> 1) - 1 : (int64_t)(raw >> 1) + maxv;
+    const int64_t sv = ev + off;
+    const bool oob = (sv < INT32_MIN) | (sv > INT32_MAX);
+    bad |= oob ? GAANS_ST_CORRUPT : 0u;
+    v = lane == L ? (oob ? 0u : (uint32_t)(int32_t)sv) : v;
   } while (em);
-  const int64_t ev = (raw & 1u) ? -(int64_t)(raw >> 1) - 1 : (int64_t)(raw >> 1) + r.y;
-  const int64_t sv = ev + (int32_t)r.z;
-  const bool oob = esc & ((sv < INT32_MIN) | (sv > INT32_MAX));
-  status |= oob ? GAANS_ST_CORRUPT : 0u;
-  v = esc ? (oob ? 0u : (uint32_t)(int32_t)sv) : v;
+  status |= bad;
 }
 
 // One decode step of the coder wave; returns the decoded value and, in em,
@@ -1343,10 +1367,9 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
       E.w32 = S.s32;
       E.safe = S.safe;
       E.n32 = S.q32;
-      E.wb = 0;
       E.q = 0;
-      E.win0 = esc_load(E, lane);
-      E.win1 = esc_load(E, kLanes + lane);
+      E.w0 = esc_load(E, lane);  // esc_window completes them after the staging
+      E.w1 = esc_load(E, kLanes + lane);
     } else if (nblk > 0) {
       load_block(0, cbx, cm);
       if (nblk > 1) load_block(1, nbx, nm);
@@ -1362,6 +1385,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
     // and one per block.
     if (wid == 0) {
       x = lane < A ? x : kStateLow;
+      esc_window(E, lane);
 #pragma unroll
       for (int b = 0; b < kPre; ++b)
 #pragma unroll
@@ -1427,8 +1451,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
         const uint16_t* s16 = reinterpret_cast<const uint16_t*>(S.s32);
         if (pad && s16[S.rp] != 0) status |= GAANS_ST_CORRUPT;
         if (E.q & 3u) {
-          const int m = (int)(E.q >> 3);
-          const uint32_t last = esc_value(E, m, esc_load(E, m)) >> (4u * (E.q & 7u));
+          const uint32_t last = esc_u32_s(E, (int)(E.q >> 3)) >> (4u * (E.q & 7u));
           if (last & ((1u << (4u * (4u - (E.q & 3u)))) - 1u)) status |= GAANS_ST_CORRUPT;
         }
       }
