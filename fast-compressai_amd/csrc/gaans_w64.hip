@@ -8,16 +8,19 @@
 // oracle (oracle/gaans_oracle.c).
 //
 // Work mapping: one workgroup per chunk (a coder wave and kMappers mapper
-// waves, 320 threads by default).
+// waves, 320 threads, for encode; one more wave, the escape reader, for
+// decode).
 //  - Wave 0 is the coder: it owns the 64 lane states and runs only the
 //    serial part of every step (renormalisation, ballot compaction, state
 //    update).
-//  - The other waves are mappers: one block of steps ahead of the coder they
-//    load symbols / indexes / latents from HBM (a block ahead again, so the
-//    loads are in flight while the previous block is mapped), look the
-//    tables up, split escapes, hash the indexes and write one 16-byte op
-//    record per lane and step into LDS; the decoder's mappers also store the
-//    decoded values a block behind.
+//  - The mappers: one block of steps ahead of the coder they load symbols /
+//    indexes / latents from HBM (a block ahead again, so the loads are in
+//    flight while the previous block is mapped), look the tables up, split
+//    escapes, hash the indexes and write one op record per lane and step
+//    into LDS (16 bytes for encode, 8 for decode); the decoder's mappers also
+//    store the decoded values a block behind.
+//  - The decoder's escape reader parses the chunk's escape section ahead of
+//    the coder into an LDS FIFO, so an escape costs the coder one LDS read.
 //  - The CDF tables of the chunk's channels (or all tables, when they are
 //    few) are staged in LDS by the whole workgroup; others are read through
 //    L1/L2.
@@ -66,22 +69,16 @@ constexpr int kLutSize = 1 << kLutBits;
 constexpr uint32_t kHashMul = 0x9E3779B9u;
 constexpr int kMaxEscNibbles = 9;  // escape count + 8 nibbles of raw
 
-// steps per block: the mappers' lead over the coder, and the steps between
-// two barriers
+// encoder steps per block: the mappers' lead over the coder, and the steps
+// between two barriers (the decoder's are a template parameter, DecGeom)
 #ifndef GAANS_ENC_SB
 #define GAANS_ENC_SB 4
 #endif
-#ifndef GAANS_DEC_SB
-#define GAANS_DEC_SB 8
-#endif
 constexpr int kEncSB = GAANS_ENC_SB;
-constexpr int kDecSB = GAANS_DEC_SB;
 constexpr int kEncPer = (kEncSB + kMappers - 1) / kMappers;  // steps per mapper wave and block
-constexpr int kDecPer = (kDecSB + kMappers - 1) / kMappers;
 // per-wave hash, status and escape nibbles, then the escape count
 constexpr int kPartBytes = (12 * kWaves + 4 + 15) / 16 * 16;
 constexpr int kRingWords = 4096;       // encoder LDS output ring (u16 words)
-constexpr int kStreamRing = 2048;      // decoder LDS stream ring (u16 words)
 constexpr int kPfU32 = 4;              // decoder stream prefetch: u32 per lane
 constexpr int kPfWords = 2 * kPfU32 * kLanes;
 constexpr int kMaxDevices = 64;
@@ -295,31 +292,32 @@ struct Tabs {
   const uint2* __restrict__ gent;
   const uint64_t* __restrict__ glut;
   const uint8_t* __restrict__ gdense;
-  const uint4* lmeta;      // {ent_base (LDS-local), nsym, offset, 0}
+  const uint4* lmeta;      // {ent_base (LDS-local), nsym, offset, ent_base (global)}
   const uint2* lent;       // encoder: both entry words
   const uint32_t* lent32;  // decoder: entry word 0
   const uint64_t* llut;    // nt x 256
   const uint8_t* ldense;
   int t_lo, nt;
   uint32_t dense_first;    // first staged dense block
+  bool dense_lds;          // decoder: dense blocks and entry words staged with the lookups
 };
 
-// Copy n 16-byte words global -> LDS with the whole workgroup, U loads in
-// flight per thread before their stores (slots past n re-copy word n - 1, so
-// nothing branches and the loads are issued together).
-template <int U>
+// Copy n 16-byte words global -> LDS with the whole workgroup (NT threads),
+// U loads in flight per thread before their stores (slots past n re-copy
+// word n - 1, so nothing branches and the loads are issued together).
+template <int NT, int U>
 __device__ __forceinline__ void copy16(uint4* dst, const uint4* __restrict__ src, uint32_t n,
                                        int tid) {
-  for (uint32_t b = tid; b < n; b += U * kThreads) {
+  for (uint32_t b = tid; b < n; b += U * NT) {
     uint4 v[U];
 #pragma unroll
     for (int k = 0; k < U; ++k) {
-      const uint32_t i = b + k * kThreads;
+      const uint32_t i = b + k * NT;
       v[k] = src[i < n ? i : n - 1];
     }
 #pragma unroll
     for (int k = 0; k < U; ++k) {
-      const uint32_t i = b + k * kThreads;
+      const uint32_t i = b + k * NT;
       dst[i < n ? i : n - 1] = v[k];
     }
   }
@@ -329,32 +327,34 @@ __device__ __forceinline__ void copy16(uint4* dst, const uint4* __restrict__ src
 // words (nd) with U loads of each kind in flight per thread before the
 // stores.  Indexes past a count re-copy its last item, so nothing branches
 // (the kinds are compile-time choices; counts are >= 1).
-template <bool kEnt, bool kEnt32, bool kDense>
+template <int NT, bool kEnt, bool kEnt32, bool kDense>
 __device__ __forceinline__ void stage_pass(const Tabs& T, uint4* lmeta, uint2* lent,
                                            uint32_t* lent32, uint4* ldense,
                                            const uint4* __restrict__ dsrc, uint32_t nt,
                                            uint32_t ne, uint32_t nd, uint32_t base0, int t_lo,
                                            int tid) {
-  constexpr int U = 4;
+  // loads in flight per thread and kind (fewer for the decoder's larger
+  // workgroup, whose waves keep more registers live across the staging)
+  constexpr int U = NT > kThreads ? 3 : 4;
   uint32_t items = nt;
   if (kEnt || kEnt32) items = items > ne ? items : ne;
   if (kDense) items = items > nd ? items : nd;
-  for (uint32_t b = tid; b < items; b += U * kThreads) {
+  for (uint32_t b = tid; b < items; b += U * NT) {
     TabMeta mv[U];
     uint2 ev[U];
     uint4 dv[U];
 #pragma unroll
     for (int k = 0; k < U; ++k) {
-      const uint32_t i = b + k * kThreads;
+      const uint32_t i = b + k * NT;
       mv[k] = T.gmeta[t_lo + (i < nt ? i : nt - 1)];
       if (kEnt || kEnt32) ev[k] = T.gent[base0 + (i < ne ? i : ne - 1)];
       if (kDense) dv[k] = dsrc[i < nd ? i : nd - 1];
     }
 #pragma unroll
     for (int k = 0; k < U; ++k) {
-      const uint32_t i = b + k * kThreads;
+      const uint32_t i = b + k * NT;
       lmeta[i < nt ? i : nt - 1] =
-          make_uint4(mv[k].ent_base - base0, mv[k].nsym, (uint32_t)mv[k].offset, 0u);
+          make_uint4(mv[k].ent_base - base0, mv[k].nsym, (uint32_t)mv[k].offset, mv[k].ent_base);
       if (kEnt) lent[i < ne ? i : ne - 1] = ev[k];
       if (kEnt32) lent32[i < ne ? i : ne - 1] = ev[k].x;
       if (kDense) ldense[i < nd ? i : nd - 1] = dv[k];
@@ -362,43 +362,45 @@ __device__ __forceinline__ void stage_pass(const Tabs& T, uint4* lmeta, uint2* l
   }
 }
 
-// Stage tables [t_lo, t_hi) of the blob into LDS (whole workgroup): the
-// encoder's metadata and entries (lent), or the decoder's lookups (llut),
-// metadata, dense blocks (ldense) and, when dense blocks are staged, entry
-// words 0 (lent32).  The lookups, which need no metadata, are copied while
-// the metadata loads are in flight; lookups and dense blocks are 16-byte
-// aligned in the blob.
+// Stage tables [t_lo, t_hi) of the blob into LDS (whole workgroup of NT
+// threads): the encoder's metadata and entries (lent), or the decoder's
+// lookups (llut), metadata and, when lent32 is given, dense blocks (ldense)
+// and entry words 0 (lent32).  The lookups, which need no metadata, are
+// copied while the metadata loads are in flight; lookups and dense blocks are
+// 16-byte aligned in the blob.
+template <int NT>
 __device__ void stage_tables(Tabs& T, uint4* lmeta, uint2* lent, uint32_t* lent32,
                              uint64_t* llut, uint8_t* ldense, uint32_t total_dense, uint32_t M,
                              int t_lo, int t_hi, int tid) {
   T.t_lo = t_lo;
   T.nt = t_hi > t_lo ? t_hi - t_lo : 0;
   T.dense_first = 0;
+  T.dense_lds = lent32 != nullptr;
   if (T.nt > 0) {
     const uint32_t nt = (uint32_t)T.nt;
     const uint32_t base0 = T.gmeta[t_lo].ent_base;
     const TabMeta last = T.gmeta[t_hi - 1];
     const uint32_t ne = last.ent_base + last.nsym - base0;
     if (lent) {
-      stage_pass<true, false, false>(T, lmeta, lent, nullptr, nullptr, nullptr, nt, ne, 0u,
-                                     base0, t_lo, tid);
+      stage_pass<NT, true, false, false>(T, lmeta, lent, nullptr, nullptr, nullptr, nt, ne, 0u,
+                                         base0, t_lo, tid);
     } else {
       const uint4* lut_src = reinterpret_cast<const uint4*>(T.glut + (int64_t)t_lo * kLutSize);
-      copy16<4>(reinterpret_cast<uint4*>(llut), lut_src, nt * (kLutSize / 2), tid);
+      copy16<NT, 4>(reinterpret_cast<uint4*>(llut), lut_src, nt * (kLutSize / 2), tid);
       if (lent32) {
         const uint32_t d0 = T.gmeta[t_lo].dense_base;
         const uint32_t d1 = (uint32_t)t_hi < M ? T.gmeta[t_hi].dense_base : total_dense;
         T.dense_first = d0;
         // without dense blocks, the pass re-copies the first lookup word
         const bool any = d1 > d0;
-        stage_pass<false, true, true>(
+        stage_pass<NT, false, true, true>(
             T, lmeta, nullptr, lent32,
             any ? reinterpret_cast<uint4*>(ldense) : reinterpret_cast<uint4*>(llut),
             any ? reinterpret_cast<const uint4*>(T.gdense + (size_t)d0 * kLutSize) : lut_src,
             nt, ne, any ? (d1 - d0) * (kLutSize / 16) : 1u, base0, t_lo, tid);
       } else {
-        stage_pass<false, false, false>(T, lmeta, nullptr, nullptr, nullptr, nullptr, nt, 1u,
-                                        0u, base0, t_lo, tid);
+        stage_pass<NT, false, false, false>(T, lmeta, nullptr, nullptr, nullptr, nullptr, nt,
+                                            1u, 0u, base0, t_lo, tid);
       }
     }
   }
@@ -681,7 +683,7 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
     tb.ldense = nullptr;
     int t_lo, t_hi;
     stage_range(a.nt_cap, a.stage_all, k, a.P, (int)a.M, t_lo, t_hi);
-    stage_tables(tb, lmeta, lent, nullptr, nullptr, nullptr, 0u, a.M, t_lo, t_hi, tid);
+    stage_tables<kThreads>(tb, lmeta, lent, nullptr, nullptr, nullptr, 0u, a.M, t_lo, t_hi, tid);
 
     // mapper wave w (1..kMappers) owns steps u = w - 1 + kMappers e of every block
     int32_t ca[kEncPer], cb[kEncPer], na[kEncPer], nb[kEncPer];
@@ -960,6 +962,21 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
 // Decoder
 // ============================================================================
 
+// Decode workgroup: wave 0 is the coder, waves 1..kMappers the mappers, the
+// last wave the escape reader.
+constexpr int kDecWaves = kMappers + 2;
+constexpr int kDecThreads = kDecWaves * kLanes;
+constexpr int kEscWave = kDecWaves - 1;
+// per wave: index hash, status, escape nibbles
+constexpr int kDecPartBytes = (12 * kDecWaves + 15) / 16 * 16;
+// control words: [1] escape entries available (set when the reader stops),
+// [2 + b] steps of block parity b whose tables are not all in LDS (bit per
+// step, set by the mappers), [4 + b] block parity b has escapes and [6 + b]
+// escape entries consumed before block parity b (set by the coder)
+constexpr int kDecCtlBytes = 32;
+constexpr uint32_t kNoSym = 0xffffu;  // record of a lane past the chunk end
+constexpr uint32_t kAllAvail = 0xffffffffu;
+
 struct DecArgs {
   const uint8_t* __restrict__ payload;
   int64_t payload_bytes;
@@ -977,24 +994,43 @@ struct DecArgs {
   uint32_t* __restrict__ status_out;
 };
 
-// Decoder LDS layout (bytes); the median buffer is there for latents only
-constexpr int kDecRingBytes = 2 * kStreamRing;
-constexpr int kDecRecBytes = 2 * kDecSB * kLanes * 16;
-constexpr int kDecInfoBytes = 2 * kDecSB * 4;
-constexpr int kDecMedBytes = 2 * kDecSB * kLanes * 4;
-constexpr int dec_fixed_lds(bool latents) {
-  return kDecRingBytes + kDecRecBytes + kDecInfoBytes + kPartBytes +
-         (latents ? kDecMedBytes : 0);
+// Decoder geometry for blocks of SB steps (the mappers' lead over the coder
+// and the steps between two barriers).
+template <int SB>
+struct DecGeom {
+  static constexpr int kPer = (SB + kMappers - 1) / kMappers;  // steps per mapper wave and block
+  static constexpr int kRing = SB >= 8 ? 2048 : 1024;          // stream ring (u16 words)
+  static constexpr int kLowWater = SB >= 8 ? 1024 : 512;
+  static constexpr int kPre = kLowWater / kPfWords;            // batches staged before block 0
+  static constexpr int kEscR = 2 * SB * kLanes;                // escape FIFO entries
+  static constexpr int kRingBytes = 2 * kRing;
+  static constexpr int kRecBytes = 2 * SB * kLanes * 8;
+  static constexpr int kEscBytes = 4 * kEscR;
+  static constexpr int kMedBytes = 2 * SB * kLanes * 4;
+  // per step of two blocks: escaping lanes (u64) and the first entry's ordinal
+  static constexpr int kEscInfoBytes = 2 * SB * 16;
+  // [ring][records][escape FIFO][medians (latents)][escape steps][parts][control]
+  static constexpr int fixed(bool latents) {
+    return kRingBytes + kRecBytes + kEscBytes + (latents ? kMedBytes : 0) + kEscInfoBytes +
+           kDecPartBytes + kDecCtlBytes;
+  }
+  static_assert(kLowWater >= SB * kLanes && kLowWater + kPfWords <= kRing && kPre >= 1,
+                "decoder stream ring too small");
+  static_assert((kDecPartBytes + kDecCtlBytes) % 16 == 0, "LDS parts 16-byte aligned");
+};
+
+int dec_fixed_lds(bool latents, int sb) {
+  return sb >= 8 ? DecGeom<8>::fixed(latents) : DecGeom<4>::fixed(latents);
 }
 
-// Mapper record of one lane and step (16 bytes), tables in LDS when the
-// step's flag is 1:
-//   x: the lane's table (LDS-local or global index)
-//   y: escape symbol (nsym - 1), or 0xffffffff for a lane past the chunk end
-//   z: table offset            w: first entry of the table
+// Mapper record of one lane and step (8 bytes), tables in LDS when the step's
+// flag is 1:
+//   x: the lane's table (LDS-local or global index) | escape symbol << 16
+//      (nsym - 1; kNoSym for a lane past the chunk end)
+//   y: table offset
 // The coder overwrites x with the decoded value.
 template <bool kImplicit>
-__device__ __forceinline__ uint4 dec_record(const DecArgs& a, const Tabs& tb, int lane, int t,
+__device__ __forceinline__ uint2 dec_record(const DecArgs& a, const Tabs& tb, int lane, int t,
                                             int len, int32_t start, int32_t in_b,
                                             uint32_t& hash, uint32_t& status, bool& all_lds) {
   const int p = lane + kLanes * t;
@@ -1007,34 +1043,32 @@ __device__ __forceinline__ uint4 dec_record(const DecArgs& a, const Tabs& tb, in
   hash += ok ? ((uint32_t)(tbi + 1) ^ ((uint32_t)p * kHashMul)) : 0u;
   const bool staged = (uint32_t)(tbi - tb.t_lo) < (uint32_t)tb.nt;
   all_lds = ballot(!staged) == 0;
-  uint32_t nsym, ebase;
-  int32_t offset;
-  if (all_lds) {
+  uint32_t nsym, offset;
+  if (all_lds) {  // separate loads per memory, as in dec_lookup
     const uint4 lm = tb.lmeta[tbi - tb.t_lo];
-    ebase = lm.x;
     nsym = lm.y;
-    offset = (int32_t)lm.z;
+    offset = lm.z;
+    asm volatile("" : "+v"(nsym), "+v"(offset));
   } else {
     const TabMeta gm = tb.gmeta[tbi];
-    ebase = gm.ent_base;
     nsym = gm.nsym;
-    offset = gm.offset;
+    offset = (uint32_t)gm.offset;
+    asm volatile("" : "+v"(nsym), "+v"(offset));
   }
-  uint4 r;
-  r.x = (uint32_t)(all_lds ? tbi - tb.t_lo : tbi);
-  r.y = act ? nsym - 1u : 0xffffffffu;
-  r.z = (uint32_t)offset;
-  r.w = ebase;
+  uint2 r;
+  r.x = (uint32_t)(all_lds ? tbi - tb.t_lo : tbi) | ((act ? nsym - 1u : kNoSym) << 16);
+  r.y = offset;
   return r;
 }
 
-// cum -> (symbol, start, freq).  One lookup resolves every bucket in which at
-// most one other symbol starts; a dense bucket (marker 0xffff) reads the
-// symbol from its dense block and then the symbol's entry.
+// cum -> (symbol, start, freq) in table t.  One lookup resolves every bucket
+// in which at most one other symbol starts; a dense bucket (marker 0xffff)
+// reads the symbol from its dense block and then the symbol's entry (LDS when
+// the dense blocks are staged, else global memory).
 template <bool kLds>
-__device__ __forceinline__ void dec_lookup(const Tabs& tb, const uint4 r, uint32_t cum, bool act,
+__device__ __forceinline__ void dec_lookup(const Tabs& tb, uint32_t t, uint32_t cum, bool act,
                                            uint32_t& s, uint32_t& st, uint32_t& fr) {
-  const uint32_t li = (r.x << kLutBits) + (cum >> (16 - kLutBits));
+  const uint32_t li = (t << kLutBits) + (cum >> (16 - kLutBits));
   const uint64_t e = kLds ? tb.llut[li] : tb.glut[li];
   const uint32_t lo = (uint32_t)e, hi = (uint32_t)(e >> 32);
   const uint32_t s0 = hi & 0xffffu, nxt = hi >> 16;
@@ -1047,27 +1081,34 @@ __device__ __forceinline__ void dec_lookup(const Tabs& tb, const uint4 r, uint32
   st = up ? st0 + fr0 : st0;
   fr = up ? nxt + 1u : fr0;
   if (__builtin_expect(dm != 0ull, 0) && (act & (nxt == 0xffffu))) {
-    const uint32_t blk = kLds ? lo - tb.dense_first : lo;
-    const uint32_t di = (blk << kLutBits) + (cum & (kLutSize - 1));
-    s = s0 + (uint32_t)(kLds ? tb.ldense[di] : tb.gdense[di]);
-    const uint32_t en = kLds ? tb.lent32[r.w + s] : tb.gent[r.w + s].x;
+    const uint32_t ci = cum & (kLutSize - 1);
+    uint32_t en;
+    // separate loads per memory (the asm keeps the compiler from merging them
+    // into one generic load, which would also wait for the stream prefetch)
+    if (kLds && tb.dense_lds) {
+      s = s0 + (uint32_t)tb.ldense[((lo - tb.dense_first) << kLutBits) + ci];
+      en = tb.lent32[tb.lmeta[t].x + s];
+      asm volatile("" : "+v"(en));
+    } else {
+      s = s0 + (uint32_t)tb.gdense[((size_t)lo << kLutBits) + ci];
+      const uint32_t eb = kLds ? tb.lmeta[t].w : tb.gmeta[t].ent_base;
+      en = tb.gent[eb + s].x;
+      asm volatile("" : "+v"(en));
+    }
     st = en & 0xffffu;
     fr = (en >> 16) + 1u;
   }
 }
 
 // Word stream of one chunk: prefetched from HBM into registers (kPfWords words
-// ahead) and copied into an LDS ring holding the words [rp, filled)
-// (positions mod kStreamRing), kPfWords words at a time.  At the start of
-// every block the coder commits the batch prefetched into registers (pf,
+// ahead) and copied into an LDS ring of kRing words holding the words
+// [rp, filled) (positions mod kRing), kPfWords words at a time.  At the start
+// of every block the coder commits the batch prefetched into registers (pf,
 // words [filled, filled + kPfWords)) when fewer than kLowWater words are
 // buffered, then prefetches the next batch.  This is the only place pf is
 // loaded, so the loads stay in flight between blocks.  A step refills at most
-// one word per lane, and a block starts with at least kDecSB * kLanes
-// buffered words, so refills need no check.
-constexpr int kLowWater = 1024;
-static_assert(kLowWater >= kDecSB * kLanes && kLowWater + kPfWords <= kStreamRing,
-              "decoder stream ring too small");
+// one word per lane, and a block starts with at least SB * kLanes buffered
+// words, so refills need no check.
 struct Stream {
   const uint32_t* __restrict__ s32;
   const uint32_t* __restrict__ safe;  // an in-bounds word of the chunk
@@ -1083,12 +1124,14 @@ __device__ __forceinline__ uint32_t stream_word32(const Stream& S, int i32) {
 }
 
 // Block start: commit pf if needed, then fetch the next batch.
+template <int SB>
 __device__ __forceinline__ void stream_block_start(Stream& S, uint32_t* ring32, int lane) {
-  const bool commit = S.filled - S.rp < kLowWater && S.filled < S.q;
+  using G = DecGeom<SB>;
+  const bool commit = S.filled - S.rp < G::kLowWater && S.filled < S.q;
   if (commit) {
 #pragma unroll
     for (int kk = 0; kk < kPfU32; ++kk)
-      ring32[((S.filled >> 1) + kk * kLanes + lane) & (kStreamRing / 2 - 1)] = S.pf[kk];
+      ring32[((S.filled >> 1) + kk * kLanes + lane) & (G::kRing / 2 - 1)] = S.pf[kk];
     S.filled = uni(S.filled + kPfWords);
 #pragma unroll
     for (int kk = 0; kk < kPfU32; ++kk)
@@ -1098,11 +1141,12 @@ __device__ __forceinline__ void stream_block_start(Stream& S, uint32_t* ring32, 
 
 // A refill past the stream end reads stale ring words; the chunk is then
 // marked corrupt by the final check that exactly the stream was consumed.
+template <int SB>
 __device__ __forceinline__ void dec_refill(bool need, uint32_t& x, Stream& S, const uint16_t* ring,
                                            int lane) {
   const uint64_t m = ballot(need);
   // every lane reads (no branch around the read); only refilling lanes keep it
-  const uint32_t w = ring[(S.rp + (int)lane_rank(m)) & (kStreamRing - 1)];
+  const uint32_t w = ring[(S.rp + (int)lane_rank(m)) & (DecGeom<SB>::kRing - 1)];
   asm volatile("" ::"v"(w));
   x = need ? ((x << 16) | w) : x;
   S.rp += __popcll(m);
@@ -1110,134 +1154,159 @@ __device__ __forceinline__ void dec_refill(bool need, uint32_t& x, Stream& S, co
 
 // Escape section of one chunk, read from the chunk's end: escape u32 m holds
 // the nibbles [8m, 8m + 8), nibble 8m + r at bits 4r; it is the stream's u32
-// n32 - 1 - m with its halves swapped.  The coder holds escape u32s [0, 128)
-// (1,024 nibbles, swapped, zero past the chunk's words) in registers across
-// the wave, loaded once before the blocks: lane i of w0 / w1 holds u32 i /
-// 64 + i, of h0 / h1 u32 i + 1 / 65 + i, so an entry (at most 2 u32s) is two
-// readlanes at one index.  Entries past the window (sections that long are
-// rare) come through scalar loads.  No vector load is issued in the loop, so
-// reading an entry never waits on the stream prefetch.
-struct Esc {
+// n32 - 1 - m with its halves swapped.  An entry is a count n then n nibbles
+// of raw, and n is the minimal count of raw (raw ? msb(raw) / 4 + 1 : 0).
+//
+// The coder only marks escapes: per step, the escaping lanes and the ordinal
+// of the step's first entry.  The mapper that stores the block (during the
+// next block) resolves the values from an LDS FIFO of kEscR = 2 SB kLanes
+// raw values (entry e in slot e mod kEscR), which the escape reader (the
+// workgroup's last wave) fills in order: during block j it parses up to
+// c_j + SB kLanes entries, c_j being the entries consumed before block j
+// (published by the coder before the barrier).  Block j consumes at most
+// SB kLanes entries, so its entries are there when block j is stored, and
+// the entries written during block j (ordinals in [c_j, c_j + SB kLanes))
+// never share a slot with those of block j - 1 that the mappers read then
+// (ordinals in [c_j - SB kLanes, c_j)).  The reader stops at the first
+// invalid entry (count > 8 or not minimal) or at the end of the chunk's
+// words, and publishes how many entries are valid; resolving more marks the
+// chunk corrupt.
+//
+// The reader holds escape u32s [base, base + 128) in registers (lane i of w0
+// / w1: u32 base + i / base + 64 + i) and parses 64 nibble positions at a
+// time: lane l decodes the entry that would start at nibble q + l (count,
+// raw value, length, validity), then a scalar walk from q over the lengths
+// marks the real entry starts, and the marked lanes write their raw values
+// to the FIFO in one store.
+struct EscReader {
   const uint32_t* __restrict__ w32;   // the chunk's words after the states
   const uint32_t* __restrict__ safe;  // an in-bounds word of the chunk
-  int n32;
-  uint32_t q;  // nibbles read
-  uint32_t w0, h0, w1, h1;
+  int n32, base;
+  uint32_t q, p;     // nibbles and entries parsed
+  bool stopped;
+  uint32_t w0, w1;   // window
 };
 
-// Stored form of escape u32 m (any word of the chunk when m is out of range).
-__device__ __forceinline__ uint32_t esc_load(const Esc& E, int m) {
-  return *(m < E.n32 ? E.w32 + (E.n32 - 1 - m) : E.safe);
-}
-
-// Escape u32 m from its stored form v.
-__device__ __forceinline__ uint32_t esc_value(const Esc& E, int m, uint32_t v) {
+// Escape u32 m (zero past the chunk's words).
+__device__ __forceinline__ uint32_t esc_word(const EscReader& E, int m) {
+  const uint32_t v = *(m < E.n32 ? E.w32 + (E.n32 - 1 - m) : E.safe);
   return m < E.n32 ? ((v >> 16) | (v << 16)) : 0u;
 }
 
-// Once the window loads (stored forms of u32 lane, 64 + lane in w0, w1) have
-// completed: swap, zero past the words, fill the companions.
-__device__ __forceinline__ void esc_window(Esc& E, int lane) {
-  E.w0 = esc_value(E, lane, E.w0);
-  E.w1 = esc_value(E, kLanes + lane, E.w1);
-  const uint32_t n0 = (uint32_t)__shfl_down((int)E.w0, 1, kLanes);
-  const uint32_t n1 = (uint32_t)__shfl_down((int)E.w1, 1, kLanes);
-  const uint32_t f1 = (uint32_t)__shfl((int)E.w1, 0, kLanes);
-  E.h0 = lane == kLanes - 1 ? f1 : n0;
-  E.h1 = lane == kLanes - 1 ? 0u : n1;  // u32 128 is read from memory
+// Escape u32 base + i of the window for lane-varying i in [0, 128).
+__device__ __forceinline__ uint32_t esc_window_word(const EscReader& E, int i) {
+  const int addr = (i & (kLanes - 1)) << 2;
+  const uint32_t a = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)E.w0);
+  const uint32_t b = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)E.w1);
+  return i < kLanes ? a : b;
 }
 
-// The same u32 through a scalar load (wave-uniform m): the payload is
-// read-only for the whole kernel, so it can be read through the constant
-// address space.
-typedef const __attribute__((address_space(4))) uint32_t* const_u32_ptr;
-__device__ __forceinline__ uint32_t esc_u32_s(const Esc& E, int m) {
-  return esc_value(E, m, *(const_u32_ptr)(m < E.n32 ? E.w32 + (E.n32 - 1 - m) : E.safe));
-}
-
-// Next entry of the escape section: its raw value (count n <= 8, else the
-// chunk is corrupt).  Wave-uniform.
-__device__ __forceinline__ uint32_t esc_next(Esc& E, uint32_t& status) {
-  const int m = (int)(E.q >> 3);  // an entry spans at most 2 u32s
-  uint32_t a0, a1;
-  if (m < kLanes) {
-    a0 = __builtin_amdgcn_readlane(E.w0, m);
-    a1 = __builtin_amdgcn_readlane(E.h0, m);
-  } else if (m < 2 * kLanes - 1) {
-    a0 = __builtin_amdgcn_readlane(E.w1, m - kLanes);
-    a1 = __builtin_amdgcn_readlane(E.h1, m - kLanes);
-  } else {
-    a0 = esc_u32_s(E, m);
-    a1 = esc_u32_s(E, m + 1);
+// Parse entries until `target` are available or the section ends.
+template <int R>
+__device__ void esc_parse(EscReader& E, uint32_t target, uint32_t* fifo, uint32_t* ctl,
+                          int lane) {
+  const uint32_t qmax = 8u * (uint32_t)E.n32;
+  while (!E.stopped && E.p < target) {
+    // the 64 positions' entries lie in u32s [q >> 3, (q >> 3) + 10)
+    while ((int)(E.q >> 3) + 10 > E.base + 2 * kLanes) {
+      E.base += kLanes;
+      E.w0 = E.w1;
+      E.w1 = esc_word(E, E.base + kLanes + lane);
+    }
+    const uint32_t pos = E.q + (uint32_t)lane;
+    const int i = (int)(pos >> 3) - E.base;
+    const uint64_t v = (((uint64_t)esc_window_word(E, i + 1) << 32) | esc_window_word(E, i)) >>
+                       (4u * (pos & 7u));
+    const uint32_t n = (uint32_t)v & 15u;
+    const uint32_t raw = (uint32_t)((v >> 4) & ((1ull << (4u * n)) - 1ull));
+    const uint32_t top = (uint32_t)(v >> (4u * n)) & 15u;  // raw's last nibble
+    // a valid entry: count <= 8, minimal (last nibble non-zero), inside the words
+    const bool valid = n <= 8u && (n == 0u || top != 0u) && pos + 1u + n <= qmax;
+    const uint64_t vm = ballot(valid);
+    const uint32_t len = 1u + n;
+    uint64_t starts = 0;
+    uint32_t at = 0, cnt = 0;
+    const uint32_t want = target - E.p;
+    while (at < (uint32_t)kLanes && cnt < want) {
+      if (!((vm >> at) & 1ull)) {
+        E.stopped = true;
+        break;
+      }
+      starts |= 1ull << at;
+      ++cnt;
+      at += (uint32_t)__builtin_amdgcn_readlane((int)len, (int)at);
+    }
+    if ((starts >> lane) & 1ull) fifo[(E.p + lane_rank(starts)) & (R - 1)] = raw;
+    E.p += cnt;
+    E.q += at;
   }
-  const uint64_t v = ((((uint64_t)a1) << 32) | a0) >> (4u * (E.q & 7u));
-  uint32_t n = (uint32_t)v & 15u;
-  if (n > 8u) {
-    status |= GAANS_ST_CORRUPT;
-    n = 0;
-  }
-  E.q = (uint32_t)uni((int)(E.q + 1u + n));
-  return (uint32_t)((v >> 4) & ((1ull << (4u * n)) - 1ull));
+  if (E.stopped && lane == 0) ctl[1] = E.p;
 }
 
-// Values of the escaping lanes em of one step (record r, values v): each takes
-// the next entry of the escape section, in lane order; the mapping
-// (CompressAI's, reference warp_ans_kernel.cu:316-327) runs on the scalar unit
-// with the lane's escape bin and offset read from r.
-__device__ __forceinline__ void dec_escapes(uint64_t em, const uint4 r, uint32_t& v, Esc& E,
+// Values of the escaping lanes em of one step, decoded by the coder as the
+// escape bin: lane L takes FIFO entry base + (escaping lanes below L), with
+// CompressAI's mapping (reference warp_ans_kernel.cu:316-327): raw odd ->
+// -(raw >> 1) - 1, even -> (raw >> 1) + escape symbol, plus the table offset.
+// v holds escape symbol + offset mod 2^32 (the coder's value for the bin),
+// off the offset.  enib counts the lane's escape nibbles (1 + n per entry).
+template <int R>
+__device__ __forceinline__ void esc_resolve(uint64_t em, uint32_t base, uint32_t off, uint32_t& v,
+                                            uint32_t avail, const uint32_t* fifo, uint32_t& enib,
                                             uint32_t& status, int lane) {
-  uint32_t bad = 0;
-  do {
-    const int L = __ffsll((unsigned long long)em) - 1;
-    em &= em - 1ull;
-    const uint32_t raw = esc_next(E, status);
-    const uint32_t maxv = __builtin_amdgcn_readlane(r.y, L);
-    const int32_t off = (int32_t)__builtin_amdgcn_readlane(r.z, L);
-    const int64_t ev = (raw & 1u) ? -(int64_t)(raw >> 1) - 1 : (int64_t)(raw >> 1) + maxv;
-    const int64_t sv = ev + off;
-    const bool oob = (sv < INT32_MIN) | (sv > INT32_MAX);
-    bad |= oob ? GAANS_ST_CORRUPT : 0u;
-    v = lane == L ? (oob ? 0u : (uint32_t)(int32_t)sv) : v;
-  } while (em);
-  status |= bad;
+  const bool e = (em >> lane) & 1ull;
+  const uint32_t idx = base + lane_rank(em);
+  const uint32_t raw = fifo[idx & (R - 1)];
+  const uint32_t maxv = v - off;  // the escape symbol (exact: it is below 2^16)
+  const int64_t sv = (int64_t)(int32_t)off +
+                     ((raw & 1u) ? -(int64_t)(raw >> 1) - 1 : (int64_t)maxv + (raw >> 1));
+  const bool bad = e & ((idx >= avail) | (sv < INT32_MIN) | (sv > INT32_MAX));
+  status |= bad ? GAANS_ST_CORRUPT : 0u;
+  v = e ? (bad ? 0u : (uint32_t)(int32_t)sv) : v;
+  enib += e ? (raw ? ((31u - (uint32_t)__clz((int)raw)) >> 2) + 2u : 1u) : 0u;
 }
 
 // One decode step of the coder wave; returns the decoded value and, in em,
-// the lanes that decoded the escape bin (their values are set afterwards by
-// dec_escapes, off the state chain).  kFull: every lane is active and no
-// offset can overflow with a symbol index.
-template <bool kLds, bool kFull>
-__device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint4 r, uint32_t& x,
+// the lanes that decoded the escape bin (their values are resolved by the
+// mappers, off the state chain).  kFull: every lane is active and no offset
+// can overflow with a symbol index.
+template <bool kLds, bool kFull, int SB>
+__device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint2 r, uint32_t& x,
                                              Stream& S, const uint16_t* ring, uint64_t& em,
                                              uint32_t& status, int lane) {
-  const bool act = kFull || r.y != 0xffffffffu;
+  const uint32_t es = r.x >> 16;
+  const bool act = kFull || es != kNoSym;
   const uint32_t cum = x & 0xffffu;
   uint32_t s, st, fr;
-  dec_lookup<kLds>(tb, r, cum, act, s, st, fr);
+  dec_lookup<kLds>(tb, r.x & 0xffffu, cum, act, s, st, fr);
   const uint32_t xn = __umul24(fr, x >> 16) + cum - st;
   x = act ? xn : x;
-  dec_refill(act & (x < kStateLow), x, S, ring, lane);
+  dec_refill<SB>(act & (x < kStateLow), x, S, ring, lane);
   // value + offset for an ordinary symbol: s < 2^16, so the int32 sum overflows
   // exactly when it wraps below the offset
-  const int32_t o = (int32_t)(s + r.z);
-  const bool esc = act & (s == r.y);
+  const int32_t o = (int32_t)(s + r.y);
+  const bool esc = act & (s == es);
   em = ballot(esc);
-  const bool oob = act & !esc & !kFull & (o < (int32_t)r.z);
+  const bool oob = act & !esc & !kFull & (o < (int32_t)r.y);
   status |= oob ? GAANS_ST_CORRUPT : 0u;
   return (uint32_t)(oob ? 0 : o);
 }
 
-template <bool kLatents, bool kImplicit>
-__global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
+template <bool kLatents, bool kImplicit, int SB>
+__global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
+  using G = DecGeom<SB>;
+  constexpr int kPer = G::kPer;
+  constexpr int R = G::kEscR;
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t* sring = reinterpret_cast<uint16_t*>(smem);
   uint32_t* sring32 = reinterpret_cast<uint32_t*>(smem);
-  uint4* recs = reinterpret_cast<uint4*>(smem + kDecRingBytes);
-  uint32_t* info = reinterpret_cast<uint32_t*>(smem + kDecRingBytes + kDecRecBytes);
-  uint32_t* part = info + 2 * kDecSB;  // per-wave hash [0, kWaves) and status [kWaves, 2 kWaves)
-  float* med = reinterpret_cast<float*>(smem + kDecRingBytes + kDecRecBytes + kDecInfoBytes +
-                                        kPartBytes);
-  uint8_t* tsm = smem + dec_fixed_lds(kLatents);
+  uint2* recs = reinterpret_cast<uint2*>(smem + G::kRingBytes);
+  uint32_t* fifo = reinterpret_cast<uint32_t*>(smem + G::kRingBytes + G::kRecBytes);
+  uint8_t* after_fifo = smem + G::kRingBytes + G::kRecBytes + G::kEscBytes;
+  float* med = reinterpret_cast<float*>(after_fifo);
+  uint4* escm = reinterpret_cast<uint4*>(after_fifo + (kLatents ? G::kMedBytes : 0));
+  uint32_t* part = reinterpret_cast<uint32_t*>(escm + 2 * SB);
+  uint32_t* ctl = part + kDecPartBytes / 4;
+  uint8_t* tsm = smem + G::fixed(kLatents);
   uint64_t* llut = reinterpret_cast<uint64_t*>(tsm);
   uint4* lmeta = reinterpret_cast<uint4*>(tsm + 8 * kLutSize * a.nt_cap);
   // [luts][meta][dense blocks][entry words 0]: every part 16-byte aligned
@@ -1248,7 +1317,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & (kLanes - 1);
   const int wid = uni(tid >> 6);  // wave role, kept in a scalar register
-  uint32_t status = 0, hash = 0;
+  uint32_t status = 0, hash = 0, enib = 0;
   const uint32_t* __restrict__ hdr = reinterpret_cast<const uint32_t*>(a.payload);
   const TabHdr* th = reinterpret_cast<const TabHdr*>(a.tables);
   bool ok = true;  // uniform over the workgroup
@@ -1268,7 +1337,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
   chunk_range(g, a.K, a.N, (int32_t)a.chunk_len, row, start, len, k);
   const int T = (len + kLanes - 1) / kLanes;
   const int A = len < kLanes ? len : kLanes;
-  const int nblk = (T + kDecSB - 1) / kDecSB;
+  const int nblk = (T + SB - 1) / SB;
   uint32_t beg = 0, endo = 0, want_hash = 0;
   int64_t cb = 0;
   if (ok) {
@@ -1282,6 +1351,9 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
       ok = false;
     }
   }
+  Stream S;  // the coder's; its final position is checked after the last barrier
+  S.rp = 0;
+  S.q = 0;
   if (ok) {
     Tabs tb;
     tb.gmeta = reinterpret_cast<const TabMeta*>(a.tables + th->meta_off);
@@ -1295,166 +1367,187 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
     tb.llut = llut;
     tb.ldense = ldense;
     const uint8_t* cdata = a.payload + a.header_bytes + beg;
+    const uint32_t* s32 = reinterpret_cast<const uint32_t*>(cdata + 4 * A);
+    const uint32_t* safe = reinterpret_cast<const uint32_t*>(cdata);
+    const int q16 = (int)((cb - 4 * A) / 2);  // u16 words after the states (even)
 
-    int32_t cbx[kDecPer], nbx[kDecPer];
-    float cm[kDecPer], nm[kDecPer];
+    int32_t cbx[kPer], nbx[kPer];
+    float cm[kPer], nm[kPer];
     auto load_block = [&](int j, int32_t* ib, float* im) {
 #pragma unroll
-      for (int e = 0; e < kDecPer; ++e) {
+      for (int e = 0; e < kPer; ++e) {
         const int u = (wid - 1) + kMappers * e;
-        if (kDecSB % kMappers != 0 && u >= kDecSB) break;
-        int p = lane + kLanes * (j * kDecSB + u);
+        if (SB % kMappers != 0 && u >= SB) break;
+        int p = lane + kLanes * (j * SB + u);
         p = p < len ? p : len - 1;  // loads stay in the chunk; results are masked
         ib[e] = kImplicit ? 0 : a.indexes[row + start + p];
         im[e] = kLatents ? a.medians[udiv((uint32_t)(start + p), a.div_hw)] : 0.0f;
       }
     };
-    auto store_block = [&](int j) {  // decoded values of block j -> HBM
-      const uint4* src = recs + (j & 1) * kDecSB * kLanes;
+    // decoded values of block j -> HBM, escapes resolved first
+    auto store_block = [&](int j) {
+      const uint2* src = recs + (j & 1) * SB * kLanes;
+      const bool any_esc = uni((int)ctl[4 + (j & 1)]) != 0;
+      const uint32_t avail = (uint32_t)uni((int)ctl[1]);
 #pragma unroll
-      for (int e = 0; e < kDecPer; ++e) {
+      for (int e = 0; e < kPer; ++e) {
         const int u = (wid - 1) + kMappers * e;
-        if (kDecSB % kMappers != 0 && u >= kDecSB) break;
-        const uint32_t v = src[u * kLanes + lane].x;
-        const int p = lane + kLanes * (j * kDecSB + u);
+        if (SB % kMappers != 0 && u >= SB) break;
+        const uint2 r = src[u * kLanes + lane];
+        uint32_t v = r.x;
+        if (any_esc && j * SB + u < T) {
+          const uint4 ei = escm[(j & 1) * SB + u];  // escaping lanes, first entry
+          const uint64_t em = (uint64_t)(uint32_t)uni((int)ei.x) |
+                              ((uint64_t)(uint32_t)uni((int)ei.y) << 32);
+          if (em) esc_resolve<R>(em, (uint32_t)uni((int)ei.z), r.y, v, avail, fifo, enib, status,
+                                 lane);
+        }
+        const int p = lane + kLanes * (j * SB + u);
         if (p < len) {
           const int64_t i = row + start + p;
           if (kLatents)
-            a.out_y[i] = __fadd_rn((float)(int32_t)v, med[((j & 1) * kDecSB + u) * kLanes + lane]);
+            a.out_y[i] = __fadd_rn((float)(int32_t)v, med[((j & 1) * SB + u) * kLanes + lane]);
           else a.out_sym[i] = (int32_t)v;
         }
       }
     };
     auto map_block = [&](int j) {
-      uint4* dst = recs + (j & 1) * kDecSB * kLanes;
+      uint2* dst = recs + (j & 1) * SB * kLanes;
 #pragma unroll
-      for (int e = 0; e < kDecPer; ++e) {
+      for (int e = 0; e < kPer; ++e) {
         const int u = (wid - 1) + kMappers * e;
-        if (kDecSB % kMappers != 0 && u >= kDecSB) break;
+        if (SB % kMappers != 0 && u >= SB) break;
         bool all_lds;
-        const uint4 r = dec_record<kImplicit>(a, tb, lane, j * kDecSB + u, len, start, cbx[e], hash,
+        const uint2 r = dec_record<kImplicit>(a, tb, lane, j * SB + u, len, start, cbx[e], hash,
                                               status, all_lds);
         dst[u * kLanes + lane] = r;
-        if (kLatents) med[((j & 1) * kDecSB + u) * kLanes + lane] = cm[e];
-        if (lane == 0) info[(j & 1) * kDecSB + u] = all_lds ? 1u : 0u;
+        if (kLatents) med[((j & 1) * SB + u) * kLanes + lane] = cm[e];
+        if (!all_lds && lane == 0)
+          __hip_atomic_fetch_or(&ctl[2 + (j & 1)], 1u << u, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_WORKGROUP);
       }
     };
 
     // Loads that do not depend on the tables are issued before the tables are
     // staged, so that they overlap: the coder's initial states and first
-    // stream words, the mappers' first two blocks of inputs.
-    constexpr int kPre = kLowWater / kPfWords;
-    Stream S;
-    Esc E;
+    // stream words, the mappers' first two blocks of inputs, the escape
+    // reader's window.
+    EscReader E;
     uint32_t x = kStateLow;
-    uint32_t w0[kPre][kPfU32];
+    uint32_t w0[G::kPre][kPfU32];
     if (wid == 0) {
-      S.s32 = reinterpret_cast<const uint32_t*>(cdata + 4 * A);
-      S.safe = reinterpret_cast<const uint32_t*>(cdata);
-      S.q = (int)((cb - 4 * A) / 2);  // u16 words after the states (even)
-      S.q32 = S.q / 2;
-      S.rp = 0;
+      S.s32 = s32;
+      S.safe = safe;
+      S.q = q16;
+      S.q32 = q16 / 2;
       S.filled = 0;
-      x = reinterpret_cast<const uint32_t*>(cdata)[lane < A ? lane : 0];  // lane < A: below
+      x = safe[lane < A ? lane : 0];  // lane < A: below
 #pragma unroll
-      for (int b = 0; b < kPre; ++b)
+      for (int b = 0; b < G::kPre; ++b)
 #pragma unroll
         for (int kk = 0; kk < kPfU32; ++kk)
           w0[b][kk] = stream_word32(S, b * (kPfWords / 2) + kk * kLanes + lane);
 #pragma unroll
       for (int kk = 0; kk < kPfU32; ++kk)
-        S.pf[kk] = stream_word32(S, kPre * (kPfWords / 2) + kk * kLanes + lane);
-      E.w32 = S.s32;
-      E.safe = S.safe;
-      E.n32 = S.q32;
+        S.pf[kk] = stream_word32(S, G::kPre * (kPfWords / 2) + kk * kLanes + lane);
+    } else if (wid == kEscWave) {
+      E.w32 = s32;
+      E.safe = safe;
+      E.n32 = q16 / 2;
+      E.base = 0;
       E.q = 0;
-      E.w0 = esc_load(E, lane);  // esc_window completes them after the staging
-      E.w1 = esc_load(E, kLanes + lane);
+      E.p = 0;
+      E.stopped = false;
+      E.w0 = esc_word(E, lane);
+      E.w1 = esc_word(E, kLanes + lane);
     } else if (nblk > 0) {
       load_block(0, cbx, cm);
       if (nblk > 1) load_block(1, nbx, nm);
     }
+    if (tid < 8) ctl[tid] = tid == 1 ? kAllAvail : 0u;
     int t_lo, t_hi;
     stage_range(a.nt_cap, a.stage_all, k, (int)a.P, (int)a.M, t_lo, t_hi);
-    stage_tables(tb, lmeta, nullptr, a.ne_cap ? lent32 : nullptr, llut,
-                 a.nd_cap ? ldense : nullptr, th->total_dense, a.M, t_lo, t_hi, tid);
+    stage_tables<kDecThreads>(tb, lmeta, nullptr, a.ne_cap ? lent32 : nullptr, llut,
+                              a.nd_cap ? ldense : nullptr, th->total_dense, a.M, t_lo, t_hi, tid);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load crosses the role split
 
-    // The coder and the mappers run separate code (the wave role is uniform
-    // per wave) that meets at the same barriers: one before the first block
-    // and one per block.
+    // The coder, the mappers and the escape reader run separate code (the
+    // wave role is uniform per wave) that meets at the same barriers: one
+    // before the first block and one per block, and one after the mappers'
+    // last store.
     if (wid == 0) {
       x = lane < A ? x : kStateLow;
-      esc_window(E, lane);
 #pragma unroll
-      for (int b = 0; b < kPre; ++b)
+      for (int b = 0; b < G::kPre; ++b)
 #pragma unroll
         for (int kk = 0; kk < kPfU32; ++kk)
-          sring32[(b * (kPfWords / 2) + kk * kLanes + lane) & (kStreamRing / 2 - 1)] = w0[b][kk];
-      S.filled = kPre * kPfWords;
+          sring32[(b * (kPfWords / 2) + kk * kLanes + lane) & (G::kRing / 2 - 1)] = w0[b][kk];
+      S.filled = G::kPre * kPfWords;
+      uint32_t ecur = 0;  // escape entries consumed
       __syncthreads();
       for (int j = 0; j < nblk; ++j) {
-        stream_block_start(S, sring32, lane);
-        uint4* src = recs + (j & 1) * kDecSB * kLanes;
-        uint4 r[kDecSB];
-        uint32_t fl[kDecSB], ov[kDecSB];
+        stream_block_start<SB>(S, sring32, lane);
+        uint2* src = recs + (j & 1) * SB * kLanes;
+        uint4* ei = escm + (j & 1) * SB;
+        uint2 r[SB];
+        uint32_t ov[SB];
 #pragma unroll
-        for (int u = 0; u < kDecSB; ++u) {
-          r[u] = src[u * kLanes + lane];
-          fl[u] = (uint32_t)uni((int)info[(j & 1) * kDecSB + u]);
-        }
-        uint32_t all_lds = 1;
-#pragma unroll
-        for (int u = 0; u < kDecSB; ++u) all_lds &= fl[u];
-        if ((j + 1) * kDecSB * kLanes <= len && all_lds && offsets_safe) {
+        for (int u = 0; u < SB; ++u) r[u] = src[u * kLanes + lane];
+        // steps whose tables are not all in LDS; cleared for block j + 2
+        const uint32_t nl = (uint32_t)uni((int)ctl[2 + (j & 1)]);
+        if (lane == 0) ctl[2 + (j & 1)] = 0u;
+        uint64_t any_em = 0;
+        if ((j + 1) * SB * kLanes <= len && nl == 0 && offsets_safe) {
           // common case: every lane of the block active, LDS tables, no
           // per-step branches
-          uint64_t em[kDecSB], any_em = 0;
+          uint64_t em[SB];
 #pragma unroll
-          for (int u = 0; u < kDecSB; ++u) {
-            ov[u] = dec_step<true, true>(tb, r[u], x, S, sring, em[u], status, lane);
+          for (int u = 0; u < SB; ++u) {
+            ov[u] = dec_step<true, true, SB>(tb, r[u], x, S, sring, em[u], status, lane);
             any_em |= em[u];
           }
           if (__builtin_expect(any_em != 0ull, 0)) {
 #pragma unroll
-            for (int u = 0; u < kDecSB; ++u)
-              if (em[u]) dec_escapes(em[u], r[u], ov[u], E, status, lane);
+            for (int u = 0; u < SB; ++u) {
+              if (lane == 0) ei[u] = make_uint4((uint32_t)em[u], (uint32_t)(em[u] >> 32), ecur, 0u);
+              ecur += (uint32_t)__popcll(em[u]);
+            }
           }
           // decoded values replace the records' x words; the mappers store them
 #pragma unroll
-          for (int u = 0; u < kDecSB; ++u)
-            reinterpret_cast<uint32_t*>(src + u * kLanes + lane)[0] = ov[u];
+          for (int u = 0; u < SB; ++u) src[u * kLanes + lane].x = ov[u];
         } else {
           // last block or tables outside LDS: one step at a time
 #pragma unroll 1
-          for (int u = 0; u < kDecSB && j * kDecSB + u < T; ++u) {
-            const uint4 ru = src[u * kLanes + lane];
+          for (int u = 0; u < SB && j * SB + u < T; ++u) {
+            const uint2 ru = src[u * kLanes + lane];
             uint64_t em;
-            uint32_t v = uni((int)info[(j & 1) * kDecSB + u])
-                             ? dec_step<true, false>(tb, ru, x, S, sring, em, status, lane)
-                             : dec_step<false, false>(tb, ru, x, S, sring, em, status, lane);
-            if (em) dec_escapes(em, ru, v, E, status, lane);
-            reinterpret_cast<uint32_t*>(src + u * kLanes + lane)[0] = v;
+            const uint32_t v = ((nl >> u) & 1u) == 0u
+                                   ? dec_step<true, false, SB>(tb, ru, x, S, sring, em, status, lane)
+                                   : dec_step<false, false, SB>(tb, ru, x, S, sring, em, status, lane);
+            if (lane == 0) ei[u] = make_uint4((uint32_t)em, (uint32_t)(em >> 32), ecur, 0u);
+            ecur += (uint32_t)__popcll(em);
+            any_em |= em;
+            src[u * kLanes + lane].x = v;
           }
+        }
+        if (lane == 0) {
+          ctl[4 + (j & 1)] = any_em != 0ull ? 1u : 0u;
+          ctl[6 + ((j + 1) & 1)] = ecur;
         }
         __syncthreads();
       }
-      // every state back at 2^16; stream, pad and escape words consumed
-      // exactly; the pad word and the unused nibbles of the last escape word
-      // are zero
       if (lane < A && x != kStateLow) status |= GAANS_ST_CORRUPT;
-      const int qe = (int)((E.q + 3u) >> 2);
-      const int pad = (S.rp + qe) & 1;
-      if (S.rp + qe + pad != S.q) {
-        status |= GAANS_ST_CORRUPT;
-      } else {
-        const uint16_t* s16 = reinterpret_cast<const uint16_t*>(S.s32);
-        if (pad && s16[S.rp] != 0) status |= GAANS_ST_CORRUPT;
-        if (E.q & 3u) {
-          const uint32_t last = esc_u32_s(E, (int)(E.q >> 3)) >> (4u * (E.q & 7u));
-          if (last & ((1u << (4u * (4u - (E.q & 3u)))) - 1u)) status |= GAANS_ST_CORRUPT;
-        }
+      __syncthreads();  // after the mappers' last store
+    } else if (wid == kEscWave) {
+      __syncthreads();
+      for (int j = 0; j < nblk; ++j) {
+        // the entries of block j: at most SB kLanes past those consumed before it
+        esc_parse<R>(E, (uint32_t)uni((int)ctl[6 + (j & 1)]) + (uint32_t)(SB * kLanes), fifo, ctl,
+                     lane);
+        __syncthreads();
       }
+      __syncthreads();
     } else {
       if (nblk > 0) map_block(0);
       __syncthreads();
@@ -1463,7 +1556,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
         if (j > 0) store_block(j - 1);
         if (j + 1 < nblk) {
 #pragma unroll
-          for (int e = 0; e < kDecPer; ++e) {
+          for (int e = 0; e < kPer; ++e) {
             cbx[e] = nbx[e];
             cm[e] = nm[e];
           }
@@ -1473,22 +1566,45 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecArgs a) {
         __syncthreads();
       }
       if (nblk > 0) store_block(nblk - 1);
+      __syncthreads();
     }
   }
   hash = wave_sum(hash);
   status = wave_or(status);
+  enib = wave_sum(enib);
   if (lane == 0) {
     part[wid] = hash;
-    part[kWaves + wid] = status;
+    part[kDecWaves + wid] = status;
+    part[2 * kDecWaves + wid] = enib;
   }
   __syncthreads();
   if (tid == 0) {
-    uint32_t hs = 0, st = 0;
-    for (int w = 0; w < kWaves; ++w) {
+    uint32_t hs = 0, st = 0, eq = 0;
+    for (int w = 0; w < kDecWaves; ++w) {
       hs += part[w];
-      st |= part[kWaves + w];
+      st |= part[kDecWaves + w];
+      eq += part[2 * kDecWaves + w];
     }
-    if (ok && hs != want_hash) st |= GAANS_ST_INDEXHASH;
+    if (ok) {
+      if (hs != want_hash) st |= GAANS_ST_INDEXHASH;
+      // stream, pad and escape words consumed exactly (eq escape nibbles);
+      // the pad word and the unused nibbles of the last escape word are zero
+      const int qe = (int)((eq + 3u) >> 2);
+      const int pad = (S.rp + qe) & 1;
+      if (S.rp + qe + pad != S.q) {
+        st |= GAANS_ST_CORRUPT;
+      } else {
+        const uint16_t* s16 = reinterpret_cast<const uint16_t*>(S.s32);
+        if (pad && s16[S.rp] != 0) st |= GAANS_ST_CORRUPT;
+        if (eq & 3u) {
+          // escape u32 eq >> 3 holds the first unused nibble (in range: the
+          // words were consumed exactly)
+          const uint32_t v = S.s32[S.q32 - 1 - (int)(eq >> 3)];
+          const uint32_t last = ((v >> 16) | (v << 16)) >> (4u * (eq & 7u));
+          if (last & ((1u << (4u * (4u - (eq & 3u)))) - 1u)) st |= GAANS_ST_CORRUPT;
+        }
+      }
+    }
     // status and counter are agent-scope atomics; the status has completed
     // before the counter is raised (no fence: decoded values need no
     // visibility before the kernel ends)
@@ -1520,7 +1636,7 @@ int check_launch(const char* what) {
 
 int check_tables_arg(const gaans_tables* t) {
   if (!t || !t->dev) return fail(GAANS_EINVAL, "tables descriptor or its device pointer is NULL");
-  if (t->M < 1) return fail(GAANS_EINVAL, "table count M must be >= 1");
+  if (t->M < 1 || t->M > 65536) return fail(GAANS_EINVAL, "table count M must be in [1, 65536]");
   if (t->bytes < (int64_t)sizeof(TabHdr) || t->bytes > 0xffffffffll)
     return fail(GAANS_EINVAL, "tables bytes %lld out of range", (long long)t->bytes);
   if (t->max_nsym < 1 || t->total_nsym < t->max_nsym || t->max_dense < 0 ||
@@ -1561,43 +1677,94 @@ int device_lds(DevLds* out) {
 
 // LDS staging plan for a launch of BK workgroups: all tables if they fit
 // and are not much larger than a chunk's channel range, else that range (P
-// tables, bounded by P times the largest table), else none.  The budget per workgroup keeps the launch in one round
-// of workgroups when the tables allow it (BK / CUs workgroups per CU), and
-// otherwise gives up workgroups per CU before it gives up staging.
+// tables, bounded by P times the largest table), else none.  The budget per
+// workgroup keeps the launch in one round of workgroups when the tables allow
+// it (BK / CUs workgroups per CU), and otherwise gives up workgroups per CU
+// before it gives up staging.
 struct Stage {
   int32_t nt_cap, ne_cap, nd_cap, stage_all;
 };
 
-Stage plan_stage(const gaans_tables* t, int64_t P, int64_t per_table, int64_t per_sym,
-                 int64_t per_dense, int64_t fixed, int64_t BK, const DevLds& d) {
-  Stage s{0, 0, 0, 0};
+// LDS of one workgroup when occ workgroups share a CU: the CU's LDS divided
+// by occ, rounded down to 1 KB, less 1 KB when several share it (measured on
+// MI355X: three workgroups of 53,632 bytes fit on a CU, three of 54,272 do
+// not).
+int64_t lds_budget(const DevLds& d, int64_t occ) {
+  int64_t b = d.per_cu / occ;
+  if (b > d.per_block) b = d.per_block;
+  b = b / 1024 * 1024;
+  return occ > 1 ? b - 1024 : b;
+}
+
+// Workgroups per CU that keep a launch of BK workgroups in one round.
+int64_t occ_target(int64_t BK, const DevLds& d, int64_t max_occ) {
+  int64_t occ = (BK + d.cus - 1) / d.cus;
+  return occ > max_occ ? max_occ : (occ < 1 ? 1 : occ);
+}
+
+// Tables staged in `budget` bytes (per table, per symbol entry and per dense
+// block costs): false if not even the chunk's range fits.
+bool fit_stage(const gaans_tables* t, int64_t P, int64_t per_table, int64_t per_sym,
+               int64_t per_dense, int64_t budget, Stage* s) {
   const int64_t all = t->M * per_table + per_sym * t->total_nsym + per_dense * t->total_dense;
   const int64_t range = P * (per_table + per_sym * (int64_t)t->max_nsym +
                              per_dense * (int64_t)t->max_dense);
-  int64_t occ = (BK + d.cus - 1) / d.cus;
-  if (occ > 4) occ = 4;
-  if (occ < 1) occ = 1;
-  for (; occ >= 1; --occ) {
-    int64_t budget = d.per_cu / occ;
-    if (budget > d.per_block) budget = d.per_block;
-    budget -= fixed;
-    // all tables when that is not much more to copy than the chunk's range
-    // (or the range does not fit): explicit indexes may use any table
-    if (all <= budget && (all <= 2 * range || range > budget)) {
-      s.nt_cap = t->M;
-      s.ne_cap = per_sym ? (int32_t)t->total_nsym : 0;
-      s.nd_cap = per_dense ? (int32_t)t->total_dense : 0;
-      s.stage_all = 1;
-      return s;
-    }
-    if (range <= budget) {
-      s.nt_cap = (int32_t)P;
-      s.ne_cap = per_sym ? (int32_t)(P * t->max_nsym) : 0;
-      s.nd_cap = per_dense ? (int32_t)(P * t->max_dense) : 0;
-      return s;
+  // all tables when that is not much more to copy than the chunk's range
+  // (or the range does not fit): explicit indexes may use any table
+  if (all <= budget && (all <= 2 * range || range > budget)) {
+    *s = Stage{t->M, per_sym ? (int32_t)t->total_nsym : 0,
+               per_dense ? (int32_t)t->total_dense : 0, 1};
+    return true;
+  }
+  if (range <= budget) {
+    *s = Stage{(int32_t)P, per_sym ? (int32_t)(P * t->max_nsym) : 0,
+               per_dense ? (int32_t)(P * t->max_dense) : 0, 0};
+    return true;
+  }
+  return false;
+}
+
+// Encoder: metadata and both entry words per symbol.
+Stage plan_encode(const gaans_tables* t, int64_t P, int64_t BK, const DevLds& d) {
+  Stage s{0, 0, 0, 0};
+  for (int64_t occ = occ_target(BK, d, 4); occ >= 1; --occ)
+    if (fit_stage(t, P, 16, 8, 0, lds_budget(d, occ) - kEncFixedLds, &s)) return s;
+  return Stage{0, 0, 0, 0};
+}
+
+// Decoder: lookups and metadata per table; dense blocks and entry words 0
+// when they are staged too.  For each workgroups-per-CU count (at most 3:
+// the kernel is built for 6 waves per SIMD, and a 6-wave workgroup puts two
+// waves on two of the CU's four SIMDs), the options in order of preference:
+// 8-step blocks with dense blocks, 4-step blocks with dense blocks (their
+// records, stream ring and escape FIFO take half the LDS), then the same
+// without dense blocks (a dense-bucket lookup then reads global memory).
+struct DecPlan {
+  Stage st;
+  int sb;
+  size_t lds;
+};
+
+DecPlan plan_decode(const gaans_tables* t, int64_t P, int64_t BK, bool latents,
+                    const DevLds& d) {
+  const int64_t per_table = 8 * kLutSize + 16;
+  const bool has_dense = t->total_dense > 0;
+  for (int64_t occ = occ_target(BK, d, 3); occ >= 1; --occ) {
+    const int64_t cap = lds_budget(d, occ);
+    for (int opt = 0; opt < 4; ++opt) {
+      const bool dense = opt < 2;
+      const int sb = (opt & 1) ? 4 : 8;
+      if (!dense && !has_dense) break;  // same as the options already tried
+      Stage s;
+      const int64_t fixed = dec_fixed_lds(latents, sb);
+      if (fit_stage(t, P, per_table, dense && has_dense ? 4 : 0, dense ? kLutSize : 0,
+                    cap - fixed, &s))
+        return DecPlan{s, sb,
+                       (size_t)(fixed + per_table * s.nt_cap + 4 * (int64_t)s.ne_cap +
+                                (int64_t)kLutSize * s.nd_cap)};
     }
   }
-  return s;
+  return DecPlan{Stage{0, 0, 0, 0}, 8, (size_t)dec_fixed_lds(latents, 8)};
 }
 
 // Allow dynamic LDS above the default limit (once per kernel and device).
@@ -1636,7 +1803,7 @@ int encode_stage1(bool latents, void* stream, const int32_t* symbols, const floa
   uint8_t* w = static_cast<uint8_t*>(ws);
   DevLds dl;
   if ((rc = device_lds(&dl))) return rc;
-  const Stage st = plan_stage(tables, P, 16, 8, 0, kEncFixedLds, L.BK, dl);
+  const Stage st = plan_encode(tables, P, L.BK, dl);
   EncArgs a;
   a.symbols = symbols;
   a.y = y;
@@ -1696,8 +1863,8 @@ int decode_impl(bool latents, void* stream, const uint8_t* payload, int64_t payl
   DevLds dl;
   if ((rc = device_lds(&dl))) return rc;
   // entry words are read only by dense-bucket lookups
-  const Stage st = plan_stage(tables, P, 8 * kLutSize + 16, tables->total_dense ? 4 : 0,
-                              kLutSize, dec_fixed_lds(latents), L.BK, dl);
+  const DecPlan plan = plan_decode(tables, P, L.BK, latents, dl);
+  const Stage& st = plan.st;
   DecArgs a;
   a.payload = payload;
   a.payload_bytes = payload_bytes;
@@ -1723,18 +1890,21 @@ int decode_impl(bool latents, void* stream, const uint8_t* payload, int64_t payl
   a.stage_all = st.stage_all;
   a.ctrl = static_cast<uint32_t*>(ctrl);
   a.status_out = status_out;
-  const size_t lds = dec_fixed_lds(latents) + (8 * kLutSize + 16) * (size_t)st.nt_cap +
-                     4 * (size_t)st.ne_cap + (size_t)kLutSize * st.nd_cap;
+  const size_t lds = plan.lds;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid((uint32_t)L.BK), block(kThreads);
+  const dim3 grid((uint32_t)L.BK), block(kDecThreads);
   auto launch = [&](auto kernel) -> int {
     int r = allow_lds(reinterpret_cast<const void*>(kernel), lds, dl);
     if (r) return r;
     kernel<<<grid, block, lds, s>>>(a);
     return check_launch("decode");
   };
-  if (latents) return indexes ? launch(k_decode<true, false>) : launch(k_decode<true, true>);
-  return indexes ? launch(k_decode<false, false>) : launch(k_decode<false, true>);
+  if (plan.sb == 4) {
+    if (latents) return indexes ? launch(k_decode<true, false, 4>) : launch(k_decode<true, true, 4>);
+    return indexes ? launch(k_decode<false, false, 4>) : launch(k_decode<false, true, 4>);
+  }
+  if (latents) return indexes ? launch(k_decode<true, false, 8>) : launch(k_decode<true, true, 8>);
+  return indexes ? launch(k_decode<false, false, 8>) : launch(k_decode<false, true, 8>);
 }
 
 uint64_t fnv_u32(uint64_t h, uint32_t v) {
@@ -1808,12 +1978,15 @@ int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, gaans_layout* o
 int gaans_tables_bytes(const int32_t* cdfs, const int32_t* cdf_sizes, int32_t M, int32_t Lmax,
                        int64_t* bytes) {
   if (!cdfs || !cdf_sizes || !bytes) return fail(GAANS_EINVAL, "NULL argument");
-  if (M < 1 || Lmax < 2) return fail(GAANS_EINVAL, "need M >= 1 tables of Lmax >= 2 entries");
+  // decode records carry a table number and an escape symbol in 16 bits each
+  if (M < 1 || M > 65536 || Lmax < 2)
+    return fail(GAANS_EINVAL, "need 1 <= M <= 65536 tables of Lmax >= 2 entries (got M=%d)", M);
   int64_t total = 0, dense = 0;
   for (int32_t t = 0; t < M; ++t) {
     const int32_t S = cdf_sizes[t];
-    if (S < 2 || S > Lmax || S > 65537)
-      return fail(GAANS_ETABLE, "table %d: cdf size %d outside [2, %d]", t, S, Lmax);
+    if (S < 2 || S > Lmax || S > 65536)
+      return fail(GAANS_ETABLE, "table %d: cdf size %d outside [2, %d]", t, S,
+                  Lmax < 65536 ? Lmax : 65536);
     total += S - 1;
     dense += count_dense(cdfs + (int64_t)t * Lmax, S);
   }

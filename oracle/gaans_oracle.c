@@ -47,7 +47,8 @@
  * REVERSE order (escape word 0 is the last u16 of the chunk), so a decoder
  * finds every escape from the chunk's end without knowing W.  After
  * decoding, every active lane is back at 2^16, the stream, the pad and the
- * escape words have all been consumed, and every count is <= 8.
+ * escape words have all been consumed, and every count is the minimal one of
+ * its raw value (raw ? msb(raw) / 4 + 1 : 0, hence <= 8).
  *
  * Header (u32 LE words):
  *   0 magic 0x31574147 ("GAW1")   1 version (2)     2 B    3 N
@@ -73,11 +74,12 @@
 
 static int check_tables(const int32_t* cdfs, int32_t M, int32_t Lmax,
                         const int32_t* sizes) {
-  if (M <= 0 || Lmax < 2) return GAANS_REF_EINVAL;
+  /* table numbers and escape symbols fit 16 bits in the GPU decoder */
+  if (M <= 0 || M > 65536 || Lmax < 2) return GAANS_REF_EINVAL;
   for (int32_t t = 0; t < M; ++t) {
     int32_t S = sizes[t];
     const int32_t* c = cdfs + (int64_t)t * Lmax;
-    if (S < 2 || S > Lmax) return GAANS_REF_ETABLE;
+    if (S < 2 || S > Lmax || S > 65536) return GAANS_REF_ETABLE;
     if (c[0] != 0 || c[S - 1] != 65536) return GAANS_REF_ETABLE;
     for (int32_t j = 0; j + 1 < S; ++j)
       if (c[j + 1] <= c[j]) return GAANS_REF_ETABLE;
@@ -600,6 +602,7 @@ int gaans_ref_decode(const uint8_t* payload, int64_t payload_len,
           }
           uint32_t raw = 0;
           for (int j = 0; j < n; ++j) raw |= nib[1 + j] << (4 * j);
+          if (n != nibble_count(raw)) return GAANS_REF_ECORRUPT; /* not minimal */
           eq += 1 + n;
           rc = unmap_escape(raw, S, offsets[tb], &orow[i]);
           if (rc) return rc;

@@ -188,6 +188,48 @@ def test_batch64_p16(backend, gpu_device, make):
     check_workload(backend, gpu_device, make())
 
 
+def test_escape_heavy_chunks_bit_exact(backend, gpu_device):
+    # every symbol of a 1x192x32x48 image escapes: each chunk's escape section
+    # holds 6,144 entries, several times the decoder's escape FIFO
+    w = synthetic.coder_512x768(seed=7)
+    rng = np.random.default_rng(7)
+    w.symbols = (w.symbols * 40 + rng.integers(-3, 4, w.symbols.shape)
+                 + np.where(rng.random(w.symbols.shape) < 0.5, 5000, -5000)).astype(np.int32)
+    w.name = "all-escape 1x192x32x48"
+    check_workload(backend, gpu_device, w)
+
+
+def test_escape_heavy_batch_bit_exact(backend, gpu_device):
+    # 48 images with the narrow tables of the 95%-zero workload and symbols
+    # drawn wider than their support: 576 chunks, so the decoder runs three
+    # workgroups per CU with 4-step blocks, and most steps carry escapes
+    w = synthetic.batch_skew(batch=48)
+    rng = np.random.default_rng(8)
+    w.symbols = np.rint(rng.laplace(0, 2.0, w.symbols.shape)).astype(np.int32)
+    w.name = "escape-heavy batch 48x192x32x48"
+    check_workload(backend, gpu_device, w)
+
+
+def test_non_minimal_escape_count_rejected(backend, gpu_device):
+    # the oracle's case (tests/test_oracle.py): count 2 for a raw value that
+    # needs one nibble, same payload length
+    import struct
+
+    cdfs, sizes, offs = (np.array([[0, 32768, 65536]], np.int32), np.array([3], np.int32),
+                         np.array([0], np.int32))
+    data = O.gaans_encode([[2]], None, cdfs, sizes, offs, 1)
+    hb = (64 + 8 + 15) // 16 * 16
+    bad = bytearray(data)
+    struct.pack_into("<H", bad, hb + 6, 0x0022)
+    say("case: non-minimal escape count")
+    c, z, o = dev(cdfs, gpu_device), dev(sizes, gpu_device), dev(offs, gpu_device)
+    idx = torch.zeros((1, 1), dtype=torch.int32, device=gpu_device)
+    good = WarpDivPayload.from_bytes(data, device=gpu_device)
+    assert backend.decode(good, idx, c, z, o).tolist() == [[2]]
+    with pytest.raises(CoderInputError, match="corrupt"):
+        backend.decode(WarpDivPayload.from_bytes(bytes(bad), device=gpu_device), idx, c, z, o)
+
+
 # ---- fused quantize / dequantize -------------------------------------------
 
 def test_fused_latents_match_quantize_then_encode(gpu_device):

@@ -205,6 +205,34 @@ def test_gaans_escape_section_word_order_without_pad():
         O.gaans_decode(bytes(bad), None, 1, 1, cdfs, sizes, offs, 1)
 
 
+def test_gaans_escape_count_must_be_minimal():
+    # one escape of raw 2 (even: value (raw >> 1) + maxv = 2): nibbles 1, 2 ->
+    # escape word 0x0021; the state 2^17 + 32768 emits nothing, so W = 0,
+    # Q = 1 and a zero pad word precedes the escape word.  Rewriting the entry
+    # as count 2, nibbles 2, 0 (same raw, same word count) must be rejected.
+    cdfs, sizes, offs = CDF2, [3], [0]
+    data = O.gaans_encode([[2]], None, cdfs, sizes, offs, 1)
+    hb = (64 + 8 + 15) // 16 * 16
+    assert struct.unpack("<IHH", data[hb:]) == ((1 << 17) + 32768, 0, 0x0021)
+    assert O.gaans_decode(data, None, 1, 1, cdfs, sizes, offs, 1).tolist() == [[2]]
+    bad = bytearray(data)
+    struct.pack_into("<H", bad, hb + 6, 0x0022)
+    with pytest.raises(O.OracleError) as err:
+        O.gaans_decode(bytes(bad), None, 1, 1, cdfs, sizes, offs, 1)
+    assert err.value.code == -6  # payload corrupt
+
+
+def test_tables_beyond_16_bit_symbol_numbers_rejected():
+    # escape symbols (cdf size - 2) and table numbers are 16-bit in the decoder
+    cdf = np.arange(65537, dtype=np.int32)[None, :]
+    with pytest.raises(O.OracleError):
+        O.gaans_encode([[0]], None, cdf, [65537], [0], 1)
+    cdf = np.arange(65536, dtype=np.int32)[None, :].copy()
+    cdf[0, -1] = 65536
+    data = O.gaans_encode([[70000]], None, cdf, [65536], [0], 1)
+    assert O.gaans_decode(data, None, 1, 1, cdf, [65536], [0], 1).tolist() == [[70000]]
+
+
 def test_gaans_chunking_and_header_offsets():
     # 3 channels of HW = 2, P = 2 -> chunks of 4 and 2 symbols; 2 rows.
     cdfs = np.array([[0, 32768, 65536]] * 3, np.int32)
