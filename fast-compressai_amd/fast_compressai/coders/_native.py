@@ -40,12 +40,24 @@ STATUS_TEXT = {
 }
 
 
+_LAYOUT_FIELDS = ("B", "N", "C", "P", "HW", "K", "chunk_len", "BK", "header_bytes",
+                  "max_payload_bytes", "cap_words", "workspace_bytes", "ws_chunk_words",
+                  "ws_chunk_status", "ws_index_hash", "ws_end_off", "ws_info", "ws_states",
+                  "ws_words", "ws_esc", "ws_esc_raw")
+
+
 class Layout(ctypes.Structure):
-    _fields_ = [(name, ctypes.c_int64) for name in (
-        "B", "N", "C", "P", "HW", "K", "chunk_len", "BK", "header_bytes",
-        "max_payload_bytes", "cap_words", "workspace_bytes", "ws_chunk_words",
-        "ws_chunk_status", "ws_index_hash", "ws_end_off", "ws_info", "ws_states",
-        "ws_words", "ws_esc", "ws_esc_raw")]
+    _fields_ = [(name, ctypes.c_int64) for name in _LAYOUT_FIELDS]
+
+
+class LayoutInts:
+    """``gaans_layout`` as plain Python ints (read without ctypes conversions)."""
+
+    __slots__ = _LAYOUT_FIELDS
+
+    def __init__(self, lay: Layout) -> None:
+        for name in _LAYOUT_FIELDS:
+            setattr(self, name, int(getattr(lay, name)))
 
 
 class Tables(ctypes.Structure):
@@ -137,12 +149,13 @@ def check(rc: int, what: str) -> None:
 _layouts: dict = {}
 
 
-def layout(B: int, N: int, C: int, P: int) -> Layout:
+def layout(B: int, N: int, C: int, P: int) -> LayoutInts:
     key = (B, N, C, P)
     out = _layouts.get(key)
     if out is None:
-        out = Layout()
-        check(lib().gaans_get_layout(B, N, C, P, ctypes.byref(out)), "layout")
+        raw = Layout()
+        check(lib().gaans_get_layout(B, N, C, P, ctypes.byref(raw)), "layout")
+        out = LayoutInts(raw)
         if len(_layouts) > 256:
             _layouts.clear()
         _layouts[key] = out

@@ -40,6 +40,9 @@ class _StreamState:
         self.status_np = self.status.numpy()
         self.info_done = self.info.data_ptr() + 16    # completion words
         self.status_done = self.status.data_ptr() + 4
+        self.ctrl_ptr = self.ctrl.data_ptr()
+        self.info_ptr = self.info.data_ptr()
+        self.status_ptr = self.status.data_ptr()
         self.workspace = torch.empty(0, dtype=torch.uint8, device=device)
 
     def ws(self, nbytes: int) -> torch.Tensor:
@@ -73,30 +76,18 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 
 
 def _index(device) -> int:
-    d = device if isinstance(device, torch.device) else torch.device(device)
+    d = device if type(device) is torch.device else torch.device(device)
     return torch.cuda.current_device() if d.index is None else d.index
 
 
-class _on_device:
-    """Make ``index`` the current device for the call (no-op when it is)."""
-
-    __slots__ = ("index", "prev")
-
-    def __init__(self, index: int) -> None:
-        self.index = index
-        self.prev = None
-
-    def __enter__(self):
-        cur = torch.cuda.current_device()
-        if cur != self.index:
-            self.prev = cur
-            torch.cuda.set_device(self.index)
-        return self
-
-    def __exit__(self, *exc):
-        if self.prev is not None:
-            torch.cuda.set_device(self.prev)
-        return False
+def _enter_device(index: int):
+    """Make ``index`` the current device; returns the device to restore
+    afterwards, or None when it already was current."""
+    cur = torch.cuda.current_device()
+    if cur == index:
+        return None
+    torch.cuda.set_device(index)
+    return cur
 
 
 @dataclass(frozen=True)
@@ -116,35 +107,43 @@ def encode(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,
     L = _native.lib()
     lay = _native.layout(B, N, C, P)
     index = _index(device)
-    with _on_device(index):
+    prev = _enter_device(index)
+    try:
         sp = torch._C._cuda_getCurrentRawStream(index)
         st = _state(index, sp)
-        ws = st.ws(int(lay.workspace_bytes))
-        out = torch.empty(int(lay.max_payload_bytes), dtype=torch.uint8, device=ws.device)
+        ws = st.ws(lay.workspace_bytes)
+        out = torch.empty(lay.max_payload_bytes, dtype=torch.uint8, device=ws.device)
         st.info_np[2] = 0
         if y is not None:
             rc = L.gaans_encode_latents(sp, y.data_ptr(), medians.data_ptr(), _ptr(indexes),
                                         tables.ref, B, N, C, P, ws.data_ptr(), ws.numel(),
-                                        st.ctrl.data_ptr(), st.info.data_ptr())
+                                        st.ctrl_ptr, st.info_ptr)
         else:
             rc = L.gaans_encode_symbols(sp, symbols.data_ptr(), _ptr(indexes), tables.ref, B, N,
-                                        C, P, ws.data_ptr(), ws.numel(), st.ctrl.data_ptr(),
-                                        st.info.data_ptr())
-        _native.check(rc, "GA-ANS encode")
+                                        C, P, ws.data_ptr(), ws.numel(), st.ctrl_ptr,
+                                        st.info_ptr)
+        if rc:
+            _native.check(rc, "GA-ANS encode")
         rc = L.gaans_encode_pack(sp, ws.data_ptr(), ws.numel(), tables.ref, B, N, C, P,
-                                 out.data_ptr(), out.numel())
-        _native.check(rc, "GA-ANS pack")
-        _native.wait_host_word(sp, st.info_done, "GA-ANS encode")  # the one host wait
+                                 out.data_ptr(), lay.max_payload_bytes)
+        if rc:
+            _native.check(rc, "GA-ANS pack")
+        rc = L.gaans_wait_host_word(sp, st.info_done)  # the one host wait
+        if rc:
+            _native.check(rc, "GA-ANS encode")
         word = int(st.info_np[2])  # 1 | status << 1 | payload bytes << 16
         total, status = word >> 16, (word >> 1) & 0x7FFF
+    finally:
+        if prev is not None:
+            torch.cuda.set_device(prev)
     if status:
         raise CoderInputError(f"GA-ANS encode failed: {_native.describe_status(status)}")
     packed = out[:total]
-    if out.numel() - total > _CLONE_SLACK_BYTES:
+    if lay.max_payload_bytes - total > _CLONE_SLACK_BYTES:
         packed = packed.clone()
-    K = int(lay.K)
+    K = lay.K
     ends = packed[64: 64 + 4 * B * K].view(torch.uint32).view(B, K)
-    return EncodedChunks(packed, ends, int(lay.header_bytes), int(lay.chunk_len), K)
+    return EncodedChunks(packed, ends, lay.header_bytes, lay.chunk_len, K)
 
 
 def decode(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int, P: int,
@@ -154,7 +153,8 @@ def decode(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int,
     [B, N] with dequantize fused."""
     L = _native.lib()
     index = _index(device)
-    with _on_device(index):
+    prev = _enter_device(index)
+    try:
         sp = torch._C._cuda_getCurrentRawStream(index)
         st = _state(index, sp)
         st.status_np[1] = 0
@@ -162,15 +162,21 @@ def decode(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int,
             out = torch.empty((B, N), dtype=torch.float32, device=packed.device)
             rc = L.gaans_decode_latents(sp, packed.data_ptr(), packed.numel(), _ptr(indexes),
                                         tables.ref, medians.data_ptr(), B, N, C, P,
-                                        out.data_ptr(), st.ctrl.data_ptr(), st.status.data_ptr())
+                                        out.data_ptr(), st.ctrl_ptr, st.status_ptr)
         else:
             out = torch.empty((B, N), dtype=torch.int32, device=packed.device)
             rc = L.gaans_decode_symbols(sp, packed.data_ptr(), packed.numel(), _ptr(indexes),
-                                        tables.ref, B, N, C, P, out.data_ptr(),
-                                        st.ctrl.data_ptr(), st.status.data_ptr())
-        _native.check(rc, "GA-ANS decode")
-        _native.wait_host_word(sp, st.status_done, "GA-ANS decode")  # the one host wait
+                                        tables.ref, B, N, C, P, out.data_ptr(), st.ctrl_ptr,
+                                        st.status_ptr)
+        if rc:
+            _native.check(rc, "GA-ANS decode")
+        rc = L.gaans_wait_host_word(sp, st.status_done)  # the one host wait
+        if rc:
+            _native.check(rc, "GA-ANS decode")
         status = int(st.status_np[1]) >> 1  # 1 | status << 1
+    finally:
+        if prev is not None:
+            torch.cuda.set_device(prev)
     if status:
         raise CoderInputError(f"warp_div decode failed: {_native.describe_status(status)}")
     return out

@@ -83,15 +83,31 @@ class TableCache:
         self._capacity = capacity
         self._entries: OrderedDict = OrderedDict()
         self._lock = threading.Lock()
+        # the last hit: the same three tensor objects, unchanged since, give
+        # the same tables (checked first, without building a key)
+        self._last = None
 
     @staticmethod
     def _key(tensors):
         # device pointers are unique across devices; dtype and device are
         # checked by the callers before tables are prepared
-        return tuple((t.data_ptr(), t._version, t.shape) for t in tensors)
+        return tuple((t.data_ptr(), t._version, t.shape, t.stride()) for t in tensors)
 
     def get(self, cdfs: torch.Tensor, cdf_sizes: torch.Tensor,
             offsets: torch.Tensor) -> PreparedTables:
+        last = self._last
+        if (last is not None and last[0] is cdfs and last[1] is cdf_sizes and last[2] is offsets
+                and last[3] == (cdfs._version, cdf_sizes._version, offsets._version,
+                                cdfs.data_ptr(), cdf_sizes.data_ptr(), offsets.data_ptr())):
+            return last[4]
+        prepared = self._get(cdfs, cdf_sizes, offsets)
+        self._last = (cdfs, cdf_sizes, offsets,
+                      (cdfs._version, cdf_sizes._version, offsets._version, cdfs.data_ptr(),
+                       cdf_sizes.data_ptr(), offsets.data_ptr()), prepared)
+        return prepared
+
+    def _get(self, cdfs: torch.Tensor, cdf_sizes: torch.Tensor,
+             offsets: torch.Tensor) -> PreparedTables:
         key = self._key((cdfs, cdf_sizes, offsets))
         with self._lock:
             hit = self._entries.get(key)

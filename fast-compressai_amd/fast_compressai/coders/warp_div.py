@@ -29,8 +29,6 @@ import hashlib
 import re
 import struct
 from dataclasses import dataclass, fields
-from typing import Sequence
-
 import torch
 
 from . import gaans
@@ -115,8 +113,9 @@ class WarpDivPayload:
         """Payload built by ``WarpDivBackend.encode`` from values it has just
         produced and checked; skips the field validation of ``__init__``."""
         obj = object.__new__(cls)
-        for f in fields(cls):
-            object.__setattr__(obj, f.name, values.get(f.name, f.default))
+        state = dict(_PAYLOAD_DEFAULTS)
+        state.update(values)
+        obj.__dict__.update(state)
         return obj
 
     @property
@@ -165,6 +164,10 @@ class WarpDivPayload:
                    symbols_per_batch=N, cdf_count=M,
                    coding_fingerprint=coding_fingerprint(digest, B, N, C, M),
                    channels=None if C == M else C)
+
+
+# field defaults of WarpDivPayload (for _from_encoder)
+_PAYLOAD_DEFAULTS = {f.name: f.default for f in fields(WarpDivPayload)}
 
 
 class WarpDivBackend:
@@ -253,18 +256,23 @@ def _validate_inputs(
     """Host-side checks of the reference (``warp_div.py:179-215``) without the
     index min/max sync (index range is checked on the device).  Returns the
     channel count used for chunking."""
-    if not isinstance(symbols, torch.Tensor) or not isinstance(indexes, torch.Tensor):
+    T = torch.Tensor
+    if not isinstance(symbols, T) or not isinstance(indexes, T):
         raise CoderInputError("symbols and indexes must be torch tensors")
-    tensors: Sequence[torch.Tensor] = (symbols, indexes, cdfs, cdf_sizes, offsets)
-    if any(not isinstance(value, torch.Tensor) for value in tensors):
+    if not (isinstance(cdfs, T) and isinstance(cdf_sizes, T) and isinstance(offsets, T)):
         raise CoderInputError("indexes, CDFs, CDF sizes, and offsets must be tensors")
     if type(p_ch) is not int or p_ch <= 0:
         raise CoderInputError("p_ch must be a positive integer")
-    if symbols.device.type != "cuda" or any(value.device != symbols.device for value in tensors):
+    dev = symbols.device
+    if (dev.type != "cuda" or indexes.device != dev or cdfs.device != dev
+            or cdf_sizes.device != dev or offsets.device != dev):
         raise CoderInputError("all coder inputs must be GPU tensors on the same device")
-    if any(value.dtype != torch.int32 for value in tensors):
+    i32 = torch.int32
+    if (symbols.dtype != i32 or indexes.dtype != i32 or cdfs.dtype != i32
+            or cdf_sizes.dtype != i32 or offsets.dtype != i32):
         raise CoderInputError("all warp_div input tensors must use torch.int32")
-    if any(not value.is_contiguous() for value in tensors):
+    if not (symbols.is_contiguous() and indexes.is_contiguous() and cdfs.is_contiguous()
+            and cdf_sizes.is_contiguous() and offsets.is_contiguous()):
         raise CoderInputError("all warp_div input tensors must be contiguous")
     if symbols.ndim != 2 or indexes.shape != symbols.shape:
         raise CoderInputError("symbols and indexes must have matching [B, N] shape")
