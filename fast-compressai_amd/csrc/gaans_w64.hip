@@ -63,9 +63,12 @@ constexpr uint32_t kMagic = 0x31574147u;  // "GAW1"
 constexpr uint32_t kVersion = 2u;
 constexpr uint32_t kParams = 0x00041040u;  // lanes 64 | precision 16 << 8 | bypass 4 << 16
 constexpr int kFixedWords = 16;
-constexpr uint32_t kTabMagic = 0x32425447u;  // "GTB2"
+constexpr uint32_t kTabMagic = 0x33425447u;  // "GTB3"
 constexpr int kLutBits = 8;
 constexpr int kLutSize = 1 << kLutBits;
+constexpr int kSubBits = 4;                 // a sub-block: 16 entries of 16 or 1 values
+constexpr int kSubSize = 1 << kSubBits;
+constexpr int kSubBytes = 8 * kSubSize;
 constexpr uint32_t kHashMul = 0x9E3779B9u;
 constexpr int kMaxEscNibbles = 9;  // escape count + 8 nibbles of raw
 
@@ -103,24 +106,27 @@ int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
 // ---- prepared table blob ---------------------------------------------------
 // [TabHdr 64 B][TabMeta x M][entries: 2 x u32 per symbol][lut: u64 x 256 x M]
-// [dense blocks: 256 x u8 each]
-// entry of symbol v: word 0 = start | (freq - 1) << 16;
-//                    word 1 = division magic of freq (enc_magic).
-// lut entry of bucket j (cum in [j << 8, (j << 8) + 255]), s = the symbol
-// containing cum = j << 8:
-//   at most one other symbol starts in the bucket:
-//     low word = entry word 0 of s, high word = s | (freq(s + 1) - 1) << 16
-//   two or more (a dense bucket):
-//     low word = index of the bucket's dense block, high word = s | 0xffff << 16;
-//     byte i of the block = (symbol containing cum = (j << 8) + i) - s
+// [sub-blocks: u64 x 16 each]
+// entry of symbol v (encoder): word 0 = start | (freq - 1) << 16;
+//                              word 1 = division magic of freq (enc_magic).
+// Decode lookup entries (u64) cover a range of cum values: 256 (the table's
+// lookup, bucket j = [j << 8, (j << 8) + 255]), 16 (second level) or 1 (third
+// level).  With s the symbol containing the range's first value:
+//   at most one other symbol starts in the range:
+//     low word = start(s) | (freq(s) - 1) << 16,
+//     high word = s | (freq(s + 1) - 1) << 16   (cum >= start + freq -> s + 1)
+//   two or more (a dense range, 256 or 16 values wide):
+//     low word = global index of a sub-block, high word = s | 0xffff << 16;
+//     the sub-block's 16 entries cover the range's 16 sub-ranges (of 16 values
+//     for a 256-value range, of one value for a 16-value range).
 struct TabHdr {
   uint32_t magic, M, total_syms, lut_bits;
   uint32_t digest_lo, digest_hi;
   uint32_t meta_off, ent_off, lut_off;  // byte offsets
   uint32_t total_bytes;
   uint32_t max_nsym;
-  uint32_t dense_off;    // byte offset of the dense blocks
-  uint32_t total_dense;  // dense blocks over all tables
+  uint32_t dense_off;    // byte offset of the sub-blocks
+  uint32_t total_dense;  // sub-blocks over all tables
   uint32_t flags;        // kTabOffsetsSafe
   uint32_t reserved[2];
 };
@@ -132,7 +138,7 @@ struct TabMeta {
   uint32_t ent_base;    // first entry of the table
   uint32_t nsym;        // S - 1 symbols; the last one (nsym - 1) is the escape bin
   int32_t offset;
-  uint32_t dense_base;  // first dense block of the table
+  uint32_t dense_base;  // first sub-block of the table
 };
 
 // Division by a wave-uniform divisor d in [1, 2^31) for numerators n < 2^31:
@@ -291,15 +297,14 @@ struct Tabs {
   const TabMeta* __restrict__ gmeta;
   const uint2* __restrict__ gent;
   const uint64_t* __restrict__ glut;
-  const uint8_t* __restrict__ gdense;
+  const uint64_t* __restrict__ gsub;
   const uint4* lmeta;      // {ent_base (LDS-local), nsym, offset, ent_base (global)}
   const uint2* lent;       // encoder: both entry words
-  const uint32_t* lent32;  // decoder: entry word 0
-  const uint64_t* llut;    // nt x 256
-  const uint8_t* ldense;
+  const uint64_t* llut;    // decoder: nt x 256 lookup entries
+  const uint64_t* lsub;    // decoder: sub-blocks of the staged tables
   int t_lo, nt;
-  uint32_t dense_first;    // first staged dense block
-  bool dense_lds;          // decoder: dense blocks and entry words staged with the lookups
+  uint32_t sub_first;      // first staged sub-block
+  bool sub_lds;            // decoder: sub-blocks staged with the lookups
 };
 
 // Copy n 16-byte words global -> LDS with the whole workgroup (NT threads),
@@ -323,22 +328,21 @@ __device__ __forceinline__ void copy16(uint4* dst, const uint4* __restrict__ src
   }
 }
 
-// One pass over the staged metadata (nt), entries (ne) and dense 16-byte
+// One pass over the staged metadata (nt), entries (ne) and sub-block 16-byte
 // words (nd) with U loads of each kind in flight per thread before the
 // stores.  Indexes past a count re-copy its last item, so nothing branches
 // (the kinds are compile-time choices; counts are >= 1).
-template <int NT, bool kEnt, bool kEnt32, bool kDense>
-__device__ __forceinline__ void stage_pass(const Tabs& T, uint4* lmeta, uint2* lent,
-                                           uint32_t* lent32, uint4* ldense,
-                                           const uint4* __restrict__ dsrc, uint32_t nt,
+template <int NT, bool kEnt, bool kSub>
+__device__ __forceinline__ void stage_pass(const Tabs& T, uint4* lmeta, uint2* lent, uint4* lsub,
+                                           const uint4* __restrict__ ssrc, uint32_t nt,
                                            uint32_t ne, uint32_t nd, uint32_t base0, int t_lo,
                                            int tid) {
   // loads in flight per thread and kind (fewer for the decoder's larger
   // workgroup, whose waves keep more registers live across the staging)
   constexpr int U = NT > kThreads ? 3 : 4;
   uint32_t items = nt;
-  if (kEnt || kEnt32) items = items > ne ? items : ne;
-  if (kDense) items = items > nd ? items : nd;
+  if (kEnt) items = items > ne ? items : ne;
+  if (kSub) items = items > nd ? items : nd;
   for (uint32_t b = tid; b < items; b += U * NT) {
     TabMeta mv[U];
     uint2 ev[U];
@@ -347,8 +351,8 @@ __device__ __forceinline__ void stage_pass(const Tabs& T, uint4* lmeta, uint2* l
     for (int k = 0; k < U; ++k) {
       const uint32_t i = b + k * NT;
       mv[k] = T.gmeta[t_lo + (i < nt ? i : nt - 1)];
-      if (kEnt || kEnt32) ev[k] = T.gent[base0 + (i < ne ? i : ne - 1)];
-      if (kDense) dv[k] = dsrc[i < nd ? i : nd - 1];
+      if (kEnt) ev[k] = T.gent[base0 + (i < ne ? i : ne - 1)];
+      if (kSub) dv[k] = ssrc[i < nd ? i : nd - 1];
     }
 #pragma unroll
     for (int k = 0; k < U; ++k) {
@@ -356,51 +360,43 @@ __device__ __forceinline__ void stage_pass(const Tabs& T, uint4* lmeta, uint2* l
       lmeta[i < nt ? i : nt - 1] =
           make_uint4(mv[k].ent_base - base0, mv[k].nsym, (uint32_t)mv[k].offset, mv[k].ent_base);
       if (kEnt) lent[i < ne ? i : ne - 1] = ev[k];
-      if (kEnt32) lent32[i < ne ? i : ne - 1] = ev[k].x;
-      if (kDense) ldense[i < nd ? i : nd - 1] = dv[k];
+      if (kSub) lsub[i < nd ? i : nd - 1] = dv[k];
     }
   }
 }
 
 // Stage tables [t_lo, t_hi) of the blob into LDS (whole workgroup of NT
 // threads): the encoder's metadata and entries (lent), or the decoder's
-// lookups (llut), metadata and, when lent32 is given, dense blocks (ldense)
-// and entry words 0 (lent32).  The lookups, which need no metadata, are
-// copied while the metadata loads are in flight; lookups and dense blocks are
-// 16-byte aligned in the blob.
+// lookups (llut), metadata and, when lsub is given, the tables' sub-blocks.
+// The lookups, which need no metadata, are copied while the metadata loads
+// are in flight; lookups and sub-blocks are 16-byte aligned in the blob.
 template <int NT>
-__device__ void stage_tables(Tabs& T, uint4* lmeta, uint2* lent, uint32_t* lent32,
-                             uint64_t* llut, uint8_t* ldense, uint32_t total_dense, uint32_t M,
-                             int t_lo, int t_hi, int tid) {
+__device__ void stage_tables(Tabs& T, uint4* lmeta, uint2* lent, uint64_t* llut, uint64_t* lsub,
+                             uint32_t total_blocks, uint32_t M, int t_lo, int t_hi, int tid) {
   T.t_lo = t_lo;
   T.nt = t_hi > t_lo ? t_hi - t_lo : 0;
-  T.dense_first = 0;
-  T.dense_lds = lent32 != nullptr;
+  T.sub_first = 0;
+  T.sub_lds = lsub != nullptr;
   if (T.nt > 0) {
     const uint32_t nt = (uint32_t)T.nt;
     const uint32_t base0 = T.gmeta[t_lo].ent_base;
-    const TabMeta last = T.gmeta[t_hi - 1];
-    const uint32_t ne = last.ent_base + last.nsym - base0;
     if (lent) {
-      stage_pass<NT, true, false, false>(T, lmeta, lent, nullptr, nullptr, nullptr, nt, ne, 0u,
-                                         base0, t_lo, tid);
+      const TabMeta last = T.gmeta[t_hi - 1];
+      const uint32_t ne = last.ent_base + last.nsym - base0;
+      stage_pass<NT, true, false>(T, lmeta, lent, nullptr, nullptr, nt, ne, 0u, base0, t_lo, tid);
     } else {
       const uint4* lut_src = reinterpret_cast<const uint4*>(T.glut + (int64_t)t_lo * kLutSize);
       copy16<NT, 4>(reinterpret_cast<uint4*>(llut), lut_src, nt * (kLutSize / 2), tid);
-      if (lent32) {
-        const uint32_t d0 = T.gmeta[t_lo].dense_base;
-        const uint32_t d1 = (uint32_t)t_hi < M ? T.gmeta[t_hi].dense_base : total_dense;
-        T.dense_first = d0;
-        // without dense blocks, the pass re-copies the first lookup word
-        const bool any = d1 > d0;
-        stage_pass<NT, false, true, true>(
-            T, lmeta, nullptr, lent32,
-            any ? reinterpret_cast<uint4*>(ldense) : reinterpret_cast<uint4*>(llut),
-            any ? reinterpret_cast<const uint4*>(T.gdense + (size_t)d0 * kLutSize) : lut_src,
-            nt, ne, any ? (d1 - d0) * (kLutSize / 16) : 1u, base0, t_lo, tid);
+      const uint32_t d0 = T.gmeta[t_lo].dense_base;
+      const uint32_t d1 = (uint32_t)t_hi < M ? T.gmeta[t_hi].dense_base : total_blocks;
+      if (lsub && d1 > d0) {
+        T.sub_first = d0;
+        stage_pass<NT, false, true>(T, lmeta, nullptr, reinterpret_cast<uint4*>(lsub),
+                                    reinterpret_cast<const uint4*>(T.gsub + (size_t)d0 * kSubSize),
+                                    nt, 1u, (d1 - d0) * (kSubBytes / 16), base0, t_lo, tid);
       } else {
-        stage_pass<NT, false, false, false>(T, lmeta, nullptr, nullptr, nullptr, nullptr, nt,
-                                            1u, 0u, base0, t_lo, tid);
+        stage_pass<NT, false, false>(T, lmeta, nullptr, nullptr, nullptr, nt, 1u, 0u, base0, t_lo,
+                                     tid);
       }
     }
   }
@@ -675,15 +671,14 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
     tb.gmeta = reinterpret_cast<const TabMeta*>(a.tables + th->meta_off);
     tb.gent = reinterpret_cast<const uint2*>(a.tables + th->ent_off);
     tb.glut = nullptr;
-    tb.gdense = nullptr;
+    tb.gsub = nullptr;
     tb.lmeta = lmeta;
     tb.lent = lent;
-    tb.lent32 = nullptr;
     tb.llut = nullptr;
-    tb.ldense = nullptr;
+    tb.lsub = nullptr;
     int t_lo, t_hi;
     stage_range(a.nt_cap, a.stage_all, k, a.P, (int)a.M, t_lo, t_hi);
-    stage_tables<kThreads>(tb, lmeta, lent, nullptr, nullptr, nullptr, 0u, a.M, t_lo, t_hi, tid);
+    stage_tables<kThreads>(tb, lmeta, lent, nullptr, nullptr, 0u, a.M, t_lo, t_hi, tid);
 
     // mapper wave w (1..kMappers) owns steps u = w - 1 + kMappers e of every block
     int32_t ca[kEncPer], cb[kEncPer], na[kEncPer], nb[kEncPer];
@@ -1061,43 +1056,50 @@ __device__ __forceinline__ uint2 dec_record(const DecArgs& a, const Tabs& tb, in
   return r;
 }
 
-// cum -> (symbol, start, freq) in table t.  One lookup resolves every bucket
-// in which at most one other symbol starts; a dense bucket (marker 0xffff)
-// reads the symbol from its dense block and then the symbol's entry (LDS when
-// the dense blocks are staged, else global memory).
+// One level down from a dense lookup entry e: entry i of its sub-block (LDS
+// when the sub-blocks are staged, else global memory).  The asm keeps the two
+// loads apart, so the compiler does not merge them into one generic load
+// (which would also wait for the stream prefetch).
+template <bool kLds>
+__device__ __forceinline__ uint64_t sub_entry(const Tabs& tb, uint64_t e, uint32_t i) {
+  uint64_t r;
+  if (kLds && tb.sub_lds) {
+    r = tb.lsub[(((uint32_t)e - tb.sub_first) << kSubBits) + i];
+    asm volatile("" : "+v"(r));
+  } else {
+    r = tb.gsub[((size_t)(uint32_t)e << kSubBits) + i];
+    asm volatile("" : "+v"(r));
+  }
+  return r;
+}
+
+__device__ __forceinline__ bool dense_entry(uint64_t e) { return (uint32_t)(e >> 48) == 0xffffu; }
+
+// cum -> (symbol, start, freq) in table t: the table's lookup entry of
+// bucket cum >> 8, for a dense bucket the entry of sub-range (cum >> 4) & 15
+// of its sub-block, for a dense sub-range the exact entry of value cum & 15
+// (see the blob layout).
 template <bool kLds>
 __device__ __forceinline__ void dec_lookup(const Tabs& tb, uint32_t t, uint32_t cum, bool act,
                                            uint32_t& s, uint32_t& st, uint32_t& fr) {
   const uint32_t li = (t << kLutBits) + (cum >> (16 - kLutBits));
-  const uint64_t e = kLds ? tb.llut[li] : tb.glut[li];
+  uint64_t e = kLds ? tb.llut[li] : tb.glut[li];
+  // the dense tests first: their scalar results are ready by the branches
+  const uint64_t dm = ballot(act & dense_entry(e));
+  asm volatile("" ::"s"(dm));
+  if (__builtin_expect(dm != 0ull, 0)) {
+    if (act & dense_entry(e)) e = sub_entry<kLds>(tb, e, (cum >> kSubBits) & (kSubSize - 1));
+    const uint64_t dm3 = ballot(act & dense_entry(e));
+    if (__builtin_expect(dm3 != 0ull, 0) && (act & dense_entry(e)))
+      e = sub_entry<kLds>(tb, e, cum & (kSubSize - 1));
+  }
   const uint32_t lo = (uint32_t)e, hi = (uint32_t)(e >> 32);
   const uint32_t s0 = hi & 0xffffu, nxt = hi >> 16;
-  // the dense test first: its scalar result is ready by the branch below
-  const uint64_t dm = ballot(act & (nxt == 0xffffu));
-  asm volatile("" ::"s"(dm));
   const uint32_t st0 = lo & 0xffffu, fr0 = (lo >> 16) + 1u;
   const bool up = cum >= st0 + fr0;
   s = up ? s0 + 1u : s0;
   st = up ? st0 + fr0 : st0;
   fr = up ? nxt + 1u : fr0;
-  if (__builtin_expect(dm != 0ull, 0) && (act & (nxt == 0xffffu))) {
-    const uint32_t ci = cum & (kLutSize - 1);
-    uint32_t en;
-    // separate loads per memory (the asm keeps the compiler from merging them
-    // into one generic load, which would also wait for the stream prefetch)
-    if (kLds && tb.dense_lds) {
-      s = s0 + (uint32_t)tb.ldense[((lo - tb.dense_first) << kLutBits) + ci];
-      en = tb.lent32[tb.lmeta[t].x + s];
-      asm volatile("" : "+v"(en));
-    } else {
-      s = s0 + (uint32_t)tb.gdense[((size_t)lo << kLutBits) + ci];
-      const uint32_t eb = kLds ? tb.lmeta[t].w : tb.gmeta[t].ent_base;
-      en = tb.gent[eb + s].x;
-      asm volatile("" : "+v"(en));
-    }
-    st = en & 0xffffu;
-    fr = (en >> 16) + 1u;
-  }
 }
 
 // Word stream of one chunk: prefetched from HBM into registers (kPfWords words
@@ -1309,9 +1311,8 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   uint8_t* tsm = smem + G::fixed(kLatents);
   uint64_t* llut = reinterpret_cast<uint64_t*>(tsm);
   uint4* lmeta = reinterpret_cast<uint4*>(tsm + 8 * kLutSize * a.nt_cap);
-  // [luts][meta][dense blocks][entry words 0]: every part 16-byte aligned
-  uint8_t* ldense = tsm + (8 * kLutSize + 16) * a.nt_cap;
-  uint32_t* lent32 = reinterpret_cast<uint32_t*>(ldense + (size_t)kLutSize * a.nd_cap);
+  // [luts][meta][sub-blocks]: every part 16-byte aligned
+  uint64_t* lsub = reinterpret_cast<uint64_t*>(tsm + (8 * kLutSize + 16) * a.nt_cap);
 
   const int64_t g = blockIdx.x;
   const int tid = threadIdx.x;
@@ -1359,13 +1360,12 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
     tb.gmeta = reinterpret_cast<const TabMeta*>(a.tables + th->meta_off);
     tb.gent = reinterpret_cast<const uint2*>(a.tables + th->ent_off);
     tb.glut = reinterpret_cast<const uint64_t*>(a.tables + th->lut_off);
-    tb.gdense = a.tables + th->dense_off;
+    tb.gsub = reinterpret_cast<const uint64_t*>(a.tables + th->dense_off);
     const bool offsets_safe = (th->flags & kTabOffsetsSafe) != 0;
     tb.lmeta = lmeta;
     tb.lent = nullptr;
-    tb.lent32 = lent32;
     tb.llut = llut;
-    tb.ldense = ldense;
+    tb.lsub = lsub;
     const uint8_t* cdata = a.payload + a.header_bytes + beg;
     const uint32_t* s32 = reinterpret_cast<const uint32_t*>(cdata + 4 * A);
     const uint32_t* safe = reinterpret_cast<const uint32_t*>(cdata);
@@ -1467,8 +1467,8 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
     if (tid < 8) ctl[tid] = tid == 1 ? kAllAvail : 0u;
     int t_lo, t_hi;
     stage_range(a.nt_cap, a.stage_all, k, (int)a.P, (int)a.M, t_lo, t_hi);
-    stage_tables<kDecThreads>(tb, lmeta, nullptr, a.ne_cap ? lent32 : nullptr, llut,
-                              a.nd_cap ? ldense : nullptr, th->total_dense, a.M, t_lo, t_hi, tid);
+    stage_tables<kDecThreads>(tb, lmeta, nullptr, llut, a.nd_cap ? lsub : nullptr,
+                              th->total_dense, a.M, t_lo, t_hi, tid);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load crosses the role split
 
     // The coder, the mappers and the escape reader run separate code (the
@@ -1732,13 +1732,13 @@ Stage plan_encode(const gaans_tables* t, int64_t P, int64_t BK, const DevLds& d)
   return Stage{0, 0, 0, 0};
 }
 
-// Decoder: lookups and metadata per table; dense blocks and entry words 0
-// when they are staged too.  For each workgroups-per-CU count (at most 3:
+// Decoder: lookups and metadata per table; sub-blocks when they are staged
+// too.  For each workgroups-per-CU count (at most 3:
 // the kernel is built for 6 waves per SIMD, and a 6-wave workgroup puts two
 // waves on two of the CU's four SIMDs), the options in order of preference:
-// 8-step blocks with dense blocks, 4-step blocks with dense blocks (their
+// 8-step blocks with sub-blocks, 4-step blocks with sub-blocks (their
 // records, stream ring and escape FIFO take half the LDS), then the same
-// without dense blocks (a dense-bucket lookup then reads global memory).
+// without sub-blocks (a dense-bucket lookup then reads global memory).
 struct DecPlan {
   Stage st;
   int sb;
@@ -1757,11 +1757,8 @@ DecPlan plan_decode(const gaans_tables* t, int64_t P, int64_t BK, bool latents,
       if (!dense && !has_dense) break;  // same as the options already tried
       Stage s;
       const int64_t fixed = dec_fixed_lds(latents, sb);
-      if (fit_stage(t, P, per_table, dense && has_dense ? 4 : 0, dense ? kLutSize : 0,
-                    cap - fixed, &s))
-        return DecPlan{s, sb,
-                       (size_t)(fixed + per_table * s.nt_cap + 4 * (int64_t)s.ne_cap +
-                                (int64_t)kLutSize * s.nd_cap)};
+      if (fit_stage(t, P, per_table, 0, dense ? kSubBytes : 0, cap - fixed, &s))
+        return DecPlan{s, sb, (size_t)(fixed + per_table * s.nt_cap + kSubBytes * (int64_t)s.nd_cap)};
     }
   }
   return DecPlan{Stage{0, 0, 0, 0}, 8, (size_t)dec_fixed_lds(latents, 8)};
@@ -1915,27 +1912,66 @@ uint64_t fnv_u32(uint64_t h, uint32_t v) {
   return h;
 }
 
-int64_t tables_size(int32_t M, int64_t total_syms, int64_t total_dense) {
+int64_t tables_size(int32_t M, int64_t total_syms, int64_t total_blocks) {
   int64_t o = sizeof(TabHdr);
   o += (int64_t)sizeof(TabMeta) * M;
   o = align_up(align_up(o, 8) + 8 * total_syms, 16);
   o += 8ll * kLutSize * M;
-  o += (int64_t)kLutSize * total_dense;
+  o += (int64_t)kSubBytes * total_blocks;
   return o;
 }
 
-// Dense decode buckets of one CDF: buckets [j << 8, (j << 8) + 255] in which
-// two or more symbols start after the bucket's first value.
-int32_t count_dense(const int32_t* c, int32_t S) {
-  int32_t n = 0, prev = -1, cnt = 0;
-  for (int32_t v = 1; v + 1 < S; ++v) {  // starts of symbols 1 .. S - 2
-    if ((c[v] & (kLutSize - 1)) == 0) continue;  // starts the bucket itself
-    const int32_t b = c[v] >> (16 - kLutBits);
-    if (b != prev) {
-      prev = b;
-      cnt = 0;
+// Decode lookup entry of the cum range [lo, lo + width) of a CDF with nsym
+// symbols (cdf c) into *out; false when the range is dense (two or more
+// symbols start after lo).  s is advanced to the symbol containing lo.
+bool lookup_entry(const int32_t* c, uint32_t nsym, uint32_t lo, uint32_t width, uint32_t& s,
+                  uint64_t* out) {
+  while (s + 1 < nsym && (uint32_t)c[s + 1] <= lo) ++s;
+  uint32_t e = s;
+  while (e + 1 < nsym && (uint32_t)c[e + 1] <= lo + width - 1) ++e;
+  if (e - s >= 2) return false;
+  const uint32_t next = s + 1 < nsym ? (uint32_t)(c[s + 2] - c[s + 1] - 1) : 0u;
+  const uint32_t lo_word = (uint32_t)c[s] | ((uint32_t)(c[s + 1] - c[s] - 1) << 16);
+  *out = (uint64_t)lo_word | ((uint64_t)(s | (next << 16)) << 32);
+  return true;
+}
+
+// Sub-blocks of one CDF (S entries): one per dense 256-value bucket, one per
+// dense 16-value sub-range of those.  Fills them when blocks is non-NULL
+// (global indices from `first`) and the table's 256 lookup entries in lut.
+int32_t build_lookup(const int32_t* c, int32_t S, uint64_t* lut, uint64_t* blocks,
+                     uint32_t first) {
+  const uint32_t nsym = (uint32_t)(S - 1);
+  int32_t n = 0;
+  uint32_t s = 0;
+  for (int j = 0; j < kLutSize; ++j) {
+    const uint32_t lo = (uint32_t)j << (16 - kLutBits);
+    uint64_t e;
+    if (lookup_entry(c, nsym, lo, 1u << (16 - kLutBits), s, &e)) {
+      if (lut) lut[j] = e;
+      continue;
     }
-    if (++cnt == 2) ++n;
+    const uint32_t b2 = (uint32_t)n++;
+    if (lut) lut[j] = (uint64_t)(first + b2) | ((uint64_t)(s | (0xffffu << 16)) << 32);
+    uint32_t s2 = s;
+    for (int i = 0; i < kSubSize; ++i) {
+      const uint32_t lo2 = lo + ((uint32_t)i << kSubBits);
+      uint64_t e2;
+      if (lookup_entry(c, nsym, lo2, kSubSize, s2, &e2)) {
+        if (blocks) blocks[(size_t)b2 * kSubSize + i] = e2;
+        continue;
+      }
+      const uint32_t b3 = (uint32_t)n++;
+      if (blocks)
+        blocks[(size_t)b2 * kSubSize + i] =
+            (uint64_t)(first + b3) | ((uint64_t)(s2 | (0xffffu << 16)) << 32);
+      uint32_t s3 = s2;
+      for (int v = 0; v < kSubSize; ++v) {
+        uint64_t e3 = 0;
+        lookup_entry(c, nsym, lo2 + (uint32_t)v, 1u, s3, &e3);  // one value: never dense
+        if (blocks) blocks[(size_t)b3 * kSubSize + v] = e3;
+      }
+    }
   }
   return n;
 }
@@ -1988,7 +2024,7 @@ int gaans_tables_bytes(const int32_t* cdfs, const int32_t* cdf_sizes, int32_t M,
       return fail(GAANS_ETABLE, "table %d: cdf size %d outside [2, %d]", t, S,
                   Lmax < 65536 ? Lmax : 65536);
     total += S - 1;
-    dense += count_dense(cdfs + (int64_t)t * Lmax, S);
+    dense += build_lookup(cdfs + (int64_t)t * Lmax, S, nullptr, nullptr, 0u);
   }
   *bytes = tables_size(M, total, dense);
   if (*bytes > 0xffffffffll) return fail(GAANS_ETABLE, "tables exceed 4 GiB");
@@ -2026,14 +2062,14 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
   for (int32_t t = 0; t < M; ++t) {
     total += cdf_sizes[t] - 1;
     if ((uint32_t)(cdf_sizes[t] - 1) > max_nsym) max_nsym = (uint32_t)(cdf_sizes[t] - 1);
-    const int32_t nd = count_dense(cdfs + (int64_t)t * Lmax, cdf_sizes[t]);
+    const int32_t nd = build_lookup(cdfs + (int64_t)t * Lmax, cdf_sizes[t], nullptr, nullptr, 0u);
     total_dense += nd;
     if (nd > max_dense) max_dense = nd;
   }
   const int64_t lut_off = align_up(ent_off + 8 * total, 16);
   uint64_t* lut = reinterpret_cast<uint64_t*>(o + lut_off);
   const int64_t dense_off = lut_off + 8ll * kLutSize * M;
-  uint8_t* dense = o + dense_off;
+  uint64_t* blocks = reinterpret_cast<uint64_t*>(o + dense_off);
   uint32_t dblk = 0;
   uint64_t dg = 0xcbf29ce484222325ull;
   dg = fnv_u32(dg, (uint32_t)M);
@@ -2054,31 +2090,8 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
       ent[2 * (base + v)] = (uint32_t)c[v] | ((f - 1u) << 16);
       ent[2 * (base + v) + 1] = enc_magic(f);
     }
-    // bucket j covers cum in [j << 8, (j << 8) + 255]
-    uint32_t s = 0;
-    for (int j = 0; j < kLutSize; ++j) {
-      const uint32_t lo = (uint32_t)j << (16 - kLutBits);
-      const uint32_t hi = lo + (1u << (16 - kLutBits)) - 1u;
-      while (s + 1 < nsym && (uint32_t)c[s + 1] <= lo) ++s;
-      uint32_t e = s;
-      while (e + 1 < nsym && (uint32_t)c[e + 1] <= hi) ++e;
-      uint32_t lo_word, hi_word;
-      if (e - s >= 2) {  // dense bucket: exact symbol offsets of its 256 values
-        uint8_t* blk = dense + (int64_t)dblk * kLutSize;
-        uint32_t v = s;
-        for (uint32_t i = 0; i < (uint32_t)kLutSize; ++i) {
-          while (v + 1 < nsym && (uint32_t)c[v + 1] <= lo + i) ++v;
-          blk[i] = (uint8_t)(v - s);
-        }
-        lo_word = dblk++;
-        hi_word = s | (0xffffu << 16);
-      } else {
-        const uint32_t next = s + 1 < nsym ? (uint32_t)(c[s + 2] - c[s + 1] - 1) : 0u;
-        lo_word = (uint32_t)c[s] | ((uint32_t)(c[s + 1] - c[s] - 1) << 16);
-        hi_word = s | (next << 16);
-      }
-      lut[(int64_t)t * kLutSize + j] = (uint64_t)lo_word | ((uint64_t)hi_word << 32);
-    }
+    dblk += (uint32_t)build_lookup(c, S, lut + (int64_t)t * kLutSize,
+                                   blocks + (size_t)dblk * kSubSize, dblk);
     base += nsym;
   }
   h->magic = kTabMagic;

@@ -6,7 +6,8 @@ tensor with ``_cdf_length`` and ``_offset`` (reference
 a compact blob built once per table set by ``gaans_tables_prepare``: per-table
 metadata, per-symbol entries (``start | (freq - 1) << 16`` and the
 encoder's division magic of ``freq``), a 256-bucket decode lookup and, for
-buckets in which several symbols start, an exact 256-value block.  The blob also carries the table digest that every payload
+buckets in which several symbols start, second- and third-level lookups of
+16 entries (16-value sub-ranges, then single values).  The blob also carries the table digest that every payload
 records, so decoding with other tables is detected on the device.
 """
 

@@ -89,9 +89,10 @@ typedef struct gaans_tables {
   int32_t max_nsym;   /* largest alphabet (cdf_size - 1) */
   int64_t total_nsym; /* sum of the alphabets */
   uint64_t digest;    /* table digest recorded in payload headers */
-  int32_t max_dense;  /* most 256-value decode buckets with >= 2 symbol starts in one table */
+  int32_t max_dense;  /* most decode sub-blocks (128 B each: one per 256-value bucket, and
+                         per 16-value sub-range, with >= 2 symbol starts) of one table */
   int32_t reserved;
-  int64_t total_dense; /* such buckets over all tables */
+  int64_t total_dense; /* decode sub-blocks over all tables */
 } gaans_tables;
 
 int gaans_abi_version(void);

@@ -68,23 +68,30 @@ def prepare_host(cdfs, sizes, offs):
     return rc, out, desc.digest
 
 
-def host_lookup(blob, t, cum):
-    """Decode lookup as the kernel does it, read from the prepared blob."""
+def host_lookup(blob, t, cum, levels=None):
+    """Decode lookup as the kernel does it, read from the prepared blob: the
+    table's entry of bucket cum >> 8, for a dense bucket entry (cum >> 4) & 15
+    of its sub-block, for a dense sub-range entry cum & 15 of the next one."""
     hdr = struct.unpack_from("<16I", blob, 0)
-    meta_off, ent_off, lut_off, dense_off = hdr[6], hdr[7], hdr[8], hdr[11]
-    ent_base, nsym, offset, dense_base = struct.unpack_from("<IIiI", blob, meta_off + 16 * t)
+    meta_off, lut_off, sub_off, total_sub = hdr[6], hdr[8], hdr[11], hdr[12]
     e = struct.unpack_from("<Q", blob, lut_off + 8 * (256 * t + (cum >> 8)))[0]
+    depth = 1
+    for shift in (4, 0):
+        if e >> 48 != 0xFFFF:
+            break
+        blk = e & 0xFFFFFFFF
+        assert blk < total_sub
+        e = struct.unpack_from("<Q", blob, sub_off + 8 * (16 * blk + ((cum >> shift) & 15)))[0]
+        depth += 1
+    assert e >> 48 != 0xFFFF
+    if levels is not None:
+        levels[depth] = levels.get(depth, 0) + 1
     lo, hi = e & 0xFFFFFFFF, e >> 32
     s0, nxt = hi & 0xFFFF, hi >> 16
-    ent = lambda v: struct.unpack_from("<I", blob, ent_off + 8 * (ent_base + v))[0]
-    if nxt != 0xFFFF:
-        st, fr = lo & 0xFFFF, (lo >> 16) + 1
-        if cum >= st + fr:
-            return s0 + 1, st + fr, nxt + 1
-        return s0, st, fr
-    assert dense_base <= lo < hdr[12]
-    v = s0 + blob[dense_off + 256 * lo + (cum & 255)]
-    return v, ent(v) & 0xFFFF, (ent(v) >> 16) + 1
+    st, fr = lo & 0xFFFF, (lo >> 16) + 1
+    if cum >= st + fr:
+        return s0 + 1, st + fr, nxt + 1
+    return s0, st, fr
 
 
 def test_prepared_tables_digest_and_lookup_exhaustive():
@@ -107,12 +114,14 @@ def test_prepared_tables_digest_and_lookup_exhaustive():
             for x in (0, f - 1, f, (f << 16) - 1, (f << 15) + 12345, 0xFFFF * f):
                 tt = (x * m) >> 32
                 assert (tt + ((x - tt) >> 1)) >> sh == x // f, (t, v, f, x)
+    levels = {}
     for t in range(6):
         c = cdfs[t, : sizes[t]]
         want = np.searchsorted(c, np.arange(65536), side="right") - 1
         for cum in range(0, 65536, 7):
-            v, start, freq = host_lookup(blob, t, cum)
+            v, start, freq = host_lookup(blob, t, cum, levels)
             assert v == want[cum] and start == c[v] and freq == c[v + 1] - c[v], (t, cum)
+    assert levels.get(2, 0) > 0  # the Laplacian tails are dense buckets
 
 
 def test_prepared_tables_dense_tail_lookup():
@@ -124,9 +133,11 @@ def test_prepared_tables_dense_tail_lookup():
     assert rc == 0
     blob = blob.tobytes()
     want = np.searchsorted(c, np.arange(65536), side="right") - 1
-    for cum in list(range(0, 65536, 13)) + [0, 1, 65535, int(c[1]), int(c[-2]) - 1]:
-        v, start, freq = host_lookup(blob, 0, cum)
+    levels = {}
+    for cum in range(65536):  # every value: all three lookup levels occur
+        v, start, freq = host_lookup(blob, 0, cum, levels)
         assert v == want[cum] and start == c[v] and freq == c[v + 1] - c[v], cum
+    assert levels.get(2, 0) > 0 and levels.get(3, 0) > 0
 
 
 @pytest.mark.parametrize("cdf,size", [([1, 65536], 2), ([0, 65535], 2), ([0, 100, 100, 65536], 4),
