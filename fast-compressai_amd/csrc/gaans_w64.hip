@@ -72,13 +72,6 @@ constexpr int kSubBytes = 8 * kSubSize;
 constexpr uint32_t kHashMul = 0x9E3779B9u;
 constexpr int kMaxEscNibbles = 9;  // escape count + 8 nibbles of raw
 
-// encoder steps per block: the mappers' lead over the coder, and the steps
-// between two barriers (the decoder's are a template parameter, DecGeom)
-#ifndef GAANS_ENC_SB
-#define GAANS_ENC_SB 4
-#endif
-constexpr int kEncSB = GAANS_ENC_SB;
-constexpr int kEncPer = (kEncSB + kMappers - 1) / kMappers;  // steps per mapper wave and block
 // per-wave hash, status and escape nibbles, then the escape count
 constexpr int kPartBytes = (12 * kWaves + 4 + 15) / 16 * 16;
 constexpr int kRingWords = 4096;       // encoder LDS output ring (u16 words)
@@ -450,9 +443,19 @@ struct EncArgs {
 
 // Encoder LDS layout (bytes)
 constexpr int kEncRingBytes = 2 * (kRingWords + kLanes);  // + one spare slot per lane
-constexpr int kEncRecBytes = 2 * kEncSB * kLanes * 16;        // two blocks of op records
-constexpr int kEncInfoBytes = 2 * kEncSB * 4;                 // per-step escape flag
-constexpr int kEncFixedLds = kEncRingBytes + kEncRecBytes + kEncInfoBytes + kPartBytes;
+
+// Encoder geometry for blocks of SB steps (the mappers' lead over the coder
+// and the steps between two barriers).
+template <int SB>
+struct EncGeom {
+  static constexpr int kPer = (SB + kMappers - 1) / kMappers;  // steps per mapper wave and block
+  static constexpr int kRecBytes = 2 * SB * kLanes * 16;       // two blocks of op records
+  static constexpr int kFlagBytes = 16;  // per block parity: steps with escapes (bit per step)
+  // [ring][records][flags][parts]
+  static constexpr int kFixed = kEncRingBytes + kRecBytes + kFlagBytes + kPartBytes;
+};
+
+int enc_fixed_lds(int sb) { return sb >= 8 ? EncGeom<8>::kFixed : EncGeom<4>::kFixed; }
 
 // Payload bytes of chunk g: states, stream and escape words, pad.
 __device__ __forceinline__ uint64_t chunk_bytes(const EncArgs& a, int64_t g) {
@@ -602,7 +605,7 @@ __device__ __forceinline__ void ring_flush(uint16_t* __restrict__ wbuf, const ui
 }
 
 // The ring holds the words [wp, fl) (positions mod kRingWords).  The coder
-// flushes it at the start of a block when fewer than kEncSB * kLanes slots are
+// flushes it at the start of a block when fewer than SB * kLanes slots are
 // free (a step emits at most one word per lane), so the steps need no check.
 __device__ __forceinline__ void emit_words(bool emit, uint32_t& x, uint16_t* ring, int& wp,
                                            int lane) {
@@ -634,15 +637,17 @@ __device__ __forceinline__ void enc_escapes(const uint4 r, uint32_t* __restrict_
   cnt = uni(cnt + __popcll(em));
 }
 
-template <bool kLatents, bool kImplicit>
+template <bool kLatents, bool kImplicit, int SB>
 __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
+  using G = EncGeom<SB>;
+  constexpr int kPer = G::kPer;
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t* ring = reinterpret_cast<uint16_t*>(smem);
   uint4* recs = reinterpret_cast<uint4*>(smem + kEncRingBytes);
-  uint32_t* info = reinterpret_cast<uint32_t*>(smem + kEncRingBytes + kEncRecBytes);
-  uint32_t* part = info + 2 * kEncSB;  // per-wave hash [0, kWaves) and status [kWaves, 2 kWaves)
-  uint4* lmeta = reinterpret_cast<uint4*>(smem + kEncFixedLds);
-  uint2* lent = reinterpret_cast<uint2*>(smem + kEncFixedLds + 16 * a.nt_cap);
+  uint32_t* eflag = reinterpret_cast<uint32_t*>(smem + kEncRingBytes + G::kRecBytes);
+  uint32_t* part = eflag + G::kFlagBytes / 4;  // per-wave hash, status, escape nibbles
+  uint4* lmeta = reinterpret_cast<uint4*>(smem + G::kFixed);
+  uint2* lent = reinterpret_cast<uint2*>(smem + G::kFixed + 16 * a.nt_cap);
 
   const int64_t g = blockIdx.x;
   const int tid = threadIdx.x;
@@ -654,7 +659,7 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
   chunk_range(g, a.K, a.N, a.chunk_len, row, start, len, k);
   const int T = (len + kLanes - 1) / kLanes;
   const int A = len < kLanes ? len : kLanes;
-  const int nblk = (T + kEncSB - 1) / kEncSB;
+  const int nblk = (T + SB - 1) / SB;
   uint16_t* __restrict__ wbuf = a.words + g * a.cap_words;
   int wp = a.cap_words;  // coder: wave-uniform write cursor (backwards)
   int fl = a.cap_words;  // coder: words at [fl, cap) are already in wbuf
@@ -663,6 +668,7 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
   int n_esc = 0;  // coder: escapes listed so far
   uint32_t* __restrict__ esc_list = a.esc_raw + g * a.chunk_len + a.chunk_len;
 
+  if (tid < 2) eflag[tid] = 0u;  // visible after the staging barrier
   const bool tab = tables_ok(a.tables, a.M, a.tables_bytes);  // uniform
   if (!tab) status |= GAANS_ST_TABLES;
   if (tab) {
@@ -681,14 +687,14 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
     stage_tables<kThreads>(tb, lmeta, lent, nullptr, nullptr, 0u, a.M, t_lo, t_hi, tid);
 
     // mapper wave w (1..kMappers) owns steps u = w - 1 + kMappers e of every block
-    int32_t ca[kEncPer], cb[kEncPer], na[kEncPer], nb[kEncPer];
-    float cm[kEncPer], nm[kEncPer];
+    int32_t ca[kPer], cb[kPer], na[kPer], nb[kPer];
+    float cm[kPer], nm[kPer];
     auto load_block = [&](int j, int32_t* ia, int32_t* ib, float* im) {
 #pragma unroll
-      for (int e = 0; e < kEncPer; ++e) {
+      for (int e = 0; e < kPer; ++e) {
         const int u = (wid - 1) + kMappers * e;
-        if (kEncSB % kMappers != 0 && u >= kEncSB) break;
-        int p = lane + kLanes * (j * kEncSB + u);
+        if (SB % kMappers != 0 && u >= SB) break;
+        int p = lane + kLanes * (j * SB + u);
         p = p < len ? p : len - 1;  // loads stay in the chunk; results are masked
         const int64_t i = row + start + p;
         if (kLatents) {
@@ -703,17 +709,18 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
     };
     auto map_steps = [&](int j, auto lds_tag) {
       constexpr bool kLds = decltype(lds_tag)::value;
-      uint4* dst = recs + (j & 1) * kEncSB * kLanes;
+      uint4* dst = recs + (j & 1) * SB * kLanes;
 #pragma unroll
-      for (int e = 0; e < kEncPer; ++e) {
+      for (int e = 0; e < kPer; ++e) {
         const int u = (wid - 1) + kMappers * e;
-        if (kEncSB % kMappers != 0 && u >= kEncSB) break;
-        const uint4 r = enc_record<kLatents, kImplicit>(a, tb, kLds, lane, j * kEncSB + u, len,
+        if (SB % kMappers != 0 && u >= SB) break;
+        const uint4 r = enc_record<kLatents, kImplicit>(a, tb, kLds, lane, j * SB + u, len,
                                                         start, ca[e], cb[e], cm[e], hash, status,
                                                         znib);
         dst[u * kLanes + lane] = r;
-        const uint32_t esc_step = ballot((r.z & 256u) != 0u) != 0ull;
-        if (lane == 0) info[(j & 1) * kEncSB + u] = esc_step;
+        if (ballot((r.z & 256u) != 0u) != 0ull && lane == 0)
+          __hip_atomic_fetch_or(&eflag[j & 1], 1u << u, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_WORKGROUP);
       }
     };
     auto map_block = [&](int j) {
@@ -722,9 +729,9 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
       if (!kImplicit && lds) {
         bool outside = false;
 #pragma unroll
-        for (int e = 0; e < kEncPer; ++e) {
+        for (int e = 0; e < kPer; ++e) {
           const int u = (wid - 1) + kMappers * e;
-          outside |= u < kEncSB && lane + kLanes * (j * kEncSB + u) < len &&
+          outside |= u < SB && lane + kLanes * (j * SB + u) < len &&
                      (uint32_t)(cb[e] - tb.t_lo) >= (uint32_t)tb.nt;
         }
         lds = ballot(outside) == 0;
@@ -741,29 +748,28 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
       __syncthreads();
       for (int j = nblk - 1; j >= 0; --j) {
         // coder: steps of block j, last to first
-        if (fl - wp > kRingWords - kEncSB * kLanes) {
+        if (fl - wp > kRingWords - SB * kLanes) {
           ring_flush(wbuf, ring, wp, fl, lane);
           fl = wp;
         }
-        const uint4* src = recs + (j & 1) * kEncSB * kLanes;
-        uint4 r[kEncSB];
-        uint32_t any_esc = 0;
+        const uint4* src = recs + (j & 1) * SB * kLanes;
+        uint4 r[SB];
 #pragma unroll
-        for (int u = 0; u < kEncSB; ++u) {
-          r[u] = src[u * kLanes + lane];
-          any_esc |= (uint32_t)uni((int)info[(j & 1) * kEncSB + u]) << u;
-        }
-        if ((j + 1) * kEncSB <= T) {
+        for (int u = 0; u < SB; ++u) r[u] = src[u * kLanes + lane];
+        // steps of the block with escapes; cleared for block j - 2
+        const uint32_t any_esc = (uint32_t)uni((int)eflag[j & 1]);
+        if (lane == 0) eflag[j & 1] = 0u;
+        if ((j + 1) * SB <= T) {
           // common case: a full block, no per-step branches
 #pragma unroll
-          for (int u = kEncSB - 1; u >= 0; --u) {
+          for (int u = SB - 1; u >= 0; --u) {
             emit_words((x >> 16) >= 65536u - (r[u].x >> 16), x, ring, wp, lane);
             x = enc_apply(x, r[u]);
           }
         } else {
 #pragma unroll
-          for (int u = kEncSB - 1; u >= 0; --u) {
-            if (j * kEncSB + u >= T) continue;
+          for (int u = SB - 1; u >= 0; --u) {
+            if (j * SB + u >= T) continue;
             emit_words((x >> 16) >= 65536u - (r[u].x >> 16), x, ring, wp, lane);
             x = enc_apply(x, r[u]);
           }
@@ -771,7 +777,7 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
         // escapes of the block (their bins are coded above): list them
         if (__builtin_expect(any_esc != 0, 0)) {
 #pragma unroll
-          for (int u = kEncSB - 1; u >= 0; --u)
+          for (int u = SB - 1; u >= 0; --u)
             if (any_esc & (1u << u)) enc_escapes(r[u], esc_list, n_esc, lane);
         }
         __syncthreads();
@@ -787,7 +793,7 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
       for (int j = nblk - 1; j >= 0; --j) {
         if (j > 0) {  // mappers: block j - 1 while the coder codes block j
 #pragma unroll
-          for (int e = 0; e < kEncPer; ++e) {
+          for (int e = 0; e < kPer; ++e) {
             ca[e] = na[e];
             cb[e] = nb[e];
             cm[e] = nm[e];
@@ -1724,12 +1730,23 @@ bool fit_stage(const gaans_tables* t, int64_t P, int64_t per_table, int64_t per_
   return false;
 }
 
-// Encoder: metadata and both entry words per symbol.
-Stage plan_encode(const gaans_tables* t, int64_t P, int64_t BK, const DevLds& d) {
-  Stage s{0, 0, 0, 0};
+// Encoder: metadata and both entry words per symbol; 8-step blocks, else
+// 4-step blocks (half the records) for each workgroups-per-CU count.
+struct EncPlan {
+  Stage st;
+  int sb;
+  size_t lds;
+};
+
+EncPlan plan_encode(const gaans_tables* t, int64_t P, int64_t BK, const DevLds& d) {
   for (int64_t occ = occ_target(BK, d, 4); occ >= 1; --occ)
-    if (fit_stage(t, P, 16, 8, 0, lds_budget(d, occ) - kEncFixedLds, &s)) return s;
-  return Stage{0, 0, 0, 0};
+    for (int sb = 8; sb >= 4; sb -= 4) {
+      Stage s;
+      const int64_t fixed = enc_fixed_lds(sb);
+      if (fit_stage(t, P, 16, 8, 0, lds_budget(d, occ) - fixed, &s))
+        return EncPlan{s, sb, (size_t)(fixed + 16 * (int64_t)s.nt_cap + 8 * (int64_t)s.ne_cap)};
+    }
+  return EncPlan{Stage{0, 0, 0, 0}, 8, (size_t)enc_fixed_lds(8)};
 }
 
 // Decoder: lookups and metadata per table; sub-blocks when they are staged
@@ -1800,7 +1817,8 @@ int encode_stage1(bool latents, void* stream, const int32_t* symbols, const floa
   uint8_t* w = static_cast<uint8_t*>(ws);
   DevLds dl;
   if ((rc = device_lds(&dl))) return rc;
-  const Stage st = plan_encode(tables, P, L.BK, dl);
+  const EncPlan plan = plan_encode(tables, P, L.BK, dl);
+  const Stage& st = plan.st;
   EncArgs a;
   a.symbols = symbols;
   a.y = y;
@@ -1831,7 +1849,7 @@ int encode_stage1(bool latents, void* stream, const int32_t* symbols, const floa
   a.esc_raw = reinterpret_cast<uint32_t*>(w + L.o_esc_raw);
   a.ctrl = static_cast<uint32_t*>(ctrl);
   a.info_out = info_out;
-  const size_t lds = kEncFixedLds + 16 * (size_t)st.nt_cap + 8 * (size_t)st.ne_cap;
+  const size_t lds = plan.lds;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid((uint32_t)L.BK), block(kThreads);
   auto launch = [&](auto kernel) -> int {
@@ -1840,8 +1858,12 @@ int encode_stage1(bool latents, void* stream, const int32_t* symbols, const floa
     kernel<<<grid, block, lds, s>>>(a);
     return check_launch("encode");
   };
-  if (latents) return indexes ? launch(k_encode<true, false>) : launch(k_encode<true, true>);
-  return indexes ? launch(k_encode<false, false>) : launch(k_encode<false, true>);
+  if (plan.sb == 4) {
+    if (latents) return indexes ? launch(k_encode<true, false, 4>) : launch(k_encode<true, true, 4>);
+    return indexes ? launch(k_encode<false, false, 4>) : launch(k_encode<false, true, 4>);
+  }
+  if (latents) return indexes ? launch(k_encode<true, false, 8>) : launch(k_encode<true, true, 8>);
+  return indexes ? launch(k_encode<false, false, 8>) : launch(k_encode<false, true, 8>);
 }
 
 int decode_impl(bool latents, void* stream, const uint8_t* payload, int64_t payload_bytes,
