@@ -63,8 +63,9 @@ def read_traffic(kernel_key: str):
     return None
 
 
-def kernel_times(L, _native, torch, backend, w, dev, reps=20):
-    """Event-timed encode / decode kernels of one workload (median, seconds)."""
+def kernel_times(L, _native, torch, backend, w, dev, reps=40):
+    """Event-timed encode / decode kernels of one workload (median over
+    batches of back-to-back launches, seconds per launch)."""
     import statistics
 
     B, N, C, P = w.batch, w.n, w.channels, w.p_ch
@@ -99,13 +100,14 @@ def kernel_times(L, _native, torch, backend, w, dev, reps=20):
             fn()
         torch.cuda.synchronize()
         ts = []
-        for _ in range(reps):
+        for _ in range(reps // 5):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(stream)
-            fn()
+            for _ in range(5):  # back-to-back launches, as in event_time
+                fn()
             e1.record(stream)
             e1.synchronize()
-            ts.append(e0.elapsed_time(e1) * 1e-3)
+            ts.append(e0.elapsed_time(e1) * 1e-3 / 5)
         res[name] = statistics.median(ts)
     torch.cuda.synchronize()
     assert int(status[0].item()) == 0 and torch.equal(out, sym)
@@ -177,18 +179,23 @@ def main():
     stream = torch.cuda.current_stream(dev)
     torch.cuda.synchronize()
 
-    def event_time(launch, reps=200):
+    def event_time(launch, reps=200, batch=20):
+        """Average kernel duration: HIP events on the launch stream around
+        batches of back-to-back launches (the kernels only read their inputs,
+        so consecutive launches are independent); median over batches and
+        the overall average, in seconds."""
         for _ in range(10):
             launch()
         torch.cuda.synchronize()
         times = []
-        for _ in range(reps):
+        for _ in range(reps // batch):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(stream)
-            launch()
+            for _ in range(batch):
+                launch()
             e1.record(stream)
             e1.synchronize()
-            times.append(e0.elapsed_time(e1) * 1e-3)
+            times.append(e0.elapsed_time(e1) * 1e-3 / batch)
         return statistics.median(times), sum(times) / len(times)
 
     def launch_decode():

@@ -111,12 +111,14 @@ int gaans_tables_bytes(const int32_t* cdfs, const int32_t* cdf_sizes, int32_t M,
 
 /* Validate CompressAI-style tables (cdfs [M, Lmax] int32 row-major, rows
  * zero-padded beyond cdf_sizes[t]; cdf[0] = 0, cdf[S-1] = 65536, strictly
- * increasing) and lay them out for the kernels: per-table metadata, packed
- * (start, freq-1) entries with the encoder's division constant, a 256-bucket
- * decode lookup per table and an exact 256-value block for each bucket in
- * which two or more symbols start.  The
- * caller copies `out` to device memory unchanged and stores its address in
- * desc->dev.  Replaces the reference's use of the raw tensors at
+ * increasing; 1 <= M <= 65536 tables of 2 <= S <= 65536 entries) and lay
+ * them out for the kernels: per-table metadata, packed (start, freq-1)
+ * entries with the encoder's division constant, a 256-bucket decode lookup
+ * per table, and for each bucket in which two or more symbols start a
+ * 16-entry second-level lookup (16-value sub-ranges), with a 16-entry
+ * third level (single values) for each such sub-range.  The caller copies
+ * `out` to device memory unchanged and stores its address in desc->dev.
+ * Replaces the reference's use of the raw tensors at
  * src/fast_compressai/coders/factorized.py:23-31. */
 int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes,
                          const int32_t* offsets, int32_t M, int32_t Lmax,
