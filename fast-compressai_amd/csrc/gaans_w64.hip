@@ -411,6 +411,37 @@ __device__ __forceinline__ void stage_range(int nt_cap, int stage_all, int k, in
   }
 }
 
+// Input modes of the coding kernels.
+constexpr int kModeSymbols = 0;   // int32 symbols; indexes given or table = channel
+constexpr int kModeLatents = 1;   // fp32 latents, per-channel medians; indexes as above
+constexpr int kModeGaussian = 2;  // fp32 latents, per-element means (optional) and scales
+
+// CompressAI's GaussianConditional.build_indexes for one scale s (the
+// third-party algorithm, restated in the oracle): lb = max(s, bound) (NaN
+// propagates, as torch.max does), index =
+// (L - 1) - #{k < L - 1 : lb <= table[k]}.  For a non-decreasing table that is
+// #{k < L - 1 : table[k] < lb}, found by a fixed-step binary search over the
+// table in LDS (pow2 = the largest power of two <= L - 1); NaN -> L - 1.
+__device__ __forceinline__ int32_t gauss_index(float s, const float* tab, int L, int pow2,
+                                               float bound) {
+  const float lb = s < bound ? bound : s;
+  int pos = 0;
+  for (int step = pow2; step > 0; step >>= 1) {
+    const int i = pos + step - 1;
+    const float t = tab[i < L - 2 ? i : L - 2];
+    pos += (pos + step <= L - 1 && t < lb) ? step : 0;
+  }
+  return lb != lb ? L - 1 : pos;
+}
+
+// Stage the scale table (L floats) into LDS with the whole workgroup; the
+// caller's next barrier publishes it.
+template <int NT>
+__device__ __forceinline__ void stage_scales(float* dst, const float* __restrict__ src, int L,
+                                             int tid) {
+  for (int i = tid; i < L; i += NT) dst[i] = src[i];
+}
+
 // ============================================================================
 // Encoder
 // ============================================================================
@@ -419,6 +450,12 @@ struct EncArgs {
   const int32_t* __restrict__ symbols;
   const float* __restrict__ y;
   const float* __restrict__ medians;
+  const float* __restrict__ means;        // Gaussian: per element, or NULL
+  const float* __restrict__ scales;       // Gaussian: per element
+  const float* __restrict__ scale_table;  // Gaussian: L non-decreasing scales
+  int32_t n_scales, scales_pow2;
+  float scale_bound;
+  uint32_t scales_lds;  // LDS byte offset of the staged scale table
   const int32_t* __restrict__ indexes;
   const uint8_t* __restrict__ tables;
   uint32_t M, tables_bytes;
@@ -538,7 +575,7 @@ __device__ void encode_finish(const EncArgs& a, int tid, uint64_t* sh) {
 // added to znib).  v is computed in 32-bit arithmetic; when sym - offset
 // overflows int32 the sign of sym tells the side and raw = 2 (v - maxv)
 // (wrapped) is exact whenever raw < 2^32, else the symbol is uncodable.
-template <bool kLatents, bool kImplicit>
+template <int kMode, bool kImplicit>
 __device__ __forceinline__ uint4 enc_record(const EncArgs& a, const Tabs& tb, bool lds, int lane,
                                             int t, int len, int32_t start, int32_t in_a,
                                             int32_t in_b, float in_m, uint32_t& hash,
@@ -552,7 +589,7 @@ __device__ __forceinline__ uint4 enc_record(const EncArgs& a, const Tabs& tb, bo
   tbi = ok ? tbi : (lds ? tb.t_lo : 0);
   hash += ok ? ((uint32_t)(tbi + 1) ^ ((uint32_t)p * kHashMul)) : 0u;
   int32_t sym;
-  if (kLatents) {
+  if (kMode != kModeSymbols) {
     const float r = rintf(__fsub_rn(__int_as_float(in_a), in_m));
     const bool rng = !(fabsf(r) < 2147483648.0f);
     status |= (ok & rng) ? GAANS_ST_RANGE : 0u;
@@ -637,7 +674,7 @@ __device__ __forceinline__ void enc_escapes(const uint4 r, uint32_t* __restrict_
   cnt = uni(cnt + __popcll(em));
 }
 
-template <bool kLatents, bool kImplicit, int SB>
+template <int kMode, bool kImplicit, int SB>
 __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
   using G = EncGeom<SB>;
   constexpr int kPer = G::kPer;
@@ -648,6 +685,7 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
   uint32_t* part = eflag + G::kFlagBytes / 4;  // per-wave hash, status, escape nibbles
   uint4* lmeta = reinterpret_cast<uint4*>(smem + G::kFixed);
   uint2* lent = reinterpret_cast<uint2*>(smem + G::kFixed + 16 * a.nt_cap);
+  float* scl = reinterpret_cast<float*>(smem + a.scales_lds);  // Gaussian: scale table
 
   const int64_t g = blockIdx.x;
   const int tid = threadIdx.x;
@@ -684,6 +722,7 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
     tb.lsub = nullptr;
     int t_lo, t_hi;
     stage_range(a.nt_cap, a.stage_all, k, a.P, (int)a.M, t_lo, t_hi);
+    if (kMode == kModeGaussian) stage_scales<kThreads>(scl, a.scale_table, a.n_scales, tid);
     stage_tables<kThreads>(tb, lmeta, lent, nullptr, nullptr, 0u, a.M, t_lo, t_hi, tid);
 
     // mapper wave w (1..kMappers) owns steps u = w - 1 + kMappers e of every block
@@ -697,14 +736,20 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
         int p = lane + kLanes * (j * SB + u);
         p = p < len ? p : len - 1;  // loads stay in the chunk; results are masked
         const int64_t i = row + start + p;
-        if (kLatents) {
+        if (kMode == kModeGaussian) {
           ia[e] = __float_as_int(a.y[i]);
-          im[e] = a.medians[udiv((uint32_t)(start + p), a.div_hw)];
+          im[e] = a.means ? a.means[i] : 0.0f;
+          ib[e] = __float_as_int(a.scales[i]);  // the index is found when the block is mapped
         } else {
-          ia[e] = a.symbols[i];
-          im[e] = 0.0f;
+          if (kMode == kModeLatents) {
+            ia[e] = __float_as_int(a.y[i]);
+            im[e] = a.medians[udiv((uint32_t)(start + p), a.div_hw)];
+          } else {
+            ia[e] = a.symbols[i];
+            im[e] = 0.0f;
+          }
+          ib[e] = kImplicit ? 0 : a.indexes[i];
         }
-        ib[e] = kImplicit ? 0 : a.indexes[i];
       }
     };
     auto map_steps = [&](int j, auto lds_tag) {
@@ -714,9 +759,8 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
       for (int e = 0; e < kPer; ++e) {
         const int u = (wid - 1) + kMappers * e;
         if (SB % kMappers != 0 && u >= SB) break;
-        const uint4 r = enc_record<kLatents, kImplicit>(a, tb, kLds, lane, j * SB + u, len,
-                                                        start, ca[e], cb[e], cm[e], hash, status,
-                                                        znib);
+        const uint4 r = enc_record<kMode, kImplicit>(a, tb, kLds, lane, j * SB + u, len, start,
+                                                     ca[e], cb[e], cm[e], hash, status, znib);
         dst[u * kLanes + lane] = r;
         if (ballot((r.z & 256u) != 0u) != 0ull && lane == 0)
           __hip_atomic_fetch_or(&eflag[j & 1], 1u << u, __ATOMIC_RELAXED,
@@ -724,6 +768,12 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
       }
     };
     auto map_block = [&](int j) {
+      if (kMode == kModeGaussian) {
+#pragma unroll
+        for (int e = 0; e < kPer; ++e)
+          cb[e] = gauss_index(__int_as_float(cb[e]), scl, a.n_scales, a.scales_pow2,
+                              a.scale_bound);
+      }
       // LDS tables for the whole block when every active lane's table is staged
       bool lds = tb.nt > 0;
       if (!kImplicit && lds) {
@@ -985,6 +1035,12 @@ struct DecArgs {
   const uint8_t* __restrict__ tables;
   uint32_t M, tables_bytes;
   const float* __restrict__ medians;
+  const float* __restrict__ means;        // Gaussian: per element, or NULL
+  const float* __restrict__ scales;       // Gaussian: per element
+  const float* __restrict__ scale_table;  // Gaussian: L non-decreasing scales
+  int32_t n_scales, scales_pow2;
+  float scale_bound;
+  uint32_t scales_lds;  // LDS byte offset of the staged scale table
   int32_t* __restrict__ out_sym;
   float* __restrict__ out_y;
   int64_t N, header_bytes, BK;
@@ -1299,8 +1355,9 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint2 r, uint
   return (uint32_t)(oob ? 0 : o);
 }
 
-template <bool kLatents, bool kImplicit, int SB>
+template <int kMode, bool kImplicit, int SB>
 __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
+  constexpr bool kLatents = kMode != kModeSymbols;  // fp32 output with a per-element add
   using G = DecGeom<SB>;
   constexpr int kPer = G::kPer;
   constexpr int R = G::kEscR;
@@ -1319,6 +1376,7 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   uint4* lmeta = reinterpret_cast<uint4*>(tsm + 8 * kLutSize * a.nt_cap);
   // [luts][meta][sub-blocks]: every part 16-byte aligned
   uint64_t* lsub = reinterpret_cast<uint64_t*>(tsm + (8 * kLutSize + 16) * a.nt_cap);
+  float* scl = reinterpret_cast<float*>(smem + a.scales_lds);  // Gaussian: scale table
 
   const int64_t g = blockIdx.x;
   const int tid = threadIdx.x;
@@ -1386,8 +1444,13 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
         if (SB % kMappers != 0 && u >= SB) break;
         int p = lane + kLanes * (j * SB + u);
         p = p < len ? p : len - 1;  // loads stay in the chunk; results are masked
-        ib[e] = kImplicit ? 0 : a.indexes[row + start + p];
-        im[e] = kLatents ? a.medians[udiv((uint32_t)(start + p), a.div_hw)] : 0.0f;
+        if (kMode == kModeGaussian) {
+          ib[e] = __float_as_int(a.scales[row + start + p]);  // index found at map time
+          im[e] = a.means ? a.means[row + start + p] : 0.0f;
+        } else {
+          ib[e] = kImplicit ? 0 : a.indexes[row + start + p];
+          im[e] = kLatents ? a.medians[udiv((uint32_t)(start + p), a.div_hw)] : 0.0f;
+        }
       }
     };
     // decoded values of block j -> HBM, escapes resolved first
@@ -1424,7 +1487,11 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
         const int u = (wid - 1) + kMappers * e;
         if (SB % kMappers != 0 && u >= SB) break;
         bool all_lds;
-        const uint2 r = dec_record<kImplicit>(a, tb, lane, j * SB + u, len, start, cbx[e], hash,
+        const int32_t ix = kMode == kModeGaussian
+                               ? gauss_index(__int_as_float(cbx[e]), scl, a.n_scales,
+                                             a.scales_pow2, a.scale_bound)
+                               : cbx[e];
+        const uint2 r = dec_record<kImplicit>(a, tb, lane, j * SB + u, len, start, ix, hash,
                                               status, all_lds);
         dst[u * kLanes + lane] = r;
         if (kLatents) med[((j & 1) * SB + u) * kLanes + lane] = cm[e];
@@ -1471,6 +1538,7 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
       if (nblk > 1) load_block(1, nbx, nm);
     }
     if (tid < 8) ctl[tid] = tid == 1 ? kAllAvail : 0u;
+    if (kMode == kModeGaussian) stage_scales<kDecThreads>(scl, a.scale_table, a.n_scales, tid);
     int t_lo, t_hi;
     stage_range(a.nt_cap, a.stage_all, k, (int)a.P, (int)a.M, t_lo, t_hi);
     stage_tables<kDecThreads>(tb, lmeta, nullptr, llut, a.nd_cap ? lsub : nullptr,
@@ -1711,7 +1779,7 @@ int64_t occ_target(int64_t BK, const DevLds& d, int64_t max_occ) {
 // Tables staged in `budget` bytes (per table, per symbol entry and per dense
 // block costs): false if not even the chunk's range fits.
 bool fit_stage(const gaans_tables* t, int64_t P, int64_t per_table, int64_t per_sym,
-               int64_t per_dense, int64_t budget, Stage* s) {
+               int64_t per_dense, int64_t budget, Stage* s, bool range_ok = true) {
   const int64_t all = t->M * per_table + per_sym * t->total_nsym + per_dense * t->total_dense;
   const int64_t range = P * (per_table + per_sym * (int64_t)t->max_nsym +
                              per_dense * (int64_t)t->max_dense);
@@ -1722,7 +1790,7 @@ bool fit_stage(const gaans_tables* t, int64_t P, int64_t per_table, int64_t per_
                per_dense ? (int32_t)t->total_dense : 0, 1};
     return true;
   }
-  if (range <= budget) {
+  if (range_ok && range <= budget) {
     *s = Stage{(int32_t)P, per_sym ? (int32_t)(P * t->max_nsym) : 0,
                per_dense ? (int32_t)(P * t->max_dense) : 0, 0};
     return true;
@@ -1738,12 +1806,16 @@ struct EncPlan {
   size_t lds;
 };
 
-EncPlan plan_encode(const gaans_tables* t, int64_t P, int64_t BK, const DevLds& d) {
+// `extra` LDS bytes follow the tables (the Gaussian mode's scale table);
+// range_ok is false when any table may serve any position (per-element
+// indexes computed from scales), so only all tables or none are staged.
+EncPlan plan_encode(const gaans_tables* t, int64_t P, int64_t BK, const DevLds& d,
+                    int64_t extra = 0, bool range_ok = true) {
   for (int64_t occ = occ_target(BK, d, 4); occ >= 1; --occ)
     for (int sb = 8; sb >= 4; sb -= 4) {
       Stage s;
       const int64_t fixed = enc_fixed_lds(sb);
-      if (fit_stage(t, P, 16, 8, 0, lds_budget(d, occ) - fixed, &s))
+      if (fit_stage(t, P, 16, 8, 0, lds_budget(d, occ) - fixed - extra, &s, range_ok))
         return EncPlan{s, sb, (size_t)(fixed + 16 * (int64_t)s.nt_cap + 8 * (int64_t)s.ne_cap)};
     }
   return EncPlan{Stage{0, 0, 0, 0}, 8, (size_t)enc_fixed_lds(8)};
@@ -1763,7 +1835,7 @@ struct DecPlan {
 };
 
 DecPlan plan_decode(const gaans_tables* t, int64_t P, int64_t BK, bool latents,
-                    const DevLds& d) {
+                    const DevLds& d, int64_t extra = 0, bool range_ok = true) {
   const int64_t per_table = 8 * kLutSize + 16;
   const bool has_dense = t->total_dense > 0;
   for (int64_t occ = occ_target(BK, d, 3); occ >= 1; --occ) {
@@ -1774,7 +1846,7 @@ DecPlan plan_decode(const gaans_tables* t, int64_t P, int64_t BK, bool latents,
       if (!dense && !has_dense) break;  // same as the options already tried
       Stage s;
       const int64_t fixed = dec_fixed_lds(latents, sb);
-      if (fit_stage(t, P, per_table, 0, dense ? kSubBytes : 0, cap - fixed, &s))
+      if (fit_stage(t, P, per_table, 0, dense ? kSubBytes : 0, cap - fixed - extra, &s, range_ok))
         return DecPlan{s, sb, (size_t)(fixed + per_table * s.nt_cap + kSubBytes * (int64_t)s.nd_cap)};
     }
   }
@@ -1801,15 +1873,42 @@ int allow_lds(const void* kernel, size_t bytes, const DevLds& d) {
   return GAANS_OK;
 }
 
-int encode_stage1(bool latents, void* stream, const int32_t* symbols, const float* y,
-                  const float* medians, const int32_t* indexes, const gaans_tables* tables,
-                  int64_t B, int64_t N, int64_t C, int64_t P, void* ws, int64_t ws_bytes,
-                  void* ctrl, uint64_t* info_out) {
+// Gaussian-mode inputs (CompressAI GaussianConditional with a scale table).
+struct GaussIn {
+  const float* means;   // per element, or NULL
+  const float* scales;  // per element
+  const float* table;   // n non-decreasing scales (device memory)
+  int32_t n;
+  float bound;
+};
+
+// Scale-table entries: the table is staged in LDS beside the coding tables.
+constexpr int32_t kMaxScales = 8192;
+
+int check_gauss(const GaussIn* g) {
+  if (!g->scales || !g->table) return fail(GAANS_EINVAL, "scales or scale table pointer is NULL");
+  if (g->n < 1 || g->n > kMaxScales)
+    return fail(GAANS_EINVAL, "scale table of %d entries outside [1, %d]", g->n, kMaxScales);
+  return GAANS_OK;
+}
+
+int32_t pow2_floor(int32_t v) {  // largest power of two <= v (0 for v < 1)
+  int32_t p = 0;
+  while (v > 0 && (p == 0 || ((int64_t)p << 1) <= v)) p = p ? p << 1 : 1;
+  return p;
+}
+
+int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y,
+                  const float* medians, const int32_t* indexes, const GaussIn* g,
+                  const gaans_tables* tables, int64_t B, int64_t N, int64_t C, int64_t P,
+                  void* ws, int64_t ws_bytes, void* ctrl, uint64_t* info_out) {
   Layout L;
   int rc = make_layout(B, N, C, P, &L);
   if (rc) return rc;
   if ((rc = check_tables_arg(tables))) return rc;
-  if (latents ? (!y || !medians) : !symbols) return fail(GAANS_EINVAL, "input pointer is NULL");
+  if (mode == kModeSymbols ? !symbols : (!y || (mode == kModeLatents && !medians)))
+    return fail(GAANS_EINVAL, "input pointer is NULL");
+  if (mode == kModeGaussian && (rc = check_gauss(g))) return rc;
   if (!ctrl) return fail(GAANS_EINVAL, "control block pointer is NULL");
   if (!ws || ws_bytes < L.ws_bytes)
     return fail(GAANS_EINVAL, "workspace too small (%lld < %lld bytes)", (long long)ws_bytes,
@@ -1817,13 +1916,21 @@ int encode_stage1(bool latents, void* stream, const int32_t* symbols, const floa
   uint8_t* w = static_cast<uint8_t*>(ws);
   DevLds dl;
   if ((rc = device_lds(&dl))) return rc;
-  const EncPlan plan = plan_encode(tables, P, L.BK, dl);
+  const int64_t extra = mode == kModeGaussian ? align_up(4 * (int64_t)g->n, 16) : 0;
+  const EncPlan plan = plan_encode(tables, P, L.BK, dl, extra, mode != kModeGaussian);
   const Stage& st = plan.st;
   EncArgs a;
   a.symbols = symbols;
   a.y = y;
   a.medians = medians;
-  a.indexes = indexes;
+  a.means = mode == kModeGaussian ? g->means : nullptr;
+  a.scales = mode == kModeGaussian ? g->scales : nullptr;
+  a.scale_table = mode == kModeGaussian ? g->table : nullptr;
+  a.n_scales = mode == kModeGaussian ? g->n : 0;
+  a.scales_pow2 = mode == kModeGaussian ? pow2_floor(g->n - 1) : 0;
+  a.scale_bound = mode == kModeGaussian ? g->bound : 0.0f;
+  a.scales_lds = (uint32_t)plan.lds;
+  a.indexes = mode == kModeGaussian ? nullptr : indexes;
   a.tables = static_cast<const uint8_t*>(tables->dev);
   a.M = (uint32_t)tables->M;
   a.tables_bytes = (uint32_t)tables->bytes;
@@ -1849,7 +1956,10 @@ int encode_stage1(bool latents, void* stream, const int32_t* symbols, const floa
   a.esc_raw = reinterpret_cast<uint32_t*>(w + L.o_esc_raw);
   a.ctrl = static_cast<uint32_t*>(ctrl);
   a.info_out = info_out;
-  const size_t lds = plan.lds;
+  const size_t lds = plan.lds + (size_t)extra;
+  if (lds > (size_t)dl.per_block)
+    return fail(GAANS_EINVAL, "encode needs %zu bytes of LDS, the device has %d", lds,
+                dl.per_block);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid((uint32_t)L.BK), block(kThreads);
   auto launch = [&](auto kernel) -> int {
@@ -1858,40 +1968,61 @@ int encode_stage1(bool latents, void* stream, const int32_t* symbols, const floa
     kernel<<<grid, block, lds, s>>>(a);
     return check_launch("encode");
   };
+  const bool imp = indexes == nullptr;
   if (plan.sb == 4) {
-    if (latents) return indexes ? launch(k_encode<true, false, 4>) : launch(k_encode<true, true, 4>);
-    return indexes ? launch(k_encode<false, false, 4>) : launch(k_encode<false, true, 4>);
+    switch (mode) {
+      case kModeGaussian: return launch(k_encode<kModeGaussian, false, 4>);
+      case kModeLatents:
+        return imp ? launch(k_encode<kModeLatents, true, 4>) : launch(k_encode<kModeLatents, false, 4>);
+      default:
+        return imp ? launch(k_encode<kModeSymbols, true, 4>) : launch(k_encode<kModeSymbols, false, 4>);
+    }
   }
-  if (latents) return indexes ? launch(k_encode<true, false, 8>) : launch(k_encode<true, true, 8>);
-  return indexes ? launch(k_encode<false, false, 8>) : launch(k_encode<false, true, 8>);
+  switch (mode) {
+    case kModeGaussian: return launch(k_encode<kModeGaussian, false, 8>);
+    case kModeLatents:
+      return imp ? launch(k_encode<kModeLatents, true, 8>) : launch(k_encode<kModeLatents, false, 8>);
+    default:
+      return imp ? launch(k_encode<kModeSymbols, true, 8>) : launch(k_encode<kModeSymbols, false, 8>);
+  }
 }
 
-int decode_impl(bool latents, void* stream, const uint8_t* payload, int64_t payload_bytes,
-                const int32_t* indexes, const gaans_tables* tables, const float* medians,
-                int64_t B, int64_t N, int64_t C, int64_t P, int32_t* out_sym, float* out_y,
-                void* ctrl, uint32_t* status_out) {
+int decode_impl(int mode, void* stream, const uint8_t* payload, int64_t payload_bytes,
+                const int32_t* indexes, const GaussIn* g, const gaans_tables* tables,
+                const float* medians, int64_t B, int64_t N, int64_t C, int64_t P,
+                int32_t* out_sym, float* out_y, void* ctrl, uint32_t* status_out) {
   Layout L;
   int rc = make_layout(B, N, C, P, &L);
   if (rc) return rc;
   if ((rc = check_tables_arg(tables))) return rc;
-  if (!payload || !status_out || !ctrl || (latents ? (!out_y || !medians) : !out_sym))
+  if (!payload || !status_out || !ctrl ||
+      (mode == kModeSymbols ? !out_sym : (!out_y || (mode == kModeLatents && !medians))))
     return fail(GAANS_EINVAL, "payload, output, control or status pointer is NULL");
+  if (mode == kModeGaussian && (rc = check_gauss(g))) return rc;
   if (payload_bytes < L.header_bytes)
     return fail(GAANS_EINVAL, "payload (%lld bytes) is shorter than its header (%lld bytes)",
                 (long long)payload_bytes, (long long)L.header_bytes);
   DevLds dl;
   if ((rc = device_lds(&dl))) return rc;
-  // entry words are read only by dense-bucket lookups
-  const DecPlan plan = plan_decode(tables, P, L.BK, latents, dl);
+  const bool latents = mode != kModeSymbols;
+  const int64_t extra = mode == kModeGaussian ? align_up(4 * (int64_t)g->n, 16) : 0;
+  const DecPlan plan = plan_decode(tables, P, L.BK, latents, dl, extra, mode != kModeGaussian);
   const Stage& st = plan.st;
   DecArgs a;
   a.payload = payload;
   a.payload_bytes = payload_bytes;
-  a.indexes = indexes;
+  a.indexes = mode == kModeGaussian ? nullptr : indexes;
   a.tables = static_cast<const uint8_t*>(tables->dev);
   a.M = (uint32_t)tables->M;
   a.tables_bytes = (uint32_t)tables->bytes;
   a.medians = medians;
+  a.means = mode == kModeGaussian ? g->means : nullptr;
+  a.scales = mode == kModeGaussian ? g->scales : nullptr;
+  a.scale_table = mode == kModeGaussian ? g->table : nullptr;
+  a.n_scales = mode == kModeGaussian ? g->n : 0;
+  a.scales_pow2 = mode == kModeGaussian ? pow2_floor(g->n - 1) : 0;
+  a.scale_bound = mode == kModeGaussian ? g->bound : 0.0f;
+  a.scales_lds = (uint32_t)plan.lds;
   a.out_sym = out_sym;
   a.out_y = out_y;
   a.N = N;
@@ -1909,7 +2040,10 @@ int decode_impl(bool latents, void* stream, const uint8_t* payload, int64_t payl
   a.stage_all = st.stage_all;
   a.ctrl = static_cast<uint32_t*>(ctrl);
   a.status_out = status_out;
-  const size_t lds = plan.lds;
+  const size_t lds = plan.lds + (size_t)extra;
+  if (lds > (size_t)dl.per_block)
+    return fail(GAANS_EINVAL, "decode needs %zu bytes of LDS, the device has %d", lds,
+                dl.per_block);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid((uint32_t)L.BK), block(kDecThreads);
   auto launch = [&](auto kernel) -> int {
@@ -1918,12 +2052,23 @@ int decode_impl(bool latents, void* stream, const uint8_t* payload, int64_t payl
     kernel<<<grid, block, lds, s>>>(a);
     return check_launch("decode");
   };
+  const bool imp = indexes == nullptr;
   if (plan.sb == 4) {
-    if (latents) return indexes ? launch(k_decode<true, false, 4>) : launch(k_decode<true, true, 4>);
-    return indexes ? launch(k_decode<false, false, 4>) : launch(k_decode<false, true, 4>);
+    switch (mode) {
+      case kModeGaussian: return launch(k_decode<kModeGaussian, false, 4>);
+      case kModeLatents:
+        return imp ? launch(k_decode<kModeLatents, true, 4>) : launch(k_decode<kModeLatents, false, 4>);
+      default:
+        return imp ? launch(k_decode<kModeSymbols, true, 4>) : launch(k_decode<kModeSymbols, false, 4>);
+    }
   }
-  if (latents) return indexes ? launch(k_decode<true, false, 8>) : launch(k_decode<true, true, 8>);
-  return indexes ? launch(k_decode<false, false, 8>) : launch(k_decode<false, true, 8>);
+  switch (mode) {
+    case kModeGaussian: return launch(k_decode<kModeGaussian, false, 8>);
+    case kModeLatents:
+      return imp ? launch(k_decode<kModeLatents, true, 8>) : launch(k_decode<kModeLatents, false, 8>);
+    default:
+      return imp ? launch(k_decode<kModeSymbols, true, 8>) : launch(k_decode<kModeSymbols, false, 8>);
+  }
 }
 
 uint64_t fnv_u32(uint64_t h, uint32_t v) {
@@ -2148,16 +2293,26 @@ int gaans_encode_symbols(void* stream, const int32_t* symbols_dev, const int32_t
                          const gaans_tables* tables, int64_t B, int64_t N, int64_t C, int64_t P,
                          void* workspace_dev, int64_t workspace_bytes, void* ctrl_dev,
                          uint64_t* info_out) {
-  return encode_stage1(false, stream, symbols_dev, nullptr, nullptr, indexes_dev, tables, B, N,
-                       C, P, workspace_dev, workspace_bytes, ctrl_dev, info_out);
+  return encode_stage1(kModeSymbols, stream, symbols_dev, nullptr, nullptr, indexes_dev, nullptr,
+                       tables, B, N, C, P, workspace_dev, workspace_bytes, ctrl_dev, info_out);
 }
 
 int gaans_encode_latents(void* stream, const float* y_dev, const float* medians_dev,
                          const int32_t* indexes_dev, const gaans_tables* tables, int64_t B,
                          int64_t N, int64_t C, int64_t P, void* workspace_dev,
                          int64_t workspace_bytes, void* ctrl_dev, uint64_t* info_out) {
-  return encode_stage1(true, stream, nullptr, y_dev, medians_dev, indexes_dev, tables, B, N, C,
-                       P, workspace_dev, workspace_bytes, ctrl_dev, info_out);
+  return encode_stage1(kModeLatents, stream, nullptr, y_dev, medians_dev, indexes_dev, nullptr,
+                       tables, B, N, C, P, workspace_dev, workspace_bytes, ctrl_dev, info_out);
+}
+
+int gaans_encode_gaussian(void* stream, const float* y_dev, const float* means_dev,
+                          const float* scales_dev, const float* scale_table_dev,
+                          int32_t n_scales, float scale_bound, const gaans_tables* tables,
+                          int64_t B, int64_t N, int64_t C, int64_t P, void* workspace_dev,
+                          int64_t workspace_bytes, void* ctrl_dev, uint64_t* info_out) {
+  const GaussIn g{means_dev, scales_dev, scale_table_dev, n_scales, scale_bound};
+  return encode_stage1(kModeGaussian, stream, nullptr, y_dev, nullptr, nullptr, &g, tables, B, N,
+                       C, P, workspace_dev, workspace_bytes, ctrl_dev, info_out);
 }
 
 int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace_bytes,
@@ -2202,16 +2357,26 @@ int gaans_decode_symbols(void* stream, const uint8_t* payload_dev, int64_t paylo
                          const int32_t* indexes_dev, const gaans_tables* tables, int64_t B,
                          int64_t N, int64_t C, int64_t P, int32_t* out_dev, void* ctrl_dev,
                          uint32_t* status_out) {
-  return decode_impl(false, stream, payload_dev, payload_bytes, indexes_dev, tables, nullptr, B,
-                     N, C, P, out_dev, nullptr, ctrl_dev, status_out);
+  return decode_impl(kModeSymbols, stream, payload_dev, payload_bytes, indexes_dev, nullptr,
+                     tables, nullptr, B, N, C, P, out_dev, nullptr, ctrl_dev, status_out);
 }
 
 int gaans_decode_latents(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
                          const int32_t* indexes_dev, const gaans_tables* tables,
                          const float* medians_dev, int64_t B, int64_t N, int64_t C, int64_t P,
                          float* y_hat_dev, void* ctrl_dev, uint32_t* status_out) {
-  return decode_impl(true, stream, payload_dev, payload_bytes, indexes_dev, tables, medians_dev,
-                     B, N, C, P, nullptr, y_hat_dev, ctrl_dev, status_out);
+  return decode_impl(kModeLatents, stream, payload_dev, payload_bytes, indexes_dev, nullptr,
+                     tables, medians_dev, B, N, C, P, nullptr, y_hat_dev, ctrl_dev, status_out);
+}
+
+int gaans_decode_gaussian(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
+                          const float* scales_dev, const float* means_dev,
+                          const float* scale_table_dev, int32_t n_scales, float scale_bound,
+                          const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
+                          int64_t P, float* y_hat_dev, void* ctrl_dev, uint32_t* status_out) {
+  const GaussIn g{means_dev, scales_dev, scale_table_dev, n_scales, scale_bound};
+  return decode_impl(kModeGaussian, stream, payload_dev, payload_bytes, nullptr, &g, tables,
+                     nullptr, B, N, C, P, nullptr, y_hat_dev, ctrl_dev, status_out);
 }
 
 int gaans_wait_host_word(void* stream, const uint32_t* word) {

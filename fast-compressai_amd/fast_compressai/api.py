@@ -7,6 +7,10 @@ sample=None, coder=None, ...) -> FastModel``.  ``coder="warp_div"`` (the
 default) deep-copies a FactorizedPrior to the GPU and routes
 ``compress``/``decompress`` through the GA-ANS HIP coder with ``P`` latent
 channels per chunk; ``coder="rans"`` keeps the model's own entropy path.
+Beyond the reference (whose warp_div path accepts only FactorizedPrior,
+``api.py:177-182``), ScaleHyperprior and MeanScaleHyperprior models are
+routed too: z through the factorized path, y through the fused
+GaussianConditional kernels (``coders/hyperprior.py``).
 
 Out of scope here (mixed-precision operator selection, not the coder path):
 ``calibration_data``, ``precision_config_path`` and ``sample`` profiling;
@@ -136,6 +140,36 @@ def _is_factorized_prior(model: nn.Module) -> bool:
             and all(hasattr(eb, name) for name in _ENTROPY_CONTRACT))
 
 
+_GC_CONTRACT = ("_quantized_cdf", "_cdf_length", "_offset", "scale_table")
+
+
+def _hyperprior_kind(model: nn.Module) -> str | None:
+    """"mean_scale" for CompressAI's ``MeanScaleHyperprior``, "scale" for
+    ``ScaleHyperprior`` (exact types when CompressAI is installed; without
+    it, a model of that class name implementing its contract: ``g_a``,
+    ``g_s``, ``h_a``, ``h_s``, an EntropyBottleneck and a GaussianConditional
+    with a scale table), else None."""
+    try:
+        from compressai.models import MeanScaleHyperprior, ScaleHyperprior
+    except ImportError:
+        MeanScaleHyperprior = ScaleHyperprior = None
+    if MeanScaleHyperprior is not None:
+        if type(model) is MeanScaleHyperprior:
+            return "mean_scale"
+        return "scale" if type(model) is ScaleHyperprior else None
+    name = type(model).__name__
+    if name not in ("MeanScaleHyperprior", "ScaleHyperprior"):
+        return None
+    eb = getattr(model, "entropy_bottleneck", None)
+    gc = getattr(model, "gaussian_conditional", None)
+    if (eb is None or gc is None
+            or not all(hasattr(model, f) for f in ("g_a", "g_s", "h_a", "h_s"))
+            or not all(hasattr(eb, f) for f in _ENTROPY_CONTRACT)
+            or not all(hasattr(gc, f) for f in _GC_CONTRACT)):
+        return None
+    return "mean_scale" if name == "MeanScaleHyperprior" else "scale"
+
+
 def accelerate(
     model: nn.Module,
     P: int | None = None,
@@ -163,8 +197,11 @@ def accelerate(
     del dataset_name, precision_config_output_dir
     p_status = "explicit" if cfg.p_ch is not None else "default"
     if cfg.coder == "warp_div":
-        if not _is_factorized_prior(model):
-            raise ConfigurationError("warp_div currently supports only CompressAI FactorizedPrior")
+        hyper = None if _is_factorized_prior(model) else _hyperprior_kind(model)
+        if hyper is None and not _is_factorized_prior(model):
+            raise ConfigurationError(
+                "warp_div supports CompressAI FactorizedPrior, ScaleHyperprior and "
+                "MeanScaleHyperprior")
         if sample is not None:
             raise ConfigurationError(
                 "warp_div precision selection uses calibration_data; legacy sample profiling is unavailable")
@@ -173,11 +210,16 @@ def accelerate(
             raise ConfigurationError("warp_div requires device='cuda'")
         if not torch.cuda.is_available():
             raise ConfigurationError("warp_div requires a GPU")
-        from .coders.factorized import FactorizedWarpDivCodec
-
         runtime_model = copy.deepcopy(model).to(target).eval()
         p_ch = cfg.p_ch if cfg.p_ch is not None else 1
-        codec = FactorizedWarpDivCodec(runtime_model, p_ch)
+        if hyper is None:
+            from .coders.factorized import FactorizedWarpDivCodec
+
+            codec = FactorizedWarpDivCodec(runtime_model, p_ch)
+        else:
+            from .coders.hyperprior import HyperpriorWarpDivCodec
+
+            codec = HyperpriorWarpDivCodec(runtime_model, p_ch, mean_scale=hyper == "mean_scale")
         wrapped = FastModel(runtime_model, device=str(target))
         wrapped._coder = codec
         report = AccelerationReport(

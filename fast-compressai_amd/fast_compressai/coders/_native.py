@@ -15,7 +15,7 @@ import threading
 from .errors import CoderDependencyError
 
 LIB_NAME = "libgaans_w64.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 CTRL_BYTES = 256
 
 # return codes
@@ -82,7 +82,7 @@ _lock = threading.Lock()
 
 
 def _declare(L) -> None:
-    p, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    p, i32, i64, f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
     T = ctypes.POINTER(Tables)
     sig = {
         "gaans_abi_version": ([], ctypes.c_int),
@@ -97,6 +97,10 @@ def _declare(L) -> None:
         "gaans_decode_symbols": ([p, p, i64, p, T, i64, i64, i64, i64, p, p, p], ctypes.c_int),
         "gaans_decode_latents": ([p, p, i64, p, T, p, i64, i64, i64, i64, p, p, p],
                                  ctypes.c_int),
+        "gaans_encode_gaussian": ([p, p, p, p, p, i32, f32, T, i64, i64, i64, i64, p, i64, p, p],
+                                  ctypes.c_int),
+        "gaans_decode_gaussian": ([p, p, i64, p, p, p, i32, f32, T, i64, i64, i64, i64, p, p, p],
+                                  ctypes.c_int),
         "gaans_wait_host_word": ([p, p], ctypes.c_int),
         "gaans_host_selftest": ([], ctypes.c_int),
     }

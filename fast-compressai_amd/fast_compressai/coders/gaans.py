@@ -90,6 +90,23 @@ def _enter_device(index: int):
     return cur
 
 
+def _check_gaussian(B: int, N: int, device, scale_table: torch.Tensor,
+                    **per_element: torch.Tensor | None) -> None:
+    """The Gaussian kernels read every per-element operand at B*N positions
+    and the scale table whole: all fp32, contiguous, on the coder's device."""
+    dev = torch.device("cuda", _index(device))
+    for name, t in (("scale_table", scale_table), *per_element.items()):
+        if t is None and name == "means":
+            continue
+        if (not isinstance(t, torch.Tensor) or t.dtype != torch.float32 or t.device != dev
+                or not t.is_contiguous()):
+            raise CoderInputError(f"{name} must be a contiguous float32 tensor on {dev}")
+        if name == "scale_table" and (t.ndim != 1 or t.numel() < 1):
+            raise CoderInputError("scale_table must be a non-empty 1-D tensor")
+        if name != "scale_table" and t.numel() != B * N:
+            raise CoderInputError(f"{name} holds {t.numel()} values, expected {B * N}")
+
+
 @dataclass(frozen=True)
 class EncodedChunks:
     packed: torch.Tensor      # uint8 [payload bytes]
@@ -174,6 +191,83 @@ def decode(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int,
         if rc:
             _native.check(rc, "GA-ANS decode")
         status = int(st.status_np[1]) >> 1  # 1 | status << 1
+    finally:
+        if prev is not None:
+            torch.cuda.set_device(prev)
+    if status:
+        raise CoderInputError(f"warp_div decode failed: {_native.describe_status(status)}")
+    return out
+
+
+def encode_gaussian(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,
+                    y: torch.Tensor, scales: torch.Tensor, scale_table: torch.Tensor,
+                    scale_bound: float, means: torch.Tensor | None = None) -> EncodedChunks:
+    """GaussianConditional encode with index building and quantize fused:
+    fp32 ``y``, ``scales`` (and ``means``) [B, N] channel-major; ``scale_table``
+    fp32 on the device, non-decreasing, one entry per table."""
+    L = _native.lib()
+    lay = _native.layout(B, N, C, P)
+    _check_gaussian(B, N, device, scale_table, y=y, scales=scales, means=means)
+    index = _index(device)
+    prev = _enter_device(index)
+    try:
+        sp = torch._C._cuda_getCurrentRawStream(index)
+        st = _state(index, sp)
+        ws = st.ws(lay.workspace_bytes)
+        out = torch.empty(lay.max_payload_bytes, dtype=torch.uint8, device=ws.device)
+        st.info_np[2] = 0
+        rc = L.gaans_encode_gaussian(sp, y.data_ptr(), _ptr(means), scales.data_ptr(),
+                                     scale_table.data_ptr(), scale_table.numel(),
+                                     float(scale_bound), tables.ref, B, N, C, P, ws.data_ptr(),
+                                     ws.numel(), st.ctrl_ptr, st.info_ptr)
+        if rc:
+            _native.check(rc, "GA-ANS Gaussian encode")
+        rc = L.gaans_encode_pack(sp, ws.data_ptr(), ws.numel(), tables.ref, B, N, C, P,
+                                 out.data_ptr(), lay.max_payload_bytes)
+        if rc:
+            _native.check(rc, "GA-ANS pack")
+        rc = L.gaans_wait_host_word(sp, st.info_done)
+        if rc:
+            _native.check(rc, "GA-ANS Gaussian encode")
+        word = int(st.info_np[2])
+        total, status = word >> 16, (word >> 1) & 0x7FFF
+    finally:
+        if prev is not None:
+            torch.cuda.set_device(prev)
+    if status:
+        raise CoderInputError(f"GA-ANS encode failed: {_native.describe_status(status)}")
+    packed = out[:total]
+    if lay.max_payload_bytes - total > _CLONE_SLACK_BYTES:
+        packed = packed.clone()
+    K = lay.K
+    ends = packed[64: 64 + 4 * B * K].view(torch.uint32).view(B, K)
+    return EncodedChunks(packed, ends, lay.header_bytes, lay.chunk_len, K)
+
+
+def decode_gaussian(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int, P: int,
+                    device, *, scales: torch.Tensor, scale_table: torch.Tensor,
+                    scale_bound: float, means: torch.Tensor | None = None) -> torch.Tensor:
+    """GaussianConditional decode with index building and dequantize fused:
+    fp32 y_hat [B, N] = fp32(symbol) + mean (fp32(symbol) without means)."""
+    L = _native.lib()
+    _check_gaussian(B, N, device, scale_table, scales=scales, means=means)
+    index = _index(device)
+    prev = _enter_device(index)
+    try:
+        sp = torch._C._cuda_getCurrentRawStream(index)
+        st = _state(index, sp)
+        st.status_np[1] = 0
+        out = torch.empty((B, N), dtype=torch.float32, device=packed.device)
+        rc = L.gaans_decode_gaussian(sp, packed.data_ptr(), packed.numel(), scales.data_ptr(),
+                                     _ptr(means), scale_table.data_ptr(), scale_table.numel(),
+                                     float(scale_bound), tables.ref, B, N, C, P, out.data_ptr(),
+                                     st.ctrl_ptr, st.status_ptr)
+        if rc:
+            _native.check(rc, "GA-ANS Gaussian decode")
+        rc = L.gaans_wait_host_word(sp, st.status_done)
+        if rc:
+            _native.check(rc, "GA-ANS Gaussian decode")
+        status = int(st.status_np[1]) >> 1
     finally:
         if prev is not None:
             torch.cuda.set_device(prev)

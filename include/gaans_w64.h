@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define GAANS_ABI_VERSION 4
+#define GAANS_ABI_VERSION 5
 #define GAANS_CTRL_BYTES 256
 
 /* return codes */
@@ -151,6 +151,25 @@ int gaans_encode_latents(void* stream, const float* y_dev, const float* medians_
                          void* workspace_dev, int64_t workspace_bytes, void* ctrl_dev,
                          uint64_t* info_out);
 
+/* Stage 1 for CompressAI's GaussianConditional (mean-scale and scale
+ * hyperpriors) with its index building and quantize fused in: for every
+ * element, index = CompressAI build_indexes(scale) over the scale table
+ * (lb = max(scale, scale_bound), NaN kept; index = (n - 1) - #{k < n - 1 :
+ * lb <= scale_table[k]}), symbol = int32(rint(y - mean)) (mean = 0 when
+ * means_dev is NULL: the scale-only hyperprior).  y, means and scales are
+ * fp32 [B, C, HW]; scale_table_dev holds n_scales (1..8192) non-decreasing
+ * finite scales in device memory, one per CDF table (tables->M == n_scales
+ * for CompressAI models; an index >= M sets GAANS_ST_INDEX).  Chunks hold P
+ * latent channels.  No counterpart in the reference's coder, whose
+ * accelerate() accepts only FactorizedPrior (src/fast_compressai/api.py:177-182);
+ * it replaces CompressAI's GaussianConditional.compress (build_indexes +
+ * quantize + RansEncoder) for those models. */
+int gaans_encode_gaussian(void* stream, const float* y_dev, const float* means_dev,
+                          const float* scales_dev, const float* scale_table_dev,
+                          int32_t n_scales, float scale_bound, const gaans_tables* tables,
+                          int64_t B, int64_t N, int64_t C, int64_t P, void* workspace_dev,
+                          int64_t workspace_bytes, void* ctrl_dev, uint64_t* info_out);
+
 /* Stage 2: write the payload (header + chunks) to out_dev.  May be enqueued
  * right after stage 1 on the same stream into a buffer of
  * layout->max_payload_bytes, or after the caller has read the payload size
@@ -179,6 +198,16 @@ int gaans_decode_latents(void* stream, const uint8_t* payload_dev, int64_t paylo
                          const int32_t* indexes_dev, const gaans_tables* tables,
                          const float* medians_dev, int64_t B, int64_t N, int64_t C,
                          int64_t P, float* y_hat_dev, void* ctrl_dev, uint32_t* status_out);
+
+/* Decode a gaans_encode_gaussian payload with the same scales, means and
+ * scale table, dequantize fused: y_hat = fp32(symbol) + mean (fp32(symbol)
+ * when means_dev is NULL), written as [B, C, HW] fp32.  Replaces CompressAI's
+ * GaussianConditional.decompress (build_indexes + RansDecoder + dequantize). */
+int gaans_decode_gaussian(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
+                          const float* scales_dev, const float* means_dev,
+                          const float* scale_table_dev, int32_t n_scales, float scale_bound,
+                          const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
+                          int64_t P, float* y_hat_dev, void* ctrl_dev, uint32_t* status_out);
 
 /* ---- completion ------------------------------------------------------------ */
 

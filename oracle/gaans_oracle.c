@@ -662,3 +662,38 @@ void gaans_ref_dequantize(const int32_t* symbols, const float* medians, int32_t 
         y_hat[i] = f + medians[c];
       }
 }
+
+/* ---- GaussianConditional indexes and per-element quantize ------------------ */
+
+/* CompressAI GaussianConditional.build_indexes (third-party; the algorithm,
+ * restated): lb = max(scale, bound) elementwise with NaN propagated (torch.max),
+ * index = (L - 1) - #{k < L - 1 : lb <= table[k]}, as its loop over
+ * scale_table[:-1] subtracting (scales <= s) computes it.  No assumption on the
+ * order of the table. */
+void gaans_ref_build_indexes(const float* scales, int64_t n, const float* table, int32_t L,
+                             float bound, int32_t* indexes) {
+  for (int64_t i = 0; i < n; ++i) {
+    float s = scales[i];
+    float lb = (s != s) ? s : (s < bound ? bound : s);
+    int32_t idx = L - 1;
+    for (int32_t k = 0; k + 1 < L; ++k) idx -= (lb <= table[k]) ? 1 : 0;
+    indexes[i] = idx;
+  }
+}
+
+/* quantize(y, "symbols", means) with per-element means (NULL: none) and
+ * dequantize(symbols, means) of CompressAI's EntropyModel, elementwise. */
+void gaans_ref_quantize_elem(const float* y, const float* means, int64_t n, int32_t* symbols) {
+  for (int64_t i = 0; i < n; ++i) {
+    volatile float d = means ? y[i] - means[i] : y[i];
+    symbols[i] = (int32_t)rintf(d);
+  }
+}
+
+void gaans_ref_dequantize_elem(const int32_t* symbols, const float* means, int64_t n,
+                               float* y_hat) {
+  for (int64_t i = 0; i < n; ++i) {
+    volatile float f = (float)symbols[i];
+    y_hat[i] = means ? f + means[i] : f;
+  }
+}

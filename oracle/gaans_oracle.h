@@ -96,6 +96,15 @@ void gaans_ref_quantize(const float* y, const float* medians, int32_t B, int32_t
 void gaans_ref_dequantize(const int32_t* symbols, const float* medians, int32_t B,
                           int32_t C, int64_t HW, float* y_hat);
 
+/* CompressAI GaussianConditional.build_indexes restated (see the .c file). */
+void gaans_ref_build_indexes(const float* scales, int64_t n, const float* table, int32_t L,
+                             float bound, int32_t* indexes);
+
+/* Elementwise quantize / dequantize with optional per-element means. */
+void gaans_ref_quantize_elem(const float* y, const float* means, int64_t n, int32_t* symbols);
+void gaans_ref_dequantize_elem(const int32_t* symbols, const float* means, int64_t n,
+                               float* y_hat);
+
 #ifdef __cplusplus
 }
 #endif

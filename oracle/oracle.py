@@ -67,6 +67,9 @@ def lib():
         L.gaans_ref_decode.argtypes = [p, i64, p, i32, i32, i32, i32, p, i32, i32, p, p, p]
         L.gaans_ref_quantize.argtypes = [p, p, i32, i32, i64, p]
         L.gaans_ref_dequantize.argtypes = [p, p, i32, i32, i64, p]
+        L.gaans_ref_build_indexes.argtypes = [p, i64, p, i32, ctypes.c_float, p]
+        L.gaans_ref_quantize_elem.argtypes = [p, p, i64, p]
+        L.gaans_ref_dequantize_elem.argtypes = [p, p, i64, p]
         for name in ("rans64_ref_encode", "rans64_ref_decode", "gaans_ref_encode",
                      "gaans_ref_decode"):
             getattr(L, name).restype = ctypes.c_int
@@ -180,4 +183,32 @@ def dequantize(symbols, medians) -> np.ndarray:
     HW = int(np.prod(s.shape[2:])) if s.ndim > 2 else 1
     out = np.zeros(s.shape, dtype=np.float32)
     lib().gaans_ref_dequantize(_ptr(s), _ptr(med), B, C, HW, _ptr(out))
+    return out
+
+
+def build_indexes(scales, scale_table, bound: float) -> np.ndarray:
+    """CompressAI GaussianConditional.build_indexes (restated): int32 indexes
+    of ``scales`` (any shape) into ``scale_table``."""
+    sc = np.ascontiguousarray(scales, np.float32)
+    tab = np.ascontiguousarray(scale_table, np.float32)
+    out = np.zeros(sc.shape, np.int32)
+    lib().gaans_ref_build_indexes(_ptr(sc), sc.size, _ptr(tab), tab.size, float(bound), _ptr(out))
+    return out
+
+
+def quantize_elem(y, means=None) -> np.ndarray:
+    """int32(rint(y - means)) elementwise (CompressAI quantize, "symbols")."""
+    yy = np.ascontiguousarray(y, np.float32)
+    m = None if means is None else np.ascontiguousarray(means, np.float32)
+    out = np.zeros(yy.shape, np.int32)
+    lib().gaans_ref_quantize_elem(_ptr(yy), None if m is None else _ptr(m), yy.size, _ptr(out))
+    return out
+
+
+def dequantize_elem(symbols, means=None) -> np.ndarray:
+    """fp32(symbols) + means elementwise (CompressAI dequantize)."""
+    s = np.ascontiguousarray(symbols, np.int32)
+    m = None if means is None else np.ascontiguousarray(means, np.float32)
+    out = np.zeros(s.shape, np.float32)
+    lib().gaans_ref_dequantize_elem(_ptr(s), None if m is None else _ptr(m), s.size, _ptr(out))
     return out

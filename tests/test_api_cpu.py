@@ -116,8 +116,24 @@ def test_config_alias_and_validation():
 
 
 def test_default_coder_is_warp_div_and_requires_supported_model():
-    with pytest.raises(fast_compressai.ConfigurationError, match="warp_div currently supports only"):
+    with pytest.raises(fast_compressai.ConfigurationError,
+                       match="warp_div supports CompressAI FactorizedPrior, ScaleHyperprior"):
         fast_compressai.accelerate(CompressAIStyleMock(), P=4, device="cuda")
+
+
+def test_hyperprior_models_are_routed_to_warp_div():
+    # the stand-ins pass the model check; without a GPU the next check fails
+    from hyperprior_stub import make_hyperprior
+
+    from fast_compressai.api import _hyperprior_kind
+
+    for mean_scale in (True, False):
+        model = make_hyperprior(mean_scale=mean_scale)
+        assert _hyperprior_kind(model) == ("mean_scale" if mean_scale else "scale")
+        if not torch.cuda.is_available():
+            with pytest.raises(fast_compressai.ConfigurationError, match="requires a GPU"):
+                fast_compressai.accelerate(model, P=4, device="cuda")
+    assert _hyperprior_kind(CompressAIStyleMock()) is None
 
 
 def test_out_of_scope_options_raise():

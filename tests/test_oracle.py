@@ -366,3 +366,63 @@ def test_dequantize_matches_torch_add():
                    [-100, 100, 2**30, -(2**31), 2**31 - 1]]], np.int32)
     ref = (torch.from_numpy(s).float() + torch.from_numpy(med)[None, :, None]).numpy()
     assert np.array_equal(O.dequantize(s, med).view(np.uint32), ref.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# GaussianConditional build_indexes and elementwise quantize (restated)
+# ---------------------------------------------------------------------------
+
+SCALE_TABLE = np.exp(np.linspace(math.log(0.11), math.log(256.0), 64)).astype(np.float32)
+
+
+def test_build_indexes_matches_searchsorted_on_sorted_tables():
+    # for a sorted table, (L - 1) - #{k < L - 1 : lb <= t_k} = #{k < L - 1 : t_k < lb},
+    # numpy's searchsorted(t[:-1], lb, 'left') computes the latter independently
+    rng = np.random.default_rng(5)
+    s = np.exp(rng.uniform(math.log(0.01), math.log(500.0), 20000)).astype(np.float32)
+    s[:64] = SCALE_TABLE  # every table value itself
+    s[64:128] = np.nextafter(SCALE_TABLE, np.float32(np.inf))
+    s[128:192] = np.nextafter(SCALE_TABLE, np.float32(0))
+    got = O.build_indexes(s, SCALE_TABLE, 0.11)
+    lb = np.maximum(s, np.float32(0.11))
+    want = np.searchsorted(SCALE_TABLE[:-1], lb, side="left")
+    assert (got == want).all()
+    assert (got[:63] == np.arange(63)).all() and got[63] == 63  # t_k -> k; the last -> L - 1
+
+
+def test_build_indexes_edge_values():
+    bound = np.float32(0.11)
+    s = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, -5.0, bound,
+                  np.nextafter(bound, np.float32(1)), 256.0, 1e30], np.float32)
+    got = O.build_indexes(s, SCALE_TABLE, float(bound)).tolist()
+    # NaN stays NaN through the lower bound, so no comparison holds: L - 1
+    assert got[0] == 63 and got[1] == 63
+    # everything at or below the bound maps to the first table entry (= bound)
+    assert got[2:7] == [0, 0, 0, 0, 0]
+    # 256 is the last table entry, which build_indexes never compares: L - 1
+    assert got[7] == 1 and got[8] == 63 and got[9] == 63
+    # a one-entry table: no comparisons, index 0
+    assert O.build_indexes(s, SCALE_TABLE[:1], 0.11).tolist() == [0] * len(s)
+
+
+def test_build_indexes_unsorted_table_is_the_literal_count():
+    # the restatement assumes no order: count of table entries (but the last)
+    # the lower-bounded scale does not exceed, subtracted from L - 1
+    t = np.array([3.0, 1.0, 2.0, 0.5], np.float32)
+    s = np.array([0.1, 1.5, 2.5, 5.0], np.float32)
+    got = O.build_indexes(s, t, 0.11).tolist()
+    assert got == [3 - 3, 3 - 2, 3 - 1, 3 - 0]
+
+
+def test_quantize_elem_and_dequantize_elem_match_torch():
+    rng = np.random.default_rng(6)
+    y = rng.normal(0, 20, 5000).astype(np.float32)
+    m = rng.normal(0, 2, 5000).astype(np.float32)
+    y[:6] = m[:6] + np.array([0.5, -0.5, 1.5, -1.5, 2.5, -0.0], np.float32)
+    ty, tm = torch.from_numpy(y), torch.from_numpy(m)
+    want = torch.round(ty - tm).int().numpy()
+    assert (O.quantize_elem(y, m) == want).all()
+    assert (O.quantize_elem(y) == torch.round(ty).int().numpy()).all()
+    yh = O.dequantize_elem(want, m)
+    assert np.array_equal(yh.view(np.uint32), (torch.from_numpy(want).float() + tm).numpy().view(np.uint32))
+    assert np.array_equal(O.dequantize_elem(want), want.astype(np.float32))
