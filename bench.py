@@ -114,6 +114,72 @@ def kernel_times(L, _native, torch, backend, w, dev, reps=40):
     return res, int(payload.packed.numel())
 
 
+def gaussian_kernel_times(L, _native, torch, p_ch, dev, reps=40):
+    """Event-timed fused GaussianConditional kernels (gaans_encode_gaussian /
+    gaans_decode_gaussian) on the mean-scale hyperprior y 1x192x32x48: fp32
+    y, means and scales in, index search and quantize in the kernel; decode
+    writes fp32 y_hat.  Scales are the scale-table entries of the workload's
+    uniform indexes, so the kernel's index search lands on those tables."""
+    import math
+
+    import numpy as np
+
+    from fast_compressai import synthetic
+    from fast_compressai.coders import gaans
+    from fast_compressai.coders.tables import prepare_tables
+
+    yw, _, y_np, means_np = synthetic.hyperprior_512x768(p_ch=p_ch)
+    B, N, C, P = yw.batch, yw.n, yw.channels, yw.p_ch
+    table_np = np.exp(np.linspace(math.log(0.11), math.log(256.0), 64)).astype(np.float32)
+    idx_np = yw.explicit_indexes()
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    y, means, scales, table = t(y_np), t(means_np), t(table_np[idx_np]), t(table_np)
+    tables = prepare_tables(t(yw.cdfs), t(yw.cdf_sizes), t(yw.offsets))
+    enc = gaans.encode_gaussian(tables, B, N, C, P, dev, y=y, scales=scales, scale_table=table,
+                                scale_bound=0.11, means=means)
+    lay = _native.layout(B, N, C, P)
+    ws = torch.empty(int(lay.workspace_bytes), dtype=torch.uint8, device=dev)
+    ctrl = torch.zeros(_native.CTRL_BYTES, dtype=torch.uint8, device=dev)
+    info = torch.zeros(4, dtype=torch.int64, device=dev)
+    status = torch.zeros(4, dtype=torch.int32, device=dev)
+    out = torch.empty_like(y)
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+
+    def encode():
+        _native.check(L.gaans_encode_gaussian(sp, y.data_ptr(), means.data_ptr(), scales.data_ptr(),
+                                              table.data_ptr(), 64, 0.11, tables.ref, B, N, C, P,
+                                              ws.data_ptr(), ws.numel(), ctrl.data_ptr(),
+                                              info.data_ptr()), "encode")
+
+    def decode():
+        _native.check(L.gaans_decode_gaussian(sp, enc.packed.data_ptr(), enc.packed.numel(),
+                                              scales.data_ptr(), means.data_ptr(),
+                                              table.data_ptr(), 64, 0.11, tables.ref, B, N, C, P,
+                                              out.data_ptr(), ctrl.data_ptr(),
+                                              status.data_ptr()), "decode")
+
+    res = {}
+    for name, fn in (("encode", encode), ("decode", decode)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps // 5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(5):
+                fn()
+            e1.record(stream)
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e-3 / 5)
+        res[name] = statistics.median(ts)
+    torch.cuda.synchronize()
+    want = torch.from_numpy(yw.symbols).to(dev).float() + means
+    assert int(status[0].item()) == 0 and torch.equal(out, want)
+    return res, int(enc.packed.numel()), B * N, yw.raw_rgb_bytes
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -243,6 +309,20 @@ def main():
                 "decode_gsym_s": round(n_sym / kt["decode"] / 1e9, 3),
                 "raw_rgb_gbps_roundtrip_kernels": round(
                     wl.raw_rgb_bytes / (kt["encode"] + kt["decode"]) / 1e9, 2),
+            }
+        for p_ch in (4, 16):
+            kt, pb, n_sym, raw_b = gaussian_kernel_times(L, _native, torch, p_ch, dev)
+            alg = 12 * n_sym + pb  # y, means, scales (or y_hat) fp32 + payload
+            extra[f"hyperprior_y_1x192x32x48_gaussian_p{p_ch}"] = {
+                "symbols": n_sym, "payload_bytes": pb,
+                "encode_hbm_frac": round(alg / kt["encode"] / 1e9 / HBM_PEAK_GBPS, 4),
+                "decode_hbm_frac": round(alg / kt["decode"] / 1e9 / HBM_PEAK_GBPS, 4),
+                "encode_kernel_us": round(kt["encode"] * 1e6, 2),
+                "decode_kernel_us": round(kt["decode"] * 1e6, 2),
+                "encode_gsym_s": round(n_sym / kt["encode"] / 1e9, 3),
+                "decode_gsym_s": round(n_sym / kt["decode"] / 1e9, 3),
+                "raw_rgb_gbps_roundtrip_kernels": round(
+                    raw_b / (kt["encode"] + kt["decode"]) / 1e9, 2),
             }
     if args.copy_probe > 0:
         nb = args.copy_probe << 20
