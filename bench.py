@@ -42,6 +42,10 @@ def parse():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="after the measurement, run one device-to-device copy of MIB MiB "
                          "(reference kernel for HBM byte counters)")
+    ap.add_argument("--pipeline", type=int, default=0, metavar="IMAGES",
+                    help="instead of the coder benchmark: compress_many / decompress_many of "
+                         "IMAGES 512x768 images through a FactorizedPrior(N=128, M=192) "
+                         "stand-in, sequential vs overlapped streams")
     return ap.parse_args()
 
 
@@ -180,12 +184,147 @@ def gaussian_kernel_times(L, _native, torch, p_ch, dev, reps=40):
     return res, int(enc.packed.numel()), B * N, yw.raw_rgb_bytes
 
 
+def balle_factorized(torch, synthetic, device, seed=0):
+    """FactorizedPrior(N=128, M=192) architecture (Balle et al. 2018: four 5x5
+    stride-2 convolutions with GDN in g_a, the transposed mirror with inverse
+    GDN in g_s), random weights, the 512x768 coder workload's 192 tables and
+    medians; the last analysis layer is rescaled so the latents of a uniform
+    random image have a standard deviation of about 2 (inside the tables'
+    Laplacian supports)."""
+    import numpy as np
+    from torch import nn
+    import torch.nn.functional as F
+
+    class GDN(nn.Module):
+        def __init__(self, ch, inverse=False):
+            super().__init__()
+            self.inverse = inverse
+            self.beta = nn.Parameter(torch.ones(ch))
+            self.gamma = nn.Parameter(0.1 * torch.eye(ch).reshape(ch, ch, 1, 1))
+
+        def forward(self, x):
+            norm = torch.sqrt(F.conv2d(x * x, self.gamma, self.beta))
+            return x * norm if self.inverse else x / norm
+
+    class EntropyBottleneck(nn.Module):
+        def __init__(self, w, medians):
+            super().__init__()
+            self.channels = len(medians)
+            med = torch.as_tensor(medians).reshape(-1, 1, 1)
+            self.quantiles = nn.Parameter(torch.cat([med - 10, med, med + 10], dim=-1))
+            self.register_buffer("_quantized_cdf", torch.from_numpy(w.cdfs))
+            self.register_buffer("_cdf_length", torch.from_numpy(w.cdf_sizes))
+            self.register_buffer("_offset", torch.from_numpy(w.offsets))
+
+        def _get_medians(self):
+            return self.quantiles[:, :, 1:2]
+
+    class FactorizedPrior(nn.Module):
+        def __init__(self, N=128, M=192):
+            super().__init__()
+            conv = lambda i, o: nn.Conv2d(i, o, 5, stride=2, padding=2)
+            deconv = lambda i, o: nn.ConvTranspose2d(i, o, 5, stride=2, padding=2,
+                                                     output_padding=1)
+            self.g_a = nn.Sequential(conv(3, N), GDN(N), conv(N, N), GDN(N), conv(N, N),
+                                     GDN(N), conv(N, M))
+            self.g_s = nn.Sequential(deconv(M, N), GDN(N, True), deconv(N, N), GDN(N, True),
+                                     deconv(N, N), GDN(N, True), deconv(N, 3))
+            w = synthetic.coder_512x768(seed=seed)
+            med = np.random.default_rng(seed).normal(0, 0.2, M).astype(np.float32)
+            self.entropy_bottleneck = EntropyBottleneck(w, med)
+
+    torch.manual_seed(seed)
+    model = FactorizedPrior().to(device).eval()
+    with torch.no_grad():
+        y = model.g_a(torch.rand(1, 3, 512, 768, device=device))
+        model.g_a[-1].weight.mul_(2.0 / float(y.std()))
+        model.g_a[-1].bias.zero_()
+    return model
+
+
+def pipeline_bench(args):
+    """compress_many / decompress_many of a sequence of 512x768 images,
+    sequential and overlapped, plus the transform-only and coder-only times
+    of the same sequence (the overlap's lower bound is their maximum)."""
+    import torch
+
+    import fast_compressai
+    from fast_compressai import synthetic
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    # deterministic convolution algorithms, so that the payloads of the two
+    # modes can be compared byte for byte (the default algorithms differ from
+    # call to call in the last bits of y)
+    torch.backends.cudnn.deterministic = True
+    torch.backends.cudnn.benchmark = False
+    model = balle_factorized(torch, synthetic, dev)
+    g = torch.Generator(device="cpu").manual_seed(1)
+    xs = [torch.rand(1, 3, 512, 768, generator=g).to(dev) for _ in range(args.pipeline)]
+    runs = {m: fast_compressai.accelerate(model, P=args.p_ch, device="cuda:0",
+                                          config={"execution_mode": m})
+            for m in ("sequential", "overlap")}
+
+    def clock(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t)
+        return statistics.median(ts) * 1e3
+
+    codec = runs["sequential"]._coder
+    res = {}
+    with torch.no_grad():  # is the transform itself run-to-run reproducible?
+        y0 = [codec.analyze(x) for x in xs]
+        y1 = [codec.analyze(x) for x in xs]
+    analysis_reproducible = all(torch.equal(a, b) for a, b in zip(y0, y1))
+    outs = {m: r.compress_many(xs) for m, r in runs.items()}
+    again = runs["sequential"].compress_many(xs)
+    for m, r in runs.items():
+        res[f"compress_{m}_ms"] = clock(lambda: r.compress_many(xs))
+        res[f"decompress_{m}_ms"] = clock(lambda: r.decompress_many(outs[m]))
+    with torch.no_grad():
+        ys = [codec.analyze(x) for x in xs]
+        yh = [codec.decode_latents(o["strings"], o["shape"]) for o in outs["sequential"]]
+        res["analysis_only_ms"] = clock(lambda: [codec.analyze(x) for x in xs])
+        res["encode_only_ms"] = clock(lambda: [codec.encode_latents(y) for y in ys])
+        res["decode_only_ms"] = clock(
+            lambda: [codec.decode_latents(o["strings"], o["shape"]) for o in outs["sequential"]])
+        res["synthesis_only_ms"] = clock(lambda: [codec.synthesize(y) for y in yh])
+    def same(u, v):
+        return all(a["strings"][0].to_bytes() == b["strings"][0].to_bytes()
+                   for a, b in zip(u, v))
+
+    bpp = statistics.mean(8 * o["strings"][0].packed.numel() / (512 * 768)
+                          for o in outs["sequential"])
+    print(json.dumps({
+        "workload": f"{args.pipeline} images 512x768, FactorizedPrior(N=128, M=192) "
+                    f"architecture, random weights, P={args.p_ch}",
+        **{k: round(v, 3) for k, v in res.items()},
+        "compress_overlap_speedup": round(res["compress_sequential_ms"]
+                                          / res["compress_overlap_ms"], 3),
+        "decompress_overlap_speedup": round(res["decompress_sequential_ms"]
+                                            / res["decompress_overlap_ms"], 3),
+        "analysis_reproducible": analysis_reproducible,
+        "payloads_sequential_vs_sequential": same(outs["sequential"], again),
+        "payloads_sequential_vs_overlap": same(outs["sequential"], outs["overlap"]),
+        "bpp": round(bpp, 4),
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this coder's "
               "multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
         sys.exit(2)
+    if args.pipeline > 0:
+        pipeline_bench(args)
+        return
 
     import numpy as np
     import torch

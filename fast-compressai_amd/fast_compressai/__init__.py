@@ -22,6 +22,9 @@ from .coders import (
     warp_div_capability,
 )
 from .config import AccelerationConfig, ConfigurationError
+from .p_ch import (PChSelection, choose_p_ch, default_p_candidates, legal_p_candidates,
+                   sweep_p_ch)
+from .pipeline import CodingPipeline
 
 __all__ = [
     "AccelerationConfig",
@@ -33,15 +36,21 @@ __all__ = [
     "CoderError",
     "CoderInputError",
     "CoderStateError",
+    "CodingPipeline",
     "CompressAIANSBackend",
     "ConfigurationError",
     "FastModel",
+    "PChSelection",
     "WarpDivBackend",
     "WarpDivPayload",
     "accelerate",
+    "choose_p_ch",
     "coder_catalog",
     "compile",
     "create_coder",
+    "default_p_candidates",
+    "legal_p_candidates",
+    "sweep_p_ch",
     "warp_div_capability",
 ]
 

@@ -88,6 +88,22 @@ class FastModel(nn.Module):
             return coder.decompress(*args, **kwargs)
         return self.model.decompress(*args, **kwargs)
 
+    def compress_many(self, inputs: Any) -> list:
+        """``compress`` of every input; with ``execution_mode="overlap"`` the
+        transforms and the coder run on two streams (``pipeline.py``)."""
+        pipeline = self.__dict__.get("_pipeline")
+        if pipeline is not None:
+            return pipeline.compress_many(inputs)
+        return [self.compress(x) for x in inputs]
+
+    def decompress_many(self, items: Any) -> list:
+        """``decompress`` of every ``compress`` result (dicts with ``strings``
+        and ``shape``), overlapped like ``compress_many``."""
+        pipeline = self.__dict__.get("_pipeline")
+        if pipeline is not None:
+            return pipeline.decompress_many(items)
+        return [self.decompress(it["strings"], it["shape"]) for it in items]
+
     def update(self, *args: Any, **kwargs: Any) -> Any:
         return self.model.update(*args, **kwargs)
 
@@ -222,6 +238,9 @@ def accelerate(
             codec = HyperpriorWarpDivCodec(runtime_model, p_ch, mean_scale=hyper == "mean_scale")
         wrapped = FastModel(runtime_model, device=str(target))
         wrapped._coder = codec
+        from .pipeline import CodingPipeline
+
+        wrapped._pipeline = CodingPipeline(codec, target, cfg.execution_mode)
         report = AccelerationReport(
             status="coder_applied", model_class=type(model).__qualname__,
             adapter_family="compressai", p_ch=p_ch, quality_budget=float(cfg.budget),
@@ -231,7 +250,8 @@ def accelerate(
             coder_status="warp_div", p_ch_applied=True, runtime_status="not_applied",
             speedup=None, p_ch_selection_status=p_status,
             message=("The MI355X GA-ANS coder is applied to compress/decompress with P_ch="
-                     f"{p_ch}; transforms stay FP32 and payloads are device-local."),
+                     f"{p_ch}; transforms stay FP32 and payloads are device-local; "
+                     f"compress_many/decompress_many run {cfg.execution_mode}."),
         )
     else:
         if sample is not None:

@@ -55,27 +55,25 @@ class FactorizedWarpDivCodec:
     def _medians(entropy) -> torch.Tensor:
         return entropy._get_medians().detach().reshape(-1)
 
-    def compress(self, x: torch.Tensor, timing: dict[str, float] | None = None):
+    # ---- phases (the pipeline runs analysis / synthesis and coding on
+    # different streams; compress / decompress chain them) --------------------
+    def analyze(self, x: torch.Tensor) -> torch.Tensor:
+        """Inference half of compress: ``y = g_a(x)``."""
         if not isinstance(x, torch.Tensor) or x.device.type != "cuda" or x.ndim != 4:
             raise CoderInputError("warp_div FactorizedPrior.compress expects a GPU NCHW tensor")
         with torch.no_grad():
-            start = torch.cuda.Event(enable_timing=True) if timing is not None else None
-            end = torch.cuda.Event(enable_timing=True) if timing is not None else None
-            if timing is not None:
-                start.record()
-            y = self.model.g_a(x)
-            entropy = self.model.entropy_bottleneck
-            if y.size(1) != entropy.channels:
-                raise CoderInputError("latent channel count does not match entropy bottleneck")
+            return self.model.g_a(x)
+
+    def encode_latents(self, y: torch.Tensor):
+        """Coding half of compress: quantize + GA-ANS encode of ``y``."""
+        entropy = self.model.entropy_bottleneck
+        if y.size(1) != entropy.channels:
+            raise CoderInputError("latent channel count does not match entropy bottleneck")
+        with torch.no_grad():
             tables = self._prepared(entropy, y.device)
             medians = self._medians(entropy)
             B, C = int(y.size(0)), int(y.size(1))
             N = int(y[0].numel())
-            if timing is not None:
-                end.record()
-                end.synchronize()
-                timing["compress_inference_ms"] = float(start.elapsed_time(end))
-                start.record()
             if y.dtype == torch.float32 and medians.dtype == torch.float32:
                 enc = gaans.encode(tables, B, N, C, self.p_ch, y.device,
                                    y=y.contiguous(), medians=medians.contiguous())
@@ -91,13 +89,10 @@ class FactorizedWarpDivCodec:
                 cdf_count=tables.M,
                 coding_fingerprint=coding_fingerprint(tables.digest, B, N, C, tables.M),
             )
-            if timing is not None:
-                end.record()
-                end.synchronize()
-                timing["compress_codec_ms"] = float(start.elapsed_time(end))
             return {"strings": [payload], "shape": tuple(y.shape[-2:])}
 
-    def decompress(self, strings, shape, timing: dict[str, float] | None = None):
+    def decode_latents(self, strings, shape) -> torch.Tensor:
+        """Coding half of decompress: GA-ANS decode + dequantize to ``y_hat``."""
         if (not isinstance(strings, (list, tuple)) or len(strings) != 1
                 or not isinstance(strings[0], WarpDivPayload)):
             raise CoderInputError("warp_div decompress expects strings=[WarpDivPayload]")
@@ -124,29 +119,56 @@ class FactorizedWarpDivCodec:
             raise CoderInputError("coding tables or indexes do not match warp_div payload")
         with torch.no_grad():
             output_shape = (B, channels, *shape)
-            start = torch.cuda.Event(enable_timing=True) if timing is not None else None
-            end = torch.cuda.Event(enable_timing=True) if timing is not None else None
-            if timing is not None:
-                start.record()
             medians = self._medians(entropy)
             if medians.dtype == torch.float32:
-                y_hat = gaans.decode(payload.packed, tables, B, N, channels, self.p_ch,
-                                     payload.packed.device,
-                                     medians=medians.contiguous()).reshape(output_shape)
-            else:
-                symbols = gaans.decode(payload.packed, tables, B, N, channels, self.p_ch,
-                                       payload.packed.device).reshape(output_shape)
-                ext = entropy._extend_ndims(entropy._get_medians().detach(), len(shape))
-                ext = ext.expand(B, *([-1] * (len(shape) + 1)))
-                y_hat = entropy.dequantize(symbols, ext, ext.dtype)
-            if timing is not None:
-                end.record()
-                end.synchronize()
-                timing["decompress_codec_ms"] = float(start.elapsed_time(end))
-                start.record()
-            result = {"x_hat": self.model.g_s(y_hat).clamp_(0, 1)}
-            if timing is not None:
-                end.record()
-                end.synchronize()
-                timing["decompress_inference_ms"] = float(start.elapsed_time(end))
-            return result
+                return gaans.decode(payload.packed, tables, B, N, channels, self.p_ch,
+                                    payload.packed.device,
+                                    medians=medians.contiguous()).reshape(output_shape)
+            symbols = gaans.decode(payload.packed, tables, B, N, channels, self.p_ch,
+                                   payload.packed.device).reshape(output_shape)
+            ext = entropy._extend_ndims(entropy._get_medians().detach(), len(shape))
+            ext = ext.expand(B, *([-1] * (len(shape) + 1)))
+            return entropy.dequantize(symbols, ext, ext.dtype)
+
+    def synthesize(self, y_hat: torch.Tensor):
+        """Inference half of decompress: ``x_hat = g_s(y_hat).clamp(0, 1)``."""
+        with torch.no_grad():
+            return {"x_hat": self.model.g_s(y_hat).clamp_(0, 1)}
+
+    # ---- the model's public paths -------------------------------------------
+    def compress(self, x: torch.Tensor, timing: dict[str, float] | None = None):
+        if timing is None:
+            return self.encode_latents(self.analyze(x))
+        with _Span(timing, "compress_inference_ms"):
+            y = self.analyze(x)
+        with _Span(timing, "compress_codec_ms"):
+            return self.encode_latents(y)
+
+    def decompress(self, strings, shape, timing: dict[str, float] | None = None):
+        if timing is None:
+            return self.synthesize(self.decode_latents(strings, shape))
+        with _Span(timing, "decompress_codec_ms"):
+            y_hat = self.decode_latents(strings, shape)
+        with _Span(timing, "decompress_inference_ms"):
+            return self.synthesize(y_hat)
+
+
+class _Span:
+    """Event-timed region on the current stream; stores milliseconds in
+    ``timing[key]`` (keys of the reference's ``timing`` dict,
+    ``src/fast_compressai/coders/factorized.py:33-107``)."""
+
+    def __init__(self, timing: dict[str, float], key: str) -> None:
+        self.timing, self.key = timing, key
+
+    def __enter__(self):
+        self.start = torch.cuda.Event(enable_timing=True)
+        self.end = torch.cuda.Event(enable_timing=True)
+        self.start.record()
+        return self
+
+    def __exit__(self, *exc):
+        self.end.record()
+        self.end.synchronize()
+        self.timing[self.key] = float(self.start.elapsed_time(self.end))
+        return False

@@ -28,6 +28,7 @@ import torch
 
 from . import gaans
 from .errors import CoderInputError
+from .factorized import _Span
 from .tables import TableCache
 from .warp_div import WarpDivBackend, WarpDivPayload, coding_fingerprint
 
@@ -146,13 +147,23 @@ class HyperpriorWarpDivCodec:
             return scales.to(torch.float32).contiguous(), means.to(torch.float32).contiguous()
         return out.to(torch.float32).contiguous(), None
 
-    # ---- public paths -----------------------------------------------------------
-    def compress(self, x: torch.Tensor, timing: dict[str, float] | None = None):
+    # ---- phases (the pipeline runs analysis / synthesis and coding on
+    # different streams; compress / decompress chain them) --------------------
+    def analyze(self, x: torch.Tensor):
+        """Inference half of compress: ``y = g_a(x)``, ``z = h_a(y)`` (mean-scale)
+        or ``h_a(|y|)`` (scale)."""
         if not isinstance(x, torch.Tensor) or x.device.type != "cuda" or x.ndim != 4:
             raise CoderInputError("warp_div hyperprior compress expects a GPU NCHW tensor")
         with torch.no_grad():
             y = self.model.g_a(x)
             z = self.model.h_a(y if self.mean_scale else torch.abs(y))
+        return y, z
+
+    def encode_latents(self, latents):
+        """Coding half of compress: z through the factorized kernels, ``h_s``,
+        y through the Gaussian kernels."""
+        y, z = latents
+        with torch.no_grad():
             z_payload, z_hat = self._z_encode(z)
             scales, means = self._params(z_hat)
             gc = self.model.gaussian_conditional
@@ -175,7 +186,8 @@ class HyperpriorWarpDivCodec:
             y_payload = _payload(enc, self.p_ch, B, N, C, tables)
             return {"strings": [y_payload, z_payload], "shape": tuple(z.shape[-2:])}
 
-    def decompress(self, strings, shape, timing: dict[str, float] | None = None):
+    def decode_latents(self, strings, shape) -> torch.Tensor:
+        """Coding half of decompress: z decode, ``h_s``, y decode to ``y_hat``."""
         if (not isinstance(strings, (list, tuple)) or len(strings) != 2
                 or not all(isinstance(s, WarpDivPayload) for s in strings)):
             raise CoderInputError("warp_div hyperprior decompress expects strings=[y, z] payloads")
@@ -209,5 +221,26 @@ class HyperpriorWarpDivCodec:
                 y_hat = sym.to(torch.float32)
                 if means is not None:
                     y_hat = y_hat + means.reshape(B, N)
-            y_hat = y_hat.reshape(scales.shape)
+            return y_hat.reshape(scales.shape)
+
+    def synthesize(self, y_hat: torch.Tensor):
+        """Inference half of decompress: ``x_hat = g_s(y_hat).clamp(0, 1)``."""
+        with torch.no_grad():
             return {"x_hat": self.model.g_s(y_hat).clamp_(0, 1)}
+
+    # ---- the model's public paths -------------------------------------------
+    def compress(self, x: torch.Tensor, timing: dict[str, float] | None = None):
+        if timing is None:
+            return self.encode_latents(self.analyze(x))
+        with _Span(timing, "compress_inference_ms"):
+            latents = self.analyze(x)
+        with _Span(timing, "compress_codec_ms"):
+            return self.encode_latents(latents)
+
+    def decompress(self, strings, shape, timing: dict[str, float] | None = None):
+        if timing is None:
+            return self.synthesize(self.decode_latents(strings, shape))
+        with _Span(timing, "decompress_codec_ms"):
+            y_hat = self.decode_latents(strings, shape)
+        with _Span(timing, "decompress_inference_ms"):
+            return self.synthesize(y_hat)
