@@ -316,6 +316,41 @@ def pipeline_bench(args):
     }), flush=True)
 
 
+def rans64_times(torch, dev, batch, reps=3):
+    """GPU decode of CompressAI-format Rans64 streams (one per image of the
+    512x768 coder workload, table = channel): seconds per launch, and the
+    oracle's single-thread decode of one stream for comparison."""
+    import numpy as np
+
+    import oracle
+    from fast_compressai import synthetic
+    from fast_compressai.coders import gaans
+    from fast_compressai.coders.tables import prepare_tables
+
+    w = synthetic.coder_512x768(seed=0, batch=batch)
+    idx = w.explicit_indexes()
+    streams = [oracle.rans64_encode(w.symbols[b], idx[b], w.cdfs, w.cdf_sizes, w.offsets)
+               for b in range(batch)]
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    tables = prepare_tables(t(w.cdfs), t(w.cdf_sizes), t(w.offsets))
+    buf, offs = gaans.pack_streams(streams, dev)
+    out = gaans.decode_rans64(buf, offs, tables, batch, w.n, w.channels, dev)
+    assert np.array_equal(out.cpu().numpy(), w.symbols)
+    stream = torch.cuda.current_stream(dev)
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        gaans.decode_rans64(buf, offs, tables, batch, w.n, w.channels, dev)
+        e1.record(stream)
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e-3)
+    c0 = time.perf_counter()
+    oracle.rans64_decode(streams[0], idx[0], w.cdfs, w.cdf_sizes, w.offsets)
+    cpu = time.perf_counter() - c0
+    return statistics.median(ts), cpu, batch * w.n, sum(len(s) for s in streams)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -462,6 +497,15 @@ def main():
                 "decode_gsym_s": round(n_sym / kt["decode"] / 1e9, 3),
                 "raw_rgb_gbps_roundtrip_kernels": round(
                     raw_b / (kt["encode"] + kt["decode"]) / 1e9, 2),
+            }
+        for batch in (1, 64, 256):
+            gpu_s, cpu_s, n_sym, nbytes = rans64_times(torch, dev, batch)
+            extra[f"rans64_decode_{batch}x192x32x48"] = {
+                "symbols": n_sym, "stream_bytes": nbytes,
+                "decode_ms": round(gpu_s * 1e3, 3),
+                "decode_gsym_s": round(n_sym / gpu_s / 1e9, 4),
+                "cpu_oracle_ms_per_stream": round(cpu_s * 1e3, 3),
+                "speedup_vs_one_cpu_thread": round(batch * cpu_s / gpu_s, 2),
             }
     if args.copy_probe > 0:
         nb = args.copy_probe << 20

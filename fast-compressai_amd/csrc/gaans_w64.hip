@@ -1700,6 +1700,281 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   }
 }
 
+// ============================================================================
+// CompressAI Rans64 streams: one stream per batch row, one lane per stream
+// ============================================================================
+//
+// CompressAI's RansEncoder.encode_with_indexes writes one serial Rans64
+// stream per image (64-bit state, L = 2^31, 32-bit words, 16-bit CDFs,
+// escapes as 4-bit bypass groups).  One stream cannot be split, so a wave
+// decodes up to 64 of them side by side, lane l < spw the stream of row
+// spw * blockIdx.x + l, in lockstep over positions.  Lanes of one wave
+// diverge at dense lookups and escapes, so the host spreads small batches
+// over more waves (down to one stream per wave).  A step: cum = x & 0xffff;
+// the prepared tables' decode lookup (LDS, same entries as the GA-ANS
+// decoder); x = freq * (x >> 16) + cum - start; one word when x < 2^31.
+// Words come from a per-lane LDS ring that the wave refills kR64Pf words at a
+// time from registers loaded one refill earlier (so their latency is off the
+// chain); a lane that runs its ring dry (long escapes) reads global memory.
+// Tables: all staged at the start when they fit; otherwise, with implicit
+// indexes (table = channel: every lane is in the same channel at the same
+// step), the current channel's table is staged when the channel changes;
+// otherwise lookups read global memory.
+
+constexpr int kCtrlR64Done = 32;
+constexpr int kCtrlR64Status = 33;
+constexpr uint64_t kR64L = 1ull << 31;
+constexpr int kR64Steps = 32;                 // steps between ring refills
+constexpr int kR64Ring = 128;                 // ring words per lane (power of two)
+constexpr int kR64Pf = 32;                    // words per lane per refill
+constexpr int kR64RingBytes = 4 * kR64Ring * kLanes;
+constexpr int kR64SubCap = 64;                // sub-blocks staged with one channel's table
+constexpr int kR64IdxBytes = 4 * kR64Steps * kLanes;  // explicit indexes of one block
+
+struct R64Args {
+  const uint8_t* __restrict__ streams;
+  int64_t streams_bytes;
+  const int64_t* __restrict__ offsets;  // B + 1 byte offsets
+  const int32_t* __restrict__ indexes;  // [B, N], or NULL: table = position / HW
+  const uint8_t* __restrict__ tables;
+  uint32_t M, tables_bytes;
+  int64_t B, N;
+  UDiv div_hw;
+  int32_t stage;       // 0: global lookups, 1: all tables staged, 2: one channel at a time
+  int32_t stage_subs;  // sub-blocks staged too
+  uint32_t lds_tabs;   // LDS byte offset of [luts][meta][sub-blocks] (after ring, indexes)
+  int32_t nt_cap;      // tables the LDS lookups hold
+  int32_t* __restrict__ out;
+  uint32_t* __restrict__ ctrl;
+  uint32_t* __restrict__ status_out;
+  uint32_t nblocks;
+  int32_t spw;  // streams per wave (lanes 0 .. spw - 1)
+};
+
+struct R64Stream {
+  const uint32_t* __restrict__ w;  // the lane's words
+  int q;                           // words in the stream (0: no valid stream)
+  int rp, filled;                  // next word; words placed in the ring
+  uint32_t pf[kR64Pf];             // the next refill
+  bool bad;
+};
+
+__device__ __forceinline__ void r64_prefetch(R64Stream& S) {
+#pragma unroll
+  for (int k = 0; k < kR64Pf; ++k) {
+    const int i = S.filled + k;
+    S.pf[k] = 0u;
+    if (i < S.q) S.pf[k] = S.w[i];
+  }
+}
+
+// Refill: lanes with room commit their prefetched words and load the next.
+__device__ __forceinline__ void r64_refill(R64Stream& S, uint32_t* ring, int lane) {
+  const bool need = S.filled - S.rp <= kR64Ring - kR64Pf && S.filled < S.q;
+  if (ballot(need) == 0ull) return;
+  if (need) {
+#pragma unroll
+    for (int k = 0; k < kR64Pf; ++k)
+      ring[((S.filled + k) & (kR64Ring - 1)) * kLanes + lane] = S.pf[k];
+    S.filled += kR64Pf;
+    r64_prefetch(S);
+  }
+}
+
+__device__ __forceinline__ uint32_t r64_next(R64Stream& S, const uint32_t* ring, int lane) {
+  uint32_t v = 0u;
+  if (S.rp < S.filled) {
+    v = ring[(S.rp & (kR64Ring - 1)) * kLanes + lane];
+  } else if (S.rp < S.q) {
+    v = S.w[S.rp];
+  }
+  S.bad |= S.rp >= S.q;
+  ++S.rp;
+  return v;
+}
+
+__device__ __forceinline__ uint32_t r64_bits4(R64Stream& S, uint64_t& x, const uint32_t* ring,
+                                              int lane) {
+  const uint32_t v = (uint32_t)x & 15u;
+  x >>= 4;
+  if (x < kR64L) x = (x << 32) | r64_next(S, ring, lane);
+  return v;
+}
+
+template <bool kImplicit>
+__global__ void __launch_bounds__(kLanes) k_rans64_decode(R64Args a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint32_t* ring = reinterpret_cast<uint32_t*>(smem);
+  int32_t* ibuf = reinterpret_cast<int32_t*>(smem + kR64RingBytes);  // explicit indexes
+  uint8_t* tsm = smem + a.lds_tabs;
+  uint64_t* llut = reinterpret_cast<uint64_t*>(tsm);
+  uint4* lmeta = reinterpret_cast<uint4*>(tsm + 8 * kLutSize * a.nt_cap);
+  uint64_t* lsub = reinterpret_cast<uint64_t*>(tsm + (8 * kLutSize + 16) * a.nt_cap);
+
+  const int lane = threadIdx.x;
+  const int64_t b = (int64_t)blockIdx.x * a.spw + lane;
+  const bool live = lane < a.spw && b < a.B;
+  uint32_t status = 0;
+  const TabHdr* th = reinterpret_cast<const TabHdr*>(a.tables);
+  const bool tab = tables_ok(a.tables, a.M, a.tables_bytes);
+  if (!tab) status |= GAANS_ST_TABLES;
+
+  // the lane's stream: [off_b, off_b+1) inside the buffer, whole words
+  R64Stream S;
+  S.w = reinterpret_cast<const uint32_t*>(a.streams);
+  S.q = 0;
+  S.rp = 0;
+  S.filled = 0;
+  S.bad = false;
+  if (live) {
+    const int64_t o0 = a.offsets[b], o1 = a.offsets[b + 1];
+    const bool fits = o0 >= 0 && o1 >= o0 && o1 <= a.streams_bytes && (o0 & 3) == 0 &&
+                      ((o1 - o0) & 3) == 0 && (o1 - o0) / 4 <= 0x7fffffff - 2 * kR64Pf;
+    if (fits && o1 - o0 >= 8 && a.N > 0) {
+      S.w = reinterpret_cast<const uint32_t*>(a.streams + o0);
+      S.q = (int)((o1 - o0) / 4);
+    } else if (a.N > 0) {
+      status |= GAANS_ST_CORRUPT;  // CompressAI's decoder needs the two state words
+    }
+  }
+  const bool act0 = live && S.q > 0 && tab;
+
+  // first refill: state words and the ring, then the next batch in flight
+  r64_prefetch(S);
+  r64_refill(S, ring, lane);
+  uint64_t x = 0;
+  if (act0) {
+    const uint32_t lo = r64_next(S, ring, lane), hi = r64_next(S, ring, lane);
+    x = (uint64_t)lo | ((uint64_t)hi << 32);
+  }
+
+  Tabs tb;
+  tb.gmeta = reinterpret_cast<const TabMeta*>(a.tables + th->meta_off);
+  tb.gent = nullptr;
+  tb.glut = reinterpret_cast<const uint64_t*>(a.tables + th->lut_off);
+  tb.gsub = reinterpret_cast<const uint64_t*>(a.tables + th->dense_off);
+  tb.lmeta = lmeta;
+  tb.lent = nullptr;
+  tb.llut = llut;
+  tb.lsub = lsub;
+  tb.t_lo = 0;
+  tb.nt = 0;
+  tb.sub_first = 0;
+  tb.sub_lds = false;
+  const bool any = ballot(act0) != 0ull;
+  const uint32_t total_dense = tab ? th->total_dense : 0u;
+  if (any && a.stage == 1)
+    stage_tables<kLanes>(tb, lmeta, nullptr, llut, a.stage_subs ? lsub : nullptr, total_dense,
+                         a.M, 0, (int)a.M, lane);
+  int cur = -1;  // staged channel (stage 2)
+  uint32_t c_nsym = 0;
+  int32_t c_off = 0;
+
+  const int64_t row = live ? b * a.N : 0;
+  const int64_t nsteps = any ? a.N : 0;
+  // explicit indexes: block j + 1's are loaded into registers while block j
+  // runs, then stored to LDS at block j + 1's start
+  int32_t nb[kR64Steps];
+  auto load_indexes = [&](int64_t i0) {
+#pragma unroll
+    for (int k = 0; k < kR64Steps; ++k) {
+      nb[k] = 0;
+      if (act0 && i0 + k < nsteps) nb[k] = a.indexes[row + i0 + k];
+    }
+  };
+  if (!kImplicit) load_indexes(0);
+  for (int64_t i0 = 0; i0 < nsteps; i0 += kR64Steps) {
+    if (!kImplicit) {
+#pragma unroll
+      for (int k = 0; k < kR64Steps; ++k) ibuf[k * kLanes + lane] = nb[k];
+      load_indexes(i0 + kR64Steps);
+    }
+    r64_refill(S, ring, lane);
+    const int n = nsteps - i0 < kR64Steps ? (int)(nsteps - i0) : kR64Steps;
+#pragma unroll 1
+    for (int k = 0; k < n; ++k) {
+      const int64_t i = i0 + k;
+      const bool act = act0 & !S.bad;
+      uint32_t t;
+      if (kImplicit) {
+        // the same in every lane: stage the channel's table when it changes
+        const int tc = uni((int)udiv((uint32_t)i, a.div_hw));
+        if (a.stage == 2 && tc != cur) {
+          cur = tc;
+          stage_tables<kLanes>(tb, lmeta, nullptr, llut, a.stage_subs ? lsub : nullptr,
+                               total_dense, a.M, cur, cur + 1, lane);
+          const uint4 lm = lmeta[0];
+          c_nsym = lm.y;
+          c_off = (int32_t)lm.z;
+        }
+        t = (uint32_t)tc;
+      } else {
+        t = (uint32_t)ibuf[k * kLanes + lane];
+      }
+      const bool bad_t = act & (t >= a.M);
+      status |= bad_t ? GAANS_ST_INDEX : 0u;
+      const bool ok = act & !bad_t;
+      t = ok ? t : 0u;
+      uint32_t nsym;
+      int32_t off;
+      uint32_t tl = t;
+      if (a.stage == 2) {
+        nsym = c_nsym;
+        off = c_off;
+        tl = 0u;
+      } else if (a.stage == 1) {
+        const uint4 lm = lmeta[t];
+        nsym = lm.y;
+        off = (int32_t)lm.z;
+      } else {
+        const TabMeta gm = tb.gmeta[t];
+        nsym = gm.nsym;
+        off = gm.offset;
+      }
+      const uint32_t cum = (uint32_t)x & 0xffffu;
+      uint32_t s, st, fr;
+      if (a.stage != 0) dec_lookup<true>(tb, tl, cum, ok, s, st, fr);
+      else dec_lookup<false>(tb, tl, cum, ok, s, st, fr);
+      x = (uint64_t)fr * (x >> 16) + cum - st;
+      if (ok && x < kR64L) x = (x << 32) | r64_next(S, ring, lane);
+      int64_t v = (int64_t)s + off;
+      if (ok && s == nsym - 1u) {  // escape: 4-bit count, then the raw value's nibbles
+        uint32_t cnt = r64_bits4(S, x, ring, lane);
+        if (cnt > 8u) {  // 15 continues the count: never for a 32-bit value
+          S.bad = true;
+          cnt = 0u;
+        }
+        uint32_t raw = 0;
+        for (uint32_t j = 0; j < cnt; ++j) raw |= r64_bits4(S, x, ring, lane) << (4u * j);
+        const int64_t u = (raw & 1u) ? -(int64_t)(raw >> 1) - 1
+                                     : (int64_t)(raw >> 1) + (int64_t)(nsym - 1u);
+        v = u + off;
+        if (v < INT32_MIN || v > INT32_MAX) S.bad = true;
+      }
+      if (ok) a.out[row + i] = (int32_t)v;
+    }
+  }
+  if (act0 && S.bad) status |= GAANS_ST_CORRUPT;
+
+  status = wave_or(status);
+  if (lane == 0) {
+    if (status)
+      __hip_atomic_fetch_or(&a.ctrl[kCtrlR64Status], status, __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const uint32_t done = __hip_atomic_fetch_add(&a.ctrl[kCtrlR64Done], 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    if (done == a.nblocks - 1u) {
+      const uint32_t all = __hip_atomic_exchange(&a.ctrl[kCtrlR64Status], 0u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+      a.status_out[0] = all;
+      __hip_atomic_store(&a.status_out[1], 1u | (all << 1), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(&a.ctrl[kCtrlR64Done], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 // ---- host helpers -------------------------------------------------------------
 
 int check_launch(const char* what) {
@@ -2143,6 +2418,81 @@ int32_t build_lookup(const int32_t* c, int32_t S, uint64_t* lut, uint64_t* block
   return n;
 }
 
+// CompressAI Rans64 streams: plan the LDS (all tables; else, with implicit
+// indexes, one channel's table at a time; else global lookups) and launch.
+int rans64_decode_impl(void* stream, const uint8_t* streams, int64_t streams_bytes,
+                       const int64_t* offsets, const int32_t* indexes,
+                       const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
+                       int32_t* out, void* ctrl, uint32_t* status_out) {
+  int rc = check_tables_arg(tables);
+  if (rc) return rc;
+  if (B < 1 || N < 1 || C < 1 || N % C != 0)
+    return fail(GAANS_EINVAL, "need B, N, C >= 1 and N %% C == 0 (B=%lld N=%lld C=%lld)",
+                (long long)B, (long long)N, (long long)C);
+  if (N > 0x7fffffffll - kR64Steps || B > 0x7fffffffll)
+    return fail(GAANS_EINVAL, "N must stay below 2^31 - %d symbols per stream", kR64Steps);
+  if (streams_bytes < 0 || (!streams && streams_bytes > 0))
+    return fail(GAANS_EINVAL, "streams pointer is NULL or streams_bytes is negative");
+  if (!offsets || !out || !ctrl || !status_out)
+    return fail(GAANS_EINVAL, "offsets, output, control or status pointer is NULL");
+  if (!indexes && C > tables->M)
+    return fail(GAANS_EINVAL, "table = channel needs a table per channel (C=%lld > M=%d)",
+                (long long)C, tables->M);
+  DevLds dl;
+  if ((rc = device_lds(&dl))) return rc;
+  const int64_t fixed = kR64RingBytes + (indexes ? kR64IdxBytes : 0);
+  const int64_t budget = (int64_t)dl.per_block - fixed;
+  const int64_t per_table = 8 * kLutSize + 16;
+  const int64_t M = tables->M;
+  int stage = 0, subs = 0;
+  int64_t nt_cap = 0, sub_cap = 0;
+  if (M * per_table + tables->total_dense * kSubBytes <= budget) {
+    stage = 1, subs = 1, nt_cap = M, sub_cap = tables->total_dense;
+  } else if (M * per_table <= budget) {
+    stage = 1, nt_cap = M;
+  } else if (!indexes) {
+    stage = 2, nt_cap = 1;
+    if (tables->max_dense <= kR64SubCap) subs = 1, sub_cap = kR64SubCap;
+  }
+  R64Args a;
+  a.streams = streams;
+  a.streams_bytes = streams_bytes;
+  a.offsets = offsets;
+  a.indexes = indexes;
+  a.tables = static_cast<const uint8_t*>(tables->dev);
+  a.M = (uint32_t)M;
+  a.tables_bytes = (uint32_t)tables->bytes;
+  a.B = B;
+  a.N = N;
+  a.div_hw = make_udiv((uint32_t)(N / C));
+  a.stage = stage;
+  a.stage_subs = subs;
+  a.lds_tabs = (uint32_t)fixed;
+  a.nt_cap = (int32_t)nt_cap;
+  a.out = out;
+  a.ctrl = static_cast<uint32_t*>(ctrl);
+  a.status_out = status_out;
+  // one stream per wave while the SIMDs have room, more (up to 64) beyond
+  const int64_t simds = 4 * (int64_t)dl.cus;
+  const int64_t spw = B <= simds ? 1 : ((B + simds - 1) / simds < kLanes ? (B + simds - 1) / simds
+                                                                          : kLanes);
+  const int64_t grid = (B + spw - 1) / spw;
+  a.spw = (int32_t)spw;
+  a.nblocks = (uint32_t)grid;
+  const size_t lds = (size_t)(fixed + nt_cap * per_table + sub_cap * kSubBytes);
+  if (lds > (size_t)dl.per_block)
+    return fail(GAANS_EINVAL, "Rans64 decode needs %zu bytes of LDS, the device has %d", lds,
+                dl.per_block);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  auto launch = [&](auto kernel) -> int {
+    int r = allow_lds(reinterpret_cast<const void*>(kernel), lds, dl);
+    if (r) return r;
+    kernel<<<dim3((uint32_t)grid), dim3(kLanes), lds, s>>>(a);
+    return check_launch("Rans64 decode");
+  };
+  return indexes ? launch(k_rans64_decode<false>) : launch(k_rans64_decode<true>);
+}
+
 }  // namespace
 
 // =============================================================================
@@ -2377,6 +2727,14 @@ int gaans_decode_gaussian(void* stream, const uint8_t* payload_dev, int64_t payl
   const GaussIn g{means_dev, scales_dev, scale_table_dev, n_scales, scale_bound};
   return decode_impl(kModeGaussian, stream, payload_dev, payload_bytes, nullptr, &g, tables,
                      nullptr, B, N, C, P, nullptr, y_hat_dev, ctrl_dev, status_out);
+}
+
+int gaans_rans64_decode(void* stream, const uint8_t* streams_dev, int64_t streams_bytes,
+                        const int64_t* offsets_dev, const int32_t* indexes_dev,
+                        const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
+                        int32_t* out_dev, void* ctrl_dev, uint32_t* status_out) {
+  return rans64_decode_impl(stream, streams_dev, streams_bytes, offsets_dev, indexes_dev, tables,
+                            B, N, C, out_dev, ctrl_dev, status_out);
 }
 
 int gaans_wait_host_word(void* stream, const uint32_t* word) {

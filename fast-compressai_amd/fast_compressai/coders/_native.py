@@ -15,7 +15,7 @@ import threading
 from .errors import CoderDependencyError
 
 LIB_NAME = "libgaans_w64.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 CTRL_BYTES = 256
 
 # return codes
@@ -101,6 +101,7 @@ def _declare(L) -> None:
                                   ctypes.c_int),
         "gaans_decode_gaussian": ([p, p, i64, p, p, p, i32, f32, T, i64, i64, i64, i64, p, p, p],
                                   ctypes.c_int),
+        "gaans_rans64_decode": ([p, p, i64, p, p, T, i64, i64, i64, p, p, p], ctypes.c_int),
         "gaans_wait_host_word": ([p, p], ctypes.c_int),
         "gaans_host_selftest": ([], ctypes.c_int),
     }

@@ -92,7 +92,13 @@ class FactorizedWarpDivCodec:
             return {"strings": [payload], "shape": tuple(y.shape[-2:])}
 
     def decode_latents(self, strings, shape) -> torch.Tensor:
-        """Coding half of decompress: GA-ANS decode + dequantize to ``y_hat``."""
+        """Coding half of decompress: GA-ANS decode + dequantize to ``y_hat``.
+        CompressAI's own bitstreams (``strings = [[bytes per image]]`` from
+        ``FactorizedPrior.compress`` with its RANS coder) decode on the GPU
+        too, one lane per image stream."""
+        if (isinstance(strings, (list, tuple)) and len(strings) == 1
+                and is_compressai_strings(strings[0])):
+            return self._decode_compressai(strings[0], shape)
         if (not isinstance(strings, (list, tuple)) or len(strings) != 1
                 or not isinstance(strings[0], WarpDivPayload)):
             raise CoderInputError("warp_div decompress expects strings=[WarpDivPayload]")
@@ -130,6 +136,24 @@ class FactorizedWarpDivCodec:
             ext = ext.expand(B, *([-1] * (len(shape) + 1)))
             return entropy.dequantize(symbols, ext, ext.dtype)
 
+    def _decode_compressai(self, streams, shape) -> torch.Tensor:
+        """EntropyBottleneck.decompress of CompressAI bitstreams: table =
+        channel, ``y_hat = float(symbol) + median``."""
+        if (not isinstance(shape, (tuple, list, torch.Size)) or len(shape) != 2
+                or any(type(d) is not int or d <= 0 for d in shape)):
+            raise CoderInputError("decompress expects a positive (height, width) shape")
+        entropy = self.model.entropy_bottleneck
+        C = entropy.channels
+        cdfs, _, _ = self._tables(entropy)
+        device = cdfs.device
+        tables = self._prepared(entropy, device)
+        B, N = len(streams), C * shape[0] * shape[1]
+        with torch.no_grad():
+            buf, offs = gaans.pack_streams(streams, device)
+            symbols = gaans.decode_rans64(buf, offs, tables, B, N, C, device)
+            medians = entropy._extend_ndims(entropy._get_medians().detach(), 2)
+            return symbols.reshape(B, C, *shape).type_as(medians) + medians
+
     def synthesize(self, y_hat: torch.Tensor):
         """Inference half of decompress: ``x_hat = g_s(y_hat).clamp(0, 1)``."""
         with torch.no_grad():
@@ -151,6 +175,12 @@ class FactorizedWarpDivCodec:
             y_hat = self.decode_latents(strings, shape)
         with _Span(timing, "decompress_inference_ms"):
             return self.synthesize(y_hat)
+
+
+def is_compressai_strings(value) -> bool:
+    """A CompressAI ``compress`` string list: one ``bytes`` per image."""
+    return (isinstance(value, (list, tuple)) and len(value) > 0
+            and all(isinstance(s, (bytes, bytearray)) for s in value))
 
 
 class _Span:

@@ -274,3 +274,61 @@ def decode_gaussian(packed: torch.Tensor, tables: PreparedTables, B: int, N: int
     if status:
         raise CoderInputError(f"warp_div decode failed: {_native.describe_status(status)}")
     return out
+
+
+def decode_rans64(streams: torch.Tensor, offsets: torch.Tensor, tables: PreparedTables, B: int,
+                  N: int, C: int, device, *, indexes: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode B CompressAI Rans64 streams (uint8 ``streams`` on the device,
+    stream b at bytes ``[offsets[b], offsets[b + 1])``, int64 ``offsets``)
+    into int32 symbols [B, N]; ``indexes`` None means table = channel."""
+    L = _native.lib()
+    dev = torch.device("cuda", _index(device))
+    if (streams.dtype != torch.uint8 or streams.device != dev or not streams.is_contiguous()
+            or offsets.dtype != torch.int64 or offsets.device != dev
+            or not offsets.is_contiguous() or offsets.numel() != B + 1):
+        raise CoderInputError("streams must be uint8 and offsets int64 [B + 1], contiguous, "
+                              f"on {dev}")
+    if indexes is not None and (indexes.dtype != torch.int32 or indexes.device != dev
+                                or not indexes.is_contiguous() or indexes.numel() != B * N):
+        raise CoderInputError(f"indexes must be a contiguous int32 [B, N] tensor on {dev}")
+    index = dev.index
+    prev = _enter_device(index)
+    try:
+        sp = torch._C._cuda_getCurrentRawStream(index)
+        st = _state(index, sp)
+        st.status_np[1] = 0
+        out = torch.empty((B, N), dtype=torch.int32, device=dev)
+        rc = L.gaans_rans64_decode(sp, streams.data_ptr() if streams.numel() else None,
+                                   streams.numel(), offsets.data_ptr(), _ptr(indexes),
+                                   tables.ref, B, N, C, out.data_ptr(), st.ctrl_ptr,
+                                   st.status_ptr)
+        if rc:
+            _native.check(rc, "Rans64 decode")
+        rc = L.gaans_wait_host_word(sp, st.status_done)
+        if rc:
+            _native.check(rc, "Rans64 decode")
+        status = int(st.status_np[1]) >> 1
+    finally:
+        if prev is not None:
+            torch.cuda.set_device(prev)
+    if status:
+        raise CoderInputError(f"Rans64 decode failed: {_native.describe_status(status)}")
+    return out
+
+
+def pack_streams(strings, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """CompressAI per-image byte strings -> (uint8 device buffer, int64
+    offsets [B + 1]), each stream starting on a 4-byte boundary."""
+    import numpy as np
+
+    if not strings or not all(isinstance(s, (bytes, bytearray)) for s in strings):
+        raise CoderInputError("expected a non-empty list of CompressAI byte strings")
+    sizes = [len(s) for s in strings]
+    if any(n % 4 for n in sizes):
+        raise CoderInputError("a Rans64 stream is a whole number of 32-bit words")
+    offs = np.zeros(len(strings) + 1, dtype=np.int64)
+    np.cumsum(sizes, out=offs[1:])
+    buf = np.frombuffer(b"".join(bytes(s) for s in strings), dtype=np.uint8)
+    dev = torch.device(device)
+    return (torch.from_numpy(buf.copy()).to(dev, non_blocking=False),
+            torch.from_numpy(offs).to(dev, non_blocking=False))

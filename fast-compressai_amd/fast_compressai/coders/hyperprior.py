@@ -28,7 +28,7 @@ import torch
 
 from . import gaans
 from .errors import CoderInputError
-from .factorized import _Span
+from .factorized import _Span, is_compressai_strings
 from .tables import TableCache
 from .warp_div import WarpDivBackend, WarpDivPayload, coding_fingerprint
 
@@ -187,7 +187,12 @@ class HyperpriorWarpDivCodec:
             return {"strings": [y_payload, z_payload], "shape": tuple(z.shape[-2:])}
 
     def decode_latents(self, strings, shape) -> torch.Tensor:
-        """Coding half of decompress: z decode, ``h_s``, y decode to ``y_hat``."""
+        """Coding half of decompress: z decode, ``h_s``, y decode to ``y_hat``.
+        CompressAI's own bitstreams (``strings = [y bytes per image, z bytes
+        per image]``) decode on the GPU too, one lane per image stream."""
+        if (isinstance(strings, (list, tuple)) and len(strings) == 2
+                and all(is_compressai_strings(s) for s in strings)):
+            return self._decode_compressai(strings, shape)
         if (not isinstance(strings, (list, tuple)) or len(strings) != 2
                 or not all(isinstance(s, WarpDivPayload) for s in strings)):
             raise CoderInputError("warp_div hyperprior decompress expects strings=[y, z] payloads")
@@ -222,6 +227,35 @@ class HyperpriorWarpDivCodec:
                 if means is not None:
                     y_hat = y_hat + means.reshape(B, N)
             return y_hat.reshape(scales.shape)
+
+    def _decode_compressai(self, strings, shape) -> torch.Tensor:
+        """CompressAI's hyperprior decompress of its own bitstreams: z by the
+        EntropyBottleneck (table = channel, + medians), scales (and means)
+        from ``h_s``, y by the GaussianConditional with ``build_indexes``
+        (computed with torch), ``y_hat = float(symbol) (+ means)``."""
+        if (not isinstance(shape, (tuple, list, torch.Size)) or len(shape) != 2
+                or any(type(d) is not int or d <= 0 for d in shape)):
+            raise CoderInputError("decompress expects a positive (height, width) shape")
+        y_strings, z_strings = strings
+        if len(y_strings) != len(z_strings):
+            raise CoderInputError("y and z string lists differ in length")
+        eb, gc = self.model.entropy_bottleneck, self.model.gaussian_conditional
+        device = eb._quantized_cdf.device
+        B, Cz = len(z_strings), eb.channels
+        with torch.no_grad():
+            ztab = self._prepared(eb, "entropy bottleneck", device)
+            buf, offs = gaans.pack_streams(z_strings, device)
+            zs = gaans.decode_rans64(buf, offs, ztab, B, Cz * shape[0] * shape[1], Cz, device)
+            med = eb._extend_ndims(eb._get_medians().detach(), 2)
+            z_hat = zs.reshape(B, Cz, *shape).type_as(med) + med
+            scales, means = self._params(z_hat)
+            C, N = int(scales.size(1)), int(scales[0].numel())
+            ytab = self._prepared(gc, "gaussian conditional", device)
+            idx = self._build_indexes(scales).reshape(B, N).contiguous()
+            buf, offs = gaans.pack_streams(y_strings, device)
+            ys = gaans.decode_rans64(buf, offs, ytab, B, N, C, device, indexes=idx)
+            y_hat = ys.reshape(scales.shape).to(torch.float32)
+            return y_hat + means if means is not None else y_hat
 
     def synthesize(self, y_hat: torch.Tensor):
         """Inference half of decompress: ``x_hat = g_s(y_hat).clamp(0, 1)``."""

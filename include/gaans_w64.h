@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define GAANS_ABI_VERSION 5
+#define GAANS_ABI_VERSION 6
 #define GAANS_CTRL_BYTES 256
 
 /* return codes */
@@ -208,6 +208,27 @@ int gaans_decode_gaussian(void* stream, const uint8_t* payload_dev, int64_t payl
                           const float* scale_table_dev, int32_t n_scales, float scale_bound,
                           const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
                           int64_t P, float* y_hat_dev, void* ctrl_dev, uint32_t* status_out);
+
+/* ---- CompressAI Rans64 bitstreams ------------------------------------------ */
+
+/* Decode B CompressAI Rans64 streams (what RansEncoder.encode_with_indexes
+ * writes for one image: 64-bit state, 32-bit words, 16-bit CDFs, escapes as
+ * 4-bit bypass groups), one stream per batch row, into int32 symbols [B, N].
+ * The streams lie back to back in streams_dev (streams_bytes bytes); stream b
+ * is bytes [offsets_dev[b], offsets_dev[b + 1]) (B + 1 int64 offsets in device
+ * memory, multiples of 4).  indexes_dev [B, N], or NULL: position i uses table
+ * i / (N / C) (EntropyBottleneck).  tables: gaans_tables_prepare of the same
+ * CDFs.  Status (as in gaans_decode_symbols): GAANS_ST_CORRUPT when a stream
+ * is too short, ends early or holds an impossible escape, GAANS_ST_INDEX for
+ * an index >= M.  One lane decodes one stream (a stream is one serial chain).
+ * Replaces CompressAI's RansDecoder.decode_with_indexes as the reference's
+ * coder="rans" path calls it (src/fast_compressai/coders/compressai_ans.py:51-87)
+ * and the reference's per-chunk GPU decode loop
+ * (src/fast_compressai/coders/cuda/ans_gpu_kernel.cu:295-394). */
+int gaans_rans64_decode(void* stream, const uint8_t* streams_dev, int64_t streams_bytes,
+                        const int64_t* offsets_dev, const int32_t* indexes_dev,
+                        const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
+                        int32_t* out_dev, void* ctrl_dev, uint32_t* status_out);
 
 /* ---- completion ------------------------------------------------------------ */
 

@@ -98,3 +98,18 @@ def test_sequential_helpers_without_a_coder_use_the_model():
     outs = fast.compress_many([1, 2])
     assert [o["strings"][0] for o in outs] == [1, 2]
     assert [r["x_hat"] for r in fast.decompress_many(outs)] == [1, 2]
+
+
+def test_compressai_string_packing():
+    from fast_compressai.coders import gaans
+    from fast_compressai.coders.factorized import is_compressai_strings
+
+    buf, offs = gaans.pack_streams([b"\1\2\3\4", b"", b"\5\6\7\10\11\12\13\14"], "cpu")
+    assert offs.tolist() == [0, 4, 4, 12] and offs.dtype.is_floating_point is False
+    assert bytes(buf.numpy()) == b"\1\2\3\4\5\6\7\10\11\12\13\14"
+    for bad in ([], [b"abc"], ["abcd"], [b"abcd", 3]):
+        with pytest.raises(fast_compressai.CoderInputError):
+            gaans.pack_streams(bad, "cpu")
+    assert is_compressai_strings([b"ab", bytearray(b"cd")])
+    assert not is_compressai_strings([]) and not is_compressai_strings([b"ab", None])
+    assert not is_compressai_strings(b"abcd")
