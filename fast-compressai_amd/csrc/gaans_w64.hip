@@ -261,10 +261,27 @@ __device__ __forceinline__ uint64_t ballot(bool pred) { return __builtin_amdgcn_
 // Keep a wave-uniform value in a scalar register.
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-__device__ __forceinline__ bool tables_ok(const uint8_t* tables, uint32_t M, uint32_t bytes) {
-  const TabHdr* h = reinterpret_cast<const TabHdr*>(tables);
-  return h->magic == kTabMagic && h->M == M && h->total_bytes == bytes &&
-         h->lut_bits == (uint32_t)kLutBits;
+// Section offsets of a prepared table blob, derived on the host from the
+// descriptor (M, symbols, sub-blocks), so the kernels address the sections
+// without first reading the blob header.
+struct BlobRef {
+  uint32_t meta_off, ent_off, lut_off, dense_off, total_dense;
+};
+
+// The blob header matches the call: magic, table count, size, lookup width
+// and the section offsets.  Branch-free, so that the header's words load in
+// one round trip.
+__device__ __forceinline__ bool tables_ok(const TabHdr& h, uint32_t M, uint32_t bytes,
+                                          const BlobRef& r) {
+  return (h.magic == kTabMagic) & (h.M == M) & (h.total_bytes == bytes) &
+         (h.lut_bits == (uint32_t)kLutBits) & (h.meta_off == r.meta_off) &
+         (h.ent_off == r.ent_off) & (h.lut_off == r.lut_off) & (h.dense_off == r.dense_off) &
+         (h.total_dense == r.total_dense);
+}
+
+// Blob header in registers (one 64-byte scalar load).
+__device__ __forceinline__ TabHdr load_tab_hdr(const uint8_t* tables) {
+  return *reinterpret_cast<const TabHdr*>(tables);
 }
 
 __device__ __forceinline__ int chunk_len_of(int64_t g, int32_t K, int32_t chunk_len, int64_t N) {
@@ -363,25 +380,46 @@ __device__ __forceinline__ void stage_pass(const Tabs& T, uint4* lmeta, uint2* l
 // lookups (llut), metadata and, when lsub is given, the tables' sub-blocks.
 // The lookups, which need no metadata, are copied while the metadata loads
 // are in flight; lookups and sub-blocks are 16-byte aligned in the blob.
+// Entry and sub-block ranges of the staged tables [t_lo, t_hi) (t_lo < M;
+// t_lo == t_hi when nothing is staged), read from the blob's metadata.  Every
+// load is unconditional, so a kernel can issue them with its other first
+// loads.
+struct StageBounds {
+  uint32_t base0, ent_end, d0, d1;
+};
+
+__device__ __forceinline__ StageBounds stage_bounds(const TabMeta* __restrict__ gmeta, int t_lo,
+                                                    int t_hi, uint32_t M,
+                                                    uint32_t total_blocks) {
+  const TabMeta lo = gmeta[t_lo];
+  const TabMeta last = gmeta[t_hi > 0 ? t_hi - 1 : 0];
+  const uint32_t next = gmeta[(uint32_t)t_hi < M ? t_hi : (int)M - 1].dense_base;
+  StageBounds b;
+  b.base0 = lo.ent_base;
+  b.ent_end = last.ent_base + last.nsym;
+  b.d0 = lo.dense_base;
+  b.d1 = (uint32_t)t_hi < M ? next : total_blocks;
+  return b;
+}
+
 template <int NT>
 __device__ void stage_tables(Tabs& T, uint4* lmeta, uint2* lent, uint64_t* llut, uint64_t* lsub,
-                             uint32_t total_blocks, uint32_t M, int t_lo, int t_hi, int tid) {
+                             const StageBounds& bd, int t_lo, int t_hi, int tid) {
   T.t_lo = t_lo;
   T.nt = t_hi > t_lo ? t_hi - t_lo : 0;
   T.sub_first = 0;
   T.sub_lds = lsub != nullptr;
   if (T.nt > 0) {
     const uint32_t nt = (uint32_t)T.nt;
-    const uint32_t base0 = T.gmeta[t_lo].ent_base;
+    const uint32_t base0 = bd.base0;
     if (lent) {
-      const TabMeta last = T.gmeta[t_hi - 1];
-      const uint32_t ne = last.ent_base + last.nsym - base0;
+      const uint32_t ne = bd.ent_end - base0;
       stage_pass<NT, true, false>(T, lmeta, lent, nullptr, nullptr, nt, ne, 0u, base0, t_lo, tid);
     } else {
       const uint4* lut_src = reinterpret_cast<const uint4*>(T.glut + (int64_t)t_lo * kLutSize);
       copy16<NT, 4>(reinterpret_cast<uint4*>(llut), lut_src, nt * (kLutSize / 2), tid);
-      const uint32_t d0 = T.gmeta[t_lo].dense_base;
-      const uint32_t d1 = (uint32_t)t_hi < M ? T.gmeta[t_hi].dense_base : total_blocks;
+      const uint32_t d0 = bd.d0;
+      const uint32_t d1 = bd.d1;
       if (lsub && d1 > d0) {
         T.sub_first = d0;
         stage_pass<NT, false, true>(T, lmeta, nullptr, reinterpret_cast<uint4*>(lsub),
@@ -459,6 +497,7 @@ struct EncArgs {
   const int32_t* __restrict__ indexes;
   const uint8_t* __restrict__ tables;
   uint32_t M, tables_bytes;
+  BlobRef blob;
   int64_t N;
   int32_t K, P, C, chunk_len;
   UDiv div_hw;
@@ -707,24 +746,18 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
   uint32_t* __restrict__ esc_list = a.esc_raw + g * a.chunk_len + a.chunk_len;
 
   if (tid < 2) eflag[tid] = 0u;  // visible after the staging barrier
-  const bool tab = tables_ok(a.tables, a.M, a.tables_bytes);  // uniform
+  const bool tab = tables_ok(load_tab_hdr(a.tables), a.M, a.tables_bytes, a.blob);  // uniform
   if (!tab) status |= GAANS_ST_TABLES;
   if (tab) {
-    const TabHdr* th = reinterpret_cast<const TabHdr*>(a.tables);
     Tabs tb;
-    tb.gmeta = reinterpret_cast<const TabMeta*>(a.tables + th->meta_off);
-    tb.gent = reinterpret_cast<const uint2*>(a.tables + th->ent_off);
+    tb.gmeta = reinterpret_cast<const TabMeta*>(a.tables + a.blob.meta_off);
+    tb.gent = reinterpret_cast<const uint2*>(a.tables + a.blob.ent_off);
     tb.glut = nullptr;
     tb.gsub = nullptr;
     tb.lmeta = lmeta;
     tb.lent = lent;
     tb.llut = nullptr;
     tb.lsub = nullptr;
-    int t_lo, t_hi;
-    stage_range(a.nt_cap, a.stage_all, k, a.P, (int)a.M, t_lo, t_hi);
-    if (kMode == kModeGaussian) stage_scales<kThreads>(scl, a.scale_table, a.n_scales, tid);
-    stage_tables<kThreads>(tb, lmeta, lent, nullptr, nullptr, 0u, a.M, t_lo, t_hi, tid);
-
     // mapper wave w (1..kMappers) owns steps u = w - 1 + kMappers e of every block
     int32_t ca[kPer], cb[kPer], na[kPer], nb[kPer];
     float cm[kPer], nm[kPer];
@@ -752,6 +785,19 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
         }
       }
     };
+    // the mappers' first two blocks of inputs need no tables: their loads
+    // are in flight while the tables are staged
+    if (wid != 0 && nblk > 0) {
+      load_block(nblk - 1, ca, cb, cm);
+      if (nblk > 1) load_block(nblk - 2, na, nb, nm);
+    }
+    int t_lo, t_hi;
+    stage_range(a.nt_cap, a.stage_all, k, a.P, (int)a.M, t_lo, t_hi);
+    if (kMode == kModeGaussian) stage_scales<kThreads>(scl, a.scale_table, a.n_scales, tid);
+    stage_tables<kThreads>(tb, lmeta, lent, nullptr, nullptr,
+                           stage_bounds(tb.gmeta, t_lo, t_hi, a.M, a.blob.total_dense), t_lo,
+                           t_hi, tid);
+
     auto map_steps = [&](int j, auto lds_tag) {
       constexpr bool kLds = decltype(lds_tag)::value;
       uint4* dst = recs + (j & 1) * SB * kLanes;
@@ -834,11 +880,7 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
       }
       if (fl > wp) ring_flush(wbuf, ring, wp, fl, lane);
     } else {
-      if (nblk > 0) {
-        load_block(nblk - 1, ca, cb, cm);
-        if (nblk > 1) load_block(nblk - 2, na, nb, nm);
-        map_block(nblk - 1);
-      }
+      if (nblk > 0) map_block(nblk - 1);
       __syncthreads();
       for (int j = nblk - 1; j >= 0; --j) {
         if (j > 0) {  // mappers: block j - 1 while the coder codes block j
@@ -1034,6 +1076,7 @@ struct DecArgs {
   const int32_t* __restrict__ indexes;
   const uint8_t* __restrict__ tables;
   uint32_t M, tables_bytes;
+  BlobRef blob;
   const float* __restrict__ medians;
   const float* __restrict__ means;        // Gaussian: per element, or NULL
   const float* __restrict__ scales;       // Gaussian: per element
@@ -1384,18 +1427,31 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   const int wid = uni(tid >> 6);  // wave role, kept in a scalar register
   uint32_t status = 0, hash = 0, enib = 0;
   const uint32_t* __restrict__ hdr = reinterpret_cast<const uint32_t*>(a.payload);
-  const TabHdr* th = reinterpret_cast<const TabHdr*>(a.tables);
-  bool ok = true;  // uniform over the workgroup
-  if (a.payload_bytes < a.header_bytes || hdr[0] != kMagic || hdr[1] != kVersion ||
-      hdr[2] != a.B || hdr[3] != (uint32_t)a.N || hdr[4] != a.C || hdr[5] != a.P ||
-      hdr[6] != a.K || hdr[7] != a.chunk_len || hdr[8] != a.M || hdr[9] != kParams) {
-    status |= GAANS_ST_HEADER;
-    ok = false;
-  } else if (!tables_ok(a.tables, a.M, a.tables_bytes) || hdr[10] != th->digest_lo ||
-             hdr[11] != th->digest_hi) {
-    status |= GAANS_ST_TABLES;
-    ok = false;
-  }
+  // Header words, the chunk's end offsets and index hash, and the table
+  // blob's header, all in one round trip: every word is read (the host has
+  // checked that the payload holds the header), the loads are issued before
+  // any of them is used (the scheduling barrier keeps them together), and
+  // the checks are branch-free.
+  const TabHdr th = load_tab_hdr(a.tables);
+  uint32_t hw[12];
+#pragma unroll
+  for (int i = 0; i < 12; ++i) hw[i] = hdr[i];
+  // end offsets of chunks g - 1 and g: two adjacent words (word 15 of the
+  // fixed header stands in for chunk -1 and is not used)
+  const uint32_t* pe = hdr + (kFixedWords - 1) + g;
+  const uint32_t e_prev = pe[0];
+  const uint32_t e_end = pe[1];
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t e_hash = hdr[kFixedWords + a.BK + g];  // needed at the end only
+  const bool hdr_ok = (hw[0] == kMagic) & (hw[1] == kVersion) & (hw[2] == a.B) &
+                      (hw[3] == (uint32_t)a.N) & (hw[4] == a.C) & (hw[5] == a.P) &
+                      (hw[6] == a.K) & (hw[7] == a.chunk_len) & (hw[8] == a.M) &
+                      (hw[9] == kParams);
+  const bool tab_ok = tables_ok(th, a.M, a.tables_bytes, a.blob) & (hw[10] == th.digest_lo) &
+                      (hw[11] == th.digest_hi);
+  const bool offsets_safe = (th.flags & kTabOffsetsSafe) != 0;
+  bool ok = hdr_ok & tab_ok;  // uniform over the workgroup
+  status |= !hdr_ok ? GAANS_ST_HEADER : (!tab_ok ? GAANS_ST_TABLES : 0u);
   int64_t row;
   int32_t start;
   int len, k;
@@ -1403,29 +1459,25 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   const int T = (len + kLanes - 1) / kLanes;
   const int A = len < kLanes ? len : kLanes;
   const int nblk = (T + SB - 1) / SB;
-  uint32_t beg = 0, endo = 0, want_hash = 0;
-  int64_t cb = 0;
-  if (ok) {
-    beg = g ? hdr[kFixedWords + g - 1] : 0u;
-    endo = hdr[kFixedWords + g];
-    want_hash = hdr[kFixedWords + a.BK + g];
-    cb = (int64_t)endo - (int64_t)beg;
-    if (endo < beg || (int64_t)endo > a.payload_bytes - a.header_bytes || (beg & 3u) ||
-        cb < 4 * A || ((cb - 4 * A) & 3)) {
-      status |= GAANS_ST_CORRUPT;
-      ok = false;
-    }
-  }
+  // the chunk's bytes: the offsets are used unconditionally, so that their
+  // loads are not moved behind the header checks
+  const uint32_t beg = g ? e_prev : 0u;
+  const uint32_t endo = e_end;
+  const uint32_t want_hash = e_hash;
+  const int64_t cb = (int64_t)endo - (int64_t)beg;
+  const bool bad_range = (endo < beg) | ((int64_t)endo > a.payload_bytes - a.header_bytes) |
+                         ((beg & 3u) != 0u) | (cb < 4 * A) | (((cb - 4 * A) & 3) != 0);
+  status |= (ok & bad_range) ? GAANS_ST_CORRUPT : 0u;
+  ok = ok & !bad_range;
   Stream S;  // the coder's; its final position is checked after the last barrier
   S.rp = 0;
   S.q = 0;
   if (ok) {
     Tabs tb;
-    tb.gmeta = reinterpret_cast<const TabMeta*>(a.tables + th->meta_off);
-    tb.gent = reinterpret_cast<const uint2*>(a.tables + th->ent_off);
-    tb.glut = reinterpret_cast<const uint64_t*>(a.tables + th->lut_off);
-    tb.gsub = reinterpret_cast<const uint64_t*>(a.tables + th->dense_off);
-    const bool offsets_safe = (th->flags & kTabOffsetsSafe) != 0;
+    tb.gmeta = reinterpret_cast<const TabMeta*>(a.tables + a.blob.meta_off);
+    tb.gent = reinterpret_cast<const uint2*>(a.tables + a.blob.ent_off);
+    tb.glut = reinterpret_cast<const uint64_t*>(a.tables + a.blob.lut_off);
+    tb.gsub = reinterpret_cast<const uint64_t*>(a.tables + a.blob.dense_off);
     tb.lmeta = lmeta;
     tb.lent = nullptr;
     tb.llut = llut;
@@ -1542,7 +1594,8 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
     int t_lo, t_hi;
     stage_range(a.nt_cap, a.stage_all, k, (int)a.P, (int)a.M, t_lo, t_hi);
     stage_tables<kDecThreads>(tb, lmeta, nullptr, llut, a.nd_cap ? lsub : nullptr,
-                              th->total_dense, a.M, t_lo, t_hi, tid);
+                              stage_bounds(tb.gmeta, t_lo, t_hi, a.M, a.blob.total_dense), t_lo,
+                              t_hi, tid);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load crosses the role split
 
     // The coder, the mappers and the escape reader run separate code (the
@@ -1738,6 +1791,7 @@ struct R64Args {
   const int32_t* __restrict__ indexes;  // [B, N], or NULL: table = position / HW
   const uint8_t* __restrict__ tables;
   uint32_t M, tables_bytes;
+  BlobRef blob;
   int64_t B, N;
   UDiv div_hw;
   int32_t stage;       // 0: global lookups, 1: all tables staged, 2: one channel at a time
@@ -1815,8 +1869,7 @@ __global__ void __launch_bounds__(kLanes) k_rans64_decode(R64Args a) {
   const int64_t b = (int64_t)blockIdx.x * a.spw + lane;
   const bool live = lane < a.spw && b < a.B;
   uint32_t status = 0;
-  const TabHdr* th = reinterpret_cast<const TabHdr*>(a.tables);
-  const bool tab = tables_ok(a.tables, a.M, a.tables_bytes);
+  const bool tab = tables_ok(load_tab_hdr(a.tables), a.M, a.tables_bytes, a.blob);
   if (!tab) status |= GAANS_ST_TABLES;
 
   // the lane's stream: [off_b, off_b+1) inside the buffer, whole words
@@ -1849,10 +1902,10 @@ __global__ void __launch_bounds__(kLanes) k_rans64_decode(R64Args a) {
   }
 
   Tabs tb;
-  tb.gmeta = reinterpret_cast<const TabMeta*>(a.tables + th->meta_off);
+  tb.gmeta = reinterpret_cast<const TabMeta*>(a.tables + a.blob.meta_off);
   tb.gent = nullptr;
-  tb.glut = reinterpret_cast<const uint64_t*>(a.tables + th->lut_off);
-  tb.gsub = reinterpret_cast<const uint64_t*>(a.tables + th->dense_off);
+  tb.glut = reinterpret_cast<const uint64_t*>(a.tables + a.blob.lut_off);
+  tb.gsub = reinterpret_cast<const uint64_t*>(a.tables + a.blob.dense_off);
   tb.lmeta = lmeta;
   tb.lent = nullptr;
   tb.llut = llut;
@@ -1862,10 +1915,11 @@ __global__ void __launch_bounds__(kLanes) k_rans64_decode(R64Args a) {
   tb.sub_first = 0;
   tb.sub_lds = false;
   const bool any = ballot(act0) != 0ull;
-  const uint32_t total_dense = tab ? th->total_dense : 0u;
+  const uint32_t total_dense = a.blob.total_dense;
   if (any && a.stage == 1)
-    stage_tables<kLanes>(tb, lmeta, nullptr, llut, a.stage_subs ? lsub : nullptr, total_dense,
-                         a.M, 0, (int)a.M, lane);
+    stage_tables<kLanes>(tb, lmeta, nullptr, llut, a.stage_subs ? lsub : nullptr,
+                         stage_bounds(tb.gmeta, 0, (int)a.M, a.M, total_dense), 0, (int)a.M,
+                         lane);
   int cur = -1;  // staged channel (stage 2)
   uint32_t c_nsym = 0;
   int32_t c_off = 0;
@@ -1899,10 +1953,11 @@ __global__ void __launch_bounds__(kLanes) k_rans64_decode(R64Args a) {
       if (kImplicit) {
         // the same in every lane: stage the channel's table when it changes
         const int tc = uni((int)udiv((uint32_t)i, a.div_hw));
-        if (a.stage == 2 && tc != cur) {
+        if (__builtin_expect(a.stage == 2 && tc != cur, 0)) {
           cur = tc;
           stage_tables<kLanes>(tb, lmeta, nullptr, llut, a.stage_subs ? lsub : nullptr,
-                               total_dense, a.M, cur, cur + 1, lane);
+                               stage_bounds(tb.gmeta, cur, cur + 1, a.M, total_dense), cur,
+                               cur + 1, lane);
           const uint4 lm = lmeta[0];
           c_nsym = lm.y;
           c_off = (int32_t)lm.z;
@@ -1991,6 +2046,25 @@ int check_tables_arg(const gaans_tables* t) {
   if (t->max_nsym < 1 || t->total_nsym < t->max_nsym || t->max_dense < 0 ||
       t->total_dense < t->max_dense)
     return fail(GAANS_EINVAL, "tables descriptor is inconsistent");
+  return GAANS_OK;
+}
+
+// Section offsets of the blob a descriptor describes (the layout written by
+// gaans_tables_prepare); the descriptor's size must match them.
+int blob_ref(const gaans_tables* t, BlobRef* r) {
+  const int64_t M = t->M;
+  const int64_t ent_off = align_up((int64_t)sizeof(TabHdr) + (int64_t)sizeof(TabMeta) * M, 8);
+  const int64_t lut_off = align_up(ent_off + 8 * t->total_nsym, 16);
+  const int64_t dense_off = lut_off + 8ll * kLutSize * M;
+  const int64_t end = dense_off + (int64_t)kSubBytes * t->total_dense;
+  if (end != t->bytes)
+    return fail(GAANS_EINVAL, "tables descriptor does not describe a prepared blob (%lld bytes "
+                "for its counts, %lld given)", (long long)end, (long long)t->bytes);
+  r->meta_off = (uint32_t)sizeof(TabHdr);
+  r->ent_off = (uint32_t)ent_off;
+  r->lut_off = (uint32_t)lut_off;
+  r->dense_off = (uint32_t)dense_off;
+  r->total_dense = (uint32_t)t->total_dense;
   return GAANS_OK;
 }
 
@@ -2188,6 +2262,8 @@ int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y
   if (!ws || ws_bytes < L.ws_bytes)
     return fail(GAANS_EINVAL, "workspace too small (%lld < %lld bytes)", (long long)ws_bytes,
                 (long long)L.ws_bytes);
+  BlobRef blob;
+  if ((rc = blob_ref(tables, &blob))) return rc;
   uint8_t* w = static_cast<uint8_t*>(ws);
   DevLds dl;
   if ((rc = device_lds(&dl))) return rc;
@@ -2209,6 +2285,7 @@ int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y
   a.tables = static_cast<const uint8_t*>(tables->dev);
   a.M = (uint32_t)tables->M;
   a.tables_bytes = (uint32_t)tables->bytes;
+  a.blob = blob;
   a.N = N;
   a.K = (int32_t)L.K;
   a.P = (int32_t)P;
@@ -2277,6 +2354,8 @@ int decode_impl(int mode, void* stream, const uint8_t* payload, int64_t payload_
   if (payload_bytes < L.header_bytes)
     return fail(GAANS_EINVAL, "payload (%lld bytes) is shorter than its header (%lld bytes)",
                 (long long)payload_bytes, (long long)L.header_bytes);
+  BlobRef blob;
+  if ((rc = blob_ref(tables, &blob))) return rc;
   DevLds dl;
   if ((rc = device_lds(&dl))) return rc;
   const bool latents = mode != kModeSymbols;
@@ -2290,6 +2369,7 @@ int decode_impl(int mode, void* stream, const uint8_t* payload, int64_t payload_
   a.tables = static_cast<const uint8_t*>(tables->dev);
   a.M = (uint32_t)tables->M;
   a.tables_bytes = (uint32_t)tables->bytes;
+  a.blob = blob;
   a.medians = medians;
   a.means = mode == kModeGaussian ? g->means : nullptr;
   a.scales = mode == kModeGaussian ? g->scales : nullptr;
@@ -2438,6 +2518,8 @@ int rans64_decode_impl(void* stream, const uint8_t* streams, int64_t streams_byt
   if (!indexes && C > tables->M)
     return fail(GAANS_EINVAL, "table = channel needs a table per channel (C=%lld > M=%d)",
                 (long long)C, tables->M);
+  BlobRef blob;
+  if ((rc = blob_ref(tables, &blob))) return rc;
   DevLds dl;
   if ((rc = device_lds(&dl))) return rc;
   const int64_t fixed = kR64RingBytes + (indexes ? kR64IdxBytes : 0);
@@ -2462,6 +2544,7 @@ int rans64_decode_impl(void* stream, const uint8_t* streams, int64_t streams_byt
   a.tables = static_cast<const uint8_t*>(tables->dev);
   a.M = (uint32_t)M;
   a.tables_bytes = (uint32_t)tables->bytes;
+  a.blob = blob;
   a.B = B;
   a.N = N;
   a.div_hw = make_udiv((uint32_t)(N / C));
