@@ -1252,10 +1252,12 @@ template <int SB>
 __device__ __forceinline__ void dec_refill(bool need, uint32_t& x, Stream& S, const uint16_t* ring,
                                            int lane) {
   const uint64_t m = ballot(need);
-  // every lane reads (no branch around the read); only refilling lanes keep it
+  // every lane reads and only refilling lanes keep the word; no select on the
+  // loaded value (which the compiler would turn into a branch around the
+  // read), and the shift is ready before the read returns
   const uint32_t w = ring[(S.rp + (int)lane_rank(m)) & (DecGeom<SB>::kRing - 1)];
-  asm volatile("" ::"v"(w));
-  x = need ? ((x << 16) | w) : x;
+  const uint32_t keep = need ? 0xffffu : 0u;
+  x = (x << (need ? 16 : 0)) | (w & keep);
   S.rp += __popcll(m);
 }
 
