@@ -63,7 +63,7 @@ constexpr uint32_t kMagic = 0x31574147u;  // "GAW1"
 constexpr uint32_t kVersion = 2u;
 constexpr uint32_t kParams = 0x00041040u;  // lanes 64 | precision 16 << 8 | bypass 4 << 16
 constexpr int kFixedWords = 16;
-constexpr uint32_t kTabMagic = 0x33425447u;  // "GTB3"
+constexpr uint32_t kTabMagic = 0x34425447u;  // "GTB4"
 constexpr int kLutBits = 8;
 constexpr int kLutSize = 1 << kLutBits;
 constexpr int kSubBits = 4;                 // a sub-block: 16 entries of 16 or 1 values
@@ -121,10 +121,16 @@ struct TabHdr {
   uint32_t dense_off;    // byte offset of the sub-blocks
   uint32_t total_dense;  // sub-blocks over all tables
   uint32_t flags;        // kTabOffsetsSafe
-  uint32_t reserved[2];
+  uint32_t clut_off;    // byte offset of the search lookups (u32 per bucket)
+  uint32_t starts_off;  // byte offset of the symbol starts (u16 per symbol)
 };
 // every offset <= INT32_MAX - 65535: symbol index + offset cannot overflow
 constexpr uint32_t kTabOffsetsSafe = 1u;
+// the search lookups are filled: at most kSearchMaxSyms symbols in all, every
+// offset at least INT32_MIN + 65536 (offset - symbol base cannot wrap)
+constexpr uint32_t kTabSearch = 2u;
+constexpr int64_t kSearchMaxSyms = 65535 - 8;
+constexpr int kStartsPad = 8;  // zero starts after the last symbol (sentinel, reads past it)
 static_assert(sizeof(TabHdr) == 64, "table header is 64 bytes");
 
 struct TabMeta {
@@ -265,7 +271,7 @@ __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlan
 // descriptor (M, symbols, sub-blocks), so the kernels address the sections
 // without first reading the blob header.
 struct BlobRef {
-  uint32_t meta_off, ent_off, lut_off, dense_off, total_dense;
+  uint32_t meta_off, ent_off, lut_off, dense_off, total_dense, clut_off, starts_off;
 };
 
 // The blob header matches the call: magic, table count, size, lookup width
@@ -276,7 +282,8 @@ __device__ __forceinline__ bool tables_ok(const TabHdr& h, uint32_t M, uint32_t 
   return (h.magic == kTabMagic) & (h.M == M) & (h.total_bytes == bytes) &
          (h.lut_bits == (uint32_t)kLutBits) & (h.meta_off == r.meta_off) &
          (h.ent_off == r.ent_off) & (h.lut_off == r.lut_off) & (h.dense_off == r.dense_off) &
-         (h.total_dense == r.total_dense);
+         (h.total_dense == r.total_dense) & (h.clut_off == r.clut_off) &
+         (h.starts_off == r.starts_off);
 }
 
 // Blob header in registers (one 64-byte scalar load).
@@ -312,6 +319,8 @@ struct Tabs {
   const uint2* lent;       // encoder: both entry words
   const uint64_t* llut;    // decoder: nt x 256 lookup entries
   const uint64_t* lsub;    // decoder: sub-blocks of the staged tables
+  const uint32_t* lclut;   // decoder, search lookups: bucket entries of all tables
+  const uint16_t* lstarts; // decoder, search lookups: symbol starts of all tables
   int t_lo, nt;
   uint32_t sub_first;      // first staged sub-block
   bool sub_lds;            // decoder: sub-blocks staged with the lookups
@@ -1090,6 +1099,7 @@ struct DecArgs {
   uint32_t B, C, P, K, chunk_len;
   UDiv div_hw;
   int32_t nt_cap, ne_cap, nd_cap, stage_all;
+  uint32_t starts_words;  // search lookups: 16-byte words of starts to stage
   uint32_t* __restrict__ ctrl;
   uint32_t* __restrict__ status_out;
 };
@@ -1161,6 +1171,28 @@ __device__ __forceinline__ uint2 dec_record(const DecArgs& a, const Tabs& tb, in
   return r;
 }
 
+// Mapper record with the search lookups (all tables in LDS): x = table |
+// blob-wide index of its escape symbol << 16 (kNoSym past the chunk end),
+// y = offset - the table's first blob-wide symbol, so that the decoded
+// blob-wide index + y is the value.
+__device__ __forceinline__ uint2 dec_record_search(const DecArgs& a, const Tabs& tb, int lane,
+                                                   int t, int len, int32_t in_b, uint32_t& hash,
+                                                   uint32_t& status) {
+  const int p = lane + kLanes * t;
+  const bool act = p < len;
+  int32_t tbi = in_b;
+  const bool bad = act & ((uint32_t)tbi >= a.M);
+  const bool ok = act & !bad;
+  status |= bad ? GAANS_ST_INDEX : 0u;
+  tbi = ok ? tbi : 0;
+  hash += ok ? ((uint32_t)(tbi + 1) ^ ((uint32_t)p * kHashMul)) : 0u;
+  const uint4 lm = tb.lmeta[tbi];
+  uint2 r;
+  r.x = (uint32_t)tbi | ((act ? lm.x + lm.y - 1u : kNoSym) << 16);
+  r.y = lm.z - lm.x;
+  return r;
+}
+
 // One level down from a dense lookup entry e: entry i of its sub-block (LDS
 // when the sub-blocks are staged, else global memory).  The asm keeps the two
 // loads apart, so the compiler does not merge them into one generic load
@@ -1205,6 +1237,65 @@ __device__ __forceinline__ void dec_lookup(const Tabs& tb, uint32_t t, uint32_t 
   s = up ? s0 + 1u : s0;
   st = up ? st0 + fr0 : st0;
   fr = up ? nxt + 1u : fr0;
+}
+
+// cum -> (symbol, start, freq) with the search lookups, all tables in LDS:
+// the bucket entry gives g, the blob-wide index of the symbol that contains
+// the bucket's first value, and n, the symbols that start inside the bucket
+// after it.  A bucket with more than three is first narrowed by a 4-way
+// search over its starts (three probe reads per round trip, uniform loop
+// while any lane has more than three left); one read of starts g .. g + 4
+// then resolves the rest.  s is blob-wide (the record carries offset - base); the freq of a
+// table's last symbol comes from the next start modulo 2^16, which is the
+// next table's first start or a zero sentinel, both 0.
+__device__ __forceinline__ void dec_lookup_search(const Tabs& tb, uint32_t t, uint32_t cum,
+                                                  bool act, uint32_t& s, uint32_t& st,
+                                                  uint32_t& fr) {
+  const uint32_t e = tb.lclut[(t << kLutBits) + (cum >> (16 - kLutBits))];
+  uint32_t g = e & 0xffffu, n = e >> 16;
+  bool wide = act & (n > 3u);
+  if (__builtin_expect(ballot(wide) != 0ull, 0)) {
+    // invariant: start(g) <= cum, and the symbol is among g .. g + n; the
+    // probes q, 2q, 3q (q = (n + 1) / 4 >= 1) split it into four ranges
+    do {
+      if (wide) {
+        const uint32_t q = (n + 1u) >> 2;
+        const bool l1 = tb.lstarts[g + q] <= cum, l2 = tb.lstarts[g + 2u * q] <= cum,
+                   l3 = tb.lstarts[g + 3u * q] <= cum;
+        const uint32_t k = (uint32_t)l1 + (uint32_t)l2 + (uint32_t)l3;
+        g += k * q;
+        n = l3 ? n - 3u * q : q - 1u;
+      }
+      wide = act & (n > 3u);
+    } while (ballot(wide) != 0ull);
+  }
+  const uint16_t* p = tb.lstarts + g;
+  const uint32_t v0 = p[0], v1 = p[1], v2 = p[2], v3 = p[3], v4 = p[4];
+  const bool b1 = (n >= 1u) & (v1 <= cum), b2 = (n >= 2u) & (v2 <= cum),
+             b3 = (n >= 3u) & (v3 <= cum);
+  const uint32_t k = (uint32_t)b1 + (uint32_t)b2 + (uint32_t)b3;
+  s = g + k;
+  st = b3 ? v3 : (b2 ? v2 : (b1 ? v1 : v0));
+  const uint32_t nx = b3 ? v4 : (b2 ? v3 : (b1 ? v2 : v1));
+  fr = ((nx - st - 1u) & 0xffffu) + 1u;
+}
+
+// Stage every table's search lookups, starts and metadata (whole workgroup
+// of NT threads); blob-wide symbol indexes stay valid in LDS.
+template <int NT>
+__device__ void stage_search(Tabs& T, uint4* lmeta, uint32_t* lclut, uint16_t* lstarts,
+                             const uint8_t* tables, const BlobRef& blob, uint32_t M,
+                             uint32_t starts_words, int tid) {
+  T.t_lo = 0;
+  T.nt = (int)M;
+  T.sub_first = 0;
+  T.sub_lds = false;
+  copy16<NT, 3>(reinterpret_cast<uint4*>(lclut),
+                reinterpret_cast<const uint4*>(tables + blob.clut_off), M * (kLutSize / 4), tid);
+  copy16<NT, 3>(reinterpret_cast<uint4*>(lstarts),
+                reinterpret_cast<const uint4*>(tables + blob.starts_off), starts_words, tid);
+  stage_pass<NT, false, false>(T, lmeta, nullptr, nullptr, nullptr, M, 1u, 0u, 0u, 0, tid);
+  __syncthreads();
 }
 
 // Word stream of one chunk: prefetched from HBM into registers (kPfWords words
@@ -1378,7 +1469,7 @@ __device__ __forceinline__ void esc_resolve(uint64_t em, uint32_t base, uint32_t
 // the lanes that decoded the escape bin (their values are resolved by the
 // mappers, off the state chain).  kFull: every lane is active and no offset
 // can overflow with a symbol index.
-template <bool kLds, bool kFull, int SB>
+template <bool kLds, bool kFull, int SB, bool kSearch = false>
 __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint2 r, uint32_t& x,
                                              Stream& S, const uint16_t* ring, uint64_t& em,
                                              uint32_t& status, int lane) {
@@ -1386,7 +1477,8 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint2 r, uint
   const bool act = kFull || es != kNoSym;
   const uint32_t cum = x & 0xffffu;
   uint32_t s, st, fr;
-  dec_lookup<kLds>(tb, r.x & 0xffffu, cum, act, s, st, fr);
+  if constexpr (kSearch) dec_lookup_search(tb, r.x & 0xffffu, cum, act, s, st, fr);
+  else dec_lookup<kLds>(tb, r.x & 0xffffu, cum, act, s, st, fr);
   const uint32_t xn = __umul24(fr, x >> 16) + cum - st;
   x = act ? xn : x;
   dec_refill<SB>(act & (x < kStateLow), x, S, ring, lane);
@@ -1400,7 +1492,7 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint2 r, uint
   return (uint32_t)(oob ? 0 : o);
 }
 
-template <int kMode, bool kImplicit, int SB>
+template <int kMode, bool kImplicit, int SB, bool kSearch = false>
 __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   constexpr bool kLatents = kMode != kModeSymbols;  // fp32 output with a per-element add
   using G = DecGeom<SB>;
@@ -1417,10 +1509,14 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   uint32_t* part = reinterpret_cast<uint32_t*>(escm + 2 * SB);
   uint32_t* ctl = part + kDecPartBytes / 4;
   uint8_t* tsm = smem + G::fixed(kLatents);
+  // [luts][meta][sub-blocks], or with the search lookups [bucket entries]
+  // [meta][starts]: every part 16-byte aligned
+  constexpr int kLutEntry = kSearch ? 4 : 8;
   uint64_t* llut = reinterpret_cast<uint64_t*>(tsm);
-  uint4* lmeta = reinterpret_cast<uint4*>(tsm + 8 * kLutSize * a.nt_cap);
-  // [luts][meta][sub-blocks]: every part 16-byte aligned
-  uint64_t* lsub = reinterpret_cast<uint64_t*>(tsm + (8 * kLutSize + 16) * a.nt_cap);
+  uint32_t* lclut = reinterpret_cast<uint32_t*>(tsm);
+  uint4* lmeta = reinterpret_cast<uint4*>(tsm + kLutEntry * kLutSize * a.nt_cap);
+  uint64_t* lsub = reinterpret_cast<uint64_t*>(tsm + (kLutEntry * kLutSize + 16) * a.nt_cap);
+  uint16_t* lstarts = reinterpret_cast<uint16_t*>(lsub);
   float* scl = reinterpret_cast<float*>(smem + a.scales_lds);  // Gaussian: scale table
 
   const int64_t g = blockIdx.x;
@@ -1484,6 +1580,8 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
     tb.lent = nullptr;
     tb.llut = llut;
     tb.lsub = lsub;
+    tb.lclut = lclut;
+    tb.lstarts = lstarts;
     const uint8_t* cdata = a.payload + a.header_bytes + beg;
     const uint32_t* s32 = reinterpret_cast<const uint32_t*>(cdata + 4 * A);
     const uint32_t* safe = reinterpret_cast<const uint32_t*>(cdata);
@@ -1517,13 +1615,17 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
         const int u = (wid - 1) + kMappers * e;
         if (SB % kMappers != 0 && u >= SB) break;
         const uint2 r = src[u * kLanes + lane];
-        uint32_t v = r.x;
+        // the coder's value: in x, or with the search lookups in y (x keeps
+        // the table, whose offset the escape mapping needs)
+        uint32_t v = kSearch ? r.y : r.x;
         if (any_esc && j * SB + u < T) {
           const uint4 ei = escm[(j & 1) * SB + u];  // escaping lanes, first entry
           const uint64_t em = (uint64_t)(uint32_t)uni((int)ei.x) |
                               ((uint64_t)(uint32_t)uni((int)ei.y) << 32);
-          if (em) esc_resolve<R>(em, (uint32_t)uni((int)ei.z), r.y, v, avail, fifo, enib, status,
-                                 lane);
+          if (em) {
+            const uint32_t off = kSearch ? tb.lmeta[r.x & 0xffffu].z : r.y;
+            esc_resolve<R>(em, (uint32_t)uni((int)ei.z), off, v, avail, fifo, enib, status, lane);
+          }
         }
         const int p = lane + kLanes * (j * SB + u);
         if (p < len) {
@@ -1545,8 +1647,14 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
                                ? gauss_index(__int_as_float(cbx[e]), scl, a.n_scales,
                                              a.scales_pow2, a.scale_bound)
                                : cbx[e];
-        const uint2 r = dec_record<kImplicit>(a, tb, lane, j * SB + u, len, start, ix, hash,
-                                              status, all_lds);
+        uint2 r;
+        if constexpr (kSearch) {
+          r = dec_record_search(a, tb, lane, j * SB + u, len, ix, hash, status);
+          all_lds = true;
+        } else {
+          r = dec_record<kImplicit>(a, tb, lane, j * SB + u, len, start, ix, hash, status,
+                                    all_lds);
+        }
         dst[u * kLanes + lane] = r;
         if (kLatents) med[((j & 1) * SB + u) * kLanes + lane] = cm[e];
         if (!all_lds && lane == 0)
@@ -1595,9 +1703,14 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
     if (kMode == kModeGaussian) stage_scales<kDecThreads>(scl, a.scale_table, a.n_scales, tid);
     int t_lo, t_hi;
     stage_range(a.nt_cap, a.stage_all, k, (int)a.P, (int)a.M, t_lo, t_hi);
-    stage_tables<kDecThreads>(tb, lmeta, nullptr, llut, a.nd_cap ? lsub : nullptr,
-                              stage_bounds(tb.gmeta, t_lo, t_hi, a.M, a.blob.total_dense), t_lo,
-                              t_hi, tid);
+    if constexpr (kSearch) {
+      stage_search<kDecThreads>(tb, lmeta, lclut, lstarts, a.tables, a.blob, a.M,
+                                a.starts_words, tid);
+    } else {
+      stage_tables<kDecThreads>(tb, lmeta, nullptr, llut, a.nd_cap ? lsub : nullptr,
+                                stage_bounds(tb.gmeta, t_lo, t_hi, a.M, a.blob.total_dense),
+                                t_lo, t_hi, tid);
+    }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load crosses the role split
 
     // The coder, the mappers and the escape reader run separate code (the
@@ -1632,7 +1745,7 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
           uint64_t em[SB];
 #pragma unroll
           for (int u = 0; u < SB; ++u) {
-            ov[u] = dec_step<true, true, SB>(tb, r[u], x, S, sring, em[u], status, lane);
+            ov[u] = dec_step<true, true, SB, kSearch>(tb, r[u], x, S, sring, em[u], status, lane);
             any_em |= em[u];
           }
           if (__builtin_expect(any_em != 0ull, 0)) {
@@ -1642,22 +1755,32 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
               ecur += (uint32_t)__popcll(em[u]);
             }
           }
-          // decoded values replace the records' x words; the mappers store them
+          // decoded values replace the records' x words (y with the search
+          // lookups); the mappers store them
 #pragma unroll
-          for (int u = 0; u < SB; ++u) src[u * kLanes + lane].x = ov[u];
+          for (int u = 0; u < SB; ++u) {
+            if constexpr (kSearch) src[u * kLanes + lane].y = ov[u];
+            else src[u * kLanes + lane].x = ov[u];
+          }
         } else {
           // last block or tables outside LDS: one step at a time
 #pragma unroll 1
           for (int u = 0; u < SB && j * SB + u < T; ++u) {
             const uint2 ru = src[u * kLanes + lane];
             uint64_t em;
-            const uint32_t v = ((nl >> u) & 1u) == 0u
-                                   ? dec_step<true, false, SB>(tb, ru, x, S, sring, em, status, lane)
-                                   : dec_step<false, false, SB>(tb, ru, x, S, sring, em, status, lane);
+            uint32_t v;
+            if constexpr (kSearch) {
+              v = dec_step<true, false, SB, true>(tb, ru, x, S, sring, em, status, lane);
+            } else {
+              v = ((nl >> u) & 1u) == 0u
+                      ? dec_step<true, false, SB>(tb, ru, x, S, sring, em, status, lane)
+                      : dec_step<false, false, SB>(tb, ru, x, S, sring, em, status, lane);
+            }
             if (lane == 0) ei[u] = make_uint4((uint32_t)em, (uint32_t)(em >> 32), ecur, 0u);
             ecur += (uint32_t)__popcll(em);
             any_em |= em;
-            src[u * kLanes + lane].x = v;
+            if constexpr (kSearch) src[u * kLanes + lane].y = v;
+            else src[u * kLanes + lane].x = v;
           }
         }
         if (lane == 0) {
@@ -2051,22 +2174,37 @@ int check_tables_arg(const gaans_tables* t) {
   return GAANS_OK;
 }
 
+// Blob sections: [header][metadata][entries][lookups][sub-blocks][search
+// lookups][starts]; the offsets of the last two follow from the counts.
+struct BlobLayout {
+  int64_t ent_off, lut_off, dense_off, clut_off, starts_off, end;
+};
+
+BlobLayout blob_layout(int64_t M, int64_t total_syms, int64_t total_blocks) {
+  BlobLayout L;
+  L.ent_off = align_up((int64_t)sizeof(TabHdr) + (int64_t)sizeof(TabMeta) * M, 8);
+  L.lut_off = align_up(L.ent_off + 8 * total_syms, 16);
+  L.dense_off = L.lut_off + 8ll * kLutSize * M;
+  L.clut_off = L.dense_off + (int64_t)kSubBytes * total_blocks;
+  L.starts_off = L.clut_off + 4ll * kLutSize * M;
+  L.end = L.starts_off + align_up(2 * (total_syms + kStartsPad), 16);
+  return L;
+}
+
 // Section offsets of the blob a descriptor describes (the layout written by
 // gaans_tables_prepare); the descriptor's size must match them.
 int blob_ref(const gaans_tables* t, BlobRef* r) {
-  const int64_t M = t->M;
-  const int64_t ent_off = align_up((int64_t)sizeof(TabHdr) + (int64_t)sizeof(TabMeta) * M, 8);
-  const int64_t lut_off = align_up(ent_off + 8 * t->total_nsym, 16);
-  const int64_t dense_off = lut_off + 8ll * kLutSize * M;
-  const int64_t end = dense_off + (int64_t)kSubBytes * t->total_dense;
-  if (end != t->bytes)
+  const BlobLayout L = blob_layout(t->M, t->total_nsym, t->total_dense);
+  if (L.end != t->bytes)
     return fail(GAANS_EINVAL, "tables descriptor does not describe a prepared blob (%lld bytes "
-                "for its counts, %lld given)", (long long)end, (long long)t->bytes);
+                "for its counts, %lld given)", (long long)L.end, (long long)t->bytes);
   r->meta_off = (uint32_t)sizeof(TabHdr);
-  r->ent_off = (uint32_t)ent_off;
-  r->lut_off = (uint32_t)lut_off;
-  r->dense_off = (uint32_t)dense_off;
+  r->ent_off = (uint32_t)L.ent_off;
+  r->lut_off = (uint32_t)L.lut_off;
+  r->dense_off = (uint32_t)L.dense_off;
   r->total_dense = (uint32_t)t->total_dense;
+  r->clut_off = (uint32_t)L.clut_off;
+  r->starts_off = (uint32_t)L.starts_off;
   return GAANS_OK;
 }
 
@@ -2173,35 +2311,58 @@ EncPlan plan_encode(const gaans_tables* t, int64_t P, int64_t BK, const DevLds& 
 }
 
 // Decoder: lookups and metadata per table; sub-blocks when they are staged
-// too.  For each workgroups-per-CU count (at most 3:
-// the kernel is built for 6 waves per SIMD, and a 6-wave workgroup puts two
-// waves on two of the CU's four SIMDs), the options in order of preference:
-// 8-step blocks with sub-blocks, 4-step blocks with sub-blocks (their
-// records, stream ring and escape FIFO take half the LDS), then the same
-// without sub-blocks (a dense-bucket lookup then reads global memory).
+// too.  For each workgroups-per-CU count (at most 3: the kernel is built for
+// 6 waves per SIMD, and a 6-wave workgroup puts two waves on two of the CU's
+// four SIMDs), the options in order of preference: 8-step blocks with
+// sub-blocks, 4-step blocks with sub-blocks (their records, stream ring and
+// escape FIFO take half the LDS); then, when the blob has them and every
+// position may use any table (explicit or computed indexes), the search
+// lookups of all tables; then the lookups without sub-blocks (a dense-bucket
+// lookup then reads global memory).
 struct DecPlan {
   Stage st;
   int sb;
   size_t lds;
+  bool search;            // the search lookups of every table
+  uint32_t starts_words;  // search: 16-byte words of starts
 };
 
+// Search lookups in LDS: every table's bucket entries and metadata, and
+// every symbol's start (with the zero padding).
+int64_t search_lds(const gaans_tables* t, uint32_t* starts_words) {
+  const int64_t sb = align_up(2 * (t->total_nsym + kStartsPad), 16);
+  *starts_words = (uint32_t)(sb / 16);
+  return (int64_t)t->M * (4 * kLutSize + 16) + sb;
+}
+
 DecPlan plan_decode(const gaans_tables* t, int64_t P, int64_t BK, bool latents,
-                    const DevLds& d, int64_t extra = 0, bool range_ok = true) {
+                    const DevLds& d, int64_t extra = 0, bool range_ok = true,
+                    bool search_ok = false) {
   const int64_t per_table = 8 * kLutSize + 16;
   const bool has_dense = t->total_dense > 0;
+  uint32_t starts_words = 0;
+  const int64_t search_bytes = search_ok ? search_lds(t, &starts_words) : 0;
   for (int64_t occ = occ_target(BK, d, 3); occ >= 1; --occ) {
     const int64_t cap = lds_budget(d, occ);
-    for (int opt = 0; opt < 4; ++opt) {
-      const bool dense = opt < 2;
+    for (int opt = 0; opt < 6; ++opt) {
       const int sb = (opt & 1) ? 4 : 8;
-      if (!dense && !has_dense) break;  // same as the options already tried
-      Stage s;
       const int64_t fixed = dec_fixed_lds(latents, sb);
+      if (opt >= 2 && !has_dense) break;  // same as the options already tried
+      if (opt == 2 || opt == 3) {
+        if (search_ok && fixed + search_bytes + extra <= cap)
+          return DecPlan{Stage{(int32_t)t->M, 0, 0, 1}, sb, (size_t)(fixed + search_bytes), true,
+                         starts_words};
+        continue;
+      }
+      const bool dense = opt < 2;
+      Stage s;
       if (fit_stage(t, P, per_table, 0, dense ? kSubBytes : 0, cap - fixed - extra, &s, range_ok))
-        return DecPlan{s, sb, (size_t)(fixed + per_table * s.nt_cap + kSubBytes * (int64_t)s.nd_cap)};
+        return DecPlan{s, sb,
+                       (size_t)(fixed + per_table * s.nt_cap + kSubBytes * (int64_t)s.nd_cap),
+                       false, 0};
     }
   }
-  return DecPlan{Stage{0, 0, 0, 0}, 8, (size_t)dec_fixed_lds(latents, 8)};
+  return DecPlan{Stage{0, 0, 0, 0}, 8, (size_t)dec_fixed_lds(latents, 8), false, 0};
 }
 
 // Allow dynamic LDS above the default limit (once per kernel and device).
@@ -2362,7 +2523,10 @@ int decode_impl(int mode, void* stream, const uint8_t* payload, int64_t payload_
   if ((rc = device_lds(&dl))) return rc;
   const bool latents = mode != kModeSymbols;
   const int64_t extra = mode == kModeGaussian ? align_up(4 * (int64_t)g->n, 16) : 0;
-  const DecPlan plan = plan_decode(tables, P, L.BK, latents, dl, extra, mode != kModeGaussian);
+  const bool search_ok =
+      (tables->flags & GAANS_TABLES_SEARCH) != 0 && (mode == kModeGaussian || indexes != nullptr);
+  const DecPlan plan =
+      plan_decode(tables, P, L.BK, latents, dl, extra, mode != kModeGaussian, search_ok);
   const Stage& st = plan.st;
   DecArgs a;
   a.payload = payload;
@@ -2395,6 +2559,7 @@ int decode_impl(int mode, void* stream, const uint8_t* payload, int64_t payload_
   a.ne_cap = st.ne_cap;
   a.nd_cap = st.nd_cap;
   a.stage_all = st.stage_all;
+  a.starts_words = plan.starts_words;
   a.ctrl = static_cast<uint32_t*>(ctrl);
   a.status_out = status_out;
   const size_t lds = plan.lds + (size_t)extra;
@@ -2410,6 +2575,19 @@ int decode_impl(int mode, void* stream, const uint8_t* payload, int64_t payload_
     return check_launch("decode");
   };
   const bool imp = indexes == nullptr;
+  if (plan.search) {  // explicit or computed indexes only
+    switch (mode) {
+      case kModeGaussian:
+        return plan.sb == 4 ? launch(k_decode<kModeGaussian, false, 4, true>)
+                            : launch(k_decode<kModeGaussian, false, 8, true>);
+      case kModeLatents:
+        return plan.sb == 4 ? launch(k_decode<kModeLatents, false, 4, true>)
+                            : launch(k_decode<kModeLatents, false, 8, true>);
+      default:
+        return plan.sb == 4 ? launch(k_decode<kModeSymbols, false, 4, true>)
+                            : launch(k_decode<kModeSymbols, false, 8, true>);
+    }
+  }
   if (plan.sb == 4) {
     switch (mode) {
       case kModeGaussian: return launch(k_decode<kModeGaussian, false, 4>);
@@ -2437,12 +2615,25 @@ uint64_t fnv_u32(uint64_t h, uint32_t v) {
 }
 
 int64_t tables_size(int32_t M, int64_t total_syms, int64_t total_blocks) {
-  int64_t o = sizeof(TabHdr);
-  o += (int64_t)sizeof(TabMeta) * M;
-  o = align_up(align_up(o, 8) + 8 * total_syms, 16);
-  o += 8ll * kLutSize * M;
-  o += (int64_t)kSubBytes * total_blocks;
-  return o;
+  return blob_layout(M, total_syms, total_blocks).end;
+}
+
+// Search lookups of one table (symbols base .. base + nsym - 1 of the blob):
+// per 256-value bucket, the symbol that contains the bucket's first value
+// (blob-wide index) in the low half and the number of symbols that start
+// inside the bucket after it in the high half; starts[base + s] = cdf[s].
+void build_search(const int32_t* c, uint32_t nsym, uint32_t base, uint32_t* clut,
+                  uint16_t* starts) {
+  for (uint32_t v = 0; v < nsym; ++v) starts[base + v] = (uint16_t)c[v];
+  const uint32_t width = 1u << (16 - kLutBits);
+  uint32_t s = 0;
+  for (uint32_t b = 0; b < (uint32_t)kLutSize; ++b) {
+    const uint32_t lo = b * width;
+    while (s + 1 < nsym && (uint32_t)c[s + 1] <= lo) ++s;
+    uint32_t n = 0;
+    while (s + 1 + n < nsym && (uint32_t)c[s + 1 + n] < lo + width) ++n;
+    clut[b] = (base + s) | ((n < 0xffffu ? n : 0xffffu) << 16);
+  }
 }
 
 // Decode lookup entry of the cum range [lo, lo + width) of a CDF with nsym
@@ -2668,10 +2859,15 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
     total_dense += nd;
     if (nd > max_dense) max_dense = nd;
   }
-  const int64_t lut_off = align_up(ent_off + 8 * total, 16);
+  const BlobLayout BL = blob_layout(M, total, total_dense);
+  const int64_t lut_off = BL.lut_off;
   uint64_t* lut = reinterpret_cast<uint64_t*>(o + lut_off);
-  const int64_t dense_off = lut_off + 8ll * kLutSize * M;
+  const int64_t dense_off = BL.dense_off;
   uint64_t* blocks = reinterpret_cast<uint64_t*>(o + dense_off);
+  uint32_t* clut = reinterpret_cast<uint32_t*>(o + BL.clut_off);
+  uint16_t* starts = reinterpret_cast<uint16_t*>(o + BL.starts_off);
+  bool search = total <= kSearchMaxSyms;
+  for (int32_t t = 0; t < M; ++t) search &= offsets[t] >= INT32_MIN + 65536;
   uint32_t dblk = 0;
   uint64_t dg = 0xcbf29ce484222325ull;
   dg = fnv_u32(dg, (uint32_t)M);
@@ -2694,6 +2890,7 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
     }
     dblk += (uint32_t)build_lookup(c, S, lut + (int64_t)t * kLutSize,
                                    blocks + (size_t)dblk * kSubSize, dblk);
+    if (search) build_search(c, nsym, base, clut + (int64_t)t * kLutSize, starts);
     base += nsym;
   }
   h->magic = kTabMagic;
@@ -2709,17 +2906,19 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
   h->max_nsym = max_nsym;
   h->dense_off = (uint32_t)dense_off;
   h->total_dense = (uint32_t)total_dense;
+  h->clut_off = (uint32_t)BL.clut_off;
+  h->starts_off = (uint32_t)BL.starts_off;
   bool safe = true;
   for (int32_t t = 0; t < M; ++t) safe &= offsets[t] <= INT32_MAX - 65535;
-  h->flags = safe ? kTabOffsetsSafe : 0u;
+  h->flags = (safe ? kTabOffsetsSafe : 0u) | (search ? kTabSearch : 0u);
   desc->dev = nullptr;
   desc->bytes = need;
+  desc->flags = search ? GAANS_TABLES_SEARCH : 0;
   desc->M = M;
   desc->max_nsym = (int32_t)max_nsym;
   desc->total_nsym = total;
   desc->digest = dg;
   desc->max_dense = max_dense;
-  desc->reserved = 0;
   desc->total_dense = total_dense;
   return GAANS_OK;
 }

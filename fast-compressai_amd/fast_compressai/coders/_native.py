@@ -15,7 +15,7 @@ import threading
 from .errors import CoderDependencyError
 
 LIB_NAME = "libgaans_w64.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 CTRL_BYTES = 256
 
 # return codes
@@ -66,7 +66,7 @@ class Tables(ctypes.Structure):
     _fields_ = [("dev", ctypes.c_void_p), ("bytes", ctypes.c_int64), ("M", ctypes.c_int32),
                 ("max_nsym", ctypes.c_int32), ("total_nsym", ctypes.c_int64),
                 ("digest", ctypes.c_uint64), ("max_dense", ctypes.c_int32),
-                ("reserved", ctypes.c_int32), ("total_dense", ctypes.c_int64)]
+                ("flags", ctypes.c_int32), ("total_dense", ctypes.c_int64)]
 
 
 def library_path() -> str:

@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define GAANS_ABI_VERSION 6
+#define GAANS_ABI_VERSION 7
 #define GAANS_CTRL_BYTES 256
 
 /* return codes */
@@ -91,9 +91,15 @@ typedef struct gaans_tables {
   uint64_t digest;    /* table digest recorded in payload headers */
   int32_t max_dense;  /* most decode sub-blocks (128 B each: one per 256-value bucket, and
                          per 16-value sub-range, with >= 2 symbol starts) of one table */
-  int32_t reserved;
+  int32_t flags;      /* GAANS_TABLES_* */
   int64_t total_dense; /* decode sub-blocks over all tables */
 } gaans_tables;
+
+/* gaans_tables.flags: the blob holds compact search lookups (one u32 per
+ * 256-value bucket and a u16 start per symbol), which the decoder uses when
+ * the sub-blocks do not fit in LDS; set when there are at most 65,527
+ * symbols in all and every offset is at least INT32_MIN + 65536. */
+#define GAANS_TABLES_SEARCH 1
 
 int gaans_abi_version(void);
 const char* gaans_last_error(void);

@@ -140,6 +140,71 @@ def test_prepared_tables_dense_tail_lookup():
     assert levels.get(2, 0) > 0 and levels.get(3, 0) > 0
 
 
+def host_search(blob, t, cum, counts=None):
+    """The decoder's search lookup, read from the prepared blob: bucket entry
+    (blob-wide symbol g containing the bucket's first value | starts inside
+    the bucket n << 16); while more than three start inside, split the range
+    four ways with three start reads; then starts g .. g + 4 resolve the
+    rest; freq from the next start modulo 2^16 (the next table's first
+    start, or the zero sentinel, is 0)."""
+    hdr = struct.unpack_from("<16I", blob, 0)
+    clut_off, starts_off = hdr[14], hdr[15]
+    ent_base = struct.unpack_from("<I", blob, hdr[6] + 16 * t)[0]
+    e = struct.unpack_from("<I", blob, clut_off + 4 * (256 * t + (cum >> 8)))[0]
+    g, n = e & 0xFFFF, e >> 16
+    rounds = 0
+    while n > 3:  # 4-way: probes q, 2q, 3q
+        q = (n + 1) >> 2
+        le = [struct.unpack_from("<H", blob, starts_off + 2 * (g + j * q))[0] <= cum
+              for j in (1, 2, 3)]
+        g += sum(le) * q
+        n = n - 3 * q if le[2] else q - 1
+        rounds += 1
+    v = struct.unpack_from("<5H", blob, starts_off + 2 * g)
+    k = sum(1 for j in (1, 2, 3) if n >= j and v[j] <= cum)
+    if counts is not None:
+        counts[rounds] = counts.get(rounds, 0) + 1
+    st, nx = v[k], v[k + 1]
+    return g + k - ent_base, st, ((nx - st - 1) & 0xFFFF) + 1
+
+
+def test_search_lookups_exhaustive():
+    # the 64 GaussianConditional-style tables of the hyperprior workload
+    # (3 .. 3,133 symbols, long freq-1 tails) and a one-symbol table
+    yw, _, _, _ = synthetic.hyperprior_512x768()
+    cdfs = np.zeros((65, yw.cdfs.shape[1]), np.int32)
+    cdfs[:64] = yw.cdfs
+    cdfs[64, :2] = [0, 65536]
+    sizes = np.concatenate([yw.cdf_sizes, [2]]).astype(np.int32)
+    offs = np.concatenate([yw.offsets, [-7]]).astype(np.int32)
+    rc, blob, _ = prepare_host(cdfs, sizes, offs)
+    assert rc == 0
+    blob = blob.tobytes()
+    hdr = struct.unpack_from("<16I", blob, 0)
+    assert hdr[13] & 2  # search lookups present
+    counts = {}
+    for t in (0, 5, 20, 40, 55, 62, 63, 64):
+        c = cdfs[t, : sizes[t]]
+        want = np.searchsorted(c, np.arange(65536), side="right") - 1
+        step = 1 if t in (63, 64) else 5
+        for cum in range(0, 65536, step):
+            v, start, freq = host_search(blob, t, cum, counts)
+            assert v == want[cum] and start == c[v] and freq == c[v + 1] - c[v], (t, cum)
+    assert counts.get(0, 0) > 0 and counts.get(1, 0) > 0 and max(counts) >= 3
+
+
+def test_search_lookups_absent_when_not_addressable():
+    # more symbols than 16-bit starts indexes reach, or an offset near INT32_MIN
+    w = synthetic.batch_uniform(batch=1)
+    reps = 300  # 300 tables of 255 symbols: 76,500 > 65,527
+    cdfs = np.repeat(w.cdfs[:1], reps, 0)
+    sizes = np.repeat(w.cdf_sizes[:1], reps)
+    rc, blob, _ = prepare_host(cdfs, sizes, np.zeros(reps, np.int32))
+    assert rc == 0 and not struct.unpack_from("<16I", blob.tobytes(), 0)[13] & 2
+    rc, blob, _ = prepare_host(w.cdfs[:2], w.cdf_sizes[:2], [0, -2**31 + 5])
+    assert rc == 0 and not struct.unpack_from("<16I", blob.tobytes(), 0)[13] & 2
+
+
 @pytest.mark.parametrize("cdf,size", [([1, 65536], 2), ([0, 65535], 2), ([0, 100, 100, 65536], 4),
                                       ([0, 65536], 1), ([0, 65536], 3)])
 def test_invalid_tables_rejected(cdf, size):
