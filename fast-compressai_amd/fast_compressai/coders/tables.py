@@ -7,8 +7,11 @@ a compact blob built once per table set by ``gaans_tables_prepare``: per-table
 metadata, per-symbol entries (``start | (freq - 1) << 16`` and the
 encoder's division magic of ``freq``), a 256-bucket decode lookup and, for
 buckets in which several symbols start, second- and third-level lookups of
-16 entries (16-value sub-ranges, then single values).  The blob also carries the table digest that every payload
-records, so decoding with other tables is detected on the device.
+16 entries (16-value sub-ranges, then single values); and the compact
+search lookups (a u32 per bucket and a u16 start per symbol) that the
+decoder stages instead when many wide tables (GaussianConditional) leave no
+room for the sub-blocks.  The blob also carries the table digest that every
+payload records, so decoding with other tables is detected on the device.
 """
 
 from __future__ import annotations
