@@ -351,3 +351,43 @@ def test_bpp_against_compressai_equivalent_stream(backend, gpu_device):
     single = len(O.rans64_encode(w.symbols[0], w.explicit_indexes()[0], w.cdfs, w.cdf_sizes,
                                  w.offsets))
     assert payload.packed.numel() <= single * 1.01
+
+
+# ---- the decoder's search lookups (many wide tables, sub-blocks not in LDS) ----
+
+def wide_gaussian_rows(B, C, HW, p_ch, seed):
+    """Rows coded with the 64 GaussianConditional-style tables of the
+    hyperprior workload (3 .. 3,132 symbols), per-element indexes, draws that
+    reach deep into the tails and past the table ranges (escapes)."""
+    yw, _, _, _ = synthetic.hyperprior_512x768()
+    rng = np.random.default_rng(seed)
+    idx = rng.integers(0, 64, size=(B, C * HW), dtype=np.int32)
+    scale = np.exp(np.linspace(np.log(0.11), np.log(256.0), 64))[idx]
+    sym = np.rint(rng.standard_normal((B, C * HW)) * scale * 1.5).astype(np.int32)
+    sym[:, ::97] = rng.integers(-5000, 5000, size=sym[:, ::97].shape, dtype=np.int32)
+    return synthetic.Workload("wide Gaussian rows", sym, idx, yw.cdfs, yw.cdf_sizes, yw.offsets,
+                              C, p_ch, 0)
+
+
+@pytest.mark.parametrize("B,C,HW,p_ch", [(3, 24, 77, 5), (2, 64, 96, 16), (1, 8, 9, 3)])
+def test_search_lookup_decoder_bit_exact(backend, gpu_device, B, C, HW, p_ch):
+    w = wide_gaussian_rows(B, C, HW, p_ch, seed=B * 100 + C)
+    check_workload(backend, gpu_device, w, channels=C)
+
+
+def test_search_lookup_decoder_rejects_corruption(backend, gpu_device):
+    w = wide_gaussian_rows(2, 24, 77, 4, seed=9)
+    payload = check_workload(backend, gpu_device, w, channels=24)
+    idx = dev(w.explicit_indexes(), gpu_device)
+    cdfs, sizes, offs = tables_on(w, gpu_device)
+    for pos in (payload.header_bytes + 11, payload.packed.numel() // 2):
+        say("case: search decoder, corrupt byte", pos)
+        bad = payload.packed.clone()
+        bad[pos] ^= 0x5A
+        with pytest.raises(CoderInputError):
+            backend.decode(replace(payload, packed=bad), idx, cdfs, sizes, offs)
+    say("case: search decoder, other indexes")
+    idx2 = idx.clone()
+    idx2[1, 7] = (idx2[1, 7] + 1) % 64
+    with pytest.raises(CoderInputError):
+        backend.decode(payload, idx2, cdfs, sizes, offs)
