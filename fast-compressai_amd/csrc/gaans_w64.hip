@@ -63,7 +63,7 @@ constexpr uint32_t kMagic = 0x31574147u;  // "GAW1"
 constexpr uint32_t kVersion = 2u;
 constexpr uint32_t kParams = 0x00041040u;  // lanes 64 | precision 16 << 8 | bypass 4 << 16
 constexpr int kFixedWords = 16;
-constexpr uint32_t kTabMagic = 0x34425447u;  // "GTB4"
+constexpr uint32_t kTabMagic = 0x35425447u;  // "GTB5"
 constexpr int kLutBits = 8;
 constexpr int kLutSize = 1 << kLutBits;
 constexpr int kSubBits = 4;                 // a sub-block: 16 entries of 16 or 1 values
@@ -106,8 +106,8 @@ int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 // lookup, bucket j = [j << 8, (j << 8) + 255]), 16 (second level) or 1 (third
 // level).  With s the symbol containing the range's first value:
 //   at most one other symbol starts in the range:
-//     low word = start(s) | (freq(s) - 1) << 16,
-//     high word = s | (freq(s + 1) - 1) << 16   (cum >= start + freq -> s + 1)
+//     low word = start(s) | (start(s + 1) - 1) << 16   (cum > that -> s + 1),
+//     high word = s | (freq(s + 1) - 1) << 16
 //   two or more (a dense range, 256 or 16 values wide):
 //     low word = global index of a sub-block, high word = s | 0xffff << 16;
 //     the sub-block's 16 entries cover the range's 16 sub-ranges (of 16 values
@@ -1230,13 +1230,14 @@ __device__ __forceinline__ void dec_lookup(const Tabs& tb, uint32_t t, uint32_t 
     if (__builtin_expect(dm3 != 0ull, 0) && (act & dense_entry(e)))
       e = sub_entry<kLds>(tb, e, cum & (kSubSize - 1));
   }
+  // the compare reads the entry directly; the rest runs beside it
   const uint32_t lo = (uint32_t)e, hi = (uint32_t)(e >> 32);
   const uint32_t s0 = hi & 0xffffu, nxt = hi >> 16;
-  const uint32_t st0 = lo & 0xffffu, fr0 = (lo >> 16) + 1u;
-  const bool up = cum >= st0 + fr0;
+  const uint32_t st0 = lo & 0xffffu, st1 = (lo >> 16) + 1u;
+  const bool up = cum >= st1;
   s = up ? s0 + 1u : s0;
-  st = up ? st0 + fr0 : st0;
-  fr = up ? nxt + 1u : fr0;
+  st = up ? st1 : st0;
+  fr = up ? nxt + 1u : st1 - st0;
 }
 
 // cum -> (symbol, start, freq) with the search lookups, all tables in LDS:
@@ -2646,7 +2647,7 @@ bool lookup_entry(const int32_t* c, uint32_t nsym, uint32_t lo, uint32_t width, 
   while (e + 1 < nsym && (uint32_t)c[e + 1] <= lo + width - 1) ++e;
   if (e - s >= 2) return false;
   const uint32_t next = s + 1 < nsym ? (uint32_t)(c[s + 2] - c[s + 1] - 1) : 0u;
-  const uint32_t lo_word = (uint32_t)c[s] | ((uint32_t)(c[s + 1] - c[s] - 1) << 16);
+  const uint32_t lo_word = (uint32_t)c[s] | ((uint32_t)(c[s + 1] - 1) << 16);
   *out = (uint64_t)lo_word | ((uint64_t)(s | (next << 16)) << 32);
   return true;
 }

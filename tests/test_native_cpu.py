@@ -88,10 +88,10 @@ def host_lookup(blob, t, cum, levels=None):
         levels[depth] = levels.get(depth, 0) + 1
     lo, hi = e & 0xFFFFFFFF, e >> 32
     s0, nxt = hi & 0xFFFF, hi >> 16
-    st, fr = lo & 0xFFFF, (lo >> 16) + 1
-    if cum >= st + fr:
-        return s0 + 1, st + fr, nxt + 1
-    return s0, st, fr
+    st0, st1 = lo & 0xFFFF, (lo >> 16) + 1  # start(s0), start(s0 + 1)
+    if cum >= st1:
+        return s0 + 1, st1, nxt + 1
+    return s0, st0, st1 - st0
 
 
 def test_prepared_tables_digest_and_lookup_exhaustive():
