@@ -458,7 +458,7 @@ def main():
     # algorithmic bytes per launch: symbols + indexes (int32) + payload
     alg_bytes = 4 * B * N + 4 * B * N + payload_bytes
     if dec_avg >= enc_avg:
-        kernel, key, dur = "k_decode<0,false,8,false> (gaans_decode_symbols)", "k_decode", dec_avg
+        kernel, key, dur = "k_decode<0,false,16,false> (gaans_decode_symbols)", "k_decode", dec_avg
     else:
         kernel, key, dur = "k_encode<0,false,8> (gaans_encode_symbols)", "k_encode", enc_avg
     achieved = alg_bytes / dur / 1e9

@@ -75,8 +75,7 @@ constexpr int kMaxEscNibbles = 9;  // escape count + 8 nibbles of raw
 // per-wave hash, status and escape nibbles, then the escape count
 constexpr int kPartBytes = (12 * kWaves + 4 + 15) / 16 * 16;
 constexpr int kRingWords = 4096;       // encoder LDS output ring (u16 words)
-constexpr int kPfU32 = 4;              // decoder stream prefetch: u32 per lane
-constexpr int kPfWords = 2 * kPfU32 * kLanes;
+constexpr int kPfU32Max = 8;  // decoder stream prefetch: u32 per lane (16-step blocks)
 constexpr int kMaxDevices = 64;
 // control block (u32 words); encoder and decoder fields on separate 64-byte lines
 constexpr int kCtrlEncDone = 0;
@@ -1109,6 +1108,8 @@ struct DecArgs {
 template <int SB>
 struct DecGeom {
   static constexpr int kPer = (SB + kMappers - 1) / kMappers;  // steps per mapper wave and block
+  static constexpr int kPfU32 = SB >= 16 ? 8 : 4;               // prefetch: u32 per lane
+  static constexpr int kPfWords = 2 * kPfU32 * kLanes;         // words per prefetch batch
   static constexpr int kRing = SB >= 8 ? 2048 : 1024;          // stream ring (u16 words)
   static constexpr int kLowWater = SB >= 8 ? 1024 : 512;
   static constexpr int kPre = kLowWater / kPfWords;            // batches staged before block 0
@@ -1124,13 +1125,18 @@ struct DecGeom {
     return kRingBytes + kRecBytes + kEscBytes + (latents ? kMedBytes : 0) + kEscInfoBytes +
            kDecPartBytes + kDecCtlBytes;
   }
-  static_assert(kLowWater >= SB * kLanes && kLowWater + kPfWords <= kRing && kPre >= 1,
+  // a block start with fewer than kLowWater words buffered commits a batch:
+  // a batch covers one block's words (at most one per lane and step), so
+  // every block starts with at least SB * kLanes words buffered
+  static_assert(kLowWater >= SB * kLanes && kPfWords >= SB * kLanes &&
+                    kLowWater + kPfWords <= kRing && kPre >= 1 && kPfU32 <= kPfU32Max,
                 "decoder stream ring too small");
   static_assert((kDecPartBytes + kDecCtlBytes) % 16 == 0, "LDS parts 16-byte aligned");
 };
 
 int dec_fixed_lds(bool latents, int sb) {
-  return sb >= 8 ? DecGeom<8>::fixed(latents) : DecGeom<4>::fixed(latents);
+  return sb >= 16 ? DecGeom<16>::fixed(latents)
+                  : (sb >= 8 ? DecGeom<8>::fixed(latents) : DecGeom<4>::fixed(latents));
 }
 
 // Mapper record of one lane and step (8 bytes), tables in LDS when the step's
@@ -1312,7 +1318,7 @@ struct Stream {
   const uint32_t* __restrict__ s32;
   const uint32_t* __restrict__ safe;  // an in-bounds word of the chunk
   int q, q32, rp, filled;
-  uint32_t pf[kPfU32];
+  uint32_t pf[kPfU32Max];  // the first DecGeom<SB>::kPfU32 in use
 };
 
 // Words past the stream end read the chunk's first state word instead (always
@@ -1329,11 +1335,11 @@ __device__ __forceinline__ void stream_block_start(Stream& S, uint32_t* ring32, 
   const bool commit = S.filled - S.rp < G::kLowWater && S.filled < S.q;
   if (commit) {
 #pragma unroll
-    for (int kk = 0; kk < kPfU32; ++kk)
+    for (int kk = 0; kk < G::kPfU32; ++kk)
       ring32[((S.filled >> 1) + kk * kLanes + lane) & (G::kRing / 2 - 1)] = S.pf[kk];
-    S.filled = uni(S.filled + kPfWords);
+    S.filled = uni(S.filled + G::kPfWords);
 #pragma unroll
-    for (int kk = 0; kk < kPfU32; ++kk)
+    for (int kk = 0; kk < G::kPfU32; ++kk)
       S.pf[kk] = stream_word32(S, (S.filled >> 1) + kk * kLanes + lane);
   }
 }
@@ -1670,7 +1676,7 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
     // reader's window.
     EscReader E;
     uint32_t x = kStateLow;
-    uint32_t w0[G::kPre][kPfU32];
+    uint32_t w0[G::kPre][G::kPfU32];
     if (wid == 0) {
       S.s32 = s32;
       S.safe = safe;
@@ -1681,11 +1687,11 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
 #pragma unroll
       for (int b = 0; b < G::kPre; ++b)
 #pragma unroll
-        for (int kk = 0; kk < kPfU32; ++kk)
-          w0[b][kk] = stream_word32(S, b * (kPfWords / 2) + kk * kLanes + lane);
+        for (int kk = 0; kk < G::kPfU32; ++kk)
+          w0[b][kk] = stream_word32(S, b * (G::kPfWords / 2) + kk * kLanes + lane);
 #pragma unroll
-      for (int kk = 0; kk < kPfU32; ++kk)
-        S.pf[kk] = stream_word32(S, G::kPre * (kPfWords / 2) + kk * kLanes + lane);
+      for (int kk = 0; kk < G::kPfU32; ++kk)
+        S.pf[kk] = stream_word32(S, G::kPre * (G::kPfWords / 2) + kk * kLanes + lane);
     } else if (wid == kEscWave) {
       E.w32 = s32;
       E.safe = safe;
@@ -1723,9 +1729,9 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
 #pragma unroll
       for (int b = 0; b < G::kPre; ++b)
 #pragma unroll
-        for (int kk = 0; kk < kPfU32; ++kk)
-          sring32[(b * (kPfWords / 2) + kk * kLanes + lane) & (G::kRing / 2 - 1)] = w0[b][kk];
-      S.filled = G::kPre * kPfWords;
+        for (int kk = 0; kk < G::kPfU32; ++kk)
+          sring32[(b * (G::kPfWords / 2) + kk * kLanes + lane) & (G::kRing / 2 - 1)] = w0[b][kk];
+      S.filled = G::kPre * G::kPfWords;
       uint32_t ecur = 0;  // escape entries consumed
       __syncthreads();
       for (int j = 0; j < nblk; ++j) {
@@ -2345,17 +2351,17 @@ DecPlan plan_decode(const gaans_tables* t, int64_t P, int64_t BK, bool latents,
   const int64_t search_bytes = search_ok ? search_lds(t, &starts_words) : 0;
   for (int64_t occ = occ_target(BK, d, 3); occ >= 1; --occ) {
     const int64_t cap = lds_budget(d, occ);
-    for (int opt = 0; opt < 6; ++opt) {
-      const int sb = (opt & 1) ? 4 : 8;
+    for (int opt = 0; opt < 9; ++opt) {
+      const int sb = 16 >> (opt % 3);  // 16-, 8-, then 4-step blocks of each kind
       const int64_t fixed = dec_fixed_lds(latents, sb);
-      if (opt >= 2 && !has_dense) break;  // same as the options already tried
-      if (opt == 2 || opt == 3) {
+      if (opt >= 3 && !has_dense) break;  // same as the options already tried
+      if (opt >= 3 && opt < 6) {
         if (search_ok && fixed + search_bytes + extra <= cap)
           return DecPlan{Stage{(int32_t)t->M, 0, 0, 1}, sb, (size_t)(fixed + search_bytes), true,
                          starts_words};
         continue;
       }
-      const bool dense = opt < 2;
+      const bool dense = opt < 3;
       Stage s;
       if (fit_stage(t, P, per_table, 0, dense ? kSubBytes : 0, cap - fixed - extra, &s, range_ok))
         return DecPlan{s, sb,
@@ -2579,14 +2585,28 @@ int decode_impl(int mode, void* stream, const uint8_t* payload, int64_t payload_
   if (plan.search) {  // explicit or computed indexes only
     switch (mode) {
       case kModeGaussian:
-        return plan.sb == 4 ? launch(k_decode<kModeGaussian, false, 4, true>)
-                            : launch(k_decode<kModeGaussian, false, 8, true>);
+        return plan.sb == 4    ? launch(k_decode<kModeGaussian, false, 4, true>)
+               : plan.sb == 8 ? launch(k_decode<kModeGaussian, false, 8, true>)
+                              : launch(k_decode<kModeGaussian, false, 16, true>);
       case kModeLatents:
-        return plan.sb == 4 ? launch(k_decode<kModeLatents, false, 4, true>)
-                            : launch(k_decode<kModeLatents, false, 8, true>);
+        return plan.sb == 4    ? launch(k_decode<kModeLatents, false, 4, true>)
+               : plan.sb == 8 ? launch(k_decode<kModeLatents, false, 8, true>)
+                              : launch(k_decode<kModeLatents, false, 16, true>);
       default:
-        return plan.sb == 4 ? launch(k_decode<kModeSymbols, false, 4, true>)
-                            : launch(k_decode<kModeSymbols, false, 8, true>);
+        return plan.sb == 4    ? launch(k_decode<kModeSymbols, false, 4, true>)
+               : plan.sb == 8 ? launch(k_decode<kModeSymbols, false, 8, true>)
+                              : launch(k_decode<kModeSymbols, false, 16, true>);
+    }
+  }
+  if (plan.sb == 16) {
+    switch (mode) {
+      case kModeGaussian: return launch(k_decode<kModeGaussian, false, 16>);
+      case kModeLatents:
+        return imp ? launch(k_decode<kModeLatents, true, 16>)
+                   : launch(k_decode<kModeLatents, false, 16>);
+      default:
+        return imp ? launch(k_decode<kModeSymbols, true, 16>)
+                   : launch(k_decode<kModeSymbols, false, 16>);
     }
   }
   if (plan.sb == 4) {
