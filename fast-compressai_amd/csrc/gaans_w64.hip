@@ -2814,6 +2814,50 @@ int rans64_decode_impl(void* stream, const uint8_t* streams, int64_t streams_byt
   return indexes ? launch(k_rans64_decode<false>) : launch(k_rans64_decode<true>);
 }
 
+// Clear n u32 words (the no-allocation entry point's control block, once per
+// device before its first use; a kernel rather than a memset so that the call
+// can be captured into a graph).
+__global__ __launch_bounds__(kLanes) void k_clear_words(uint32_t* __restrict__ p, int n) {
+  for (int i = threadIdx.x; i < n; i += kLanes) p[i] = 0u;
+}
+
+}  // namespace
+
+// Device scratch of the no-allocation encode entry point
+// (gaans_encode_symbols_noalloc): the control block (GAANS_CTRL_BYTES) then
+// the encode workspace.  One copy per GPU, held until the process ends; every
+// call on a GPU shares it.  Host code never uses this name as an address: the
+// device address comes from hipGetSymbolAddress (noalloc_scratch below).
+static __device__ __align__(256) uint8_t scratch[GAANS_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+// Address of `scratch` on the current device, looked up once per device
+// (with that device current) and its control block cleared on `stream`
+// before the first call that uses it; the encode kernels leave the control
+// block zeroed again after every launch.
+int noalloc_scratch(hipStream_t stream, uint8_t** out) {
+  static std::mutex mu;
+  static uint8_t* addr[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(GAANS_EHIP, "hipGetDevice failed");
+  std::lock_guard<std::mutex> g(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(GAANS_EHIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+    k_clear_words<<<1, kLanes, 0, stream>>>(static_cast<uint32_t*>(p), GAANS_CTRL_BYTES / 4);
+    const int rc = check_launch("scratch clear");
+    if (rc) return rc;
+    addr[dev] = static_cast<uint8_t*>(p);
+  }
+  *out = addr[dev];
+  return GAANS_OK;
+}
+
 }  // namespace
 
 // =============================================================================
@@ -3030,6 +3074,34 @@ int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace
   a.M = (uint32_t)tables->M;
   k_pack<<<dim3((uint32_t)L.BK), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(a);
   return check_launch("pack");
+}
+
+int gaans_encode_symbols_noalloc(void* stream, const int32_t* symbols_dev,
+                                 const int32_t* indexes_dev, const gaans_tables* tables,
+                                 int64_t B, int64_t N, int64_t C, int64_t P, uint8_t* out_dev,
+                                 int64_t out_bytes, uint64_t* info_out) {
+  Layout L;
+  int rc = make_layout(B, N, C, P, &L);
+  if (rc) return rc;
+  // the size limit first: it needs no device
+  const int64_t need = (int64_t)GAANS_CTRL_BYTES + L.ws_bytes;
+  if (need > (int64_t)GAANS_NOALLOC_SCRATCH_BYTES)
+    return fail(GAANS_EINVAL,
+                "B=%lld x N=%lld at P=%lld needs %lld bytes of device scratch; the "
+                "no-allocation encode holds %lld (use gaans_encode_symbols with a workspace)",
+                (long long)B, (long long)N, (long long)P, (long long)need,
+                (long long)GAANS_NOALLOC_SCRATCH_BYTES);
+  if (!info_out) return fail(GAANS_EINVAL, "info_out pointer is NULL");
+  if (!out_dev || out_bytes < L.header_bytes)
+    return fail(GAANS_EINVAL, "output buffer smaller than the payload header");
+  uint8_t* base = nullptr;
+  if ((rc = noalloc_scratch(static_cast<hipStream_t>(stream), &base))) return rc;
+  void* ctrl = base;
+  void* ws = base + GAANS_CTRL_BYTES;
+  rc = encode_stage1(kModeSymbols, stream, symbols_dev, nullptr, nullptr, indexes_dev, nullptr,
+                     tables, B, N, C, P, ws, L.ws_bytes, ctrl, info_out);
+  if (rc) return rc;
+  return gaans_encode_pack(stream, ws, L.ws_bytes, tables, B, N, C, P, out_dev, out_bytes);
 }
 
 int gaans_decode_symbols(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,

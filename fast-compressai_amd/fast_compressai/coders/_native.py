@@ -17,6 +17,7 @@ from .errors import CoderDependencyError
 LIB_NAME = "libgaans_w64.so"
 ABI_VERSION = 7
 CTRL_BYTES = 256
+NOALLOC_SCRATCH_BYTES = 16 * 1024 * 1024  # GAANS_NOALLOC_SCRATCH_BYTES
 
 # return codes
 OK, EINVAL, ETABLE, EHIP = 0, 1, 2, 3
@@ -94,6 +95,8 @@ def _declare(L) -> None:
         "gaans_encode_latents": ([p, p, p, p, T, i64, i64, i64, i64, p, i64, p, p],
                                  ctypes.c_int),
         "gaans_encode_pack": ([p, p, i64, T, i64, i64, i64, i64, p, i64], ctypes.c_int),
+        "gaans_encode_symbols_noalloc": ([p, p, p, T, i64, i64, i64, i64, p, i64, p],
+                                         ctypes.c_int),
         "gaans_decode_symbols": ([p, p, i64, p, T, i64, i64, i64, i64, p, p, p], ctypes.c_int),
         "gaans_decode_latents": ([p, p, i64, p, T, p, i64, i64, i64, i64, p, p, p],
                                  ctypes.c_int),

@@ -186,6 +186,28 @@ int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace
                       const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
                       int64_t P, uint8_t* out_dev, int64_t out_bytes);
 
+/* Stage 1 and stage 2 of gaans_encode_symbols in one call that allocates
+ * nothing and takes no workspace or control block: both live in a static
+ * device array of GAANS_NOALLOC_SCRATCH_BYTES per GPU (its control block
+ * first, GAANS_CTRL_BYTES, then the workspace), held until the process ends.
+ * The caller passes the inputs, the payload buffer (out_dev, out_bytes; as in
+ * gaans_encode_pack, best sized to layout->max_payload_bytes) and info_out
+ * (3 u64 in device or pinned host memory, as in gaans_encode_symbols; the
+ * completion word info_out[2] carries size and status).  The first call on a
+ * GPU looks the array up and clears its control block on `stream`; the
+ * kernels leave it zeroed after every launch.  Shapes whose control block and
+ * workspace exceed the array return GAANS_EINVAL before any device work.
+ * Every call on one GPU shares the array: calls that overlap on one GPU (other
+ * streams, other threads) race and must be ordered by the caller.
+ * No counterpart in the reference: this entry point is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Calls no hipMalloc / hipFree. */
+#define GAANS_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+int gaans_encode_symbols_noalloc(void* stream, const int32_t* symbols_dev,
+                                 const int32_t* indexes_dev, const gaans_tables* tables,
+                                 int64_t B, int64_t N, int64_t C, int64_t P, uint8_t* out_dev,
+                                 int64_t out_bytes, uint64_t* info_out);
+
 /* ---- decode ------------------------------------------------------------- */
 
 /* Decode a payload into int32 symbols [B, N].  The last block writes the
