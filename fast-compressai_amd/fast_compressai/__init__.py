@@ -7,7 +7,6 @@ catalog, running hand-written HIP kernels for gfx950.
 
 from .api import AccelerationReport, FastModel, accelerate, compile
 from .coders import (
-    Bitstream,
     BitstreamError,
     CoderCapability,
     CoderDependencyError,
@@ -29,7 +28,6 @@ from .pipeline import CodingPipeline
 __all__ = [
     "AccelerationConfig",
     "AccelerationReport",
-    "Bitstream",
     "BitstreamError",
     "CoderCapability",
     "CoderDependencyError",

@@ -1,7 +1,6 @@
 """GA-ANS (MI355X) and CompressAI RANS entropy coder backends."""
 
 from .capabilities import CoderCapability, coder_catalog, create_coder, warp_div_capability
-from .compressai_ans import Bitstream, CompressAIANSBackend
 from .errors import (
     BitstreamError,
     CoderDependencyError,
@@ -9,10 +8,10 @@ from .errors import (
     CoderInputError,
     CoderStateError,
 )
+from .rans_host import CompressAIANSBackend
 from .warp_div import WarpDivBackend, WarpDivPayload
 
 __all__ = [
-    "Bitstream",
     "BitstreamError",
     "CoderCapability",
     "CoderDependencyError",

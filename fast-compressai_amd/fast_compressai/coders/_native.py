@@ -148,10 +148,16 @@ def last_error() -> str:
 
 
 def check(rc: int, what: str) -> None:
+    """Raise for a nonzero return code: bad arguments or tables
+    (GAANS_EINVAL, GAANS_ETABLE) are the caller's inputs (CoderInputError, a
+    ValueError); a HIP runtime failure (GAANS_EHIP: a failed launch or
+    attribute call, or a stream that reported an error) is not, and raises
+    CoderError (a RuntimeError)."""
     if rc != OK:
-        from .errors import CoderInputError
+        from .errors import CoderError, CoderInputError
 
-        raise CoderInputError(f"{what} failed: {last_error()} (code {rc})")
+        cls = CoderInputError if rc in (EINVAL, ETABLE) else CoderError
+        raise cls(f"{what} failed: {last_error()} (code {rc})")
 
 
 _layouts: dict = {}

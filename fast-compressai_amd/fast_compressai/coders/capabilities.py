@@ -1,8 +1,10 @@
-"""Coder capability discovery without loading the native library.
+"""Which coders this build offers and whether the GPU one can run here.
 
-Mirrors ``src/fast_compressai/coders/capabilities.py:11-49`` of the reference:
-``warp_div_capability`` reports whether the GA-ANS GPU coder can run, and
-``coder_catalog`` / ``create_coder`` list and build the two coders.
+Same names as the reference's ``src/fast_compressai/coders/capabilities.py:11-49``
+(``warp_div_capability``, ``coder_catalog``, ``create_coder`` and the
+``CoderCapability`` record), answered for this build: the GA-ANS coder needs
+a visible GPU and the built HIP library, which is only looked for on disk
+here, not loaded.
 """
 
 from __future__ import annotations
@@ -43,14 +45,16 @@ def warp_div_capability(device: torch.device | str | None = None) -> CoderCapabi
 
 
 def coder_catalog() -> tuple[str, ...]:
-    """Return exactly the supported entropy coder backend identifiers."""
+    """Names ``create_coder`` accepts: CompressAI's CPU RANS and the GA-ANS
+    GPU coder."""
     return ("compressai-rans", "warp_div")
 
 
 def create_coder(name: str):
-    """Construct one supported backend without loading unrelated backends."""
+    """An instance of the coder called ``name``; only that coder's module
+    (and its dependency: CompressAI, or the HIP library) is loaded."""
     if name == "compressai-rans":
-        from .compressai_ans import CompressAIANSBackend
+        from .rans_host import CompressAIANSBackend
 
         return CompressAIANSBackend()
     if name == "warp_div":

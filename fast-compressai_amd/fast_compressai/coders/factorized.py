@@ -138,19 +138,20 @@ class FactorizedWarpDivCodec:
 
     def _decode_compressai(self, streams, shape) -> torch.Tensor:
         """EntropyBottleneck.decompress of CompressAI bitstreams: table =
-        channel, ``y_hat = float(symbol) + median``."""
+        channel, ``y_hat = float(symbol) + median``; small batches go to
+        CompressAI's host decoder when it is importable (see
+        ``gaans.decode_compressai_strings``)."""
         if (not isinstance(shape, (tuple, list, torch.Size)) or len(shape) != 2
                 or any(type(d) is not int or d <= 0 for d in shape)):
             raise CoderInputError("decompress expects a positive (height, width) shape")
         entropy = self.model.entropy_bottleneck
         C = entropy.channels
-        cdfs, _, _ = self._tables(entropy)
-        device = cdfs.device
+        raw = self._tables(entropy)
+        device = raw[0].device
         tables = self._prepared(entropy, device)
         B, N = len(streams), C * shape[0] * shape[1]
         with torch.no_grad():
-            buf, offs = gaans.pack_streams(streams, device)
-            symbols = gaans.decode_rans64(buf, offs, tables, B, N, C, device)
+            symbols = gaans.decode_compressai_strings(streams, tables, raw, B, N, C, device)
             medians = entropy._extend_ndims(entropy._get_medians().detach(), 2)
             return symbols.reshape(B, C, *shape).type_as(medians) + medians
 

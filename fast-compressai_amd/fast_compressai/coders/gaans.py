@@ -316,6 +316,28 @@ def decode_rans64(streams: torch.Tensor, offsets: torch.Tensor, tables: Prepared
     return out
 
 
+def decode_compressai_strings(strings, prepared: PreparedTables, raw_tables, B: int, N: int,
+                              C: int, device, *,
+                              indexes: torch.Tensor | None = None) -> torch.Tensor:
+    """int32 symbols [B, N] on ``device`` of B CompressAI Rans64 strings (one
+    per image), decoded where ``rans_host.rans64_route`` says is faster:
+    CompressAI's host decoder for small batches when CompressAI is
+    importable, else the GPU Rans64 decoder.  ``raw_tables`` are the
+    CompressAI tables (cdfs, lengths, offsets) for the host decoder;
+    ``indexes`` None means table = channel."""
+    from .rans_host import CompressAIANSBackend, rans64_route
+
+    if rans64_route(len(strings)) == "host":
+        if indexes is None:
+            idx = torch.arange(C, dtype=torch.int32).repeat_interleave(N // C).expand(B, N)
+        else:
+            idx = indexes.reshape(B, N)
+        out = CompressAIANSBackend().decode_rows(strings, idx, *raw_tables)
+        return torch.from_numpy(out).to(device)
+    buf, offs = pack_streams(strings, device)
+    return decode_rans64(buf, offs, prepared, B, N, C, device, indexes=indexes)
+
+
 def pack_streams(strings, device) -> tuple[torch.Tensor, torch.Tensor]:
     """CompressAI per-image byte strings -> (uint8 device buffer, int64
     offsets [B + 1]), each stream starting on a 4-byte boundary."""

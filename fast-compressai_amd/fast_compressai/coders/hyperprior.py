@@ -244,16 +244,17 @@ class HyperpriorWarpDivCodec:
         B, Cz = len(z_strings), eb.channels
         with torch.no_grad():
             ztab = self._prepared(eb, "entropy bottleneck", device)
-            buf, offs = gaans.pack_streams(z_strings, device)
-            zs = gaans.decode_rans64(buf, offs, ztab, B, Cz * shape[0] * shape[1], Cz, device)
+            zs = gaans.decode_compressai_strings(z_strings, ztab, _tables(eb, "entropy bottleneck"),
+                                                 B, Cz * shape[0] * shape[1], Cz, device)
             med = eb._extend_ndims(eb._get_medians().detach(), 2)
             z_hat = zs.reshape(B, Cz, *shape).type_as(med) + med
             scales, means = self._params(z_hat)
             C, N = int(scales.size(1)), int(scales[0].numel())
             ytab = self._prepared(gc, "gaussian conditional", device)
             idx = self._build_indexes(scales).reshape(B, N).contiguous()
-            buf, offs = gaans.pack_streams(y_strings, device)
-            ys = gaans.decode_rans64(buf, offs, ytab, B, N, C, device, indexes=idx)
+            ys = gaans.decode_compressai_strings(y_strings, ytab,
+                                                 _tables(gc, "gaussian conditional"), B, N, C,
+                                                 device, indexes=idx)
             y_hat = ys.reshape(scales.shape).to(torch.float32)
             return y_hat + means if means is not None else y_hat
 

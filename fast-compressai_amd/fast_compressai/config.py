@@ -1,25 +1,51 @@
 """Public configuration of ``accelerate``.
 
-``AccelerationConfig`` keeps the reference's fields and validation
-(``src/fast_compressai/config.py:14-101``): ``P`` is stored as ``p_ch``
-(latent channels per independently coded GA-ANS chunk), ``coder`` is
-``"warp_div"`` (default) or ``"rans"``, and a mapping may spell ``P`` or
-``p_ch`` but not both.
+``AccelerationConfig`` has the reference's fields, defaults and accepted
+values (``src/fast_compressai/config.py:14-101``), so configurations written
+for it load here: ``p_ch`` (spelled ``P`` in a mapping; latent channels per
+independently coded GA-ANS chunk) is a positive int or None, ``coder`` is
+``"warp_div"`` (default) or ``"rans"``, ``budget`` a finite non-negative
+number, ``execution_mode`` ``"sequential"`` or ``"overlap"``, the paths and
+the device strings.  Validation is a table of per-field rules; a mapping is
+merged with the keyword overrides, and a key given twice (``P`` and
+``p_ch``, or a mapping key and the same keyword) is rejected.
 """
 
 from __future__ import annotations
 
 import math
-from dataclasses import asdict, dataclass
-from typing import Any, Mapping
+from dataclasses import asdict, dataclass, fields
+from typing import Any, Callable, Mapping
 
 
 class ConfigurationError(ValueError):
     """Raised when an acceleration configuration is invalid."""
 
 
-_FIELDS = {"p_ch", "budget", "coder", "device", "profile_path", "precision_config_path",
-           "execution_mode"}
+def _optional_str(value: Any) -> bool:
+    return value is None or isinstance(value, str)
+
+
+def _p_ch_ok(value: Any) -> bool:
+    return value is None or (type(value) is int and value > 0)
+
+
+def _budget_ok(value: Any) -> bool:
+    return (isinstance(value, (int, float)) and not isinstance(value, bool)
+            and math.isfinite(float(value)) and value >= 0)
+
+
+# field -> (rule, what the field must be)
+_RULES: dict[str, tuple[Callable[[Any], bool], str]] = {
+    "p_ch": (_p_ch_ok, "P (p_ch) must be a positive integer or None"),
+    "budget": (_budget_ok, "budget must be a finite, non-negative number"),
+    "coder": (lambda v: v in ("warp_div", "rans"), "coder must be 'warp_div' or 'rans'"),
+    "device": (_optional_str, "device must be a string or None"),
+    "profile_path": (_optional_str, "profile_path must be a string or None"),
+    "precision_config_path": (_optional_str, "precision_config_path must be a string or None"),
+    "execution_mode": (lambda v: v in ("sequential", "overlap"),
+                       "execution_mode must be 'sequential' or 'overlap'"),
+}
 
 
 @dataclass(frozen=True)
@@ -33,56 +59,55 @@ class AccelerationConfig:
     execution_mode: str = "sequential"
 
     def __post_init__(self) -> None:
-        if self.p_ch is not None and (type(self.p_ch) is not int or self.p_ch <= 0):
-            raise ConfigurationError("P (p_ch) must be a positive integer or None")
-        if self.coder not in {"warp_div", "rans"}:
-            raise ConfigurationError("coder must be 'warp_div' or 'rans'")
-        if isinstance(self.budget, bool) or not isinstance(self.budget, (int, float)):
-            raise ConfigurationError("budget must be a non-negative finite RD/quality value")
-        if self.budget < 0 or not math.isfinite(float(self.budget)):
-            raise ConfigurationError("budget must be a non-negative finite RD/quality value")
-        for name in ("device", "profile_path", "precision_config_path"):
-            value = getattr(self, name)
-            if value is not None and not isinstance(value, str):
-                raise ConfigurationError(f"{name} must be a string or None")
-        if self.execution_mode not in {"sequential", "overlap"}:
-            raise ConfigurationError("execution_mode must be 'sequential' or 'overlap'")
+        for name, (rule, message) in _RULES.items():
+            if not rule(getattr(self, name)):
+                raise ConfigurationError(message)
 
     @classmethod
     def from_value(cls, value: "AccelerationConfig | Mapping[str, Any] | None", *,
                    P: int | None = None, budget: float | None = None, device: str | None = None,
                    coder: str | None = None,
                    precision_config_path: str | None = None) -> "AccelerationConfig":
-        overrides = {"p_ch": P, "budget": budget, "device": device, "coder": coder,
-                     "precision_config_path": precision_config_path}
-        if value is None:
-            return cls(p_ch=P, budget=0.0 if budget is None else budget, device=device,
-                       coder="warp_div" if coder is None else coder,
-                       precision_config_path=precision_config_path)
+        """Build a config from None (defaults), an existing config (returned
+        as is; keyword overrides are not combined with it) or a mapping,
+        with the keyword arguments applied on top."""
+        given = {k: v for k, v in (("p_ch", P), ("budget", budget), ("device", device),
+                                   ("coder", coder),
+                                   ("precision_config_path", precision_config_path))
+                 if v is not None}
         if isinstance(value, cls):
-            if any(v is not None for v in overrides.values()):
-                raise ConfigurationError("do not combine config with P/budget/device/coder overrides")
-            return value
-        if isinstance(value, Mapping):
-            data = dict(value)
-            if "P" in data:
-                if "p_ch" in data:
-                    raise ConfigurationError("use only one of P and p_ch")
-                data["p_ch"] = data.pop("P")
-            for key, override in overrides.items():
-                if override is not None:
-                    if key in data:
-                        raise ConfigurationError(f"{key} specified both in config and as an argument")
-                    data[key] = override
-            unknown = set(data) - _FIELDS
-            if unknown:
+            if given:
                 raise ConfigurationError(
-                    f"unknown acceleration config field(s): {', '.join(sorted(map(str, unknown)))}")
-            try:
-                return cls(**data)
-            except TypeError as exc:
-                raise ConfigurationError(str(exc)) from exc
-        raise ConfigurationError("config must be None, AccelerationConfig, or a mapping")
+                    "an AccelerationConfig cannot be combined with P/budget/device/coder/"
+                    "precision_config_path arguments")
+            return value
+        if value is None:
+            base: dict[str, Any] = {}
+        elif isinstance(value, Mapping):
+            base = _canonical_keys(value)
+        else:
+            raise ConfigurationError("config must be None, an AccelerationConfig or a mapping")
+        twice = sorted(set(base) & set(given))
+        if twice:
+            raise ConfigurationError(
+                f"{', '.join(twice)} given both in the config mapping and as an argument")
+        merged = {**base, **given}
+        known = {f.name for f in fields(cls)}
+        extra = sorted(map(str, set(merged) - known))
+        if extra:
+            raise ConfigurationError(f"unknown acceleration config field(s): {', '.join(extra)}")
+        return cls(**merged)
 
     def to_dict(self) -> dict[str, Any]:
         return asdict(self)
+
+
+def _canonical_keys(mapping: Mapping[str, Any]) -> dict[str, Any]:
+    """The mapping with ``P`` renamed to ``p_ch`` (only one of the two may
+    be present)."""
+    data = dict(mapping)
+    if "P" in data:
+        if "p_ch" in data:
+            raise ConfigurationError("give P or p_ch, not both")
+        data["p_ch"] = data.pop("P")
+    return data

@@ -19,6 +19,7 @@ import statistics
 from dataclasses import dataclass
 from typing import Any, Mapping, Sequence
 
+import numpy as np
 import torch
 
 
@@ -33,14 +34,19 @@ class PChSelection:
 
 def legal_p_candidates(channel_count: int,
                        candidates: Sequence[int] | None = None) -> tuple[int, ...]:
-    """Sorted distinct integer candidates in [1, channel_count]."""
-    if type(channel_count) is not int or channel_count < 1:
-        raise ValueError("channel_count must be a positive integer")
-    pool = range(1, channel_count + 1) if candidates is None else candidates
-    legal = sorted({p for p in pool if type(p) is int and 1 <= p <= channel_count})
-    if not legal:
-        raise ValueError("no legal P_ch candidates")
-    return tuple(legal)
+    """The distinct candidates that are chunk widths the coder accepts for
+    ``channel_count`` latent channels (ints in [1, channel_count]), ascending;
+    all widths when ``candidates`` is None."""
+    if isinstance(channel_count, bool) or not isinstance(channel_count, int) or channel_count < 1:
+        raise ValueError(f"channel_count must be a positive int, got {channel_count!r}")
+    if candidates is None:
+        return tuple(range(1, channel_count + 1))
+    width_ok = np.frompyfunc(lambda p: type(p) is int and 0 < p <= channel_count, 1, 1)
+    pool = np.array(list(candidates), dtype=object)
+    kept = np.unique(pool[width_ok(pool).astype(bool)].astype(np.int64)) if pool.size else pool
+    if kept.size == 0:
+        raise ValueError(f"none of the P_ch candidates is a width in [1, {channel_count}]")
+    return tuple(int(p) for p in kept)
 
 
 def default_p_candidates(channel_count: int) -> tuple[int, ...]:
@@ -48,11 +54,52 @@ def default_p_candidates(channel_count: int) -> tuple[int, ...]:
                                               128, 192, 256, 320))
 
 
-def _positive(value: object, name: str) -> float:
-    if (isinstance(value, bool) or not isinstance(value, (int, float))
-            or not math.isfinite(float(value)) or value <= 0):
-        raise ValueError(f"{name} must be a finite positive number")
-    return float(value)
+@dataclass(frozen=True)
+class _Measured:
+    """One usable measurement: P, the codec's time and its imbalance
+    ``|codec / inference - 1|``."""
+
+    p: int
+    codec_ms: float
+    imbalance: float
+
+
+def _measured(record: Mapping[str, object]) -> _Measured | None:
+    p = record.get("p_ch")
+    if type(p) is not int or p < 1:
+        return None  # not a P measurement
+    times = []
+    for key in ("inference_total_ms", "codec_total_ms"):
+        v = record.get(key)
+        ok = isinstance(v, (int, float)) and not isinstance(v, bool) and math.isfinite(v) and v > 0
+        if not ok:
+            raise ValueError(f"{key} of the P_ch={p} record must be a finite positive number")
+        times.append(float(v))
+    inference, codec = times
+    return _Measured(p, codec, abs(codec / inference - 1.0))
+
+
+def _plateau(points: Sequence[_Measured], delta: float, patience: int) -> dict[str, object]:
+    """Neighbouring P values whose codec times differ by at most ``delta``
+    (relative) are flat steps; the first ``patience`` flat steps in a row are
+    reported as a plateau (diagnostic only)."""
+    codec = np.array([pt.codec_ms for pt in points])
+    rel = np.abs(np.diff(codec)) / np.maximum(codec[:-1], 1e-12)
+    steps = [{"from_p_ch": a.p, "to_p_ch": b.p, "relative_delta": float(r)}
+             for a, b, r in zip(points, points[1:], rel)]
+    out: dict[str, object] = {"detected": False, "pairs": steps}
+    if len(steps) < patience:
+        return out
+    flat = (rel <= delta).astype(np.int64)
+    # flat steps in a window of `patience` ending at each step
+    window = np.convolve(flat, np.ones(patience, dtype=np.int64))[: len(flat)]
+    ends = np.flatnonzero(window >= patience)
+    if ends.size:
+        end = int(ends[0])
+        out.update(detected=True, start_p_ch=steps[end - patience + 1]["from_p_ch"],
+                   end_p_ch=steps[end]["to_p_ch"],
+                   interpretation="codec-time changes within measurement variation")
+    return out
 
 
 def choose_p_ch(measurements: Sequence[Mapping[str, object]], *,
@@ -60,43 +107,34 @@ def choose_p_ch(measurements: Sequence[Mapping[str, object]], *,
                 plateau_patience: int = 2) -> PChSelection:
     """Pick P from records holding ``p_ch``, ``inference_total_ms`` and
     ``codec_total_ms`` (records without a positive integer ``p_ch`` are
-    skipped)."""
+    skipped).  Each candidate is ranked by ``(balanced, P)`` when it is
+    balanced (imbalance within ``relative_tolerance``), else by ``(not
+    balanced, -imbalance, P)``: the best is the largest balanced P (fewer
+    chunks: fewer flushed states, lower bpp) or, when none is balanced, the
+    most balanced P, ties to the larger one."""
     if not 0 <= relative_tolerance < 1:
-        raise ValueError("relative_tolerance must be in [0, 1)")
+        raise ValueError(f"relative_tolerance must lie in [0, 1), got {relative_tolerance!r}")
     if plateau_delta < 0:
-        raise ValueError("plateau_delta must be non-negative")
+        raise ValueError(f"plateau_delta must be >= 0, got {plateau_delta!r}")
     if type(plateau_patience) is not int or plateau_patience < 1:
-        raise ValueError("plateau_patience must be positive")
-    rows = []  # (p, ratio error, codec ms)
-    for m in measurements:
-        p = m.get("p_ch")
-        if type(p) is not int or p < 1:
-            continue
-        inference = _positive(m.get("inference_total_ms"), "inference_total_ms")
-        codec = _positive(m.get("codec_total_ms"), "codec_total_ms")
-        rows.append((p, abs(codec / inference - 1.0), codec))
-    if not rows:
-        raise ValueError("no usable P_ch measurements")
-    rows.sort()
-    pairs = [{"from_p_ch": a[0], "to_p_ch": b[0],
-              "relative_delta": abs(b[2] - a[2]) / max(a[2], 1e-12)}
-             for a, b in zip(rows, rows[1:])]
-    plateau: dict[str, object] = {"detected": False, "pairs": pairs}
-    streak = 0
-    for i, pair in enumerate(pairs):
-        streak = streak + 1 if pair["relative_delta"] <= plateau_delta else 0
-        if streak >= plateau_patience:
-            plateau.update(detected=True, start_p_ch=pairs[i - streak + 1]["from_p_ch"],
-                           end_p_ch=pair["to_p_ch"],
-                           interpretation="codec-time changes within measurement variation")
-            break
-    balanced = [r for r in rows if r[1] <= relative_tolerance]
-    if balanced:
-        p, err, _ = max(balanced, key=lambda r: r[0])
-        return PChSelection(p, "auto_selected", "largest_relative_error_pass", err, plateau)
-    p, err, _ = min(rows, key=lambda r: (r[1], -r[0]))
-    return PChSelection(p, "fallback_closest_balance", "no_candidate_within_relative_tolerance",
-                        err, plateau)
+        raise ValueError(f"plateau_patience must be an int >= 1, got {plateau_patience!r}")
+    points = sorted((pt for pt in map(_measured, measurements) if pt is not None),
+                    key=lambda pt: (pt.p, pt.codec_ms))
+    if not points:
+        raise ValueError("no usable P_ch measurement among the records")
+    plateau = _plateau(points, plateau_delta, plateau_patience)
+
+    def rank(pt: _Measured):
+        if pt.imbalance <= relative_tolerance:
+            return (1, pt.p, 0.0)
+        return (0, -pt.imbalance, pt.p)
+
+    best = max(points, key=rank)
+    if best.imbalance <= relative_tolerance:
+        return PChSelection(best.p, "auto_selected", "largest_relative_error_pass",
+                            best.imbalance, plateau)
+    return PChSelection(best.p, "fallback_closest_balance",
+                        "no_candidate_within_relative_tolerance", best.imbalance, plateau)
 
 
 def sweep_p_ch(model: Any, samples: Sequence[torch.Tensor], *,

@@ -212,3 +212,18 @@ def test_invalid_tables_rejected(cdf, size):
     cdfs[0, : len(cdf)] = cdf
     rc, _, _ = prepare_host(cdfs, [size], [0])
     assert rc == _native.ETABLE
+
+
+def test_return_codes_map_to_error_classes():
+    # input problems are CoderInputError (a ValueError); a HIP runtime failure
+    # is a CoderError (a RuntimeError) but not an input error
+    from fast_compressai.coders.errors import CoderError, CoderInputError
+
+    _native.check(_native.OK, "ok")
+    for rc in (_native.EINVAL, _native.ETABLE):
+        with pytest.raises(CoderInputError, match=f"code {rc}"):
+            _native.check(rc, "call")
+    with pytest.raises(CoderError, match="code 3") as info:
+        _native.check(_native.EHIP, "call")
+    assert not isinstance(info.value, ValueError)
+    assert isinstance(info.value, RuntimeError)
