@@ -46,22 +46,44 @@ def parse():
                     help="instead of the coder benchmark: compress_many / decompress_many of "
                          "IMAGES 512x768 images through a FactorizedPrior(N=128, M=192) "
                          "stand-in, sequential vs overlapped streams")
+    ap.add_argument("--kernels", default=None, choices=sorted(KERNEL_WORKLOADS) + ["copy"],
+                    help="instead of the benchmark: launch only the encode and decode kernels "
+                         "of one workload (--reps times each, after 3 untimed launches) and "
+                         "print their event times; 'copy' runs one device copy of --copy-probe "
+                         "MiB.  For rocprofv3 counter runs.")
+    ap.add_argument("--reps", type=int, default=10)
     return ap.parse_args()
 
 
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "hbm_traffic_coder_512x768_p4.txt")
+def _kernel_workloads():
+    from fast_compressai import synthetic
+
+    return {
+        "coder_512x768_p4": lambda: synthetic.coder_512x768(seed=0, p_ch=4),
+        "highres_2160x3840_p8": synthetic.highres_2160x3840,
+        "batch64_skew_p16": synthetic.batch_skew,
+        "batch64_uniform_p16": synthetic.batch_uniform,
+    }
 
 
-def read_traffic(kernel_key: str):
-    """HBM bytes per launch of ``kernel_key`` from the committed counter
-    summary (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy's reading);
-    None when there is no summary for it."""
+# workloads of --kernels: the four symbol workloads, and the fused Gaussian
+# kernels on the mean-scale hyperprior's y at P = 4 and 16
+KERNEL_WORKLOADS = ("coder_512x768_p4", "highres_2160x3840_p8", "batch64_skew_p16",
+                    "batch64_uniform_p16", "hyperprior_y_p4", "hyperprior_y_p16")
+
+
+def read_traffic(workload: str, kernel_key: str):
+    """HBM bytes per launch of ``kernel_key`` ("k_encode" / "k_decode") on
+    ``workload`` from the committed counter summary
+    ``profiles/counters_<workload>.txt`` (FETCH_SIZE + WRITE_SIZE, each
+    scaled by what it reads for a plain copy); None without a summary."""
+    path = os.path.join(REPO, "profiles", f"counters_{workload}.txt")
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             for line in f:
                 parts = line.split()
-                if len(parts) >= 2 and parts[0] == kernel_key and parts[1].startswith("bytes="):
-                    return int(parts[1].split("=", 1)[1])
+                if len(parts) >= 3 and parts[0] == "traffic" and parts[1] == kernel_key:
+                    return int(parts[2].split("=", 1)[1])
     except OSError:
         return None
     return None
@@ -351,6 +373,42 @@ def rans64_times(torch, dev, batch, reps=3):
     return statistics.median(ts), cpu, batch * w.n, sum(len(s) for s in streams)
 
 
+def kernels_only(args):
+    """--kernels: one workload's encode and decode kernels (or one device
+    copy), for counter runs; prints the event-timed averages."""
+    import torch
+
+    from fast_compressai.coders import WarpDivBackend, _native
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.kernels == "copy":
+        nb = max(args.copy_probe, 1) << 20
+        src = torch.empty(nb, dtype=torch.uint8, device=dev)
+        src.fill_(7)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"kernels": "copy", "bytes": nb}), flush=True)
+        return
+    L = _native.lib()
+    reps = max(5, args.reps // 5 * 5)
+    if args.kernels.startswith("hyperprior_y_p"):
+        kt, pb, n_sym, _ = gaussian_kernel_times(L, _native, torch, int(args.kernels[14:]), dev,
+                                                 reps=reps)
+        alg = 12 * n_sym + pb
+    else:
+        w = _kernel_workloads()[args.kernels]()
+        kt, pb = kernel_times(L, _native, torch, WarpDivBackend(), w, dev, reps=reps)
+        n_sym = w.batch * w.n
+        alg = 8 * n_sym + pb
+    print(json.dumps({"kernels": args.kernels, "symbols": n_sym, "payload_bytes": pb,
+                      "alg_bytes_per_launch": alg,
+                      "encode_us": round(kt["encode"] * 1e6, 2),
+                      "decode_us": round(kt["decode"] * 1e6, 2)}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -359,6 +417,9 @@ def main():
         sys.exit(2)
     if args.pipeline > 0:
         pipeline_bench(args)
+        return
+    if args.kernels:
+        kernels_only(args)
         return
 
     import numpy as np
@@ -462,19 +523,30 @@ def main():
     else:
         kernel, key, dur = "k_encode<0,false,8> (gaans_encode_symbols)", "k_encode", enc_avg
     achieved = alg_bytes / dur / 1e9
-    traffic = read_traffic(key)
+    traffic = read_traffic("coder_512x768_p4", key)
 
     # ---- kernel times of the other workload shapes (parity-tested configs) --
     extra = {}
     if not args.no_extra:
-        for label, wl in (("highres_1x320x136x240_p8", synthetic.highres_2160x3840()),
+        def counter_traffic(label, alg):
+            """HBM bytes per launch from the committed counter summary, and
+            their ratio to the algorithmic bytes"""
+            out = {}
+            for k in ("encode", "decode"):
+                t = read_traffic(label, f"k_{k}")
+                out[f"{k}_traffic_bytes"] = t
+                out[f"{k}_traffic_over_alg"] = None if t is None else round(t / alg, 3)
+            return out
+
+        for label, wl in (("highres_2160x3840_p8", synthetic.highres_2160x3840()),
                           ("batch64_skew_p16", synthetic.batch_skew()),
                           ("batch64_uniform_p16", synthetic.batch_uniform())):
             kt, pb = kernel_times(L, _native, torch, backend, wl, dev)
             n_sym = wl.batch * wl.n
             alg = 8 * n_sym + pb  # symbols + indexes (int32) + payload, either direction
             extra[label] = {
-                "symbols": n_sym, "payload_bytes": pb,
+                "symbols": n_sym, "payload_bytes": pb, "alg_bytes_per_launch": alg,
+                **counter_traffic(label, alg),
                 "encode_hbm_frac": round(alg / kt["encode"] / 1e9 / HBM_PEAK_GBPS, 4),
                 "decode_hbm_frac": round(alg / kt["decode"] / 1e9 / HBM_PEAK_GBPS, 4),
                 "encode_kernel_us": round(kt["encode"] * 1e6, 2),
@@ -487,8 +559,10 @@ def main():
         for p_ch in (4, 16):
             kt, pb, n_sym, raw_b = gaussian_kernel_times(L, _native, torch, p_ch, dev)
             alg = 12 * n_sym + pb  # y, means, scales (or y_hat) fp32 + payload
-            extra[f"hyperprior_y_1x192x32x48_gaussian_p{p_ch}"] = {
-                "symbols": n_sym, "payload_bytes": pb,
+            extra[f"hyperprior_y_p{p_ch}"] = {
+                "workload": f"mean-scale hyperprior y 1x192x32x48, fused Gaussian kernels, P={p_ch}",
+                "symbols": n_sym, "payload_bytes": pb, "alg_bytes_per_launch": alg,
+                **counter_traffic(f"hyperprior_y_p{p_ch}", alg),
                 "encode_hbm_frac": round(alg / kt["encode"] / 1e9 / HBM_PEAK_GBPS, 4),
                 "decode_hbm_frac": round(alg / kt["decode"] / 1e9 / HBM_PEAK_GBPS, 4),
                 "encode_kernel_us": round(kt["encode"] * 1e6, 2),
