@@ -1,11 +1,12 @@
 // GA-ANS wave64 latent coder for MI355X (gfx950): HIP kernels + C ABI.
 //
-// Format: one chunk = P latent channels; 64 lanes, one 32-bit rANS state per
-// lane (x in [2^16, 2^32), 16-bit renormalisation words, 16-bit CDF
-// precision); lane l owns positions l + 64 t of the chunk.  The words a step
-// emits are ordered by lane (wave ballot + mbcnt prefix); the decoder hands
-// refill words out in the same order.  The bytes are defined by the CPU
-// oracle (oracle/gaans_oracle.c).
+// Format: one chunk = P latent channels; 64 lanes, I = 1, 2 or 4 interleaved
+// 32-bit rANS states per lane (x in [2^16, 2^32), 16-bit renormalisation
+// words, 16-bit CDF precision); lane l owns positions l + 64 t of the chunk
+// and codes step t with its state slot t mod I, so I consecutive steps are
+// independent chains.  The words a step emits are ordered by lane (wave
+// ballot + mbcnt prefix); the decoder hands refill words out in the same
+// order.  The bytes are defined by the CPU oracle (oracle/gaans_oracle.c).
 //
 // Work mapping: one workgroup per chunk (a coder wave and kMappers mapper
 // waves, 320 threads, for encode; one more wave, the escape reader, for
@@ -60,7 +61,7 @@ constexpr int kWaves = kMappers + 1;     // + the coder wave
 constexpr int kThreads = kWaves * kLanes;
 constexpr uint32_t kStateLow = 1u << 16;  // rANS L
 constexpr uint32_t kMagic = 0x31574147u;  // "GAW1"
-constexpr uint32_t kVersion = 2u;
+constexpr uint32_t kVersion = 3u;
 constexpr uint32_t kParams = 0x00041040u;  // lanes 64 | precision 16 << 8 | bypass 4 << 16
 constexpr int kFixedWords = 16;
 constexpr uint32_t kTabMagic = 0x35425447u;  // "GTB5"
@@ -192,22 +193,39 @@ __host__ __device__ inline uint32_t enc_div(uint32_t x, uint32_t m, uint32_t sh)
   return (t + ((x - t) >> 1)) >> sh;
 }
 
+// Index hash term of chunk position p with table tb: MurmurHash3's 32-bit
+// finaliser (Appleby) of p * 0x9E3779B9 + tb + 1; a chunk's hash is the sum
+// of its terms mod 2^32 (a bijective finaliser, so positions that trade
+// tables change the sum except with probability about 2^-32).
+__host__ __device__ __forceinline__ uint32_t index_term(uint32_t p, uint32_t tb) {
+  uint32_t h = p * kHashMul + tb + 1u;
+  h ^= h >> 16;
+  h *= 0x85EBCA6Bu;
+  h ^= h >> 13;
+  h *= 0xC2B2AE35u;
+  h ^= h >> 16;
+  return h;
+}
+
 struct Layout {
-  int64_t B, N, C, P, HW, K, chunk_len, BK, header_bytes, max_payload, cap_words, ws_bytes;
+  int64_t B, N, C, P, I, HW, K, chunk_len, BK, header_bytes, max_payload, cap_words, ws_bytes;
   int64_t o_words_cnt, o_status, o_hash, o_end, o_info, o_states, o_words, o_esc, o_esc_raw;
 };
 
-int make_layout(int64_t B, int64_t N, int64_t C, int64_t P, Layout* L) {
+int make_layout(int64_t B, int64_t N, int64_t C, int64_t P, int64_t I, Layout* L) {
   if (B < 1 || N < 1 || C < 1 || P < 1)
     return fail(GAANS_EINVAL, "B, N, C and P must be >= 1 (got %lld, %lld, %lld, %lld)",
                 (long long)B, (long long)N, (long long)C, (long long)P);
+  if (I != 1 && I != 2 && I != 4)
+    return fail(GAANS_EINVAL, "interleave must be 1, 2 or 4 states per lane (got %lld)",
+                (long long)I);
   if (N % C != 0)
     return fail(GAANS_EINVAL, "symbols per row N=%lld is not a multiple of channels C=%lld",
                 (long long)N, (long long)C);
   if (P > C) return fail(GAANS_EINVAL, "P=%lld exceeds channels C=%lld", (long long)P, (long long)C);
   if (N >= ((int64_t)1 << 31) || B >= ((int64_t)1 << 31))
     return fail(GAANS_EINVAL, "B and N must be < 2^31");
-  L->B = B; L->N = N; L->C = C; L->P = P;
+  L->B = B; L->N = N; L->C = C; L->P = P; L->I = I;
   L->HW = N / C;
   L->K = (C + P - 1) / P;
   L->chunk_len = P * L->HW;
@@ -218,7 +236,7 @@ int make_layout(int64_t B, int64_t N, int64_t C, int64_t P, Layout* L) {
   L->header_bytes = align_up(4 * kFixedWords + 8 * L->BK, 16);
   // per symbol at most one stream word and 9 escape nibbles; per chunk the
   // states, a pad word and a partly used escape word
-  L->max_payload = L->header_bytes + B * N * 7 + L->BK * (4 * kLanes + 8);
+  L->max_payload = L->header_bytes + B * N * 7 + L->BK * (4 * kLanes * I + 8);
   L->cap_words = align_up(L->chunk_len + 2, 2);
   int64_t o = 0;
   L->o_words_cnt = o; o = align_up(o + 4 * L->BK, 256);
@@ -226,7 +244,7 @@ int make_layout(int64_t B, int64_t N, int64_t C, int64_t P, Layout* L) {
   L->o_hash = o;      o = align_up(o + 4 * L->BK, 256);
   L->o_end = o;       o = align_up(o + 4 * L->BK, 256);
   L->o_info = o;      o = align_up(o + 32, 256);
-  L->o_states = o;    o = align_up(o + 4 * kLanes * L->BK, 256);
+  L->o_states = o;    o = align_up(o + 4 * kLanes * I * L->BK, 256);
   L->o_words = o;     o = align_up(o + 2 * L->cap_words * L->BK, 256);
   L->o_esc = o;       o = align_up(o + 8 * L->BK, 256);
   L->o_esc_raw = o;   o = align_up(o + 4 * L->chunk_len * L->BK, 256);
@@ -508,6 +526,7 @@ struct EncArgs {
   BlobRef blob;
   int64_t N;
   int32_t K, P, C, chunk_len;
+  int32_t I;  // interleave: state slots per lane
   UDiv div_hw;
   int32_t cap_words;
   int64_t BK, header_bytes;
@@ -543,10 +562,17 @@ int enc_fixed_lds(int sb) {
   return sb >= 16 ? EncGeom<16>::kFixed : (sb >= 8 ? EncGeom<8>::kFixed : EncGeom<4>::kFixed);
 }
 
+// State slots a chunk of len symbols flushes: min(I, T) of its A lanes.
+__host__ __device__ __forceinline__ int slots_used(int len, int I) {
+  const int T = (len + kLanes - 1) / kLanes;
+  return T < I ? T : I;
+}
+
 // Payload bytes of chunk g: states, stream and escape words, pad.
 __device__ __forceinline__ uint64_t chunk_bytes(const EncArgs& a, int64_t g) {
   const int len = chunk_len_of(g, a.K, a.chunk_len, a.N);
-  const uint32_t A = len < kLanes ? (uint32_t)len : (uint32_t)kLanes;
+  const uint32_t A = (len < kLanes ? (uint32_t)len : (uint32_t)kLanes) *
+                     (uint32_t)slots_used(len, a.I);
   const uint32_t W = __hip_atomic_load(&a.chunk_words[g], __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
   const uint32_t Z = __hip_atomic_load(&a.esc[g].y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -636,7 +662,7 @@ __device__ __forceinline__ uint4 enc_record(const EncArgs& a, const Tabs& tb, bo
   const bool ok = act & !bad;
   status |= bad ? GAANS_ST_INDEX : 0u;
   tbi = ok ? tbi : (lds ? tb.t_lo : 0);
-  hash += ok ? ((uint32_t)(tbi + 1) ^ ((uint32_t)p * kHashMul)) : 0u;
+  hash += ok ? index_term((uint32_t)p, (uint32_t)tbi) : 0u;
   int32_t sym;
   if (kMode != kModeSymbols) {
     const float r = rintf(__fsub_rn(__int_as_float(in_a), in_m));
@@ -723,8 +749,9 @@ __device__ __forceinline__ void enc_escapes(const uint4 r, uint32_t* __restrict_
   cnt = uni(cnt + __popcll(em));
 }
 
-template <int kMode, bool kImplicit, int SB>
+template <int kMode, bool kImplicit, int SB, int NI>
 __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
+  static_assert(SB % NI == 0, "a block holds whole rounds of the state slots");
   using G = EncGeom<SB>;
   constexpr int kPer = G::kPer;
   extern __shared__ __align__(16) uint8_t smem[];
@@ -750,7 +777,11 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
   uint16_t* __restrict__ wbuf = a.words + g * a.cap_words;
   int wp = a.cap_words;  // coder: wave-uniform write cursor (backwards)
   int fl = a.cap_words;  // coder: words at [fl, cap) are already in wbuf
-  uint32_t x = kStateLow;
+  // the lane's state slots: step t codes with slot t mod NI (block starts are
+  // multiples of NI, so slot (u mod NI) for step u of a block)
+  uint32_t x[NI];
+#pragma unroll
+  for (int q = 0; q < NI; ++q) x[q] = kStateLow;
   uint32_t hash = 0, status = 0, znib = 0;
   int n_esc = 0;  // coder: escapes listed so far
   uint32_t* __restrict__ esc_list = a.esc_raw + g * a.chunk_len + a.chunk_len;
@@ -874,15 +905,17 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
             // common case: a full block, no per-step branches
 #pragma unroll
             for (int k = H - 1; k >= 0; --k) {
-              emit_words((x >> 16) >= 65536u - (r[k].x >> 16), x, ring, wp, lane);
-              x = enc_apply(x, r[k]);
+              uint32_t& xs = x[(h * H + k) % NI];
+              emit_words((xs >> 16) >= 65536u - (r[k].x >> 16), xs, ring, wp, lane);
+              xs = enc_apply(xs, r[k]);
             }
           } else {
 #pragma unroll
             for (int k = H - 1; k >= 0; --k) {
               if (j * SB + h * H + k >= T) continue;
-              emit_words((x >> 16) >= 65536u - (r[k].x >> 16), x, ring, wp, lane);
-              x = enc_apply(x, r[k]);
+              uint32_t& xs = x[(h * H + k) % NI];
+              emit_words((xs >> 16) >= 65536u - (r[k].x >> 16), xs, ring, wp, lane);
+              xs = enc_apply(xs, r[k]);
             }
           }
           // escapes of the group (their bins are coded above): list them,
@@ -915,7 +948,12 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
     }
   }
 
-  if (wid == 0 && lane < A) a.states[g * kLanes + lane] = x;
+  if (wid == 0 && lane < A) {
+    const int sl = slots_used(len, NI);
+#pragma unroll
+    for (int q = 0; q < NI; ++q)
+      if (q < sl) a.states[(g * NI + q) * kLanes + lane] = x[q];
+  }
   hash = wave_sum(hash);
   status = wave_or(status);
   znib = wave_sum(znib);
@@ -969,7 +1007,7 @@ struct PackArgs {
   const uint8_t* __restrict__ tables;
   uint8_t* __restrict__ out;
   int64_t out_bytes, header_bytes, cap_words, BK, N;
-  uint32_t B, N32, C, P, K, chunk_len, M;
+  uint32_t B, N32, C, P, K, chunk_len, M, I;
 };
 
 __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
@@ -999,6 +1037,7 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
         case 9: w = kParams; break;
         case 10: w = th->digest_lo; break;
         case 11: w = th->digest_hi; break;
+        case 12: w = a.I; break;
         default: w = 0; break;
       }
       hdr[tid] = w;
@@ -1008,15 +1047,17 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
   if ((int64_t)a.header_bytes + endo > a.out_bytes || endo < beg) return;
   const int len = chunk_len_of(g, (int32_t)a.K, (int32_t)a.chunk_len, a.N);
   const int A = len < kLanes ? len : kLanes;
+  const int nst = A * slots_used(len, (int)a.I);  // final states: slot-major, A each
   const int64_t W = a.chunk_words[g];
   const uint2 ez = a.esc[g];  // escape count, escape nibbles
   int64_t U = W + (ez.y + 3u) / 4u;
   U += U & 1;  // u16 words after the states: stream, pad, escape words
   uint8_t* dst = a.out + a.header_bytes + beg;
   uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
-  for (int j = tid; j < A; j += 256) d32[j] = a.states[g * kLanes + j];
+  for (int j = tid; j < nst; j += 256)
+    d32[j] = a.states[(g * a.I + j / A) * kLanes + j % A];
   const uint16_t* src = a.words + g * a.cap_words + (a.cap_words - W);
-  uint32_t* w32 = reinterpret_cast<uint32_t*>(dst + 4 * A);
+  uint32_t* w32 = reinterpret_cast<uint32_t*>(dst + 4 * nst);
   const int64_t n32 = U / 2;
   for (int64_t j = tid; j < n32; j += 256) {
     const uint32_t lo = (2 * j < W) ? src[2 * j] : 0u;
@@ -1165,7 +1206,7 @@ __device__ __forceinline__ uint2 dec_record(const DecArgs& a, const Tabs& tb, in
   const bool ok = act & !bad;
   status |= bad ? GAANS_ST_INDEX : 0u;
   tbi = ok ? tbi : (tb.nt > 0 ? tb.t_lo : 0);
-  hash += ok ? ((uint32_t)(tbi + 1) ^ ((uint32_t)p * kHashMul)) : 0u;
+  hash += ok ? index_term((uint32_t)p, (uint32_t)tbi) : 0u;
   const bool staged = (uint32_t)(tbi - tb.t_lo) < (uint32_t)tb.nt;
   all_lds = ballot(!staged) == 0;
   uint32_t nsym, offset;
@@ -1200,7 +1241,7 @@ __device__ __forceinline__ uint2 dec_record_search(const DecArgs& a, const Tabs&
   const bool ok = act & !bad;
   status |= bad ? GAANS_ST_INDEX : 0u;
   tbi = ok ? tbi : 0;
-  hash += ok ? ((uint32_t)(tbi + 1) ^ ((uint32_t)p * kHashMul)) : 0u;
+  hash += ok ? index_term((uint32_t)p, (uint32_t)tbi) : 0u;
   const uint4 lm = tb.lmeta[tbi];
   uint2 r;
   r.x = (uint32_t)tbi | ((act ? lm.x + lm.y - 1u : kNoSym) << 16);
@@ -1508,8 +1549,9 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint2 r, uint
   return (uint32_t)(oob ? 0 : o);
 }
 
-template <int kMode, bool kImplicit, int SB, bool kSearch = false>
+template <int kMode, bool kImplicit, int SB, bool kSearch, int NI>
 __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
+  static_assert(SB % NI == 0, "a block holds whole rounds of the state slots");
   constexpr bool kLatents = kMode != kModeSymbols;  // fp32 output with a per-element add
   using G = DecGeom<SB>;
   constexpr int kPer = G::kPer;
@@ -1547,9 +1589,9 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   // any of them is used (the scheduling barrier keeps them together), and
   // the checks are branch-free.
   const TabHdr th = load_tab_hdr(a.tables);
-  uint32_t hw[12];
+  uint32_t hw[13];
 #pragma unroll
-  for (int i = 0; i < 12; ++i) hw[i] = hdr[i];
+  for (int i = 0; i < 13; ++i) hw[i] = hdr[i];
   // end offsets of chunks g - 1 and g: two adjacent words (word 15 of the
   // fixed header stands in for chunk -1 and is not used)
   const uint32_t* pe = hdr + (kFixedWords - 1) + g;
@@ -1560,7 +1602,7 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   const bool hdr_ok = (hw[0] == kMagic) & (hw[1] == kVersion) & (hw[2] == a.B) &
                       (hw[3] == (uint32_t)a.N) & (hw[4] == a.C) & (hw[5] == a.P) &
                       (hw[6] == a.K) & (hw[7] == a.chunk_len) & (hw[8] == a.M) &
-                      (hw[9] == kParams);
+                      (hw[9] == kParams) & (hw[12] == (uint32_t)NI);
   const bool tab_ok = tables_ok(th, a.M, a.tables_bytes, a.blob) & (hw[10] == th.digest_lo) &
                       (hw[11] == th.digest_hi);
   const bool offsets_safe = (th.flags & kTabOffsetsSafe) != 0;
@@ -1572,6 +1614,8 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   chunk_range(g, a.K, a.N, (int32_t)a.chunk_len, row, start, len, k);
   const int T = (len + kLanes - 1) / kLanes;
   const int A = len < kLanes ? len : kLanes;
+  const int SL = slots_used(len, NI);  // state slots flushed per lane
+  const int nst = SL * A;
   const int nblk = (T + SB - 1) / SB;
   // the chunk's bytes: the offsets are used unconditionally, so that their
   // loads are not moved behind the header checks
@@ -1580,7 +1624,7 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   const uint32_t want_hash = e_hash;
   const int64_t cb = (int64_t)endo - (int64_t)beg;
   const bool bad_range = (endo < beg) | ((int64_t)endo > a.payload_bytes - a.header_bytes) |
-                         ((beg & 3u) != 0u) | (cb < 4 * A) | (((cb - 4 * A) & 3) != 0);
+                         ((beg & 3u) != 0u) | (cb < 4 * nst) | (((cb - 4 * nst) & 3) != 0);
   status |= (ok & bad_range) ? GAANS_ST_CORRUPT : 0u;
   ok = ok & !bad_range;
   Stream S;  // the coder's; its final position is checked after the last barrier
@@ -1599,9 +1643,9 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
     tb.lclut = lclut;
     tb.lstarts = lstarts;
     const uint8_t* cdata = a.payload + a.header_bytes + beg;
-    const uint32_t* s32 = reinterpret_cast<const uint32_t*>(cdata + 4 * A);
+    const uint32_t* s32 = reinterpret_cast<const uint32_t*>(cdata + 4 * nst);
     const uint32_t* safe = reinterpret_cast<const uint32_t*>(cdata);
-    const int q16 = (int)((cb - 4 * A) / 2);  // u16 words after the states (even)
+    const int q16 = (int)((cb - 4 * nst) / 2);  // u16 words after the states (even)
 
     int32_t cbx[kPer], nbx[kPer];
     float cm[kPer], nm[kPer];
@@ -1684,7 +1728,10 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
     // stream words, the mappers' first two blocks of inputs, the escape
     // reader's window.
     EscReader E;
-    uint32_t x = kStateLow;
+    // the lane's state slots: step t decodes with slot t mod NI
+    uint32_t x[NI];
+#pragma unroll
+    for (int q = 0; q < NI; ++q) x[q] = kStateLow;
     uint32_t w0[G::kPre][G::kPfU32];
     if (wid == 0) {
       S.s32 = s32;
@@ -1692,7 +1739,9 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
       S.q = q16;
       S.q32 = q16 / 2;
       S.filled = 0;
-      x = safe[lane < A ? lane : 0];  // lane < A: below
+#pragma unroll
+      for (int q = 0; q < NI; ++q)  // slot q of lane l: state q * A + l (lane < A: below)
+        x[q] = safe[(q < SL ? q : 0) * A + (lane < A ? lane : 0)];
 #pragma unroll
       for (int b = 0; b < G::kPre; ++b)
 #pragma unroll
@@ -1734,7 +1783,8 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
     // before the first block and one per block, and one after the mappers'
     // last store.
     if (wid == 0) {
-      x = lane < A ? x : kStateLow;
+#pragma unroll
+      for (int q = 0; q < NI; ++q) x[q] = (lane < A && q < SL) ? x[q] : kStateLow;
 #pragma unroll
       for (int b = 0; b < G::kPre; ++b)
 #pragma unroll
@@ -1761,7 +1811,8 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
           uint64_t em[SB];
 #pragma unroll
           for (int u = 0; u < SB; ++u) {
-            ov[u] = dec_step<true, true, SB, kSearch>(tb, r[u], x, S, sring, em[u], status, lane);
+            ov[u] = dec_step<true, true, SB, kSearch>(tb, r[u], x[u % NI], S, sring, em[u],
+                                                      status, lane);
             any_em |= em[u];
           }
           if (__builtin_expect(any_em != 0ull, 0)) {
@@ -1779,19 +1830,26 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
             else src[u * kLanes + lane].x = ov[u];
           }
         } else {
-          // last block or tables outside LDS: one step at a time
+          // last block or tables outside LDS: one step at a time, the slot
+          // in use rotated into x[0] (a full block rotates every slot back
+          // into place; after a partial last block only the final check,
+          // which takes the slots in any order, follows)
 #pragma unroll 1
           for (int u = 0; u < SB && j * SB + u < T; ++u) {
             const uint2 ru = src[u * kLanes + lane];
             uint64_t em;
             uint32_t v;
             if constexpr (kSearch) {
-              v = dec_step<true, false, SB, true>(tb, ru, x, S, sring, em, status, lane);
+              v = dec_step<true, false, SB, true>(tb, ru, x[0], S, sring, em, status, lane);
             } else {
               v = ((nl >> u) & 1u) == 0u
-                      ? dec_step<true, false, SB>(tb, ru, x, S, sring, em, status, lane)
-                      : dec_step<false, false, SB>(tb, ru, x, S, sring, em, status, lane);
+                      ? dec_step<true, false, SB>(tb, ru, x[0], S, sring, em, status, lane)
+                      : dec_step<false, false, SB>(tb, ru, x[0], S, sring, em, status, lane);
             }
+            const uint32_t x0 = x[0];
+#pragma unroll
+            for (int q = 0; q + 1 < NI; ++q) x[q] = x[q + 1];
+            x[NI - 1] = x0;
             if (lane == 0) ei[u] = make_uint4((uint32_t)em, (uint32_t)(em >> 32), ecur, 0u);
             ecur += (uint32_t)__popcll(em);
             any_em |= em;
@@ -1805,7 +1863,9 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
         }
         __syncthreads();
       }
-      if (lane < A && x != kStateLow) status |= GAANS_ST_CORRUPT;
+#pragma unroll
+      for (int q = 0; q < NI; ++q)
+        if (lane < A && x[q] != kStateLow) status |= GAANS_ST_CORRUPT;
       __syncthreads();  // after the mappers' last store
     } else if (wid == kEscWave) {
       __syncthreads();
@@ -2427,12 +2487,84 @@ int32_t pow2_floor(int32_t v) {  // largest power of two <= v (0 for v < 1)
   return p;
 }
 
+// Kernel of a launch: template arguments chosen at run time.
+using EncKernel = void (*)(EncArgs);
+using DecKernel = void (*)(DecArgs);
+
+template <int kMode, bool kImp, int SB>
+EncKernel enc_kernel_ni(int ni) {
+  return ni == 4 ? k_encode<kMode, kImp, SB, 4>
+                 : (ni == 2 ? k_encode<kMode, kImp, SB, 2> : k_encode<kMode, kImp, SB, 1>);
+}
+
+template <int kMode, bool kImp>
+EncKernel enc_kernel_sb(int sb, int ni) {
+  return sb == 4 ? enc_kernel_ni<kMode, kImp, 4>(ni) : enc_kernel_ni<kMode, kImp, 8>(ni);
+}
+
+// Encode kernel of a mode, index kind, block size and interleave; 16-step
+// blocks are built for explicit or computed indexes only (with table =
+// channel the 16-step kernel needs private scratch).
+EncKernel enc_kernel(int mode, bool imp, int sb, int ni) {
+  if (sb == 16) {
+    switch (mode) {
+      case kModeGaussian: return enc_kernel_ni<kModeGaussian, false, 16>(ni);
+      case kModeLatents: return enc_kernel_ni<kModeLatents, false, 16>(ni);
+      default: return enc_kernel_ni<kModeSymbols, false, 16>(ni);
+    }
+  }
+  switch (mode) {
+    case kModeGaussian: return enc_kernel_sb<kModeGaussian, false>(sb, ni);
+    case kModeLatents:
+      return imp ? enc_kernel_sb<kModeLatents, true>(sb, ni)
+                 : enc_kernel_sb<kModeLatents, false>(sb, ni);
+    default:
+      return imp ? enc_kernel_sb<kModeSymbols, true>(sb, ni)
+                 : enc_kernel_sb<kModeSymbols, false>(sb, ni);
+  }
+}
+
+template <int kMode, bool kImp, int SB, bool kSearch>
+DecKernel dec_kernel_ni(int ni) {
+  return ni == 4 ? k_decode<kMode, kImp, SB, kSearch, 4>
+                 : (ni == 2 ? k_decode<kMode, kImp, SB, kSearch, 2>
+                            : k_decode<kMode, kImp, SB, kSearch, 1>);
+}
+
+template <int kMode, bool kImp, bool kSearch>
+DecKernel dec_kernel_sb(int sb, int ni) {
+  return sb == 4 ? dec_kernel_ni<kMode, kImp, 4, kSearch>(ni)
+                 : (sb == 8 ? dec_kernel_ni<kMode, kImp, 8, kSearch>(ni)
+                            : dec_kernel_ni<kMode, kImp, 16, kSearch>(ni));
+}
+
+// Decode kernel of a mode, index kind, block size, lookup kind and
+// interleave (the search lookups serve explicit or computed indexes only).
+DecKernel dec_kernel(int mode, bool imp, int sb, bool search, int ni) {
+  if (search) {
+    switch (mode) {
+      case kModeGaussian: return dec_kernel_sb<kModeGaussian, false, true>(sb, ni);
+      case kModeLatents: return dec_kernel_sb<kModeLatents, false, true>(sb, ni);
+      default: return dec_kernel_sb<kModeSymbols, false, true>(sb, ni);
+    }
+  }
+  switch (mode) {
+    case kModeGaussian: return dec_kernel_sb<kModeGaussian, false, false>(sb, ni);
+    case kModeLatents:
+      return imp ? dec_kernel_sb<kModeLatents, true, false>(sb, ni)
+                 : dec_kernel_sb<kModeLatents, false, false>(sb, ni);
+    default:
+      return imp ? dec_kernel_sb<kModeSymbols, true, false>(sb, ni)
+                 : dec_kernel_sb<kModeSymbols, false, false>(sb, ni);
+  }
+}
+
 int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y,
                   const float* medians, const int32_t* indexes, const GaussIn* g,
                   const gaans_tables* tables, int64_t B, int64_t N, int64_t C, int64_t P,
-                  void* ws, int64_t ws_bytes, void* ctrl, uint64_t* info_out) {
+                  int64_t I, void* ws, int64_t ws_bytes, void* ctrl, uint64_t* info_out) {
   Layout L;
-  int rc = make_layout(B, N, C, P, &L);
+  int rc = make_layout(B, N, C, P, I, &L);
   if (rc) return rc;
   if ((rc = check_tables_arg(tables))) return rc;
   if (mode == kModeSymbols ? !symbols : (!y || (mode == kModeLatents && !medians)))
@@ -2478,6 +2610,7 @@ int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y
   a.P = (int32_t)P;
   a.C = (int32_t)C;
   a.chunk_len = (int32_t)L.chunk_len;
+  a.I = (int32_t)I;
   a.div_hw = make_udiv((uint32_t)L.HW);
   a.cap_words = (int32_t)L.cap_words;
   a.BK = L.BK;
@@ -2499,46 +2632,18 @@ int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y
   if (lds > (size_t)dl.per_block)
     return fail(GAANS_EINVAL, "encode needs %zu bytes of LDS, the device has %d", lds,
                 dl.per_block);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid((uint32_t)L.BK), block(kThreads);
-  auto launch = [&](auto kernel) -> int {
-    int r = allow_lds(reinterpret_cast<const void*>(kernel), lds, dl);
-    if (r) return r;
-    kernel<<<grid, block, lds, s>>>(a);
-    return check_launch("encode");
-  };
-  const bool imp = indexes == nullptr;
-  if (plan.sb == 16) {
-    switch (mode) {
-      case kModeGaussian: return launch(k_encode<kModeGaussian, false, 16>);
-      case kModeLatents: return launch(k_encode<kModeLatents, false, 16>);
-      default: return launch(k_encode<kModeSymbols, false, 16>);
-    }
-  }
-  if (plan.sb == 4) {
-    switch (mode) {
-      case kModeGaussian: return launch(k_encode<kModeGaussian, false, 4>);
-      case kModeLatents:
-        return imp ? launch(k_encode<kModeLatents, true, 4>) : launch(k_encode<kModeLatents, false, 4>);
-      default:
-        return imp ? launch(k_encode<kModeSymbols, true, 4>) : launch(k_encode<kModeSymbols, false, 4>);
-    }
-  }
-  switch (mode) {
-    case kModeGaussian: return launch(k_encode<kModeGaussian, false, 8>);
-    case kModeLatents:
-      return imp ? launch(k_encode<kModeLatents, true, 8>) : launch(k_encode<kModeLatents, false, 8>);
-    default:
-      return imp ? launch(k_encode<kModeSymbols, true, 8>) : launch(k_encode<kModeSymbols, false, 8>);
-  }
+  const EncKernel kernel = enc_kernel(mode, indexes == nullptr, plan.sb, (int)I);
+  if ((rc = allow_lds(reinterpret_cast<const void*>(kernel), lds, dl))) return rc;
+  kernel<<<dim3((uint32_t)L.BK), dim3(kThreads), lds, static_cast<hipStream_t>(stream)>>>(a);
+  return check_launch("encode");
 }
 
 int decode_impl(int mode, void* stream, const uint8_t* payload, int64_t payload_bytes,
                 const int32_t* indexes, const GaussIn* g, const gaans_tables* tables,
-                const float* medians, int64_t B, int64_t N, int64_t C, int64_t P,
+                const float* medians, int64_t B, int64_t N, int64_t C, int64_t P, int64_t I,
                 int32_t* out_sym, float* out_y, void* ctrl, uint32_t* status_out) {
   Layout L;
-  int rc = make_layout(B, N, C, P, &L);
+  int rc = make_layout(B, N, C, P, I, &L);
   if (rc) return rc;
   if ((rc = check_tables_arg(tables))) return rc;
   if (!payload || !status_out || !ctrl ||
@@ -2597,58 +2702,10 @@ int decode_impl(int mode, void* stream, const uint8_t* payload, int64_t payload_
   if (lds > (size_t)dl.per_block)
     return fail(GAANS_EINVAL, "decode needs %zu bytes of LDS, the device has %d", lds,
                 dl.per_block);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid((uint32_t)L.BK), block(kDecThreads);
-  auto launch = [&](auto kernel) -> int {
-    int r = allow_lds(reinterpret_cast<const void*>(kernel), lds, dl);
-    if (r) return r;
-    kernel<<<grid, block, lds, s>>>(a);
-    return check_launch("decode");
-  };
-  const bool imp = indexes == nullptr;
-  if (plan.search) {  // explicit or computed indexes only
-    switch (mode) {
-      case kModeGaussian:
-        return plan.sb == 4    ? launch(k_decode<kModeGaussian, false, 4, true>)
-               : plan.sb == 8 ? launch(k_decode<kModeGaussian, false, 8, true>)
-                              : launch(k_decode<kModeGaussian, false, 16, true>);
-      case kModeLatents:
-        return plan.sb == 4    ? launch(k_decode<kModeLatents, false, 4, true>)
-               : plan.sb == 8 ? launch(k_decode<kModeLatents, false, 8, true>)
-                              : launch(k_decode<kModeLatents, false, 16, true>);
-      default:
-        return plan.sb == 4    ? launch(k_decode<kModeSymbols, false, 4, true>)
-               : plan.sb == 8 ? launch(k_decode<kModeSymbols, false, 8, true>)
-                              : launch(k_decode<kModeSymbols, false, 16, true>);
-    }
-  }
-  if (plan.sb == 16) {
-    switch (mode) {
-      case kModeGaussian: return launch(k_decode<kModeGaussian, false, 16>);
-      case kModeLatents:
-        return imp ? launch(k_decode<kModeLatents, true, 16>)
-                   : launch(k_decode<kModeLatents, false, 16>);
-      default:
-        return imp ? launch(k_decode<kModeSymbols, true, 16>)
-                   : launch(k_decode<kModeSymbols, false, 16>);
-    }
-  }
-  if (plan.sb == 4) {
-    switch (mode) {
-      case kModeGaussian: return launch(k_decode<kModeGaussian, false, 4>);
-      case kModeLatents:
-        return imp ? launch(k_decode<kModeLatents, true, 4>) : launch(k_decode<kModeLatents, false, 4>);
-      default:
-        return imp ? launch(k_decode<kModeSymbols, true, 4>) : launch(k_decode<kModeSymbols, false, 4>);
-    }
-  }
-  switch (mode) {
-    case kModeGaussian: return launch(k_decode<kModeGaussian, false, 8>);
-    case kModeLatents:
-      return imp ? launch(k_decode<kModeLatents, true, 8>) : launch(k_decode<kModeLatents, false, 8>);
-    default:
-      return imp ? launch(k_decode<kModeSymbols, true, 8>) : launch(k_decode<kModeSymbols, false, 8>);
-  }
+  const DecKernel kernel = dec_kernel(mode, indexes == nullptr, plan.sb, plan.search, (int)I);
+  if ((rc = allow_lds(reinterpret_cast<const void*>(kernel), lds, dl))) return rc;
+  kernel<<<dim3((uint32_t)L.BK), dim3(kDecThreads), lds, static_cast<hipStream_t>(stream)>>>(a);
+  return check_launch("decode");
 }
 
 uint64_t fnv_u32(uint64_t h, uint32_t v) {
@@ -2870,12 +2927,13 @@ int gaans_abi_version(void) { return GAANS_ABI_VERSION; }
 
 const char* gaans_last_error(void) { return g_last_error.c_str(); }
 
-int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, gaans_layout* out) {
+int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
+                     gaans_layout* out) {
   if (!out) return fail(GAANS_EINVAL, "layout pointer is NULL");
   Layout L;
-  int rc = make_layout(B, N, C, P, &L);
+  int rc = make_layout(B, N, C, P, interleave, &L);
   if (rc) return rc;
-  out->B = L.B; out->N = L.N; out->C = L.C; out->P = L.P;
+  out->B = L.B; out->N = L.N; out->C = L.C; out->P = L.P; out->I = L.I;
   out->HW = L.HW; out->K = L.K; out->chunk_len = L.chunk_len; out->BK = L.BK;
   out->header_bytes = L.header_bytes;
   out->max_payload_bytes = L.max_payload;
@@ -2890,6 +2948,28 @@ int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, gaans_layout* o
   out->ws_words = L.o_words;
   out->ws_esc = L.o_esc;
   out->ws_esc_raw = L.o_esc_raw;
+  return GAANS_OK;
+}
+
+int gaans_choose_interleave(const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
+                            int64_t P, double budget, int32_t* interleave) {
+  if (!tables || !interleave) return fail(GAANS_EINVAL, "NULL argument");
+  Layout L;
+  int rc = make_layout(B, N, C, P, 1, &L);
+  if (rc) return rc;
+  if (!(budget >= 0.0) || !(tables->mean_bits >= 0.0f))
+    return fail(GAANS_EINVAL, "budget and the tables' mean_bits must be non-negative numbers");
+  const int64_t len = L.chunk_len < L.N ? L.chunk_len : L.N;  // a full chunk
+  const int64_t A = len < kLanes ? len : kLanes;
+  const double expected = (double)len * tables->mean_bits / 8.0 + 4.0 * (double)A;
+  *interleave = 1;
+  for (int I = 4; I >= 2; I >>= 1) {
+    const double extra = 4.0 * (double)A * (slots_used((int)len, I) - 1);
+    if (extra > 0.0 && extra <= budget * expected) {
+      *interleave = I;
+      break;
+    }
+  }
   return GAANS_OK;
 }
 
@@ -2958,6 +3038,7 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
   bool search = total <= kSearchMaxSyms;
   for (int32_t t = 0; t < M; ++t) search &= offsets[t] >= INT32_MIN + 65536;
   uint32_t dblk = 0;
+  double bits = 0.0;  // sum over tables of the table's entropy
   uint64_t dg = 0xcbf29ce484222325ull;
   dg = fnv_u32(dg, (uint32_t)M);
   uint32_t base = 0;
@@ -2976,6 +3057,8 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
       const uint32_t f = (uint32_t)(c[v + 1] - c[v]);
       ent[2 * (base + v)] = (uint32_t)c[v] | ((f - 1u) << 16);
       ent[2 * (base + v) + 1] = enc_magic(f);
+      const double pr = f / 65536.0;
+      bits -= pr * log2(pr);
     }
     dblk += (uint32_t)build_lookup(c, S, lut + (int64_t)t * kLutSize,
                                    blocks + (size_t)dblk * kSubSize, dblk);
@@ -3009,40 +3092,45 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
   desc->digest = dg;
   desc->max_dense = max_dense;
   desc->total_dense = total_dense;
+  desc->mean_bits = (float)(bits / M);
+  desc->reserved = 0;
   return GAANS_OK;
 }
 
 int gaans_encode_symbols(void* stream, const int32_t* symbols_dev, const int32_t* indexes_dev,
                          const gaans_tables* tables, int64_t B, int64_t N, int64_t C, int64_t P,
-                         void* workspace_dev, int64_t workspace_bytes, void* ctrl_dev,
-                         uint64_t* info_out) {
+                         int32_t interleave, void* workspace_dev, int64_t workspace_bytes,
+                         void* ctrl_dev, uint64_t* info_out) {
   return encode_stage1(kModeSymbols, stream, symbols_dev, nullptr, nullptr, indexes_dev, nullptr,
-                       tables, B, N, C, P, workspace_dev, workspace_bytes, ctrl_dev, info_out);
+                       tables, B, N, C, P, interleave, workspace_dev, workspace_bytes, ctrl_dev,
+                       info_out);
 }
 
 int gaans_encode_latents(void* stream, const float* y_dev, const float* medians_dev,
                          const int32_t* indexes_dev, const gaans_tables* tables, int64_t B,
-                         int64_t N, int64_t C, int64_t P, void* workspace_dev,
+                         int64_t N, int64_t C, int64_t P, int32_t interleave, void* workspace_dev,
                          int64_t workspace_bytes, void* ctrl_dev, uint64_t* info_out) {
   return encode_stage1(kModeLatents, stream, nullptr, y_dev, medians_dev, indexes_dev, nullptr,
-                       tables, B, N, C, P, workspace_dev, workspace_bytes, ctrl_dev, info_out);
+                       tables, B, N, C, P, interleave, workspace_dev, workspace_bytes, ctrl_dev,
+                       info_out);
 }
 
 int gaans_encode_gaussian(void* stream, const float* y_dev, const float* means_dev,
                           const float* scales_dev, const float* scale_table_dev,
                           int32_t n_scales, float scale_bound, const gaans_tables* tables,
-                          int64_t B, int64_t N, int64_t C, int64_t P, void* workspace_dev,
-                          int64_t workspace_bytes, void* ctrl_dev, uint64_t* info_out) {
+                          int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
+                          void* workspace_dev, int64_t workspace_bytes, void* ctrl_dev,
+                          uint64_t* info_out) {
   const GaussIn g{means_dev, scales_dev, scale_table_dev, n_scales, scale_bound};
   return encode_stage1(kModeGaussian, stream, nullptr, y_dev, nullptr, nullptr, &g, tables, B, N,
-                       C, P, workspace_dev, workspace_bytes, ctrl_dev, info_out);
+                       C, P, interleave, workspace_dev, workspace_bytes, ctrl_dev, info_out);
 }
 
 int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace_bytes,
                       const gaans_tables* tables, int64_t B, int64_t N, int64_t C, int64_t P,
-                      uint8_t* out_dev, int64_t out_bytes) {
+                      int32_t interleave, uint8_t* out_dev, int64_t out_bytes) {
   Layout L;
-  int rc = make_layout(B, N, C, P, &L);
+  int rc = make_layout(B, N, C, P, interleave, &L);
   if (rc) return rc;
   if ((rc = check_tables_arg(tables))) return rc;
   if (!workspace_dev || workspace_bytes < L.ws_bytes)
@@ -3072,16 +3160,17 @@ int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace
   a.K = (uint32_t)L.K;
   a.chunk_len = (uint32_t)L.chunk_len;
   a.M = (uint32_t)tables->M;
+  a.I = (uint32_t)L.I;
   k_pack<<<dim3((uint32_t)L.BK), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(a);
   return check_launch("pack");
 }
 
 int gaans_encode_symbols_noalloc(void* stream, const int32_t* symbols_dev,
                                  const int32_t* indexes_dev, const gaans_tables* tables,
-                                 int64_t B, int64_t N, int64_t C, int64_t P, uint8_t* out_dev,
-                                 int64_t out_bytes, uint64_t* info_out) {
+                                 int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
+                                 uint8_t* out_dev, int64_t out_bytes, uint64_t* info_out) {
   Layout L;
-  int rc = make_layout(B, N, C, P, &L);
+  int rc = make_layout(B, N, C, P, interleave, &L);
   if (rc) return rc;
   // the size limit first: it needs no device
   const int64_t need = (int64_t)GAANS_CTRL_BYTES + L.ws_bytes;
@@ -3099,35 +3188,40 @@ int gaans_encode_symbols_noalloc(void* stream, const int32_t* symbols_dev,
   void* ctrl = base;
   void* ws = base + GAANS_CTRL_BYTES;
   rc = encode_stage1(kModeSymbols, stream, symbols_dev, nullptr, nullptr, indexes_dev, nullptr,
-                     tables, B, N, C, P, ws, L.ws_bytes, ctrl, info_out);
+                     tables, B, N, C, P, interleave, ws, L.ws_bytes, ctrl, info_out);
   if (rc) return rc;
-  return gaans_encode_pack(stream, ws, L.ws_bytes, tables, B, N, C, P, out_dev, out_bytes);
+  return gaans_encode_pack(stream, ws, L.ws_bytes, tables, B, N, C, P, interleave, out_dev,
+                           out_bytes);
 }
 
 int gaans_decode_symbols(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
                          const int32_t* indexes_dev, const gaans_tables* tables, int64_t B,
-                         int64_t N, int64_t C, int64_t P, int32_t* out_dev, void* ctrl_dev,
-                         uint32_t* status_out) {
+                         int64_t N, int64_t C, int64_t P, int32_t interleave, int32_t* out_dev,
+                         void* ctrl_dev, uint32_t* status_out) {
   return decode_impl(kModeSymbols, stream, payload_dev, payload_bytes, indexes_dev, nullptr,
-                     tables, nullptr, B, N, C, P, out_dev, nullptr, ctrl_dev, status_out);
+                     tables, nullptr, B, N, C, P, interleave, out_dev, nullptr, ctrl_dev,
+                     status_out);
 }
 
 int gaans_decode_latents(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
                          const int32_t* indexes_dev, const gaans_tables* tables,
                          const float* medians_dev, int64_t B, int64_t N, int64_t C, int64_t P,
-                         float* y_hat_dev, void* ctrl_dev, uint32_t* status_out) {
+                         int32_t interleave, float* y_hat_dev, void* ctrl_dev,
+                         uint32_t* status_out) {
   return decode_impl(kModeLatents, stream, payload_dev, payload_bytes, indexes_dev, nullptr,
-                     tables, medians_dev, B, N, C, P, nullptr, y_hat_dev, ctrl_dev, status_out);
+                     tables, medians_dev, B, N, C, P, interleave, nullptr, y_hat_dev, ctrl_dev,
+                     status_out);
 }
 
 int gaans_decode_gaussian(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
                           const float* scales_dev, const float* means_dev,
                           const float* scale_table_dev, int32_t n_scales, float scale_bound,
                           const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
-                          int64_t P, float* y_hat_dev, void* ctrl_dev, uint32_t* status_out) {
+                          int64_t P, int32_t interleave, float* y_hat_dev, void* ctrl_dev,
+                          uint32_t* status_out) {
   const GaussIn g{means_dev, scales_dev, scale_table_dev, n_scales, scale_bound};
   return decode_impl(kModeGaussian, stream, payload_dev, payload_bytes, nullptr, &g, tables,
-                     nullptr, B, N, C, P, nullptr, y_hat_dev, ctrl_dev, status_out);
+                     nullptr, B, N, C, P, interleave, nullptr, y_hat_dev, ctrl_dev, status_out);
 }
 
 int gaans_rans64_decode(void* stream, const uint8_t* streams_dev, int64_t streams_bytes,

@@ -15,7 +15,7 @@ import threading
 from .errors import CoderDependencyError
 
 LIB_NAME = "libgaans_w64.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 CTRL_BYTES = 256
 NOALLOC_SCRATCH_BYTES = 16 * 1024 * 1024  # GAANS_NOALLOC_SCRATCH_BYTES
 
@@ -41,7 +41,7 @@ STATUS_TEXT = {
 }
 
 
-_LAYOUT_FIELDS = ("B", "N", "C", "P", "HW", "K", "chunk_len", "BK", "header_bytes",
+_LAYOUT_FIELDS = ("B", "N", "C", "P", "I", "HW", "K", "chunk_len", "BK", "header_bytes",
                   "max_payload_bytes", "cap_words", "workspace_bytes", "ws_chunk_words",
                   "ws_chunk_status", "ws_index_hash", "ws_end_off", "ws_info", "ws_states",
                   "ws_words", "ws_esc", "ws_esc_raw")
@@ -67,7 +67,8 @@ class Tables(ctypes.Structure):
     _fields_ = [("dev", ctypes.c_void_p), ("bytes", ctypes.c_int64), ("M", ctypes.c_int32),
                 ("max_nsym", ctypes.c_int32), ("total_nsym", ctypes.c_int64),
                 ("digest", ctypes.c_uint64), ("max_dense", ctypes.c_int32),
-                ("flags", ctypes.c_int32), ("total_dense", ctypes.c_int64)]
+                ("flags", ctypes.c_int32), ("total_dense", ctypes.c_int64),
+                ("mean_bits", ctypes.c_float), ("reserved", ctypes.c_int32)]
 
 
 def library_path() -> str:
@@ -88,22 +89,26 @@ def _declare(L) -> None:
     sig = {
         "gaans_abi_version": ([], ctypes.c_int),
         "gaans_last_error": ([], ctypes.c_char_p),
-        "gaans_get_layout": ([i64, i64, i64, i64, ctypes.POINTER(Layout)], ctypes.c_int),
+        "gaans_get_layout": ([i64, i64, i64, i64, i32, ctypes.POINTER(Layout)], ctypes.c_int),
+        "gaans_choose_interleave": ([T, i64, i64, i64, i64, ctypes.c_double,
+                                     ctypes.POINTER(ctypes.c_int32)], ctypes.c_int),
         "gaans_tables_bytes": ([p, p, i32, i32, ctypes.POINTER(ctypes.c_int64)], ctypes.c_int),
         "gaans_tables_prepare": ([p, p, p, i32, i32, p, i64, T], ctypes.c_int),
-        "gaans_encode_symbols": ([p, p, p, T, i64, i64, i64, i64, p, i64, p, p], ctypes.c_int),
-        "gaans_encode_latents": ([p, p, p, p, T, i64, i64, i64, i64, p, i64, p, p],
+        "gaans_encode_symbols": ([p, p, p, T, i64, i64, i64, i64, i32, p, i64, p, p],
                                  ctypes.c_int),
-        "gaans_encode_pack": ([p, p, i64, T, i64, i64, i64, i64, p, i64], ctypes.c_int),
-        "gaans_encode_symbols_noalloc": ([p, p, p, T, i64, i64, i64, i64, p, i64, p],
+        "gaans_encode_latents": ([p, p, p, p, T, i64, i64, i64, i64, i32, p, i64, p, p],
+                                 ctypes.c_int),
+        "gaans_encode_pack": ([p, p, i64, T, i64, i64, i64, i64, i32, p, i64], ctypes.c_int),
+        "gaans_encode_symbols_noalloc": ([p, p, p, T, i64, i64, i64, i64, i32, p, i64, p],
                                          ctypes.c_int),
-        "gaans_decode_symbols": ([p, p, i64, p, T, i64, i64, i64, i64, p, p, p], ctypes.c_int),
-        "gaans_decode_latents": ([p, p, i64, p, T, p, i64, i64, i64, i64, p, p, p],
+        "gaans_decode_symbols": ([p, p, i64, p, T, i64, i64, i64, i64, i32, p, p, p],
                                  ctypes.c_int),
-        "gaans_encode_gaussian": ([p, p, p, p, p, i32, f32, T, i64, i64, i64, i64, p, i64, p, p],
-                                  ctypes.c_int),
-        "gaans_decode_gaussian": ([p, p, i64, p, p, p, i32, f32, T, i64, i64, i64, i64, p, p, p],
-                                  ctypes.c_int),
+        "gaans_decode_latents": ([p, p, i64, p, T, p, i64, i64, i64, i64, i32, p, p, p],
+                                 ctypes.c_int),
+        "gaans_encode_gaussian": ([p, p, p, p, p, i32, f32, T, i64, i64, i64, i64, i32, p, i64, p,
+                                   p], ctypes.c_int),
+        "gaans_decode_gaussian": ([p, p, i64, p, p, p, i32, f32, T, i64, i64, i64, i64, i32, p, p,
+                                   p], ctypes.c_int),
         "gaans_rans64_decode": ([p, p, i64, p, p, T, i64, i64, i64, p, p, p], ctypes.c_int),
         "gaans_wait_host_word": ([p, p], ctypes.c_int),
         "gaans_host_selftest": ([], ctypes.c_int),
@@ -163,12 +168,12 @@ def check(rc: int, what: str) -> None:
 _layouts: dict = {}
 
 
-def layout(B: int, N: int, C: int, P: int) -> LayoutInts:
-    key = (B, N, C, P)
+def layout(B: int, N: int, C: int, P: int, I: int = 1) -> LayoutInts:
+    key = (B, N, C, P, I)
     out = _layouts.get(key)
     if out is None:
         raw = Layout()
-        check(lib().gaans_get_layout(B, N, C, P, ctypes.byref(raw)), "layout")
+        check(lib().gaans_get_layout(B, N, C, P, I, ctypes.byref(raw)), "layout")
         out = LayoutInts(raw)
         if len(_layouts) > 256:
             _layouts.clear()

@@ -9,8 +9,12 @@ payloads and ``CoderDependencyError`` for a missing library or device.
 
 Differences that follow from the new format:
 
-* ``format_id`` is ``"gaans-w64-v2"``; payloads of the reference's
+* ``format_id`` is ``"gaans-w64-v3"``; payloads of the reference's
   ``warpans-v2`` format are rejected.
+* ``interleave`` (keyword of ``encode``, field of the payload) is the number
+  of rANS states per lane, 1, 2 or 4; None (the default) lets the coder pick
+  the most whose extra flushed states stay within 1% of the expected payload
+  (``gaans.choose_interleave``).
 * ``WarpDivPayload.chunk_ends`` (uint32 ``[B, K]``, exposed also under the
   reference's name ``max_rounds``) holds each chunk's end offset in the
   payload data, not a round count.
@@ -36,8 +40,8 @@ from .capabilities import warp_div_capability
 from .errors import CoderDependencyError, CoderInputError
 from .tables import PreparedTables, TableCache
 
-FORMAT_ID = "gaans-w64-v2"
-FORMAT_VERSION = 2
+FORMAT_ID = "gaans-w64-v3"
+FORMAT_VERSION = 3
 _HEADER_MAGIC = 0x31574147
 _FIXED_HEADER_BYTES = 64
 _SHA256_HEX = re.compile(r"[0-9a-f]{64}")
@@ -70,10 +74,13 @@ class WarpDivPayload:
     format_id: str = FORMAT_ID
     format_version: int = FORMAT_VERSION
     channels: int | None = None
+    interleave: int = 1
 
     def __post_init__(self) -> None:
         if self.format_id != FORMAT_ID or self.format_version != FORMAT_VERSION:
             raise CoderInputError("unsupported warp_div payload format")
+        if type(self.interleave) is not int or self.interleave not in (1, 2, 4):
+            raise CoderInputError("warp_div interleave must be 1, 2 or 4")
         if (not isinstance(self.packed, torch.Tensor) or self.packed.device.type != "cuda"
                 or self.packed.dtype != torch.uint8 or not self.packed.is_contiguous()):
             raise CoderInputError("packed payload must be contiguous GPU uint8")
@@ -141,7 +148,8 @@ class WarpDivPayload:
     def from_bytes(cls, data: bytes, device: torch.device | str = "cuda",
                    cdf_count: int | None = None) -> "WarpDivPayload":
         """Rebuild a payload from ``to_bytes`` output (header fields
-        B, N, C, P, K, chunk_len, M, table digest and chunk offsets)."""
+        B, N, C, P, K, chunk_len, M, table digest, interleave and chunk
+        offsets)."""
         if len(data) < _FIXED_HEADER_BYTES:
             raise CoderInputError("warp_div payload header is truncated")
         words = struct.unpack_from("<16I", data, 0)
@@ -163,7 +171,7 @@ class WarpDivPayload:
                    header_bytes=hb, chunk_len=chunk_len, p_ch=P, batch=B,
                    symbols_per_batch=N, cdf_count=M,
                    coding_fingerprint=coding_fingerprint(digest, B, N, C, M),
-                   channels=None if C == M else C)
+                   channels=None if C == M else C, interleave=words[12])
 
 
 # field defaults of WarpDivPayload (for _from_encoder)
@@ -200,12 +208,14 @@ class WarpDivBackend:
         *,
         p_ch: int,
         channels: int | None = None,
+        interleave: int | None = None,
     ) -> WarpDivPayload:
         C = _validate_inputs(symbols, indexes, cdfs, cdf_sizes, offsets, p_ch, channels)
         tables = self.prepared_tables(cdfs, cdf_sizes, offsets)
         B, N = int(symbols.shape[0]), int(symbols.shape[1])
+        interleave = gaans.resolve_interleave(interleave, tables, B, N, C, p_ch)
         enc = gaans.encode(tables, B, N, C, p_ch, symbols.device, symbols=symbols,
-                           indexes=indexes)
+                           indexes=indexes, interleave=interleave)
         return WarpDivPayload._from_encoder(
             packed=enc.packed,
             chunk_ends=enc.chunk_ends,
@@ -217,6 +227,7 @@ class WarpDivBackend:
             cdf_count=int(cdfs.shape[0]),
             coding_fingerprint=coding_fingerprint(tables.digest, B, N, C, int(cdfs.shape[0])),
             channels=None if channels is None else int(channels),
+            interleave=interleave,
         )
 
     def decode(
@@ -241,7 +252,8 @@ class WarpDivBackend:
                 coding_fingerprint(tables.digest, B, N, C, payload.cdf_count):
             raise CoderInputError("coding tables or indexes do not match warp_div payload")
         return gaans.decode(payload.packed, tables, B, N, C, payload.p_ch,
-                            payload.packed.device, indexes=indexes)
+                            payload.packed.device, indexes=indexes,
+                            interleave=payload.interleave)
 
 
 def _validate_inputs(

@@ -36,7 +36,13 @@
  *    the stream has finished, or, with pinned host memory, once the
  *    launch's completion word is set (gaans_wait_host_word).
  *
- * Payload format "gaans-w64-v2": defined byte for byte by the CPU oracle,
+ *  - `interleave` (I) is the number of rANS states per lane, 1, 2 or 4: step t
+ *    of a chunk codes with its lanes' state slot t mod I, so I consecutive
+ *    steps are independent chains (more instruction-level parallelism on the
+ *    serial chain, 4 * 64 * (I - 1) more flushed bytes per chunk).  The
+ *    payload header records it and decode must be called with the same value.
+ *
+ * Payload format "gaans-w64-v3": defined byte for byte by the CPU oracle,
  * oracle/gaans_oracle.c.
  */
 #ifndef GAANS_W64_H
@@ -49,7 +55,7 @@
 extern "C" {
 #endif
 
-#define GAANS_ABI_VERSION 7
+#define GAANS_ABI_VERSION 8
 #define GAANS_CTRL_BYTES 256
 
 /* return codes */
@@ -70,6 +76,7 @@ extern "C" {
 /* Shape of one coding call (pure host arithmetic, see gaans_get_layout). */
 typedef struct gaans_layout {
   int64_t B, N, C, P;     /* batch rows, symbols per row, channels, channels per chunk */
+  int64_t I;              /* interleave: rANS states per lane */
   int64_t HW, K, chunk_len, BK;
   int64_t header_bytes;   /* payload header size (multiple of 16) */
   int64_t max_payload_bytes; /* worst case: every symbol an escape with 8 nibbles */
@@ -93,6 +100,8 @@ typedef struct gaans_tables {
                          per 16-value sub-range, with >= 2 symbol starts) of one table */
   int32_t flags;      /* GAANS_TABLES_* */
   int64_t total_dense; /* decode sub-blocks over all tables */
+  float mean_bits;     /* mean over the tables of their entropy (bits per symbol) */
+  int32_t reserved;
 } gaans_tables;
 
 /* gaans_tables.flags: the blob holds compact search lookups (one u32 per
@@ -104,9 +113,20 @@ typedef struct gaans_tables {
 int gaans_abi_version(void);
 const char* gaans_last_error(void);
 
-/* Chunking and buffer sizes for B rows of N symbols, C channels, P per chunk.
- * Requires B, N, C, P >= 1, N % C == 0, P <= C. */
-int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, gaans_layout* out);
+/* Chunking and buffer sizes for B rows of N symbols, C channels, P per chunk
+ * and `interleave` states per lane.  Requires B, N, C, P >= 1, N % C == 0,
+ * P <= C, interleave in {1, 2, 4}. */
+int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
+                     gaans_layout* out);
+
+/* The interleave this library picks for a shape (pure host arithmetic): the
+ * largest of 4, 2, 1 whose extra flushed states (4 bytes per lane and extra
+ * slot in use) stay within `budget` (a fraction: 0.01 = 1%) of a chunk's
+ * expected payload, estimated as chunk symbols * tables->mean_bits / 8 plus
+ * the states.  No counterpart in the reference (one 64-bit state per lane,
+ * warp_ans_kernel_v2.cu:121-126). */
+int gaans_choose_interleave(const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
+                            int64_t P, double budget, int32_t* interleave);
 
 /* ---- table upload (host memory) ----------------------------------------- */
 
@@ -144,7 +164,7 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes,
  * src/fast_compressai/coders/cuda/warp_ans_kernel_v2.cu:183-273. */
 int gaans_encode_symbols(void* stream, const int32_t* symbols_dev,
                          const int32_t* indexes_dev, const gaans_tables* tables,
-                         int64_t B, int64_t N, int64_t C, int64_t P,
+                         int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
                          void* workspace_dev, int64_t workspace_bytes, void* ctrl_dev,
                          uint64_t* info_out);
 
@@ -153,7 +173,7 @@ int gaans_encode_symbols(void* stream, const int32_t* symbols_dev,
  * Reference: FactorizedWarpDivCodec.compress, factorized.py:46-59. */
 int gaans_encode_latents(void* stream, const float* y_dev, const float* medians_dev,
                          const int32_t* indexes_dev, const gaans_tables* tables,
-                         int64_t B, int64_t N, int64_t C, int64_t P,
+                         int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
                          void* workspace_dev, int64_t workspace_bytes, void* ctrl_dev,
                          uint64_t* info_out);
 
@@ -173,8 +193,9 @@ int gaans_encode_latents(void* stream, const float* y_dev, const float* medians_
 int gaans_encode_gaussian(void* stream, const float* y_dev, const float* means_dev,
                           const float* scales_dev, const float* scale_table_dev,
                           int32_t n_scales, float scale_bound, const gaans_tables* tables,
-                          int64_t B, int64_t N, int64_t C, int64_t P, void* workspace_dev,
-                          int64_t workspace_bytes, void* ctrl_dev, uint64_t* info_out);
+                          int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
+                          void* workspace_dev, int64_t workspace_bytes, void* ctrl_dev,
+                          uint64_t* info_out);
 
 /* Stage 2: write the payload (header + chunks) to out_dev.  May be enqueued
  * right after stage 1 on the same stream into a buffer of
@@ -184,7 +205,7 @@ int gaans_encode_gaussian(void* stream, const float* y_dev, const float* means_d
  * warp_ans_kernel_v2.cu:274-296. */
 int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace_bytes,
                       const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
-                      int64_t P, uint8_t* out_dev, int64_t out_bytes);
+                      int64_t P, int32_t interleave, uint8_t* out_dev, int64_t out_bytes);
 
 /* Stage 1 and stage 2 of gaans_encode_symbols in one call that allocates
  * nothing and takes no workspace or control block: both live in a static
@@ -205,8 +226,8 @@ int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace
 #define GAANS_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
 int gaans_encode_symbols_noalloc(void* stream, const int32_t* symbols_dev,
                                  const int32_t* indexes_dev, const gaans_tables* tables,
-                                 int64_t B, int64_t N, int64_t C, int64_t P, uint8_t* out_dev,
-                                 int64_t out_bytes, uint64_t* info_out);
+                                 int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
+                                 uint8_t* out_dev, int64_t out_bytes, uint64_t* info_out);
 
 /* ---- decode ------------------------------------------------------------- */
 
@@ -217,15 +238,16 @@ int gaans_encode_symbols_noalloc(void* stream, const int32_t* symbols_dev,
  * Reference: decode_with_indexes_warp_cuda, warp_ans_kernel.cu:477-544. */
 int gaans_decode_symbols(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
                          const int32_t* indexes_dev, const gaans_tables* tables,
-                         int64_t B, int64_t N, int64_t C, int64_t P, int32_t* out_dev,
-                         void* ctrl_dev, uint32_t* status_out);
+                         int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
+                         int32_t* out_dev, void* ctrl_dev, uint32_t* status_out);
 
 /* Decode with CompressAI's dequantize fused in: y_hat = fp32(symbol) +
  * medians[c], written as [B, C, HW] fp32. */
 int gaans_decode_latents(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
                          const int32_t* indexes_dev, const gaans_tables* tables,
                          const float* medians_dev, int64_t B, int64_t N, int64_t C,
-                         int64_t P, float* y_hat_dev, void* ctrl_dev, uint32_t* status_out);
+                         int64_t P, int32_t interleave, float* y_hat_dev, void* ctrl_dev,
+                         uint32_t* status_out);
 
 /* Decode a gaans_encode_gaussian payload with the same scales, means and
  * scale table, dequantize fused: y_hat = fp32(symbol) + mean (fp32(symbol)
@@ -235,7 +257,8 @@ int gaans_decode_gaussian(void* stream, const uint8_t* payload_dev, int64_t payl
                           const float* scales_dev, const float* means_dev,
                           const float* scale_table_dev, int32_t n_scales, float scale_bound,
                           const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
-                          int64_t P, float* y_hat_dev, void* ctrl_dev, uint32_t* status_out);
+                          int64_t P, int32_t interleave, float* y_hat_dev, void* ctrl_dev,
+                          uint32_t* status_out);
 
 /* ---- CompressAI Rans64 bitstreams ------------------------------------------ */
 

@@ -75,7 +75,8 @@ def test_config1_accelerate_matches_oracle(gpu_device, p_ch):
     y_np, med_np = y.cpu().numpy(), med.cpu().numpy()
     symbols = oracle.quantize(y_np, med_np)
     assert np.array_equal(symbols, torch.round(y - med.reshape(1, -1, 1, 1)).int().cpu().numpy())
-    want = oracle.gaans_encode(symbols.reshape(1, -1), None, *tabs, p_ch)
+    want = oracle.gaans_encode(symbols.reshape(1, -1), None, *tabs, p_ch,
+                               interleave=payload.interleave)
     assert payload.to_bytes() == want
     want_y_hat = oracle.dequantize(symbols, med_np)
     assert np.array_equal(y_hat.cpu().numpy(), want_y_hat)

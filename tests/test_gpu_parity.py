@@ -35,16 +35,19 @@ def tables_on(w, device):
     return dev(w.cdfs, device), dev(w.cdf_sizes, device), dev(w.offsets, device)
 
 
-def check_workload(backend, device, w, channels=None, bytes_check=True):
-    say("case:", w.name, "P =", w.p_ch, "shape", w.symbols.shape)
+def check_workload(backend, device, w, channels=None, bytes_check=True, interleave=None):
+    say("case:", w.name, "P =", w.p_ch, "shape", w.symbols.shape, "interleave", interleave)
     sym = dev(w.symbols, device)
     idx = dev(w.explicit_indexes(), device)
     cdfs, sizes, offs = tables_on(w, device)
-    payload = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=w.p_ch, channels=channels)
+    payload = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=w.p_ch, channels=channels,
+                             interleave=interleave)
     torch.cuda.synchronize()
+    if interleave is not None:
+        assert payload.interleave == interleave
     if bytes_check:
         ref = O.gaans_encode(w.symbols, w.indexes, w.cdfs, w.cdf_sizes, w.offsets, w.p_ch,
-                             channels)
+                             channels, payload.interleave)
         got = payload.to_bytes()
         assert len(got) == len(ref)
         assert got == ref
@@ -80,13 +83,14 @@ def test_reference_round_trip_escape_symbols(backend, gpu_device):
 
 # ---- hand-derived KAT payloads (see tests/test_oracle.py) -------------------
 
-def test_kat_payloads_bit_exact(backend, gpu_device):
+@pytest.mark.parametrize("interleave", [1, 2, 4])
+def test_kat_payloads_bit_exact(backend, gpu_device, interleave):
     cdf = list(range(17)) + [65536]
     s = [(5 * p + 3) % 16 for p in range(130)]
-    s[129] = 17
+    s[3], s[70], s[129] = -1, 56, 17
     w = synthetic.Workload("KAT 130", np.array([s], np.int32), None, np.array([cdf], np.int32),
                            np.array([18], np.int32), np.array([0], np.int32), 1, 1, 0)
-    check_workload(backend, gpu_device, w)
+    check_workload(backend, gpu_device, w, interleave=interleave)
     w = synthetic.Workload("KAT 2", np.zeros((1, 2), np.int32), None,
                            np.array([[0, 32768, 65536]], np.int32), np.array([3], np.int32),
                            np.array([0], np.int32), 1, 1, 0)
@@ -108,8 +112,9 @@ def random_tables(rng, M, max_size):
     return cdfs, sizes, rng.integers(-20, 20, M).astype(np.int32)
 
 
-def test_random_shapes_bit_exact(backend, gpu_device):
-    rng = np.random.default_rng(11)
+@pytest.mark.parametrize("interleave", [1, 2, 4])
+def test_random_shapes_bit_exact(backend, gpu_device, interleave):
+    rng = np.random.default_rng(11 + interleave)
     for trial in range(40):
         B, C = int(rng.integers(1, 4)), int(rng.integers(1, 13))
         HW = int(rng.choice([1, 3, 16, 63, 64, 65, 200, 777]))
@@ -120,11 +125,12 @@ def test_random_shapes_bit_exact(backend, gpu_device):
             k = int(rng.integers(s.size))
             s.flat[k] = int(rng.choice([2**30 + 7, -(2**31) + 40, 2**20, -(2**16)]))
         w = synthetic.Workload(f"random trial {trial}", s, None, cdfs, sizes, offs, C, P, 0)
-        check_workload(backend, gpu_device, w)
+        check_workload(backend, gpu_device, w, interleave=interleave)
 
 
-def test_explicit_random_indexes_bit_exact(backend, gpu_device):
-    rng = np.random.default_rng(12)
+@pytest.mark.parametrize("interleave", [1, 2, 4])
+def test_explicit_random_indexes_bit_exact(backend, gpu_device, interleave):
+    rng = np.random.default_rng(12 + interleave)
     for trial in range(10):
         M, C, HW = int(rng.integers(1, 9)), int(rng.integers(1, 9)), int(rng.integers(1, 300))
         P = int(rng.integers(1, C + 1))
@@ -132,13 +138,47 @@ def test_explicit_random_indexes_bit_exact(backend, gpu_device):
         s = rng.integers(-30, 30, (2, C * HW)).astype(np.int32)
         idx = rng.integers(0, M, (2, C * HW)).astype(np.int32)
         w = synthetic.Workload(f"explicit trial {trial}", s, idx, cdfs, sizes, offs, C, P, 0)
-        check_workload(backend, gpu_device, w, channels=C)
+        check_workload(backend, gpu_device, w, channels=C, interleave=interleave)
+
+
+def test_long_chunks_with_partial_last_block(backend, gpu_device):
+    # chunks of 32,800 symbols (C=8, HW=4100, P=8): 513 steps, so the
+    # encoder's 16-step blocks end with a one-step block; explicit indexes
+    # with escapes, then the fused latents path with explicit indexes
+    rng = np.random.default_rng(21)
+    w0 = synthetic.coder_512x768(seed=21)
+    C, HW = 8, 4100
+    cdfs, sizes, offs = w0.cdfs[:C], w0.cdf_sizes[:C], w0.offsets[:C]
+    idx = np.repeat(np.arange(C, dtype=np.int32), HW)[None]
+    s = np.rint(rng.laplace(0, 2.0, (1, C * HW))).astype(np.int32)
+    s[0, ::211] = rng.integers(-90000, 90000, s[0, ::211].shape)
+    for I in (1, 2, 4):
+        w = synthetic.Workload("long chunks 1x8x4100", s, idx, cdfs, sizes, offs, C, C, 0)
+        check_workload(backend, gpu_device, w, interleave=I)
+    tables = prepare_tables(dev(cdfs, gpu_device), dev(sizes, gpu_device), dev(offs, gpu_device))
+    med = rng.normal(0, 0.3, C).astype(np.float32)
+    y = (s.reshape(1, C, HW) + med[None, :, None]
+         + rng.uniform(-0.49, 0.49, (1, C, HW))).astype(np.float32)
+    sym = O.quantize(y, med).reshape(1, -1)
+    for I in (1, 4):
+        say("case: fused latents, explicit indexes, 1x8x4100 P=8, interleave", I)
+        enc = gaans.encode(tables, 1, C * HW, C, C, gpu_device, y=dev(y, gpu_device),
+                           medians=dev(med, gpu_device), indexes=dev(idx, gpu_device),
+                           interleave=I)
+        assert enc.packed.cpu().numpy().tobytes() == O.gaans_encode(sym, idx, cdfs, sizes, offs,
+                                                                      C, C, I)
+        y_hat = gaans.decode(enc.packed, tables, 1, C * HW, C, C, gpu_device,
+                             medians=dev(med, gpu_device), indexes=dev(idx, gpu_device),
+                             interleave=I)
+        want = O.dequantize(sym.reshape(1, C, HW), med).reshape(1, -1)
+        assert np.array_equal(y_hat.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
 # ---- benchmark shapes at full size -----------------------------------------
 
-def test_coder_512x768_p4_bit_exact(backend, gpu_device):
-    check_workload(backend, gpu_device, synthetic.coder_512x768())
+@pytest.mark.parametrize("interleave", [None, 2, 4])
+def test_coder_512x768_p4_bit_exact(backend, gpu_device, interleave):
+    check_workload(backend, gpu_device, synthetic.coder_512x768(), interleave=interleave)
 
 
 def test_side_stream_calls_without_device_sync(backend, gpu_device):
@@ -154,7 +194,7 @@ def test_side_stream_calls_without_device_sync(backend, gpu_device):
         idx = dev(w.explicit_indexes(), gpu_device)
         cdfs, sizes, offs = tables_on(w, gpu_device)
         for rep in range(4):
-            payload = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=w.p_ch)
+            payload = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=w.p_ch, interleave=1)
             assert payload.to_bytes() == ref, rep
             out = backend.decode(payload, idx, cdfs, sizes, offs)
             assert torch.equal(out, sym), rep
@@ -179,16 +219,19 @@ def test_hyperprior_y_gaussian_tables(backend, gpu_device, p_ch):
     check_workload(backend, gpu_device, zw)
 
 
-def test_highres_2160x3840_p8(backend, gpu_device):
-    check_workload(backend, gpu_device, synthetic.highres_2160x3840())
+@pytest.mark.parametrize("interleave", [None, 1, 2])
+def test_highres_2160x3840_p8(backend, gpu_device, interleave):
+    check_workload(backend, gpu_device, synthetic.highres_2160x3840(), interleave=interleave)
 
 
+@pytest.mark.parametrize("interleave", [None, 2])
 @pytest.mark.parametrize("make", [synthetic.batch_skew, synthetic.batch_uniform])
-def test_batch64_p16(backend, gpu_device, make):
-    check_workload(backend, gpu_device, make())
+def test_batch64_p16(backend, gpu_device, make, interleave):
+    check_workload(backend, gpu_device, make(), interleave=interleave)
 
 
-def test_escape_heavy_chunks_bit_exact(backend, gpu_device):
+@pytest.mark.parametrize("interleave", [1, 4])
+def test_escape_heavy_chunks_bit_exact(backend, gpu_device, interleave):
     # every symbol of a 1x192x32x48 image escapes: each chunk's escape section
     # holds 6,144 entries, several times the decoder's escape FIFO
     w = synthetic.coder_512x768(seed=7)
@@ -196,7 +239,7 @@ def test_escape_heavy_chunks_bit_exact(backend, gpu_device):
     w.symbols = (w.symbols * 40 + rng.integers(-3, 4, w.symbols.shape)
                  + np.where(rng.random(w.symbols.shape) < 0.5, 5000, -5000)).astype(np.int32)
     w.name = "all-escape 1x192x32x48"
-    check_workload(backend, gpu_device, w)
+    check_workload(backend, gpu_device, w, interleave=interleave)
 
 
 def test_escape_heavy_batch_bit_exact(backend, gpu_device):

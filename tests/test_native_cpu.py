@@ -46,6 +46,45 @@ def test_layout_matches_format():
             _native.layout(*bad)
 
 
+def test_interleave_layout_and_choice():
+    N = 192 * 1536
+    one, four = _native.layout(1, N, 192, 4, 1), _native.layout(1, N, 192, 4, 4)
+    assert one.I == 1 and four.I == 4
+    # three more state slots of 64 lanes per chunk, 48 chunks
+    assert four.max_payload_bytes - one.max_payload_bytes == 48 * 64 * 4 * 3
+    assert four.workspace_bytes > one.workspace_bytes
+    with pytest.raises(Exception):
+        _native.layout(1, 64, 1, 1, 3)
+    L = _native.lib()
+    # the tables' mean entropy: 1 bit (two halves) and 1.5 bits (1/4, 1/4, 1/2)
+    cdfs = np.array([[0, 32768, 65536, 0], [0, 16384, 32768, 65536]], np.int32)
+    sizes, offs = np.array([3, 4], np.int32), np.zeros(2, np.int32)
+    nb = ctypes.c_int64()
+    assert L.gaans_tables_bytes(cdfs.ctypes.data, sizes.ctypes.data, 2, 4, ctypes.byref(nb)) == 0
+    blob, desc = np.zeros(nb.value, np.uint8), _native.Tables()
+    assert L.gaans_tables_prepare(cdfs.ctypes.data, sizes.ctypes.data, offs.ctypes.data, 2, 4,
+                                  blob.ctypes.data, nb.value, ctypes.byref(desc)) == 0
+    assert desc.mean_bits == pytest.approx(1.25, abs=1e-6)
+
+    def choose(bits, B, N, C, P, budget=0.01):
+        d = _native.Tables()
+        d.mean_bits = bits
+        out = ctypes.c_int32(0)
+        assert L.gaans_choose_interleave(ctypes.byref(d), B, N, C, P, budget,
+                                         ctypes.byref(out)) == 0
+        return out.value
+
+    # 2160x3840 latent, P=8: 261,120 symbols a chunk at 3.74 bits is about
+    # 122 KB; three more slots cost 768 B (0.63%), one more 256 B (0.21%)
+    assert choose(3.74, 1, 320 * 32640, 320, 8) == 4
+    assert choose(3.74, 1, 320 * 32640, 320, 8, budget=0.006) == 2
+    assert choose(3.74, 1, 320 * 32640, 320, 8, budget=0.001) == 1
+    # 512x768 latent, P=4: 6,144 symbols at 2.67 bits (about 2 KB) -> one state
+    assert choose(2.67, 1, N, 192, 4) == 1
+    # one step per chunk uses one slot whatever the interleave: nothing to gain
+    assert choose(8.0, 1, 64 * 12, 12, 1) == 1
+
+
 def prepare_host(cdfs, sizes, offs):
     L = _native.lib()
     cdfs = np.ascontiguousarray(cdfs, np.int32)

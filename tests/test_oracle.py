@@ -118,16 +118,55 @@ def test_table_digest_definition():
     assert O.table_digest(cdfs, sizes, offs) == fnv1a64(table_digest_bytes(cdfs, sizes, offs))
 
 
+def fmix32(h):
+    """MurmurHash3's 32-bit finaliser (Appleby)."""
+    h &= 0xFFFFFFFF
+    h ^= h >> 16
+    h = (h * 0x85EBCA6B) & 0xFFFFFFFF
+    h ^= h >> 13
+    h = (h * 0xC2B2AE35) & 0xFFFFFFFF
+    return h ^ (h >> 16)
+
+
 def hash_of(tables_per_position):
     h = 0
     for p, tb in enumerate(tables_per_position):
-        h += (tb + 1) ^ ((p * 0x9E3779B9) & 0xFFFFFFFF)
+        h += fmix32(p * 0x9E3779B9 + tb + 1)
     return h & 0xFFFFFFFF
 
 
-def header_words(B, N, C, P, K, chunk_len, M, digest):
-    return [0x31574147, 2, B, N, C, P, K, chunk_len, M, 0x00041040,
-            digest & 0xFFFFFFFF, digest >> 32, 0, 0, 0, 0]
+def test_index_term_is_murmur3_finaliser():
+    # published value of MurmurHash3's fmix32: fmix32(1) = 0x514E28B7, and the
+    # finaliser fixes 0; position 0 of table 0 hashes key 1
+    assert fmix32(1) == 0x514E28B7 and fmix32(0) == 0
+    assert O.index_term(0, 0) == 0x514E28B7
+    for p, tb in ((1, 0), (0, 5), (4, 1), (261119, 319), (2**31 - 1, 65535)):
+        assert O.index_term(p, tb) == fmix32(p * 0x9E3779B9 + tb + 1)
+
+
+def test_index_hash_detects_a_swapped_pair():
+    # tables 0 and 1 traded between positions p and p + 4: with the additive
+    # term (tb + 1) XOR p*0x9E3779B9 (0x9E3779B9 = 1 mod 4) the sums agree;
+    # the finaliser separates them
+    def additive(tabs):
+        return sum((tb + 1) ^ ((p * 0x9E3779B9) & 0xFFFFFFFF)
+                   for p, tb in enumerate(tabs)) & 0xFFFFFFFF
+    base = [0, 1, 2, 1, 2, 1, 0, 0]
+    swapped = list(base)
+    swapped[0], swapped[4] = base[4], base[0]
+    assert swapped != base and additive(swapped) == additive(base)
+    assert hash_of(swapped) != hash_of(base)
+    # the oracle's payload records the finaliser hash of each chunk
+    cdfs = np.array([[0, 32768, 65536]] * 3, np.int32)
+    for tabs in (base, swapped):
+        data = O.gaans_encode(np.zeros((1, 8), np.int32), np.array([tabs], np.int32), cdfs,
+                              [3] * 3, [0] * 3, 1, channels=1)
+        assert struct.unpack_from("<I", data, 64 + 4)[0] == hash_of(tabs)
+
+
+def header_words(B, N, C, P, K, chunk_len, M, digest, interleave=1):
+    return [0x31574147, 3, B, N, C, P, K, chunk_len, M, 0x00041040,
+            digest & 0xFFFFFFFF, digest >> 32, interleave, 0, 0, 0]
 
 
 def test_gaans_kat_two_lanes_no_renorm():
@@ -184,6 +223,64 @@ def test_gaans_kat_lane_order_group_order_and_escape_section():
     hdr = header_words(1, 130, 1, 1, 1, 130, 1, dg) + [516, hash_of([0] * 130), 0, 0]
     assert data == struct.pack("<20I", *hdr) + chunk
     assert O.gaans_decode(data, None, 1, 130, cdfs, sizes, offs, 1).tolist() == [s]
+
+
+def test_gaans_kat_two_interleaved_states():
+    # the 130-symbol chunk with I = 2: steps 0 and 2 code with state slot 0,
+    # step 1 with slot 1 (every slot starts at 2^16).  Encoder, t = 2 (slot 0,
+    # lanes 0 and 1): lane 0 emits its initial 0x0000 and holds 0x10000 +
+    # s[128]; lane 1 (escape) holds 0x10020.  t = 1 (slot 1, all initial):
+    # every lane but 6 emits 0x0000 and holds 0x10000 + s[64 + l]; lane 6
+    # (escape) holds 0x10020.  t = 0 (slot 0): lane 0 emits s[128], lane 1
+    # emits 0x0020, lanes 2..63 but 3 emit their initial 0x0000; lane 3
+    # (escape) ends at 0x10020 from the initial state.  Stream: step 0's
+    # group, step 1's, step 2's (63 + 63 + 1 = 127 words); the escape section
+    # and its pad are the same as with one state.
+    cdfs, sizes, offs, s = kat_130()
+    data = O.gaans_encode([s], None, cdfs, sizes, offs, 1, interleave=2)
+    stream = [s[128], 0x0020] + [0] * 61 + [0] * 63 + [0] + [0, 0x0215, 0x0211]
+    slot0 = [0x10000 + s[l] for l in range(64)]
+    slot0[3] = 0x10020
+    slot1 = [0x10000 + s[64 + l] for l in range(64)]
+    slot1[6] = 0x10020
+    chunk = struct.pack("<128I", *(slot0 + slot1)) + struct.pack(f"<{len(stream)}H", *stream)
+    assert len(chunk) == 772
+    dg = fnv1a64(table_digest_bytes(cdfs, sizes, offs))
+    hdr = header_words(1, 130, 1, 1, 1, 130, 1, dg, interleave=2) + [772, hash_of([0] * 130),
+                                                                     0, 0]
+    assert data == struct.pack("<20I", *hdr) + chunk
+    assert O.gaans_decode(data, None, 1, 130, cdfs, sizes, offs, 1, interleave=2).tolist() == [s]
+    # the interleave is part of the format: decoding with another one fails
+    for other in (1, 4):
+        with pytest.raises(O.OracleError):
+            O.gaans_decode(data, None, 1, 130, cdfs, sizes, offs, 1, interleave=other)
+
+
+def test_gaans_state_slots_in_use_and_interleave_round_trips():
+    # a chunk of T steps flushes min(I, T) slots of A states
+    cdfs, sizes, offs = CDF2, [3], [0]
+    for n, interleave, slots in ((1, 4, 1), (64, 4, 1), (65, 4, 2), (200, 4, 4), (130, 2, 2)):
+        data = O.gaans_encode(np.zeros((1, n), np.int32), None, cdfs, sizes, offs, 1,
+                              interleave=interleave)
+        A = min(n, 64)
+        assert struct.unpack_from("<I", data, 64)[0] >= 4 * A * slots
+        hb = (64 + 8 + 15) // 16 * 16
+        # every state of a freq-2^15 symbol run stays in [2^16, 2^32) and the
+        # words of 2 bits per symbol: total 4 A slots + 2 words
+        T = (n + 63) // 64
+        words = len(data) - hb - 4 * A * slots
+        assert words % 2 == 0 and words <= 2 * (T * 64)
+    rng = np.random.default_rng(7)
+    for trial in range(24):
+        B, C = int(rng.integers(1, 3)), int(rng.integers(1, 6))
+        HW, P = int(rng.integers(1, 400)), int(rng.integers(1, C + 1))
+        cdfs, sizes, offs = random_tables(rng, C, int(rng.integers(2, 20)))
+        s = rng.integers(-30, 30, (B, C * HW)).astype(np.int32)
+        for interleave in (1, 2, 4):
+            data = O.gaans_encode(s, None, cdfs, sizes, offs, P, interleave=interleave)
+            out = O.gaans_decode(data, None, B, C * HW, cdfs, sizes, offs, P,
+                                 interleave=interleave)
+            assert (out == s).all()
 
 
 def test_gaans_escape_section_word_order_without_pad():

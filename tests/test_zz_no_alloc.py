@@ -16,13 +16,13 @@ from fast_compressai.coders import _native, gaans
 from fast_compressai.coders.tables import prepare_tables
 
 
-def _noalloc(L, tables, sym, idx, B, N, C, P, dev):
-    lay = _native.layout(B, N, C, P)
+def _noalloc(L, tables, sym, idx, B, N, C, P, I, dev):
+    lay = _native.layout(B, N, C, P, I)
     out = torch.zeros(lay.max_payload_bytes, dtype=torch.uint8, device=dev)
     info = torch.zeros(4, dtype=torch.int64, device=dev)
     sp = torch.cuda.current_stream(dev).cuda_stream
     rc = L.gaans_encode_symbols_noalloc(sp, sym.data_ptr(), None if idx is None else idx.data_ptr(),
-                                        tables.ref, B, N, C, P, out.data_ptr(), out.numel(),
+                                        tables.ref, B, N, C, P, I, out.data_ptr(), out.numel(),
                                         info.data_ptr())
     _native.check(rc, "no-allocation encode")
     torch.cuda.synchronize(dev)
@@ -39,10 +39,11 @@ def test_noalloc_matches_workspace_encode_twice(gpu_device):
     big = synthetic.coder_512x768(seed=3, p_ch=4)           # 1x192x32x48, explicit indexes
     small = synthetic.coder_512x768(seed=4, p_ch=5)          # then 12 channels of it
     cases = [
-        ("1x192x32x48 P=4 explicit indexes", big, big.symbols, big.explicit_indexes(), 192, 4),
-        ("1x12x32x48 P=5 implicit indexes", small, small.symbols[:, :12 * 1536], None, 12, 5),
+        ("1x192x32x48 P=4 explicit indexes", big, big.symbols, big.explicit_indexes(), 192, 4, 1),
+        ("1x12x32x48 P=5 implicit indexes, 2 states per lane", small,
+         small.symbols[:, :12 * 1536], None, 12, 5, 2),
     ]
-    for name, w, sym_np, idx_np, C, P in cases:
+    for name, w, sym_np, idx_np, C, P, I in cases:
         print("case: no-alloc encode", name, flush=True)
         M = C if idx_np is None else w.cdfs.shape[0]
         t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
@@ -50,22 +51,22 @@ def test_noalloc_matches_workspace_encode_twice(gpu_device):
         B, N = sym_np.shape
         sym = t(sym_np)
         idx = None if idx_np is None else t(idx_np)
-        got, status = _noalloc(L, tables, sym, idx, B, N, C, P, dev)
+        got, status = _noalloc(L, tables, sym, idx, B, N, C, P, I, dev)
         assert status == 0
-        ref = gaans.encode(tables, B, N, C, P, dev, symbols=sym, indexes=idx)
+        ref = gaans.encode(tables, B, N, C, P, dev, symbols=sym, indexes=idx, interleave=I)
         assert got == ref.packed.cpu().numpy().tobytes()
         want = oracle.gaans_encode(sym_np, idx_np, w.cdfs[:M], w.cdf_sizes[:M], w.offsets[:M], P,
-                                   channels=C)
+                                   channels=C, interleave=I)
         assert got == want
 
 
 def test_noalloc_rejects_shapes_beyond_its_scratch():
     L = _native.lib()
     B, N, C, P = 64, 192 * 1536, 192, 16  # about 113 MB of workspace
-    lay = _native.layout(B, N, C, P)
+    lay = _native.layout(B, N, C, P, 1)
     assert lay.workspace_bytes + _native.CTRL_BYTES > _native.NOALLOC_SCRATCH_BYTES
     desc = _native.Tables()
-    rc = L.gaans_encode_symbols_noalloc(None, None, None, ctypes.byref(desc), B, N, C, P, None,
+    rc = L.gaans_encode_symbols_noalloc(None, None, None, ctypes.byref(desc), B, N, C, P, 1, None,
                                         0, None)
     assert rc == _native.EINVAL
     msg = _native.last_error()
