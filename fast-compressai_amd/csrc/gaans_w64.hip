@@ -56,8 +56,12 @@ constexpr int kLanes = 64;
 #ifndef GAANS_MAPPERS
 #define GAANS_MAPPERS 4
 #endif
-constexpr int kMappers = GAANS_MAPPERS;  // mapper waves per workgroup
-constexpr int kWaves = kMappers + 1;     // + the coder wave
+constexpr int kMappers = GAANS_MAPPERS;  // mapper waves per decode workgroup
+#ifndef GAANS_ENC_MAPPERS
+#define GAANS_ENC_MAPPERS GAANS_MAPPERS
+#endif
+constexpr int kEncMappers = GAANS_ENC_MAPPERS;  // mapper waves per encode workgroup
+constexpr int kWaves = kEncMappers + 1;  // encoder: + the coder wave
 constexpr int kThreads = kWaves * kLanes;
 constexpr uint32_t kStateLow = 1u << 16;  // rANS L
 constexpr uint32_t kMagic = 0x31574147u;  // "GAW1"
@@ -498,6 +502,32 @@ __device__ __forceinline__ int32_t gauss_index(float s, const float* tab, int L,
   return lb != lb ? L - 1 : pos;
 }
 
+// gauss_index of KP scales at once (in: the scales' bits, out: the
+// indexes): the KP searches advance together, so each round's KP table
+// reads are in flight at the same time.
+template <int KP>
+__device__ __forceinline__ void gauss_indexes(int32_t* io, const float* tab, int L, int pow2,
+                                              float bound) {
+  float lb[KP];
+  int pos[KP];
+#pragma unroll
+  for (int e = 0; e < KP; ++e) {
+    const float s = __int_as_float(io[e]);
+    lb[e] = s < bound ? bound : s;
+    pos[e] = 0;
+  }
+  for (int step = pow2; step > 0; step >>= 1) {
+#pragma unroll
+    for (int e = 0; e < KP; ++e) {
+      const int i = pos[e] + step - 1;
+      const float t = tab[i < L - 2 ? i : L - 2];
+      pos[e] += (pos[e] + step <= L - 1 && t < lb[e]) ? step : 0;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < KP; ++e) io[e] = lb[e] != lb[e] ? L - 1 : pos[e];
+}
+
 // Stage the scale table (L floats) into LDS with the whole workgroup; the
 // caller's next barrier publishes it.
 template <int NT>
@@ -551,7 +581,8 @@ constexpr int kEncRingBytes = 2 * (kRingWords + kLanes);  // + one spare slot pe
 // and the steps between two barriers).
 template <int SB>
 struct EncGeom {
-  static constexpr int kPer = (SB + kMappers - 1) / kMappers;  // steps per mapper wave and block
+  // steps per mapper wave and block
+  static constexpr int kPer = (SB + kEncMappers - 1) / kEncMappers;
   static constexpr int kRecBytes = 2 * SB * kLanes * 16;       // two blocks of op records
   static constexpr int kFlagBytes = 16;  // per block parity: steps with escapes (bit per step)
   // [ring][records][flags][parts]
@@ -650,63 +681,86 @@ __device__ void encode_finish(const EncArgs& a, int tid, uint64_t* sh) {
 // added to znib).  v is computed in 32-bit arithmetic; when sym - offset
 // overflows int32 the sign of sym tells the side and raw = 2 (v - maxv)
 // (wrapped) is exact whenever raw < 2^32, else the symbol is uncodable.
-template <int kMode, bool kImplicit>
-__device__ __forceinline__ uint4 enc_record(const EncArgs& a, const Tabs& tb, bool lds, int lane,
-                                            int t, int len, int32_t start, int32_t in_a,
-                                            int32_t in_b, float in_m, uint32_t& hash,
-                                            uint32_t& status, uint32_t& znib) {
-  const int p = lane + kLanes * t;
-  const bool act = p < len;
-  int32_t tbi = kImplicit ? (int32_t)udiv((uint32_t)(start + p), a.div_hw) : in_b;
-  const bool bad = act & ((uint32_t)tbi >= a.M);
-  const bool ok = act & !bad;
-  status |= bad ? GAANS_ST_INDEX : 0u;
-  tbi = ok ? tbi : (lds ? tb.t_lo : 0);
-  hash += ok ? index_term((uint32_t)p, (uint32_t)tbi) : 0u;
-  int32_t sym;
-  if (kMode != kModeSymbols) {
-    const float r = rintf(__fsub_rn(__int_as_float(in_a), in_m));
-    const bool rng = !(fabsf(r) < 2147483648.0f);
-    status |= (ok & rng) ? GAANS_ST_RANGE : 0u;
-    sym = (int32_t)(rng ? 0.0f : r);
-  } else {
-    sym = in_a;
+//
+// A mapper wave builds the records of its KP steps of a block together
+// (steps t0 + tstep e, e < nvalid; the others are inactive): the table
+// numbers, symbols and index hash of all KP steps first, then their table
+// metadata reads, then their entry reads, so that each kind of LDS (or L2)
+// read is in flight for all KP steps at once rather than one step after the
+// other.
+template <int kMode, bool kImplicit, bool kLds, int KP>
+__device__ __forceinline__ void enc_records(const EncArgs& a, const Tabs& tb, int lane, int t0,
+                                            int tstep, int nvalid, int len, int32_t start,
+                                            const int32_t* in_a, const int32_t* in_b,
+                                            const float* in_m, uint32_t& hash, uint32_t& status,
+                                            uint32_t& znib, uint4* rec) {
+  bool ok[KP];
+  int32_t sym[KP], offset[KP];
+  uint32_t ebase[KP], nsym[KP];
+#pragma unroll
+  for (int e = 0; e < KP; ++e) {
+    const int p = lane + kLanes * (t0 + tstep * e);
+    const bool act = (e < nvalid) & (p < len);
+    int32_t tbi = kImplicit ? (int32_t)udiv((uint32_t)(start + p), a.div_hw) : in_b[e];
+    const bool bad = act & ((uint32_t)tbi >= a.M);
+    ok[e] = act & !bad;
+    status |= bad ? GAANS_ST_INDEX : 0u;
+    tbi = ok[e] ? tbi : (kLds ? tb.t_lo : 0);
+    hash += ok[e] ? index_term((uint32_t)p, (uint32_t)tbi) : 0u;
+    if (kMode != kModeSymbols) {
+      const float r = rintf(__fsub_rn(__int_as_float(in_a[e]), in_m[e]));
+      const bool rng = !(fabsf(r) < 2147483648.0f);
+      status |= (ok[e] & rng) ? GAANS_ST_RANGE : 0u;
+      sym[e] = (int32_t)(rng ? 0.0f : r);
+    } else {
+      sym[e] = in_a[e];
+    }
+    if (kLds) {
+      const uint4 m = tb.lmeta[tbi - tb.t_lo];
+      ebase[e] = m.x;
+      nsym[e] = m.y;
+      offset[e] = (int32_t)m.z;
+    } else {
+      const TabMeta m = tb.gmeta[tbi];
+      ebase[e] = m.ent_base;
+      nsym[e] = m.nsym;
+      offset[e] = m.offset;
+    }
   }
-  uint32_t ebase, nsym;
-  int32_t offset;
-  if (lds) {
-    const uint4 m = tb.lmeta[tbi - tb.t_lo];
-    ebase = m.x;
-    nsym = m.y;
-    offset = (int32_t)m.z;
-  } else {
-    const TabMeta m = tb.gmeta[tbi];
-    ebase = m.ent_base;
-    nsym = m.nsym;
-    offset = m.offset;
+  int32_t v[KP];
+  bool ovf[KP], esc[KP];
+  uint2 ent[KP];
+#pragma unroll
+  for (int e = 0; e < KP; ++e) {
+    v[e] = (int32_t)((uint32_t)sym[e] - (uint32_t)offset[e]);
+    const int32_t maxv = (int32_t)nsym[e] - 1;
+    ovf[e] = ((sym[e] ^ offset[e]) & (sym[e] ^ v[e])) < 0;
+    const bool out = ((uint32_t)v[e] >= (uint32_t)maxv) | ovf[e];
+    esc[e] = ok[e] & out;
+    const uint32_t at = ebase[e] + (uint32_t)(out ? maxv : v[e]);
+    ent[e] = kLds ? tb.lent[at] : tb.gent[at];
   }
-  const int32_t v = (int32_t)((uint32_t)sym - (uint32_t)offset);
-  const int32_t maxv = (int32_t)nsym - 1;
-  const bool ovf = ((sym ^ offset) & (sym ^ v)) < 0;
-  const bool out = ((uint32_t)v >= (uint32_t)maxv) | ovf;
-  const bool esc = ok & out;
-  const int32_t vv = out ? maxv : v;
-  const uint2 e = lds ? tb.lent[ebase + (uint32_t)vv] : tb.gent[ebase + (uint32_t)vv];
-  // escape split
-  const uint32_t d = (uint32_t)v - (uint32_t)maxv;
-  const bool lo = ovf ? (sym < 0) : (v < 0);
-  status |= (ok & ovf & (lo | (d >= 0x80000000u))) ? GAANS_ST_RANGE : 0u;
-  const uint32_t raw = esc ? (lo ? ~((uint32_t)v << 1) : (d << 1)) : 0u;
-  const uint32_t nn = raw ? ((31u - (uint32_t)__clz((int)raw)) >> 2) + 1u : 0u;
-  znib += esc ? nn + 1u : 0u;
-  const uint32_t fr = (e.x >> 16) + 1u;
-  const uint32_t sh = fr >= 2u ? enc_shift(fr) : 0u;
-  uint4 r;
-  r.x = ok ? ((e.x & 0xffffu) | ((65536u - fr) << 16)) : 0u;
-  r.y = ok ? e.y : 1u;
-  r.z = (ok ? sh : 15u) | ((ok & (fr == 1u)) ? 32u : 0u) | (esc ? 256u : 0u);
-  r.w = raw;
-  return r;
+#pragma unroll
+  for (int e = 0; e < KP; ++e) {
+    // escape split
+    const uint32_t d = (uint32_t)v[e] - (nsym[e] - 1u);
+    const bool lo = ovf[e] ? (sym[e] < 0) : (v[e] < 0);
+    status |= (ok[e] & ovf[e] & (lo | (d >= 0x80000000u))) ? GAANS_ST_RANGE : 0u;
+    // raw = esc ? (lo ? ~(v << 1) : d << 1) : 0, as bit selects (no branch)
+    const uint32_t m_lo = 0u - (uint32_t)lo;
+    const uint32_t raw = ((~((uint32_t)v[e] << 1) & m_lo) | ((d << 1) & ~m_lo)) &
+                         (0u - (uint32_t)esc[e]);
+    const uint32_t nn = raw ? ((31u - (uint32_t)__clz((int)raw)) >> 2) + 1u : 0u;
+    znib += esc[e] ? nn + 1u : 0u;
+    const uint32_t fr = (ent[e].x >> 16) + 1u;
+    const uint32_t sh = fr >= 2u ? enc_shift(fr) : 0u;
+    uint4 r;
+    r.x = ok[e] ? ((ent[e].x & 0xffffu) | ((65536u - fr) << 16)) : 0u;
+    r.y = ok[e] ? ent[e].y : 1u;
+    r.z = (ok[e] ? sh : 15u) | ((ok[e] & (fr == 1u)) ? 32u : 0u) | (esc[e] ? 256u : 0u);
+    r.w = raw;
+    rec[e] = r;
+  }
 }
 
 // Encoder LDS ring: kRingWords words + one spare slot per lane, which lanes
@@ -724,10 +778,16 @@ __device__ __forceinline__ void emit_words(bool emit, uint32_t& x, uint16_t* rin
   const uint64_t m = ballot(emit);
   const int c = __popcll(m);
   wp = uni(wp - c);
-  const uint32_t slot =
-      emit ? ((uint32_t)(wp + (int)lane_rank(m)) & (kRingWords - 1)) : (uint32_t)(kRingWords + lane);
+  // Branch-free: the slot and the shift are bit selects on an all-ones /
+  // zero mask that the compiler cannot see through (as a select on `emit`
+  // it becomes an exec-masked block, which keeps the steps of other state
+  // slots from being scheduled in between).
+  uint32_t e = 0u - (uint32_t)emit;
+  asm("" : "+v"(e));  // opaque, but free to schedule
+  const uint32_t pos = (uint32_t)(wp + (int)lane_rank(m)) & (kRingWords - 1);
+  const uint32_t slot = (pos & e) | ((uint32_t)(kRingWords + lane) & ~e);
   ring[slot] = (uint16_t)x;
-  x = emit ? (x >> 16) : x;
+  x >>= (e & 16u);
 }
 
 // main rANS op: x' = ((x / freq) << 16) + x % freq + start = x + start + q (65536 - freq)
@@ -735,6 +795,34 @@ __device__ __forceinline__ uint32_t enc_apply(uint32_t x, uint4 r) {
   const uint32_t q = enc_div(x, r.y, r.z & 31u);
   const uint32_t xn = __umul24(q, r.x >> 16) + (x + (r.x & 0xffffu));
   return (r.z & 32u) ? ((x << 16) + (r.x & 0xffffu)) : xn;
+}
+
+// NI consecutive steps of a full block, step q with state slot q, coded in
+// the encoder's order (q = NI - 1 first): the NI renormalisation tests and
+// ballots first, then the ring writes (the words of later steps go first:
+// groups are prepended), then the NI state updates.  The steps are
+// independent but for the ring cursor, so their work can interleave.  Same
+// results as NI emit_words + enc_apply in that order.
+template <int NI>
+__device__ __forceinline__ void enc_group(const uint4* r, uint32_t* x, uint16_t* ring, int& wp,
+                                          int lane) {
+  uint64_t m[NI];
+  uint32_t e[NI];
+#pragma unroll
+  for (int q = NI - 1; q >= 0; --q) {
+    const bool emit = (x[q] >> 16) >= 65536u - (r[q].x >> 16);
+    m[q] = ballot(emit);
+    e[q] = 0u - (uint32_t)emit;
+    asm("" : "+v"(e[q]));  // bit selects below, not an exec-masked block
+  }
+#pragma unroll
+  for (int q = NI - 1; q >= 0; --q) {
+    wp = uni(wp - __popcll(m[q]));
+    const uint32_t pos = (uint32_t)(wp + (int)lane_rank(m[q])) & (kRingWords - 1);
+    ring[(pos & e[q]) | ((uint32_t)(kRingWords + lane) & ~e[q])] = (uint16_t)x[q];
+  }
+#pragma unroll
+  for (int q = NI - 1; q >= 0; --q) x[q] = enc_apply(x[q] >> (e[q] & 16u), r[q]);
 }
 
 // Escapes of one step into the chunk's escape list: slots are taken from the
@@ -799,14 +887,15 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
     tb.lent = lent;
     tb.llut = nullptr;
     tb.lsub = nullptr;
-    // mapper wave w (1..kMappers) owns steps u = w - 1 + kMappers e of every block
-    int32_t ca[kPer], cb[kPer], na[kPer], nb[kPer];
-    float cm[kPer], nm[kPer];
+    // mapper wave w (1..kEncMappers) owns steps u = w - 1 + kEncMappers e of every block
+    // (steps a wave does not own keep these zeros)
+    int32_t ca[kPer] = {}, cb[kPer] = {}, na[kPer] = {}, nb[kPer] = {};
+    float cm[kPer] = {}, nm[kPer] = {};
     auto load_block = [&](int j, int32_t* ia, int32_t* ib, float* im) {
 #pragma unroll
       for (int e = 0; e < kPer; ++e) {
-        const int u = (wid - 1) + kMappers * e;
-        if (SB % kMappers != 0 && u >= SB) break;
+        const int u = (wid - 1) + kEncMappers * e;
+        if (SB % kEncMappers != 0 && u >= SB) break;
         int p = lane + kLanes * (j * SB + u);
         p = p < len ? p : len - 1;  // loads stay in the chunk; results are masked
         const int64_t i = row + start + p;
@@ -839,35 +928,36 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
                            stage_bounds(tb.gmeta, t_lo, t_hi, a.M, a.blob.total_dense), t_lo,
                            t_hi, tid);
 
+    // this wave's steps per block: u = wid - 1 + kEncMappers e < SB
+    const int nvalid = SB % kEncMappers == 0 ? kPer : (SB - wid + kEncMappers) / kEncMappers;
     auto map_steps = [&](int j, auto lds_tag) {
       constexpr bool kLds = decltype(lds_tag)::value;
       uint4* dst = recs + (j & 1) * SB * kLanes;
+      uint4 r[kPer];
+      enc_records<kMode, kImplicit, kLds, kPer>(a, tb, lane, j * SB + wid - 1, kEncMappers,
+                                                nvalid, len, start, ca, cb, cm, hash, status,
+                                                znib, r);
+      uint32_t eb = 0;  // steps of the block with escapes
 #pragma unroll
       for (int e = 0; e < kPer; ++e) {
-        const int u = (wid - 1) + kMappers * e;
-        if (SB % kMappers != 0 && u >= SB) break;
-        const uint4 r = enc_record<kMode, kImplicit>(a, tb, kLds, lane, j * SB + u, len, start,
-                                                     ca[e], cb[e], cm[e], hash, status, znib);
-        dst[u * kLanes + lane] = r;
-        if (ballot((r.z & 256u) != 0u) != 0ull && lane == 0)
-          __hip_atomic_fetch_or(&eflag[j & 1], 1u << u, __ATOMIC_RELAXED,
-                                __HIP_MEMORY_SCOPE_WORKGROUP);
+        const int u = (wid - 1) + kEncMappers * e;
+        if (SB % kEncMappers != 0 && u >= SB) break;
+        dst[u * kLanes + lane] = r[e];
+        eb |= ballot((r[e].z & 256u) != 0u) != 0ull ? 1u << u : 0u;
       }
+      if (eb != 0u && lane == 0)
+        __hip_atomic_fetch_or(&eflag[j & 1], eb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     };
     auto map_block = [&](int j) {
-      if (kMode == kModeGaussian) {
-#pragma unroll
-        for (int e = 0; e < kPer; ++e)
-          cb[e] = gauss_index(__int_as_float(cb[e]), scl, a.n_scales, a.scales_pow2,
-                              a.scale_bound);
-      }
+      if (kMode == kModeGaussian)
+        gauss_indexes<kPer>(cb, scl, a.n_scales, a.scales_pow2, a.scale_bound);
       // LDS tables for the whole block when every active lane's table is staged
       bool lds = tb.nt > 0;
       if (!kImplicit && lds) {
         bool outside = false;
 #pragma unroll
         for (int e = 0; e < kPer; ++e) {
-          const int u = (wid - 1) + kMappers * e;
+          const int u = (wid - 1) + kEncMappers * e;
           outside |= u < SB && lane + kLanes * (j * SB + u) < len &&
                      (uint32_t)(cb[e] - tb.t_lo) >= (uint32_t)tb.nt;
         }
@@ -896,19 +986,17 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
         const bool full = (j + 1) * SB <= T;
         // the block's records in groups of at most 8 steps, last group first
         constexpr int H = SB > 8 ? 8 : SB;
+        static_assert(H % NI == 0, "groups of NI steps tile a group of records");
 #pragma unroll
         for (int h = SB / H - 1; h >= 0; --h) {
           uint4 r[H];
 #pragma unroll
           for (int k = 0; k < H; ++k) r[k] = src[(h * H + k) * kLanes + lane];
           if (full) {
-            // common case: a full block, no per-step branches
+            // common case: a full block, no per-step branches; NI steps at a
+            // time (H is a multiple of NI, so step h H + k0 + q uses slot q)
 #pragma unroll
-            for (int k = H - 1; k >= 0; --k) {
-              uint32_t& xs = x[(h * H + k) % NI];
-              emit_words((xs >> 16) >= 65536u - (r[k].x >> 16), xs, ring, wp, lane);
-              xs = enc_apply(xs, r[k]);
-            }
+            for (int k0 = H - NI; k0 >= 0; k0 -= NI) enc_group<NI>(r + k0, x, ring, wp, lane);
           } else {
 #pragma unroll
             for (int k = H - 1; k >= 0; --k) {
@@ -1549,6 +1637,74 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint2 r, uint
   return (uint32_t)(oob ? 0 : o);
 }
 
+// NI consecutive steps of a full block (every lane active, tables in LDS,
+// offsets that cannot overflow), step q with state slot q: the NI lookups
+// are issued together, dense buckets are resolved for the whole group with
+// one uniform branch per level, and after the state updates the NI refills
+// read their words together (step q's words follow those of the steps
+// before it).  So the group waits for each kind of LDS read once instead of
+// once per step.  Same results as NI calls of dec_step<true, true, SB>.
+template <int NI, int SB>
+__device__ __forceinline__ void dec_group(const Tabs& tb, const uint2* r, uint32_t* x, Stream& S,
+                                          const uint16_t* ring, uint64_t* em, uint32_t* ov,
+                                          int lane) {
+  uint64_t e[NI];
+  uint32_t cum[NI];
+#pragma unroll
+  for (int q = 0; q < NI; ++q) {
+    cum[q] = x[q] & 0xffffu;
+    e[q] = tb.llut[((r[q].x & 0xffffu) << kLutBits) + (cum[q] >> (16 - kLutBits))];
+  }
+  bool d = false;
+#pragma unroll
+  for (int q = 0; q < NI; ++q) d |= dense_entry(e[q]);
+  const uint64_t dm = ballot(d);
+  asm volatile("" ::"s"(dm));
+  if (__builtin_expect(dm != 0ull, 0)) {
+#pragma unroll
+    for (int q = 0; q < NI; ++q)
+      if (dense_entry(e[q])) e[q] = sub_entry<true>(tb, e[q], (cum[q] >> kSubBits) & (kSubSize - 1));
+    bool d3 = false;
+#pragma unroll
+    for (int q = 0; q < NI; ++q) d3 |= dense_entry(e[q]);
+    if (__builtin_expect(ballot(d3) != 0ull, 0)) {
+#pragma unroll
+      for (int q = 0; q < NI; ++q)
+        if (dense_entry(e[q])) e[q] = sub_entry<true>(tb, e[q], cum[q] & (kSubSize - 1));
+    }
+  }
+  uint64_t m[NI];
+  uint32_t s[NI];
+#pragma unroll
+  for (int q = 0; q < NI; ++q) {
+    const uint32_t lo = (uint32_t)e[q], hi = (uint32_t)(e[q] >> 32);
+    const uint32_t s0 = hi & 0xffffu, nxt = hi >> 16;
+    const uint32_t st0 = lo & 0xffffu, st1 = (lo >> 16) + 1u;
+    const bool up = cum[q] >= st1;
+    s[q] = up ? s0 + 1u : s0;
+    const uint32_t st = up ? st1 : st0;
+    const uint32_t fr = up ? nxt + 1u : st1 - st0;
+    x[q] = __umul24(fr, x[q] >> 16) + cum[q] - st;
+    m[q] = ballot(x[q] < kStateLow);
+  }
+  int pos = S.rp;
+  uint32_t w[NI];
+#pragma unroll
+  for (int q = 0; q < NI; ++q) {
+    w[q] = ring[(pos + (int)lane_rank(m[q])) & (DecGeom<SB>::kRing - 1)];
+    pos += __popcll(m[q]);
+  }
+  S.rp = pos;
+#pragma unroll
+  for (int q = 0; q < NI; ++q) {
+    const bool need = (m[q] >> lane) & 1ull;
+    const uint32_t keep = need ? 0xffffu : 0u;
+    x[q] = (x[q] << (need ? 16 : 0)) | (w[q] & keep);
+    em[q] = ballot(s[q] == (r[q].x >> 16));
+    ov[q] = s[q] + r[q].y;
+  }
+}
+
 template <int kMode, bool kImplicit, int SB, bool kSearch, int NI>
 __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   static_assert(SB % NI == 0, "a block holds whole rounds of the state slots");
@@ -1809,12 +1965,18 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
           // common case: every lane of the block active, LDS tables, no
           // per-step branches
           uint64_t em[SB];
+          if constexpr (kSearch) {
 #pragma unroll
-          for (int u = 0; u < SB; ++u) {
-            ov[u] = dec_step<true, true, SB, kSearch>(tb, r[u], x[u % NI], S, sring, em[u],
-                                                      status, lane);
-            any_em |= em[u];
+            for (int u = 0; u < SB; ++u)
+              ov[u] = dec_step<true, true, SB, kSearch>(tb, r[u], x[u % NI], S, sring, em[u],
+                                                        status, lane);
+          } else {
+#pragma unroll
+            for (int u = 0; u < SB; u += NI)
+              dec_group<NI, SB>(tb, r + u, x, S, sring, em + u, ov + u, lane);
           }
+#pragma unroll
+          for (int u = 0; u < SB; ++u) any_em |= em[u];
           if (__builtin_expect(any_em != 0ull, 0)) {
 #pragma unroll
             for (int u = 0; u < SB; ++u) {
