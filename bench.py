@@ -52,8 +52,8 @@ def parse():
                          "print their event times; 'copy' runs one device copy of --copy-probe "
                          "MiB.  For rocprofv3 counter runs.")
     ap.add_argument("--reps", type=int, default=10)
-    ap.add_argument("--interleave", type=int, default=None, choices=(1, 2, 4),
-                    help="rANS states per lane for --kernels (default: the coder's choice)")
+    ap.add_argument("--segments", type=int, default=None,
+                    help="coding units per chunk for --kernels (default: the coder's choice)")
     return ap.parse_args()
 
 
@@ -91,20 +91,20 @@ def read_traffic(workload: str, kernel_key: str):
     return None
 
 
-def kernel_times(L, _native, torch, backend, w, dev, reps=40, interleave=None):
+def kernel_times(L, _native, torch, backend, w, dev, reps=40, segments=None):
     """Event-timed encode / decode kernels of one workload (median over
     batches of back-to-back launches, seconds per launch), the payload size
-    and the interleave used (the coder's choice unless one is given)."""
+    and the segments per chunk used (the coder's choice unless one is given)."""
     import statistics
 
     B, N, C, P = w.batch, w.n, w.channels, w.p_ch
     sym = torch.from_numpy(w.symbols).to(dev)
     idx = torch.from_numpy(w.explicit_indexes()).to(dev)
     cdfs, sizes, offs = (torch.from_numpy(a).to(dev) for a in (w.cdfs, w.cdf_sizes, w.offsets))
-    payload = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=P, interleave=interleave)
-    I = payload.interleave
+    payload = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=P, segments=segments)
+    S = payload.segments
     tables = backend.prepared_tables(cdfs, sizes, offs)
-    lay = _native.layout(B, N, C, P, I)
+    lay = _native.layout(B, N, C, P, S)
     ws = torch.empty(int(lay.workspace_bytes), dtype=torch.uint8, device=dev)
     ctrl = torch.zeros(_native.CTRL_BYTES, dtype=torch.uint8, device=dev)
     info = torch.zeros(4, dtype=torch.int64, device=dev)
@@ -115,13 +115,13 @@ def kernel_times(L, _native, torch, backend, w, dev, reps=40, interleave=None):
 
     def enc():
         _native.check(L.gaans_encode_symbols(sp, sym.data_ptr(), idx.data_ptr(), tables.ref, B, N,
-                                             C, P, I, ws.data_ptr(), ws.numel(), ctrl.data_ptr(),
+                                             C, P, S, ws.data_ptr(), ws.numel(), ctrl.data_ptr(),
                                              info.data_ptr()), "encode")
 
     def dec():
         _native.check(L.gaans_decode_symbols(sp, payload.packed.data_ptr(),
                                              payload.packed.numel(), idx.data_ptr(), tables.ref,
-                                             B, N, C, P, I, out.data_ptr(), ctrl.data_ptr(),
+                                             B, N, C, P, S, out.data_ptr(), ctrl.data_ptr(),
                                              status.data_ptr()), "decode")
 
     res = {}
@@ -141,10 +141,10 @@ def kernel_times(L, _native, torch, backend, w, dev, reps=40, interleave=None):
         res[name] = statistics.median(ts)
     torch.cuda.synchronize()
     assert int(status[0].item()) == 0 and torch.equal(out, sym)
-    return res, int(payload.packed.numel()), I
+    return res, int(payload.packed.numel()), S
 
 
-def gaussian_kernel_times(L, _native, torch, p_ch, dev, reps=40, interleave=1):
+def gaussian_kernel_times(L, _native, torch, p_ch, dev, reps=40, segments=None):
     """Event-timed fused GaussianConditional kernels (gaans_encode_gaussian /
     gaans_decode_gaussian) on the mean-scale hyperprior y 1x192x32x48: fp32
     y, means and scales in, index search and quantize in the kernel; decode
@@ -165,10 +165,10 @@ def gaussian_kernel_times(L, _native, torch, p_ch, dev, reps=40, interleave=1):
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
     y, means, scales, table = t(y_np), t(means_np), t(table_np[idx_np]), t(table_np)
     tables = prepare_tables(t(yw.cdfs), t(yw.cdf_sizes), t(yw.offsets))
-    I = gaans.resolve_interleave(interleave, tables, B, N, C, P)
+    S = gaans.resolve_segments(segments, tables, B, N, C, P, dev)
     enc = gaans.encode_gaussian(tables, B, N, C, P, dev, y=y, scales=scales, scale_table=table,
-                                scale_bound=0.11, means=means, interleave=I)
-    lay = _native.layout(B, N, C, P, I)
+                                scale_bound=0.11, means=means, segments=S)
+    lay = _native.layout(B, N, C, P, S)
     ws = torch.empty(int(lay.workspace_bytes), dtype=torch.uint8, device=dev)
     ctrl = torch.zeros(_native.CTRL_BYTES, dtype=torch.uint8, device=dev)
     info = torch.zeros(4, dtype=torch.int64, device=dev)
@@ -180,14 +180,14 @@ def gaussian_kernel_times(L, _native, torch, p_ch, dev, reps=40, interleave=1):
     def encode():
         _native.check(L.gaans_encode_gaussian(sp, y.data_ptr(), means.data_ptr(), scales.data_ptr(),
                                               table.data_ptr(), 64, 0.11, tables.ref, B, N, C, P,
-                                              I, ws.data_ptr(), ws.numel(), ctrl.data_ptr(),
+                                              S, ws.data_ptr(), ws.numel(), ctrl.data_ptr(),
                                               info.data_ptr()), "encode")
 
     def decode():
         _native.check(L.gaans_decode_gaussian(sp, enc.packed.data_ptr(), enc.packed.numel(),
                                               scales.data_ptr(), means.data_ptr(),
                                               table.data_ptr(), 64, 0.11, tables.ref, B, N, C, P,
-                                              I, out.data_ptr(), ctrl.data_ptr(),
+                                              S, out.data_ptr(), ctrl.data_ptr(),
                                               status.data_ptr()), "decode")
 
     res = {}
@@ -208,7 +208,7 @@ def gaussian_kernel_times(L, _native, torch, p_ch, dev, reps=40, interleave=1):
     torch.cuda.synchronize()
     want = torch.from_numpy(yw.symbols).to(dev).float() + means
     assert int(status[0].item()) == 0 and torch.equal(out, want)
-    return res, int(enc.packed.numel()), B * N, yw.raw_rgb_bytes, I
+    return res, int(enc.packed.numel()), B * N, yw.raw_rgb_bytes, S
 
 
 def balle_factorized(torch, synthetic, device, seed=0):
@@ -400,16 +400,16 @@ def kernels_only(args):
     L = _native.lib()
     reps = max(5, args.reps // 5 * 5)
     if args.kernels.startswith("hyperprior_y_p"):
-        kt, pb, n_sym, _, I = gaussian_kernel_times(L, _native, torch, int(args.kernels[14:]),
-                                                    dev, reps=reps, interleave=args.interleave)
+        kt, pb, n_sym, _, S = gaussian_kernel_times(L, _native, torch, int(args.kernels[14:]),
+                                                    dev, reps=reps, segments=args.segments)
         alg = 12 * n_sym + pb
     else:
         w = _kernel_workloads()[args.kernels]()
-        kt, pb, I = kernel_times(L, _native, torch, WarpDivBackend(), w, dev, reps=reps,
-                                 interleave=args.interleave)
+        kt, pb, S = kernel_times(L, _native, torch, WarpDivBackend(), w, dev, reps=reps,
+                                 segments=args.segments)
         n_sym = w.batch * w.n
         alg = 8 * n_sym + pb
-    print(json.dumps({"kernels": args.kernels, "interleave": I, "symbols": n_sym,
+    print(json.dumps({"kernels": args.kernels, "segments": S, "symbols": n_sym,
                       "payload_bytes": pb,
                       "alg_bytes_per_launch": alg,
                       "encode_us": round(kt["encode"] * 1e6, 2),
@@ -478,8 +478,8 @@ def main():
     # ---- kernel time with HIP events on the launch stream -----------------
     L = _native.lib()
     tables = backend.prepared_tables(cdfs, sizes, offs)
-    I = payload.interleave
-    lay = _native.layout(B, N, C, P, I)
+    S = payload.segments
+    lay = _native.layout(B, N, C, P, S)
     ws = torch.empty(int(lay.workspace_bytes), dtype=torch.uint8, device=dev)
     ctrl = torch.zeros(_native.CTRL_BYTES, dtype=torch.uint8, device=dev)
     info = torch.zeros(4, dtype=torch.int64, device=dev)
@@ -510,12 +510,12 @@ def main():
     def launch_decode():
         _native.check(L.gaans_decode_symbols(stream.cuda_stream, payload.packed.data_ptr(),
                                              payload_bytes, idx.data_ptr(), tables.ref, B, N, C,
-                                             P, I, out.data_ptr(), ctrl.data_ptr(),
+                                             P, S, out.data_ptr(), ctrl.data_ptr(),
                                              status.data_ptr()), "decode")
 
     def launch_encode():
         _native.check(L.gaans_encode_symbols(stream.cuda_stream, sym.data_ptr(), idx.data_ptr(),
-                                             tables.ref, B, N, C, P, I, ws.data_ptr(), ws.numel(),
+                                             tables.ref, B, N, C, P, S, ws.data_ptr(), ws.numel(),
                                              ctrl.data_ptr(), info.data_ptr()), "encode")
 
     dec_med, dec_avg = event_time(launch_decode)
@@ -527,9 +527,9 @@ def main():
     # algorithmic bytes per launch: symbols + indexes (int32) + payload
     alg_bytes = 4 * B * N + 4 * B * N + payload_bytes
     if dec_avg >= enc_avg:
-        kernel, key, dur = f"k_decode<0,false,16,false,{I}> (gaans_decode_symbols)", "k_decode", dec_avg
+        kernel, key, dur = "k_decode<0,false,16,false> (gaans_decode_symbols)", "k_decode", dec_avg
     else:
-        kernel, key, dur = f"k_encode<0,false,8,{I}> (gaans_encode_symbols)", "k_encode", enc_avg
+        kernel, key, dur = "k_encode<0,false,8> (gaans_encode_symbols)", "k_encode", enc_avg
     achieved = alg_bytes / dur / 1e9
     traffic = read_traffic("coder_512x768_p4", key)
 
@@ -553,7 +553,7 @@ def main():
             n_sym = wl.batch * wl.n
             alg = 8 * n_sym + pb  # symbols + indexes (int32) + payload, either direction
             extra[label] = {
-                "symbols": n_sym, "payload_bytes": pb, "interleave": wl_i,
+                "symbols": n_sym, "payload_bytes": pb, "segments": wl_i,
                 "alg_bytes_per_launch": alg,
                 **counter_traffic(label, alg),
                 "encode_hbm_frac": round(alg / kt["encode"] / 1e9 / HBM_PEAK_GBPS, 4),

@@ -1,16 +1,17 @@
 // GA-ANS wave64 latent coder for MI355X (gfx950): HIP kernels + C ABI.
 //
-// Format: one chunk = P latent channels; 64 lanes, I = 1, 2 or 4 interleaved
-// 32-bit rANS states per lane (x in [2^16, 2^32), 16-bit renormalisation
-// words, 16-bit CDF precision); lane l owns positions l + 64 t of the chunk
-// and codes step t with its state slot t mod I, so I consecutive steps are
-// independent chains.  The words a step emits are ordered by lane (wave
-// ballot + mbcnt prefix); the decoder hands refill words out in the same
-// order.  The bytes are defined by the CPU oracle (oracle/gaans_oracle.c).
+// Format: one chunk = P latent channels, split into S segments of whole
+// 64-position steps; a segment is a coding unit with 64 lanes and one 32-bit
+// rANS state per lane (x in [2^16, 2^32), 16-bit renormalisation words,
+// 16-bit CDF precision); lane l owns positions l + 64 t of the unit.  The
+// words a step emits are ordered by lane (wave ballot + mbcnt prefix); the
+// decoder hands refill words out in the same order.  The bytes are defined
+// by the CPU oracle (oracle/gaans_oracle.c).
 //
-// Work mapping: one workgroup per chunk (a coder wave and kMappers mapper
-// waves, 320 threads, for encode; one more wave, the escape reader, for
-// decode).
+// Work mapping: one workgroup per coding unit (a coder wave and mapper
+// waves for encode; one more wave, the escape reader, for decode).  A chunk's
+// S units run on S CUs, so S > 1 puts a launch of few long chunks on more of
+// the chip.
 //  - Wave 0 is the coder: it owns the 64 lane states and runs only the
 //    serial part of every step (renormalisation, ballot compaction, state
 //    update).
@@ -43,8 +44,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
-
 #include <string>
 #include <type_traits>
 
@@ -65,7 +66,8 @@ constexpr int kWaves = kEncMappers + 1;  // encoder: + the coder wave
 constexpr int kThreads = kWaves * kLanes;
 constexpr uint32_t kStateLow = 1u << 16;  // rANS L
 constexpr uint32_t kMagic = 0x31574147u;  // "GAW1"
-constexpr uint32_t kVersion = 3u;
+constexpr uint32_t kVersion = 4u;
+constexpr int kMaxSegments = 256;  // segments per chunk
 constexpr uint32_t kParams = 0x00041040u;  // lanes 64 | precision 16 << 8 | bypass 4 << 16
 constexpr int kFixedWords = 16;
 constexpr uint32_t kTabMagic = 0x35425447u;  // "GTB5"
@@ -211,47 +213,61 @@ __host__ __device__ __forceinline__ uint32_t index_term(uint32_t p, uint32_t tb)
   return h;
 }
 
+// Chunks and coding units.  Chunk k of a row covers the positions
+// [k chunk_len, min((k + 1) chunk_len, N)) (P channels), Tc steps of 64
+// positions; it is split into S segments, segment s holding the steps
+// [floor(s Tc / S), floor((s + 1) Tc / S)).  A segment is a coding unit, coded
+// independently (own states, stream and escape section) by its own
+// workgroup: unit g = (b K + k) S + s, U = B K S units.
 struct Layout {
-  int64_t B, N, C, P, I, HW, K, chunk_len, BK, header_bytes, max_payload, cap_words, ws_bytes;
+  int64_t B, N, C, P, S, HW, K, chunk_len, U, seg_cap, header_bytes, max_payload, cap_words,
+      ws_bytes;
   int64_t o_words_cnt, o_status, o_hash, o_end, o_info, o_states, o_words, o_esc, o_esc_raw;
 };
 
-int make_layout(int64_t B, int64_t N, int64_t C, int64_t P, int64_t I, Layout* L) {
+int make_layout(int64_t B, int64_t N, int64_t C, int64_t P, int64_t S, Layout* L) {
   if (B < 1 || N < 1 || C < 1 || P < 1)
     return fail(GAANS_EINVAL, "B, N, C and P must be >= 1 (got %lld, %lld, %lld, %lld)",
                 (long long)B, (long long)N, (long long)C, (long long)P);
-  if (I != 1 && I != 2 && I != 4)
-    return fail(GAANS_EINVAL, "interleave must be 1, 2 or 4 states per lane (got %lld)",
-                (long long)I);
   if (N % C != 0)
     return fail(GAANS_EINVAL, "symbols per row N=%lld is not a multiple of channels C=%lld",
                 (long long)N, (long long)C);
   if (P > C) return fail(GAANS_EINVAL, "P=%lld exceeds channels C=%lld", (long long)P, (long long)C);
   if (N >= ((int64_t)1 << 31) || B >= ((int64_t)1 << 31))
     return fail(GAANS_EINVAL, "B and N must be < 2^31");
-  L->B = B; L->N = N; L->C = C; L->P = P; L->I = I;
+  L->B = B; L->N = N; L->C = C; L->P = P; L->S = S;
   L->HW = N / C;
   L->K = (C + P - 1) / P;
   L->chunk_len = P * L->HW;
-  L->BK = B * L->K;
-  if (L->BK >= ((int64_t)1 << 31)) return fail(GAANS_EINVAL, "too many chunks");
+  // every segment holds at least one step: S <= the steps of the last
+  // (shortest) chunk of a row
+  const int64_t t_last = (N - (L->K - 1) * L->chunk_len + kLanes - 1) / kLanes;
+  if (S < 1 || S > kMaxSegments || S > t_last)
+    return fail(GAANS_EINVAL,
+                "segments per chunk must be in [1, %lld] for this shape (got %lld)",
+                (long long)(t_last < kMaxSegments ? t_last : kMaxSegments), (long long)S);
+  L->U = B * L->K * S;
+  if (L->U >= ((int64_t)1 << 31)) return fail(GAANS_EINVAL, "too many coding units");
   if ((int64_t)kMaxEscNibbles * L->chunk_len + 8 >= ((int64_t)1 << 31))
     return fail(GAANS_EINVAL, "chunk of %lld symbols is too large", (long long)L->chunk_len);
-  L->header_bytes = align_up(4 * kFixedWords + 8 * L->BK, 16);
-  // per symbol at most one stream word and 9 escape nibbles; per chunk the
+  // the longest unit: ceil(Tc / S) steps of the longest chunk
+  const int64_t tc = (L->chunk_len + kLanes - 1) / kLanes;
+  L->seg_cap = std::min<int64_t>(L->chunk_len, kLanes * ((tc + S - 1) / S));
+  L->header_bytes = align_up(4 * kFixedWords + 8 * L->U, 16);
+  // per symbol at most one stream word and 9 escape nibbles; per unit the
   // states, a pad word and a partly used escape word
-  L->max_payload = L->header_bytes + B * N * 7 + L->BK * (4 * kLanes * I + 8);
-  L->cap_words = align_up(L->chunk_len + 2, 2);
+  L->max_payload = L->header_bytes + B * N * 7 + L->U * (4 * kLanes + 8);
+  L->cap_words = align_up(L->seg_cap + 2, 2);
   int64_t o = 0;
-  L->o_words_cnt = o; o = align_up(o + 4 * L->BK, 256);
-  L->o_status = o;    o = align_up(o + 4 * L->BK, 256);
-  L->o_hash = o;      o = align_up(o + 4 * L->BK, 256);
-  L->o_end = o;       o = align_up(o + 4 * L->BK, 256);
+  L->o_words_cnt = o; o = align_up(o + 4 * L->U, 256);
+  L->o_status = o;    o = align_up(o + 4 * L->U, 256);
+  L->o_hash = o;      o = align_up(o + 4 * L->U, 256);
+  L->o_end = o;       o = align_up(o + 4 * L->U, 256);
   L->o_info = o;      o = align_up(o + 32, 256);
-  L->o_states = o;    o = align_up(o + 4 * kLanes * I * L->BK, 256);
-  L->o_words = o;     o = align_up(o + 2 * L->cap_words * L->BK, 256);
-  L->o_esc = o;       o = align_up(o + 8 * L->BK, 256);
-  L->o_esc_raw = o;   o = align_up(o + 4 * L->chunk_len * L->BK, 256);
+  L->o_states = o;    o = align_up(o + 4 * kLanes * L->U, 256);
+  L->o_words = o;     o = align_up(o + 2 * L->cap_words * L->U, 256);
+  L->o_esc = o;       o = align_up(o + 8 * L->U, 256);
+  L->o_esc_raw = o;   o = align_up(o + 4 * L->seg_cap * L->U, 256);
   L->ws_bytes = o;
   return GAANS_OK;
 }
@@ -312,21 +328,33 @@ __device__ __forceinline__ TabHdr load_tab_hdr(const uint8_t* tables) {
   return *reinterpret_cast<const TabHdr*>(tables);
 }
 
-__device__ __forceinline__ int chunk_len_of(int64_t g, int32_t K, int32_t chunk_len, int64_t N) {
-  const int64_t k = g % K;
-  const int64_t s = k * chunk_len;
-  const int64_t e = s + chunk_len < N ? s + chunk_len : N;
-  return (int)(e - s);
+// Coding unit g = (b K + k) S + s (see Layout): row offset b N, first
+// position in the row, symbol count, and chunk k.
+__host__ __device__ __forceinline__ void unit_range(int64_t g, int32_t K, int32_t S, int64_t N,
+                                                    int32_t chunk_len, int64_t& row,
+                                                    int32_t& start, int& len, int& k) {
+  const int64_t per_row = (int64_t)K * S;
+  const int64_t b = g / per_row;
+  const int32_t r = (int32_t)(g - b * per_row);
+  k = r / S;
+  const int32_t s = r - k * S;
+  row = b * N;
+  const int32_t cs = k * chunk_len;
+  const int32_t ce = (int64_t)cs + chunk_len < N ? cs + chunk_len : (int32_t)N;
+  const int32_t tc = (ce - cs + kLanes - 1) / kLanes;
+  const int32_t t0 = (int32_t)((int64_t)s * tc / S), t1 = (int32_t)((int64_t)(s + 1) * tc / S);
+  start = cs + kLanes * t0;
+  const int32_t e = cs + kLanes * t1 < ce ? cs + kLanes * t1 : ce;
+  len = e - start;
 }
 
-__device__ __forceinline__ void chunk_range(int64_t g, int64_t K, int64_t N, int32_t chunk_len,
-                                            int64_t& row, int32_t& start, int& len, int& k) {
-  const int64_t b = g / K;
-  k = (int)(g - b * K);
-  row = b * N;
-  start = k * chunk_len;
-  const int32_t endp = (int64_t)start + chunk_len < N ? start + chunk_len : (int32_t)N;
-  len = endp - start;
+__host__ __device__ __forceinline__ int unit_len(int64_t g, int32_t K, int32_t S, int64_t N,
+                                                 int32_t chunk_len) {
+  int64_t row;
+  int32_t start;
+  int len, k;
+  unit_range(g, K, S, N, chunk_len, row, start, len, k);
+  return len;
 }
 
 // Tables of one chunk: a staged range [t_lo, t_lo + nt) in LDS, the rest in
@@ -556,10 +584,11 @@ struct EncArgs {
   BlobRef blob;
   int64_t N;
   int32_t K, P, C, chunk_len;
-  int32_t I;  // interleave: state slots per lane
+  int32_t S;        // segments per chunk
+  int32_t seg_cap;  // most symbols of a unit (escape list slots per unit)
   UDiv div_hw;
   int32_t cap_words;
-  int64_t BK, header_bytes;
+  int64_t units, header_bytes;  // coding units (B K S)
   int32_t nt_cap, stage_all;
   uint32_t* __restrict__ chunk_words;
   uint32_t* __restrict__ chunk_status;
@@ -568,8 +597,8 @@ struct EncArgs {
   uint64_t* __restrict__ ws_info;
   uint32_t* __restrict__ states;
   uint16_t* __restrict__ words;
-  uint2* __restrict__ esc;          // per chunk: escape count, escape nibbles
-  uint32_t* __restrict__ esc_raw;   // per chunk: chunk_len slots, filled from the end
+  uint2* __restrict__ esc;          // per unit: escape count, escape nibbles
+  uint32_t* __restrict__ esc_raw;   // per unit: seg_cap slots, filled from the end
   uint32_t* __restrict__ ctrl;
   uint64_t* __restrict__ info_out;
 };
@@ -593,17 +622,10 @@ int enc_fixed_lds(int sb) {
   return sb >= 16 ? EncGeom<16>::kFixed : (sb >= 8 ? EncGeom<8>::kFixed : EncGeom<4>::kFixed);
 }
 
-// State slots a chunk of len symbols flushes: min(I, T) of its A lanes.
-__host__ __device__ __forceinline__ int slots_used(int len, int I) {
-  const int T = (len + kLanes - 1) / kLanes;
-  return T < I ? T : I;
-}
-
-// Payload bytes of chunk g: states, stream and escape words, pad.
-__device__ __forceinline__ uint64_t chunk_bytes(const EncArgs& a, int64_t g) {
-  const int len = chunk_len_of(g, a.K, a.chunk_len, a.N);
-  const uint32_t A = (len < kLanes ? (uint32_t)len : (uint32_t)kLanes) *
-                     (uint32_t)slots_used(len, a.I);
+// Payload bytes of unit g: states, stream and escape words, pad.
+__device__ __forceinline__ uint64_t unit_bytes(const EncArgs& a, int64_t g) {
+  const int len = unit_len(g, a.K, a.S, a.N, a.chunk_len);
+  const uint32_t A = len < kLanes ? (uint32_t)len : (uint32_t)kLanes;
   const uint32_t W = __hip_atomic_load(&a.chunk_words[g], __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
   const uint32_t Z = __hip_atomic_load(&a.esc[g].y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -611,8 +633,8 @@ __device__ __forceinline__ uint64_t chunk_bytes(const EncArgs& a, int64_t g) {
   return 4ull * A + 2ull * (U + (U & 1u));
 }
 
-// Last workgroup of an encode launch (all waves): chunk end offsets, payload
-// size and status.  The chunks are scanned kThreads at a time, one per
+// Last workgroup of an encode launch (all waves): unit end offsets, payload
+// size and status.  The units are scanned kThreads at a time, one per
 // thread, with the next tile's loads issued before the current tile's scan.
 // The completion word carries size and status in one 64-bit store, so the
 // host can read it as soon as it lands (no system-wide cache write-back).
@@ -621,15 +643,15 @@ __device__ void encode_finish(const EncArgs& a, int tid, uint64_t* sh) {
   uint64_t carry = 0;
   uint32_t st = 0;
   uint64_t v = 0;
-  if (tid < a.BK) {
-    v = chunk_bytes(a, tid);
+  if (tid < a.units) {
+    v = unit_bytes(a, tid);
     st |= __hip_atomic_load(&a.chunk_status[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  for (int64_t base = 0; base < a.BK; base += kThreads) {
+  for (int64_t base = 0; base < a.units; base += kThreads) {
     const int64_t g = base + tid;
     uint64_t vn = 0;
-    if (g + kThreads < a.BK) {
-      vn = chunk_bytes(a, g + kThreads);
+    if (g + kThreads < a.units) {
+      vn = unit_bytes(a, g + kThreads);
       st |= __hip_atomic_load(&a.chunk_status[g + kThreads], __ATOMIC_RELAXED,
                               __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -643,7 +665,7 @@ __device__ void encode_finish(const EncArgs& a, int tid, uint64_t* sh) {
     }
     __syncthreads();
     incl += before + carry;
-    if (g < a.BK) {
+    if (g < a.units) {
       a.end_off[g] = (uint32_t)incl;
       if (incl > 0xffffffffull) st |= GAANS_ST_SIZE;
     }
@@ -780,8 +802,7 @@ __device__ __forceinline__ void emit_words(bool emit, uint32_t& x, uint16_t* rin
   wp = uni(wp - c);
   // Branch-free: the slot and the shift are bit selects on an all-ones /
   // zero mask that the compiler cannot see through (as a select on `emit`
-  // it becomes an exec-masked block, which keeps the steps of other state
-  // slots from being scheduled in between).
+  // it becomes an exec-masked block).
   uint32_t e = 0u - (uint32_t)emit;
   asm("" : "+v"(e));  // opaque, but free to schedule
   const uint32_t pos = (uint32_t)(wp + (int)lane_rank(m)) & (kRingWords - 1);
@@ -797,35 +818,7 @@ __device__ __forceinline__ uint32_t enc_apply(uint32_t x, uint4 r) {
   return (r.z & 32u) ? ((x << 16) + (r.x & 0xffffu)) : xn;
 }
 
-// NI consecutive steps of a full block, step q with state slot q, coded in
-// the encoder's order (q = NI - 1 first): the NI renormalisation tests and
-// ballots first, then the ring writes (the words of later steps go first:
-// groups are prepended), then the NI state updates.  The steps are
-// independent but for the ring cursor, so their work can interleave.  Same
-// results as NI emit_words + enc_apply in that order.
-template <int NI>
-__device__ __forceinline__ void enc_group(const uint4* r, uint32_t* x, uint16_t* ring, int& wp,
-                                          int lane) {
-  uint64_t m[NI];
-  uint32_t e[NI];
-#pragma unroll
-  for (int q = NI - 1; q >= 0; --q) {
-    const bool emit = (x[q] >> 16) >= 65536u - (r[q].x >> 16);
-    m[q] = ballot(emit);
-    e[q] = 0u - (uint32_t)emit;
-    asm("" : "+v"(e[q]));  // bit selects below, not an exec-masked block
-  }
-#pragma unroll
-  for (int q = NI - 1; q >= 0; --q) {
-    wp = uni(wp - __popcll(m[q]));
-    const uint32_t pos = (uint32_t)(wp + (int)lane_rank(m[q])) & (kRingWords - 1);
-    ring[(pos & e[q]) | ((uint32_t)(kRingWords + lane) & ~e[q])] = (uint16_t)x[q];
-  }
-#pragma unroll
-  for (int q = NI - 1; q >= 0; --q) x[q] = enc_apply(x[q] >> (e[q] & 16u), r[q]);
-}
-
-// Escapes of one step into the chunk's escape list: slots are taken from the
+// Escapes of one step into the unit's escape list: slots are taken from the
 // end of the list, highest lane first, so that the list, read forwards, is in
 // position order (the coder walks the steps last to first).
 __device__ __forceinline__ void enc_escapes(const uint4 r, uint32_t* __restrict__ list,
@@ -837,9 +830,8 @@ __device__ __forceinline__ void enc_escapes(const uint4 r, uint32_t* __restrict_
   cnt = uni(cnt + __popcll(em));
 }
 
-template <int kMode, bool kImplicit, int SB, int NI>
+template <int kMode, bool kImplicit, int SB>
 __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
-  static_assert(SB % NI == 0, "a block holds whole rounds of the state slots");
   using G = EncGeom<SB>;
   constexpr int kPer = G::kPer;
   extern __shared__ __align__(16) uint8_t smem[];
@@ -858,21 +850,17 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
   int64_t row;
   int32_t start;
   int len, k;
-  chunk_range(g, a.K, a.N, a.chunk_len, row, start, len, k);
+  unit_range(g, a.K, a.S, a.N, a.chunk_len, row, start, len, k);
   const int T = (len + kLanes - 1) / kLanes;
   const int A = len < kLanes ? len : kLanes;
   const int nblk = (T + SB - 1) / SB;
   uint16_t* __restrict__ wbuf = a.words + g * a.cap_words;
   int wp = a.cap_words;  // coder: wave-uniform write cursor (backwards)
   int fl = a.cap_words;  // coder: words at [fl, cap) are already in wbuf
-  // the lane's state slots: step t codes with slot t mod NI (block starts are
-  // multiples of NI, so slot (u mod NI) for step u of a block)
-  uint32_t x[NI];
-#pragma unroll
-  for (int q = 0; q < NI; ++q) x[q] = kStateLow;
+  uint32_t x = kStateLow;
   uint32_t hash = 0, status = 0, znib = 0;
   int n_esc = 0;  // coder: escapes listed so far
-  uint32_t* __restrict__ esc_list = a.esc_raw + g * a.chunk_len + a.chunk_len;
+  uint32_t* __restrict__ esc_list = a.esc_raw + g * a.seg_cap + a.seg_cap;
 
   if (tid < 2) eflag[tid] = 0u;  // visible after the staging barrier
   const bool tab = tables_ok(load_tab_hdr(a.tables), a.M, a.tables_bytes, a.blob);  // uniform
@@ -986,24 +974,24 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
         const bool full = (j + 1) * SB <= T;
         // the block's records in groups of at most 8 steps, last group first
         constexpr int H = SB > 8 ? 8 : SB;
-        static_assert(H % NI == 0, "groups of NI steps tile a group of records");
 #pragma unroll
         for (int h = SB / H - 1; h >= 0; --h) {
           uint4 r[H];
 #pragma unroll
           for (int k = 0; k < H; ++k) r[k] = src[(h * H + k) * kLanes + lane];
           if (full) {
-            // common case: a full block, no per-step branches; NI steps at a
-            // time (H is a multiple of NI, so step h H + k0 + q uses slot q)
+            // common case: a full block, no per-step branches
 #pragma unroll
-            for (int k0 = H - NI; k0 >= 0; k0 -= NI) enc_group<NI>(r + k0, x, ring, wp, lane);
+            for (int k = H - 1; k >= 0; --k) {
+              emit_words((x >> 16) >= 65536u - (r[k].x >> 16), x, ring, wp, lane);
+              x = enc_apply(x, r[k]);
+            }
           } else {
 #pragma unroll
             for (int k = H - 1; k >= 0; --k) {
               if (j * SB + h * H + k >= T) continue;
-              uint32_t& xs = x[(h * H + k) % NI];
-              emit_words((xs >> 16) >= 65536u - (r[k].x >> 16), xs, ring, wp, lane);
-              xs = enc_apply(xs, r[k]);
+              emit_words((x >> 16) >= 65536u - (r[k].x >> 16), x, ring, wp, lane);
+              x = enc_apply(x, r[k]);
             }
           }
           // escapes of the group (their bins are coded above): list them,
@@ -1037,10 +1025,7 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
   }
 
   if (wid == 0 && lane < A) {
-    const int sl = slots_used(len, NI);
-#pragma unroll
-    for (int q = 0; q < NI; ++q)
-      if (q < sl) a.states[(g * NI + q) * kLanes + lane] = x[q];
+    a.states[g * kLanes + lane] = x;
   }
   hash = wave_sum(hash);
   status = wave_or(status);
@@ -1074,7 +1059,7 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
                                      __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
-  if (part[0] == (uint32_t)(a.BK - 1)) {  // uniform: the last workgroup to finish
+  if (part[0] == (uint32_t)(a.units - 1)) {  // uniform: the last workgroup to finish
     __syncthreads();  // every wave has read part[0] before it is reused
     encode_finish(a, tid, reinterpret_cast<uint64_t*>(part));
   }
@@ -1094,8 +1079,8 @@ struct PackArgs {
   const uint32_t* __restrict__ esc_raw;
   const uint8_t* __restrict__ tables;
   uint8_t* __restrict__ out;
-  int64_t out_bytes, header_bytes, cap_words, BK, N;
-  uint32_t B, N32, C, P, K, chunk_len, M, I;
+  int64_t out_bytes, header_bytes, cap_words, units, N;
+  uint32_t B, N32, C, P, K, chunk_len, M, S, seg_cap;
 };
 
 __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
@@ -1106,7 +1091,7 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
   uint32_t* __restrict__ hdr = reinterpret_cast<uint32_t*>(a.out);
   if (tid == 0) {
     hdr[kFixedWords + g] = endo;
-    hdr[kFixedWords + a.BK + g] = a.index_hash[g];
+    hdr[kFixedWords + a.units + g] = a.index_hash[g];
   }
   if (g == 0) {
     const TabHdr* th = reinterpret_cast<const TabHdr*>(a.tables);
@@ -1125,27 +1110,25 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
         case 9: w = kParams; break;
         case 10: w = th->digest_lo; break;
         case 11: w = th->digest_hi; break;
-        case 12: w = a.I; break;
+        case 12: w = a.S; break;
         default: w = 0; break;
       }
       hdr[tid] = w;
     }
-    for (int64_t j = kFixedWords + 2 * a.BK + tid; j < a.header_bytes / 4; j += 256) hdr[j] = 0;
+    for (int64_t j = kFixedWords + 2 * a.units + tid; j < a.header_bytes / 4; j += 256) hdr[j] = 0;
   }
   if ((int64_t)a.header_bytes + endo > a.out_bytes || endo < beg) return;
-  const int len = chunk_len_of(g, (int32_t)a.K, (int32_t)a.chunk_len, a.N);
-  const int A = len < kLanes ? len : kLanes;
-  const int nst = A * slots_used(len, (int)a.I);  // final states: slot-major, A each
+  const int len = unit_len(g, (int32_t)a.K, (int32_t)a.S, a.N, (int32_t)a.chunk_len);
+  const int A = len < kLanes ? len : kLanes;  // final states
   const int64_t W = a.chunk_words[g];
   const uint2 ez = a.esc[g];  // escape count, escape nibbles
   int64_t U = W + (ez.y + 3u) / 4u;
   U += U & 1;  // u16 words after the states: stream, pad, escape words
   uint8_t* dst = a.out + a.header_bytes + beg;
   uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
-  for (int j = tid; j < nst; j += 256)
-    d32[j] = a.states[(g * a.I + j / A) * kLanes + j % A];
+  for (int j = tid; j < A; j += 256) d32[j] = a.states[g * kLanes + j];
   const uint16_t* src = a.words + g * a.cap_words + (a.cap_words - W);
-  uint32_t* w32 = reinterpret_cast<uint32_t*>(dst + 4 * nst);
+  uint32_t* w32 = reinterpret_cast<uint32_t*>(dst + 4 * A);
   const int64_t n32 = U / 2;
   for (int64_t j = tid; j < n32; j += 256) {
     const uint32_t lo = (2 * j < W) ? src[2 * j] : 0u;
@@ -1163,7 +1146,7 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
   __syncthreads();
   const int wv = tid >> 6, lane = tid & 63;
   const uint32_t E = ez.x;
-  const uint32_t* __restrict__ lst = a.esc_raw + g * (int64_t)a.chunk_len + (a.chunk_len - E);
+  const uint32_t* __restrict__ lst = a.esc_raw + g * (int64_t)a.seg_cap + (a.seg_cap - E);
   uint32_t carry = 0;
   for (uint32_t i0 = 0; i0 < E; i0 += 256) {
     const uint32_t i = i0 + tid;
@@ -1232,8 +1215,8 @@ struct DecArgs {
   uint32_t scales_lds;  // LDS byte offset of the staged scale table
   int32_t* __restrict__ out_sym;
   float* __restrict__ out_y;
-  int64_t N, header_bytes, BK;
-  uint32_t B, C, P, K, chunk_len;
+  int64_t N, header_bytes, units;
+  uint32_t B, C, P, K, chunk_len, S;
   UDiv div_hw;
   int32_t nt_cap, ne_cap, nd_cap, stage_all;
   uint32_t starts_words;  // search lookups: 16-byte words of starts to stage
@@ -1637,77 +1620,8 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint2 r, uint
   return (uint32_t)(oob ? 0 : o);
 }
 
-// NI consecutive steps of a full block (every lane active, tables in LDS,
-// offsets that cannot overflow), step q with state slot q: the NI lookups
-// are issued together, dense buckets are resolved for the whole group with
-// one uniform branch per level, and after the state updates the NI refills
-// read their words together (step q's words follow those of the steps
-// before it).  So the group waits for each kind of LDS read once instead of
-// once per step.  Same results as NI calls of dec_step<true, true, SB>.
-template <int NI, int SB>
-__device__ __forceinline__ void dec_group(const Tabs& tb, const uint2* r, uint32_t* x, Stream& S,
-                                          const uint16_t* ring, uint64_t* em, uint32_t* ov,
-                                          int lane) {
-  uint64_t e[NI];
-  uint32_t cum[NI];
-#pragma unroll
-  for (int q = 0; q < NI; ++q) {
-    cum[q] = x[q] & 0xffffu;
-    e[q] = tb.llut[((r[q].x & 0xffffu) << kLutBits) + (cum[q] >> (16 - kLutBits))];
-  }
-  bool d = false;
-#pragma unroll
-  for (int q = 0; q < NI; ++q) d |= dense_entry(e[q]);
-  const uint64_t dm = ballot(d);
-  asm volatile("" ::"s"(dm));
-  if (__builtin_expect(dm != 0ull, 0)) {
-#pragma unroll
-    for (int q = 0; q < NI; ++q)
-      if (dense_entry(e[q])) e[q] = sub_entry<true>(tb, e[q], (cum[q] >> kSubBits) & (kSubSize - 1));
-    bool d3 = false;
-#pragma unroll
-    for (int q = 0; q < NI; ++q) d3 |= dense_entry(e[q]);
-    if (__builtin_expect(ballot(d3) != 0ull, 0)) {
-#pragma unroll
-      for (int q = 0; q < NI; ++q)
-        if (dense_entry(e[q])) e[q] = sub_entry<true>(tb, e[q], cum[q] & (kSubSize - 1));
-    }
-  }
-  uint64_t m[NI];
-  uint32_t s[NI];
-#pragma unroll
-  for (int q = 0; q < NI; ++q) {
-    const uint32_t lo = (uint32_t)e[q], hi = (uint32_t)(e[q] >> 32);
-    const uint32_t s0 = hi & 0xffffu, nxt = hi >> 16;
-    const uint32_t st0 = lo & 0xffffu, st1 = (lo >> 16) + 1u;
-    const bool up = cum[q] >= st1;
-    s[q] = up ? s0 + 1u : s0;
-    const uint32_t st = up ? st1 : st0;
-    const uint32_t fr = up ? nxt + 1u : st1 - st0;
-    x[q] = __umul24(fr, x[q] >> 16) + cum[q] - st;
-    m[q] = ballot(x[q] < kStateLow);
-  }
-  int pos = S.rp;
-  uint32_t w[NI];
-#pragma unroll
-  for (int q = 0; q < NI; ++q) {
-    w[q] = ring[(pos + (int)lane_rank(m[q])) & (DecGeom<SB>::kRing - 1)];
-    pos += __popcll(m[q]);
-  }
-  S.rp = pos;
-#pragma unroll
-  for (int q = 0; q < NI; ++q) {
-    const bool need = (m[q] >> lane) & 1ull;
-    const uint32_t keep = need ? 0xffffu : 0u;
-    x[q] = (x[q] << (need ? 16 : 0)) | (w[q] & keep);
-    em[q] = ballot(s[q] == (r[q].x >> 16));
-    ov[q] = s[q] + r[q].y;
-  }
-}
-
-template <int kMode, bool kImplicit, int SB, bool kSearch, int NI>
+template <int kMode, bool kImplicit, int SB, bool kSearch>
 __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
-  static_assert(SB % NI == 0, "a block holds whole rounds of the state slots");
   constexpr bool kLatents = kMode != kModeSymbols;  // fp32 output with a per-element add
   using G = DecGeom<SB>;
   constexpr int kPer = G::kPer;
@@ -1739,7 +1653,7 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   const int wid = uni(tid >> 6);  // wave role, kept in a scalar register
   uint32_t status = 0, hash = 0, enib = 0;
   const uint32_t* __restrict__ hdr = reinterpret_cast<const uint32_t*>(a.payload);
-  // Header words, the chunk's end offsets and index hash, and the table
+  // Header words, the unit's end offsets and index hash, and the table
   // blob's header, all in one round trip: every word is read (the host has
   // checked that the payload holds the header), the loads are issued before
   // any of them is used (the scheduling barrier keeps them together), and
@@ -1748,17 +1662,17 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   uint32_t hw[13];
 #pragma unroll
   for (int i = 0; i < 13; ++i) hw[i] = hdr[i];
-  // end offsets of chunks g - 1 and g: two adjacent words (word 15 of the
-  // fixed header stands in for chunk -1 and is not used)
+  // end offsets of units g - 1 and g: two adjacent words (word 15 of the
+  // fixed header stands in for unit -1 and is not used)
   const uint32_t* pe = hdr + (kFixedWords - 1) + g;
   const uint32_t e_prev = pe[0];
   const uint32_t e_end = pe[1];
   __builtin_amdgcn_sched_barrier(0);
-  const uint32_t e_hash = hdr[kFixedWords + a.BK + g];  // needed at the end only
+  const uint32_t e_hash = hdr[kFixedWords + a.units + g];  // needed at the end only
   const bool hdr_ok = (hw[0] == kMagic) & (hw[1] == kVersion) & (hw[2] == a.B) &
                       (hw[3] == (uint32_t)a.N) & (hw[4] == a.C) & (hw[5] == a.P) &
                       (hw[6] == a.K) & (hw[7] == a.chunk_len) & (hw[8] == a.M) &
-                      (hw[9] == kParams) & (hw[12] == (uint32_t)NI);
+                      (hw[9] == kParams) & (hw[12] == a.S);
   const bool tab_ok = tables_ok(th, a.M, a.tables_bytes, a.blob) & (hw[10] == th.digest_lo) &
                       (hw[11] == th.digest_hi);
   const bool offsets_safe = (th.flags & kTabOffsetsSafe) != 0;
@@ -1767,13 +1681,12 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   int64_t row;
   int32_t start;
   int len, k;
-  chunk_range(g, a.K, a.N, (int32_t)a.chunk_len, row, start, len, k);
+  unit_range(g, (int32_t)a.K, (int32_t)a.S, a.N, (int32_t)a.chunk_len, row, start, len, k);
   const int T = (len + kLanes - 1) / kLanes;
   const int A = len < kLanes ? len : kLanes;
-  const int SL = slots_used(len, NI);  // state slots flushed per lane
-  const int nst = SL * A;
+  const int nst = A;  // final states
   const int nblk = (T + SB - 1) / SB;
-  // the chunk's bytes: the offsets are used unconditionally, so that their
+  // the unit's bytes: the offsets are used unconditionally, so that their
   // loads are not moved behind the header checks
   const uint32_t beg = g ? e_prev : 0u;
   const uint32_t endo = e_end;
@@ -1884,10 +1797,7 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
     // stream words, the mappers' first two blocks of inputs, the escape
     // reader's window.
     EscReader E;
-    // the lane's state slots: step t decodes with slot t mod NI
-    uint32_t x[NI];
-#pragma unroll
-    for (int q = 0; q < NI; ++q) x[q] = kStateLow;
+    uint32_t x = kStateLow;
     uint32_t w0[G::kPre][G::kPfU32];
     if (wid == 0) {
       S.s32 = s32;
@@ -1895,9 +1805,7 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
       S.q = q16;
       S.q32 = q16 / 2;
       S.filled = 0;
-#pragma unroll
-      for (int q = 0; q < NI; ++q)  // slot q of lane l: state q * A + l (lane < A: below)
-        x[q] = safe[(q < SL ? q : 0) * A + (lane < A ? lane : 0)];
+      x = safe[lane < A ? lane : 0];  // lanes >= A: below
 #pragma unroll
       for (int b = 0; b < G::kPre; ++b)
 #pragma unroll
@@ -1939,8 +1847,7 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
     // before the first block and one per block, and one after the mappers'
     // last store.
     if (wid == 0) {
-#pragma unroll
-      for (int q = 0; q < NI; ++q) x[q] = (lane < A && q < SL) ? x[q] : kStateLow;
+      x = lane < A ? x : kStateLow;
 #pragma unroll
       for (int b = 0; b < G::kPre; ++b)
 #pragma unroll
@@ -1965,18 +1872,11 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
           // common case: every lane of the block active, LDS tables, no
           // per-step branches
           uint64_t em[SB];
-          if constexpr (kSearch) {
 #pragma unroll
-            for (int u = 0; u < SB; ++u)
-              ov[u] = dec_step<true, true, SB, kSearch>(tb, r[u], x[u % NI], S, sring, em[u],
-                                                        status, lane);
-          } else {
-#pragma unroll
-            for (int u = 0; u < SB; u += NI)
-              dec_group<NI, SB>(tb, r + u, x, S, sring, em + u, ov + u, lane);
+          for (int u = 0; u < SB; ++u) {
+            ov[u] = dec_step<true, true, SB, kSearch>(tb, r[u], x, S, sring, em[u], status, lane);
+            any_em |= em[u];
           }
-#pragma unroll
-          for (int u = 0; u < SB; ++u) any_em |= em[u];
           if (__builtin_expect(any_em != 0ull, 0)) {
 #pragma unroll
             for (int u = 0; u < SB; ++u) {
@@ -1992,26 +1892,19 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
             else src[u * kLanes + lane].x = ov[u];
           }
         } else {
-          // last block or tables outside LDS: one step at a time, the slot
-          // in use rotated into x[0] (a full block rotates every slot back
-          // into place; after a partial last block only the final check,
-          // which takes the slots in any order, follows)
+          // last block or tables outside LDS: one step at a time
 #pragma unroll 1
           for (int u = 0; u < SB && j * SB + u < T; ++u) {
             const uint2 ru = src[u * kLanes + lane];
             uint64_t em;
             uint32_t v;
             if constexpr (kSearch) {
-              v = dec_step<true, false, SB, true>(tb, ru, x[0], S, sring, em, status, lane);
+              v = dec_step<true, false, SB, true>(tb, ru, x, S, sring, em, status, lane);
             } else {
               v = ((nl >> u) & 1u) == 0u
-                      ? dec_step<true, false, SB>(tb, ru, x[0], S, sring, em, status, lane)
-                      : dec_step<false, false, SB>(tb, ru, x[0], S, sring, em, status, lane);
+                      ? dec_step<true, false, SB>(tb, ru, x, S, sring, em, status, lane)
+                      : dec_step<false, false, SB>(tb, ru, x, S, sring, em, status, lane);
             }
-            const uint32_t x0 = x[0];
-#pragma unroll
-            for (int q = 0; q + 1 < NI; ++q) x[q] = x[q + 1];
-            x[NI - 1] = x0;
             if (lane == 0) ei[u] = make_uint4((uint32_t)em, (uint32_t)(em >> 32), ecur, 0u);
             ecur += (uint32_t)__popcll(em);
             any_em |= em;
@@ -2025,9 +1918,7 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
         }
         __syncthreads();
       }
-#pragma unroll
-      for (int q = 0; q < NI; ++q)
-        if (lane < A && x[q] != kStateLow) status |= GAANS_ST_CORRUPT;
+      if (lane < A && x != kStateLow) status |= GAANS_ST_CORRUPT;
       __syncthreads();  // after the mappers' last store
     } else if (wid == kEscWave) {
       __syncthreads();
@@ -2104,7 +1995,7 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     const uint32_t done = __hip_atomic_fetch_add(&a.ctrl[kCtrlDecDone], 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
-    if (done == (uint32_t)(a.BK - 1)) {
+    if (done == (uint32_t)(a.units - 1)) {
       const uint32_t all = __hip_atomic_exchange(&a.ctrl[kCtrlDecStatus], 0u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
       a.status_out[0] = all;
@@ -2476,11 +2367,11 @@ int device_lds(DevLds* out) {
   return GAANS_OK;
 }
 
-// LDS staging plan for a launch of BK workgroups: all tables if they fit
+// LDS staging plan for a launch of `units` workgroups: all tables if they fit
 // and are not much larger than a chunk's channel range, else that range (P
 // tables, bounded by P times the largest table), else none.  The budget per
 // workgroup keeps the launch in one round of workgroups when the tables allow
-// it (BK / CUs workgroups per CU), and otherwise gives up workgroups per CU
+// it (units / CUs workgroups per CU), and otherwise gives up workgroups per CU
 // before it gives up staging.
 struct Stage {
   int32_t nt_cap, ne_cap, nd_cap, stage_all;
@@ -2497,9 +2388,9 @@ int64_t lds_budget(const DevLds& d, int64_t occ) {
   return occ > 1 ? b - 1024 : b;
 }
 
-// Workgroups per CU that keep a launch of BK workgroups in one round.
-int64_t occ_target(int64_t BK, const DevLds& d, int64_t max_occ) {
-  int64_t occ = (BK + d.cus - 1) / d.cus;
+// Workgroups per CU that keep a launch of units workgroups in one round.
+int64_t occ_target(int64_t units, const DevLds& d, int64_t max_occ) {
+  int64_t occ = (units + d.cus - 1) / d.cus;
   return occ > max_occ ? max_occ : (occ < 1 ? 1 : occ);
 }
 
@@ -2536,10 +2427,10 @@ struct EncPlan {
 // `extra` LDS bytes follow the tables (the Gaussian mode's scale table);
 // range_ok is false when any table may serve any position (per-element
 // indexes computed from scales), so only all tables or none are staged.
-EncPlan plan_encode(const gaans_tables* t, int64_t P, int64_t BK, const DevLds& d,
+EncPlan plan_encode(const gaans_tables* t, int64_t P, int64_t units, const DevLds& d,
                     int64_t extra = 0, bool range_ok = true,
                     bool allow16 = false) {
-  for (int64_t occ = occ_target(BK, d, 4); occ >= 1; --occ)
+  for (int64_t occ = occ_target(units, d, 4); occ >= 1; --occ)
     for (int sb = allow16 ? 16 : 8; sb >= 4; sb >>= 1) {
       Stage s;
       const int64_t fixed = enc_fixed_lds(sb);
@@ -2574,14 +2465,14 @@ int64_t search_lds(const gaans_tables* t, uint32_t* starts_words) {
   return (int64_t)t->M * (4 * kLutSize + 16) + sb;
 }
 
-DecPlan plan_decode(const gaans_tables* t, int64_t P, int64_t BK, bool latents,
+DecPlan plan_decode(const gaans_tables* t, int64_t P, int64_t units, bool latents,
                     const DevLds& d, int64_t extra = 0, bool range_ok = true,
                     bool search_ok = false) {
   const int64_t per_table = 8 * kLutSize + 16;
   const bool has_dense = t->total_dense > 0;
   uint32_t starts_words = 0;
   const int64_t search_bytes = search_ok ? search_lds(t, &starts_words) : 0;
-  for (int64_t occ = occ_target(BK, d, 3); occ >= 1; --occ) {
+  for (int64_t occ = occ_target(units, d, 3); occ >= 1; --occ) {
     const int64_t cap = lds_budget(d, occ);
     for (int opt = 0; opt < 9; ++opt) {
       const int sb = 16 >> (opt % 3);  // 16-, 8-, then 4-step blocks of each kind
@@ -2653,80 +2544,64 @@ int32_t pow2_floor(int32_t v) {  // largest power of two <= v (0 for v < 1)
 using EncKernel = void (*)(EncArgs);
 using DecKernel = void (*)(DecArgs);
 
-template <int kMode, bool kImp, int SB>
-EncKernel enc_kernel_ni(int ni) {
-  return ni == 4 ? k_encode<kMode, kImp, SB, 4>
-                 : (ni == 2 ? k_encode<kMode, kImp, SB, 2> : k_encode<kMode, kImp, SB, 1>);
-}
-
 template <int kMode, bool kImp>
-EncKernel enc_kernel_sb(int sb, int ni) {
-  return sb == 4 ? enc_kernel_ni<kMode, kImp, 4>(ni) : enc_kernel_ni<kMode, kImp, 8>(ni);
+EncKernel enc_kernel_sb(int sb) {
+  return sb == 4 ? k_encode<kMode, kImp, 4> : k_encode<kMode, kImp, 8>;
 }
 
-// Encode kernel of a mode, index kind, block size and interleave; 16-step
-// blocks are built for explicit or computed indexes only (with table =
-// channel the 16-step kernel needs private scratch).
-EncKernel enc_kernel(int mode, bool imp, int sb, int ni) {
+// Encode kernel of a mode, index kind and block size; 16-step blocks are
+// built for explicit or computed indexes only (with table = channel the
+// 16-step kernel needs private scratch).
+EncKernel enc_kernel(int mode, bool imp, int sb) {
   if (sb == 16) {
     switch (mode) {
-      case kModeGaussian: return enc_kernel_ni<kModeGaussian, false, 16>(ni);
-      case kModeLatents: return enc_kernel_ni<kModeLatents, false, 16>(ni);
-      default: return enc_kernel_ni<kModeSymbols, false, 16>(ni);
+      case kModeGaussian: return k_encode<kModeGaussian, false, 16>;
+      case kModeLatents: return k_encode<kModeLatents, false, 16>;
+      default: return k_encode<kModeSymbols, false, 16>;
     }
   }
   switch (mode) {
-    case kModeGaussian: return enc_kernel_sb<kModeGaussian, false>(sb, ni);
+    case kModeGaussian: return enc_kernel_sb<kModeGaussian, false>(sb);
     case kModeLatents:
-      return imp ? enc_kernel_sb<kModeLatents, true>(sb, ni)
-                 : enc_kernel_sb<kModeLatents, false>(sb, ni);
+      return imp ? enc_kernel_sb<kModeLatents, true>(sb) : enc_kernel_sb<kModeLatents, false>(sb);
     default:
-      return imp ? enc_kernel_sb<kModeSymbols, true>(sb, ni)
-                 : enc_kernel_sb<kModeSymbols, false>(sb, ni);
+      return imp ? enc_kernel_sb<kModeSymbols, true>(sb) : enc_kernel_sb<kModeSymbols, false>(sb);
   }
-}
-
-template <int kMode, bool kImp, int SB, bool kSearch>
-DecKernel dec_kernel_ni(int ni) {
-  return ni == 4 ? k_decode<kMode, kImp, SB, kSearch, 4>
-                 : (ni == 2 ? k_decode<kMode, kImp, SB, kSearch, 2>
-                            : k_decode<kMode, kImp, SB, kSearch, 1>);
 }
 
 template <int kMode, bool kImp, bool kSearch>
-DecKernel dec_kernel_sb(int sb, int ni) {
-  return sb == 4 ? dec_kernel_ni<kMode, kImp, 4, kSearch>(ni)
-                 : (sb == 8 ? dec_kernel_ni<kMode, kImp, 8, kSearch>(ni)
-                            : dec_kernel_ni<kMode, kImp, 16, kSearch>(ni));
+DecKernel dec_kernel_sb(int sb) {
+  return sb == 4 ? k_decode<kMode, kImp, 4, kSearch>
+                 : (sb == 8 ? k_decode<kMode, kImp, 8, kSearch> : k_decode<kMode, kImp, 16, kSearch>);
 }
 
-// Decode kernel of a mode, index kind, block size, lookup kind and
-// interleave (the search lookups serve explicit or computed indexes only).
-DecKernel dec_kernel(int mode, bool imp, int sb, bool search, int ni) {
+// Decode kernel of a mode, index kind, block size and lookup kind (the
+// search lookups serve explicit or computed indexes only).
+DecKernel dec_kernel(int mode, bool imp, int sb, bool search) {
   if (search) {
     switch (mode) {
-      case kModeGaussian: return dec_kernel_sb<kModeGaussian, false, true>(sb, ni);
-      case kModeLatents: return dec_kernel_sb<kModeLatents, false, true>(sb, ni);
-      default: return dec_kernel_sb<kModeSymbols, false, true>(sb, ni);
+      case kModeGaussian: return dec_kernel_sb<kModeGaussian, false, true>(sb);
+      case kModeLatents: return dec_kernel_sb<kModeLatents, false, true>(sb);
+      default: return dec_kernel_sb<kModeSymbols, false, true>(sb);
     }
   }
   switch (mode) {
-    case kModeGaussian: return dec_kernel_sb<kModeGaussian, false, false>(sb, ni);
+    case kModeGaussian: return dec_kernel_sb<kModeGaussian, false, false>(sb);
     case kModeLatents:
-      return imp ? dec_kernel_sb<kModeLatents, true, false>(sb, ni)
-                 : dec_kernel_sb<kModeLatents, false, false>(sb, ni);
+      return imp ? dec_kernel_sb<kModeLatents, true, false>(sb)
+                 : dec_kernel_sb<kModeLatents, false, false>(sb);
     default:
-      return imp ? dec_kernel_sb<kModeSymbols, true, false>(sb, ni)
-                 : dec_kernel_sb<kModeSymbols, false, false>(sb, ni);
+      return imp ? dec_kernel_sb<kModeSymbols, true, false>(sb)
+                 : dec_kernel_sb<kModeSymbols, false, false>(sb);
   }
 }
 
 int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y,
                   const float* medians, const int32_t* indexes, const GaussIn* g,
                   const gaans_tables* tables, int64_t B, int64_t N, int64_t C, int64_t P,
-                  int64_t I, void* ws, int64_t ws_bytes, void* ctrl, uint64_t* info_out) {
+                  int64_t S, void* ws, int64_t ws_bytes, void* ctrl, uint64_t* info_out) {
   Layout L;
-  int rc = make_layout(B, N, C, P, I, &L);
+  int rc = make_layout(B, N, C, P, S, &L);
   if (rc) return rc;
   if ((rc = check_tables_arg(tables))) return rc;
   if (mode == kModeSymbols ? !symbols : (!y || (mode == kModeLatents && !medians)))
@@ -2742,14 +2617,14 @@ int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y
   DevLds dl;
   if ((rc = device_lds(&dl))) return rc;
   const int64_t extra = mode == kModeGaussian ? align_up(4 * (int64_t)g->n, 16) : 0;
-  // 16-step blocks for long chunks only (the coder waits for the first
-  // block to be mapped, so short chunks lose more than the per-block saving
+  // 16-step blocks for long units only (the coder waits for the first
+  // block to be mapped, so short units lose more than the per-block saving
   // gains: measured slower at 96 steps, faster at 4,080), and with explicit
   // or computed indexes only (with table = channel the 16-step kernel needs
   // private scratch)
-  const bool long_chunks = L.chunk_len >= 512 * kLanes;
-  const EncPlan plan = plan_encode(tables, P, L.BK, dl, extra, mode != kModeGaussian,
-                                   long_chunks && (indexes || g));
+  const bool long_units = L.seg_cap >= 512 * kLanes;
+  const EncPlan plan = plan_encode(tables, P, L.U, dl, extra, mode != kModeGaussian,
+                                   long_units && (indexes || g));
   const Stage& st = plan.st;
   EncArgs a;
   a.symbols = symbols;
@@ -2772,10 +2647,11 @@ int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y
   a.P = (int32_t)P;
   a.C = (int32_t)C;
   a.chunk_len = (int32_t)L.chunk_len;
-  a.I = (int32_t)I;
+  a.S = (int32_t)S;
+  a.seg_cap = (int32_t)L.seg_cap;
   a.div_hw = make_udiv((uint32_t)L.HW);
   a.cap_words = (int32_t)L.cap_words;
-  a.BK = L.BK;
+  a.units = L.U;
   a.header_bytes = L.header_bytes;
   a.nt_cap = st.nt_cap;
   a.stage_all = st.stage_all;
@@ -2794,18 +2670,18 @@ int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y
   if (lds > (size_t)dl.per_block)
     return fail(GAANS_EINVAL, "encode needs %zu bytes of LDS, the device has %d", lds,
                 dl.per_block);
-  const EncKernel kernel = enc_kernel(mode, indexes == nullptr, plan.sb, (int)I);
+  const EncKernel kernel = enc_kernel(mode, indexes == nullptr, plan.sb);
   if ((rc = allow_lds(reinterpret_cast<const void*>(kernel), lds, dl))) return rc;
-  kernel<<<dim3((uint32_t)L.BK), dim3(kThreads), lds, static_cast<hipStream_t>(stream)>>>(a);
+  kernel<<<dim3((uint32_t)L.U), dim3(kThreads), lds, static_cast<hipStream_t>(stream)>>>(a);
   return check_launch("encode");
 }
 
 int decode_impl(int mode, void* stream, const uint8_t* payload, int64_t payload_bytes,
                 const int32_t* indexes, const GaussIn* g, const gaans_tables* tables,
-                const float* medians, int64_t B, int64_t N, int64_t C, int64_t P, int64_t I,
+                const float* medians, int64_t B, int64_t N, int64_t C, int64_t P, int64_t S,
                 int32_t* out_sym, float* out_y, void* ctrl, uint32_t* status_out) {
   Layout L;
-  int rc = make_layout(B, N, C, P, I, &L);
+  int rc = make_layout(B, N, C, P, S, &L);
   if (rc) return rc;
   if ((rc = check_tables_arg(tables))) return rc;
   if (!payload || !status_out || !ctrl ||
@@ -2824,7 +2700,7 @@ int decode_impl(int mode, void* stream, const uint8_t* payload, int64_t payload_
   const bool search_ok =
       (tables->flags & GAANS_TABLES_SEARCH) != 0 && (mode == kModeGaussian || indexes != nullptr);
   const DecPlan plan =
-      plan_decode(tables, P, L.BK, latents, dl, extra, mode != kModeGaussian, search_ok);
+      plan_decode(tables, P, L.U, latents, dl, extra, mode != kModeGaussian, search_ok);
   const Stage& st = plan.st;
   DecArgs a;
   a.payload = payload;
@@ -2846,12 +2722,13 @@ int decode_impl(int mode, void* stream, const uint8_t* payload, int64_t payload_
   a.out_y = out_y;
   a.N = N;
   a.header_bytes = L.header_bytes;
-  a.BK = L.BK;
+  a.units = L.U;
   a.B = (uint32_t)B;
   a.C = (uint32_t)C;
   a.P = (uint32_t)P;
   a.K = (uint32_t)L.K;
   a.chunk_len = (uint32_t)L.chunk_len;
+  a.S = (uint32_t)S;
   a.div_hw = make_udiv((uint32_t)L.HW);
   a.nt_cap = st.nt_cap;
   a.ne_cap = st.ne_cap;
@@ -2864,9 +2741,9 @@ int decode_impl(int mode, void* stream, const uint8_t* payload, int64_t payload_
   if (lds > (size_t)dl.per_block)
     return fail(GAANS_EINVAL, "decode needs %zu bytes of LDS, the device has %d", lds,
                 dl.per_block);
-  const DecKernel kernel = dec_kernel(mode, indexes == nullptr, plan.sb, plan.search, (int)I);
+  const DecKernel kernel = dec_kernel(mode, indexes == nullptr, plan.sb, plan.search);
   if ((rc = allow_lds(reinterpret_cast<const void*>(kernel), lds, dl))) return rc;
-  kernel<<<dim3((uint32_t)L.BK), dim3(kDecThreads), lds, static_cast<hipStream_t>(stream)>>>(a);
+  kernel<<<dim3((uint32_t)L.U), dim3(kDecThreads), lds, static_cast<hipStream_t>(stream)>>>(a);
   return check_launch("decode");
 }
 
@@ -3089,14 +2966,14 @@ int gaans_abi_version(void) { return GAANS_ABI_VERSION; }
 
 const char* gaans_last_error(void) { return g_last_error.c_str(); }
 
-int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
+int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, int32_t segments,
                      gaans_layout* out) {
   if (!out) return fail(GAANS_EINVAL, "layout pointer is NULL");
   Layout L;
-  int rc = make_layout(B, N, C, P, interleave, &L);
+  int rc = make_layout(B, N, C, P, segments, &L);
   if (rc) return rc;
-  out->B = L.B; out->N = L.N; out->C = L.C; out->P = L.P; out->I = L.I;
-  out->HW = L.HW; out->K = L.K; out->chunk_len = L.chunk_len; out->BK = L.BK;
+  out->B = L.B; out->N = L.N; out->C = L.C; out->P = L.P; out->S = L.S;
+  out->HW = L.HW; out->K = L.K; out->chunk_len = L.chunk_len; out->U = L.U;
   out->header_bytes = L.header_bytes;
   out->max_payload_bytes = L.max_payload;
   out->cap_words = L.cap_words;
@@ -3113,25 +2990,30 @@ int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, int32_t interle
   return GAANS_OK;
 }
 
-int gaans_choose_interleave(const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
-                            int64_t P, double budget, int32_t* interleave) {
-  if (!tables || !interleave) return fail(GAANS_EINVAL, "NULL argument");
+int gaans_choose_segments(const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
+                          int64_t P, double budget, int64_t target_units, int32_t* segments) {
+  if (!tables || !segments) return fail(GAANS_EINVAL, "NULL argument");
   Layout L;
   int rc = make_layout(B, N, C, P, 1, &L);
   if (rc) return rc;
   if (!(budget >= 0.0) || !(tables->mean_bits >= 0.0f))
     return fail(GAANS_EINVAL, "budget and the tables' mean_bits must be non-negative numbers");
-  const int64_t len = L.chunk_len < L.N ? L.chunk_len : L.N;  // a full chunk
+  // the most segments the shape allows: one step each in the shortest chunk
+  const int64_t t_last = (N - (L.K - 1) * L.chunk_len + kLanes - 1) / kLanes;
+  int64_t s = std::min<int64_t>(kMaxSegments, t_last);
+  // enough units to fill target_units workgroups, no more
+  if (target_units > 0) s = std::min<int64_t>(s, (target_units + L.U - 1) / L.U);
+  // bytes an added unit costs, against the expected bytes of a full chunk:
+  // its A final states (4 A) less what its fresh initial states absorb
+  // before they emit, plus a pad and a partly used escape word; measured
+  // 200-203 bytes per added unit of 64 lanes on every workload of the
+  // benchmark (2160x3840 P=8, 512x768 P=4, hyperprior y P=16), so 3.125 A + 4
+  const int64_t len = L.chunk_len < L.N ? L.chunk_len : L.N;
   const int64_t A = len < kLanes ? len : kLanes;
   const double expected = (double)len * tables->mean_bits / 8.0 + 4.0 * (double)A;
-  *interleave = 1;
-  for (int I = 4; I >= 2; I >>= 1) {
-    const double extra = 4.0 * (double)A * (slots_used((int)len, I) - 1);
-    if (extra > 0.0 && extra <= budget * expected) {
-      *interleave = I;
-      break;
-    }
-  }
+  const double per_seg = 3.125 * (double)A + 4.0;
+  s = std::min<int64_t>(s, 1 + (int64_t)(budget * expected / per_seg));
+  *segments = (int32_t)std::max<int64_t>(s, 1);
   return GAANS_OK;
 }
 
@@ -3261,38 +3143,38 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
 
 int gaans_encode_symbols(void* stream, const int32_t* symbols_dev, const int32_t* indexes_dev,
                          const gaans_tables* tables, int64_t B, int64_t N, int64_t C, int64_t P,
-                         int32_t interleave, void* workspace_dev, int64_t workspace_bytes,
+                         int32_t segments, void* workspace_dev, int64_t workspace_bytes,
                          void* ctrl_dev, uint64_t* info_out) {
   return encode_stage1(kModeSymbols, stream, symbols_dev, nullptr, nullptr, indexes_dev, nullptr,
-                       tables, B, N, C, P, interleave, workspace_dev, workspace_bytes, ctrl_dev,
+                       tables, B, N, C, P, segments, workspace_dev, workspace_bytes, ctrl_dev,
                        info_out);
 }
 
 int gaans_encode_latents(void* stream, const float* y_dev, const float* medians_dev,
                          const int32_t* indexes_dev, const gaans_tables* tables, int64_t B,
-                         int64_t N, int64_t C, int64_t P, int32_t interleave, void* workspace_dev,
+                         int64_t N, int64_t C, int64_t P, int32_t segments, void* workspace_dev,
                          int64_t workspace_bytes, void* ctrl_dev, uint64_t* info_out) {
   return encode_stage1(kModeLatents, stream, nullptr, y_dev, medians_dev, indexes_dev, nullptr,
-                       tables, B, N, C, P, interleave, workspace_dev, workspace_bytes, ctrl_dev,
+                       tables, B, N, C, P, segments, workspace_dev, workspace_bytes, ctrl_dev,
                        info_out);
 }
 
 int gaans_encode_gaussian(void* stream, const float* y_dev, const float* means_dev,
                           const float* scales_dev, const float* scale_table_dev,
                           int32_t n_scales, float scale_bound, const gaans_tables* tables,
-                          int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
+                          int64_t B, int64_t N, int64_t C, int64_t P, int32_t segments,
                           void* workspace_dev, int64_t workspace_bytes, void* ctrl_dev,
                           uint64_t* info_out) {
   const GaussIn g{means_dev, scales_dev, scale_table_dev, n_scales, scale_bound};
   return encode_stage1(kModeGaussian, stream, nullptr, y_dev, nullptr, nullptr, &g, tables, B, N,
-                       C, P, interleave, workspace_dev, workspace_bytes, ctrl_dev, info_out);
+                       C, P, segments, workspace_dev, workspace_bytes, ctrl_dev, info_out);
 }
 
 int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace_bytes,
                       const gaans_tables* tables, int64_t B, int64_t N, int64_t C, int64_t P,
-                      int32_t interleave, uint8_t* out_dev, int64_t out_bytes) {
+                      int32_t segments, uint8_t* out_dev, int64_t out_bytes) {
   Layout L;
-  int rc = make_layout(B, N, C, P, interleave, &L);
+  int rc = make_layout(B, N, C, P, segments, &L);
   if (rc) return rc;
   if ((rc = check_tables_arg(tables))) return rc;
   if (!workspace_dev || workspace_bytes < L.ws_bytes)
@@ -3313,7 +3195,7 @@ int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace
   a.out_bytes = out_bytes;
   a.header_bytes = L.header_bytes;
   a.cap_words = L.cap_words;
-  a.BK = L.BK;
+  a.units = L.U;
   a.N = N;
   a.B = (uint32_t)B;
   a.N32 = (uint32_t)N;
@@ -3322,17 +3204,18 @@ int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace
   a.K = (uint32_t)L.K;
   a.chunk_len = (uint32_t)L.chunk_len;
   a.M = (uint32_t)tables->M;
-  a.I = (uint32_t)L.I;
-  k_pack<<<dim3((uint32_t)L.BK), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(a);
+  a.S = (uint32_t)L.S;
+  a.seg_cap = (uint32_t)L.seg_cap;
+  k_pack<<<dim3((uint32_t)L.U), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(a);
   return check_launch("pack");
 }
 
 int gaans_encode_symbols_noalloc(void* stream, const int32_t* symbols_dev,
                                  const int32_t* indexes_dev, const gaans_tables* tables,
-                                 int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
+                                 int64_t B, int64_t N, int64_t C, int64_t P, int32_t segments,
                                  uint8_t* out_dev, int64_t out_bytes, uint64_t* info_out) {
   Layout L;
-  int rc = make_layout(B, N, C, P, interleave, &L);
+  int rc = make_layout(B, N, C, P, segments, &L);
   if (rc) return rc;
   // the size limit first: it needs no device
   const int64_t need = (int64_t)GAANS_CTRL_BYTES + L.ws_bytes;
@@ -3350,28 +3233,28 @@ int gaans_encode_symbols_noalloc(void* stream, const int32_t* symbols_dev,
   void* ctrl = base;
   void* ws = base + GAANS_CTRL_BYTES;
   rc = encode_stage1(kModeSymbols, stream, symbols_dev, nullptr, nullptr, indexes_dev, nullptr,
-                     tables, B, N, C, P, interleave, ws, L.ws_bytes, ctrl, info_out);
+                     tables, B, N, C, P, segments, ws, L.ws_bytes, ctrl, info_out);
   if (rc) return rc;
-  return gaans_encode_pack(stream, ws, L.ws_bytes, tables, B, N, C, P, interleave, out_dev,
+  return gaans_encode_pack(stream, ws, L.ws_bytes, tables, B, N, C, P, segments, out_dev,
                            out_bytes);
 }
 
 int gaans_decode_symbols(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
                          const int32_t* indexes_dev, const gaans_tables* tables, int64_t B,
-                         int64_t N, int64_t C, int64_t P, int32_t interleave, int32_t* out_dev,
+                         int64_t N, int64_t C, int64_t P, int32_t segments, int32_t* out_dev,
                          void* ctrl_dev, uint32_t* status_out) {
   return decode_impl(kModeSymbols, stream, payload_dev, payload_bytes, indexes_dev, nullptr,
-                     tables, nullptr, B, N, C, P, interleave, out_dev, nullptr, ctrl_dev,
+                     tables, nullptr, B, N, C, P, segments, out_dev, nullptr, ctrl_dev,
                      status_out);
 }
 
 int gaans_decode_latents(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
                          const int32_t* indexes_dev, const gaans_tables* tables,
                          const float* medians_dev, int64_t B, int64_t N, int64_t C, int64_t P,
-                         int32_t interleave, float* y_hat_dev, void* ctrl_dev,
+                         int32_t segments, float* y_hat_dev, void* ctrl_dev,
                          uint32_t* status_out) {
   return decode_impl(kModeLatents, stream, payload_dev, payload_bytes, indexes_dev, nullptr,
-                     tables, medians_dev, B, N, C, P, interleave, nullptr, y_hat_dev, ctrl_dev,
+                     tables, medians_dev, B, N, C, P, segments, nullptr, y_hat_dev, ctrl_dev,
                      status_out);
 }
 
@@ -3379,11 +3262,11 @@ int gaans_decode_gaussian(void* stream, const uint8_t* payload_dev, int64_t payl
                           const float* scales_dev, const float* means_dev,
                           const float* scale_table_dev, int32_t n_scales, float scale_bound,
                           const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
-                          int64_t P, int32_t interleave, float* y_hat_dev, void* ctrl_dev,
+                          int64_t P, int32_t segments, float* y_hat_dev, void* ctrl_dev,
                           uint32_t* status_out) {
   const GaussIn g{means_dev, scales_dev, scale_table_dev, n_scales, scale_bound};
   return decode_impl(kModeGaussian, stream, payload_dev, payload_bytes, nullptr, &g, tables,
-                     nullptr, B, N, C, P, interleave, nullptr, y_hat_dev, ctrl_dev, status_out);
+                     nullptr, B, N, C, P, segments, nullptr, y_hat_dev, ctrl_dev, status_out);
 }
 
 int gaans_rans64_decode(void* stream, const uint8_t* streams_dev, int64_t streams_bytes,

@@ -231,12 +231,12 @@ def accelerate(
         if hyper is None:
             from .coders.factorized import FactorizedWarpDivCodec
 
-            codec = FactorizedWarpDivCodec(runtime_model, p_ch, interleave=cfg.interleave)
+            codec = FactorizedWarpDivCodec(runtime_model, p_ch, segments=cfg.segments)
         else:
             from .coders.hyperprior import HyperpriorWarpDivCodec
 
             codec = HyperpriorWarpDivCodec(runtime_model, p_ch, mean_scale=hyper == "mean_scale",
-                                           interleave=cfg.interleave)
+                                           segments=cfg.segments)
         wrapped = FastModel(runtime_model, device=str(target))
         wrapped._coder = codec
         from .pipeline import CodingPipeline

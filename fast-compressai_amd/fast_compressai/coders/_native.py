@@ -15,7 +15,7 @@ import threading
 from .errors import CoderDependencyError
 
 LIB_NAME = "libgaans_w64.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 CTRL_BYTES = 256
 NOALLOC_SCRATCH_BYTES = 16 * 1024 * 1024  # GAANS_NOALLOC_SCRATCH_BYTES
 
@@ -41,7 +41,7 @@ STATUS_TEXT = {
 }
 
 
-_LAYOUT_FIELDS = ("B", "N", "C", "P", "I", "HW", "K", "chunk_len", "BK", "header_bytes",
+_LAYOUT_FIELDS = ("B", "N", "C", "P", "S", "HW", "K", "chunk_len", "U", "header_bytes",
                   "max_payload_bytes", "cap_words", "workspace_bytes", "ws_chunk_words",
                   "ws_chunk_status", "ws_index_hash", "ws_end_off", "ws_info", "ws_states",
                   "ws_words", "ws_esc", "ws_esc_raw")
@@ -90,8 +90,8 @@ def _declare(L) -> None:
         "gaans_abi_version": ([], ctypes.c_int),
         "gaans_last_error": ([], ctypes.c_char_p),
         "gaans_get_layout": ([i64, i64, i64, i64, i32, ctypes.POINTER(Layout)], ctypes.c_int),
-        "gaans_choose_interleave": ([T, i64, i64, i64, i64, ctypes.c_double,
-                                     ctypes.POINTER(ctypes.c_int32)], ctypes.c_int),
+        "gaans_choose_segments": ([T, i64, i64, i64, i64, ctypes.c_double, i64,
+                                   ctypes.POINTER(ctypes.c_int32)], ctypes.c_int),
         "gaans_tables_bytes": ([p, p, i32, i32, ctypes.POINTER(ctypes.c_int64)], ctypes.c_int),
         "gaans_tables_prepare": ([p, p, p, i32, i32, p, i64, T], ctypes.c_int),
         "gaans_encode_symbols": ([p, p, p, T, i64, i64, i64, i64, i32, p, i64, p, p],
@@ -168,12 +168,14 @@ def check(rc: int, what: str) -> None:
 _layouts: dict = {}
 
 
-def layout(B: int, N: int, C: int, P: int, I: int = 1) -> LayoutInts:
-    key = (B, N, C, P, I)
+def layout(B: int, N: int, C: int, P: int, S: int = 1) -> LayoutInts:
+    """``gaans_layout`` of B rows of N symbols, C channels, P per chunk and S
+    segments per chunk (cached)."""
+    key = (B, N, C, P, S)
     out = _layouts.get(key)
     if out is None:
         raw = Layout()
-        check(lib().gaans_get_layout(B, N, C, P, I, ctypes.byref(raw)), "layout")
+        check(lib().gaans_get_layout(B, N, C, P, S, ctypes.byref(raw)), "layout")
         out = LayoutInts(raw)
         if len(_layouts) > 256:
             _layouts.clear()

@@ -23,10 +23,10 @@ from .warp_div import WarpDivBackend, WarpDivPayload, coding_fingerprint
 class FactorizedWarpDivCodec:
     """Keep Balle's transforms/quantizer while replacing its entropy coder."""
 
-    def __init__(self, model, p_ch: int, interleave: int | None = None) -> None:
+    def __init__(self, model, p_ch: int, segments: int | None = None) -> None:
         self.model = model
         self.p_ch = p_ch
-        self.interleave = interleave  # rANS states per lane; None: chosen per shape
+        self.segments = segments  # coding units per chunk; None: chosen per shape
         self.backend = WarpDivBackend()
         self._cache = TableCache(capacity=2)
         entropy = model.entropy_bottleneck
@@ -75,23 +75,23 @@ class FactorizedWarpDivCodec:
             medians = self._medians(entropy)
             B, C = int(y.size(0)), int(y.size(1))
             N = int(y[0].numel())
-            I = gaans.resolve_interleave(self.interleave, tables, B, N, C, self.p_ch)
+            S = gaans.resolve_segments(self.segments, tables, B, N, C, self.p_ch, y.device)
             if y.dtype == torch.float32 and medians.dtype == torch.float32:
                 enc = gaans.encode(tables, B, N, C, self.p_ch, y.device,
-                                   y=y.contiguous(), medians=medians.contiguous(), interleave=I)
+                                   y=y.contiguous(), medians=medians.contiguous(), segments=S)
             else:
                 # non-fp32 latents: CompressAI's own quantize, then the coder
                 ext = entropy._extend_ndims(entropy._get_medians().detach(), y.ndim - 2)
                 symbols = entropy.quantize(y, "symbols", ext.expand(B, *([-1] * (y.ndim - 1))))
                 enc = gaans.encode(tables, B, N, C, self.p_ch, y.device,
                                    symbols=symbols.reshape(B, -1).to(torch.int32).contiguous(),
-                                   interleave=I)
+                                   segments=S)
             payload = WarpDivPayload(
                 packed=enc.packed, chunk_ends=enc.chunk_ends, header_bytes=enc.header_bytes,
                 chunk_len=enc.chunk_len, p_ch=self.p_ch, batch=B, symbols_per_batch=N,
                 cdf_count=tables.M,
                 coding_fingerprint=coding_fingerprint(tables.digest, B, N, C, tables.M),
-                interleave=I,
+                segments=S,
             )
             return {"strings": [payload], "shape": tuple(y.shape[-2:])}
 
@@ -130,13 +130,13 @@ class FactorizedWarpDivCodec:
         with torch.no_grad():
             output_shape = (B, channels, *shape)
             medians = self._medians(entropy)
-            I = payload.interleave
+            S = payload.segments
             if medians.dtype == torch.float32:
                 return gaans.decode(payload.packed, tables, B, N, channels, self.p_ch,
                                     payload.packed.device, medians=medians.contiguous(),
-                                    interleave=I).reshape(output_shape)
+                                    segments=S).reshape(output_shape)
             symbols = gaans.decode(payload.packed, tables, B, N, channels, self.p_ch,
-                                   payload.packed.device, interleave=I).reshape(output_shape)
+                                   payload.packed.device, segments=S).reshape(output_shape)
             ext = entropy._extend_ndims(entropy._get_medians().detach(), len(shape))
             ext = ext.expand(B, *([-1] * (len(shape) + 1)))
             return entropy.dequantize(symbols, ext, ext.dtype)

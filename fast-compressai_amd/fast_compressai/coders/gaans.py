@@ -108,63 +108,79 @@ def _check_gaussian(B: int, N: int, device, scale_table: torch.Tensor,
             raise CoderInputError(f"{name} holds {t.numel()} values, expected {B * N}")
 
 
-# bpp budget of the automatic interleave: the extra flushed states may cost
-# up to this fraction of a chunk's expected payload
-INTERLEAVE_BUDGET = 0.01
+# bpp budget of the automatic segment count: the states and padding of the
+# added coding units may cost up to this fraction of a chunk's expected payload
+SEGMENT_BUDGET = 0.006
 
 
-def choose_interleave(tables: PreparedTables, B: int, N: int, C: int, P: int,
-                      budget: float = INTERLEAVE_BUDGET) -> int:
-    """rANS states per lane (1, 2 or 4) for a shape: the most whose extra
-    flushed states stay within ``budget`` of a chunk's expected payload
-    (``gaans_choose_interleave``, estimated from the tables' entropy)."""
-    key = (tables.digest, B, N, C, P, budget)
-    got = _interleaves.get(key)
+def _cu_count(device) -> int:
+    index = _index(device)
+    got = _cus.get(index)
     if got is None:
-        out = ctypes.c_int32(0)
-        _native.check(_native.lib().gaans_choose_interleave(tables.ref, B, N, C, P, float(budget),
-                                                            ctypes.byref(out)),
-                      "interleave choice")
-        got = int(out.value)
-        if len(_interleaves) > 1024:
-            _interleaves.clear()
-        _interleaves[key] = got
+        got = int(torch.cuda.get_device_properties(index).multi_processor_count)
+        _cus[index] = got
     return got
 
 
-_interleaves: dict = {}
+_cus: dict = {}
 
 
-def resolve_interleave(interleave: int | None, tables: PreparedTables, B: int, N: int, C: int,
-                       P: int) -> int:
-    """``interleave`` as given (1, 2 or 4), or the automatic choice for None."""
-    if interleave is None:
-        return choose_interleave(tables, B, N, C, P)
-    if interleave not in (1, 2, 4) or type(interleave) is not int:
-        raise CoderInputError("interleave must be 1, 2 or 4 rANS states per lane (or None)")
-    return interleave
+def choose_segments(tables: PreparedTables, B: int, N: int, C: int, P: int, device=None,
+                    budget: float = SEGMENT_BUDGET, target_units: int | None = None) -> int:
+    """Segments per chunk for a shape (``gaans_choose_segments``): enough
+    coding units to give every CU of ``device`` one (``target_units``, by
+    default its CU count), within ``budget`` of extra bytes (estimated from
+    the tables' entropy) and the shape's limit."""
+    if target_units is None:
+        target_units = _cu_count(device if device is not None else torch.cuda.current_device())
+    key = (tables.digest, B, N, C, P, budget, target_units)
+    got = _segments.get(key)
+    if got is None:
+        out = ctypes.c_int32(0)
+        _native.check(_native.lib().gaans_choose_segments(tables.ref, B, N, C, P, float(budget),
+                                                          int(target_units), ctypes.byref(out)),
+                      "segment choice")
+        got = int(out.value)
+        if len(_segments) > 1024:
+            _segments.clear()
+        _segments[key] = got
+    return got
+
+
+_segments: dict = {}
+
+
+def resolve_segments(segments: int | None, tables: PreparedTables, B: int, N: int, C: int,
+                     P: int, device=None) -> int:
+    """``segments`` as given (validated by the layout), or the automatic
+    choice for None."""
+    if segments is None:
+        return choose_segments(tables, B, N, C, P, device)
+    if type(segments) is not int or segments < 1:
+        raise CoderInputError("segments must be a positive int (or None for the automatic choice)")
+    return segments
 
 
 @dataclass(frozen=True)
 class EncodedChunks:
     packed: torch.Tensor      # uint8 [payload bytes]
-    chunk_ends: torch.Tensor  # uint32 [B, K] view of the header's chunk end offsets
+    chunk_ends: torch.Tensor  # uint32 [B, K S] view of the header's unit end offsets
     header_bytes: int
     chunk_len: int
     K: int
-    interleave: int = 1
+    segments: int = 1
 
 
 def encode(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,
            symbols: torch.Tensor | None = None, indexes: torch.Tensor | None = None,
            y: torch.Tensor | None = None, medians: torch.Tensor | None = None,
-           interleave: int = 1) -> EncodedChunks:
+           segments: int = 1) -> EncodedChunks:
     """Encode int32 ``symbols`` [B, N], or fp32 latents ``y`` with per-channel
     ``medians`` (quantize fused).  ``indexes`` None means channel-major
-    tables; ``interleave`` rANS states per lane (1, 2 or 4)."""
+    tables; ``segments`` coding units per chunk."""
     L = _native.lib()
-    I = interleave
-    lay = _native.layout(B, N, C, P, I)
+    S = segments
+    lay = _native.layout(B, N, C, P, S)
     index = _index(device)
     prev = _enter_device(index)
     try:
@@ -175,15 +191,15 @@ def encode(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,
         st.info_np[2] = 0
         if y is not None:
             rc = L.gaans_encode_latents(sp, y.data_ptr(), medians.data_ptr(), _ptr(indexes),
-                                        tables.ref, B, N, C, P, I, ws.data_ptr(), ws.numel(),
+                                        tables.ref, B, N, C, P, S, ws.data_ptr(), ws.numel(),
                                         st.ctrl_ptr, st.info_ptr)
         else:
             rc = L.gaans_encode_symbols(sp, symbols.data_ptr(), _ptr(indexes), tables.ref, B, N,
-                                        C, P, I, ws.data_ptr(), ws.numel(), st.ctrl_ptr,
+                                        C, P, S, ws.data_ptr(), ws.numel(), st.ctrl_ptr,
                                         st.info_ptr)
         if rc:
             _native.check(rc, "GA-ANS encode")
-        rc = L.gaans_encode_pack(sp, ws.data_ptr(), ws.numel(), tables.ref, B, N, C, P, I,
+        rc = L.gaans_encode_pack(sp, ws.data_ptr(), ws.numel(), tables.ref, B, N, C, P, S,
                                  out.data_ptr(), lay.max_payload_bytes)
         if rc:
             _native.check(rc, "GA-ANS pack")
@@ -201,16 +217,16 @@ def encode(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,
     if lay.max_payload_bytes - total > _CLONE_SLACK_BYTES:
         packed = packed.clone()
     K = lay.K
-    ends = packed[64: 64 + 4 * B * K].view(torch.uint32).view(B, K)
-    return EncodedChunks(packed, ends, lay.header_bytes, lay.chunk_len, K, I)
+    ends = packed[64: 64 + 4 * lay.U].view(torch.uint32).view(B, K * S)
+    return EncodedChunks(packed, ends, lay.header_bytes, lay.chunk_len, K, S)
 
 
 def decode(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int, P: int,
            device, *, indexes: torch.Tensor | None = None,
-           medians: torch.Tensor | None = None, interleave: int = 1) -> torch.Tensor:
+           medians: torch.Tensor | None = None, segments: int = 1) -> torch.Tensor:
     """Decode to int32 symbols [B, N], or (``medians`` given) to fp32 y_hat
-    [B, N] with dequantize fused; ``interleave`` as recorded in the payload."""
-    I = interleave
+    [B, N] with dequantize fused; ``segments`` as recorded in the payload."""
+    S = segments
     L = _native.lib()
     index = _index(device)
     prev = _enter_device(index)
@@ -221,12 +237,12 @@ def decode(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int,
         if medians is not None:
             out = torch.empty((B, N), dtype=torch.float32, device=packed.device)
             rc = L.gaans_decode_latents(sp, packed.data_ptr(), packed.numel(), _ptr(indexes),
-                                        tables.ref, medians.data_ptr(), B, N, C, P, I,
+                                        tables.ref, medians.data_ptr(), B, N, C, P, S,
                                         out.data_ptr(), st.ctrl_ptr, st.status_ptr)
         else:
             out = torch.empty((B, N), dtype=torch.int32, device=packed.device)
             rc = L.gaans_decode_symbols(sp, packed.data_ptr(), packed.numel(), _ptr(indexes),
-                                        tables.ref, B, N, C, P, I, out.data_ptr(), st.ctrl_ptr,
+                                        tables.ref, B, N, C, P, S, out.data_ptr(), st.ctrl_ptr,
                                         st.status_ptr)
         if rc:
             _native.check(rc, "GA-ANS decode")
@@ -245,13 +261,13 @@ def decode(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int,
 def encode_gaussian(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,
                     y: torch.Tensor, scales: torch.Tensor, scale_table: torch.Tensor,
                     scale_bound: float, means: torch.Tensor | None = None,
-                    interleave: int = 1) -> EncodedChunks:
+                    segments: int = 1) -> EncodedChunks:
     """GaussianConditional encode with index building and quantize fused:
     fp32 ``y``, ``scales`` (and ``means``) [B, N] channel-major; ``scale_table``
     fp32 on the device, non-decreasing, one entry per table."""
     L = _native.lib()
-    I = interleave
-    lay = _native.layout(B, N, C, P, I)
+    S = segments
+    lay = _native.layout(B, N, C, P, S)
     _check_gaussian(B, N, device, scale_table, y=y, scales=scales, means=means)
     index = _index(device)
     prev = _enter_device(index)
@@ -263,11 +279,11 @@ def encode_gaussian(tables: PreparedTables, B: int, N: int, C: int, P: int, devi
         st.info_np[2] = 0
         rc = L.gaans_encode_gaussian(sp, y.data_ptr(), _ptr(means), scales.data_ptr(),
                                      scale_table.data_ptr(), scale_table.numel(),
-                                     float(scale_bound), tables.ref, B, N, C, P, I,
+                                     float(scale_bound), tables.ref, B, N, C, P, S,
                                      ws.data_ptr(), ws.numel(), st.ctrl_ptr, st.info_ptr)
         if rc:
             _native.check(rc, "GA-ANS Gaussian encode")
-        rc = L.gaans_encode_pack(sp, ws.data_ptr(), ws.numel(), tables.ref, B, N, C, P, I,
+        rc = L.gaans_encode_pack(sp, ws.data_ptr(), ws.numel(), tables.ref, B, N, C, P, S,
                                  out.data_ptr(), lay.max_payload_bytes)
         if rc:
             _native.check(rc, "GA-ANS pack")
@@ -285,14 +301,14 @@ def encode_gaussian(tables: PreparedTables, B: int, N: int, C: int, P: int, devi
     if lay.max_payload_bytes - total > _CLONE_SLACK_BYTES:
         packed = packed.clone()
     K = lay.K
-    ends = packed[64: 64 + 4 * B * K].view(torch.uint32).view(B, K)
-    return EncodedChunks(packed, ends, lay.header_bytes, lay.chunk_len, K, I)
+    ends = packed[64: 64 + 4 * lay.U].view(torch.uint32).view(B, K * S)
+    return EncodedChunks(packed, ends, lay.header_bytes, lay.chunk_len, K, S)
 
 
 def decode_gaussian(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int, P: int,
                     device, *, scales: torch.Tensor, scale_table: torch.Tensor,
                     scale_bound: float, means: torch.Tensor | None = None,
-                    interleave: int = 1) -> torch.Tensor:
+                    segments: int = 1) -> torch.Tensor:
     """GaussianConditional decode with index building and dequantize fused:
     fp32 y_hat [B, N] = fp32(symbol) + mean (fp32(symbol) without means)."""
     L = _native.lib()
@@ -306,7 +322,7 @@ def decode_gaussian(packed: torch.Tensor, tables: PreparedTables, B: int, N: int
         out = torch.empty((B, N), dtype=torch.float32, device=packed.device)
         rc = L.gaans_decode_gaussian(sp, packed.data_ptr(), packed.numel(), scales.data_ptr(),
                                      _ptr(means), scale_table.data_ptr(), scale_table.numel(),
-                                     float(scale_bound), tables.ref, B, N, C, P, interleave,
+                                     float(scale_bound), tables.ref, B, N, C, P, segments,
                                      out.data_ptr(), st.ctrl_ptr, st.status_ptr)
         if rc:
             _native.check(rc, "GA-ANS Gaussian decode")

@@ -50,7 +50,7 @@ def _payload(enc, p_ch: int, B: int, N: int, C: int, tables) -> WarpDivPayload:
         packed=enc.packed, chunk_ends=enc.chunk_ends, header_bytes=enc.header_bytes,
         chunk_len=enc.chunk_len, p_ch=p_ch, batch=B, symbols_per_batch=N, cdf_count=tables.M,
         coding_fingerprint=coding_fingerprint(tables.digest, B, N, C, tables.M),
-        channels=None if C == tables.M else C, interleave=enc.interleave)
+        channels=None if C == tables.M else C, segments=enc.segments)
 
 
 class HyperpriorWarpDivCodec:
@@ -61,11 +61,11 @@ class HyperpriorWarpDivCodec:
     ``z = h_a(|y|)``)."""
 
     def __init__(self, model, p_ch: int, mean_scale: bool,
-                 interleave: int | None = None) -> None:
+                 segments: int | None = None) -> None:
         self.model = model
         self.p_ch = p_ch
         self.mean_scale = mean_scale
-        self.interleave = interleave  # rANS states per lane; None: chosen per shape
+        self.segments = segments  # coding units per chunk; None: chosen per shape
         self.backend = WarpDivBackend()
         self._cache = TableCache(capacity=4)
         eb, gc = model.entropy_bottleneck, model.gaussian_conditional
@@ -119,9 +119,9 @@ class HyperpriorWarpDivCodec:
         med = eb._get_medians().detach().reshape(-1).to(torch.float32).contiguous()
         B, C, N = int(z.size(0)), int(z.size(1)), int(z[0].numel())
         P = min(self.p_ch, C)
-        I = gaans.resolve_interleave(self.interleave, tables, B, N, C, P)
+        S = gaans.resolve_segments(self.segments, tables, B, N, C, P, z.device)
         enc = gaans.encode(tables, B, N, C, P, z.device, y=z.to(torch.float32).contiguous(),
-                           medians=med, interleave=I)
+                           medians=med, segments=S)
         # z_hat = dequantize(quantize(z)), as CompressAI's compress recomputes it
         m4 = med.reshape(1, C, 1, 1)
         z_hat = torch.round(z.to(torch.float32) - m4).int().to(torch.float32) + m4
@@ -140,7 +140,7 @@ class HyperpriorWarpDivCodec:
             raise CoderInputError("coding tables do not match the z payload")
         med = eb._get_medians().detach().reshape(-1).to(torch.float32).contiguous()
         z_hat = gaans.decode(payload.packed, tables, B, N, C, payload.p_ch, payload.packed.device,
-                             medians=med, interleave=payload.interleave)
+                             medians=med, segments=payload.segments)
         return z_hat.reshape(B, C, *shape)
 
     def _params(self, z_hat: torch.Tensor):
@@ -177,18 +177,18 @@ class HyperpriorWarpDivCodec:
             if not 1 <= self.p_ch <= C:
                 raise CoderInputError(f"P must be between 1 and {C} for this model")
             yf = y.to(torch.float32).contiguous()
-            I = gaans.resolve_interleave(self.interleave, tables, B, N, C, self.p_ch)
+            S = gaans.resolve_segments(self.segments, tables, B, N, C, self.p_ch, y.device)
             if self.fused_indexes:
                 enc = gaans.encode_gaussian(tables, B, N, C, self.p_ch, y.device, y=yf,
                                             scales=scales, scale_table=self._scale_table(y.device),
                                             scale_bound=self.scale_bound, means=means,
-                                            interleave=I)
+                                            segments=S)
             else:
                 idx = self._build_indexes(scales).reshape(B, N).contiguous()
                 sym = torch.round(yf - means if means is not None else yf).int()
                 enc = gaans.encode(tables, B, N, C, self.p_ch, y.device,
                                    symbols=sym.reshape(B, N).contiguous(), indexes=idx,
-                                   interleave=I)
+                                   segments=S)
             y_payload = _payload(enc, self.p_ch, B, N, C, tables)
             return {"strings": [y_payload, z_payload], "shape": tuple(z.shape[-2:])}
 
@@ -225,12 +225,12 @@ class HyperpriorWarpDivCodec:
                                               y_payload.packed.device, scales=scales,
                                               scale_table=self._scale_table(scales.device),
                                               scale_bound=self.scale_bound, means=means,
-                                              interleave=y_payload.interleave)
+                                              segments=y_payload.segments)
             else:
                 idx = self._build_indexes(scales).reshape(B, N).contiguous()
                 sym = gaans.decode(y_payload.packed, tables, B, N, C, self.p_ch,
                                    y_payload.packed.device, indexes=idx,
-                                   interleave=y_payload.interleave)
+                                   segments=y_payload.segments)
                 y_hat = sym.to(torch.float32)
                 if means is not None:
                     y_hat = y_hat + means.reshape(B, N)

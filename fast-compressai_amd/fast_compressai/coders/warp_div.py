@@ -9,15 +9,15 @@ payloads and ``CoderDependencyError`` for a missing library or device.
 
 Differences that follow from the new format:
 
-* ``format_id`` is ``"gaans-w64-v3"``; payloads of the reference's
+* ``format_id`` is ``"gaans-w64-v4"``; payloads of the reference's
   ``warpans-v2`` format are rejected.
-* ``interleave`` (keyword of ``encode``, field of the payload) is the number
-  of rANS states per lane, 1, 2 or 4; None (the default) lets the coder pick
-  the most whose extra flushed states stay within 1% of the expected payload
-  (``gaans.choose_interleave``).
-* ``WarpDivPayload.chunk_ends`` (uint32 ``[B, K]``, exposed also under the
-  reference's name ``max_rounds``) holds each chunk's end offset in the
-  payload data, not a round count.
+* ``segments`` (keyword of ``encode``, field of the payload) splits every
+  chunk of P channels into that many independently coded units (1..256);
+  None (the default) lets the coder pick enough units for the device's CUs
+  within 0.6% of extra payload (``gaans.choose_segments``).
+* ``WarpDivPayload.chunk_ends`` (uint32 ``[B, K S]``, exposed also under the
+  reference's name ``max_rounds``) holds each coding unit's end offset in
+  the payload data, not a round count.
 * Index range, index content and table identity are checked on the device
   (status word) instead of with host syncs and a SHA-256 of every index.
   ``coding_fingerprint`` is a SHA-256 of the table digest and the shapes, so
@@ -40,15 +40,16 @@ from .capabilities import warp_div_capability
 from .errors import CoderDependencyError, CoderInputError
 from .tables import PreparedTables, TableCache
 
-FORMAT_ID = "gaans-w64-v3"
-FORMAT_VERSION = 3
+FORMAT_ID = "gaans-w64-v4"
+FORMAT_VERSION = 4
+MAX_SEGMENTS = 256
 _HEADER_MAGIC = 0x31574147
 _FIXED_HEADER_BYTES = 64
 _SHA256_HEX = re.compile(r"[0-9a-f]{64}")
 
 
-def header_bytes_for(batch: int, chunks: int) -> int:
-    return (_FIXED_HEADER_BYTES + 8 * batch * chunks + 15) // 16 * 16
+def header_bytes_for(batch: int, units_per_row: int) -> int:
+    return (_FIXED_HEADER_BYTES + 8 * batch * units_per_row + 15) // 16 * 16
 
 
 @functools.lru_cache(maxsize=256)
@@ -74,13 +75,13 @@ class WarpDivPayload:
     format_id: str = FORMAT_ID
     format_version: int = FORMAT_VERSION
     channels: int | None = None
-    interleave: int = 1
+    segments: int = 1
 
     def __post_init__(self) -> None:
         if self.format_id != FORMAT_ID or self.format_version != FORMAT_VERSION:
             raise CoderInputError("unsupported warp_div payload format")
-        if type(self.interleave) is not int or self.interleave not in (1, 2, 4):
-            raise CoderInputError("warp_div interleave must be 1, 2 or 4")
+        if type(self.segments) is not int or not 1 <= self.segments <= MAX_SEGMENTS:
+            raise CoderInputError(f"warp_div segments must be in [1, {MAX_SEGMENTS}]")
         if (not isinstance(self.packed, torch.Tensor) or self.packed.device.type != "cuda"
                 or self.packed.dtype != torch.uint8 or not self.packed.is_contiguous()):
             raise CoderInputError("packed payload must be contiguous GPU uint8")
@@ -103,12 +104,12 @@ class WarpDivPayload:
             raise CoderInputError("warp_div channels must be a positive integer")
         if self.p_ch > channels or self.symbols_per_batch % channels:
             raise CoderInputError("warp_div payload P_ch/channel metadata is inconsistent")
-        expected_chunks = (channels + self.p_ch - 1) // self.p_ch
-        if tuple(self.chunk_ends.shape) != (self.batch, expected_chunks):
+        units = (channels + self.p_ch - 1) // self.p_ch * self.segments
+        if tuple(self.chunk_ends.shape) != (self.batch, units):
             raise CoderInputError("warp_div chunk table shape does not match payload metadata")
         if self.chunk_len != self.p_ch * (self.symbols_per_batch // channels):
             raise CoderInputError("warp_div chunk_len does not match P_ch and symbol dimensions")
-        if self.header_bytes != header_bytes_for(self.batch, expected_chunks):
+        if self.header_bytes != header_bytes_for(self.batch, units):
             raise CoderInputError("warp_div header size does not match chunk metadata")
         if self.header_bytes > self.packed.numel():
             raise CoderInputError("warp_div header exceeds packed payload size")
@@ -131,13 +132,14 @@ class WarpDivPayload:
 
     @property
     def max_rounds(self) -> torch.Tensor:
-        """The per-chunk table ``[B, K]`` under the reference's attribute name
-        (here: chunk end offsets, see ``chunk_ends``)."""
+        """The per-unit table ``[B, K S]`` under the reference's attribute
+        name (here: coding unit end offsets, see ``chunk_ends``)."""
         return self.chunk_ends
 
     @property
     def chunks(self) -> int:
-        return int(self.chunk_ends.shape[1])
+        """Chunks (of P channels) per batch row."""
+        return int(self.chunk_ends.shape[1]) // self.segments
 
     def to_bytes(self) -> bytes:
         """Host copy of the payload (header + chunk streams); the format is
@@ -148,7 +150,7 @@ class WarpDivPayload:
     def from_bytes(cls, data: bytes, device: torch.device | str = "cuda",
                    cdf_count: int | None = None) -> "WarpDivPayload":
         """Rebuild a payload from ``to_bytes`` output (header fields
-        B, N, C, P, K, chunk_len, M, table digest, interleave and chunk
+        B, N, C, P, K, chunk_len, M, table digest, segments and unit end
         offsets)."""
         if len(data) < _FIXED_HEADER_BYTES:
             raise CoderInputError("warp_div payload header is truncated")
@@ -156,22 +158,23 @@ class WarpDivPayload:
         if words[0] != _HEADER_MAGIC or words[1] != FORMAT_VERSION:
             raise CoderInputError("warp_div payload header has an unknown magic or version")
         B, N, C, P, K, chunk_len, M = words[2:9]
-        if B <= 0 or K <= 0:
+        S = words[12]
+        if B <= 0 or K <= 0 or not 1 <= S <= MAX_SEGMENTS:
             raise CoderInputError("warp_div payload header is inconsistent")
-        hb = header_bytes_for(B, K)
+        hb = header_bytes_for(B, K * S)
         if len(data) < hb:
             raise CoderInputError("warp_div payload header is truncated")
         if cdf_count is not None and cdf_count != M:
             raise CoderInputError("CDF count does not match payload metadata")
         digest = words[10] | (words[11] << 32)
-        ends = torch.frombuffer(bytearray(data[64: 64 + 4 * B * K]), dtype=torch.uint8)
+        ends = torch.frombuffer(bytearray(data[64: 64 + 4 * B * K * S]), dtype=torch.uint8)
         dev = torch.device(device)
         packed = torch.frombuffer(bytearray(data), dtype=torch.uint8).to(dev)
-        return cls(packed=packed, chunk_ends=ends.to(dev).view(torch.uint32).view(B, K),
+        return cls(packed=packed, chunk_ends=ends.to(dev).view(torch.uint32).view(B, K * S),
                    header_bytes=hb, chunk_len=chunk_len, p_ch=P, batch=B,
                    symbols_per_batch=N, cdf_count=M,
                    coding_fingerprint=coding_fingerprint(digest, B, N, C, M),
-                   channels=None if C == M else C, interleave=words[12])
+                   channels=None if C == M else C, segments=S)
 
 
 # field defaults of WarpDivPayload (for _from_encoder)
@@ -208,14 +211,14 @@ class WarpDivBackend:
         *,
         p_ch: int,
         channels: int | None = None,
-        interleave: int | None = None,
+        segments: int | None = None,
     ) -> WarpDivPayload:
         C = _validate_inputs(symbols, indexes, cdfs, cdf_sizes, offsets, p_ch, channels)
         tables = self.prepared_tables(cdfs, cdf_sizes, offsets)
         B, N = int(symbols.shape[0]), int(symbols.shape[1])
-        interleave = gaans.resolve_interleave(interleave, tables, B, N, C, p_ch)
+        segments = gaans.resolve_segments(segments, tables, B, N, C, p_ch, symbols.device)
         enc = gaans.encode(tables, B, N, C, p_ch, symbols.device, symbols=symbols,
-                           indexes=indexes, interleave=interleave)
+                           indexes=indexes, segments=segments)
         return WarpDivPayload._from_encoder(
             packed=enc.packed,
             chunk_ends=enc.chunk_ends,
@@ -227,7 +230,7 @@ class WarpDivBackend:
             cdf_count=int(cdfs.shape[0]),
             coding_fingerprint=coding_fingerprint(tables.digest, B, N, C, int(cdfs.shape[0])),
             channels=None if channels is None else int(channels),
-            interleave=interleave,
+            segments=segments,
         )
 
     def decode(
@@ -253,7 +256,7 @@ class WarpDivBackend:
             raise CoderInputError("coding tables or indexes do not match warp_div payload")
         return gaans.decode(payload.packed, tables, B, N, C, payload.p_ch,
                             payload.packed.device, indexes=indexes,
-                            interleave=payload.interleave)
+                            segments=payload.segments)
 
 
 def _validate_inputs(

@@ -2,8 +2,8 @@
 
 ``AccelerationConfig`` has the reference's fields, defaults and accepted
 values (``src/fast_compressai/config.py:14-101``), so configurations written
-for it load here (plus ``interleave``, the GA-ANS rANS states per lane: 1, 2,
-4 or None for the coder's choice): ``p_ch`` (spelled ``P`` in a mapping; latent channels per
+for it load here (plus ``segments``, the GA-ANS coding units per chunk: 1 to
+256, or None for the coder's choice): ``p_ch`` (spelled ``P`` in a mapping; latent channels per
 independently coded GA-ANS chunk) is a positive int or None, ``coder`` is
 ``"warp_div"`` (default) or ``"rans"``, ``budget`` a finite non-negative
 number, ``execution_mode`` ``"sequential"`` or ``"overlap"``, the paths and
@@ -46,8 +46,8 @@ _RULES: dict[str, tuple[Callable[[Any], bool], str]] = {
     "precision_config_path": (_optional_str, "precision_config_path must be a string or None"),
     "execution_mode": (lambda v: v in ("sequential", "overlap"),
                        "execution_mode must be 'sequential' or 'overlap'"),
-    "interleave": (lambda v: v is None or (type(v) is int and v in (1, 2, 4)),
-                   "interleave must be 1, 2 or 4 rANS states per lane, or None (automatic)"),
+    "segments": (lambda v: v is None or (type(v) is int and 1 <= v <= 256),
+                 "segments must be an int in [1, 256] (coding units per chunk), or None (automatic)"),
 }
 
 
@@ -60,9 +60,9 @@ class AccelerationConfig:
     profile_path: str | None = None
     precision_config_path: str | None = None
     execution_mode: str = "sequential"
-    # GA-ANS rANS states per lane (beyond the reference's fields); None lets
+    # GA-ANS coding units per chunk (beyond the reference's fields); None lets
     # the coder choose per shape
-    interleave: int | None = None
+    segments: int | None = None
 
     def __post_init__(self) -> None:
         for name, (rule, message) in _RULES.items():

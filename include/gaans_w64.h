@@ -36,13 +36,17 @@
  *    the stream has finished, or, with pinned host memory, once the
  *    launch's completion word is set (gaans_wait_host_word).
  *
- *  - `interleave` (I) is the number of rANS states per lane, 1, 2 or 4: step t
- *    of a chunk codes with its lanes' state slot t mod I, so I consecutive
- *    steps are independent chains (more instruction-level parallelism on the
- *    serial chain, 4 * 64 * (I - 1) more flushed bytes per chunk).  The
- *    payload header records it and decode must be called with the same value.
+ *  - `segments` (S, 1..256) splits every chunk of P channels into S
+ *    segments of whole 64-position steps (segment s: steps
+ *    [floor(s Tc / S), floor((s+1) Tc / S)) of a Tc-step chunk).  Each
+ *    segment is a coding unit with its own states, words and escapes, coded
+ *    by its own workgroup, so a launch of few long chunks uses S times more
+ *    CUs, for 4 * 64 more bytes per extra unit.  Every unit holds at least
+ *    one step: S <= the steps of a row's last (shortest) chunk.  The payload
+ *    header records S and decode must be called with the same value.
+ *    U = B * K * S coding units per call.
  *
- * Payload format "gaans-w64-v3": defined byte for byte by the CPU oracle,
+ * Payload format "gaans-w64-v4": defined byte for byte by the CPU oracle,
  * oracle/gaans_oracle.c.
  */
 #ifndef GAANS_W64_H
@@ -55,7 +59,7 @@
 extern "C" {
 #endif
 
-#define GAANS_ABI_VERSION 8
+#define GAANS_ABI_VERSION 9
 #define GAANS_CTRL_BYTES 256
 
 /* return codes */
@@ -69,18 +73,19 @@ extern "C" {
 #define GAANS_ST_INDEX 0x02u     /* table index out of range */
 #define GAANS_ST_HEADER 0x04u    /* payload header does not match the call */
 #define GAANS_ST_TABLES 0x08u    /* payload made with other tables, or bad table blob */
-#define GAANS_ST_CORRUPT 0x10u   /* chunk offsets or rANS stream inconsistent */
+#define GAANS_ST_CORRUPT 0x10u   /* unit offsets or rANS stream inconsistent */
 #define GAANS_ST_INDEXHASH 0x20u /* payload made with other indexes */
 #define GAANS_ST_SIZE 0x40u      /* payload would exceed the 4 GiB format limit */
 
 /* Shape of one coding call (pure host arithmetic, see gaans_get_layout). */
 typedef struct gaans_layout {
   int64_t B, N, C, P;     /* batch rows, symbols per row, channels, channels per chunk */
-  int64_t I;              /* interleave: rANS states per lane */
-  int64_t HW, K, chunk_len, BK;
+  int64_t S;              /* segments per chunk */
+  int64_t HW, K, chunk_len;
+  int64_t U;              /* coding units: B * K * S */
   int64_t header_bytes;   /* payload header size (multiple of 16) */
   int64_t max_payload_bytes; /* worst case: every symbol an escape with 8 nibbles */
-  int64_t cap_words;      /* staging words per chunk (worst case) */
+  int64_t cap_words;      /* staging words per unit (worst case) */
   int64_t workspace_bytes;
   /* byte offsets inside the encode workspace */
   int64_t ws_chunk_words, ws_chunk_status, ws_index_hash, ws_end_off, ws_info,
@@ -114,19 +119,23 @@ int gaans_abi_version(void);
 const char* gaans_last_error(void);
 
 /* Chunking and buffer sizes for B rows of N symbols, C channels, P per chunk
- * and `interleave` states per lane.  Requires B, N, C, P >= 1, N % C == 0,
- * P <= C, interleave in {1, 2, 4}. */
-int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
+ * and `segments` per chunk.  Requires B, N, C, P >= 1, N % C == 0, P <= C,
+ * 1 <= segments <= min(256, steps of a row's last chunk). */
+int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, int32_t segments,
                      gaans_layout* out);
 
-/* The interleave this library picks for a shape (pure host arithmetic): the
- * largest of 4, 2, 1 whose extra flushed states (4 bytes per lane and extra
- * slot in use) stay within `budget` (a fraction: 0.01 = 1%) of a chunk's
- * expected payload, estimated as chunk symbols * tables->mean_bits / 8 plus
- * the states.  No counterpart in the reference (one 64-bit state per lane,
+/* The segments per chunk this library picks for a shape (pure host
+ * arithmetic): the most that (a) the shape allows, (b) are needed for
+ * B * K * S >= target_units (no limit when target_units <= 0; callers pass
+ * the device's CU count), and (c) keep the extra bytes of the added units
+ * (3.125 bytes per lane plus 4, as measured: an added unit's final states
+ * less what its fresh states absorb, a pad and a partly used escape word)
+ * within `budget` (a fraction: 0.006 = 0.6%) of a chunk's expected payload,
+ * estimated as chunk symbols * tables->mean_bits / 8 plus its states.  No
+ * counterpart in the reference (one chunk is one warp's serial loop,
  * warp_ans_kernel_v2.cu:121-126). */
-int gaans_choose_interleave(const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
-                            int64_t P, double budget, int32_t* interleave);
+int gaans_choose_segments(const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
+                          int64_t P, double budget, int64_t target_units, int32_t* segments);
 
 /* ---- table upload (host memory) ----------------------------------------- */
 
@@ -152,8 +161,8 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes,
 
 /* ---- encode ------------------------------------------------------------- */
 
-/* Stage 1: code every chunk into `workspace_dev` (layout->workspace_bytes).
- * The launch's last block scans the chunk sizes into payload offsets and
+/* Stage 1: code every unit into `workspace_dev` (layout->workspace_bytes).
+ * The launch's last block scans the unit sizes into payload offsets and
  * writes info = {u64 payload bytes incl. header, u64 status} both to the
  * workspace (at layout->ws_info) and, when info_out is not NULL, to
  * info_out[0..1] (device or pinned host memory), and the completion word
@@ -164,7 +173,7 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes,
  * src/fast_compressai/coders/cuda/warp_ans_kernel_v2.cu:183-273. */
 int gaans_encode_symbols(void* stream, const int32_t* symbols_dev,
                          const int32_t* indexes_dev, const gaans_tables* tables,
-                         int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
+                         int64_t B, int64_t N, int64_t C, int64_t P, int32_t segments,
                          void* workspace_dev, int64_t workspace_bytes, void* ctrl_dev,
                          uint64_t* info_out);
 
@@ -173,7 +182,7 @@ int gaans_encode_symbols(void* stream, const int32_t* symbols_dev,
  * Reference: FactorizedWarpDivCodec.compress, factorized.py:46-59. */
 int gaans_encode_latents(void* stream, const float* y_dev, const float* medians_dev,
                          const int32_t* indexes_dev, const gaans_tables* tables,
-                         int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
+                         int64_t B, int64_t N, int64_t C, int64_t P, int32_t segments,
                          void* workspace_dev, int64_t workspace_bytes, void* ctrl_dev,
                          uint64_t* info_out);
 
@@ -193,19 +202,19 @@ int gaans_encode_latents(void* stream, const float* y_dev, const float* medians_
 int gaans_encode_gaussian(void* stream, const float* y_dev, const float* means_dev,
                           const float* scales_dev, const float* scale_table_dev,
                           int32_t n_scales, float scale_bound, const gaans_tables* tables,
-                          int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
+                          int64_t B, int64_t N, int64_t C, int64_t P, int32_t segments,
                           void* workspace_dev, int64_t workspace_bytes, void* ctrl_dev,
                           uint64_t* info_out);
 
-/* Stage 2: write the payload (header + chunks) to out_dev.  May be enqueued
+/* Stage 2: write the payload (header + units) to out_dev.  May be enqueued
  * right after stage 1 on the same stream into a buffer of
  * layout->max_payload_bytes, or after the caller has read the payload size
- * into an exact buffer; chunks that would not fit out_bytes are skipped.
+ * into an exact buffer; units that would not fit out_bytes are skipped.
  * Reference: write_warp_tight_header_kernel and warp_pack_tight_payload_kernel,
  * warp_ans_kernel_v2.cu:274-296. */
 int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace_bytes,
                       const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
-                      int64_t P, int32_t interleave, uint8_t* out_dev, int64_t out_bytes);
+                      int64_t P, int32_t segments, uint8_t* out_dev, int64_t out_bytes);
 
 /* Stage 1 and stage 2 of gaans_encode_symbols in one call that allocates
  * nothing and takes no workspace or control block: both live in a static
@@ -226,7 +235,7 @@ int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace
 #define GAANS_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
 int gaans_encode_symbols_noalloc(void* stream, const int32_t* symbols_dev,
                                  const int32_t* indexes_dev, const gaans_tables* tables,
-                                 int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
+                                 int64_t B, int64_t N, int64_t C, int64_t P, int32_t segments,
                                  uint8_t* out_dev, int64_t out_bytes, uint64_t* info_out);
 
 /* ---- decode ------------------------------------------------------------- */
@@ -238,7 +247,7 @@ int gaans_encode_symbols_noalloc(void* stream, const int32_t* symbols_dev,
  * Reference: decode_with_indexes_warp_cuda, warp_ans_kernel.cu:477-544. */
 int gaans_decode_symbols(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
                          const int32_t* indexes_dev, const gaans_tables* tables,
-                         int64_t B, int64_t N, int64_t C, int64_t P, int32_t interleave,
+                         int64_t B, int64_t N, int64_t C, int64_t P, int32_t segments,
                          int32_t* out_dev, void* ctrl_dev, uint32_t* status_out);
 
 /* Decode with CompressAI's dequantize fused in: y_hat = fp32(symbol) +
@@ -246,7 +255,7 @@ int gaans_decode_symbols(void* stream, const uint8_t* payload_dev, int64_t paylo
 int gaans_decode_latents(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
                          const int32_t* indexes_dev, const gaans_tables* tables,
                          const float* medians_dev, int64_t B, int64_t N, int64_t C,
-                         int64_t P, int32_t interleave, float* y_hat_dev, void* ctrl_dev,
+                         int64_t P, int32_t segments, float* y_hat_dev, void* ctrl_dev,
                          uint32_t* status_out);
 
 /* Decode a gaans_encode_gaussian payload with the same scales, means and
@@ -257,7 +266,7 @@ int gaans_decode_gaussian(void* stream, const uint8_t* payload_dev, int64_t payl
                           const float* scales_dev, const float* means_dev,
                           const float* scale_table_dev, int32_t n_scales, float scale_bound,
                           const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
-                          int64_t P, int32_t interleave, float* y_hat_dev, void* ctrl_dev,
+                          int64_t P, int32_t segments, float* y_hat_dev, void* ctrl_dev,
                           uint32_t* status_out);
 
 /* ---- CompressAI Rans64 bitstreams ------------------------------------------ */

@@ -3,22 +3,26 @@
  * (see gaans_oracle.h): the product path never links or calls this file.
  *
  * ===========================================================================
- * The wave64 GA-ANS payload format, "gaans-w64-v3"
+ * The wave64 GA-ANS payload format, "gaans-w64-v4"
  * ===========================================================================
- * Coding parameters: 16-bit CDF precision; I = 1, 2 or 4 interleaved 32-bit
- * rANS states per lane ("interleave"), x in [2^16, 2^32), initial state
- * 2^16; 16-bit renormalisation words; 4-bit escape nibbles; 64 lanes per
- * chunk.
+ * Coding parameters: 16-bit CDF precision; one 32-bit rANS state per lane,
+ * x in [2^16, 2^32), initial state 2^16; 16-bit renormalisation words;
+ * 4-bit escape nibbles; 64 lanes per coding unit.
  *
  * Chunking.  A batch row holds N symbols, channel-major: C channels of
  * HW = N / C positions.  P channels form one chunk, K = ceil(C / P) chunks per
- * row, chunk_len = P * HW.  Chunk g = b * K + k covers positions
- * [k*chunk_len, min((k+1)*chunk_len, N)) of row b; len = its symbol count.
- * A = min(64, len) lanes are active; lane l owns positions l + 64 t (t >= 0)
- * of the chunk, so the 64 lanes of one step read 64 consecutive positions.
- * Step t codes with state slot t mod I of every lane (T = ceil(len / 64)
- * steps; slots >= min(I, T) are never used), so consecutive steps of a lane
- * are independent rANS chains and only the word order ties them together.
+ * row, chunk_len = P * HW; chunk k of row b covers positions
+ * [k*chunk_len, min((k+1)*chunk_len, N)), clen of them, Tc = ceil(clen / 64)
+ * steps of 64 positions.  Each chunk is split into S segments
+ * ("segments per chunk", 1 <= S <= min(256, Tc of every chunk)): segment s
+ * covers the steps [floor(s Tc / S), floor((s+1) Tc / S)) of the chunk, i.e.
+ * positions [64 floor(s Tc / S), min(64 floor((s+1) Tc / S), clen)).  A
+ * segment is a coding unit: unit g = (b K + k) S + s, U = B K S units, each
+ * coded on its own (own states, own word stream, own escape section), so
+ * the units of a chunk can be coded in parallel.  In a unit of len symbols
+ * A = min(64, len) lanes are active; lane l owns positions l + 64 t
+ * (t >= 0) of the unit, so the 64 lanes of one step read 64 consecutive
+ * positions; T = ceil(len / 64) steps.
  *
  * Symbol mapping (CompressAI's escape scheme; reference
  * warp_ans_kernel_v2.cu:139-169).  With table tb = index of the position,
@@ -35,37 +39,35 @@
  *   decode: cum = x & 0xffff; v = the symbol with cdf[v] <= cum < cdf[v+1];
  *           x = freq * (x >> 16) + cum - start;
  *           if x < 2^16: x = (x << 16) | next word
- * (x is the lane's state slot t mod I).
  * The encoder walks steps t = T-1 .. 0; the words emitted in one step form
- * a group, ordered by lane index, and each group is PREPENDED to the chunk's
+ * a group, ordered by lane index, and each group is PREPENDED to the unit's
  * word stream.  The decoder reads the stream forwards: at step t the lanes
  * that need a refill take the next words in lane order.
  *
- * Escape section.  The escapes of a chunk, in position order, form a nibble
+ * Escape section.  The escapes of a unit, in position order, form a nibble
  * sequence: for each escape its count n, then its n nibbles of raw, low
  * nibble first (the same 4 + 4n bits as CompressAI's bypass coding).
  * Nibble i of the sequence is bits 4 (i & 3) of escape word i >> 2; unused
  * nibbles of the last word are zero; Q = ceil(nibbles / 4) words.
  *
- * Chunk bytes: the final states, min(I, T) x A u32 LE (slot 0 of lanes
- * 0 .. A-1, then slot 1, ...), the W words of the rANS stream (u16 LE), one
- * zero u16 if W + Q is odd, then the Q escape words in REVERSE order (escape
- * word 0 is the last u16 of the chunk), so a decoder finds every escape from
- * the chunk's end without knowing W.  After decoding, every state slot of
- * every active lane is back at 2^16, the stream, the pad and the
- * escape words have all been consumed, and every count is the minimal one of
- * its raw value (raw ? msb(raw) / 4 + 1 : 0, hence <= 8).
+ * Unit bytes: the A final states (u32 LE, lane order), the W words of the
+ * rANS stream (u16 LE), one zero u16 if W + Q is odd, then the Q escape
+ * words in REVERSE order (escape word 0 is the last u16 of the unit), so a
+ * decoder finds every escape from the unit's end without knowing W.  After
+ * decoding, every active lane's state is back at 2^16, the stream, the pad
+ * and the escape words have all been consumed, and every count is the
+ * minimal one of its raw value (raw ? msb(raw) / 4 + 1 : 0, hence <= 8).
  *
  * Header (u32 LE words):
- *   0 magic 0x31574147 ("GAW1")   1 version (3)     2 B    3 N
+ *   0 magic 0x31574147 ("GAW1")   1 version (4)     2 B    3 N
  *   4 C    5 P    6 K    7 chunk_len    8 M (table count)
  *   9 params 0x00041040 (lanes 64 | precision 16 << 8 | bypass 4 << 16)
- *   10,11 table digest (FNV-1a 64, low word first)   12 interleave I
+ *   10,11 table digest (FNV-1a 64, low word first)   12 segments S
  *   13..15 zero
- *   then B*K u32 chunk end offsets (bytes, relative to the data start),
- *   then B*K u32 index hashes; zero padding to a multiple of 16 bytes.
- * Data start = header bytes; chunk g spans [end[g-1], end[g]) of the data.
- * Index hash of a chunk: sum over its positions p (0-based in the chunk) of
+ *   then U u32 unit end offsets (bytes, relative to the data start),
+ *   then U u32 index hashes; zero padding to a multiple of 16 bytes.
+ * Data start = header bytes; unit g spans [end[g-1], end[g]) of the data.
+ * Index hash of a unit: sum over its positions p (0-based in the unit) of
  *   fmix32((p * 0x9E3779B9 + tb + 1) mod 2^32), mod 2^32, with fmix32 the
  *   finaliser of MurmurHash3 (Appleby): h ^= h >> 16; h *= 0x85EBCA6B;
  *   h ^= h >> 13; h *= 0xC2B2AE35; h ^= h >> 16 (mod 2^32).  The finaliser is
@@ -309,37 +311,55 @@ int rans64_ref_decode(const uint32_t* words, int64_t n_words,
 #define W_LANES 64
 #define W_L ((uint32_t)1 << 16)
 #define W_MAGIC 0x31574147u
-#define W_VERSION 3u
+#define W_VERSION 4u
 #define W_PARAMS 0x00041040u
 #define W_FIXED_WORDS 16
 
-#define W_MAX_I 4
+#define W_MAX_SEGMENTS 256
 
 typedef struct {
-  int32_t K, chunk_len, HW, I;
-  int64_t BK, header_bytes;
+  int32_t N, K, chunk_len, HW, S;
+  int64_t U, header_bytes;
 } w_layout;
 
-static int w_layout_of(int32_t B, int32_t N, int32_t C, int32_t P, int32_t I, w_layout* L) {
+static int w_layout_of(int32_t B, int32_t N, int32_t C, int32_t P, int32_t S, w_layout* L) {
   if (B <= 0 || N <= 0 || C <= 0 || P <= 0 || P > C || N % C != 0)
     return GAANS_REF_EINVAL;
-  if (I != 1 && I != 2 && I != 4) return GAANS_REF_EINVAL;
-  L->I = I;
+  L->N = N;
   L->HW = N / C;
   L->K = (C + P - 1) / P;
   if ((int64_t)P * L->HW > INT32_MAX) return GAANS_REF_EINVAL;
   L->chunk_len = P * L->HW;
-  L->BK = (int64_t)B * L->K;
-  L->header_bytes = ((4 * W_FIXED_WORDS + 8 * L->BK) + 15) / 16 * 16;
+  /* every segment holds at least one step: S <= the steps of the last
+   * (shortest) chunk of a row */
+  int64_t last = (int64_t)N - (int64_t)(L->K - 1) * L->chunk_len;
+  if (S < 1 || S > W_MAX_SEGMENTS || S > (last + W_LANES - 1) / W_LANES) return GAANS_REF_EINVAL;
+  L->S = S;
+  L->U = (int64_t)B * L->K * S;
+  L->header_bytes = ((4 * W_FIXED_WORDS + 8 * L->U) + 15) / 16 * 16;
   return GAANS_REF_OK;
 }
 
-int64_t gaans_ref_max_payload_bytes(int32_t B, int32_t N, int32_t C, int32_t P, int32_t I) {
+/* row b and the positions [*start, *start + *len) of unit g */
+static void w_unit(const w_layout* L, int64_t g, int64_t* b, int64_t* start, int32_t* len) {
+  int64_t per_row = (int64_t)L->K * L->S;
+  *b = g / per_row;
+  int64_t r = g % per_row, k = r / L->S, s = r % L->S;
+  int64_t cs = k * (int64_t)L->chunk_len;
+  int64_t ce = cs + L->chunk_len < L->N ? cs + L->chunk_len : L->N;
+  int64_t Tc = (ce - cs + W_LANES - 1) / W_LANES;
+  int64_t t0 = s * Tc / L->S, t1 = (s + 1) * Tc / L->S;
+  int64_t e = cs + W_LANES * t1 < ce ? cs + W_LANES * t1 : ce;
+  *start = cs + W_LANES * t0;
+  *len = (int32_t)(e - *start);
+}
+
+int64_t gaans_ref_max_payload_bytes(int32_t B, int32_t N, int32_t C, int32_t P, int32_t S) {
   w_layout L;
-  if (w_layout_of(B, N, C, P, I, &L)) return -1;
-  /* per symbol at most one word and 9 escape nibbles; per chunk 64 I states,
+  if (w_layout_of(B, N, C, P, S, &L)) return -1;
+  /* per symbol at most one word and 9 escape nibbles; per unit 64 states,
    * a pad word and a partly used escape word */
-  return L.header_bytes + (int64_t)B * N * 7 + L.BK * (4 * W_LANES * I + 8);
+  return L.header_bytes + (int64_t)B * N * 7 + L.U * (4 * W_LANES + 8);
 }
 
 /* MurmurHash3's 32-bit finaliser (Austin Appleby, public domain) */
@@ -352,7 +372,7 @@ static uint32_t fmix32(uint32_t h) {
   return h;
 }
 
-/* index hash term of chunk position p with table tb */
+/* index hash term of unit position p with table tb */
 static uint32_t index_term(int64_t p, int32_t tb) {
   return fmix32((uint32_t)p * 0x9E3779B9u + (uint32_t)tb + 1u);
 }
@@ -393,7 +413,7 @@ static uint32_t get_u32(const uint8_t* p) {
   return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
 }
 
-/* nibble sequence of a chunk's escape section (grows as needed) */
+/* nibble sequence of a unit's escape section (grows as needed) */
 typedef struct {
   uint8_t* nib;
   int64_t n, cap;
@@ -411,13 +431,12 @@ static int w_nibs_push(w_nibs* z, uint32_t v) {
   return GAANS_REF_OK;
 }
 
-static int w_encode_chunk(const int32_t* sym, const int32_t* idx_row, int64_t start,
-                          int32_t len, int32_t HW, int32_t I, const int32_t* cdfs, int32_t M,
+static int w_encode_unit(const int32_t* sym, const int32_t* idx_row, int64_t start,
+                          int32_t len, int32_t HW, const int32_t* cdfs, int32_t M,
                           int32_t Lmax, const int32_t* sizes, const int32_t* offsets,
                           uint8_t** out, int64_t* out_bytes, uint32_t* hash_out) {
   int A = len < W_LANES ? len : W_LANES;
   int T = (len + W_LANES - 1) / W_LANES;
-  int SL = T < I ? T : I; /* state slots in use */
   uint32_t* st_ = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)(2 * (int64_t)len + 1));
   int64_t cap = (int64_t)len + 2;
   uint16_t* buf = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)cap);
@@ -446,14 +465,11 @@ static int w_encode_chunk(const int32_t* sym, const int32_t* idx_row, int64_t st
       if (rc) goto fail;
     }
   }
-  /* pass 2: rANS, steps last to first, one word group per step; step t
-   * codes with state slot t mod I */
-  uint32_t xs[W_MAX_I][W_LANES];
-  for (int k = 0; k < W_MAX_I; ++k)
-    for (int l = 0; l < W_LANES; ++l) xs[k][l] = W_L;
+  /* pass 2: rANS, steps last to first, one word group per step */
+  uint32_t x[W_LANES];
+  for (int l = 0; l < W_LANES; ++l) x[l] = W_L;
   int64_t wp = cap;
   for (int t = T - 1; t >= 0; --t) {
-    uint32_t* x = xs[t % I];
     int emit[W_LANES];
     int cnt = 0;
     for (int l = 0; l < W_LANES; ++l) {
@@ -479,13 +495,11 @@ static int w_encode_chunk(const int32_t* sym, const int32_t* idx_row, int64_t st
     int64_t Q = (z.n + 3) / 4;
     int64_t pad = (W + Q) & 1;
     int64_t U = W + pad + Q;
-    int64_t nst = (int64_t)SL * A; /* final states: slot-major, A lanes each */
-    int64_t bytes = 4 * nst + 2 * U;
+    int64_t bytes = 4 * (int64_t)A + 2 * U;
     uint8_t* o = (uint8_t*)calloc((size_t)bytes, 1);
     if (!o) { rc = GAANS_REF_ESPACE; goto fail; }
-    for (int k = 0; k < SL; ++k)
-      for (int l = 0; l < A; ++l) put_u32(o + 4 * ((int64_t)k * A + l), xs[k][l]);
-    uint8_t* w16 = o + 4 * nst;
+    for (int l = 0; l < A; ++l) put_u32(o + 4 * l, x[l]);
+    uint8_t* w16 = o + 4 * (int64_t)A;
     for (int64_t k = 0; k < W; ++k) {
       w16[2 * k] = (uint8_t)buf[wp + k];
       w16[2 * k + 1] = (uint8_t)(buf[wp + k] >> 8);
@@ -493,7 +507,7 @@ static int w_encode_chunk(const int32_t* sym, const int32_t* idx_row, int64_t st
     for (int64_t j = 0; j < Q; ++j) {
       uint32_t e = 0;
       for (int q = 0; q < 4 && 4 * j + q < z.n; ++q) e |= (uint32_t)z.nib[4 * j + q] << (4 * q);
-      int64_t pos = U - 1 - j; /* escape word j, counted from the chunk end */
+      int64_t pos = U - 1 - j; /* escape word j, counted from the unit end */
       w16[2 * pos] = (uint8_t)e;
       w16[2 * pos + 1] = (uint8_t)(e >> 8);
     }
@@ -509,31 +523,31 @@ fail:
 }
 
 int gaans_ref_encode(const int32_t* symbols, const int32_t* indexes,
-                     int32_t B, int32_t N, int32_t C, int32_t P, int32_t I,
+                     int32_t B, int32_t N, int32_t C, int32_t P, int32_t S,
                      const int32_t* cdfs, int32_t M, int32_t Lmax,
                      const int32_t* cdf_sizes, const int32_t* offsets,
                      uint8_t* out, int64_t out_cap, int64_t* out_len) {
   w_layout L;
-  int rc = w_layout_of(B, N, C, P, I, &L);
+  int rc = w_layout_of(B, N, C, P, S, &L);
   if (rc) return rc;
   rc = check_tables(cdfs, M, Lmax, cdf_sizes);
   if (rc) return rc;
-  uint8_t** chunks = (uint8_t**)calloc((size_t)L.BK, sizeof(uint8_t*));
-  int64_t* cbytes = (int64_t*)calloc((size_t)L.BK, sizeof(int64_t));
-  uint32_t* hashes = (uint32_t*)calloc((size_t)L.BK, sizeof(uint32_t));
-  if (!chunks || !cbytes || !hashes) { rc = GAANS_REF_ESPACE; goto done; }
-  for (int64_t g = 0; g < L.BK; ++g) {
-    int64_t b = g / L.K, k = g % L.K;
-    int64_t start = k * (int64_t)L.chunk_len;
-    int64_t end = start + L.chunk_len < N ? start + L.chunk_len : N;
-    rc = w_encode_chunk(symbols + b * (int64_t)N, indexes ? indexes + b * (int64_t)N : NULL,
-                        start, (int32_t)(end - start), L.HW, I, cdfs, M, Lmax, cdf_sizes,
-                        offsets, &chunks[g], &cbytes[g], &hashes[g]);
+  uint8_t** units = (uint8_t**)calloc((size_t)L.U, sizeof(uint8_t*));
+  int64_t* cbytes = (int64_t*)calloc((size_t)L.U, sizeof(int64_t));
+  uint32_t* hashes = (uint32_t*)calloc((size_t)L.U, sizeof(uint32_t));
+  if (!units || !cbytes || !hashes) { rc = GAANS_REF_ESPACE; goto done; }
+  for (int64_t g = 0; g < L.U; ++g) {
+    int64_t b, start;
+    int32_t len;
+    w_unit(&L, g, &b, &start, &len);
+    rc = w_encode_unit(symbols + b * (int64_t)N, indexes ? indexes + b * (int64_t)N : NULL,
+                       start, len, L.HW, cdfs, M, Lmax, cdf_sizes, offsets, &units[g],
+                       &cbytes[g], &hashes[g]);
     if (rc) goto done;
   }
   {
     int64_t total = L.header_bytes;
-    for (int64_t g = 0; g < L.BK; ++g) total += cbytes[g];
+    for (int64_t g = 0; g < L.U; ++g) total += cbytes[g];
     if (total - L.header_bytes > (int64_t)UINT32_MAX) { rc = GAANS_REF_ESPACE; goto done; }
     if (total > out_cap) { rc = GAANS_REF_ESPACE; goto done; }
     memset(out, 0, (size_t)L.header_bytes);
@@ -541,22 +555,22 @@ int gaans_ref_encode(const int32_t* symbols, const int32_t* indexes,
     uint32_t hw[W_FIXED_WORDS] = {W_MAGIC, W_VERSION, (uint32_t)B, (uint32_t)N,
                                   (uint32_t)C, (uint32_t)P, (uint32_t)L.K,
                                   (uint32_t)L.chunk_len, (uint32_t)M, W_PARAMS,
-                                  (uint32_t)digest, (uint32_t)(digest >> 32), (uint32_t)I,
+                                  (uint32_t)digest, (uint32_t)(digest >> 32), (uint32_t)S,
                                   0, 0, 0};
     for (int w = 0; w < W_FIXED_WORDS; ++w) put_u32(out + 4 * w, hw[w]);
     int64_t pos = 0;
-    for (int64_t g = 0; g < L.BK; ++g) {
-      memcpy(out + L.header_bytes + pos, chunks[g], (size_t)cbytes[g]);
+    for (int64_t g = 0; g < L.U; ++g) {
+      memcpy(out + L.header_bytes + pos, units[g], (size_t)cbytes[g]);
       pos += cbytes[g];
       put_u32(out + 4 * W_FIXED_WORDS + 4 * g, (uint32_t)pos);
-      put_u32(out + 4 * W_FIXED_WORDS + 4 * L.BK + 4 * g, hashes[g]);
+      put_u32(out + 4 * W_FIXED_WORDS + 4 * L.U + 4 * g, hashes[g]);
     }
     *out_len = total;
   }
 done:
-  if (chunks)
-    for (int64_t g = 0; g < L.BK; ++g) free(chunks[g]);
-  free(chunks);
+  if (units)
+    for (int64_t g = 0; g < L.U; ++g) free(units[g]);
+  free(units);
   free(cbytes);
   free(hashes);
   return rc;
@@ -564,12 +578,12 @@ done:
 
 int gaans_ref_decode(const uint8_t* payload, int64_t payload_len,
                      const int32_t* indexes,
-                     int32_t B, int32_t N, int32_t C, int32_t P, int32_t I,
+                     int32_t B, int32_t N, int32_t C, int32_t P, int32_t S,
                      const int32_t* cdfs, int32_t M, int32_t Lmax,
                      const int32_t* cdf_sizes, const int32_t* offsets,
                      int32_t* out_symbols) {
   w_layout L;
-  int rc = w_layout_of(B, N, C, P, I, &L);
+  int rc = w_layout_of(B, N, C, P, S, &L);
   if (rc) return rc;
   rc = check_tables(cdfs, M, Lmax, cdf_sizes);
   if (rc) return rc;
@@ -577,7 +591,7 @@ int gaans_ref_decode(const uint8_t* payload, int64_t payload_len,
   uint64_t digest = gaans_ref_table_digest(cdfs, M, Lmax, cdf_sizes, offsets);
   uint32_t want[13] = {W_MAGIC, W_VERSION, (uint32_t)B, (uint32_t)N, (uint32_t)C,
                        (uint32_t)P, (uint32_t)L.K, (uint32_t)L.chunk_len, (uint32_t)M,
-                       W_PARAMS, (uint32_t)digest, (uint32_t)(digest >> 32), (uint32_t)I};
+                       W_PARAMS, (uint32_t)digest, (uint32_t)(digest >> 32), (uint32_t)S};
   for (int w = 0; w < 10; ++w)
     if (get_u32(payload + 4 * w) != want[w]) return GAANS_REF_ECORRUPT;
   for (int w = 10; w < 12; ++w)
@@ -586,18 +600,16 @@ int gaans_ref_decode(const uint8_t* payload, int64_t payload_len,
   const uint8_t* data = payload + L.header_bytes;
   int64_t data_len = payload_len - L.header_bytes;
   uint32_t prev = 0;
-  for (int64_t g = 0; g < L.BK; ++g) {
+  for (int64_t g = 0; g < L.U; ++g) {
     uint32_t endo = get_u32(payload + 4 * W_FIXED_WORDS + 4 * g);
-    uint32_t want_hash = get_u32(payload + 4 * W_FIXED_WORDS + 4 * L.BK + 4 * g);
+    uint32_t want_hash = get_u32(payload + 4 * W_FIXED_WORDS + 4 * L.U + 4 * g);
     if (endo < prev || (int64_t)endo > data_len) return GAANS_REF_ECORRUPT;
-    int64_t b = g / L.K, k = g % L.K;
-    int64_t start = k * (int64_t)L.chunk_len;
-    int64_t end = start + L.chunk_len < N ? start + L.chunk_len : N;
-    int32_t len = (int32_t)(end - start);
+    int64_t b, start;
+    int32_t len;
+    w_unit(&L, g, &b, &start, &len);
     int A = len < W_LANES ? len : W_LANES;
     int T = (len + W_LANES - 1) / W_LANES;
-    int SL = T < I ? T : I;
-    int64_t nst = (int64_t)SL * A;
+    int64_t nst = A;
     const uint8_t* cp = data + prev;
     int64_t cbytes = (int64_t)endo - prev;
     if (cbytes < 4 * nst || ((cbytes - 4 * nst) & 3)) return GAANS_REF_ECORRUPT;
@@ -605,15 +617,12 @@ int gaans_ref_decode(const uint8_t* payload, int64_t payload_len,
     const uint8_t* wbase = cp + 4 * nst;
     int64_t rp = 0;  /* stream words read */
     int64_t eq = 0;  /* escape nibbles read */
-    uint32_t xs[W_MAX_I][W_LANES];
-    for (int k = 0; k < W_MAX_I; ++k)
-      for (int l = 0; l < W_LANES; ++l)
-        xs[k][l] = (k < SL && l < A) ? get_u32(cp + 4 * ((int64_t)k * A + l)) : W_L;
+    uint32_t x[W_LANES];
+    for (int l = 0; l < W_LANES; ++l) x[l] = l < A ? get_u32(cp + 4 * (int64_t)l) : W_L;
     const int32_t* idx_row = indexes ? indexes + b * (int64_t)N : NULL;
     int32_t* orow = out_symbols + b * (int64_t)N;
     uint32_t hash = 0;
     for (int t = 0; t < T; ++t) {
-      uint32_t* x = xs[t % I];
       int need[W_LANES];
       for (int l = 0; l < W_LANES; ++l) {
         int64_t p = l + (int64_t)W_LANES * t;
@@ -635,7 +644,7 @@ int gaans_ref_decode(const uint8_t* payload, int64_t payload_len,
           for (int j = 0; j < 9; ++j) nib[j] = 0;
           int n = 0;
           for (int j = 0; j <= n; ++j) {
-            int64_t wi = (eq + j) >> 2; /* escape word, from the chunk end */
+            int64_t wi = (eq + j) >> 2; /* escape word, from the unit end */
             if (wi >= U) return GAANS_REF_ECORRUPT;
             int64_t pos = U - 1 - wi;
             uint32_t e = (uint32_t)wbase[2 * pos] | ((uint32_t)wbase[2 * pos + 1] << 8);
@@ -663,9 +672,8 @@ int gaans_ref_decode(const uint8_t* payload, int64_t payload_len,
         x[l] = (x[l] << 16) | w;
       }
     }
-    for (int k = 0; k < W_MAX_I; ++k)
-      for (int l = 0; l < A; ++l)
-        if (xs[k][l] != W_L) return GAANS_REF_ECORRUPT;
+    for (int l = 0; l < A; ++l)
+      if (x[l] != W_L) return GAANS_REF_ECORRUPT;
     {
       int64_t Q = (eq + 3) / 4;
       int64_t pad = (rp + Q) & 1;

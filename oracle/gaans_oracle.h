@@ -65,11 +65,11 @@ int rans64_ref_decode(const uint32_t* words, int64_t n_words,
 
 /* ---- wave64 GA-ANS format ------------------------------------------------ */
 
-/* Upper bound on the payload size (bytes) for the given shape and
- * interleave I (1, 2 or 4 rANS states per lane). */
-int64_t gaans_ref_max_payload_bytes(int32_t B, int32_t N, int32_t C, int32_t P, int32_t I);
+/* Upper bound on the payload size (bytes) for the given shape and S
+ * segments per chunk; -1 for an invalid shape or S. */
+int64_t gaans_ref_max_payload_bytes(int32_t B, int32_t N, int32_t C, int32_t P, int32_t S);
 
-/* One position's term of a chunk's index hash: MurmurHash3 fmix32 of
+/* One position's term of a coding unit's index hash: MurmurHash3 fmix32 of
  * (p * 0x9E3779B9 + tb + 1) mod 2^32. */
 uint32_t gaans_ref_index_term(int64_t p, int32_t tb);
 
@@ -79,14 +79,14 @@ uint64_t gaans_ref_table_digest(const int32_t* cdfs, int32_t M, int32_t Lmax,
 
 /* indexes may be NULL: then the table of position i is its channel i / (N/C). */
 int gaans_ref_encode(const int32_t* symbols, const int32_t* indexes,
-                     int32_t B, int32_t N, int32_t C, int32_t P, int32_t I,
+                     int32_t B, int32_t N, int32_t C, int32_t P, int32_t S,
                      const int32_t* cdfs, int32_t M, int32_t Lmax,
                      const int32_t* cdf_sizes, const int32_t* offsets,
                      uint8_t* out, int64_t out_cap, int64_t* out_len);
 
 int gaans_ref_decode(const uint8_t* payload, int64_t payload_len,
                      const int32_t* indexes,
-                     int32_t B, int32_t N, int32_t C, int32_t P, int32_t I,
+                     int32_t B, int32_t N, int32_t C, int32_t P, int32_t S,
                      const int32_t* cdfs, int32_t M, int32_t Lmax,
                      const int32_t* cdf_sizes, const int32_t* offsets,
                      int32_t* out_symbols);

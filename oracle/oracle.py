@@ -135,10 +135,10 @@ def index_term(p: int, tb: int) -> int:
 
 
 def gaans_encode(symbols, indexes, cdfs, cdf_sizes, offsets, p_ch: int,
-                 channels: int | None = None, interleave: int = 1) -> bytes:
+                 channels: int | None = None, segments: int = 1) -> bytes:
     """Payload bytes of the wave64 format.  ``symbols`` is [B, N];
     ``indexes`` is [B, N] or None (channel-major: table = channel);
-    ``interleave`` rANS states per lane (1, 2 or 4)."""
+    ``segments`` independently coded segments per chunk."""
     s = _i32(symbols)
     if s.ndim != 2:
         raise ValueError("symbols must be [B, N]")
@@ -146,13 +146,13 @@ def gaans_encode(symbols, indexes, cdfs, cdf_sizes, offsets, p_ch: int,
     cdfs, sizes, offs = _tables(cdfs, cdf_sizes, offsets)
     C = cdfs.shape[0] if channels is None else int(channels)
     ix = None if indexes is None else _i32(indexes).reshape(B, N)
-    cap = lib().gaans_ref_max_payload_bytes(B, N, C, p_ch, interleave)
+    cap = lib().gaans_ref_max_payload_bytes(B, N, C, p_ch, segments)
     if cap < 0:
         raise OracleError(-1, "gaans_encode")
     out = np.zeros(cap, dtype=np.uint8)
     n = ctypes.c_int64(0)
     rc = lib().gaans_ref_encode(_ptr(s), None if ix is None else _ptr(ix), B, N, C, p_ch,
-                                interleave, _ptr(cdfs), cdfs.shape[0], cdfs.shape[1], _ptr(sizes),
+                                segments, _ptr(cdfs), cdfs.shape[0], cdfs.shape[1], _ptr(sizes),
                                 _ptr(offs), _ptr(out), cap, ctypes.byref(n))
     if rc:
         raise OracleError(rc, "gaans_encode")
@@ -160,14 +160,14 @@ def gaans_encode(symbols, indexes, cdfs, cdf_sizes, offsets, p_ch: int,
 
 
 def gaans_decode(payload: bytes, indexes, B: int, N: int, cdfs, cdf_sizes, offsets,
-                 p_ch: int, channels: int | None = None, interleave: int = 1) -> np.ndarray:
+                 p_ch: int, channels: int | None = None, segments: int = 1) -> np.ndarray:
     cdfs, sizes, offs = _tables(cdfs, cdf_sizes, offsets)
     C = cdfs.shape[0] if channels is None else int(channels)
     ix = None if indexes is None else _i32(indexes).reshape(B, N)
     buf = np.frombuffer(bytes(payload), dtype=np.uint8)
     out = np.zeros((B, N), dtype=np.int32)
     rc = lib().gaans_ref_decode(_ptr(buf), buf.size, None if ix is None else _ptr(ix), B, N,
-                                C, p_ch, interleave, _ptr(cdfs), cdfs.shape[0], cdfs.shape[1],
+                                C, p_ch, segments, _ptr(cdfs), cdfs.shape[0], cdfs.shape[1],
                                 _ptr(sizes), _ptr(offs), _ptr(out))
     if rc:
         raise OracleError(rc, "gaans_decode")

@@ -30,7 +30,8 @@ def laplace_tables(M, max_cdf, seed):
 
 def cases():
     rng = np.random.default_rng(20261201)
-    # 1. explicit indexes, ragged last chunk (C=6, P=4), escapes
+    # 1. explicit indexes, ragged last chunk (C=6, P=4), escapes; two segments
+    #    per chunk (the last chunk has two steps)
     cdfs, sizes, offs = laplace_tables(6, 24, 1)
     B, C, HW = 2, 6, 37
     idx = rng.integers(0, 6, size=(B, C * HW), dtype=np.int32)
@@ -39,14 +40,15 @@ def cases():
     sym[1, 77] = -70000
     yield "symbols_explicit", dict(symbols=sym, indexes=idx, cdfs=cdfs, cdf_sizes=sizes,
                                    offsets=offs, p_ch=np.int32(4), channels=np.int32(C),
-                                   interleave=np.int32(2))
+                                   segments=np.int32(2))
     # 2. implicit indexes (table = channel), one lane-short chunk (HW*P < 64)
     B, C, HW = 3, 6, 5
     sym = np.rint(rng.laplace(0, 2, size=(B, C * HW))).astype(np.int32)
     yield "symbols_implicit", dict(symbols=sym, indexes=np.zeros(0, np.int32), cdfs=cdfs,
                                    cdf_sizes=sizes, offsets=offs, p_ch=np.int32(2),
-                                   channels=np.int32(C), interleave=np.int32(1))
-    # 3. fused quantize: fp32 latents and per-channel medians
+                                   channels=np.int32(C), segments=np.int32(1))
+    # 3. fused quantize: fp32 latents and per-channel medians; three segments
+    #    (one step each)
     B, C, HW = 1, 6, 50
     med = rng.normal(0, 0.3, C).astype(np.float32)
     y = (rng.laplace(0, 2, size=(B, C, HW)) + med[None, :, None]).astype(np.float32)
@@ -54,7 +56,7 @@ def cases():
     sym = O.quantize(y, med).reshape(B, -1)
     yield "latents", dict(y=y.reshape(B, -1), medians=med, symbols=sym, cdfs=cdfs,
                           cdf_sizes=sizes, offsets=offs, p_ch=np.int32(3), channels=np.int32(C),
-                          interleave=np.int32(4))
+                          segments=np.int32(3))
     # 4. Gaussian: build_indexes over a log-spaced scale table, means
     table, gcdfs, gsizes, goffs = gaussian_tables()
     B, C, HW = 1, 4, 40
@@ -67,7 +69,7 @@ def cases():
     sym = O.quantize_elem(y, means)
     yield "gaussian", dict(y=y, scales=scales, means=means, scale_table=table, bound=np.float32(0.11),
                            indexes=idx, symbols=sym, cdfs=gcdfs, cdf_sizes=gsizes, offsets=goffs,
-                           p_ch=np.int32(2), channels=np.int32(C), interleave=np.int32(2))
+                           p_ch=np.int32(2), channels=np.int32(C), segments=np.int32(2))
 
 
 def gaussian_tables():
@@ -89,7 +91,7 @@ def main():
         full = (idx if idx is not None and idx.size else
                 np.repeat(np.arange(C, dtype=np.int32), N // C)[None].repeat(B, 0))
         payload = O.gaans_encode(sym, full if idx is not None and idx.size else None, cdfs,
-                                 sizes, offs, int(c["p_ch"]), C, int(c["interleave"]))
+                                 sizes, offs, int(c["p_ch"]), C, int(c["segments"]))
         streams = [O.rans64_encode(sym[b], full[b], cdfs, sizes, offs) for b in range(B)]
         lens = np.array([len(s) for s in streams], np.int64)
         np.savez(os.path.join(HERE, f"{name}.npz"), **c,

@@ -20,7 +20,7 @@ def load(name):
     c["streams"] = [blob[e - n:e] for n, e in zip(lens, ends)]
     c["channels"] = int(c["channels"])
     c["p_ch"] = int(c["p_ch"])
-    c["interleave"] = int(c["interleave"])
+    c["segments"] = int(c["segments"])
     sym = c["symbols"]
     B, N = sym.shape
     idx = c.get("indexes")

@@ -76,7 +76,7 @@ def test_config1_accelerate_matches_oracle(gpu_device, p_ch):
     symbols = oracle.quantize(y_np, med_np)
     assert np.array_equal(symbols, torch.round(y - med.reshape(1, -1, 1, 1)).int().cpu().numpy())
     want = oracle.gaans_encode(symbols.reshape(1, -1), None, *tabs, p_ch,
-                               interleave=payload.interleave)
+                               segments=payload.segments)
     assert payload.to_bytes() == want
     want_y_hat = oracle.dequantize(symbols, med_np)
     assert np.array_equal(y_hat.cpu().numpy(), want_y_hat)

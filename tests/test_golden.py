@@ -15,11 +15,11 @@ def test_oracle_reproduces_golden_bytes(name):
     B, N = sym.shape
     idx = c["full_indexes"]
     payload = O.gaans_encode(sym, idx if c["explicit"] else None, cdfs, sizes, offs, c["p_ch"],
-                             c["channels"], c["interleave"])
+                             c["channels"], c["segments"])
     assert payload == c["payload"]
     assert np.array_equal(O.gaans_decode(payload, idx if c["explicit"] else None, B, N, cdfs,
                                          sizes, offs, c["p_ch"], c["channels"],
-                                         c["interleave"]), sym)
+                                         c["segments"]), sym)
     for b in range(B):
         assert O.rans64_encode(sym[b], idx[b], cdfs, sizes, offs) == c["streams"][b]
         assert np.array_equal(O.rans64_decode(c["streams"][b], idx[b], cdfs, sizes, offs), sym[b])

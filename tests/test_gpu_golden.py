@@ -26,26 +26,26 @@ def test_kernels_reproduce_golden_bytes(gpu_device, name):
     print("case: golden", name, flush=True)
     sym = c["symbols"]
     B, N = sym.shape
-    C, P, I = c["channels"], c["p_ch"], c["interleave"]
+    C, P, S = c["channels"], c["p_ch"], c["segments"]
     tables = prepare_tables(dev(c["cdfs"], gpu_device), dev(c["cdf_sizes"], gpu_device),
                             dev(c["offsets"], gpu_device))
     idx = dev(c["full_indexes"], gpu_device) if c["explicit"] else None
     if name == "latents":
         med = dev(c["medians"], gpu_device)
         enc = gaans.encode(tables, B, N, C, P, gpu_device, y=dev(c["y"], gpu_device), medians=med,
-                           interleave=I)
-        out = gaans.decode(enc.packed, tables, B, N, C, P, gpu_device, medians=med, interleave=I)
+                           segments=S)
+        out = gaans.decode(enc.packed, tables, B, N, C, P, gpu_device, medians=med, segments=S)
         want = O.dequantize(sym.reshape(B, C, -1), c["medians"]).reshape(B, N)
     elif name == "gaussian":
         g = dict(scales=dev(c["scales"], gpu_device), scale_table=dev(c["scale_table"], gpu_device),
-                 scale_bound=float(c["bound"]), means=dev(c["means"], gpu_device), interleave=I)
+                 scale_bound=float(c["bound"]), means=dev(c["means"], gpu_device), segments=S)
         enc = gaans.encode_gaussian(tables, B, N, C, P, gpu_device, y=dev(c["y"], gpu_device), **g)
         out = gaans.decode_gaussian(enc.packed, tables, B, N, C, P, gpu_device, **g)
         want = O.dequantize_elem(sym, c["means"])
     else:
         enc = gaans.encode(tables, B, N, C, P, gpu_device, symbols=dev(sym, gpu_device),
-                           indexes=idx, interleave=I)
-        out = gaans.decode(enc.packed, tables, B, N, C, P, gpu_device, indexes=idx, interleave=I)
+                           indexes=idx, segments=S)
+        out = gaans.decode(enc.packed, tables, B, N, C, P, gpu_device, indexes=idx, segments=S)
         want = sym
     assert enc.packed.cpu().numpy().tobytes() == c["payload"]
     got = out.cpu().numpy()

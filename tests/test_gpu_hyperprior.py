@@ -49,35 +49,36 @@ def gaussian_case(B, C, H, W, seed, with_means=True, edge=False):
 
 
 # the mean-scale hyperprior's y at full size for every P of the sweep; a
-# 1x192x33x48 latent at P=24 (38,016-symbol chunks: 594 steps, so the
-# encoder's 16-step blocks end with a partial block); small ragged shapes
+# 1x192x33x48 latent at P=24 (38,016-symbol chunks: 594 steps, so with one
+# segment the encoder's 16-step blocks end with a partial block); small
+# ragged shapes (1x24x5x7 at P=5: 3-step chunks, the most segments)
 @pytest.mark.parametrize("with_means", [True, False])
-@pytest.mark.parametrize("shape,p_ch,interleave", [
+@pytest.mark.parametrize("shape,p_ch,segments", [
     ((1, 192, 32, 48), 1, 1), ((1, 192, 32, 48), 4, 1), ((1, 192, 32, 48), 16, 2),
-    ((1, 192, 32, 48), 64, 4), ((1, 192, 32, 48), 192, 1), ((1, 192, 33, 48), 24, 1),
+    ((1, 192, 32, 48), 64, 4), ((1, 192, 32, 48), 192, 8), ((1, 192, 33, 48), 24, 1),
     ((1, 192, 33, 48), 24, 4), ((2, 16, 8, 12), 1, 1), ((2, 16, 8, 12), 16, 2),
-    ((1, 24, 5, 7), 5, 4)])
-def test_fused_gaussian_matches_oracle(gpu_device, shape, p_ch, interleave, with_means):
+    ((1, 24, 5, 7), 5, 3)])
+def test_fused_gaussian_matches_oracle(gpu_device, shape, p_ch, segments, with_means):
     B, C, H, W = shape
-    say("case: gaussian", shape, "P", p_ch, "interleave", interleave, "means", with_means)
+    say("case: gaussian", shape, "P", p_ch, "segments", segments, "means", with_means)
     table, cdfs, sizes, offsets, y, means, scales = gaussian_case(
         B, C, H, W, seed=C + p_ch, with_means=with_means, edge=True)
     N = C * H * W
     idx = O.build_indexes(scales, table, 0.11)
     sym = O.quantize_elem(y, means)
-    ref = O.gaans_encode(sym, idx, cdfs, sizes, offsets, p_ch, C, interleave)
+    ref = O.gaans_encode(sym, idx, cdfs, sizes, offsets, p_ch, C, segments)
     tables = prepare_tables(dev(cdfs, gpu_device), dev(sizes, gpu_device), dev(offsets, gpu_device))
     dm = dev(means, gpu_device) if means is not None else None
     enc = gaans.encode_gaussian(tables, B, N, C, p_ch, gpu_device, y=dev(y, gpu_device),
                                 scales=dev(scales, gpu_device),
                                 scale_table=dev(table, gpu_device), scale_bound=0.11, means=dm,
-                                interleave=interleave)
+                                segments=segments)
     got = enc.packed.cpu().numpy().tobytes()
     assert len(got) == len(ref) and got == ref
     y_hat = gaans.decode_gaussian(enc.packed, tables, B, N, C, p_ch, gpu_device,
                                   scales=dev(scales, gpu_device),
                                   scale_table=dev(table, gpu_device), scale_bound=0.11, means=dm,
-                                  interleave=interleave)
+                                  segments=segments)
     want = O.dequantize_elem(sym, means)
     assert np.array_equal(y_hat.cpu().numpy().view(np.uint32), want.view(np.uint32))
 

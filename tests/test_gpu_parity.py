@@ -35,19 +35,31 @@ def tables_on(w, device):
     return dev(w.cdfs, device), dev(w.cdf_sizes, device), dev(w.offsets, device)
 
 
-def check_workload(backend, device, w, channels=None, bytes_check=True, interleave=None):
-    say("case:", w.name, "P =", w.p_ch, "shape", w.symbols.shape, "interleave", interleave)
+def max_segments(w, channels=None):
+    """The most segments per chunk a workload's shape allows (one step each
+    in a row's last chunk)."""
+    C = w.channels if channels is None else channels
+    N = w.symbols.shape[1]
+    cl = w.p_ch * (N // C)
+    K = -(-C // w.p_ch)
+    return min(256, -(-(N - (K - 1) * cl) // 64))
+
+
+def check_workload(backend, device, w, channels=None, bytes_check=True, segments=None):
+    if segments is not None:
+        segments = min(segments, max_segments(w, channels))
+    say("case:", w.name, "P =", w.p_ch, "shape", w.symbols.shape, "segments", segments)
     sym = dev(w.symbols, device)
     idx = dev(w.explicit_indexes(), device)
     cdfs, sizes, offs = tables_on(w, device)
     payload = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=w.p_ch, channels=channels,
-                             interleave=interleave)
+                             segments=segments)
     torch.cuda.synchronize()
-    if interleave is not None:
-        assert payload.interleave == interleave
+    if segments is not None:
+        assert payload.segments == segments
     if bytes_check:
         ref = O.gaans_encode(w.symbols, w.indexes, w.cdfs, w.cdf_sizes, w.offsets, w.p_ch,
-                             channels, payload.interleave)
+                             channels, payload.segments)
         got = payload.to_bytes()
         assert len(got) == len(ref)
         assert got == ref
@@ -83,14 +95,14 @@ def test_reference_round_trip_escape_symbols(backend, gpu_device):
 
 # ---- hand-derived KAT payloads (see tests/test_oracle.py) -------------------
 
-@pytest.mark.parametrize("interleave", [1, 2, 4])
-def test_kat_payloads_bit_exact(backend, gpu_device, interleave):
+@pytest.mark.parametrize("segments", [1, 2, 3])
+def test_kat_payloads_bit_exact(backend, gpu_device, segments):
     cdf = list(range(17)) + [65536]
     s = [(5 * p + 3) % 16 for p in range(130)]
     s[3], s[70], s[129] = -1, 56, 17
     w = synthetic.Workload("KAT 130", np.array([s], np.int32), None, np.array([cdf], np.int32),
                            np.array([18], np.int32), np.array([0], np.int32), 1, 1, 0)
-    check_workload(backend, gpu_device, w, interleave=interleave)
+    check_workload(backend, gpu_device, w, segments=segments)
     w = synthetic.Workload("KAT 2", np.zeros((1, 2), np.int32), None,
                            np.array([[0, 32768, 65536]], np.int32), np.array([3], np.int32),
                            np.array([0], np.int32), 1, 1, 0)
@@ -112,9 +124,10 @@ def random_tables(rng, M, max_size):
     return cdfs, sizes, rng.integers(-20, 20, M).astype(np.int32)
 
 
-@pytest.mark.parametrize("interleave", [1, 2, 4])
-def test_random_shapes_bit_exact(backend, gpu_device, interleave):
-    rng = np.random.default_rng(11 + interleave)
+@pytest.mark.parametrize("segments", [1, 2, 5])
+def test_random_shapes_bit_exact(backend, gpu_device, segments):
+    # segments: as asked, or the most the shape allows
+    rng = np.random.default_rng(11 + segments)
     for trial in range(40):
         B, C = int(rng.integers(1, 4)), int(rng.integers(1, 13))
         HW = int(rng.choice([1, 3, 16, 63, 64, 65, 200, 777]))
@@ -125,12 +138,12 @@ def test_random_shapes_bit_exact(backend, gpu_device, interleave):
             k = int(rng.integers(s.size))
             s.flat[k] = int(rng.choice([2**30 + 7, -(2**31) + 40, 2**20, -(2**16)]))
         w = synthetic.Workload(f"random trial {trial}", s, None, cdfs, sizes, offs, C, P, 0)
-        check_workload(backend, gpu_device, w, interleave=interleave)
+        check_workload(backend, gpu_device, w, segments=segments)
 
 
-@pytest.mark.parametrize("interleave", [1, 2, 4])
-def test_explicit_random_indexes_bit_exact(backend, gpu_device, interleave):
-    rng = np.random.default_rng(12 + interleave)
+@pytest.mark.parametrize("segments", [1, 2, 5])
+def test_explicit_random_indexes_bit_exact(backend, gpu_device, segments):
+    rng = np.random.default_rng(12 + segments)
     for trial in range(10):
         M, C, HW = int(rng.integers(1, 9)), int(rng.integers(1, 9)), int(rng.integers(1, 300))
         P = int(rng.integers(1, C + 1))
@@ -138,12 +151,13 @@ def test_explicit_random_indexes_bit_exact(backend, gpu_device, interleave):
         s = rng.integers(-30, 30, (2, C * HW)).astype(np.int32)
         idx = rng.integers(0, M, (2, C * HW)).astype(np.int32)
         w = synthetic.Workload(f"explicit trial {trial}", s, idx, cdfs, sizes, offs, C, P, 0)
-        check_workload(backend, gpu_device, w, channels=C, interleave=interleave)
+        check_workload(backend, gpu_device, w, channels=C, segments=segments)
 
 
 def test_long_chunks_with_partial_last_block(backend, gpu_device):
-    # chunks of 32,800 symbols (C=8, HW=4100, P=8): 513 steps, so the
-    # encoder's 16-step blocks end with a one-step block; explicit indexes
+    # chunks of 32,800 symbols (C=8, HW=4100, P=8): 513 steps, so with one
+    # segment the encoder's 16-step blocks end with a one-step block (two and
+    # five segments: units of 256/257 and 102/103 steps); explicit indexes
     # with escapes, then the fused latents path with explicit indexes
     rng = np.random.default_rng(21)
     w0 = synthetic.coder_512x768(seed=21)
@@ -152,33 +166,33 @@ def test_long_chunks_with_partial_last_block(backend, gpu_device):
     idx = np.repeat(np.arange(C, dtype=np.int32), HW)[None]
     s = np.rint(rng.laplace(0, 2.0, (1, C * HW))).astype(np.int32)
     s[0, ::211] = rng.integers(-90000, 90000, s[0, ::211].shape)
-    for I in (1, 2, 4):
+    for S in (1, 2, 5):
         w = synthetic.Workload("long chunks 1x8x4100", s, idx, cdfs, sizes, offs, C, C, 0)
-        check_workload(backend, gpu_device, w, interleave=I)
+        check_workload(backend, gpu_device, w, segments=S)
     tables = prepare_tables(dev(cdfs, gpu_device), dev(sizes, gpu_device), dev(offs, gpu_device))
     med = rng.normal(0, 0.3, C).astype(np.float32)
     y = (s.reshape(1, C, HW) + med[None, :, None]
          + rng.uniform(-0.49, 0.49, (1, C, HW))).astype(np.float32)
     sym = O.quantize(y, med).reshape(1, -1)
-    for I in (1, 4):
-        say("case: fused latents, explicit indexes, 1x8x4100 P=8, interleave", I)
+    for S in (1, 4):
+        say("case: fused latents, explicit indexes, 1x8x4100 P=8, segments", S)
         enc = gaans.encode(tables, 1, C * HW, C, C, gpu_device, y=dev(y, gpu_device),
                            medians=dev(med, gpu_device), indexes=dev(idx, gpu_device),
-                           interleave=I)
+                           segments=S)
         assert enc.packed.cpu().numpy().tobytes() == O.gaans_encode(sym, idx, cdfs, sizes, offs,
-                                                                      C, C, I)
+                                                                      C, C, S)
         y_hat = gaans.decode(enc.packed, tables, 1, C * HW, C, C, gpu_device,
                              medians=dev(med, gpu_device), indexes=dev(idx, gpu_device),
-                             interleave=I)
+                             segments=S)
         want = O.dequantize(sym.reshape(1, C, HW), med).reshape(1, -1)
         assert np.array_equal(y_hat.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
 # ---- benchmark shapes at full size -----------------------------------------
 
-@pytest.mark.parametrize("interleave", [None, 2, 4])
-def test_coder_512x768_p4_bit_exact(backend, gpu_device, interleave):
-    check_workload(backend, gpu_device, synthetic.coder_512x768(), interleave=interleave)
+@pytest.mark.parametrize("segments", [None, 2, 3])
+def test_coder_512x768_p4_bit_exact(backend, gpu_device, segments):
+    check_workload(backend, gpu_device, synthetic.coder_512x768(), segments=segments)
 
 
 def test_side_stream_calls_without_device_sync(backend, gpu_device):
@@ -194,7 +208,7 @@ def test_side_stream_calls_without_device_sync(backend, gpu_device):
         idx = dev(w.explicit_indexes(), gpu_device)
         cdfs, sizes, offs = tables_on(w, gpu_device)
         for rep in range(4):
-            payload = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=w.p_ch, interleave=1)
+            payload = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=w.p_ch, segments=1)
             assert payload.to_bytes() == ref, rep
             out = backend.decode(payload, idx, cdfs, sizes, offs)
             assert torch.equal(out, sym), rep
@@ -219,19 +233,19 @@ def test_hyperprior_y_gaussian_tables(backend, gpu_device, p_ch):
     check_workload(backend, gpu_device, zw)
 
 
-@pytest.mark.parametrize("interleave", [None, 1, 2])
-def test_highres_2160x3840_p8(backend, gpu_device, interleave):
-    check_workload(backend, gpu_device, synthetic.highres_2160x3840(), interleave=interleave)
+@pytest.mark.parametrize("segments", [None, 1, 7])
+def test_highres_2160x3840_p8(backend, gpu_device, segments):
+    check_workload(backend, gpu_device, synthetic.highres_2160x3840(), segments=segments)
 
 
-@pytest.mark.parametrize("interleave", [None, 2])
+@pytest.mark.parametrize("segments", [None, 2])
 @pytest.mark.parametrize("make", [synthetic.batch_skew, synthetic.batch_uniform])
-def test_batch64_p16(backend, gpu_device, make, interleave):
-    check_workload(backend, gpu_device, make(), interleave=interleave)
+def test_batch64_p16(backend, gpu_device, make, segments):
+    check_workload(backend, gpu_device, make(), segments=segments)
 
 
-@pytest.mark.parametrize("interleave", [1, 4])
-def test_escape_heavy_chunks_bit_exact(backend, gpu_device, interleave):
+@pytest.mark.parametrize("segments", [1, 4])
+def test_escape_heavy_chunks_bit_exact(backend, gpu_device, segments):
     # every symbol of a 1x192x32x48 image escapes: each chunk's escape section
     # holds 6,144 entries, several times the decoder's escape FIFO
     w = synthetic.coder_512x768(seed=7)
@@ -239,7 +253,7 @@ def test_escape_heavy_chunks_bit_exact(backend, gpu_device, interleave):
     w.symbols = (w.symbols * 40 + rng.integers(-3, 4, w.symbols.shape)
                  + np.where(rng.random(w.symbols.shape) < 0.5, 5000, -5000)).astype(np.int32)
     w.name = "all-escape 1x192x32x48"
-    check_workload(backend, gpu_device, w, interleave=interleave)
+    check_workload(backend, gpu_device, w, segments=segments)
 
 
 def test_escape_heavy_batch_bit_exact(backend, gpu_device):

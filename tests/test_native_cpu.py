@@ -34,11 +34,11 @@ def test_host_selftest_division_constants():
 
 def test_layout_matches_format():
     lay = _native.layout(1, 192 * 32 * 48, 192, 4)
-    assert (lay.K, lay.chunk_len, lay.BK, lay.HW) == (48, 6144, 48, 1536)
+    assert (lay.K, lay.chunk_len, lay.U, lay.HW, lay.S) == (48, 6144, 48, 1536, 1)
     assert lay.header_bytes == (64 + 8 * 48 + 15) // 16 * 16
     lay = _native.layout(64, 192 * 1536, 192, 16)
-    assert (lay.K, lay.BK, lay.chunk_len) == (12, 768, 24576)
-    assert lay.workspace_bytes >= lay.BK * lay.cap_words * 2
+    assert (lay.K, lay.U, lay.chunk_len) == (12, 768, 24576)
+    assert lay.workspace_bytes >= lay.U * lay.cap_words * 2
     lay = _native.layout(1, 128 * 96, 128, 5)  # C not a multiple of P
     assert lay.K == 26 and lay.chunk_len == 480
     for bad in ((0, 4, 1, 1), (1, 5, 2, 1), (1, 4, 2, 3)):
@@ -46,15 +46,23 @@ def test_layout_matches_format():
             _native.layout(*bad)
 
 
-def test_interleave_layout_and_choice():
+def test_segment_layout_and_choice():
     N = 192 * 1536
-    one, four = _native.layout(1, N, 192, 4, 1), _native.layout(1, N, 192, 4, 4)
-    assert one.I == 1 and four.I == 4
-    # three more state slots of 64 lanes per chunk, 48 chunks
-    assert four.max_payload_bytes - one.max_payload_bytes == 48 * 64 * 4 * 3
-    assert four.workspace_bytes > one.workspace_bytes
-    with pytest.raises(Exception):
-        _native.layout(1, 64, 1, 1, 3)
+    one, three = _native.layout(1, N, 192, 4, 1), _native.layout(1, N, 192, 4, 3)
+    assert (one.S, three.S, one.U, three.U) == (1, 3, 48, 144)
+    # two more units of 64 states (+ pad and escape word) per chunk, 48 chunks
+    assert three.max_payload_bytes - three.header_bytes - (
+        one.max_payload_bytes - one.header_bytes) == 48 * 2 * (64 * 4 + 8)
+    assert three.header_bytes == (64 + 8 * 144 + 15) // 16 * 16
+    # a unit holds at most ceil(96 / 3) = 32 steps: its staging words
+    assert three.cap_words == 32 * 64 + 2
+    # at least one step per segment (the shortest chunk decides), at most 256
+    _native.layout(1, N, 192, 4, 96)
+    for bad in ((1, N, 192, 4, 97), (1, N, 192, 4, 0), (1, 64 * 300, 1, 1, 257),
+                (1, 3 * 64, 3, 2, 2)):
+        with pytest.raises(Exception):
+            _native.layout(*bad)
+    _native.layout(1, 64 * 300, 1, 1, 256)
     L = _native.lib()
     # the tables' mean entropy: 1 bit (two halves) and 1.5 bits (1/4, 1/4, 1/2)
     cdfs = np.array([[0, 32768, 65536, 0], [0, 16384, 32768, 65536]], np.int32)
@@ -66,23 +74,29 @@ def test_interleave_layout_and_choice():
                                   blob.ctypes.data, nb.value, ctypes.byref(desc)) == 0
     assert desc.mean_bits == pytest.approx(1.25, abs=1e-6)
 
-    def choose(bits, B, N, C, P, budget=0.01):
+    def choose(bits, B, N, C, P, budget=0.006, target=256):
         d = _native.Tables()
         d.mean_bits = bits
         out = ctypes.c_int32(0)
-        assert L.gaans_choose_interleave(ctypes.byref(d), B, N, C, P, budget,
-                                         ctypes.byref(out)) == 0
+        assert L.gaans_choose_segments(ctypes.byref(d), B, N, C, P, budget, target,
+                                       ctypes.byref(out)) == 0
         return out.value
 
-    # 2160x3840 latent, P=8: 261,120 symbols a chunk at 3.74 bits is about
-    # 122 KB; three more slots cost 768 B (0.63%), one more 256 B (0.21%)
+    # 2160x3840 latent, P=8: 40 chunks of 261,120 symbols at 3.74 bits, about
+    # 122,330 B each; an added unit costs 3.125 * 64 + 4 = 204 B (0.17%):
+    # 0.6% allows 3 more (1 + floor(734 / 204))
     assert choose(3.74, 1, 320 * 32640, 320, 8) == 4
-    assert choose(3.74, 1, 320 * 32640, 320, 8, budget=0.006) == 2
+    assert choose(3.74, 1, 320 * 32640, 320, 8, budget=0.01) == 6
+    assert choose(3.74, 1, 320 * 32640, 320, 8, budget=0.1) == 7  # 280 units fill 256 CUs
+    # without a unit target: 1 + floor(0.1 * 122,330 / 204) = 60
+    assert choose(3.74, 1, 320 * 32640, 320, 8, budget=0.1, target=0) == 60
     assert choose(3.74, 1, 320 * 32640, 320, 8, budget=0.001) == 1
-    # 512x768 latent, P=4: 6,144 symbols at 2.67 bits (about 2 KB) -> one state
+    # 512x768 latent, P=4: 6,144 symbols at 2.67 bits (about 2 KB): one unit
     assert choose(2.67, 1, N, 192, 4) == 1
-    # one step per chunk uses one slot whatever the interleave: nothing to gain
-    assert choose(8.0, 1, 64 * 12, 12, 1) == 1
+    # 768 chunks already fill the device
+    assert choose(8.0, 64, N, 192, 16, budget=1.0) == 1
+    # one step per chunk: nothing to split
+    assert choose(8.0, 1, 64 * 12, 12, 1, budget=1.0) == 1
 
 
 def prepare_host(cdfs, sizes, offs):

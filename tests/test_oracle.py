@@ -164,9 +164,9 @@ def test_index_hash_detects_a_swapped_pair():
         assert struct.unpack_from("<I", data, 64 + 4)[0] == hash_of(tabs)
 
 
-def header_words(B, N, C, P, K, chunk_len, M, digest, interleave=1):
-    return [0x31574147, 3, B, N, C, P, K, chunk_len, M, 0x00041040,
-            digest & 0xFFFFFFFF, digest >> 32, interleave, 0, 0, 0]
+def header_words(B, N, C, P, K, chunk_len, M, digest, segments=1):
+    return [0x31574147, 4, B, N, C, P, K, chunk_len, M, 0x00041040,
+            digest & 0xFFFFFFFF, digest >> 32, segments, 0, 0, 0]
 
 
 def test_gaans_kat_two_lanes_no_renorm():
@@ -225,62 +225,102 @@ def test_gaans_kat_lane_order_group_order_and_escape_section():
     assert O.gaans_decode(data, None, 1, 130, cdfs, sizes, offs, 1).tolist() == [s]
 
 
-def test_gaans_kat_two_interleaved_states():
-    # the 130-symbol chunk with I = 2: steps 0 and 2 code with state slot 0,
-    # step 1 with slot 1 (every slot starts at 2^16).  Encoder, t = 2 (slot 0,
-    # lanes 0 and 1): lane 0 emits its initial 0x0000 and holds 0x10000 +
-    # s[128]; lane 1 (escape) holds 0x10020.  t = 1 (slot 1, all initial):
-    # every lane but 6 emits 0x0000 and holds 0x10000 + s[64 + l]; lane 6
-    # (escape) holds 0x10020.  t = 0 (slot 0): lane 0 emits s[128], lane 1
-    # emits 0x0020, lanes 2..63 but 3 emit their initial 0x0000; lane 3
-    # (escape) ends at 0x10020 from the initial state.  Stream: step 0's
-    # group, step 1's, step 2's (63 + 63 + 1 = 127 words); the escape section
-    # and its pad are the same as with one state.
+def test_gaans_kat_three_segments():
+    # the 130-symbol chunk (3 steps) in S = 3 segments: unit s is step s alone,
+    # coded from fresh states.  Unit 0 (positions 0..63): every lane but 3
+    # emits its initial 0x0000 and holds 0x10000 + s[l]; lane 3 (escape, raw 1:
+    # nibbles 1, 1 -> word 0x0011) holds 0x10020.  63 + 1 words: no pad.
+    # Unit 1 (64..127): the same with s[64 + l], lane 6 escapes (raw 0x50:
+    # nibbles 2, 0, 5 -> word 0x0502).  Unit 2 (128, 129; two lanes): lane 0
+    # emits 0x0000 and holds 0x10000 + s[128]; lane 1 escapes (raw 2: nibbles
+    # 1, 2 -> word 0x0021) and holds 0x10020; 1 + 1 words, no pad.
     cdfs, sizes, offs, s = kat_130()
-    data = O.gaans_encode([s], None, cdfs, sizes, offs, 1, interleave=2)
-    stream = [s[128], 0x0020] + [0] * 61 + [0] * 63 + [0] + [0, 0x0215, 0x0211]
-    slot0 = [0x10000 + s[l] for l in range(64)]
-    slot0[3] = 0x10020
-    slot1 = [0x10000 + s[64 + l] for l in range(64)]
-    slot1[6] = 0x10020
-    chunk = struct.pack("<128I", *(slot0 + slot1)) + struct.pack(f"<{len(stream)}H", *stream)
-    assert len(chunk) == 772
+    data = O.gaans_encode([s], None, cdfs, sizes, offs, 1, segments=3)
+    st0 = [0x10000 + s[l] for l in range(64)]
+    st0[3] = 0x10020
+    st1 = [0x10000 + s[64 + l] for l in range(64)]
+    st1[6] = 0x10020
+    u0 = struct.pack("<64I", *st0) + struct.pack("<64H", *([0] * 63 + [0x0011]))
+    u1 = struct.pack("<64I", *st1) + struct.pack("<64H", *([0] * 63 + [0x0502]))
+    u2 = struct.pack("<2I", 0x10000 + s[128], 0x10020) + struct.pack("<2H", 0, 0x0021)
+    assert (len(u0), len(u1), len(u2)) == (384, 384, 12)
     dg = fnv1a64(table_digest_bytes(cdfs, sizes, offs))
-    hdr = header_words(1, 130, 1, 1, 1, 130, 1, dg, interleave=2) + [772, hash_of([0] * 130),
-                                                                     0, 0]
-    assert data == struct.pack("<20I", *hdr) + chunk
-    assert O.gaans_decode(data, None, 1, 130, cdfs, sizes, offs, 1, interleave=2).tolist() == [s]
-    # the interleave is part of the format: decoding with another one fails
-    for other in (1, 4):
+    # 3 units: header 64 + 24 bytes, padded to 96
+    hdr = header_words(1, 130, 1, 1, 1, 130, 1, dg, segments=3) + [
+        384, 768, 780, hash_of([0] * 64), hash_of([0] * 64), hash_of([0] * 2), 0, 0]
+    assert data == struct.pack("<24I", *hdr) + u0 + u1 + u2
+    assert O.gaans_decode(data, None, 1, 130, cdfs, sizes, offs, 1, segments=3).tolist() == [s]
+    # the segment count is part of the format: decoding with another one fails
+    for other in (1, 2):
         with pytest.raises(O.OracleError):
-            O.gaans_decode(data, None, 1, 130, cdfs, sizes, offs, 1, interleave=other)
+            O.gaans_decode(data, None, 1, 130, cdfs, sizes, offs, 1, segments=other)
 
 
-def test_gaans_state_slots_in_use_and_interleave_round_trips():
-    # a chunk of T steps flushes min(I, T) slots of A states
-    cdfs, sizes, offs = CDF2, [3], [0]
-    for n, interleave, slots in ((1, 4, 1), (64, 4, 1), (65, 4, 2), (200, 4, 4), (130, 2, 2)):
-        data = O.gaans_encode(np.zeros((1, n), np.int32), None, cdfs, sizes, offs, 1,
-                              interleave=interleave)
-        A = min(n, 64)
-        assert struct.unpack_from("<I", data, 64)[0] >= 4 * A * slots
-        hb = (64 + 8 + 15) // 16 * 16
-        # every state of a freq-2^15 symbol run stays in [2^16, 2^32) and the
-        # words of 2 bits per symbol: total 4 A slots + 2 words
-        T = (n + 63) // 64
-        words = len(data) - hb - 4 * A * slots
-        assert words % 2 == 0 and words <= 2 * (T * 64)
-    rng = np.random.default_rng(7)
-    for trial in range(24):
+def segment_bounds(T, S):
+    """Steps of a T-step chunk in segment s: [floor(s T / S), floor((s+1) T / S))."""
+    return [(s * T // S, (s + 1) * T // S) for s in range(S)]
+
+
+def test_gaans_segments_are_independent_units():
+    # Every unit of an S-segment payload is, byte for byte, the one-chunk
+    # payload of its own positions coded alone (B = 1, one channel, the
+    # positions' tables as explicit indexes): same states, words, escapes
+    # and index hash.  The segment bounds are computed here independently of
+    # the oracle.
+    rng = np.random.default_rng(5)
+    for trial in range(20):
         B, C = int(rng.integers(1, 3)), int(rng.integers(1, 6))
-        HW, P = int(rng.integers(1, 400)), int(rng.integers(1, C + 1))
+        HW, P = int(rng.integers(1, 500)), int(rng.integers(1, C + 1))
+        N, K = C * HW, -(-C // P)
         cdfs, sizes, offs = random_tables(rng, C, int(rng.integers(2, 20)))
-        s = rng.integers(-30, 30, (B, C * HW)).astype(np.int32)
-        for interleave in (1, 2, 4):
-            data = O.gaans_encode(s, None, cdfs, sizes, offs, P, interleave=interleave)
-            out = O.gaans_decode(data, None, B, C * HW, cdfs, sizes, offs, P,
-                                 interleave=interleave)
-            assert (out == s).all()
+        s = rng.integers(-30, 30, (B, N)).astype(np.int32)
+        Tmin = -(-(N - (K - 1) * P * HW) // 64)
+        S = int(rng.integers(1, min(Tmin, 9) + 1))
+        data = O.gaans_encode(s, None, cdfs, sizes, offs, P, segments=S)
+        U = B * K * S
+        hb = (64 + 8 * U + 15) // 16 * 16
+        ends = struct.unpack_from(f"<{U}I", data, 64)
+        hashes = struct.unpack_from(f"<{U}I", data, 64 + 4 * U)
+        prev, g = 0, 0
+        for b in range(B):
+            for k in range(K):
+                cs, ce = k * P * HW, min((k + 1) * P * HW, N)
+                for t0, t1 in segment_bounds(-(-(ce - cs) // 64), S):
+                    lo, hi = cs + 64 * t0, min(cs + 64 * t1, ce)
+                    assert hi > lo
+                    seg = s[b, lo:hi][None]
+                    tabs = (np.arange(lo, hi) // HW).astype(np.int32)[None]
+                    alone = O.gaans_encode(seg, tabs, cdfs, sizes, offs, 1, channels=1)
+                    hb1 = (64 + 8 + 15) // 16 * 16
+                    assert data[hb + prev: hb + ends[g]] == alone[hb1:]
+                    assert hashes[g] == struct.unpack_from("<I", alone, 68)[0]
+                    prev, g = ends[g], g + 1
+        assert hb + prev == len(data)
+        out = O.gaans_decode(data, None, B, N, cdfs, sizes, offs, P, segments=S)
+        assert (out == s).all()
+
+
+def test_gaans_segment_count_limits():
+    cdfs, sizes, offs = CDF2, [3], [0]
+    z = np.zeros((1, 200), np.int32)  # one chunk of 4 steps
+    for S in (1, 2, 3, 4):
+        data = O.gaans_encode(z, None, cdfs, sizes, offs, 1, segments=S)
+        assert O.gaans_decode(data, None, 1, 200, cdfs, sizes, offs, 1, segments=S).tolist() == z.tolist()
+    # at least one step per segment, at most 256 segments, at least one
+    for S in (0, 5, -1):
+        with pytest.raises(O.OracleError):
+            O.gaans_encode(z, None, cdfs, sizes, offs, 1, segments=S)
+    # the limit is set by the shortest chunk of a row: C = 3, P = 2, HW = 64:
+    # chunks of 2 and 1 steps
+    z3 = np.zeros((1, 192), np.int32)
+    t3 = [[0, 32768, 65536]] * 3
+    O.gaans_encode(z3, None, t3, [3] * 3, [0] * 3, 2, segments=1)
+    with pytest.raises(O.OracleError):
+        O.gaans_encode(z3, None, t3, [3] * 3, [0] * 3, 2, segments=2)
+    big = np.zeros((1, 64 * 300), np.int32)
+    O.gaans_encode(big, None, cdfs, sizes, offs, 1, segments=256)
+    with pytest.raises(O.OracleError):
+        O.gaans_encode(big, None, cdfs, sizes, offs, 1, segments=257)
 
 
 def test_gaans_escape_section_word_order_without_pad():

@@ -16,13 +16,13 @@ from fast_compressai.coders import _native, gaans
 from fast_compressai.coders.tables import prepare_tables
 
 
-def _noalloc(L, tables, sym, idx, B, N, C, P, I, dev):
-    lay = _native.layout(B, N, C, P, I)
+def _noalloc(L, tables, sym, idx, B, N, C, P, S, dev):
+    lay = _native.layout(B, N, C, P, S)
     out = torch.zeros(lay.max_payload_bytes, dtype=torch.uint8, device=dev)
     info = torch.zeros(4, dtype=torch.int64, device=dev)
     sp = torch.cuda.current_stream(dev).cuda_stream
     rc = L.gaans_encode_symbols_noalloc(sp, sym.data_ptr(), None if idx is None else idx.data_ptr(),
-                                        tables.ref, B, N, C, P, I, out.data_ptr(), out.numel(),
+                                        tables.ref, B, N, C, P, S, out.data_ptr(), out.numel(),
                                         info.data_ptr())
     _native.check(rc, "no-allocation encode")
     torch.cuda.synchronize(dev)
@@ -40,10 +40,10 @@ def test_noalloc_matches_workspace_encode_twice(gpu_device):
     small = synthetic.coder_512x768(seed=4, p_ch=5)          # then 12 channels of it
     cases = [
         ("1x192x32x48 P=4 explicit indexes", big, big.symbols, big.explicit_indexes(), 192, 4, 1),
-        ("1x12x32x48 P=5 implicit indexes, 2 states per lane", small,
-         small.symbols[:, :12 * 1536], None, 12, 5, 2),
+        ("1x12x32x48 P=5 implicit indexes, 3 segments per chunk", small,
+         small.symbols[:, :12 * 1536], None, 12, 5, 3),
     ]
-    for name, w, sym_np, idx_np, C, P, I in cases:
+    for name, w, sym_np, idx_np, C, P, S in cases:
         print("case: no-alloc encode", name, flush=True)
         M = C if idx_np is None else w.cdfs.shape[0]
         t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
@@ -51,12 +51,12 @@ def test_noalloc_matches_workspace_encode_twice(gpu_device):
         B, N = sym_np.shape
         sym = t(sym_np)
         idx = None if idx_np is None else t(idx_np)
-        got, status = _noalloc(L, tables, sym, idx, B, N, C, P, I, dev)
+        got, status = _noalloc(L, tables, sym, idx, B, N, C, P, S, dev)
         assert status == 0
-        ref = gaans.encode(tables, B, N, C, P, dev, symbols=sym, indexes=idx, interleave=I)
+        ref = gaans.encode(tables, B, N, C, P, dev, symbols=sym, indexes=idx, segments=S)
         assert got == ref.packed.cpu().numpy().tobytes()
         want = oracle.gaans_encode(sym_np, idx_np, w.cdfs[:M], w.cdf_sizes[:M], w.offsets[:M], P,
-                                   channels=C, interleave=I)
+                                   channels=C, segments=S)
         assert got == want
 
 
