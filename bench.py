@@ -208,7 +208,8 @@ def gaussian_kernel_times(L, _native, torch, p_ch, dev, reps=40, segments=None):
     torch.cuda.synchronize()
     want = torch.from_numpy(yw.symbols).to(dev).float() + means
     assert int(status[0].item()) == 0 and torch.equal(out, want)
-    return res, int(enc.packed.numel()), B * N, yw.raw_rgb_bytes, S
+    return res, int(enc.packed.numel()), B * N, yw.raw_rgb_bytes, S, input_sha256(
+        y_np, means_np, table_np[idx_np])
 
 
 def balle_factorized(torch, synthetic, device, seed=0):
@@ -343,6 +344,95 @@ def pipeline_bench(args):
     }), flush=True)
 
 
+def input_sha256(*arrays) -> str:
+    """SHA-256 of a workload's input arrays (their bytes, in order)."""
+    import hashlib
+
+    import numpy as np
+
+    h = hashlib.sha256()
+    for a in arrays:
+        if a is not None:
+            h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+def rans64_bytes(w, idx=None) -> int:
+    """Bytes of the CompressAI-equivalent stream of a workload: one Rans64
+    stream per image (oracle restatement of CompressAI's RansEncoder)."""
+    import oracle
+
+    idx = w.explicit_indexes() if idx is None else idx
+    return sum(len(oracle.rans64_encode(w.symbols[b], idx[b], w.cdfs, w.cdf_sizes, w.offsets))
+               for b in range(w.batch))
+
+
+def bpp_record(torch, dev, backend):
+    """Payload size of every parity-tested configuration and P (the
+    coder's automatic segment count, and one segment) against the
+    CompressAI-equivalent stream of the same symbols."""
+    from fast_compressai import synthetic
+
+    cases = [(f"512x768 P={p}", synthetic.coder_512x768(p_ch=p), None) for p in (1, 4, 16, 192)]
+    for p in (1, 4, 16, 64, 192):
+        yw, _, _, _ = synthetic.hyperprior_512x768(p_ch=p)
+        cases.append((f"hyperprior y 512x768 P={p}", yw, 192))
+    cases += [("2160x3840 P=8", synthetic.highres_2160x3840(), None),
+              ("batch64 skew P=16", synthetic.batch_skew(), None),
+              ("batch64 uniform P=16", synthetic.batch_uniform(), None)]
+    out = {}
+    ref_cache = {}
+    for name, w, channels in cases:
+        sym = torch.from_numpy(w.symbols).to(dev)
+        idx_np = w.explicit_indexes()
+        idx = torch.from_numpy(idx_np).to(dev)
+        cdfs, sizes, offs = (torch.from_numpy(a).to(dev) for a in (w.cdfs, w.cdf_sizes, w.offsets))
+        key = (w.name, w.symbols.shape)
+        if key not in ref_cache:
+            ref_cache[key] = rans64_bytes(w, idx_np)
+        ref = ref_cache[key]
+        raw_px = w.raw_rgb_bytes // 3
+        row = {"rans64_bytes": ref, "rans64_bpp": round(8 * ref / raw_px, 4),
+               "input_sha256": input_sha256(w.symbols, idx_np)}
+        for label, seg in (("auto", None), ("s1", 1)):
+            p = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=w.p_ch, channels=channels,
+                               segments=seg)
+            nb = int(p.packed.numel())
+            row[f"{label}_segments"] = p.segments
+            row[f"{label}_bytes"] = nb
+            row[f"{label}_bpp"] = round(8 * nb / raw_px, 4)
+            row[f"{label}_over_rans64_pct"] = round(100.0 * (nb / ref - 1.0), 3)
+        out[name] = row
+    return out
+
+
+def cpu_allcores(w, seconds: float):
+    """CompressAI-equivalent Rans64 encode + decode of every image of a
+    batch workload on all host cores available to this process (one image
+    per task, a thread pool over the oracle's C calls, which release the
+    GIL), repeated for about `seconds`; images per second, cores used."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import oracle
+
+    cores = len(os.sched_getaffinity(0))
+    idx = w.explicit_indexes()
+
+    def one(b):
+        data = oracle.rans64_encode(w.symbols[b], idx[b], w.cdfs, w.cdf_sizes, w.offsets)
+        dec = oracle.rans64_decode(data, idx[b], w.cdfs, w.cdf_sizes, w.offsets)
+        return bool((dec == w.symbols[b]).all())
+
+    done, t0 = 0, time.perf_counter()
+    with ThreadPoolExecutor(max_workers=cores) as ex:
+        while True:
+            assert all(ex.map(one, range(w.batch)))
+            done += w.batch
+            if time.perf_counter() - t0 >= seconds:
+                break
+    return done / (time.perf_counter() - t0), cores, done
+
+
 def rans64_times(torch, dev, batch, reps=3):
     """GPU decode of CompressAI-format Rans64 streams (one per image of the
     512x768 coder workload, table = channel): seconds per launch, and the
@@ -400,7 +490,7 @@ def kernels_only(args):
     L = _native.lib()
     reps = max(5, args.reps // 5 * 5)
     if args.kernels.startswith("hyperprior_y_p"):
-        kt, pb, n_sym, _, S = gaussian_kernel_times(L, _native, torch, int(args.kernels[14:]),
+        kt, pb, n_sym, _, S, _ = gaussian_kernel_times(L, _native, torch, int(args.kernels[14:]),
                                                     dev, reps=reps, segments=args.segments)
         alg = 12 * n_sym + pb
     else:
@@ -554,6 +644,7 @@ def main():
             alg = 8 * n_sym + pb  # symbols + indexes (int32) + payload, either direction
             extra[label] = {
                 "symbols": n_sym, "payload_bytes": pb, "segments": wl_i,
+                "input_sha256": input_sha256(wl.symbols, wl.explicit_indexes()),
                 "alg_bytes_per_launch": alg,
                 **counter_traffic(label, alg),
                 "encode_hbm_frac": round(alg / kt["encode"] / 1e9 / HBM_PEAK_GBPS, 4),
@@ -566,11 +657,12 @@ def main():
                     wl.raw_rgb_bytes / (kt["encode"] + kt["decode"]) / 1e9, 2),
             }
         for p_ch in (4, 16):
-            kt, pb, n_sym, raw_b, _ = gaussian_kernel_times(L, _native, torch, p_ch, dev)
+            kt, pb, n_sym, raw_b, seg, sha = gaussian_kernel_times(L, _native, torch, p_ch, dev)
             alg = 12 * n_sym + pb  # y, means, scales (or y_hat) fp32 + payload
             extra[f"hyperprior_y_p{p_ch}"] = {
                 "workload": f"mean-scale hyperprior y 1x192x32x48, fused Gaussian kernels, P={p_ch}",
-                "symbols": n_sym, "payload_bytes": pb, "alg_bytes_per_launch": alg,
+                "symbols": n_sym, "payload_bytes": pb, "segments": seg, "input_sha256": sha,
+                "alg_bytes_per_launch": alg,
                 **counter_traffic(f"hyperprior_y_p{p_ch}", alg),
                 "encode_hbm_frac": round(alg / kt["encode"] / 1e9 / HBM_PEAK_GBPS, 4),
                 "decode_hbm_frac": round(alg / kt["decode"] / 1e9 / HBM_PEAK_GBPS, 4),
@@ -599,6 +691,10 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
 
+    # ---- payload size of every configuration and P against the
+    # CompressAI-equivalent stream ----------------------------------------------
+    bpp = None if args.no_extra else bpp_record(torch, dev, backend)
+
     # ---- CPU baseline: CompressAI-equivalent Rans64, one stream per image --
     import oracle
 
@@ -619,6 +715,24 @@ def main():
     cpu_step = statistics.median(cpu_enc) + statistics.median(cpu_dec)
     raw = w.raw_rgb_bytes
     cpu_gbps = raw / cpu_step / 1e9
+    allcores = None
+    if not args.no_extra:
+        # the 64-image batch (uniform draw) on every host core, beside the
+        # GPU kernels' time for the same batch
+        wb = synthetic.batch_uniform()
+        ips, cores, n_img = cpu_allcores(wb, min(10.0, args.cpu_seconds))
+        gpu_kt = extra.get("batch64_uniform_p16", {})
+        gpu_s = (gpu_kt.get("encode_kernel_us", 0) + gpu_kt.get("decode_kernel_us", 0)) * 1e-6
+        allcores = {
+            "workload": "batch64 uniform 64x192x32x48, P=16 (GPU) / one Rans64 stream per "
+                        "image (CPU)",
+            "cores": cores, "images_timed": n_img,
+            "images_per_s": round(ips, 2),
+            "raw_rgb_gbps": round(ips * wb.raw_rgb_bytes / wb.batch / 1e9, 4),
+            "gpu_kernels_raw_rgb_gbps": (round(wb.raw_rgb_bytes / gpu_s / 1e9, 3)
+                                         if gpu_s else None),
+            "input_sha256": input_sha256(wb.symbols, wb.explicit_indexes()),
+        }
 
     value = raw / (ms_per_step * 1e-3) / 1e9
     rec = {
@@ -638,7 +752,8 @@ def main():
             "workload": "coder-only 1x192x32x48 int32 symbols + indexes (512x768 RGB, M=192, "
                         "Laplacian scales log-U[0.1,8], CDF<=64), P=4, encode+decode via "
                         "WarpDivBackend",
-            "batch": B, "p_ch": P, "symbols": B * N, "raw_rgb_bytes": raw,
+            "batch": B, "p_ch": P, "segments": payload.segments, "symbols": B * N,
+            "raw_rgb_bytes": raw, "input_sha256": input_sha256(w.symbols, w.explicit_indexes()),
         },
         "encode_gbps": round(raw / enc_s / 1e9, 4),
         "decode_gbps": round(raw / dec_s / 1e9, 4),
@@ -666,9 +781,14 @@ def main():
                        f"conversion); median encode {statistics.median(cpu_enc)*1e3:.3f} ms, "
                        f"decode {statistics.median(cpu_dec)*1e3:.3f} ms"),
             "speedup_gpu_over_cpu": round(value / cpu_gbps, 2),
+            "host_cores_available": len(os.sched_getaffinity(0)),
         },
         "other_configs_kernels": extra,
     }
+    if bpp is not None:
+        rec["bpp_by_config"] = bpp
+    if allcores is not None:
+        rec["cpu_baseline_allcores_batch64"] = allcores
     print(json.dumps(rec), flush=True)
 
 

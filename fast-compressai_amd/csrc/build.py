@@ -14,7 +14,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG_ROOT = os.path.dirname(HERE)
 REPO = os.path.dirname(PKG_ROOT)
-SOURCES = [os.path.join(HERE, "gaans_w64.hip")]
+SOURCES = [os.path.join(HERE, "gaans_w64.hip"), os.path.join(HERE, "gaans_host.cpp")]
 OUT = os.path.join(PKG_ROOT, "fast_compressai", "coders", "lib", "libgaans_w64.so")
 ARCH = os.environ.get("GAANS_OFFLOAD_ARCH", "gfx950")
 

@@ -49,11 +49,13 @@
 #include <string>
 #include <type_traits>
 
+#include "gaans_common.h"
 #include "gaans_w64.h"
+
+using namespace gaans;
 
 namespace {
 
-constexpr int kLanes = 64;
 #ifndef GAANS_MAPPERS
 #define GAANS_MAPPERS 4
 #endif
@@ -64,20 +66,6 @@ constexpr int kMappers = GAANS_MAPPERS;  // mapper waves per decode workgroup
 constexpr int kEncMappers = GAANS_ENC_MAPPERS;  // mapper waves per encode workgroup
 constexpr int kWaves = kEncMappers + 1;  // encoder: + the coder wave
 constexpr int kThreads = kWaves * kLanes;
-constexpr uint32_t kStateLow = 1u << 16;  // rANS L
-constexpr uint32_t kMagic = 0x31574147u;  // "GAW1"
-constexpr uint32_t kVersion = 4u;
-constexpr int kMaxSegments = 256;  // segments per chunk
-constexpr uint32_t kParams = 0x00041040u;  // lanes 64 | precision 16 << 8 | bypass 4 << 16
-constexpr int kFixedWords = 16;
-constexpr uint32_t kTabMagic = 0x35425447u;  // "GTB5"
-constexpr int kLutBits = 8;
-constexpr int kLutSize = 1 << kLutBits;
-constexpr int kSubBits = 4;                 // a sub-block: 16 entries of 16 or 1 values
-constexpr int kSubSize = 1 << kSubBits;
-constexpr int kSubBytes = 8 * kSubSize;
-constexpr uint32_t kHashMul = 0x9E3779B9u;
-constexpr int kMaxEscNibbles = 9;  // escape count + 8 nibbles of raw
 
 // per-wave hash, status and escape nibbles, then the escape count
 constexpr int kPartBytes = (12 * kWaves + 4 + 15) / 16 * 16;
@@ -89,188 +77,7 @@ constexpr int kCtrlEncDone = 0;
 constexpr int kCtrlDecDone = 16;
 constexpr int kCtrlDecStatus = 17;
 
-thread_local std::string g_last_error;
 
-int fail(int code, const char* fmt, ...) {
-  char buf[512];
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(buf, sizeof(buf), fmt, ap);
-  va_end(ap);
-  g_last_error = buf;
-  return code;
-}
-
-int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
-
-// ---- prepared table blob ---------------------------------------------------
-// [TabHdr 64 B][TabMeta x M][entries: 2 x u32 per symbol][lut: u64 x 256 x M]
-// [sub-blocks: u64 x 16 each]
-// entry of symbol v (encoder): word 0 = start | (freq - 1) << 16;
-//                              word 1 = division magic of freq (enc_magic).
-// Decode lookup entries (u64) cover a range of cum values: 256 (the table's
-// lookup, bucket j = [j << 8, (j << 8) + 255]), 16 (second level) or 1 (third
-// level).  With s the symbol containing the range's first value:
-//   at most one other symbol starts in the range:
-//     low word = start(s) | (start(s + 1) - 1) << 16   (cum > that -> s + 1),
-//     high word = s | (freq(s + 1) - 1) << 16
-//   two or more (a dense range, 256 or 16 values wide):
-//     low word = global index of a sub-block, high word = s | 0xffff << 16;
-//     the sub-block's 16 entries cover the range's 16 sub-ranges (of 16 values
-//     for a 256-value range, of one value for a 16-value range).
-struct TabHdr {
-  uint32_t magic, M, total_syms, lut_bits;
-  uint32_t digest_lo, digest_hi;
-  uint32_t meta_off, ent_off, lut_off;  // byte offsets
-  uint32_t total_bytes;
-  uint32_t max_nsym;
-  uint32_t dense_off;    // byte offset of the sub-blocks
-  uint32_t total_dense;  // sub-blocks over all tables
-  uint32_t flags;        // kTabOffsetsSafe
-  uint32_t clut_off;    // byte offset of the search lookups (u32 per bucket)
-  uint32_t starts_off;  // byte offset of the symbol starts (u16 per symbol)
-};
-// every offset <= INT32_MAX - 65535: symbol index + offset cannot overflow
-constexpr uint32_t kTabOffsetsSafe = 1u;
-// the search lookups are filled: at most kSearchMaxSyms symbols in all, every
-// offset at least INT32_MIN + 65536 (offset - symbol base cannot wrap)
-constexpr uint32_t kTabSearch = 2u;
-constexpr int64_t kSearchMaxSyms = 65535 - 8;
-constexpr int kStartsPad = 8;  // zero starts after the last symbol (sentinel, reads past it)
-static_assert(sizeof(TabHdr) == 64, "table header is 64 bytes");
-
-struct TabMeta {
-  uint32_t ent_base;    // first entry of the table
-  uint32_t nsym;        // S - 1 symbols; the last one (nsym - 1) is the escape bin
-  int32_t offset;
-  uint32_t dense_base;  // first sub-block of the table
-};
-
-// Division by a wave-uniform divisor d in [1, 2^31) for numerators n < 2^31:
-// q = (mulhi(n, m) + n) >> s with s = ceil(log2 d), m = floor(2^(32+s) / d) - 2^32 + 1
-// (Granlund & Montgomery, "Division by invariant integers using
-// multiplication", PLDI 1994, round-up variant).
-struct UDiv {
-  uint32_t m, s;
-};
-
-__host__ __device__ inline uint32_t mulhi32(uint32_t a, uint32_t b) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  return __umulhi(a, b);
-#else
-  return (uint32_t)(((uint64_t)a * b) >> 32);
-#endif
-}
-
-__host__ __device__ inline uint32_t udiv(uint32_t n, UDiv d) {
-  return (mulhi32(n, d.m) + n) >> d.s;
-}
-
-UDiv make_udiv(uint32_t d) {
-  uint32_t s = 0;
-  while (((uint64_t)1 << s) < d) ++s;
-  uint64_t m = (((uint64_t)1 << (32 + s)) / d) - ((uint64_t)1 << 32) + 1;
-  return UDiv{(uint32_t)m, s};
-}
-
-// Encoder division x / f over the full 32-bit range for f in [2, 65536]
-// (Granlund & Montgomery, PLDI 1994, figure 4.1): l = ceil(log2 f),
-// m = floor(2^32 (2^l - f) / f) + 1, t = mulhi(x, m),
-// q = (t + ((x - t) >> 1)) >> (l - 1).  f = 1 is handled by the caller.
-uint32_t enc_magic(uint32_t f) {
-  if (f < 2) return 0;
-  uint32_t l = 0;
-  while (((uint64_t)1 << l) < f) ++l;
-  return (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << l) - f)) / f + 1);
-}
-
-__host__ __device__ inline uint32_t enc_shift(uint32_t f) {  // l - 1, for f >= 2
-#if defined(__HIP_DEVICE_COMPILE__)
-  return 31u - (uint32_t)__clz((int)(f - 1u));
-#else
-  uint32_t l = 0;
-  while (((uint64_t)1 << l) < f) ++l;
-  return l - 1;
-#endif
-}
-
-__host__ __device__ inline uint32_t enc_div(uint32_t x, uint32_t m, uint32_t sh) {
-  const uint32_t t = mulhi32(x, m);
-  return (t + ((x - t) >> 1)) >> sh;
-}
-
-// Index hash term of chunk position p with table tb: MurmurHash3's 32-bit
-// finaliser (Appleby) of p * 0x9E3779B9 + tb + 1; a chunk's hash is the sum
-// of its terms mod 2^32 (a bijective finaliser, so positions that trade
-// tables change the sum except with probability about 2^-32).
-__host__ __device__ __forceinline__ uint32_t index_term(uint32_t p, uint32_t tb) {
-  uint32_t h = p * kHashMul + tb + 1u;
-  h ^= h >> 16;
-  h *= 0x85EBCA6Bu;
-  h ^= h >> 13;
-  h *= 0xC2B2AE35u;
-  h ^= h >> 16;
-  return h;
-}
-
-// Chunks and coding units.  Chunk k of a row covers the positions
-// [k chunk_len, min((k + 1) chunk_len, N)) (P channels), Tc steps of 64
-// positions; it is split into S segments, segment s holding the steps
-// [floor(s Tc / S), floor((s + 1) Tc / S)).  A segment is a coding unit, coded
-// independently (own states, stream and escape section) by its own
-// workgroup: unit g = (b K + k) S + s, U = B K S units.
-struct Layout {
-  int64_t B, N, C, P, S, HW, K, chunk_len, U, seg_cap, header_bytes, max_payload, cap_words,
-      ws_bytes;
-  int64_t o_words_cnt, o_status, o_hash, o_end, o_info, o_states, o_words, o_esc, o_esc_raw;
-};
-
-int make_layout(int64_t B, int64_t N, int64_t C, int64_t P, int64_t S, Layout* L) {
-  if (B < 1 || N < 1 || C < 1 || P < 1)
-    return fail(GAANS_EINVAL, "B, N, C and P must be >= 1 (got %lld, %lld, %lld, %lld)",
-                (long long)B, (long long)N, (long long)C, (long long)P);
-  if (N % C != 0)
-    return fail(GAANS_EINVAL, "symbols per row N=%lld is not a multiple of channels C=%lld",
-                (long long)N, (long long)C);
-  if (P > C) return fail(GAANS_EINVAL, "P=%lld exceeds channels C=%lld", (long long)P, (long long)C);
-  if (N >= ((int64_t)1 << 31) || B >= ((int64_t)1 << 31))
-    return fail(GAANS_EINVAL, "B and N must be < 2^31");
-  L->B = B; L->N = N; L->C = C; L->P = P; L->S = S;
-  L->HW = N / C;
-  L->K = (C + P - 1) / P;
-  L->chunk_len = P * L->HW;
-  // every segment holds at least one step: S <= the steps of the last
-  // (shortest) chunk of a row
-  const int64_t t_last = (N - (L->K - 1) * L->chunk_len + kLanes - 1) / kLanes;
-  if (S < 1 || S > kMaxSegments || S > t_last)
-    return fail(GAANS_EINVAL,
-                "segments per chunk must be in [1, %lld] for this shape (got %lld)",
-                (long long)(t_last < kMaxSegments ? t_last : kMaxSegments), (long long)S);
-  L->U = B * L->K * S;
-  if (L->U >= ((int64_t)1 << 31)) return fail(GAANS_EINVAL, "too many coding units");
-  if ((int64_t)kMaxEscNibbles * L->chunk_len + 8 >= ((int64_t)1 << 31))
-    return fail(GAANS_EINVAL, "chunk of %lld symbols is too large", (long long)L->chunk_len);
-  // the longest unit: ceil(Tc / S) steps of the longest chunk
-  const int64_t tc = (L->chunk_len + kLanes - 1) / kLanes;
-  L->seg_cap = std::min<int64_t>(L->chunk_len, kLanes * ((tc + S - 1) / S));
-  L->header_bytes = align_up(4 * kFixedWords + 8 * L->U, 16);
-  // per symbol at most one stream word and 9 escape nibbles; per unit the
-  // states, a pad word and a partly used escape word
-  L->max_payload = L->header_bytes + B * N * 7 + L->U * (4 * kLanes + 8);
-  L->cap_words = align_up(L->seg_cap + 2, 2);
-  int64_t o = 0;
-  L->o_words_cnt = o; o = align_up(o + 4 * L->U, 256);
-  L->o_status = o;    o = align_up(o + 4 * L->U, 256);
-  L->o_hash = o;      o = align_up(o + 4 * L->U, 256);
-  L->o_end = o;       o = align_up(o + 4 * L->U, 256);
-  L->o_info = o;      o = align_up(o + 32, 256);
-  L->o_states = o;    o = align_up(o + 4 * kLanes * L->U, 256);
-  L->o_words = o;     o = align_up(o + 2 * L->cap_words * L->U, 256);
-  L->o_esc = o;       o = align_up(o + 8 * L->U, 256);
-  L->o_esc_raw = o;   o = align_up(o + 4 * L->seg_cap * L->U, 256);
-  L->ws_bytes = o;
-  return GAANS_OK;
-}
 
 // ---- wave helpers -----------------------------------------------------------
 
@@ -328,37 +135,6 @@ __device__ __forceinline__ TabHdr load_tab_hdr(const uint8_t* tables) {
   return *reinterpret_cast<const TabHdr*>(tables);
 }
 
-// Coding unit g = (b K + k) S + s (see Layout): row offset b N, first
-// position in the row, symbol count, and chunk k.
-__host__ __device__ __forceinline__ void unit_range(int64_t g, int32_t K, int32_t S, int64_t N,
-                                                    int32_t chunk_len, int64_t& row,
-                                                    int32_t& start, int& len, int& k) {
-  const int64_t per_row = (int64_t)K * S;
-  const int64_t b = g / per_row;
-  const int32_t r = (int32_t)(g - b * per_row);
-  k = r / S;
-  const int32_t s = r - k * S;
-  row = b * N;
-  const int32_t cs = k * chunk_len;
-  const int32_t ce = (int64_t)cs + chunk_len < N ? cs + chunk_len : (int32_t)N;
-  const int32_t tc = (ce - cs + kLanes - 1) / kLanes;
-  const int32_t t0 = (int32_t)((int64_t)s * tc / S), t1 = (int32_t)((int64_t)(s + 1) * tc / S);
-  start = cs + kLanes * t0;
-  const int32_t e = cs + kLanes * t1 < ce ? cs + kLanes * t1 : ce;
-  len = e - start;
-}
-
-__host__ __device__ __forceinline__ int unit_len(int64_t g, int32_t K, int32_t S, int64_t N,
-                                                 int32_t chunk_len) {
-  int64_t row;
-  int32_t start;
-  int len, k;
-  unit_range(g, K, S, N, chunk_len, row, start, len, k);
-  return len;
-}
-
-// Tables of one chunk: a staged range [t_lo, t_lo + nt) in LDS, the rest in
-// global memory.
 struct Tabs {
   const TabMeta* __restrict__ gmeta;
   const uint2* __restrict__ gent;
@@ -2303,23 +2079,6 @@ int check_tables_arg(const gaans_tables* t) {
   return GAANS_OK;
 }
 
-// Blob sections: [header][metadata][entries][lookups][sub-blocks][search
-// lookups][starts]; the offsets of the last two follow from the counts.
-struct BlobLayout {
-  int64_t ent_off, lut_off, dense_off, clut_off, starts_off, end;
-};
-
-BlobLayout blob_layout(int64_t M, int64_t total_syms, int64_t total_blocks) {
-  BlobLayout L;
-  L.ent_off = align_up((int64_t)sizeof(TabHdr) + (int64_t)sizeof(TabMeta) * M, 8);
-  L.lut_off = align_up(L.ent_off + 8 * total_syms, 16);
-  L.dense_off = L.lut_off + 8ll * kLutSize * M;
-  L.clut_off = L.dense_off + (int64_t)kSubBytes * total_blocks;
-  L.starts_off = L.clut_off + 4ll * kLutSize * M;
-  L.end = L.starts_off + align_up(2 * (total_syms + kStartsPad), 16);
-  return L;
-}
-
 // Section offsets of the blob a descriptor describes (the layout written by
 // gaans_tables_prepare); the descriptor's size must match them.
 int blob_ref(const gaans_tables* t, BlobRef* r) {
@@ -2747,91 +2506,6 @@ int decode_impl(int mode, void* stream, const uint8_t* payload, int64_t payload_
   return check_launch("decode");
 }
 
-uint64_t fnv_u32(uint64_t h, uint32_t v) {
-  for (int i = 0; i < 4; ++i) {
-    h ^= (v >> (8 * i)) & 0xffu;
-    h *= 0x100000001b3ull;
-  }
-  return h;
-}
-
-int64_t tables_size(int32_t M, int64_t total_syms, int64_t total_blocks) {
-  return blob_layout(M, total_syms, total_blocks).end;
-}
-
-// Search lookups of one table (symbols base .. base + nsym - 1 of the blob):
-// per 256-value bucket, the symbol that contains the bucket's first value
-// (blob-wide index) in the low half and the number of symbols that start
-// inside the bucket after it in the high half; starts[base + s] = cdf[s].
-void build_search(const int32_t* c, uint32_t nsym, uint32_t base, uint32_t* clut,
-                  uint16_t* starts) {
-  for (uint32_t v = 0; v < nsym; ++v) starts[base + v] = (uint16_t)c[v];
-  const uint32_t width = 1u << (16 - kLutBits);
-  uint32_t s = 0;
-  for (uint32_t b = 0; b < (uint32_t)kLutSize; ++b) {
-    const uint32_t lo = b * width;
-    while (s + 1 < nsym && (uint32_t)c[s + 1] <= lo) ++s;
-    uint32_t n = 0;
-    while (s + 1 + n < nsym && (uint32_t)c[s + 1 + n] < lo + width) ++n;
-    clut[b] = (base + s) | ((n < 0xffffu ? n : 0xffffu) << 16);
-  }
-}
-
-// Decode lookup entry of the cum range [lo, lo + width) of a CDF with nsym
-// symbols (cdf c) into *out; false when the range is dense (two or more
-// symbols start after lo).  s is advanced to the symbol containing lo.
-bool lookup_entry(const int32_t* c, uint32_t nsym, uint32_t lo, uint32_t width, uint32_t& s,
-                  uint64_t* out) {
-  while (s + 1 < nsym && (uint32_t)c[s + 1] <= lo) ++s;
-  uint32_t e = s;
-  while (e + 1 < nsym && (uint32_t)c[e + 1] <= lo + width - 1) ++e;
-  if (e - s >= 2) return false;
-  const uint32_t next = s + 1 < nsym ? (uint32_t)(c[s + 2] - c[s + 1] - 1) : 0u;
-  const uint32_t lo_word = (uint32_t)c[s] | ((uint32_t)(c[s + 1] - 1) << 16);
-  *out = (uint64_t)lo_word | ((uint64_t)(s | (next << 16)) << 32);
-  return true;
-}
-
-// Sub-blocks of one CDF (S entries): one per dense 256-value bucket, one per
-// dense 16-value sub-range of those.  Fills them when blocks is non-NULL
-// (global indices from `first`) and the table's 256 lookup entries in lut.
-int32_t build_lookup(const int32_t* c, int32_t S, uint64_t* lut, uint64_t* blocks,
-                     uint32_t first) {
-  const uint32_t nsym = (uint32_t)(S - 1);
-  int32_t n = 0;
-  uint32_t s = 0;
-  for (int j = 0; j < kLutSize; ++j) {
-    const uint32_t lo = (uint32_t)j << (16 - kLutBits);
-    uint64_t e;
-    if (lookup_entry(c, nsym, lo, 1u << (16 - kLutBits), s, &e)) {
-      if (lut) lut[j] = e;
-      continue;
-    }
-    const uint32_t b2 = (uint32_t)n++;
-    if (lut) lut[j] = (uint64_t)(first + b2) | ((uint64_t)(s | (0xffffu << 16)) << 32);
-    uint32_t s2 = s;
-    for (int i = 0; i < kSubSize; ++i) {
-      const uint32_t lo2 = lo + ((uint32_t)i << kSubBits);
-      uint64_t e2;
-      if (lookup_entry(c, nsym, lo2, kSubSize, s2, &e2)) {
-        if (blocks) blocks[(size_t)b2 * kSubSize + i] = e2;
-        continue;
-      }
-      const uint32_t b3 = (uint32_t)n++;
-      if (blocks)
-        blocks[(size_t)b2 * kSubSize + i] =
-            (uint64_t)(first + b3) | ((uint64_t)(s2 | (0xffffu << 16)) << 32);
-      uint32_t s3 = s2;
-      for (int v = 0; v < kSubSize; ++v) {
-        uint64_t e3 = 0;
-        lookup_entry(c, nsym, lo2 + (uint32_t)v, 1u, s3, &e3);  // one value: never dense
-        if (blocks) blocks[(size_t)b3 * kSubSize + v] = e3;
-      }
-    }
-  }
-  return n;
-}
-
 // CompressAI Rans64 streams: plan the LDS (all tables; else, with implicit
 // indexes, one channel's table at a time; else global lookups) and launch.
 int rans64_decode_impl(void* stream, const uint8_t* streams, int64_t streams_bytes,
@@ -2961,185 +2635,6 @@ int noalloc_scratch(hipStream_t stream, uint8_t** out) {
 // =============================================================================
 
 extern "C" {
-
-int gaans_abi_version(void) { return GAANS_ABI_VERSION; }
-
-const char* gaans_last_error(void) { return g_last_error.c_str(); }
-
-int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, int32_t segments,
-                     gaans_layout* out) {
-  if (!out) return fail(GAANS_EINVAL, "layout pointer is NULL");
-  Layout L;
-  int rc = make_layout(B, N, C, P, segments, &L);
-  if (rc) return rc;
-  out->B = L.B; out->N = L.N; out->C = L.C; out->P = L.P; out->S = L.S;
-  out->HW = L.HW; out->K = L.K; out->chunk_len = L.chunk_len; out->U = L.U;
-  out->header_bytes = L.header_bytes;
-  out->max_payload_bytes = L.max_payload;
-  out->cap_words = L.cap_words;
-  out->workspace_bytes = L.ws_bytes;
-  out->ws_chunk_words = L.o_words_cnt;
-  out->ws_chunk_status = L.o_status;
-  out->ws_index_hash = L.o_hash;
-  out->ws_end_off = L.o_end;
-  out->ws_info = L.o_info;
-  out->ws_states = L.o_states;
-  out->ws_words = L.o_words;
-  out->ws_esc = L.o_esc;
-  out->ws_esc_raw = L.o_esc_raw;
-  return GAANS_OK;
-}
-
-int gaans_choose_segments(const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
-                          int64_t P, double budget, int64_t target_units, int32_t* segments) {
-  if (!tables || !segments) return fail(GAANS_EINVAL, "NULL argument");
-  Layout L;
-  int rc = make_layout(B, N, C, P, 1, &L);
-  if (rc) return rc;
-  if (!(budget >= 0.0) || !(tables->mean_bits >= 0.0f))
-    return fail(GAANS_EINVAL, "budget and the tables' mean_bits must be non-negative numbers");
-  // the most segments the shape allows: one step each in the shortest chunk
-  const int64_t t_last = (N - (L.K - 1) * L.chunk_len + kLanes - 1) / kLanes;
-  int64_t s = std::min<int64_t>(kMaxSegments, t_last);
-  // enough units to fill target_units workgroups, no more
-  if (target_units > 0) s = std::min<int64_t>(s, (target_units + L.U - 1) / L.U);
-  // bytes an added unit costs, against the expected bytes of a full chunk:
-  // its A final states (4 A) less what its fresh initial states absorb
-  // before they emit, plus a pad and a partly used escape word; measured
-  // 200-203 bytes per added unit of 64 lanes on every workload of the
-  // benchmark (2160x3840 P=8, 512x768 P=4, hyperprior y P=16), so 3.125 A + 4
-  const int64_t len = L.chunk_len < L.N ? L.chunk_len : L.N;
-  const int64_t A = len < kLanes ? len : kLanes;
-  const double expected = (double)len * tables->mean_bits / 8.0 + 4.0 * (double)A;
-  const double per_seg = 3.125 * (double)A + 4.0;
-  s = std::min<int64_t>(s, 1 + (int64_t)(budget * expected / per_seg));
-  *segments = (int32_t)std::max<int64_t>(s, 1);
-  return GAANS_OK;
-}
-
-int gaans_tables_bytes(const int32_t* cdfs, const int32_t* cdf_sizes, int32_t M, int32_t Lmax,
-                       int64_t* bytes) {
-  if (!cdfs || !cdf_sizes || !bytes) return fail(GAANS_EINVAL, "NULL argument");
-  // decode records carry a table number and an escape symbol in 16 bits each
-  if (M < 1 || M > 65536 || Lmax < 2)
-    return fail(GAANS_EINVAL, "need 1 <= M <= 65536 tables of Lmax >= 2 entries (got M=%d)", M);
-  int64_t total = 0, dense = 0;
-  for (int32_t t = 0; t < M; ++t) {
-    const int32_t S = cdf_sizes[t];
-    if (S < 2 || S > Lmax || S > 65536)
-      return fail(GAANS_ETABLE, "table %d: cdf size %d outside [2, %d]", t, S,
-                  Lmax < 65536 ? Lmax : 65536);
-    total += S - 1;
-    dense += build_lookup(cdfs + (int64_t)t * Lmax, S, nullptr, nullptr, 0u);
-  }
-  *bytes = tables_size(M, total, dense);
-  if (*bytes > 0xffffffffll) return fail(GAANS_ETABLE, "tables exceed 4 GiB");
-  return GAANS_OK;
-}
-
-int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const int32_t* offsets,
-                         int32_t M, int32_t Lmax, void* out, int64_t out_bytes,
-                         gaans_tables* desc) {
-  if (!cdfs || !offsets || !out || !desc) return fail(GAANS_EINVAL, "NULL argument");
-  int64_t need = 0;
-  int rc = gaans_tables_bytes(cdfs, cdf_sizes, M, Lmax, &need);
-  if (rc) return rc;
-  if (out_bytes < need)
-    return fail(GAANS_EINVAL, "table buffer too small (%lld < %lld)", (long long)out_bytes,
-                (long long)need);
-  for (int32_t t = 0; t < M; ++t) {
-    const int32_t S = cdf_sizes[t];
-    const int32_t* c = cdfs + (int64_t)t * Lmax;
-    if (c[0] != 0 || c[S - 1] != 65536)
-      return fail(GAANS_ETABLE, "table %d: CDF must start at 0 and end at 65536", t);
-    for (int32_t j = 0; j + 1 < S; ++j)
-      if (c[j + 1] <= c[j])
-        return fail(GAANS_ETABLE, "table %d: CDF is not strictly increasing at entry %d", t, j);
-  }
-  uint8_t* o = static_cast<uint8_t*>(out);
-  memset(o, 0, (size_t)need);
-  TabHdr* h = reinterpret_cast<TabHdr*>(o);
-  TabMeta* meta = reinterpret_cast<TabMeta*>(o + sizeof(TabHdr));
-  const int64_t ent_off = align_up(sizeof(TabHdr) + (int64_t)sizeof(TabMeta) * M, 8);
-  uint32_t* ent = reinterpret_cast<uint32_t*>(o + ent_off);
-  int64_t total = 0, total_dense = 0;
-  uint32_t max_nsym = 0;
-  int32_t max_dense = 0;
-  for (int32_t t = 0; t < M; ++t) {
-    total += cdf_sizes[t] - 1;
-    if ((uint32_t)(cdf_sizes[t] - 1) > max_nsym) max_nsym = (uint32_t)(cdf_sizes[t] - 1);
-    const int32_t nd = build_lookup(cdfs + (int64_t)t * Lmax, cdf_sizes[t], nullptr, nullptr, 0u);
-    total_dense += nd;
-    if (nd > max_dense) max_dense = nd;
-  }
-  const BlobLayout BL = blob_layout(M, total, total_dense);
-  const int64_t lut_off = BL.lut_off;
-  uint64_t* lut = reinterpret_cast<uint64_t*>(o + lut_off);
-  const int64_t dense_off = BL.dense_off;
-  uint64_t* blocks = reinterpret_cast<uint64_t*>(o + dense_off);
-  uint32_t* clut = reinterpret_cast<uint32_t*>(o + BL.clut_off);
-  uint16_t* starts = reinterpret_cast<uint16_t*>(o + BL.starts_off);
-  bool search = total <= kSearchMaxSyms;
-  for (int32_t t = 0; t < M; ++t) search &= offsets[t] >= INT32_MIN + 65536;
-  uint32_t dblk = 0;
-  double bits = 0.0;  // sum over tables of the table's entropy
-  uint64_t dg = 0xcbf29ce484222325ull;
-  dg = fnv_u32(dg, (uint32_t)M);
-  uint32_t base = 0;
-  for (int32_t t = 0; t < M; ++t) {
-    const int32_t S = cdf_sizes[t];
-    const int32_t* c = cdfs + (int64_t)t * Lmax;
-    dg = fnv_u32(dg, (uint32_t)S);
-    dg = fnv_u32(dg, (uint32_t)offsets[t]);
-    for (int32_t j = 0; j < S; ++j) dg = fnv_u32(dg, (uint32_t)c[j]);
-    const uint32_t nsym = (uint32_t)(S - 1);
-    meta[t].ent_base = base;
-    meta[t].nsym = nsym;
-    meta[t].offset = offsets[t];
-    meta[t].dense_base = dblk;
-    for (uint32_t v = 0; v < nsym; ++v) {
-      const uint32_t f = (uint32_t)(c[v + 1] - c[v]);
-      ent[2 * (base + v)] = (uint32_t)c[v] | ((f - 1u) << 16);
-      ent[2 * (base + v) + 1] = enc_magic(f);
-      const double pr = f / 65536.0;
-      bits -= pr * log2(pr);
-    }
-    dblk += (uint32_t)build_lookup(c, S, lut + (int64_t)t * kLutSize,
-                                   blocks + (size_t)dblk * kSubSize, dblk);
-    if (search) build_search(c, nsym, base, clut + (int64_t)t * kLutSize, starts);
-    base += nsym;
-  }
-  h->magic = kTabMagic;
-  h->M = (uint32_t)M;
-  h->total_syms = (uint32_t)total;
-  h->lut_bits = kLutBits;
-  h->digest_lo = (uint32_t)dg;
-  h->digest_hi = (uint32_t)(dg >> 32);
-  h->meta_off = sizeof(TabHdr);
-  h->ent_off = (uint32_t)ent_off;
-  h->lut_off = (uint32_t)lut_off;
-  h->total_bytes = (uint32_t)need;
-  h->max_nsym = max_nsym;
-  h->dense_off = (uint32_t)dense_off;
-  h->total_dense = (uint32_t)total_dense;
-  h->clut_off = (uint32_t)BL.clut_off;
-  h->starts_off = (uint32_t)BL.starts_off;
-  bool safe = true;
-  for (int32_t t = 0; t < M; ++t) safe &= offsets[t] <= INT32_MAX - 65535;
-  h->flags = (safe ? kTabOffsetsSafe : 0u) | (search ? kTabSearch : 0u);
-  desc->dev = nullptr;
-  desc->bytes = need;
-  desc->flags = search ? GAANS_TABLES_SEARCH : 0;
-  desc->M = M;
-  desc->max_nsym = (int32_t)max_nsym;
-  desc->total_nsym = total;
-  desc->digest = dg;
-  desc->max_dense = max_dense;
-  desc->total_dense = total_dense;
-  desc->mean_bits = (float)(bits / M);
-  desc->reserved = 0;
-  return GAANS_OK;
-}
 
 int gaans_encode_symbols(void* stream, const int32_t* symbols_dev, const int32_t* indexes_dev,
                          const gaans_tables* tables, int64_t B, int64_t N, int64_t C, int64_t P,
@@ -3291,47 +2786,6 @@ int gaans_wait_host_word(void* stream, const uint32_t* word) {
         return fail(GAANS_EHIP, "stream reported an error: %s", hipGetErrorString(e));
     }
   }
-}
-
-int gaans_host_selftest(void) {
-  // 1. magic division by the channel length: every divisor class against exact division
-  const uint32_t ds[] = {1, 2, 3, 5, 7, 16, 48, 64, 96, 100, 255, 256, 1000, 1536, 4096,
-                         32640, 65535, 65536, 65537, 1000003, (1u << 30) - 1, 1u << 30,
-                         (1u << 31) - 1};
-  uint64_t rng = 0x243F6A8885A308D3ull;
-  for (uint32_t d : ds) {
-    UDiv u = make_udiv(d);
-    for (int i = 0; i < 20000; ++i) {
-      rng = rng * 6364136223846793005ull + 1442695040888963407ull;
-      uint32_t n = (uint32_t)(rng >> 33);  // < 2^31
-      if (i < 64) n = (uint32_t)i;
-      if (i >= 64 && i < 128) n = (uint32_t)((uint64_t)d * (uint64_t)(i - 63) - 1u);
-      if (n >= (1u << 31)) continue;
-      if (udiv(n, u) != n / d) return fail(1, "udiv selftest failed d=%u n=%u", d, n);
-    }
-    if (udiv((1u << 31) - 1u, u) != ((1u << 31) - 1u) / d)
-      return fail(1, "udiv selftest failed at n=2^31-1, d=%u", d);
-  }
-  // 2. encoder division: the full-range magic of every freq in [2, 65536] at
-  //    quotient boundaries and at the ends of the coded range [0, f 2^16)
-  for (uint32_t f = 2; f <= 65536; ++f) {
-    const uint32_t m = enc_magic(f), sh = enc_shift(f);
-    const uint32_t xmax = (uint32_t)(((uint64_t)f << 16) - 1u);
-    const uint32_t xs[10] = {0u, 1u, f - 1u, f, f + 1u, xmax, xmax - 1u, xmax - f,
-                             xmax / 2u, (uint32_t)(((uint64_t)xmax * 2654435761u) >> 32)};
-    for (int k = 0; k < 10; ++k) {
-      const uint32_t x = xs[k];
-      if (enc_div(x, m, sh) != x / f)
-        return fail(2, "encoder division selftest failed f=%u x=%u", f, x);
-    }
-    for (uint32_t qq = 1; qq < 65536u; qq = qq * 3u + 1u) {
-      const uint64_t lo = (uint64_t)qq * f;
-      if (lo > xmax) break;
-      if (enc_div((uint32_t)lo, m, sh) != qq || enc_div((uint32_t)(lo - 1u), m, sh) != qq - 1u)
-        return fail(2, "encoder division selftest failed f=%u q=%u", f, qq);
-    }
-  }
-  return GAANS_OK;
 }
 
 }  // extern "C"

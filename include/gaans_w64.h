@@ -140,7 +140,8 @@ int gaans_choose_segments(const gaans_tables* tables, int64_t B, int64_t N, int6
 /* ---- table upload (host memory) ----------------------------------------- */
 
 /* Bytes of the prepared table blob for M tables (cdfs [M, Lmax] and
- * cdf_sizes in host memory; the size depends on the CDF values). */
+ * cdf_sizes in host memory; the size depends on the CDF values).  Validates
+ * the tables as gaans_tables_prepare does (GAANS_ETABLE otherwise). */
 int gaans_tables_bytes(const int32_t* cdfs, const int32_t* cdf_sizes, int32_t M, int32_t Lmax,
                        int64_t* bytes);
 

@@ -23,7 +23,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "lib", "libgaans_oracle.so")
+# GAANS_ORACLE_LIB selects another build of the same source (the sanitizer
+# tests load one built with -fsanitize=address,undefined)
+_LIB_PATH = os.environ.get("GAANS_ORACLE_LIB") or os.path.join(_HERE, "lib", "libgaans_oracle.so")
 _lib = None
 
 ERRORS = {

@@ -1,0 +1,82 @@
+"""CPU runs under AddressSanitizer and UndefinedBehaviorSanitizer.
+
+1. The library's host-only code (fast-compressai_amd/csrc/gaans_host.cpp:
+   table validation and preparation, layout, segment choice, self test) is
+   built with g++ -fsanitize=address,undefined and driven by
+   tests/host_fuzz.py with valid and malformed tables and shapes.
+2. The oracle (oracle/gaans_oracle.c) is built the same way
+   (make -C oracle SAN=... OUT=...) and its own tests (tests/test_oracle.py,
+   tests/test_golden.py) run against that build.
+
+Each run is a child process with the sanitizer runtimes preloaded (the Python
+interpreter itself is not instrumented); any report aborts it with a non-zero
+status.
+"""
+
+import os
+import shutil
+import subprocess
+import sys
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+SAN = ["-fsanitize=address,undefined", "-fno-sanitize-recover=all", "-fno-omit-frame-pointer",
+       "-g"]
+
+
+def runtimes():
+    libs = []
+    for name in ("libasan.so", "libubsan.so"):
+        path = subprocess.run(["gcc", f"-print-file-name={name}"], capture_output=True,
+                              text=True).stdout.strip()
+        if not os.path.isabs(path) or not os.path.exists(path):
+            return None
+        libs.append(path)
+    return " ".join(libs)
+
+
+def env_with_sanitizers(preload, **extra):
+    env = dict(os.environ)
+    env["LD_PRELOAD"] = preload
+    env["ASAN_OPTIONS"] = "detect_leaks=0:abort_on_error=1"
+    env["UBSAN_OPTIONS"] = "print_stacktrace=1:halt_on_error=1"
+    env.update(extra)
+    return env
+
+
+needs_toolchain = pytest.mark.skipif(
+    shutil.which("g++") is None or shutil.which("make") is None or runtimes() is None,
+    reason="g++, make or the ASan/UBSan runtimes are not available")
+
+
+@needs_toolchain
+def test_host_code_under_asan_ubsan(tmp_path):
+    lib = tmp_path / "libgaans_host_san.so"
+    csrc = os.path.join(REPO, "fast-compressai_amd", "csrc")
+    subprocess.run(["g++", "-std=c++17", "-O1", *SAN, "-fPIC", "-shared",
+                    "-I", os.path.join(REPO, "include"), "-I", csrc,
+                    os.path.join(csrc, "gaans_host.cpp"), "-o", str(lib)], check=True)
+    proc = subprocess.run([sys.executable, os.path.join(REPO, "tests", "host_fuzz.py"), str(lib),
+                           "300"], env=env_with_sanitizers(runtimes()), capture_output=True,
+                          text=True, timeout=600)
+    report = proc.stdout[-3000:] + proc.stderr[-3000:]
+    assert proc.returncode == 0, report
+    assert "host fuzz ok" in proc.stdout
+    assert "runtime error" not in proc.stderr and "AddressSanitizer" not in proc.stderr, report
+
+
+@needs_toolchain
+def test_oracle_under_asan_ubsan(tmp_path):
+    lib = tmp_path / "libgaans_oracle_san.so"
+    subprocess.run(["make", "-s", "-C", os.path.join(REPO, "oracle"), f"OUT={lib}",
+                    "SAN=" + " ".join(SAN)], check=True)
+    proc = subprocess.run(
+        [sys.executable, "-m", "pytest", "-q", "-p", "no:cacheprovider",
+         os.path.join(REPO, "tests", "test_oracle.py"),
+         os.path.join(REPO, "tests", "test_golden.py")],
+        cwd=REPO, env=env_with_sanitizers(runtimes(), GAANS_ORACLE_LIB=str(lib)),
+        capture_output=True, text=True, timeout=900)
+    report = proc.stdout[-3000:] + proc.stderr[-3000:]
+    assert proc.returncode == 0, report
+    assert "runtime error" not in proc.stderr and "AddressSanitizer" not in proc.stderr, report
