@@ -60,17 +60,20 @@ namespace {
 #define GAANS_MAPPERS 4
 #endif
 constexpr int kMappers = GAANS_MAPPERS;  // mapper waves per decode workgroup
-#ifndef GAANS_ENC_MAPPERS
-#define GAANS_ENC_MAPPERS GAANS_MAPPERS
-#endif
-constexpr int kEncMappers = GAANS_ENC_MAPPERS;  // mapper waves per encode workgroup
-constexpr int kWaves = kEncMappers + 1;  // encoder: + the coder wave
-constexpr int kThreads = kWaves * kLanes;
+// Encode workgroups: a coder wave and 4 mapper waves when several
+// workgroups share a CU, 8 when each has a CU to itself (the mappers are the
+// encoder's slower half: 8 take the 2160x3840 latent from 456 to 446 us and
+// the hyperprior y at P=16 from 91 to 68 us, while at three workgroups per
+// CU 8 cost more than they bring)
+constexpr int kEncMaxWaves = 9;
 
 // per-wave hash, status and escape nibbles, then the escape count
-constexpr int kPartBytes = (12 * kWaves + 4 + 15) / 16 * 16;
+constexpr int kPartBytes = (12 * kEncMaxWaves + 4 + 15) / 16 * 16;
 constexpr int kRingWords = 4096;       // encoder LDS output ring (u16 words)
 constexpr int kPfU32Max = 8;  // decoder stream prefetch: u32 per lane (16-step blocks)
+// word 3 of a raw buffer resource on gfx9 (32-bit data format; stride 0, so
+// num_records counts bytes)
+constexpr int kBufferFlags = 0x00020000;
 constexpr int kMaxDevices = 64;
 // control block (u32 words); encoder and decoder fields on separate 64-byte lines
 constexpr int kCtrlEncDone = 0;
@@ -183,7 +186,7 @@ __device__ __forceinline__ void stage_pass(const Tabs& T, uint4* lmeta, uint2* l
                                            int tid) {
   // loads in flight per thread and kind (fewer for the decoder's larger
   // workgroup, whose waves keep more registers live across the staging)
-  constexpr int U = NT > kThreads ? 3 : 4;
+  constexpr int U = NT >= 384 ? 3 : 4;
   uint32_t items = nt;
   if (kEnt) items = items > ne ? items : ne;
   if (kSub) items = items > nd ? items : nd;
@@ -384,18 +387,21 @@ constexpr int kEncRingBytes = 2 * (kRingWords + kLanes);  // + one spare slot pe
 
 // Encoder geometry for blocks of SB steps (the mappers' lead over the coder
 // and the steps between two barriers).
-template <int SB>
+template <int SB, int NM>
 struct EncGeom {
+  static constexpr int kWaves = NM + 1;  // the coder and NM mappers
+  static constexpr int kThreads = kWaves * kLanes;
   // steps per mapper wave and block
-  static constexpr int kPer = (SB + kEncMappers - 1) / kEncMappers;
+  static constexpr int kPer = (SB + NM - 1) / NM;
   static constexpr int kRecBytes = 2 * SB * kLanes * 16;       // two blocks of op records
   static constexpr int kFlagBytes = 16;  // per block parity: steps with escapes (bit per step)
   // [ring][records][flags][parts]
   static constexpr int kFixed = kEncRingBytes + kRecBytes + kFlagBytes + kPartBytes;
 };
 
-int enc_fixed_lds(int sb) {
-  return sb >= 16 ? EncGeom<16>::kFixed : (sb >= 8 ? EncGeom<8>::kFixed : EncGeom<4>::kFixed);
+int enc_fixed_lds(int sb) {  // the same for either mapper count
+  return sb >= 16 ? EncGeom<16, 4>::kFixed
+                  : (sb >= 8 ? EncGeom<8, 4>::kFixed : EncGeom<4, 4>::kFixed);
 }
 
 // Payload bytes of unit g: states, stream and escape words, pad.
@@ -414,7 +420,9 @@ __device__ __forceinline__ uint64_t unit_bytes(const EncArgs& a, int64_t g) {
 // thread, with the next tile's loads issued before the current tile's scan.
 // The completion word carries size and status in one 64-bit store, so the
 // host can read it as soon as it lands (no system-wide cache write-back).
+template <int NT>
 __device__ void encode_finish(const EncArgs& a, int tid, uint64_t* sh) {
+  constexpr int kThreads = NT, kWaves = NT / kLanes;
   const int lane = tid & (kLanes - 1), wv = tid >> 6;
   uint64_t carry = 0;
   uint32_t st = 0;
@@ -606,9 +614,11 @@ __device__ __forceinline__ void enc_escapes(const uint4 r, uint32_t* __restrict_
   cnt = uni(cnt + __popcll(em));
 }
 
-template <int kMode, bool kImplicit, int SB>
-__global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
-  using G = EncGeom<SB>;
+template <int kMode, bool kImplicit, int SB, int NM>
+__global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
+  using G = EncGeom<SB, NM>;
+  constexpr int kEncMappers = NM;
+  constexpr int kWaves = G::kWaves, kThreads = G::kThreads;
   constexpr int kPer = G::kPer;
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t* ring = reinterpret_cast<uint16_t*>(smem);
@@ -837,7 +847,7 @@ __global__ __launch_bounds__(kThreads) void k_encode(EncArgs a) {
   __syncthreads();
   if (part[0] == (uint32_t)(a.units - 1)) {  // uniform: the last workgroup to finish
     __syncthreads();  // every wave has read part[0] before it is reused
-    encode_finish(a, tid, reinterpret_cast<uint64_t*>(part));
+    encode_finish<kThreads>(a, tid, reinterpret_cast<uint64_t*>(part));
   }
 }
 
@@ -1213,16 +1223,29 @@ __device__ void stage_search(Tabs& T, uint4* lmeta, uint32_t* lclut, uint16_t* l
 // words, so refills need no check.
 struct Stream {
   const uint32_t* __restrict__ s32;
-  const uint32_t* __restrict__ safe;  // an in-bounds word of the chunk
+  uint32_t lane_off;  // 4 * lane: the loads' only per-lane operand
   int q, q32, rp, filled;
   uint32_t pf[kPfU32Max];  // the first DecGeom<SB>::kPfU32 in use
 };
 
-// Words past the stream end read the chunk's first state word instead (always
-// in bounds), so the loads need no branch; a refill that reaches them marks
-// the chunk corrupt.
+// u32 i32 + lane of the unit's words (i32 wave-uniform).  The load goes
+// through a buffer resource of the words from i32 on (scalar base and size):
+// past the unit's end it reads 0, with no branch (a refill that reaches such
+// words marks the unit corrupt).  Its only vector operand is the
+// loop-invariant lane offset: the compiler waits for a load to return before
+// any of its vector operands is overwritten, so with a computed vector
+// address the next block's first LDS read waited for the prefetch, which
+// made the one-batch-ahead prefetch synchronous.
 __device__ __forceinline__ uint32_t stream_word32(const Stream& S, int i32) {
-  return *(i32 < S.q32 ? S.s32 + i32 : S.safe);
+  // base and size are wave-uniform: kept in scalar registers (a resource in
+  // vector registers makes the compiler loop over the lanes' values)
+  const uint64_t base = reinterpret_cast<uint64_t>(S.s32 + i32);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(base >> 32));
+  const int left = uni(S.q32 > i32 ? S.q32 - i32 : 0);
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), 0, 4 * left, kBufferFlags);
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)S.lane_off, 0, 0);
 }
 
 // Block start: commit pf if needed, then fetch the next batch.
@@ -1237,7 +1260,7 @@ __device__ __forceinline__ void stream_block_start(Stream& S, uint32_t* ring32, 
     S.filled = uni(S.filled + G::kPfWords);
 #pragma unroll
     for (int kk = 0; kk < G::kPfU32; ++kk)
-      S.pf[kk] = stream_word32(S, (S.filled >> 1) + kk * kLanes + lane);
+      S.pf[kk] = stream_word32(S, (S.filled >> 1) + kk * kLanes);
   }
 }
 
@@ -1247,12 +1270,15 @@ template <int SB>
 __device__ __forceinline__ void dec_refill(bool need, uint32_t& x, Stream& S, const uint16_t* ring,
                                            int lane) {
   const uint64_t m = ballot(need);
-  // every lane reads and only refilling lanes keep the word; no select on the
-  // loaded value (which the compiler would turn into a branch around the
-  // read), and the shift is ready before the read returns
-  const uint32_t w = ring[(S.rp + (int)lane_rank(m)) & (DecGeom<SB>::kRing - 1)];
-  const uint32_t keep = need ? 0xffffu : 0u;
-  x = (x << (need ? 16 : 0)) | (w & keep);
+  // every lane reads (the lane's rank among the refilling lanes, counted on
+  // top of the stream position by mbcnt's accumulator) and only refilling
+  // lanes keep the word: the read stays unconditional (an opaque value for
+  // the compiler, so the select is not turned into a branch around it)
+  const uint32_t pos = __builtin_amdgcn_mbcnt_hi(
+      (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, (uint32_t)S.rp));
+  uint32_t w = ring[pos & (DecGeom<SB>::kRing - 1)];
+  asm volatile("" : "+v"(w));
+  x = need ? ((x << 16) | w) : x;
   S.rp += __popcll(m);
 }
 
@@ -1577,7 +1603,7 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
     uint32_t w0[G::kPre][G::kPfU32];
     if (wid == 0) {
       S.s32 = s32;
-      S.safe = safe;
+      S.lane_off = 4u * (uint32_t)lane;
       S.q = q16;
       S.q32 = q16 / 2;
       S.filled = 0;
@@ -1586,10 +1612,10 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
       for (int b = 0; b < G::kPre; ++b)
 #pragma unroll
         for (int kk = 0; kk < G::kPfU32; ++kk)
-          w0[b][kk] = stream_word32(S, b * (G::kPfWords / 2) + kk * kLanes + lane);
+          w0[b][kk] = stream_word32(S, b * (G::kPfWords / 2) + kk * kLanes);
 #pragma unroll
       for (int kk = 0; kk < G::kPfU32; ++kk)
-        S.pf[kk] = stream_word32(S, G::kPre * (G::kPfWords / 2) + kk * kLanes + lane);
+        S.pf[kk] = stream_word32(S, G::kPre * (G::kPfWords / 2) + kk * kLanes);
     } else if (wid == kEscWave) {
       E.w32 = s32;
       E.safe = safe;
@@ -1633,7 +1659,6 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
       uint32_t ecur = 0;  // escape entries consumed
       __syncthreads();
       for (int j = 0; j < nblk; ++j) {
-        stream_block_start<SB>(S, sring32, lane);
         uint2* src = recs + (j & 1) * SB * kLanes;
         uint4* ei = escm + (j & 1) * SB;
         uint2 r[SB];
@@ -1643,6 +1668,10 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
         // steps whose tables are not all in LDS; cleared for block j + 2
         const uint32_t nl = (uint32_t)uni((int)ctl[2 + (j & 1)]);
         if (lane == 0) ctl[2 + (j & 1)] = 0u;
+        // after the block's LDS reads: the compiler makes the first LDS read
+        // after the prefetch loads wait for them, so they are issued after
+        // the records are read and return during the block's steps
+        stream_block_start<SB>(S, sring32, lane);
         uint64_t any_em = 0;
         if ((j + 1) * SB * kLanes <= len && nl == 0 && offsets_safe) {
           // common case: every lane of the block active, LDS tables, no
@@ -2181,6 +2210,7 @@ struct EncPlan {
   Stage st;
   int sb;
   size_t lds;
+  int64_t occ;  // workgroups per CU the plan allows
 };
 
 // `extra` LDS bytes follow the tables (the Gaussian mode's scale table);
@@ -2194,9 +2224,10 @@ EncPlan plan_encode(const gaans_tables* t, int64_t P, int64_t units, const DevLd
       Stage s;
       const int64_t fixed = enc_fixed_lds(sb);
       if (fit_stage(t, P, 16, 8, 0, lds_budget(d, occ) - fixed - extra, &s, range_ok))
-        return EncPlan{s, sb, (size_t)(fixed + 16 * (int64_t)s.nt_cap + 8 * (int64_t)s.ne_cap)};
+        return EncPlan{s, sb, (size_t)(fixed + 16 * (int64_t)s.nt_cap + 8 * (int64_t)s.ne_cap),
+                       occ};
     }
-  return EncPlan{Stage{0, 0, 0, 0}, 8, (size_t)enc_fixed_lds(8)};
+  return EncPlan{Stage{0, 0, 0, 0}, 8, (size_t)enc_fixed_lds(8), 1};
 }
 
 // Decoder: lookups and metadata per table; sub-blocks when they are staged
@@ -2303,28 +2334,35 @@ int32_t pow2_floor(int32_t v) {  // largest power of two <= v (0 for v < 1)
 using EncKernel = void (*)(EncArgs);
 using DecKernel = void (*)(DecArgs);
 
-template <int kMode, bool kImp>
-EncKernel enc_kernel_sb(int sb) {
-  return sb == 4 ? k_encode<kMode, kImp, 4> : k_encode<kMode, kImp, 8>;
+template <int kMode, bool kImp, int SB>
+EncKernel enc_kernel_nm(int nm) {
+  return nm == 8 ? k_encode<kMode, kImp, SB, 8> : k_encode<kMode, kImp, SB, 4>;
 }
 
-// Encode kernel of a mode, index kind and block size; 16-step blocks are
-// built for explicit or computed indexes only (with table = channel the
-// 16-step kernel needs private scratch).
-EncKernel enc_kernel(int mode, bool imp, int sb) {
+template <int kMode, bool kImp>
+EncKernel enc_kernel_sb(int sb, int nm) {
+  return sb == 4 ? enc_kernel_nm<kMode, kImp, 4>(nm) : enc_kernel_nm<kMode, kImp, 8>(nm);
+}
+
+// Encode kernel of a mode, index kind, block size and mapper count; 16-step
+// blocks are built for explicit or computed indexes only (with table =
+// channel the 16-step kernel needs private scratch).
+EncKernel enc_kernel(int mode, bool imp, int sb, int nm) {
   if (sb == 16) {
     switch (mode) {
-      case kModeGaussian: return k_encode<kModeGaussian, false, 16>;
-      case kModeLatents: return k_encode<kModeLatents, false, 16>;
-      default: return k_encode<kModeSymbols, false, 16>;
+      case kModeGaussian: return enc_kernel_nm<kModeGaussian, false, 16>(nm);
+      case kModeLatents: return enc_kernel_nm<kModeLatents, false, 16>(nm);
+      default: return enc_kernel_nm<kModeSymbols, false, 16>(nm);
     }
   }
   switch (mode) {
-    case kModeGaussian: return enc_kernel_sb<kModeGaussian, false>(sb);
+    case kModeGaussian: return enc_kernel_sb<kModeGaussian, false>(sb, nm);
     case kModeLatents:
-      return imp ? enc_kernel_sb<kModeLatents, true>(sb) : enc_kernel_sb<kModeLatents, false>(sb);
+      return imp ? enc_kernel_sb<kModeLatents, true>(sb, nm)
+                 : enc_kernel_sb<kModeLatents, false>(sb, nm);
     default:
-      return imp ? enc_kernel_sb<kModeSymbols, true>(sb) : enc_kernel_sb<kModeSymbols, false>(sb);
+      return imp ? enc_kernel_sb<kModeSymbols, true>(sb, nm)
+                 : enc_kernel_sb<kModeSymbols, false>(sb, nm);
   }
 }
 
@@ -2429,9 +2467,12 @@ int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y
   if (lds > (size_t)dl.per_block)
     return fail(GAANS_EINVAL, "encode needs %zu bytes of LDS, the device has %d", lds,
                 dl.per_block);
-  const EncKernel kernel = enc_kernel(mode, indexes == nullptr, plan.sb);
+  // 8 mapper waves when every workgroup has a CU to itself
+  const int nm = plan.occ == 1 && L.U <= dl.cus ? 8 : 4;
+  const EncKernel kernel = enc_kernel(mode, indexes == nullptr, plan.sb, nm);
   if ((rc = allow_lds(reinterpret_cast<const void*>(kernel), lds, dl))) return rc;
-  kernel<<<dim3((uint32_t)L.U), dim3(kThreads), lds, static_cast<hipStream_t>(stream)>>>(a);
+  kernel<<<dim3((uint32_t)L.U), dim3((uint32_t)((nm + 1) * kLanes)), lds,
+           static_cast<hipStream_t>(stream)>>>(a);
   return check_launch("encode");
 }
 
