@@ -478,7 +478,8 @@ __device__ void encode_finish(const EncArgs& a, int tid, uint64_t* sh) {
 // Op record of one lane and step (16 bytes):
 //   x: start | (65536 - freq) << 16      (identity op: 0)
 //   y: division magic of freq            (enc_div)
-//   z: shift | (freq == 1) << 5 | escape << 8
+//   z: shift | (freq == 1) << 5 | escape << 8 | (freq - 1) << 16
+//      (identity op: 15 | 0xffff << 16, so that it never emits)
 //   w: escape raw value
 // CompressAI's escape split (reference warp_ans_kernel_v2.cu:139-164):
 // v = sym - offset; v < 0 -> raw = -2v - 1, v >= maxv -> raw = 2 (v - maxv),
@@ -563,10 +564,92 @@ __device__ __forceinline__ void enc_records(const EncArgs& a, const Tabs& tb, in
     uint4 r;
     r.x = ok[e] ? ((ent[e].x & 0xffffu) | ((65536u - fr) << 16)) : 0u;
     r.y = ok[e] ? ent[e].y : 1u;
-    r.z = (ok[e] ? sh : 15u) | ((ok[e] & (fr == 1u)) ? 32u : 0u) | (esc[e] ? 256u : 0u);
+    r.z = (ok[e] ? sh | (ent[e].x & 0xffff0000u) : 0xffff000fu) |
+          ((ok[e] & (fr == 1u)) ? 32u : 0u) | (esc[e] ? 256u : 0u);
     r.w = raw;
     rec[e] = r;
   }
+}
+
+// The records of a full block whose indexes and values are all in range,
+// with the tables in LDS and every table offset at most INT32_MAX - 65535:
+// the same records as enc_records, with the escape split computed only for
+// the steps that have an escaping lane.  With such offsets, sym - offset
+// wraps only to values of at least 65536, so (uint32)(sym - offset) <
+// nsym - 1 tests "ordinary" alone.  Returns false, having changed nothing,
+// when a lane of the block has an index outside the staged tables or a value
+// outside int32 (the caller then maps the block with enc_records); else sets
+// bit e of esc_steps for each step e with an escape.
+//   x = start | (65535 - (freq - 1)) << 16 = entry word 0 ^ 0xffff0000
+//   z = 31 - ffbh(freq - 1): the shift for freq >= 2, and 32 (the freq-1
+//       flag) for freq = 1, where ffbh(0) = 0xffffffff; | 256 for an escape;
+//       | (freq - 1) << 16 = entry word 0's high half
+template <int kMode, bool kImplicit, int KP>
+__device__ __forceinline__ bool enc_records_fast(const EncArgs& a, const Tabs& tb, int lane,
+                                                 int t0, int tstep, int32_t start,
+                                                 const int32_t* in_a, const int32_t* in_b,
+                                                 const float* in_m, uint32_t& hash,
+                                                 uint32_t& status, uint32_t& znib,
+                                                 uint32_t& esc_steps, uint4* rec) {
+  int32_t sym[KP];
+  uint32_t tbl[KP];
+  uint32_t h = 0;
+  uint64_t bad = 0;  // lane masks (one compare per step, no bool arithmetic)
+#pragma unroll
+  for (int e = 0; e < KP; ++e) {
+    const int p = lane + kLanes * (t0 + tstep * e);
+    const int32_t tbi = kImplicit ? (int32_t)udiv((uint32_t)(start + p), a.div_hw) : in_b[e];
+    bad |= ballot((uint32_t)(tbi - tb.t_lo) >= (uint32_t)tb.nt);  // staged tables are below M
+    tbl[e] = (uint32_t)tbi;
+    h += index_term((uint32_t)p, (uint32_t)tbi);
+    if (kMode != kModeSymbols) {
+      const float r = rintf(__fsub_rn(__int_as_float(in_a[e]), in_m[e]));
+      bad |= ballot(!(fabsf(r) < 2147483648.0f));
+      sym[e] = (int32_t)r;
+    } else {
+      sym[e] = in_a[e];
+    }
+  }
+  if (bad != 0ull) return false;
+  uint32_t at[KP], v[KP], maxv[KP], off[KP];
+  uint64_t om[KP];
+#pragma unroll
+  for (int e = 0; e < KP; ++e) {
+    const uint4 m = tb.lmeta[tbl[e] - tb.t_lo];
+    v[e] = (uint32_t)sym[e] - m.z;
+    maxv[e] = m.y - 1u;
+    off[e] = m.z;
+    const bool out = v[e] >= maxv[e];
+    om[e] = ballot(out);
+    at[e] = m.x + (out ? maxv[e] : v[e]);
+  }
+  uint32_t es = 0;
+#pragma unroll
+  for (int e = 0; e < KP; ++e) {
+    const uint2 ent = tb.lent[at[e]];
+    uint32_t lz;
+    asm("v_ffbh_u32 %0, %1" : "=v"(lz) : "v"(ent.x >> 16));
+    rec[e] = make_uint4(ent.x ^ 0xffff0000u, ent.y, (31u - lz) | (ent.x & 0xffff0000u), 0u);
+    if (om[e] != 0ull) {
+      // the escape split of enc_records for this step's escaping lanes
+      const bool esc = (om[e] >> lane) & 1ull;
+      const int32_t sv = sym[e], ov = (int32_t)off[e], vv = (int32_t)v[e];
+      const bool ovf = ((sv ^ ov) & (sv ^ vv)) < 0;
+      const uint32_t d = v[e] - maxv[e];
+      const bool lo = ovf ? (sv < 0) : (vv < 0);
+      status |= (esc & ovf & (lo | (d >= 0x80000000u))) ? GAANS_ST_RANGE : 0u;
+      const uint32_t m_lo = 0u - (uint32_t)lo;
+      const uint32_t raw = ((~(v[e] << 1) & m_lo) | ((d << 1) & ~m_lo)) & (0u - (uint32_t)esc);
+      const uint32_t nn = raw ? ((31u - (uint32_t)__clz((int)raw)) >> 2) + 1u : 0u;
+      znib += esc ? nn + 1u : 0u;
+      rec[e].z |= esc ? 256u : 0u;
+      rec[e].w = raw;
+      es |= 1u << e;
+    }
+  }
+  esc_steps = es;
+  hash += h;
+  return true;
 }
 
 // Encoder LDS ring: kRingWords words + one spare slot per lane, which lanes
@@ -579,27 +662,26 @@ __device__ __forceinline__ void ring_flush(uint16_t* __restrict__ wbuf, const ui
 // The ring holds the words [wp, fl) (positions mod kRingWords).  The coder
 // flushes it at the start of a block when fewer than SB * kLanes slots are
 // free (a step emits at most one word per lane), so the steps need no check.
-__device__ __forceinline__ void emit_words(bool emit, uint32_t& x, uint16_t* ring, int& wp,
+// A lane emits when x >= freq << 16, i.e. (x >> 16) > freq - 1 (z's high
+// half): one compare of the two high halves.
+__device__ __forceinline__ void emit_words(uint32_t z, uint32_t& x, uint16_t* ring, int& wp,
                                            int lane) {
+  const bool emit = (x >> 16) > (z >> 16);
   const uint64_t m = ballot(emit);
-  const int c = __popcll(m);
-  wp = uni(wp - c);
-  // Branch-free: the slot and the shift are bit selects on an all-ones /
-  // zero mask that the compiler cannot see through (as a select on `emit`
-  // it becomes an exec-masked block).
-  uint32_t e = 0u - (uint32_t)emit;
-  asm("" : "+v"(e));  // opaque, but free to schedule
-  const uint32_t pos = (uint32_t)(wp + (int)lane_rank(m)) & (kRingWords - 1);
-  const uint32_t slot = (pos & e) | ((uint32_t)(kRingWords + lane) & ~e);
-  ring[slot] = (uint16_t)x;
-  x >>= (e & 16u);
+  wp = uni(wp - __popcll(m));
+  // an exec-masked store: the slot's address is computed by the emitting
+  // lanes only, and the others skip it
+  if (emit) ring[(uint32_t)(wp + (int)lane_rank(m)) & (kRingWords - 1)] = (uint16_t)x;
+  x = emit ? x >> 16 : x;
 }
 
-// main rANS op: x' = ((x / freq) << 16) + x % freq + start = x + start + q (65536 - freq)
+// main rANS op: x' = ((x / freq) << 16) + x % freq + start = x + start + q (65536 - freq);
+// z's low byte is the shift, or 32 (+ shift 0) for freq = 1
 __device__ __forceinline__ uint32_t enc_apply(uint32_t x, uint4 r) {
   const uint32_t q = enc_div(x, r.y, r.z & 31u);
-  const uint32_t xn = __umul24(q, r.x >> 16) + (x + (r.x & 0xffffu));
-  return (r.z & 32u) ? ((x << 16) + (r.x & 0xffffu)) : xn;
+  const uint32_t xs = x + (r.x & 0xffffu);
+  const uint32_t xn = __umul24(q, r.x >> 16) + xs;
+  return (r.z & 0xffu) >= 32u ? ((x << 16) | (r.x & 0xffffu)) : xn;
 }
 
 // Escapes of one step into the unit's escape list: slots are taken from the
@@ -649,7 +731,9 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
   uint32_t* __restrict__ esc_list = a.esc_raw + g * a.seg_cap + a.seg_cap;
 
   if (tid < 2) eflag[tid] = 0u;  // visible after the staging barrier
-  const bool tab = tables_ok(load_tab_hdr(a.tables), a.M, a.tables_bytes, a.blob);  // uniform
+  const TabHdr th = load_tab_hdr(a.tables);
+  const bool tab = tables_ok(th, a.M, a.tables_bytes, a.blob);  // uniform
+  const bool offsets_safe = (th.flags & kTabOffsetsSafe) != 0;
   if (!tab) status |= GAANS_ST_TABLES;
   if (tab) {
     Tabs tb;
@@ -708,16 +792,26 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
       constexpr bool kLds = decltype(lds_tag)::value;
       uint4* dst = recs + (j & 1) * SB * kLanes;
       uint4 r[kPer];
-      enc_records<kMode, kImplicit, kLds, kPer>(a, tb, lane, j * SB + wid - 1, kEncMappers,
-                                                nvalid, len, start, ca, cb, cm, hash, status,
-                                                znib, r);
-      uint32_t eb = 0;  // steps of the block with escapes
+      bool fast = false;
+      uint32_t esc_steps = 0;
+      if constexpr (kLds) {
+        if (offsets_safe && nvalid == kPer && (j + 1) * SB * kLanes <= len)
+          fast = enc_records_fast<kMode, kImplicit, kPer>(a, tb, lane, j * SB + wid - 1,
+                                                          kEncMappers, start, ca, cb, cm, hash,
+                                                          status, znib, esc_steps, r);
+      }
+      if (!fast)
+        enc_records<kMode, kImplicit, kLds, kPer>(a, tb, lane, j * SB + wid - 1, kEncMappers,
+                                                  nvalid, len, start, ca, cb, cm, hash, status,
+                                                  znib, r);
+      uint32_t eb = 0;  // steps of the block with escapes (none on the fast path)
 #pragma unroll
       for (int e = 0; e < kPer; ++e) {
         const int u = (wid - 1) + kEncMappers * e;
         if (SB % kEncMappers != 0 && u >= SB) break;
         dst[u * kLanes + lane] = r[e];
-        eb |= ballot((r[e].z & 256u) != 0u) != 0ull ? 1u << u : 0u;
+        if (fast) eb |= ((esc_steps >> e) & 1u) << u;
+        else eb |= ballot((r[e].z & 256u) != 0u) != 0ull ? 1u << u : 0u;
       }
       if (eb != 0u && lane == 0)
         __hip_atomic_fetch_or(&eflag[j & 1], eb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -769,14 +863,14 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
             // common case: a full block, no per-step branches
 #pragma unroll
             for (int k = H - 1; k >= 0; --k) {
-              emit_words((x >> 16) >= 65536u - (r[k].x >> 16), x, ring, wp, lane);
+              emit_words(r[k].z, x, ring, wp, lane);
               x = enc_apply(x, r[k]);
             }
           } else {
 #pragma unroll
             for (int k = H - 1; k >= 0; --k) {
               if (j * SB + h * H + k >= T) continue;
-              emit_words((x >> 16) >= 65536u - (r[k].x >> 16), x, ring, wp, lane);
+              emit_words(r[k].z, x, ring, wp, lane);
               x = enc_apply(x, r[k]);
             }
           }
@@ -1657,6 +1751,10 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
           sring32[(b * (G::kPfWords / 2) + kk * kLanes + lane) & (G::kRing / 2 - 1)] = w0[b][kk];
       S.filled = G::kPre * G::kPfWords;
       uint32_t ecur = 0;  // escape entries consumed
+      // The coder's chain of dependent steps bounds the block loop; its
+      // instructions go first when mapper or escape waves of this or another
+      // workgroup on the CU compete for the same SIMD.
+      __builtin_amdgcn_s_setprio(3);
       __syncthreads();
       for (int j = 0; j < nblk; ++j) {
         uint2* src = recs + (j & 1) * SB * kLanes;
