@@ -290,6 +290,9 @@ __device__ __forceinline__ void stage_range(int nt_cap, int stage_all, int k, in
 constexpr int kModeSymbols = 0;   // int32 symbols; indexes given or table = channel
 constexpr int kModeLatents = 1;   // fp32 latents, per-channel medians; indexes as above
 constexpr int kModeGaussian = 2;  // fp32 latents, per-element means (optional) and scales
+static_assert(kModeSymbols == GAANS_MODE_SYMBOLS && kModeLatents == GAANS_MODE_LATENTS &&
+                  kModeGaussian == GAANS_MODE_GAUSSIAN,
+              "plan modes are the kernel modes");
 
 // CompressAI's GaussianConditional.build_indexes for one scale s (the
 // third-party algorithm, restated in the oracle): lb = max(s, bound) (NaN
@@ -2491,58 +2494,58 @@ DecKernel dec_kernel(int mode, bool imp, int sb, bool search) {
   }
 }
 
-int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y,
-                  const float* medians, const int32_t* indexes, const GaussIn* g,
-                  const gaans_tables* tables, int64_t B, int64_t N, int64_t C, int64_t P,
-                  int64_t S, void* ws, int64_t ws_bytes, void* ctrl, uint64_t* info_out) {
-  Layout L;
-  int rc = make_layout(B, N, C, P, S, &L);
-  if (rc) return rc;
+// One encode launch: kernel, geometry and arguments.
+struct EncLaunch {
+  EncKernel kernel;
+  uint32_t grid, block;
+  size_t lds;
+  EncArgs a;
+};
+
+// The parts of an encode launch that follow from the mode, the index kind
+// (implicit: table = channel), the tables and the shape; the per-call
+// pointers are left NULL (encode_bind sets them).
+int encode_prepare(int mode, bool implicit, int32_t n_scales, float scale_bound,
+                   const gaans_tables* tables, const Layout& L, EncLaunch* e) {
+  int rc;
   if ((rc = check_tables_arg(tables))) return rc;
-  if (mode == kModeSymbols ? !symbols : (!y || (mode == kModeLatents && !medians)))
-    return fail(GAANS_EINVAL, "input pointer is NULL");
-  if (mode == kModeGaussian && (rc = check_gauss(g))) return rc;
-  if (!ctrl) return fail(GAANS_EINVAL, "control block pointer is NULL");
-  if (!ws || ws_bytes < L.ws_bytes)
-    return fail(GAANS_EINVAL, "workspace too small (%lld < %lld bytes)", (long long)ws_bytes,
-                (long long)L.ws_bytes);
+  if (mode == kModeGaussian && (n_scales < 1 || n_scales > kMaxScales))
+    return fail(GAANS_EINVAL, "scale table of %d entries outside [1, %d]", n_scales, kMaxScales);
   BlobRef blob;
   if ((rc = blob_ref(tables, &blob))) return rc;
-  uint8_t* w = static_cast<uint8_t*>(ws);
   DevLds dl;
   if ((rc = device_lds(&dl))) return rc;
-  const int64_t extra = mode == kModeGaussian ? align_up(4 * (int64_t)g->n, 16) : 0;
+  const int64_t extra = mode == kModeGaussian ? align_up(4 * (int64_t)n_scales, 16) : 0;
   // 16-step blocks for long units only (the coder waits for the first
   // block to be mapped, so short units lose more than the per-block saving
   // gains: measured slower at 96 steps, faster at 4,080), and with explicit
   // or computed indexes only (with table = channel the 16-step kernel needs
   // private scratch)
   const bool long_units = L.seg_cap >= 512 * kLanes;
-  const EncPlan plan = plan_encode(tables, P, L.U, dl, extra, mode != kModeGaussian,
-                                   long_units && (indexes || g));
+  const bool gauss = mode == kModeGaussian;
+  if (gauss) implicit = false;
+  const EncPlan plan = plan_encode(tables, L.P, L.U, dl, extra, !gauss, long_units && !implicit);
   const Stage& st = plan.st;
-  EncArgs a;
-  a.symbols = symbols;
-  a.y = y;
-  a.medians = medians;
-  a.means = mode == kModeGaussian ? g->means : nullptr;
-  a.scales = mode == kModeGaussian ? g->scales : nullptr;
-  a.scale_table = mode == kModeGaussian ? g->table : nullptr;
-  a.n_scales = mode == kModeGaussian ? g->n : 0;
-  a.scales_pow2 = mode == kModeGaussian ? pow2_floor(g->n - 1) : 0;
-  a.scale_bound = mode == kModeGaussian ? g->bound : 0.0f;
+  const size_t lds = plan.lds + (size_t)extra;
+  if (lds > (size_t)dl.per_block)
+    return fail(GAANS_EINVAL, "encode needs %zu bytes of LDS, the device has %d", lds,
+                dl.per_block);
+  EncArgs& a = e->a;
+  memset(&a, 0, sizeof(a));
+  a.n_scales = gauss ? n_scales : 0;
+  a.scales_pow2 = gauss ? pow2_floor(n_scales - 1) : 0;
+  a.scale_bound = gauss ? scale_bound : 0.0f;
   a.scales_lds = (uint32_t)plan.lds;
-  a.indexes = mode == kModeGaussian ? nullptr : indexes;
   a.tables = static_cast<const uint8_t*>(tables->dev);
   a.M = (uint32_t)tables->M;
   a.tables_bytes = (uint32_t)tables->bytes;
   a.blob = blob;
-  a.N = N;
+  a.N = L.N;
   a.K = (int32_t)L.K;
-  a.P = (int32_t)P;
-  a.C = (int32_t)C;
+  a.P = (int32_t)L.P;
+  a.C = (int32_t)L.C;
   a.chunk_len = (int32_t)L.chunk_len;
-  a.S = (int32_t)S;
+  a.S = (int32_t)L.S;
   a.seg_cap = (int32_t)L.seg_cap;
   a.div_hw = make_udiv((uint32_t)L.HW);
   a.cap_words = (int32_t)L.cap_words;
@@ -2550,6 +2553,47 @@ int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y
   a.header_bytes = L.header_bytes;
   a.nt_cap = st.nt_cap;
   a.stage_all = st.stage_all;
+  // 8 mapper waves when every workgroup has a CU to itself
+  const int nm = plan.occ == 1 && L.U <= dl.cus ? 8 : 4;
+  e->kernel = enc_kernel(mode, implicit, plan.sb, nm);
+  e->grid = (uint32_t)L.U;
+  e->block = (uint32_t)((nm + 1) * kLanes);
+  e->lds = lds;
+  return allow_lds(reinterpret_cast<const void*>(e->kernel), lds, dl);
+}
+
+// Checks of an encode call's pointers (before any device query).
+int encode_check(int mode, bool implicit, const Layout& L, const int32_t* symbols,
+                 const float* y, const float* medians, const int32_t* indexes, const GaussIn* g,
+                 const void* ws, int64_t ws_bytes, const void* ctrl) {
+  if (mode == kModeSymbols ? !symbols : (!y || (mode == kModeLatents && !medians)))
+    return fail(GAANS_EINVAL, "input pointer is NULL");
+  if (mode == kModeGaussian) {
+    if (!g->scales || !g->table)
+      return fail(GAANS_EINVAL, "scales or scale table pointer is NULL");
+  } else if (implicit != (indexes == nullptr)) {
+    return fail(GAANS_EINVAL, implicit ? "indexes given to a plan made for table = channel"
+                                       : "indexes missing for a plan made for explicit indexes");
+  }
+  if (!ctrl) return fail(GAANS_EINVAL, "control block pointer is NULL");
+  if (!ws || ws_bytes < L.ws_bytes)
+    return fail(GAANS_EINVAL, "workspace too small (%lld < %lld bytes)", (long long)ws_bytes,
+                (long long)L.ws_bytes);
+  return GAANS_OK;
+}
+
+// Per-call pointers of an encode launch (the workspace carved by the layout).
+void encode_bind(int mode, EncArgs& a, const Layout& L, const int32_t* symbols, const float* y,
+                 const float* medians, const int32_t* indexes, const GaussIn* g, void* ws,
+                 void* ctrl, uint64_t* info_out) {
+  uint8_t* w = static_cast<uint8_t*>(ws);
+  a.symbols = symbols;
+  a.y = y;
+  a.medians = medians;
+  a.means = mode == kModeGaussian ? g->means : nullptr;
+  a.scales = mode == kModeGaussian ? g->scales : nullptr;
+  a.scale_table = mode == kModeGaussian ? g->table : nullptr;
+  a.indexes = mode == kModeGaussian ? nullptr : indexes;
   a.chunk_words = reinterpret_cast<uint32_t*>(w + L.o_words_cnt);
   a.chunk_status = reinterpret_cast<uint32_t*>(w + L.o_status);
   a.index_hash = reinterpret_cast<uint32_t*>(w + L.o_hash);
@@ -2561,17 +2605,134 @@ int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y
   a.esc_raw = reinterpret_cast<uint32_t*>(w + L.o_esc_raw);
   a.ctrl = static_cast<uint32_t*>(ctrl);
   a.info_out = info_out;
+}
+
+int encode_launch(const EncLaunch& e, void* stream) {
+  e.kernel<<<dim3(e.grid), dim3(e.block), e.lds, static_cast<hipStream_t>(stream)>>>(e.a);
+  return check_launch("encode");
+}
+
+int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y,
+                  const float* medians, const int32_t* indexes, const GaussIn* g,
+                  const gaans_tables* tables, int64_t B, int64_t N, int64_t C, int64_t P,
+                  int64_t S, void* ws, int64_t ws_bytes, void* ctrl, uint64_t* info_out) {
+  Layout L;
+  int rc = make_layout(B, N, C, P, S, &L);
+  if (rc) return rc;
+  if ((rc = check_tables_arg(tables))) return rc;
+  if (mode == kModeGaussian && (rc = check_gauss(g))) return rc;
+  const bool implicit = indexes == nullptr;
+  if ((rc = encode_check(mode, implicit, L, symbols, y, medians, indexes, g, ws, ws_bytes, ctrl)))
+    return rc;
+  EncLaunch e;
+  if ((rc = encode_prepare(mode, implicit, g ? g->n : 0, g ? g->bound : 0.0f, tables, L, &e)))
+    return rc;
+  encode_bind(mode, e.a, L, symbols, y, medians, indexes, g, ws, ctrl, info_out);
+  return encode_launch(e, stream);
+}
+
+// One decode launch: kernel, geometry and arguments.
+struct DecLaunch {
+  DecKernel kernel;
+  uint32_t grid, block;
+  size_t lds;
+  DecArgs a;
+};
+
+// The parts of a decode launch that follow from the mode, the index kind,
+// the tables and the shape; per-call pointers are left NULL (decode_bind).
+int decode_prepare(int mode, bool implicit, int32_t n_scales, float scale_bound,
+                   const gaans_tables* tables, const Layout& L, DecLaunch* e) {
+  int rc;
+  if ((rc = check_tables_arg(tables))) return rc;
+  if (mode == kModeGaussian && (n_scales < 1 || n_scales > kMaxScales))
+    return fail(GAANS_EINVAL, "scale table of %d entries outside [1, %d]", n_scales, kMaxScales);
+  BlobRef blob;
+  if ((rc = blob_ref(tables, &blob))) return rc;
+  DevLds dl;
+  if ((rc = device_lds(&dl))) return rc;
+  const bool gauss = mode == kModeGaussian;
+  if (gauss) implicit = false;
+  const bool latents = mode != kModeSymbols;
+  const int64_t extra = gauss ? align_up(4 * (int64_t)n_scales, 16) : 0;
+  const bool search_ok = (tables->flags & GAANS_TABLES_SEARCH) != 0 && !implicit;
+  const DecPlan plan = plan_decode(tables, L.P, L.U, latents, dl, extra, !gauss, search_ok);
+  const Stage& st = plan.st;
   const size_t lds = plan.lds + (size_t)extra;
   if (lds > (size_t)dl.per_block)
-    return fail(GAANS_EINVAL, "encode needs %zu bytes of LDS, the device has %d", lds,
+    return fail(GAANS_EINVAL, "decode needs %zu bytes of LDS, the device has %d", lds,
                 dl.per_block);
-  // 8 mapper waves when every workgroup has a CU to itself
-  const int nm = plan.occ == 1 && L.U <= dl.cus ? 8 : 4;
-  const EncKernel kernel = enc_kernel(mode, indexes == nullptr, plan.sb, nm);
-  if ((rc = allow_lds(reinterpret_cast<const void*>(kernel), lds, dl))) return rc;
-  kernel<<<dim3((uint32_t)L.U), dim3((uint32_t)((nm + 1) * kLanes)), lds,
-           static_cast<hipStream_t>(stream)>>>(a);
-  return check_launch("encode");
+  DecArgs& a = e->a;
+  memset(&a, 0, sizeof(a));
+  a.tables = static_cast<const uint8_t*>(tables->dev);
+  a.M = (uint32_t)tables->M;
+  a.tables_bytes = (uint32_t)tables->bytes;
+  a.blob = blob;
+  a.n_scales = gauss ? n_scales : 0;
+  a.scales_pow2 = gauss ? pow2_floor(n_scales - 1) : 0;
+  a.scale_bound = gauss ? scale_bound : 0.0f;
+  a.scales_lds = (uint32_t)plan.lds;
+  a.N = L.N;
+  a.header_bytes = L.header_bytes;
+  a.units = L.U;
+  a.B = (uint32_t)L.B;
+  a.C = (uint32_t)L.C;
+  a.P = (uint32_t)L.P;
+  a.K = (uint32_t)L.K;
+  a.chunk_len = (uint32_t)L.chunk_len;
+  a.S = (uint32_t)L.S;
+  a.div_hw = make_udiv((uint32_t)L.HW);
+  a.nt_cap = st.nt_cap;
+  a.ne_cap = st.ne_cap;
+  a.nd_cap = st.nd_cap;
+  a.stage_all = st.stage_all;
+  a.starts_words = plan.starts_words;
+  e->kernel = dec_kernel(mode, implicit, plan.sb, plan.search);
+  e->grid = (uint32_t)L.U;
+  e->block = (uint32_t)kDecThreads;
+  e->lds = lds;
+  return allow_lds(reinterpret_cast<const void*>(e->kernel), lds, dl);
+}
+
+// Checks of a decode call's pointers (before any device query).
+int decode_check(int mode, bool implicit, const Layout& L, const uint8_t* payload,
+                 int64_t payload_bytes, const int32_t* indexes, const GaussIn* g,
+                 const float* medians, const void* out, const void* ctrl,
+                 const uint32_t* status_out) {
+  if (!payload || !status_out || !ctrl || !out || (mode == kModeLatents && !medians))
+    return fail(GAANS_EINVAL, "payload, output, control or status pointer is NULL");
+  if (mode == kModeGaussian) {
+    if (!g->scales || !g->table)
+      return fail(GAANS_EINVAL, "scales or scale table pointer is NULL");
+  } else if (implicit != (indexes == nullptr)) {
+    return fail(GAANS_EINVAL, implicit ? "indexes given to a plan made for table = channel"
+                                       : "indexes missing for a plan made for explicit indexes");
+  }
+  if (payload_bytes < L.header_bytes)
+    return fail(GAANS_EINVAL, "payload (%lld bytes) is shorter than its header (%lld bytes)",
+                (long long)payload_bytes, (long long)L.header_bytes);
+  return GAANS_OK;
+}
+
+void decode_bind(int mode, DecArgs& a, const uint8_t* payload, int64_t payload_bytes,
+                 const int32_t* indexes, const GaussIn* g, const float* medians, void* out,
+                 void* ctrl, uint32_t* status_out) {
+  a.payload = payload;
+  a.payload_bytes = payload_bytes;
+  a.indexes = mode == kModeGaussian ? nullptr : indexes;
+  a.medians = medians;
+  a.means = mode == kModeGaussian ? g->means : nullptr;
+  a.scales = mode == kModeGaussian ? g->scales : nullptr;
+  a.scale_table = mode == kModeGaussian ? g->table : nullptr;
+  a.out_sym = mode == kModeSymbols ? static_cast<int32_t*>(out) : nullptr;
+  a.out_y = mode == kModeSymbols ? nullptr : static_cast<float*>(out);
+  a.ctrl = static_cast<uint32_t*>(ctrl);
+  a.status_out = status_out;
+}
+
+int decode_launch(const DecLaunch& e, void* stream) {
+  e.kernel<<<dim3(e.grid), dim3(e.block), e.lds, static_cast<hipStream_t>(stream)>>>(e.a);
+  return check_launch("decode");
 }
 
 int decode_impl(int mode, void* stream, const uint8_t* payload, int64_t payload_bytes,
@@ -2582,67 +2743,17 @@ int decode_impl(int mode, void* stream, const uint8_t* payload, int64_t payload_
   int rc = make_layout(B, N, C, P, S, &L);
   if (rc) return rc;
   if ((rc = check_tables_arg(tables))) return rc;
-  if (!payload || !status_out || !ctrl ||
-      (mode == kModeSymbols ? !out_sym : (!out_y || (mode == kModeLatents && !medians))))
-    return fail(GAANS_EINVAL, "payload, output, control or status pointer is NULL");
   if (mode == kModeGaussian && (rc = check_gauss(g))) return rc;
-  if (payload_bytes < L.header_bytes)
-    return fail(GAANS_EINVAL, "payload (%lld bytes) is shorter than its header (%lld bytes)",
-                (long long)payload_bytes, (long long)L.header_bytes);
-  BlobRef blob;
-  if ((rc = blob_ref(tables, &blob))) return rc;
-  DevLds dl;
-  if ((rc = device_lds(&dl))) return rc;
-  const bool latents = mode != kModeSymbols;
-  const int64_t extra = mode == kModeGaussian ? align_up(4 * (int64_t)g->n, 16) : 0;
-  const bool search_ok =
-      (tables->flags & GAANS_TABLES_SEARCH) != 0 && (mode == kModeGaussian || indexes != nullptr);
-  const DecPlan plan =
-      plan_decode(tables, P, L.U, latents, dl, extra, mode != kModeGaussian, search_ok);
-  const Stage& st = plan.st;
-  DecArgs a;
-  a.payload = payload;
-  a.payload_bytes = payload_bytes;
-  a.indexes = mode == kModeGaussian ? nullptr : indexes;
-  a.tables = static_cast<const uint8_t*>(tables->dev);
-  a.M = (uint32_t)tables->M;
-  a.tables_bytes = (uint32_t)tables->bytes;
-  a.blob = blob;
-  a.medians = medians;
-  a.means = mode == kModeGaussian ? g->means : nullptr;
-  a.scales = mode == kModeGaussian ? g->scales : nullptr;
-  a.scale_table = mode == kModeGaussian ? g->table : nullptr;
-  a.n_scales = mode == kModeGaussian ? g->n : 0;
-  a.scales_pow2 = mode == kModeGaussian ? pow2_floor(g->n - 1) : 0;
-  a.scale_bound = mode == kModeGaussian ? g->bound : 0.0f;
-  a.scales_lds = (uint32_t)plan.lds;
-  a.out_sym = out_sym;
-  a.out_y = out_y;
-  a.N = N;
-  a.header_bytes = L.header_bytes;
-  a.units = L.U;
-  a.B = (uint32_t)B;
-  a.C = (uint32_t)C;
-  a.P = (uint32_t)P;
-  a.K = (uint32_t)L.K;
-  a.chunk_len = (uint32_t)L.chunk_len;
-  a.S = (uint32_t)S;
-  a.div_hw = make_udiv((uint32_t)L.HW);
-  a.nt_cap = st.nt_cap;
-  a.ne_cap = st.ne_cap;
-  a.nd_cap = st.nd_cap;
-  a.stage_all = st.stage_all;
-  a.starts_words = plan.starts_words;
-  a.ctrl = static_cast<uint32_t*>(ctrl);
-  a.status_out = status_out;
-  const size_t lds = plan.lds + (size_t)extra;
-  if (lds > (size_t)dl.per_block)
-    return fail(GAANS_EINVAL, "decode needs %zu bytes of LDS, the device has %d", lds,
-                dl.per_block);
-  const DecKernel kernel = dec_kernel(mode, indexes == nullptr, plan.sb, plan.search);
-  if ((rc = allow_lds(reinterpret_cast<const void*>(kernel), lds, dl))) return rc;
-  kernel<<<dim3((uint32_t)L.U), dim3(kDecThreads), lds, static_cast<hipStream_t>(stream)>>>(a);
-  return check_launch("decode");
+  const bool implicit = indexes == nullptr;
+  void* out = mode == kModeSymbols ? static_cast<void*>(out_sym) : static_cast<void*>(out_y);
+  if ((rc = decode_check(mode, implicit, L, payload, payload_bytes, indexes, g, medians, out, ctrl,
+                         status_out)))
+    return rc;
+  DecLaunch e;
+  if ((rc = decode_prepare(mode, implicit, g ? g->n : 0, g ? g->bound : 0.0f, tables, L, &e)))
+    return rc;
+  decode_bind(mode, e.a, payload, payload_bytes, indexes, g, medians, out, ctrl, status_out);
+  return decode_launch(e, stream);
 }
 
 // CompressAI Rans64 streams: plan the LDS (all tables; else, with implicit
@@ -2726,6 +2837,102 @@ int rans64_decode_impl(void* stream, const uint8_t* streams, int64_t streams_byt
 // Clear n u32 words (the no-allocation entry point's control block, once per
 // device before its first use; a kernel rather than a memset so that the call
 // can be captured into a graph).
+// Pack launch: the shape part (pack_prepare), the per-call pointers
+// (pack_bind) and the launch.
+void pack_prepare(const gaans_tables* tables, const Layout& L, PackArgs& a) {
+  memset(&a, 0, sizeof(a));
+  a.tables = static_cast<const uint8_t*>(tables->dev);
+  a.header_bytes = L.header_bytes;
+  a.cap_words = L.cap_words;
+  a.units = L.U;
+  a.N = L.N;
+  a.B = (uint32_t)L.B;
+  a.N32 = (uint32_t)L.N;
+  a.C = (uint32_t)L.C;
+  a.P = (uint32_t)L.P;
+  a.K = (uint32_t)L.K;
+  a.chunk_len = (uint32_t)L.chunk_len;
+  a.M = (uint32_t)tables->M;
+  a.S = (uint32_t)L.S;
+  a.seg_cap = (uint32_t)L.seg_cap;
+}
+
+void pack_bind(PackArgs& a, const Layout& L, const void* ws, uint8_t* out, int64_t out_bytes) {
+  const uint8_t* w = static_cast<const uint8_t*>(ws);
+  a.chunk_words = reinterpret_cast<const uint32_t*>(w + L.o_words_cnt);
+  a.index_hash = reinterpret_cast<const uint32_t*>(w + L.o_hash);
+  a.end_off = reinterpret_cast<const uint32_t*>(w + L.o_end);
+  a.states = reinterpret_cast<const uint32_t*>(w + L.o_states);
+  a.words = reinterpret_cast<const uint16_t*>(w + L.o_words);
+  a.esc = reinterpret_cast<const uint2*>(w + L.o_esc);
+  a.esc_raw = reinterpret_cast<const uint32_t*>(w + L.o_esc_raw);
+  a.out = out;
+  a.out_bytes = out_bytes;
+}
+
+int pack_launch(const PackArgs& a, void* stream) {
+  k_pack<<<dim3((uint32_t)a.units), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(a);
+  return check_launch("pack");
+}
+
+// ---- call plans -----------------------------------------------------------
+// A plan holds an encode (launch + pack) or decode launch with every
+// shape-dependent field filled; a run copies it, sets the call's pointers and
+// launches.  Stored in the caller's gaans_plan (opaque bytes).
+constexpr uint32_t kPlanEncMagic = 0x4E504147u;  // "GAPN" (encode)
+constexpr uint32_t kPlanDecMagic = 0x44504147u;  // "GAPD" (decode)
+
+struct PlanHead {
+  uint32_t magic;
+  int32_t mode, implicit, dev;
+  Layout L;
+};
+struct EncPlanRec {
+  PlanHead h;
+  EncLaunch e;
+  PackArgs pack;
+};
+struct DecPlanRec {
+  PlanHead h;
+  DecLaunch e;
+};
+static_assert(sizeof(EncPlanRec) <= GAANS_PLAN_BYTES && sizeof(DecPlanRec) <= GAANS_PLAN_BYTES,
+              "gaans_plan too small");
+static_assert(alignof(EncPlanRec) <= 8 && alignof(DecPlanRec) <= 8, "gaans_plan alignment");
+
+int plan_mode(int32_t mode) {
+  return mode == GAANS_MODE_SYMBOLS || mode == GAANS_MODE_LATENTS || mode == GAANS_MODE_GAUSSIAN
+             ? GAANS_OK
+             : fail(GAANS_EINVAL, "plan mode %d is not a GAANS_MODE_* value", mode);
+}
+
+// The device a plan was made on must be current when it runs (its kernels'
+// LDS limits and launch shape were set up there).
+int plan_device(const PlanHead& h) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(GAANS_EHIP, "hipGetDevice failed");
+  if (dev != h.dev)
+    return fail(GAANS_EINVAL, "plan made on device %d runs with device %d current", h.dev, dev);
+  return GAANS_OK;
+}
+
+// Spin until the word a launch sets on completion is nonzero (see
+// gaans_wait_host_word).
+int wait_word(void* stream, const uint32_t* word) {
+  for (uint32_t i = 1;; ++i) {
+    if (__atomic_load_n(word, __ATOMIC_ACQUIRE) != 0) return GAANS_OK;
+    if ((i & 255u) == 0) {
+      const hipError_t e = hipStreamQuery(static_cast<hipStream_t>(stream));
+      if (e == hipSuccess) {
+        if (__atomic_load_n(word, __ATOMIC_ACQUIRE) != 0) return GAANS_OK;
+        return fail(GAANS_EHIP, "stream finished without setting the completion word");
+      }
+      if (e != hipErrorNotReady)
+        return fail(GAANS_EHIP, "stream reported an error: %s", hipGetErrorString(e));
+    }
+  }
+}
+
 __global__ __launch_bounds__(kLanes) void k_clear_words(uint32_t* __restrict__ p, int n) {
   for (int i = threadIdx.x; i < n; i += kLanes) p[i] = 0u;
 }
@@ -2815,33 +3022,10 @@ int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace
     return fail(GAANS_EINVAL, "workspace too small");
   if (!out_dev || out_bytes < L.header_bytes)
     return fail(GAANS_EINVAL, "output buffer smaller than the payload header");
-  const uint8_t* w = static_cast<const uint8_t*>(workspace_dev);
   PackArgs a;
-  a.chunk_words = reinterpret_cast<const uint32_t*>(w + L.o_words_cnt);
-  a.index_hash = reinterpret_cast<const uint32_t*>(w + L.o_hash);
-  a.end_off = reinterpret_cast<const uint32_t*>(w + L.o_end);
-  a.states = reinterpret_cast<const uint32_t*>(w + L.o_states);
-  a.words = reinterpret_cast<const uint16_t*>(w + L.o_words);
-  a.esc = reinterpret_cast<const uint2*>(w + L.o_esc);
-  a.esc_raw = reinterpret_cast<const uint32_t*>(w + L.o_esc_raw);
-  a.tables = static_cast<const uint8_t*>(tables->dev);
-  a.out = out_dev;
-  a.out_bytes = out_bytes;
-  a.header_bytes = L.header_bytes;
-  a.cap_words = L.cap_words;
-  a.units = L.U;
-  a.N = N;
-  a.B = (uint32_t)B;
-  a.N32 = (uint32_t)N;
-  a.C = (uint32_t)C;
-  a.P = (uint32_t)P;
-  a.K = (uint32_t)L.K;
-  a.chunk_len = (uint32_t)L.chunk_len;
-  a.M = (uint32_t)tables->M;
-  a.S = (uint32_t)L.S;
-  a.seg_cap = (uint32_t)L.seg_cap;
-  k_pack<<<dim3((uint32_t)L.U), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(a);
-  return check_launch("pack");
+  pack_prepare(tables, L, a);
+  pack_bind(a, L, workspace_dev, out_dev, out_bytes);
+  return pack_launch(a, stream);
 }
 
 int gaans_encode_symbols_noalloc(void* stream, const int32_t* symbols_dev,
@@ -2911,20 +3095,123 @@ int gaans_rans64_decode(void* stream, const uint8_t* streams_dev, int64_t stream
                             B, N, C, out_dev, ctrl_dev, status_out);
 }
 
+int gaans_plan_encode(const gaans_tables* tables, int32_t mode, int32_t explicit_indexes,
+                      int32_t n_scales, float scale_bound, int64_t B, int64_t N, int64_t C,
+                      int64_t P, int32_t segments, gaans_plan* plan) {
+  if (!plan) return fail(GAANS_EINVAL, "plan pointer is NULL");
+  memset(plan, 0, sizeof(*plan));
+  int rc = plan_mode(mode);
+  if (rc) return rc;
+  EncPlanRec* r = reinterpret_cast<EncPlanRec*>(plan);
+  if ((rc = make_layout(B, N, C, P, segments, &r->h.L))) return rc;
+  const bool implicit = mode != GAANS_MODE_GAUSSIAN && !explicit_indexes;
+  if ((rc = encode_prepare(mode, implicit, n_scales, scale_bound, tables, r->h.L, &r->e)))
+    return rc;
+  pack_prepare(tables, r->h.L, r->pack);
+  r->h.mode = mode;
+  r->h.implicit = implicit;
+  if (hipGetDevice(&r->h.dev) != hipSuccess) return fail(GAANS_EHIP, "hipGetDevice failed");
+  r->h.magic = kPlanEncMagic;
+  return GAANS_OK;
+}
+
+int gaans_plan_decode(const gaans_tables* tables, int32_t mode, int32_t explicit_indexes,
+                      int32_t n_scales, float scale_bound, int64_t B, int64_t N, int64_t C,
+                      int64_t P, int32_t segments, gaans_plan* plan) {
+  if (!plan) return fail(GAANS_EINVAL, "plan pointer is NULL");
+  memset(plan, 0, sizeof(*plan));
+  int rc = plan_mode(mode);
+  if (rc) return rc;
+  DecPlanRec* r = reinterpret_cast<DecPlanRec*>(plan);
+  if ((rc = make_layout(B, N, C, P, segments, &r->h.L))) return rc;
+  const bool implicit = mode != GAANS_MODE_GAUSSIAN && !explicit_indexes;
+  if ((rc = decode_prepare(mode, implicit, n_scales, scale_bound, tables, r->h.L, &r->e)))
+    return rc;
+  r->h.mode = mode;
+  r->h.implicit = implicit;
+  if (hipGetDevice(&r->h.dev) != hipSuccess) return fail(GAANS_EHIP, "hipGetDevice failed");
+  r->h.magic = kPlanDecMagic;
+  return GAANS_OK;
+}
+
+int gaans_run_encode(const gaans_plan* plan, void* stream, const void* in0, const void* in1,
+                     const void* in2, const void* in3, void* workspace_dev,
+                     int64_t workspace_bytes, void* ctrl_dev, uint8_t* out_dev,
+                     int64_t out_bytes, uint64_t* info_host) {
+  const EncPlanRec* r = reinterpret_cast<const EncPlanRec*>(plan);
+  if (!r || r->h.magic != kPlanEncMagic)
+    return fail(GAANS_EINVAL, "not an encode plan (gaans_plan_encode)");
+  const Layout& L = r->h.L;
+  const int mode = r->h.mode;
+  if (!info_host) return fail(GAANS_EINVAL, "info_host pointer is NULL");
+  if (!out_dev || out_bytes < L.max_payload)
+    return fail(GAANS_EINVAL, "payload buffer of %lld bytes, the plan's worst case is %lld",
+                (long long)out_bytes, (long long)L.max_payload);
+  const int32_t* symbols = nullptr;
+  const int32_t* indexes = nullptr;
+  const float *y = nullptr, *medians = nullptr;
+  GaussIn g{nullptr, nullptr, nullptr, r->e.a.n_scales, r->e.a.scale_bound};
+  if (mode == GAANS_MODE_SYMBOLS) {
+    symbols = static_cast<const int32_t*>(in0);
+    indexes = static_cast<const int32_t*>(in1);
+  } else if (mode == GAANS_MODE_LATENTS) {
+    y = static_cast<const float*>(in0);
+    medians = static_cast<const float*>(in1);
+    indexes = static_cast<const int32_t*>(in2);
+  } else {
+    y = static_cast<const float*>(in0);
+    g.means = static_cast<const float*>(in1);
+    g.scales = static_cast<const float*>(in2);
+    g.table = static_cast<const float*>(in3);
+  }
+  int rc = encode_check(mode, r->h.implicit, L, symbols, y, medians, indexes, &g, workspace_dev,
+                        workspace_bytes, ctrl_dev);
+  if (rc || (rc = plan_device(r->h))) return rc;
+  EncLaunch e = r->e;
+  encode_bind(mode, e.a, L, symbols, y, medians, indexes, &g, workspace_dev, ctrl_dev, info_host);
+  PackArgs pk = r->pack;
+  pack_bind(pk, L, workspace_dev, out_dev, out_bytes);
+  uint32_t* done = reinterpret_cast<uint32_t*>(&info_host[2]);  // low half of info[2]
+  __atomic_store_n(done, 0u, __ATOMIC_RELEASE);
+  if ((rc = encode_launch(e, stream)) || (rc = pack_launch(pk, stream))) return rc;
+  return wait_word(stream, done);
+}
+
+int gaans_run_decode(const gaans_plan* plan, void* stream, const uint8_t* payload_dev,
+                     int64_t payload_bytes, const void* in0, const void* in1, const void* in2,
+                     void* out_dev, void* ctrl_dev, uint32_t* status_host) {
+  const DecPlanRec* r = reinterpret_cast<const DecPlanRec*>(plan);
+  if (!r || r->h.magic != kPlanDecMagic)
+    return fail(GAANS_EINVAL, "not a decode plan (gaans_plan_decode)");
+  const int mode = r->h.mode;
+  const int32_t* indexes = nullptr;
+  const float* medians = nullptr;
+  GaussIn g{nullptr, nullptr, nullptr, r->e.a.n_scales, r->e.a.scale_bound};
+  if (mode == GAANS_MODE_SYMBOLS) {
+    indexes = static_cast<const int32_t*>(in0);
+  } else if (mode == GAANS_MODE_LATENTS) {
+    medians = static_cast<const float*>(in0);
+    indexes = static_cast<const int32_t*>(in1);
+  } else {
+    g.scales = static_cast<const float*>(in0);
+    g.means = static_cast<const float*>(in1);
+    g.table = static_cast<const float*>(in2);
+  }
+  int rc = decode_check(mode, r->h.implicit, r->h.L, payload_dev, payload_bytes, indexes, &g,
+                        medians, out_dev, ctrl_dev, status_host);
+  if (rc || (rc = plan_device(r->h))) return rc;
+  DecLaunch e = r->e;
+  decode_bind(mode, e.a, payload_dev, payload_bytes, indexes, &g, medians, out_dev, ctrl_dev,
+              status_host);
+  uint32_t* done = status_host + 1;
+  __atomic_store_n(done, 0u, __ATOMIC_RELEASE);
+  if ((rc = decode_launch(e, stream))) return rc;
+  return wait_word(stream, done);
+}
+
 int gaans_wait_host_word(void* stream, const uint32_t* word) {
   if (!word) return fail(GAANS_EINVAL, "completion word pointer is NULL");
-  for (uint32_t i = 1;; ++i) {
-    if (__atomic_load_n(word, __ATOMIC_ACQUIRE) != 0) return GAANS_OK;
-    if ((i & 255u) == 0) {
-      const hipError_t e = hipStreamQuery(static_cast<hipStream_t>(stream));
-      if (e == hipSuccess) {
-        if (__atomic_load_n(word, __ATOMIC_ACQUIRE) != 0) return GAANS_OK;
-        return fail(GAANS_EHIP, "stream finished without setting the completion word");
-      }
-      if (e != hipErrorNotReady)
-        return fail(GAANS_EHIP, "stream reported an error: %s", hipGetErrorString(e));
-    }
-  }
+  return wait_word(stream, word);
 }
 
 }  // extern "C"

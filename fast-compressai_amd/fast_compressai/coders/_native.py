@@ -15,8 +15,11 @@ import threading
 from .errors import CoderDependencyError
 
 LIB_NAME = "libgaans_w64.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 CTRL_BYTES = 256
+PLAN_BYTES = 1536  # GAANS_PLAN_BYTES
+# plan modes (GAANS_MODE_*)
+MODE_SYMBOLS, MODE_LATENTS, MODE_GAUSSIAN = 0, 1, 2
 NOALLOC_SCRATCH_BYTES = 16 * 1024 * 1024  # GAANS_NOALLOC_SCRATCH_BYTES
 
 # return codes
@@ -111,6 +114,11 @@ def _declare(L) -> None:
                                    p], ctypes.c_int),
         "gaans_rans64_decode": ([p, p, i64, p, p, T, i64, i64, i64, p, p, p], ctypes.c_int),
         "gaans_wait_host_word": ([p, p], ctypes.c_int),
+        # plans are passed by address (c_void_p): no byref object per call
+        "gaans_plan_encode": ([T, i32, i32, i32, f32, i64, i64, i64, i64, i32, p], ctypes.c_int),
+        "gaans_plan_decode": ([T, i32, i32, i32, f32, i64, i64, i64, i64, i32, p], ctypes.c_int),
+        "gaans_run_encode": ([p, p, p, p, p, p, p, i64, p, p, i64, p], ctypes.c_int),
+        "gaans_run_decode": ([p, p, p, i64, p, p, p, p, p, p], ctypes.c_int),
         "gaans_host_selftest": ([], ctypes.c_int),
     }
     for name, (args, res) in sig.items():

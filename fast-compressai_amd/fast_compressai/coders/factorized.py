@@ -86,8 +86,8 @@ class FactorizedWarpDivCodec:
                 enc = gaans.encode(tables, B, N, C, self.p_ch, y.device,
                                    symbols=symbols.reshape(B, -1).to(torch.int32).contiguous(),
                                    segments=S)
-            payload = WarpDivPayload(
-                packed=enc.packed, chunk_ends=enc.chunk_ends, header_bytes=enc.header_bytes,
+            payload = WarpDivPayload._from_encoder(
+                packed=enc.packed, header_bytes=enc.header_bytes,
                 chunk_len=enc.chunk_len, p_ch=self.p_ch, batch=B, symbols_per_batch=N,
                 cdf_count=tables.M,
                 coding_fingerprint=coding_fingerprint(tables.digest, B, N, C, tables.M),

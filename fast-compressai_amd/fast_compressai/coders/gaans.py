@@ -6,12 +6,15 @@ pinned host buffers that the kernels' last workgroup writes the payload
 size / status into, and a completion word that carries both.  Calls on one stream are
 ordered, so these buffers are never shared by two calls in flight.
 
-Encode enqueues the coding kernel and the pack kernel back to back (the
-pack writes into a worst-case-sized buffer), then waits for the coding
-kernel's completion word and reads the payload size; the pack kernel may
-still be running when encode returns, ordered before any later work on the
-stream.  Decode enqueues one kernel and waits for its completion word to
-read the status word.  Reference host APIs replaced:
+Each shape gets a call plan (``gaans_plan_encode`` / ``gaans_plan_decode``:
+layout, LDS plan, kernel variant and argument block, computed once and kept
+with the prepared tables), so a call is one short C call.  Encode
+(``gaans_run_encode``) enqueues the coding kernel and the pack kernel back
+to back (the pack writes into a worst-case-sized buffer), then waits for
+the coding kernel's completion word and reads the payload size; the pack
+kernel may still be running when encode returns, ordered before any later
+work on the stream.  Decode (``gaans_run_decode``) enqueues one kernel and
+waits for its completion word to read the status word.  Reference host APIs replaced:
 ``encode_with_indexes_warp_v2_cuda`` (``warp_ans_kernel_v2.cu:183-306``, two
 syncs and six launches) and ``decode_with_indexes_warp_cuda``
 (``warp_ans_kernel.cu:477-544``, one sync and four launches).
@@ -45,11 +48,11 @@ class _StreamState:
         self.info_ptr = self.info.data_ptr()
         self.status_ptr = self.status.data_ptr()
         self.workspace = torch.empty(0, dtype=torch.uint8, device=device)
+        self.device = device
 
     def ws(self, nbytes: int) -> torch.Tensor:
         if self.workspace.numel() < nbytes:
-            self.workspace = torch.empty(nbytes, dtype=torch.uint8,
-                                         device=self.workspace.device)
+            self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         return self.workspace
 
 
@@ -164,91 +167,89 @@ def resolve_segments(segments: int | None, tables: PreparedTables, B: int, N: in
 @dataclass(frozen=True)
 class EncodedChunks:
     packed: torch.Tensor      # uint8 [payload bytes]
-    chunk_ends: torch.Tensor  # uint32 [B, K S] view of the header's unit end offsets
     header_bytes: int
     chunk_len: int
     K: int
     segments: int = 1
+    batch: int = 1
+
+    @property
+    def chunk_ends(self) -> torch.Tensor:
+        """uint32 [B, K S] view of the header's unit end offsets."""
+        units = self.K * self.segments
+        return self.packed[64: 64 + 4 * self.batch * units].view(torch.uint32).view(
+            self.batch, units)
 
 
-def encode(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,
-           symbols: torch.Tensor | None = None, indexes: torch.Tensor | None = None,
-           y: torch.Tensor | None = None, medians: torch.Tensor | None = None,
-           segments: int = 1) -> EncodedChunks:
-    """Encode int32 ``symbols`` [B, N], or fp32 latents ``y`` with per-channel
-    ``medians`` (quantize fused).  ``indexes`` None means channel-major
-    tables; ``segments`` coding units per chunk."""
-    L = _native.lib()
-    S = segments
-    lay = _native.layout(B, N, C, P, S)
+def _plan(tables: PreparedTables, decode: bool, mode: int, explicit: bool, B: int, N: int,
+          C: int, P: int, S: int, index: int, n_scales: int = 0, bound: float = 0.0):
+    """The call plan (``gaans_plan_encode`` / ``gaans_plan_decode``) of a
+    shape, cached on the tables it refers to (so it never outlives their
+    blob); made with device ``index`` current.  Returns (plan buffer, its
+    address, layout)."""
+    key = (decode, mode, explicit, B, N, C, P, S, index, n_scales, bound)
+    got = tables.plans.get(key)
+    if got is None:
+        L = _native.lib()
+        lay = _native.layout(B, N, C, P, S)
+        buf = (ctypes.c_uint64 * (_native.PLAN_BYTES // 8))()
+        make = L.gaans_plan_decode if decode else L.gaans_plan_encode
+        _native.check(make(tables.ref, mode, int(explicit), n_scales, bound, B, N, C, P, S,
+                           ctypes.addressof(buf)), "GA-ANS plan")
+        got = (buf, ctypes.addressof(buf), lay)
+        if len(tables.plans) > 64:
+            tables.plans.clear()
+        tables.plans[key] = got
+    return got
+
+
+def _run_encode(tables: PreparedTables, mode: int, explicit: bool, B: int, N: int, C: int,
+                P: int, S: int, device, in0: int, in1, in2, in3, what: str,
+                n_scales: int = 0, bound: float = 0.0) -> EncodedChunks:
+    """Plan (cached), enqueue coding + pack into a worst-case buffer, wait for
+    the completion word and slice the payload."""
     index = _index(device)
     prev = _enter_device(index)
     try:
+        _, plan, lay = _plan(tables, False, mode, explicit, B, N, C, P, S, index, n_scales, bound)
         sp = torch._C._cuda_getCurrentRawStream(index)
         st = _state(index, sp)
         ws = st.ws(lay.workspace_bytes)
-        out = torch.empty(lay.max_payload_bytes, dtype=torch.uint8, device=ws.device)
-        st.info_np[2] = 0
-        if y is not None:
-            rc = L.gaans_encode_latents(sp, y.data_ptr(), medians.data_ptr(), _ptr(indexes),
-                                        tables.ref, B, N, C, P, S, ws.data_ptr(), ws.numel(),
-                                        st.ctrl_ptr, st.info_ptr)
-        else:
-            rc = L.gaans_encode_symbols(sp, symbols.data_ptr(), _ptr(indexes), tables.ref, B, N,
-                                        C, P, S, ws.data_ptr(), ws.numel(), st.ctrl_ptr,
-                                        st.info_ptr)
+        out = torch.empty(lay.max_payload_bytes, dtype=torch.uint8, device=st.device)
+        rc = _native.lib().gaans_run_encode(plan, sp, in0, in1, in2, in3, ws.data_ptr(),
+                                            ws.numel(), st.ctrl_ptr, out.data_ptr(),
+                                            lay.max_payload_bytes, st.info_ptr)
         if rc:
-            _native.check(rc, "GA-ANS encode")
-        rc = L.gaans_encode_pack(sp, ws.data_ptr(), ws.numel(), tables.ref, B, N, C, P, S,
-                                 out.data_ptr(), lay.max_payload_bytes)
-        if rc:
-            _native.check(rc, "GA-ANS pack")
-        rc = L.gaans_wait_host_word(sp, st.info_done)  # the one host wait
-        if rc:
-            _native.check(rc, "GA-ANS encode")
+            _native.check(rc, what)
         word = int(st.info_np[2])  # 1 | status << 1 | payload bytes << 16
-        total, status = word >> 16, (word >> 1) & 0x7FFF
     finally:
         if prev is not None:
             torch.cuda.set_device(prev)
+    total, status = word >> 16, (word >> 1) & 0x7FFF
     if status:
         raise CoderInputError(f"GA-ANS encode failed: {_native.describe_status(status)}")
     packed = out[:total]
     if lay.max_payload_bytes - total > _CLONE_SLACK_BYTES:
         packed = packed.clone()
-    K = lay.K
-    ends = packed[64: 64 + 4 * lay.U].view(torch.uint32).view(B, K * S)
-    return EncodedChunks(packed, ends, lay.header_bytes, lay.chunk_len, K, S)
+    return EncodedChunks(packed, lay.header_bytes, lay.chunk_len, lay.K, S, B)
 
 
-def decode(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int, P: int,
-           device, *, indexes: torch.Tensor | None = None,
-           medians: torch.Tensor | None = None, segments: int = 1) -> torch.Tensor:
-    """Decode to int32 symbols [B, N], or (``medians`` given) to fp32 y_hat
-    [B, N] with dequantize fused; ``segments`` as recorded in the payload."""
-    S = segments
-    L = _native.lib()
+def _run_decode(tables: PreparedTables, mode: int, explicit: bool, B: int, N: int, C: int,
+                P: int, S: int, device, packed: torch.Tensor, in0, in1, in2,
+                dtype: torch.dtype, what: str, n_scales: int = 0,
+                bound: float = 0.0) -> torch.Tensor:
     index = _index(device)
     prev = _enter_device(index)
     try:
+        _, plan, _lay = _plan(tables, True, mode, explicit, B, N, C, P, S, index, n_scales, bound)
         sp = torch._C._cuda_getCurrentRawStream(index)
         st = _state(index, sp)
-        st.status_np[1] = 0
-        if medians is not None:
-            out = torch.empty((B, N), dtype=torch.float32, device=packed.device)
-            rc = L.gaans_decode_latents(sp, packed.data_ptr(), packed.numel(), _ptr(indexes),
-                                        tables.ref, medians.data_ptr(), B, N, C, P, S,
-                                        out.data_ptr(), st.ctrl_ptr, st.status_ptr)
-        else:
-            out = torch.empty((B, N), dtype=torch.int32, device=packed.device)
-            rc = L.gaans_decode_symbols(sp, packed.data_ptr(), packed.numel(), _ptr(indexes),
-                                        tables.ref, B, N, C, P, S, out.data_ptr(), st.ctrl_ptr,
-                                        st.status_ptr)
+        out = torch.empty((B, N), dtype=dtype, device=st.device)
+        rc = _native.lib().gaans_run_decode(plan, sp, packed.data_ptr(), packed.numel(), in0,
+                                            in1, in2, out.data_ptr(), st.ctrl_ptr,
+                                            st.status_ptr)
         if rc:
-            _native.check(rc, "GA-ANS decode")
-        rc = L.gaans_wait_host_word(sp, st.status_done)  # the one host wait
-        if rc:
-            _native.check(rc, "GA-ANS decode")
+            _native.check(rc, what)
         status = int(st.status_np[1]) >> 1  # 1 | status << 1
     finally:
         if prev is not None:
@@ -258,6 +259,34 @@ def decode(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int,
     return out
 
 
+def encode(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,
+           symbols: torch.Tensor | None = None, indexes: torch.Tensor | None = None,
+           y: torch.Tensor | None = None, medians: torch.Tensor | None = None,
+           segments: int = 1) -> EncodedChunks:
+    """Encode int32 ``symbols`` [B, N], or fp32 latents ``y`` with per-channel
+    ``medians`` (quantize fused).  ``indexes`` None means channel-major
+    tables; ``segments`` coding units per chunk."""
+    if y is not None:
+        return _run_encode(tables, _native.MODE_LATENTS, indexes is not None, B, N, C, P,
+                           segments, device, y.data_ptr(), medians.data_ptr(), _ptr(indexes),
+                           None, "GA-ANS encode")
+    return _run_encode(tables, _native.MODE_SYMBOLS, indexes is not None, B, N, C, P, segments,
+                       device, symbols.data_ptr(), _ptr(indexes), None, None, "GA-ANS encode")
+
+
+def decode(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int, P: int,
+           device, *, indexes: torch.Tensor | None = None,
+           medians: torch.Tensor | None = None, segments: int = 1) -> torch.Tensor:
+    """Decode to int32 symbols [B, N], or (``medians`` given) to fp32 y_hat
+    [B, N] with dequantize fused; ``segments`` as recorded in the payload."""
+    if medians is not None:
+        return _run_decode(tables, _native.MODE_LATENTS, indexes is not None, B, N, C, P,
+                           segments, device, packed, medians.data_ptr(), _ptr(indexes), None,
+                           torch.float32, "GA-ANS decode")
+    return _run_decode(tables, _native.MODE_SYMBOLS, indexes is not None, B, N, C, P, segments,
+                       device, packed, _ptr(indexes), None, None, torch.int32, "GA-ANS decode")
+
+
 def encode_gaussian(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,
                     y: torch.Tensor, scales: torch.Tensor, scale_table: torch.Tensor,
                     scale_bound: float, means: torch.Tensor | None = None,
@@ -265,44 +294,10 @@ def encode_gaussian(tables: PreparedTables, B: int, N: int, C: int, P: int, devi
     """GaussianConditional encode with index building and quantize fused:
     fp32 ``y``, ``scales`` (and ``means``) [B, N] channel-major; ``scale_table``
     fp32 on the device, non-decreasing, one entry per table."""
-    L = _native.lib()
-    S = segments
-    lay = _native.layout(B, N, C, P, S)
     _check_gaussian(B, N, device, scale_table, y=y, scales=scales, means=means)
-    index = _index(device)
-    prev = _enter_device(index)
-    try:
-        sp = torch._C._cuda_getCurrentRawStream(index)
-        st = _state(index, sp)
-        ws = st.ws(lay.workspace_bytes)
-        out = torch.empty(lay.max_payload_bytes, dtype=torch.uint8, device=ws.device)
-        st.info_np[2] = 0
-        rc = L.gaans_encode_gaussian(sp, y.data_ptr(), _ptr(means), scales.data_ptr(),
-                                     scale_table.data_ptr(), scale_table.numel(),
-                                     float(scale_bound), tables.ref, B, N, C, P, S,
-                                     ws.data_ptr(), ws.numel(), st.ctrl_ptr, st.info_ptr)
-        if rc:
-            _native.check(rc, "GA-ANS Gaussian encode")
-        rc = L.gaans_encode_pack(sp, ws.data_ptr(), ws.numel(), tables.ref, B, N, C, P, S,
-                                 out.data_ptr(), lay.max_payload_bytes)
-        if rc:
-            _native.check(rc, "GA-ANS pack")
-        rc = L.gaans_wait_host_word(sp, st.info_done)
-        if rc:
-            _native.check(rc, "GA-ANS Gaussian encode")
-        word = int(st.info_np[2])
-        total, status = word >> 16, (word >> 1) & 0x7FFF
-    finally:
-        if prev is not None:
-            torch.cuda.set_device(prev)
-    if status:
-        raise CoderInputError(f"GA-ANS encode failed: {_native.describe_status(status)}")
-    packed = out[:total]
-    if lay.max_payload_bytes - total > _CLONE_SLACK_BYTES:
-        packed = packed.clone()
-    K = lay.K
-    ends = packed[64: 64 + 4 * lay.U].view(torch.uint32).view(B, K * S)
-    return EncodedChunks(packed, ends, lay.header_bytes, lay.chunk_len, K, S)
+    return _run_encode(tables, _native.MODE_GAUSSIAN, True, B, N, C, P, segments, device,
+                       y.data_ptr(), _ptr(means), scales.data_ptr(), scale_table.data_ptr(),
+                       "GA-ANS Gaussian encode", scale_table.numel(), float(scale_bound))
 
 
 def decode_gaussian(packed: torch.Tensor, tables: PreparedTables, B: int, N: int, C: int, P: int,
@@ -311,31 +306,10 @@ def decode_gaussian(packed: torch.Tensor, tables: PreparedTables, B: int, N: int
                     segments: int = 1) -> torch.Tensor:
     """GaussianConditional decode with index building and dequantize fused:
     fp32 y_hat [B, N] = fp32(symbol) + mean (fp32(symbol) without means)."""
-    L = _native.lib()
     _check_gaussian(B, N, device, scale_table, scales=scales, means=means)
-    index = _index(device)
-    prev = _enter_device(index)
-    try:
-        sp = torch._C._cuda_getCurrentRawStream(index)
-        st = _state(index, sp)
-        st.status_np[1] = 0
-        out = torch.empty((B, N), dtype=torch.float32, device=packed.device)
-        rc = L.gaans_decode_gaussian(sp, packed.data_ptr(), packed.numel(), scales.data_ptr(),
-                                     _ptr(means), scale_table.data_ptr(), scale_table.numel(),
-                                     float(scale_bound), tables.ref, B, N, C, P, segments,
-                                     out.data_ptr(), st.ctrl_ptr, st.status_ptr)
-        if rc:
-            _native.check(rc, "GA-ANS Gaussian decode")
-        rc = L.gaans_wait_host_word(sp, st.status_done)
-        if rc:
-            _native.check(rc, "GA-ANS Gaussian decode")
-        status = int(st.status_np[1]) >> 1
-    finally:
-        if prev is not None:
-            torch.cuda.set_device(prev)
-    if status:
-        raise CoderInputError(f"warp_div decode failed: {_native.describe_status(status)}")
-    return out
+    return _run_decode(tables, _native.MODE_GAUSSIAN, True, B, N, C, P, segments, device, packed,
+                       scales.data_ptr(), _ptr(means), scale_table.data_ptr(), torch.float32,
+                       "GA-ANS Gaussian decode", scale_table.numel(), float(scale_bound))
 
 
 def decode_rans64(streams: torch.Tensor, offsets: torch.Tensor, tables: PreparedTables, B: int,

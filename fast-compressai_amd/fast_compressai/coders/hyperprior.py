@@ -47,7 +47,7 @@ def _tables(module, what: str):
 
 def _payload(enc, p_ch: int, B: int, N: int, C: int, tables) -> WarpDivPayload:
     return WarpDivPayload._from_encoder(
-        packed=enc.packed, chunk_ends=enc.chunk_ends, header_bytes=enc.header_bytes,
+        packed=enc.packed, header_bytes=enc.header_bytes,
         chunk_len=enc.chunk_len, p_ch=p_ch, batch=B, symbols_per_batch=N, cdf_count=tables.M,
         coding_fingerprint=coding_fingerprint(tables.digest, B, N, C, tables.M),
         channels=None if C == tables.M else C, segments=enc.segments)

@@ -19,7 +19,7 @@ from __future__ import annotations
 import ctypes
 import threading
 from collections import OrderedDict
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import numpy as np
 import torch
@@ -36,6 +36,9 @@ class PreparedTables:
     Lmax: int
     digest: int
     desc: _native.Tables  # C descriptor pointing at ``blob``
+    device: torch.device = None  # the device of ``blob``
+    # call plans of these tables by shape (gaans.py); they point into ``blob``
+    plans: dict = field(default_factory=dict, compare=False, repr=False)
 
     @property
     def ref(self):
@@ -75,7 +78,7 @@ def prepare_tables(cdfs: torch.Tensor, cdf_sizes: torch.Tensor, offsets: torch.T
     blob = torch.from_numpy(host).to(dev)
     desc.dev = blob.data_ptr()
     return PreparedTables(blob=blob, nbytes=int(nbytes.value), M=M, Lmax=Lmax,
-                          digest=int(desc.digest), desc=desc)
+                          digest=int(desc.digest), desc=desc, device=blob.device)
 
 
 class TableCache:
@@ -96,6 +99,16 @@ class TableCache:
         # device pointers are unique across devices; dtype and device are
         # checked by the callers before tables are prepared
         return tuple((t.data_ptr(), t._version, t.shape, t.stride()) for t in tensors)
+
+    def hit(self, cdfs, cdf_sizes, offsets) -> PreparedTables | None:
+        """The tables of the last call when these are the same three tensor
+        objects, unchanged since (in-place version and storage); else None."""
+        last = self._last
+        if (last is not None and last[0] is cdfs and last[1] is cdf_sizes and last[2] is offsets
+                and last[3] == (cdfs._version, cdf_sizes._version, offsets._version,
+                                cdfs.data_ptr(), cdf_sizes.data_ptr(), offsets.data_ptr())):
+            return last[4]
+        return None
 
     def get(self, cdfs: torch.Tensor, cdf_sizes: torch.Tensor,
             offsets: torch.Tensor) -> PreparedTables:

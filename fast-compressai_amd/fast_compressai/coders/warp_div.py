@@ -32,7 +32,7 @@ import functools
 import hashlib
 import re
 import struct
-from dataclasses import dataclass, fields
+from dataclasses import MISSING, dataclass, fields
 import torch
 
 from . import gaans
@@ -119,12 +119,27 @@ class WarpDivPayload:
     @classmethod
     def _from_encoder(cls, **values) -> "WarpDivPayload":
         """Payload built by ``WarpDivBackend.encode`` from values it has just
-        produced and checked; skips the field validation of ``__init__``."""
+        produced and checked; skips the field validation of ``__init__``.
+        Without ``chunk_ends`` the field is built on first use, as a view of
+        the header's unit end offsets."""
         obj = object.__new__(cls)
         state = dict(_PAYLOAD_DEFAULTS)
         state.update(values)
         obj.__dict__.update(state)
         return obj
+
+    def __getattr__(self, name: str):
+        # only reached for attributes missing from the instance: the lazily
+        # built chunk_ends of an encoder-made payload
+        d = self.__dict__
+        if name != "chunk_ends" or "packed" not in d:
+            raise AttributeError(name)
+        channels = d["cdf_count"] if d["channels"] is None else d["channels"]
+        units = (channels + d["p_ch"] - 1) // d["p_ch"] * d["segments"]
+        B = d["batch"]
+        ends = d["packed"][64: 64 + 4 * B * units].view(torch.uint32).view(B, units)
+        d["chunk_ends"] = ends
+        return ends
 
     @property
     def coded_channels(self) -> int:
@@ -178,7 +193,7 @@ class WarpDivPayload:
 
 
 # field defaults of WarpDivPayload (for _from_encoder)
-_PAYLOAD_DEFAULTS = {f.name: f.default for f in fields(WarpDivPayload)}
+_PAYLOAD_DEFAULTS = {f.name: f.default for f in fields(WarpDivPayload) if f.default is not MISSING}
 
 
 class WarpDivBackend:
@@ -213,22 +228,25 @@ class WarpDivBackend:
         channels: int | None = None,
         segments: int | None = None,
     ) -> WarpDivPayload:
-        C = _validate_inputs(symbols, indexes, cdfs, cdf_sizes, offsets, p_ch, channels)
-        tables = self.prepared_tables(cdfs, cdf_sizes, offsets)
+        tables = self._tables.hit(cdfs, cdf_sizes, offsets)
+        if tables is None:
+            C = _validate_inputs(symbols, indexes, cdfs, cdf_sizes, offsets, p_ch, channels)
+            tables = self.prepared_tables(cdfs, cdf_sizes, offsets)
+        else:  # the same table tensors as the last call: their checks passed then
+            C = _validate_data(symbols, indexes, p_ch, channels, tables)
         B, N = int(symbols.shape[0]), int(symbols.shape[1])
         segments = gaans.resolve_segments(segments, tables, B, N, C, p_ch, symbols.device)
         enc = gaans.encode(tables, B, N, C, p_ch, symbols.device, symbols=symbols,
                            indexes=indexes, segments=segments)
         return WarpDivPayload._from_encoder(
             packed=enc.packed,
-            chunk_ends=enc.chunk_ends,
             header_bytes=enc.header_bytes,
             chunk_len=enc.chunk_len,
             p_ch=int(p_ch),
             batch=B,
             symbols_per_batch=N,
-            cdf_count=int(cdfs.shape[0]),
-            coding_fingerprint=coding_fingerprint(tables.digest, B, N, C, int(cdfs.shape[0])),
+            cdf_count=tables.M,
+            coding_fingerprint=coding_fingerprint(tables.digest, B, N, C, tables.M),
             channels=None if channels is None else int(channels),
             segments=segments,
         )
@@ -243,13 +261,18 @@ class WarpDivBackend:
     ) -> torch.Tensor:
         if not isinstance(payload, WarpDivPayload):
             raise CoderInputError("warp_div decode expects WarpDivPayload")
-        C = _validate_inputs(indexes, indexes, cdfs, cdf_sizes, offsets, payload.p_ch,
-                             payload.channels)
+        tables = self._tables.hit(cdfs, cdf_sizes, offsets)
+        if tables is None:
+            C = _validate_inputs(indexes, indexes, cdfs, cdf_sizes, offsets, payload.p_ch,
+                                 payload.channels)
+        else:
+            C = _validate_data(indexes, indexes, payload.p_ch, payload.channels, tables)
         if tuple(indexes.shape) != (payload.batch, payload.symbols_per_batch):
             raise CoderInputError("indexes shape does not match payload metadata")
         if cdfs.shape[0] != payload.cdf_count or indexes.device != payload.packed.device:
             raise CoderInputError("CDF count or GPU device does not match payload metadata")
-        tables = self.prepared_tables(cdfs, cdf_sizes, offsets)
+        if tables is None:
+            tables = self.prepared_tables(cdfs, cdf_sizes, offsets)
         B, N = payload.batch, payload.symbols_per_batch
         if payload.coding_fingerprint is not None and payload.coding_fingerprint != \
                 coding_fingerprint(tables.digest, B, N, C, payload.cdf_count):
@@ -257,6 +280,38 @@ class WarpDivBackend:
         return gaans.decode(payload.packed, tables, B, N, C, payload.p_ch,
                             payload.packed.device, indexes=indexes,
                             segments=payload.segments)
+
+
+def _validate_data(symbols: torch.Tensor, indexes: torch.Tensor, p_ch: int,
+                   channels: int | None, tables: PreparedTables) -> int:
+    """The checks of ``_validate_inputs`` that concern the symbols and indexes,
+    for table tensors that passed them on an earlier call (same messages).
+    Returns the channel count used for chunking."""
+    T = torch.Tensor
+    if not isinstance(symbols, T) or not isinstance(indexes, T):
+        raise CoderInputError("symbols and indexes must be torch tensors")
+    if type(p_ch) is not int or p_ch <= 0:
+        raise CoderInputError("p_ch must be a positive integer")
+    dev = symbols.device
+    if dev != tables.device or indexes.device != dev:
+        raise CoderInputError("all coder inputs must be GPU tensors on the same device")
+    if symbols.dtype != torch.int32 or indexes.dtype != torch.int32:
+        raise CoderInputError("all warp_div input tensors must use torch.int32")
+    if not (symbols.is_contiguous() and indexes.is_contiguous()):
+        raise CoderInputError("all warp_div input tensors must be contiguous")
+    shape = symbols.shape
+    if len(shape) != 2 or indexes.shape != shape:
+        raise CoderInputError("symbols and indexes must have matching [B, N] shape")
+    if shape[0] <= 0 or shape[1] <= 0:
+        raise CoderInputError("empty symbols are not supported by this WarpANS format")
+    C = tables.M if channels is None else channels
+    if type(C) is not int or C <= 0:
+        raise CoderInputError("channels must be a positive integer")
+    if shape[1] % C != 0:
+        raise CoderInputError("symbols per batch must be divisible by the channel count")
+    if p_ch > C:
+        raise CoderInputError("p_ch cannot exceed the number of CDF channels")
+    return C
 
 
 def _validate_inputs(

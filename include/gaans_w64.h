@@ -59,7 +59,7 @@
 extern "C" {
 #endif
 
-#define GAANS_ABI_VERSION 9
+#define GAANS_ABI_VERSION 10
 #define GAANS_CTRL_BYTES 256
 
 /* return codes */
@@ -303,6 +303,74 @@ int gaans_rans64_decode(void* stream, const uint8_t* streams_dev, int64_t stream
  * word.  Replaces the stream synchronisations of the reference's host code
  * (warp_ans_kernel_v2.cu:275-276, warp_div.py:63-65). */
 int gaans_wait_host_word(void* stream, const uint32_t* word);
+
+/* ---- call plans: repeated calls of one shape --------------------------------- */
+
+/* A plan is the shape-dependent part of an encode (coding + pack launch) or
+ * decode launch -- layout, LDS staging plan, kernel variant, launch geometry
+ * and argument block -- computed once by gaans_plan_encode / gaans_plan_decode
+ * with the device it will run on current.  gaans_run_encode / gaans_run_decode
+ * then only set the call's pointers, enqueue and wait: the same kernels and
+ * bytes as the gaans_encode_* + gaans_encode_pack + gaans_wait_host_word and
+ * gaans_decode_* + gaans_wait_host_word sequences, without recomputing the
+ * plan or converting a long argument list on every call.  A plan refers to
+ * the table blob at tables->dev: the blob must outlive every run of the plan.
+ * A plan is plain bytes owned by the caller; runs only read it, so one plan
+ * may serve several streams (each with its own control block).  No
+ * counterpart in the reference, whose host code recomputes its launch on
+ * every call (warp_ans_kernel_v2.cu:183-306, warp_ans_kernel.cu:477-544). */
+#define GAANS_PLAN_BYTES 1536
+typedef struct gaans_plan {
+  uint64_t opaque[GAANS_PLAN_BYTES / 8];
+} gaans_plan;
+
+/* plan modes: the inputs a run takes (see gaans_run_encode / _decode) */
+#define GAANS_MODE_SYMBOLS 0  /* int32 symbols (gaans_encode_symbols / gaans_decode_symbols) */
+#define GAANS_MODE_LATENTS 1  /* fp32 latents + medians (gaans_encode_latents / _decode_latents) */
+#define GAANS_MODE_GAUSSIAN 2 /* GaussianConditional (gaans_encode_gaussian / _decode_gaussian) */
+
+/* Plan an encode of B x N symbols (C channels, P per chunk, `segments` per
+ * chunk) with `tables`.  explicit_indexes: runs pass an indexes array (0:
+ * table = channel; ignored for GAANS_MODE_GAUSSIAN).  n_scales and
+ * scale_bound: the Gaussian scale table's length and CompressAI's lower scale
+ * bound (ignored for the other modes). */
+int gaans_plan_encode(const gaans_tables* tables, int32_t mode, int32_t explicit_indexes,
+                      int32_t n_scales, float scale_bound, int64_t B, int64_t N, int64_t C,
+                      int64_t P, int32_t segments, gaans_plan* plan);
+
+/* Plan a decode; arguments as for gaans_plan_encode. */
+int gaans_plan_decode(const gaans_tables* tables, int32_t mode, int32_t explicit_indexes,
+                      int32_t n_scales, float scale_bound, int64_t B, int64_t N, int64_t C,
+                      int64_t P, int32_t segments, gaans_plan* plan);
+
+/* Encode with a plan: enqueue the coding and pack kernels on `stream` into
+ * out_dev (at least the layout's max_payload_bytes), then wait for the
+ * completion word info_host[2] (pinned host memory, 3 u64; the run clears it
+ * before the launch).  On return info_host[2] = 1 | status << 1 | payload
+ * bytes << 16, as for gaans_encode_symbols; the pack kernel may still run,
+ * ordered on `stream`.  Device inputs by mode:
+ *   GAANS_MODE_SYMBOLS:  in0 symbols int32 [B, N], in1 indexes int32 [B, N]
+ *                        (NULL for a table = channel plan)
+ *   GAANS_MODE_LATENTS:  in0 y fp32 [B, N], in1 medians fp32 [C], in2 indexes
+ *                        (as above)
+ *   GAANS_MODE_GAUSSIAN: in0 y, in1 means (or NULL), in2 scales, all fp32
+ *                        [B, N]; in3 the scale table (n_scales fp32)
+ * Unused inputs are ignored. */
+int gaans_run_encode(const gaans_plan* plan, void* stream, const void* in0, const void* in1,
+                     const void* in2, const void* in3, void* workspace_dev,
+                     int64_t workspace_bytes, void* ctrl_dev, uint8_t* out_dev,
+                     int64_t out_bytes, uint64_t* info_host);
+
+/* Decode with a plan into out_dev (int32 symbols for GAANS_MODE_SYMBOLS, fp32
+ * y_hat otherwise, [B, N]) and wait for the completion word status_host[1]
+ * (pinned host memory, 2 u32; cleared by the run); status_host[0] and the
+ * word's status bits as for gaans_decode_symbols.  Device inputs by mode:
+ *   GAANS_MODE_SYMBOLS:  in0 indexes (NULL for a table = channel plan)
+ *   GAANS_MODE_LATENTS:  in0 medians fp32 [C], in1 indexes (as above)
+ *   GAANS_MODE_GAUSSIAN: in0 scales, in1 means (or NULL), in2 the scale table */
+int gaans_run_decode(const gaans_plan* plan, void* stream, const uint8_t* payload_dev,
+                     int64_t payload_bytes, const void* in0, const void* in1, const void* in2,
+                     void* out_dev, void* ctrl_dev, uint32_t* status_host);
 
 /* ---- host self test ------------------------------------------------------- */
 

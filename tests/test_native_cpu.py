@@ -280,3 +280,34 @@ def test_return_codes_map_to_error_classes():
         _native.check(_native.EHIP, "call")
     assert not isinstance(info.value, ValueError)
     assert isinstance(info.value, RuntimeError)
+
+
+def test_plan_and_run_reject_bad_arguments_before_device_work():
+    # argument errors are found on the host, before any device query (no GPU
+    # here): a NULL plan, an unknown mode, a bad shape, and runs with a plan
+    # that gaans_plan_* did not fill (or filled for the other direction)
+    L = _native.lib()
+    plan = (ctypes.c_uint64 * (_native.PLAN_BYTES // 8))()
+    addr = ctypes.addressof(plan)
+    desc = _native.Tables()
+    assert L.gaans_plan_encode(ctypes.byref(desc), 0, 1, 0, 0.0, 1, 64, 1, 1, 1, None) \
+        == _native.EINVAL
+    assert L.gaans_plan_encode(ctypes.byref(desc), 7, 1, 0, 0.0, 1, 64, 1, 1, 1, addr) \
+        == _native.EINVAL
+    assert "mode" in _native.last_error()
+    assert L.gaans_plan_decode(ctypes.byref(desc), 0, 1, 0, 0.0, 1, 65, 2, 1, 1, addr) \
+        == _native.EINVAL  # N % C != 0
+    assert L.gaans_plan_encode(ctypes.byref(desc), 0, 1, 0, 0.0, 1, 64, 1, 1, 1, addr) \
+        == _native.EINVAL  # descriptor without a blob
+    info = (ctypes.c_uint64 * 3)()
+    status = (ctypes.c_uint32 * 2)()
+    fake = 1 << 20  # never dereferenced: the runs stop at the plan check
+    assert L.gaans_run_encode(addr, None, fake, None, None, None, fake, 1 << 20, fake, fake,
+                              1 << 20, ctypes.addressof(info)) == _native.EINVAL
+    assert "encode plan" in _native.last_error()
+    assert L.gaans_run_decode(addr, None, fake, 1 << 20, None, None, None, fake, fake,
+                              ctypes.addressof(status)) == _native.EINVAL
+    assert "decode plan" in _native.last_error()
+    assert L.gaans_run_encode(None, None, fake, None, None, None, fake, 1 << 20, fake, fake,
+                              1 << 20, ctypes.addressof(info)) == _native.EINVAL
+    assert ctypes.sizeof(plan) == _native.PLAN_BYTES
