@@ -52,6 +52,10 @@ def parse():
                          "print their event times; 'copy' runs one device copy of --copy-probe "
                          "MiB.  For rocprofv3 counter runs.")
     ap.add_argument("--reps", type=int, default=10)
+    ap.add_argument("--phases", action="store_true",
+                    help="with --kernels: also run each kernel once with phase timestamps "
+                         "(gaans_debug_phases) and print the per-unit breakdown; loads the "
+                         "measurement build lib/libgaans_w64_phases.so (csrc/build.py --phases)")
     ap.add_argument("--segments", type=int, default=None,
                     help="coding units per chunk for --kernels (default: the coder's choice)")
     return ap.parse_args()
@@ -91,7 +95,66 @@ def read_traffic(workload: str, kernel_key: str):
     return None
 
 
-def kernel_times(L, _native, torch, backend, w, dev, reps=40, segments=None):
+def phase_breakdown(L, torch, dev, units, steps, fn):
+    """Run ``fn`` (one kernel launch) once with phase timestamps on and
+    summarise them (gaans_debug_phases slots): microseconds from the earliest
+    unit's entry to each phase (median and max over units), the last unit's
+    completion word, and shader cycles per coding step (the slowest unit's
+    first to last step over its steps)."""
+    import ctypes
+
+    import numpy as np
+
+    from fast_compressai.coders import _native
+
+    slots = _native.PHASE_SLOTS
+    buf = torch.zeros(units * slots, dtype=torch.int64, device=dev)
+    khz = ctypes.c_int32(0)
+    torch.cuda.synchronize()
+    _native.check(L.gaans_debug_phases(buf.data_ptr(), units, ctypes.byref(khz)), "phases")
+    try:
+        fn()
+        torch.cuda.synchronize()
+    finally:
+        _native.check(L.gaans_debug_phases(None, 0, None), "phases off")
+    t = buf.cpu().numpy().reshape(units, slots).astype(np.float64)
+    us = 1e3 / khz.value  # microseconds per real-time tick
+    t0 = t[:, 0].min()
+    names = {0: "entry", 1: "first_loads_in", 2: "tables_staged", 3: "first_step",
+             4: "after_last_step",
+             5: "before_counter", 6: "after_counter"}
+    out = {"wall_clock_khz": khz.value, "units": units}
+    for i, name in names.items():
+        rel = (t[:, i] - t0) * us
+        out[name + "_us"] = [round(float(np.median(rel)), 2), round(float(rel.max()), 2)]
+    done = t[:, 7][t[:, 7] > 0]
+    out["completion_word_us"] = round(float((done.max() - t0) * us), 2) if done.size else None
+    cyc = t[:, 13] - t[:, 12]
+    slow = int(np.argmax(cyc))
+    out["cycles_per_step_slowest_unit"] = round(float(cyc[slow]) / max(1, steps[slow]), 1)
+    out["cycles_per_step_median"] = round(float(np.median(cyc / np.maximum(1, steps))), 1)
+    out["steps_slowest_unit"] = int(steps[slow])
+    out["step_loop_us_median"] = round(float(np.median((t[:, 4] - t[:, 3]) * us)), 2)
+    return out
+
+
+def unit_steps(B, N, C, P, S):
+    """Coding steps of every unit (64 positions a step), unit order."""
+    import math
+
+    K = math.ceil(C / P)
+    chunk_len = P * (N // C)
+    out = []
+    for b in range(B):
+        for k in range(K):
+            ln = min(chunk_len, N - k * chunk_len)
+            tc = (ln + 63) // 64
+            for s_ in range(S):
+                out.append((s_ + 1) * tc // S - s_ * tc // S)
+    return out
+
+
+def kernel_times(L, _native, torch, backend, w, dev, reps=40, segments=None, phases=False):
     """Event-timed encode / decode kernels of one workload (median over
     batches of back-to-back launches, seconds per launch), the payload size
     and the segments per chunk used (the coder's choice unless one is given)."""
@@ -141,10 +204,14 @@ def kernel_times(L, _native, torch, backend, w, dev, reps=40, segments=None):
         res[name] = statistics.median(ts)
     torch.cuda.synchronize()
     assert int(status[0].item()) == 0 and torch.equal(out, sym)
+    if phases:
+        steps = unit_steps(B, N, C, P, S)
+        res["phases"] = {name: phase_breakdown(L, torch, dev, int(lay.U), steps, fn)
+                         for name, fn in (("encode", enc), ("decode", dec))}
     return res, int(payload.packed.numel()), S
 
 
-def gaussian_kernel_times(L, _native, torch, p_ch, dev, reps=40, segments=None):
+def gaussian_kernel_times(L, _native, torch, p_ch, dev, reps=40, segments=None, phases=False):
     """Event-timed fused GaussianConditional kernels (gaans_encode_gaussian /
     gaans_decode_gaussian) on the mean-scale hyperprior y 1x192x32x48: fp32
     y, means and scales in, index search and quantize in the kernel; decode
@@ -208,6 +275,10 @@ def gaussian_kernel_times(L, _native, torch, p_ch, dev, reps=40, segments=None):
     torch.cuda.synchronize()
     want = torch.from_numpy(yw.symbols).to(dev).float() + means
     assert int(status[0].item()) == 0 and torch.equal(out, want)
+    if phases:
+        steps = unit_steps(B, N, C, P, S)
+        res["phases"] = {name: phase_breakdown(L, torch, dev, int(lay.U), steps, fn)
+                         for name, fn in (("encode", encode), ("decode", decode))}
     return res, int(enc.packed.numel()), B * N, yw.raw_rgb_bytes, S, input_sha256(
         y_np, means_np, table_np[idx_np])
 
@@ -491,23 +562,28 @@ def kernels_only(args):
     reps = max(5, args.reps // 5 * 5)
     if args.kernels.startswith("hyperprior_y_p"):
         kt, pb, n_sym, _, S, _ = gaussian_kernel_times(L, _native, torch, int(args.kernels[14:]),
-                                                    dev, reps=reps, segments=args.segments)
+                                                    dev, reps=reps, segments=args.segments,
+                                                    phases=args.phases)
         alg = 12 * n_sym + pb
     else:
         w = _kernel_workloads()[args.kernels]()
         kt, pb, S = kernel_times(L, _native, torch, WarpDivBackend(), w, dev, reps=reps,
-                                 segments=args.segments)
+                                 segments=args.segments, phases=args.phases)
         n_sym = w.batch * w.n
         alg = 8 * n_sym + pb
     print(json.dumps({"kernels": args.kernels, "segments": S, "symbols": n_sym,
                       "payload_bytes": pb,
                       "alg_bytes_per_launch": alg,
                       "encode_us": round(kt["encode"] * 1e6, 2),
-                      "decode_us": round(kt["decode"] * 1e6, 2)}), flush=True)
+                      "decode_us": round(kt["decode"] * 1e6, 2),
+                      **({"phases": kt["phases"]} if args.phases else {})}), flush=True)
 
 
 def main():
     args = parse()
+    if args.phases:
+        # the measurement build of the library (csrc/build.py --phases)
+        os.environ["GAANS_PHASE_TIMES"] = "1"
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this coder's "
               "multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)

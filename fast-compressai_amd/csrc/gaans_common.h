@@ -31,12 +31,20 @@ constexpr uint32_t kVersion = 4u;
 constexpr int kMaxSegments = 256;  // segments per chunk
 constexpr uint32_t kParams = 0x00041040u;  // lanes 64 | precision 16 << 8 | bypass 4 << 16
 constexpr int kFixedWords = 16;
-constexpr uint32_t kTabMagic = 0x35425447u;  // "GTB5"
+constexpr uint32_t kTabMagic = 0x36425447u;  // "GTB6"
 constexpr int kLutBits = 8;
 constexpr int kLutSize = 1 << kLutBits;
 constexpr int kSubBits = 4;                 // a sub-block: 16 entries of 16 or 1 values
 constexpr int kSubSize = 1 << kSubBits;
 constexpr int kSubBytes = 8 * kSubSize;
+// wide decode lookups: 2048 buckets of 32 values per table, a dense bucket
+// (two or more symbols starting after its first value) resolved by one
+// sub-block of 16 two-value ranges (never dense); built for blobs of at most
+// kWideMaxTables tables (16 KB of lookups per table)
+constexpr int kWideBits = 11;
+constexpr int kWideSize = 1 << kWideBits;
+constexpr int kWideSubShift = 16 - kWideBits - kSubBits;  // a sub-range: 2 values
+constexpr int kWideMaxTables = 4096;
 constexpr uint32_t kHashMul = 0x9E3779B9u;
 constexpr int kMaxEscNibbles = 9;  // escape count + 8 nibbles of raw
 
@@ -69,9 +77,13 @@ struct TabHdr {
   uint32_t max_nsym;
   uint32_t dense_off;    // byte offset of the sub-blocks
   uint32_t total_dense;  // sub-blocks over all tables
-  uint32_t flags;        // kTabOffsetsSafe
+  uint32_t flags;        // kTabOffsetsSafe, kTabSearch, kTabWide
   uint32_t clut_off;    // byte offset of the search lookups (u32 per bucket)
   uint32_t starts_off;  // byte offset of the symbol starts (u16 per symbol)
+  uint32_t wide_off;    // byte offset of the wide lookups (u64 x kWideSize per table)
+  uint32_t wdense_off;  // byte offset of the wide lookups' sub-blocks
+  uint32_t wbase_off;   // byte offset of each table's first wide sub-block (u32 x (M + 1))
+  uint32_t total_wide;  // wide sub-blocks over all tables
 };
 // every offset <= INT32_MAX - 65535: symbol index + offset cannot overflow
 constexpr uint32_t kTabOffsetsSafe = 1u;
@@ -80,7 +92,9 @@ constexpr uint32_t kTabOffsetsSafe = 1u;
 constexpr uint32_t kTabSearch = 2u;
 constexpr int64_t kSearchMaxSyms = 65535 - 8;
 constexpr int kStartsPad = 8;  // zero starts after the last symbol (sentinel, reads past it)
-static_assert(sizeof(TabHdr) == 64, "table header is 64 bytes");
+// the wide lookups are built (M <= kWideMaxTables)
+constexpr uint32_t kTabWide = 4u;
+static_assert(sizeof(TabHdr) == 80, "table header is 80 bytes");
 
 struct TabMeta {
   uint32_t ent_base;    // first entry of the table
@@ -192,19 +206,25 @@ GAANS_HD int unit_len(int64_t g, int32_t K, int32_t S, int64_t N,
 // global memory.
 
 // Blob sections: [header][metadata][entries][lookups][sub-blocks][search
-// lookups][starts]; the offsets of the last two follow from the counts.
+// lookups][starts][wide lookups][wide sub-blocks][wide bases]; the offsets
+// follow from the counts (the wide sections are empty unless `wide`).
 struct BlobLayout {
-  int64_t ent_off, lut_off, dense_off, clut_off, starts_off, end;
+  int64_t ent_off, lut_off, dense_off, clut_off, starts_off, wide_off, wdense_off, wbase_off,
+      end;
 };
 
-inline BlobLayout blob_layout(int64_t M, int64_t total_syms, int64_t total_blocks) {
+inline BlobLayout blob_layout(int64_t M, int64_t total_syms, int64_t total_blocks, bool wide,
+                              int64_t total_wide) {
   BlobLayout L;
   L.ent_off = align_up((int64_t)sizeof(TabHdr) + (int64_t)sizeof(TabMeta) * M, 8);
   L.lut_off = align_up(L.ent_off + 8 * total_syms, 16);
   L.dense_off = L.lut_off + 8ll * kLutSize * M;
   L.clut_off = L.dense_off + (int64_t)kSubBytes * total_blocks;
   L.starts_off = L.clut_off + 4ll * kLutSize * M;
-  L.end = L.starts_off + align_up(2 * (total_syms + kStartsPad), 16);
+  L.wide_off = L.starts_off + align_up(2 * (total_syms + kStartsPad), 16);
+  L.wdense_off = L.wide_off + (wide ? 8ll * kWideSize * M : 0);
+  L.wbase_off = L.wdense_off + (wide ? (int64_t)kSubBytes * total_wide : 0);
+  L.end = L.wbase_off + (wide ? align_up(4 * (M + 1), 16) : 0);
   return L;
 }
 

@@ -105,8 +105,8 @@ uint64_t fnv_u32(uint64_t h, uint32_t v) {
   return h;
 }
 
-int64_t tables_size(int32_t M, int64_t total_syms, int64_t total_blocks) {
-  return blob_layout(M, total_syms, total_blocks).end;
+int64_t tables_size(int32_t M, int64_t total_syms, int64_t total_blocks, int64_t total_wide) {
+  return blob_layout(M, total_syms, total_blocks, M <= kWideMaxTables, total_wide).end;
 }
 
 // Search lookups of one table (symbols base .. base + nsym - 1 of the blob):
@@ -182,6 +182,37 @@ int32_t build_lookup(const int32_t* c, int32_t S, uint64_t* lut, uint64_t* block
   return n;
 }
 
+// Wide lookups of one CDF (S entries): kWideSize entries of 32-value
+// buckets in lut and, for each dense bucket, a sub-block of 16 two-value
+// ranges (global indices from `first`; filled when blocks is non-NULL).
+// Returns the table's sub-blocks.
+int32_t build_wide(const int32_t* c, int32_t S, uint64_t* lut, uint64_t* blocks,
+                   uint32_t first) {
+  const uint32_t nsym = (uint32_t)(S - 1);
+  const uint32_t width = 1u << (16 - kWideBits);
+  const uint32_t sub_width = 1u << kWideSubShift;
+  int32_t n = 0;
+  uint32_t s = 0;
+  for (int j = 0; j < kWideSize; ++j) {
+    const uint32_t lo = (uint32_t)j * width;
+    uint64_t e;
+    if (lookup_entry(c, nsym, lo, width, s, &e)) {
+      if (lut) lut[j] = e;
+      continue;
+    }
+    const uint32_t b2 = (uint32_t)n++;
+    if (lut) lut[j] = (uint64_t)(first + b2) | ((uint64_t)(s | (0xffffu << 16)) << 32);
+    uint32_t s2 = s;
+    for (int i = 0; i < kSubSize; ++i) {
+      uint64_t e2 = 0;
+      // a two-value range holds at most one start after its first value
+      lookup_entry(c, nsym, lo + (uint32_t)i * sub_width, sub_width, s2, &e2);
+      if (blocks) blocks[(size_t)b2 * kSubSize + i] = e2;
+    }
+  }
+  return n;
+}
+
 }  // namespace
 
 using namespace gaans;
@@ -249,7 +280,7 @@ int gaans_tables_bytes(const int32_t* cdfs, const int32_t* cdf_sizes, int32_t M,
   // decode records carry a table number and an escape symbol in 16 bits each
   if (M < 1 || M > 65536 || Lmax < 2)
     return fail(GAANS_EINVAL, "need 1 <= M <= 65536 tables of Lmax >= 2 entries (got M=%d)", M);
-  int64_t total = 0, dense = 0;
+  int64_t total = 0, dense = 0, wide = 0;
   for (int32_t t = 0; t < M; ++t) {
     const int32_t S = cdf_sizes[t];
     if (S < 2 || S > Lmax || S > 65536)
@@ -265,8 +296,9 @@ int gaans_tables_bytes(const int32_t* cdfs, const int32_t* cdf_sizes, int32_t M,
         return fail(GAANS_ETABLE, "table %d: CDF is not strictly increasing at entry %d", t, j);
     total += S - 1;
     dense += build_lookup(c, S, nullptr, nullptr, 0u);
+    if (M <= kWideMaxTables) wide += build_wide(c, S, nullptr, nullptr, 0u);
   }
-  *bytes = tables_size(M, total, dense);
+  *bytes = tables_size(M, total, dense, wide);
   if (*bytes > 0xffffffffll) return fail(GAANS_ETABLE, "tables exceed 4 GiB");
   return GAANS_OK;
 }
@@ -287,17 +319,27 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
   TabMeta* meta = reinterpret_cast<TabMeta*>(o + sizeof(TabHdr));
   const int64_t ent_off = align_up(sizeof(TabHdr) + (int64_t)sizeof(TabMeta) * M, 8);
   uint32_t* ent = reinterpret_cast<uint32_t*>(o + ent_off);
-  int64_t total = 0, total_dense = 0;
+  const bool wide = M <= kWideMaxTables;
+  int64_t total = 0, total_dense = 0, total_wide = 0;
   uint32_t max_nsym = 0;
-  int32_t max_dense = 0;
+  int32_t max_dense = 0, max_wide = 0;
   for (int32_t t = 0; t < M; ++t) {
     total += cdf_sizes[t] - 1;
     if ((uint32_t)(cdf_sizes[t] - 1) > max_nsym) max_nsym = (uint32_t)(cdf_sizes[t] - 1);
     const int32_t nd = build_lookup(cdfs + (int64_t)t * Lmax, cdf_sizes[t], nullptr, nullptr, 0u);
     total_dense += nd;
     if (nd > max_dense) max_dense = nd;
+    if (wide) {
+      const int32_t nw = build_wide(cdfs + (int64_t)t * Lmax, cdf_sizes[t], nullptr, nullptr, 0u);
+      total_wide += nw;
+      if (nw > max_wide) max_wide = nw;
+    }
   }
-  const BlobLayout BL = blob_layout(M, total, total_dense);
+  const BlobLayout BL = blob_layout(M, total, total_dense, wide, total_wide);
+  uint64_t* wlut = reinterpret_cast<uint64_t*>(o + BL.wide_off);
+  uint64_t* wblocks = reinterpret_cast<uint64_t*>(o + BL.wdense_off);
+  uint32_t* wbase = reinterpret_cast<uint32_t*>(o + BL.wbase_off);
+  uint32_t wblk = 0;
   const int64_t lut_off = BL.lut_off;
   uint64_t* lut = reinterpret_cast<uint64_t*>(o + lut_off);
   const int64_t dense_off = BL.dense_off;
@@ -331,9 +373,15 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
     }
     dblk += (uint32_t)build_lookup(c, S, lut + (int64_t)t * kLutSize,
                                    blocks + (size_t)dblk * kSubSize, dblk);
+    if (wide) {
+      wbase[t] = wblk;
+      wblk += (uint32_t)build_wide(c, S, wlut + (int64_t)t * kWideSize,
+                                   wblocks + (size_t)wblk * kSubSize, wblk);
+    }
     if (search) build_search(c, nsym, base, clut + (int64_t)t * kLutSize, starts);
     base += nsym;
   }
+  if (wide) wbase[M] = wblk;
   h->magic = kTabMagic;
   h->M = (uint32_t)M;
   h->total_syms = (uint32_t)total;
@@ -349,12 +397,16 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
   h->total_dense = (uint32_t)total_dense;
   h->clut_off = (uint32_t)BL.clut_off;
   h->starts_off = (uint32_t)BL.starts_off;
+  h->wide_off = (uint32_t)BL.wide_off;
+  h->wdense_off = (uint32_t)BL.wdense_off;
+  h->wbase_off = (uint32_t)BL.wbase_off;
+  h->total_wide = (uint32_t)total_wide;
   bool safe = true;
   for (int32_t t = 0; t < M; ++t) safe &= offsets[t] <= INT32_MAX - 65535;
-  h->flags = (safe ? kTabOffsetsSafe : 0u) | (search ? kTabSearch : 0u);
+  h->flags = (safe ? kTabOffsetsSafe : 0u) | (search ? kTabSearch : 0u) | (wide ? kTabWide : 0u);
   desc->dev = nullptr;
   desc->bytes = need;
-  desc->flags = search ? GAANS_TABLES_SEARCH : 0;
+  desc->flags = (search ? GAANS_TABLES_SEARCH : 0) | (wide ? GAANS_TABLES_WIDE : 0);
   desc->M = M;
   desc->max_nsym = (int32_t)max_nsym;
   desc->total_nsym = total;
@@ -362,7 +414,8 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
   desc->max_dense = max_dense;
   desc->total_dense = total_dense;
   desc->mean_bits = (float)(bits / M);
-  desc->reserved = 0;
+  desc->max_wide = max_wide;
+  desc->total_wide = total_wide;
   return GAANS_OK;
 }
 

@@ -67,20 +67,69 @@ constexpr int kMappers = GAANS_MAPPERS;  // mapper waves per decode workgroup
 // CU 8 cost more than they bring)
 constexpr int kEncMaxWaves = 9;
 
-// per-wave hash, status and escape nibbles, then the escape count
-constexpr int kPartBytes = (12 * kEncMaxWaves + 4 + 15) / 16 * 16;
+// per-wave hash, status and escape nibbles, then the escape count, the unit's
+// word count and the completion counter's value
+constexpr int kPartBytes = (12 * kEncMaxWaves + 12 + 15) / 16 * 16;
 constexpr int kRingWords = 4096;       // encoder LDS output ring (u16 words)
 constexpr int kPfU32Max = 8;  // decoder stream prefetch: u32 per lane (16-step blocks)
 // word 3 of a raw buffer resource on gfx9 (32-bit data format; stride 0, so
 // num_records counts bytes)
 constexpr int kBufferFlags = 0x00020000;
 constexpr int kMaxDevices = 64;
+
+// Phase timestamps (measurement only; a library built with
+// GAANS_PHASE_TIMES, see gaans_debug_phases).  The coder wave takes the
+// constant-rate real-time counter (slots 0-11) or the shader clock (slots
+// 12-15) into scalar registers at each point, and thread 0 stores its unit's
+// slots once, after the unit's counter atomic, so the points add no vector
+// registers to the coding loop.  In the default build every call is empty.
+struct PhaseBuf {
+  uint64_t* __restrict__ p;
+  int64_t units;  // units that have slots
+};
+struct PhaseClock {
+#ifdef GAANS_PHASE_TIMES
+  uint64_t t[8] = {}, c12 = 0, c13 = 0;
+  __device__ __forceinline__ void mark(int i) { t[i] = __builtin_amdgcn_s_memrealtime(); }
+  __device__ __forceinline__ void cycles(int i) {
+    (i == 12 ? c12 : c13) = __builtin_amdgcn_s_memtime();
+  }
+  static constexpr int kPhaseSlots = GAANS_PHASE_SLOTS;
+  // slots [lo, hi) of t (and, with lo == 0, the two shader-clock slots)
+  __device__ __forceinline__ void store(const PhaseBuf& b, int64_t g, int lo, int hi) const {
+    if (b.p != nullptr && g < b.units) {
+      uint64_t* d = b.p + g * kPhaseSlots;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (i >= lo && i < hi) d[i] = t[i];
+      if (lo == 0) {
+        d[12] = c12;
+        d[13] = c13;
+      }
+    }
+  }
+  // thread 0 of the last unit: the completion word is out
+  __device__ __forceinline__ void store_done(const PhaseBuf& b, int64_t g) const {
+    if (b.p != nullptr && g < b.units) b.p[g * kPhaseSlots + 7] = __builtin_amdgcn_s_memrealtime();
+  }
+  // after an atomic whose return marks the point: wait for it first
+  __device__ __forceinline__ void mark_after_loads(int i) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    mark(i);
+  }
+#else
+  __device__ __forceinline__ void mark(int) {}
+  __device__ __forceinline__ void cycles(int) {}
+  __device__ __forceinline__ void store(const PhaseBuf&, int64_t, int, int) const {}
+  __device__ __forceinline__ void store_done(const PhaseBuf&, int64_t) const {}
+  __device__ __forceinline__ void mark_after_loads(int) {}
+#endif
+};
+
 // control block (u32 words); encoder and decoder fields on separate 64-byte lines
 constexpr int kCtrlEncDone = 0;
 constexpr int kCtrlDecDone = 16;
 constexpr int kCtrlDecStatus = 17;
-
-
 
 // ---- wave helpers -----------------------------------------------------------
 
@@ -119,6 +168,7 @@ __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlan
 // without first reading the blob header.
 struct BlobRef {
   uint32_t meta_off, ent_off, lut_off, dense_off, total_dense, clut_off, starts_off;
+  uint32_t wide_off, wdense_off, wbase_off, total_wide;
 };
 
 // The blob header matches the call: magic, table count, size, lookup width
@@ -130,7 +180,9 @@ __device__ __forceinline__ bool tables_ok(const TabHdr& h, uint32_t M, uint32_t 
          (h.lut_bits == (uint32_t)kLutBits) & (h.meta_off == r.meta_off) &
          (h.ent_off == r.ent_off) & (h.lut_off == r.lut_off) & (h.dense_off == r.dense_off) &
          (h.total_dense == r.total_dense) & (h.clut_off == r.clut_off) &
-         (h.starts_off == r.starts_off);
+         (h.starts_off == r.starts_off) & (h.wide_off == r.wide_off) &
+         (h.wdense_off == r.wdense_off) & (h.wbase_off == r.wbase_off) &
+         (h.total_wide == r.total_wide);
 }
 
 // Blob header in registers (one 64-byte scalar load).
@@ -145,7 +197,7 @@ struct Tabs {
   const uint64_t* __restrict__ gsub;
   const uint4* lmeta;      // {ent_base (LDS-local), nsym, offset, ent_base (global)}
   const uint2* lent;       // encoder: both entry words
-  const uint64_t* llut;    // decoder: nt x 256 lookup entries
+  const uint64_t* llut;    // decoder: nt x 256 (wide: nt x kWideSize) lookup entries
   const uint64_t* lsub;    // decoder: sub-blocks of the staged tables
   const uint32_t* lclut;   // decoder, search lookups: bucket entries of all tables
   const uint16_t* lstarts; // decoder, search lookups: symbol starts of all tables
@@ -239,7 +291,20 @@ __device__ __forceinline__ StageBounds stage_bounds(const TabMeta* __restrict__ 
   return b;
 }
 
-template <int NT>
+// Wide-lookup sub-block range of the staged tables [t_lo, t_hi) from the
+// blob's per-table bases (M + 1 of them, so t_hi = M is in range).
+__device__ __forceinline__ StageBounds stage_bounds_wide(const uint32_t* __restrict__ wbase,
+                                                         int t_lo, int t_hi) {
+  StageBounds b;
+  b.base0 = 0u;
+  b.ent_end = 0u;
+  b.d0 = wbase[t_lo];
+  b.d1 = wbase[t_hi];
+  return b;
+}
+
+// LB: lookup entries per table (kLutSize, or kWideSize for the wide lookups)
+template <int NT, int LB = kLutSize>
 __device__ void stage_tables(Tabs& T, uint4* lmeta, uint2* lent, uint64_t* llut, uint64_t* lsub,
                              const StageBounds& bd, int t_lo, int t_hi, int tid) {
   T.t_lo = t_lo;
@@ -253,8 +318,8 @@ __device__ void stage_tables(Tabs& T, uint4* lmeta, uint2* lent, uint64_t* llut,
       const uint32_t ne = bd.ent_end - base0;
       stage_pass<NT, true, false>(T, lmeta, lent, nullptr, nullptr, nt, ne, 0u, base0, t_lo, tid);
     } else {
-      const uint4* lut_src = reinterpret_cast<const uint4*>(T.glut + (int64_t)t_lo * kLutSize);
-      copy16<NT, 4>(reinterpret_cast<uint4*>(llut), lut_src, nt * (kLutSize / 2), tid);
+      const uint4* lut_src = reinterpret_cast<const uint4*>(T.glut + (int64_t)t_lo * LB);
+      copy16<NT, 4>(reinterpret_cast<uint4*>(llut), lut_src, nt * (LB / 2), tid);
       const uint32_t d0 = bd.d0;
       const uint32_t d1 = bd.d1;
       if (lsub && d1 > d0) {
@@ -383,6 +448,7 @@ struct EncArgs {
   uint32_t* __restrict__ esc_raw;   // per unit: seg_cap slots, filled from the end
   uint32_t* __restrict__ ctrl;
   uint64_t* __restrict__ info_out;
+  PhaseBuf phase;
 };
 
 // Encoder LDS layout (bytes)
@@ -718,6 +784,8 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & (kLanes - 1);
   const int wid = uni(tid >> 6);  // wave role, kept in a scalar register
+  PhaseClock pc;
+  if (wid == 0) pc.mark(0);
   int64_t row;
   int32_t start;
   int len, k;
@@ -734,60 +802,66 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
   uint32_t* __restrict__ esc_list = a.esc_raw + g * a.seg_cap + a.seg_cap;
 
   if (tid < 2) eflag[tid] = 0u;  // visible after the staging barrier
+  int t_lo, t_hi;
+  stage_range(a.nt_cap, a.stage_all, k, a.P, (int)a.M, t_lo, t_hi);
+  const TabMeta* __restrict__ gmeta = reinterpret_cast<const TabMeta*>(a.tables + a.blob.meta_off);
+  // the table blob's header and the staged range's metadata in one round
+  // trip (the metadata lies in the blob whatever its content and is used
+  // only when the header check passes)
   const TabHdr th = load_tab_hdr(a.tables);
+  const StageBounds bd = stage_bounds(gmeta, t_lo, t_hi, a.M, a.blob.total_dense);
+  __builtin_amdgcn_sched_barrier(0);
+  Tabs tb;
+  tb.gmeta = gmeta;
+  tb.gent = reinterpret_cast<const uint2*>(a.tables + a.blob.ent_off);
+  tb.glut = nullptr;
+  tb.gsub = nullptr;
+  tb.lmeta = lmeta;
+  tb.lent = lent;
+  tb.llut = nullptr;
+  tb.lsub = nullptr;
+  // mapper wave w (1..kEncMappers) owns steps u = w - 1 + kEncMappers e of every block
+  // (steps a wave does not own keep these zeros)
+  int32_t ca[kPer] = {}, cb[kPer] = {}, na[kPer] = {}, nb[kPer] = {};
+  float cm[kPer] = {}, nm[kPer] = {};
+  auto load_block = [&](int j, int32_t* ia, int32_t* ib, float* im) {
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      const int u = (wid - 1) + kEncMappers * e;
+      if (SB % kEncMappers != 0 && u >= SB) break;
+      int p = lane + kLanes * (j * SB + u);
+      p = p < len ? p : len - 1;  // loads stay in the chunk; results are masked
+      const int64_t i = row + start + p;
+      if (kMode == kModeGaussian) {
+        ia[e] = __float_as_int(a.y[i]);
+        im[e] = a.means ? a.means[i] : 0.0f;
+        ib[e] = __float_as_int(a.scales[i]);  // the index is found when the block is mapped
+      } else {
+        if (kMode == kModeLatents) {
+          ia[e] = __float_as_int(a.y[i]);
+          im[e] = a.medians[udiv((uint32_t)(start + p), a.div_hw)];
+        } else {
+          ia[e] = a.symbols[i];
+          im[e] = 0.0f;
+        }
+        ib[e] = kImplicit ? 0 : a.indexes[i];
+      }
+    }
+  };
+  // the mappers' first two blocks of inputs need neither the table check nor
+  // the tables: they are in flight while the tables are staged
+  if (wid != 0 && nblk > 0) {
+    load_block(nblk - 1, ca, cb, cm);
+    if (nblk > 1) load_block(nblk - 2, na, nb, nm);
+  }
+  if (wid == 0) pc.mark_after_loads(1);  // table header and metadata are in
   const bool tab = tables_ok(th, a.M, a.tables_bytes, a.blob);  // uniform
   const bool offsets_safe = (th.flags & kTabOffsetsSafe) != 0;
   if (!tab) status |= GAANS_ST_TABLES;
   if (tab) {
-    Tabs tb;
-    tb.gmeta = reinterpret_cast<const TabMeta*>(a.tables + a.blob.meta_off);
-    tb.gent = reinterpret_cast<const uint2*>(a.tables + a.blob.ent_off);
-    tb.glut = nullptr;
-    tb.gsub = nullptr;
-    tb.lmeta = lmeta;
-    tb.lent = lent;
-    tb.llut = nullptr;
-    tb.lsub = nullptr;
-    // mapper wave w (1..kEncMappers) owns steps u = w - 1 + kEncMappers e of every block
-    // (steps a wave does not own keep these zeros)
-    int32_t ca[kPer] = {}, cb[kPer] = {}, na[kPer] = {}, nb[kPer] = {};
-    float cm[kPer] = {}, nm[kPer] = {};
-    auto load_block = [&](int j, int32_t* ia, int32_t* ib, float* im) {
-#pragma unroll
-      for (int e = 0; e < kPer; ++e) {
-        const int u = (wid - 1) + kEncMappers * e;
-        if (SB % kEncMappers != 0 && u >= SB) break;
-        int p = lane + kLanes * (j * SB + u);
-        p = p < len ? p : len - 1;  // loads stay in the chunk; results are masked
-        const int64_t i = row + start + p;
-        if (kMode == kModeGaussian) {
-          ia[e] = __float_as_int(a.y[i]);
-          im[e] = a.means ? a.means[i] : 0.0f;
-          ib[e] = __float_as_int(a.scales[i]);  // the index is found when the block is mapped
-        } else {
-          if (kMode == kModeLatents) {
-            ia[e] = __float_as_int(a.y[i]);
-            im[e] = a.medians[udiv((uint32_t)(start + p), a.div_hw)];
-          } else {
-            ia[e] = a.symbols[i];
-            im[e] = 0.0f;
-          }
-          ib[e] = kImplicit ? 0 : a.indexes[i];
-        }
-      }
-    };
-    // the mappers' first two blocks of inputs need no tables: their loads
-    // are in flight while the tables are staged
-    if (wid != 0 && nblk > 0) {
-      load_block(nblk - 1, ca, cb, cm);
-      if (nblk > 1) load_block(nblk - 2, na, nb, nm);
-    }
-    int t_lo, t_hi;
-    stage_range(a.nt_cap, a.stage_all, k, a.P, (int)a.M, t_lo, t_hi);
     if (kMode == kModeGaussian) stage_scales<kThreads>(scl, a.scale_table, a.n_scales, tid);
-    stage_tables<kThreads>(tb, lmeta, lent, nullptr, nullptr,
-                           stage_bounds(tb.gmeta, t_lo, t_hi, a.M, a.blob.total_dense), t_lo,
-                           t_hi, tid);
+    stage_tables<kThreads>(tb, lmeta, lent, nullptr, nullptr, bd, t_lo, t_hi, tid);
+    if (wid == 0) pc.mark(2);
 
     // this wave's steps per block: u = wid - 1 + kEncMappers e < SB
     const int nvalid = SB % kEncMappers == 0 ? kPer : (SB - wid + kEncMappers) / kEncMappers;
@@ -844,6 +918,8 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
     // loads in flight out of the coder's wait bookkeeping.
     if (wid == 0) {
       __syncthreads();
+      pc.mark(3);
+      pc.cycles(12);
       for (int j = nblk - 1; j >= 0; --j) {
         // coder: steps of block j, last to first
         if (fl - wp > kRingWords - SB * kLanes) {
@@ -887,6 +963,8 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
         }
         __syncthreads();
       }
+      pc.cycles(13);
+      pc.mark(4);
       if (fl > wp) ring_flush(wbuf, ring, wp, fl, lane);
     } else {
       if (nblk > 0) map_block(nblk - 1);
@@ -917,10 +995,17 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
     part[wid] = hash;
     part[kWaves + wid] = status;
     part[2 * kWaves + wid] = znib;
-    if (wid == 0) part[3 * kWaves] = (uint32_t)n_esc;
+    if (wid == 0) {
+      part[3 * kWaves] = (uint32_t)n_esc;
+      part[3 * kWaves + 1] = (uint32_t)(a.cap_words - wp);
+    }
   }
   __syncthreads();
-  if (tid == 0) {
+  // The unit's counts are published by the first mapper wave, which has no
+  // stores in flight, so that its wait for them does not also wait for the
+  // coder wave's flush of the words and states (read by the pack kernel,
+  // after this kernel has ended).
+  if (tid == kLanes) {
     uint32_t hs = 0, ss = 0, zs = 0;
     for (int w = 0; w < kWaves; ++w) {
       hs += part[w];
@@ -933,18 +1018,24 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
     // is stored with agent-scope atomics, which are coherent across the
     // device, and has completed before the counter is raised: no fence, so
     // no write-back of the XCD's whole L2.
-    __hip_atomic_store(&a.chunk_words[g], (uint32_t)(a.cap_words - wp), __ATOMIC_RELAXED,
+    __hip_atomic_store(&a.chunk_words[g], part[3 * kWaves + 1], __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(&a.chunk_status[g], ss, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(&a.esc[g].y, zs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    part[0] = __hip_atomic_fetch_add(&a.ctrl[kCtrlEncDone], 1u, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
+    pc.mark(5);
+    const uint32_t done = __hip_atomic_fetch_add(&a.ctrl[kCtrlEncDone], 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    pc.mark_after_loads(6);  // the atomic returned
+    pc.store(a.phase, g, 5, 7);
+    part[3 * kWaves + 2] = done;
   }
+  if (tid == 0) pc.store(a.phase, g, 0, 5);  // the coder wave's points
   __syncthreads();
-  if (part[0] == (uint32_t)(a.units - 1)) {  // uniform: the last workgroup to finish
-    __syncthreads();  // every wave has read part[0] before it is reused
+  if (part[3 * kWaves + 2] == (uint32_t)(a.units - 1)) {  // uniform: the last workgroup
+    __syncthreads();  // every wave has read the counter before part is reused
     encode_finish<kThreads>(a, tid, reinterpret_cast<uint64_t*>(part));
+    if (tid == 0) pc.store_done(a.phase, g);
   }
 }
 
@@ -1105,6 +1196,7 @@ struct DecArgs {
   uint32_t starts_words;  // search lookups: 16-byte words of starts to stage
   uint32_t* __restrict__ ctrl;
   uint32_t* __restrict__ status_out;
+  PhaseBuf phase;
 };
 
 // Decoder geometry for blocks of SB steps (the mappers' lead over the coder
@@ -1225,20 +1317,27 @@ __device__ __forceinline__ bool dense_entry(uint64_t e) { return (uint32_t)(e >>
 // cum -> (symbol, start, freq) in table t: the table's lookup entry of
 // bucket cum >> 8, for a dense bucket the entry of sub-range (cum >> 4) & 15
 // of its sub-block, for a dense sub-range the exact entry of value cum & 15
-// (see the blob layout).
-template <bool kLds>
+// (see the blob layout).  kWide: the wide lookups, bucket cum >> 5 and, for
+// a dense bucket, sub-range (cum >> 1) & 15 of its sub-block.
+template <bool kLds, bool kWide = false>
 __device__ __forceinline__ void dec_lookup(const Tabs& tb, uint32_t t, uint32_t cum, bool act,
                                            uint32_t& s, uint32_t& st, uint32_t& fr) {
-  const uint32_t li = (t << kLutBits) + (cum >> (16 - kLutBits));
+  constexpr int kB = kWide ? kWideBits : kLutBits;
+  const uint32_t li = (t << kB) + (cum >> (16 - kB));
   uint64_t e = kLds ? tb.llut[li] : tb.glut[li];
   // the dense tests first: their scalar results are ready by the branches
   const uint64_t dm = ballot(act & dense_entry(e));
   asm volatile("" ::"s"(dm));
   if (__builtin_expect(dm != 0ull, 0)) {
-    if (act & dense_entry(e)) e = sub_entry<kLds>(tb, e, (cum >> kSubBits) & (kSubSize - 1));
-    const uint64_t dm3 = ballot(act & dense_entry(e));
-    if (__builtin_expect(dm3 != 0ull, 0) && (act & dense_entry(e)))
-      e = sub_entry<kLds>(tb, e, cum & (kSubSize - 1));
+    if constexpr (kWide) {
+      // a wide bucket's sub-ranges (two values) are never dense
+      if (act & dense_entry(e)) e = sub_entry<kLds>(tb, e, (cum >> kWideSubShift) & (kSubSize - 1));
+    } else {
+      if (act & dense_entry(e)) e = sub_entry<kLds>(tb, e, (cum >> kSubBits) & (kSubSize - 1));
+      const uint64_t dm3 = ballot(act & dense_entry(e));
+      if (__builtin_expect(dm3 != 0ull, 0) && (act & dense_entry(e)))
+        e = sub_entry<kLds>(tb, e, cum & (kSubSize - 1));
+    }
   }
   // the compare reads the entry directly; the rest runs beside it
   const uint32_t lo = (uint32_t)e, hi = (uint32_t)(e >> 32);
@@ -1407,17 +1506,26 @@ __device__ __forceinline__ void dec_refill(bool need, uint32_t& x, Stream& S, co
 // to the FIFO in one store.
 struct EscReader {
   const uint32_t* __restrict__ w32;   // the chunk's words after the states
-  const uint32_t* __restrict__ safe;  // an in-bounds word of the chunk
   int n32, base;
   uint32_t q, p;     // nibbles and entries parsed
   bool stopped;
   uint32_t w0, w1;   // window
 };
 
-// Escape u32 m (zero past the chunk's words).
+// Escape u32 m (zero past the chunk's words).  A buffer load over the
+// chunk's n32 words (wave-uniform base and size in scalar registers): for m
+// >= n32 the byte offset 4 (n32 - 1 - m) wraps past the buffer's size and
+// the load returns 0, so no branch goes around the load (a branch made each
+// load wait for its data before the next one was issued).
 __device__ __forceinline__ uint32_t esc_word(const EscReader& E, int m) {
-  const uint32_t v = *(m < E.n32 ? E.w32 + (E.n32 - 1 - m) : E.safe);
-  return m < E.n32 ? ((v >> 16) | (v << 16)) : 0u;
+  const uint64_t base = reinterpret_cast<uint64_t>(E.w32);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(base >> 32));
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), 0, 4 * uni(E.n32), kBufferFlags);
+  const uint32_t v =
+      __builtin_amdgcn_raw_buffer_load_b32(r, (int)(4u * (uint32_t)(E.n32 - 1 - m)), 0, 0);
+  return (v >> 16) | (v << 16);
 }
 
 // Escape u32 base + i of the window for lane-varying i in [0, 128).
@@ -1496,7 +1604,7 @@ __device__ __forceinline__ void esc_resolve(uint64_t em, uint32_t base, uint32_t
 // the lanes that decoded the escape bin (their values are resolved by the
 // mappers, off the state chain).  kFull: every lane is active and no offset
 // can overflow with a symbol index.
-template <bool kLds, bool kFull, int SB, bool kSearch = false>
+template <bool kLds, bool kFull, int SB, bool kSearch = false, bool kWide = false>
 __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint2 r, uint32_t& x,
                                              Stream& S, const uint16_t* ring, uint64_t& em,
                                              uint32_t& status, int lane) {
@@ -1505,7 +1613,7 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint2 r, uint
   const uint32_t cum = x & 0xffffu;
   uint32_t s, st, fr;
   if constexpr (kSearch) dec_lookup_search(tb, r.x & 0xffffu, cum, act, s, st, fr);
-  else dec_lookup<kLds>(tb, r.x & 0xffffu, cum, act, s, st, fr);
+  else dec_lookup<kLds, kWide>(tb, r.x & 0xffffu, cum, act, s, st, fr);
   const uint32_t xn = __umul24(fr, x >> 16) + cum - st;
   x = act ? xn : x;
   dec_refill<SB>(act & (x < kStateLow), x, S, ring, lane);
@@ -1519,8 +1627,18 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint2 r, uint
   return (uint32_t)(oob ? 0 : o);
 }
 
-template <int kMode, bool kImplicit, int SB, bool kSearch>
-__global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
+// Waves per SIMD the decoder is built for: 6 (see the LDS plan); the
+// measurement build allows 5, since its phase points would otherwise push
+// the 16-step kernels past the 80 registers of 6 waves into scratch (its
+// phase times at three workgroups per CU are therefore approximate).
+#ifdef GAANS_PHASE_TIMES
+constexpr int kDecWavesPerSimd = 5;
+#else
+constexpr int kDecWavesPerSimd = 6;
+#endif
+
+template <int kMode, bool kImplicit, int SB, bool kSearch, bool kWide>
+__global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArgs a) {
   constexpr bool kLatents = kMode != kModeSymbols;  // fp32 output with a per-element add
   using G = DecGeom<SB>;
   constexpr int kPer = G::kPer;
@@ -1538,11 +1656,13 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   uint8_t* tsm = smem + G::fixed(kLatents);
   // [luts][meta][sub-blocks], or with the search lookups [bucket entries]
   // [meta][starts]: every part 16-byte aligned
+  static_assert(!(kSearch && kWide), "the search lookups have no wide form");
   constexpr int kLutEntry = kSearch ? 4 : 8;
+  constexpr int kLB = kWide ? kWideSize : kLutSize;  // lookup entries per staged table
   uint64_t* llut = reinterpret_cast<uint64_t*>(tsm);
   uint32_t* lclut = reinterpret_cast<uint32_t*>(tsm);
-  uint4* lmeta = reinterpret_cast<uint4*>(tsm + kLutEntry * kLutSize * a.nt_cap);
-  uint64_t* lsub = reinterpret_cast<uint64_t*>(tsm + (kLutEntry * kLutSize + 16) * a.nt_cap);
+  uint4* lmeta = reinterpret_cast<uint4*>(tsm + kLutEntry * kLB * a.nt_cap);
+  uint64_t* lsub = reinterpret_cast<uint64_t*>(tsm + (kLutEntry * kLB + 16) * a.nt_cap);
   uint16_t* lstarts = reinterpret_cast<uint16_t*>(lsub);
   float* scl = reinterpret_cast<float*>(smem + a.scales_lds);  // Gaussian: scale table
 
@@ -1550,13 +1670,28 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & (kLanes - 1);
   const int wid = uni(tid >> 6);  // wave role, kept in a scalar register
+  PhaseClock pc;
+  if (wid == 0) pc.mark(0);
   uint32_t status = 0, hash = 0, enib = 0;
   const uint32_t* __restrict__ hdr = reinterpret_cast<const uint32_t*>(a.payload);
-  // Header words, the unit's end offsets and index hash, and the table
-  // blob's header, all in one round trip: every word is read (the host has
-  // checked that the payload holds the header), the loads are issued before
-  // any of them is used (the scheduling barrier keeps them together), and
-  // the checks are branch-free.
+  int64_t row;
+  int32_t start;
+  int len, k;
+  unit_range(g, (int32_t)a.K, (int32_t)a.S, a.N, (int32_t)a.chunk_len, row, start, len, k);
+  const int T = (len + kLanes - 1) / kLanes;
+  const int A = len < kLanes ? len : kLanes;
+  const int nst = A;  // final states
+  const int nblk = (T + SB - 1) / SB;
+  int t_lo, t_hi;
+  stage_range(a.nt_cap, a.stage_all, k, (int)a.P, (int)a.M, t_lo, t_hi);
+  const TabMeta* __restrict__ gmeta = reinterpret_cast<const TabMeta*>(a.tables + a.blob.meta_off);
+  // Header words, the unit's end offsets and index hash, the table blob's
+  // header and the staged range's metadata, all in one round trip: every
+  // word is read (the host has checked that the payload holds the header;
+  // the metadata lies in the blob whatever its content and is used only
+  // when the checks pass), the loads are issued before any of them is used
+  // (the scheduling barrier keeps them together), and the checks are
+  // branch-free.
   const TabHdr th = load_tab_hdr(a.tables);
   uint32_t hw[13];
 #pragma unroll
@@ -1566,8 +1701,52 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   const uint32_t* pe = hdr + (kFixedWords - 1) + g;
   const uint32_t e_prev = pe[0];
   const uint32_t e_end = pe[1];
+  const StageBounds bd =
+      kSearch ? StageBounds{0u, 0u, 0u, 0u}
+              : (kWide ? stage_bounds_wide(reinterpret_cast<const uint32_t*>(a.tables +
+                                                                             a.blob.wbase_off),
+                                           t_lo, t_hi)
+                       : stage_bounds(gmeta, t_lo, t_hi, a.M, a.blob.total_dense));
   __builtin_amdgcn_sched_barrier(0);
   const uint32_t e_hash = hdr[kFixedWords + a.units + g];  // needed at the end only
+  Tabs tb;
+  tb.gmeta = gmeta;
+  tb.gent = reinterpret_cast<const uint2*>(a.tables + a.blob.ent_off);
+  tb.glut = reinterpret_cast<const uint64_t*>(a.tables +
+                                              (kWide ? a.blob.wide_off : a.blob.lut_off));
+  tb.gsub = reinterpret_cast<const uint64_t*>(a.tables +
+                                              (kWide ? a.blob.wdense_off : a.blob.dense_off));
+  tb.lmeta = lmeta;
+  tb.lent = nullptr;
+  tb.llut = llut;
+  tb.lsub = lsub;
+  tb.lclut = lclut;
+  tb.lstarts = lstarts;
+  int32_t cbx[kPer], nbx[kPer];
+  float cm[kPer], nm[kPer];
+  auto load_block = [&](int j, int32_t* ib, float* im) {
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      const int u = (wid - 1) + kMappers * e;
+      if (SB % kMappers != 0 && u >= SB) break;
+      int p = lane + kLanes * (j * SB + u);
+      p = p < len ? p : len - 1;  // loads stay in the chunk; results are masked
+      if (kMode == kModeGaussian) {
+        ib[e] = __float_as_int(a.scales[row + start + p]);  // index found at map time
+        im[e] = a.means ? a.means[row + start + p] : 0.0f;
+      } else {
+        ib[e] = kImplicit ? 0 : a.indexes[row + start + p];
+        im[e] = kLatents ? a.medians[udiv((uint32_t)(start + p), a.div_hw)] : 0.0f;
+      }
+    }
+  };
+  // the mappers' first two blocks of inputs need neither the header checks
+  // nor the tables
+  if (wid != 0 && wid != kEscWave && nblk > 0) {
+    load_block(0, cbx, cm);
+    if (nblk > 1) load_block(1, nbx, nm);
+  }
+  if (wid == 0) pc.mark_after_loads(1);  // header, offsets and metadata are in
   const bool hdr_ok = (hw[0] == kMagic) & (hw[1] == kVersion) & (hw[2] == a.B) &
                       (hw[3] == (uint32_t)a.N) & (hw[4] == a.C) & (hw[5] == a.P) &
                       (hw[6] == a.K) & (hw[7] == a.chunk_len) & (hw[8] == a.M) &
@@ -1577,14 +1756,6 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   const bool offsets_safe = (th.flags & kTabOffsetsSafe) != 0;
   bool ok = hdr_ok & tab_ok;  // uniform over the workgroup
   status |= !hdr_ok ? GAANS_ST_HEADER : (!tab_ok ? GAANS_ST_TABLES : 0u);
-  int64_t row;
-  int32_t start;
-  int len, k;
-  unit_range(g, (int32_t)a.K, (int32_t)a.S, a.N, (int32_t)a.chunk_len, row, start, len, k);
-  const int T = (len + kLanes - 1) / kLanes;
-  const int A = len < kLanes ? len : kLanes;
-  const int nst = A;  // final states
-  const int nblk = (T + SB - 1) / SB;
   // the unit's bytes: the offsets are used unconditionally, so that their
   // loads are not moved behind the header checks
   const uint32_t beg = g ? e_prev : 0u;
@@ -1599,40 +1770,11 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
   S.rp = 0;
   S.q = 0;
   if (ok) {
-    Tabs tb;
-    tb.gmeta = reinterpret_cast<const TabMeta*>(a.tables + a.blob.meta_off);
-    tb.gent = reinterpret_cast<const uint2*>(a.tables + a.blob.ent_off);
-    tb.glut = reinterpret_cast<const uint64_t*>(a.tables + a.blob.lut_off);
-    tb.gsub = reinterpret_cast<const uint64_t*>(a.tables + a.blob.dense_off);
-    tb.lmeta = lmeta;
-    tb.lent = nullptr;
-    tb.llut = llut;
-    tb.lsub = lsub;
-    tb.lclut = lclut;
-    tb.lstarts = lstarts;
     const uint8_t* cdata = a.payload + a.header_bytes + beg;
     const uint32_t* s32 = reinterpret_cast<const uint32_t*>(cdata + 4 * nst);
     const uint32_t* safe = reinterpret_cast<const uint32_t*>(cdata);
     const int q16 = (int)((cb - 4 * nst) / 2);  // u16 words after the states (even)
 
-    int32_t cbx[kPer], nbx[kPer];
-    float cm[kPer], nm[kPer];
-    auto load_block = [&](int j, int32_t* ib, float* im) {
-#pragma unroll
-      for (int e = 0; e < kPer; ++e) {
-        const int u = (wid - 1) + kMappers * e;
-        if (SB % kMappers != 0 && u >= SB) break;
-        int p = lane + kLanes * (j * SB + u);
-        p = p < len ? p : len - 1;  // loads stay in the chunk; results are masked
-        if (kMode == kModeGaussian) {
-          ib[e] = __float_as_int(a.scales[row + start + p]);  // index found at map time
-          im[e] = a.means ? a.means[row + start + p] : 0.0f;
-        } else {
-          ib[e] = kImplicit ? 0 : a.indexes[row + start + p];
-          im[e] = kLatents ? a.medians[udiv((uint32_t)(start + p), a.div_hw)] : 0.0f;
-        }
-      }
-    };
     // decoded values of block j -> HBM, escapes resolved first
     auto store_block = [&](int j) {
       const uint2* src = recs + (j & 1) * SB * kLanes;
@@ -1715,7 +1857,6 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
         S.pf[kk] = stream_word32(S, G::kPre * (G::kPfWords / 2) + kk * kLanes);
     } else if (wid == kEscWave) {
       E.w32 = s32;
-      E.safe = safe;
       E.n32 = q16 / 2;
       E.base = 0;
       E.q = 0;
@@ -1723,23 +1864,18 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
       E.stopped = false;
       E.w0 = esc_word(E, lane);
       E.w1 = esc_word(E, kLanes + lane);
-    } else if (nblk > 0) {
-      load_block(0, cbx, cm);
-      if (nblk > 1) load_block(1, nbx, nm);
     }
     if (tid < 8) ctl[tid] = tid == 1 ? kAllAvail : 0u;
     if (kMode == kModeGaussian) stage_scales<kDecThreads>(scl, a.scale_table, a.n_scales, tid);
-    int t_lo, t_hi;
-    stage_range(a.nt_cap, a.stage_all, k, (int)a.P, (int)a.M, t_lo, t_hi);
     if constexpr (kSearch) {
       stage_search<kDecThreads>(tb, lmeta, lclut, lstarts, a.tables, a.blob, a.M,
                                 a.starts_words, tid);
     } else {
-      stage_tables<kDecThreads>(tb, lmeta, nullptr, llut, a.nd_cap ? lsub : nullptr,
-                                stage_bounds(tb.gmeta, t_lo, t_hi, a.M, a.blob.total_dense),
-                                t_lo, t_hi, tid);
+      stage_tables<kDecThreads, kLB>(tb, lmeta, nullptr, llut, a.nd_cap ? lsub : nullptr, bd,
+                                     t_lo, t_hi, tid);
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load crosses the role split
+    if (wid == 0) pc.mark(2);
 
     // The coder, the mappers and the escape reader run separate code (the
     // wave role is uniform per wave) that meets at the same barriers: one
@@ -1759,6 +1895,8 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
       // workgroup on the CU compete for the same SIMD.
       __builtin_amdgcn_s_setprio(3);
       __syncthreads();
+      pc.mark(3);
+      pc.cycles(12);
       for (int j = 0; j < nblk; ++j) {
         uint2* src = recs + (j & 1) * SB * kLanes;
         uint4* ei = escm + (j & 1) * SB;
@@ -1780,7 +1918,8 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
           uint64_t em[SB];
 #pragma unroll
           for (int u = 0; u < SB; ++u) {
-            ov[u] = dec_step<true, true, SB, kSearch>(tb, r[u], x, S, sring, em[u], status, lane);
+            ov[u] = dec_step<true, true, SB, kSearch, kWide>(tb, r[u], x, S, sring, em[u], status,
+                                                            lane);
             any_em |= em[u];
           }
           if (__builtin_expect(any_em != 0ull, 0)) {
@@ -1808,8 +1947,10 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
               v = dec_step<true, false, SB, true>(tb, ru, x, S, sring, em, status, lane);
             } else {
               v = ((nl >> u) & 1u) == 0u
-                      ? dec_step<true, false, SB>(tb, ru, x, S, sring, em, status, lane)
-                      : dec_step<false, false, SB>(tb, ru, x, S, sring, em, status, lane);
+                      ? dec_step<true, false, SB, false, kWide>(tb, ru, x, S, sring, em, status,
+                                                               lane)
+                      : dec_step<false, false, SB, false, kWide>(tb, ru, x, S, sring, em, status,
+                                                                lane);
             }
             if (lane == 0) ei[u] = make_uint4((uint32_t)em, (uint32_t)(em >> 32), ecur, 0u);
             ecur += (uint32_t)__popcll(em);
@@ -1824,6 +1965,8 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
         }
         __syncthreads();
       }
+      pc.cycles(13);
+      pc.mark(4);
       if (lane < A && x != kStateLow) status |= GAANS_ST_CORRUPT;
       __syncthreads();  // after the mappers' last store
     } else if (wid == kEscWave) {
@@ -1881,13 +2024,21 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
       if (S.rp + qe + pad != S.q) {
         st |= GAANS_ST_CORRUPT;
       } else {
+        // u16 word i of the stream: from the ring while it still holds it
+        // (the ring keeps the last kRing words committed, [filled - kRing,
+        // filled)), else from global memory
         const uint16_t* s16 = reinterpret_cast<const uint16_t*>(S.s32);
-        if (pad && s16[S.rp] != 0) st |= GAANS_ST_CORRUPT;
+        auto word16 = [&](int i) -> uint32_t {
+          if (i < S.filled && i >= S.filled - G::kRing) return sring[i & (G::kRing - 1)];
+          return s16[i];
+        };
+        if (pad && word16(S.rp) != 0) st |= GAANS_ST_CORRUPT;
         if (eq & 3u) {
           // escape u32 eq >> 3 holds the first unused nibble (in range: the
-          // words were consumed exactly)
-          const uint32_t v = S.s32[S.q32 - 1 - (int)(eq >> 3)];
-          const uint32_t last = ((v >> 16) | (v << 16)) >> (4u * (eq & 7u));
+          // words were consumed exactly); its halves are swapped in the stream
+          const int m = S.q32 - 1 - (int)(eq >> 3);
+          const uint32_t v = word16(2 * m + 1) | (word16(2 * m) << 16);
+          const uint32_t last = v >> (4u * (eq & 7u));
           if (last & ((1u << (4u * (4u - (eq & 3u)))) - 1u)) st |= GAANS_ST_CORRUPT;
         }
       }
@@ -1899,8 +2050,11 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
       __hip_atomic_fetch_or(&a.ctrl[kCtrlDecStatus], st, __ATOMIC_RELAXED,
                             __HIP_MEMORY_SCOPE_AGENT);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    pc.mark(5);
     const uint32_t done = __hip_atomic_fetch_add(&a.ctrl[kCtrlDecDone], 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
+    pc.mark_after_loads(6);  // the atomic returned
+    pc.store(a.phase, g, 0, 7);
     if (done == (uint32_t)(a.units - 1)) {
       const uint32_t all = __hip_atomic_exchange(&a.ctrl[kCtrlDecStatus], 0u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
@@ -1909,6 +2063,7 @@ __global__ __launch_bounds__(kDecThreads, 6) void k_decode(DecArgs a) {
       __hip_atomic_store(&a.status_out[1], 1u | (all << 1), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_SYSTEM);
       __hip_atomic_store(&a.ctrl[kCtrlDecDone], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pc.store_done(a.phase, g);
     }
   }
 }
@@ -2204,7 +2359,8 @@ int check_tables_arg(const gaans_tables* t) {
   if (t->bytes < (int64_t)sizeof(TabHdr) || t->bytes > 0xffffffffll)
     return fail(GAANS_EINVAL, "tables bytes %lld out of range", (long long)t->bytes);
   if (t->max_nsym < 1 || t->total_nsym < t->max_nsym || t->max_dense < 0 ||
-      t->total_dense < t->max_dense)
+      t->total_dense < t->max_dense || t->max_wide < 0 || t->total_wide < t->max_wide ||
+      t->total_wide > 0xffffffffll)
     return fail(GAANS_EINVAL, "tables descriptor is inconsistent");
   return GAANS_OK;
 }
@@ -2212,7 +2368,11 @@ int check_tables_arg(const gaans_tables* t) {
 // Section offsets of the blob a descriptor describes (the layout written by
 // gaans_tables_prepare); the descriptor's size must match them.
 int blob_ref(const gaans_tables* t, BlobRef* r) {
-  const BlobLayout L = blob_layout(t->M, t->total_nsym, t->total_dense);
+  const bool wide = (t->flags & GAANS_TABLES_WIDE) != 0;
+  if (wide != (t->M <= kWideMaxTables))
+    return fail(GAANS_EINVAL, "tables descriptor: wide lookups exist exactly for M <= %d",
+                kWideMaxTables);
+  const BlobLayout L = blob_layout(t->M, t->total_nsym, t->total_dense, wide, t->total_wide);
   if (L.end != t->bytes)
     return fail(GAANS_EINVAL, "tables descriptor does not describe a prepared blob (%lld bytes "
                 "for its counts, %lld given)", (long long)L.end, (long long)t->bytes);
@@ -2223,6 +2383,10 @@ int blob_ref(const gaans_tables* t, BlobRef* r) {
   r->total_dense = (uint32_t)t->total_dense;
   r->clut_off = (uint32_t)L.clut_off;
   r->starts_off = (uint32_t)L.starts_off;
+  r->wide_off = (uint32_t)L.wide_off;
+  r->wdense_off = (uint32_t)L.wdense_off;
+  r->wbase_off = (uint32_t)L.wbase_off;
+  r->total_wide = (uint32_t)t->total_wide;
   return GAANS_OK;
 }
 
@@ -2285,21 +2449,23 @@ int64_t occ_target(int64_t units, const DevLds& d, int64_t max_occ) {
 
 // Tables staged in `budget` bytes (per table, per symbol entry and per dense
 // block costs): false if not even the chunk's range fits.
+// wide: the sub-blocks are the wide lookups' (max_wide, total_wide).
 bool fit_stage(const gaans_tables* t, int64_t P, int64_t per_table, int64_t per_sym,
-               int64_t per_dense, int64_t budget, Stage* s, bool range_ok = true) {
-  const int64_t all = t->M * per_table + per_sym * t->total_nsym + per_dense * t->total_dense;
-  const int64_t range = P * (per_table + per_sym * (int64_t)t->max_nsym +
-                             per_dense * (int64_t)t->max_dense);
+               int64_t per_dense, int64_t budget, Stage* s, bool range_ok = true,
+               bool wide = false) {
+  const int64_t max_d = wide ? t->max_wide : t->max_dense;
+  const int64_t total_d = wide ? t->total_wide : t->total_dense;
+  const int64_t all = t->M * per_table + per_sym * t->total_nsym + per_dense * total_d;
+  const int64_t range = P * (per_table + per_sym * (int64_t)t->max_nsym + per_dense * max_d);
   // all tables when that is not much more to copy than the chunk's range
   // (or the range does not fit): explicit indexes may use any table
   if (all <= budget && (all <= 2 * range || range > budget)) {
-    *s = Stage{t->M, per_sym ? (int32_t)t->total_nsym : 0,
-               per_dense ? (int32_t)t->total_dense : 0, 1};
+    *s = Stage{t->M, per_sym ? (int32_t)t->total_nsym : 0, per_dense ? (int32_t)total_d : 0, 1};
     return true;
   }
   if (range_ok && range <= budget) {
     *s = Stage{(int32_t)P, per_sym ? (int32_t)(P * t->max_nsym) : 0,
-               per_dense ? (int32_t)(P * t->max_dense) : 0, 0};
+               per_dense ? (int32_t)(P * max_d) : 0, 0};
     return true;
   }
   return false;
@@ -2346,6 +2512,7 @@ struct DecPlan {
   size_t lds;
   bool search;            // the search lookups of every table
   uint32_t starts_words;  // search: 16-byte words of starts
+  bool wide;              // the wide lookups
 };
 
 // Search lookups in LDS: every table's bucket entries and metadata, and
@@ -2360,11 +2527,22 @@ DecPlan plan_decode(const gaans_tables* t, int64_t P, int64_t units, bool latent
                     const DevLds& d, int64_t extra = 0, bool range_ok = true,
                     bool search_ok = false) {
   const int64_t per_table = 8 * kLutSize + 16;
+  const int64_t per_wide = 8 * kWideSize + 16;
+  const bool wide_ok = (t->flags & GAANS_TABLES_WIDE) != 0;
   const bool has_dense = t->total_dense > 0;
   uint32_t starts_words = 0;
   const int64_t search_bytes = search_ok ? search_lds(t, &starts_words) : 0;
   for (int64_t occ = occ_target(units, d, 3); occ >= 1; --occ) {
     const int64_t cap = lds_budget(d, occ);
+    // the wide lookups with their sub-blocks, with 16- or 8-step blocks
+    for (int sb = 16; wide_ok && sb >= 8; sb >>= 1) {
+      const int64_t fixed = dec_fixed_lds(latents, sb);
+      Stage s;
+      if (fit_stage(t, P, per_wide, 0, kSubBytes, cap - fixed - extra, &s, range_ok, true))
+        return DecPlan{s, sb,
+                       (size_t)(fixed + per_wide * s.nt_cap + kSubBytes * (int64_t)s.nd_cap),
+                       false, 0, true};
+    }
     for (int opt = 0; opt < 9; ++opt) {
       const int sb = 16 >> (opt % 3);  // 16-, 8-, then 4-step blocks of each kind
       const int64_t fixed = dec_fixed_lds(latents, sb);
@@ -2372,7 +2550,7 @@ DecPlan plan_decode(const gaans_tables* t, int64_t P, int64_t units, bool latent
       if (opt >= 3 && opt < 6) {
         if (search_ok && fixed + search_bytes + extra <= cap)
           return DecPlan{Stage{(int32_t)t->M, 0, 0, 1}, sb, (size_t)(fixed + search_bytes), true,
-                         starts_words};
+                         starts_words, false};
         continue;
       }
       const bool dense = opt < 3;
@@ -2380,10 +2558,10 @@ DecPlan plan_decode(const gaans_tables* t, int64_t P, int64_t units, bool latent
       if (fit_stage(t, P, per_table, 0, dense ? kSubBytes : 0, cap - fixed - extra, &s, range_ok))
         return DecPlan{s, sb,
                        (size_t)(fixed + per_table * s.nt_cap + kSubBytes * (int64_t)s.nd_cap),
-                       false, 0};
+                       false, 0, false};
     }
   }
-  return DecPlan{Stage{0, 0, 0, 0}, 8, (size_t)dec_fixed_lds(latents, 8), false, 0};
+  return DecPlan{Stage{0, 0, 0, 0}, 8, (size_t)dec_fixed_lds(latents, 8), false, 0, false};
 }
 
 // Allow dynamic LDS above the default limit (once per kernel and device).
@@ -2467,20 +2645,40 @@ EncKernel enc_kernel(int mode, bool imp, int sb, int nm) {
   }
 }
 
-template <int kMode, bool kImp, bool kSearch>
+template <int kMode, bool kImp, bool kSearch, bool kWide = false>
 DecKernel dec_kernel_sb(int sb) {
-  return sb == 4 ? k_decode<kMode, kImp, 4, kSearch>
-                 : (sb == 8 ? k_decode<kMode, kImp, 8, kSearch> : k_decode<kMode, kImp, 16, kSearch>);
+  return sb == 4 ? k_decode<kMode, kImp, 4, kSearch, kWide>
+                 : (sb == 8 ? k_decode<kMode, kImp, 8, kSearch, kWide>
+                            : k_decode<kMode, kImp, 16, kSearch, kWide>);
 }
 
 // Decode kernel of a mode, index kind, block size and lookup kind (the
-// search lookups serve explicit or computed indexes only).
-DecKernel dec_kernel(int mode, bool imp, int sb, bool search) {
+// search lookups serve explicit or computed indexes only; the wide lookups
+// are staged with 8- or 16-step blocks only).
+DecKernel dec_kernel(int mode, bool imp, int sb, bool search, bool wide) {
   if (search) {
     switch (mode) {
       case kModeGaussian: return dec_kernel_sb<kModeGaussian, false, true>(sb);
       case kModeLatents: return dec_kernel_sb<kModeLatents, false, true>(sb);
       default: return dec_kernel_sb<kModeSymbols, false, true>(sb);
+    }
+  }
+  if (wide) {
+    const int w = sb == 8 ? 8 : 16;
+    switch (mode) {
+      case kModeGaussian:
+        return w == 8 ? k_decode<kModeGaussian, false, 8, false, true>
+                      : k_decode<kModeGaussian, false, 16, false, true>;
+      case kModeLatents:
+        return imp ? (w == 8 ? k_decode<kModeLatents, true, 8, false, true>
+                             : k_decode<kModeLatents, true, 16, false, true>)
+                   : (w == 8 ? k_decode<kModeLatents, false, 8, false, true>
+                             : k_decode<kModeLatents, false, 16, false, true>);
+      default:
+        return imp ? (w == 8 ? k_decode<kModeSymbols, true, 8, false, true>
+                             : k_decode<kModeSymbols, true, 16, false, true>)
+                   : (w == 8 ? k_decode<kModeSymbols, false, 8, false, true>
+                             : k_decode<kModeSymbols, false, 16, false, true>);
     }
   }
   switch (mode) {
@@ -2493,6 +2691,9 @@ DecKernel dec_kernel(int mode, bool imp, int sb, bool search) {
                  : dec_kernel_sb<kModeSymbols, false, false>(sb);
   }
 }
+
+// Phase buffer of later launches (gaans_debug_phases).
+PhaseBuf g_phase{nullptr, 0};
 
 // One encode launch: kernel, geometry and arguments.
 struct EncLaunch {
@@ -2605,6 +2806,7 @@ void encode_bind(int mode, EncArgs& a, const Layout& L, const int32_t* symbols, 
   a.esc_raw = reinterpret_cast<uint32_t*>(w + L.o_esc_raw);
   a.ctrl = static_cast<uint32_t*>(ctrl);
   a.info_out = info_out;
+  a.phase = g_phase;
 }
 
 int encode_launch(const EncLaunch& e, void* stream) {
@@ -2687,7 +2889,7 @@ int decode_prepare(int mode, bool implicit, int32_t n_scales, float scale_bound,
   a.nd_cap = st.nd_cap;
   a.stage_all = st.stage_all;
   a.starts_words = plan.starts_words;
-  e->kernel = dec_kernel(mode, implicit, plan.sb, plan.search);
+  e->kernel = dec_kernel(mode, implicit, plan.sb, plan.search, plan.wide);
   e->grid = (uint32_t)L.U;
   e->block = (uint32_t)kDecThreads;
   e->lds = lds;
@@ -2728,6 +2930,7 @@ void decode_bind(int mode, DecArgs& a, const uint8_t* payload, int64_t payload_b
   a.out_y = mode == kModeSymbols ? nullptr : static_cast<float*>(out);
   a.ctrl = static_cast<uint32_t*>(ctrl);
   a.status_out = status_out;
+  a.phase = g_phase;
 }
 
 int decode_launch(const DecLaunch& e, void* stream) {
@@ -3207,6 +3410,27 @@ int gaans_run_decode(const gaans_plan* plan, void* stream, const uint8_t* payloa
   __atomic_store_n(done, 0u, __ATOMIC_RELEASE);
   if ((rc = decode_launch(e, stream))) return rc;
   return wait_word(stream, done);
+}
+
+int gaans_debug_phases(void* buffer_dev, int64_t units, int32_t* wall_clock_khz) {
+#ifndef GAANS_PHASE_TIMES
+  if (buffer_dev != nullptr && units > 0)
+    return fail(GAANS_EINVAL, "this library is built without phase timestamps "
+                "(build the GAANS_PHASE_TIMES variant)");
+#endif
+  if (wall_clock_khz) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(wall_clock_khz, hipDeviceAttributeWallClockRate, dev) !=
+            hipSuccess)
+      return fail(GAANS_EHIP, "cannot query the device's wall clock rate");
+  }
+  if (buffer_dev == nullptr || units <= 0) {
+    g_phase = PhaseBuf{nullptr, 0};
+    return GAANS_OK;
+  }
+  g_phase = PhaseBuf{static_cast<uint64_t*>(buffer_dev), units};  // kPhaseSlots u64 per unit
+  return GAANS_OK;
 }
 
 int gaans_wait_host_word(void* stream, const uint32_t* word) {

@@ -15,9 +15,10 @@ import threading
 from .errors import CoderDependencyError
 
 LIB_NAME = "libgaans_w64.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 CTRL_BYTES = 256
 PLAN_BYTES = 1536  # GAANS_PLAN_BYTES
+PHASE_SLOTS = 16  # GAANS_PHASE_SLOTS
 # plan modes (GAANS_MODE_*)
 MODE_SYMBOLS, MODE_LATENTS, MODE_GAUSSIAN = 0, 1, 2
 NOALLOC_SCRATCH_BYTES = 16 * 1024 * 1024  # GAANS_NOALLOC_SCRATCH_BYTES
@@ -71,11 +72,18 @@ class Tables(ctypes.Structure):
                 ("max_nsym", ctypes.c_int32), ("total_nsym", ctypes.c_int64),
                 ("digest", ctypes.c_uint64), ("max_dense", ctypes.c_int32),
                 ("flags", ctypes.c_int32), ("total_dense", ctypes.c_int64),
-                ("mean_bits", ctypes.c_float), ("reserved", ctypes.c_int32)]
+                ("mean_bits", ctypes.c_float), ("max_wide", ctypes.c_int32),
+                ("total_wide", ctypes.c_int64)]
+
+
+# GAANS_PHASE_TIMES=1 selects the measurement build (kernels that record phase
+# timestamps; csrc/build.py --phases), for bench.py --phases only
+LIB_NAME_PHASES = "libgaans_w64_phases.so"
 
 
 def library_path() -> str:
-    return os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", LIB_NAME)
+    name = LIB_NAME_PHASES if os.environ.get("GAANS_PHASE_TIMES") == "1" else LIB_NAME
+    return os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", name)
 
 
 def library_available() -> bool:
@@ -114,6 +122,7 @@ def _declare(L) -> None:
                                    p], ctypes.c_int),
         "gaans_rans64_decode": ([p, p, i64, p, p, T, i64, i64, i64, p, p, p], ctypes.c_int),
         "gaans_wait_host_word": ([p, p], ctypes.c_int),
+        "gaans_debug_phases": ([p, i64, ctypes.POINTER(ctypes.c_int32)], ctypes.c_int),
         # plans are passed by address (c_void_p): no byref object per call
         "gaans_plan_encode": ([T, i32, i32, i32, f32, i64, i64, i64, i64, i32, p], ctypes.c_int),
         "gaans_plan_decode": ([T, i32, i32, i32, f32, i64, i64, i64, i64, i32, p], ctypes.c_int),

@@ -59,7 +59,7 @@
 extern "C" {
 #endif
 
-#define GAANS_ABI_VERSION 10
+#define GAANS_ABI_VERSION 11
 #define GAANS_CTRL_BYTES 256
 
 /* return codes */
@@ -106,7 +106,8 @@ typedef struct gaans_tables {
   int32_t flags;      /* GAANS_TABLES_* */
   int64_t total_dense; /* decode sub-blocks over all tables */
   float mean_bits;     /* mean over the tables of their entropy (bits per symbol) */
-  int32_t reserved;
+  int32_t max_wide;    /* most wide-lookup sub-blocks of one table (GAANS_TABLES_WIDE) */
+  int64_t total_wide;  /* wide-lookup sub-blocks over all tables */
 } gaans_tables;
 
 /* gaans_tables.flags: the blob holds compact search lookups (one u32 per
@@ -114,6 +115,12 @@ typedef struct gaans_tables {
  * the sub-blocks do not fit in LDS; set when there are at most 65,527
  * symbols in all and every offset is at least INT32_MIN + 65536. */
 #define GAANS_TABLES_SEARCH 1
+/* gaans_tables.flags: the blob holds wide decode lookups (2048 buckets of 32
+ * values per table, 16 KB, and a 16-entry sub-block of two-value ranges for
+ * every bucket in which two or more symbols start after its first value),
+ * which the decoder stages instead of the 256-bucket ones when they fit in
+ * LDS: fewer steps need a second lookup, none a third; set for M <= 4096. */
+#define GAANS_TABLES_WIDE 2
 
 int gaans_abi_version(void);
 const char* gaans_last_error(void);
@@ -371,6 +378,29 @@ int gaans_run_encode(const gaans_plan* plan, void* stream, const void* in0, cons
 int gaans_run_decode(const gaans_plan* plan, void* stream, const uint8_t* payload_dev,
                      int64_t payload_bytes, const void* in0, const void* in1, const void* in2,
                      void* out_dev, void* ctrl_dev, uint32_t* status_host);
+
+/* ---- measurement ------------------------------------------------------------ */
+
+/* Phase timestamps of later encode and decode launches (measurement only; a
+ * library built with GAANS_PHASE_TIMES defined -- the default build returns
+ * GAANS_EINVAL for a non-NULL buffer and its kernels record nothing):
+ * with buffer_dev set (device memory of GAANS_PHASE_SLOTS u64 per coding
+ * unit, `units` units), unit u < units of every later gaans_encode_* /
+ * gaans_decode_* / gaans_run_* launch writes slots of buffer_dev[16u ..
+ * 16u + 15]: the device's constant-rate real-time counter
+ * (hipDeviceAttributeWallClockRate) at 0 kernel entry, 1 the unit's first
+ * loads returned (payload header, table header and metadata; the mark
+ * waits for them), 2 tables staged,
+ * 3 the first coding step (first block ready), 4 after the last step,
+ * 5 before and 6 after the unit's completion-counter atomic, 7 (last unit to
+ * finish only) after the completion word; the shader clock at 12 the first
+ * and 13 after the last step.  Other slots are not written.  NULL (or
+ * units <= 0) turns it off; a launch picks the setting up when it is bound,
+ * so it is process-wide and not for concurrent callers.  The points are taken
+ * in scalar registers and stored once per unit.  wall_clock_khz (may be NULL) receives the real-time
+ * counter's rate on the current device.  No counterpart in the reference. */
+#define GAANS_PHASE_SLOTS 16
+int gaans_debug_phases(void* buffer_dev, int64_t units, int32_t* wall_clock_khz);
 
 /* ---- host self test ------------------------------------------------------- */
 

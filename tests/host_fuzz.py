@@ -26,7 +26,8 @@ class Tables(ctypes.Structure):  # gaans_tables (include/gaans_w64.h)
                 ("max_nsym", ctypes.c_int32), ("total_nsym", ctypes.c_int64),
                 ("digest", ctypes.c_uint64), ("max_dense", ctypes.c_int32),
                 ("flags", ctypes.c_int32), ("total_dense", ctypes.c_int64),
-                ("mean_bits", ctypes.c_float), ("reserved", ctypes.c_int32)]
+                ("mean_bits", ctypes.c_float), ("max_wide", ctypes.c_int32),
+                ("total_wide", ctypes.c_int64)]
 
 
 class Layout(ctypes.Structure):  # gaans_layout

@@ -147,6 +147,70 @@ def host_lookup(blob, t, cum, levels=None):
     return s0, st0, st1 - st0
 
 
+def host_lookup_wide(blob, t, cum, levels=None):
+    """The wide decode lookup as the kernel does it, read from the prepared
+    blob: entry cum >> 5 of the table's 2048, for a dense bucket entry
+    (cum >> 1) & 15 of its sub-block, which is never dense."""
+    hdr = struct.unpack_from("<20I", blob, 0)
+    wide_off, wdense_off, total_wide = hdr[16], hdr[17], hdr[19]
+    e = struct.unpack_from("<Q", blob, wide_off + 8 * (2048 * t + (cum >> 5)))[0]
+    depth = 1
+    if e >> 48 == 0xFFFF:
+        blk = e & 0xFFFFFFFF
+        assert blk < total_wide
+        e = struct.unpack_from("<Q", blob, wdense_off + 8 * (16 * blk + ((cum >> 1) & 15)))[0]
+        depth = 2
+    assert e >> 48 != 0xFFFF
+    if levels is not None:
+        levels[depth] = levels.get(depth, 0) + 1
+    lo, hi = e & 0xFFFFFFFF, e >> 32
+    s0, nxt = hi & 0xFFFF, hi >> 16
+    st0, st1 = lo & 0xFFFF, (lo >> 16) + 1
+    if cum >= st1:
+        return s0 + 1, st1, nxt + 1
+    return s0, st0, st1 - st0
+
+
+def wide_bases(blob, M):
+    hdr = struct.unpack_from("<20I", blob, 0)
+    return struct.unpack_from(f"<{M + 1}I", blob, hdr[18])
+
+
+def test_wide_lookups_exhaustive():
+    # every cum value of the 512x768 tables (Laplacian tails) and of the
+    # hyperprior's widest GaussianConditional tables (freq-1 tails) against
+    # np.searchsorted; the per-table sub-block bases partition the sub-blocks
+    w = synthetic.coder_512x768()
+    yw, _, _, _ = synthetic.hyperprior_512x768()
+    for cdfs, sizes, offs, tabs in ((w.cdfs[:6], w.cdf_sizes[:6], w.offsets[:6], range(6)),
+                                    (yw.cdfs, yw.cdf_sizes, yw.offsets, (0, 31, 62, 63))):
+        rc, blob, _ = prepare_host(cdfs, sizes, offs)
+        assert rc == 0
+        blob = blob.tobytes()
+        hdr = struct.unpack_from("<20I", blob, 0)
+        assert hdr[13] & 4  # wide lookups present
+        bases = wide_bases(blob, cdfs.shape[0])
+        assert bases[0] == 0 and bases[-1] == hdr[19] and list(bases) == sorted(bases)
+        levels = {}
+        for t in tabs:
+            c = cdfs[t, : sizes[t]]
+            want = np.searchsorted(c, np.arange(65536), side="right") - 1
+            for cum in range(65536):
+                v, start, freq = host_lookup_wide(blob, t, cum, levels)
+                assert v == want[cum] and start == c[v] and freq == c[v + 1] - c[v], (t, cum)
+        assert levels.get(2, 0) > 0  # dense buckets exist and resolve in one more read
+
+
+def test_wide_lookups_only_for_at_most_4096_tables():
+    w = synthetic.coder_512x768()
+    cdfs = np.repeat(w.cdfs[:1], 4097, 0)
+    sizes = np.repeat(w.cdf_sizes[:1], 4097)
+    rc, blob, _ = prepare_host(cdfs, sizes, np.zeros(4097, np.int32))
+    assert rc == 0 and not struct.unpack_from("<20I", blob.tobytes(), 0)[13] & 4
+    rc, blob, _ = prepare_host(cdfs[:4096], sizes[:4096], np.zeros(4096, np.int32))
+    assert rc == 0 and struct.unpack_from("<20I", blob.tobytes(), 0)[13] & 4
+
+
 def test_prepared_tables_digest_and_lookup_exhaustive():
     w = synthetic.coder_512x768()
     cdfs, sizes, offs = w.cdfs[:6], w.cdf_sizes[:6], w.offsets[:6]
