@@ -206,31 +206,33 @@ struct Tabs {
   bool sub_lds;            // decoder: sub-blocks staged with the lookups
 };
 
-// Copy n 16-byte words global -> LDS with the whole workgroup (NT threads),
-// U loads in flight per thread before their stores (slots past n re-copy
-// word n - 1, so nothing branches and the loads are issued together).
-template <int NT, int U>
-__device__ __forceinline__ void copy16(uint4* dst, const uint4* __restrict__ src, uint32_t n,
-                                       int tid) {
-  for (uint32_t b = tid; b < n; b += U * NT) {
-    uint4 v[U];
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const uint32_t i = b + k * NT;
-      v[k] = src[i < n ? i : n - 1];
-    }
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const uint32_t i = b + k * NT;
-      dst[i < n ? i : n - 1] = v[k];
-    }
-  }
-}
-
 // One pass over the staged metadata (nt), entries (ne) and sub-block 16-byte
 // words (nd) with U loads of each kind in flight per thread before the
 // stores.  Indexes past a count re-copy its last item, so nothing branches
 // (the kinds are compile-time choices; counts are >= 1).
+// Copy n 16-byte words global -> LDS with direct-to-LDS loads (gfx950
+// global_load_lds_dwordx4: no registers, every load of the copy in flight at
+// once): wave w of the NT threads issues the 64-word (1 KB) chunks w, w + W,
+// ...; lane i of chunk c moves word 64 c + i to dst + 64 c + i (the LDS
+// address is the chunk base, wave-uniform, plus 16 bytes per lane); lanes
+// past n are masked off and write nothing.  The data is in LDS once the
+// wave's vector-memory counter reaches zero: callers wait for it before the
+// barrier that publishes the copy.
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+template <int NT>
+__device__ __forceinline__ void copy16_dma(uint4* dst, const uint4* __restrict__ src, uint32_t n,
+                                           int tid) {
+  constexpr uint32_t W = NT / kLanes;
+  const uint32_t lane = (uint32_t)tid & (kLanes - 1);
+  for (uint32_t c = (uint32_t)__builtin_amdgcn_readfirstlane(tid >> 6); c * kLanes < n; c += W) {
+    const uint32_t i = c * kLanes + lane;
+    if (i < n)
+      __builtin_amdgcn_global_load_lds((global_void_t*)(src + i), (lds_void_t*)(dst + c * kLanes),
+                                       16, 0, 0);
+  }
+}
+
 template <int NT, bool kEnt, bool kSub>
 __device__ __forceinline__ void stage_pass(const Tabs& T, uint4* lmeta, uint2* lent, uint4* lsub,
                                            const uint4* __restrict__ ssrc, uint32_t nt,
@@ -318,19 +320,21 @@ __device__ void stage_tables(Tabs& T, uint4* lmeta, uint2* lent, uint64_t* llut,
       const uint32_t ne = bd.ent_end - base0;
       stage_pass<NT, true, false>(T, lmeta, lent, nullptr, nullptr, nt, ne, 0u, base0, t_lo, tid);
     } else {
+      // lookups and sub-blocks straight into LDS, the metadata rows through
+      // registers (they are rewritten)
       const uint4* lut_src = reinterpret_cast<const uint4*>(T.glut + (int64_t)t_lo * LB);
-      copy16<NT, 4>(reinterpret_cast<uint4*>(llut), lut_src, nt * (LB / 2), tid);
+      copy16_dma<NT>(reinterpret_cast<uint4*>(llut), lut_src, nt * (LB / 2), tid);
       const uint32_t d0 = bd.d0;
       const uint32_t d1 = bd.d1;
       if (lsub && d1 > d0) {
         T.sub_first = d0;
-        stage_pass<NT, false, true>(T, lmeta, nullptr, reinterpret_cast<uint4*>(lsub),
-                                    reinterpret_cast<const uint4*>(T.gsub + (size_t)d0 * kSubSize),
-                                    nt, 1u, (d1 - d0) * (kSubBytes / 16), base0, t_lo, tid);
-      } else {
-        stage_pass<NT, false, false>(T, lmeta, nullptr, nullptr, nullptr, nt, 1u, 0u, base0, t_lo,
-                                     tid);
+        copy16_dma<NT>(reinterpret_cast<uint4*>(lsub),
+                       reinterpret_cast<const uint4*>(T.gsub + (size_t)d0 * kSubSize),
+                       (d1 - d0) * (kSubBytes / 16), tid);
       }
+      stage_pass<NT, false, false>(T, lmeta, nullptr, nullptr, nullptr, nt, 1u, 0u, base0, t_lo,
+                                   tid);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's direct-to-LDS copies are in
     }
   }
   __syncthreads();
@@ -1400,11 +1404,12 @@ __device__ void stage_search(Tabs& T, uint4* lmeta, uint32_t* lclut, uint16_t* l
   T.nt = (int)M;
   T.sub_first = 0;
   T.sub_lds = false;
-  copy16<NT, 3>(reinterpret_cast<uint4*>(lclut),
-                reinterpret_cast<const uint4*>(tables + blob.clut_off), M * (kLutSize / 4), tid);
-  copy16<NT, 3>(reinterpret_cast<uint4*>(lstarts),
-                reinterpret_cast<const uint4*>(tables + blob.starts_off), starts_words, tid);
+  copy16_dma<NT>(reinterpret_cast<uint4*>(lclut),
+                 reinterpret_cast<const uint4*>(tables + blob.clut_off), M * (kLutSize / 4), tid);
+  copy16_dma<NT>(reinterpret_cast<uint4*>(lstarts),
+                 reinterpret_cast<const uint4*>(tables + blob.starts_off), starts_words, tid);
   stage_pass<NT, false, false>(T, lmeta, nullptr, nullptr, nullptr, M, 1u, 0u, 0u, 0, tid);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's direct-to-LDS copies are in
   __syncthreads();
 }
 

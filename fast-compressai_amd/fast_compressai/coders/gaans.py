@@ -24,7 +24,6 @@ from __future__ import annotations
 
 import ctypes
 import threading
-from dataclasses import dataclass
 
 import torch
 
@@ -86,8 +85,10 @@ def _index(device) -> int:
 
 def _enter_device(index: int):
     """Make ``index`` the current device; returns the device to restore
-    afterwards, or None when it already was current."""
-    cur = torch.cuda.current_device()
+    afterwards, or None when it already was current.  (The caller's tensors
+    are on a GPU, so torch's device runtime is initialised and the current
+    device is read directly.)"""
+    cur = torch._C._cuda_getDevice()
     if cur == index:
         return None
     torch.cuda.set_device(index)
@@ -164,14 +165,20 @@ def resolve_segments(segments: int | None, tables: PreparedTables, B: int, N: in
     return segments
 
 
-@dataclass(frozen=True)
 class EncodedChunks:
-    packed: torch.Tensor      # uint8 [payload bytes]
-    header_bytes: int
-    chunk_len: int
-    K: int
-    segments: int = 1
-    batch: int = 1
+    """One encode's payload (uint8 ``packed``, header included) and the
+    layout values a payload object records."""
+
+    __slots__ = ("packed", "header_bytes", "chunk_len", "K", "segments", "batch")
+
+    def __init__(self, packed: torch.Tensor, header_bytes: int, chunk_len: int, K: int,
+                 segments: int = 1, batch: int = 1) -> None:
+        self.packed = packed
+        self.header_bytes = header_bytes
+        self.chunk_len = chunk_len
+        self.K = K
+        self.segments = segments
+        self.batch = batch
 
     @property
     def chunk_ends(self) -> torch.Tensor:
@@ -179,6 +186,11 @@ class EncodedChunks:
         units = self.K * self.segments
         return self.packed[64: 64 + 4 * self.batch * units].view(torch.uint32).view(
             self.batch, units)
+
+
+def layout(B: int, N: int, C: int, P: int, S: int) -> "_native.LayoutInts":
+    """The coding layout of a shape (cached)."""
+    return _native.layout(B, N, C, P, S)
 
 
 def _plan(tables: PreparedTables, decode: bool, mode: int, explicit: bool, B: int, N: int,
