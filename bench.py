@@ -95,6 +95,21 @@ def read_traffic(workload: str, kernel_key: str):
     return None
 
 
+def read_kernel_name(workload: str, kernel_key: str):
+    """The kernel's full name in the committed summary of ``workload`` (the
+    template instance the kernel trace saw), or None."""
+    path = os.path.join(REPO, "profiles", f"counters_{workload}.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(f"[{kernel_key}] "):
+                    name = line.split(" ", 1)[1].strip()
+                    return name.replace("void (anonymous namespace)::", "").split("((anon")[0]
+    except OSError:
+        return None
+    return None
+
+
 def phase_breakdown(L, torch, dev, units, steps, fn):
     """Run ``fn`` (one kernel launch) once with phase timestamps on and
     summarise them (gaans_debug_phases slots): microseconds from the earliest
@@ -693,9 +708,12 @@ def main():
     # algorithmic bytes per launch: symbols + indexes (int32) + payload
     alg_bytes = 4 * B * N + 4 * B * N + payload_bytes
     if dec_avg >= enc_avg:
-        kernel, key, dur = "k_decode<0,false,16,false> (gaans_decode_symbols)", "k_decode", dec_avg
+        key, dur, entry = "k_decode", dec_avg, "gaans_decode_symbols"
     else:
-        kernel, key, dur = "k_encode<0,false,8> (gaans_encode_symbols)", "k_encode", enc_avg
+        key, dur, entry = "k_encode", enc_avg, "gaans_encode_symbols"
+    # the template instance the LDS plan launches, as the committed kernel
+    # trace of this workload names it
+    kernel = f"{read_kernel_name('coder_512x768_p4', key) or key} ({entry})"
     achieved = alg_bytes / dur / 1e9
     traffic = read_traffic("coder_512x768_p4", key)
 
