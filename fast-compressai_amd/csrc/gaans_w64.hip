@@ -70,7 +70,7 @@ constexpr int kEncMaxWaves = 9;
 // per-wave hash, status and escape nibbles, then the escape count, the unit's
 // word count and the completion counter's value
 constexpr int kPartBytes = (12 * kEncMaxWaves + 12 + 15) / 16 * 16;
-constexpr int kRingWords = 4096;       // encoder LDS output ring (u16 words)
+constexpr int kRingWords = 4096;       // encoder LDS output ring (u16 words), the most a plan uses
 constexpr int kPfU32Max = 8;  // decoder stream prefetch: u32 per lane (16-step blocks)
 // word 3 of a raw buffer resource on gfx9 (32-bit data format; stride 0, so
 // num_records counts bytes)
@@ -441,6 +441,7 @@ struct EncArgs {
   int32_t cap_words;
   int64_t units, header_bytes;  // coding units (B K S)
   int32_t nt_cap, stage_all;
+  uint32_t ring_mask;  // output ring words - 1 (a power of two, >= 2 SB kLanes)
   uint32_t* __restrict__ chunk_words;
   uint32_t* __restrict__ chunk_status;
   uint32_t* __restrict__ index_hash;
@@ -455,8 +456,10 @@ struct EncArgs {
   PhaseBuf phase;
 };
 
-// Encoder LDS layout (bytes)
-constexpr int kEncRingBytes = 2 * (kRingWords + kLanes);  // + one spare slot per lane
+// Encoder LDS layout (bytes): the output ring of `ring` u16 words (a power
+// of two chosen by the plan, at least two blocks' worst case) plus one spare
+// slot per lane, then the geometry's records, flags and parts
+constexpr int enc_ring_bytes(int ring) { return 2 * (ring + kLanes); }
 
 // Encoder geometry for blocks of SB steps (the mappers' lead over the coder
 // and the steps between two barriers).
@@ -468,13 +471,13 @@ struct EncGeom {
   static constexpr int kPer = (SB + NM - 1) / NM;
   static constexpr int kRecBytes = 2 * SB * kLanes * 16;       // two blocks of op records
   static constexpr int kFlagBytes = 16;  // per block parity: steps with escapes (bit per step)
-  // [ring][records][flags][parts]
-  static constexpr int kFixed = kEncRingBytes + kRecBytes + kFlagBytes + kPartBytes;
+  // [ring][records][flags][parts]: the part after the ring
+  static constexpr int kTail = kRecBytes + kFlagBytes + kPartBytes;
 };
 
-int enc_fixed_lds(int sb) {  // the same for either mapper count
-  return sb >= 16 ? EncGeom<16, 4>::kFixed
-                  : (sb >= 8 ? EncGeom<8, 4>::kFixed : EncGeom<4, 4>::kFixed);
+int enc_fixed_lds(int sb, int ring) {  // the same for either mapper count
+  return enc_ring_bytes(ring) + (sb >= 16 ? EncGeom<16, 4>::kTail
+                                          : (sb >= 8 ? EncGeom<8, 4>::kTail : EncGeom<4, 4>::kTail));
 }
 
 // Payload bytes of unit g: states, stream and escape words, pad.
@@ -725,26 +728,26 @@ __device__ __forceinline__ bool enc_records_fast(const EncArgs& a, const Tabs& t
   return true;
 }
 
-// Encoder LDS ring: kRingWords words + one spare slot per lane, which lanes
-// that emit nothing write to (so the store needs no branch).
+// Encoder LDS ring: ring_mask + 1 words (a power of two) and one spare slot
+// per lane.
 __device__ __forceinline__ void ring_flush(uint16_t* __restrict__ wbuf, const uint16_t* ring,
-                                           int wp, int fl, int lane) {
-  for (int pos = wp + lane; pos < fl; pos += kLanes) wbuf[pos] = ring[pos & (kRingWords - 1)];
+                                           int wp, int fl, int lane, uint32_t ring_mask) {
+  for (int pos = wp + lane; pos < fl; pos += kLanes) wbuf[pos] = ring[pos & ring_mask];
 }
 
-// The ring holds the words [wp, fl) (positions mod kRingWords).  The coder
+// The ring holds the words [wp, fl) (positions mod the ring size).  The coder
 // flushes it at the start of a block when fewer than SB * kLanes slots are
 // free (a step emits at most one word per lane), so the steps need no check.
 // A lane emits when x >= freq << 16, i.e. (x >> 16) > freq - 1 (z's high
 // half): one compare of the two high halves.
 __device__ __forceinline__ void emit_words(uint32_t z, uint32_t& x, uint16_t* ring, int& wp,
-                                           int lane) {
+                                           int lane, uint32_t ring_mask) {
   const bool emit = (x >> 16) > (z >> 16);
   const uint64_t m = ballot(emit);
   wp = uni(wp - __popcll(m));
   // an exec-masked store: the slot's address is computed by the emitting
   // lanes only, and the others skip it
-  if (emit) ring[(uint32_t)(wp + (int)lane_rank(m)) & (kRingWords - 1)] = (uint16_t)x;
+  if (emit) ring[(uint32_t)(wp + (int)lane_rank(m)) & ring_mask] = (uint16_t)x;
   x = emit ? x >> 16 : x;
 }
 
@@ -777,11 +780,13 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
   constexpr int kPer = G::kPer;
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t* ring = reinterpret_cast<uint16_t*>(smem);
-  uint4* recs = reinterpret_cast<uint4*>(smem + kEncRingBytes);
-  uint32_t* eflag = reinterpret_cast<uint32_t*>(smem + kEncRingBytes + G::kRecBytes);
+  const uint32_t ring_mask = a.ring_mask;  // ring words - 1
+  const uint32_t ring_bytes = (uint32_t)enc_ring_bytes((int)ring_mask + 1);
+  uint4* recs = reinterpret_cast<uint4*>(smem + ring_bytes);
+  uint32_t* eflag = reinterpret_cast<uint32_t*>(smem + ring_bytes + G::kRecBytes);
   uint32_t* part = eflag + G::kFlagBytes / 4;  // per-wave hash, status, escape nibbles
-  uint4* lmeta = reinterpret_cast<uint4*>(smem + G::kFixed);
-  uint2* lent = reinterpret_cast<uint2*>(smem + G::kFixed + 16 * a.nt_cap);
+  uint4* lmeta = reinterpret_cast<uint4*>(smem + ring_bytes + G::kTail);
+  uint2* lent = reinterpret_cast<uint2*>(smem + ring_bytes + G::kTail + 16 * a.nt_cap);
   float* scl = reinterpret_cast<float*>(smem + a.scales_lds);  // Gaussian: scale table
 
   const int64_t g = blockIdx.x;
@@ -926,8 +931,8 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
       pc.cycles(12);
       for (int j = nblk - 1; j >= 0; --j) {
         // coder: steps of block j, last to first
-        if (fl - wp > kRingWords - SB * kLanes) {
-          ring_flush(wbuf, ring, wp, fl, lane);
+        if (fl - wp > (int)ring_mask + 1 - SB * kLanes) {
+          ring_flush(wbuf, ring, wp, fl, lane, ring_mask);
           fl = wp;
         }
         const uint4* src = recs + (j & 1) * SB * kLanes;
@@ -946,14 +951,14 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
             // common case: a full block, no per-step branches
 #pragma unroll
             for (int k = H - 1; k >= 0; --k) {
-              emit_words(r[k].z, x, ring, wp, lane);
+              emit_words(r[k].z, x, ring, wp, lane, ring_mask);
               x = enc_apply(x, r[k]);
             }
           } else {
 #pragma unroll
             for (int k = H - 1; k >= 0; --k) {
               if (j * SB + h * H + k >= T) continue;
-              emit_words(r[k].z, x, ring, wp, lane);
+              emit_words(r[k].z, x, ring, wp, lane, ring_mask);
               x = enc_apply(x, r[k]);
             }
           }
@@ -969,7 +974,7 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
       }
       pc.cycles(13);
       pc.mark(4);
-      if (fl > wp) ring_flush(wbuf, ring, wp, fl, lane);
+      if (fl > wp) ring_flush(wbuf, ring, wp, fl, lane, ring_mask);
     } else {
       if (nblk > 0) map_block(nblk - 1);
       __syncthreads();
@@ -2483,23 +2488,31 @@ struct EncPlan {
   int sb;
   size_t lds;
   int64_t occ;  // workgroups per CU the plan allows
+  int ring;     // output ring words
 };
 
 // `extra` LDS bytes follow the tables (the Gaussian mode's scale table);
 // range_ok is false when any table may serve any position (per-element
 // indexes computed from scales), so only all tables or none are staged.
+// For each block size the output ring shrinks from 4096 words to 2048 and
+// 1024 (never below two blocks' worst case) before the block size does:
+// a smaller ring only flushes more often, a smaller block doubles the
+// per-block work (the batch-64 uniform workload's 16 staged tables of 255
+// symbols fit next to 8-step blocks with a 1024-word ring).
 EncPlan plan_encode(const gaans_tables* t, int64_t P, int64_t units, const DevLds& d,
                     int64_t extra = 0, bool range_ok = true,
                     bool allow16 = false) {
   for (int64_t occ = occ_target(units, d, 4); occ >= 1; --occ)
-    for (int sb = allow16 ? 16 : 8; sb >= 4; sb >>= 1) {
-      Stage s;
-      const int64_t fixed = enc_fixed_lds(sb);
-      if (fit_stage(t, P, 16, 8, 0, lds_budget(d, occ) - fixed - extra, &s, range_ok))
-        return EncPlan{s, sb, (size_t)(fixed + 16 * (int64_t)s.nt_cap + 8 * (int64_t)s.ne_cap),
-                       occ};
-    }
-  return EncPlan{Stage{0, 0, 0, 0}, 8, (size_t)enc_fixed_lds(8), 1};
+    for (int sb = allow16 ? 16 : 8; sb >= 4; sb >>= 1)
+      for (int ring = kRingWords; ring >= 2 * sb * kLanes && ring >= 1024; ring >>= 1) {
+        Stage s;
+        const int64_t fixed = enc_fixed_lds(sb, ring);
+        if (fit_stage(t, P, 16, 8, 0, lds_budget(d, occ) - fixed - extra, &s, range_ok))
+          return EncPlan{s, sb,
+                         (size_t)(fixed + 16 * (int64_t)s.nt_cap + 8 * (int64_t)s.ne_cap), occ,
+                         ring};
+      }
+  return EncPlan{Stage{0, 0, 0, 0}, 8, (size_t)enc_fixed_lds(8, kRingWords), 1, kRingWords};
 }
 
 // Decoder: lookups and metadata per table; sub-blocks when they are staged
@@ -2759,6 +2772,7 @@ int encode_prepare(int mode, bool implicit, int32_t n_scales, float scale_bound,
   a.header_bytes = L.header_bytes;
   a.nt_cap = st.nt_cap;
   a.stage_all = st.stage_all;
+  a.ring_mask = (uint32_t)(plan.ring - 1);
   // 8 mapper waves when every workgroup has a CU to itself
   const int nm = plan.occ == 1 && L.U <= dl.cus ? 8 : 4;
   e->kernel = enc_kernel(mode, implicit, plan.sb, nm);
