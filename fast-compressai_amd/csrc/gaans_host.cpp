@@ -66,7 +66,9 @@ int make_layout(int64_t B, int64_t N, int64_t C, int64_t P, int64_t S, Layout* L
                 "segments per chunk must be in [1, %lld] for this shape (got %lld)",
                 (long long)(t_last < kMaxSegments ? t_last : kMaxSegments), (long long)S);
   L->U = B * L->K * S;
-  if (L->U >= ((int64_t)1 << 31)) return fail(GAANS_EINVAL, "too many coding units");
+  // the encoder's completion counter holds the unit count in 24 bits
+  if (L->U >= ((int64_t)1 << 24))
+    return fail(GAANS_EINVAL, "too many coding units (%lld, at most 2^24 - 1)", (long long)L->U);
   if ((int64_t)kMaxEscNibbles * L->chunk_len + 8 >= ((int64_t)1 << 31))
     return fail(GAANS_EINVAL, "chunk of %lld symbols is too large", (long long)L->chunk_len);
   // the longest unit: ceil(Tc / S) steps of the longest chunk
@@ -76,6 +78,10 @@ int make_layout(int64_t B, int64_t N, int64_t C, int64_t P, int64_t S, Layout* L
   // per symbol at most one stream word and 9 escape nibbles; per unit the
   // states, a pad word and a partly used escape word
   L->max_payload = L->header_bytes + B * N * 7 + L->U * (4 * kLanes + 8);
+  // ... and the payload body in 36 bits of u32 words
+  if (L->max_payload >= ((int64_t)1 << 38))
+    return fail(GAANS_EINVAL, "shape too large (worst-case payload of %lld bytes)",
+                (long long)L->max_payload);
   L->cap_words = align_up(L->seg_cap + 2, 2);
   int64_t o = 0;
   L->o_words_cnt = o; o = align_up(o + 4 * L->U, 256);

@@ -108,7 +108,7 @@ struct PhaseClock {
       }
     }
   }
-  // thread 0 of the last unit: the completion word is out
+  // the thread that wrote the completion word, just after
   __device__ __forceinline__ void store_done(const PhaseBuf& b, int64_t g) const {
     if (b.p != nullptr && g < b.units) b.p[g * kPhaseSlots + 7] = __builtin_amdgcn_s_memrealtime();
   }
@@ -126,7 +126,8 @@ struct PhaseClock {
 #endif
 };
 
-// control block (u32 words); encoder and decoder fields on separate 64-byte lines
+// control block (u32 word indexes; the encoder's counter is a u64 at word 0);
+// encoder and decoder fields on separate 64-byte lines
 constexpr int kCtrlEncDone = 0;
 constexpr int kCtrlDecDone = 16;
 constexpr int kCtrlDecStatus = 17;
@@ -443,7 +444,6 @@ struct EncArgs {
   int32_t nt_cap, stage_all;
   uint32_t ring_mask;  // output ring words - 1 (a power of two, >= 2 SB kLanes)
   uint32_t* __restrict__ chunk_words;
-  uint32_t* __restrict__ chunk_status;
   uint32_t* __restrict__ index_hash;
   uint32_t* __restrict__ end_off;
   uint64_t* __restrict__ ws_info;
@@ -480,41 +480,70 @@ int enc_fixed_lds(int sb, int ring) {  // the same for either mapper count
                                           : (sb >= 8 ? EncGeom<8, 4>::kTail : EncGeom<4, 4>::kTail));
 }
 
-// Payload bytes of unit g: states, stream and escape words, pad.
-__device__ __forceinline__ uint64_t unit_bytes(const EncArgs& a, int64_t g) {
-  const int len = unit_len(g, a.K, a.S, a.N, a.chunk_len);
-  const uint32_t A = len < kLanes ? (uint32_t)len : (uint32_t)kLanes;
-  const uint32_t W = __hip_atomic_load(&a.chunk_words[g], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-  const uint32_t Z = __hip_atomic_load(&a.esc[g].y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint64_t U = (uint64_t)W + (Z + 3u) / 4u;  // stream + escape words
-  return 4ull * A + 2ull * (U + (U & 1u));
+// Payload size of a unit in u32 words: A final states, then the stream's W
+// u16 words and the escape section's Z nibbles (4 to a u16 word), padded to
+// an even number of u16 words.
+__device__ __forceinline__ uint32_t unit_quads(int A, uint32_t W, uint32_t Z) {
+  const uint32_t U = W + (Z + 3u) / 4u;
+  return (uint32_t)A + (U + (U & 1u)) / 2u;
 }
 
-// Last workgroup of an encode launch (all waves): unit end offsets, payload
-// size and status.  The units are scanned kThreads at a time, one per
-// thread, with the next tile's loads issued before the current tile's scan.
-// The completion word carries size and status in one 64-bit store, so the
-// host can read it as soon as it lands (no system-wide cache write-back).
+// Encode completion counter: one u64 in the control block, units done in
+// bits 0..23, payload body u32 words in bits 24..59, the OR of the units'
+// status bits in bits 60..63.  A unit ORs in its status (rarely), waits for
+// that and its count stores, then adds 1 | its words << 24; atomics on one
+// address take effect in program order, so the unit whose add returns units - 1 done holds the
+// payload size and status of the whole launch with no further memory round
+// trip.  The host keeps units below 2^24 and the worst-case payload below
+// 2^38 bytes, so no field carries into the next.
+constexpr int kEncCountBits = 24, kEncStShift = 60;
+constexpr uint64_t kEncCountMask = (1ull << kEncCountBits) - 1;
+static_assert((GAANS_ST_RANGE | GAANS_ST_INDEX | GAANS_ST_TABLES) < 16,
+              "encode status bits fit the completion counter");
+
+// The unit that completed the launch (one thread): payload size and status
+// to the workspace and the host's completion word (size and status in one
+// 64-bit store, so the host can read it as soon as it lands: no system-wide
+// cache write-back), then the counter back to zero for the next launch.
+__device__ void encode_finish(const EncArgs& a, uint64_t word) {
+  const uint64_t body = 4ull * ((word << (64 - kEncStShift)) >> (64 - kEncStShift + kEncCountBits));
+  uint32_t st = (uint32_t)(word >> kEncStShift);
+  if (body > 0xffffffffull) st |= GAANS_ST_SIZE;  // unit end offsets are u32
+  const uint64_t total = (uint64_t)a.header_bytes + body;
+  a.ws_info[0] = total;
+  a.ws_info[1] = st;
+  if (a.info_out) {
+    a.info_out[0] = total;
+    a.info_out[1] = st;
+    __hip_atomic_store(&a.info_out[2], 1ull | ((uint64_t)st << 1) | (total << 16),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(a.ctrl + kCtrlEncDone), 0ull, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Last workgroup of an encode launch (all threads), after the completion
+// word is out: the unit end offsets (payload body bytes up to and including
+// each unit) for the pack kernel, kThreads units at a time, the next tile's
+// counts loaded before the current tile's scan.  A body past 4 GiB wraps
+// here; the completion word carries GAANS_ST_SIZE then, and the pack kernel
+// skips a unit whose offsets decrease.
 template <int NT>
-__device__ void encode_finish(const EncArgs& a, int tid, uint64_t* sh) {
+__device__ void unit_end_offsets(const EncArgs& a, int tid, uint64_t* sh) {
   constexpr int kThreads = NT, kWaves = NT / kLanes;
   const int lane = tid & (kLanes - 1), wv = tid >> 6;
+  auto bytes = [&](int64_t g) -> uint64_t {
+    const int len = unit_len(g, a.K, a.S, a.N, a.chunk_len);
+    const uint32_t W = __hip_atomic_load(&a.chunk_words[g], __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t Z = __hip_atomic_load(&a.esc[g].y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return 4ull * unit_quads(len < kLanes ? len : kLanes, W, Z);
+  };
   uint64_t carry = 0;
-  uint32_t st = 0;
-  uint64_t v = 0;
-  if (tid < a.units) {
-    v = unit_bytes(a, tid);
-    st |= __hip_atomic_load(&a.chunk_status[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  uint64_t v = tid < a.units ? bytes(tid) : 0ull;
   for (int64_t base = 0; base < a.units; base += kThreads) {
     const int64_t g = base + tid;
-    uint64_t vn = 0;
-    if (g + kThreads < a.units) {
-      vn = unit_bytes(a, g + kThreads);
-      st |= __hip_atomic_load(&a.chunk_status[g + kThreads], __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
-    }
+    const uint64_t vn = g + kThreads < a.units ? bytes(g + kThreads) : 0ull;
     uint64_t incl = wave_incl_scan(v, lane);
     if (lane == kLanes - 1) sh[wv] = incl;
     __syncthreads();
@@ -524,30 +553,9 @@ __device__ void encode_finish(const EncArgs& a, int tid, uint64_t* sh) {
       tot += sh[w];
     }
     __syncthreads();
-    incl += before + carry;
-    if (g < a.units) {
-      a.end_off[g] = (uint32_t)incl;
-      if (incl > 0xffffffffull) st |= GAANS_ST_SIZE;
-    }
+    if (g < a.units) a.end_off[g] = (uint32_t)(incl + before + carry);
     carry += tot;
     v = vn;
-  }
-  st = wave_or(st);
-  uint32_t* sst = reinterpret_cast<uint32_t*>(sh);
-  if (lane == 0) sst[wv] = st;
-  __syncthreads();
-  if (tid == 0) {
-    for (int w = 1; w < kWaves; ++w) st |= sst[w];
-    const uint64_t total = (uint64_t)a.header_bytes + carry;
-    a.ws_info[0] = total;
-    a.ws_info[1] = st;
-    if (a.info_out) {
-      a.info_out[0] = total;
-      a.info_out[1] = st;
-      __hip_atomic_store(&a.info_out[2], 1ull | ((uint64_t)st << 1) | (total << 16),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
-    __hip_atomic_store(&a.ctrl[kCtrlEncDone], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -974,7 +982,6 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
       }
       pc.cycles(13);
       pc.mark(4);
-      if (fl > wp) ring_flush(wbuf, ring, wp, fl, lane, ring_mask);
     } else {
       if (nblk > 0) map_block(nblk - 1);
       __syncthreads();
@@ -994,9 +1001,6 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
     }
   }
 
-  if (wid == 0 && lane < A) {
-    a.states[g * kLanes + lane] = x;
-  }
   hash = wave_sum(hash);
   status = wave_or(status);
   znib = wave_sum(znib);
@@ -1010,10 +1014,19 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
     }
   }
   __syncthreads();
+  // The coder wave's last words and final states are stored only now: the
+  // reductions above wait for the mappers' loads, and a wait for loads also
+  // waits for every store issued before them.  Pack reads them after this
+  // kernel has ended.
+  if (wid == 0) {
+    if (fl > wp) ring_flush(wbuf, ring, wp, fl, lane, ring_mask);
+    if (lane < A) a.states[g * kLanes + lane] = x;
+  }
   // The unit's counts are published by the first mapper wave, which has no
-  // stores in flight, so that its wait for them does not also wait for the
-  // coder wave's flush of the words and states (read by the pack kernel,
-  // after this kernel has ended).
+  // stores in flight.  What the last workgroup reads (maybe on another XCD,
+  // behind another L2) is stored with agent-scope atomics, coherent across
+  // the device, and has completed before the counter is raised: no fence, so
+  // no write-back of the XCD's whole L2.
   if (tid == kLanes) {
     uint32_t hs = 0, ss = 0, zs = 0;
     for (int w = 0; w < kWaves; ++w) {
@@ -1021,30 +1034,34 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
       ss |= part[kWaves + w];
       zs += part[2 * kWaves + w];
     }
-    a.index_hash[g] = hs;          // read by the pack kernel only
+    const uint32_t W = part[3 * kWaves + 1];
+    a.index_hash[g] = hs;  // read by the pack kernel only
     a.esc[g].x = part[3 * kWaves];
-    // What the last workgroup reads (maybe on another XCD, behind another L2)
-    // is stored with agent-scope atomics, which are coherent across the
-    // device, and has completed before the counter is raised: no fence, so
-    // no write-back of the XCD's whole L2.
-    __hip_atomic_store(&a.chunk_words[g], part[3 * kWaves + 1], __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&a.chunk_status[g], ss, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&a.chunk_words[g], W, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(&a.esc[g].y, zs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint64_t* done = reinterpret_cast<uint64_t*>(a.ctrl + kCtrlEncDone);
+    if (ss)
+      __hip_atomic_fetch_or(done, (uint64_t)ss << kEncStShift, __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const uint64_t inc = 1ull | ((uint64_t)unit_quads(A, W, zs) << kEncCountBits);
     pc.mark(5);
-    const uint32_t done = __hip_atomic_fetch_add(&a.ctrl[kCtrlEncDone], 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t old = __hip_atomic_fetch_add(done, inc, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
     pc.mark_after_loads(6);  // the atomic returned
     pc.store(a.phase, g, 5, 7);
-    part[3 * kWaves + 2] = done;
+    const bool last = (old & kEncCountMask) == (uint64_t)(a.units - 1);
+    if (last) {
+      encode_finish(a, old + inc);
+      pc.store_done(a.phase, g);
+    }
+    part[3 * kWaves + 2] = last;
   }
   if (tid == 0) pc.store(a.phase, g, 0, 5);  // the coder wave's points
   __syncthreads();
-  if (part[3 * kWaves + 2] == (uint32_t)(a.units - 1)) {  // uniform: the last workgroup
-    __syncthreads();  // every wave has read the counter before part is reused
-    encode_finish<kThreads>(a, tid, reinterpret_cast<uint64_t*>(part));
-    if (tid == 0) pc.store_done(a.phase, g);
+  if (part[3 * kWaves + 2]) {  // uniform: the last workgroup
+    __syncthreads();  // every wave has read the flag before part is reused
+    unit_end_offsets<kThreads>(a, tid, reinterpret_cast<uint64_t*>(part));
   }
 }
 
@@ -2815,7 +2832,6 @@ void encode_bind(int mode, EncArgs& a, const Layout& L, const int32_t* symbols, 
   a.scale_table = mode == kModeGaussian ? g->table : nullptr;
   a.indexes = mode == kModeGaussian ? nullptr : indexes;
   a.chunk_words = reinterpret_cast<uint32_t*>(w + L.o_words_cnt);
-  a.chunk_status = reinterpret_cast<uint32_t*>(w + L.o_status);
   a.index_hash = reinterpret_cast<uint32_t*>(w + L.o_hash);
   a.end_off = reinterpret_cast<uint32_t*>(w + L.o_end);
   a.ws_info = reinterpret_cast<uint64_t*>(w + L.o_info);
