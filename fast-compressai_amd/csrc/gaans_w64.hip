@@ -129,8 +129,7 @@ struct PhaseClock {
 // control block (u32 word indexes; the encoder's counter is a u64 at word 0);
 // encoder and decoder fields on separate 64-byte lines
 constexpr int kCtrlEncDone = 0;
-constexpr int kCtrlDecDone = 16;
-constexpr int kCtrlDecStatus = 17;
+constexpr int kCtrlDecDone = 16;  // u64: units done, status << 32
 
 // ---- wave helpers -----------------------------------------------------------
 
@@ -1796,6 +1795,20 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
   Stream S;  // the coder's; its final position is checked after the last barrier
   S.rp = 0;
   S.q = 0;
+  // each wave's hash, status and escape nibbles -> part, before its last
+  // barrier; the mappers publish before they issue the last block's stores,
+  // since a wait for loads (the reductions') also waits for stores issued
+  // before them
+  auto publish = [&]() {
+    hash = wave_sum(hash);
+    status = wave_or(status);
+    enib = wave_sum(enib);
+    if (lane == 0) {
+      part[wid] = hash;
+      part[kDecWaves + wid] = status;
+      part[2 * kDecWaves + wid] = enib;
+    }
+  };
   if (ok) {
     const uint8_t* cdata = a.payload + a.header_bytes + beg;
     const uint32_t* s32 = reinterpret_cast<const uint32_t*>(cdata + 4 * nst);
@@ -1803,10 +1816,11 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
     const int q16 = (int)((cb - 4 * nst) / 2);  // u16 words after the states (even)
 
     // decoded values of block j -> HBM, escapes resolved first
-    auto store_block = [&](int j) {
+    auto store_block = [&](int j, bool last) {
       const uint2* src = recs + (j & 1) * SB * kLanes;
       const bool any_esc = uni((int)ctl[4 + (j & 1)]) != 0;
       const uint32_t avail = (uint32_t)uni((int)ctl[1]);
+      uint32_t vals[kPer];
 #pragma unroll
       for (int e = 0; e < kPer; ++e) {
         const int u = (wid - 1) + kMappers * e;
@@ -1824,12 +1838,20 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
             esc_resolve<R>(em, (uint32_t)uni((int)ei.z), off, v, avail, fifo, enib, status, lane);
           }
         }
+        vals[e] = v;
+      }
+      if (last) publish();
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) {
+        const int u = (wid - 1) + kMappers * e;
+        if (SB % kMappers != 0 && u >= SB) break;
         const int p = lane + kLanes * (j * SB + u);
         if (p < len) {
           const int64_t i = row + start + p;
           if (kLatents)
-            a.out_y[i] = __fadd_rn((float)(int32_t)v, med[((j & 1) * SB + u) * kLanes + lane]);
-          else a.out_sym[i] = (int32_t)v;
+            a.out_y[i] = __fadd_rn((float)(int32_t)vals[e],
+                                   med[((j & 1) * SB + u) * kLanes + lane]);
+          else a.out_sym[i] = (int32_t)vals[e];
         }
       }
     };
@@ -1995,6 +2017,7 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
       pc.cycles(13);
       pc.mark(4);
       if (lane < A && x != kStateLow) status |= GAANS_ST_CORRUPT;
+      publish();
       __syncthreads();  // after the mappers' last store
     } else if (wid == kEscWave) {
       __syncthreads();
@@ -2004,13 +2027,14 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
                      lane);
         __syncthreads();
       }
+      publish();
       __syncthreads();
     } else {
       if (nblk > 0) map_block(0);
       __syncthreads();
       for (int j = 0; j < nblk; ++j) {
         // mappers: store block j - 1 and map block j + 1 while the coder decodes block j
-        if (j > 0) store_block(j - 1);
+        if (j > 0) store_block(j - 1, false);
         if (j + 1 < nblk) {
 #pragma unroll
           for (int e = 0; e < kPer; ++e) {
@@ -2022,19 +2046,15 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
         }
         __syncthreads();
       }
-      if (nblk > 0) store_block(nblk - 1);
+      if (nblk > 0) store_block(nblk - 1, true);
+      else publish();
       __syncthreads();
     }
   }
-  hash = wave_sum(hash);
-  status = wave_or(status);
-  enib = wave_sum(enib);
-  if (lane == 0) {
-    part[wid] = hash;
-    part[kDecWaves + wid] = status;
-    part[2 * kDecWaves + wid] = enib;
+  if (!ok) {  // uniform
+    publish();
+    __syncthreads();
   }
-  __syncthreads();
   if (tid == 0) {
     uint32_t hs = 0, st = 0, eq = 0;
     for (int w = 0; w < kDecWaves; ++w) {
@@ -2070,26 +2090,29 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
         }
       }
     }
-    // status and counter are agent-scope atomics; the status has completed
-    // before the counter is raised (no fence: decoded values need no
-    // visibility before the kernel ends)
-    if (st)
-      __hip_atomic_fetch_or(&a.ctrl[kCtrlDecStatus], st, __ATOMIC_RELAXED,
-                            __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // Completion counter: one u64, units done in the low half, the OR of
+    // the units' status bits in the high half.  A unit with status ORs it in
+    // first (and waits for it); atomics on one address take effect in
+    // program order, so the add that returns units - 1 done carries every
+    // unit's status.  No fence: decoded values need no visibility before
+    // the kernel ends.
+    uint64_t* done = reinterpret_cast<uint64_t*>(a.ctrl + kCtrlDecDone);
+    if (st) {
+      __hip_atomic_fetch_or(done, (uint64_t)st << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     pc.mark(5);
-    const uint32_t done = __hip_atomic_fetch_add(&a.ctrl[kCtrlDecDone], 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t old = __hip_atomic_fetch_add(done, 1ull, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
     pc.mark_after_loads(6);  // the atomic returned
     pc.store(a.phase, g, 0, 7);
-    if (done == (uint32_t)(a.units - 1)) {
-      const uint32_t all = __hip_atomic_exchange(&a.ctrl[kCtrlDecStatus], 0u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
+    if ((uint32_t)old == (uint32_t)(a.units - 1)) {
+      const uint32_t all = (uint32_t)(old >> 32);
       a.status_out[0] = all;
       // completion word with the status, one store (no system-wide write-back)
       __hip_atomic_store(&a.status_out[1], 1u | (all << 1), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_SYSTEM);
-      __hip_atomic_store(&a.ctrl[kCtrlDecDone], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(done, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       pc.store_done(a.phase, g);
     }
   }
