@@ -1085,12 +1085,17 @@ struct PackArgs {
 __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
   const int64_t g = blockIdx.x;
   const int tid = threadIdx.x;
+  // the unit's offsets, counts and hash are independent loads, issued
+  // together (not behind the offsets' bounds check)
   const uint32_t beg = g ? a.end_off[g - 1] : 0u;
   const uint32_t endo = a.end_off[g];
+  const int64_t W = a.chunk_words[g];
+  const uint2 ez = a.esc[g];  // escape count, escape nibbles
+  const uint32_t ihash = a.index_hash[g];
   uint32_t* __restrict__ hdr = reinterpret_cast<uint32_t*>(a.out);
   if (tid == 0) {
     hdr[kFixedWords + g] = endo;
-    hdr[kFixedWords + a.units + g] = a.index_hash[g];
+    hdr[kFixedWords + a.units + g] = ihash;
   }
   if (g == 0) {
     const TabHdr* th = reinterpret_cast<const TabHdr*>(a.tables);
@@ -1119,8 +1124,6 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
   if ((int64_t)a.header_bytes + endo > a.out_bytes || endo < beg) return;
   const int len = unit_len(g, (int32_t)a.K, (int32_t)a.S, a.N, (int32_t)a.chunk_len);
   const int A = len < kLanes ? len : kLanes;  // final states
-  const int64_t W = a.chunk_words[g];
-  const uint2 ez = a.esc[g];  // escape count, escape nibbles
   int64_t U = W + (ez.y + 3u) / 4u;
   U += U & 1;  // u16 words after the states: stream, pad, escape words
   uint8_t* dst = a.out + a.header_bytes + beg;
