@@ -44,7 +44,9 @@
  *    CUs, for 4 * 64 more bytes per extra unit.  Every unit holds at least
  *    one step: S <= the steps of a row's last (shortest) chunk.  The payload
  *    header records S and decode must be called with the same value.
- *    U = B * K * S coding units per call.
+ *    U = B * K * S coding units per call, at most 2^24 - 1, and a shape's
+ *    worst-case payload (7 bytes per symbol plus 264 per unit) must stay
+ *    below 2^38 bytes; larger calls return GAANS_EINVAL.
  *
  * Payload format "gaans-w64-v4": defined byte for byte by the CPU oracle,
  * oracle/gaans_oracle.c.

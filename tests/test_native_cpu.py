@@ -32,6 +32,19 @@ def test_host_selftest_division_constants():
     assert _native.lib().gaans_host_selftest() == 0, _native.last_error()
 
 
+def test_layout_limits_of_the_completion_counters():
+    # the encoder's completion counter is one 64-bit word: units in 24 bits,
+    # the payload body in 36 bits of u32 words; larger shapes are refused
+    # before any device work
+    from fast_compressai.coders import CoderInputError
+    assert _native.layout(2**24 - 1, 64, 1, 1).U == 2**24 - 1
+    with pytest.raises(CoderInputError, match="too many coding units"):
+        _native.layout(2**24, 64, 1, 1)
+    assert _native.layout(16, 2**30, 2**16, 1).U == 2**20  # 7.5e10-byte worst case
+    with pytest.raises(CoderInputError, match="shape too large"):
+        _native.layout(64, 2**30, 2**16, 1)  # 4.8e11 bytes >= 2^38
+
+
 def test_layout_matches_format():
     lay = _native.layout(1, 192 * 32 * 48, 192, 4)
     assert (lay.K, lay.chunk_len, lay.U, lay.HW, lay.S) == (48, 6144, 48, 1536, 1)
