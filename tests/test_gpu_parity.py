@@ -389,6 +389,14 @@ def test_out_of_range_index_rejected(backend, gpu_device, encoded):
     idx2[0, 17] = 192
     with pytest.raises(CoderInputError, match="outside"):
         backend.encode(sym, idx2, cdfs, sizes, offs, p_ch=4)
+    # two units (the first and the last chunk) report it in the same launch;
+    # the completion counter is left clean for the next call, whose payload
+    # is the one made before
+    idx2[0, idx.shape[1] - 1] = -1
+    with pytest.raises(CoderInputError, match="outside"):
+        backend.encode(sym, idx2, cdfs, sizes, offs, p_ch=4)
+    again = backend.encode(sym, idx, cdfs, sizes, offs, p_ch=4)
+    assert torch.equal(again.packed, payload.packed)
 
 
 def test_payload_bytes_round_trip(backend, gpu_device, encoded):
