@@ -148,6 +148,25 @@ __device__ __forceinline__ uint32_t wave_or(uint32_t v) {
   return v;
 }
 
+// Sum / OR over the wave's 64 lanes (all active), returned wave-uniform: a
+// scan inside each 16-lane row by DPP row shifts (lanes shifted in from
+// outside the row read 0), then the four rows' last lanes read out.  The
+// cross-lane steps are VALU operations of a few cycles each, where the
+// butterfly above waits for the LDS unit's permute six times.
+template <bool kOr>
+__device__ __forceinline__ uint32_t wave_fold_dpp(uint32_t v) {
+  auto step = [&](uint32_t t) { v = kOr ? (v | t) : (v + t); };
+  step((uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true));  // row_shr:1
+  step((uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true));  // row_shr:2
+  step((uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true));  // row_shr:4
+  step((uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true));  // row_shr:8
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 15);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 31);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 47);
+  const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+  return kOr ? (r0 | r1 | r2 | r3) : (r0 + r1 + r2 + r3);
+}
+
 __device__ __forceinline__ uint64_t wave_incl_scan(uint64_t v, int lane) {
   for (int off = 1; off < 64; off <<= 1) {
     const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)v, off, 64);
@@ -1000,9 +1019,9 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
     }
   }
 
-  hash = wave_sum(hash);
-  status = wave_or(status);
-  znib = wave_sum(znib);
+  hash = wave_fold_dpp<false>(hash);
+  status = wave_fold_dpp<true>(status);
+  znib = wave_fold_dpp<false>(znib);
   if (lane == 0) {
     part[wid] = hash;
     part[kWaves + wid] = status;
@@ -1803,9 +1822,9 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
   // since a wait for loads (the reductions') also waits for stores issued
   // before them
   auto publish = [&]() {
-    hash = wave_sum(hash);
-    status = wave_or(status);
-    enib = wave_sum(enib);
+    hash = wave_fold_dpp<false>(hash);
+    status = wave_fold_dpp<true>(status);
+    enib = wave_fold_dpp<false>(enib);
     if (lane == 0) {
       part[wid] = hash;
       part[kDecWaves + wid] = status;
