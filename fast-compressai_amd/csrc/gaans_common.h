@@ -169,7 +169,8 @@ uint32_t enc_magic(uint32_t f);
 struct Layout {
   int64_t B, N, C, P, S, HW, K, chunk_len, U, seg_cap, header_bytes, max_payload, cap_words,
       ws_bytes;
-  int64_t o_words_cnt, o_status, o_hash, o_end, o_info, o_states, o_words, o_esc, o_esc_raw;
+  int64_t o_words_cnt, o_status, o_hash, o_end, o_info, o_states, o_words, o_esc, o_esc_raw,
+      o_look;
 };
 int make_layout(int64_t B, int64_t N, int64_t C, int64_t P, int64_t S, Layout* L);
 

@@ -84,6 +84,9 @@ int make_layout(int64_t B, int64_t N, int64_t C, int64_t P, int64_t S, Layout* L
                 (long long)L->max_payload);
   L->cap_words = align_up(L->seg_cap + 2, 2);
   int64_t o = 0;
+  // the fused encode's look-back words first: their place does not depend
+  // on the shape, so one zeroing serves every shape that uses the workspace
+  L->o_look = o;      o = align_up(o + 8 * L->U, 256);
   L->o_words_cnt = o; o = align_up(o + 4 * L->U, 256);
   L->o_status = o;    o = align_up(o + 4 * L->U, 256);
   L->o_hash = o;      o = align_up(o + 4 * L->U, 256);
@@ -250,6 +253,7 @@ int gaans_get_layout(int64_t B, int64_t N, int64_t C, int64_t P, int32_t segment
   out->ws_words = L.o_words;
   out->ws_esc = L.o_esc;
   out->ws_esc_raw = L.o_esc_raw;
+  out->ws_look = L.o_look;
   return GAANS_OK;
 }
 

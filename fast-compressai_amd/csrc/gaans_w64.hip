@@ -68,8 +68,11 @@ constexpr int kMappers = GAANS_MAPPERS;  // mapper waves per decode workgroup
 constexpr int kEncMaxWaves = 9;
 
 // per-wave hash, status and escape nibbles, then the escape count, the unit's
-// word count and the completion counter's value
+// word count and the completion counter's value; the coder's final output
+// ring cursors in the last two words
 constexpr int kPartBytes = (12 * kEncMaxWaves + 12 + 15) / 16 * 16;
+constexpr int kPartWp = kPartBytes / 4 - 2, kPartFl = kPartBytes / 4 - 1;
+static_assert(kPartWp >= 3 * kEncMaxWaves + 3, "encoder LDS parts overlap");
 constexpr int kRingWords = 4096;       // encoder LDS output ring (u16 words), the most a plan uses
 constexpr int kPfU32Max = 8;  // decoder stream prefetch: u32 per lane (16-step blocks)
 // word 3 of a raw buffer resource on gfx9 (32-bit data format; stride 0, so
@@ -129,18 +132,26 @@ struct PhaseClock {
 // control block (u32 word indexes; the encoder's counter is a u64 at word 0);
 // encoder and decoder fields on separate 64-byte lines
 constexpr int kCtrlEncDone = 0;
-constexpr int kCtrlDecDone = 16;  // u64: units done, status << 32
+constexpr int kCtrlEncFin = 8;      // fused encode: units past their look-back
+constexpr int kCtrlDecDone = 16;    // u64: units done, status << 32
+constexpr int kCtrlEncTicket = 32;  // fused encode: unit numbers handed out
+
+// Look-back word of a unit (fused encode+pack), one u64 in the workspace:
+// flag in bits 62-63 (0: nothing yet, 1: the unit's own size, 2: its
+// inclusive prefix), status bits in 48-55, payload body u32 words in 0-39
+// (the host keeps the worst-case body below 2^36 words).
+constexpr uint64_t kLookAgg = 1ull << 62, kLookInc = 2ull << 62;
+constexpr int kLookStShift = 48;
+constexpr uint64_t kLookValMask = (1ull << 40) - 1;
+// a look-back gives up after this many ticks of the 100 MHz real-time
+// counter (10 s) and reports GAANS_ST_TIMEOUT: no kernel waits forever
+constexpr uint64_t kLookSpinTicks = 1000000000ull;
 
 // ---- wave helpers -----------------------------------------------------------
 
 __device__ __forceinline__ uint32_t lane_rank(uint64_t mask) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                    __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
-}
-
-__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
-  for (int off = 32; off > 0; off >>= 1) v += (uint32_t)__shfl_xor((int)v, off, 64);
-  return v;
 }
 
 __device__ __forceinline__ uint32_t wave_or(uint32_t v) {
@@ -471,6 +482,13 @@ struct EncArgs {
   uint32_t* __restrict__ esc_raw;   // per unit: seg_cap slots, filled from the end
   uint32_t* __restrict__ ctrl;
   uint64_t* __restrict__ info_out;
+  // pack fused into the coding kernel (NULL: stage 1 only, k_pack follows):
+  // the payload buffer (at least the layout's worst case) and the per-unit
+  // look-back words (workspace, zero before the launch and left zero)
+  uint8_t* __restrict__ out;
+  int64_t out_bytes;
+  uint64_t* __restrict__ look;
+  uint32_t B;
   PhaseBuf phase;
 };
 
@@ -798,6 +816,250 @@ __device__ __forceinline__ void enc_escapes(const uint4 r, uint32_t* __restrict_
   cnt = uni(cnt + __popcll(em));
 }
 
+// Escape section of a unit (NT threads of a workgroup): entry i (position
+// order, raw value lst[i], E entries) is the count n then the n nibbles of
+// raw, at nibble offset o_i = sum of (1 + n) over the entries before it.
+// Escape word j is the u16 at U - 1 - j of the unit's U u16 words after its
+// states (w32: those words as n32 = U / 2 u32), so the nibbles [8m, 8m + 8)
+// (escape words 2m, 2m + 1) form the u32 at n32 - 1 - m with its halves
+// swapped.  Entries share words: they are OR-ed into zeros, which the caller
+// has stored (and waited for) before the barrier that precedes this call.
+// wtot: NT / 64 u32 of LDS.
+template <int NT>
+__device__ void pack_escapes(const uint32_t* __restrict__ lst, uint32_t E, uint32_t* w32,
+                             int64_t n32, int tid, uint32_t* wtot) {
+  constexpr int kW = NT / kLanes;
+  const int wv = tid >> 6, lane = tid & (kLanes - 1);
+  uint32_t carry = 0;
+  for (uint32_t i0 = 0; i0 < E; i0 += NT) {
+    const uint32_t i = i0 + tid;
+    const uint32_t raw = i < E ? lst[i] : 0u;
+    const uint32_t n = raw ? ((31u - (uint32_t)__clz((int)raw)) >> 2) + 1u : 0u;
+    const uint32_t c = i < E ? n + 1u : 0u;
+    uint32_t incl = c;
+    for (int off = 1; off < kLanes; off <<= 1) {
+      const uint32_t o = (uint32_t)__shfl_up((int)incl, off, kLanes);
+      if (lane >= off) incl += o;
+    }
+    if (lane == kLanes - 1) wtot[wv] = incl;
+    __syncthreads();
+    uint32_t before = 0, total = 0;
+    for (int w = 0; w < kW; ++w) {
+      before += w < wv ? wtot[w] : 0u;
+      total += wtot[w];
+    }
+    __syncthreads();
+    const uint32_t o = carry + before + incl - c;
+    carry += total;
+    const uint64_t v = ((uint64_t)n | ((uint64_t)raw << 4)) << (4 * (o & 7u));
+    const int64_t m = o >> 3;
+    const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+    if (lo && m < n32)
+      __hip_atomic_fetch_or(&w32[n32 - 1 - m], (lo >> 16) | (lo << 16), __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    if (hi && m + 1 < n32)
+      __hip_atomic_fetch_or(&w32[n32 - 2 - m], (hi >> 16) | (hi << 16), __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// The 16 fixed header words (thread i < 16 writes word i) and the zero
+// padding after the unit tables (NT threads).
+template <int NT>
+__device__ __forceinline__ void write_fixed_header(uint32_t* hdr, int tid, uint32_t B,
+                                                   uint32_t N, uint32_t C, uint32_t P,
+                                                   uint32_t K, uint32_t chunk_len, uint32_t M,
+                                                   uint32_t S, uint32_t dig_lo, uint32_t dig_hi,
+                                                   int64_t units, int64_t header_bytes) {
+  if (tid < kFixedWords) {
+    uint32_t w = 0;
+    switch (tid) {
+      case 0: w = kMagic; break;
+      case 1: w = kVersion; break;
+      case 2: w = B; break;
+      case 3: w = N; break;
+      case 4: w = C; break;
+      case 5: w = P; break;
+      case 6: w = K; break;
+      case 7: w = chunk_len; break;
+      case 8: w = M; break;
+      case 9: w = kParams; break;
+      case 10: w = dig_lo; break;
+      case 11: w = dig_hi; break;
+      case 12: w = S; break;
+      default: w = 0; break;
+    }
+    hdr[tid] = w;
+  }
+  for (int64_t j = kFixedWords + 2 * units + tid; j < header_bytes / 4; j += NT) hdr[j] = 0;
+}
+
+// Sum over the wave's 64 lanes of values below 2^40 (a 24-bit low part and
+// the rest, each summed without overflow).
+__device__ __forceinline__ uint64_t wave_sum40(uint64_t v) {
+  const uint32_t lo = wave_fold_dpp<false>((uint32_t)v & 0xffffffu);
+  const uint32_t hi = wave_fold_dpp<false>((uint32_t)(v >> 24));
+  return (uint64_t)lo + ((uint64_t)hi << 24);
+}
+
+// Decoupled look-back of unit g (one whole wave): the exclusive prefix of
+// the payload body (u32 words) and the OR of the status bits of units
+// 0 .. g - 1.  Lane i reads the look-back word of unit j - i; the window
+// counts when every unit up to the nearest one with an inclusive prefix has
+// published its size (the prefix is then that inclusive value plus the
+// sizes after it), or when all 64 have sizes and none a prefix (the window
+// moves 64 units back).  Otherwise it reads again.  The words are agent-scope
+// atomics: only their own values are exchanged, so relaxed loads suffice.
+// After kLookSpinTicks the unit stops waiting and reports GAANS_ST_TIMEOUT
+// (its prefix is then at most the true one, so its copy stays in bounds).
+__device__ __forceinline__ uint64_t look_back(const uint64_t* look, int64_t g, int lane,
+                                              uint32_t& st) {
+  uint64_t excl = 0;
+  int64_t j = g - 1;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  while (j >= 0) {
+    const int64_t p = j - lane;
+    uint64_t v = kLookInc;  // before unit 0: an inclusive prefix of zero
+    if (p >= 0) v = __hip_atomic_load(&look[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t f = (uint32_t)(v >> 62);
+    const uint64_t inc = ballot(f == 2u), none = ballot(f == 0u);
+    // lanes up to and including the nearest inclusive prefix (all without one)
+    const uint64_t span = inc ? ((inc & (0ull - inc)) << 1) - 1ull : ~0ull;
+    if ((none & span) == 0ull) {
+      const uint64_t w = ((span >> lane) & 1ull) ? v : 0ull;
+      excl += wave_sum40(w & kLookValMask);
+      st |= wave_fold_dpp<true>((uint32_t)(w >> kLookStShift) & 0xffu);
+      if (inc) break;
+      j -= kLanes;
+      continue;
+    }
+    if (__builtin_amdgcn_s_memrealtime() - t0 > kLookSpinTicks) {
+      st |= GAANS_ST_TIMEOUT;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return excl;
+}
+
+// Completion of an encode launch (one thread): payload size and status to
+// the workspace and, when given, the caller's info words, the completion
+// word last (size and status in one 64-bit store, so the host can read it as
+// soon as it lands: no system-wide cache write-back).
+__device__ __forceinline__ void encode_complete(const EncArgs& a, uint64_t total, uint32_t st) {
+  a.ws_info[0] = total;
+  a.ws_info[1] = st;
+  if (a.info_out) {
+    a.info_out[0] = total;
+    a.info_out[1] = st;
+    __hip_atomic_store(&a.info_out[2], 1ull | ((uint64_t)st << 1) | (total << 16),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
+// Pack fused into the coding kernel (all NT threads of unit g's workgroup,
+// after the barrier that publishes the unit's parts): the first mapper wave
+// publishes the unit's size, looks back for its offset and publishes its
+// inclusive prefix; the unit with the last number writes the completion word
+// right away, and the last unit past its look-back clears the look-back
+// words and counters for the next launch.  Then the workgroup writes the
+// unit's header entries (unit 0 also the fixed header), its final states
+// (coder lanes), its words -- from the LDS ring, and from the staging slot
+// for the part flushed earlier -- and its escape section.  Replaces the
+// separate pack kernel (reference warp_ans_kernel_v2.cu:274-296).
+template <int NT, int kWaves>
+__device__ void fused_pack(const EncArgs& a, int64_t g, int tid, int lane, int wid, int A,
+                           uint32_t x, const uint32_t* part, const uint16_t* ring,
+                           uint32_t ring_mask, const uint16_t* __restrict__ wbuf, uint64_t* scr,
+                           uint32_t dig_lo, uint32_t dig_hi, PhaseClock& pc) {
+  uint32_t hs = 0, ss = 0, zs = 0;
+  for (int w = 0; w < kWaves; ++w) {
+    hs += part[w];
+    ss |= part[kWaves + w];
+    zs += part[2 * kWaves + w];
+  }
+  const uint32_t E = part[3 * kWaves];
+  const uint32_t W = part[3 * kWaves + 1];
+  const int wp = (int)part[kPartWp], fl = (int)part[kPartFl];
+  const uint64_t q = unit_quads(A, W, zs);  // this unit's u32 words
+  if (wid == 1) {
+    pc.mark(5);
+    if (g > 0 && lane == 0)
+      __hip_atomic_store(&a.look[g], kLookAgg | ((uint64_t)ss << kLookStShift) | q,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t st = ss;
+    const uint64_t excl = look_back(a.look, g, lane, st);
+    pc.mark_after_loads(6);
+    if (lane == 0) {
+      __hip_atomic_store(&a.look[g], kLookInc | ((uint64_t)(st & 0xffu) << kLookStShift) |
+                                         (excl + q),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      scr[0] = excl;
+      pc.store(a.phase, g, 5, 7);
+      if (g == a.units - 1) {
+        const uint64_t body = 4ull * (excl + q);
+        // unit end offsets are u32; a total past the buffer (look-back words
+        // not zeroed, against the contract) is reported the same way
+        if (body > 0xffffffffull || (uint64_t)a.header_bytes + body > (uint64_t)a.out_bytes)
+          st |= GAANS_ST_SIZE;
+        encode_complete(a, (uint64_t)a.header_bytes + body, st);
+        pc.store_done(a.phase, g);
+      }
+    }
+    // the last unit past its look-back: no unit reads look-back words any
+    // more, so they and the counters are cleared for the next launch
+    uint32_t fin = 0;
+    if (lane == 0)
+      fin = __hip_atomic_fetch_add(a.ctrl + kCtrlEncFin, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    fin = (uint32_t)__builtin_amdgcn_readfirstlane((int)fin);
+    if ((int64_t)fin == a.units - 1) {
+      for (int64_t p = lane; p < a.units; p += kLanes)
+        __hip_atomic_store(&a.look[p], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane == 0) {
+        __hip_atomic_store(a.ctrl + kCtrlEncFin, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.ctrl + kCtrlEncTicket, 0u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  if (tid == 0) pc.store(a.phase, g, 0, 5);  // the coder wave's points
+  __syncthreads();
+  const uint64_t excl = scr[0];
+  const int64_t off = a.header_bytes + 4 * (int64_t)excl;
+  if (off + 4 * (int64_t)q > a.out_bytes) return;  // uniform; the host sizes out for the worst case
+  uint32_t* hdr = reinterpret_cast<uint32_t*>(a.out);
+  if (tid == 0) {
+    hdr[kFixedWords + g] = (uint32_t)(4ull * (excl + q));
+    hdr[kFixedWords + a.units + g] = hs;
+  }
+  if (g == 0)
+    write_fixed_header<NT>(hdr, tid, a.B, (uint32_t)a.N, (uint32_t)a.C, (uint32_t)a.P,
+                           (uint32_t)a.K, (uint32_t)a.chunk_len, a.M, (uint32_t)a.S, dig_lo,
+                           dig_hi, a.units, a.header_bytes);
+  uint32_t* d32 = reinterpret_cast<uint32_t*>(a.out + off);
+  if (wid == 0 && lane < A) d32[lane] = x;
+  // u16 words after the states: stream, pad, escape words (zero here)
+  uint32_t U16 = W + (zs + 3u) / 4u;
+  U16 += U16 & 1u;
+  const int64_t n32 = U16 / 2;
+  uint32_t* w32 = d32 + A;
+  const int cap = a.cap_words;
+  for (int64_t j = tid; j < n32; j += NT) {
+    const int p0 = wp + 2 * (int)j, p1 = p0 + 1;
+    uint32_t lo = 0, hi = 0;
+    if (p0 < cap) lo = p0 < fl ? ring[p0 & ring_mask] : wbuf[p0];
+    if (p1 < cap) hi = p1 < fl ? ring[p1 & ring_mask] : wbuf[p1];
+    w32[j] = lo | (hi << 16);
+  }
+  if (E > 0) {  // uniform
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    pack_escapes<NT>(a.esc_raw + g * (int64_t)a.seg_cap + (a.seg_cap - E), E, w32, n32, tid,
+                     reinterpret_cast<uint32_t*>(scr + 2));
+  }
+}
+
 template <int kMode, bool kImplicit, int SB, int NM>
 __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
   using G = EncGeom<SB, NM>;
@@ -815,12 +1077,31 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
   uint2* lent = reinterpret_cast<uint2*>(smem + ring_bytes + G::kTail + 16 * a.nt_cap);
   float* scl = reinterpret_cast<float*>(smem + a.scales_lds);  // Gaussian: scale table
 
-  const int64_t g = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = tid & (kLanes - 1);
   const int wid = uni(tid >> 6);  // wave role, kept in a scalar register
   PhaseClock pc;
   if (wid == 0) pc.mark(0);
+  // the table blob's header does not depend on the unit: its load is in
+  // flight while the unit number is fetched
+  const TabHdr th = load_tab_hdr(a.tables);
+  const bool fused = a.out != nullptr;  // uniform: pack fused into this kernel
+  int64_t g = blockIdx.x;
+  if (fused) {
+    // Unit number from the launch's ticket counter, in the order the
+    // workgroups start: a unit's look-back only waits on units with lower
+    // numbers, which have started and run without waiting on it, so every
+    // wait ends whatever order or residency the hardware gives the grid.
+    if (tid == 0)
+      eflag[2] = __hip_atomic_fetch_add(a.ctrl + kCtrlEncTicket, 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    // a counter that did not start at zero (a control block shared or not
+    // zeroed, against the contract) still gives every unit number once, in
+    // range; the look-backs then end by their time limit
+    const uint32_t t = (uint32_t)uni((int)eflag[2]);
+    g = t < (uint64_t)a.units ? t : t % (uint32_t)a.units;
+  }
   int64_t row;
   int32_t start;
   int len, k;
@@ -840,10 +1121,9 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
   int t_lo, t_hi;
   stage_range(a.nt_cap, a.stage_all, k, a.P, (int)a.M, t_lo, t_hi);
   const TabMeta* __restrict__ gmeta = reinterpret_cast<const TabMeta*>(a.tables + a.blob.meta_off);
-  // the table blob's header and the staged range's metadata in one round
-  // trip (the metadata lies in the blob whatever its content and is used
-  // only when the header check passes)
-  const TabHdr th = load_tab_hdr(a.tables);
+  // the staged range's metadata in the same round trip as the blob header
+  // (the metadata lies in the blob whatever its content and is used only
+  // when the header check passes)
   const StageBounds bd = stage_bounds(gmeta, t_lo, t_hi, a.M, a.blob.total_dense);
   __builtin_amdgcn_sched_barrier(0);
   Tabs tb;
@@ -859,7 +1139,7 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
   // (steps a wave does not own keep these zeros)
   int32_t ca[kPer] = {}, cb[kPer] = {}, na[kPer] = {}, nb[kPer] = {};
   float cm[kPer] = {}, nm[kPer] = {};
-  auto load_block = [&](int j, int32_t* ia, int32_t* ib, float* im) {
+  auto load_block = [&](int j, int32_t* ia, int32_t* ib, float* im) __attribute__((always_inline)) {
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
       const int u = (wid - 1) + kEncMappers * e;
@@ -900,7 +1180,7 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
 
     // this wave's steps per block: u = wid - 1 + kEncMappers e < SB
     const int nvalid = SB % kEncMappers == 0 ? kPer : (SB - wid + kEncMappers) / kEncMappers;
-    auto map_steps = [&](int j, auto lds_tag) {
+    auto map_steps = [&](int j, auto lds_tag) __attribute__((always_inline)) {
       constexpr bool kLds = decltype(lds_tag)::value;
       uint4* dst = recs + (j & 1) * SB * kLanes;
       uint4 r[kPer];
@@ -928,7 +1208,7 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
       if (eb != 0u && lane == 0)
         __hip_atomic_fetch_or(&eflag[j & 1], eb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     };
-    auto map_block = [&](int j) {
+    auto map_block = [&](int j) __attribute__((always_inline)) {
       if (kMode == kModeGaussian)
         gauss_indexes<kPer>(cb, scl, a.n_scales, a.scales_pow2, a.scale_bound);
       // LDS tables for the whole block when every active lane's table is staged
@@ -1029,7 +1309,19 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
     if (wid == 0) {
       part[3 * kWaves] = (uint32_t)n_esc;
       part[3 * kWaves + 1] = (uint32_t)(a.cap_words - wp);
+      part[kPartWp] = (uint32_t)wp;
+      part[kPartFl] = (uint32_t)fl;
     }
+  }
+  if (fused) {
+    // the coder's ring flushes and escape list are in memory before the
+    // other waves read them back
+    if (wid == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    fused_pack<kThreads, kWaves>(a, g, tid, lane, wid, A, x, part, ring, ring_mask, wbuf,
+                                 reinterpret_cast<uint64_t*>(recs), th.digest_lo, th.digest_hi,
+                                 pc);
+    return;
   }
   __syncthreads();
   // The coder wave's last words and final states are stored only now: the
@@ -1118,27 +1410,8 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
   }
   if (g == 0) {
     const TabHdr* th = reinterpret_cast<const TabHdr*>(a.tables);
-    if (tid < kFixedWords) {
-      uint32_t w = 0;
-      switch (tid) {
-        case 0: w = kMagic; break;
-        case 1: w = kVersion; break;
-        case 2: w = a.B; break;
-        case 3: w = a.N32; break;
-        case 4: w = a.C; break;
-        case 5: w = a.P; break;
-        case 6: w = a.K; break;
-        case 7: w = a.chunk_len; break;
-        case 8: w = a.M; break;
-        case 9: w = kParams; break;
-        case 10: w = th->digest_lo; break;
-        case 11: w = th->digest_hi; break;
-        case 12: w = a.S; break;
-        default: w = 0; break;
-      }
-      hdr[tid] = w;
-    }
-    for (int64_t j = kFixedWords + 2 * a.units + tid; j < a.header_bytes / 4; j += 256) hdr[j] = 0;
+    write_fixed_header<256>(hdr, tid, a.B, a.N32, a.C, a.P, a.K, a.chunk_len, a.M, a.S,
+                            th->digest_lo, th->digest_hi, a.units, a.header_bytes);
   }
   if ((int64_t)a.header_bytes + endo > a.out_bytes || endo < beg) return;
   const int len = unit_len(g, (int32_t)a.K, (int32_t)a.S, a.N, (int32_t)a.chunk_len);
@@ -1157,48 +1430,12 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
     w32[j] = lo | (hi << 16);
   }
   if (ez.x == 0) return;
-  // Escape section: entry i (position order) is the count n then the n
-  // nibbles of raw, at nibble offset o_i = sum of (1 + n) over the entries
-  // before it.  Escape word j is the u16 at U - 1 - j, so the nibbles
-  // [8m, 8m + 8) (escape words 2m, 2m + 1) form the u32 at U / 2 - 1 - m with
-  // its halves swapped.  Entries share words: they are OR-ed into the zeros
-  // written above.
   __shared__ uint32_t wtot[4];
+  // the zeros above are stored before any wave ORs into them
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  const int wv = tid >> 6, lane = tid & 63;
   const uint32_t E = ez.x;
-  const uint32_t* __restrict__ lst = a.esc_raw + g * (int64_t)a.seg_cap + (a.seg_cap - E);
-  uint32_t carry = 0;
-  for (uint32_t i0 = 0; i0 < E; i0 += 256) {
-    const uint32_t i = i0 + tid;
-    const uint32_t raw = i < E ? lst[i] : 0u;
-    const uint32_t n = raw ? ((31u - (uint32_t)__clz((int)raw)) >> 2) + 1u : 0u;
-    const uint32_t c = i < E ? n + 1u : 0u;
-    uint32_t incl = c;
-    for (int off = 1; off < 64; off <<= 1) {
-      const uint32_t o = (uint32_t)__shfl_up((int)incl, off, 64);
-      if (lane >= off) incl += o;
-    }
-    if (lane == 63) wtot[wv] = incl;
-    __syncthreads();
-    uint32_t before = 0, total = 0;
-    for (int w = 0; w < 4; ++w) {
-      before += w < wv ? wtot[w] : 0u;
-      total += wtot[w];
-    }
-    __syncthreads();
-    const uint32_t o = carry + before + incl - c;
-    carry += total;
-    const uint64_t v = ((uint64_t)n | ((uint64_t)raw << 4)) << (4 * (o & 7u));
-    const int64_t m = o >> 3;
-    const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-    if (lo && m < n32)
-      __hip_atomic_fetch_or(&w32[n32 - 1 - m], (lo >> 16) | (lo << 16), __ATOMIC_RELAXED,
-                            __HIP_MEMORY_SCOPE_AGENT);
-    if (hi && m + 1 < n32)
-      __hip_atomic_fetch_or(&w32[n32 - 2 - m], (hi >> 16) | (hi << 16), __ATOMIC_RELAXED,
-                            __HIP_MEMORY_SCOPE_AGENT);
-  }
+  pack_escapes<256>(a.esc_raw + g * (int64_t)a.seg_cap + (a.seg_cap - E), E, w32, n32, tid, wtot);
 }
 
 // ============================================================================
@@ -2832,6 +3069,7 @@ int encode_prepare(int mode, bool implicit, int32_t n_scales, float scale_bound,
   a.cap_words = (int32_t)L.cap_words;
   a.units = L.U;
   a.header_bytes = L.header_bytes;
+  a.B = (uint32_t)L.B;
   a.nt_cap = st.nt_cap;
   a.stage_all = st.stage_all;
   a.ring_mask = (uint32_t)(plan.ring - 1);
@@ -2886,7 +3124,22 @@ void encode_bind(int mode, EncArgs& a, const Layout& L, const int32_t* symbols, 
   a.esc_raw = reinterpret_cast<uint32_t*>(w + L.o_esc_raw);
   a.ctrl = static_cast<uint32_t*>(ctrl);
   a.info_out = info_out;
+  a.look = reinterpret_cast<uint64_t*>(w + L.o_look);
+  a.out = nullptr;  // stage 1 only unless the caller fuses the pack (encode_fuse)
+  a.out_bytes = 0;
   a.phase = g_phase;
+}
+
+// Fuse the pack into an encode launch: the payload buffer must hold the
+// shape's worst case, since each unit writes at the offset its look-back
+// finds before the launch's size is known.
+int encode_fuse(EncArgs& a, const Layout& L, uint8_t* out, int64_t out_bytes) {
+  if (!out || out_bytes < L.max_payload)
+    return fail(GAANS_EINVAL, "payload buffer of %lld bytes, the shape's worst case is %lld",
+                (long long)out_bytes, (long long)L.max_payload);
+  a.out = out;
+  a.out_bytes = out_bytes;
+  return GAANS_OK;
 }
 
 int encode_launch(const EncLaunch& e, void* stream) {
@@ -2894,10 +3147,12 @@ int encode_launch(const EncLaunch& e, void* stream) {
   return check_launch("encode");
 }
 
+// out != NULL: the pack fused into the launch (payload buffer of out_bytes)
 int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y,
                   const float* medians, const int32_t* indexes, const GaussIn* g,
                   const gaans_tables* tables, int64_t B, int64_t N, int64_t C, int64_t P,
-                  int64_t S, void* ws, int64_t ws_bytes, void* ctrl, uint64_t* info_out) {
+                  int64_t S, void* ws, int64_t ws_bytes, void* ctrl, uint64_t* info_out,
+                  uint8_t* out = nullptr, int64_t out_bytes = 0) {
   Layout L;
   int rc = make_layout(B, N, C, P, S, &L);
   if (rc) return rc;
@@ -2910,6 +3165,7 @@ int encode_stage1(int mode, void* stream, const int32_t* symbols, const float* y
   if ((rc = encode_prepare(mode, implicit, g ? g->n : 0, g ? g->bound : 0.0f, tables, L, &e)))
     return rc;
   encode_bind(mode, e.a, L, symbols, y, medians, indexes, g, ws, ctrl, info_out);
+  if (out && (rc = encode_fuse(e.a, L, out, out_bytes))) return rc;
   return encode_launch(e, stream);
 }
 
@@ -3159,7 +3415,7 @@ int pack_launch(const PackArgs& a, void* stream) {
 }
 
 // ---- call plans -----------------------------------------------------------
-// A plan holds an encode (launch + pack) or decode launch with every
+// A plan holds an encode (pack fused) or decode launch with every
 // shape-dependent field filled; a run copies it, sets the call's pointers and
 // launches.  Stored in the caller's gaans_plan (opaque bytes).
 constexpr uint32_t kPlanEncMagic = 0x4E504147u;  // "GAPN" (encode)
@@ -3173,7 +3429,6 @@ struct PlanHead {
 struct EncPlanRec {
   PlanHead h;
   EncLaunch e;
-  PackArgs pack;
 };
 struct DecPlanRec {
   PlanHead h;
@@ -3216,8 +3471,9 @@ int wait_word(void* stream, const uint32_t* word) {
   }
 }
 
-__global__ __launch_bounds__(kLanes) void k_clear_words(uint32_t* __restrict__ p, int n) {
-  for (int i = threadIdx.x; i < n; i += kLanes) p[i] = 0u;
+__global__ __launch_bounds__(256) void k_clear_words(uint32_t* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    p[i] = 0u;
 }
 
 }  // namespace
@@ -3232,9 +3488,10 @@ static __device__ __align__(256) uint8_t scratch[GAANS_NOALLOC_SCRATCH_BYTES];
 namespace {
 
 // Address of `scratch` on the current device, looked up once per device
-// (with that device current) and its control block cleared on `stream`
-// before the first call that uses it; the encode kernels leave the control
-// block zeroed again after every launch.
+// (with that device current) and cleared on `stream` before the first call
+// that uses it (control block and workspace, whose look-back words the fused
+// encode needs zeroed); the encode kernels leave the control block and the
+// look-back words zeroed again after every launch.
 int noalloc_scratch(hipStream_t stream, uint8_t** out) {
   static std::mutex mu;
   static uint8_t* addr[kMaxDevices];
@@ -3248,7 +3505,8 @@ int noalloc_scratch(hipStream_t stream, uint8_t** out) {
     if (e != hipSuccess || !p)
       return fail(GAANS_EHIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
                   hipGetErrorString(e));
-    k_clear_words<<<1, kLanes, 0, stream>>>(static_cast<uint32_t*>(p), GAANS_CTRL_BYTES / 4);
+    k_clear_words<<<256, 256, 0, stream>>>(static_cast<uint32_t*>(p),
+                                           (int64_t)GAANS_NOALLOC_SCRATCH_BYTES / 4);
     const int rc = check_launch("scratch clear");
     if (rc) return rc;
     addr[dev] = static_cast<uint8_t*>(p);
@@ -3327,17 +3585,18 @@ int gaans_encode_symbols_noalloc(void* stream, const int32_t* symbols_dev,
                 (long long)B, (long long)N, (long long)P, (long long)need,
                 (long long)GAANS_NOALLOC_SCRATCH_BYTES);
   if (!info_out) return fail(GAANS_EINVAL, "info_out pointer is NULL");
-  if (!out_dev || out_bytes < L.header_bytes)
-    return fail(GAANS_EINVAL, "output buffer smaller than the payload header");
+  // every unit writes at the offset its look-back finds: the buffer must
+  // hold the worst case (also checked by encode_fuse, before any device work)
+  if (!out_dev || out_bytes < L.max_payload)
+    return fail(GAANS_EINVAL, "payload buffer of %lld bytes, the shape's worst case is %lld",
+                (long long)out_bytes, (long long)L.max_payload);
   uint8_t* base = nullptr;
   if ((rc = noalloc_scratch(static_cast<hipStream_t>(stream), &base))) return rc;
   void* ctrl = base;
   void* ws = base + GAANS_CTRL_BYTES;
-  rc = encode_stage1(kModeSymbols, stream, symbols_dev, nullptr, nullptr, indexes_dev, nullptr,
-                     tables, B, N, C, P, segments, ws, L.ws_bytes, ctrl, info_out);
-  if (rc) return rc;
-  return gaans_encode_pack(stream, ws, L.ws_bytes, tables, B, N, C, P, segments, out_dev,
-                           out_bytes);
+  return encode_stage1(kModeSymbols, stream, symbols_dev, nullptr, nullptr, indexes_dev, nullptr,
+                       tables, B, N, C, P, segments, ws, L.ws_bytes, ctrl, info_out, out_dev,
+                       out_bytes);
 }
 
 int gaans_decode_symbols(void* stream, const uint8_t* payload_dev, int64_t payload_bytes,
@@ -3390,7 +3649,6 @@ int gaans_plan_encode(const gaans_tables* tables, int32_t mode, int32_t explicit
   const bool implicit = mode != GAANS_MODE_GAUSSIAN && !explicit_indexes;
   if ((rc = encode_prepare(mode, implicit, n_scales, scale_bound, tables, r->h.L, &r->e)))
     return rc;
-  pack_prepare(tables, r->h.L, r->pack);
   r->h.mode = mode;
   r->h.implicit = implicit;
   if (hipGetDevice(&r->h.dev) != hipSuccess) return fail(GAANS_EHIP, "hipGetDevice failed");
@@ -3421,15 +3679,23 @@ int gaans_run_encode(const gaans_plan* plan, void* stream, const void* in0, cons
                      const void* in2, const void* in3, void* workspace_dev,
                      int64_t workspace_bytes, void* ctrl_dev, uint8_t* out_dev,
                      int64_t out_bytes, uint64_t* info_host) {
+  if (!info_host) return fail(GAANS_EINVAL, "info_host pointer is NULL");
+  uint32_t* done = reinterpret_cast<uint32_t*>(&info_host[2]);  // low half of info[2]
+  __atomic_store_n(done, 0u, __ATOMIC_RELEASE);
+  const int rc = gaans_enqueue_encode(plan, stream, in0, in1, in2, in3, workspace_dev,
+                                      workspace_bytes, ctrl_dev, out_dev, out_bytes, info_host);
+  return rc ? rc : wait_word(stream, done);
+}
+
+int gaans_enqueue_encode(const gaans_plan* plan, void* stream, const void* in0, const void* in1,
+                         const void* in2, const void* in3, void* workspace_dev,
+                         int64_t workspace_bytes, void* ctrl_dev, uint8_t* out_dev,
+                         int64_t out_bytes, uint64_t* info_out) {
   const EncPlanRec* r = reinterpret_cast<const EncPlanRec*>(plan);
   if (!r || r->h.magic != kPlanEncMagic)
     return fail(GAANS_EINVAL, "not an encode plan (gaans_plan_encode)");
   const Layout& L = r->h.L;
   const int mode = r->h.mode;
-  if (!info_host) return fail(GAANS_EINVAL, "info_host pointer is NULL");
-  if (!out_dev || out_bytes < L.max_payload)
-    return fail(GAANS_EINVAL, "payload buffer of %lld bytes, the plan's worst case is %lld",
-                (long long)out_bytes, (long long)L.max_payload);
   const int32_t* symbols = nullptr;
   const int32_t* indexes = nullptr;
   const float *y = nullptr, *medians = nullptr;
@@ -3451,18 +3717,25 @@ int gaans_run_encode(const gaans_plan* plan, void* stream, const void* in0, cons
                         workspace_bytes, ctrl_dev);
   if (rc || (rc = plan_device(r->h))) return rc;
   EncLaunch e = r->e;
-  encode_bind(mode, e.a, L, symbols, y, medians, indexes, &g, workspace_dev, ctrl_dev, info_host);
-  PackArgs pk = r->pack;
-  pack_bind(pk, L, workspace_dev, out_dev, out_bytes);
-  uint32_t* done = reinterpret_cast<uint32_t*>(&info_host[2]);  // low half of info[2]
-  __atomic_store_n(done, 0u, __ATOMIC_RELEASE);
-  if ((rc = encode_launch(e, stream)) || (rc = pack_launch(pk, stream))) return rc;
-  return wait_word(stream, done);
+  encode_bind(mode, e.a, L, symbols, y, medians, indexes, &g, workspace_dev, ctrl_dev, info_out);
+  if ((rc = encode_fuse(e.a, L, out_dev, out_bytes))) return rc;
+  return encode_launch(e, stream);
 }
 
 int gaans_run_decode(const gaans_plan* plan, void* stream, const uint8_t* payload_dev,
                      int64_t payload_bytes, const void* in0, const void* in1, const void* in2,
                      void* out_dev, void* ctrl_dev, uint32_t* status_host) {
+  if (!status_host) return fail(GAANS_EINVAL, "status pointer is NULL");
+  uint32_t* done = status_host + 1;
+  __atomic_store_n(done, 0u, __ATOMIC_RELEASE);
+  const int rc = gaans_enqueue_decode(plan, stream, payload_dev, payload_bytes, in0, in1, in2,
+                                      out_dev, ctrl_dev, status_host);
+  return rc ? rc : wait_word(stream, done);
+}
+
+int gaans_enqueue_decode(const gaans_plan* plan, void* stream, const uint8_t* payload_dev,
+                         int64_t payload_bytes, const void* in0, const void* in1,
+                         const void* in2, void* out_dev, void* ctrl_dev, uint32_t* status_host) {
   const DecPlanRec* r = reinterpret_cast<const DecPlanRec*>(plan);
   if (!r || r->h.magic != kPlanDecMagic)
     return fail(GAANS_EINVAL, "not a decode plan (gaans_plan_decode)");
@@ -3486,10 +3759,7 @@ int gaans_run_decode(const gaans_plan* plan, void* stream, const uint8_t* payloa
   DecLaunch e = r->e;
   decode_bind(mode, e.a, payload_dev, payload_bytes, indexes, &g, medians, out_dev, ctrl_dev,
               status_host);
-  uint32_t* done = status_host + 1;
-  __atomic_store_n(done, 0u, __ATOMIC_RELEASE);
-  if ((rc = decode_launch(e, stream))) return rc;
-  return wait_word(stream, done);
+  return decode_launch(e, stream);
 }
 
 int gaans_debug_phases(void* buffer_dev, int64_t units, int32_t* wall_clock_khz) {

@@ -15,7 +15,7 @@ import threading
 from .errors import CoderDependencyError
 
 LIB_NAME = "libgaans_w64.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 CTRL_BYTES = 256
 PLAN_BYTES = 1536  # GAANS_PLAN_BYTES
 PHASE_SLOTS = 16  # GAANS_PHASE_SLOTS
@@ -33,6 +33,7 @@ ST_TABLES = 0x08
 ST_CORRUPT = 0x10
 ST_INDEXHASH = 0x20
 ST_SIZE = 0x40
+ST_TIMEOUT = 0x80
 
 STATUS_TEXT = {
     ST_RANGE: "a symbol cannot be coded (escape value >= 2^32 or non-finite latent)",
@@ -42,13 +43,14 @@ STATUS_TEXT = {
     ST_CORRUPT: "payload chunk offsets or rANS stream are corrupt",
     ST_INDEXHASH: "indexes do not match the payload",
     ST_SIZE: "payload would exceed the 4 GiB format limit",
+    ST_TIMEOUT: "an encode unit gave up waiting for the units before it",
 }
 
 
 _LAYOUT_FIELDS = ("B", "N", "C", "P", "S", "HW", "K", "chunk_len", "U", "header_bytes",
                   "max_payload_bytes", "cap_words", "workspace_bytes", "ws_chunk_words",
                   "ws_chunk_status", "ws_index_hash", "ws_end_off", "ws_info", "ws_states",
-                  "ws_words", "ws_esc", "ws_esc_raw")
+                  "ws_words", "ws_esc", "ws_esc_raw", "ws_look")
 
 
 class Layout(ctypes.Structure):
@@ -128,6 +130,8 @@ def _declare(L) -> None:
         "gaans_plan_decode": ([T, i32, i32, i32, f32, i64, i64, i64, i64, i32, p], ctypes.c_int),
         "gaans_run_encode": ([p, p, p, p, p, p, p, i64, p, p, i64, p], ctypes.c_int),
         "gaans_run_decode": ([p, p, p, i64, p, p, p, p, p, p], ctypes.c_int),
+        "gaans_enqueue_encode": ([p, p, p, p, p, p, p, i64, p, p, i64, p], ctypes.c_int),
+        "gaans_enqueue_decode": ([p, p, p, i64, p, p, p, p, p, p], ctypes.c_int),
         "gaans_host_selftest": ([], ctypes.c_int),
     }
     for name, (args, res) in sig.items():

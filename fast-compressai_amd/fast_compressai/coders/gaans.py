@@ -1,20 +1,24 @@
 """Device-side GA-ANS engine: thin wrappers over the C ABI.
 
 Per (device, stream) the engine keeps a control block (device memory, zeroed
-once; every launch leaves it zeroed), a reusable workspace, and two small
-pinned host buffers that the kernels' last workgroup writes the payload
-size / status into, and a completion word that carries both.  Calls on one stream are
-ordered, so these buffers are never shared by two calls in flight.
+once; every launch leaves it zeroed), a reusable workspace (zeroed when it
+is allocated: the fused encode's look-back words must start at zero, and
+every launch leaves them so), and two small pinned host buffers that the
+kernels write the payload size / status into, and a completion word that
+carries both.  The device orders calls on one stream; the pinned words are
+also shared by the host threads that call on that stream, so a lock per
+(device, stream) is held from a call's launch until its words are read.
 
 Each shape gets a call plan (``gaans_plan_encode`` / ``gaans_plan_decode``:
 layout, LDS plan, kernel variant and argument block, computed once and kept
 with the prepared tables), so a call is one short C call.  Encode
-(``gaans_run_encode``) enqueues the coding kernel and the pack kernel back
-to back (the pack writes into a worst-case-sized buffer), then waits for
-the coding kernel's completion word and reads the payload size; the pack
-kernel may still be running when encode returns, ordered before any later
-work on the stream.  Decode (``gaans_run_decode``) enqueues one kernel and
-waits for its completion word to read the status word.  Reference host APIs replaced:
+(``gaans_run_encode``) enqueues one kernel that codes and packs into a
+worst-case-sized buffer (each unit finds its payload offset by a decoupled
+look-back over the units before it), then waits for the completion word
+and reads the payload size; other units may still be writing their words
+when encode returns, ordered before any later work on the stream.  Decode
+(``gaans_run_decode``) enqueues one kernel and waits for its completion word
+to read the status word.  Reference host APIs replaced:
 ``encode_with_indexes_warp_v2_cuda`` (``warp_ans_kernel_v2.cu:183-306``, two
 syncs and six launches) and ``decode_with_indexes_warp_cuda``
 (``warp_ans_kernel.cu:477-544``, one sync and four launches).
@@ -46,12 +50,15 @@ class _StreamState:
         self.ctrl_ptr = self.ctrl.data_ptr()
         self.info_ptr = self.info.data_ptr()
         self.status_ptr = self.status.data_ptr()
-        self.workspace = torch.empty(0, dtype=torch.uint8, device=device)
+        self.workspace = torch.zeros(0, dtype=torch.uint8, device=device)
         self.device = device
+        self.lock = threading.Lock()
 
     def ws(self, nbytes: int) -> torch.Tensor:
+        """The workspace, grown (and zeroed) when a shape needs more; the
+        caller holds ``lock``."""
         if self.workspace.numel() < nbytes:
-            self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+            self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
         return self.workspace
 
 
@@ -226,14 +233,15 @@ def _run_encode(tables: PreparedTables, mode: int, explicit: bool, B: int, N: in
         _, plan, lay = _plan(tables, False, mode, explicit, B, N, C, P, S, index, n_scales, bound)
         sp = torch._C._cuda_getCurrentRawStream(index)
         st = _state(index, sp)
-        ws = st.ws(lay.workspace_bytes)
         out = torch.empty(lay.max_payload_bytes, dtype=torch.uint8, device=st.device)
-        rc = _native.lib().gaans_run_encode(plan, sp, in0, in1, in2, in3, ws.data_ptr(),
-                                            ws.numel(), st.ctrl_ptr, out.data_ptr(),
-                                            lay.max_payload_bytes, st.info_ptr)
+        with st.lock:
+            ws = st.ws(lay.workspace_bytes)
+            rc = _native.lib().gaans_run_encode(plan, sp, in0, in1, in2, in3, ws.data_ptr(),
+                                                ws.numel(), st.ctrl_ptr, out.data_ptr(),
+                                                lay.max_payload_bytes, st.info_ptr)
+            word = int(st.info_np[2])  # 1 | status << 1 | payload bytes << 16
         if rc:
             _native.check(rc, what)
-        word = int(st.info_np[2])  # 1 | status << 1 | payload bytes << 16
     finally:
         if prev is not None:
             torch.cuda.set_device(prev)
@@ -257,12 +265,13 @@ def _run_decode(tables: PreparedTables, mode: int, explicit: bool, B: int, N: in
         sp = torch._C._cuda_getCurrentRawStream(index)
         st = _state(index, sp)
         out = torch.empty((B, N), dtype=dtype, device=st.device)
-        rc = _native.lib().gaans_run_decode(plan, sp, packed.data_ptr(), packed.numel(), in0,
-                                            in1, in2, out.data_ptr(), st.ctrl_ptr,
-                                            st.status_ptr)
+        with st.lock:
+            rc = _native.lib().gaans_run_decode(plan, sp, packed.data_ptr(), packed.numel(), in0,
+                                                in1, in2, out.data_ptr(), st.ctrl_ptr,
+                                                st.status_ptr)
+            status = int(st.status_np[1]) >> 1  # 1 | status << 1
         if rc:
             _native.check(rc, what)
-        status = int(st.status_np[1]) >> 1  # 1 | status << 1
     finally:
         if prev is not None:
             torch.cuda.set_device(prev)
@@ -344,18 +353,18 @@ def decode_rans64(streams: torch.Tensor, offsets: torch.Tensor, tables: Prepared
     try:
         sp = torch._C._cuda_getCurrentRawStream(index)
         st = _state(index, sp)
-        st.status_np[1] = 0
         out = torch.empty((B, N), dtype=torch.int32, device=dev)
-        rc = L.gaans_rans64_decode(sp, streams.data_ptr() if streams.numel() else None,
-                                   streams.numel(), offsets.data_ptr(), _ptr(indexes),
-                                   tables.ref, B, N, C, out.data_ptr(), st.ctrl_ptr,
-                                   st.status_ptr)
+        with st.lock:
+            st.status_np[1] = 0
+            rc = L.gaans_rans64_decode(sp, streams.data_ptr() if streams.numel() else None,
+                                       streams.numel(), offsets.data_ptr(), _ptr(indexes),
+                                       tables.ref, B, N, C, out.data_ptr(), st.ctrl_ptr,
+                                       st.status_ptr)
+            if rc == 0:
+                rc = L.gaans_wait_host_word(sp, st.status_done)
+            status = int(st.status_np[1]) >> 1
         if rc:
             _native.check(rc, "Rans64 decode")
-        rc = L.gaans_wait_host_word(sp, st.status_done)
-        if rc:
-            _native.check(rc, "Rans64 decode")
-        status = int(st.status_np[1]) >> 1
     finally:
         if prev is not None:
             torch.cuda.set_device(prev)

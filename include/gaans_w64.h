@@ -61,7 +61,7 @@
 extern "C" {
 #endif
 
-#define GAANS_ABI_VERSION 11
+#define GAANS_ABI_VERSION 12
 #define GAANS_CTRL_BYTES 256
 
 /* return codes */
@@ -78,6 +78,7 @@ extern "C" {
 #define GAANS_ST_CORRUPT 0x10u   /* unit offsets or rANS stream inconsistent */
 #define GAANS_ST_INDEXHASH 0x20u /* payload made with other indexes */
 #define GAANS_ST_SIZE 0x40u      /* payload would exceed the 4 GiB format limit */
+#define GAANS_ST_TIMEOUT 0x80u   /* a fused encode unit waited 10 s for the units before it */
 
 /* Shape of one coding call (pure host arithmetic, see gaans_get_layout). */
 typedef struct gaans_layout {
@@ -92,6 +93,11 @@ typedef struct gaans_layout {
   /* byte offsets inside the encode workspace */
   int64_t ws_chunk_words, ws_chunk_status, ws_index_hash, ws_end_off, ws_info,
       ws_states, ws_words, ws_esc, ws_esc_raw;
+  /* the fused encode's look-back words (8 bytes per unit, at offset 0, so
+   * that their place does not depend on the shape): zero before the first
+   * fused encode (gaans_run_encode, gaans_enqueue_encode) that uses the
+   * workspace; every such launch leaves them zero */
+  int64_t ws_look;
 } gaans_layout;
 
 /* Prepared tables: filled by gaans_tables_prepare except `dev`, which the
@@ -226,19 +232,20 @@ int gaans_encode_pack(void* stream, const void* workspace_dev, int64_t workspace
                       const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
                       int64_t P, int32_t segments, uint8_t* out_dev, int64_t out_bytes);
 
-/* Stage 1 and stage 2 of gaans_encode_symbols in one call that allocates
- * nothing and takes no workspace or control block: both live in a static
- * device array of GAANS_NOALLOC_SCRATCH_BYTES per GPU (its control block
- * first, GAANS_CTRL_BYTES, then the workspace), held until the process ends.
- * The caller passes the inputs, the payload buffer (out_dev, out_bytes; as in
- * gaans_encode_pack, best sized to layout->max_payload_bytes) and info_out
- * (3 u64 in device or pinned host memory, as in gaans_encode_symbols; the
- * completion word info_out[2] carries size and status).  The first call on a
- * GPU looks the array up and clears its control block on `stream`; the
- * kernels leave it zeroed after every launch.  Shapes whose control block and
- * workspace exceed the array return GAANS_EINVAL before any device work.
- * Every call on one GPU shares the array: calls that overlap on one GPU (other
- * streams, other threads) race and must be ordered by the caller.
+/* gaans_encode_symbols + gaans_encode_pack as one fused kernel (as
+ * gaans_run_encode) in a call that allocates nothing and takes no workspace
+ * or control block: both live in a static device array of
+ * GAANS_NOALLOC_SCRATCH_BYTES per GPU (its control block first,
+ * GAANS_CTRL_BYTES, then the workspace), held until the process ends.  The
+ * caller passes the inputs, the payload buffer (out_dev, out_bytes: at least
+ * layout->max_payload_bytes, else GAANS_EINVAL) and info_out (3 u64 in device
+ * or pinned host memory, as in gaans_encode_symbols; the completion word
+ * info_out[2] carries size and status).  The first call on a GPU looks the
+ * array up and clears it on `stream`; the kernels leave its control block
+ * and look-back words zeroed after every launch.  Shapes whose control block
+ * and workspace exceed the array return GAANS_EINVAL before any device work.
+ * Every call on one GPU shares the array: calls that overlap on one GPU
+ * (other streams, other threads) race and must be ordered by the caller.
  * No counterpart in the reference: this entry point is for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  Calls no hipMalloc / hipFree. */
@@ -319,9 +326,10 @@ int gaans_wait_host_word(void* stream, const uint32_t* word);
  * decode launch -- layout, LDS staging plan, kernel variant, launch geometry
  * and argument block -- computed once by gaans_plan_encode / gaans_plan_decode
  * with the device it will run on current.  gaans_run_encode / gaans_run_decode
- * then only set the call's pointers, enqueue and wait: the same kernels and
- * bytes as the gaans_encode_* + gaans_encode_pack + gaans_wait_host_word and
- * gaans_decode_* + gaans_wait_host_word sequences, without recomputing the
+ * then only set the call's pointers, enqueue and wait: the same bytes as the
+ * gaans_encode_* + gaans_encode_pack + gaans_wait_host_word and
+ * gaans_decode_* + gaans_wait_host_word sequences (the encode in one fused
+ * kernel instead of two), without recomputing the
  * plan or converting a long argument list on every call.  A plan refers to
  * the table blob at tables->dev: the blob must outlive every run of the plan.
  * A plan is plain bytes owned by the caller; runs only read it, so one plan
@@ -352,23 +360,40 @@ int gaans_plan_decode(const gaans_tables* tables, int32_t mode, int32_t explicit
                       int32_t n_scales, float scale_bound, int64_t B, int64_t N, int64_t C,
                       int64_t P, int32_t segments, gaans_plan* plan);
 
-/* Encode with a plan: enqueue the coding and pack kernels on `stream` into
- * out_dev (at least the layout's max_payload_bytes), then wait for the
- * completion word info_host[2] (pinned host memory, 3 u64; the run clears it
- * before the launch).  On return info_host[2] = 1 | status << 1 | payload
- * bytes << 16, as for gaans_encode_symbols; the pack kernel may still run,
- * ordered on `stream`.  Device inputs by mode:
+/* Encode with a plan: enqueue one kernel on `stream` that codes every unit
+ * and packs the payload into out_dev (at least the layout's
+ * max_payload_bytes), then wait for the completion word info_host[2]
+ * (pinned host memory, 3 u64; the run clears it before the launch).  On
+ * return info_host[2] = 1 | status << 1 | payload bytes << 16, as for
+ * gaans_encode_symbols; the kernel may still be writing other units' words,
+ * ordered on `stream` before any later work.  The pack is fused: each unit
+ * takes its number from a ticket counter in the control block, publishes its
+ * size, finds its payload offset by a decoupled look-back over the units
+ * before it (workspace words at layout->ws_look, which must be zero before
+ * the first such launch on a workspace; every launch leaves them zero) and
+ * writes its own part of the payload.  Device inputs by mode:
  *   GAANS_MODE_SYMBOLS:  in0 symbols int32 [B, N], in1 indexes int32 [B, N]
  *                        (NULL for a table = channel plan)
  *   GAANS_MODE_LATENTS:  in0 y fp32 [B, N], in1 medians fp32 [C], in2 indexes
  *                        (as above)
  *   GAANS_MODE_GAUSSIAN: in0 y, in1 means (or NULL), in2 scales, all fp32
  *                        [B, N]; in3 the scale table (n_scales fp32)
- * Unused inputs are ignored. */
+ * Unused inputs are ignored.  Reference: encode_with_indexes_warp_v2_cuda
+ * (warp_ans_kernel_v2.cu:183-306: six launches and two host syncs). */
 int gaans_run_encode(const gaans_plan* plan, void* stream, const void* in0, const void* in1,
                      const void* in2, const void* in3, void* workspace_dev,
                      int64_t workspace_bytes, void* ctrl_dev, uint8_t* out_dev,
                      int64_t out_bytes, uint64_t* info_host);
+
+/* gaans_run_encode without the wait: enqueue the fused encode kernel and
+ * return.  info_out (3 u64, device or pinned host memory) receives the
+ * payload size, status and completion word as for gaans_encode_symbols.  For
+ * callers that order their own work after the encode (graph capture,
+ * pipelines, kernel timing).  No counterpart in the reference. */
+int gaans_enqueue_encode(const gaans_plan* plan, void* stream, const void* in0, const void* in1,
+                         const void* in2, const void* in3, void* workspace_dev,
+                         int64_t workspace_bytes, void* ctrl_dev, uint8_t* out_dev,
+                         int64_t out_bytes, uint64_t* info_out);
 
 /* Decode with a plan into out_dev (int32 symbols for GAANS_MODE_SYMBOLS, fp32
  * y_hat otherwise, [B, N]) and wait for the completion word status_host[1]
@@ -380,6 +405,13 @@ int gaans_run_encode(const gaans_plan* plan, void* stream, const void* in0, cons
 int gaans_run_decode(const gaans_plan* plan, void* stream, const uint8_t* payload_dev,
                      int64_t payload_bytes, const void* in0, const void* in1, const void* in2,
                      void* out_dev, void* ctrl_dev, uint32_t* status_host);
+
+/* gaans_run_decode without the wait: enqueue the decode kernel and return;
+ * status_out (2 u32, device or pinned host memory) as for
+ * gaans_decode_symbols.  No counterpart in the reference. */
+int gaans_enqueue_decode(const gaans_plan* plan, void* stream, const uint8_t* payload_dev,
+                         int64_t payload_bytes, const void* in0, const void* in1,
+                         const void* in2, void* out_dev, void* ctrl_dev, uint32_t* status_out);
 
 /* ---- measurement ------------------------------------------------------------ */
 

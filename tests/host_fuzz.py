@@ -35,7 +35,7 @@ class Layout(ctypes.Structure):  # gaans_layout
         "B", "N", "C", "P", "S", "HW", "K", "chunk_len", "U", "header_bytes",
         "max_payload_bytes", "cap_words", "workspace_bytes", "ws_chunk_words",
         "ws_chunk_status", "ws_index_hash", "ws_end_off", "ws_info", "ws_states", "ws_words",
-        "ws_esc", "ws_esc_raw")]
+        "ws_esc", "ws_esc_raw", "ws_look")]
 
 
 def load(path):

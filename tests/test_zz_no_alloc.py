@@ -1,8 +1,9 @@
-"""The no-allocation encode entry point (gaans_encode_symbols_noalloc): its
-payload bytes equal those of gaans_encode_symbols + gaans_encode_pack with a
-caller workspace, on two calls in a row (the second with a smaller input, so
-that stale scratch contents from the first would show), and shapes beyond its
-static scratch are rejected before any device work."""
+"""The no-allocation encode entry point (gaans_encode_symbols_noalloc, one
+fused encode+pack kernel over a static device scratch): its payload bytes
+equal those of the workspace encode and of the oracle on two calls in a row
+(the second with a smaller input, so that stale scratch contents from the
+first would show); shapes beyond its static scratch and payload buffers
+below the shape's worst case are rejected before any device work."""
 
 import ctypes
 
@@ -71,3 +72,19 @@ def test_noalloc_rejects_shapes_beyond_its_scratch():
     assert rc == _native.EINVAL
     msg = _native.last_error()
     assert "scratch" in msg and str(_native.NOALLOC_SCRATCH_BYTES) in msg
+
+
+def test_noalloc_rejects_a_payload_buffer_below_the_worst_case():
+    """Each unit writes at the offset its look-back finds, before the
+    launch's size is known: a buffer below the worst case could be
+    overrun, so it is refused (GAANS_EINVAL) with no device work."""
+    L = _native.lib()
+    B, N, C, P = 1, 192 * 1536, 192, 4
+    lay = _native.layout(B, N, C, P, 1)
+    desc = _native.Tables()
+    info = (ctypes.c_uint64 * 4)()
+    for nbytes in (lay.header_bytes, lay.max_payload_bytes - 1):
+        rc = L.gaans_encode_symbols_noalloc(None, None, None, ctypes.byref(desc), B, N, C, P, 1,
+                                            ctypes.addressof(info), nbytes, ctypes.addressof(info))
+        assert rc == _native.EINVAL
+        assert "worst case" in _native.last_error()
