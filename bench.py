@@ -152,6 +152,10 @@ def phase_breakdown(L, torch, dev, units, steps, fn):
     out["cycles_per_step_slowest_unit"] = round(float(cyc[slow]) / max(1, steps[slow]), 1)
     out["cycles_per_step_median"] = round(float(np.median(cyc / np.maximum(1, steps))), 1)
     out["steps_slowest_unit"] = int(steps[slow])
+    # the coder's cycles in its block barriers (waiting for the other waves)
+    bar = t[:, 14] / np.maximum(1, steps)
+    out["barrier_cycles_per_step_median"] = round(float(np.median(bar)), 1)
+    out["barrier_cycles_per_step_slowest_unit"] = round(float(bar[slow]), 1)
     out["step_loop_us_median"] = round(float(np.median((t[:, 4] - t[:, 3]) * us)), 2)
     return out
 

@@ -92,11 +92,14 @@ struct PhaseBuf {
 };
 struct PhaseClock {
 #ifdef GAANS_PHASE_TIMES
-  uint64_t t[8] = {}, c12 = 0, c13 = 0;
+  uint64_t t[8] = {}, c12 = 0, c13 = 0, bw = 0, b0 = 0;
   __device__ __forceinline__ void mark(int i) { t[i] = __builtin_amdgcn_s_memrealtime(); }
   __device__ __forceinline__ void cycles(int i) {
     (i == 12 ? c12 : c13) = __builtin_amdgcn_s_memtime();
   }
+  // shader cycles the coder spends in its block barriers (slot 14)
+  __device__ __forceinline__ void bar_in() { b0 = __builtin_amdgcn_s_memtime(); }
+  __device__ __forceinline__ void bar_out() { bw += __builtin_amdgcn_s_memtime() - b0; }
   static constexpr int kPhaseSlots = GAANS_PHASE_SLOTS;
   // slots [lo, hi) of t (and, with lo == 0, the two shader-clock slots)
   __device__ __forceinline__ void store(const PhaseBuf& b, int64_t g, int lo, int hi) const {
@@ -108,6 +111,7 @@ struct PhaseClock {
       if (lo == 0) {
         d[12] = c12;
         d[13] = c13;
+        d[14] = bw;
       }
     }
   }
@@ -123,6 +127,8 @@ struct PhaseClock {
 #else
   __device__ __forceinline__ void mark(int) {}
   __device__ __forceinline__ void cycles(int) {}
+  __device__ __forceinline__ void bar_in() {}
+  __device__ __forceinline__ void bar_out() {}
   __device__ __forceinline__ void store(const PhaseBuf&, int64_t, int, int) const {}
   __device__ __forceinline__ void store_done(const PhaseBuf&, int64_t) const {}
   __device__ __forceinline__ void mark_after_loads(int) {}
@@ -489,6 +495,9 @@ struct EncArgs {
   int64_t out_bytes;
   uint64_t* __restrict__ look;
   uint32_t B;
+  // fused: unit numbers from the control block's ticket counter (the grid
+  // may not fit the device in one round), else the workgroup index
+  uint32_t ticket;
   PhaseBuf phase;
 };
 
@@ -1087,11 +1096,15 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
   const TabHdr th = load_tab_hdr(a.tables);
   const bool fused = a.out != nullptr;  // uniform: pack fused into this kernel
   int64_t g = blockIdx.x;
-  if (fused) {
+  if (fused && a.ticket) {
     // Unit number from the launch's ticket counter, in the order the
     // workgroups start: a unit's look-back only waits on units with lower
     // numbers, which have started and run without waiting on it, so every
     // wait ends whatever order or residency the hardware gives the grid.
+    // (When the whole grid fits on the device at once the host sets no
+    // ticket and the unit is the workgroup index: every unit can be resident
+    // together, so a unit never waits on one that cannot start -- and the
+    // one atomic all workgroups would take first costs about 6 us at 768.)
     if (tid == 0)
       eflag[2] = __hip_atomic_fetch_add(a.ctrl + kCtrlEncTicket, 1u, __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT);
@@ -1276,7 +1289,9 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
               if (any_esc & (1u << (h * H + k))) enc_escapes(r[k], esc_list, n_esc, lane);
           }
         }
+        pc.bar_in();
         __syncthreads();
+        pc.bar_out();
       }
       pc.cycles(13);
       pc.mark(4);
@@ -2271,7 +2286,9 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
           ctl[4 + (j & 1)] = any_em != 0ull ? 1u : 0u;
           ctl[6 + ((j + 1) & 1)] = ecur;
         }
+        pc.bar_in();
         __syncthreads();
+        pc.bar_out();
       }
       pc.cycles(13);
       pc.mark(4);
@@ -3073,6 +3090,9 @@ int encode_prepare(int mode, bool implicit, int32_t n_scales, float scale_bound,
   a.nt_cap = st.nt_cap;
   a.stage_all = st.stage_all;
   a.ring_mask = (uint32_t)(plan.ring - 1);
+  // fused encode: unit numbers from tickets unless the grid fits the device
+  // in one round at the plan's workgroups per CU
+  a.ticket = L.U > plan.occ * (int64_t)dl.cus ? 1u : 0u;
   // 8 mapper waves when every workgroup has a CU to itself
   const int nm = plan.occ == 1 && L.U <= dl.cus ? 8 : 4;
   e->kernel = enc_kernel(mode, implicit, plan.sb, nm);

@@ -426,9 +426,11 @@ int gaans_enqueue_decode(const gaans_plan* plan, void* stream, const uint8_t* pa
  * loads returned (payload header, table header and metadata; the mark
  * waits for them), 2 tables staged,
  * 3 the first coding step (first block ready), 4 after the last step,
- * 5 before and 6 after the unit's completion-counter atomic, 7 (last unit to
- * finish only) after the completion word; the shader clock at 12 the first
- * and 13 after the last step.  Other slots are not written.  NULL (or
+ * 5 before and 6 after the unit's completion-counter atomic (fused encode:
+ * its look-back), 7 (the unit that wrote the completion word) after it; the
+ * shader clock at 12 the first and 13 after the last step, and 14 the shader
+ * cycles the coder wave spent in its block barriers.  Other slots are not
+ * written.  NULL (or
  * units <= 0) turns it off; a launch picks the setting up when it is bound,
  * so it is process-wide and not for concurrent callers.  The points are taken
  * in scalar registers and stored once per unit.  wall_clock_khz (may be NULL) receives the real-time
