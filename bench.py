@@ -156,6 +156,23 @@ def phase_breakdown(L, torch, dev, units, steps, fn):
     bar = t[:, 14] / np.maximum(1, steps)
     out["barrier_cycles_per_step_median"] = round(float(np.median(bar)), 1)
     out["barrier_cycles_per_step_slowest_unit"] = round(float(bar[slow]), 1)
+    # placement of the coder waves (HW_ID: SIMD bits 4-5, CU 8-11, SH 12,
+    # SE 13-15; XCC_ID in the high half): how many coders share a SIMD, and
+    # the median step cycles of units by that count
+    hw = buf.cpu().numpy().reshape(units, slots)[:, 15].astype(np.uint64)
+    hid = (hw & np.uint64(0xffffffff)).astype(np.int64)
+    xcc = (hw >> np.uint64(32)).astype(np.int64) & 0xf
+    cu_key = xcc * 4096 + ((hid >> 8) & 0xff)  # XCC, SE/SH, CU
+    simd = (hid >> 4) & 3
+    from collections import Counter
+    per_simd = Counter(zip(cu_key.tolist(), simd.tolist()))
+    share = np.array([per_simd[(c, s_)] for c, s_ in zip(cu_key.tolist(), simd.tolist())])
+    cps = cyc / np.maximum(1, steps)
+    out["coders_per_simd_histogram"] = {int(k): int(v) for k, v in Counter(share.tolist()).items()}
+    out["cycles_per_step_by_coders_on_simd"] = {
+        int(k): round(float(np.median(cps[share == k])), 1) for k in sorted(set(share.tolist()))}
+    per_cu = Counter(cu_key.tolist())
+    out["units_per_cu_histogram"] = {int(k): int(v) for k, v in Counter(per_cu.values()).items()}
     out["step_loop_us_median"] = round(float(np.median((t[:, 4] - t[:, 3]) * us)), 2)
     return out
 

@@ -92,8 +92,16 @@ struct PhaseBuf {
 };
 struct PhaseClock {
 #ifdef GAANS_PHASE_TIMES
-  uint64_t t[8] = {}, c12 = 0, c13 = 0, bw = 0, b0 = 0;
-  __device__ __forceinline__ void mark(int i) { t[i] = __builtin_amdgcn_s_memrealtime(); }
+  uint64_t t[8] = {}, c12 = 0, c13 = 0, bw = 0, b0 = 0, hw = 0;
+  __device__ __forceinline__ void mark(int i) {
+    t[i] = __builtin_amdgcn_s_memrealtime();
+    if (i == 0) {  // where the coder wave runs: XCC_ID << 32 | HW_ID (SIMD, CU, SE)
+      uint32_t h, xc;
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(h));
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xc));
+      hw = ((uint64_t)xc << 32) | h;
+    }
+  }
   __device__ __forceinline__ void cycles(int i) {
     (i == 12 ? c12 : c13) = __builtin_amdgcn_s_memtime();
   }
@@ -112,6 +120,7 @@ struct PhaseClock {
         d[12] = c12;
         d[13] = c13;
         d[14] = bw;
+        d[15] = hw;
       }
     }
   }
@@ -2868,15 +2877,21 @@ DecPlan plan_decode(const gaans_tables* t, int64_t P, int64_t units, bool latent
   const int64_t search_bytes = search_ok ? search_lds(t, &starts_words) : 0;
   for (int64_t occ = occ_target(units, d, 3); occ >= 1; --occ) {
     const int64_t cap = lds_budget(d, occ);
-    // the wide lookups with their sub-blocks, with 16- or 8-step blocks
-    for (int sb = 16; wide_ok && sb >= 8; sb >>= 1) {
-      const int64_t fixed = dec_fixed_lds(latents, sb);
-      Stage s;
-      if (fit_stage(t, P, per_wide, 0, kSubBytes, cap - fixed - extra, &s, range_ok, true))
-        return DecPlan{s, sb,
-                       (size_t)(fixed + per_wide * s.nt_cap + kSubBytes * (int64_t)s.nd_cap),
-                       false, 0, true};
-    }
+    // the wide lookups with their sub-blocks, then without them (a dense
+    // wide bucket then reads its two-value sub-range from global memory:
+    // the 2160x3840 latent's 8 tables of up to 256 symbols leave no room for
+    // their sub-blocks, and the 256-value buckets gave its wide-table units
+    // a second or third read in most steps), with 16- or 8-step blocks
+    for (int subs = 1; wide_ok && subs >= 0; --subs)
+      for (int sb = 16; sb >= 8; sb >>= 1) {
+        const int64_t fixed = dec_fixed_lds(latents, sb);
+        Stage s;
+        if (fit_stage(t, P, per_wide, 0, subs ? kSubBytes : 0, cap - fixed - extra, &s, range_ok,
+                      true))
+          return DecPlan{s, sb,
+                         (size_t)(fixed + per_wide * s.nt_cap + kSubBytes * (int64_t)s.nd_cap),
+                         false, 0, true};
+      }
     for (int opt = 0; opt < 9; ++opt) {
       const int sb = 16 >> (opt % 3);  // 16-, 8-, then 4-step blocks of each kind
       const int64_t fixed = dec_fixed_lds(latents, sb);
