@@ -507,6 +507,7 @@ struct EncArgs {
   // fused: unit numbers from the control block's ticket counter (the grid
   // may not fit the device in one round), else the workgroup index
   uint32_t ticket;
+  uint32_t lds_bytes;  // the launch's dynamic LDS
   PhaseBuf phase;
 };
 
@@ -989,7 +990,8 @@ template <int NT, int kWaves>
 __device__ void fused_pack(const EncArgs& a, int64_t g, int tid, int lane, int wid, int A,
                            uint32_t x, const uint32_t* part, const uint16_t* ring,
                            uint32_t ring_mask, const uint16_t* __restrict__ wbuf, uint64_t* scr,
-                           uint32_t dig_lo, uint32_t dig_hi, PhaseClock& pc) {
+                           uint32_t dig_lo, uint32_t dig_hi, uint32_t* stg, uint32_t stg_bytes,
+                           PhaseClock& pc) {
   uint32_t hs = 0, ss = 0, zs = 0;
   for (int w = 0; w < kWaves; ++w) {
     hs += part[w];
@@ -1000,6 +1002,29 @@ __device__ void fused_pack(const EncArgs& a, int64_t g, int tid, int lane, int w
   const uint32_t W = part[3 * kWaves + 1];
   const int wp = (int)part[kPartWp], fl = (int)part[kPartFl];
   const uint64_t q = unit_quads(A, W, zs);  // this unit's u32 words
+  const int cap = a.cap_words;
+  // The words flushed to the staging slot, [fl, cap), as u32 from the even
+  // position f0: copied into LDS by the other waves while the first mapper
+  // wave looks back (most units wait there for the slowest unit before them),
+  // so that after it the copy only writes to HBM.  Read from the slot
+  // directly when they do not fit.
+  const int f0 = fl & ~1;
+  const int n32f = (cap - f0) >> 1;  // cap is even
+  const bool staged = (uint32_t)n32f * 4u <= stg_bytes;  // uniform
+  if (wid != 1 && staged && n32f > 0) {
+    const uint32_t* __restrict__ src = reinterpret_cast<const uint32_t*>(wbuf + f0);
+    constexpr int NTs = NT - kLanes;  // every wave but the first mapper wave
+    const int t2 = tid < kLanes ? tid : tid - kLanes;
+    int i = t2;
+    for (; i + 3 * NTs < n32f; i += 4 * NTs) {
+      const uint32_t v0 = src[i], v1 = src[i + NTs], v2 = src[i + 2 * NTs], v3 = src[i + 3 * NTs];
+      stg[i] = v0;
+      stg[i + NTs] = v1;
+      stg[i + 2 * NTs] = v2;
+      stg[i + 3 * NTs] = v3;
+    }
+    for (; i < n32f; i += NTs) stg[i] = src[i];
+  }
   if (wid == 1) {
     pc.mark(5);
     if (g > 0 && lane == 0)
@@ -1062,12 +1087,12 @@ __device__ void fused_pack(const EncArgs& a, int64_t g, int tid, int lane, int w
   U16 += U16 & 1u;
   const int64_t n32 = U16 / 2;
   uint32_t* w32 = d32 + A;
-  const int cap = a.cap_words;
+  const uint16_t* stg16 = reinterpret_cast<const uint16_t*>(stg);
   for (int64_t j = tid; j < n32; j += NT) {
     const int p0 = wp + 2 * (int)j, p1 = p0 + 1;
     uint32_t lo = 0, hi = 0;
-    if (p0 < cap) lo = p0 < fl ? ring[p0 & ring_mask] : wbuf[p0];
-    if (p1 < cap) hi = p1 < fl ? ring[p1 & ring_mask] : wbuf[p1];
+    if (p0 < cap) lo = p0 < fl ? ring[p0 & ring_mask] : (staged ? stg16[p0 - f0] : wbuf[p0]);
+    if (p1 < cap) hi = p1 < fl ? ring[p1 & ring_mask] : (staged ? stg16[p1 - f0] : wbuf[p1]);
     w32[j] = lo | (hi << 16);
   }
   if (E > 0) {  // uniform
@@ -1342,9 +1367,12 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
     // other waves read them back
     if (wid == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    // the tables' LDS (and the scale table's) is free now: the flushed words
+    // are staged there
     fused_pack<kThreads, kWaves>(a, g, tid, lane, wid, A, x, part, ring, ring_mask, wbuf,
                                  reinterpret_cast<uint64_t*>(recs), th.digest_lo, th.digest_hi,
-                                 pc);
+                                 reinterpret_cast<uint32_t*>(lmeta),
+                                 a.lds_bytes - (ring_bytes + (uint32_t)G::kTail), pc);
     return;
   }
   __syncthreads();
@@ -3108,6 +3136,7 @@ int encode_prepare(int mode, bool implicit, int32_t n_scales, float scale_bound,
   // fused encode: unit numbers from tickets unless the grid fits the device
   // in one round at the plan's workgroups per CU
   a.ticket = L.U > plan.occ * (int64_t)dl.cus ? 1u : 0u;
+  a.lds_bytes = (uint32_t)lds;
   // 8 mapper waves when every workgroup has a CU to itself
   const int nm = plan.occ == 1 && L.U <= dl.cus ? 8 : 4;
   e->kernel = enc_kernel(mode, implicit, plan.sb, nm);
