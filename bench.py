@@ -579,9 +579,11 @@ def cpu_allcores(w, seconds: float):
 
 
 def rans64_times(torch, dev, batch, reps=3):
-    """GPU decode of CompressAI-format Rans64 streams (one per image of the
-    512x768 coder workload, table = channel): seconds per launch, and the
-    oracle's single-thread decode of one stream for comparison."""
+    """Decode of CompressAI-format Rans64 streams (one per image of the
+    512x768 coder workload, table = channel): the GPU kernel (seconds per
+    launch), this library's host decoder (gaans_rans64_decode_host: the batch
+    on every host thread, and one stream on one thread) and the oracle's
+    single-thread decode of one stream."""
     import numpy as np
 
     import oracle
@@ -610,7 +612,19 @@ def rans64_times(torch, dev, batch, reps=3):
     c0 = time.perf_counter()
     oracle.rans64_decode(streams[0], idx[0], w.cdfs, w.cdf_sizes, w.offsets)
     cpu = time.perf_counter() - c0
-    return statistics.median(ts), cpu, batch * w.n, sum(len(s) for s in streams)
+    from fast_compressai.coders.rans_host import decode_rows_host, host_threads
+
+    def host(strs, threads):
+        t0 = time.perf_counter()
+        got = decode_rows_host(strs, None, w.cdfs, w.cdf_sizes, w.offsets, N=w.n, C=w.channels,
+                               threads=threads)
+        return time.perf_counter() - t0, got
+
+    host_all, got = host(streams, None)
+    assert np.array_equal(got, w.symbols)
+    host_one = min(host(streams[:1], 1)[0] for _ in range(3))
+    return (statistics.median(ts), cpu, batch * w.n, sum(len(s) for s in streams), host_all,
+            host_one, host_threads())
 
 
 def copy_bandwidth(torch, dev, mib=1024, reps=10):
@@ -840,13 +854,19 @@ def main():
                     raw_b / (kt2["encode"] + kt2["decode"]) / 1e9, 2),
             }
         for batch in (1, 64, 256):
-            gpu_s, cpu_s, n_sym, nbytes = rans64_times(torch, dev, batch)
+            gpu_s, cpu_s, n_sym, nbytes, host_s, host1_s, threads = rans64_times(torch, dev,
+                                                                                 batch)
             extra[f"rans64_decode_{batch}x192x32x48"] = {
                 "symbols": n_sym, "stream_bytes": nbytes,
                 "decode_ms": round(gpu_s * 1e3, 3),
                 "decode_gsym_s": round(n_sym / gpu_s / 1e9, 4),
                 "cpu_oracle_ms_per_stream": round(cpu_s * 1e3, 3),
                 "speedup_vs_one_cpu_thread": round(batch * cpu_s / gpu_s, 2),
+                "host_decoder_ms": round(host_s * 1e3, 3),
+                "host_decoder_threads": threads,
+                "host_decoder_one_stream_one_thread_ms": round(host1_s * 1e3, 3),
+                "route": __import__("fast_compressai.coders.rans_host",
+                                    fromlist=["rans64_route"]).rans64_route(batch),
             }
     if args.copy_probe > 0:
         nb = args.copy_probe << 20

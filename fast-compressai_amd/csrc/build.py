@@ -19,7 +19,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG_ROOT = os.path.dirname(HERE)
 REPO = os.path.dirname(PKG_ROOT)
-SOURCES = [os.path.join(HERE, "gaans_w64.hip"), os.path.join(HERE, "gaans_host.cpp")]
+SOURCES = [os.path.join(HERE, "gaans_w64.hip"), os.path.join(HERE, "gaans_host.cpp"),
+           os.path.join(HERE, "rans64_host.cpp")]
 OUT = os.path.join(PKG_ROOT, "fast_compressai", "coders", "lib", "libgaans_w64.so")
 OUT_PHASES = os.path.join(PKG_ROOT, "fast_compressai", "coders", "lib", "libgaans_w64_phases.so")
 ARCH = os.environ.get("GAANS_OFFLOAD_ARCH", "gfx950")

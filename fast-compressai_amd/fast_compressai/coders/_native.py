@@ -123,6 +123,8 @@ def _declare(L) -> None:
         "gaans_decode_gaussian": ([p, p, i64, p, p, p, i32, f32, T, i64, i64, i64, i64, i32, p, p,
                                    p], ctypes.c_int),
         "gaans_rans64_decode": ([p, p, i64, p, p, T, i64, i64, i64, p, p, p], ctypes.c_int),
+        "gaans_rans64_decode_host": ([p, p, p, p, p, p, i32, i32, i64, i64, i64, i32, p, p],
+                                     ctypes.c_int),
         "gaans_wait_host_word": ([p, p], ctypes.c_int),
         "gaans_debug_phases": ([p, i64, ctypes.POINTER(ctypes.c_int32)], ctypes.c_int),
         # plans are passed by address (c_void_p): no byref object per call

@@ -377,19 +377,16 @@ def decode_compressai_strings(strings, prepared: PreparedTables, raw_tables, B: 
                               C: int, device, *,
                               indexes: torch.Tensor | None = None) -> torch.Tensor:
     """int32 symbols [B, N] on ``device`` of B CompressAI Rans64 strings (one
-    per image), decoded where ``rans_host.rans64_route`` says is faster:
-    CompressAI's host decoder for small batches when CompressAI is
-    importable, else the GPU Rans64 decoder.  ``raw_tables`` are the
+    per image), decoded where ``rans_host.rans64_route`` says is faster: this
+    library's host decoder (streams over the host's threads) for batches too
+    small for the GPU, else the GPU Rans64 decoder.  ``raw_tables`` are the
     CompressAI tables (cdfs, lengths, offsets) for the host decoder;
     ``indexes`` None means table = channel."""
-    from .rans_host import CompressAIANSBackend, rans64_route
+    from .rans_host import decode_rows_host, rans64_route
 
     if rans64_route(len(strings)) == "host":
-        if indexes is None:
-            idx = torch.arange(C, dtype=torch.int32).repeat_interleave(N // C).expand(B, N)
-        else:
-            idx = indexes.reshape(B, N)
-        out = CompressAIANSBackend().decode_rows(strings, idx, *raw_tables)
+        idx = None if indexes is None else indexes.reshape(B, N)
+        out = decode_rows_host(strings, idx, *raw_tables, N=N, C=C)
         return torch.from_numpy(out).to(device)
     buf, offs = pack_streams(strings, device)
     return decode_rans64(buf, offs, prepared, B, N, C, device, indexes=indexes)

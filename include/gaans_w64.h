@@ -307,6 +307,23 @@ int gaans_rans64_decode(void* stream, const uint8_t* streams_dev, int64_t stream
                         const gaans_tables* tables, int64_t B, int64_t N, int64_t C,
                         int32_t* out_dev, void* ctrl_dev, uint32_t* status_out);
 
+/* The same CompressAI Rans64 streams decoded on the host CPU, for batches too
+ * small to fill the GPU: host pointers only (streams: B concatenated byte
+ * strings, stream b at bytes [stream_offsets[b], stream_offsets[b + 1]);
+ * indexes int32 [B, N] or NULL for table = channel; CompressAI's tables cdfs
+ * [M, Lmax], cdf_sizes [M], offsets [M]).  Streams are shared out over
+ * `threads` threads (<= 0: one per hardware thread).  out: int32 [B, N];
+ * *status: the OR of GAANS_ST_CORRUPT (short stream, impossible escape,
+ * value outside int32) and GAANS_ST_INDEX over the streams (a stream stops at
+ * its first error).  Returns GAANS_ETABLE for tables that are not 16-bit
+ * quantized CDFs.  Replaces CompressAI's RansDecoder.decode_with_indexes on
+ * the reference's CPU path (src/fast_compressai/coders/compressai_ans.py:51-87). */
+int gaans_rans64_decode_host(const uint8_t* streams, const int64_t* stream_offsets,
+                             const int32_t* indexes, const int32_t* cdfs,
+                             const int32_t* cdf_sizes, const int32_t* offsets, int32_t M,
+                             int32_t Lmax, int64_t B, int64_t N, int64_t C, int32_t threads,
+                             int32_t* out, uint32_t* status);
+
 /* ---- completion ------------------------------------------------------------ */
 
 /* Wait on the host for a launch's completion word (encode: low half of

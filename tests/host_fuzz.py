@@ -46,6 +46,7 @@ def load(path):
     L.gaans_get_layout.argtypes = [i64, i64, i64, i64, i32, ctypes.POINTER(Layout)]
     L.gaans_choose_segments.argtypes = [ctypes.POINTER(Tables), i64, i64, i64, i64,
                                         ctypes.c_double, i64, ctypes.POINTER(i32)]
+    L.gaans_rans64_decode_host.argtypes = [p, p, p, p, p, p, i32, i32, i64, i64, i64, i32, p, p]
     L.gaans_last_error.restype = ctypes.c_char_p
     return L
 
@@ -169,6 +170,41 @@ def check_layout(L, rng):
             assert lay.max_payload_bytes >= lay.header_bytes
 
 
+def check_rans64_host(L, rng):
+    """The host Rans64 decoder on byte strings that are random, empty, odd
+    lengths or random tails of words, with valid or malformed tables and
+    indexes in and out of range: every call returns, and nothing is read or
+    written out of bounds (ASan)."""
+    M, Lmax = int(rng.integers(1, 10)), int(rng.integers(2, 120))
+    cdfs, sizes, offs = tables(rng, M, Lmax)
+    if rng.random() < 0.2:
+        t = int(rng.integers(0, M))
+        cdfs[t, 0] = 5  # malformed: rejected before any stream is read
+    B = int(rng.integers(1, 6))
+    C = int(rng.integers(1, M + 1))
+    N = C * int(rng.integers(1, 40))
+    strings = []
+    for _ in range(B):
+        n = int(rng.choice([0, 3, 4, 8, 12, int(rng.integers(0, 4 * N + 16))]))
+        strings.append(rng.integers(0, 256, n, dtype=np.int64).astype(np.uint8).tobytes())
+    so = np.zeros(B + 1, np.int64)
+    np.cumsum([len(x) for x in strings], out=so[1:])
+    buf = np.frombuffer(b"".join(strings) + b"\0", np.uint8)  # never empty
+    idx = None
+    if rng.random() < 0.5:
+        idx = rng.integers(-2, M + 2, (B, N), dtype=np.int64).astype(np.int32)
+    out = np.zeros((B, N), np.int32)
+    st = ctypes.c_uint32(0)
+    rc = L.gaans_rans64_decode_host(buf.ctypes.data, so.ctypes.data,
+                                    None if idx is None else idx.ctypes.data, cdfs.ctypes.data,
+                                    sizes.ctypes.data, offs.ctypes.data, M, Lmax, B, N, C,
+                                    int(rng.integers(0, 4)), out.ctypes.data, ctypes.byref(st))
+    tables_valid = all(table_ok(cdfs[u], int(sizes[u]), Lmax) for u in range(M))
+    assert (rc == 0) == tables_valid, (rc, L.gaans_last_error())
+    if rc == 0:
+        assert st.value & ~0x12 == 0  # GAANS_ST_CORRUPT | GAANS_ST_INDEX only
+
+
 def main():
     L = load(sys.argv[1])
     iters = int(sys.argv[2]) if len(sys.argv) > 2 else 300
@@ -178,6 +214,7 @@ def main():
         check_valid(L, rng)
         check_malformed(L, rng)
         check_layout(L, rng)
+        check_rans64_host(L, rng)
     d = Tables()
     out = ctypes.c_int32(0)
     for bits, budget in ((float("nan"), 0.01), (-1.0, 0.01), (2.0, float("nan")), (2.0, -1.0)):

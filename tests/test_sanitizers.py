@@ -1,9 +1,10 @@
 """CPU runs under AddressSanitizer and UndefinedBehaviorSanitizer.
 
 1. The library's host-only code (fast-compressai_amd/csrc/gaans_host.cpp:
-   table validation and preparation, layout, segment choice, self test) is
-   built with g++ -fsanitize=address,undefined and driven by
-   tests/host_fuzz.py with valid and malformed tables and shapes.
+   table validation and preparation, layout, segment choice, self test; and
+   rans64_host.cpp: the host decoder of CompressAI Rans64 streams) is built
+   with g++ -fsanitize=address,undefined and driven by tests/host_fuzz.py with
+   valid and malformed tables, shapes and byte strings.
 2. The oracle (oracle/gaans_oracle.c) is built the same way
    (make -C oracle SAN=... OUT=...) and its own tests (tests/test_oracle.py,
    tests/test_golden.py) run against that build.
@@ -56,7 +57,8 @@ def test_host_code_under_asan_ubsan(tmp_path):
     csrc = os.path.join(REPO, "fast-compressai_amd", "csrc")
     subprocess.run(["g++", "-std=c++17", "-O1", *SAN, "-fPIC", "-shared",
                     "-I", os.path.join(REPO, "include"), "-I", csrc,
-                    os.path.join(csrc, "gaans_host.cpp"), "-o", str(lib)], check=True)
+                    os.path.join(csrc, "gaans_host.cpp"), os.path.join(csrc, "rans64_host.cpp"),
+                    "-pthread", "-o", str(lib)], check=True)
     proc = subprocess.run([sys.executable, os.path.join(REPO, "tests", "host_fuzz.py"), str(lib),
                            "300"], env=env_with_sanitizers(runtimes()), capture_output=True,
                           text=True, timeout=600)
