@@ -2865,7 +2865,9 @@ EncPlan plan_encode(const gaans_tables* t, int64_t P, int64_t units, const DevLd
                          (size_t)(fixed + 16 * (int64_t)s.nt_cap + 8 * (int64_t)s.ne_cap), occ,
                          ring};
       }
-  return EncPlan{Stage{0, 0, 0, 0}, 8, (size_t)enc_fixed_lds(8, kRingWords), 1, kRingWords};
+  // no tables staged (they read through L1/L2): the largest block allowed
+  const int sb = allow16 ? 16 : 8;
+  return EncPlan{Stage{0, 0, 0, 0}, sb, (size_t)enc_fixed_lds(sb, kRingWords), 1, kRingWords};
 }
 
 // Decoder: lookups and metadata per table; sub-blocks when they are staged
@@ -3102,7 +3104,13 @@ int encode_prepare(int mode, bool implicit, int32_t n_scales, float scale_bound,
   const bool long_units = L.seg_cap >= 512 * kLanes;
   const bool gauss = mode == kModeGaussian;
   if (gauss) implicit = false;
-  const EncPlan plan = plan_encode(tables, L.P, L.U, dl, extra, !gauss, long_units && !implicit);
+  // The Gaussian mode's mappers (a scale-table search and table reads from
+  // L2 per element) are the slower half at any length: with 8-step blocks
+  // the coder waited about 135 of its 350 cycles per step at the barriers
+  // (mean-scale hyperprior y, P = 4 and 16), and 16-step blocks give each
+  // mapper wave two steps per block to overlap.
+  const EncPlan plan = plan_encode(tables, L.P, L.U, dl, extra, !gauss,
+                                   (long_units || gauss) && !implicit);
   const Stage& st = plan.st;
   const size_t lds = plan.lds + (size_t)extra;
   if (lds > (size_t)dl.per_block)
