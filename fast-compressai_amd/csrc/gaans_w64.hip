@@ -1745,6 +1745,74 @@ __device__ void stage_search(Tabs& T, uint4* lmeta, uint32_t* lclut, uint16_t* l
   __syncthreads();
 }
 
+// Decoder staging in two halves.  stage_early, at kernel entry (it needs
+// neither the payload header nor the blob's checks, only the staged range):
+// the lookups' copy straight into LDS -- the staged tables' lookups, or every
+// table's search lookups and symbol starts -- and one metadata row per
+// thread into registers.  stage_late, once the checks pass: the sub-blocks'
+// copy (its range comes from the blob's metadata), the metadata rows into
+// LDS, the wait for this wave's copies and the barrier.  The first copies are
+// then in flight during the header's round trip instead of after it.
+struct EarlyStage {
+  int t_lo, nt;
+  TabMeta row;  // metadata of staged table t_lo + tid (tid < nt)
+};
+
+template <int NT, int LB, bool kSearch>
+__device__ __forceinline__ EarlyStage stage_early(const Tabs& T, uint64_t* llut, uint32_t* lclut,
+                                                  uint16_t* lstarts, const uint8_t* tables,
+                                                  const BlobRef& blob, uint32_t M,
+                                                  uint32_t starts_words, int t_lo, int t_hi,
+                                                  int tid) {
+  EarlyStage e;
+  e.t_lo = kSearch ? 0 : t_lo;
+  e.nt = kSearch ? (int)M : (t_hi > t_lo ? t_hi - t_lo : 0);
+  e.row = TabMeta{0u, 0u, 0, 0u};
+  if (e.nt > 0) {
+    if constexpr (kSearch) {
+      copy16_dma<NT>(reinterpret_cast<uint4*>(lclut),
+                     reinterpret_cast<const uint4*>(tables + blob.clut_off), M * (kLutSize / 4),
+                     tid);
+      copy16_dma<NT>(reinterpret_cast<uint4*>(lstarts),
+                     reinterpret_cast<const uint4*>(tables + blob.starts_off), starts_words, tid);
+    } else {
+      copy16_dma<NT>(reinterpret_cast<uint4*>(llut),
+                     reinterpret_cast<const uint4*>(T.glut + (int64_t)t_lo * LB),
+                     (uint32_t)e.nt * (LB / 2), tid);
+    }
+    e.row = T.gmeta[e.t_lo + (tid < e.nt ? tid : e.nt - 1)];
+  }
+  return e;
+}
+
+template <int NT, bool kSearch>
+__device__ __forceinline__ void stage_late(Tabs& T, const EarlyStage& e, uint4* lmeta,
+                                           uint64_t* lsub, const StageBounds& bd, int tid) {
+  T.t_lo = e.t_lo;
+  T.nt = e.nt;
+  T.sub_first = 0;
+  T.sub_lds = !kSearch && lsub != nullptr;
+  if (e.nt > 0) {
+    const uint32_t base0 = kSearch ? 0u : bd.base0;
+    if (!kSearch && lsub && bd.d1 > bd.d0) {
+      T.sub_first = bd.d0;
+      copy16_dma<NT>(reinterpret_cast<uint4*>(lsub),
+                     reinterpret_cast<const uint4*>(T.gsub + (size_t)bd.d0 * kSubSize),
+                     (bd.d1 - bd.d0) * (kSubBytes / 16), tid);
+    }
+    if (e.nt <= NT) {
+      if (tid < e.nt)
+        lmeta[tid] = make_uint4(e.row.ent_base - base0, e.row.nsym, (uint32_t)e.row.offset,
+                                e.row.ent_base);
+    } else {
+      stage_pass<NT, false, false>(T, lmeta, nullptr, nullptr, nullptr, (uint32_t)e.nt, 1u, 0u,
+                                   base0, e.t_lo, tid);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's direct-to-LDS copies are in
+  }
+  __syncthreads();
+}
+
 // Word stream of one chunk: prefetched from HBM into registers (kPfWords words
 // ahead) and copied into an LDS ring of kRing words holding the words
 // [rp, filled) (positions mod kRing), kPfWords words at a time.  At the start
@@ -2059,6 +2127,8 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
   tb.lsub = lsub;
   tb.lclut = lclut;
   tb.lstarts = lstarts;
+  const EarlyStage est = stage_early<kDecThreads, kLB, kSearch>(
+      tb, llut, lclut, lstarts, a.tables, a.blob, a.M, a.starts_words, t_lo, t_hi, tid);
   int32_t cbx[kPer], nbx[kPer];
   float cm[kPer], nm[kPer];
   auto load_block = [&](int j, int32_t* ib, float* im) {
@@ -2227,13 +2297,7 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
     }
     if (tid < 8) ctl[tid] = tid == 1 ? kAllAvail : 0u;
     if (kMode == kModeGaussian) stage_scales<kDecThreads>(scl, a.scale_table, a.n_scales, tid);
-    if constexpr (kSearch) {
-      stage_search<kDecThreads>(tb, lmeta, lclut, lstarts, a.tables, a.blob, a.M,
-                                a.starts_words, tid);
-    } else {
-      stage_tables<kDecThreads, kLB>(tb, lmeta, nullptr, llut, a.nd_cap ? lsub : nullptr, bd,
-                                     t_lo, t_hi, tid);
-    }
+    stage_late<kDecThreads, kSearch>(tb, est, lmeta, a.nd_cap ? lsub : nullptr, bd, tid);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load crosses the role split
     if (wid == 0) pc.mark(2);
 
@@ -2365,6 +2429,8 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
     }
   }
   if (!ok) {  // uniform
+    // the early copies into LDS have landed before the workgroup ends
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     publish();
     __syncthreads();
   }
