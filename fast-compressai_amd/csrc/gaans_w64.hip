@@ -312,10 +312,11 @@ __device__ __forceinline__ void stage_pass(const Tabs& T, uint4* lmeta, uint2* l
 }
 
 // Stage tables [t_lo, t_hi) of the blob into LDS (whole workgroup of NT
-// threads): the encoder's metadata and entries (lent), or the decoder's
-// lookups (llut), metadata and, when lsub is given, the tables' sub-blocks.
-// The lookups, which need no metadata, are copied while the metadata loads
-// are in flight; lookups and sub-blocks are 16-byte aligned in the blob.
+// threads): the encoder's metadata and entries (lent), or the lookups
+// (llut), metadata and, when lsub is given, the tables' sub-blocks.  The
+// entries and lookups are copied straight into LDS while the metadata loads
+// are in flight; entries, lookups and sub-blocks are 16-byte aligned in the
+// blob.
 // Entry and sub-block ranges of the staged tables [t_lo, t_hi) (t_lo < M;
 // t_lo == t_hi when nothing is staged), read from the blob's metadata.  Every
 // load is unconditional, so a kernel can issue them with its other first
@@ -362,8 +363,16 @@ __device__ void stage_tables(Tabs& T, uint4* lmeta, uint2* lent, uint64_t* llut,
     const uint32_t nt = (uint32_t)T.nt;
     const uint32_t base0 = bd.base0;
     if (lent) {
-      const uint32_t ne = bd.ent_end - base0;
-      stage_pass<NT, true, false>(T, lmeta, lent, nullptr, nullptr, nt, ne, 0u, base0, t_lo, tid);
+      // the entries straight into LDS from the even entry at or below the
+      // range's first (16-byte aligned: the blob's entry section is), one
+      // round trip however many there are; the metadata rows through
+      // registers, their entry bases taken relative to that even entry
+      const uint32_t b2 = base0 & ~1u;
+      copy16_dma<NT>(reinterpret_cast<uint4*>(lent),
+                     reinterpret_cast<const uint4*>(T.gent + b2), (bd.ent_end - b2 + 1u) / 2u,
+                     tid);
+      stage_pass<NT, false, false>(T, lmeta, nullptr, nullptr, nullptr, nt, 1u, 0u, b2, t_lo, tid);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's direct-to-LDS copies are in
     } else {
       // lookups and sub-blocks straight into LDS, the metadata rows through
       // registers (they are rewritten)
@@ -2925,7 +2934,9 @@ EncPlan plan_encode(const gaans_tables* t, int64_t P, int64_t units, const DevLd
     for (int sb = allow16 ? 16 : 8; sb >= 4; sb >>= 1)
       for (int ring = kRingWords; ring >= 2 * sb * kLanes && ring >= 1024; ring >>= 1) {
         Stage s;
-        const int64_t fixed = enc_fixed_lds(sb, ring);
+        // + 2 entries: the staged copy starts at an even entry and ends on a
+        // whole 16-byte word (stage_tables)
+        const int64_t fixed = enc_fixed_lds(sb, ring) + 16;
         if (fit_stage(t, P, 16, 8, 0, lds_budget(d, occ) - fixed - extra, &s, range_ok))
           return EncPlan{s, sb,
                          (size_t)(fixed + 16 * (int64_t)s.nt_cap + 8 * (int64_t)s.ne_cap), occ,
