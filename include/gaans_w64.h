@@ -330,8 +330,9 @@ int gaans_rans64_decode_host(const uint8_t* streams, const int64_t* stream_offse
  * info_out[2]; decode: status_out[1]) in pinned host memory that the caller
  * set to 0 before the launch.  Returns GAANS_OK once the word is nonzero; the
  * word itself carries the size and status (info_out[0..1] and status_out[0]
- * are only guaranteed after the stream has finished).  Later work on the
- * stream (the pack kernel) may still run, ordered on `stream` as usual.  Returns
+ * are only guaranteed after the stream has finished).  The packing (the fused
+ * encode kernel's own, or the pack kernel) may still run, and later work is
+ * ordered after it on `stream` as usual.  Returns
  * GAANS_EHIP when the stream reports an error or drains without setting the
  * word.  Replaces the stream synchronisations of the reference's host code
  * (warp_ans_kernel_v2.cu:275-276, warp_div.py:63-65). */
