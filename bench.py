@@ -140,9 +140,12 @@ def phase_breakdown(L, torch, dev, units, steps, fn):
     t0 = t[:, 0].min()
     names = {0: "entry", 1: "first_loads_in", 2: "tables_staged", 3: "first_step",
              4: "after_last_step",
-             5: "before_counter", 6: "after_counter"}
+             5: "before_counter", 6: "after_counter",
+             8: "pack_offset_known", 9: "pack_words_issued", 10: "pack_stores_done"}
     out = {"wall_clock_khz": khz.value, "units": units}
     for i, name in names.items():
+        if i >= 8 and not (t[:, i] > 0).all():
+            continue  # the fused encoder's pack points only
         rel = (t[:, i] - t0) * us
         out[name + "_us"] = [round(float(np.median(rel)), 2), round(float(rel.max()), 2)]
     done = t[:, 7][t[:, 7] > 0]

@@ -82,7 +82,9 @@ int make_layout(int64_t B, int64_t N, int64_t C, int64_t P, int64_t S, Layout* L
   if (L->max_payload >= ((int64_t)1 << 38))
     return fail(GAANS_EINVAL, "shape too large (worst-case payload of %lld bytes)",
                 (long long)L->max_payload);
-  L->cap_words = align_up(L->seg_cap + 2, 2);
+  // whole 16-byte chunks, so that every unit's staging slot is 16-byte
+  // aligned (the fused encode copies it to LDS in 16-byte pieces)
+  L->cap_words = align_up(L->seg_cap + 2, 8);
   int64_t o = 0;
   // the fused encode's look-back words first: their place does not depend
   // on the shape, so one zeroing serves every shape that uses the workspace

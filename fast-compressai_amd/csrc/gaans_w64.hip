@@ -90,14 +90,23 @@ struct PhaseBuf {
   uint64_t* __restrict__ p;
   int64_t units;  // units that have slots
 };
+// The wave's HW_ID register: wave slot (bits 0-3), SIMD (4-5), CU (8-11),
+// shader array (12), shader engine (13-14), thread-group slot on the CU
+// (16-19).
+__device__ __forceinline__ uint32_t hw_id() {
+  uint32_t h;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(h));
+  return h;
+}
+
 struct PhaseClock {
 #ifdef GAANS_PHASE_TIMES
-  uint64_t t[8] = {}, c12 = 0, c13 = 0, bw = 0, b0 = 0, hw = 0;
+  uint64_t t[12] = {}, c12 = 0, c13 = 0, bw = 0, b0 = 0, hw = 0;
   __device__ __forceinline__ void mark(int i) {
     t[i] = __builtin_amdgcn_s_memrealtime();
     if (i == 0) {  // where the coder wave runs: XCC_ID << 32 | HW_ID (SIMD, CU, SE)
-      uint32_t h, xc;
-      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(h));
+      const uint32_t h = hw_id();
+      uint32_t xc;
       asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xc));
       hw = ((uint64_t)xc << 32) | h;
     }
@@ -114,7 +123,7 @@ struct PhaseClock {
     if (b.p != nullptr && g < b.units) {
       uint64_t* d = b.p + g * kPhaseSlots;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < 12; ++i)
         if (i >= lo && i < hi) d[i] = t[i];
       if (lo == 0) {
         d[12] = c12;
@@ -207,6 +216,21 @@ __device__ __forceinline__ uint64_t ballot(bool pred) { return __builtin_amdgcn_
 
 // Keep a wave-uniform value in a scalar register.
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// A buffer resource over the n 4-byte elements at base + 4 first (wave-uniform
+// arguments, kept in scalar registers: a resource in vector registers makes
+// the compiler loop over the lanes' values).  Loads at byte offsets >= 4 n
+// return 0 without touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t unit_rsrc(const void* base, int64_t first,
+                                                            int64_t n) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base) + 4ull * (uint64_t)first;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
+  const uint64_t bytes = 4ull * (uint64_t)(n > 0 ? n : 0);
+  const int nrec = (int)(uint32_t)(bytes < 0xffffffffull ? bytes : 0xffffffffull);
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), 0,
+                                           uni(nrec), kBufferFlags);
+}
 
 // Section offsets of a prepared table blob, derived on the host from the
 // descriptor (M, symbols, sub-blocks), so the kernels address the sections
@@ -517,6 +541,9 @@ struct EncArgs {
   // may not fit the device in one round), else the workgroup index
   uint32_t ticket;
   uint32_t lds_bytes;  // the launch's dynamic LDS
+  // several workgroups share a CU: the coder role goes to a wave on the SIMD
+  // numbered by the workgroup's slot on the CU
+  uint32_t elect;
   PhaseBuf phase;
 };
 
@@ -932,40 +959,58 @@ __device__ __forceinline__ uint64_t wave_sum40(uint64_t v) {
 
 // Decoupled look-back of unit g (one whole wave): the exclusive prefix of
 // the payload body (u32 words) and the OR of the status bits of units
-// 0 .. g - 1.  Lane i reads the look-back word of unit j - i; the window
-// counts when every unit up to the nearest one with an inclusive prefix has
-// published its size (the prefix is then that inclusive value plus the
-// sizes after it), or when all 64 have sizes and none a prefix (the window
-// moves 64 units back).  Otherwise it reads again.  The words are agent-scope
-// atomics: only their own values are exchanged, so relaxed loads suffice.
-// After kLookSpinTicks the unit stops waiting and reports GAANS_ST_TIMEOUT
-// (its prefix is then at most the true one, so its copy stays in bounds).
+// 0 .. g - 1.  Lane i of window r reads the look-back word of unit
+// j - 64 r - i; kLookWindows windows are read per round trip (all the loads
+// in flight together) and taken in order: a window counts when every unit up
+// to the nearest one with an inclusive prefix has published its size (the
+// prefix is then that inclusive value plus the sizes after it), or when all
+// 64 have sizes and none a prefix (the next window follows).  A window with a
+// unit that has published nothing is read again (with the ones behind it).
+// The words are agent-scope atomics: only their own values are exchanged, so
+// relaxed loads suffice.  After kLookSpinTicks the unit stops waiting and
+// reports GAANS_ST_TIMEOUT (its prefix is then at most the true one, so its
+// copy stays in bounds).
+constexpr int kLookWindows = 4;
 __device__ __forceinline__ uint64_t look_back(const uint64_t* look, int64_t g, int lane,
                                               uint32_t& st) {
   uint64_t excl = 0;
   int64_t j = g - 1;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   while (j >= 0) {
-    const int64_t p = j - lane;
-    uint64_t v = kLookInc;  // before unit 0: an inclusive prefix of zero
-    if (p >= 0) v = __hip_atomic_load(&look[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t f = (uint32_t)(v >> 62);
-    const uint64_t inc = ballot(f == 2u), none = ballot(f == 0u);
-    // lanes up to and including the nearest inclusive prefix (all without one)
-    const uint64_t span = inc ? ((inc & (0ull - inc)) << 1) - 1ull : ~0ull;
-    if ((none & span) == 0ull) {
-      const uint64_t w = ((span >> lane) & 1ull) ? v : 0ull;
-      excl += wave_sum40(w & kLookValMask);
-      st |= wave_fold_dpp<true>((uint32_t)(w >> kLookStShift) & 0xffu);
-      if (inc) break;
-      j -= kLanes;
-      continue;
+    uint64_t v[kLookWindows];
+#pragma unroll
+    for (int r = 0; r < kLookWindows; ++r) {
+      const int64_t p = j - kLanes * r - lane;
+      v[r] = kLookInc;  // before unit 0: an inclusive prefix of zero
+      if (p >= 0) v[r] = __hip_atomic_load(&look[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (__builtin_amdgcn_s_memrealtime() - t0 > kLookSpinTicks) {
-      st |= GAANS_ST_TIMEOUT;
-      break;
+    bool done = false, stalled = false;
+#pragma unroll
+    for (int r = 0; r < kLookWindows; ++r) {
+      if (!done && !stalled) {  // uniform
+        const uint32_t f = (uint32_t)(v[r] >> 62);
+        const uint64_t inc = ballot(f == 2u), none = ballot(f == 0u);
+        // lanes up to and including the nearest inclusive prefix (all without one)
+        const uint64_t span = inc ? ((inc & (0ull - inc)) << 1) - 1ull : ~0ull;
+        if ((none & span) == 0ull) {
+          const uint64_t w = ((span >> lane) & 1ull) ? v[r] : 0ull;
+          excl += wave_sum40(w & kLookValMask);
+          st |= wave_fold_dpp<true>((uint32_t)(w >> kLookStShift) & 0xffu);
+          if (inc) done = true;
+          else j -= kLanes;
+        } else {
+          stalled = true;
+        }
+      }
     }
-    __builtin_amdgcn_s_sleep(1);
+    if (done) break;
+    if (stalled) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > kLookSpinTicks) {
+        st |= GAANS_ST_TIMEOUT;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
   }
   return excl;
 }
@@ -1012,27 +1057,22 @@ __device__ void fused_pack(const EncArgs& a, int64_t g, int tid, int lane, int w
   const int wp = (int)part[kPartWp], fl = (int)part[kPartFl];
   const uint64_t q = unit_quads(A, W, zs);  // this unit's u32 words
   const int cap = a.cap_words;
-  // The words flushed to the staging slot, [fl, cap), as u32 from the even
-  // position f0: copied into LDS by the other waves while the first mapper
-  // wave looks back (most units wait there for the slowest unit before them),
-  // so that after it the copy only writes to HBM.  Read from the slot
-  // directly when they do not fit.
-  const int f0 = fl & ~1;
-  const int n32f = (cap - f0) >> 1;  // cap is even
-  const bool staged = (uint32_t)n32f * 4u <= stg_bytes;  // uniform
-  if (wid != 1 && staged && n32f > 0) {
-    const uint32_t* __restrict__ src = reinterpret_cast<const uint32_t*>(wbuf + f0);
-    constexpr int NTs = NT - kLanes;  // every wave but the first mapper wave
+  // The words flushed to the staging slot, [fl, cap), from the position f0
+  // of a 16-byte boundary (the slot is 16-byte aligned and cap a multiple of
+  // 8 words): copied straight into LDS by the other waves while the first
+  // mapper wave looks back (most units wait there for the slowest unit
+  // before them), every load of the copy in flight at once, so that after it
+  // the copy only writes to HBM.  Read from the slot directly when they do
+  // not fit.
+  const int f0 = fl & ~7;
+  const uint32_t n16 = (uint32_t)(cap - f0) >> 3;
+  const bool staged = n16 * 16u <= stg_bytes;  // uniform
+  if (wid != 1 && staged && n16 > 0) {
+    // every wave but the first mapper wave, numbered densely
     const int t2 = tid < kLanes ? tid : tid - kLanes;
-    int i = t2;
-    for (; i + 3 * NTs < n32f; i += 4 * NTs) {
-      const uint32_t v0 = src[i], v1 = src[i + NTs], v2 = src[i + 2 * NTs], v3 = src[i + 3 * NTs];
-      stg[i] = v0;
-      stg[i + NTs] = v1;
-      stg[i + 2 * NTs] = v2;
-      stg[i + 3 * NTs] = v3;
-    }
-    for (; i < n32f; i += NTs) stg[i] = src[i];
+    copy16_dma<NT - kLanes>(reinterpret_cast<uint4*>(stg),
+                            reinterpret_cast<const uint4*>(wbuf + f0), n16, t2);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // in LDS before the barrier
   }
   if (wid == 1) {
     pc.mark(5);
@@ -1077,6 +1117,7 @@ __device__ void fused_pack(const EncArgs& a, int64_t g, int tid, int lane, int w
   }
   if (tid == 0) pc.store(a.phase, g, 0, 5);  // the coder wave's points
   __syncthreads();
+  pc.mark(8);  // the unit's payload offset is known
   const uint64_t excl = scr[0];
   const int64_t off = a.header_bytes + 4 * (int64_t)excl;
   if (off + 4 * (int64_t)q > a.out_bytes) return;  // uniform; the host sizes out for the worst case
@@ -1104,12 +1145,15 @@ __device__ void fused_pack(const EncArgs& a, int64_t g, int tid, int lane, int w
     if (p1 < cap) hi = p1 < fl ? ring[p1 & ring_mask] : (staged ? stg16[p1 - f0] : wbuf[p1]);
     w32[j] = lo | (hi << 16);
   }
+  pc.mark(9);  // the words' stores are issued
   if (E > 0) {  // uniform
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     pack_escapes<NT>(a.esc_raw + g * (int64_t)a.seg_cap + (a.seg_cap - E), E, w32, n32, tid,
                      reinterpret_cast<uint32_t*>(scr + 2));
   }
+  pc.mark_after_loads(10);  // every store of the coder wave has completed
+  if (tid == 0) pc.store(a.phase, g, 8, 11);
 }
 
 template <int kMode, bool kImplicit, int SB, int NM>
@@ -1129,17 +1173,18 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
   uint2* lent = reinterpret_cast<uint2*>(smem + ring_bytes + G::kTail + 16 * a.nt_cap);
   float* scl = reinterpret_cast<float*>(smem + a.scales_lds);  // Gaussian: scale table
 
-  const int tid = threadIdx.x;
-  const int lane = tid & (kLanes - 1);
-  const int wid = uni(tid >> 6);  // wave role, kept in a scalar register
+  const int lane = (int)threadIdx.x & (kLanes - 1);
+  const int hw_wave = uni((int)threadIdx.x >> 6);
   PhaseClock pc;
-  if (wid == 0) pc.mark(0);
+  pc.mark(0);
   // the table blob's header does not depend on the unit: its load is in
   // flight while the unit number is fetched
   const TabHdr th = load_tab_hdr(a.tables);
   const bool fused = a.out != nullptr;  // uniform: pack fused into this kernel
-  int64_t g = blockIdx.x;
-  if (fused && a.ticket) {
+  const bool ticket = fused && a.ticket;
+  const uint32_t hwid = hw_id();
+  if (a.elect | ticket) {
+    if (a.elect && lane == 0) part[hw_wave] = (hwid >> 4) & 3u;  // this wave's SIMD
     // Unit number from the launch's ticket counter, in the order the
     // workgroups start: a unit's look-back only waits on units with lower
     // numbers, which have started and run without waiting on it, so every
@@ -1148,10 +1193,29 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
     // ticket and the unit is the workgroup index: every unit can be resident
     // together, so a unit never waits on one that cannot start -- and the
     // one atomic all workgroups would take first costs about 6 us at 768.)
-    if (tid == 0)
+    if (ticket && threadIdx.x == 0)
       eflag[2] = __hip_atomic_fetch_add(a.ctrl + kCtrlEncTicket, 1u, __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
+  }
+  // Wave roles: the coder is role 0, the mappers 1 .. NM.  Several
+  // workgroups on one CU each put their coder on the SIMD numbered by their
+  // slot on the CU (HW_ID's thread-group field), when one of their waves is
+  // there: the coders then have SIMDs of their own, where the hardware's
+  // placement sometimes put two on one SIMD (the younger then got about a
+  // quarter fewer issue cycles).  Roles are a permutation of the waves, and
+  // the thread index below follows the role, so cooperative loops are
+  // unchanged.
+  int coder = 0;
+  if (a.elect) {
+    const uint32_t want = (hwid >> 16) & 3u;
+    for (int w = kWaves - 1; w >= 0; --w)
+      coder = (uint32_t)uni((int)part[w]) == want ? w : coder;
+  }
+  const int wid = uni(hw_wave == coder ? 0 : (hw_wave < coder ? hw_wave + 1 : hw_wave));
+  const int tid = wid * kLanes + lane;
+  int64_t g = blockIdx.x;
+  if (ticket) {
     // a counter that did not start at zero (a control block shared or not
     // zeroed, against the contract) still gives every unit number once, in
     // range; the look-backs then end by their time limit
@@ -1195,27 +1259,42 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
   // (steps a wave does not own keep these zeros)
   int32_t ca[kPer] = {}, cb[kPer] = {}, na[kPer] = {}, nb[kPer] = {};
   float cm[kPer] = {}, nm[kPer] = {};
+  // The unit's inputs as buffer resources over its len positions: a load's
+  // address is the lane's constant byte offset plus the step's (one add, no
+  // 64-bit address arithmetic per load), and lanes past the unit's end read
+  // 0 (their results are masked).
+  const void* in_a_ptr = kMode == kModeSymbols ? (const void*)a.symbols : (const void*)a.y;
+  const void* in_b_ptr = kMode == kModeGaussian ? (const void*)a.scales : (const void*)a.indexes;
+  const bool has_b = kMode == kModeGaussian || !kImplicit;
+  const bool has_m = kMode == kModeGaussian && a.means != nullptr;
+  const __amdgpu_buffer_rsrc_t rin_a = unit_rsrc(in_a_ptr, row + start, len);
+  const __amdgpu_buffer_rsrc_t rin_b = unit_rsrc(has_b ? in_b_ptr : in_a_ptr, row + start,
+                                                 has_b ? len : 0);
+  const __amdgpu_buffer_rsrc_t rin_m = unit_rsrc(has_m ? (const void*)a.means : in_a_ptr,
+                                                 row + start, has_m ? len : 0);
+  const int lane4 = 4 * lane;
   auto load_block = [&](int j, int32_t* ia, int32_t* ib, float* im) __attribute__((always_inline)) {
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
       const int u = (wid - 1) + kEncMappers * e;
       if (SB % kEncMappers != 0 && u >= SB) break;
-      int p = lane + kLanes * (j * SB + u);
-      p = p < len ? p : len - 1;  // loads stay in the chunk; results are masked
-      const int64_t i = row + start + p;
+      // the range check covers the vector offset only (not a scalar one),
+      // so the step's offset is added to the lane's
+      const int vo = lane4 + uni(4 * kLanes * (j * SB + u));
+      ia[e] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rin_a, vo, 0, 0);
       if (kMode == kModeGaussian) {
-        ia[e] = __float_as_int(a.y[i]);
-        im[e] = a.means ? a.means[i] : 0.0f;
-        ib[e] = __float_as_int(a.scales[i]);  // the index is found when the block is mapped
+        im[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin_m, vo, 0, 0));
+        // the index is found from the scale when the block is mapped
+        ib[e] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rin_b, vo, 0, 0);
       } else {
         if (kMode == kModeLatents) {
-          ia[e] = __float_as_int(a.y[i]);
+          int p = lane + kLanes * (j * SB + u);
+          p = p < len ? p : len - 1;  // the median's channel stays in the chunk
           im[e] = a.medians[udiv((uint32_t)(start + p), a.div_hw)];
         } else {
-          ia[e] = a.symbols[i];
           im[e] = 0.0f;
         }
-        ib[e] = kImplicit ? 0 : a.indexes[i];
+        ib[e] = kImplicit ? 0 : (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rin_b, vo, 0, 0);
       }
     }
   };
@@ -1236,23 +1315,12 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
 
     // this wave's steps per block: u = wid - 1 + kEncMappers e < SB
     const int nvalid = SB % kEncMappers == 0 ? kPer : (SB - wid + kEncMappers) / kEncMappers;
-    auto map_steps = [&](int j, auto lds_tag) __attribute__((always_inline)) {
-      constexpr bool kLds = decltype(lds_tag)::value;
+    // the block's records into the LDS slot of block j, and its steps with
+    // escapes into the block's flag word
+    auto put_records = [&](int j, const uint4* r, bool fast, uint32_t esc_steps)
+                           __attribute__((always_inline)) {
       uint4* dst = recs + (j & 1) * SB * kLanes;
-      uint4 r[kPer];
-      bool fast = false;
-      uint32_t esc_steps = 0;
-      if constexpr (kLds) {
-        if (offsets_safe && nvalid == kPer && (j + 1) * SB * kLanes <= len)
-          fast = enc_records_fast<kMode, kImplicit, kPer>(a, tb, lane, j * SB + wid - 1,
-                                                          kEncMappers, start, ca, cb, cm, hash,
-                                                          status, znib, esc_steps, r);
-      }
-      if (!fast)
-        enc_records<kMode, kImplicit, kLds, kPer>(a, tb, lane, j * SB + wid - 1, kEncMappers,
-                                                  nvalid, len, start, ca, cb, cm, hash, status,
-                                                  znib, r);
-      uint32_t eb = 0;  // steps of the block with escapes (none on the fast path)
+      uint32_t eb = 0;
 #pragma unroll
       for (int e = 0; e < kPer; ++e) {
         const int u = (wid - 1) + kEncMappers * e;
@@ -1264,9 +1332,30 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
       if (eb != 0u && lane == 0)
         __hip_atomic_fetch_or(&eflag[j & 1], eb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     };
+    auto map_steps = [&](int j, auto lds_tag) __attribute__((always_inline)) {
+      constexpr bool kLds = decltype(lds_tag)::value;
+      uint4 r[kPer];
+      enc_records<kMode, kImplicit, kLds, kPer>(a, tb, lane, j * SB + wid - 1, kEncMappers,
+                                                nvalid, len, start, ca, cb, cm, hash, status,
+                                                znib, r);
+      put_records(j, r, false, 0u);
+    };
     auto map_block = [&](int j) __attribute__((always_inline)) {
       if (kMode == kModeGaussian)
         gauss_indexes<kPer>(cb, scl, a.n_scales, a.scales_pow2, a.scale_bound);
+      // A full block first tries the fast path, which checks by itself that
+      // every table is staged and every value in range (and changes nothing
+      // when it declines), so the check below runs only for the rest.
+      if (tb.nt > 0 && offsets_safe && nvalid == kPer && (j + 1) * SB * kLanes <= len) {
+        uint4 r[kPer];
+        uint32_t esc_steps = 0;
+        if (enc_records_fast<kMode, kImplicit, kPer>(a, tb, lane, j * SB + wid - 1, kEncMappers,
+                                                     start, ca, cb, cm, hash, status, znib,
+                                                     esc_steps, r)) {
+          put_records(j, r, true, esc_steps);
+          return;
+        }
+      }
       // LDS tables for the whole block when every active lane's table is staged
       bool lds = tb.nt > 0;
       if (!kImplicit && lds) {
@@ -1288,6 +1377,10 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
     // and one per block.  Keeping the roles apart also keeps the mappers'
     // loads in flight out of the coder's wait bookkeeping.
     if (wid == 0) {
+      // The coder's chain of dependent steps bounds the block loop; its
+      // instructions go first when mapper waves of this or another
+      // workgroup on the CU compete for the same SIMD.
+      __builtin_amdgcn_s_setprio(3);
       __syncthreads();
       pc.mark(3);
       pc.cycles(12);
@@ -3221,6 +3314,7 @@ int encode_prepare(int mode, bool implicit, int32_t n_scales, float scale_bound,
   // fused encode: unit numbers from tickets unless the grid fits the device
   // in one round at the plan's workgroups per CU
   a.ticket = L.U > plan.occ * (int64_t)dl.cus ? 1u : 0u;
+  a.elect = L.U > (int64_t)dl.cus ? 1u : 0u;
   a.lds_bytes = (uint32_t)lds;
   // 8 mapper waves when every workgroup has a CU to itself
   const int nm = plan.occ == 1 && L.U <= dl.cus ? 8 : 4;

@@ -446,9 +446,11 @@ int gaans_enqueue_decode(const gaans_plan* plan, void* stream, const uint8_t* pa
  * 3 the first coding step (first block ready), 4 after the last step,
  * 5 before and 6 after the unit's completion-counter atomic (fused encode:
  * its look-back), 7 (the unit that wrote the completion word) after it; the
- * shader clock at 12 the first and 13 after the last step, and 14 the shader
- * cycles the coder wave spent in its block barriers.  Other slots are not
- * written.  NULL (or
+ * fused encode's pack at 8 (the unit's payload offset known), 9 (the word
+ * stores issued) and 10 (its stores completed); the shader clock at 12 the
+ * first and 13 after the last step, 14 the shader cycles the coder wave spent
+ * in its block barriers, and 15 the coder wave's XCC_ID << 32 | HW_ID.
+ * Other slots are not written.  NULL (or
  * units <= 0) turns it off; a launch picks the setting up when it is bound,
  * so it is process-wide and not for concurrent callers.  The points are taken
  * in scalar registers and stored once per unit.  wall_clock_khz (may be NULL) receives the real-time

@@ -67,8 +67,9 @@ def test_segment_layout_and_choice():
     assert three.max_payload_bytes - three.header_bytes - (
         one.max_payload_bytes - one.header_bytes) == 48 * 2 * (64 * 4 + 8)
     assert three.header_bytes == (64 + 8 * 144 + 15) // 16 * 16
-    # a unit holds at most ceil(96 / 3) = 32 steps: its staging words
-    assert three.cap_words == 32 * 64 + 2
+    # a unit holds at most ceil(96 / 3) = 32 steps: its staging words (one
+    # per symbol, 2 more, rounded to whole 16-byte chunks)
+    assert three.cap_words == 32 * 64 + 8
     # at least one step per segment (the shortest chunk decides), at most 256
     _native.layout(1, N, 192, 4, 96)
     for bad in ((1, N, 192, 4, 97), (1, N, 192, 4, 0), (1, 64 * 300, 1, 1, 257),
