@@ -31,7 +31,7 @@ constexpr uint32_t kVersion = 4u;
 constexpr int kMaxSegments = 256;  // segments per chunk
 constexpr uint32_t kParams = 0x00041040u;  // lanes 64 | precision 16 << 8 | bypass 4 << 16
 constexpr int kFixedWords = 16;
-constexpr uint32_t kTabMagic = 0x36425447u;  // "GTB6"
+constexpr uint32_t kTabMagic = 0x37425447u;  // "GTB7"
 constexpr int kLutBits = 8;
 constexpr int kLutSize = 1 << kLutBits;
 constexpr int kSubBits = 4;                 // a sub-block: 16 entries of 16 or 1 values

@@ -121,9 +121,11 @@ int64_t tables_size(int32_t M, int64_t total_syms, int64_t total_blocks, int64_t
 }
 
 // Search lookups of one table (symbols base .. base + nsym - 1 of the blob):
-// per 256-value bucket, the symbol that contains the bucket's first value
-// (blob-wide index) in the low half and the number of symbols that start
-// inside the bucket after it in the high half; starts[base + s] = cdf[s].
+// per 256-value bucket, the symbol g that contains the bucket's first value
+// (blob-wide index, bits 0-15), the number n of symbols that start inside
+// the bucket after it (bits 16-23: at most 255, one per value after the
+// first) and the number h of those that start in its first half (bits
+// 24-31); starts[base + s] = cdf[s].
 void build_search(const int32_t* c, uint32_t nsym, uint32_t base, uint32_t* clut,
                   uint16_t* starts) {
   for (uint32_t v = 0; v < nsym; ++v) starts[base + v] = (uint16_t)c[v];
@@ -132,9 +134,12 @@ void build_search(const int32_t* c, uint32_t nsym, uint32_t base, uint32_t* clut
   for (uint32_t b = 0; b < (uint32_t)kLutSize; ++b) {
     const uint32_t lo = b * width;
     while (s + 1 < nsym && (uint32_t)c[s + 1] <= lo) ++s;
-    uint32_t n = 0;
-    while (s + 1 + n < nsym && (uint32_t)c[s + 1 + n] < lo + width) ++n;
-    clut[b] = (base + s) | ((n < 0xffffu ? n : 0xffffu) << 16);
+    uint32_t n = 0, h = 0;
+    while (s + 1 + n < nsym && (uint32_t)c[s + 1 + n] < lo + width) {
+      h += (uint32_t)c[s + 1 + n] < lo + width / 2 ? 1u : 0u;
+      ++n;
+    }
+    clut[b] = (base + s) | (n << 16) | (h << 24);
   }
 }
 

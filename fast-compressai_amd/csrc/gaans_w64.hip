@@ -1787,24 +1787,30 @@ __device__ __forceinline__ void dec_lookup(const Tabs& tb, uint32_t t, uint32_t 
   fr = up ? nxt + 1u : st1 - st0;
 }
 
-// cum -> (symbol, start, freq) with the search lookups, all tables in LDS:
-// the bucket entry gives g, the blob-wide index of the symbol that contains
-// the bucket's first value, and n, the symbols that start inside the bucket
-// after it.  A bucket with more than three is first narrowed by a 4-way
-// search over its starts (three probe reads per round trip, uniform loop
-// while any lane has more than three left); one read of starts g .. g + 4
-// then resolves the rest.  s is blob-wide (the record carries offset - base); the freq of a
-// table's last symbol comes from the next start modulo 2^16, which is the
-// next table's first start or a zero sentinel, both 0.
+// cum -> (symbol, start, freq) with the search lookups, all tables in LDS.
+// The bucket entry gives g, the blob-wide index of the symbol that contains
+// the bucket's first value, n, the symbols that start inside the bucket
+// after it, and h, those of them that start in its first half, so the
+// symbol is among g .. g + h when cum is in the first half and among
+// g + h .. g + n otherwise.  More than three candidates are first narrowed
+// by a 4-way search over their starts (three probe reads per round trip,
+// uniform loop while any lane has more than three left); one read of starts
+// g .. g + 4 then resolves the rest.  s is blob-wide (the record carries
+// offset - base); the freq of a table's last symbol comes from the next
+// start modulo 2^16, which is the next table's first start or a zero
+// sentinel, both 0.
 __device__ __forceinline__ void dec_lookup_search(const Tabs& tb, uint32_t t, uint32_t cum,
                                                   bool act, uint32_t& s, uint32_t& st,
                                                   uint32_t& fr) {
   const uint32_t e = tb.lclut[(t << kLutBits) + (cum >> (16 - kLutBits))];
-  uint32_t g = e & 0xffffu, n = e >> 16;
+  const uint32_t n0 = (e >> 16) & 0xffu, h = e >> 24;
+  const bool upper = (cum & (1u << (15 - kLutBits))) != 0u;
+  // invariant: start(g) <= cum, and the symbol is among g .. g + n
+  uint32_t g = (e & 0xffffu) + (upper ? h : 0u);
+  uint32_t n = upper ? n0 - h : h;
   bool wide = act & (n > 3u);
   if (__builtin_expect(ballot(wide) != 0ull, 0)) {
-    // invariant: start(g) <= cum, and the symbol is among g .. g + n; the
-    // probes q, 2q, 3q (q = (n + 1) / 4 >= 1) split it into four ranges
+    // the probes q, 2q, 3q (q = (n + 1) / 4 >= 1) split it into four ranges
     do {
       if (wide) {
         const uint32_t q = (n + 1u) >> 2;

@@ -273,16 +273,20 @@ def test_prepared_tables_dense_tail_lookup():
 
 def host_search(blob, t, cum, counts=None):
     """The decoder's search lookup, read from the prepared blob: bucket entry
-    (blob-wide symbol g containing the bucket's first value | starts inside
-    the bucket n << 16); while more than three start inside, split the range
-    four ways with three start reads; then starts g .. g + 4 resolve the
-    rest; freq from the next start modulo 2^16 (the next table's first
-    start, or the zero sentinel, is 0)."""
+    (blob-wide symbol g containing the bucket's first value | starts n inside
+    the bucket after it << 16 | those h of them in its first half << 24); the
+    half that holds cum narrows the candidates to g .. g + h or g + h ..
+    g + n; while more than three remain, split them four ways with three
+    start reads; then starts g .. g + 4 resolve the rest; freq from the next
+    start modulo 2^16 (the next table's first start, or the zero sentinel,
+    is 0).  counts[rounds] tallies the 4-way rounds."""
     hdr = struct.unpack_from("<16I", blob, 0)
     clut_off, starts_off = hdr[14], hdr[15]
     ent_base = struct.unpack_from("<I", blob, hdr[6] + 16 * t)[0]
     e = struct.unpack_from("<I", blob, clut_off + 4 * (256 * t + (cum >> 8)))[0]
-    g, n = e & 0xFFFF, e >> 16
+    n0, h = (e >> 16) & 0xFF, e >> 24
+    assert h <= n0
+    g, n = ((e & 0xFFFF) + h, n0 - h) if cum & 128 else (e & 0xFFFF, h)
     rounds = 0
     while n > 3:  # 4-way: probes q, 2q, 3q
         q = (n + 1) >> 2
