@@ -181,7 +181,8 @@ def phase_breakdown(L, torch, dev, units, steps, fn):
 
 
 def unit_steps(B, N, C, P, S):
-    """Coding steps of every unit (64 positions a step), unit order."""
+    """Coding steps of every unit (64 positions a step), unit order: segment s
+    of a Tc-step chunk holds the steps s, s + S, ..."""
     import math
 
     K = math.ceil(C / P)
@@ -192,7 +193,7 @@ def unit_steps(B, N, C, P, S):
             ln = min(chunk_len, N - k * chunk_len)
             tc = (ln + 63) // 64
             for s_ in range(S):
-                out.append((s_ + 1) * tc // S - s_ * tc // S)
+                out.append((tc - s_ + S - 1) // S)
     return out
 
 

@@ -27,7 +27,7 @@ namespace gaans {
 constexpr int kLanes = 64;
 constexpr uint32_t kStateLow = 1u << 16;  // rANS L
 constexpr uint32_t kMagic = 0x31574147u;  // "GAW1"
-constexpr uint32_t kVersion = 4u;
+constexpr uint32_t kVersion = 5u;
 constexpr int kMaxSegments = 256;  // segments per chunk
 constexpr uint32_t kParams = 0x00041040u;  // lanes 64 | precision 16 << 8 | bypass 4 << 16
 constexpr int kFixedWords = 16;
@@ -162,10 +162,11 @@ uint32_t enc_magic(uint32_t f);
 
 // Chunks and coding units.  Chunk k of a row covers the positions
 // [k chunk_len, min((k + 1) chunk_len, N)) (P channels), Tc steps of 64
-// positions; it is split into S segments, segment s holding the steps
-// [floor(s Tc / S), floor((s + 1) Tc / S)).  A segment is a coding unit, coded
-// independently (own states, stream and escape section) by its own
-// workgroup: unit g = (b K + k) S + s, U = B K S units.
+// positions; it is split into S interleaved segments, segment s holding the
+// steps s, s + S, s + 2 S, ... (so every segment sees the chunk's channels in
+// equal shares).  A segment is a coding unit, coded independently (own
+// states, stream and escape section) by its own workgroup:
+// unit g = (b K + k) S + s, U = B K S units.
 struct Layout {
   int64_t B, N, C, P, S, HW, K, chunk_len, U, seg_cap, header_bytes, max_payload, cap_words,
       ws_bytes;
@@ -188,10 +189,18 @@ GAANS_HD void unit_range(int64_t g, int32_t K, int32_t S, int64_t N,
   const int32_t cs = k * chunk_len;
   const int32_t ce = (int64_t)cs + chunk_len < N ? cs + chunk_len : (int32_t)N;
   const int32_t tc = (ce - cs + kLanes - 1) / kLanes;
-  const int32_t t0 = (int32_t)((int64_t)s * tc / S), t1 = (int32_t)((int64_t)(s + 1) * tc / S);
-  start = cs + kLanes * t0;
-  const int32_t e = cs + kLanes * t1 < ce ? cs + kLanes * t1 : ce;
-  len = e - start;
+  // the unit's steps s, s + S, ..., s + S (T - 1) of the chunk; only the
+  // chunk's last step (unit (tc - 1) mod S) may be partial
+  const int32_t T = (tc - s + S - 1) / S;
+  const int32_t last = s + S * (T - 1);
+  start = cs + kLanes * s;
+  len = kLanes * T - (last == tc - 1 ? kLanes * tc - (ce - cs) : 0);
+}
+
+// Row position of unit position p (lane p mod 64 of the unit's step p / 64)
+// in a unit that starts at row position start, S segments per chunk.
+GAANS_HD int32_t unit_pos(int32_t start, int32_t S, int32_t p) {
+  return start + p + kLanes * (S - 1) * (p >> 6);
 }
 
 GAANS_HD int unit_len(int64_t g, int32_t K, int32_t S, int64_t N,

@@ -683,7 +683,8 @@ __device__ __forceinline__ void enc_records(const EncArgs& a, const Tabs& tb, in
   for (int e = 0; e < KP; ++e) {
     const int p = lane + kLanes * (t0 + tstep * e);
     const bool act = (e < nvalid) & (p < len);
-    int32_t tbi = kImplicit ? (int32_t)udiv((uint32_t)(start + p), a.div_hw) : in_b[e];
+    int32_t tbi =
+        kImplicit ? (int32_t)udiv((uint32_t)unit_pos(start, a.S, p), a.div_hw) : in_b[e];
     const bool bad = act & ((uint32_t)tbi >= a.M);
     ok[e] = act & !bad;
     status |= bad ? GAANS_ST_INDEX : 0u;
@@ -773,7 +774,8 @@ __device__ __forceinline__ bool enc_records_fast(const EncArgs& a, const Tabs& t
 #pragma unroll
   for (int e = 0; e < KP; ++e) {
     const int p = lane + kLanes * (t0 + tstep * e);
-    const int32_t tbi = kImplicit ? (int32_t)udiv((uint32_t)(start + p), a.div_hw) : in_b[e];
+    const int32_t tbi =
+        kImplicit ? (int32_t)udiv((uint32_t)unit_pos(start, a.S, p), a.div_hw) : in_b[e];
     bad |= ballot((uint32_t)(tbi - tb.t_lo) >= (uint32_t)tb.nt);  // staged tables are below M
     tbl[e] = (uint32_t)tbi;
     h += index_term((uint32_t)p, (uint32_t)tbi);
@@ -1267,11 +1269,14 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
   const void* in_b_ptr = kMode == kModeGaussian ? (const void*)a.scales : (const void*)a.indexes;
   const bool has_b = kMode == kModeGaussian || !kImplicit;
   const bool has_m = kMode == kModeGaussian && a.means != nullptr;
-  const __amdgpu_buffer_rsrc_t rin_a = unit_rsrc(in_a_ptr, row + start, len);
+  // positions start .. start + span - 1 of the row hold the unit's steps
+  // (every S-th step of the chunk from the unit's first)
+  const int span = len > 0 ? unit_pos(start, a.S, len - 1) + 1 - start : 0;
+  const __amdgpu_buffer_rsrc_t rin_a = unit_rsrc(in_a_ptr, row + start, span);
   const __amdgpu_buffer_rsrc_t rin_b = unit_rsrc(has_b ? in_b_ptr : in_a_ptr, row + start,
-                                                 has_b ? len : 0);
+                                                 has_b ? span : 0);
   const __amdgpu_buffer_rsrc_t rin_m = unit_rsrc(has_m ? (const void*)a.means : in_a_ptr,
-                                                 row + start, has_m ? len : 0);
+                                                 row + start, has_m ? span : 0);
   const int lane4 = 4 * lane;
   auto load_block = [&](int j, int32_t* ia, int32_t* ib, float* im) __attribute__((always_inline)) {
 #pragma unroll
@@ -1280,7 +1285,7 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
       if (SB % kEncMappers != 0 && u >= SB) break;
       // the range check covers the vector offset only (not a scalar one),
       // so the step's offset is added to the lane's
-      const int vo = lane4 + uni(4 * kLanes * (j * SB + u));
+      const int vo = lane4 + uni(4 * kLanes * a.S * (j * SB + u));
       ia[e] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rin_a, vo, 0, 0);
       if (kMode == kModeGaussian) {
         im[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin_m, vo, 0, 0));
@@ -1290,7 +1295,7 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
         if (kMode == kModeLatents) {
           int p = lane + kLanes * (j * SB + u);
           p = p < len ? p : len - 1;  // the median's channel stays in the chunk
-          im[e] = a.medians[udiv((uint32_t)(start + p), a.div_hw)];
+          im[e] = a.medians[udiv((uint32_t)unit_pos(start, a.S, p), a.div_hw)];
         } else {
           im[e] = 0.0f;
         }
@@ -1685,7 +1690,8 @@ __device__ __forceinline__ uint2 dec_record(const DecArgs& a, const Tabs& tb, in
                                             uint32_t& hash, uint32_t& status, bool& all_lds) {
   const int p = lane + kLanes * t;
   const bool act = p < len;
-  int32_t tbi = kImplicit ? (int32_t)udiv((uint32_t)(start + p), a.div_hw) : in_b;
+  int32_t tbi =
+      kImplicit ? (int32_t)udiv((uint32_t)unit_pos(start, (int32_t)a.S, p), a.div_hw) : in_b;
   const bool bad = act & ((uint32_t)tbi >= a.M);
   const bool ok = act & !bad;
   status |= bad ? GAANS_ST_INDEX : 0u;
@@ -2246,12 +2252,13 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
       if (SB % kMappers != 0 && u >= SB) break;
       int p = lane + kLanes * (j * SB + u);
       p = p < len ? p : len - 1;  // loads stay in the chunk; results are masked
+      const int32_t q = unit_pos(start, (int32_t)a.S, p);  // row position
       if (kMode == kModeGaussian) {
-        ib[e] = __float_as_int(a.scales[row + start + p]);  // index found at map time
-        im[e] = a.means ? a.means[row + start + p] : 0.0f;
+        ib[e] = __float_as_int(a.scales[row + q]);  // index found at map time
+        im[e] = a.means ? a.means[row + q] : 0.0f;
       } else {
-        ib[e] = kImplicit ? 0 : a.indexes[row + start + p];
-        im[e] = kLatents ? a.medians[udiv((uint32_t)(start + p), a.div_hw)] : 0.0f;
+        ib[e] = kImplicit ? 0 : a.indexes[row + q];
+        im[e] = kLatents ? a.medians[udiv((uint32_t)q, a.div_hw)] : 0.0f;
       }
     }
   };
@@ -2336,7 +2343,7 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
         if (SB % kMappers != 0 && u >= SB) break;
         const int p = lane + kLanes * (j * SB + u);
         if (p < len) {
-          const int64_t i = row + start + p;
+          const int64_t i = row + unit_pos(start, (int32_t)a.S, p);
           if (kLatents)
             a.out_y[i] = __fadd_rn((float)(int32_t)vals[e],
                                    med[((j & 1) * SB + u) * kLanes + lane]);

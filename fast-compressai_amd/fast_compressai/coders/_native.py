@@ -15,7 +15,7 @@ import threading
 from .errors import CoderDependencyError
 
 LIB_NAME = "libgaans_w64.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 CTRL_BYTES = 256
 PLAN_BYTES = 1536  # GAANS_PLAN_BYTES
 PHASE_SLOTS = 16  # GAANS_PHASE_SLOTS

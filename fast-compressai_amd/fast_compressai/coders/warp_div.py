@@ -9,7 +9,7 @@ payloads and ``CoderDependencyError`` for a missing library or device.
 
 Differences that follow from the new format:
 
-* ``format_id`` is ``"gaans-w64-v4"``; payloads of the reference's
+* ``format_id`` is ``"gaans-w64-v5"``; payloads of the reference's
   ``warpans-v2`` format are rejected.
 * ``segments`` (keyword of ``encode``, field of the payload) splits every
   chunk of P channels into that many independently coded units (1..256);
@@ -40,8 +40,8 @@ from .capabilities import warp_div_capability
 from .errors import CoderDependencyError, CoderInputError
 from .tables import PreparedTables, TableCache
 
-FORMAT_ID = "gaans-w64-v4"
-FORMAT_VERSION = 4
+FORMAT_ID = "gaans-w64-v5"
+FORMAT_VERSION = 5
 MAX_SEGMENTS = 256
 _HEADER_MAGIC = 0x31574147
 _FIXED_HEADER_BYTES = 64

@@ -37,18 +37,19 @@
  *    launch's completion word is set (gaans_wait_host_word).
  *
  *  - `segments` (S, 1..256) splits every chunk of P channels into S
- *    segments of whole 64-position steps (segment s: steps
- *    [floor(s Tc / S), floor((s+1) Tc / S)) of a Tc-step chunk).  Each
- *    segment is a coding unit with its own states, words and escapes, coded
- *    by its own workgroup, so a launch of few long chunks uses S times more
- *    CUs, for 4 * 64 more bytes per extra unit.  Every unit holds at least
- *    one step: S <= the steps of a row's last (shortest) chunk.  The payload
- *    header records S and decode must be called with the same value.
+ *    interleaved segments of whole 64-position steps (segment s: steps s,
+ *    s + S, s + 2 S, ... of the chunk, so every segment sees the chunk's
+ *    channels in equal shares).  Each segment is a coding unit with its own
+ *    states, words and escapes, coded by its own workgroup, so a launch of
+ *    few long chunks uses S times more CUs, for 4 * 64 more bytes per extra
+ *    unit.  Every unit holds at least one step: S <= the steps of a row's
+ *    last (shortest) chunk.  The payload header records S and decode must be
+ *    called with the same value.
  *    U = B * K * S coding units per call, at most 2^24 - 1, and a shape's
  *    worst-case payload (7 bytes per symbol plus 264 per unit) must stay
  *    below 2^38 bytes; larger calls return GAANS_EINVAL.
  *
- * Payload format "gaans-w64-v4": defined byte for byte by the CPU oracle,
+ * Payload format "gaans-w64-v5": defined byte for byte by the CPU oracle,
  * oracle/gaans_oracle.c.
  */
 #ifndef GAANS_W64_H
@@ -61,7 +62,7 @@
 extern "C" {
 #endif
 
-#define GAANS_ABI_VERSION 12
+#define GAANS_ABI_VERSION 13
 #define GAANS_CTRL_BYTES 256
 
 /* return codes */

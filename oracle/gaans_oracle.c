@@ -3,7 +3,7 @@
  * (see gaans_oracle.h): the product path never links or calls this file.
  *
  * ===========================================================================
- * The wave64 GA-ANS payload format, "gaans-w64-v4"
+ * The wave64 GA-ANS payload format, "gaans-w64-v5"
  * ===========================================================================
  * Coding parameters: 16-bit CDF precision; one 32-bit rANS state per lane,
  * x in [2^16, 2^32), initial state 2^16; 16-bit renormalisation words;
@@ -13,16 +13,19 @@
  * HW = N / C positions.  P channels form one chunk, K = ceil(C / P) chunks per
  * row, chunk_len = P * HW; chunk k of row b covers positions
  * [k*chunk_len, min((k+1)*chunk_len, N)), clen of them, Tc = ceil(clen / 64)
- * steps of 64 positions.  Each chunk is split into S segments
- * ("segments per chunk", 1 <= S <= min(256, Tc of every chunk)): segment s
- * covers the steps [floor(s Tc / S), floor((s+1) Tc / S)) of the chunk, i.e.
- * positions [64 floor(s Tc / S), min(64 floor((s+1) Tc / S), clen)).  A
- * segment is a coding unit: unit g = (b K + k) S + s, U = B K S units, each
- * coded on its own (own states, own word stream, own escape section), so
- * the units of a chunk can be coded in parallel.  In a unit of len symbols
- * A = min(64, len) lanes are active; lane l owns positions l + 64 t
- * (t >= 0) of the unit, so the 64 lanes of one step read 64 consecutive
- * positions; T = ceil(len / 64) steps.
+ * steps of 64 positions (step j: chunk positions [64 j, min(64 j + 64, clen))).
+ * Each chunk is split into S interleaved segments ("segments per chunk",
+ * 1 <= S <= min(256, Tc of every chunk)): segment s holds the steps
+ * s, s + S, s + 2 S, ... of the chunk, T = ceil((Tc - s) / S) of them, so
+ * the segments of a chunk see its channels in equal shares.  A segment is a
+ * coding unit: unit g = (b K + k) S + s, U = B K S units, each coded on its
+ * own (own states, own word stream, own escape section), so the units of a
+ * chunk can be coded in parallel.  The unit's steps, in that order, give its
+ * len positions: unit position p = l + 64 t (lane l of unit step t) is chunk
+ * position 64 (s + S t) + l; len = 64 T, less the lanes the chunk's last
+ * step lacks when that step is the unit's last (unit s = (Tc - 1) mod S).
+ * In a unit A = min(64, len) lanes are active, so the 64 lanes of one step
+ * read 64 consecutive positions.
  *
  * Symbol mapping (CompressAI's escape scheme; reference
  * warp_ans_kernel_v2.cu:139-169).  With table tb = index of the position,
@@ -311,7 +314,7 @@ int rans64_ref_decode(const uint32_t* words, int64_t n_words,
 #define W_LANES 64
 #define W_L ((uint32_t)1 << 16)
 #define W_MAGIC 0x31574147u
-#define W_VERSION 4u
+#define W_VERSION 5u
 #define W_PARAMS 0x00041040u
 #define W_FIXED_WORDS 16
 
@@ -340,7 +343,8 @@ static int w_layout_of(int32_t B, int32_t N, int32_t C, int32_t P, int32_t S, w_
   return GAANS_REF_OK;
 }
 
-/* row b and the positions [*start, *start + *len) of unit g */
+/* row b, the row position *start of unit g's first symbol and its symbol
+ * count *len (see w_pos for the others) */
 static void w_unit(const w_layout* L, int64_t g, int64_t* b, int64_t* start, int32_t* len) {
   int64_t per_row = (int64_t)L->K * L->S;
   *b = g / per_row;
@@ -348,10 +352,16 @@ static void w_unit(const w_layout* L, int64_t g, int64_t* b, int64_t* start, int
   int64_t cs = k * (int64_t)L->chunk_len;
   int64_t ce = cs + L->chunk_len < L->N ? cs + L->chunk_len : L->N;
   int64_t Tc = (ce - cs + W_LANES - 1) / W_LANES;
-  int64_t t0 = s * Tc / L->S, t1 = (s + 1) * Tc / L->S;
-  int64_t e = cs + W_LANES * t1 < ce ? cs + W_LANES * t1 : ce;
-  *start = cs + W_LANES * t0;
-  *len = (int32_t)(e - *start);
+  int64_t T = (Tc - s + L->S - 1) / L->S;  /* steps s, s + S, ..., s + S (T - 1) */
+  int64_t last = s + L->S * (T - 1);      /* the unit's last step */
+  *start = cs + W_LANES * s;
+  *len = (int32_t)(W_LANES * T - (last == Tc - 1 ? W_LANES * Tc - (ce - cs) : 0));
+}
+
+/* row position of unit position p (lane p mod 64 of unit step p / 64) in a
+ * unit that starts at row position start, S segments per chunk */
+static int64_t w_pos(int64_t start, int32_t S, int64_t p) {
+  return start + p + (int64_t)W_LANES * (S - 1) * (p / W_LANES);
 }
 
 int64_t gaans_ref_max_payload_bytes(int32_t B, int32_t N, int32_t C, int32_t P, int32_t S) {
@@ -432,7 +442,7 @@ static int w_nibs_push(w_nibs* z, uint32_t v) {
 }
 
 static int w_encode_unit(const int32_t* sym, const int32_t* idx_row, int64_t start,
-                          int32_t len, int32_t HW, const int32_t* cdfs, int32_t M,
+                          int32_t len, int32_t S_seg, int32_t HW, const int32_t* cdfs, int32_t M,
                           int32_t Lmax, const int32_t* sizes, const int32_t* offsets,
                           uint8_t** out, int64_t* out_bytes, uint32_t* hash_out) {
   int A = len < W_LANES ? len : W_LANES;
@@ -448,7 +458,7 @@ static int w_encode_unit(const int32_t* sym, const int32_t* idx_row, int64_t sta
   uint32_t hash = 0;
   /* pass 1, position order: rANS op of every symbol and the escape section */
   for (int32_t p = 0; p < len; ++p) {
-    int64_t i = start + p;
+    int64_t i = w_pos(start, S_seg, p);
     int32_t tb = idx_row ? idx_row[i] : (int32_t)(i / HW);
     if (tb < 0 || tb >= M) { rc = GAANS_REF_EINDEX; goto fail; }
     hash += index_term(p, tb);
@@ -541,7 +551,7 @@ int gaans_ref_encode(const int32_t* symbols, const int32_t* indexes,
     int32_t len;
     w_unit(&L, g, &b, &start, &len);
     rc = w_encode_unit(symbols + b * (int64_t)N, indexes ? indexes + b * (int64_t)N : NULL,
-                       start, len, L.HW, cdfs, M, Lmax, cdf_sizes, offsets, &units[g],
+                       start, len, L.S, L.HW, cdfs, M, Lmax, cdf_sizes, offsets, &units[g],
                        &cbytes[g], &hashes[g]);
     if (rc) goto done;
   }
@@ -628,7 +638,7 @@ int gaans_ref_decode(const uint8_t* payload, int64_t payload_len,
         int64_t p = l + (int64_t)W_LANES * t;
         need[l] = 0;
         if (p >= len) continue;
-        int64_t i = start + p;
+        int64_t i = w_pos(start, L.S, p);
         int32_t tb = idx_row ? idx_row[i] : (int32_t)(i / L.HW);
         if (tb < 0 || tb >= M) return GAANS_REF_EINDEX;
         hash += index_term(p, tb);

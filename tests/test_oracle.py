@@ -165,7 +165,7 @@ def test_index_hash_detects_a_swapped_pair():
 
 
 def header_words(B, N, C, P, K, chunk_len, M, digest, segments=1):
-    return [0x31574147, 4, B, N, C, P, K, chunk_len, M, 0x00041040,
+    return [0x31574147, 5, B, N, C, P, K, chunk_len, M, 0x00041040,
             digest & 0xFFFFFFFF, digest >> 32, segments, 0, 0, 0]
 
 
@@ -256,17 +256,46 @@ def test_gaans_kat_three_segments():
             O.gaans_decode(data, None, 1, 130, cdfs, sizes, offs, 1, segments=other)
 
 
-def segment_bounds(T, S):
-    """Steps of a T-step chunk in segment s: [floor(s T / S), floor((s+1) T / S))."""
-    return [(s * T // S, (s + 1) * T // S) for s in range(S)]
+def test_gaans_kat_two_interleaved_segments():
+    # the 130-symbol chunk (3 steps) in S = 2 segments: unit 0 is steps 0 and
+    # 2 (positions 0..63, then 128 and 129 as its step 1), unit 1 is step 1.
+    # Unit 0, walked last step first: at its step 1 lane 0 emits its initial
+    # 0x0000 and holds 0x10000 + s[128]; lane 1 escapes (raw 2) and holds
+    # 0x10020; the other lanes are inactive.  At its step 0 lane 0 emits
+    # s[128] and lane 1 emits 0x0020 (both then hold 0x10000 + s[l]), lane 3
+    # escapes (raw 1) from 0x10000 to 0x10020 with no word, every other lane
+    # emits 0x0000.  Stream: step 0's group (63 words), then step 1's (1).
+    # Escapes in unit position order: p=3 -> [1, 1], p=65 -> [1, 2]: nibbles
+    # 1,1,1,2 -> word 0x2111; 64 + 1 words is odd, so a zero pad precedes it.
+    # Unit 1 is step 1 coded alone (as unit 1 of the three-segment case).
+    cdfs, sizes, offs, s = kat_130()
+    data = O.gaans_encode([s], None, cdfs, sizes, offs, 1, segments=2)
+    st0 = [0x10000 + s[l] for l in range(64)]
+    st0[3] = 0x10020
+    w0 = [s[128], 0x0020] + [0] * 61 + [0] + [0, 0x2111]
+    st1 = [0x10000 + s[64 + l] for l in range(64)]
+    st1[6] = 0x10020
+    u0 = struct.pack("<64I", *st0) + struct.pack(f"<{len(w0)}H", *w0)
+    u1 = struct.pack("<64I", *st1) + struct.pack("<64H", *([0] * 63 + [0x0502]))
+    assert (len(u0), len(u1)) == (388, 384)
+    dg = fnv1a64(table_digest_bytes(cdfs, sizes, offs))
+    hdr = header_words(1, 130, 1, 1, 1, 130, 1, dg, segments=2) + [
+        388, 772, hash_of([0] * 66), hash_of([0] * 64)]
+    assert data == struct.pack("<20I", *hdr) + u0 + u1
+    assert O.gaans_decode(data, None, 1, 130, cdfs, sizes, offs, 1, segments=2).tolist() == [s]
+
+
+def segment_steps(T, S):
+    """Steps of a T-step chunk in segment s, in the unit's order: s, s + S, ..."""
+    return [list(range(s, T, S)) for s in range(S)]
 
 
 def test_gaans_segments_are_independent_units():
     # Every unit of an S-segment payload is, byte for byte, the one-chunk
-    # payload of its own positions coded alone (B = 1, one channel, the
-    # positions' tables as explicit indexes): same states, words, escapes
-    # and index hash.  The segment bounds are computed here independently of
-    # the oracle.
+    # payload of its own positions, in its steps' order, coded alone (B = 1,
+    # one channel, the positions' tables as explicit indexes): same states,
+    # words, escapes and index hash.  The segments' steps are computed here
+    # independently of the oracle.
     rng = np.random.default_rng(5)
     for trial in range(20):
         B, C = int(rng.integers(1, 3)), int(rng.integers(1, 6))
@@ -285,11 +314,12 @@ def test_gaans_segments_are_independent_units():
         for b in range(B):
             for k in range(K):
                 cs, ce = k * P * HW, min((k + 1) * P * HW, N)
-                for t0, t1 in segment_bounds(-(-(ce - cs) // 64), S):
-                    lo, hi = cs + 64 * t0, min(cs + 64 * t1, ce)
-                    assert hi > lo
-                    seg = s[b, lo:hi][None]
-                    tabs = (np.arange(lo, hi) // HW).astype(np.int32)[None]
+                for steps in segment_steps(-(-(ce - cs) // 64), S):
+                    assert steps
+                    pos = np.concatenate([np.arange(cs + 64 * j, min(cs + 64 * j + 64, ce))
+                                          for j in steps])
+                    seg = s[b, pos][None]
+                    tabs = (pos // HW).astype(np.int32)[None]
                     alone = O.gaans_encode(seg, tabs, cdfs, sizes, offs, 1, channels=1)
                     hb1 = (64 + 8 + 15) // 16 * 16
                     assert data[hb + prev: hb + ends[g]] == alone[hb1:]
