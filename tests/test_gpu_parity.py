@@ -154,6 +154,32 @@ def test_explicit_random_indexes_bit_exact(backend, gpu_device, segments):
         check_workload(backend, gpu_device, w, channels=C, segments=segments)
 
 
+@pytest.mark.parametrize("segments", [1, 2])
+def test_offsets_near_int32_max_bit_exact(backend, gpu_device, segments):
+    # Table offsets above INT32_MAX - 65535 turn the kernels' fast record
+    # paths off (symbol - offset may then leave 32 bits; the blob's flag says
+    # so), so full blocks take the checked paths: escapes below the tables'
+    # ranges down to offset - 2^31 (the lowest codable value, raw 2^32 - 1)
+    # and above them up to INT32_MAX, next to in-range symbols, with a ragged
+    # last step.
+    rng = np.random.default_rng(31)
+    C, HW, P = 6, 64 * 12 + 5, 3
+    cdfs, sizes, _ = random_tables(rng, C, 12)
+    offs = (2**31 - 100 - rng.integers(0, 60000, C)).astype(np.int64)
+    sym = np.empty((1, C * HW), np.int64)
+    for c in range(C):
+        o, S = int(offs[c]), int(sizes[c])
+        kind = rng.integers(0, 10, HW)
+        inside = o + rng.integers(0, max(1, S - 2), HW)
+        below = o - 2**31 + rng.integers(0, 1000, HW)
+        above = 2**31 - 1 - rng.integers(0, 1000, HW)
+        sym[0, c * HW:(c + 1) * HW] = np.where(kind < 7, inside, np.where(kind < 9, above, below))
+    assert sym.min() >= -2**31 and sym.max() <= 2**31 - 1
+    w = synthetic.Workload("offsets near INT32_MAX", sym.astype(np.int32), None, cdfs, sizes,
+                           offs.astype(np.int32), C, P, 0)
+    check_workload(backend, gpu_device, w, segments=segments)
+
+
 def test_long_chunks_with_partial_last_block(backend, gpu_device):
     # chunks of 32,800 symbols (C=8, HW=4100, P=8): 513 steps, so with one
     # segment the encoder's 16-step blocks end with a one-step block (two and
