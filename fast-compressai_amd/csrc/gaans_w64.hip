@@ -45,6 +45,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <chrono>
 #include <mutex>
 #include <string>
 #include <type_traits>
@@ -3712,10 +3713,18 @@ int plan_device(const PlanHead& h) {
 
 // Spin until the word a launch sets on completion is nonzero (see
 // gaans_wait_host_word).
+// Spins on the word; the stream is queried (a failed stream, or one that
+// drained without setting the word, ends the wait) once per 100 us of
+// spinning, so that the runtime call does not delay the word's detection
+// (a query every few hundred reads kept the thread inside it much of the
+// time).
 int wait_word(void* stream, const uint32_t* word) {
+  using clock = std::chrono::steady_clock;
+  constexpr auto kQueryEvery = std::chrono::microseconds(100);
+  auto next = clock::now() + kQueryEvery;
   for (uint32_t i = 1;; ++i) {
     if (__atomic_load_n(word, __ATOMIC_ACQUIRE) != 0) return GAANS_OK;
-    if ((i & 255u) == 0) {
+    if ((i & 63u) == 0 && clock::now() >= next) {
       const hipError_t e = hipStreamQuery(static_cast<hipStream_t>(stream));
       if (e == hipSuccess) {
         if (__atomic_load_n(word, __ATOMIC_ACQUIRE) != 0) return GAANS_OK;
@@ -3723,6 +3732,7 @@ int wait_word(void* stream, const uint32_t* word) {
       }
       if (e != hipErrorNotReady)
         return fail(GAANS_EHIP, "stream reported an error: %s", hipGetErrorString(e));
+      next = clock::now() + kQueryEvery;
     }
   }
 }

@@ -35,7 +35,7 @@ from . import _native
 from .errors import CoderInputError
 from .tables import PreparedTables
 
-_CLONE_SLACK_BYTES = 32 << 20  # keep a view of the worst-case buffer below this waste
+CLONE_SLACK_BYTES = 32 << 20  # keep a view of the worst-case buffer below this waste
 
 
 class _StreamState:
@@ -222,11 +222,12 @@ def _plan(tables: PreparedTables, decode: bool, mode: int, explicit: bool, B: in
     return got
 
 
-def _run_encode(tables: PreparedTables, mode: int, explicit: bool, B: int, N: int, C: int,
-                P: int, S: int, device, in0: int, in1, in2, in3, what: str,
-                n_scales: int = 0, bound: float = 0.0) -> EncodedChunks:
-    """Plan (cached), enqueue coding + pack into a worst-case buffer, wait for
-    the completion word and slice the payload."""
+def _run_encode_raw(tables: PreparedTables, mode: int, explicit: bool, B: int, N: int, C: int,
+                    P: int, S: int, device, in0: int, in1, in2, in3, what: str,
+                    n_scales: int = 0, bound: float = 0.0):
+    """Plan (cached), enqueue coding + pack into a worst-case buffer and wait
+    for the completion word.  Returns (buffer, payload bytes, layout): the
+    payload is the buffer's first bytes."""
     index = _index(device)
     prev = _enter_device(index)
     try:
@@ -248,8 +249,18 @@ def _run_encode(tables: PreparedTables, mode: int, explicit: bool, B: int, N: in
     total, status = word >> 16, (word >> 1) & 0x7FFF
     if status:
         raise CoderInputError(f"GA-ANS encode failed: {_native.describe_status(status)}")
+    return out, total, lay
+
+
+def _run_encode(tables: PreparedTables, mode: int, explicit: bool, B: int, N: int, C: int,
+                P: int, S: int, device, in0: int, in1, in2, in3, what: str,
+                n_scales: int = 0, bound: float = 0.0) -> EncodedChunks:
+    """``_run_encode_raw`` with the payload sliced out of the buffer (copied
+    when the buffer would waste more than CLONE_SLACK_BYTES)."""
+    out, total, lay = _run_encode_raw(tables, mode, explicit, B, N, C, P, S, device, in0, in1,
+                                      in2, in3, what, n_scales, bound)
     packed = out[:total]
-    if lay.max_payload_bytes - total > _CLONE_SLACK_BYTES:
+    if lay.max_payload_bytes - total > CLONE_SLACK_BYTES:
         packed = packed.clone()
     return EncodedChunks(packed, lay.header_bytes, lay.chunk_len, lay.K, S, B)
 
@@ -258,6 +269,17 @@ def _run_decode(tables: PreparedTables, mode: int, explicit: bool, B: int, N: in
                 P: int, S: int, device, packed: torch.Tensor, in0, in1, in2,
                 dtype: torch.dtype, what: str, n_scales: int = 0,
                 bound: float = 0.0) -> torch.Tensor:
+    return _run_decode_ptr(tables, mode, explicit, B, N, C, P, S, device, packed.data_ptr(),
+                           packed.numel(), in0, in1, in2, dtype, what, n_scales, bound)
+
+
+def _run_decode_ptr(tables: PreparedTables, mode: int, explicit: bool, B: int, N: int, C: int,
+                    P: int, S: int, device, payload_ptr: int, payload_bytes: int, in0, in1,
+                    in2, dtype: torch.dtype, what: str, n_scales: int = 0,
+                    bound: float = 0.0) -> torch.Tensor:
+    """Decode the payload of ``payload_bytes`` bytes at device address
+    ``payload_ptr`` (on ``device``) with the shape's plan; waits for the
+    completion word."""
     index = _index(device)
     prev = _enter_device(index)
     try:
@@ -266,7 +288,7 @@ def _run_decode(tables: PreparedTables, mode: int, explicit: bool, B: int, N: in
         st = _state(index, sp)
         out = torch.empty((B, N), dtype=dtype, device=st.device)
         with st.lock:
-            rc = _native.lib().gaans_run_decode(plan, sp, packed.data_ptr(), packed.numel(), in0,
+            rc = _native.lib().gaans_run_decode(plan, sp, payload_ptr, payload_bytes, in0,
                                                 in1, in2, out.data_ptr(), st.ctrl_ptr,
                                                 st.status_ptr)
             status = int(st.status_np[1]) >> 1  # 1 | status << 1
@@ -278,6 +300,26 @@ def _run_decode(tables: PreparedTables, mode: int, explicit: bool, B: int, N: in
     if status:
         raise CoderInputError(f"warp_div decode failed: {_native.describe_status(status)}")
     return out
+
+
+def encode_symbols_raw(tables: PreparedTables, B: int, N: int, C: int, P: int, device,
+                       symbols: torch.Tensor, indexes: torch.Tensor | None, segments: int):
+    """``encode`` of int32 symbols, returning (worst-case buffer, payload
+    bytes): the payload is the buffer's first bytes (no slice made)."""
+    out, total, _ = _run_encode_raw(tables, _native.MODE_SYMBOLS, indexes is not None, B, N, C,
+                                    P, segments, device, symbols.data_ptr(), _ptr(indexes),
+                                    None, None, "GA-ANS encode")
+    return out, total
+
+
+def decode_symbols_ptr(payload_ptr: int, payload_bytes: int, tables: PreparedTables, B: int,
+                       N: int, C: int, P: int, device, indexes: torch.Tensor | None,
+                       segments: int) -> torch.Tensor:
+    """``decode`` of int32 symbols from a payload given by device address and
+    size."""
+    return _run_decode_ptr(tables, _native.MODE_SYMBOLS, indexes is not None, B, N, C, P,
+                           segments, device, payload_ptr, payload_bytes, _ptr(indexes), None,
+                           None, torch.int32, "GA-ANS decode")
 
 
 def encode(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,

@@ -130,14 +130,23 @@ class WarpDivPayload:
 
     def __getattr__(self, name: str):
         # only reached for attributes missing from the instance: the lazily
-        # built chunk_ends of an encoder-made payload
+        # built fields of an encoder-made payload -- packed (the first
+        # _nbytes bytes of the encoder's buffer _buf) and chunk_ends
         d = self.__dict__
-        if name != "chunk_ends" or "packed" not in d:
+        if name == "packed":
+            buf = d.get("_buf")
+            if buf is None:
+                raise AttributeError(name)
+            packed = buf[: d["_nbytes"]]
+            d["packed"] = packed
+            del d["_buf"]
+            return packed
+        if name != "chunk_ends" or ("packed" not in d and "_buf" not in d):
             raise AttributeError(name)
         channels = d["cdf_count"] if d["channels"] is None else d["channels"]
         units = (channels + d["p_ch"] - 1) // d["p_ch"] * d["segments"]
         B = d["batch"]
-        ends = d["packed"][64: 64 + 4 * B * units].view(torch.uint32).view(B, units)
+        ends = self.packed[64: 64 + 4 * B * units].view(torch.uint32).view(B, units)
         d["chunk_ends"] = ends
         return ends
 
@@ -257,12 +266,16 @@ class WarpDivBackend:
             if len(self._shapes) > 64:
                 self._shapes.clear()
             self._shapes[key] = memo
-        enc = gaans.encode(tables, B, N, C, p_ch, device, symbols=symbols, indexes=indexes,
-                           segments=memo[1])
+        buf, nbytes = gaans.encode_symbols_raw(tables, B, N, C, p_ch, device, symbols, indexes,
+                                               memo[1])
         payload = object.__new__(WarpDivPayload)  # fields produced and checked here
         state = payload.__dict__
         state.update(memo[2])
-        state["packed"] = enc.packed
+        if buf.numel() - nbytes > gaans.CLONE_SLACK_BYTES:
+            state["packed"] = buf[:nbytes].clone()
+        else:  # packed is sliced from the buffer on first use
+            state["_buf"] = buf
+            state["_nbytes"] = nbytes
         return payload
 
     def decode(
@@ -284,13 +297,18 @@ class WarpDivBackend:
             key = (d["p_ch"], d["channels"], d["batch"], d["symbols_per_batch"], d["cdf_count"],
                    d["coding_fingerprint"], d["segments"])
             memo = self._decode_shapes.get(key)
-            packed = d["packed"]
+            packed = d.get("packed")
+            if packed is None:  # an encoder-made payload not sliced yet
+                packed, nbytes = d["_buf"], d["_nbytes"]
+            else:
+                nbytes = packed.numel()
             if (memo is not None and memo[0] is tables and isinstance(indexes, torch.Tensor)
                     and indexes.dtype == torch.int32 and indexes.device == memo[2]
                     and packed.device == memo[2] and indexes.is_contiguous()
                     and indexes.shape == memo[3]):
-                return gaans.decode(packed, tables, d["batch"], d["symbols_per_batch"], memo[1],
-                                    d["p_ch"], memo[2], indexes=indexes, segments=d["segments"])
+                return gaans.decode_symbols_ptr(packed.data_ptr(), nbytes, tables, d["batch"],
+                                                d["symbols_per_batch"], memo[1], d["p_ch"],
+                                                memo[2], indexes, d["segments"])
         if tables is None:
             C = _validate_inputs(indexes, indexes, cdfs, cdf_sizes, offsets, payload.p_ch,
                                  payload.channels)
