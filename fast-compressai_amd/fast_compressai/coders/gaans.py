@@ -302,24 +302,77 @@ def _run_decode_ptr(tables: PreparedTables, mode: int, explicit: bool, B: int, N
     return out
 
 
+def _symbols_call(tables: PreparedTables, decode: bool, explicit: bool, B: int, N: int, C: int,
+                  P: int, S: int, index: int, sp: int):
+    """What a symbols-mode call on stream ``sp`` of device ``index`` needs
+    besides its pointers, cached on the tables per (shape, stream): (plan
+    address, worst-case payload bytes, workspace bytes, stream state, the C
+    entry point, plan buffer).  Device ``index`` is current."""
+    key = ("call", decode, explicit, B, N, C, P, S, index, sp)
+    ctx = tables.plans.get(key)
+    if ctx is None:
+        buf, plan, lay = _plan(tables, decode, _native.MODE_SYMBOLS, explicit, B, N, C, P, S,
+                               index)
+        L = _native.lib()
+        ctx = (plan, lay.max_payload_bytes, lay.workspace_bytes, _state(index, sp),
+               L.gaans_run_decode if decode else L.gaans_run_encode, buf)
+        tables.plans[key] = ctx
+    return ctx
+
+
 def encode_symbols_raw(tables: PreparedTables, B: int, N: int, C: int, P: int, device,
                        symbols: torch.Tensor, indexes: torch.Tensor | None, segments: int):
     """``encode`` of int32 symbols, returning (worst-case buffer, payload
-    bytes): the payload is the buffer's first bytes (no slice made)."""
-    out, total, _ = _run_encode_raw(tables, _native.MODE_SYMBOLS, indexes is not None, B, N, C,
-                                    P, segments, device, symbols.data_ptr(), _ptr(indexes),
-                                    None, None, "GA-ANS encode")
-    return out, total
+    bytes): the payload is the buffer's first bytes (no slice made).  With
+    the device current, one cached lookup gives the plan and stream state."""
+    index = device.index
+    if index is None or torch._C._cuda_getDevice() != index:
+        out, total, _ = _run_encode_raw(tables, _native.MODE_SYMBOLS, indexes is not None, B, N,
+                                        C, P, segments, device, symbols.data_ptr(),
+                                        _ptr(indexes), None, None, "GA-ANS encode")
+        return out, total
+    sp = torch._C._cuda_getCurrentRawStream(index)
+    plan, max_bytes, ws_bytes, st, run, _ = _symbols_call(
+        tables, False, indexes is not None, B, N, C, P, segments, index, sp)
+    out = torch.empty(max_bytes, dtype=torch.uint8, device=st.device)
+    with st.lock:
+        ws = st.ws(ws_bytes)
+        rc = run(plan, sp, symbols.data_ptr(), None if indexes is None else indexes.data_ptr(),
+                 None, None, ws.data_ptr(), ws.numel(), st.ctrl_ptr, out.data_ptr(), max_bytes,
+                 st.info_ptr)
+        word = int(st.info_np[2])  # 1 | status << 1 | payload bytes << 16
+    if rc:
+        _native.check(rc, "GA-ANS encode")
+    status = (word >> 1) & 0x7FFF
+    if status:
+        raise CoderInputError(f"GA-ANS encode failed: {_native.describe_status(status)}")
+    return out, word >> 16
 
 
 def decode_symbols_ptr(payload_ptr: int, payload_bytes: int, tables: PreparedTables, B: int,
                        N: int, C: int, P: int, device, indexes: torch.Tensor | None,
                        segments: int) -> torch.Tensor:
     """``decode`` of int32 symbols from a payload given by device address and
-    size."""
-    return _run_decode_ptr(tables, _native.MODE_SYMBOLS, indexes is not None, B, N, C, P,
-                           segments, device, payload_ptr, payload_bytes, _ptr(indexes), None,
-                           None, torch.int32, "GA-ANS decode")
+    size (the cached call context of ``encode_symbols_raw``)."""
+    index = device.index
+    if index is None or torch._C._cuda_getDevice() != index:
+        return _run_decode_ptr(tables, _native.MODE_SYMBOLS, indexes is not None, B, N, C, P,
+                               segments, device, payload_ptr, payload_bytes, _ptr(indexes), None,
+                               None, torch.int32, "GA-ANS decode")
+    sp = torch._C._cuda_getCurrentRawStream(index)
+    plan, _, _, st, run, _ = _symbols_call(tables, True, indexes is not None, B, N, C, P,
+                                           segments, index, sp)
+    out = torch.empty((B, N), dtype=torch.int32, device=st.device)
+    with st.lock:
+        rc = run(plan, sp, payload_ptr, payload_bytes,
+                 None if indexes is None else indexes.data_ptr(), None, None, out.data_ptr(),
+                 st.ctrl_ptr, st.status_ptr)
+        status = int(st.status_np[1]) >> 1  # 1 | status << 1
+    if rc:
+        _native.check(rc, "GA-ANS decode")
+    if status:
+        raise CoderInputError(f"warp_div decode failed: {_native.describe_status(status)}")
+    return out
 
 
 def encode(tables: PreparedTables, B: int, N: int, C: int, P: int, device, *,
