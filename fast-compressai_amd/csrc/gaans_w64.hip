@@ -273,7 +273,7 @@ struct Tabs {
   const uint16_t* lstarts; // decoder, search lookups: symbol starts of all tables
   int t_lo, nt;
   uint32_t sub_first;      // first staged sub-block
-  bool sub_lds;            // decoder: sub-blocks staged with the lookups
+  uint32_t sub_n;          // decoder: sub-blocks sub_first .. + sub_n - 1 are in LDS
 };
 
 // One pass over the staged metadata (nt), entries (ne) and sub-block 16-byte
@@ -383,7 +383,7 @@ __device__ void stage_tables(Tabs& T, uint4* lmeta, uint2* lent, uint64_t* llut,
   T.t_lo = t_lo;
   T.nt = t_hi > t_lo ? t_hi - t_lo : 0;
   T.sub_first = 0;
-  T.sub_lds = lsub != nullptr;
+  T.sub_n = 0;
   if (T.nt > 0) {
     const uint32_t nt = (uint32_t)T.nt;
     const uint32_t base0 = bd.base0;
@@ -407,6 +407,7 @@ __device__ void stage_tables(Tabs& T, uint4* lmeta, uint2* lent, uint64_t* llut,
       const uint32_t d1 = bd.d1;
       if (lsub && d1 > d0) {
         T.sub_first = d0;
+        T.sub_n = d1 - d0;
         copy16_dma<NT>(reinterpret_cast<uint4*>(lsub),
                        reinterpret_cast<const uint4*>(T.gsub + (size_t)d0 * kSubSize),
                        (d1 - d0) * (kSubBytes / 16), tid);
@@ -1747,7 +1748,7 @@ __device__ __forceinline__ uint2 dec_record_search(const DecArgs& a, const Tabs&
 template <bool kLds>
 __device__ __forceinline__ uint64_t sub_entry(const Tabs& tb, uint64_t e, uint32_t i) {
   uint64_t r;
-  if (kLds && tb.sub_lds) {
+  if (kLds && (uint32_t)e - tb.sub_first < tb.sub_n) {
     r = tb.lsub[(((uint32_t)e - tb.sub_first) << kSubBits) + i];
     asm volatile("" : "+v"(r));
   } else {
@@ -1850,7 +1851,7 @@ __device__ void stage_search(Tabs& T, uint4* lmeta, uint32_t* lclut, uint16_t* l
   T.t_lo = 0;
   T.nt = (int)M;
   T.sub_first = 0;
-  T.sub_lds = false;
+  T.sub_n = 0;
   copy16_dma<NT>(reinterpret_cast<uint4*>(lclut),
                  reinterpret_cast<const uint4*>(tables + blob.clut_off), M * (kLutSize / 4), tid);
   copy16_dma<NT>(reinterpret_cast<uint4*>(lstarts),
@@ -1902,18 +1903,22 @@ __device__ __forceinline__ EarlyStage stage_early(const Tabs& T, uint64_t* llut,
 
 template <int NT, bool kSearch>
 __device__ __forceinline__ void stage_late(Tabs& T, const EarlyStage& e, uint4* lmeta,
-                                           uint64_t* lsub, const StageBounds& bd, int tid) {
+                                           uint64_t* lsub, uint32_t sub_cap,
+                                           const StageBounds& bd, int tid) {
   T.t_lo = e.t_lo;
   T.nt = e.nt;
   T.sub_first = 0;
-  T.sub_lds = !kSearch && lsub != nullptr;
+  T.sub_n = 0;
   if (e.nt > 0) {
     const uint32_t base0 = kSearch ? 0u : bd.base0;
     if (!kSearch && lsub && bd.d1 > bd.d0) {
+      // the range's first sub_cap sub-blocks (a plan may hold fewer than the
+      // range has: the others are read from global memory)
       T.sub_first = bd.d0;
+      T.sub_n = bd.d1 - bd.d0 < sub_cap ? bd.d1 - bd.d0 : sub_cap;
       copy16_dma<NT>(reinterpret_cast<uint4*>(lsub),
                      reinterpret_cast<const uint4*>(T.gsub + (size_t)bd.d0 * kSubSize),
-                     (bd.d1 - bd.d0) * (kSubBytes / 16), tid);
+                     T.sub_n * (kSubBytes / 16), tid);
     }
     if (e.nt <= NT) {
       if (tid < e.nt)
@@ -2413,7 +2418,8 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
     }
     if (tid < 8) ctl[tid] = tid == 1 ? kAllAvail : 0u;
     if (kMode == kModeGaussian) stage_scales<kDecThreads>(scl, a.scale_table, a.n_scales, tid);
-    stage_late<kDecThreads, kSearch>(tb, est, lmeta, a.nd_cap ? lsub : nullptr, bd, tid);
+    stage_late<kDecThreads, kSearch>(tb, est, lmeta, a.nd_cap ? lsub : nullptr,
+                                     (uint32_t)a.nd_cap, bd, tid);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load crosses the role split
     if (wid == 0) pc.mark(2);
 
@@ -2773,7 +2779,7 @@ __global__ void __launch_bounds__(kLanes) k_rans64_decode(R64Args a) {
   tb.t_lo = 0;
   tb.nt = 0;
   tb.sub_first = 0;
-  tb.sub_lds = false;
+  tb.sub_n = 0;
   const bool any = ballot(act0) != 0ull;
   const uint32_t total_dense = a.blob.total_dense;
   if (any && a.stage == 1)
@@ -3091,20 +3097,32 @@ DecPlan plan_decode(const gaans_tables* t, int64_t P, int64_t units, bool latent
   const int64_t search_bytes = search_ok ? search_lds(t, &starts_words) : 0;
   for (int64_t occ = occ_target(units, d, 3); occ >= 1; --occ) {
     const int64_t cap = lds_budget(d, occ);
-    // the wide lookups with their sub-blocks, then without them (a dense
-    // wide bucket then reads its two-value sub-range from global memory:
-    // the 2160x3840 latent's 8 tables of up to 256 symbols leave no room for
-    // their sub-blocks, and the 256-value buckets gave its wide-table units
-    // a second or third read in most steps), with 16- or 8-step blocks
-    for (int subs = 1; wide_ok && subs >= 0; --subs)
+    // The wide lookups with 16- or 8-step blocks and: all of a range's
+    // sub-blocks (room for P times the largest per table); else as many as
+    // the rest of the LDS holds when that is half again a typical range's
+    // count (P times the mean per table), a unit staging its range's first
+    // ones and reading the others from global memory (the 2160x3840
+    // latent's chunks of 8 tables need 30-115 sub-blocks, 8 x 26 by the
+    // bound; 8-step blocks leave room for 124); else none (a dense wide
+    // bucket then reads its two-value sub-range from global memory, where
+    // the 256-value buckets gave the wide-table units a second or third
+    // read in most steps).
+    const int64_t typical = (P * t->total_wide + t->M - 1) / t->M * 3 / 2;
+    for (int subs = 2; wide_ok && subs >= 0; --subs)
       for (int sb = 16; sb >= 8; sb >>= 1) {
         const int64_t fixed = dec_fixed_lds(latents, sb);
         Stage s;
-        if (fit_stage(t, P, per_wide, 0, subs ? kSubBytes : 0, cap - fixed - extra, &s, range_ok,
-                      true))
-          return DecPlan{s, sb,
-                         (size_t)(fixed + per_wide * s.nt_cap + kSubBytes * (int64_t)s.nd_cap),
-                         false, 0, true};
+        if (!fit_stage(t, P, per_wide, 0, subs == 2 ? kSubBytes : 0, cap - fixed - extra, &s,
+                       range_ok, true))
+          continue;
+        if (subs == 1) {  // partial: the sub-blocks the rest of the LDS holds
+          const int64_t room = (cap - fixed - extra - per_wide * s.nt_cap) / kSubBytes;
+          if (t->total_wide == 0 || room < typical || room < 1) continue;
+          s.nd_cap = (int32_t)(room < (int64_t)t->total_wide ? room : t->total_wide);
+        }
+        return DecPlan{s, sb,
+                       (size_t)(fixed + per_wide * s.nt_cap + kSubBytes * (int64_t)s.nd_cap),
+                       false, 0, true};
       }
     for (int opt = 0; opt < 9; ++opt) {
       const int sb = 16 >> (opt % 3);  // 16-, 8-, then 4-step blocks of each kind
