@@ -123,31 +123,37 @@ GAANS_HDI uint32_t udiv(uint32_t n, UDiv d) {
   return (mulhi32(n, d.m) + n) >> d.s;
 }
 
-// Encoder division x / f over the full 32-bit range for f in [2, 65536]
-// (Granlund & Montgomery, PLDI 1994, figure 4.1): l = ceil(log2 f),
-// m = floor(2^32 (2^l - f) / f) + 1 (enc_magic), t = mulhi(x, m),
-// q = (t + ((x - t) >> 1)) >> (l - 1).  f = 1 is handled by the caller.
-GAANS_HDI uint32_t enc_shift(uint32_t f) {  // l - 1, for f >= 2
+// Encoder division x / f for f in [1, 65536] and x < f 2^16 (the coder's
+// state after renormalisation): l = ceil(log2 f) (enc_shift), M = 2^32 + m
+// with m = floor(2^32 (2^l - f) / f) + 1 (enc_magic; 0 for f = 1), then
+// q = floor(x M / 2^(32 + l)) (Granlund & Montgomery, PLDI 1994, theorem
+// 4.2: 2^(32+l) < M f <= 2^(32+l) + 2^l, exact for every x < 2^32).  x M =
+// x m + x 2^32, so its high word is mulhi(x, m) + x, which for x < f 2^16
+// stays below 2^32 (x M < 2^(48+l) <= 2^64): two ops and a shift, and f = 1
+// (m = 0, l = 0) needs no special case.
+GAANS_HDI uint32_t enc_shift(uint32_t f) {  // l = ceil(log2 f): bits of f - 1
 #if defined(__HIP_DEVICE_COMPILE__)
-  return 31u - (uint32_t)__clz((int)(f - 1u));
+  return 32u - (uint32_t)__clz((int)(f - 1u));
 #else
   uint32_t l = 0;
   while (((uint64_t)1 << l) < f) ++l;
-  return l - 1;
+  return l;
 #endif
 }
 
-GAANS_HDI uint32_t enc_div(uint32_t x, uint32_t m, uint32_t sh) {
-  const uint32_t t = mulhi32(x, m);
-  return (t + ((x - t) >> 1)) >> sh;
+GAANS_HDI uint32_t enc_div(uint32_t x, uint32_t m, uint32_t l) {
+  return (mulhi32(x, m) + x) >> (l & 31u);
 }
 
 // Index hash term of chunk position p with table tb: MurmurHash3's 32-bit
 // finaliser (Appleby) of p * 0x9E3779B9 + tb + 1; a chunk's hash is the sum
 // of its terms mod 2^32 (a bijective finaliser, so positions that trade
 // tables change the sum except with probability about 2^-32).
-GAANS_HD uint32_t index_term(uint32_t p, uint32_t tb) {
-  uint32_t h = p * kHashMul + tb + 1u;
+// index_term_pk takes pk = p * 0x9E3779B9 (mod 2^32): the positions
+// lane + 64 t of a unit's steps give pk = lane * 0x9E3779B9 + t * (64 *
+// 0x9E3779B9), a per-lane constant plus a uniform term, one add per step.
+GAANS_HD uint32_t index_term_pk(uint32_t pk, uint32_t tb) {
+  uint32_t h = pk + tb + 1u;
   h ^= h >> 16;
   h *= 0x85EBCA6Bu;
   h ^= h >> 13;
@@ -155,6 +161,11 @@ GAANS_HD uint32_t index_term(uint32_t p, uint32_t tb) {
   h ^= h >> 16;
   return h;
 }
+
+GAANS_HD uint32_t index_term(uint32_t p, uint32_t tb) { return index_term_pk(p * kHashMul, tb); }
+
+// The uniform part of pk for step t (index_term_pk).
+GAANS_HD uint32_t hash_step(int t) { return (uint32_t)t * ((uint32_t)64 * kHashMul); }
 
 // Host side of udiv (make_udiv) and of enc_div (enc_magic: m above).
 UDiv make_udiv(uint32_t d);

@@ -455,9 +455,9 @@ int gaans_host_selftest(void) {
     if (udiv((1u << 31) - 1u, u) != ((1u << 31) - 1u) / d)
       return fail(1, "udiv selftest failed at n=2^31-1, d=%u", d);
   }
-  // 2. encoder division: the full-range magic of every freq in [2, 65536] at
-  //    quotient boundaries and at the ends of the coded range [0, f 2^16)
-  for (uint32_t f = 2; f <= 65536; ++f) {
+  // 2. encoder division: the magic of every freq in [1, 65536] at quotient
+  //    boundaries and at the ends of the coded range [0, f 2^16)
+  for (uint32_t f = 1; f <= 65536; ++f) {
     const uint32_t m = enc_magic(f), sh = enc_shift(f);
     const uint32_t xmax = (uint32_t)(((uint64_t)f << 16) - 1u);
     const uint32_t xs[10] = {0u, 1u, f - 1u, f, f + 1u, xmax, xmax - 1u, xmax - f,

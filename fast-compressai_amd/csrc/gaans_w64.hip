@@ -655,7 +655,7 @@ __device__ void unit_end_offsets(const EncArgs& a, int tid, uint64_t* sh) {
 // Op record of one lane and step (16 bytes):
 //   x: start | (65536 - freq) << 16      (identity op: 0)
 //   y: division magic of freq            (enc_div)
-//   z: shift | (freq == 1) << 5 | escape << 8 | (freq - 1) << 16
+//   z: shift (enc_shift) | escape << 8 | (freq - 1) << 16
 //      (identity op: 15 | 0xffff << 16, so that it never emits)
 //   w: escape raw value
 // CompressAI's escape split (reference warp_ans_kernel_v2.cu:139-164):
@@ -691,7 +691,8 @@ __device__ __forceinline__ void enc_records(const EncArgs& a, const Tabs& tb, in
     ok[e] = act & !bad;
     status |= bad ? GAANS_ST_INDEX : 0u;
     tbi = ok[e] ? tbi : (kLds ? tb.t_lo : 0);
-    hash += ok[e] ? index_term((uint32_t)p, (uint32_t)tbi) : 0u;
+    hash += ok[e] ? index_term_pk(lane * kHashMul + hash_step(t0 + tstep * e), (uint32_t)tbi)
+                  : 0u;
     if (kMode != kModeSymbols) {
       const float r = rintf(__fsub_rn(__int_as_float(in_a[e]), in_m[e]));
       const bool rng = !(fabsf(r) < 2147483648.0f);
@@ -738,12 +739,11 @@ __device__ __forceinline__ void enc_records(const EncArgs& a, const Tabs& tb, in
     const uint32_t nn = raw ? ((31u - (uint32_t)__clz((int)raw)) >> 2) + 1u : 0u;
     znib += esc[e] ? nn + 1u : 0u;
     const uint32_t fr = (ent[e].x >> 16) + 1u;
-    const uint32_t sh = fr >= 2u ? enc_shift(fr) : 0u;
+    const uint32_t sh = enc_shift(fr);
     uint4 r;
     r.x = ok[e] ? ((ent[e].x & 0xffffu) | ((65536u - fr) << 16)) : 0u;
     r.y = ok[e] ? ent[e].y : 1u;
-    r.z = (ok[e] ? sh | (ent[e].x & 0xffff0000u) : 0xffff000fu) |
-          ((ok[e] & (fr == 1u)) ? 32u : 0u) | (esc[e] ? 256u : 0u);
+    r.z = (ok[e] ? sh | (ent[e].x & 0xffff0000u) : 0xffff000fu) | (esc[e] ? 256u : 0u);
     r.w = raw;
     rec[e] = r;
   }
@@ -780,7 +780,7 @@ __device__ __forceinline__ bool enc_records_fast(const EncArgs& a, const Tabs& t
         kImplicit ? (int32_t)udiv((uint32_t)unit_pos(start, a.S, p), a.div_hw) : in_b[e];
     bad |= ballot((uint32_t)(tbi - tb.t_lo) >= (uint32_t)tb.nt);  // staged tables are below M
     tbl[e] = (uint32_t)tbi;
-    h += index_term((uint32_t)p, (uint32_t)tbi);
+    h += index_term_pk(lane * kHashMul + hash_step(t0 + tstep * e), (uint32_t)tbi);
     if (kMode != kModeSymbols) {
       const float r = rintf(__fsub_rn(__int_as_float(in_a[e]), in_m[e]));
       bad |= ballot(!(fabsf(r) < 2147483648.0f));
@@ -806,8 +806,10 @@ __device__ __forceinline__ bool enc_records_fast(const EncArgs& a, const Tabs& t
 #pragma unroll
   for (int e = 0; e < KP; ++e) {
     const uint2 ent = tb.lent[at[e]];
+    // enc_shift: 31 - clz(2 (freq - 1) + 1) (never of zero), from the
+    // entry's (freq - 1) << 16 | start
     uint32_t lz;
-    asm("v_ffbh_u32 %0, %1" : "=v"(lz) : "v"(ent.x >> 16));
+    asm("v_ffbh_u32 %0, %1" : "=v"(lz) : "v"((ent.x >> 15) | 1u));
     rec[e] = make_uint4(ent.x ^ 0xffff0000u, ent.y, (31u - lz) | (ent.x & 0xffff0000u), 0u);
     if (om[e] != 0ull) {
       // the escape split of enc_records for this step's escaping lanes
@@ -832,7 +834,7 @@ __device__ __forceinline__ bool enc_records_fast(const EncArgs& a, const Tabs& t
 }
 
 // Encoder LDS ring: ring_mask + 1 words (a power of two) and one spare slot
-// per lane.
+// per lane (where a step's lanes that emit nothing store).
 __device__ __forceinline__ void ring_flush(uint16_t* __restrict__ wbuf, const uint16_t* ring,
                                            int wp, int fl, int lane, uint32_t ring_mask) {
   for (int pos = wp + lane; pos < fl; pos += kLanes) wbuf[pos] = ring[pos & ring_mask];
@@ -842,25 +844,41 @@ __device__ __forceinline__ void ring_flush(uint16_t* __restrict__ wbuf, const ui
 // flushes it at the start of a block when fewer than SB * kLanes slots are
 // free (a step emits at most one word per lane), so the steps need no check.
 // A lane emits when x >= freq << 16, i.e. (x >> 16) > freq - 1 (z's high
-// half): one compare of the two high halves.
+// half): one compare of the two high halves.  Every lane stores, the ones
+// that emit nothing to their spare slot: selects on the compare's mask
+// rather than an exec-masked branch (three scalar instructions more per
+// step, and no interleaving of consecutive steps).  Written as one asm
+// block because the compiler turns the selects back into a branch in some
+// instantiations; inside it the mask (VCC) is read by vector instructions
+// no sooner than the second after the compare that writes it.
 __device__ __forceinline__ void emit_words(uint32_t z, uint32_t& x, uint16_t* ring, int& wp,
-                                           int lane, uint32_t ring_mask) {
-  const bool emit = (x >> 16) > (z >> 16);
-  const uint64_t m = ballot(emit);
-  wp = uni(wp - __popcll(m));
-  // an exec-masked store: the slot's address is computed by the emitting
-  // lanes only, and the others skip it
-  if (emit) ring[(uint32_t)(wp + (int)lane_rank(m)) & ring_mask] = (uint16_t)x;
-  x = emit ? x >> 16 : x;
+                                           uint32_t spare, uint32_t ring_mask) {
+  uint32_t xn, cnt, slot;
+  int w = uni(wp);
+  asm volatile(
+      "v_lshrrev_b32 %[xn], 16, %[x]\n\t"
+      "v_cmp_gt_u32_sdwa vcc, %[xn], %[z] src0_sel:DWORD src1_sel:WORD_1\n\t"
+      "s_bcnt1_i32_b64 %[cnt], vcc\n\t"
+      "s_sub_i32 %[w], %[w], %[cnt]\n\t"
+      "v_mov_b32 %[slot], %[w]\n\t"
+      "v_cndmask_b32 %[xn], %[x], %[xn], vcc\n\t"
+      "v_mbcnt_lo_u32_b32 %[slot], vcc_lo, %[slot]\n\t"
+      "v_mbcnt_hi_u32_b32 %[slot], vcc_hi, %[slot]\n\t"
+      "v_and_b32 %[slot], %[mask], %[slot]\n\t"
+      "v_cndmask_b32 %[slot], %[spare], %[slot], vcc"
+      : [xn] "=&v"(xn), [cnt] "=&s"(cnt), [slot] "=&v"(slot), [w] "+s"(w)
+      : [x] "v"(x), [z] "v"(z), [mask] "s"(ring_mask), [spare] "v"(spare)
+      : "vcc", "scc");
+  wp = w;
+  ring[slot] = (uint16_t)x;
+  x = xn;
 }
 
-// main rANS op: x' = ((x / freq) << 16) + x % freq + start = x + start + q (65536 - freq);
-// z's low byte is the shift, or 32 (+ shift 0) for freq = 1
+// main rANS op: x' = ((x / freq) << 16) + x % freq + start = x + start + q (65536 - freq)
+// (for freq = 1 too: q = x < 2^16, x' = x 2^16 + start)
 __device__ __forceinline__ uint32_t enc_apply(uint32_t x, uint4 r) {
-  const uint32_t q = enc_div(x, r.y, r.z & 31u);
-  const uint32_t xs = x + (r.x & 0xffffu);
-  const uint32_t xn = __umul24(q, r.x >> 16) + xs;
-  return (r.z & 0xffu) >= 32u ? ((x << 16) | (r.x & 0xffffu)) : xn;
+  const uint32_t q = enc_div(x, r.y, r.z);
+  return __umul24(q, r.x >> 16) + x + (r.x & 0xffffu);
 }
 
 // Escapes of one step into the unit's escape list: slots are taken from the
@@ -1142,12 +1160,33 @@ __device__ void fused_pack(const EncArgs& a, int64_t g, int tid, int lane, int w
   const int64_t n32 = U16 / 2;
   uint32_t* w32 = d32 + A;
   const uint16_t* stg16 = reinterpret_cast<const uint16_t*>(stg);
-  for (int64_t j = tid; j < n32; j += NT) {
-    const int p0 = wp + 2 * (int)j, p1 = p0 + 1;
-    uint32_t lo = 0, hi = 0;
-    if (p0 < cap) lo = p0 < fl ? ring[p0 & ring_mask] : (staged ? stg16[p0 - f0] : wbuf[p0]);
-    if (p1 < cap) hi = p1 < fl ? ring[p1 & ring_mask] : (staged ? stg16[p1 - f0] : wbuf[p1]);
-    w32[j] = lo | (hi << 16);
+  if (staged) {
+    for (int j = tid; j < (int)n32; j += NT) {
+      const int p0 = wp + 2 * j, p1 = p0 + 1;
+      uint32_t lo = 0, hi = 0;
+      if (p0 < cap) lo = p0 < fl ? ring[p0 & ring_mask] : stg16[p0 - f0];
+      if (p1 < cap) hi = p1 < fl ? ring[p1 & ring_mask] : stg16[p1 - f0];
+      w32[j] = lo | (hi << 16);
+    }
+  } else {
+    // from the slot in global memory: kPackBatch words' loads in flight per
+    // thread before their stores (a store may alias a later load for the
+    // compiler, which then keeps each load behind the store before it)
+    constexpr int kPackBatch = 8;
+    for (int j0 = tid; j0 < (int)n32; j0 += NT * kPackBatch) {
+      uint32_t v[kPackBatch];
+#pragma unroll
+      for (int u = 0; u < kPackBatch; ++u) {
+        const int p0 = wp + 2 * (j0 + u * NT), p1 = p0 + 1;
+        uint32_t lo = 0, hi = 0;
+        if (p0 < cap) lo = p0 < fl ? ring[p0 & ring_mask] : wbuf[p0];
+        if (p1 < cap) hi = p1 < fl ? ring[p1 & ring_mask] : wbuf[p1];
+        v[u] = lo | (hi << 16);
+      }
+#pragma unroll
+      for (int u = 0; u < kPackBatch; ++u)
+        if (j0 + u * NT < (int)n32) w32[j0 + u * NT] = v[u];
+    }
   }
   pc.mark(9);  // the words' stores are issued
   if (E > 0) {  // uniform
@@ -1388,6 +1427,7 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
       // instructions go first when mapper waves of this or another
       // workgroup on the CU compete for the same SIMD.
       __builtin_amdgcn_s_setprio(3);
+      const uint32_t spare = ring_mask + 1u + (uint32_t)lane;
       __syncthreads();
       pc.mark(3);
       pc.cycles(12);
@@ -1413,14 +1453,14 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
             // common case: a full block, no per-step branches
 #pragma unroll
             for (int k = H - 1; k >= 0; --k) {
-              emit_words(r[k].z, x, ring, wp, lane, ring_mask);
+              emit_words(r[k].z, x, ring, wp, spare, ring_mask);
               x = enc_apply(x, r[k]);
             }
           } else {
 #pragma unroll
             for (int k = H - 1; k >= 0; --k) {
               if (j * SB + h * H + k >= T) continue;
-              emit_words(r[k].z, x, ring, wp, lane, ring_mask);
+              emit_words(r[k].z, x, ring, wp, spare, ring_mask);
               x = enc_apply(x, r[k]);
             }
           }
@@ -1698,7 +1738,7 @@ __device__ __forceinline__ uint2 dec_record(const DecArgs& a, const Tabs& tb, in
   const bool ok = act & !bad;
   status |= bad ? GAANS_ST_INDEX : 0u;
   tbi = ok ? tbi : (tb.nt > 0 ? tb.t_lo : 0);
-  hash += ok ? index_term((uint32_t)p, (uint32_t)tbi) : 0u;
+  hash += ok ? index_term_pk(lane * kHashMul + hash_step(t), (uint32_t)tbi) : 0u;
   const bool staged = (uint32_t)(tbi - tb.t_lo) < (uint32_t)tb.nt;
   all_lds = ballot(!staged) == 0;
   uint32_t nsym, offset;
@@ -1733,7 +1773,7 @@ __device__ __forceinline__ uint2 dec_record_search(const DecArgs& a, const Tabs&
   const bool ok = act & !bad;
   status |= bad ? GAANS_ST_INDEX : 0u;
   tbi = ok ? tbi : 0;
-  hash += ok ? index_term((uint32_t)p, (uint32_t)tbi) : 0u;
+  hash += ok ? index_term_pk(lane * kHashMul + hash_step(t), (uint32_t)tbi) : 0u;
   const uint4 lm = tb.lmeta[tbi];
   uint2 r;
   r.x = (uint32_t)tbi | ((act ? lm.x + lm.y - 1u : kNoSym) << 16);
@@ -3314,10 +3354,21 @@ int encode_prepare(int mode, bool implicit, int32_t n_scales, float scale_bound,
   const EncPlan plan = plan_encode(tables, L.P, L.U, dl, extra, !gauss,
                                    (long_units || gauss) && !implicit);
   const Stage& st = plan.st;
-  const size_t lds = plan.lds + (size_t)extra;
+  size_t lds = plan.lds + (size_t)extra;
   if (lds > (size_t)dl.per_block)
     return fail(GAANS_EINVAL, "encode needs %zu bytes of LDS, the device has %d", lds,
                 dl.per_block);
+  // When the whole grid is resident at once, the LDS the plan's workgroups
+  // per CU leave each one costs nothing: the fused pack stages the unit's
+  // flushed words there (at most the slot, 2 cap_words bytes, past the
+  // ring and the block records) rather than reading them from global memory
+  // (the 2160x3840 latent's units flush 20-30 KB, more than their 17 KB of
+  // tables).
+  if (L.U <= plan.occ * (int64_t)dl.cus) {
+    const int64_t want = (int64_t)lds + 2 * L.cap_words + 16;
+    const int64_t room = lds_budget(dl, plan.occ);
+    if ((int64_t)lds < room) lds = (size_t)(want < room ? want : room);
+  }
   EncArgs& a = e->a;
   memset(&a, 0, sizeof(a));
   a.n_scales = gauss ? n_scales : 0;
