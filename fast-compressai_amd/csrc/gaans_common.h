@@ -149,11 +149,8 @@ GAANS_HDI uint32_t enc_div(uint32_t x, uint32_t m, uint32_t l) {
 // finaliser (Appleby) of p * 0x9E3779B9 + tb + 1; a chunk's hash is the sum
 // of its terms mod 2^32 (a bijective finaliser, so positions that trade
 // tables change the sum except with probability about 2^-32).
-// index_term_pk takes pk = p * 0x9E3779B9 (mod 2^32): the positions
-// lane + 64 t of a unit's steps give pk = lane * 0x9E3779B9 + t * (64 *
-// 0x9E3779B9), a per-lane constant plus a uniform term, one add per step.
-GAANS_HD uint32_t index_term_pk(uint32_t pk, uint32_t tb) {
-  uint32_t h = pk + tb + 1u;
+GAANS_HD uint32_t index_term(uint32_t p, uint32_t tb) {
+  uint32_t h = p * kHashMul + tb + 1u;
   h ^= h >> 16;
   h *= 0x85EBCA6Bu;
   h ^= h >> 13;
@@ -162,10 +159,6 @@ GAANS_HD uint32_t index_term_pk(uint32_t pk, uint32_t tb) {
   return h;
 }
 
-GAANS_HD uint32_t index_term(uint32_t p, uint32_t tb) { return index_term_pk(p * kHashMul, tb); }
-
-// The uniform part of pk for step t (index_term_pk).
-GAANS_HD uint32_t hash_step(int t) { return (uint32_t)t * ((uint32_t)64 * kHashMul); }
 
 // Host side of udiv (make_udiv) and of enc_div (enc_magic: m above).
 UDiv make_udiv(uint32_t d);

@@ -691,8 +691,7 @@ __device__ __forceinline__ void enc_records(const EncArgs& a, const Tabs& tb, in
     ok[e] = act & !bad;
     status |= bad ? GAANS_ST_INDEX : 0u;
     tbi = ok[e] ? tbi : (kLds ? tb.t_lo : 0);
-    hash += ok[e] ? index_term_pk(lane * kHashMul + hash_step(t0 + tstep * e), (uint32_t)tbi)
-                  : 0u;
+    hash += ok[e] ? index_term((uint32_t)p, (uint32_t)tbi) : 0u;
     if (kMode != kModeSymbols) {
       const float r = rintf(__fsub_rn(__int_as_float(in_a[e]), in_m[e]));
       const bool rng = !(fabsf(r) < 2147483648.0f);
@@ -780,7 +779,7 @@ __device__ __forceinline__ bool enc_records_fast(const EncArgs& a, const Tabs& t
         kImplicit ? (int32_t)udiv((uint32_t)unit_pos(start, a.S, p), a.div_hw) : in_b[e];
     bad |= ballot((uint32_t)(tbi - tb.t_lo) >= (uint32_t)tb.nt);  // staged tables are below M
     tbl[e] = (uint32_t)tbi;
-    h += index_term_pk(lane * kHashMul + hash_step(t0 + tstep * e), (uint32_t)tbi);
+    h += index_term((uint32_t)p, (uint32_t)tbi);
     if (kMode != kModeSymbols) {
       const float r = rintf(__fsub_rn(__int_as_float(in_a[e]), in_m[e]));
       bad |= ballot(!(fabsf(r) < 2147483648.0f));
@@ -845,33 +844,21 @@ __device__ __forceinline__ void ring_flush(uint16_t* __restrict__ wbuf, const ui
 // free (a step emits at most one word per lane), so the steps need no check.
 // A lane emits when x >= freq << 16, i.e. (x >> 16) > freq - 1 (z's high
 // half): one compare of the two high halves.  Every lane stores, the ones
-// that emit nothing to their spare slot: selects on the compare's mask
-// rather than an exec-masked branch (three scalar instructions more per
-// step, and no interleaving of consecutive steps).  Written as one asm
-// block because the compiler turns the selects back into a branch in some
-// instantiations; inside it the mask (VCC) is read by vector instructions
-// no sooner than the second after the compare that writes it.
+// that emit nothing to their spare slot (spare = ring_mask + 1 + lane,
+// computed once per wave): selects on the compare rather than an
+// exec-masked branch, which costs three scalar instructions more per step
+// and keeps consecutive steps from interleaving.  (With the spare slot
+// computed here the compiler turned the selects back into a branch.)
 __device__ __forceinline__ void emit_words(uint32_t z, uint32_t& x, uint16_t* ring, int& wp,
                                            uint32_t spare, uint32_t ring_mask) {
-  uint32_t xn, cnt, slot;
-  int w = uni(wp);
-  asm volatile(
-      "v_lshrrev_b32 %[xn], 16, %[x]\n\t"
-      "v_cmp_gt_u32_sdwa vcc, %[xn], %[z] src0_sel:DWORD src1_sel:WORD_1\n\t"
-      "s_bcnt1_i32_b64 %[cnt], vcc\n\t"
-      "s_sub_i32 %[w], %[w], %[cnt]\n\t"
-      "v_mov_b32 %[slot], %[w]\n\t"
-      "v_cndmask_b32 %[xn], %[x], %[xn], vcc\n\t"
-      "v_mbcnt_lo_u32_b32 %[slot], vcc_lo, %[slot]\n\t"
-      "v_mbcnt_hi_u32_b32 %[slot], vcc_hi, %[slot]\n\t"
-      "v_and_b32 %[slot], %[mask], %[slot]\n\t"
-      "v_cndmask_b32 %[slot], %[spare], %[slot], vcc"
-      : [xn] "=&v"(xn), [cnt] "=&s"(cnt), [slot] "=&v"(slot), [w] "+s"(w)
-      : [x] "v"(x), [z] "v"(z), [mask] "s"(ring_mask), [spare] "v"(spare)
-      : "vcc", "scc");
-  wp = w;
-  ring[slot] = (uint16_t)x;
-  x = xn;
+  const bool emit = (x >> 16) > (z >> 16);
+  const uint64_t m = ballot(emit);
+  wp = uni(wp - __popcll(m));
+  // wp + the number of emitting lanes below this one
+  const uint32_t pos = (uint32_t)__builtin_amdgcn_mbcnt_hi(
+      (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, (uint32_t)wp));
+  ring[emit ? pos & ring_mask : spare] = (uint16_t)x;
+  x = emit ? x >> 16 : x;
 }
 
 // main rANS op: x' = ((x / freq) << 16) + x % freq + start = x + start + q (65536 - freq)
@@ -1738,7 +1725,7 @@ __device__ __forceinline__ uint2 dec_record(const DecArgs& a, const Tabs& tb, in
   const bool ok = act & !bad;
   status |= bad ? GAANS_ST_INDEX : 0u;
   tbi = ok ? tbi : (tb.nt > 0 ? tb.t_lo : 0);
-  hash += ok ? index_term_pk(lane * kHashMul + hash_step(t), (uint32_t)tbi) : 0u;
+  hash += ok ? index_term((uint32_t)p, (uint32_t)tbi) : 0u;
   const bool staged = (uint32_t)(tbi - tb.t_lo) < (uint32_t)tb.nt;
   all_lds = ballot(!staged) == 0;
   uint32_t nsym, offset;
@@ -1773,7 +1760,7 @@ __device__ __forceinline__ uint2 dec_record_search(const DecArgs& a, const Tabs&
   const bool ok = act & !bad;
   status |= bad ? GAANS_ST_INDEX : 0u;
   tbi = ok ? tbi : 0;
-  hash += ok ? index_term_pk(lane * kHashMul + hash_step(t), (uint32_t)tbi) : 0u;
+  hash += ok ? index_term((uint32_t)p, (uint32_t)tbi) : 0u;
   const uint4 lm = tb.lmeta[tbi];
   uint2 r;
   r.x = (uint32_t)tbi | ((act ? lm.x + lm.y - 1u : kNoSym) << 16);
