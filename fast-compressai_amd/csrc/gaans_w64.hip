@@ -2014,20 +2014,27 @@ __device__ __forceinline__ void stream_block_start(Stream& S, uint32_t* ring32, 
 
 // A refill past the stream end reads stale ring words; the chunk is then
 // marked corrupt by the final check that exactly the stream was consumed.
-template <int SB>
+// Every lane reads (the lane's rank among the refilling lanes, counted on top
+// of the stream position by mbcnt's accumulator) and only refilling lanes
+// keep the word (the read's value is opaque to the compiler, so the select
+// is not turned into an exec-masked branch around it).  kSkip: the read is
+// skipped when no lane refills (a uniform branch on the compare).  Measured
+// on MI355X: with one workgroup per CU, where the step's latency bounds the
+// launch, the branch lengthens the step (2160x3840 latent 231 -> 238 us,
+// 512x768 23.8 -> 24.4 us); with several per CU, where issue slots do, it
+// saves them (batch-64 skew 101 -> 95 us, uniform 95 -> 90 us).
+template <int SB, bool kSkip>
 __device__ __forceinline__ void dec_refill(bool need, uint32_t& x, Stream& S, const uint16_t* ring,
                                            int lane) {
   const uint64_t m = ballot(need);
-  // every lane reads (the lane's rank among the refilling lanes, counted on
-  // top of the stream position by mbcnt's accumulator) and only refilling
-  // lanes keep the word: the read stays unconditional (an opaque value for
-  // the compiler, so the select is not turned into a branch around it)
-  const uint32_t pos = __builtin_amdgcn_mbcnt_hi(
-      (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, (uint32_t)S.rp));
-  uint32_t w = ring[pos & (DecGeom<SB>::kRing - 1)];
-  asm volatile("" : "+v"(w));
-  x = need ? ((x << 16) | w) : x;
-  S.rp += __popcll(m);
+  if (!kSkip || m != 0ull) {
+    const uint32_t pos = __builtin_amdgcn_mbcnt_hi(
+        (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, (uint32_t)S.rp));
+    uint32_t w = ring[pos & (DecGeom<SB>::kRing - 1)];
+    asm volatile("" : "+v"(w));
+    x = need ? ((x << 16) | w) : x;
+    S.rp += __popcll(m);
+  }
 }
 
 // Escape section of one chunk, read from the chunk's end: escape u32 m holds
@@ -2156,7 +2163,8 @@ __device__ __forceinline__ void esc_resolve(uint64_t em, uint32_t base, uint32_t
 // the lanes that decoded the escape bin (their values are resolved by the
 // mappers, off the state chain).  kFull: every lane is active and no offset
 // can overflow with a symbol index.
-template <bool kLds, bool kFull, int SB, bool kSearch = false, bool kWide = false>
+template <bool kLds, bool kFull, int SB, bool kSearch = false, bool kWide = false,
+          bool kSkip = false>
 __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint2 r, uint32_t& x,
                                              Stream& S, const uint16_t* ring, uint64_t& em,
                                              uint32_t& status, int lane) {
@@ -2168,7 +2176,7 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint2 r, uint
   else dec_lookup<kLds, kWide>(tb, r.x & 0xffffu, cum, act, s, st, fr);
   const uint32_t xn = __umul24(fr, x >> 16) + cum - st;
   x = act ? xn : x;
-  dec_refill<SB>(act & (x < kStateLow), x, S, ring, lane);
+  dec_refill<SB, kSkip>(act & (x < kStateLow), x, S, ring, lane);
   // value + offset for an ordinary symbol: s < 2^16, so the int32 sum overflows
   // exactly when it wraps below the offset
   const int32_t o = (int32_t)(s + r.y);
@@ -2189,7 +2197,7 @@ constexpr int kDecWavesPerSimd = 5;
 constexpr int kDecWavesPerSimd = 6;
 #endif
 
-template <int kMode, bool kImplicit, int SB, bool kSearch, bool kWide>
+template <int kMode, bool kImplicit, int SB, bool kSearch, bool kWide, bool kSkip = false>
 __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArgs a) {
   constexpr bool kLatents = kMode != kModeSymbols;  // fp32 output with a per-element add
   using G = DecGeom<SB>;
@@ -2491,8 +2499,8 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
           uint64_t em[SB];
 #pragma unroll
           for (int u = 0; u < SB; ++u) {
-            ov[u] = dec_step<true, true, SB, kSearch, kWide>(tb, r[u], x, S, sring, em[u], status,
-                                                            lane);
+            ov[u] = dec_step<true, true, SB, kSearch, kWide, kSkip>(tb, r[u], x, S, sring, em[u],
+                                                                 status, lane);
             any_em |= em[u];
           }
           if (__builtin_expect(any_em != 0ull, 0)) {
@@ -3253,17 +3261,18 @@ EncKernel enc_kernel(int mode, bool imp, int sb, int nm) {
   }
 }
 
-template <int kMode, bool kImp, bool kSearch, bool kWide = false>
+template <int kMode, bool kImp, bool kSearch, bool kWide = false, bool kSkip = false>
 DecKernel dec_kernel_sb(int sb) {
-  return sb == 4 ? k_decode<kMode, kImp, 4, kSearch, kWide>
-                 : (sb == 8 ? k_decode<kMode, kImp, 8, kSearch, kWide>
-                            : k_decode<kMode, kImp, 16, kSearch, kWide>);
+  return sb == 4 ? k_decode<kMode, kImp, 4, kSearch, kWide, kSkip>
+                 : (sb == 8 ? k_decode<kMode, kImp, 8, kSearch, kWide, kSkip>
+                            : k_decode<kMode, kImp, 16, kSearch, kWide, kSkip>);
 }
 
 // Decode kernel of a mode, index kind, block size and lookup kind (the
 // search lookups serve explicit or computed indexes only; the wide lookups
-// are staged with 8- or 16-step blocks only).
-DecKernel dec_kernel(int mode, bool imp, int sb, bool search, bool wide) {
+// are staged with 8- or 16-step blocks only).  skip: the variant whose steps
+// skip the refill read when no lane refills, for the 256-bucket lookups.
+DecKernel dec_kernel(int mode, bool imp, int sb, bool search, bool wide, bool skip) {
   if (search) {
     switch (mode) {
       case kModeGaussian: return dec_kernel_sb<kModeGaussian, false, true>(sb);
@@ -3287,6 +3296,17 @@ DecKernel dec_kernel(int mode, bool imp, int sb, bool search, bool wide) {
                              : k_decode<kModeSymbols, true, 16, false, true>)
                    : (w == 8 ? k_decode<kModeSymbols, false, 8, false, true>
                              : k_decode<kModeSymbols, false, 16, false, true>);
+    }
+  }
+  if (skip) {
+    switch (mode) {
+      case kModeGaussian: return dec_kernel_sb<kModeGaussian, false, false, false, true>(sb);
+      case kModeLatents:
+        return imp ? dec_kernel_sb<kModeLatents, true, false, false, true>(sb)
+                   : dec_kernel_sb<kModeLatents, false, false, false, true>(sb);
+      default:
+        return imp ? dec_kernel_sb<kModeSymbols, true, false, false, true>(sb)
+                   : dec_kernel_sb<kModeSymbols, false, false, false, true>(sb);
     }
   }
   switch (mode) {
@@ -3538,7 +3558,9 @@ int decode_prepare(int mode, bool implicit, int32_t n_scales, float scale_bound,
   a.nd_cap = st.nd_cap;
   a.stage_all = st.stage_all;
   a.starts_words = plan.starts_words;
-  e->kernel = dec_kernel(mode, implicit, plan.sb, plan.search, plan.wide);
+  // the refill-skipping steps when the grid needs more than one workgroup
+  // per CU (issue slots, not one unit's step latency, bound the launch)
+  e->kernel = dec_kernel(mode, implicit, plan.sb, plan.search, plan.wide, L.U > (int64_t)dl.cus);
   e->grid = (uint32_t)L.U;
   e->block = (uint32_t)kDecThreads;
   e->lds = lds;

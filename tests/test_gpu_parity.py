@@ -342,6 +342,30 @@ def test_fused_latents_match_quantize_then_encode(gpu_device):
     assert torch.equal(y_hat.view(B, C, HW), sym_t.type_as(mt) + mt)
 
 
+def test_fused_latents_many_workgroups_per_cu(gpu_device):
+    """32 images at P = 16: 384 coding units, more than the device's CUs, so
+    the decoder's steps skip the refill read when no lane refills (the
+    256-bucket lookups of 16 tables per unit)."""
+    w = synthetic.coder_512x768(seed=5, batch=32, p_ch=16)
+    rng = np.random.default_rng(5)
+    B, N, C = w.batch, w.n, w.channels
+    med = rng.normal(0, 0.3, C).astype(np.float32)
+    HW = N // C
+    y = (w.symbols.reshape(B, C, HW) + med[None, :, None]
+         + rng.uniform(-0.5, 0.5, (B, C, HW))).astype(np.float32)
+    sym_ref = O.quantize(y, med)
+    tables = prepare_tables(*tables_on(w, gpu_device))
+    say("case: fused latents 32x192x32x48 P=16")
+    enc = gaans.encode(tables, B, N, C, 16, gpu_device, y=dev(y, gpu_device),
+                       medians=dev(med, gpu_device), segments=1)
+    ref = O.gaans_encode(sym_ref.reshape(B, N), None, w.cdfs, w.cdf_sizes, w.offsets, 16)
+    assert enc.packed.cpu().numpy().tobytes() == ref
+    y_hat = gaans.decode(enc.packed, tables, B, N, C, 16, gpu_device,
+                         medians=dev(med, gpu_device), segments=1)
+    ref_hat = O.dequantize(sym_ref, med).reshape(B, N)
+    assert np.array_equal(y_hat.cpu().numpy().view(np.uint32), ref_hat.view(np.uint32))
+
+
 def test_fused_latents_reject_non_finite(gpu_device):
     w = synthetic.coder_512x768()
     tables = prepare_tables(*tables_on(w, gpu_device))
