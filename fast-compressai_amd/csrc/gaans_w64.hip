@@ -1709,11 +1709,13 @@ int dec_fixed_lds(bool latents, int sb) {
 
 // Mapper record of one lane and step (8 bytes), tables in LDS when the step's
 // flag is 1:
-//   x: the lane's table (LDS-local or global index) | escape symbol << 16
-//      (nsym - 1; kNoSym for a lane past the chunk end)
+//   x: the lane's table | escape symbol << 16 (nsym - 1; kNoSym for a lane
+//      past the chunk end); the table is the LDS-local index times the
+//      lookup's bucket count (its first bucket: one add fewer per step for
+//      the coder), or the global index
 //   y: table offset
 // The coder overwrites x with the decoded value.
-template <bool kImplicit>
+template <bool kImplicit, bool kWide>
 __device__ __forceinline__ uint2 dec_record(const DecArgs& a, const Tabs& tb, int lane, int t,
                                             int len, int32_t start, int32_t in_b,
                                             uint32_t& hash, uint32_t& status, bool& all_lds) {
@@ -1741,7 +1743,8 @@ __device__ __forceinline__ uint2 dec_record(const DecArgs& a, const Tabs& tb, in
     asm volatile("" : "+v"(nsym), "+v"(offset));
   }
   uint2 r;
-  r.x = (uint32_t)(all_lds ? tbi - tb.t_lo : tbi) | ((act ? nsym - 1u : kNoSym) << 16);
+  constexpr int kB = kWide ? kWideBits : kLutBits;
+  r.x = (uint32_t)(all_lds ? (tbi - tb.t_lo) << kB : tbi) | ((act ? nsym - 1u : kNoSym) << 16);
   r.y = offset;
   return r;
 }
@@ -1796,7 +1799,8 @@ template <bool kLds, bool kWide = false>
 __device__ __forceinline__ void dec_lookup(const Tabs& tb, uint32_t t, uint32_t cum, bool act,
                                            uint32_t& s, uint32_t& st, uint32_t& fr) {
   constexpr int kB = kWide ? kWideBits : kLutBits;
-  const uint32_t li = (t << kB) + (cum >> (16 - kB));
+  // t: the LDS-local table's first bucket, or the global table index
+  const uint32_t li = (kLds ? t : t << kB) + (cum >> (16 - kB));
   uint64_t e = kLds ? tb.llut[li] : tb.glut[li];
   // the dense tests first: their scalar results are ready by the branches
   const uint64_t dm = ballot(act & dense_entry(e));
@@ -2408,8 +2412,8 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
           r = dec_record_search(a, tb, lane, j * SB + u, len, ix, hash, status);
           all_lds = true;
         } else {
-          r = dec_record<kImplicit>(a, tb, lane, j * SB + u, len, start, ix, hash, status,
-                                    all_lds);
+          r = dec_record<kImplicit, kWide>(a, tb, lane, j * SB + u, len, start, ix, hash,
+                                           status, all_lds);
         }
         dst[u * kLanes + lane] = r;
         if (kLatents) med[((j & 1) * SB + u) * kLanes + lane] = cm[e];
@@ -2889,7 +2893,7 @@ __global__ void __launch_bounds__(kLanes) k_rans64_decode(R64Args a) {
       }
       const uint32_t cum = (uint32_t)x & 0xffffu;
       uint32_t s, st, fr;
-      if (a.stage != 0) dec_lookup<true>(tb, tl, cum, ok, s, st, fr);
+      if (a.stage != 0) dec_lookup<true>(tb, tl << kLutBits, cum, ok, s, st, fr);
       else dec_lookup<false>(tb, tl, cum, ok, s, st, fr);
       x = (uint64_t)fr * (x >> 16) + cum - st;
       if (ok && x < kR64L) x = (x << 32) | r64_next(S, ring, lane);
