@@ -1790,21 +1790,42 @@ __device__ __forceinline__ uint64_t sub_entry(const Tabs& tb, uint64_t e, uint32
 
 __device__ __forceinline__ bool dense_entry(uint64_t e) { return (uint32_t)(e >> 48) == 0xffffu; }
 
+// (symbol, start, freq) from a lookup entry with at most one other start
+// (see the blob layout): s or s + 1.
+__device__ __forceinline__ void lut_pick(uint64_t e, uint32_t cum, uint32_t& s, uint32_t& st,
+                                         uint32_t& fr) {
+  const uint32_t lo = (uint32_t)e, hi = (uint32_t)(e >> 32);
+  const uint32_t st0 = lo & 0xffffu, st1 = (lo >> 16) + 1u;
+  const bool up = cum >= st1;
+  s = (hi & 0xffffu) + (up ? 1u : 0u);
+  st = up ? st1 : st0;
+  fr = up ? (hi >> 16) + 1u : st1 - st0;
+}
+
 // cum -> (symbol, start, freq) in table t: the table's lookup entry of
 // bucket cum >> 8, for a dense bucket the entry of sub-range (cum >> 4) & 15
 // of its sub-block, for a dense sub-range the exact entry of value cum & 15
 // (see the blob layout).  kWide: the wide lookups, bucket cum >> 5 and, for
-// a dense bucket, sub-range (cum >> 1) & 15 of its sub-block.
-template <bool kLds, bool kWide = false>
+// a dense bucket, sub-range (cum >> 1) & 15 of its sub-block.  t is the
+// staged table's first bucket (kLds) or the global table index.  kEarly: the
+// entry is decoded before the dense test's branch (the asm keeps it there)
+// and a dense lane's values are redone from the entry one or two levels
+// down, which overlaps the branch's latency with that work (512x768 decode
+// 23.6 -> 23.2 us with one workgroup per CU); else after it, which spends
+// no issue slots on the redone work (batch-64 skew decode 95.9 -> 93.9 us
+// with three per CU).
+template <bool kLds, bool kWide = false, bool kEarly = false>
 __device__ __forceinline__ void dec_lookup(const Tabs& tb, uint32_t t, uint32_t cum, bool act,
                                            uint32_t& s, uint32_t& st, uint32_t& fr) {
   constexpr int kB = kWide ? kWideBits : kLutBits;
-  // t: the LDS-local table's first bucket, or the global table index
   const uint32_t li = (kLds ? t : t << kB) + (cum >> (16 - kB));
   uint64_t e = kLds ? tb.llut[li] : tb.glut[li];
-  // the dense tests first: their scalar results are ready by the branches
+  if (kEarly) {
+    lut_pick(e, cum, s, st, fr);
+    asm volatile("" : "+v"(s), "+v"(st), "+v"(fr));
+  }
   const uint64_t dm = ballot(act & dense_entry(e));
-  asm volatile("" ::"s"(dm));
+  if (!kEarly) asm volatile("" ::"s"(dm));
   if (__builtin_expect(dm != 0ull, 0)) {
     if constexpr (kWide) {
       // a wide bucket's sub-ranges (two values) are never dense
@@ -1815,15 +1836,9 @@ __device__ __forceinline__ void dec_lookup(const Tabs& tb, uint32_t t, uint32_t 
       if (__builtin_expect(dm3 != 0ull, 0) && (act & dense_entry(e)))
         e = sub_entry<kLds>(tb, e, cum & (kSubSize - 1));
     }
+    if (kEarly) lut_pick(e, cum, s, st, fr);
   }
-  // the compare reads the entry directly; the rest runs beside it
-  const uint32_t lo = (uint32_t)e, hi = (uint32_t)(e >> 32);
-  const uint32_t s0 = hi & 0xffffu, nxt = hi >> 16;
-  const uint32_t st0 = lo & 0xffffu, st1 = (lo >> 16) + 1u;
-  const bool up = cum >= st1;
-  s = up ? s0 + 1u : s0;
-  st = up ? st1 : st0;
-  fr = up ? nxt + 1u : st1 - st0;
+  if (!kEarly) lut_pick(e, cum, s, st, fr);
 }
 
 // cum -> (symbol, start, freq) with the search lookups, all tables in LDS.
@@ -2032,6 +2047,8 @@ __device__ __forceinline__ void dec_refill(bool need, uint32_t& x, Stream& S, co
                                            int lane) {
   const uint64_t m = ballot(need);
   if (!kSkip || m != 0ull) {
+    // the ring position (< kRing) plus the rank: past the end it reads the
+    // mirrored first words
     const uint32_t pos = __builtin_amdgcn_mbcnt_hi(
         (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, (uint32_t)S.rp));
     uint32_t w = ring[pos & (DecGeom<SB>::kRing - 1)];
@@ -2177,7 +2194,7 @@ __device__ __forceinline__ uint32_t dec_step(const Tabs& tb, const uint2 r, uint
   const uint32_t cum = x & 0xffffu;
   uint32_t s, st, fr;
   if constexpr (kSearch) dec_lookup_search(tb, r.x & 0xffffu, cum, act, s, st, fr);
-  else dec_lookup<kLds, kWide>(tb, r.x & 0xffffu, cum, act, s, st, fr);
+  else dec_lookup<kLds, kWide, !kSkip>(tb, r.x & 0xffffu, cum, act, s, st, fr);
   const uint32_t xn = __umul24(fr, x >> 16) + cum - st;
   x = act ? xn : x;
   dec_refill<SB, kSkip>(act & (x < kStateLow), x, S, ring, lane);
@@ -3142,7 +3159,7 @@ DecPlan plan_decode(const gaans_tables* t, int64_t P, int64_t units, bool latent
     // count (P times the mean per table), a unit staging its range's first
     // ones and reading the others from global memory (the 2160x3840
     // latent's chunks of 8 tables need 30-115 sub-blocks, 8 x 26 by the
-    // bound; 8-step blocks leave room for 124); else none (a dense wide
+    // bound; 8-step blocks leave room for 123); else none (a dense wide
     // bucket then reads its two-value sub-range from global memory, where
     // the 256-value buckets gave the wide-table units a second or third
     // read in most steps).
