@@ -4127,6 +4127,19 @@ int gaans_enqueue_decode(const gaans_plan* plan, void* stream, const uint8_t* pa
   return decode_launch(e, stream);
 }
 
+int gaans_run_encode_call(const gaans_encode_call* c) {
+  if (!c) return fail(GAANS_EINVAL, "call pointer is NULL");
+  return gaans_run_encode(c->plan, c->stream, c->in[0], c->in[1], c->in[2], c->in[3],
+                          c->workspace_dev, c->workspace_bytes, c->ctrl_dev, c->out_dev,
+                          c->out_bytes, c->info_host);
+}
+
+int gaans_run_decode_call(const gaans_decode_call* c) {
+  if (!c) return fail(GAANS_EINVAL, "call pointer is NULL");
+  return gaans_run_decode(c->plan, c->stream, c->payload_dev, c->payload_bytes, c->in[0],
+                          c->in[1], c->in[2], c->out_dev, c->ctrl_dev, c->status_host);
+}
+
 int gaans_debug_phases(void* buffer_dev, int64_t units, int32_t* wall_clock_khz) {
 #ifndef GAANS_PHASE_TIMES
   if (buffer_dev != nullptr && units > 0)

@@ -15,7 +15,7 @@ import threading
 from .errors import CoderDependencyError
 
 LIB_NAME = "libgaans_w64.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 CTRL_BYTES = 256
 PLAN_BYTES = 1536  # GAANS_PLAN_BYTES
 PHASE_SLOTS = 16  # GAANS_PHASE_SLOTS
@@ -78,6 +78,27 @@ class Tables(ctypes.Structure):
                 ("total_wide", ctypes.c_int64)]
 
 
+class EncodeCall(ctypes.Structure):
+    """``gaans_encode_call``: gaans_run_encode's arguments (gaans_run_encode_call)."""
+
+    _fields_ = [("plan", ctypes.c_void_p), ("stream", ctypes.c_void_p),
+                ("in0", ctypes.c_void_p), ("in1", ctypes.c_void_p), ("in2", ctypes.c_void_p),
+                ("in3", ctypes.c_void_p), ("workspace_dev", ctypes.c_void_p),
+                ("workspace_bytes", ctypes.c_int64), ("ctrl_dev", ctypes.c_void_p),
+                ("out_dev", ctypes.c_void_p), ("out_bytes", ctypes.c_int64),
+                ("info_host", ctypes.c_void_p)]
+
+
+class DecodeCall(ctypes.Structure):
+    """``gaans_decode_call``: gaans_run_decode's arguments (gaans_run_decode_call)."""
+
+    _fields_ = [("plan", ctypes.c_void_p), ("stream", ctypes.c_void_p),
+                ("payload_dev", ctypes.c_void_p), ("payload_bytes", ctypes.c_int64),
+                ("in0", ctypes.c_void_p), ("in1", ctypes.c_void_p), ("in2", ctypes.c_void_p),
+                ("out_dev", ctypes.c_void_p), ("ctrl_dev", ctypes.c_void_p),
+                ("status_host", ctypes.c_void_p)]
+
+
 # GAANS_PHASE_TIMES=1 selects the measurement build (kernels that record phase
 # timestamps; csrc/build.py --phases), for bench.py --phases only
 LIB_NAME_PHASES = "libgaans_w64_phases.so"
@@ -134,6 +155,9 @@ def _declare(L) -> None:
         "gaans_run_decode": ([p, p, p, i64, p, p, p, p, p, p], ctypes.c_int),
         "gaans_enqueue_encode": ([p, p, p, p, p, p, p, i64, p, p, i64, p], ctypes.c_int),
         "gaans_enqueue_decode": ([p, p, p, i64, p, p, p, p, p, p], ctypes.c_int),
+        # struct addresses (c_void_p): one argument to convert per call
+        "gaans_run_encode_call": ([p], ctypes.c_int),
+        "gaans_run_decode_call": ([p], ctypes.c_int),
         "gaans_host_selftest": ([], ctypes.c_int),
     }
     for name, (args, res) in sig.items():

@@ -302,20 +302,43 @@ def _run_decode_ptr(tables: PreparedTables, mode: int, explicit: bool, B: int, N
     return out
 
 
+class _Call:
+    """A symbols-mode call context on one stream of one device (cached on the
+    tables per shape and stream): the plan, its sizes and stream state, and
+    the argument struct of gaans_run_encode_call / _decode_call with the
+    fields that do not change from call to call already set."""
+
+    __slots__ = ("plan_buf", "max_bytes", "ws_bytes", "st", "args", "addr", "run", "ws")
+
+    def __init__(self, tables: PreparedTables, decode: bool, explicit: bool, B: int, N: int,
+                 C: int, P: int, S: int, index: int, sp: int) -> None:
+        self.plan_buf, plan, lay = _plan(tables, decode, _native.MODE_SYMBOLS, explicit, B, N, C,
+                                         P, S, index)
+        self.max_bytes = lay.max_payload_bytes
+        self.ws_bytes = lay.workspace_bytes
+        self.st = st = _state(index, sp)
+        L = _native.lib()
+        if decode:
+            self.args = _native.DecodeCall(plan=plan, stream=sp, ctrl_dev=st.ctrl_ptr,
+                                           status_host=st.status_ptr)
+            self.run = L.gaans_run_decode_call
+        else:
+            self.args = _native.EncodeCall(plan=plan, stream=sp, ctrl_dev=st.ctrl_ptr,
+                                           out_bytes=lay.max_payload_bytes,
+                                           info_host=st.info_ptr)
+            self.run = L.gaans_run_encode_call
+        self.addr = ctypes.addressof(self.args)
+        self.ws = None  # the workspace tensor whose address the struct holds
+
+
 def _symbols_call(tables: PreparedTables, decode: bool, explicit: bool, B: int, N: int, C: int,
-                  P: int, S: int, index: int, sp: int):
-    """What a symbols-mode call on stream ``sp`` of device ``index`` needs
-    besides its pointers, cached on the tables per (shape, stream): (plan
-    address, worst-case payload bytes, workspace bytes, stream state, the C
-    entry point, plan buffer).  Device ``index`` is current."""
+                  P: int, S: int, index: int, sp: int) -> _Call:
+    """The call context of a symbols-mode call on stream ``sp`` of device
+    ``index`` (current)."""
     key = ("call", decode, explicit, B, N, C, P, S, index, sp)
     ctx = tables.plans.get(key)
     if ctx is None:
-        buf, plan, lay = _plan(tables, decode, _native.MODE_SYMBOLS, explicit, B, N, C, P, S,
-                               index)
-        L = _native.lib()
-        ctx = (plan, lay.max_payload_bytes, lay.workspace_bytes, _state(index, sp),
-               L.gaans_run_decode if decode else L.gaans_run_encode, buf)
+        ctx = _Call(tables, decode, explicit, B, N, C, P, S, index, sp)
         tables.plans[key] = ctx
     return ctx
 
@@ -332,14 +355,20 @@ def encode_symbols_raw(tables: PreparedTables, B: int, N: int, C: int, P: int, d
                                         _ptr(indexes), None, None, "GA-ANS encode")
         return out, total
     sp = torch._C._cuda_getCurrentRawStream(index)
-    plan, max_bytes, ws_bytes, st, run, _ = _symbols_call(
-        tables, False, indexes is not None, B, N, C, P, segments, index, sp)
-    out = torch.empty(max_bytes, dtype=torch.uint8, device=st.device)
+    c = _symbols_call(tables, False, indexes is not None, B, N, C, P, segments, index, sp)
+    st = c.st
+    out = torch.empty(c.max_bytes, dtype=torch.uint8, device=st.device)
     with st.lock:
-        ws = st.ws(ws_bytes)
-        rc = run(plan, sp, symbols.data_ptr(), None if indexes is None else indexes.data_ptr(),
-                 None, None, ws.data_ptr(), ws.numel(), st.ctrl_ptr, out.data_ptr(), max_bytes,
-                 st.info_ptr)
+        a = c.args
+        ws = st.ws(c.ws_bytes)
+        if ws is not c.ws:
+            a.workspace_dev = ws.data_ptr()
+            a.workspace_bytes = ws.numel()
+            c.ws = ws
+        a.in0 = symbols.data_ptr()
+        a.in1 = None if indexes is None else indexes.data_ptr()
+        a.out_dev = out.data_ptr()
+        rc = c.run(c.addr)
         word = int(st.info_np[2])  # 1 | status << 1 | payload bytes << 16
     if rc:
         _native.check(rc, "GA-ANS encode")
@@ -360,13 +389,16 @@ def decode_symbols_ptr(payload_ptr: int, payload_bytes: int, tables: PreparedTab
                                segments, device, payload_ptr, payload_bytes, _ptr(indexes), None,
                                None, torch.int32, "GA-ANS decode")
     sp = torch._C._cuda_getCurrentRawStream(index)
-    plan, _, _, st, run, _ = _symbols_call(tables, True, indexes is not None, B, N, C, P,
-                                           segments, index, sp)
+    c = _symbols_call(tables, True, indexes is not None, B, N, C, P, segments, index, sp)
+    st = c.st
     out = torch.empty((B, N), dtype=torch.int32, device=st.device)
     with st.lock:
-        rc = run(plan, sp, payload_ptr, payload_bytes,
-                 None if indexes is None else indexes.data_ptr(), None, None, out.data_ptr(),
-                 st.ctrl_ptr, st.status_ptr)
+        a = c.args
+        a.payload_dev = payload_ptr
+        a.payload_bytes = payload_bytes
+        a.in0 = None if indexes is None else indexes.data_ptr()
+        a.out_dev = out.data_ptr()
+        rc = c.run(c.addr)
         status = int(st.status_np[1]) >> 1  # 1 | status << 1
     if rc:
         _native.check(rc, "GA-ANS decode")

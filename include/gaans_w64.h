@@ -62,7 +62,7 @@
 extern "C" {
 #endif
 
-#define GAANS_ABI_VERSION 13
+#define GAANS_ABI_VERSION 14
 #define GAANS_CTRL_BYTES 256
 
 /* return codes */
@@ -431,6 +431,38 @@ int gaans_run_decode(const gaans_plan* plan, void* stream, const uint8_t* payloa
 int gaans_enqueue_decode(const gaans_plan* plan, void* stream, const uint8_t* payload_dev,
                          int64_t payload_bytes, const void* in0, const void* in1,
                          const void* in2, void* out_dev, void* ctrl_dev, uint32_t* status_out);
+
+/* gaans_run_encode / gaans_run_decode with their arguments in one struct
+ * (same meaning, same behaviour): for bindings whose per-call cost is the
+ * argument conversion itself (ctypes converts each argument on every call),
+ * which keep one struct per plan and stream, set the fields that change
+ * (inputs, output, workspace) and pass its address.  No counterpart in the
+ * reference (its binding is a pybind11 module, ans_gpu.cpp:25-30). */
+typedef struct gaans_encode_call {
+  const gaans_plan* plan;
+  void* stream;
+  const void* in[4];
+  void* workspace_dev;
+  int64_t workspace_bytes;
+  void* ctrl_dev;
+  uint8_t* out_dev;
+  int64_t out_bytes;
+  uint64_t* info_host;
+} gaans_encode_call;
+
+typedef struct gaans_decode_call {
+  const gaans_plan* plan;
+  void* stream;
+  const uint8_t* payload_dev;
+  int64_t payload_bytes;
+  const void* in[3];
+  void* out_dev;
+  void* ctrl_dev;
+  uint32_t* status_host;
+} gaans_decode_call;
+
+int gaans_run_encode_call(const gaans_encode_call* call);
+int gaans_run_decode_call(const gaans_decode_call* call);
 
 /* ---- measurement ------------------------------------------------------------ */
 

@@ -393,3 +393,57 @@ def test_plan_and_run_reject_bad_arguments_before_device_work():
     assert L.gaans_run_encode(None, None, fake, None, None, None, fake, 1 << 20, fake, fake,
                               1 << 20, ctypes.addressof(info)) == _native.EINVAL
     assert ctypes.sizeof(plan) == _native.PLAN_BYTES
+
+
+def test_call_structs_match_the_header(tmp_path):
+    # the ctypes mirrors of gaans_encode_call / gaans_decode_call against the
+    # C compiler's offsets and sizes for the header's structs
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    probes = []
+    for cname, cls in (("gaans_encode_call", _native.EncodeCall),
+                       ("gaans_decode_call", _native.DecodeCall)):
+        probes.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            member = {"in0": "in[0]", "in1": "in[1]", "in2": "in[2]",
+                      "in3": "in[3]"}.get(fname, fname)
+            probes.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {member}));')
+    src = tmp_path / "probe.c"
+    src.write_text("#include <stddef.h>\n#include <stdio.h>\n#include \"gaans_w64.h\"\n"
+                   "int main(void) {\n" + "\n".join(probes) + "\nreturn 0;\n}\n")
+    exe = tmp_path / "probe"
+    subprocess.run([cc, "-I", os.path.join(REPO, "include"), str(src), "-o", str(exe)],
+                   check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True,
+                               text=True).stdout.splitlines():
+        cname, field, val = line.split()
+        got[(cname, field)] = int(val)
+    for cname, cls in (("gaans_encode_call", _native.EncodeCall),
+                       ("gaans_decode_call", _native.DecodeCall)):
+        assert got[(cname, "size")] == ctypes.sizeof(cls)
+        for fname, _ in cls._fields_:
+            assert got[(cname, fname)] == getattr(cls, fname).offset, (cname, fname)
+
+
+def test_call_struct_entries_reject_bad_arguments():
+    L = _native.lib()
+    assert L.gaans_run_encode_call(None) == _native.EINVAL
+    assert L.gaans_run_decode_call(None) == _native.EINVAL
+    plan = (ctypes.c_uint64 * (_native.PLAN_BYTES // 8))()  # not filled by gaans_plan_*
+    info = (ctypes.c_uint64 * 3)()
+    status = (ctypes.c_uint32 * 2)()
+    fake = 1 << 20  # never dereferenced: the runs stop at the plan check
+    e = _native.EncodeCall(plan=ctypes.addressof(plan), in0=fake, workspace_dev=fake,
+                           workspace_bytes=1 << 20, ctrl_dev=fake, out_dev=fake,
+                           out_bytes=1 << 20, info_host=ctypes.addressof(info))
+    assert L.gaans_run_encode_call(ctypes.addressof(e)) == _native.EINVAL
+    assert "encode plan" in _native.last_error()
+    d = _native.DecodeCall(plan=ctypes.addressof(plan), payload_dev=fake, payload_bytes=1 << 20,
+                           out_dev=fake, ctrl_dev=fake, status_host=ctypes.addressof(status))
+    assert L.gaans_run_decode_call(ctypes.addressof(d)) == _native.EINVAL
+    assert "decode plan" in _native.last_error()
