@@ -834,9 +834,23 @@ __device__ __forceinline__ bool enc_records_fast(const EncArgs& a, const Tabs& t
 
 // Encoder LDS ring: ring_mask + 1 words (a power of two) and one spare slot
 // per lane (where a step's lanes that emit nothing store).
+// Words [wp, fl) to the staging slot: the ones before the first multiple
+// of 4 and after the last one word per lane, the rest 4 words (8 bytes) per
+// lane (the ring's size is a multiple of 4 words, so such a group never
+// straddles its wrap; the slot is 16-byte aligned).
 __device__ __forceinline__ void ring_flush(uint16_t* __restrict__ wbuf, const uint16_t* ring,
                                            int wp, int fl, int lane, uint32_t ring_mask) {
-  for (int pos = wp + lane; pos < fl; pos += kLanes) wbuf[pos] = ring[pos & ring_mask];
+  const int a0 = (wp + 3) & ~3, a1 = fl & ~3;
+  if (a0 >= a1) {  // uniform: fewer than one aligned group
+    for (int pos = wp + lane; pos < fl; pos += kLanes) wbuf[pos] = ring[pos & ring_mask];
+    return;
+  }
+  if (lane < a0 - wp) wbuf[wp + lane] = ring[(wp + lane) & ring_mask];
+  if (lane < fl - a1) wbuf[a1 + lane] = ring[(a1 + lane) & ring_mask];
+  const uint2* r64 = reinterpret_cast<const uint2*>(ring);
+  uint2* w64 = reinterpret_cast<uint2*>(wbuf);
+  const uint32_t m64 = ring_mask >> 2;
+  for (int i = (a0 >> 2) + lane; i < (a1 >> 2); i += kLanes) w64[i] = r64[(uint32_t)i & m64];
 }
 
 // The ring holds the words [wp, fl) (positions mod the ring size).  The coder
