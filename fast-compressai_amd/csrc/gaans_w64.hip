@@ -443,6 +443,36 @@ static_assert(kModeSymbols == GAANS_MODE_SYMBOLS && kModeLatents == GAANS_MODE_L
                   kModeGaussian == GAANS_MODE_GAUSSIAN,
               "plan modes are the kernel modes");
 
+// Tables of at most kGaussFast + 1 scales are searched in two levels, one
+// LDS read each instead of one per halving: the count c of the 8 values
+// table[8i + 7] below lb (kept in registers, GaussCoarse; +inf for 8i + 7
+// >= L - 1), then the count of table[8c .. 8c + 7] below lb, which is exact
+// for a non-decreasing table.  The staged table is padded with +inf from
+// entry L - 1 on (the search never reads entry L - 1) to L + 8, past the
+// last entry the second level can read (8c + 7 <= L + 6).
+constexpr int kGaussFast = 64;
+constexpr int kGaussPad = 8;  // +inf entries staged after the table
+struct GaussCoarse {
+  float v[8];
+};
+__device__ __forceinline__ GaussCoarse gauss_coarse(const float* tab, int L) {
+  GaussCoarse c;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    c.v[i] = L <= kGaussFast + 1 && 8 * i + 7 < L - 1 ? tab[8 * i + 7] : __builtin_inff();
+  return c;
+}
+__device__ __forceinline__ int32_t gauss_index_fast(float lb, const float* tab,
+                                                    const GaussCoarse& c) {
+  int k = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) k += c.v[i] < lb ? 1 : 0;
+  const float4 a = *reinterpret_cast<const float4*>(tab + 8 * k);
+  const float4 b = *reinterpret_cast<const float4*>(tab + 8 * k + 4);
+  return 8 * k + (a.x < lb) + (a.y < lb) + (a.z < lb) + (a.w < lb) + (b.x < lb) + (b.y < lb) +
+         (b.z < lb) + (b.w < lb);
+}
+
 // CompressAI's GaussianConditional.build_indexes for one scale s (the
 // third-party algorithm, restated in the oracle): lb = max(s, bound) (NaN
 // propagates, as torch.max does), index =
@@ -450,8 +480,9 @@ static_assert(kModeSymbols == GAANS_MODE_SYMBOLS && kModeLatents == GAANS_MODE_L
 // #{k < L - 1 : table[k] < lb}, found by a fixed-step binary search over the
 // table in LDS (pow2 = the largest power of two <= L - 1); NaN -> L - 1.
 __device__ __forceinline__ int32_t gauss_index(float s, const float* tab, int L, int pow2,
-                                               float bound) {
+                                               float bound, const GaussCoarse& gc) {
   const float lb = s < bound ? bound : s;
+  if (L <= kGaussFast + 1) return lb != lb ? L - 1 : gauss_index_fast(lb, tab, gc);
   int pos = 0;
   for (int step = pow2; step > 0; step >>= 1) {
     const int i = pos + step - 1;
@@ -466,7 +497,7 @@ __device__ __forceinline__ int32_t gauss_index(float s, const float* tab, int L,
 // reads are in flight at the same time.
 template <int KP>
 __device__ __forceinline__ void gauss_indexes(int32_t* io, const float* tab, int L, int pow2,
-                                              float bound) {
+                                              float bound, const GaussCoarse& gc) {
   float lb[KP];
   int pos[KP];
 #pragma unroll
@@ -474,6 +505,13 @@ __device__ __forceinline__ void gauss_indexes(int32_t* io, const float* tab, int
     const float s = __int_as_float(io[e]);
     lb[e] = s < bound ? bound : s;
     pos[e] = 0;
+  }
+  if (L <= kGaussFast + 1) {  // uniform
+#pragma unroll
+    for (int e = 0; e < KP; ++e) pos[e] = gauss_index_fast(lb[e], tab, gc);
+#pragma unroll
+    for (int e = 0; e < KP; ++e) io[e] = lb[e] != lb[e] ? L - 1 : pos[e];
+    return;
   }
   for (int step = pow2; step > 0; step >>= 1) {
 #pragma unroll
@@ -487,12 +525,13 @@ __device__ __forceinline__ void gauss_indexes(int32_t* io, const float* tab, int
   for (int e = 0; e < KP; ++e) io[e] = lb[e] != lb[e] ? L - 1 : pos[e];
 }
 
-// Stage the scale table (L floats) into LDS with the whole workgroup; the
-// caller's next barrier publishes it.
+// Stage the scale table into LDS with the whole workgroup: entries 0 ..
+// L - 2, then +inf up to L + kGaussPad (see gauss_index_fast); the caller's
+// next barrier publishes it.
 template <int NT>
 __device__ __forceinline__ void stage_scales(float* dst, const float* __restrict__ src, int L,
                                              int tid) {
-  for (int i = tid; i < L; i += NT) dst[i] = src[i];
+  for (int i = tid; i < L + kGaussPad; i += NT) dst[i] = i < L - 1 ? src[i] : __builtin_inff();
 }
 
 // ============================================================================
@@ -1359,6 +1398,9 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
     if (kMode == kModeGaussian) stage_scales<kThreads>(scl, a.scale_table, a.n_scales, tid);
     stage_tables<kThreads>(tb, lmeta, lent, nullptr, nullptr, bd, t_lo, t_hi, tid);
     if (wid == 0) pc.mark(2);
+    // the scale table's coarse level, after the staging barrier
+    GaussCoarse gc{};
+    if (kMode == kModeGaussian && wid != 0) gc = gauss_coarse(scl, a.n_scales);
 
     // this wave's steps per block: u = wid - 1 + kEncMappers e < SB
     const int nvalid = SB % kEncMappers == 0 ? kPer : (SB - wid + kEncMappers) / kEncMappers;
@@ -1389,7 +1431,7 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
     };
     auto map_block = [&](int j) __attribute__((always_inline)) {
       if (kMode == kModeGaussian)
-        gauss_indexes<kPer>(cb, scl, a.n_scales, a.scales_pow2, a.scale_bound);
+        gauss_indexes<kPer>(cb, scl, a.n_scales, a.scales_pow2, a.scale_bound, gc);
       // A full block first tries the fast path, which checks by itself that
       // every table is staged and every value in range (and changes nothing
       // when it declines), so the check below runs only for the rest.
@@ -2427,6 +2469,7 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
         }
       }
     };
+    GaussCoarse gc{};  // the mappers': the scale table's coarse level
     auto map_block = [&](int j) {
       uint2* dst = recs + (j & 1) * SB * kLanes;
 #pragma unroll
@@ -2436,7 +2479,7 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
         bool all_lds;
         const int32_t ix = kMode == kModeGaussian
                                ? gauss_index(__int_as_float(cbx[e]), scl, a.n_scales,
-                                             a.scales_pow2, a.scale_bound)
+                                             a.scales_pow2, a.scale_bound, gc)
                                : cbx[e];
         uint2 r;
         if constexpr (kSearch) {
@@ -2599,6 +2642,7 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
       publish();
       __syncthreads();
     } else {
+      if (kMode == kModeGaussian) gc = gauss_coarse(scl, a.n_scales);  // staged, published
       if (nblk > 0) map_block(0);
       __syncthreads();
       for (int j = 0; j < nblk; ++j) {
@@ -3379,7 +3423,9 @@ int encode_prepare(int mode, bool implicit, int32_t n_scales, float scale_bound,
   if ((rc = blob_ref(tables, &blob))) return rc;
   DevLds dl;
   if ((rc = device_lds(&dl))) return rc;
-  const int64_t extra = mode == kModeGaussian ? align_up(4 * (int64_t)n_scales, 16) : 0;
+  // the scale table, padded (stage_scales), at a 16-byte aligned offset
+  const int64_t extra =
+      mode == kModeGaussian ? align_up(4 * ((int64_t)n_scales + kGaussPad), 16) + 16 : 0;
   // 16-step blocks for long units only (the coder waits for the first
   // block to be mapped, so short units lose more than the per-block saving
   // gains: measured slower at 96 steps, faster at 4,080), and with explicit
@@ -3416,7 +3462,7 @@ int encode_prepare(int mode, bool implicit, int32_t n_scales, float scale_bound,
   a.n_scales = gauss ? n_scales : 0;
   a.scales_pow2 = gauss ? pow2_floor(n_scales - 1) : 0;
   a.scale_bound = gauss ? scale_bound : 0.0f;
-  a.scales_lds = (uint32_t)plan.lds;
+  a.scales_lds = (uint32_t)align_up((int64_t)plan.lds, 16);
   a.tables = static_cast<const uint8_t*>(tables->dev);
   a.M = (uint32_t)tables->M;
   a.tables_bytes = (uint32_t)tables->bytes;
@@ -3560,7 +3606,8 @@ int decode_prepare(int mode, bool implicit, int32_t n_scales, float scale_bound,
   const bool gauss = mode == kModeGaussian;
   if (gauss) implicit = false;
   const bool latents = mode != kModeSymbols;
-  const int64_t extra = gauss ? align_up(4 * (int64_t)n_scales, 16) : 0;
+  const int64_t extra =
+      gauss ? align_up(4 * ((int64_t)n_scales + kGaussPad), 16) + 16 : 0;  // as for the encoder
   const bool search_ok = (tables->flags & GAANS_TABLES_SEARCH) != 0 && !implicit;
   const DecPlan plan = plan_decode(tables, L.P, L.U, latents, dl, extra, !gauss, search_ok);
   const Stage& st = plan.st;
@@ -3577,7 +3624,7 @@ int decode_prepare(int mode, bool implicit, int32_t n_scales, float scale_bound,
   a.n_scales = gauss ? n_scales : 0;
   a.scales_pow2 = gauss ? pow2_floor(n_scales - 1) : 0;
   a.scale_bound = gauss ? scale_bound : 0.0f;
-  a.scales_lds = (uint32_t)plan.lds;
+  a.scales_lds = (uint32_t)align_up((int64_t)plan.lds, 16);
   a.N = L.N;
   a.header_bytes = L.header_bytes;
   a.units = L.U;
