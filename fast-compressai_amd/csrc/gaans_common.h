@@ -31,7 +31,7 @@ constexpr uint32_t kVersion = 5u;
 constexpr int kMaxSegments = 256;  // segments per chunk
 constexpr uint32_t kParams = 0x00041040u;  // lanes 64 | precision 16 << 8 | bypass 4 << 16
 constexpr int kFixedWords = 16;
-constexpr uint32_t kTabMagic = 0x37425447u;  // "GTB7"
+constexpr uint32_t kTabMagic = 0x38425447u;  // "GTB8"
 constexpr int kLutBits = 8;
 constexpr int kLutSize = 1 << kLutBits;
 constexpr int kSubBits = 4;                 // a sub-block: 16 entries of 16 or 1 values
@@ -78,7 +78,7 @@ struct TabHdr {
   uint32_t dense_off;    // byte offset of the sub-blocks
   uint32_t total_dense;  // sub-blocks over all tables
   uint32_t flags;        // kTabOffsetsSafe, kTabSearch, kTabWide
-  uint32_t clut_off;    // byte offset of the search lookups (u32 per bucket)
+  uint32_t clut_off;    // byte offset of the search lookups (u32 per segment)
   uint32_t starts_off;  // byte offset of the symbol starts (u16 per symbol)
   uint32_t wide_off;    // byte offset of the wide lookups (u64 x kWideSize per table)
   uint32_t wdense_off;  // byte offset of the wide lookups' sub-blocks
@@ -87,11 +87,30 @@ struct TabHdr {
 };
 // every offset <= INT32_MAX - 65535: symbol index + offset cannot overflow
 constexpr uint32_t kTabOffsetsSafe = 1u;
-// the search lookups are filled: at most kSearchMaxSyms symbols in all, every
-// offset at least INT32_MIN + 65536 (offset - symbol base cannot wrap)
+// the search lookups are filled: at most kSearchMaxSyms starts in all (the
+// symbols and kStartsTablePad per table), every offset at least INT32_MIN +
+// 65536 (offset - starts base cannot wrap)
 constexpr uint32_t kTabSearch = 2u;
 constexpr int64_t kSearchMaxSyms = 65535 - 8;
+// Search lookup segments of a table: 32-value parts of its first and last
+// kSearchFine 256-value buckets (entries 0-31: [0, 1024), 32-63: [64512,
+// 65536), so a part's entry is (cum >> 5) & 63), then one entry per bucket
+// (entry 64 + (cum >> 8); those of the 2 kSearchFine end buckets are filled
+// but not read).
+constexpr int kSearchFine = 4;
+constexpr int kSearchFineBits = 5;
+constexpr int kSearchParts = 2 * kSearchFine * (256 >> kSearchFineBits);
+constexpr int kSearchEntries = kSearchParts + 256;
+static_assert(kSearchParts == 64 && kSearchEntries % 4 == 0, "search segments");
 constexpr int kStartsPad = 8;  // zero starts after the last symbol (sentinel, reads past it)
+// Search lookups' starts: start - 1 (mod 2^16) of each symbol, table after
+// table, each followed by kStartsTablePad entries 0xffff, then kStartsPad
+// more (reads past the end).  A table's symbol v is at starts index
+// ent_base + kStartsTablePad * table + v.
+constexpr int kStartsTablePad = 3;
+inline int64_t search_starts(int64_t M, int64_t total_syms) {
+  return total_syms + kStartsTablePad * M + kStartsPad;
+}
 // the wide lookups are built (M <= kWideMaxTables)
 constexpr uint32_t kTabWide = 4u;
 static_assert(sizeof(TabHdr) == 80, "table header is 80 bytes");
@@ -234,8 +253,8 @@ inline BlobLayout blob_layout(int64_t M, int64_t total_syms, int64_t total_block
   L.lut_off = align_up(L.ent_off + 8 * total_syms, 16);
   L.dense_off = L.lut_off + 8ll * kLutSize * M;
   L.clut_off = L.dense_off + (int64_t)kSubBytes * total_blocks;
-  L.starts_off = L.clut_off + 4ll * kLutSize * M;
-  L.wide_off = L.starts_off + align_up(2 * (total_syms + kStartsPad), 16);
+  L.starts_off = L.clut_off + 4ll * kSearchEntries * M;
+  L.wide_off = L.starts_off + align_up(2 * search_starts(M, total_syms), 16);
   L.wdense_off = L.wide_off + (wide ? 8ll * kWideSize * M : 0);
   L.wbase_off = L.wdense_off + (wide ? (int64_t)kSubBytes * total_wide : 0);
   L.end = L.wbase_off + (wide ? align_up(4 * (M + 1), 16) : 0);

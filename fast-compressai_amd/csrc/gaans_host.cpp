@@ -120,26 +120,71 @@ int64_t tables_size(int32_t M, int64_t total_syms, int64_t total_blocks, int64_t
   return blob_layout(M, total_syms, total_blocks, M <= kWideMaxTables, total_wide).end;
 }
 
-// Search lookups of one table (symbols base .. base + nsym - 1 of the blob):
-// per 256-value bucket, the symbol g that contains the bucket's first value
-// (blob-wide index, bits 0-15), the number n of symbols that start inside
-// the bucket after it (bits 16-23: at most 255, one per value after the
-// first) and the number h of those that start in its first half (bits
-// 24-31); starts[base + s] = cdf[s].
-void build_search(const int32_t* c, uint32_t nsym, uint32_t base, uint32_t* clut,
+// Search lookups of one table, whose symbol v has starts index pbase + v
+// (see kStartsTablePad): starts[pbase + v] = cdf[v] - 1 mod 2^16 (0xffff for
+// symbol 0), then kStartsTablePad entries 0xffff, so that "start - 1 < cum"
+// holds for the symbols that start at or below cum and for no padding; and
+// one u32 per segment of the cum range (kSearchEntries: 32-value parts of
+// the first and the last kSearchFine buckets, then every 256-value bucket).
+// With u = cum & 255, a fitted segment's entry G (bits 0-15), m (bits
+// 16-23), 0 (bits 24-31) puts c = G + ((u * m) >> 8) at most three starts
+// indexes below the symbol that contains cum and never above it, and never
+// below the table's first symbol, so one read of starts c .. c + 4 resolves
+// it.  A bucket's line starts at its first value's symbol g (G = g, the
+// smallest m that meets both bounds); a part's may start anywhere (the first
+// m, in increasing order, for which some G >= 0 meets them; G is then the
+// largest).  A segment that no line fits gets G = g, m = 0 and in bits
+// 24-31 n, the symbols that start inside it after g (4 to 255: m = 0 fits
+// the segments with n <= 3); its lookup searches g .. g + n.
+void build_search(const int32_t* c, uint32_t nsym, uint32_t pbase, uint32_t* clut,
                   uint16_t* starts) {
-  for (uint32_t v = 0; v < nsym; ++v) starts[base + v] = (uint16_t)c[v];
-  const uint32_t width = 1u << (16 - kLutBits);
-  uint32_t s = 0;
-  for (uint32_t b = 0; b < (uint32_t)kLutSize; ++b) {
-    const uint32_t lo = b * width;
-    while (s + 1 < nsym && (uint32_t)c[s + 1] <= lo) ++s;
-    uint32_t n = 0, h = 0;
-    while (s + 1 + n < nsym && (uint32_t)c[s + 1 + n] < lo + width) {
-      h += (uint32_t)c[s + 1 + n] < lo + width / 2 ? 1u : 0u;
-      ++n;
+  for (uint32_t v = 0; v < nsym; ++v) starts[pbase + v] = (uint16_t)(c[v] - 1);
+  for (int i = 0; i < kStartsTablePad; ++i) starts[pbase + nsym + (uint32_t)i] = 0xffffu;
+  constexpr uint32_t kFineN = (uint32_t)kSearchParts / 2;  // parts at each end
+  for (uint32_t j = 0; j < (uint32_t)kSearchEntries; ++j) {
+    const bool part = j < (uint32_t)kSearchParts;
+    const uint32_t w = part ? 1u << kSearchFineBits : 256u;
+    const uint32_t lo = part ? (j < kFineN ? j * w : 65536u - kSearchFine * 256u + (j - kFineN) * w)
+                             : (j - (uint32_t)kSearchParts) * 256u;
+    // the symbol containing lo (c[0] = 0 <= lo), the symbol at each value
+    const uint32_t s0 = (uint32_t)(std::upper_bound(c, c + nsym, (int32_t)lo) - c) - 1u;
+    uint32_t sym[256];
+    uint32_t n = 0;
+    for (uint32_t o = 0; o < w; ++o) {
+      while (s0 + n + 1 < nsym && (uint32_t)c[s0 + n + 1] <= lo + o) ++n;
+      sym[o] = pbase + s0 + n;
     }
-    clut[b] = (base + s) | (n << 16) | (h << 24);
+    const uint32_t u0 = lo & 255u, g = pbase + s0;
+    uint32_t entry = g | (n << 24);  // the search entry unless a line fits
+    if (!part) {
+      // c = g + floor(u m / 256): m >= ceil((d - 3) 256 / u), m <= ((d + 1) 256 - 1) / u
+      uint32_t m_lo = 0, m_hi = 255;
+      for (uint32_t o = 1; o < w; ++o) {
+        const uint32_t d = sym[o] - g;
+        if (d > 3u) {
+          const uint32_t need = ((d - 3u) * 256u + o - 1u) / o;
+          m_lo = need > m_lo ? need : m_lo;
+        }
+        const uint32_t cap = ((d + 1u) * 256u - 1u) / o;
+        m_hi = cap < m_hi ? cap : m_hi;
+      }
+      if (m_lo <= m_hi) entry = g | (m_lo << 16);
+    } else {
+      for (uint32_t m = 0; m < 256u; ++m) {
+        int64_t g_lo = (int64_t)pbase - (int64_t)((u0 * m) >> 8), g_hi = INT64_MAX;
+        g_lo = g_lo > 0 ? g_lo : 0;
+        for (uint32_t o = 0; o < w; ++o) {
+          const int64_t r = (int64_t)sym[o] - (int64_t)(((u0 + o) * m) >> 8);
+          g_lo = r - 3 > g_lo ? r - 3 : g_lo;
+          g_hi = r < g_hi ? r : g_hi;
+        }
+        if (g_lo <= g_hi) {
+          entry = (uint32_t)g_hi | (m << 16);
+          break;
+        }
+      }
+    }
+    clut[j] = entry;
   }
 }
 
@@ -363,7 +408,9 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
   uint64_t* blocks = reinterpret_cast<uint64_t*>(o + dense_off);
   uint32_t* clut = reinterpret_cast<uint32_t*>(o + BL.clut_off);
   uint16_t* starts = reinterpret_cast<uint16_t*>(o + BL.starts_off);
-  bool search = total <= kSearchMaxSyms;
+  // the decoder's records carry a table's first segment in 16 bits
+  bool search = total + (int64_t)kStartsTablePad * M <= kSearchMaxSyms &&
+                (int64_t)M * kSearchEntries <= 65536;
   for (int32_t t = 0; t < M; ++t) search &= offsets[t] >= INT32_MIN + 65536;
   uint32_t dblk = 0;
   double bits = 0.0;  // sum over tables of the table's entropy
@@ -395,7 +442,9 @@ int gaans_tables_prepare(const int32_t* cdfs, const int32_t* cdf_sizes, const in
       wblk += (uint32_t)build_wide(c, S, wlut + (int64_t)t * kWideSize,
                                    wblocks + (size_t)wblk * kSubSize, wblk);
     }
-    if (search) build_search(c, nsym, base, clut + (int64_t)t * kLutSize, starts);
+    if (search)
+      build_search(c, nsym, base + (uint32_t)(kStartsTablePad * t),
+                   clut + (int64_t)t * kSearchEntries, starts);
     base += nsym;
   }
   if (wide) wbase[M] = wblk;

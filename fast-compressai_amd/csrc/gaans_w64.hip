@@ -1805,10 +1805,11 @@ __device__ __forceinline__ uint2 dec_record(const DecArgs& a, const Tabs& tb, in
   return r;
 }
 
-// Mapper record with the search lookups (all tables in LDS): x = table |
-// blob-wide index of its escape symbol << 16 (kNoSym past the chunk end),
-// y = offset - the table's first blob-wide symbol, so that the decoded
-// blob-wide index + y is the value.
+// Mapper record with the search lookups (all tables in LDS): x = the table's
+// first segment (table * kSearchEntries, below 2^16 when the blob has the
+// search lookups) | starts index of its escape symbol << 16 (kNoSym past the
+// chunk end), y = offset - the starts index of its symbol 0, so that the
+// decoded starts index + y is the value.
 __device__ __forceinline__ uint2 dec_record_search(const DecArgs& a, const Tabs& tb, int lane,
                                                    int t, int len, int32_t in_b, uint32_t& hash,
                                                    uint32_t& status) {
@@ -1822,8 +1823,9 @@ __device__ __forceinline__ uint2 dec_record_search(const DecArgs& a, const Tabs&
   hash += ok ? index_term((uint32_t)p, (uint32_t)tbi) : 0u;
   const uint4 lm = tb.lmeta[tbi];
   uint2 r;
-  r.x = (uint32_t)tbi | ((act ? lm.x + lm.y - 1u : kNoSym) << 16);
-  r.y = lm.z - lm.x;
+  const uint32_t first = lm.x + (uint32_t)(kStartsTablePad * tbi);  // starts index of symbol 0
+  r.x = (uint32_t)tbi * (uint32_t)kSearchEntries | ((act ? first + lm.y - 1u : kNoSym) << 16);
+  r.y = lm.z - first;
   return r;
 }
 
@@ -1897,51 +1899,75 @@ __device__ __forceinline__ void dec_lookup(const Tabs& tb, uint32_t t, uint32_t 
   if (!kEarly) lut_pick(e, cum, s, st, fr);
 }
 
-// cum -> (symbol, start, freq) with the search lookups, all tables in LDS.
-// The bucket entry gives g, the blob-wide index of the symbol that contains
-// the bucket's first value, n, the symbols that start inside the bucket
-// after it, and h, those of them that start in its first half, so the
-// symbol is among g .. g + h when cum is in the first half and among
-// g + h .. g + n otherwise.  More than three candidates are first narrowed
-// by a 4-way search over their starts (three probe reads per round trip,
-// uniform loop while any lane has more than three left); one read of starts
-// g .. g + 4 then resolves the rest.  s is blob-wide (the record carries
-// offset - base); the freq of a table's last symbol comes from the next
-// start modulo 2^16, which is the next table's first start or a zero
-// sentinel, both 0.
+// cum -> (symbol, start, freq) with the search lookups, all tables in LDS;
+// t is the table's first segment.  The segment of cum is a 32-value part in
+// the table's first or last kSearchFine buckets (entry (cum >> 5) & 63),
+// else its 256-value bucket (entry 64 + (cum >> 8)); both entries are read
+// at once and the segment's kept, which leaves one op and a shift before the
+// read.  A fitted entry's line c = G + (((cum & 255) * m) >> 8) is at most
+// three starts indexes below cum's symbol and never above it, so one read
+// of starts c .. c + 4 resolves it; the starts hold start - 1, and the
+// padding after each table 0xffff, so "start - 1 < cum" counts exactly the
+// candidates at or below cum, with no test of the table's end.  A segment
+// no line fits (bits 24-31: n > 3 symbols after its first) has all n + 1
+// candidates from G: more than three are first narrowed by a 4-way search
+// over their starts (three probe reads per round trip, uniform loop while
+// any lane has more than three left).  s is the starts index (the record
+// carries offset - the table's first index).
 __device__ __forceinline__ void dec_lookup_search(const Tabs& tb, uint32_t t, uint32_t cum,
                                                   bool act, uint32_t& s, uint32_t& st,
                                                   uint32_t& fr) {
-  const uint32_t e = tb.lclut[(t << kLutBits) + (cum >> (16 - kLutBits))];
-  const uint32_t n0 = (e >> 16) & 0xffu, h = e >> 24;
-  const bool upper = (cum & (1u << (15 - kLutBits))) != 0u;
-  // invariant: start(g) <= cum, and the symbol is among g .. g + n
-  uint32_t g = (e & 0xffffu) + (upper ? h : 0u);
-  uint32_t n = upper ? n0 - h : h;
-  bool wide = act & (n > 3u);
+  static_assert(kSearchFine == 4 && kSearchFineBits == 5 && kSearchParts == 64,
+                "segment arithmetic below");
+  uint32_t eb = tb.lclut[t + kSearchParts + (cum >> 8)];
+  uint32_t ep = tb.lclut[t + ((cum >> 5) & 63u)];
+  asm("" : "+v"(eb), "+v"(ep));  // two reads, not one of a selected address
+  const bool fine = ((cum + 1024u) & 0xffffu) < 2048u;  // cum < 1024 or cum >= 64512
+  const uint32_t e = fine ? ep : eb;
+  // y = (c << 8) + a fraction: c = y >> 8, the word holding start c y >> 9
+  const uint32_t y = __umul24(cum & 0xffu, (e >> 16) & 0xffu) + ((e & 0xffffu) << 8);
+  uint32_t g = y >> 8;
+  const uint32_t* pw = reinterpret_cast<const uint32_t*>(tb.lstarts) + (y >> 9);
+  uint32_t w0 = pw[0], w1 = pw[1], w2 = pw[2];
+  asm("" : "+v"(w0), "+v"(w1), "+v"(w2));
+  uint32_t nl = e >> 24;  // candidates after g: 0 for a fitted segment
+  bool wide = act & (nl > 3u);
   if (__builtin_expect(ballot(wide) != 0ull, 0)) {
-    // the probes q, 2q, 3q (q = (n + 1) / 4 >= 1) split it into four ranges
+    // the probes q, 2q, 3q (q = (nl + 1) / 4 >= 1) split it into four ranges
     do {
       if (wide) {
-        const uint32_t q = (n + 1u) >> 2;
-        const bool l1 = tb.lstarts[g + q] <= cum, l2 = tb.lstarts[g + 2u * q] <= cum,
-                   l3 = tb.lstarts[g + 3u * q] <= cum;
-        const uint32_t k = (uint32_t)l1 + (uint32_t)l2 + (uint32_t)l3;
-        g += k * q;
-        n = l3 ? n - 3u * q : q - 1u;
+        const uint32_t q = (nl + 1u) >> 2;
+        const bool l1 = tb.lstarts[g + q] < cum, l2 = tb.lstarts[g + 2u * q] < cum,
+                   l3 = tb.lstarts[g + 3u * q] < cum;
+        const uint32_t kk = (uint32_t)l1 + (uint32_t)l2 + (uint32_t)l3;
+        g += kk * q;
+        nl = l3 ? nl - 3u * q : q - 1u;
       }
-      wide = act & (n > 3u);
+      wide = act & (nl > 3u);
     } while (ballot(wide) != 0ull);
+    const uint32_t* pg = reinterpret_cast<const uint32_t*>(tb.lstarts) + (g >> 1);
+    w0 = pg[0];
+    w1 = pg[1];
+    w2 = pg[2];
   }
-  const uint16_t* p = tb.lstarts + g;
-  const uint32_t v0 = p[0], v1 = p[1], v2 = p[2], v3 = p[3], v4 = p[4];
-  const bool b1 = (n >= 1u) & (v1 <= cum), b2 = (n >= 2u) & (v2 <= cum),
-             b3 = (n >= 3u) & (v3 <= cum);
-  const uint32_t k = (uint32_t)b1 + (uint32_t)b2 + (uint32_t)b3;
-  s = g + k;
-  st = b3 ? v3 : (b2 ? v2 : (b1 ? v1 : v0));
-  const uint32_t nx = b3 ? v4 : (b2 ? v3 : (b1 ? v2 : v1));
-  fr = ((nx - st - 1u) & 0xffffu) + 1u;
+  // starts g .. g + 4 from the three aligned words that hold them (a b64
+  // read at a 2-byte address costs about 55 cycles more than aligned reads)
+  const uint32_t sb = (g & 1u) << 1;  // byte shift of start g in w0
+  const uint32_t a01 = __builtin_amdgcn_alignbyte(w1, w0, sb),
+                 a23 = __builtin_amdgcn_alignbyte(w2, w1, sb);
+  const uint32_t v0 = a01 & 0xffffu, v1 = a01 >> 16, v2 = a23 & 0xffffu, v3 = a23 >> 16;
+  uint32_t v4 = (w2 >> (sb << 3)) & 0xffffu;
+  asm volatile("" : "+v"(v4));  // computed for every lane: selects below, not a branch
+  // candidates past the symbol (or the table) hold larger starts or 0xffff
+  const bool b1 = v1 < cum, b2 = v2 < cum, b3 = v3 < cum;
+  const uint32_t kk = (uint32_t)b1 + (uint32_t)b2 + (uint32_t)b3;
+  s = g + kk;
+  const uint32_t sm = b3 ? v3 : (b2 ? v2 : (b1 ? v1 : v0));  // start - 1
+  const uint32_t nx = b3 ? v4 : (b2 ? v3 : (b1 ? v2 : v1));   // next start - 1
+  // freq: the next start - start mod 2^16 (2^16 for a one-symbol table), and
+  // start mod 2^16 (a table's first symbol holds 0xffff)
+  fr = ((nx - sm - 1u) & 0xffffu) + 1u;
+  st = (sm + 1u) & 0xffffu;
 }
 
 // Stage every table's search lookups, starts and metadata (whole workgroup
@@ -1955,7 +1981,7 @@ __device__ void stage_search(Tabs& T, uint4* lmeta, uint32_t* lclut, uint16_t* l
   T.sub_first = 0;
   T.sub_n = 0;
   copy16_dma<NT>(reinterpret_cast<uint4*>(lclut),
-                 reinterpret_cast<const uint4*>(tables + blob.clut_off), M * (kLutSize / 4), tid);
+                 reinterpret_cast<const uint4*>(tables + blob.clut_off), M * (kSearchEntries / 4), tid);
   copy16_dma<NT>(reinterpret_cast<uint4*>(lstarts),
                  reinterpret_cast<const uint4*>(tables + blob.starts_off), starts_words, tid);
   stage_pass<NT, false, false>(T, lmeta, nullptr, nullptr, nullptr, M, 1u, 0u, 0u, 0, tid);
@@ -1989,8 +2015,8 @@ __device__ __forceinline__ EarlyStage stage_early(const Tabs& T, uint64_t* llut,
   if (e.nt > 0) {
     if constexpr (kSearch) {
       copy16_dma<NT>(reinterpret_cast<uint4*>(lclut),
-                     reinterpret_cast<const uint4*>(tables + blob.clut_off), M * (kLutSize / 4),
-                     tid);
+                     reinterpret_cast<const uint4*>(tables + blob.clut_off),
+                     M * (kSearchEntries / 4), tid);
       copy16_dma<NT>(reinterpret_cast<uint4*>(lstarts),
                      reinterpret_cast<const uint4*>(tables + blob.starts_off), starts_words, tid);
     } else {
@@ -2295,7 +2321,8 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
   // [meta][starts]: every part 16-byte aligned
   static_assert(!(kSearch && kWide), "the search lookups have no wide form");
   constexpr int kLutEntry = kSearch ? 4 : 8;
-  constexpr int kLB = kWide ? kWideSize : kLutSize;  // lookup entries per staged table
+  // lookup entries per staged table
+  constexpr int kLB = kSearch ? kSearchEntries : (kWide ? kWideSize : kLutSize);
   uint64_t* llut = reinterpret_cast<uint64_t*>(tsm);
   uint32_t* lclut = reinterpret_cast<uint32_t*>(tsm);
   uint4* lmeta = reinterpret_cast<uint4*>(tsm + kLutEntry * kLB * a.nt_cap);
@@ -2441,14 +2468,16 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
         if (SB % kMappers != 0 && u >= SB) break;
         const uint2 r = src[u * kLanes + lane];
         // the coder's value: in x, or with the search lookups in y (x keeps
-        // the table, whose offset the escape mapping needs)
+        // the table's first segment, whose table's offset the escape mapping
+        // needs)
         uint32_t v = kSearch ? r.y : r.x;
         if (any_esc && j * SB + u < T) {
           const uint4 ei = escm[(j & 1) * SB + u];  // escaping lanes, first entry
           const uint64_t em = (uint64_t)(uint32_t)uni((int)ei.x) |
                               ((uint64_t)(uint32_t)uni((int)ei.y) << 32);
           if (em) {
-            const uint32_t off = kSearch ? tb.lmeta[r.x & 0xffffu].z : r.y;
+            const uint32_t off =
+                kSearch ? tb.lmeta[(r.x & 0xffffu) / (uint32_t)kSearchEntries].z : r.y;
             esc_resolve<R>(em, (uint32_t)uni((int)ei.z), off, v, avail, fifo, enib, status, lane);
           }
         }
@@ -3195,9 +3224,9 @@ struct DecPlan {
 // Search lookups in LDS: every table's bucket entries and metadata, and
 // every symbol's start (with the zero padding).
 int64_t search_lds(const gaans_tables* t, uint32_t* starts_words) {
-  const int64_t sb = align_up(2 * (t->total_nsym + kStartsPad), 16);
+  const int64_t sb = align_up(2 * search_starts(t->M, t->total_nsym), 16);
   *starts_words = (uint32_t)(sb / 16);
-  return (int64_t)t->M * (4 * kLutSize + 16) + sb;
+  return (int64_t)t->M * (4 * kSearchEntries + 16) + sb;
 }
 
 DecPlan plan_decode(const gaans_tables* t, int64_t P, int64_t units, bool latents,

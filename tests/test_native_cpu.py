@@ -271,61 +271,78 @@ def test_prepared_tables_dense_tail_lookup():
     assert levels.get(2, 0) > 0 and levels.get(3, 0) > 0
 
 
-def host_search(blob, t, cum, counts=None):
-    """The decoder's search lookup, read from the prepared blob: bucket entry
-    (blob-wide symbol g containing the bucket's first value | starts n inside
-    the bucket after it << 16 | those h of them in its first half << 24); the
-    half that holds cum narrows the candidates to g .. g + h or g + h ..
-    g + n; while more than three remain, split them four ways with three
-    start reads; then starts g .. g + 4 resolve the rest; freq from the next
-    start modulo 2^16 (the next table's first start, or the zero sentinel,
-    is 0).  counts[rounds] tallies the 4-way rounds."""
+SEARCH_ENTRIES = 320  # segments per table: 64 parts of 32 values, then the 256 buckets
+
+
+def host_search(blob, t):
+    """The decoder's search lookup of every cum value of table t, read from
+    the prepared blob.  Starts: start - 1 mod 2^16 of every symbol, each
+    table followed by three 0xFFFF, so table t's symbol v is at starts index
+    ent_base + 3 t + v.  Segment of cum: a 32-value part when cum < 1024 or
+    cum >= 64512 (entry (cum >> 5) & 63), else its 256-value bucket (entry
+    64 + (cum >> 8)).  Entry: G | m << 16 | n << 24.  n = 0: c = G + (((cum
+    & 255) * m) >> 8); n > 0: c = G, and n + 1 candidates are narrowed four
+    ways (three start reads a round) while more than three remain.  Then
+    "start - 1 < cum" over starts c + 1 .. c + 3 counts the symbol's offset
+    from c; freq from the next start mod 2^16 (2^16 for a one-symbol table).
+    Returns the table's symbol, start and freq per cum and the 4-way rounds
+    per cum."""
     hdr = struct.unpack_from("<16I", blob, 0)
-    clut_off, starts_off = hdr[14], hdr[15]
-    ent_base = struct.unpack_from("<I", blob, hdr[6] + 16 * t)[0]
-    e = struct.unpack_from("<I", blob, clut_off + 4 * (256 * t + (cum >> 8)))[0]
-    n0, h = (e >> 16) & 0xFF, e >> 24
-    assert h <= n0
-    g, n = ((e & 0xFFFF) + h, n0 - h) if cum & 128 else (e & 0xFFFF, h)
-    rounds = 0
-    while n > 3:  # 4-way: probes q, 2q, 3q
-        q = (n + 1) >> 2
-        le = [struct.unpack_from("<H", blob, starts_off + 2 * (g + j * q))[0] <= cum
-              for j in (1, 2, 3)]
-        g += sum(le) * q
-        n = n - 3 * q if le[2] else q - 1
-        rounds += 1
-    v = struct.unpack_from("<5H", blob, starts_off + 2 * g)
-    k = sum(1 for j in (1, 2, 3) if n >= j and v[j] <= cum)
-    if counts is not None:
-        counts[rounds] = counts.get(rounds, 0) + 1
-    st, nx = v[k], v[k + 1]
-    return g + k - ent_base, st, ((nx - st - 1) & 0xFFFF) + 1
+    M, clut_off, starts_off = hdr[1], hdr[14], hdr[15]
+    first = struct.unpack_from("<I", blob, hdr[6] + 16 * t)[0] + 3 * t
+    clut = np.frombuffer(blob, "<u4", SEARCH_ENTRIES * M, clut_off).astype(np.int64)
+    starts = np.frombuffer(blob, "<u2", hdr[2] + 3 * M + 8, starts_off).astype(np.int64)
+    cum = np.arange(65536, dtype=np.int64)
+    fine = ((cum + 1024) & 0xFFFF) < 2048
+    e = clut[SEARCH_ENTRIES * t + np.where(fine, (cum >> 5) & 63, 64 + (cum >> 8))]
+    m, nl = (e >> 16) & 0xFF, e >> 24
+    g = (((e & 0xFFFF) << 8) + (cum & 0xFF) * m) >> 8
+    rounds = np.zeros(65536, np.int64)
+    while (nl > 3).any():  # 4-way: probes q, 2q, 3q
+        w = nl > 3
+        q = (nl + 1) >> 2
+        le = [np.where(w, starts[np.where(w, g + j * q, 0)] < cum, False) for j in (1, 2, 3)]
+        g = g + np.where(w, (le[0].astype(np.int64) + le[1] + le[2]) * q, 0)
+        nl = np.where(w, np.where(le[2], nl - 3 * q, q - 1), nl)
+        rounds += w
+    v = starts[g[:, None] + np.arange(5)]
+    kk = (v[:, 1] < cum).astype(np.int64) + (v[:, 2] < cum) + (v[:, 3] < cum)
+    sm = v[np.arange(65536), kk]
+    nx = v[np.arange(65536), kk + 1]
+    return g + kk - first, (sm + 1) & 0xFFFF, ((nx - sm - 1) & 0xFFFF) + 1, rounds
 
 
 def test_search_lookups_exhaustive():
     # the 64 GaussianConditional-style tables of the hyperprior workload
-    # (3 .. 3,133 symbols, long freq-1 tails) and a one-symbol table
+    # (3 .. 3,133 symbols, long freq-1 tails), a one-symbol table, and a
+    # table that no slope fits (a wide symbol, then 300 freq-1 symbols in a
+    # 256-value bucket), every cum value of every table
     yw, _, _, _ = synthetic.hyperprior_512x768()
-    cdfs = np.zeros((65, yw.cdfs.shape[1]), np.int32)
+    cdfs = np.zeros((66, yw.cdfs.shape[1]), np.int32)
     cdfs[:64] = yw.cdfs
     cdfs[64, :2] = [0, 65536]
-    sizes = np.concatenate([yw.cdf_sizes, [2]]).astype(np.int32)
-    offs = np.concatenate([yw.offsets, [-7]]).astype(np.int32)
+    odd = np.concatenate([[0], 40000 + np.arange(300), [65536]])
+    cdfs[65, : len(odd)] = odd
+    sizes = np.concatenate([yw.cdf_sizes, [2, len(odd)]]).astype(np.int32)
+    offs = np.concatenate([yw.offsets, [-7, 3]]).astype(np.int32)
     rc, blob, _ = prepare_host(cdfs, sizes, offs)
     assert rc == 0
     blob = blob.tobytes()
     hdr = struct.unpack_from("<16I", blob, 0)
     assert hdr[13] & 2  # search lookups present
-    counts = {}
-    for t in (0, 5, 20, 40, 55, 62, 63, 64):
+    assert hdr[15] - hdr[14] == 4 * SEARCH_ENTRIES * 66
+    rounds_seen = np.zeros(8, np.int64)
+    for t in range(66):
         c = cdfs[t, : sizes[t]]
         want = np.searchsorted(c, np.arange(65536), side="right") - 1
-        step = 1 if t in (63, 64) else 5
-        for cum in range(0, 65536, step):
-            v, start, freq = host_search(blob, t, cum, counts)
-            assert v == want[cum] and start == c[v] and freq == c[v + 1] - c[v], (t, cum)
-    assert counts.get(0, 0) > 0 and counts.get(1, 0) > 0 and max(counts) >= 3
+        v, start, freq, rounds = host_search(blob, t)
+        bad = np.flatnonzero((v != want) | (start != c[want]) | (freq != c[want + 1] - c[want]))
+        assert bad.size == 0, (t, bad[:5])
+        rounds_seen += np.bincount(rounds, minlength=8)[:8]
+    # the slopes resolve nearly every value in one read; the unfitted
+    # segments (tails of the Gaussian tables, the odd table) search
+    assert rounds_seen[0] > 0.98 * rounds_seen.sum()
+    assert rounds_seen[1:].sum() > 0 and rounds_seen[3:].sum() > 0
 
 
 def test_search_lookups_absent_when_not_addressable():
