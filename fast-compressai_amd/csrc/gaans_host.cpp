@@ -126,15 +126,15 @@ int64_t tables_size(int32_t M, int64_t total_syms, int64_t total_blocks, int64_t
 // holds for the symbols that start at or below cum and for no padding; and
 // one u32 per segment of the cum range (kSearchEntries: 32-value parts of
 // the first and the last kSearchFine buckets, then every 256-value bucket).
-// With u = cum & 255, a fitted segment's entry G (bits 0-15), m (bits
-// 16-23), 0 (bits 24-31) puts c = G + ((u * m) >> 8) at most three starts
+// With u = cum & 255, a fitted segment's entry m (bits 0-7), 0 (bits 8-15),
+// G (bits 16-31) puts c = G + ((u * m) >> 8) at most three starts
 // indexes below the symbol that contains cum and never above it, and never
 // below the table's first symbol, so one read of starts c .. c + 4 resolves
 // it.  A bucket's line starts at its first value's symbol g (G = g, the
 // smallest m that meets both bounds); a part's may start anywhere (the first
 // m, in increasing order, for which some G >= 0 meets them; G is then the
 // largest).  A segment that no line fits gets G = g, m = 0 and in bits
-// 24-31 n, the symbols that start inside it after g (4 to 255: m = 0 fits
+// 8-15 n, the symbols that start inside it after g (4 to 255: m = 0 fits
 // the segments with n <= 3); its lookup searches g .. g + n.
 void build_search(const int32_t* c, uint32_t nsym, uint32_t pbase, uint32_t* clut,
                   uint16_t* starts) {
@@ -155,7 +155,7 @@ void build_search(const int32_t* c, uint32_t nsym, uint32_t pbase, uint32_t* clu
       sym[o] = pbase + s0 + n;
     }
     const uint32_t u0 = lo & 255u, g = pbase + s0;
-    uint32_t entry = g | (n << 24);  // the search entry unless a line fits
+    uint32_t entry = (g << 16) | (n << 8);  // the search entry unless a line fits
     if (!part) {
       // c = g + floor(u m / 256): m >= ceil((d - 3) 256 / u), m <= ((d + 1) 256 - 1) / u
       uint32_t m_lo = 0, m_hi = 255;
@@ -168,7 +168,7 @@ void build_search(const int32_t* c, uint32_t nsym, uint32_t pbase, uint32_t* clu
         const uint32_t cap = ((d + 1u) * 256u - 1u) / o;
         m_hi = cap < m_hi ? cap : m_hi;
       }
-      if (m_lo <= m_hi) entry = g | (m_lo << 16);
+      if (m_lo <= m_hi) entry = (g << 16) | m_lo;
     } else {
       for (uint32_t m = 0; m < 256u; ++m) {
         int64_t g_lo = (int64_t)pbase - (int64_t)((u0 * m) >> 8), g_hi = INT64_MAX;
@@ -179,7 +179,7 @@ void build_search(const int32_t* c, uint32_t nsym, uint32_t pbase, uint32_t* clu
           g_hi = r < g_hi ? r : g_hi;
         }
         if (g_lo <= g_hi) {
-          entry = (uint32_t)g_hi | (m << 16);
+          entry = ((uint32_t)g_hi << 16) | m;
           break;
         }
       }

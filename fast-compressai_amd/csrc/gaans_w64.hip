@@ -1904,12 +1904,13 @@ __device__ __forceinline__ void dec_lookup(const Tabs& tb, uint32_t t, uint32_t 
 // the table's first or last kSearchFine buckets (entry (cum >> 5) & 63),
 // else its 256-value bucket (entry 64 + (cum >> 8)); both entries are read
 // at once and the segment's kept, which leaves one op and a shift before the
-// read.  A fitted entry's line c = G + (((cum & 255) * m) >> 8) is at most
+// read.  A fitted entry's (m | 0 << 8 | G << 16) line c = G + (((cum & 255)
+// * m) >> 8) is at most
 // three starts indexes below cum's symbol and never above it, so one read
 // of starts c .. c + 4 resolves it; the starts hold start - 1, and the
 // padding after each table 0xffff, so "start - 1 < cum" counts exactly the
 // candidates at or below cum, with no test of the table's end.  A segment
-// no line fits (bits 24-31: n > 3 symbols after its first) has all n + 1
+// no line fits (bits 8-15: n > 3 symbols after its first) has all n + 1
 // candidates from G: more than three are first narrowed by a 4-way search
 // over their starts (three probe reads per round trip, uniform loop while
 // any lane has more than three left).  s is the starts index (the record
@@ -1923,15 +1924,14 @@ __device__ __forceinline__ void dec_lookup_search(const Tabs& tb, uint32_t t, ui
   uint32_t ep = tb.lclut[t + ((cum >> 5) & 63u)];
   asm("" : "+v"(eb), "+v"(ep));  // two reads, not one of a selected address
   const bool fine = ((cum + 1024u) & 0xffffu) < 2048u;  // cum < 1024 or cum >= 64512
-  const uint32_t e = fine ? ep : eb;
-  // y = (c << 8) + a fraction: c = y >> 8, the word holding start c y >> 9
-  const uint32_t y = __umul24(cum & 0xffu, (e >> 16) & 0xffu) + ((e & 0xffffu) << 8);
-  uint32_t g = y >> 8;
-  const uint32_t* pw = reinterpret_cast<const uint32_t*>(tb.lstarts) + (y >> 9);
+  const uint32_t e = fine ? ep : eb;  // m | n << 8 | G << 16
+  uint32_t g = (e >> 16) + (__umul24(cum & 0xffu, e & 0xffu) >> 8);
+  // the words holding starts g .. g + 4 (below), read before the search test
+  const uint32_t* pw = reinterpret_cast<const uint32_t*>(tb.lstarts) + (g >> 1);
   uint32_t w0 = pw[0], w1 = pw[1], w2 = pw[2];
   asm("" : "+v"(w0), "+v"(w1), "+v"(w2));
-  uint32_t nl = e >> 24;  // candidates after g: 0 for a fitted segment
-  bool wide = act & (nl > 3u);
+  uint32_t nl = (e >> 8) & 0xffu;  // candidates after g: 0 for a fitted segment
+  bool wide = act & ((e & 0xffffu) > 0x3ffu);  // nl > 3
   if (__builtin_expect(ballot(wide) != 0ull, 0)) {
     // the probes q, 2q, 3q (q = (nl + 1) / 4 >= 1) split it into four ranges
     do {
@@ -2327,7 +2327,11 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
   uint32_t* lclut = reinterpret_cast<uint32_t*>(tsm);
   uint4* lmeta = reinterpret_cast<uint4*>(tsm + kLutEntry * kLB * a.nt_cap);
   uint64_t* lsub = reinterpret_cast<uint64_t*>(tsm + (kLutEntry * kLB + 16) * a.nt_cap);
-  uint16_t* lstarts = reinterpret_cast<uint16_t*>(lsub);
+  // the starts' LDS offset in one scalar register (the compiler would split
+  // it into a register and a constant, one add more per lookup)
+  int starts_off = G::fixed(kLatents) + (kLutEntry * kLB + 16) * a.nt_cap;
+  asm("" : "+s"(starts_off));
+  uint16_t* lstarts = reinterpret_cast<uint16_t*>(smem + starts_off);
   float* scl = reinterpret_cast<float*>(smem + a.scales_lds);  // Gaussian: scale table
 
   const int64_t g = blockIdx.x;

@@ -280,7 +280,7 @@ def host_search(blob, t):
     table followed by three 0xFFFF, so table t's symbol v is at starts index
     ent_base + 3 t + v.  Segment of cum: a 32-value part when cum < 1024 or
     cum >= 64512 (entry (cum >> 5) & 63), else its 256-value bucket (entry
-    64 + (cum >> 8)).  Entry: G | m << 16 | n << 24.  n = 0: c = G + (((cum
+    64 + (cum >> 8)).  Entry: m | n << 8 | G << 16.  n = 0: c = G + (((cum
     & 255) * m) >> 8); n > 0: c = G, and n + 1 candidates are narrowed four
     ways (three start reads a round) while more than three remain.  Then
     "start - 1 < cum" over starts c + 1 .. c + 3 counts the symbol's offset
@@ -295,8 +295,8 @@ def host_search(blob, t):
     cum = np.arange(65536, dtype=np.int64)
     fine = ((cum + 1024) & 0xFFFF) < 2048
     e = clut[SEARCH_ENTRIES * t + np.where(fine, (cum >> 5) & 63, 64 + (cum >> 8))]
-    m, nl = (e >> 16) & 0xFF, e >> 24
-    g = (((e & 0xFFFF) << 8) + (cum & 0xFF) * m) >> 8
+    m, nl = e & 0xFF, (e >> 8) & 0xFF
+    g = (e >> 16) + (((cum & 0xFF) * m) >> 8)
     rounds = np.zeros(65536, np.int64)
     while (nl > 3).any():  # 4-way: probes q, 2q, 3q
         w = nl > 3
