@@ -2651,10 +2651,9 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
             else src[u * kLanes + lane].x = v;
           }
         }
-        if (lane == 0) {
-          ctl[4 + (j & 1)] = any_em != 0ull ? 1u : 0u;
-          ctl[6 + ((j + 1) & 1)] = ecur;
-        }
+        // every lane writes the same (uniform) values: no exec-mask branch
+        ctl[4 + (j & 1)] = any_em != 0ull ? 1u : 0u;
+        ctl[6 + ((j + 1) & 1)] = ecur;
         pc.bar_in();
         __syncthreads();
         pc.bar_out();
