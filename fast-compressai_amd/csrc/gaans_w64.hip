@@ -924,12 +924,12 @@ __device__ __forceinline__ uint32_t enc_apply(uint32_t x, uint4 r) {
 // Escapes of one step into the unit's escape list: slots are taken from the
 // end of the list, highest lane first, so that the list, read forwards, is in
 // position order (the coder walks the steps last to first).
-__device__ __forceinline__ void enc_escapes(const uint4 r, uint32_t* __restrict__ list,
+__device__ __forceinline__ void enc_escapes(uint32_t z, uint32_t raw, uint32_t* __restrict__ list,
                                             int& cnt, int lane) {
-  const bool esc = (r.z & 256u) != 0u;
+  const bool esc = (z & 256u) != 0u;
   const uint64_t em = ballot(esc);
   const int above = __popcll(lane < 63 ? em >> (lane + 1) : 0ull);
-  if (esc) list[-1 - (cnt + above)] = r.w;
+  if (esc) list[-1 - (cnt + above)] = raw;
   cnt = uni(cnt + __popcll(em));
 }
 
@@ -1245,6 +1245,14 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
   constexpr int kEncMappers = NM;
   constexpr int kWaves = G::kWaves, kThreads = G::kThreads;
   constexpr int kPer = G::kPer;
+  // Who lists the escapes: with eight mappers (a CU to each workgroup) the
+  // first mapper wave, off the coder's chain (2160x3840 latent encode 95 ->
+  // 89 us, hyperprior y 45 -> 44 us at P=16); else the coder, since with
+  // four mappers and several workgroups per CU the mappers have no time to
+  // spare (batch-64 uniform 67 -> 72 us with the listing moved), and the
+  // latents' mappers, which quantize, neither (512x768 latent 17.7 -> 18.1
+  // us).
+  constexpr bool kMList = NM == 8 && kMode != kModeLatents;
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t* ring = reinterpret_cast<uint16_t*>(smem);
   const uint32_t ring_mask = a.ring_mask;  // ring words - 1
@@ -1317,7 +1325,7 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
   int fl = a.cap_words;  // coder: words at [fl, cap) are already in wbuf
   uint32_t x = kStateLow;
   uint32_t hash = 0, status = 0, znib = 0;
-  int n_esc = 0;  // coder: escapes listed so far
+  int n_esc = 0;  // escapes listed so far (by the coder, or the first mapper wave)
   uint32_t* __restrict__ esc_list = a.esc_raw + g * a.seg_cap + a.seg_cap;
 
   if (tid < 2) eflag[tid] = 0u;  // visible after the staging barrier
@@ -1481,9 +1489,10 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
           fl = wp;
         }
         const uint4* src = recs + (j & 1) * SB * kLanes;
-        // steps of the block with escapes; cleared for block j - 2
-        const uint32_t any_esc = (uint32_t)uni((int)eflag[j & 1]);
-        if (lane == 0) eflag[j & 1] = 0u;
+        // steps of the block with escapes when the coder lists them; cleared
+        // for block j - 2
+        const uint32_t any_esc = kMList ? 0u : (uint32_t)uni((int)eflag[j & 1]);
+        if (!kMList && lane == 0) eflag[j & 1] = 0u;
         const bool full = (j + 1) * SB <= T;
         // the block's records in groups of at most 8 steps, last group first
         constexpr int H = SB > 8 ? 8 : SB;
@@ -1512,7 +1521,7 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
           if (__builtin_expect(any_esc != 0, 0)) {
 #pragma unroll
             for (int k = H - 1; k >= 0; --k)
-              if (any_esc & (1u << (h * H + k))) enc_escapes(r[k], esc_list, n_esc, lane);
+              if (any_esc & (1u << (h * H + k))) enc_escapes(r[k].z, r[k].w, esc_list, n_esc, lane);
           }
         }
         pc.bar_in();
@@ -1525,6 +1534,35 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
       if (nblk > 0) map_block(nblk - 1);
       __syncthreads();
       for (int j = nblk - 1; j >= 0; --j) {
+        // kMList: the first mapper wave lists the escapes of block j (their
+        // bins are coded by the coder meanwhile) from the block's records,
+        // last step first, so the list stays in position order, eight steps'
+        // escape words read at a time (one wait for each group).  The steps'
+        // flags are cleared for block j - 2, which is mapped after the next
+        // barrier.
+        if (kMList && wid == 1) {
+          const uint32_t any_esc = (uint32_t)uni((int)eflag[j & 1]);
+          eflag[j & 1] = 0u;
+          if (any_esc != 0u) {
+            const uint4* src = recs + (j & 1) * SB * kLanes;
+            constexpr int G8 = SB > 8 ? 8 : SB;
+#pragma unroll
+            for (int hh = SB / G8 - 1; hh >= 0; --hh) {
+              const uint32_t gb = (any_esc >> (hh * G8)) & ((1u << G8) - 1u);
+              if (gb == 0u) continue;
+              uint32_t z[G8], w[G8];
+#pragma unroll
+              for (int k = 0; k < G8; ++k) {
+                const uint4 rr = src[(hh * G8 + k) * kLanes + lane];
+                z[k] = rr.z;
+                w[k] = rr.w;
+              }
+#pragma unroll
+              for (int k = G8 - 1; k >= 0; --k)
+                if (gb & (1u << k)) enc_escapes(z[k], w[k], esc_list, n_esc, lane);
+            }
+          }
+        }
         if (j > 0) {  // mappers: block j - 1 while the coder codes block j
 #pragma unroll
           for (int e = 0; e < kPer; ++e) {
@@ -1547,17 +1585,17 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
     part[wid] = hash;
     part[kWaves + wid] = status;
     part[2 * kWaves + wid] = znib;
+    if (wid == (kMList ? 1 : 0)) part[3 * kWaves] = (uint32_t)n_esc;
     if (wid == 0) {
-      part[3 * kWaves] = (uint32_t)n_esc;
       part[3 * kWaves + 1] = (uint32_t)(a.cap_words - wp);
       part[kPartWp] = (uint32_t)wp;
       part[kPartFl] = (uint32_t)fl;
     }
   }
   if (fused) {
-    // the coder's ring flushes and escape list are in memory before the
-    // other waves read them back
-    if (wid == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // the coder's ring flushes and the escape list (the coder's or the first
+    // mapper's) are in memory before the other waves read them back
+    if (wid <= 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     // the tables' LDS (and the scale table's) is free now: the flushed words
     // are staged there
@@ -1576,8 +1614,9 @@ __global__ __launch_bounds__((NM + 1) * kLanes) void k_encode(EncArgs a) {
     if (fl > wp) ring_flush(wbuf, ring, wp, fl, lane, ring_mask);
     if (lane < A) a.states[g * kLanes + lane] = x;
   }
-  // The unit's counts are published by the first mapper wave, which has no
-  // stores in flight.  What the last workgroup reads (maybe on another XCD,
+  // The unit's counts are published by the first mapper wave (its escape
+  // list stores, if any, complete before the counter too: the wait below
+  // covers them; the pack kernel reads the list).  What the last workgroup reads (maybe on another XCD,
   // behind another L2) is stored with agent-scope atomics, coherent across
   // the device, and has completed before the counter is raised: no fence, so
   // no write-back of the XCD's whole L2.
