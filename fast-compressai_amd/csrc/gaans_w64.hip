@@ -2148,9 +2148,12 @@ __device__ __forceinline__ void stream_block_start(Stream& S, uint32_t* ring32, 
   using G = DecGeom<SB>;
   const bool commit = S.filled - S.rp < G::kLowWater && S.filled < S.q;
   if (commit) {
+    // a batch starts at a multiple of its size in the ring, which holds a
+    // whole number of batches: it never wraps, one mask for all its words
+    static_assert((G::kRing / 2) % (G::kPfWords / 2) == 0, "ring of whole batches");
+    uint32_t* dst = ring32 + (((uint32_t)S.filled >> 1) & (G::kRing / 2 - 1)) + lane;
 #pragma unroll
-    for (int kk = 0; kk < G::kPfU32; ++kk)
-      ring32[((S.filled >> 1) + kk * kLanes + lane) & (G::kRing / 2 - 1)] = S.pf[kk];
+    for (int kk = 0; kk < G::kPfU32; ++kk) dst[kk * kLanes] = S.pf[kk];
     S.filled = uni(S.filled + G::kPfWords);
     stream_batch32<G::kPfU32>(S, S.filled >> 1, S.pf);
   }
@@ -2637,7 +2640,7 @@ __global__ __launch_bounds__(kDecThreads, kDecWavesPerSimd) void k_decode(DecArg
         // steps whose tables are not all in LDS; cleared for block j + 2 (the
         // search lookups stage every table: no read, no wait)
         const uint32_t nl = kSearch ? 0u : (uint32_t)uni((int)ctl[2 + (j & 1)]);
-        if (!kSearch && lane == 0) ctl[2 + (j & 1)] = 0u;
+        if (!kSearch) ctl[2 + (j & 1)] = 0u;  // every lane: no exec-mask branch
         // after the block's LDS reads: the compiler makes the first LDS read
         // after the prefetch loads wait for them, so they are issued after
         // the records are read and return during the block's steps
