@@ -1962,7 +1962,7 @@ __device__ __forceinline__ void dec_lookup_search(const Tabs& tb, uint32_t t, ui
   uint32_t eb = tb.lclut[t + kSearchParts + (cum >> 8)];
   uint32_t ep = tb.lclut[t + ((cum >> 5) & 63u)];
   asm("" : "+v"(eb), "+v"(ep));  // two reads, not one of a selected address
-  const bool fine = ((cum + 1024u) & 0xffffu) < 2048u;  // cum < 1024 or cum >= 64512
+  const bool fine = (uint16_t)(cum + 1024u) < 2048u;  // cum < 1024 or cum >= 64512
   const uint32_t e = fine ? ep : eb;  // m | n << 8 | G << 16
   uint32_t g = (e >> 16) + (__umul24(cum & 0xffu, e & 0xffu) >> 8);
   // the words holding starts g .. g + 4 (below), read before the search test
@@ -1991,11 +1991,13 @@ __device__ __forceinline__ void dec_lookup_search(const Tabs& tb, uint32_t t, ui
   }
   // starts g .. g + 4 from the three aligned words that hold them (a b64
   // read at a 2-byte address costs about 55 cycles more than aligned reads)
-  const uint32_t sb = (g & 1u) << 1;  // byte shift of start g in w0
-  const uint32_t a01 = __builtin_amdgcn_alignbyte(w1, w0, sb),
-                 a23 = __builtin_amdgcn_alignbyte(w2, w1, sb);
+  // start g's byte shift in w0 is 2 (g & 1): v_alignbyte_b32 reads the low
+  // two bits of its shift operand and v_bfe_u32 the low five of its offset,
+  // so g << 1 and g << 4 serve as they are (no mask)
+  const uint32_t a01 = __builtin_amdgcn_alignbyte(w1, w0, g << 1),
+                 a23 = __builtin_amdgcn_alignbyte(w2, w1, g << 1);
   const uint32_t v0 = a01 & 0xffffu, v1 = a01 >> 16, v2 = a23 & 0xffffu, v3 = a23 >> 16;
-  uint32_t v4 = (w2 >> (sb << 3)) & 0xffffu;
+  uint32_t v4 = __builtin_amdgcn_ubfe(w2, g << 4, 16);
   asm volatile("" : "+v"(v4));  // computed for every lane: selects below, not a branch
   // candidates past the symbol (or the table) hold larger starts or 0xffff
   const bool b1 = v1 < cum, b2 = v2 < cum, b3 = v3 < cum;
